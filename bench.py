@@ -1,0 +1,221 @@
+"""Throughput of the HIP openTSNE-style t-SNE gradient loop on one MI355X.
+
+Workload: 1,000,000 x 50 float32 Gaussian mixture
+(50 components, means ~ N(0, 6^2 I), unit std), exact KNN with k = 90
+(computed on the GPU with torch as input preparation), perplexity 30, PCA
+initialisation, and the reference schedule: 250 early-exaggeration
+iterations (exaggeration 12, momentum 0.5) then 500 (momentum 0.8), learning
+rate n / 12, reference CPU grid policy (256 nodes per axis at this n).
+
+A step is one gradient iteration (repulsion + attraction + update +
+centring).  Inputs (P, layout, optimiser state) are resident in HBM before
+the timed region; the P construction is timed separately.  After W untimed
+warm-up iterations the state is reset to the initialisation and the timed
+region runs the first K iterations of the schedule (K = 750 is the whole
+run).  Per-kernel durations come from HIP events recorded on the library's
+own stream around every kernel of the timed region.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=750)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--n", type=int, default=0, help="override the number of points (smaller smoke runs)")
+    ap.add_argument("--grid", type=int, default=0, help="grid nodes per axis; 0 = reference CPU policy")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the t-SNE path is built and measured on a single MI355X "
+              "(multi-GPU sharding is a design note, not part of this build).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import fastembedr_amd as fe
+    from fastembedr_amd import synthetic
+
+    if not fe.available():
+        log("no gfx950 device visible to the HIP backend")
+        return 1
+    sched = synthetic.SCHEDULE
+    spec = synthetic.CONFIGS[args.config]
+    n = args.n or spec.n
+    k = sched["k"]
+    t0 = time.perf_counter()
+    x, _ = synthetic.gaussian_mixture(spec, seed=1, n=n)
+    log(f"data {x.shape} in {time.perf_counter() - t0:.1f}s")
+    t0 = time.perf_counter()
+    idx, dist = synthetic.exact_knn_torch(x, k, chunk=4096)
+    torch.cuda.synchronize()
+    log(f"exact KNN k={k} in {time.perf_counter() - t0:.1f}s")
+    y0 = synthetic.pca_init(x)
+    idx_r, dist_r = synthetic.to_r_layout(idx, dist, one_based=True)
+    del idx, dist
+    torch.cuda.empty_cache()
+
+    sess = fe.TsneSession(idx_r, dist_r, perplexity=sched["perplexity"], index_offset=1, grid_size=args.grid)
+    p_build_ms = sess.p_build_ms
+    nnz = sess.nnz
+    g = sess.grid_size
+    log(f"P build {p_build_ms:.1f} ms, nnz={nnz}, grid={g}")
+
+    ee = sched["early_exaggeration_iter"]
+    lr = n / 12.0
+
+    def schedule_run(count: int) -> None:
+        early = min(count, ee)
+        if early:
+            sess.run(early, sched["early_exaggeration"], sched["initial_momentum"], lr, sched["min_gain"],
+                     sched["max_step_norm"])
+        if count - early:
+            sess.run(count - early, sched["exaggeration"], sched["final_momentum"], lr, sched["min_gain"],
+                     sched["max_step_norm"])
+
+    # warm-up (untimed), then reset to the initialisation
+    sess.set_state(y0)
+    sess.center()
+    schedule_run(args.warmup)
+    sess.sync()
+    sess.set_state(y0)
+    sess.center()
+    sess.sync()
+
+    sess.set_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    schedule_run(args.steps)
+    sess.sync()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    timing = sess.timing()
+    sess.set_timing(False)
+    y_final = sess.y
+    if not np.all(np.isfinite(y_final)):
+        log("non-finite layout after the timed region")
+        return 1
+    its = args.steps / wall
+    ms_per_step = 1000.0 * wall / args.steps
+    per_kernel = {name: (tot / cnt if cnt else 0.0) for name, (cnt, tot) in timing.items()}
+    rep_kernels = ["spread", "kernel_rows", "kernel_cols", "charge_rows", "conv_cols", "inverse_rows"]
+    rep_ms = sum(per_kernel[kname] for kname in rep_kernels)
+    dom = "attract_update"
+    dom_ms = per_kernel[dom]
+    # Algorithmic bytes of one attract_update launch: CSR col + val streamed
+    # once (8 nnz), row pointers (4 (n + 1)), and the fused update's point
+    # state: y_i, gains, update read (24 n) and written (24 n).  Neighbour
+    # gathers and grid reads are cache-resident and not counted.
+    dom_bytes = 8.0 * nnz + 4.0 * (n + 1) + 48.0 * n
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9 if dom_ms > 0 else 0.0
+    log(f"{its:.1f} it/s, {ms_per_step:.3f} ms/step, repulsion {rep_ms:.3f} ms, {dom} {dom_ms:.3f} ms "
+        f"({achieved:.0f} GB/s)")
+    log("per-kernel ms: " + ", ".join(f"{kk}={v:.4f}" for kk, v in per_kernel.items()))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(sess, y0, n, lr, sched, args.cpu_seconds)
+    sess.close()
+
+    line = {
+        "metric": "t-SNE gradient iterations/sec at N=1M (2D); ms per FFT repulsion step; % HBM peak",
+        "value": round(its, 3),
+        "unit": "iterations/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"config{args.config}: {n} x 50 Gaussian mixture ({spec.components} components), "
+                        f"exact KNN k={k}, perplexity 30, 250 early-exaggeration + 500 iterations, "
+                        f"PCA init, grid {g}x{g} ({'reference CPU policy' if args.grid == 0 else 'explicit'})",
+            "n": n,
+            "k": k,
+            "nnz": nnz,
+            "grid_nodes_per_axis": g,
+            "timed_iterations": f"first {args.steps} of the 750-iteration schedule",
+        },
+        "ms_per_repulsion_step": round(rep_ms, 4),
+        "p_build_ms": round(p_build_ms, 2),
+        "per_kernel_ms": {kk: round(v, 5) for kk, v in per_kernel.items()},
+        "roofline": {
+            "kernel": dom,
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes": int(dom_bytes),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline(sess, y0, n, lr, sched, budget_s):
+    """The CPU oracle (a restatement of the reference CPU path) on the same P
+    and initialisation, timed on this host's cores for a bounded number of
+    early-exaggeration iterations (gradient + update + centring)."""
+    from oracle import oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    P = oracle.OracleP.wrap(*sess.csr())
+    y = np.array(y0, np.float32, copy=True)
+    oracle.zero_mean(y)
+    t0 = time.perf_counter()
+    y, _, _ = P.optimize(y, 1, 0, sched["early_exaggeration"], 1.0, lr, False, sched["initial_momentum"],
+                         sched["final_momentum"], threads=threads)
+    one = time.perf_counter() - t0
+    iters = max(1, min(200, int(budget_s / max(one, 1e-3))))
+    t0 = time.perf_counter()
+    P.optimize(y, iters, 0, sched["early_exaggeration"], 1.0, lr, False, sched["initial_momentum"],
+               sched["final_momentum"], threads=threads)
+    dt = time.perf_counter() - t0
+    log(f"CPU oracle: {iters} iterations in {dt:.1f}s on {threads} threads")
+    return {
+        "value": round(iters / dt, 4),
+        "unit": "iterations/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{iters} early-exaggeration iterations (after 1 untimed) of the same n={n} problem, "
+                  f"same P and initialisation, reference CPU grid policy",
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

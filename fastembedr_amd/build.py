@@ -1,0 +1,79 @@
+"""Builds the gfx950 HIP library in-tree (fastembedr_amd/lib/libfastembedr_hip.so).
+
+The library is plain HIP C++ behind the C ABI of include/fastembedr_hip.h;
+nothing in it depends on torch.  Run ``python -m fastembedr_amd.build``.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB_DIR = PKG / "lib"
+LIB = LIB_DIR / "libfastembedr_hip.so"
+BUILD_DIR = ROOT / "_build" / "hip"
+
+ARCH = os.environ.get("FASTEMBEDR_HIP_ARCH", "gfx950")
+
+# Device-code flags.  Packed fp32 instructions are switched off (they have
+# given silent wrong results on these boxes); denormals are kept so that the
+# perplexity search matches a CPU build bit for bit wherever exp/log agree.
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall", "-D__HIP_PLATFORM_AMD__"]
+
+
+def _hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cand = Path(rocm) / "bin" / "hipcc"
+    if cand.exists():
+        return str(cand)
+    found = shutil.which("hipcc")
+    if not found:
+        raise RuntimeError("hipcc not found (set ROCM_PATH)")
+    return found
+
+
+def _run(cmd: list[str]) -> None:
+    print("+", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build(verbose: bool = True) -> Path:
+    hipcc = _hipcc()
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    inc = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
+    kobj = BUILD_DIR / "embedding_hip_kernels.o"
+    sobj = BUILD_DIR / "embedding_hip_session.o"
+    _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(CSRC / "embedding_hip_kernels.hip"), "-o", str(kobj)])
+    _run([hipcc, *HOST_FLAGS, *inc, "-c", str(CSRC / "embedding_hip_session.cpp"), "-o", str(sobj)])
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", str(kobj), str(sobj), "-o", str(tmp)])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle() -> Path:
+    _run(["make", "-s", "-C", str(ROOT / "oracle")])
+    return ROOT / "oracle" / "_build" / "libtsne_oracle.so"
+
+
+if __name__ == "__main__":
+    build()
+    if "--oracle" in sys.argv:
+        build_oracle()

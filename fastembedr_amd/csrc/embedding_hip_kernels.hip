@@ -1,0 +1,1193 @@
+// gfx950 (CDNA4) kernels of the openTSNE-style t-SNE gradient loop.
+//
+// Wave64 throughout.  Nothing here uses MFMA: the loop is HBM/L2-bound
+// (CSR streaming, grid FFTs) and its arithmetic is fp32 vector work.
+//
+// Kernel map (reference semantics in src/tsne_neighbors.cpp of
+// tkcaccia/fastEmbedR):
+//   k_row_search        per-row fp32 perplexity bisection (:488-538) and the
+//                       directed edges of both orientations (:566-579)
+//   sort + k_mark_heads + scan + k_compact
+//                       duplicate merge in fp64 and symmetric CSR (:581-648)
+//   k_stats             bounding box + fp64 mean -> grid geometry
+//                       (:1089-1110, :1200-1211)
+//   k_spread            bilinear charge spreading (:1111-1148)
+//   k_kernel_rows/cols  spectrum of the Cauchy kernel and its square (:860-897)
+//   k_charge_rows, k_conv_cols, k_inverse_rows
+//                       zero-padded 2-D convolution (:899-941) with
+//                       real-input packing, pruned rows and fused products;
+//                       sum of q (:1150-1163) as a grid dot product
+//   k_attract<mode>     CSR attraction (:985-1012) + bilinear read-back
+//                       (:1165-1180) + gains/momentum/clip update (:1217-1256)
+//                       + statistics for the next iteration's centring
+//   k_exact_rep, k_kl_rows
+//                       exact O(n^2) terms for checking (:1014-1074, :958-983,
+//                       :1258-1285)
+
+#include <hip/hip_runtime.h>
+
+#include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_scan.hpp>
+
+#include <cfloat>
+#include <cmath>
+
+#include "tsne_device.h"
+
+namespace fehip {
+namespace {
+
+constexpr int kWave = 64;
+
+constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
+
+__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
+  return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+__device__ __forceinline__ float2 cscale(float2 a, float s) { return make_float2(a.x * s, a.y * s); }
+__device__ __forceinline__ float2 conjf2(float2 a) { return make_float2(a.x, -a.y); }
+// i * a
+__device__ __forceinline__ float2 mul_i(float2 a) { return make_float2(-a.y, a.x); }
+
+// ---------------------------------------------------------------------------
+// Reductions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ void combine(BlockStats& a, const BlockStats& b) {
+  a.min_x = fminf(a.min_x, b.min_x);
+  a.max_x = fmaxf(a.max_x, b.max_x);
+  a.min_y = fminf(a.min_y, b.min_y);
+  a.max_y = fmaxf(a.max_y, b.max_y);
+  a.sum_x += b.sum_x;
+  a.sum_y += b.sum_y;
+}
+
+__device__ __forceinline__ BlockStats stats_identity() {
+  BlockStats s;
+  s.min_x = FLT_MAX;
+  s.max_x = -FLT_MAX;
+  s.min_y = FLT_MAX;
+  s.max_y = -FLT_MAX;
+  s.sum_x = 0.0;
+  s.sum_y = 0.0;
+  return s;
+}
+
+__device__ __forceinline__ BlockStats wave_stats(BlockStats s) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    BlockStats o;
+    o.min_x = __shfl_xor(s.min_x, off, kWave);
+    o.max_x = __shfl_xor(s.max_x, off, kWave);
+    o.min_y = __shfl_xor(s.min_y, off, kWave);
+    o.max_y = __shfl_xor(s.max_y, off, kWave);
+    o.sum_x = __shfl_xor(s.sum_x, off, kWave);
+    o.sum_y = __shfl_xor(s.sum_y, off, kWave);
+    combine(s, o);
+  }
+  return s;
+}
+
+// Block-wide reduction; the result is valid in thread 0.  Fixed order, so the
+// result is deterministic for a fixed launch shape.
+template <int NT>
+__device__ BlockStats block_stats(BlockStats s) {
+  __shared__ BlockStats part[NT / kWave];
+  s = wave_stats(s);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    BlockStats t = part[0];
+    for (int w = 1; w < NT / kWave; ++w) combine(t, part[w]);
+    s = t;
+  }
+  __syncthreads();
+  return s;
+}
+
+template <int NT>
+__device__ double block_sum(double v) {
+  __shared__ double part[NT / kWave];
+  v = wave_sum(v);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = v;
+  __syncthreads();
+  double t = 0.0;
+  if (threadIdx.x == 0) {
+    for (int w = 0; w < NT / kWave; ++w) t += part[w];
+  }
+  __syncthreads();
+  return t;
+}
+
+// "Last block done": publishes this block's partial, and returns true in the
+// block that arrives last (after an acquire fence, so every partial is visible).
+__device__ bool arrive_last(unsigned int* ticket) {
+  __shared__ bool last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned int t = atomicAdd(ticket, 1u);
+    last = (t == gridDim.x - 1);
+  }
+  __syncthreads();
+  if (last) __threadfence();
+  return last;
+}
+
+// Grid geometry from the bounding box and mean of the stored layout
+// (src/tsne_neighbors.cpp:1089-1110 and :1200-1211).  Subtracting a constant
+// is monotone under rounding, so the box of the centred layout is the centred
+// box of the stored one.  fp32, no contraction, same operation order.
+__device__ void set_geometry(DeviceScalars* sc, const BlockStats& t, int n, int g, bool center) {
+#pragma clang fp contract(off)
+  const double mx = t.sum_x / static_cast<double>(n);
+  const double my = t.sum_y / static_cast<double>(n);
+  const float sx = center ? static_cast<float>(mx) : 0.0f;
+  const float sy = center ? static_cast<float>(my) : 0.0f;
+  const float mnx = t.min_x - sx, mxx = t.max_x - sx;
+  const float mny = t.min_y - sy, mxy = t.max_y - sy;
+  const float cx = 0.5f * (mnx + mxx);
+  const float cy = 0.5f * (mny + mxy);
+  const float ex = mxx - mnx, ey = mxy - mny;
+  float span = (ex < ey) ? ey : ex;
+  if (!isfinite(span) || span <= 0.0f) span = 1.0f;
+  const float half = 0.55f * span + 1.0e-3f;
+  const float h = (2.0f * half) / static_cast<float>(g - 1);
+  sc->shift_x = sx;
+  sc->shift_y = sy;
+  sc->lo_x = cx - half;
+  sc->lo_y = cy - half;
+  sc->h = h;
+  sc->inv_h = 1.0f / h;
+  sc->mean_x = mx;
+  sc->mean_y = my;
+  sc->min_x = mnx;
+  sc->max_x = mxx;
+  sc->min_y = mny;
+  sc->max_y = mxy;
+}
+
+template <int NT>
+__device__ void finish_stats(BlockStats local, BlockStats* partial, DeviceScalars* sc, int n, int g, bool center) {
+  BlockStats s = block_stats<NT>(local);
+  if (threadIdx.x == 0) partial[blockIdx.x] = s;
+  if (!arrive_last(&sc->ticket_stats)) return;
+  BlockStats acc = stats_identity();
+  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += NT) {
+    const BlockStats* src = partial + b;
+    BlockStats o;
+    o.min_x = __builtin_nontemporal_load(&src->min_x);
+    o.max_x = __builtin_nontemporal_load(&src->max_x);
+    o.min_y = __builtin_nontemporal_load(&src->min_y);
+    o.max_y = __builtin_nontemporal_load(&src->max_y);
+    o.sum_x = __builtin_nontemporal_load(&src->sum_x);
+    o.sum_y = __builtin_nontemporal_load(&src->sum_y);
+    combine(acc, o);
+  }
+  acc = block_stats<NT>(acc);
+  if (threadIdx.x == 0) {
+    set_geometry(sc, acc, n, g, center);
+    sc->ticket_stats = 0u;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// P construction
+// ---------------------------------------------------------------------------
+constexpr int kSearchThreads = 64;
+
+// One thread per row; the row's squared distances are staged in LDS as
+// [column][thread] (conflict-free).  Input is column-major, so both the
+// distance and the index reads are coalesced across the wave.  The search is
+// the reference's fp32 algorithm in the same operation order; the two loops
+// of the reference (mass, then entropy) are fused, which does not change
+// either accumulation order.
+template <typename DT>
+__global__ __launch_bounds__(kSearchThreads) void k_row_search(const int* __restrict__ idx_cm,
+                                                               const DT* __restrict__ dist_cm, int n, int k,
+                                                               int offset, float log_perp,
+                                                               float* __restrict__ p_cond,
+                                                               std::uint64_t* __restrict__ keys,
+                                                               float* __restrict__ vals, int key_bits,
+                                                               double* __restrict__ mass_partial,
+                                                               DeviceScalars* sc) {
+#pragma clang fp contract(off)
+  extern __shared__ float sq[];
+  const int t = threadIdx.x;
+  const int i = blockIdx.x * kSearchThreads + t;
+  const bool active = i < n;
+  unsigned int bad = 0u;
+  if (active) {
+    for (int j = 0; j < k; ++j) {
+      const float d = static_cast<float>(dist_cm[static_cast<std::size_t>(j) * n + i]);
+      if (!isfinite(d) || d < 0.0f) bad |= kErrDistance;
+      sq[j * kSearchThreads + t] = d * d;
+    }
+  }
+  double mass_sum = 0.0;
+  unsigned long long self = 0ull;
+  if (active) {
+    float beta = 1.0f;
+    float lo = -FLT_MAX;
+    float hi = FLT_MAX;
+    float mass = FLT_MIN;
+    float beta_eval = beta;
+    bool done = false;
+    for (int step = 0; !done && step < 200; ++step) {
+      beta_eval = beta;
+      mass = FLT_MIN;
+      float ent = 0.0f;
+      for (int j = 0; j < k; ++j) {
+        const float s = sq[j * kSearchThreads + t];
+        const float w = expf(-beta * s);
+        mass += w;
+        ent += beta * (s * w);
+      }
+      ent = ent / mass + logf(mass);
+      const float gap = ent - log_perp;
+      if (fabsf(gap) < 1e-5f) {
+        done = true;
+      } else if (gap > 0.0f) {
+        lo = beta;
+        beta = (hi == FLT_MAX || hi == -FLT_MAX) ? beta * 2.0f : (beta + hi) * 0.5f;
+      } else {
+        hi = beta;
+        beta = (lo == -FLT_MAX || lo == FLT_MAX) ? beta * 0.5f : (beta + lo) * 0.5f;
+      }
+    }
+    const float inv = 1.0f / mass;
+    const std::uint64_t sentinel = (key_bits >= 32) ? ~0ull : ((1ull << (2 * key_bits)) - 1ull);
+    for (int j = 0; j < k; ++j) {
+      const std::size_t e = static_cast<std::size_t>(j) * n + i;
+      const float p = expf(-beta_eval * sq[j * kSearchThreads + t]) * inv;
+      p_cond[e] = p;
+      const int nb = idx_cm[e] - offset;
+      if (nb < 0 || nb >= n) bad |= kErrIndex;
+      if (nb == i || nb < 0 || nb >= n) {
+        keys[2 * e] = sentinel;
+        keys[2 * e + 1] = sentinel;
+        vals[2 * e] = 0.0f;
+        vals[2 * e + 1] = 0.0f;
+        ++self;
+      } else {
+        keys[2 * e] = (static_cast<std::uint64_t>(i) << key_bits) | static_cast<std::uint64_t>(nb);
+        keys[2 * e + 1] = (static_cast<std::uint64_t>(nb) << key_bits) | static_cast<std::uint64_t>(i);
+        vals[2 * e] = p;
+        vals[2 * e + 1] = p;
+        mass_sum += static_cast<double>(p);
+      }
+    }
+  }
+  mass_sum = wave_sum(mass_sum);
+  if (t == 0) {
+    mass_partial[blockIdx.x] = mass_sum;
+  }
+  for (int off = kWave / 2; off > 0; off >>= 1) self += __shfl_xor(self, off, kWave);
+  unsigned int bad_all = bad;
+  for (int off = kWave / 2; off > 0; off >>= 1) bad_all |= __shfl_xor(bad_all, off, kWave);
+  if (t == 0) {
+    if (self) atomicAdd(&sc->self_edges, self);
+    if (bad_all) atomicOr(&sc->error_flags, bad_all);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_finalize_mass(const double* __restrict__ partial, int blocks,
+                                                       DeviceScalars* sc) {
+  double acc = 0.0;
+  for (int b = threadIdx.x; b < blocks; b += 256) acc += partial[b];
+  acc = block_sum<256>(acc);
+  if (threadIdx.x == 0) sc->total_mass = acc;
+}
+
+__global__ __launch_bounds__(256) void k_mark_heads(const std::uint64_t* __restrict__ keys, std::size_t count,
+                                                    int* __restrict__ heads) {
+  const std::size_t e = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= count) return;
+  heads[e] = (e == 0 || keys[e] != keys[e - 1]) ? 1 : 0;
+}
+
+// One thread per run head: fp64 sum of the run (the reference sums the
+// duplicates of a key in fp64, src/tsne_neighbors.cpp:590-597), scaled by
+// float(0.5 / total_mass) after narrowing (:632-637).  Row pointers are filled
+// at each row change; the last entry closes the remaining rows.
+__global__ __launch_bounds__(256) void k_compact(const std::uint64_t* __restrict__ keys,
+                                                 const float* __restrict__ vals, const int* __restrict__ heads,
+                                                 const int* __restrict__ pos, std::size_t count, int key_bits,
+                                                 int n, const DeviceScalars* sc, int* __restrict__ row_ptr,
+                                                 int* __restrict__ col, float* __restrict__ val) {
+  const std::size_t e = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= count) return;
+  const std::uint64_t mask = (1ull << key_bits) - 1ull;
+  const std::uint64_t key = keys[e];
+  const int row = static_cast<int>(key >> key_bits);
+  if (heads[e]) {
+    const int u = pos[e];
+    double s = 0.0;
+    for (std::size_t f = e; f < count && keys[f] == key; ++f) s += static_cast<double>(vals[f]);
+    const float norm = static_cast<float>(0.5 / sc->total_mass);
+    col[u] = static_cast<int>(key & mask);
+    val[u] = static_cast<float>(s) * norm;
+    const int prev_row = (e == 0) ? -1 : static_cast<int>(keys[e - 1] >> key_bits);
+    for (int r = prev_row + 1; r <= row; ++r) row_ptr[r] = u;
+  }
+  if (e == count - 1) {
+    const int nnz = pos[e] + heads[e];
+    for (int r = row + 1; r <= n; ++r) row_ptr[r] = nnz;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Layout statistics, spreading, centring
+// ---------------------------------------------------------------------------
+constexpr int kPointThreads = 256;
+
+__global__ __launch_bounds__(kPointThreads) void k_stats(const float2* __restrict__ y, int n, int g, int center,
+                                                         BlockStats* __restrict__ partial, DeviceScalars* sc) {
+  BlockStats s = stats_identity();
+  for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += gridDim.x * kPointThreads) {
+    const float2 v = y[i];
+    s.min_x = fminf(s.min_x, v.x);
+    s.max_x = fmaxf(s.max_x, v.x);
+    s.min_y = fminf(s.min_y, v.y);
+    s.max_y = fmaxf(s.max_y, v.y);
+    s.sum_x += static_cast<double>(v.x);
+    s.sum_y += static_cast<double>(v.y);
+  }
+  finish_stats<kPointThreads>(s, partial, sc, n, g, center != 0);
+}
+
+// Bilinear weights of one point, exactly as the reference computes them
+// (src/tsne_neighbors.cpp:1116-1133).
+struct Bilinear {
+  int x0, y0;
+  float tx, ty;
+};
+
+__device__ __forceinline__ Bilinear locate(float px, float py, const DeviceScalars& s, int g) {
+#pragma clang fp contract(off)
+  const float top = static_cast<float>(g - 1);
+  const float ux = fmaxf(0.0f, fminf(top, (px - s.lo_x) * s.inv_h));
+  const float uy = fmaxf(0.0f, fminf(top, (py - s.lo_y) * s.inv_h));
+  Bilinear b;
+  b.x0 = max(0, min(g - 2, static_cast<int>(floorf(ux))));
+  b.y0 = max(0, min(g - 2, static_cast<int>(floorf(uy))));
+  b.tx = ux - static_cast<float>(b.x0);
+  b.ty = uy - static_cast<float>(b.y0);
+  return b;
+}
+
+__global__ __launch_bounds__(kPointThreads) void k_spread(const float2* __restrict__ y_stored,
+                                                          float2* __restrict__ y_cur, const DeviceScalars* sc,
+                                                          float* __restrict__ mass, float* __restrict__ mass_x,
+                                                          float* __restrict__ mass_y, int n, int g) {
+#pragma clang fp contract(off)
+  const DeviceScalars s = *sc;
+  for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += gridDim.x * kPointThreads) {
+    const float2 r = y_stored[i];
+    const float px = r.x - s.shift_x;
+    const float py = r.y - s.shift_y;
+    y_cur[i] = make_float2(px, py);
+    const Bilinear b = locate(px, py, s, g);
+    const float w00 = (1.0f - b.tx) * (1.0f - b.ty);
+    const float w10 = b.tx * (1.0f - b.ty);
+    const float w01 = (1.0f - b.tx) * b.ty;
+    const float w11 = b.tx * b.ty;
+    const int a00 = b.y0 * g + b.x0;
+    const int a10 = a00 + 1;
+    const int a01 = a00 + g;
+    const int a11 = a01 + 1;
+    atomicAdd(mass + a00, w00);
+    atomicAdd(mass + a10, w10);
+    atomicAdd(mass + a01, w01);
+    atomicAdd(mass + a11, w11);
+    atomicAdd(mass_x + a00, w00 * px);
+    atomicAdd(mass_x + a10, w10 * px);
+    atomicAdd(mass_x + a01, w01 * px);
+    atomicAdd(mass_x + a11, w11 * px);
+    atomicAdd(mass_y + a00, w00 * py);
+    atomicAdd(mass_y + a10, w10 * py);
+    atomicAdd(mass_y + a01, w01 * py);
+    atomicAdd(mass_y + a11, w11 * py);
+  }
+}
+
+__global__ __launch_bounds__(kPointThreads) void k_commit(float2* __restrict__ y, const DeviceScalars* sc, int n) {
+  const float sx = sc->shift_x, sy = sc->shift_y;
+  for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += gridDim.x * kPointThreads) {
+    const float2 v = y[i];
+    y[i] = make_float2(v.x - sx, v.y - sy);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LDS Stockham FFT
+//
+// NSEQ sequences of length F, sequence q at s + q * F, transformed in place by
+// NT threads.  Radix-4 stages (Ns = 1, 4, 16, ...) then one radix-2 stage
+// when log2(F) is odd; every stage reads its inputs to registers, barriers,
+// and writes the Stockham-permuted outputs, so the result is in natural order.
+// Twiddles come from a 4096-entry table of e^{-2 pi i m / 4096} (computed in
+// fp64 on the host); INV conjugates them and leaves the result unscaled.
+// ---------------------------------------------------------------------------
+template <bool INV>
+__device__ __forceinline__ float2 twiddle(const float2* __restrict__ tw, int m) {
+  const float2 w = tw[m];
+  return INV ? make_float2(w.x, -w.y) : w;
+}
+
+template <int F, int NSEQ, int NT, bool INV>
+__device__ __forceinline__ void fft_lds(float2* s, const float2* __restrict__ tw) {
+  constexpr int LOG2F = ilog2(F);
+  constexpr int Q = F / 4;
+  constexpr int TOT = NSEQ * Q;
+  constexpr int BPT = (TOT + NT - 1) / NT;
+  constexpr int TWS = kTwiddleLen / F;
+#pragma unroll
+  for (int stage = 0; stage < LOG2F / 2; ++stage) {
+    const int ns = 1 << (2 * stage);
+    float2 v[BPT][4];
+#pragma unroll
+    for (int b = 0; b < BPT; ++b) {
+      const int t = threadIdx.x + b * NT;
+      if (TOT % NT == 0 || t < TOT) {
+        const int q = t / Q;
+        const int j = t - q * Q;
+        const float2* src = s + q * F;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[b][r] = src[j + r * Q];
+        const int kk = j & (ns - 1);
+        const int step = (F / (4 * ns)) * kk * TWS;
+        v[b][1] = cmul(v[b][1], twiddle<INV>(tw, step));
+        v[b][2] = cmul(v[b][2], twiddle<INV>(tw, 2 * step));
+        v[b][3] = cmul(v[b][3], twiddle<INV>(tw, 3 * step));
+        const float2 a = cadd(v[b][0], v[b][2]);
+        const float2 c = csub(v[b][0], v[b][2]);
+        const float2 d = cadd(v[b][1], v[b][3]);
+        const float2 e = csub(v[b][1], v[b][3]);
+        // forward: (-i) * e, inverse: (+i) * e
+        const float2 er = INV ? make_float2(-e.y, e.x) : make_float2(e.y, -e.x);
+        v[b][0] = cadd(a, d);
+        v[b][1] = cadd(c, er);
+        v[b][2] = csub(a, d);
+        v[b][3] = csub(c, er);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < BPT; ++b) {
+      const int t = threadIdx.x + b * NT;
+      if (TOT % NT == 0 || t < TOT) {
+        const int q = t / Q;
+        const int j = t - q * Q;
+        const int kk = j & (ns - 1);
+        float2* dst = s + q * F + (j - kk) * 4 + kk;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[r * ns] = v[b][r];
+      }
+    }
+    __syncthreads();
+  }
+  if (LOG2F & 1) {
+    constexpr int H2 = F / 2;
+    constexpr int TOT2 = NSEQ * H2;
+#pragma unroll
+    for (int b = 0; b < (TOT2 + NT - 1) / NT; ++b) {
+      const int t = threadIdx.x + b * NT;
+      if (TOT2 % NT == 0 || t < TOT2) {
+        const int q = t / H2;
+        const int j = t - q * H2;
+        float2* base = s + q * F;
+        const float2 v0 = base[j];
+        const float2 v1 = cmul(base[j + H2], twiddle<INV>(tw, j * TWS));
+        base[j] = cadd(v0, v1);
+        base[j + H2] = csub(v0, v1);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int F>
+struct Shape {
+  static constexpr int G = F / 2;
+  static constexpr int H = F / 2 + 1;
+  static constexpr int KROWS = F >= 1024 ? 1 : 1024 / F;  // single-sequence rows per block
+  static constexpr int CROWS = F >= 512 ? 1 : 512 / F;    // two-sequence rows per block
+  static constexpr int CCOLS = F >= 256 ? 1 : 256 / F;    // four-buffer columns per block
+  static constexpr int NT = 256;
+};
+
+// Row transforms of the kernel quadrant.  Row y in [0, F/2] of the wrapped
+// (F x F) kernel holds K1 = 1 / (1 + h^2 (dx^2 + dy^2)) and K2 = K1^2 at
+// |dx|, |dy| <= G - 1 (src/tsne_neighbors.cpp:878-897), packed as K1 + i K2.
+// Both are real and even, so the transform of the packed row is R1 + i R2
+// with R1, R2 real and even in kx: only kx in [0, F/2] is kept.
+template <int F>
+__global__ __launch_bounds__(256) void k_kernel_rows(const DeviceScalars* sc, const float2* __restrict__ tw,
+                                                     float2* __restrict__ k_rows) {
+  using S = Shape<F>;
+  __shared__ float2 lds[S::KROWS * F];
+  const float h = sc->h;
+  const int row0 = blockIdx.x * S::KROWS;
+  for (int e = threadIdx.x; e < S::KROWS * F; e += S::NT) {
+    const int r = e / F;
+    const int x = e - r * F;
+    const int y = row0 + r;
+    float2 v = make_float2(0.0f, 0.0f);
+    if (y < S::G && x != S::G) {
+      const int dx = x < S::G ? x : x - F;
+      const float ox = static_cast<float>(dx) * h;
+      const float oy = static_cast<float>(y) * h;
+      const float q = 1.0f / (1.0f + (ox * ox + oy * oy));
+      v = make_float2(q, q * q);
+    }
+    lds[e] = v;
+  }
+  __syncthreads();
+  fft_lds<F, S::KROWS, S::NT, false>(lds, tw);
+  for (int e = threadIdx.x; e < S::KROWS * S::H; e += S::NT) {
+    const int r = e / S::H;
+    const int kx = e - r * S::H;
+    const int y = row0 + r;
+    if (y < S::H) k_rows[y * S::H + kx] = lds[r * F + kx];
+  }
+}
+
+// Column transforms of the kernel: column kx of the row transforms is even
+// in y, so it is rebuilt from rows [0, F/2]; the output is (K1^, K2^) for
+// ky in [0, F/2].
+template <int F>
+__global__ __launch_bounds__(256) void k_kernel_cols(const float2* __restrict__ k_rows,
+                                                     const float2* __restrict__ tw, float2* __restrict__ k_hat) {
+  using S = Shape<F>;
+  __shared__ float2 lds[S::KROWS * F];
+  const int col0 = blockIdx.x * S::KROWS;
+  for (int e = threadIdx.x; e < S::KROWS * F; e += S::NT) {
+    const int y = e / S::KROWS;
+    const int c = e - y * S::KROWS;
+    const int kx = col0 + c;
+    const int ys = y <= F / 2 ? y : F - y;
+    lds[c * F + y] = kx < S::H ? k_rows[ys * S::H + kx] : make_float2(0.0f, 0.0f);
+  }
+  __syncthreads();
+  fft_lds<F, S::KROWS, S::NT, false>(lds, tw);
+  for (int e = threadIdx.x; e < S::KROWS * S::H; e += S::NT) {
+    const int ky = e / S::KROWS;
+    const int c = e - ky * S::KROWS;
+    const int kx = col0 + c;
+    if (kx < S::H) k_hat[ky * S::H + kx] = lds[c * F + ky];
+  }
+}
+
+// Row transforms of the charges.  Row y < G of A = mass + i mass_x and of
+// B = mass_y (zero-padded to F) is transformed; the real-input spectra are
+// separated with the Hermitian mirror, M[k] = (A[k] + conj A[-k]) / 2 and
+// Mx[k] = (A[k] - conj A[-k]) / 2i, and only kx in [0, F/2] is stored.
+template <int F>
+__global__ __launch_bounds__(256) void k_charge_rows(const float* __restrict__ mass,
+                                                     const float* __restrict__ mass_x,
+                                                     const float* __restrict__ mass_y,
+                                                     const float2* __restrict__ tw, float2* __restrict__ m_rows,
+                                                     float2* __restrict__ mx_rows, float2* __restrict__ my_rows) {
+  using S = Shape<F>;
+  __shared__ float2 lds[2 * S::CROWS * F];
+  const int row0 = blockIdx.x * S::CROWS;
+  for (int e = threadIdx.x; e < S::CROWS * F; e += S::NT) {
+    const int r = e / F;
+    const int x = e - r * F;
+    const int y = row0 + r;
+    float2 a = make_float2(0.0f, 0.0f), b = make_float2(0.0f, 0.0f);
+    if (x < S::G && y < S::G) {
+      const int at = y * S::G + x;
+      a = make_float2(mass[at], mass_x[at]);
+      b = make_float2(mass_y[at], 0.0f);
+    }
+    lds[(2 * r) * F + x] = a;
+    lds[(2 * r + 1) * F + x] = b;
+  }
+  __syncthreads();
+  fft_lds<F, 2 * S::CROWS, S::NT, false>(lds, tw);
+  for (int e = threadIdx.x; e < S::CROWS * S::H; e += S::NT) {
+    const int r = e / S::H;
+    const int kx = e - r * S::H;
+    const int y = row0 + r;
+    if (y >= S::G) continue;
+    const float2 a = lds[(2 * r) * F + kx];
+    const float2 b = conjf2(lds[(2 * r) * F + ((F - kx) & (F - 1))]);
+    const float2 sum = cadd(a, b);
+    const float2 dif = csub(a, b);
+    m_rows[y * S::H + kx] = cscale(sum, 0.5f);
+    mx_rows[y * S::H + kx] = make_float2(0.5f * dif.y, -0.5f * dif.x);
+    my_rows[y * S::H + kx] = lds[(2 * r + 1) * F + kx];
+  }
+}
+
+// Column pass with the spectral products fused between the forward and
+// inverse transforms.  For each stored column kx: forward transforms of the
+// three charge columns (rows >= G are the zero padding), products with the
+// real kernel spectra, inverse transforms of the four potentials, and only
+// rows y < G are written (the rest of the padded result is never read).
+//   X  = M  K1^ -> q      V1 = M  K2^ -> q2
+//   V2 = Mx K2^ -> xq2    Y  = My K2^ -> yq2
+template <int F>
+__global__ __launch_bounds__(256) void k_conv_cols(const float2* __restrict__ m_rows,
+                                                   const float2* __restrict__ mx_rows,
+                                                   const float2* __restrict__ my_rows,
+                                                   const float2* __restrict__ k_hat,
+                                                   const float2* __restrict__ tw, float2* __restrict__ x_rows,
+                                                   float2* __restrict__ v1_rows, float2* __restrict__ v2_rows,
+                                                   float2* __restrict__ y_rows) {
+  using S = Shape<F>;
+  constexpr int C = S::CCOLS;
+  __shared__ float2 lds[4 * C * F];
+  const int col0 = blockIdx.x * C;
+  for (int e = threadIdx.x; e < C * F; e += S::NT) {
+    const int y = e / C;
+    const int c = e - y * C;
+    const int kx = col0 + c;
+    float2 a = make_float2(0.0f, 0.0f), b = a, d = a;
+    if (y < S::G && kx < S::H) {
+      const int at = y * S::H + kx;
+      a = m_rows[at];
+      b = mx_rows[at];
+      d = my_rows[at];
+    }
+    lds[(0 * C + c) * F + y] = a;
+    lds[(1 * C + c) * F + y] = b;
+    lds[(2 * C + c) * F + y] = d;
+  }
+  __syncthreads();
+  fft_lds<F, 3 * C, S::NT, false>(lds, tw);
+  for (int e = threadIdx.x; e < C * F; e += S::NT) {
+    const int ky = e / C;
+    const int c = e - ky * C;
+    const int kx = col0 + c;
+    const int ks = ky <= F / 2 ? ky : F - ky;
+    const float2 kk = kx < S::H ? k_hat[ks * S::H + kx] : make_float2(0.0f, 0.0f);
+    const float2 m = lds[(0 * C + c) * F + ky];
+    const float2 mx = lds[(1 * C + c) * F + ky];
+    const float2 my = lds[(2 * C + c) * F + ky];
+    lds[(0 * C + c) * F + ky] = cscale(m, kk.x);
+    lds[(3 * C + c) * F + ky] = cscale(m, kk.y);
+    lds[(1 * C + c) * F + ky] = cscale(mx, kk.y);
+    lds[(2 * C + c) * F + ky] = cscale(my, kk.y);
+  }
+  __syncthreads();
+  fft_lds<F, 4 * C, S::NT, true>(lds, tw);
+  for (int e = threadIdx.x; e < C * S::G; e += S::NT) {
+    const int y = e / C;
+    const int c = e - y * C;
+    const int kx = col0 + c;
+    if (kx >= S::H) continue;
+    const int at = y * S::H + kx;
+    x_rows[at] = lds[(0 * C + c) * F + y];
+    v2_rows[at] = lds[(1 * C + c) * F + y];
+    y_rows[at] = lds[(2 * C + c) * F + y];
+    v1_rows[at] = lds[(3 * C + c) * F + y];
+  }
+}
+
+// Inverse row pass.  The potential rows are spectra of real rows stored for
+// kx <= F/2; two of them are packed per transform, U = X + i Y and
+// V = V1 + i V2, with the upper half rebuilt from conjugates.  Outputs for
+// x < G are scaled by 1/F^2 and stored as (q2, xq2, yq2, q) per node.  The sum
+// over points of the bilinear read of q equals sum over nodes of mass * q,
+// because read-back and spreading use the same weights; it is accumulated
+// here in fp64, and the charge grids are cleared for the next iteration.
+template <int F>
+__global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__ x_rows,
+                                                      const float2* __restrict__ v1_rows,
+                                                      const float2* __restrict__ v2_rows,
+                                                      const float2* __restrict__ y_rows,
+                                                      const float2* __restrict__ tw, float* __restrict__ mass,
+                                                      float* __restrict__ mass_x, float* __restrict__ mass_y,
+                                                      float4* __restrict__ field, double* __restrict__ partial,
+                                                      int n, DeviceScalars* sc) {
+  using S = Shape<F>;
+  __shared__ float2 lds[2 * S::CROWS * F];
+  const int row0 = blockIdx.x * S::CROWS;
+  for (int e = threadIdx.x; e < S::CROWS * F; e += S::NT) {
+    const int r = e / F;
+    const int kx = e - r * F;
+    const int y = row0 + r;
+    float2 u = make_float2(0.0f, 0.0f), v = u;
+    if (y < S::G) {
+      const bool low = kx <= F / 2;
+      const int at = y * S::H + (low ? kx : F - kx);
+      float2 X = x_rows[at], Y = y_rows[at], V1 = v1_rows[at], V2 = v2_rows[at];
+      if (!low) {
+        X = conjf2(X);
+        Y = conjf2(Y);
+        V1 = conjf2(V1);
+        V2 = conjf2(V2);
+      }
+      u = cadd(X, mul_i(Y));
+      v = cadd(V1, mul_i(V2));
+    }
+    lds[(2 * r) * F + kx] = u;
+    lds[(2 * r + 1) * F + kx] = v;
+  }
+  __syncthreads();
+  fft_lds<F, 2 * S::CROWS, S::NT, true>(lds, tw);
+  const float scale = 1.0f / (static_cast<float>(F) * static_cast<float>(F));
+  double acc = 0.0;
+  for (int e = threadIdx.x; e < S::CROWS * S::G; e += S::NT) {
+    const int r = e / S::G;
+    const int x = e - r * S::G;
+    const int y = row0 + r;
+    if (y >= S::G) continue;
+    const float2 u = cscale(lds[(2 * r) * F + x], scale);
+    const float2 v = cscale(lds[(2 * r + 1) * F + x], scale);
+    const int at = y * S::G + x;
+    field[at] = make_float4(v.x, v.y, u.y, u.x);
+    acc += static_cast<double>(mass[at]) * static_cast<double>(u.x);
+    mass[at] = 0.0f;
+    mass_x[at] = 0.0f;
+    mass_y[at] = 0.0f;
+  }
+  acc = block_sum<S::NT>(acc);
+  if (threadIdx.x == 0) partial[blockIdx.x] = acc;
+  if (!arrive_last(&sc->ticket_sumq)) return;
+  double tot = 0.0;
+  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += S::NT) tot += __builtin_nontemporal_load(partial + b);
+  tot = block_sum<S::NT>(tot);
+  if (threadIdx.x == 0) {
+    sc->sum_q = tot;
+    const double z = tot - static_cast<double>(n);
+    sc->inv_sum_q = static_cast<float>(1.0 / (z > static_cast<double>(FLT_MIN) ? z : static_cast<double>(FLT_MIN)));
+    sc->ticket_sumq = 0u;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Attraction + read-back + update
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float sign0(float v) { return v == 0.0f ? 0.0f : (v < 0.0f ? -1.0f : 1.0f); }
+
+// Bilinear read of one field component (src/tsne_neighbors.cpp:760-781).
+__device__ __forceinline__ float blend(float v00, float v10, float v01, float v11, float tx, float ty) {
+#pragma clang fp contract(off)
+  return (1.0f - tx) * (1.0f - ty) * v00 + tx * (1.0f - ty) * v10 + (1.0f - tx) * ty * v01 + tx * ty * v11;
+}
+
+// L lanes per CSR row: col/val streamed in L-wide coalesced segments, y_j
+// gathered, a shuffle reduction per row.  The row's leader then adds the
+// grid repulsion (or an exact one) and applies the update.
+template <int MODE, int L>
+__global__ __launch_bounds__(256) void k_attract(const int* __restrict__ row_ptr, const int* __restrict__ col,
+                                                 const float* __restrict__ val, const float2* __restrict__ y_cur,
+                                                 float2* __restrict__ y_out, float2* __restrict__ update,
+                                                 float2* __restrict__ gains, float2* __restrict__ grad_out,
+                                                 const float2* __restrict__ exact_rep,
+                                                 const float4* __restrict__ field, int g, UpdateParams up,
+                                                 BlockStats* __restrict__ partial, DeviceScalars* sc, int n) {
+  constexpr int RPB = 256 / L;
+  const DeviceScalars s = *sc;
+  const int lane = threadIdx.x & (L - 1);
+  BlockStats st = stats_identity();
+  const float inv_exact = (MODE == kModeGradientExact)
+                              ? static_cast<float>(1.0 / (s.exact_z > static_cast<double>(FLT_MIN)
+                                                              ? s.exact_z
+                                                              : static_cast<double>(FLT_MIN)))
+                              : 0.0f;
+  for (int base = blockIdx.x * RPB; base < n; base += gridDim.x * RPB) {
+    const int i = base + threadIdx.x / L;
+    float ax = 0.0f, ay = 0.0f;
+    float2 yi = make_float2(0.0f, 0.0f);
+    if (i < n) {
+      yi = y_cur[i];
+      const int e1 = row_ptr[i + 1];
+      for (int e = row_ptr[i] + lane; e < e1; e += L) {
+        const int j = col[e];
+        const float p = val[e];
+        const float2 yj = y_cur[j];
+        const float dx = yi.x - yj.x;
+        const float dy = yi.y - yj.y;
+        const float q = 1.0f / (1.0f + (dx * dx + dy * dy));
+        const float c = up.exaggeration * p * q;
+        ax += c * dx;
+        ay += c * dy;
+      }
+    }
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) {
+      ax += __shfl_xor(ax, off, L);
+      ay += __shfl_xor(ay, off, L);
+    }
+    if (lane != 0 || i >= n) continue;
+    float gx, gy;
+    {
+#pragma clang fp contract(off)
+      if (MODE == kModeGradientExact) {
+        const float2 r = exact_rep[i];
+        gx = r.x * inv_exact;
+        gy = r.y * inv_exact;
+      } else {
+        const Bilinear b = locate(yi.x, yi.y, s, g);
+        const int a00 = b.y0 * g + b.x0;
+        const float4 f00 = field[a00];
+        const float4 f10 = field[a00 + 1];
+        const float4 f01 = field[a00 + g];
+        const float4 f11 = field[a00 + g + 1];
+        const float q2 = blend(f00.x, f10.x, f01.x, f11.x, b.tx, b.ty);
+        const float xq2 = blend(f00.y, f10.y, f01.y, f11.y, b.tx, b.ty);
+        const float yq2 = blend(f00.z, f10.z, f01.z, f11.z, b.tx, b.ty);
+        gx = -(yi.x * q2 - xq2) * s.inv_sum_q;
+        gy = -(yi.y * q2 - yq2) * s.inv_sum_q;
+      }
+      gx += ax;
+      gy += ay;
+    }
+    if (MODE != kModeUpdate) {
+      grad_out[i] = make_float2(gx, gy);
+      continue;
+    }
+    {
+#pragma clang fp contract(off)
+      float2 gn = gains[i];
+      float2 u = update[i];
+      if (sign0(u.x) != sign0(gx)) {
+        gn.x += 0.2f;
+      } else {
+        gn.x = gn.x * 0.8f + up.min_gain;
+      }
+      if (gn.x < up.min_gain) gn.x = up.min_gain;
+      u.x = up.momentum * u.x - up.learning_rate * gn.x * gx;
+      float norm_sq = 0.0f;
+      norm_sq += u.x * u.x;
+      if (sign0(u.y) != sign0(gy)) {
+        gn.y += 0.2f;
+      } else {
+        gn.y = gn.y * 0.8f + up.min_gain;
+      }
+      if (gn.y < up.min_gain) gn.y = up.min_gain;
+      u.y = up.momentum * u.y - up.learning_rate * gn.y * gy;
+      norm_sq += u.y * u.y;
+      float scale = 1.0f;
+      if (up.clip && norm_sq > up.max_step_norm * up.max_step_norm) {
+        scale = up.max_step_norm / sqrtf(fmaxf(norm_sq, FLT_MIN));
+      }
+      u.x *= scale;
+      u.y *= scale;
+      const float2 yn = make_float2(yi.x + u.x, yi.y + u.y);
+      gains[i] = gn;
+      update[i] = u;
+      y_out[i] = yn;
+      st.min_x = fminf(st.min_x, yn.x);
+      st.max_x = fmaxf(st.max_x, yn.x);
+      st.min_y = fminf(st.min_y, yn.y);
+      st.max_y = fmaxf(st.max_y, yn.y);
+      st.sum_x += static_cast<double>(yn.x);
+      st.sum_y += static_cast<double>(yn.y);
+    }
+  }
+  if (MODE == kModeUpdate) finish_stats<256>(st, partial, sc, n, g, true);
+}
+
+// ---------------------------------------------------------------------------
+// Exact O(n^2) terms
+// ---------------------------------------------------------------------------
+// rep_i = -sum_{j != i} q_ij^2 (y_i - y_j) with q in fp32, and the normaliser
+// sum_{i != j} q_ij in fp64 (src/tsne_neighbors.cpp:1024-1048).
+__global__ __launch_bounds__(256) void k_exact_rep(const float2* __restrict__ y, int n, float2* __restrict__ rep,
+                                                   double* __restrict__ partial, DeviceScalars* sc) {
+  __shared__ float2 tile[256];
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const float2 yi = i < n ? y[i] : make_float2(0.0f, 0.0f);
+  float rx = 0.0f, ry = 0.0f;
+  double z = 0.0;
+  for (int b0 = 0; b0 < n; b0 += 256) {
+    const int j = b0 + threadIdx.x;
+    tile[threadIdx.x] = j < n ? y[j] : make_float2(0.0f, 0.0f);
+    __syncthreads();
+    const int lim = min(256, n - b0);
+    if (i < n) {
+      for (int t = 0; t < lim; ++t) {
+        if (b0 + t == i) continue;
+        const float2 yj = tile[t];
+        const float dx = yi.x - yj.x;
+        const float dy = yi.y - yj.y;
+        const float q = 1.0f / (1.0f + (dx * dx + dy * dy));
+        z += static_cast<double>(q);
+        const float c = -(q * q);
+        rx += c * dx;
+        ry += c * dy;
+      }
+    }
+    __syncthreads();
+  }
+  if (i < n) rep[i] = make_float2(rx, ry);
+  z = block_sum<256>(z);
+  if (threadIdx.x == 0) partial[blockIdx.x] = z;
+  if (!arrive_last(&sc->ticket_exact)) return;
+  double tot = 0.0;
+  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += 256) tot += __builtin_nontemporal_load(partial + b);
+  tot = block_sum<256>(tot);
+  if (threadIdx.x == 0) {
+    sc->exact_z = tot;
+    sc->ticket_exact = 0u;
+  }
+}
+
+// sum_{i != j} 1 / (1 + |y_i - y_j|^2) with the squared distance in fp32 and
+// the reciprocal in fp64, as the KL's normaliser (src/tsne_neighbors.cpp:958-983).
+__global__ __launch_bounds__(256) void k_exact_z_double(const float2* __restrict__ y, int n,
+                                                        double* __restrict__ partial) {
+  __shared__ float2 tile[256];
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const float2 yi = i < n ? y[i] : make_float2(0.0f, 0.0f);
+  double z = 0.0;
+  for (int b0 = 0; b0 < n; b0 += 256) {
+    const int j = b0 + threadIdx.x;
+    tile[threadIdx.x] = j < n ? y[j] : make_float2(0.0f, 0.0f);
+    __syncthreads();
+    const int lim = min(256, n - b0);
+    if (i < n) {
+      for (int t = 0; t < lim; ++t) {
+        if (b0 + t == i) continue;
+        const float2 yj = tile[t];
+        float r2 = 0.0f;
+        const float dx = yi.x - yj.x;
+        r2 += dx * dx;
+        const float dy = yi.y - yj.y;
+        r2 += dy * dy;
+        z += 1.0 / (1.0 + static_cast<double>(r2));
+      }
+    }
+    __syncthreads();
+  }
+  z = block_sum<256>(z);
+  if (threadIdx.x == 0) partial[blockIdx.x] = z;
+}
+
+__global__ __launch_bounds__(256) void k_kl_rows(const int* __restrict__ row_ptr, const int* __restrict__ col,
+                                                 const float* __restrict__ val, const float2* __restrict__ y,
+                                                 int n, double sum_q, double* __restrict__ partial) {
+  double acc = 0.0;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+    const float2 yi = y[i];
+    for (int e = row_ptr[i]; e < row_ptr[i + 1]; ++e) {
+      const float2 yj = y[col[e]];
+      float r2 = 0.0f;
+      const float dx = yi.x - yj.x;
+      r2 += dx * dx;
+      const float dy = yi.y - yj.y;
+      r2 += dy * dy;
+      const double p = static_cast<double>(val[e]);
+      const double q = (1.0 / (1.0 + static_cast<double>(r2))) / sum_q;
+      acc += p * log((p + 1e-9) / (q + 1e-9));
+    }
+  }
+  acc = block_sum<256>(acc);
+  if (threadIdx.x == 0) partial[blockIdx.x] = acc;
+}
+
+template <int F>
+hipError_t grid_fft_launch(int which, GridBuffers& gb, const DeviceScalars* sc_const, DeviceScalars* sc,
+                           const float2* tw, int n, hipStream_t stream) {
+  using S = Shape<F>;
+  switch (which) {
+    case 0:
+      k_kernel_rows<F><<<(S::H + S::KROWS - 1) / S::KROWS, S::NT, 0, stream>>>(sc_const, tw, gb.k_rows);
+      break;
+    case 1:
+      k_kernel_cols<F><<<(S::H + S::KROWS - 1) / S::KROWS, S::NT, 0, stream>>>(gb.k_rows, tw, gb.k_hat);
+      break;
+    case 2:
+      k_charge_rows<F><<<(S::G + S::CROWS - 1) / S::CROWS, S::NT, 0, stream>>>(
+          gb.mass, gb.mass_x, gb.mass_y, tw, gb.m_rows, gb.mx_rows, gb.my_rows);
+      break;
+    case 3:
+      k_conv_cols<F><<<(S::H + S::CCOLS - 1) / S::CCOLS, S::NT, 0, stream>>>(
+          gb.m_rows, gb.mx_rows, gb.my_rows, gb.k_hat, tw, gb.x_rows, gb.v1_rows, gb.v2_rows, gb.y_rows);
+      break;
+    case 4:
+      k_inverse_rows<F><<<(S::G + S::CROWS - 1) / S::CROWS, S::NT, 0, stream>>>(
+          gb.x_rows, gb.v1_rows, gb.v2_rows, gb.y_rows, tw, gb.mass, gb.mass_x, gb.mass_y, gb.field,
+          gb.sumq_partial, n, sc);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t grid_fft_dispatch(int which, GridBuffers& gb, DeviceScalars* sc, const float2* tw, int n,
+                             hipStream_t stream) {
+  switch (2 * gb.g) {
+    case 64: return grid_fft_launch<64>(which, gb, sc, sc, tw, n, stream);
+    case 128: return grid_fft_launch<128>(which, gb, sc, sc, tw, n, stream);
+    case 256: return grid_fft_launch<256>(which, gb, sc, sc, tw, n, stream);
+    case 512: return grid_fft_launch<512>(which, gb, sc, sc, tw, n, stream);
+    case 1024: return grid_fft_launch<1024>(which, gb, sc, sc, tw, n, stream);
+    case 2048: return grid_fft_launch<2048>(which, gb, sc, sc, tw, n, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int MODE, int L>
+hipError_t attract_launch(const Csr& p, const float2* y_cur, float2* y_out, float2* update, float2* gains,
+                          float2* grad_out, const float2* exact_rep, const GridBuffers& gb, const UpdateParams& up,
+                          BlockStats* partial, DeviceScalars* sc, hipStream_t stream) {
+  constexpr int RPB = 256 / L;
+  const int needed = (p.n + RPB - 1) / RPB;
+  const int blocks = needed < 2048 ? needed : 2048;
+  k_attract<MODE, L><<<blocks, 256, 0, stream>>>(p.row_ptr, p.col, p.val, y_cur, y_out, update, gains, grad_out,
+                                                 exact_rep, gb.field, gb.g, up, partial, sc, p.n);
+  return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t attract_lanes(int lanes, const Csr& p, const float2* y_cur, float2* y_out, float2* update,
+                         float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
+                         const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, hipStream_t stream) {
+  switch (lanes) {
+    case 8: return attract_launch<MODE, 8>(p, y_cur, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc, stream);
+    case 16: return attract_launch<MODE, 16>(p, y_cur, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc, stream);
+    case 32: return attract_launch<MODE, 32>(p, y_cur, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc, stream);
+    case 64: return attract_launch<MODE, 64>(p, y_cur, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+hipError_t launch_row_search(const int* idx_cm, const void* dist_cm, bool dist_is_double, int n, int k,
+                             int index_offset, float log_perplexity, float* p_cond, std::uint64_t* keys,
+                             float* vals, int key_bits, double* mass_partial, int mass_blocks, DeviceScalars* sc,
+                             hipStream_t stream) {
+  const std::size_t lds = static_cast<std::size_t>(k) * kSearchThreads * sizeof(float);
+  if (dist_is_double) {
+    k_row_search<double><<<mass_blocks, kSearchThreads, lds, stream>>>(
+        idx_cm, static_cast<const double*>(dist_cm), n, k, index_offset, log_perplexity, p_cond, keys, vals,
+        key_bits, mass_partial, sc);
+  } else {
+    k_row_search<float><<<mass_blocks, kSearchThreads, lds, stream>>>(
+        idx_cm, static_cast<const float*>(dist_cm), n, k, index_offset, log_perplexity, p_cond, keys, vals,
+        key_bits, mass_partial, sc);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_finalize_mass(const double* mass_partial, int blocks, DeviceScalars* sc, hipStream_t stream) {
+  k_finalize_mass<<<1, 256, 0, stream>>>(mass_partial, blocks, sc);
+  return hipGetLastError();
+}
+
+hipError_t sort_edges(void* temp, std::size_t& temp_bytes, const std::uint64_t* keys_in, std::uint64_t* keys_out,
+                      const float* vals_in, float* vals_out, std::size_t count, int end_bit, hipStream_t stream) {
+  return rocprim::radix_sort_pairs(temp, temp_bytes, keys_in, keys_out, vals_in, vals_out, count, 0u,
+                                   static_cast<unsigned int>(end_bit), stream);
+}
+
+hipError_t launch_mark_heads(const std::uint64_t* keys, std::size_t count, int* heads, hipStream_t stream) {
+  if (count == 0) return hipSuccess;
+  const unsigned int blocks = static_cast<unsigned int>((count + 255) / 256);
+  k_mark_heads<<<blocks, 256, 0, stream>>>(keys, count, heads);
+  return hipGetLastError();
+}
+
+hipError_t scan_heads(void* temp, std::size_t& temp_bytes, const int* heads, int* pos, std::size_t count,
+                      hipStream_t stream) {
+  return rocprim::exclusive_scan(temp, temp_bytes, heads, pos, 0, count, rocprim::plus<int>(), stream);
+}
+
+hipError_t launch_compact(const std::uint64_t* keys, const float* vals, const int* heads, const int* pos,
+                          std::size_t count, int key_bits, int n, const DeviceScalars* sc, int* row_ptr, int* col,
+                          float* val, hipStream_t stream) {
+  if (count == 0) return hipSuccess;
+  const unsigned int blocks = static_cast<unsigned int>((count + 255) / 256);
+  k_compact<<<blocks, 256, 0, stream>>>(keys, vals, heads, pos, count, key_bits, n, sc, row_ptr, col, val);
+  return hipGetLastError();
+}
+
+int reduce_blocks_for(int n) {
+  const int needed = (n + kPointThreads - 1) / kPointThreads;
+  return needed < 1 ? 1 : (needed < 2048 ? needed : 2048);
+}
+
+hipError_t launch_stats(const float2* y, int n, int g, int center, BlockStats* partial, DeviceScalars* sc,
+                        hipStream_t stream) {
+  k_stats<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(y, n, g, center, partial, sc);
+  return hipGetLastError();
+}
+
+hipError_t launch_spread(const float2* y_stored, float2* y_cur, const DeviceScalars* sc, GridBuffers& gb, int n,
+                         hipStream_t stream) {
+  k_spread<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(y_stored, y_cur, sc, gb.mass, gb.mass_x, gb.mass_y,
+                                                               n, gb.g);
+  return hipGetLastError();
+}
+
+hipError_t launch_kernel_rows(GridBuffers& gb, const DeviceScalars* sc, const float2* tw, hipStream_t stream) {
+  return grid_fft_dispatch(0, gb, const_cast<DeviceScalars*>(sc), tw, 0, stream);
+}
+hipError_t launch_kernel_cols(GridBuffers& gb, const float2* tw, hipStream_t stream) {
+  return grid_fft_dispatch(1, gb, nullptr, tw, 0, stream);
+}
+hipError_t launch_charge_rows(GridBuffers& gb, const float2* tw, hipStream_t stream) {
+  return grid_fft_dispatch(2, gb, nullptr, tw, 0, stream);
+}
+hipError_t launch_conv_cols(GridBuffers& gb, const float2* tw, hipStream_t stream) {
+  return grid_fft_dispatch(3, gb, nullptr, tw, 0, stream);
+}
+hipError_t launch_inverse_rows(GridBuffers& gb, const float2* tw, int n, DeviceScalars* sc, hipStream_t stream) {
+  return grid_fft_dispatch(4, gb, sc, tw, n, stream);
+}
+
+hipError_t launch_attract(int mode, const Csr& p, const float2* y_cur, float2* y_out, float2* update,
+                          float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
+                          const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int lanes_per_row,
+                          hipStream_t stream) {
+  switch (mode) {
+    case kModeUpdate:
+      return attract_lanes<kModeUpdate>(lanes_per_row, p, y_cur, y_out, update, gains, grad_out, exact_rep, gb, up,
+                                        partial, sc, stream);
+    case kModeGradientGrid:
+      return attract_lanes<kModeGradientGrid>(lanes_per_row, p, y_cur, y_out, update, gains, grad_out, exact_rep,
+                                              gb, up, partial, sc, stream);
+    case kModeGradientExact:
+      return attract_lanes<kModeGradientExact>(lanes_per_row, p, y_cur, y_out, update, gains, grad_out, exact_rep,
+                                               gb, up, partial, sc, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_commit(float2* y, const DeviceScalars* sc, int n, hipStream_t stream) {
+  k_commit<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(y, sc, n);
+  return hipGetLastError();
+}
+
+int exact_blocks_for(int n) { return (n + 255) / 256; }
+
+hipError_t launch_exact_repulsion(const float2* y, int n, float2* rep, double* z_partial, DeviceScalars* sc,
+                                  hipStream_t stream) {
+  k_exact_rep<<<exact_blocks_for(n), 256, 0, stream>>>(y, n, rep, z_partial, sc);
+  return hipGetLastError();
+}
+
+hipError_t launch_exact_z_double(const float2* y, int n, double* z_partial, hipStream_t stream) {
+  k_exact_z_double<<<exact_blocks_for(n), 256, 0, stream>>>(y, n, z_partial);
+  return hipGetLastError();
+}
+
+hipError_t launch_kl_rows(const Csr& p, const float2* y, double sum_q, double* partial, int blocks,
+                          hipStream_t stream) {
+  k_kl_rows<<<blocks, 256, 0, stream>>>(p.row_ptr, p.col, p.val, y, p.n, sum_q, partial);
+  return hipGetLastError();
+}
+
+}  // namespace fehip

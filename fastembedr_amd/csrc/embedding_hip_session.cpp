@@ -1,0 +1,833 @@
+// Host orchestration and C ABI of the gfx950 openTSNE-style t-SNE backend.
+//
+// One session = one device arena holding P (CSR), the optimiser state and the
+// grid work buffers, plus one HIP stream at default priority.  Every
+// iteration is enqueued without a host round trip: the kernels exchange the
+// grid geometry and the repulsion normaliser through DeviceScalars.
+//
+// Error convention (src/embedding_cuda_kernels.cpp:55-72, 3753-3755 of the
+// reference): entry points return 0 / 1, and a thread-local message is kept
+// for fastembedr_hip_embedding_last_error().
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <limits>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "../../include/fastembedr_hip.h"
+#include "tsne_device.h"
+
+using fehip::BlockStats;
+using fehip::Csr;
+using fehip::DeviceScalars;
+using fehip::GridBuffers;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+bool hip_ok(hipError_t code, const char* where) {
+  if (code == hipSuccess) return true;
+  set_error(std::string(where) + ": " + hipGetErrorString(code));
+  return false;
+}
+
+std::size_t align_up(std::size_t v, std::size_t a = 256) { return (v + a - 1) & ~(a - 1); }
+
+int env_int(const char* name, int fallback) {
+  const char* raw = std::getenv(name);
+  if (raw == nullptr || raw[0] == '\0') return fallback;
+  char* end = nullptr;
+  const long v = std::strtol(raw, &end, 10);
+  if (end == raw || v <= 0 || v > std::numeric_limits<int>::max()) return fallback;
+  return static_cast<int>(v);
+}
+
+// The reference CPU backend's grid policy (src/tsne_neighbors.cpp:392-398).
+int policy_grid_size(int n) {
+  const int fallback = n >= 50000 ? 256 : (n >= 10000 ? 128 : 64);
+  const int requested = env_int("FASTEMBEDR_TSNE_FFT_GRID", fallback);
+  int g = 32;
+  while (g < requested && g < 512) g <<= 1;
+  return std::max(32, std::min(512, g));
+}
+
+int resolve_grid_size(int n, int requested) {
+  if (requested <= 0) return policy_grid_size(n);
+  int g = 32;
+  while (g < requested && g < fehip::kMaxGrid) g <<= 1;
+  return g;
+}
+
+// Carves 256-byte aligned buffers out of one hipMalloc.
+struct Arena {
+  char* base = nullptr;
+  std::size_t size = 0;
+  std::size_t used = 0;
+  bool init(std::size_t bytes, const char* what) {
+    size = bytes;
+    used = 0;
+    void* p = nullptr;
+    if (!hip_ok(hipMalloc(&p, bytes), what)) return false;
+    base = static_cast<char*>(p);
+    return true;
+  }
+  template <typename T>
+  T* take(std::size_t count) {
+    const std::size_t bytes = align_up(count * sizeof(T));
+    if (used + bytes > size) return nullptr;
+    T* p = reinterpret_cast<T*>(base + used);
+    used += bytes;
+    return p;
+  }
+  void release() {
+    if (base != nullptr) (void)hipFree(base);
+    base = nullptr;
+    size = used = 0;
+  }
+};
+
+bool memory_preflight(std::size_t bytes, const char* where) {
+  std::size_t free_b = 0, total_b = 0;
+  if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return true;
+  const std::size_t reserve = free_b / 20;
+  if (bytes > free_b - reserve) {
+    set_error(std::string(where) + ": device memory request exceeds available memory; required " +
+              std::to_string(bytes) + " bytes, free " + std::to_string(free_b) + " bytes");
+    return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+struct fastembedr_hip_tsne {
+  int n = 0;
+  int k = 0;
+  int lanes = 16;
+  hipStream_t stream = nullptr;
+  Arena arena;
+  DeviceScalars* sc = nullptr;
+  Csr p;
+  float* p_cond = nullptr;
+  float2* y_a = nullptr;    // stored layout (raw between iterations)
+  float2* y_b = nullptr;    // centred layout of the current iteration
+  float2* update = nullptr;
+  float2* gains = nullptr;
+  float2* grad = nullptr;
+  float2* exact_rep = nullptr;
+  float2* tw = nullptr;
+  BlockStats* partial = nullptr;
+  double* dpartial = nullptr;
+  int dpartial_len = 0;
+  GridBuffers gb;
+  double p_build_ms = 0.0;
+  bool timing = false;
+  std::vector<hipEvent_t> events;
+  std::vector<int> event_kernel;
+  long long launches[fehip::kKernelCount] = {};
+  double total_ms[fehip::kKernelCount] = {};
+
+  ~fastembedr_hip_tsne() {
+    if (stream != nullptr) (void)hipStreamSynchronize(stream);
+    for (hipEvent_t e : events) (void)hipEventDestroy(e);
+    arena.release();
+    if (stream != nullptr) (void)hipStreamDestroy(stream);
+  }
+
+  // Enqueues one kernel, bracketed by events when timing is on.
+  template <typename Launch>
+  bool timed(int kernel_id, const char* what, Launch&& launch) {
+    std::size_t slot = 0;
+    if (timing) {
+      slot = event_kernel.size();
+      while (events.size() < 2 * (slot + 1)) {
+        hipEvent_t e;
+        if (!hip_ok(hipEventCreate(&e), "hipEventCreate")) return false;
+        events.push_back(e);
+      }
+      event_kernel.push_back(kernel_id);
+      if (!hip_ok(hipEventRecord(events[2 * slot], stream), "hipEventRecord")) return false;
+    }
+    if (!hip_ok(launch(), what)) return false;
+    if (timing && !hip_ok(hipEventRecord(events[2 * slot + 1], stream), "hipEventRecord")) return false;
+    return true;
+  }
+
+  bool harvest_timing() {
+    if (!timing || event_kernel.empty()) return true;
+    if (!hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize(timing)")) return false;
+    for (std::size_t s = 0; s < event_kernel.size(); ++s) {
+      float ms = 0.0f;
+      if (!hip_ok(hipEventElapsedTime(&ms, events[2 * s], events[2 * s + 1]), "hipEventElapsedTime")) return false;
+      launches[event_kernel[s]] += 1;
+      total_ms[event_kernel[s]] += ms;
+    }
+    event_kernel.clear();
+    return true;
+  }
+};
+
+namespace {
+
+const char* kKernelNames[fehip::kKernelCount] = {
+    "stats", "spread", "kernel_rows", "kernel_cols", "charge_rows",
+    "conv_cols", "inverse_rows", "attract_update", "commit"};
+
+int key_bits_for(int n) {
+  int b = 1;
+  while ((1LL << b) <= static_cast<long long>(n)) ++b;
+  return b;
+}
+
+bool upload_twiddles(fastembedr_hip_tsne* s) {
+  std::vector<float2> host(fehip::kTwiddleLen);
+  for (int m = 0; m < fehip::kTwiddleLen; ++m) {
+    const double ang = -2.0 * M_PI * static_cast<double>(m) / static_cast<double>(fehip::kTwiddleLen);
+    host[m] = make_float2(static_cast<float>(std::cos(ang)), static_cast<float>(std::sin(ang)));
+  }
+  return hip_ok(hipMemcpyAsync(s->tw, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice, s->stream),
+                "hipMemcpy(twiddles)");
+}
+
+// Builds P from KNN (src/tsne_neighbors.cpp:540-648 semantics) and allocates
+// the iteration buffers.
+int create_session(const int* indices, const void* distances, bool dist_double, int n, int k, float perplexity,
+                   int index_offset, int on_device, int grid_size, fastembedr_hip_tsne** out) {
+  g_last_error.clear();
+  *out = nullptr;
+  if (indices == nullptr || distances == nullptr) {
+    set_error("null HIP openTSNE input pointer");
+    return 1;
+  }
+  if (n < 2 || k < 1) {
+    set_error("KNN input must have at least two rows and one neighbor column.");
+    return 1;
+  }
+  if (k > 256) {
+    // Same cap as the reference CUDA backend (src/embedding_cuda_impl.cpp:384);
+    // the search stages k x 64 squared distances in LDS (64 KB at k = 256).
+    set_error("HIP openTSNE FFT-grid currently supports at most 256 neighbors.");
+    return 1;
+  }
+  if (!(perplexity > 0.0f) || !std::isfinite(perplexity)) {
+    set_error("perplexity must be positive");
+    return 1;
+  }
+  if (index_offset != 0 && index_offset != 1) {
+    set_error("index_offset must be 0 or 1");
+    return 1;
+  }
+  int dev_count = 0;
+  if (!hip_ok(hipGetDeviceCount(&dev_count), "hipGetDeviceCount")) return 1;
+  if (dev_count < 1) {
+    set_error("No HIP device is available.");
+    return 1;
+  }
+
+  auto* s = new fastembedr_hip_tsne();
+  s->n = n;
+  s->k = k;
+  const int g = resolve_grid_size(n, grid_size);
+  if (!hip_ok(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate")) {
+    delete s;
+    return 1;
+  }
+  hipEvent_t t0, t1;
+  (void)hipEventCreate(&t0);
+  (void)hipEventCreate(&t1);
+
+  const std::size_t nk = static_cast<std::size_t>(n) * k;
+  const std::size_t edges = 2 * nk;
+  const int key_bits = key_bits_for(n);
+  const int search_blocks = (n + 63) / 64;
+
+  // Scratch for the construction of P (released before returning).
+  Arena scratch;
+  std::size_t sort_temp = 0, scan_temp = 0;
+  if (!hip_ok(fehip::sort_edges(nullptr, sort_temp, nullptr, nullptr, nullptr, nullptr, edges, 2 * key_bits,
+                                s->stream),
+              "radix_sort_pairs(size query)") ||
+      !hip_ok(fehip::scan_heads(nullptr, scan_temp, nullptr, nullptr, edges, s->stream), "exclusive_scan(size query)")) {
+    delete s;
+    return 1;
+  }
+  const std::size_t in_bytes = on_device ? 0 : align_up(nk * sizeof(int)) + align_up(nk * (dist_double ? 8 : 4));
+  const std::size_t scratch_bytes = in_bytes + 2 * align_up(edges * 8) + 2 * align_up(edges * 4) +
+                                    2 * align_up(edges * 4) + align_up(std::max(sort_temp, scan_temp)) +
+                                    align_up(search_blocks * sizeof(double)) + 4096;
+  // Persistent part: everything except CSR col/val (added once nnz is known).
+  const int dpart = std::max(fehip::kMaxReduceBlocks, fehip::exact_blocks_for(n));
+  const std::size_t gg = static_cast<std::size_t>(g) * g;
+  const std::size_t hh = static_cast<std::size_t>(g + 1);
+  const std::size_t persistent_fixed =
+      align_up(sizeof(DeviceScalars)) + align_up(nk * 4) + align_up((n + 1) * sizeof(int)) +
+      6 * align_up(static_cast<std::size_t>(n) * sizeof(float2)) + align_up(fehip::kTwiddleLen * sizeof(float2)) +
+      align_up(fehip::kMaxReduceBlocks * sizeof(BlockStats)) + align_up(dpart * sizeof(double)) +
+      3 * align_up(gg * 4) + align_up(gg * sizeof(float4)) + 2 * align_up(hh * hh * sizeof(float2)) +
+      7 * align_up(g * hh * sizeof(float2)) + align_up(fehip::kMaxReduceBlocks * sizeof(double)) + 4096;
+  if (!memory_preflight(scratch_bytes + persistent_fixed + edges * 8, "HIP openTSNE allocation preflight") ||
+      !scratch.init(scratch_bytes, "hipMalloc(P construction scratch)")) {
+    delete s;
+    return 1;
+  }
+
+  const int* d_idx = indices;
+  const void* d_dist = distances;
+  if (!on_device) {
+    int* di = scratch.take<int>(nk);
+    char* dd = scratch.take<char>(nk * (dist_double ? 8 : 4));
+    if (!hip_ok(hipMemcpyAsync(di, indices, nk * sizeof(int), hipMemcpyHostToDevice, s->stream),
+                "hipMemcpy(indices H2D)") ||
+        !hip_ok(hipMemcpyAsync(dd, distances, nk * (dist_double ? 8 : 4), hipMemcpyHostToDevice, s->stream),
+                "hipMemcpy(distances H2D)")) {
+      scratch.release();
+      delete s;
+      return 1;
+    }
+    d_idx = di;
+    d_dist = dd;
+  }
+  auto* keys_a = scratch.take<std::uint64_t>(edges);
+  auto* keys_b = scratch.take<std::uint64_t>(edges);
+  auto* vals_a = scratch.take<float>(edges);
+  auto* vals_b = scratch.take<float>(edges);
+  auto* heads = scratch.take<int>(edges);
+  auto* pos = scratch.take<int>(edges);
+  void* temp = scratch.take<char>(std::max(sort_temp, scan_temp));
+  auto* mass_partial = scratch.take<double>(search_blocks);
+
+  // Persistent buffers (P values and columns are added after nnz is known).
+  std::size_t csr_bytes_guess = 2 * align_up(edges * 4);
+  if (!s->arena.init(persistent_fixed + csr_bytes_guess, "hipMalloc(HIP openTSNE arena)")) {
+    scratch.release();
+    delete s;
+    return 1;
+  }
+  s->sc = s->arena.take<DeviceScalars>(1);
+  s->p_cond = s->arena.take<float>(nk);
+  s->p.row_ptr = s->arena.take<int>(n + 1);
+  s->y_a = s->arena.take<float2>(n);
+  s->y_b = s->arena.take<float2>(n);
+  s->update = s->arena.take<float2>(n);
+  s->gains = s->arena.take<float2>(n);
+  s->grad = s->arena.take<float2>(n);
+  s->exact_rep = s->arena.take<float2>(n);
+  s->tw = s->arena.take<float2>(fehip::kTwiddleLen);
+  s->partial = s->arena.take<BlockStats>(fehip::kMaxReduceBlocks);
+  s->dpartial = s->arena.take<double>(dpart);
+  s->dpartial_len = dpart;
+  s->gb.g = g;
+  s->gb.mass = s->arena.take<float>(gg);
+  s->gb.mass_x = s->arena.take<float>(gg);
+  s->gb.mass_y = s->arena.take<float>(gg);
+  s->gb.field = s->arena.take<float4>(gg);
+  s->gb.k_rows = s->arena.take<float2>(hh * hh);
+  s->gb.k_hat = s->arena.take<float2>(hh * hh);
+  s->gb.m_rows = s->arena.take<float2>(g * hh);
+  s->gb.mx_rows = s->arena.take<float2>(g * hh);
+  s->gb.my_rows = s->arena.take<float2>(g * hh);
+  s->gb.x_rows = s->arena.take<float2>(g * hh);
+  s->gb.v1_rows = s->arena.take<float2>(g * hh);
+  s->gb.v2_rows = s->arena.take<float2>(g * hh);
+  s->gb.y_rows = s->arena.take<float2>(g * hh);
+  s->gb.sumq_partial = s->arena.take<double>(fehip::kMaxReduceBlocks);
+
+  auto fail = [&](void) {
+    scratch.release();
+    delete s;
+    return 1;
+  };
+  if (!hip_ok(hipMemsetAsync(s->sc, 0, sizeof(DeviceScalars), s->stream), "hipMemset(scalars)") ||
+      !hip_ok(hipMemsetAsync(s->gb.mass, 0, gg * 4, s->stream), "hipMemset(grid)") ||
+      !hip_ok(hipMemsetAsync(s->gb.mass_x, 0, gg * 4, s->stream), "hipMemset(grid)") ||
+      !hip_ok(hipMemsetAsync(s->gb.mass_y, 0, gg * 4, s->stream), "hipMemset(grid)") ||
+      !upload_twiddles(s)) {
+    return fail();
+  }
+
+  (void)hipEventRecord(t0, s->stream);
+  const float log_perp = static_cast<float>(std::log(static_cast<double>(perplexity)));
+  if (!hip_ok(fehip::launch_row_search(d_idx, d_dist, dist_double, n, k, index_offset, log_perp, s->p_cond, keys_a,
+                                       vals_a, key_bits, mass_partial, search_blocks, s->sc, s->stream),
+              "row_search launch") ||
+      !hip_ok(fehip::launch_finalize_mass(mass_partial, search_blocks, s->sc, s->stream), "finalize_mass launch")) {
+    return fail();
+  }
+  DeviceScalars host_sc;
+  if (!hip_ok(hipMemcpyAsync(&host_sc, s->sc, sizeof(DeviceScalars), hipMemcpyDeviceToHost, s->stream),
+              "hipMemcpy(scalars D2H)") ||
+      !hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize(row search)")) {
+    return fail();
+  }
+  if (host_sc.error_flags & fehip::kErrIndex) {
+    set_error("KNN indices are out of range.");
+    return fail();
+  }
+  if (host_sc.error_flags & fehip::kErrDistance) {
+    set_error("KNN distances must be finite and non-negative.");
+    return fail();
+  }
+  const std::size_t valid = edges - 2 * static_cast<std::size_t>(host_sc.self_edges);
+  if (valid == 0) {
+    set_error("KNN graph produced no non-self t-SNE edges.");
+    return fail();
+  }
+  if (!std::isfinite(host_sc.total_mass) || host_sc.total_mass <= 0.0) {
+    set_error("t-SNE probability normalization failed.");
+    return fail();
+  }
+  std::size_t tb = sort_temp;
+  if (!hip_ok(fehip::sort_edges(temp, tb, keys_a, keys_b, vals_a, vals_b, edges, 2 * key_bits, s->stream),
+              "radix_sort_pairs") ||
+      !hip_ok(fehip::launch_mark_heads(keys_b, valid, heads, s->stream), "mark_heads launch")) {
+    return fail();
+  }
+  tb = scan_temp;
+  if (!hip_ok(fehip::scan_heads(temp, tb, heads, pos, valid, s->stream), "exclusive_scan")) return fail();
+  int last_pos = 0, last_head = 0;
+  if (!hip_ok(hipMemcpyAsync(&last_pos, pos + (valid - 1), sizeof(int), hipMemcpyDeviceToHost, s->stream),
+              "hipMemcpy(nnz)") ||
+      !hip_ok(hipMemcpyAsync(&last_head, heads + (valid - 1), sizeof(int), hipMemcpyDeviceToHost, s->stream),
+              "hipMemcpy(nnz)") ||
+      !hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize(scan)")) {
+    return fail();
+  }
+  const long long nnz = static_cast<long long>(last_pos) + last_head;
+  s->p.n = n;
+  s->p.nnz = nnz;
+  s->p.col = s->arena.take<int>(static_cast<std::size_t>(nnz));
+  s->p.val = s->arena.take<float>(static_cast<std::size_t>(nnz));
+  if (s->p.col == nullptr || s->p.val == nullptr) {
+    set_error("internal: CSR does not fit the arena");
+    return fail();
+  }
+  if (!hip_ok(fehip::launch_compact(keys_b, vals_b, heads, pos, valid, key_bits, n, s->sc, s->p.row_ptr, s->p.col,
+                                    s->p.val, s->stream),
+              "compact launch")) {
+    return fail();
+  }
+  (void)hipEventRecord(t1, s->stream);
+  if (!hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize(P build)")) return fail();
+  float ms = 0.0f;
+  (void)hipEventElapsedTime(&ms, t0, t1);
+  s->p_build_ms = ms;
+  (void)hipEventDestroy(t0);
+  (void)hipEventDestroy(t1);
+  scratch.release();
+
+  // Lanes per CSR row: enough to cover the mean row in a few passes.
+  const double mean_row = static_cast<double>(nnz) / n;
+  int lanes = mean_row > 96.0 ? 32 : (mean_row > 24.0 ? 16 : 8);
+  lanes = env_int("FASTEMBEDR_HIP_ATTRACT_LANES", lanes);
+  if (lanes != 8 && lanes != 16 && lanes != 32 && lanes != 64) lanes = 16;
+  s->lanes = lanes;
+  *out = s;
+  return 0;
+}
+
+bool enqueue_gradient_fields(fastembedr_hip_tsne* s, bool stats_first, int center) {
+  const int n = s->n;
+  if (stats_first &&
+      !s->timed(fehip::kKStats, "stats launch",
+                [&] { return fehip::launch_stats(s->y_a, n, s->gb.g, center, s->partial, s->sc, s->stream); })) {
+    return false;
+  }
+  return s->timed(fehip::kKSpread, "spread launch",
+                  [&] { return fehip::launch_spread(s->y_a, s->y_b, s->sc, s->gb, n, s->stream); }) &&
+         s->timed(fehip::kKKernelRows, "kernel_rows launch",
+                  [&] { return fehip::launch_kernel_rows(s->gb, s->sc, s->tw, s->stream); }) &&
+         s->timed(fehip::kKKernelCols, "kernel_cols launch",
+                  [&] { return fehip::launch_kernel_cols(s->gb, s->tw, s->stream); }) &&
+         s->timed(fehip::kKChargeRows, "charge_rows launch",
+                  [&] { return fehip::launch_charge_rows(s->gb, s->tw, s->stream); }) &&
+         s->timed(fehip::kKConvCols, "conv_cols launch",
+                  [&] { return fehip::launch_conv_cols(s->gb, s->tw, s->stream); }) &&
+         s->timed(fehip::kKInverseRows, "inverse_rows launch",
+                  [&] { return fehip::launch_inverse_rows(s->gb, s->tw, n, s->sc, s->stream); });
+}
+
+bool valid_state_args(const fastembedr_hip_tsne* s) {
+  if (s == nullptr) {
+    set_error("null HIP openTSNE session");
+    return false;
+  }
+  return true;
+}
+
+std::vector<float> random_init(int n, unsigned int seed) {
+  // src/tsne_neighbors.cpp:1693-1700: mt19937(seed), normal_distribution<float>(0, 1e-4).
+  std::vector<float> y(2 * static_cast<std::size_t>(n));
+  std::mt19937 rng(seed);
+  std::normal_distribution<float> normal(0.0f, 1.0e-4f);
+  for (float& v : y) v = normal(rng);
+  return y;
+}
+
+template <typename DT>
+int one_shot(const int* indices, const DT* distances, const float* init, int has_init, int n, int k,
+             int n_components, float perplexity, int early_exaggeration_iter, int n_iter, float early_exaggeration,
+             float exaggeration, float learning_rate, int learning_rate_auto, float initial_momentum,
+             float final_momentum, float min_gain, float max_step_norm, unsigned int seed, int index_offset,
+             float* out, int on_device) {
+  g_last_error.clear();
+  if (indices == nullptr || distances == nullptr || out == nullptr || (has_init && init == nullptr)) {
+    set_error("null HIP openTSNE input pointer");
+    return 1;
+  }
+  if (n < 2 || k < 1 || n_components != 2 || !(perplexity > 0.0f) || early_exaggeration_iter < 0 || n_iter < 0 ||
+      early_exaggeration_iter + n_iter < 1 || !(early_exaggeration > 0.0f) || !(exaggeration > 0.0f) ||
+      (!learning_rate_auto && !(learning_rate > 0.0f)) || initial_momentum < 0.0f || final_momentum < 0.0f ||
+      !(min_gain > 0.0f)) {
+    set_error("invalid HIP openTSNE FFT-grid dimensions or parameters");
+    return 1;
+  }
+  if (static_cast<double>(n - 1) < 3.0 * static_cast<double>(perplexity)) {
+    set_error("perplexity is too large for the number of samples.");
+    return 1;
+  }
+  fastembedr_hip_tsne* s = nullptr;
+  if (create_session(indices, distances, sizeof(DT) == 8, n, k, perplexity, index_offset, on_device, 0, &s) != 0) {
+    return 1;
+  }
+  std::vector<float> y0;
+  if (has_init) {
+    y0.assign(init, init + 2 * static_cast<std::size_t>(n));
+  } else {
+    y0 = random_init(n, seed);
+  }
+  int rc = fastembedr_hip_tsne_set_state(s, y0.data(), nullptr, nullptr);
+  if (rc == 0) rc = fastembedr_hip_tsne_center(s);
+  const auto phase_lr = [&](float ex) {
+    return learning_rate_auto ? static_cast<float>(static_cast<double>(n) / std::max(static_cast<double>(ex), DBL_MIN))
+                              : learning_rate;
+  };
+  if (rc == 0 && early_exaggeration_iter > 0) {
+    rc = fastembedr_hip_tsne_run(s, early_exaggeration_iter, early_exaggeration, initial_momentum,
+                                 phase_lr(early_exaggeration), min_gain, max_step_norm);
+  }
+  if (rc == 0 && n_iter > 0) {
+    rc = fastembedr_hip_tsne_run(s, n_iter, exaggeration, final_momentum, phase_lr(exaggeration), min_gain,
+                                 max_step_norm);
+  }
+  if (rc == 0) rc = fastembedr_hip_tsne_get_state(s, out, nullptr, nullptr);
+  const std::string msg = g_last_error;
+  fastembedr_hip_tsne_destroy(s);
+  if (rc != 0) g_last_error = msg;
+  return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fastembedr_hip_embedding_last_error(void) { return g_last_error.c_str(); }
+
+bool fastembedr_hip_available(void) {
+  int count = 0;
+  const hipError_t code = hipGetDeviceCount(&count);
+  if (code != hipSuccess) {
+    set_error(std::string("hipGetDeviceCount: ") + hipGetErrorString(code));
+    return false;
+  }
+  if (count < 1) return false;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return false;
+  return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+}
+
+int fastembedr_hip_opentsne_fft_from_knn_float(const int* indices, const float* distances, const float* init,
+                                               int has_init, int n, int k, int n_components, float perplexity,
+                                               int early_exaggeration_iter, int n_iter, float early_exaggeration,
+                                               float exaggeration, float learning_rate, int learning_rate_auto,
+                                               float initial_momentum, float final_momentum, float min_gain,
+                                               float max_step_norm, unsigned int seed, int index_offset,
+                                               float* out) {
+  return one_shot<float>(indices, distances, init, has_init, n, k, n_components, perplexity,
+                         early_exaggeration_iter, n_iter, early_exaggeration, exaggeration, learning_rate,
+                         learning_rate_auto, initial_momentum, final_momentum, min_gain, max_step_norm, seed,
+                         index_offset, out, 0);
+}
+
+int fastembedr_hip_opentsne_fft_from_knn(const int* indices, const double* distances, const float* init,
+                                         int has_init, int n, int k, int n_components, float perplexity,
+                                         int early_exaggeration_iter, int n_iter, float early_exaggeration,
+                                         float exaggeration, float learning_rate, int learning_rate_auto,
+                                         float initial_momentum, float final_momentum, float min_gain,
+                                         float max_step_norm, unsigned int seed, int index_offset, float* out) {
+  return one_shot<double>(indices, distances, init, has_init, n, k, n_components, perplexity,
+                          early_exaggeration_iter, n_iter, early_exaggeration, exaggeration, learning_rate,
+                          learning_rate_auto, initial_momentum, final_momentum, min_gain, max_step_norm, seed,
+                          index_offset, out, 0);
+}
+
+int fastembedr_hip_opentsne_fft_from_device_knn_float(const int* indices, const float* distances,
+                                                      const float* init, int has_init, int n, int k,
+                                                      int n_components, float perplexity,
+                                                      int early_exaggeration_iter, int n_iter,
+                                                      float early_exaggeration, float exaggeration,
+                                                      float learning_rate, int learning_rate_auto,
+                                                      float initial_momentum, float final_momentum, float min_gain,
+                                                      float max_step_norm, unsigned int seed, int index_offset,
+                                                      float* out) {
+  return one_shot<float>(indices, distances, init, has_init, n, k, n_components, perplexity,
+                         early_exaggeration_iter, n_iter, early_exaggeration, exaggeration, learning_rate,
+                         learning_rate_auto, initial_momentum, final_momentum, min_gain, max_step_norm, seed,
+                         index_offset, out, 1);
+}
+
+int fastembedr_hip_tsne_create(const int* indices, const float* distances, int n, int k, float perplexity,
+                               int index_offset, int inputs_on_device, int grid_size,
+                               fastembedr_hip_tsne** out_session) {
+  if (out_session == nullptr) {
+    set_error("null session output pointer");
+    return 1;
+  }
+  return create_session(indices, distances, false, n, k, perplexity, index_offset, inputs_on_device, grid_size,
+                        out_session);
+}
+
+void fastembedr_hip_tsne_destroy(fastembedr_hip_tsne* session) { delete session; }
+
+int fastembedr_hip_tsne_p_nnz(const fastembedr_hip_tsne* s, long long* nnz) {
+  if (!valid_state_args(s) || nnz == nullptr) return 1;
+  *nnz = s->p.nnz;
+  return 0;
+}
+
+int fastembedr_hip_tsne_copy_p(const fastembedr_hip_tsne* s, int* row_ptr, int* col, float* val) {
+  if (!valid_state_args(s)) return 1;
+  if (row_ptr != nullptr &&
+      !hip_ok(hipMemcpy(row_ptr, s->p.row_ptr, (s->n + 1) * sizeof(int), hipMemcpyDeviceToHost), "copy row_ptr"))
+    return 1;
+  if (col != nullptr &&
+      !hip_ok(hipMemcpy(col, s->p.col, static_cast<std::size_t>(s->p.nnz) * sizeof(int), hipMemcpyDeviceToHost),
+              "copy col"))
+    return 1;
+  if (val != nullptr &&
+      !hip_ok(hipMemcpy(val, s->p.val, static_cast<std::size_t>(s->p.nnz) * sizeof(float), hipMemcpyDeviceToHost),
+              "copy val"))
+    return 1;
+  return 0;
+}
+
+int fastembedr_hip_tsne_copy_conditional_p(const fastembedr_hip_tsne* s, float* p_cond) {
+  if (!valid_state_args(s) || p_cond == nullptr) return 1;
+  return hip_ok(hipMemcpy(p_cond, s->p_cond, static_cast<std::size_t>(s->n) * s->k * sizeof(float),
+                          hipMemcpyDeviceToHost),
+                "copy conditional P")
+             ? 0
+             : 1;
+}
+
+int fastembedr_hip_tsne_grid_size(const fastembedr_hip_tsne* s, int* grid_size) {
+  if (!valid_state_args(s) || grid_size == nullptr) return 1;
+  *grid_size = s->gb.g;
+  return 0;
+}
+
+int fastembedr_hip_tsne_set_state(fastembedr_hip_tsne* s, const float* y, const float* update, const float* gains) {
+  if (!valid_state_args(s) || y == nullptr) {
+    if (y == nullptr) set_error("null layout pointer");
+    return 1;
+  }
+  const std::size_t bytes = static_cast<std::size_t>(s->n) * sizeof(float2);
+  std::vector<float> fill;
+  if (!hip_ok(hipMemcpyAsync(s->y_a, y, bytes, hipMemcpyHostToDevice, s->stream), "set_state y")) return 1;
+  if (update != nullptr) {
+    if (!hip_ok(hipMemcpyAsync(s->update, update, bytes, hipMemcpyHostToDevice, s->stream), "set_state update"))
+      return 1;
+  } else if (!hip_ok(hipMemsetAsync(s->update, 0, bytes, s->stream), "set_state update")) {
+    return 1;
+  }
+  if (gains != nullptr) {
+    if (!hip_ok(hipMemcpyAsync(s->gains, gains, bytes, hipMemcpyHostToDevice, s->stream), "set_state gains")) return 1;
+  } else {
+    fill.assign(2 * static_cast<std::size_t>(s->n), 1.0f);
+    if (!hip_ok(hipMemcpyAsync(s->gains, fill.data(), bytes, hipMemcpyHostToDevice, s->stream), "set_state gains"))
+      return 1;
+  }
+  return hip_ok(hipStreamSynchronize(s->stream), "set_state sync") ? 0 : 1;
+}
+
+int fastembedr_hip_tsne_get_state(fastembedr_hip_tsne* s, float* y, float* update, float* gains) {
+  if (!valid_state_args(s)) return 1;
+  const std::size_t bytes = static_cast<std::size_t>(s->n) * sizeof(float2);
+  if (y != nullptr && !hip_ok(hipMemcpyAsync(y, s->y_a, bytes, hipMemcpyDeviceToHost, s->stream), "get_state y"))
+    return 1;
+  if (update != nullptr &&
+      !hip_ok(hipMemcpyAsync(update, s->update, bytes, hipMemcpyDeviceToHost, s->stream), "get_state update"))
+    return 1;
+  if (gains != nullptr &&
+      !hip_ok(hipMemcpyAsync(gains, s->gains, bytes, hipMemcpyDeviceToHost, s->stream), "get_state gains"))
+    return 1;
+  return hip_ok(hipStreamSynchronize(s->stream), "get_state sync") ? 0 : 1;
+}
+
+int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int repulsion, float* grad_out) {
+  if (!valid_state_args(s) || grad_out == nullptr) return 1;
+  g_last_error.clear();
+  fehip::UpdateParams up{exaggeration, 0.0f, 0.0f, 0.0f, 0.0f, 0};
+  const bool was_timing = s->timing;
+  s->timing = false;
+  bool ok = true;
+  if (repulsion == FASTEMBEDR_HIP_REPULSION_EXACT) {
+    ok = hip_ok(fehip::launch_exact_repulsion(s->y_a, s->n, s->exact_rep, s->dpartial, s->sc, s->stream),
+                "exact repulsion launch") &&
+         hip_ok(fehip::launch_attract(fehip::kModeGradientExact, s->p, s->y_a, nullptr, nullptr, nullptr, s->grad,
+                                      s->exact_rep, s->gb, up, s->partial, s->sc, s->lanes, s->stream),
+                "attract launch");
+  } else if (repulsion == FASTEMBEDR_HIP_REPULSION_GRID) {
+    ok = enqueue_gradient_fields(s, true, 0) &&
+         hip_ok(fehip::launch_attract(fehip::kModeGradientGrid, s->p, s->y_b, nullptr, nullptr, nullptr, s->grad,
+                                      nullptr, s->gb, up, s->partial, s->sc, s->lanes, s->stream),
+                "attract launch");
+  } else {
+    set_error("unsupported repulsion mode");
+    ok = false;
+  }
+  s->timing = was_timing;
+  if (!ok) return 1;
+  if (!hip_ok(hipMemcpyAsync(grad_out, s->grad, static_cast<std::size_t>(s->n) * sizeof(float2),
+                             hipMemcpyDeviceToHost, s->stream),
+              "copy gradient") ||
+      !hip_ok(hipStreamSynchronize(s->stream), "gradient sync")) {
+    return 1;
+  }
+  return 0;
+}
+
+int fastembedr_hip_tsne_center(fastembedr_hip_tsne* s) {
+  if (!valid_state_args(s)) return 1;
+  if (!hip_ok(fehip::launch_stats(s->y_a, s->n, s->gb.g, 1, s->partial, s->sc, s->stream), "stats launch") ||
+      !hip_ok(fehip::launch_commit(s->y_a, s->sc, s->n, s->stream), "commit launch")) {
+    return 1;
+  }
+  return 0;
+}
+
+int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggeration, float momentum,
+                            float learning_rate, float min_gain, float max_step_norm) {
+  if (!valid_state_args(s)) return 1;
+  g_last_error.clear();
+  if (n_iter < 0) {
+    set_error("n_iter must be non-negative");
+    return 1;
+  }
+  if (n_iter == 0) return 0;
+  fehip::UpdateParams up;
+  up.exaggeration = exaggeration;
+  up.momentum = momentum;
+  up.learning_rate = learning_rate;
+  up.min_gain = min_gain;
+  up.max_step_norm = max_step_norm;
+  up.clip = (std::isfinite(max_step_norm) && max_step_norm > 0.0f) ? 1 : 0;
+  const int n = s->n;
+  if (!s->timed(fehip::kKStats, "stats launch",
+                [&] { return fehip::launch_stats(s->y_a, n, s->gb.g, 0, s->partial, s->sc, s->stream); })) {
+    return 1;
+  }
+  for (int it = 0; it < n_iter; ++it) {
+    if (!enqueue_gradient_fields(s, false, 0)) return 1;
+    if (!s->timed(fehip::kKAttractUpdate, "attract launch", [&] {
+          return fehip::launch_attract(fehip::kModeUpdate, s->p, s->y_b, s->y_a, s->update, s->gains, nullptr,
+                                       nullptr, s->gb, up, s->partial, s->sc, s->lanes, s->stream);
+        })) {
+      return 1;
+    }
+  }
+  if (!s->timed(fehip::kKCommit, "commit launch",
+                [&] { return fehip::launch_commit(s->y_a, s->sc, n, s->stream); })) {
+    return 1;
+  }
+  return s->harvest_timing() ? 0 : 1;
+}
+
+int fastembedr_hip_tsne_sync(fastembedr_hip_tsne* s) {
+  if (!valid_state_args(s)) return 1;
+  return hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize") ? 0 : 1;
+}
+
+int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* s, double* kl) {
+  if (!valid_state_args(s) || kl == nullptr) return 1;
+  const int zb = fehip::exact_blocks_for(s->n);
+  std::vector<double> part(static_cast<std::size_t>(std::max(zb, 1024)));
+  if (!hip_ok(fehip::launch_exact_z_double(s->y_a, s->n, s->dpartial, s->stream), "exact_z launch") ||
+      !hip_ok(hipMemcpyAsync(part.data(), s->dpartial, zb * sizeof(double), hipMemcpyDeviceToHost, s->stream),
+              "copy z partials") ||
+      !hip_ok(hipStreamSynchronize(s->stream), "kl sync")) {
+    return 1;
+  }
+  double z = 0.0;
+  for (int b = 0; b < zb; ++b) z += part[b];
+  const double sum_q = static_cast<double>(static_cast<float>(std::max(z, static_cast<double>(FLT_MIN))));
+  const int kb = 1024;
+  if (!hip_ok(fehip::launch_kl_rows(s->p, s->y_a, sum_q, s->dpartial, kb, s->stream), "kl launch") ||
+      !hip_ok(hipMemcpyAsync(part.data(), s->dpartial, kb * sizeof(double), hipMemcpyDeviceToHost, s->stream),
+              "copy kl partials") ||
+      !hip_ok(hipStreamSynchronize(s->stream), "kl sync")) {
+    return 1;
+  }
+  double total = 0.0;
+  for (int b = 0; b < kb; ++b) total += part[b];
+  *kl = total;
+  return 0;
+}
+
+int fastembedr_hip_tsne_set_timing(fastembedr_hip_tsne* s, int enabled) {
+  if (!valid_state_args(s)) return 1;
+  if (!s->harvest_timing()) return 1;
+  s->timing = enabled != 0;
+  if (enabled) {
+    std::fill(std::begin(s->launches), std::end(s->launches), 0LL);
+    std::fill(std::begin(s->total_ms), std::end(s->total_ms), 0.0);
+  }
+  return 0;
+}
+
+int fastembedr_hip_tsne_timing_stats(fastembedr_hip_tsne* s, int max_kernels, long long* launches,
+                                     double* total_ms) {
+  if (!valid_state_args(s)) return 1;
+  if (!s->harvest_timing()) return 1;
+  const int m = std::min(max_kernels, static_cast<int>(fehip::kKernelCount));
+  for (int i = 0; i < m; ++i) {
+    if (launches != nullptr) launches[i] = s->launches[i];
+    if (total_ms != nullptr) total_ms[i] = s->total_ms[i];
+  }
+  return 0;
+}
+
+const char* fastembedr_hip_tsne_kernel_name(int kernel_id) {
+  if (kernel_id < 0 || kernel_id >= fehip::kKernelCount) return "";
+  return kKernelNames[kernel_id];
+}
+
+int fastembedr_hip_tsne_kernel_count(void) { return fehip::kKernelCount; }
+
+int fastembedr_hip_random_init(int n, unsigned int seed, float* out) {
+  if (n < 1 || out == nullptr) {
+    set_error("invalid random_init arguments");
+    return 1;
+  }
+  const std::vector<float> y = random_init(n, seed);
+  std::copy(y.begin(), y.end(), out);
+  return 0;
+}
+
+int fastembedr_hip_tsne_p_build_ms(const fastembedr_hip_tsne* s, double* ms) {
+  if (!valid_state_args(s) || ms == nullptr) return 1;
+  *ms = s->p_build_ms;
+  return 0;
+}
+
+}  // extern "C"

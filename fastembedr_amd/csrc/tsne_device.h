@@ -1,0 +1,135 @@
+// Internal interface between the host orchestration (embedding_hip_session.cpp)
+// and the gfx950 kernels (embedding_hip_kernels.hip).  Not part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace fehip {
+
+// Per-session scalars that the kernels read and write on the device, so that
+// an iteration never waits for the host.  Written by the "last block" of the
+// reductions (stats -> geometry, inverse rows -> sum of q).
+struct alignas(16) DeviceScalars {
+  float shift_x, shift_y;   // subtracted from the stored layout to centre it
+  float lo_x, lo_y;         // grid origin in centred coordinates
+  float h, inv_h;           // node spacing and its reciprocal
+  float inv_sum_q;          // 1 / max(sum_q - n, FLT_MIN), fp32
+  float pad0;
+  double sum_q;             // sum over nodes of mass * q (self terms included)
+  double mean_x, mean_y;    // fp64 mean of the stored layout
+  float min_x, max_x, min_y, max_y;  // bounding box of the centred layout
+  double exact_z;           // exact-repulsion normaliser (pairs i != j)
+  double total_mass;        // sum of directed p_{j|i} over non-self columns
+  unsigned int ticket_stats;
+  unsigned int ticket_sumq;
+  unsigned int ticket_exact;
+  unsigned int error_flags;  // bit 0: index out of range, bit 1: bad distance
+  unsigned long long self_edges;
+};
+
+struct BlockStats {
+  float min_x, max_x, min_y, max_y;
+  double sum_x, sum_y;
+};
+
+constexpr int kMaxReduceBlocks = 4096;
+constexpr int kTwiddleLen = 4096;     // e^{-2 pi i m / 4096}, m in [0, 4096)
+constexpr int kMaxGrid = 1024;        // nodes per axis (FFT length 2048)
+
+enum ErrorBits : unsigned int { kErrIndex = 1u, kErrDistance = 2u };
+
+enum KernelId : int {
+  kKStats = 0,
+  kKSpread,
+  kKKernelRows,
+  kKKernelCols,
+  kKChargeRows,
+  kKConvCols,
+  kKInverseRows,
+  kKAttractUpdate,
+  kKCommit,
+  kKernelCount
+};
+
+// Buffers of one grid configuration (g nodes per axis, f = 2g, hh = g + 1).
+struct GridBuffers {
+  int g = 0;
+  float* mass = nullptr;     // g*g, zero between iterations
+  float* mass_x = nullptr;
+  float* mass_y = nullptr;
+  float4* field = nullptr;   // g*g of (q2, xq2, yq2, q)
+  float2* k_rows = nullptr;  // hh*hh: row transforms of the kernel quadrant
+  float2* k_hat = nullptr;   // hh*hh: (K1^, K2^) quadrant
+  float2* m_rows = nullptr;  // g*hh each: half-spectrum rows of the charges
+  float2* mx_rows = nullptr;
+  float2* my_rows = nullptr;
+  float2* x_rows = nullptr;  // g*hh each: half-spectrum rows of the potentials
+  float2* v1_rows = nullptr;
+  float2* v2_rows = nullptr;
+  float2* y_rows = nullptr;
+  double* sumq_partial = nullptr;  // kMaxReduceBlocks
+};
+
+struct Csr {
+  int n = 0;
+  long long nnz = 0;
+  int* row_ptr = nullptr;
+  int* col = nullptr;
+  float* val = nullptr;
+};
+
+// ---- P construction -------------------------------------------------------
+// Row search + directed edge emission (both orientations); self edges get the
+// sentinel key and are counted.  `dist_is_double` selects the input type.
+hipError_t launch_row_search(const int* idx_cm, const void* dist_cm, bool dist_is_double, int n, int k,
+                             int index_offset, float log_perplexity, float* p_cond, std::uint64_t* keys,
+                             float* vals, int key_bits, double* mass_partial, int mass_blocks,
+                             DeviceScalars* sc, hipStream_t stream);
+hipError_t launch_finalize_mass(const double* mass_partial, int blocks, DeviceScalars* sc, hipStream_t stream);
+hipError_t sort_edges(void* temp, std::size_t& temp_bytes, const std::uint64_t* keys_in, std::uint64_t* keys_out,
+                      const float* vals_in, float* vals_out, std::size_t count, int end_bit, hipStream_t stream);
+hipError_t launch_mark_heads(const std::uint64_t* keys, std::size_t count, int* heads, hipStream_t stream);
+hipError_t scan_heads(void* temp, std::size_t& temp_bytes, const int* heads, int* pos, std::size_t count,
+                      hipStream_t stream);
+hipError_t launch_compact(const std::uint64_t* keys, const float* vals, const int* heads, const int* pos,
+                          std::size_t count, int key_bits, int n, const DeviceScalars* sc, int* row_ptr, int* col,
+                          float* val, hipStream_t stream);
+
+// ---- iteration ------------------------------------------------------------
+int reduce_blocks_for(int n);
+hipError_t launch_stats(const float2* y, int n, int g, int center, BlockStats* partial, DeviceScalars* sc,
+                        hipStream_t stream);
+hipError_t launch_spread(const float2* y_stored, float2* y_cur, const DeviceScalars* sc, GridBuffers& gb, int n,
+                         hipStream_t stream);
+hipError_t launch_kernel_rows(GridBuffers& gb, const DeviceScalars* sc, const float2* tw, hipStream_t stream);
+hipError_t launch_kernel_cols(GridBuffers& gb, const float2* tw, hipStream_t stream);
+hipError_t launch_charge_rows(GridBuffers& gb, const float2* tw, hipStream_t stream);
+hipError_t launch_conv_cols(GridBuffers& gb, const float2* tw, hipStream_t stream);
+hipError_t launch_inverse_rows(GridBuffers& gb, const float2* tw, int n, DeviceScalars* sc, hipStream_t stream);
+
+enum AttractMode : int { kModeUpdate = 0, kModeGradientGrid = 1, kModeGradientExact = 2 };
+struct UpdateParams {
+  float exaggeration;
+  float momentum;
+  float learning_rate;
+  float min_gain;
+  float max_step_norm;
+  int clip;
+};
+hipError_t launch_attract(int mode, const Csr& p, const float2* y_cur, float2* y_out, float2* update, float2* gains,
+                          float2* grad_out, const float2* exact_rep, const GridBuffers& gb, const UpdateParams& up,
+                          BlockStats* partial, DeviceScalars* sc, int lanes_per_row, hipStream_t stream);
+hipError_t launch_commit(float2* y, const DeviceScalars* sc, int n, hipStream_t stream);
+
+// ---- exact O(n^2) terms (gradient check and KL) ----------------------------
+hipError_t launch_exact_repulsion(const float2* y, int n, float2* rep, double* z_partial, DeviceScalars* sc,
+                                  hipStream_t stream);
+hipError_t launch_exact_z_double(const float2* y, int n, double* z_partial, hipStream_t stream);
+int exact_blocks_for(int n);
+hipError_t launch_kl_rows(const Csr& p, const float2* y, double sum_q, double* partial, int blocks,
+                          hipStream_t stream);
+
+}  // namespace fehip

@@ -1,0 +1,185 @@
+/*
+ * fastembedr_hip.h -- C ABI of the MI355X (gfx950) openTSNE-style t-SNE backend.
+ *
+ * Plain pointers and sizes only.  Every entry point returns 0 on success and
+ * 1 on failure (the reference's convention); the failure message is then
+ * available from fastembedr_hip_embedding_last_error() on the same thread.
+ *
+ * Layouts (identical to the reference's CUDA ABI):
+ *   indices, distances : n x k, column-major (element (i, j) at j * n + i),
+ *                        R matrix order; index_offset is 0 or 1.
+ *   init, out, y       : n x 2 row-major interleaved (x0, y0, x1, y1, ...).
+ *
+ * Numerics follow the reference's CPU backend (src/tsne_neighbors.cpp):
+ * fp32 perplexity search, symmetric CSR P normalised by the total directed
+ * mass, the bilinear FFT grid with the CPU grid-size policy (honouring
+ * FASTEMBEDR_TSNE_FFT_GRID), the sign(0) == 0 gains rule and per-iteration
+ * centring.  Differences from that backend are limited to fp32 summation
+ * order (parallel reductions and float atomics).
+ */
+#ifndef FASTEMBEDR_HIP_H
+#define FASTEMBEDR_HIP_H
+
+#include <stdbool.h>
+
+#if defined(__GNUC__)
+#define FASTEMBEDR_HIP_API __attribute__((visibility("default")))
+#else
+#define FASTEMBEDR_HIP_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Replaces fastembedr_cuda_embedding_last_error()
+ * (src/embedding_cuda_kernels.cpp:3753-3755). */
+FASTEMBEDR_HIP_API const char* fastembedr_hip_embedding_last_error(void);
+
+/* Replaces fastembedr_cuda_available() (src/embedding_cuda_kernels.cpp:3757-3765):
+ * true when a HIP device is present and it is a gfx950 part. */
+FASTEMBEDR_HIP_API bool fastembedr_hip_available(void);
+
+/* Replaces fastembedr_cuda_opentsne_fft_from_knn_float
+ * (src/embedding_cuda_kernels.cpp:6039-6066; declared in
+ * src/embedding_cuda_impl.cpp:79-183).  Same 21 parameters, same meaning:
+ * host KNN (float32 distances), optional host init (has_init != 0), two-phase
+ * optimisation, final layout copied to host `out`.  has_init == 0 draws the
+ * reference CPU backend's initialisation: mt19937(seed) feeding
+ * normal_distribution<float>(0, 1e-4) (src/tsne_neighbors.cpp:1693-1700).
+ * learning_rate_auto != 0 uses n / exaggeration per phase.  max_step_norm
+ * that is not finite or <= 0 disables the per-point step clip. */
+FASTEMBEDR_HIP_API int fastembedr_hip_opentsne_fft_from_knn_float(
+    const int* indices, const float* distances, const float* init, int has_init,
+    int n, int k, int n_components, float perplexity,
+    int early_exaggeration_iter, int n_iter,
+    float early_exaggeration, float exaggeration,
+    float learning_rate, int learning_rate_auto,
+    float initial_momentum, float final_momentum,
+    float min_gain, float max_step_norm,
+    unsigned int seed, int index_offset, float* out);
+
+/* Replaces fastembedr_cuda_opentsne_fft_from_knn (double distances)
+ * (src/embedding_cuda_kernels.cpp:6010-6037).  Distances are narrowed to fp32
+ * on the device, as the reference CPU path narrows them on copy
+ * (src/tsne_neighbors.cpp:342-350). */
+FASTEMBEDR_HIP_API int fastembedr_hip_opentsne_fft_from_knn(
+    const int* indices, const double* distances, const float* init, int has_init,
+    int n, int k, int n_components, float perplexity,
+    int early_exaggeration_iter, int n_iter,
+    float early_exaggeration, float exaggeration,
+    float learning_rate, int learning_rate_auto,
+    float initial_momentum, float final_momentum,
+    float min_gain, float max_step_norm,
+    unsigned int seed, int index_offset, float* out);
+
+/* Replaces fastembedr_cuda_opentsne_fft_from_device_knn_float
+ * (src/embedding_cuda_kernels.cpp:6068-6094): indices and distances are
+ * device pointers (borrowed, column-major n x k); init and out stay on the
+ * host, as in the reference. */
+FASTEMBEDR_HIP_API int fastembedr_hip_opentsne_fft_from_device_knn_float(
+    const int* indices, const float* distances, const float* init, int has_init,
+    int n, int k, int n_components, float perplexity,
+    int early_exaggeration_iter, int n_iter,
+    float early_exaggeration, float exaggeration,
+    float learning_rate, int learning_rate_auto,
+    float initial_momentum, float final_momentum,
+    float min_gain, float max_step_norm,
+    unsigned int seed, int index_offset, float* out);
+
+/* ------------------------------------------------------------------------
+ * Session ABI.  No counterpart in the reference: the reference exposes only
+ * the one-shot calls above.  These entry points split the same work into
+ * P construction, per-iteration steps and state transfer so that parity can
+ * be checked per stage (P, one gradient, one update) and throughput can be
+ * timed with inputs already resident in HBM.  The one-shot calls above are
+ * implemented on top of them.
+ * ---------------------------------------------------------------------- */
+typedef struct fastembedr_hip_tsne fastembedr_hip_tsne;
+
+/* Repulsion modes. */
+#define FASTEMBEDR_HIP_REPULSION_GRID 0     /* bilinear FFT grid (reference) */
+#define FASTEMBEDR_HIP_REPULSION_EXACT 1    /* O(n^2) pairwise (checking only) */
+#define FASTEMBEDR_HIP_REPULSION_LAGRANGE 2 /* FIt-SNE order-p Lagrange grid */
+
+/* Builds P on the device from KNN (host or device pointers, column-major).
+ * grid_size == 0 selects the reference CPU policy (64/128/256 by n,
+ * FASTEMBEDR_TSNE_FFT_GRID override, clamped to [32, 512]); an explicit grid
+ * size is rounded up to a power of two in [32, 1024].  1 <= k <= 256. */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_create(const int* indices, const float* distances,
+                               int n, int k, float perplexity, int index_offset,
+                               int inputs_on_device, int grid_size,
+                               fastembedr_hip_tsne** out_session);
+
+FASTEMBEDR_HIP_API void fastembedr_hip_tsne_destroy(fastembedr_hip_tsne* session);
+
+/* Number of stored entries of the symmetric CSR P (both triangles). */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_p_nnz(const fastembedr_hip_tsne* session, long long* nnz);
+
+/* Copies P to host arrays of sizes n + 1, nnz, nnz. */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_copy_p(const fastembedr_hip_tsne* session,
+                               int* row_ptr, int* col, float* val);
+
+/* Conditional p_{j|i} from the perplexity search, column-major n x k (host). */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_copy_conditional_p(const fastembedr_hip_tsne* session,
+                                           float* p_cond);
+
+/* Grid nodes per axis used by the bilinear repulsion. */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_grid_size(const fastembedr_hip_tsne* session, int* grid_size);
+
+/* Sets the optimiser state from host arrays (n x 2 each).  update and gains
+ * may be NULL: they are then reset to 0 and 1 (the reference's start state). */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_set_state(fastembedr_hip_tsne* session, const float* y,
+                                  const float* update, const float* gains);
+
+/* Copies the optimiser state to host arrays; any pointer may be NULL. */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_get_state(fastembedr_hip_tsne* session, float* y,
+                                  float* update, float* gains);
+
+/* Gradient at the current y without changing the state (no centring):
+ * the reference's compute_gradient_fft_grid_f (src/tsne_neighbors.cpp:1076-1182)
+ * or, for REPULSION_EXACT, compute_gradient_pair_symmetric_f (:1014-1074). */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* session, float exaggeration,
+                                 int repulsion, float* grad_out);
+
+/* Centres y (the reference's zero_mean_f, src/tsne_neighbors.cpp:1200-1211). */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_center(fastembedr_hip_tsne* session);
+
+/* Runs n_iter iterations of gradient + update + centring with fixed phase
+ * parameters (src/tsne_neighbors.cpp:1749-1802).  Asynchronous with respect
+ * to the host; fastembedr_hip_tsne_sync() waits. */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_run(fastembedr_hip_tsne* session, int n_iter,
+                            float exaggeration, float momentum, float learning_rate,
+                            float min_gain, float max_step_norm);
+
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_sync(fastembedr_hip_tsne* session);
+
+/* Exact KL(P || Q) at the current y (src/tsne_neighbors.cpp:1258-1285), with
+ * the O(n^2) normalisation computed on the device in fp64. */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* session, double* kl);
+
+/* Per-kernel timing.  While enabled, run() records HIP events around every
+ * kernel on the session's stream; stats returns, per kernel id, the number
+ * of launches timed and their summed duration in milliseconds.  Kernel ids
+ * and names: fastembedr_hip_tsne_kernel_name(). */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_set_timing(fastembedr_hip_tsne* session, int enabled);
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_timing_stats(fastembedr_hip_tsne* session, int max_kernels,
+                                     long long* launches, double* total_ms);
+FASTEMBEDR_HIP_API const char* fastembedr_hip_tsne_kernel_name(int kernel_id);
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kernel_count(void);
+
+/* Host-side helper with no ABI counterpart in the reference: writes the
+ * initialisation that the one-shot calls use when has_init == 0, i.e. the
+ * reference CPU driver's mt19937(seed) + normal_distribution<float>(0, 1e-4)
+ * draw (src/tsne_neighbors.cpp:1693-1700), n x 2 row-major, so that session
+ * users start from the same layout. */
+FASTEMBEDR_HIP_API int fastembedr_hip_random_init(int n, unsigned int seed, float* out);
+
+/* Wall time of the P construction in milliseconds (device events). */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_p_build_ms(const fastembedr_hip_tsne* session, double* ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTEMBEDR_HIP_H */

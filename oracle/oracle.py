@@ -1,0 +1,188 @@
+"""ctypes view of the CPU oracle (oracle/tsne_oracle.cpp).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker.  The product path never loads it.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "_build" / "libtsne_oracle.so"
+
+METHOD_GRID = 0
+METHOD_EXACT = 1
+METHOD_LAGRANGE = 2
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB.exists():
+        build()
+    lib = C.CDLL(str(LIB))
+    P, I, F, D = C.c_void_p, C.c_int, C.c_float, C.c_double
+    sig = {
+        "tsne_oracle_last_error": (C.c_char_p, []),
+        "tsne_oracle_policy_grid_size": (I, [I]),
+        "tsne_oracle_conditional_p": (I, [P, I, I, D, P, P, P]),
+        "tsne_oracle_build_p": (P, [P, P, I, I, D, I]),
+        "tsne_oracle_wrap_p": (P, [P, P, P, I]),
+        "tsne_oracle_p_nnz": (C.c_longlong, [P]),
+        "tsne_oracle_p_copy": (None, [P, P, P, P]),
+        "tsne_oracle_p_free": (None, [P]),
+        "tsne_oracle_gradient": (I, [P, P, I, F, I, I, I, I, I, P]),
+        "tsne_oracle_grid_fields": (I, [P, P, I, I, I, P, P]),
+        "tsne_oracle_update": (None, [P, P, P, P, I, F, F, F, F, I]),
+        "tsne_oracle_zero_mean": (None, [P, I]),
+        "tsne_oracle_kl": (D, [P, P, I, I, P]),
+        "tsne_oracle_optimize": (I, [P, P, I, I, I, D, D, D, I, D, D, D, D, I, I, I, I, P, P]),
+        "tsne_oracle_random_init": (None, [P, I, C.c_uint]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _p(a):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+def _err() -> str:
+    return load().tsne_oracle_last_error().decode()
+
+
+def policy_grid_size(n: int) -> int:
+    return int(load().tsne_oracle_policy_grid_size(n))
+
+
+def conditional_p(distances: np.ndarray, perplexity: float):
+    """Row search only: (p (n, k) float32, beta (n,), steps (n,))."""
+    d = np.asfortranarray(distances, dtype=np.float32)
+    n, k = d.shape
+    p = np.empty((n, k), np.float32, order="F")
+    beta = np.empty(n, np.float32)
+    steps = np.empty(n, np.int32)
+    load().tsne_oracle_conditional_p(_p(d), n, k, float(perplexity), _p(p), _p(beta), _p(steps))
+    return p, beta, steps
+
+
+class OracleP:
+    """Symmetric CSR P built (or wrapped) on the CPU."""
+
+    def __init__(self, handle, n: int):
+        self.h = C.c_void_p(handle)
+        self.n = n
+
+    @classmethod
+    def build(cls, indices: np.ndarray, distances: np.ndarray, perplexity: float, threads: int = 1) -> "OracleP":
+        idx = np.asfortranarray(indices, dtype=np.int32)
+        dist = np.asfortranarray(distances, dtype=np.float32)
+        n, k = idx.shape
+        h = load().tsne_oracle_build_p(_p(idx), _p(dist), n, k, float(perplexity), int(threads))
+        if not h:
+            raise ValueError(_err())
+        return cls(h, n)
+
+    @classmethod
+    def wrap(cls, row_ptr, col, val) -> "OracleP":
+        rp = np.ascontiguousarray(row_ptr, np.int32)
+        cc = np.ascontiguousarray(col, np.int32)
+        vv = np.ascontiguousarray(val, np.float32)
+        n = rp.size - 1
+        return cls(load().tsne_oracle_wrap_p(_p(rp), _p(cc), _p(vv), n), n)
+
+    def __del__(self):
+        try:
+            if self.h:
+                load().tsne_oracle_p_free(self.h)
+                self.h = C.c_void_p()
+        except Exception:
+            pass
+
+    @property
+    def nnz(self) -> int:
+        return int(load().tsne_oracle_p_nnz(self.h))
+
+    def csr(self):
+        nnz = self.nnz
+        rp = np.empty(self.n + 1, np.int32)
+        col = np.empty(nnz, np.int32)
+        val = np.empty(nnz, np.float32)
+        load().tsne_oracle_p_copy(self.h, _p(rp), _p(col), _p(val))
+        return rp, col, val
+
+    def gradient(self, y: np.ndarray, exaggeration: float = 1.0, method: int = METHOD_GRID, grid_size: int = 0,
+                 threads: int = 1, lagrange_order: int = 3, min_intervals: int = 50) -> np.ndarray:
+        y = np.ascontiguousarray(y, np.float32).reshape(self.n, 2)
+        g = np.empty((self.n, 2), np.float32)
+        rc = load().tsne_oracle_gradient(self.h, _p(y), self.n, float(exaggeration), int(method), int(grid_size),
+                                         int(lagrange_order), int(min_intervals), int(threads), _p(g))
+        if rc != 0:
+            raise ValueError(_err())
+        return g
+
+    def grid_fields(self, y: np.ndarray, grid_size: int = 0, threads: int = 1):
+        """(geometry (lo_x, lo_y, h, 1/h), fields (4, g, g): q, q2, xq2, yq2)."""
+        y = np.ascontiguousarray(y, np.float32).reshape(self.n, 2)
+        geom = np.empty(4, np.float32)
+        g = int(load().tsne_oracle_grid_fields(self.h, _p(y), self.n, int(grid_size), int(threads), _p(geom), None))
+        fields = np.empty((4, g, g), np.float32)
+        load().tsne_oracle_grid_fields(self.h, _p(y), self.n, int(grid_size), int(threads), _p(geom), _p(fields))
+        return geom, fields
+
+    def kl(self, y: np.ndarray, threads: int = 1, row_costs: bool = False):
+        y = np.ascontiguousarray(y, np.float32).reshape(self.n, 2)
+        rc = np.empty(self.n, np.float64) if row_costs else None
+        v = float(load().tsne_oracle_kl(self.h, _p(y), self.n, int(threads), _p(rc)))
+        return (v, rc) if row_costs else v
+
+    def optimize(self, y0: np.ndarray, early_iter: int, n_iter: int, early_ex: float, ex: float,
+                 learning_rate: float, learning_rate_auto: bool, m0: float, m1: float, min_gain: float = 0.01,
+                 max_step_norm: float = 5.0, method: int = METHOD_GRID, grid_size: int = 0, threads: int = 1,
+                 record_costs: bool = False):
+        y = np.array(y0, dtype=np.float32, copy=True).reshape(self.n, 2)
+        total = early_iter + n_iter
+        cap = max(1, -(-total // 50))
+        costs = np.zeros(cap, np.float64)
+        its = np.zeros(cap, np.int32)
+        rec = load().tsne_oracle_optimize(self.h, _p(y), self.n, int(early_iter), int(n_iter), float(early_ex),
+                                          float(ex), float(learning_rate), int(bool(learning_rate_auto)), float(m0),
+                                          float(m1), float(min_gain), float(max_step_norm), int(method),
+                                          int(grid_size), int(threads), int(bool(record_costs)), _p(costs), _p(its))
+        if rec < 0:
+            raise ValueError(_err())
+        return y, costs[:rec], its[:rec]
+
+
+def update(y, upd, gains, grad, lr, momentum, min_gain=0.01, max_step_norm=5.0, threads=1):
+    """In-place update of float32 arrays (n, 2)."""
+    n = y.shape[0]
+    load().tsne_oracle_update(_p(y), _p(upd), _p(gains), _p(grad), n, float(lr), float(momentum), float(min_gain),
+                              float(max_step_norm), int(threads))
+
+
+def zero_mean(y):
+    load().tsne_oracle_zero_mean(_p(y), y.shape[0])
+
+
+def random_init(n: int, seed: int) -> np.ndarray:
+    y = np.empty((n, 2), np.float32)
+    load().tsne_oracle_random_init(_p(y), n, int(seed) & 0xFFFFFFFF)
+    return y

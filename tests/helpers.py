@@ -1,0 +1,67 @@
+"""Shared numpy restatements and fixtures for the tests (closed forms used to
+pin the oracle, and small seeded KNN problems)."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from fastembedr_amd import synthetic
+
+
+def small_problem(n=600, dim=8, k=24, components=4, seed=3, one_based=True):
+    spec = synthetic.MixtureSpec(n=n, dim=dim, components=components, mean_sd=4.0)
+    x, labels = synthetic.gaussian_mixture(spec, seed=seed)
+    idx, dist = synthetic.exact_knn_numpy(x, k)
+    idx_r, dist_r = synthetic.to_r_layout(idx, dist, one_based=one_based)
+    return x, labels, idx_r, dist_r
+
+
+def csr_to_dense(row_ptr, col, val, n):
+    m = np.zeros((n, n), np.float64)
+    for i in range(n):
+        s, e = row_ptr[i], row_ptr[i + 1]
+        m[i, col[s:e]] += val[s:e]
+    return m
+
+
+def exact_gradient_numpy(y, p_dense, ex):
+    """openTSNE-convention gradient: ex * sum_j p_ij q_ij (yi - yj) - sum_j q_ij^2 (yi - yj) / Z."""
+    y = y.astype(np.float64)
+    d = y[:, None, :] - y[None, :, :]
+    r2 = (d * d).sum(-1)
+    q = 1.0 / (1.0 + r2)
+    np.fill_diagonal(q, 0.0)
+    z = q.sum()
+    rep = -((q * q)[:, :, None] * d).sum(1) / z
+    att = ex * ((p_dense * q)[:, :, None] * d).sum(1)
+    return rep + att
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def knn_preservation(x_high, y_low, k=15, sample=2000, seed=4):
+    """Share of each sampled point's k nearest low-dimensional neighbours that
+    are among its k nearest high-dimensional ones, within the sample; ties
+    broken by index (src/embedding_utils.cpp:1582-1752, knn_preservation)."""
+    n = x_high.shape[0]
+    rng = np.random.default_rng(seed)
+    keep = np.sort(rng.choice(n, size=min(sample, n), replace=False))
+    xh = x_high[keep].astype(np.float64)
+    yl = y_low[keep].astype(np.float64)
+    m = keep.size
+
+    def ranks(z):
+        sq = (z * z).sum(1)
+        d = sq[:, None] + sq[None, :] - 2 * z @ z.T
+        np.fill_diagonal(d, np.inf)
+        order = np.lexsort((np.broadcast_to(np.arange(m), (m, m)), d), axis=1)
+        return order
+
+    oh = ranks(xh)[:, :k]
+    ol = ranks(yl)[:, :k]
+    shared = sum(len(np.intersect1d(oh[i], ol[i], assume_unique=True)) for i in range(m))
+    return shared / (m * k)

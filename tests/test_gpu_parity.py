@@ -1,0 +1,262 @@
+"""HIP backend vs the CPU oracle on identical seeded inputs (through the C ABI).
+
+Tolerances:
+  P (conditional and symmetric)   relative L2 error <= 1e-5, identical sparsity
+  gradient from the same y        relative L2 error <= 1e-3 (float atomics and
+                                  parallel sums reorder fp32 additions)
+  final KL divergence             within 1 % of the oracle's
+  15-NN preservation              within 0.01 of the oracle's
+"""
+
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+from fastembedr_amd import _lib, synthetic
+from tests.helpers import knn_preservation, rel_l2, small_problem
+
+pytestmark = pytest.mark.gpu
+
+P_TOL = 1e-5
+GRAD_TOL = 1e-3
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def mid_problem():
+    x, labels, idx, dist = small_problem(n=3000, dim=20, k=45, components=6, seed=21)
+    return x, idx, dist
+
+
+@pytest.fixture(scope="module")
+def config0():
+    spec = synthetic.CONFIGS[0]
+    x, labels = synthetic.gaussian_mixture(spec, seed=1)
+    idx, dist = synthetic.exact_knn_numpy(x, 90)
+    idx_r, dist_r = synthetic.to_r_layout(idx, dist, one_based=True)
+    return x, idx_r, dist_r, synthetic.pca_init(x)
+
+
+def test_conditional_p_matches_oracle(hip, oracle_mod, mid_problem):
+    _say("case: conditional P, n=3000 k=45 perplexity=15")
+    x, idx, dist = mid_problem
+    with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+        pc = s.conditional_p()
+    ref, _, steps = oracle_mod.conditional_p(dist, 15.0)
+    assert rel_l2(pc, ref) <= P_TOL
+    same = np.mean(pc == ref)
+    _say(f"bit-identical conditional entries: {same:.4f}")
+    assert same > 0.5
+
+
+@pytest.mark.parametrize("n,k,perp", [(3000, 45, 15.0), (10000, 90, 30.0)])
+def test_symmetric_p_matches_oracle(hip, oracle_mod, n, k, perp):
+    _say(f"case: symmetric P n={n} k={k}")
+    x, _, idx, dist = small_problem(n=n, dim=30, k=k, components=8, seed=n)
+    with hip.TsneSession(idx, dist, perplexity=perp, index_offset=1) as s:
+        rp, col, val = s.csr()
+        build_ms = s.p_build_ms
+    _say(f"P build {build_ms:.2f} ms, nnz {col.size}")
+    P = oracle_mod.OracleP.build(idx, dist, perp, threads=4)
+    rp0, col0, val0 = P.csr()
+    np.testing.assert_array_equal(rp, rp0)
+    np.testing.assert_array_equal(col, col0)
+    assert rel_l2(val, val0) <= P_TOL
+    assert abs(float(val.astype(np.float64).sum()) - 1.0) < 1e-5
+
+
+def test_p_with_self_columns_and_zero_based(hip, oracle_mod):
+    _say("case: P with a self column, 0-based indices")
+    x, _, idx, dist = small_problem(n=800, k=20, one_based=False)
+    idx2 = np.asfortranarray(np.concatenate([np.arange(800)[:, None], idx[:, :-1]], axis=1).astype(np.int32))
+    dist2 = np.asfortranarray(np.concatenate([np.zeros((800, 1), np.float32), dist[:, :-1]], axis=1))
+    with hip.TsneSession(idx2, dist2, perplexity=5.0, index_offset=0) as s:
+        rp, col, val = s.csr()
+    P = oracle_mod.OracleP.build(idx2, dist2, 5.0)
+    rp0, col0, val0 = P.csr()
+    np.testing.assert_array_equal(rp, rp0)
+    np.testing.assert_array_equal(col, col0)
+    assert rel_l2(val, val0) <= P_TOL
+
+
+def test_p_single_neighbor_and_duplicates(hip, oracle_mod):
+    _say("case: P with k=1 and with a duplicated neighbour")
+    x, _, idx, dist = small_problem(n=300, k=6)
+    for i2, d2, perp in ((idx[:, :1], dist[:, :1], 0.5), (idx, dist, 1.5)):
+        i2 = np.asfortranarray(i2.copy())
+        d2 = np.asfortranarray(d2.copy())
+        if i2.shape[1] > 1:
+            i2[::5, 1] = i2[::5, 0]
+            d2[::5, 1] = d2[::5, 0]
+        with hip.TsneSession(i2, d2, perplexity=perp, index_offset=1) as s:
+            rp, col, val = s.csr()
+        rp0, col0, val0 = oracle_mod.OracleP.build(i2, d2, perp).csr()
+        np.testing.assert_array_equal(col, col0)
+        assert rel_l2(val, val0) <= P_TOL
+
+
+def test_p_input_errors(hip):
+    _say("case: P input validation")
+    x, _, idx, dist = small_problem(n=200, k=8)
+    bad = idx.copy()
+    bad[7, 3] = 10_000
+    with pytest.raises(_lib.HipBackendError, match="out of range"):
+        hip.TsneSession(bad, dist, perplexity=2.0, index_offset=1)
+    badd = dist.copy()
+    badd[9, 1] = np.nan
+    with pytest.raises(_lib.HipBackendError, match="finite and non-negative"):
+        hip.TsneSession(idx, badd, perplexity=2.0, index_offset=1)
+    with pytest.raises(_lib.HipBackendError, match="at most 256"):
+        hip.TsneSession(np.ones((300, 257), np.int32), np.ones((300, 257), np.float32), perplexity=2.0)
+
+
+@pytest.mark.parametrize("grid", [0, 32, 128, 512, 1024])
+def test_gradient_matches_oracle(hip, oracle_mod, mid_problem, grid):
+    _say(f"case: gradient grid={grid}")
+    x, idx, dist = mid_problem
+    rng = np.random.default_rng(grid + 1)
+    with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1, grid_size=grid) as s:
+        P = oracle_mod.OracleP.wrap(*s.csr())
+        for scale, ex in ((1e-4, 12.0), (2.0, 12.0), (25.0, 1.0)):
+            y = (rng.standard_normal((3000, 2)) * scale).astype(np.float32)
+            s.set_state(y)
+            g = s.gradient(ex)
+            ref = P.gradient(y, ex, grid_size=grid if grid else 0, threads=4)
+            err = rel_l2(g, ref)
+            _say(f"  scale={scale} ex={ex} relL2={err:.2e}")
+            assert err <= GRAD_TOL
+
+
+def test_exact_gradient_matches_oracle(hip, oracle_mod, mid_problem):
+    _say("case: exact gradient")
+    x, idx, dist = mid_problem
+    rng = np.random.default_rng(3)
+    y = (rng.standard_normal((3000, 2)) * 5).astype(np.float32)
+    with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+        P = oracle_mod.OracleP.wrap(*s.csr())
+        s.set_state(y)
+        g = s.gradient(4.0, repulsion=_lib.REPULSION_EXACT)
+    ref = P.gradient(y, 4.0, method=oracle_mod.METHOD_EXACT, threads=4)
+    assert rel_l2(g, ref) <= 1e-5
+
+
+def test_iterations_track_oracle(hip, oracle_mod, mid_problem):
+    """One and then ten full iterations (gradient, update, centring) from the
+    same state; the trajectories agree to the gradient tolerance."""
+    _say("case: iterations vs oracle")
+    x, idx, dist = mid_problem
+    y0 = synthetic.pca_init(x)
+    with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+        P = oracle_mod.OracleP.wrap(*s.csr())
+        s.set_state(y0)
+        s.center()
+        s.run(1, 12.0, 0.5, 3000 / 12.0, 0.01, 5.0)
+        y1, u1, g1 = s.get_state()
+        y_ref = y0.copy()
+        oracle_mod.zero_mean(y_ref)
+        upd = np.zeros_like(y_ref)
+        gains = np.ones_like(y_ref)
+        grad = P.gradient(y_ref, 12.0, threads=4)
+        oracle_mod.update(y_ref, upd, gains, grad, 3000 / 12.0, 0.5)
+        oracle_mod.zero_mean(y_ref)
+        assert rel_l2(y1, y_ref) <= 1e-4
+        np.testing.assert_array_equal(g1, gains)
+        s.run(9, 12.0, 0.5, 3000 / 12.0, 0.01, 5.0)
+        y10 = s.y
+    yo, _, _ = P.optimize(y0, 10, 0, 12.0, 1.0, 3000 / 12.0, False, 0.5, 0.8, threads=4)
+    err = rel_l2(y10, yo)
+    _say(f"  10 iterations relL2={err:.2e}")
+    assert err <= GRAD_TOL
+
+
+def test_kl_matches_oracle(hip, oracle_mod, mid_problem):
+    _say("case: exact KL on the device")
+    x, idx, dist = mid_problem
+    rng = np.random.default_rng(12)
+    y = (rng.standard_normal((3000, 2)) * 3).astype(np.float32)
+    with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+        s.set_state(y)
+        kl = s.kl()
+        P = oracle_mod.OracleP.wrap(*s.csr())
+    ref = P.kl(y, threads=4)
+    assert abs(kl - ref) <= 1e-6 * abs(ref)
+
+
+def _one_shot(fn_name, idx, dist, init, n_early, n_norm, device=False):
+    lib = _lib.load()
+    n, k = idx.shape
+    out = np.empty((n, 2), np.float32)
+    fn = getattr(lib, fn_name)
+    rc = fn(C.c_void_p(idx) if device else C.c_void_p(idx.ctypes.data),
+            C.c_void_p(dist) if device else C.c_void_p(dist.ctypes.data),
+            C.c_void_p(init.ctypes.data) if init is not None else None, int(init is not None), n, k, 2, 30.0,
+            n_early, n_norm, 12.0, 1.0, n / 12.0, 0, 0.5, 0.8, 0.01, 5.0, 1, 1, C.c_void_p(out.ctypes.data))
+    _lib.check(rc, fn_name)
+    return out
+
+
+def test_end_to_end_config0_kl_and_knn_preservation(hip, oracle_mod, config0):
+    """Config 0 (10,000 x 50, k=90, perplexity 30, 250 + 500 iterations),
+    one-shot C ABI vs the oracle's full run from the same PCA init."""
+    x, idx, dist, y0 = config0
+    n = x.shape[0]
+    _say("case: config 0 end to end (one-shot ABI)")
+    y_hip = _one_shot("fastembedr_hip_opentsne_fft_from_knn_float", idx, dist, y0, 250, 500)
+    P = oracle_mod.OracleP.build(idx, dist, 30.0, threads=8)
+    y_cpu, _, _ = P.optimize(y0, 250, 500, 12.0, 1.0, n / 12.0, False, 0.5, 0.8, threads=8)
+    kl_hip = P.kl(y_hip, threads=8)
+    kl_cpu = P.kl(y_cpu, threads=8)
+    pres_hip = knn_preservation(x, y_hip, 15)
+    pres_cpu = knn_preservation(x, y_cpu, 15)
+    _say(f"  KL hip={kl_hip:.5f} cpu={kl_cpu:.5f}; 15-NN hip={pres_hip:.4f} cpu={pres_cpu:.4f}")
+    assert np.all(np.isfinite(y_hip))
+    assert abs(kl_hip - kl_cpu) <= 0.01 * kl_cpu
+    assert abs(pres_hip - pres_cpu) <= 0.01
+
+
+def test_one_shot_variants_agree(hip, mid_problem):
+    """double-distance and device-KNN entry points give the float entry's result."""
+    import torch
+
+    _say("case: one-shot variants")
+    x, idx, dist = mid_problem
+    y0 = synthetic.pca_init(x)
+    a = _one_shot("fastembedr_hip_opentsne_fft_from_knn_float", idx, dist, y0, 20, 20)
+    b = _one_shot("fastembedr_hip_opentsne_fft_from_knn", idx, np.asfortranarray(dist, np.float64), y0, 20, 20)
+    ti = torch.as_tensor(np.ascontiguousarray(idx.T)).cuda()  # (k, n) row-major == (n, k) column-major
+    td = torch.as_tensor(np.ascontiguousarray(dist.T)).cuda()
+    c = _one_shot("fastembedr_hip_opentsne_fft_from_device_knn_float", ti.data_ptr(), td.data_ptr(), y0, 20, 20,
+                  device=True)
+    torch.cuda.synchronize()
+    assert rel_l2(b, a) <= GRAD_TOL
+    assert rel_l2(c, a) <= GRAD_TOL
+
+
+def test_random_init_matches_reference_generator(hip, oracle_mod):
+    lib = _lib.load()
+    y = np.empty((1000, 2), np.float32)
+    _lib.check(lib.fastembedr_hip_random_init(1000, 42, C.c_void_p(y.ctypes.data)), "random_init")
+    np.testing.assert_array_equal(y, oracle_mod.random_init(1000, 42))
+
+
+def test_opentsne_knn_api(hip):
+    _say("case: opentsne_knn API mirror")
+    x, _, idx, dist = small_problem(n=1200, k=40, seed=8)
+    res = hip.opentsne_knn(idx, dist, n_neighbors=30, perplexity=10.0, early_exaggeration_iter=30, n_iter=40,
+                           seed=3)
+    assert res.layout.shape == (1200, 2) and np.all(np.isfinite(res.layout))
+    assert res.config["backend"] == "hip"
+    assert res.config["optimizer"] == "opentsne_fitsne_fft_grid_native_hip"
+    assert res.config["repulsion"] == "fft_grid_hip"
+    assert res.config["learning_rate"] == "auto_opt_sne_n_over_early_exaggeration"
+    assert res.config["learning_rate_early"] == res.config["learning_rate_normal"] == 1200 / 12.0
+    rec = hip.opentsne_knn({"indices": idx, "distances": dist}, n_neighbors=30, perplexity=10.0,
+                           early_exaggeration_iter=30, n_iter=40, seed=3, record_costs=True)
+    assert list(rec.itercost_iterations) == [50, 70]
+    assert np.all(np.isfinite(rec.itercosts))
