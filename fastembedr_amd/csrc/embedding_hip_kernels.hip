@@ -30,6 +30,7 @@
 #include <rocprim/device/device_scan.hpp>
 
 #include <cfloat>
+#include <algorithm>
 #include <cmath>
 
 #include "tsne_device.h"
@@ -385,38 +386,201 @@ __device__ __forceinline__ Bilinear locate(float px, float py, const DeviceScala
   return b;
 }
 
-__global__ __launch_bounds__(kPointThreads) void k_spread(const float2* __restrict__ y_stored,
-                                                          float2* __restrict__ y_cur, const DeviceScalars* sc,
-                                                          float* __restrict__ mass, float* __restrict__ mass_x,
-                                                          float* __restrict__ mass_y, int n, int g) {
+// ---------------------------------------------------------------------------
+// Tile-binned spreading.  Points are counted per tile of kTile x kTile cells
+// (LDS histogram, one global atomic per block and tile), the counts are
+// scanned into tile ranges and work items of at most kChunk points, points
+// are scattered into tile order (LDS ranks, one global atomic per batch and
+// tile), and each work item accumulates its points' bilinear charges into a
+// (kTile + 1)^2 node window in LDS before adding the window to the grid.  A
+// wave whose points all lie in one cell (collapsed clusters) first reduces
+// its 12 charges across lanes, so LDS atomics never serialise 64-deep there.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int tile_of(const Bilinear& b, int ta) { return (b.y0 / kTile) * ta + b.x0 / kTile; }
+
+__global__ __launch_bounds__(kPointThreads) void k_bin_count(const float2* __restrict__ y_stored,
+                                                             float2* __restrict__ y_cur, const DeviceScalars* sc,
+                                                             int* __restrict__ tile_count, int n, int g, int ta) {
 #pragma clang fp contract(off)
+  __shared__ int hist[kMaxTiles];
+  const int tiles = ta * ta;
+  for (int t = threadIdx.x; t < tiles; t += kPointThreads) hist[t] = 0;
+  __syncthreads();
   const DeviceScalars s = *sc;
   for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += gridDim.x * kPointThreads) {
     const float2 r = y_stored[i];
     const float px = r.x - s.shift_x;
     const float py = r.y - s.shift_y;
     y_cur[i] = make_float2(px, py);
-    const Bilinear b = locate(px, py, s, g);
-    const float w00 = (1.0f - b.tx) * (1.0f - b.ty);
-    const float w10 = b.tx * (1.0f - b.ty);
-    const float w01 = (1.0f - b.tx) * b.ty;
-    const float w11 = b.tx * b.ty;
-    const int a00 = b.y0 * g + b.x0;
-    const int a10 = a00 + 1;
-    const int a01 = a00 + g;
-    const int a11 = a01 + 1;
-    atomicAdd(mass + a00, w00);
-    atomicAdd(mass + a10, w10);
-    atomicAdd(mass + a01, w01);
-    atomicAdd(mass + a11, w11);
-    atomicAdd(mass_x + a00, w00 * px);
-    atomicAdd(mass_x + a10, w10 * px);
-    atomicAdd(mass_x + a01, w01 * px);
-    atomicAdd(mass_x + a11, w11 * px);
-    atomicAdd(mass_y + a00, w00 * py);
-    atomicAdd(mass_y + a10, w10 * py);
-    atomicAdd(mass_y + a01, w01 * py);
-    atomicAdd(mass_y + a11, w11 * py);
+    atomicAdd(&hist[tile_of(locate(px, py, s, g), ta)], 1);
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < tiles; t += kPointThreads) {
+    if (hist[t] != 0) atomicAdd(tile_count + t, hist[t]);
+  }
+}
+
+// Exclusive scan of up to kMaxTiles counts by one block of 1024 threads
+// (four entries per thread, then a Hillis-Steele scan of the thread sums).
+__device__ int block_exclusive_scan4(int (&v)[4], int* part) {
+  const int t = threadIdx.x;
+  int s = v[0] + v[1] + v[2] + v[3];
+  part[t] = s;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int add = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += add;
+    __syncthreads();
+  }
+  const int total = part[1023];
+  int run = part[t] - s;
+  for (int q = 0; q < 4; ++q) {
+    const int c = v[q];
+    v[q] = run;
+    run += c;
+  }
+  __syncthreads();
+  return total;
+}
+
+__global__ __launch_bounds__(1024) void k_bin_plan(int* __restrict__ tile_count, int* __restrict__ tile_cursor,
+                                                   int4* __restrict__ items, DeviceScalars* sc, int tiles) {
+  __shared__ int part[1024];
+  int cnt[4], start[4], chunks[4], base[4];
+  for (int q = 0; q < 4; ++q) {
+    const int t = threadIdx.x * 4 + q;
+    cnt[q] = t < tiles ? tile_count[t] : 0;
+    if (t < tiles) tile_count[t] = 0;  // ready for the next iteration's count
+    start[q] = cnt[q];
+    chunks[q] = (cnt[q] + kChunk - 1) / kChunk;
+    base[q] = chunks[q];
+  }
+  block_exclusive_scan4(start, part);
+  const int total_items = block_exclusive_scan4(base, part);
+  for (int q = 0; q < 4; ++q) {
+    const int t = threadIdx.x * 4 + q;
+    if (t >= tiles) continue;
+    tile_cursor[t] = start[q];
+    for (int c = 0; c < chunks[q]; ++c) {
+      const int b = start[q] + c * kChunk;
+      const int e = min(start[q] + cnt[q], b + kChunk);
+      items[base[q] + c] = make_int4(t, b, e, 0);
+    }
+  }
+  if (threadIdx.x == 0) sc->num_items = total_items;
+}
+
+constexpr int kScatterPerThread = 4;
+
+__global__ __launch_bounds__(kPointThreads) void k_bin_scatter(const float2* __restrict__ y_cur,
+                                                               const DeviceScalars* sc,
+                                                               int* __restrict__ tile_cursor,
+                                                               float2* __restrict__ binned, int n, int g, int ta) {
+  __shared__ int hist[kMaxTiles];
+  __shared__ int base[kMaxTiles];
+  const int tiles = ta * ta;
+  const DeviceScalars s = *sc;
+  constexpr int kBatch = kPointThreads * kScatterPerThread;
+  for (int b0 = blockIdx.x * kBatch; b0 < n; b0 += gridDim.x * kBatch) {
+    for (int t = threadIdx.x; t < tiles; t += kPointThreads) hist[t] = 0;
+    __syncthreads();
+    float2 v[kScatterPerThread];
+    int tile[kScatterPerThread], rank[kScatterPerThread];
+#pragma unroll
+    for (int q = 0; q < kScatterPerThread; ++q) {
+      const int i = b0 + q * kPointThreads + threadIdx.x;
+      tile[q] = -1;
+      if (i < n) {
+        v[q] = y_cur[i];
+        tile[q] = tile_of(locate(v[q].x, v[q].y, s, g), ta);
+        rank[q] = atomicAdd(&hist[tile[q]], 1);
+      }
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < tiles; t += kPointThreads) {
+      const int c = hist[t];
+      if (c != 0) base[t] = atomicAdd(tile_cursor + t, c);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kScatterPerThread; ++q) {
+      if (tile[q] >= 0) binned[base[tile[q]] + rank[q]] = v[q];
+    }
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__global__ __launch_bounds__(kPointThreads) void k_spread_tiles(const float2* __restrict__ binned,
+                                                                const int4* __restrict__ items,
+                                                                const DeviceScalars* sc, float* __restrict__ mass,
+                                                                float* __restrict__ mass_x,
+                                                                float* __restrict__ mass_y, int g, int ta) {
+#pragma clang fp contract(off)
+  constexpr int W = kTile + 1;
+  __shared__ float acc[3 * W * W];
+  if (static_cast<int>(blockIdx.x) >= sc->num_items) return;
+  const int4 it = items[blockIdx.x];
+  const int tx = it.x % ta, ty = it.x / ta;
+  const int x_base = tx * kTile, y_base = ty * kTile;
+  for (int e = threadIdx.x; e < 3 * W * W; e += kPointThreads) acc[e] = 0.0f;
+  __syncthreads();
+  const DeviceScalars s = *sc;
+  for (int p0 = it.y; p0 < it.z; p0 += kPointThreads) {
+    const int p = p0 + static_cast<int>(threadIdx.x);
+    const bool valid = p < it.z;
+    const float2 v = valid ? binned[p] : binned[it.y];
+    const Bilinear b = locate(v.x, v.y, s, g);
+    const float w00 = valid ? (1.0f - b.tx) * (1.0f - b.ty) : 0.0f;
+    const float w10 = valid ? b.tx * (1.0f - b.ty) : 0.0f;
+    const float w01 = valid ? (1.0f - b.tx) * b.ty : 0.0f;
+    const float w11 = valid ? b.tx * b.ty : 0.0f;
+    const int node = (b.y0 - y_base) * W + (b.x0 - x_base);
+    const int lead = __shfl(node, 0, kWave);
+    if (__all(node == lead)) {
+      const float c[12] = {w00, w10, w01, w11, w00 * v.x, w10 * v.x, w01 * v.x, w11 * v.x,
+                           w00 * v.y, w10 * v.y, w01 * v.y, w11 * v.y};
+      float r[12];
+#pragma unroll
+      for (int q = 0; q < 12; ++q) r[q] = wave_sum_f(c[q]);
+      if ((threadIdx.x & (kWave - 1)) == 0) {
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+          float* a = acc + m * W * W + lead;
+          atomicAdd(a, r[4 * m + 0]);
+          atomicAdd(a + 1, r[4 * m + 1]);
+          atomicAdd(a + W, r[4 * m + 2]);
+          atomicAdd(a + W + 1, r[4 * m + 3]);
+        }
+      }
+    } else if (valid) {
+      const float mv[3] = {1.0f, v.x, v.y};
+#pragma unroll
+      for (int m = 0; m < 3; ++m) {
+        float* a = acc + m * W * W + node;
+        atomicAdd(a, m == 0 ? w00 : w00 * mv[m]);
+        atomicAdd(a + 1, m == 0 ? w10 : w10 * mv[m]);
+        atomicAdd(a + W, m == 0 ? w01 : w01 * mv[m]);
+        atomicAdd(a + W + 1, m == 0 ? w11 : w11 * mv[m]);
+      }
+    }
+  }
+  __syncthreads();
+  float* grids[3] = {mass, mass_x, mass_y};
+  for (int e = threadIdx.x; e < 3 * W * W; e += kPointThreads) {
+    const float val = acc[e];
+    if (val == 0.0f) continue;
+    const int m = e / (W * W);
+    const int node = e - m * W * W;
+    const int gx = x_base + node % W;
+    const int gy = y_base + node / W;
+    if (gx < g && gy < g) atomicAdd(grids[m] + gy * g + gx, val);
   }
 }
 
@@ -801,21 +965,56 @@ __global__ __launch_bounds__(256) void k_attract(const int* __restrict__ row_ptr
                               : 0.0f;
   for (int base = blockIdx.x * RPB; base < n; base += gridDim.x * RPB) {
     const int i = base + threadIdx.x / L;
+    const bool row_ok = i < n;
     float ax = 0.0f, ay = 0.0f;
     float2 yi = make_float2(0.0f, 0.0f);
-    if (i < n) {
+    // Leader-only loads are issued before the neighbour loop so that their
+    // latency overlaps it.
+    const bool leader = lane == 0 && row_ok;
+    Bilinear b{0, 0, 0.0f, 0.0f};
+    float4 f00 = make_float4(0.f, 0.f, 0.f, 0.f), f10 = f00, f01 = f00, f11 = f00;
+    float2 gn = make_float2(1.0f, 1.0f), u = make_float2(0.0f, 0.0f);
+    if (row_ok) {
       yi = y_cur[i];
+      if (leader) {
+        if (MODE != kModeGradientExact) {
+          b = locate(yi.x, yi.y, s, g);
+          const int a00 = b.y0 * g + b.x0;
+          f00 = field[a00];
+          f10 = field[a00 + 1];
+          f01 = field[a00 + g];
+          f11 = field[a00 + g + 1];
+        }
+        if (MODE == kModeUpdate) {
+          gn = gains[i];
+          u = update[i];
+        }
+      }
       const int e1 = row_ptr[i + 1];
-      for (int e = row_ptr[i] + lane; e < e1; e += L) {
-        const int j = col[e];
-        const float p = val[e];
-        const float2 yj = y_cur[j];
-        const float dx = yi.x - yj.x;
-        const float dy = yi.y - yj.y;
-        const float q = 1.0f / (1.0f + (dx * dx + dy * dy));
-        const float c = up.exaggeration * p * q;
-        ax += c * dx;
-        ay += c * dy;
+      // Four independent gathers in flight per lane; out-of-row slots point
+      // at row i itself with p = 0 and contribute nothing.
+      for (int e = row_ptr[i] + lane; e < e1; e += 4 * L) {
+        int j[4];
+        float p[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int eq = e + q * L;
+          const bool ok = eq < e1;
+          j[q] = ok ? col[eq] : i;
+          p[q] = ok ? val[eq] : 0.0f;
+        }
+        float2 yj[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) yj[q] = y_cur[j[q]];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float dx = yi.x - yj[q].x;
+          const float dy = yi.y - yj[q].y;
+          const float qq = 1.0f / (1.0f + (dx * dx + dy * dy));
+          const float c = up.exaggeration * p[q] * qq;
+          ax += c * dx;
+          ay += c * dy;
+        }
       }
     }
 #pragma unroll
@@ -823,7 +1022,7 @@ __global__ __launch_bounds__(256) void k_attract(const int* __restrict__ row_ptr
       ax += __shfl_xor(ax, off, L);
       ay += __shfl_xor(ay, off, L);
     }
-    if (lane != 0 || i >= n) continue;
+    if (!leader) continue;
     float gx, gy;
     {
 #pragma clang fp contract(off)
@@ -832,12 +1031,6 @@ __global__ __launch_bounds__(256) void k_attract(const int* __restrict__ row_ptr
         gx = r.x * inv_exact;
         gy = r.y * inv_exact;
       } else {
-        const Bilinear b = locate(yi.x, yi.y, s, g);
-        const int a00 = b.y0 * g + b.x0;
-        const float4 f00 = field[a00];
-        const float4 f10 = field[a00 + 1];
-        const float4 f01 = field[a00 + g];
-        const float4 f11 = field[a00 + g + 1];
         const float q2 = blend(f00.x, f10.x, f01.x, f11.x, b.tx, b.ty);
         const float xq2 = blend(f00.y, f10.y, f01.y, f11.y, b.tx, b.ty);
         const float yq2 = blend(f00.z, f10.z, f01.z, f11.z, b.tx, b.ty);
@@ -853,8 +1046,6 @@ __global__ __launch_bounds__(256) void k_attract(const int* __restrict__ row_ptr
     }
     {
 #pragma clang fp contract(off)
-      float2 gn = gains[i];
-      float2 u = update[i];
       if (sign0(u.x) != sign0(gx)) {
         gn.x += 0.2f;
       } else {
@@ -991,6 +1182,90 @@ __global__ __launch_bounds__(256) void k_kl_rows(const int* __restrict__ row_ptr
   if (threadIdx.x == 0) partial[blockIdx.x] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// Locality renumbering
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ unsigned int spread_bits16(unsigned int v) {
+  v &= 0xffffu;
+  v = (v | (v << 8)) & 0x00ff00ffu;
+  v = (v | (v << 4)) & 0x0f0f0f0fu;
+  v = (v | (v << 2)) & 0x33333333u;
+  v = (v | (v << 1)) & 0x55555555u;
+  return v;
+}
+
+// 32-bit Morton key of each point on a 65536^2 lattice over the bounding box
+// of the layout (stored values minus the pending centring shift).
+__global__ __launch_bounds__(kPointThreads) void k_morton_keys(const float2* __restrict__ y, const DeviceScalars* sc,
+                                                               int n, unsigned int* __restrict__ keys,
+                                                               int* __restrict__ idx) {
+  const DeviceScalars s = *sc;
+  const float sx = fmaxf(s.max_x - s.min_x, 1e-30f);
+  const float sy = fmaxf(s.max_y - s.min_y, 1e-30f);
+  for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += gridDim.x * kPointThreads) {
+    const float2 v = y[i];
+    const float ux = fminf(fmaxf((v.x - s.shift_x - s.min_x) / sx, 0.0f), 1.0f);
+    const float uy = fminf(fmaxf((v.y - s.shift_y - s.min_y) / sy, 0.0f), 1.0f);
+    const unsigned int qx = static_cast<unsigned int>(ux * 65535.0f);
+    const unsigned int qy = static_cast<unsigned int>(uy * 65535.0f);
+    keys[i] = spread_bits16(qx) | (spread_bits16(qy) << 1);
+    idx[i] = i;
+  }
+}
+
+__global__ __launch_bounds__(kPointThreads) void k_apply_order(const int* __restrict__ order, int n,
+                                                               const int* __restrict__ perm_old,
+                                                               int* __restrict__ perm_new, int* __restrict__ map,
+                                                               const float2* __restrict__ y_old,
+                                                               float2* __restrict__ y_new,
+                                                               const float2* __restrict__ u_old,
+                                                               float2* __restrict__ u_new,
+                                                               const float2* __restrict__ g_old,
+                                                               float2* __restrict__ g_new,
+                                                               const int* __restrict__ rp_old, int* __restrict__ len) {
+  for (int q = blockIdx.x * kPointThreads + threadIdx.x; q <= n; q += gridDim.x * kPointThreads) {
+    if (q == n) {
+      len[n] = 0;
+      continue;
+    }
+    const int r = order[q];
+    perm_new[q] = perm_old[r];
+    map[r] = q;
+    y_new[q] = y_old[r];
+    u_new[q] = u_old[r];
+    g_new[q] = g_old[r];
+    len[q] = rp_old[r + 1] - rp_old[r];
+  }
+}
+
+// One wave per new row; columns are renamed to the new numbering.
+__global__ __launch_bounds__(256) void k_copy_rows(const int* __restrict__ order, const int* __restrict__ map,
+                                                   const int* __restrict__ rp_old, const int* __restrict__ col_old,
+                                                   const float* __restrict__ val_old, const int* __restrict__ rp_new,
+                                                   int* __restrict__ col_new, float* __restrict__ val_new, int n) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int q = (blockIdx.x * 256 + threadIdx.x) / kWave; q < n; q += gridDim.x * (256 / kWave)) {
+    const int r = order[q];
+    const int b = rp_old[r];
+    const int len = rp_old[r + 1] - b;
+    const int d = rp_new[q];
+    for (int t = lane; t < len; t += kWave) {
+      col_new[d + t] = map[col_old[b + t]];
+      val_new[d + t] = val_old[b + t];
+    }
+  }
+}
+
+__global__ __launch_bounds__(kPointThreads) void k_invert(const int* __restrict__ perm, int* __restrict__ inv, int n) {
+  for (int q = blockIdx.x * kPointThreads + threadIdx.x; q < n; q += gridDim.x * kPointThreads) inv[perm[q]] = q;
+}
+
+__global__ __launch_bounds__(kPointThreads) void k_gather2(const float2* __restrict__ src,
+                                                           const int* __restrict__ idx, float2* __restrict__ dst,
+                                                           int n) {
+  for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += gridDim.x * kPointThreads) dst[i] = src[idx[i]];
+}
+
 template <int F>
 hipError_t grid_fft_launch(int which, GridBuffers& gb, const DeviceScalars* sc_const, DeviceScalars* sc,
                            const float2* tw, int n, hipStream_t stream) {
@@ -1124,10 +1399,34 @@ hipError_t launch_stats(const float2* y, int n, int g, int center, BlockStats* p
   return hipGetLastError();
 }
 
-hipError_t launch_spread(const float2* y_stored, float2* y_cur, const DeviceScalars* sc, GridBuffers& gb, int n,
-                         hipStream_t stream) {
-  k_spread<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(y_stored, y_cur, sc, gb.mass, gb.mass_x, gb.mass_y,
-                                                               n, gb.g);
+hipError_t launch_bin_count(const float2* y_stored, float2* y_cur, const DeviceScalars* sc, GridBuffers& gb, int n,
+                            hipStream_t stream) {
+  const int ta = tiles_per_axis(gb.g);
+  const int blocks = std::min(reduce_blocks_for(n), 1024);
+  k_bin_count<<<blocks, kPointThreads, 0, stream>>>(y_stored, y_cur, sc, gb.tile_count, n, gb.g, ta);
+  return hipGetLastError();
+}
+
+hipError_t launch_bin_plan(GridBuffers& gb, DeviceScalars* sc, hipStream_t stream) {
+  const int ta = tiles_per_axis(gb.g);
+  k_bin_plan<<<1, 1024, 0, stream>>>(gb.tile_count, gb.tile_cursor, gb.items, sc, ta * ta);
+  return hipGetLastError();
+}
+
+hipError_t launch_bin_scatter(const float2* y_cur, const DeviceScalars* sc, GridBuffers& gb, int n,
+                              hipStream_t stream) {
+  const int ta = tiles_per_axis(gb.g);
+  constexpr int kBatch = kPointThreads * kScatterPerThread;
+  const int needed = (n + kBatch - 1) / kBatch;
+  const int blocks = std::max(1, std::min(needed, 1024));
+  k_bin_scatter<<<blocks, kPointThreads, 0, stream>>>(y_cur, sc, gb.tile_cursor, gb.binned, n, gb.g, ta);
+  return hipGetLastError();
+}
+
+hipError_t launch_spread_tiles(const DeviceScalars* sc, GridBuffers& gb, int n, hipStream_t stream) {
+  const int ta = tiles_per_axis(gb.g);
+  k_spread_tiles<<<max_spread_items(n, gb.g), kPointThreads, 0, stream>>>(gb.binned, gb.items, sc, gb.mass,
+                                                                          gb.mass_x, gb.mass_y, gb.g, ta);
   return hipGetLastError();
 }
 
@@ -1168,6 +1467,61 @@ hipError_t launch_attract(int mode, const Csr& p, const float2* y_cur, float2* y
 
 hipError_t launch_commit(float2* y, const DeviceScalars* sc, int n, hipStream_t stream) {
   k_commit<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(y, sc, n);
+  return hipGetLastError();
+}
+
+hipError_t renumber_temp_bytes(int n, std::size_t& bytes) {
+  std::size_t sort_b = 0, scan_b = 0;
+  hipError_t e = rocprim::radix_sort_pairs(nullptr, sort_b, static_cast<const unsigned int*>(nullptr),
+                                           static_cast<unsigned int*>(nullptr), static_cast<const int*>(nullptr),
+                                           static_cast<int*>(nullptr), static_cast<std::size_t>(n), 0u, 32u);
+  if (e != hipSuccess) return e;
+  e = rocprim::exclusive_scan(nullptr, scan_b, static_cast<const int*>(nullptr), static_cast<int*>(nullptr), 0,
+                              static_cast<std::size_t>(n) + 1, rocprim::plus<int>());
+  bytes = std::max(sort_b, scan_b);
+  return e;
+}
+
+hipError_t launch_morton_keys(const float2* y, const DeviceScalars* sc, int n, Renumber& r, hipStream_t stream) {
+  k_morton_keys<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(y, sc, n, r.keys_in, r.idx_in);
+  return hipGetLastError();
+}
+
+hipError_t sort_morton(Renumber& r, int n, hipStream_t stream) {
+  std::size_t tb = r.temp_bytes;
+  return rocprim::radix_sort_pairs(r.temp, tb, r.keys_in, r.keys_out, r.idx_in, r.order,
+                                   static_cast<std::size_t>(n), 0u, 32u, stream);
+}
+
+hipError_t launch_apply_order(const Renumber& r, int n, const int* perm_old, int* perm_new, const float2* y_old,
+                              float2* y_new, const float2* u_old, float2* u_new, const float2* g_old, float2* g_new,
+                              const int* rp_old, hipStream_t stream) {
+  k_apply_order<<<reduce_blocks_for(n + 1), kPointThreads, 0, stream>>>(r.order, n, perm_old, perm_new, r.map,
+                                                                        y_old, y_new, u_old, u_new, g_old, g_new,
+                                                                        rp_old, r.len);
+  return hipGetLastError();
+}
+
+hipError_t scan_row_lengths(Renumber& r, int n, int* rp_new, hipStream_t stream) {
+  std::size_t tb = r.temp_bytes;
+  return rocprim::exclusive_scan(r.temp, tb, r.len, rp_new, 0, static_cast<std::size_t>(n) + 1,
+                                 rocprim::plus<int>(), stream);
+}
+
+hipError_t launch_copy_rows(const Renumber& r, int n, const Csr& src, Csr& dst, hipStream_t stream) {
+  const int blocks = std::max(1, std::min((n + 3) / 4, 8192));
+  k_copy_rows<<<blocks, 256, 0, stream>>>(r.order, r.map, src.row_ptr, src.col, src.val, dst.row_ptr, dst.col,
+                                          dst.val, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_invert(const int* perm, int* inv, int n, hipStream_t stream) {
+  k_invert<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(perm, inv, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather2(const float2* src, const int* idx, float2* dst, int n, hipStream_t stream) {
+  k_gather2<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(src, idx, dst, n);
   return hipGetLastError();
 }
 

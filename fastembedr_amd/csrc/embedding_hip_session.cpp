@@ -117,14 +117,31 @@ struct fastembedr_hip_tsne {
   int lanes = 16;
   hipStream_t stream = nullptr;
   Arena arena;
+  Arena work_arena;         // working-order CSR copies, permutations, state double buffers
   DeviceScalars* sc = nullptr;
-  Csr p;
+  Csr p;                    // P in the caller's numbering (columns ascending)
+  Csr pw[2];                // P in the working numbering (after renumbering)
+  int wi = -1;              // current working copy; -1: working numbering == caller's
   float* p_cond = nullptr;
-  float2* y_a = nullptr;    // stored layout (raw between iterations)
-  float2* y_b = nullptr;    // centred layout of the current iteration
-  float2* update = nullptr;
-  float2* gains = nullptr;
+  // Optimiser state in the working numbering, double-buffered for renumbering.
+  float2* ys[2] = {nullptr, nullptr};   // stored layout (raw between iterations)
+  float2* us[2] = {nullptr, nullptr};   // update
+  float2* gs[2] = {nullptr, nullptr};   // gains
+  int si = 0;
+  int* perm[2] = {nullptr, nullptr};    // working index -> caller's index
+  int pi = 0;
+  int* inv_perm = nullptr;              // caller's index -> working index
+  fehip::Renumber rn;
+  int reorder_period = 50;
+  int since_reorder = 0;
+  float2* y_b = nullptr;    // centred layout of the current iteration (also scratch)
   float2* grad = nullptr;
+
+  bool renumbered() const { return wi >= 0; }
+  const Csr& work_p() const { return wi < 0 ? p : pw[wi]; }
+  float2* y_a() const { return ys[si]; }
+  float2* update() const { return us[si]; }
+  float2* gains() const { return gs[si]; }
   float2* exact_rep = nullptr;
   float2* tw = nullptr;
   BlockStats* partial = nullptr;
@@ -141,6 +158,7 @@ struct fastembedr_hip_tsne {
   ~fastembedr_hip_tsne() {
     if (stream != nullptr) (void)hipStreamSynchronize(stream);
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
+    work_arena.release();
     arena.release();
     if (stream != nullptr) (void)hipStreamDestroy(stream);
   }
@@ -181,8 +199,8 @@ struct fastembedr_hip_tsne {
 namespace {
 
 const char* kKernelNames[fehip::kKernelCount] = {
-    "stats", "spread", "kernel_rows", "kernel_cols", "charge_rows",
-    "conv_cols", "inverse_rows", "attract_update", "commit"};
+    "stats", "bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols", "charge_rows",
+    "conv_cols", "inverse_rows", "attract_update", "commit", "renumber"};
 
 int key_bits_for(int n) {
   int b = 1;
@@ -196,8 +214,109 @@ bool upload_twiddles(fastembedr_hip_tsne* s) {
     const double ang = -2.0 * M_PI * static_cast<double>(m) / static_cast<double>(fehip::kTwiddleLen);
     host[m] = make_float2(static_cast<float>(std::cos(ang)), static_cast<float>(std::sin(ang)));
   }
-  return hip_ok(hipMemcpyAsync(s->tw, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice, s->stream),
+  // Synchronous: `host` is released when this function returns.
+  return hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize(twiddles)") &&
+         hip_ok(hipMemcpy(s->tw, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice),
                 "hipMemcpy(twiddles)");
+}
+
+// Working-numbering buffers: two CSR copies, permutations, the second half of
+// the state double buffers and the renumbering scratch.  perm starts as the
+// identity, so until the first renumbering the working numbering is the
+// caller's.
+bool alloc_working_buffers(fastembedr_hip_tsne* s) {
+  const int n = s->n;
+  const std::size_t nnz = static_cast<std::size_t>(s->p.nnz);
+  std::size_t temp = 0;
+  if (!hip_ok(fehip::renumber_temp_bytes(n, temp), "renumber size query")) return false;
+  const std::size_t nn = static_cast<std::size_t>(n);
+  const std::size_t bytes = 2 * (align_up((nn + 1) * 4) + align_up(nnz * 4) + align_up(nnz * 4)) +
+                            3 * align_up(nn * 4) + 3 * align_up(nn * sizeof(float2)) + 2 * align_up(nn * 4) +
+                            3 * align_up(nn * 4) + align_up((nn + 1) * 4) + align_up(temp) + 4096;
+  if (!memory_preflight(bytes, "HIP openTSNE working buffers") ||
+      !s->work_arena.init(bytes, "hipMalloc(HIP openTSNE working buffers)")) {
+    return false;
+  }
+  Arena& a = s->work_arena;
+  for (int w = 0; w < 2; ++w) {
+    s->pw[w].n = n;
+    s->pw[w].nnz = s->p.nnz;
+    s->pw[w].row_ptr = a.take<int>(nn + 1);
+    s->pw[w].col = a.take<int>(nnz);
+    s->pw[w].val = a.take<float>(nnz);
+  }
+  s->perm[0] = a.take<int>(nn);
+  s->perm[1] = a.take<int>(nn);
+  s->inv_perm = a.take<int>(nn);
+  s->ys[1] = a.take<float2>(nn);
+  s->us[1] = a.take<float2>(nn);
+  s->gs[1] = a.take<float2>(nn);
+  s->rn.keys_in = a.take<unsigned int>(nn);
+  s->rn.keys_out = a.take<unsigned int>(nn);
+  s->rn.idx_in = a.take<int>(nn);
+  s->rn.order = a.take<int>(nn);
+  s->rn.map = a.take<int>(nn);
+  s->rn.len = a.take<int>(nn + 1);
+  s->rn.temp = a.take<char>(temp);
+  s->rn.temp_bytes = temp;
+  if (s->rn.temp == nullptr) {
+    set_error("internal: working buffers do not fit their arena");
+    return false;
+  }
+  std::vector<int> iota(nn);
+  for (int i = 0; i < n; ++i) iota[static_cast<std::size_t>(i)] = i;
+  return hip_ok(hipMemcpy(s->perm[0], iota.data(), nn * 4, hipMemcpyHostToDevice), "perm init") &&
+         hip_ok(hipMemcpy(s->inv_perm, iota.data(), nn * 4, hipMemcpyHostToDevice), "perm init");
+}
+
+// Renumbers points by the Morton order of the current layout: permutes the
+// state, rebuilds the working CSR in the new numbering and updates the
+// permutations.  Needs the bounding box and pending shift in DeviceScalars
+// (set by the stats kernel or by the previous update).  Stream-ordered, no
+// host synchronisation.
+hipError_t enqueue_renumber(fastembedr_hip_tsne* s) {
+  const int n = s->n;
+  const int next = s->wi < 0 ? 0 : 1 - s->wi;
+  const Csr& src = s->work_p();
+  Csr& dst = s->pw[next];
+  hipError_t e = fehip::launch_morton_keys(s->ys[s->si], s->sc, n, s->rn, s->stream);
+  if (e == hipSuccess) e = fehip::sort_morton(s->rn, n, s->stream);
+  if (e == hipSuccess)
+    e = fehip::launch_apply_order(s->rn, n, s->perm[s->pi], s->perm[1 - s->pi], s->ys[s->si], s->ys[1 - s->si],
+                                  s->us[s->si], s->us[1 - s->si], s->gs[s->si], s->gs[1 - s->si], src.row_ptr,
+                                  s->stream);
+  if (e == hipSuccess) e = fehip::scan_row_lengths(s->rn, n, dst.row_ptr, s->stream);
+  if (e == hipSuccess) e = fehip::launch_copy_rows(s->rn, n, src, dst, s->stream);
+  if (e == hipSuccess) e = fehip::launch_invert(s->perm[1 - s->pi], s->inv_perm, n, s->stream);
+  if (e != hipSuccess) return e;
+  s->wi = next;
+  s->si = 1 - s->si;
+  s->pi = 1 - s->pi;
+  s->since_reorder = 0;
+  return hipSuccess;
+}
+
+// Host (caller's numbering) -> working numbering, through y_b as staging.
+bool upload_permuted(fastembedr_hip_tsne* s, const float* host, float2* dst) {
+  const std::size_t bytes = static_cast<std::size_t>(s->n) * sizeof(float2);
+  if (!s->renumbered()) {
+    return hip_ok(hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, s->stream), "state upload");
+  }
+  return hip_ok(hipMemcpyAsync(s->y_b, host, bytes, hipMemcpyHostToDevice, s->stream), "state upload") &&
+         hip_ok(fehip::launch_gather2(s->y_b, s->perm[s->pi], dst, s->n, s->stream), "permute launch") &&
+         hip_ok(hipStreamSynchronize(s->stream), "state upload sync");
+}
+
+// Working numbering -> host (caller's numbering), through y_b as staging.
+bool download_permuted(fastembedr_hip_tsne* s, const float2* src, float* host) {
+  const std::size_t bytes = static_cast<std::size_t>(s->n) * sizeof(float2);
+  if (!s->renumbered()) {
+    return hip_ok(hipMemcpyAsync(host, src, bytes, hipMemcpyDeviceToHost, s->stream), "state download") &&
+           hip_ok(hipStreamSynchronize(s->stream), "state download sync");
+  }
+  return hip_ok(fehip::launch_gather2(src, s->inv_perm, s->y_b, s->n, s->stream), "permute launch") &&
+         hip_ok(hipMemcpyAsync(host, s->y_b, bytes, hipMemcpyDeviceToHost, s->stream), "state download") &&
+         hip_ok(hipStreamSynchronize(s->stream), "state download sync");
 }
 
 // Builds P from KNN (src/tsne_neighbors.cpp:540-648 semantics) and allocates
@@ -275,7 +394,10 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
       6 * align_up(static_cast<std::size_t>(n) * sizeof(float2)) + align_up(fehip::kTwiddleLen * sizeof(float2)) +
       align_up(fehip::kMaxReduceBlocks * sizeof(BlockStats)) + align_up(dpart * sizeof(double)) +
       3 * align_up(gg * 4) + align_up(gg * sizeof(float4)) + 2 * align_up(hh * hh * sizeof(float2)) +
-      7 * align_up(g * hh * sizeof(float2)) + align_up(fehip::kMaxReduceBlocks * sizeof(double)) + 4096;
+      7 * align_up(g * hh * sizeof(float2)) + align_up(fehip::kMaxReduceBlocks * sizeof(double)) +
+      2 * align_up(fehip::kMaxTiles * sizeof(int)) +
+      align_up(static_cast<std::size_t>(fehip::max_spread_items(n, g)) * sizeof(int4)) +
+      align_up(static_cast<std::size_t>(n) * sizeof(float2)) + 4096;
   if (!memory_preflight(scratch_bytes + persistent_fixed + edges * 8, "HIP openTSNE allocation preflight") ||
       !scratch.init(scratch_bytes, "hipMalloc(P construction scratch)")) {
     delete s;
@@ -317,10 +439,10 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   s->sc = s->arena.take<DeviceScalars>(1);
   s->p_cond = s->arena.take<float>(nk);
   s->p.row_ptr = s->arena.take<int>(n + 1);
-  s->y_a = s->arena.take<float2>(n);
+  s->ys[0] = s->arena.take<float2>(n);
   s->y_b = s->arena.take<float2>(n);
-  s->update = s->arena.take<float2>(n);
-  s->gains = s->arena.take<float2>(n);
+  s->us[0] = s->arena.take<float2>(n);
+  s->gs[0] = s->arena.take<float2>(n);
   s->grad = s->arena.take<float2>(n);
   s->exact_rep = s->arena.take<float2>(n);
   s->tw = s->arena.take<float2>(fehip::kTwiddleLen);
@@ -342,6 +464,10 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   s->gb.v2_rows = s->arena.take<float2>(g * hh);
   s->gb.y_rows = s->arena.take<float2>(g * hh);
   s->gb.sumq_partial = s->arena.take<double>(fehip::kMaxReduceBlocks);
+  s->gb.tile_count = s->arena.take<int>(fehip::kMaxTiles);
+  s->gb.tile_cursor = s->arena.take<int>(fehip::kMaxTiles);
+  s->gb.items = s->arena.take<int4>(fehip::max_spread_items(n, g));
+  s->gb.binned = s->arena.take<float2>(n);
 
   auto fail = [&](void) {
     scratch.release();
@@ -352,6 +478,7 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
       !hip_ok(hipMemsetAsync(s->gb.mass, 0, gg * 4, s->stream), "hipMemset(grid)") ||
       !hip_ok(hipMemsetAsync(s->gb.mass_x, 0, gg * 4, s->stream), "hipMemset(grid)") ||
       !hip_ok(hipMemsetAsync(s->gb.mass_y, 0, gg * 4, s->stream), "hipMemset(grid)") ||
+      !hip_ok(hipMemsetAsync(s->gb.tile_count, 0, fehip::kMaxTiles * sizeof(int), s->stream), "hipMemset(tiles)") ||
       !upload_twiddles(s)) {
     return fail();
   }
@@ -393,7 +520,14 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
       !hip_ok(fehip::launch_mark_heads(keys_b, valid, heads, s->stream), "mark_heads launch")) {
     return fail();
   }
-  tb = scan_temp;
+  tb = 0;
+  if (!hip_ok(fehip::scan_heads(nullptr, tb, heads, pos, valid, s->stream), "exclusive_scan(size query)")) {
+    return fail();
+  }
+  if (tb > std::max(sort_temp, scan_temp)) {
+    set_error("internal: scan scratch larger than reserved");
+    return fail();
+  }
   if (!hip_ok(fehip::scan_heads(temp, tb, heads, pos, valid, s->stream), "exclusive_scan")) return fail();
   int last_pos = 0, last_head = 0;
   if (!hip_ok(hipMemcpyAsync(&last_pos, pos + (valid - 1), sizeof(int), hipMemcpyDeviceToHost, s->stream),
@@ -428,10 +562,18 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
 
   // Lanes per CSR row: enough to cover the mean row in a few passes.
   const double mean_row = static_cast<double>(nnz) / n;
-  int lanes = mean_row > 96.0 ? 32 : (mean_row > 24.0 ? 16 : 8);
+  int lanes = mean_row > 24.0 ? 16 : 8;
   lanes = env_int("FASTEMBEDR_HIP_ATTRACT_LANES", lanes);
   if (lanes != 8 && lanes != 16 && lanes != 32 && lanes != 64) lanes = 16;
   s->lanes = lanes;
+  s->reorder_period = env_int("FASTEMBEDR_HIP_RENUMBER_PERIOD", 50);
+  if (const char* off = std::getenv("FASTEMBEDR_HIP_RENUMBER_PERIOD")) {
+    if (std::strcmp(off, "0") == 0) s->reorder_period = 0;
+  }
+  if (!alloc_working_buffers(s)) {
+    delete s;
+    return 1;
+  }
   *out = s;
   return 0;
 }
@@ -440,11 +582,17 @@ bool enqueue_gradient_fields(fastembedr_hip_tsne* s, bool stats_first, int cente
   const int n = s->n;
   if (stats_first &&
       !s->timed(fehip::kKStats, "stats launch",
-                [&] { return fehip::launch_stats(s->y_a, n, s->gb.g, center, s->partial, s->sc, s->stream); })) {
+                [&] { return fehip::launch_stats(s->y_a(), n, s->gb.g, center, s->partial, s->sc, s->stream); })) {
     return false;
   }
-  return s->timed(fehip::kKSpread, "spread launch",
-                  [&] { return fehip::launch_spread(s->y_a, s->y_b, s->sc, s->gb, n, s->stream); }) &&
+  return s->timed(fehip::kKBinCount, "bin_count launch",
+                  [&] { return fehip::launch_bin_count(s->y_a(), s->y_b, s->sc, s->gb, n, s->stream); }) &&
+         s->timed(fehip::kKBinPlan, "bin_plan launch",
+                  [&] { return fehip::launch_bin_plan(s->gb, s->sc, s->stream); }) &&
+         s->timed(fehip::kKBinScatter, "bin_scatter launch",
+                  [&] { return fehip::launch_bin_scatter(s->y_b, s->sc, s->gb, n, s->stream); }) &&
+         s->timed(fehip::kKSpread, "spread launch",
+                  [&] { return fehip::launch_spread_tiles(s->sc, s->gb, n, s->stream); }) &&
          s->timed(fehip::kKKernelRows, "kernel_rows launch",
                   [&] { return fehip::launch_kernel_rows(s->gb, s->sc, s->tw, s->stream); }) &&
          s->timed(fehip::kKKernelCols, "kernel_cols launch",
@@ -643,18 +791,17 @@ int fastembedr_hip_tsne_set_state(fastembedr_hip_tsne* s, const float* y, const 
   }
   const std::size_t bytes = static_cast<std::size_t>(s->n) * sizeof(float2);
   std::vector<float> fill;
-  if (!hip_ok(hipMemcpyAsync(s->y_a, y, bytes, hipMemcpyHostToDevice, s->stream), "set_state y")) return 1;
+  if (!upload_permuted(s, y, s->y_a())) return 1;
   if (update != nullptr) {
-    if (!hip_ok(hipMemcpyAsync(s->update, update, bytes, hipMemcpyHostToDevice, s->stream), "set_state update"))
-      return 1;
-  } else if (!hip_ok(hipMemsetAsync(s->update, 0, bytes, s->stream), "set_state update")) {
+    if (!upload_permuted(s, update, s->update())) return 1;
+  } else if (!hip_ok(hipMemsetAsync(s->update(), 0, bytes, s->stream), "set_state update")) {
     return 1;
   }
   if (gains != nullptr) {
-    if (!hip_ok(hipMemcpyAsync(s->gains, gains, bytes, hipMemcpyHostToDevice, s->stream), "set_state gains")) return 1;
+    if (!upload_permuted(s, gains, s->gains())) return 1;
   } else {
     fill.assign(2 * static_cast<std::size_t>(s->n), 1.0f);
-    if (!hip_ok(hipMemcpyAsync(s->gains, fill.data(), bytes, hipMemcpyHostToDevice, s->stream), "set_state gains"))
+    if (!hip_ok(hipMemcpyAsync(s->gains(), fill.data(), bytes, hipMemcpyHostToDevice, s->stream), "set_state gains"))
       return 1;
   }
   return hip_ok(hipStreamSynchronize(s->stream), "set_state sync") ? 0 : 1;
@@ -662,16 +809,10 @@ int fastembedr_hip_tsne_set_state(fastembedr_hip_tsne* s, const float* y, const 
 
 int fastembedr_hip_tsne_get_state(fastembedr_hip_tsne* s, float* y, float* update, float* gains) {
   if (!valid_state_args(s)) return 1;
-  const std::size_t bytes = static_cast<std::size_t>(s->n) * sizeof(float2);
-  if (y != nullptr && !hip_ok(hipMemcpyAsync(y, s->y_a, bytes, hipMemcpyDeviceToHost, s->stream), "get_state y"))
-    return 1;
-  if (update != nullptr &&
-      !hip_ok(hipMemcpyAsync(update, s->update, bytes, hipMemcpyDeviceToHost, s->stream), "get_state update"))
-    return 1;
-  if (gains != nullptr &&
-      !hip_ok(hipMemcpyAsync(gains, s->gains, bytes, hipMemcpyDeviceToHost, s->stream), "get_state gains"))
-    return 1;
-  return hip_ok(hipStreamSynchronize(s->stream), "get_state sync") ? 0 : 1;
+  if (y != nullptr && !download_permuted(s, s->y_a(), y)) return 1;
+  if (update != nullptr && !download_permuted(s, s->update(), update)) return 1;
+  if (gains != nullptr && !download_permuted(s, s->gains(), gains)) return 1;
+  return 0;
 }
 
 int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int repulsion, float* grad_out) {
@@ -682,14 +823,14 @@ int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int
   s->timing = false;
   bool ok = true;
   if (repulsion == FASTEMBEDR_HIP_REPULSION_EXACT) {
-    ok = hip_ok(fehip::launch_exact_repulsion(s->y_a, s->n, s->exact_rep, s->dpartial, s->sc, s->stream),
+    ok = hip_ok(fehip::launch_exact_repulsion(s->y_a(), s->n, s->exact_rep, s->dpartial, s->sc, s->stream),
                 "exact repulsion launch") &&
-         hip_ok(fehip::launch_attract(fehip::kModeGradientExact, s->p, s->y_a, nullptr, nullptr, nullptr, s->grad,
+         hip_ok(fehip::launch_attract(fehip::kModeGradientExact, s->work_p(), s->y_a(), nullptr, nullptr, nullptr, s->grad,
                                       s->exact_rep, s->gb, up, s->partial, s->sc, s->lanes, s->stream),
                 "attract launch");
   } else if (repulsion == FASTEMBEDR_HIP_REPULSION_GRID) {
     ok = enqueue_gradient_fields(s, true, 0) &&
-         hip_ok(fehip::launch_attract(fehip::kModeGradientGrid, s->p, s->y_b, nullptr, nullptr, nullptr, s->grad,
+         hip_ok(fehip::launch_attract(fehip::kModeGradientGrid, s->work_p(), s->y_b, nullptr, nullptr, nullptr, s->grad,
                                       nullptr, s->gb, up, s->partial, s->sc, s->lanes, s->stream),
                 "attract launch");
   } else {
@@ -698,19 +839,13 @@ int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int
   }
   s->timing = was_timing;
   if (!ok) return 1;
-  if (!hip_ok(hipMemcpyAsync(grad_out, s->grad, static_cast<std::size_t>(s->n) * sizeof(float2),
-                             hipMemcpyDeviceToHost, s->stream),
-              "copy gradient") ||
-      !hip_ok(hipStreamSynchronize(s->stream), "gradient sync")) {
-    return 1;
-  }
-  return 0;
+  return download_permuted(s, s->grad, grad_out) ? 0 : 1;
 }
 
 int fastembedr_hip_tsne_center(fastembedr_hip_tsne* s) {
   if (!valid_state_args(s)) return 1;
-  if (!hip_ok(fehip::launch_stats(s->y_a, s->n, s->gb.g, 1, s->partial, s->sc, s->stream), "stats launch") ||
-      !hip_ok(fehip::launch_commit(s->y_a, s->sc, s->n, s->stream), "commit launch")) {
+  if (!hip_ok(fehip::launch_stats(s->y_a(), s->n, s->gb.g, 1, s->partial, s->sc, s->stream), "stats launch") ||
+      !hip_ok(fehip::launch_commit(s->y_a(), s->sc, s->n, s->stream), "commit launch")) {
     return 1;
   }
   return 0;
@@ -734,20 +869,27 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
   up.clip = (std::isfinite(max_step_norm) && max_step_norm > 0.0f) ? 1 : 0;
   const int n = s->n;
   if (!s->timed(fehip::kKStats, "stats launch",
-                [&] { return fehip::launch_stats(s->y_a, n, s->gb.g, 0, s->partial, s->sc, s->stream); })) {
+                [&] { return fehip::launch_stats(s->y_a(), n, s->gb.g, 0, s->partial, s->sc, s->stream); })) {
     return 1;
   }
   for (int it = 0; it < n_iter; ++it) {
+    // Renumber before the first iteration ever run and then every
+    // reorder_period iterations; the bounding box and pending shift it needs
+    // are in DeviceScalars (stats kernel above, or the previous update).
+    if (s->reorder_period > 0 && (!s->renumbered() || s->since_reorder >= s->reorder_period)) {
+      if (!s->timed(fehip::kKRenumber, "renumber", [&] { return enqueue_renumber(s); })) return 1;
+    }
+    ++s->since_reorder;
     if (!enqueue_gradient_fields(s, false, 0)) return 1;
     if (!s->timed(fehip::kKAttractUpdate, "attract launch", [&] {
-          return fehip::launch_attract(fehip::kModeUpdate, s->p, s->y_b, s->y_a, s->update, s->gains, nullptr,
+          return fehip::launch_attract(fehip::kModeUpdate, s->work_p(), s->y_b, s->y_a(), s->update(), s->gains(), nullptr,
                                        nullptr, s->gb, up, s->partial, s->sc, s->lanes, s->stream);
         })) {
       return 1;
     }
   }
   if (!s->timed(fehip::kKCommit, "commit launch",
-                [&] { return fehip::launch_commit(s->y_a, s->sc, n, s->stream); })) {
+                [&] { return fehip::launch_commit(s->y_a(), s->sc, n, s->stream); })) {
     return 1;
   }
   return s->harvest_timing() ? 0 : 1;
@@ -762,7 +904,7 @@ int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* s, double* kl) {
   if (!valid_state_args(s) || kl == nullptr) return 1;
   const int zb = fehip::exact_blocks_for(s->n);
   std::vector<double> part(static_cast<std::size_t>(std::max(zb, 1024)));
-  if (!hip_ok(fehip::launch_exact_z_double(s->y_a, s->n, s->dpartial, s->stream), "exact_z launch") ||
+  if (!hip_ok(fehip::launch_exact_z_double(s->y_a(), s->n, s->dpartial, s->stream), "exact_z launch") ||
       !hip_ok(hipMemcpyAsync(part.data(), s->dpartial, zb * sizeof(double), hipMemcpyDeviceToHost, s->stream),
               "copy z partials") ||
       !hip_ok(hipStreamSynchronize(s->stream), "kl sync")) {
@@ -772,7 +914,7 @@ int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* s, double* kl) {
   for (int b = 0; b < zb; ++b) z += part[b];
   const double sum_q = static_cast<double>(static_cast<float>(std::max(z, static_cast<double>(FLT_MIN))));
   const int kb = 1024;
-  if (!hip_ok(fehip::launch_kl_rows(s->p, s->y_a, sum_q, s->dpartial, kb, s->stream), "kl launch") ||
+  if (!hip_ok(fehip::launch_kl_rows(s->work_p(), s->y_a(), sum_q, s->dpartial, kb, s->stream), "kl launch") ||
       !hip_ok(hipMemcpyAsync(part.data(), s->dpartial, kb * sizeof(double), hipMemcpyDeviceToHost, s->stream),
               "copy kl partials") ||
       !hip_ok(hipStreamSynchronize(s->stream), "kl sync")) {

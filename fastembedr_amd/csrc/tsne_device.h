@@ -28,6 +28,8 @@ struct alignas(16) DeviceScalars {
   unsigned int ticket_exact;
   unsigned int error_flags;  // bit 0: index out of range, bit 1: bad distance
   unsigned long long self_edges;
+  int num_items;             // spread work items of the current iteration
+  int pad1;
 };
 
 struct BlockStats {
@@ -39,10 +41,24 @@ constexpr int kMaxReduceBlocks = 4096;
 constexpr int kTwiddleLen = 4096;     // e^{-2 pi i m / 4096}, m in [0, 4096)
 constexpr int kMaxGrid = 1024;        // nodes per axis (FFT length 2048)
 
+// Spreading is binned by tiles of kTile x kTile cells; each work item is at
+// most kChunk points of one tile, accumulated in LDS ((kTile + 1)^2 nodes).
+constexpr int kTile = 16;
+constexpr int kChunk = 2048;
+constexpr int kMaxTilesPerAxis = (kMaxGrid - 2) / kTile + 1;  // 64
+constexpr int kMaxTiles = kMaxTilesPerAxis * kMaxTilesPerAxis;
+inline int tiles_per_axis(int g) { return (g - 2) / kTile + 1; }
+inline int max_spread_items(int n, int g) {
+  return (n + kChunk - 1) / kChunk + tiles_per_axis(g) * tiles_per_axis(g);
+}
+
 enum ErrorBits : unsigned int { kErrIndex = 1u, kErrDistance = 2u };
 
 enum KernelId : int {
   kKStats = 0,
+  kKBinCount,
+  kKBinPlan,
+  kKBinScatter,
   kKSpread,
   kKKernelRows,
   kKKernelCols,
@@ -51,6 +67,7 @@ enum KernelId : int {
   kKInverseRows,
   kKAttractUpdate,
   kKCommit,
+  kKRenumber,
   kKernelCount
 };
 
@@ -71,6 +88,11 @@ struct GridBuffers {
   float2* v2_rows = nullptr;
   float2* y_rows = nullptr;
   double* sumq_partial = nullptr;  // kMaxReduceBlocks
+  // spreading bins
+  int* tile_count = nullptr;   // kMaxTiles, zero between iterations
+  int* tile_cursor = nullptr;  // kMaxTiles
+  int4* items = nullptr;       // max_spread_items(n, g): (tile, begin, end, -)
+  float2* binned = nullptr;    // n centred points in tile order
 };
 
 struct Csr {
@@ -102,8 +124,14 @@ hipError_t launch_compact(const std::uint64_t* keys, const float* vals, const in
 int reduce_blocks_for(int n);
 hipError_t launch_stats(const float2* y, int n, int g, int center, BlockStats* partial, DeviceScalars* sc,
                         hipStream_t stream);
-hipError_t launch_spread(const float2* y_stored, float2* y_cur, const DeviceScalars* sc, GridBuffers& gb, int n,
-                         hipStream_t stream);
+// Spreading in four launches: centre + count points per tile, plan (scan and
+// work items), scatter into tile order, per-item LDS accumulation.
+hipError_t launch_bin_count(const float2* y_stored, float2* y_cur, const DeviceScalars* sc, GridBuffers& gb, int n,
+                            hipStream_t stream);
+hipError_t launch_bin_plan(GridBuffers& gb, DeviceScalars* sc, hipStream_t stream);
+hipError_t launch_bin_scatter(const float2* y_cur, const DeviceScalars* sc, GridBuffers& gb, int n,
+                              hipStream_t stream);
+hipError_t launch_spread_tiles(const DeviceScalars* sc, GridBuffers& gb, int n, hipStream_t stream);
 hipError_t launch_kernel_rows(GridBuffers& gb, const DeviceScalars* sc, const float2* tw, hipStream_t stream);
 hipError_t launch_kernel_cols(GridBuffers& gb, const float2* tw, hipStream_t stream);
 hipError_t launch_charge_rows(GridBuffers& gb, const float2* tw, hipStream_t stream);
@@ -123,6 +151,31 @@ hipError_t launch_attract(int mode, const Csr& p, const float2* y_cur, float2* y
                           float2* grad_out, const float2* exact_rep, const GridBuffers& gb, const UpdateParams& up,
                           BlockStats* partial, DeviceScalars* sc, int lanes_per_row, hipStream_t stream);
 hipError_t launch_commit(float2* y, const DeviceScalars* sc, int n, hipStream_t stream);
+
+// ---- locality renumbering ---------------------------------------------------
+// Points are renumbered by the Morton order of the current layout so that
+// CSR neighbours sit close in memory.  `order[q]` is the old working index of
+// new index q; perm maps working -> original indices.
+struct Renumber {
+  unsigned int* keys_in = nullptr;
+  unsigned int* keys_out = nullptr;
+  int* idx_in = nullptr;
+  int* order = nullptr;
+  int* map = nullptr;   // old working index -> new working index
+  int* len = nullptr;   // n + 1 row lengths, then the new row pointers
+  void* temp = nullptr;
+  std::size_t temp_bytes = 0;
+};
+hipError_t renumber_temp_bytes(int n, std::size_t& bytes);
+hipError_t launch_morton_keys(const float2* y, const DeviceScalars* sc, int n, Renumber& r, hipStream_t stream);
+hipError_t sort_morton(Renumber& r, int n, hipStream_t stream);
+hipError_t launch_apply_order(const Renumber& r, int n, const int* perm_old, int* perm_new, const float2* y_old,
+                              float2* y_new, const float2* u_old, float2* u_new, const float2* g_old, float2* g_new,
+                              const int* rp_old, hipStream_t stream);
+hipError_t scan_row_lengths(Renumber& r, int n, int* rp_new, hipStream_t stream);
+hipError_t launch_copy_rows(const Renumber& r, int n, const Csr& src, Csr& dst, hipStream_t stream);
+hipError_t launch_invert(const int* perm, int* inv, int n, hipStream_t stream);
+hipError_t launch_gather2(const float2* src, const int* idx, float2* dst, int n, hipStream_t stream);
 
 // ---- exact O(n^2) terms (gradient check and KL) ----------------------------
 hipError_t launch_exact_repulsion(const float2* y, int n, float2* rep, double* z_partial, DeviceScalars* sc,

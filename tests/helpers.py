@@ -16,6 +16,38 @@ def small_problem(n=600, dim=8, k=24, components=4, seed=3, one_based=True):
     return x, labels, idx_r, dist_r
 
 
+class DeviceArray:
+    """A host array copied into device memory with the HIP runtime that the
+    backend library already loaded (no second runtime in the process)."""
+
+    def __init__(self, host: np.ndarray):
+        import ctypes as C
+
+        from fastembedr_amd import _lib
+
+        _lib.load()
+        self._hip = C.CDLL("libamdhip64.so.7")
+        self._hip.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+        self._hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        self._hip.hipFree.argtypes = [C.c_void_p]
+        host = np.ascontiguousarray(host)
+        self.nbytes = host.nbytes
+        self.ptr = C.c_void_p()
+        if self._hip.hipMalloc(C.byref(self.ptr), self.nbytes) != 0:
+            raise RuntimeError("hipMalloc failed")
+        if self._hip.hipMemcpy(self.ptr, C.c_void_p(host.ctypes.data), self.nbytes, 1) != 0:
+            raise RuntimeError("hipMemcpy failed")
+
+    @property
+    def address(self) -> int:
+        return int(self.ptr.value)
+
+    def free(self):
+        if self.ptr:
+            self._hip.hipFree(self.ptr)
+            self.ptr = None
+
+
 def csr_to_dense(row_ptr, col, val, n):
     m = np.zeros((n, n), np.float64)
     for i in range(n):

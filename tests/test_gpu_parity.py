@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 from fastembedr_amd import _lib, synthetic
-from tests.helpers import knn_preservation, rel_l2, small_problem
+from tests.helpers import DeviceArray, knn_preservation, rel_l2, small_problem
 
 pytestmark = pytest.mark.gpu
 
@@ -146,33 +146,65 @@ def test_exact_gradient_matches_oracle(hip, oracle_mod, mid_problem):
     assert rel_l2(g, ref) <= 1e-5
 
 
-def test_iterations_track_oracle(hip, oracle_mod, mid_problem):
-    """One and then ten full iterations (gradient, update, centring) from the
-    same state; the trajectories agree to the gradient tolerance."""
-    _say("case: iterations vs oracle")
+@pytest.mark.parametrize("phase", ["early", "normal"])
+def test_each_iteration_matches_oracle(hip, oracle_mod, mid_problem, phase):
+    """Per-iteration parity: from the device's own state (y, update, gains) at
+    every step, one oracle iteration (gradient, update, centring) and one
+    device iteration agree; the step taken (y_{t+1} - y_t) to the gradient
+    tolerance, and the gains exactly except where a gradient component sits
+    at rounding level."""
     x, idx, dist = mid_problem
+    n = x.shape[0]
+    ex, mom = (12.0, 0.5) if phase == "early" else (1.0, 0.8)
+    _say(f"case: per-iteration parity ({phase} phase)")
+    y0 = synthetic.pca_init(x) * (1.0 if phase == "early" else 3e4)
+    with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+        P = oracle_mod.OracleP.wrap(*s.csr())
+        s.set_state(y0)
+        s.center()
+        if phase == "normal":
+            s.run(30, 12.0, 0.5, n / 12.0, 0.01, 5.0)
+        worst = 0.0
+        for t in range(12):
+            y, u, g = s.get_state()
+            s.run(1, ex, mom, n / 12.0, 0.01, 5.0)
+            y1, u1, g1 = s.get_state()
+            yr, ur, gr = y.copy(), u.copy(), g.copy()
+            grad = P.gradient(yr, ex, threads=4)
+            oracle_mod.update(yr, ur, gr, grad, n / 12.0, mom)
+            oracle_mod.zero_mean(yr)
+            err = rel_l2(y1 - y, yr - y)
+            worst = max(worst, err)
+            assert err <= GRAD_TOL, (t, err)
+            assert np.mean(g1 != gr) <= 1e-3, t
+        _say(f"  worst per-step relL2 {worst:.2e}")
+
+
+def test_free_run_divergence_is_rounding_level(hip, oracle_mod, mid_problem):
+    """Twenty free-running iterations from the same initialisation.  The
+    iteration amplifies rounding (sign-driven gains, early exaggeration), so
+    the yardstick is the oracle against itself: the same run started from a
+    layout perturbed by about four ulps.  The device run may not diverge from
+    the oracle by more than a small multiple of that."""
+    x, idx, dist = mid_problem
+    n = x.shape[0]
+    _say("case: 20 free-running iterations")
     y0 = synthetic.pca_init(x)
     with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
         P = oracle_mod.OracleP.wrap(*s.csr())
         s.set_state(y0)
         s.center()
-        s.run(1, 12.0, 0.5, 3000 / 12.0, 0.01, 5.0)
-        y1, u1, g1 = s.get_state()
-        y_ref = y0.copy()
-        oracle_mod.zero_mean(y_ref)
-        upd = np.zeros_like(y_ref)
-        gains = np.ones_like(y_ref)
-        grad = P.gradient(y_ref, 12.0, threads=4)
-        oracle_mod.update(y_ref, upd, gains, grad, 3000 / 12.0, 0.5)
-        oracle_mod.zero_mean(y_ref)
-        assert rel_l2(y1, y_ref) <= 1e-4
-        np.testing.assert_array_equal(g1, gains)
-        s.run(9, 12.0, 0.5, 3000 / 12.0, 0.01, 5.0)
-        y10 = s.y
-    yo, _, _ = P.optimize(y0, 10, 0, 12.0, 1.0, 3000 / 12.0, False, 0.5, 0.8, threads=4)
-    err = rel_l2(y10, yo)
-    _say(f"  10 iterations relL2={err:.2e}")
-    assert err <= GRAD_TOL
+        s.run(20, 12.0, 0.5, n / 12.0, 0.01, 5.0)
+        y20 = s.y
+    args = (20, 0, 12.0, 1.0, n / 12.0, False, 0.5, 0.8)
+    yo, _, _ = P.optimize(y0, *args, threads=4)
+    rng = np.random.default_rng(0)
+    y0p = (y0 * (1.0 + 4.8e-7 * rng.standard_normal(y0.shape))).astype(np.float32)
+    yp, _, _ = P.optimize(y0p, *args, threads=4)
+    err = rel_l2(y20, yo)
+    ref = rel_l2(yp, yo)
+    _say(f"  20 iterations relL2 hip-vs-oracle={err:.2e}, oracle-vs-perturbed-oracle={ref:.2e}")
+    assert err <= max(5.0 * ref, 1e-4)
 
 
 def test_kl_matches_oracle(hip, oracle_mod, mid_problem):
@@ -188,9 +220,9 @@ def test_kl_matches_oracle(hip, oracle_mod, mid_problem):
     assert abs(kl - ref) <= 1e-6 * abs(ref)
 
 
-def _one_shot(fn_name, idx, dist, init, n_early, n_norm, device=False):
+def _one_shot(fn_name, idx, dist, init, n_early, n_norm, device=False, shape=None):
     lib = _lib.load()
-    n, k = idx.shape
+    n, k = shape if device else idx.shape
     out = np.empty((n, 2), np.float32)
     fn = getattr(lib, fn_name)
     rc = fn(C.c_void_p(idx) if device else C.c_void_p(idx.ctypes.data),
@@ -222,18 +254,19 @@ def test_end_to_end_config0_kl_and_knn_preservation(hip, oracle_mod, config0):
 
 def test_one_shot_variants_agree(hip, mid_problem):
     """double-distance and device-KNN entry points give the float entry's result."""
-    import torch
-
     _say("case: one-shot variants")
     x, idx, dist = mid_problem
     y0 = synthetic.pca_init(x)
-    a = _one_shot("fastembedr_hip_opentsne_fft_from_knn_float", idx, dist, y0, 20, 20)
-    b = _one_shot("fastembedr_hip_opentsne_fft_from_knn", idx, np.asfortranarray(dist, np.float64), y0, 20, 20)
-    ti = torch.as_tensor(np.ascontiguousarray(idx.T)).cuda()  # (k, n) row-major == (n, k) column-major
-    td = torch.as_tensor(np.ascontiguousarray(dist.T)).cuda()
-    c = _one_shot("fastembedr_hip_opentsne_fft_from_device_knn_float", ti.data_ptr(), td.data_ptr(), y0, 20, 20,
-                  device=True)
-    torch.cuda.synchronize()
+    a = _one_shot("fastembedr_hip_opentsne_fft_from_knn_float", idx, dist, y0, 5, 5)
+    b = _one_shot("fastembedr_hip_opentsne_fft_from_knn", idx, np.asfortranarray(dist, np.float64), y0, 5, 5)
+    di = DeviceArray(np.asfortranarray(idx, np.int32).T)  # (k, n) C-order bytes == (n, k) column-major
+    dd = DeviceArray(np.asfortranarray(dist, np.float32).T)
+    try:
+        c = _one_shot("fastembedr_hip_opentsne_fft_from_device_knn_float", di.address, dd.address, y0, 5, 5,
+                      device=True, shape=idx.shape)
+    finally:
+        di.free()
+        dd.free()
     assert rel_l2(b, a) <= GRAD_TOL
     assert rel_l2(c, a) <= GRAD_TOL
 
