@@ -49,6 +49,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--grid", type=int, default=0, help="grid nodes per axis; 0 = reference CPU policy")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="run one device-to-device copy of this size first (counter calibration under rocprofv3)")
     return ap.parse_args()
 
 
@@ -67,6 +69,15 @@ def main() -> int:
     if not fe.available():
         log("no gfx950 device visible to the HIP backend")
         return 1
+    if args.calibrate_copy_mib > 0:
+        # A plain copy kernel of known size: its FETCH_SIZE / WRITE_SIZE under
+        # rocprofv3 give the factor between counter units and bytes.
+        src = torch.ones(args.calibrate_copy_mib * (1 << 18), dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {src.numel() * 4} bytes read, {dst.numel() * 4} bytes written")
+        del src, dst
     sched = synthetic.SCHEDULE
     spec = synthetic.CONFIGS[args.config]
     n = args.n or spec.n
@@ -128,13 +139,15 @@ def main() -> int:
     per_kernel = {name: (tot / cnt if cnt else 0.0) for name, (cnt, tot) in timing.items()}
     rep_kernels = ["spread", "kernel_rows", "kernel_cols", "charge_rows", "conv_cols", "inverse_rows"]
     rep_ms = sum(per_kernel[kname] for kname in rep_kernels)
-    dom = "attract_update"
+    dom = max(timing, key=lambda kname: timing[kname][1])  # largest total time in the timed region
     dom_ms = per_kernel[dom]
-    # Algorithmic bytes of one attract_update launch: CSR col + val streamed
-    # once (8 nnz), row pointers (4 (n + 1)), and the fused update's point
-    # state: y_i, gains, update read (24 n) and written (24 n).  Neighbour
-    # gathers and grid reads are cache-resident and not counted.
-    dom_bytes = 8.0 * nnz + 4.0 * (n + 1) + 48.0 * n
+    # Algorithmic bytes per launch.  attract: CSR col + val streamed once
+    # (8 nnz), row pointers (4 (n + 1)), y_i read and the row sum written
+    # (16 n); neighbour gathers y_j are counted as cache-resident, as the
+    # grid reads are.  update: y_i, attraction, gains, update read (32 n) and
+    # y, gains, update written (24 n).
+    alg_bytes = {"attract": 8.0 * nnz + 4.0 * (n + 1) + 16.0 * n, "update": 56.0 * n}
+    dom_bytes = alg_bytes.get(dom, 0.0)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9 if dom_ms > 0 else 0.0
     log(f"{its:.1f} it/s, {ms_per_step:.3f} ms/step, repulsion {rep_ms:.3f} ms, {dom} {dom_ms:.3f} ms "
         f"({achieved:.0f} GB/s)")

@@ -129,20 +129,10 @@ __device__ double block_sum(double v) {
   return t;
 }
 
-// "Last block done": publishes this block's partial, and returns true in the
-// block that arrives last (after an acquire fence, so every partial is visible).
-__device__ bool arrive_last(unsigned int* ticket) {
-  __shared__ bool last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned int t = atomicAdd(ticket, 1u);
-    last = (t == gridDim.x - 1);
-  }
-  __syncthreads();
-  if (last) __threadfence();
-  return last;
-}
+// Grid-wide reductions write one partial per block and are finished by a
+// separate single-block kernel.  (A "last block done" finish would need a
+// device-scope release fence in every block, which on multi-XCD parts writes
+// back the L2 each time.)
 
 // Grid geometry from the bounding box and mean of the stored layout
 // (src/tsne_neighbors.cpp:1089-1110 and :1200-1211).  Subtracting a constant
@@ -178,27 +168,19 @@ __device__ void set_geometry(DeviceScalars* sc, const BlockStats& t, int n, int 
 }
 
 template <int NT>
-__device__ void finish_stats(BlockStats local, BlockStats* partial, DeviceScalars* sc, int n, int g, bool center) {
+__device__ void publish_stats(BlockStats local, BlockStats* partial) {
   BlockStats s = block_stats<NT>(local);
   if (threadIdx.x == 0) partial[blockIdx.x] = s;
-  if (!arrive_last(&sc->ticket_stats)) return;
+}
+
+// Reduces the per-block statistics in a fixed order (deterministic) and sets
+// the grid geometry.
+__global__ __launch_bounds__(256) void k_finalize_stats(const BlockStats* __restrict__ partial, int blocks,
+                                                        DeviceScalars* sc, int n, int g, int center) {
   BlockStats acc = stats_identity();
-  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += NT) {
-    const BlockStats* src = partial + b;
-    BlockStats o;
-    o.min_x = __builtin_nontemporal_load(&src->min_x);
-    o.max_x = __builtin_nontemporal_load(&src->max_x);
-    o.min_y = __builtin_nontemporal_load(&src->min_y);
-    o.max_y = __builtin_nontemporal_load(&src->max_y);
-    o.sum_x = __builtin_nontemporal_load(&src->sum_x);
-    o.sum_y = __builtin_nontemporal_load(&src->sum_y);
-    combine(acc, o);
-  }
-  acc = block_stats<NT>(acc);
-  if (threadIdx.x == 0) {
-    set_geometry(sc, acc, n, g, center);
-    sc->ticket_stats = 0u;
-  }
+  for (int b = threadIdx.x; b < blocks; b += 256) combine(acc, partial[b]);
+  acc = block_stats<256>(acc);
+  if (threadIdx.x == 0) set_geometry(sc, acc, n, g, center != 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -363,7 +345,7 @@ __global__ __launch_bounds__(kPointThreads) void k_stats(const float2* __restric
     s.sum_x += static_cast<double>(v.x);
     s.sum_y += static_cast<double>(v.y);
   }
-  finish_stats<kPointThreads>(s, partial, sc, n, g, center != 0);
+  publish_stats<kPointThreads>(s, partial);
 }
 
 // Bilinear weights of one point, exactly as the reference computes them
@@ -920,15 +902,18 @@ __global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__
   }
   acc = block_sum<S::NT>(acc);
   if (threadIdx.x == 0) partial[blockIdx.x] = acc;
-  if (!arrive_last(&sc->ticket_sumq)) return;
+}
+
+// sum_q and its fp32 reciprocal normaliser (src/tsne_neighbors.cpp:1160-1163).
+__global__ __launch_bounds__(256) void k_finalize_sumq(const double* __restrict__ partial, int blocks, int n,
+                                                       DeviceScalars* sc) {
   double tot = 0.0;
-  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += S::NT) tot += __builtin_nontemporal_load(partial + b);
-  tot = block_sum<S::NT>(tot);
+  for (int b = threadIdx.x; b < blocks; b += 256) tot += partial[b];
+  tot = block_sum<256>(tot);
   if (threadIdx.x == 0) {
     sc->sum_q = tot;
     const double z = tot - static_cast<double>(n);
     sc->inv_sum_q = static_cast<float>(1.0 / (z > static_cast<double>(FLT_MIN) ? z : static_cast<double>(FLT_MIN)));
-    sc->ticket_sumq = 0u;
   }
 }
 
@@ -943,75 +928,55 @@ __device__ __forceinline__ float blend(float v00, float v10, float v01, float v1
   return (1.0f - tx) * (1.0f - ty) * v00 + tx * (1.0f - ty) * v10 + (1.0f - tx) * ty * v01 + tx * ty * v11;
 }
 
-// L lanes per CSR row: col/val streamed in L-wide coalesced segments, y_j
-// gathered, a shuffle reduction per row.  The row's leader then adds the
-// grid repulsion (or an exact one) and applies the update.
-template <int MODE, int L>
+// Attraction, one CSR row per L lanes: col/val streamed in L-wide coalesced
+// segments, kUnroll gathers of y_j in flight per lane, a shuffle reduction
+// per row, and the row sum written out (src/tsne_neighbors.cpp:985-1012).
+// Only this loop is in the kernel, so it keeps few registers and a high
+// occupancy, which is what hides the gather latency.
+//
+// XCD-aware row mapping: workgroups are dispatched round-robin over the
+// XCDs, so block b runs on XCD b % xcds.  Each XCD is given one contiguous
+// range of row groups; with points numbered cluster-contiguously, the y_j
+// that an XCD gathers then stay within about 1/xcds of y and hit its own L2.
+constexpr int kUnroll = 8;
+
+template <int L>
 __global__ __launch_bounds__(256) void k_attract(const int* __restrict__ row_ptr, const int* __restrict__ col,
                                                  const float* __restrict__ val, const float2* __restrict__ y_cur,
-                                                 float2* __restrict__ y_out, float2* __restrict__ update,
-                                                 float2* __restrict__ gains, float2* __restrict__ grad_out,
-                                                 const float2* __restrict__ exact_rep,
-                                                 const float4* __restrict__ field, int g, UpdateParams up,
-                                                 BlockStats* __restrict__ partial, DeviceScalars* sc, int n) {
+                                                 float2* __restrict__ attr, float exaggeration, int n, int xcds) {
   constexpr int RPB = 256 / L;
-  const DeviceScalars s = *sc;
   const int lane = threadIdx.x & (L - 1);
-  BlockStats st = stats_identity();
-  const float inv_exact = (MODE == kModeGradientExact)
-                              ? static_cast<float>(1.0 / (s.exact_z > static_cast<double>(FLT_MIN)
-                                                              ? s.exact_z
-                                                              : static_cast<double>(FLT_MIN)))
-                              : 0.0f;
-  for (int base = blockIdx.x * RPB; base < n; base += gridDim.x * RPB) {
-    const int i = base + threadIdx.x / L;
-    const bool row_ok = i < n;
+  const int groups = (n + RPB - 1) / RPB;
+  const int xcd = static_cast<int>(blockIdx.x) % xcds;
+  const int blocks_per_xcd = static_cast<int>(gridDim.x) / xcds;
+  const int per_xcd = (groups + xcds - 1) / xcds;
+  const int g_end = min(groups, (xcd + 1) * per_xcd);
+  for (int grp = xcd * per_xcd + static_cast<int>(blockIdx.x) / xcds; grp < g_end; grp += blocks_per_xcd) {
+    const int i = grp * RPB + threadIdx.x / L;
     float ax = 0.0f, ay = 0.0f;
-    float2 yi = make_float2(0.0f, 0.0f);
-    // Leader-only loads are issued before the neighbour loop so that their
-    // latency overlaps it.
-    const bool leader = lane == 0 && row_ok;
-    Bilinear b{0, 0, 0.0f, 0.0f};
-    float4 f00 = make_float4(0.f, 0.f, 0.f, 0.f), f10 = f00, f01 = f00, f11 = f00;
-    float2 gn = make_float2(1.0f, 1.0f), u = make_float2(0.0f, 0.0f);
-    if (row_ok) {
-      yi = y_cur[i];
-      if (leader) {
-        if (MODE != kModeGradientExact) {
-          b = locate(yi.x, yi.y, s, g);
-          const int a00 = b.y0 * g + b.x0;
-          f00 = field[a00];
-          f10 = field[a00 + 1];
-          f01 = field[a00 + g];
-          f11 = field[a00 + g + 1];
-        }
-        if (MODE == kModeUpdate) {
-          gn = gains[i];
-          u = update[i];
-        }
-      }
+    if (i < n) {
+      const float2 yi = y_cur[i];
       const int e1 = row_ptr[i + 1];
-      // Four independent gathers in flight per lane; out-of-row slots point
-      // at row i itself with p = 0 and contribute nothing.
-      for (int e = row_ptr[i] + lane; e < e1; e += 4 * L) {
-        int j[4];
-        float p[4];
+      // Out-of-row slots point at row i itself with p = 0: no contribution.
+      for (int e = row_ptr[i] + lane; e < e1; e += kUnroll * L) {
+        int j[kUnroll];
+        float p[kUnroll];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < kUnroll; ++q) {
           const int eq = e + q * L;
           const bool ok = eq < e1;
           j[q] = ok ? col[eq] : i;
           p[q] = ok ? val[eq] : 0.0f;
         }
-        float2 yj[4];
+        float2 yj[kUnroll];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) yj[q] = y_cur[j[q]];
+        for (int q = 0; q < kUnroll; ++q) yj[q] = y_cur[j[q]];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < kUnroll; ++q) {
           const float dx = yi.x - yj[q].x;
           const float dy = yi.y - yj[q].y;
           const float qq = 1.0f / (1.0f + (dx * dx + dy * dy));
-          const float c = up.exaggeration * p[q] * qq;
+          const float c = exaggeration * p[q] * qq;
           ax += c * dx;
           ay += c * dy;
         }
@@ -1022,66 +987,96 @@ __global__ __launch_bounds__(256) void k_attract(const int* __restrict__ row_ptr
       ax += __shfl_xor(ax, off, L);
       ay += __shfl_xor(ay, off, L);
     }
-    if (!leader) continue;
-    float gx, gy;
-    {
+    if (lane == 0 && i < n) attr[i] = make_float2(ax, ay);
+  }
+}
+
+// Point-parallel second half of an iteration: the grid repulsion read back
+// at the point (src/tsne_neighbors.cpp:1165-1180) or an exact one, plus the
+// attraction, gives the gradient; then the gains/momentum/step-clip update
+// (src/tsne_neighbors.cpp:1217-1256), and the bounding box and fp64 mean of
+// the new layout for the next iteration's centring and grid.
+template <int MODE>
+__global__ __launch_bounds__(kPointThreads) void k_update(const float2* __restrict__ y_cur,
+                                                          const float2* __restrict__ attr,
+                                                          float2* __restrict__ y_out, float2* __restrict__ update,
+                                                          float2* __restrict__ gains, float2* __restrict__ grad_out,
+                                                          const float2* __restrict__ exact_rep,
+                                                          const float4* __restrict__ field, int g, UpdateParams up,
+                                                          BlockStats* __restrict__ partial, DeviceScalars* sc,
+                                                          int n) {
 #pragma clang fp contract(off)
-      if (MODE == kModeGradientExact) {
-        const float2 r = exact_rep[i];
-        gx = r.x * inv_exact;
-        gy = r.y * inv_exact;
-      } else {
-        const float q2 = blend(f00.x, f10.x, f01.x, f11.x, b.tx, b.ty);
-        const float xq2 = blend(f00.y, f10.y, f01.y, f11.y, b.tx, b.ty);
-        const float yq2 = blend(f00.z, f10.z, f01.z, f11.z, b.tx, b.ty);
-        gx = -(yi.x * q2 - xq2) * s.inv_sum_q;
-        gy = -(yi.y * q2 - yq2) * s.inv_sum_q;
-      }
-      gx += ax;
-      gy += ay;
+  const DeviceScalars s = *sc;
+  BlockStats st = stats_identity();
+  const float inv_exact = (MODE == kModeGradientExact)
+                              ? static_cast<float>(1.0 / (s.exact_z > static_cast<double>(FLT_MIN)
+                                                              ? s.exact_z
+                                                              : static_cast<double>(FLT_MIN)))
+                              : 0.0f;
+  for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += gridDim.x * kPointThreads) {
+    const float2 yi = y_cur[i];
+    const float2 a = attr[i];
+    float gx, gy;
+    if (MODE == kModeGradientExact) {
+      const float2 r = exact_rep[i];
+      gx = r.x * inv_exact;
+      gy = r.y * inv_exact;
+    } else {
+      const Bilinear b = locate(yi.x, yi.y, s, g);
+      const int a00 = b.y0 * g + b.x0;
+      const float4 f00 = field[a00];
+      const float4 f10 = field[a00 + 1];
+      const float4 f01 = field[a00 + g];
+      const float4 f11 = field[a00 + g + 1];
+      const float q2 = blend(f00.x, f10.x, f01.x, f11.x, b.tx, b.ty);
+      const float xq2 = blend(f00.y, f10.y, f01.y, f11.y, b.tx, b.ty);
+      const float yq2 = blend(f00.z, f10.z, f01.z, f11.z, b.tx, b.ty);
+      gx = -(yi.x * q2 - xq2) * s.inv_sum_q;
+      gy = -(yi.y * q2 - yq2) * s.inv_sum_q;
     }
+    gx += a.x;
+    gy += a.y;
     if (MODE != kModeUpdate) {
       grad_out[i] = make_float2(gx, gy);
       continue;
     }
-    {
-#pragma clang fp contract(off)
-      if (sign0(u.x) != sign0(gx)) {
-        gn.x += 0.2f;
-      } else {
-        gn.x = gn.x * 0.8f + up.min_gain;
-      }
-      if (gn.x < up.min_gain) gn.x = up.min_gain;
-      u.x = up.momentum * u.x - up.learning_rate * gn.x * gx;
-      float norm_sq = 0.0f;
-      norm_sq += u.x * u.x;
-      if (sign0(u.y) != sign0(gy)) {
-        gn.y += 0.2f;
-      } else {
-        gn.y = gn.y * 0.8f + up.min_gain;
-      }
-      if (gn.y < up.min_gain) gn.y = up.min_gain;
-      u.y = up.momentum * u.y - up.learning_rate * gn.y * gy;
-      norm_sq += u.y * u.y;
-      float scale = 1.0f;
-      if (up.clip && norm_sq > up.max_step_norm * up.max_step_norm) {
-        scale = up.max_step_norm / sqrtf(fmaxf(norm_sq, FLT_MIN));
-      }
-      u.x *= scale;
-      u.y *= scale;
-      const float2 yn = make_float2(yi.x + u.x, yi.y + u.y);
-      gains[i] = gn;
-      update[i] = u;
-      y_out[i] = yn;
-      st.min_x = fminf(st.min_x, yn.x);
-      st.max_x = fmaxf(st.max_x, yn.x);
-      st.min_y = fminf(st.min_y, yn.y);
-      st.max_y = fmaxf(st.max_y, yn.y);
-      st.sum_x += static_cast<double>(yn.x);
-      st.sum_y += static_cast<double>(yn.y);
+    float2 gn = gains[i];
+    float2 u = update[i];
+    if (sign0(u.x) != sign0(gx)) {
+      gn.x += 0.2f;
+    } else {
+      gn.x = gn.x * 0.8f + up.min_gain;
     }
+    if (gn.x < up.min_gain) gn.x = up.min_gain;
+    u.x = up.momentum * u.x - up.learning_rate * gn.x * gx;
+    float norm_sq = 0.0f;
+    norm_sq += u.x * u.x;
+    if (sign0(u.y) != sign0(gy)) {
+      gn.y += 0.2f;
+    } else {
+      gn.y = gn.y * 0.8f + up.min_gain;
+    }
+    if (gn.y < up.min_gain) gn.y = up.min_gain;
+    u.y = up.momentum * u.y - up.learning_rate * gn.y * gy;
+    norm_sq += u.y * u.y;
+    float scale = 1.0f;
+    if (up.clip && norm_sq > up.max_step_norm * up.max_step_norm) {
+      scale = up.max_step_norm / sqrtf(fmaxf(norm_sq, FLT_MIN));
+    }
+    u.x *= scale;
+    u.y *= scale;
+    const float2 yn = make_float2(yi.x + u.x, yi.y + u.y);
+    gains[i] = gn;
+    update[i] = u;
+    y_out[i] = yn;
+    st.min_x = fminf(st.min_x, yn.x);
+    st.max_x = fmaxf(st.max_x, yn.x);
+    st.min_y = fminf(st.min_y, yn.y);
+    st.max_y = fmaxf(st.max_y, yn.y);
+    st.sum_x += static_cast<double>(yn.x);
+    st.sum_y += static_cast<double>(yn.y);
   }
-  if (MODE == kModeUpdate) finish_stats<256>(st, partial, sc, n, g, true);
+  if (MODE == kModeUpdate) publish_stats<kPointThreads>(st, partial);
 }
 
 // ---------------------------------------------------------------------------
@@ -1119,14 +1114,14 @@ __global__ __launch_bounds__(256) void k_exact_rep(const float2* __restrict__ y,
   if (i < n) rep[i] = make_float2(rx, ry);
   z = block_sum<256>(z);
   if (threadIdx.x == 0) partial[blockIdx.x] = z;
-  if (!arrive_last(&sc->ticket_exact)) return;
+}
+
+__global__ __launch_bounds__(256) void k_finalize_exact(const double* __restrict__ partial, int blocks,
+                                                        DeviceScalars* sc) {
   double tot = 0.0;
-  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += 256) tot += __builtin_nontemporal_load(partial + b);
+  for (int b = threadIdx.x; b < blocks; b += 256) tot += partial[b];
   tot = block_sum<256>(tot);
-  if (threadIdx.x == 0) {
-    sc->exact_z = tot;
-    sc->ticket_exact = 0u;
-  }
+  if (threadIdx.x == 0) sc->exact_z = tot;
 }
 
 // sum_{i != j} 1 / (1 + |y_i - y_j|^2) with the squared distance in fp32 and
@@ -1194,10 +1189,14 @@ __device__ __forceinline__ unsigned int spread_bits16(unsigned int v) {
   return v;
 }
 
-// 32-bit Morton key of each point on a 65536^2 lattice over the bounding box
-// of the layout (stored values minus the pending centring shift).
+// Sort key of each point: its connected component in the high 32 bits (so
+// components are numbered contiguously), then the 32-bit Morton code of its
+// position on a 65536^2 lattice over the bounding box of the layout (stored
+// values minus the pending centring shift).
 __global__ __launch_bounds__(kPointThreads) void k_morton_keys(const float2* __restrict__ y, const DeviceScalars* sc,
-                                                               int n, unsigned int* __restrict__ keys,
+                                                               int n, const int* __restrict__ component,
+                                                               const int* __restrict__ perm,
+                                                               unsigned long long* __restrict__ keys,
                                                                int* __restrict__ idx) {
   const DeviceScalars s = *sc;
   const float sx = fmaxf(s.max_x - s.min_x, 1e-30f);
@@ -1208,8 +1207,34 @@ __global__ __launch_bounds__(kPointThreads) void k_morton_keys(const float2* __r
     const float uy = fminf(fmaxf((v.y - s.shift_y - s.min_y) / sy, 0.0f), 1.0f);
     const unsigned int qx = static_cast<unsigned int>(ux * 65535.0f);
     const unsigned int qy = static_cast<unsigned int>(uy * 65535.0f);
-    keys[i] = spread_bits16(qx) | (spread_bits16(qy) << 1);
+    const unsigned long long comp = static_cast<unsigned long long>(component[perm[i]]);
+    keys[i] = (comp << 32) | (spread_bits16(qx) | (spread_bits16(qy) << 1));
     idx[i] = i;
+  }
+}
+
+__global__ __launch_bounds__(kPointThreads) void k_label_init(int* __restrict__ label, int n) {
+  for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += gridDim.x * kPointThreads) label[i] = i;
+}
+
+// One min-label propagation sweep (a wave per row) followed in the same pass
+// by pointer jumping.  Labels only decrease and always name a member of the
+// same component, so concurrent reads of partly updated labels are safe.
+__global__ __launch_bounds__(256) void k_label_step(const int* __restrict__ row_ptr, const int* __restrict__ col,
+                                                    int* label, int* changed, int n) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int i = (blockIdx.x * 256 + threadIdx.x) / kWave; i < n; i += gridDim.x * (256 / kWave)) {
+    int m = label[i];
+    for (int e = row_ptr[i] + lane; e < row_ptr[i + 1]; e += kWave) m = min(m, label[col[e]]);
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) m = min(m, __shfl_xor(m, off, kWave));
+    if (lane == 0) {
+      m = min(m, label[m]);
+      if (m < label[i]) {
+        label[i] = m;
+        *changed = 1;
+      }
+    }
   }
 }
 
@@ -1289,6 +1314,7 @@ hipError_t grid_fft_launch(int which, GridBuffers& gb, const DeviceScalars* sc_c
       k_inverse_rows<F><<<(S::G + S::CROWS - 1) / S::CROWS, S::NT, 0, stream>>>(
           gb.x_rows, gb.v1_rows, gb.v2_rows, gb.y_rows, tw, gb.mass, gb.mass_x, gb.mass_y, gb.field,
           gb.sumq_partial, n, sc);
+      k_finalize_sumq<<<1, 256, 0, stream>>>(gb.sumq_partial, (S::G + S::CROWS - 1) / S::CROWS, n, sc);
       break;
     default:
       return hipErrorInvalidValue;
@@ -1309,29 +1335,26 @@ hipError_t grid_fft_dispatch(int which, GridBuffers& gb, DeviceScalars* sc, cons
   }
 }
 
-template <int MODE, int L>
-hipError_t attract_launch(const Csr& p, const float2* y_cur, float2* y_out, float2* update, float2* gains,
-                          float2* grad_out, const float2* exact_rep, const GridBuffers& gb, const UpdateParams& up,
-                          BlockStats* partial, DeviceScalars* sc, hipStream_t stream) {
+template <int L>
+hipError_t attract_launch(const Csr& p, const float2* y_cur, float2* attr, float exaggeration, int xcds,
+                          hipStream_t stream) {
   constexpr int RPB = 256 / L;
   const int needed = (p.n + RPB - 1) / RPB;
-  const int blocks = needed < 2048 ? needed : 2048;
-  k_attract<MODE, L><<<blocks, 256, 0, stream>>>(p.row_ptr, p.col, p.val, y_cur, y_out, update, gains, grad_out,
-                                                 exact_rep, gb.field, gb.g, up, partial, sc, p.n);
+  // a whole number of blocks per XCD
+  const int blocks = std::max(xcds, (std::min(needed, 4096) / xcds) * xcds);
+  k_attract<L><<<blocks, 256, 0, stream>>>(p.row_ptr, p.col, p.val, y_cur, attr, exaggeration, p.n, xcds);
   return hipGetLastError();
 }
 
 template <int MODE>
-hipError_t attract_lanes(int lanes, const Csr& p, const float2* y_cur, float2* y_out, float2* update,
-                         float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
-                         const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, hipStream_t stream) {
-  switch (lanes) {
-    case 8: return attract_launch<MODE, 8>(p, y_cur, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc, stream);
-    case 16: return attract_launch<MODE, 16>(p, y_cur, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc, stream);
-    case 32: return attract_launch<MODE, 32>(p, y_cur, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc, stream);
-    case 64: return attract_launch<MODE, 64>(p, y_cur, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc, stream);
-    default: return hipErrorInvalidValue;
-  }
+hipError_t update_launch(const float2* y_cur, const float2* attr, float2* y_out, float2* update, float2* gains,
+                         float2* grad_out, const float2* exact_rep, const GridBuffers& gb, const UpdateParams& up,
+                         BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream) {
+  const int blocks = reduce_blocks_for(n);
+  k_update<MODE><<<blocks, kPointThreads, 0, stream>>>(y_cur, attr, y_out, update, gains, grad_out, exact_rep,
+                                                       gb.field, gb.g, up, partial, sc, n);
+  if (MODE == kModeUpdate) k_finalize_stats<<<1, 256, 0, stream>>>(partial, blocks, sc, n, gb.g, 1);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -1395,7 +1418,9 @@ int reduce_blocks_for(int n) {
 
 hipError_t launch_stats(const float2* y, int n, int g, int center, BlockStats* partial, DeviceScalars* sc,
                         hipStream_t stream) {
-  k_stats<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(y, n, g, center, partial, sc);
+  const int blocks = reduce_blocks_for(n);
+  k_stats<<<blocks, kPointThreads, 0, stream>>>(y, n, g, center, partial, sc);
+  k_finalize_stats<<<1, 256, 0, stream>>>(partial, blocks, sc, n, g, center);
   return hipGetLastError();
 }
 
@@ -1446,20 +1471,30 @@ hipError_t launch_inverse_rows(GridBuffers& gb, const float2* tw, int n, DeviceS
   return grid_fft_dispatch(4, gb, sc, tw, n, stream);
 }
 
-hipError_t launch_attract(int mode, const Csr& p, const float2* y_cur, float2* y_out, float2* update,
-                          float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
-                          const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int lanes_per_row,
-                          hipStream_t stream) {
+hipError_t launch_attract(const Csr& p, const float2* y_cur, float2* attr, float exaggeration, int lanes_per_row,
+                          int xcds, hipStream_t stream) {
+  switch (lanes_per_row) {
+    case 8: return attract_launch<8>(p, y_cur, attr, exaggeration, xcds, stream);
+    case 16: return attract_launch<16>(p, y_cur, attr, exaggeration, xcds, stream);
+    case 32: return attract_launch<32>(p, y_cur, attr, exaggeration, xcds, stream);
+    case 64: return attract_launch<64>(p, y_cur, attr, exaggeration, xcds, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_update(int mode, const float2* y_cur, const float2* attr, float2* y_out, float2* update,
+                         float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
+                         const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream) {
   switch (mode) {
     case kModeUpdate:
-      return attract_lanes<kModeUpdate>(lanes_per_row, p, y_cur, y_out, update, gains, grad_out, exact_rep, gb, up,
-                                        partial, sc, stream);
+      return update_launch<kModeUpdate>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc,
+                                        n, stream);
     case kModeGradientGrid:
-      return attract_lanes<kModeGradientGrid>(lanes_per_row, p, y_cur, y_out, update, gains, grad_out, exact_rep,
-                                              gb, up, partial, sc, stream);
+      return update_launch<kModeGradientGrid>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up,
+                                              partial, sc, n, stream);
     case kModeGradientExact:
-      return attract_lanes<kModeGradientExact>(lanes_per_row, p, y_cur, y_out, update, gains, grad_out, exact_rep,
-                                               gb, up, partial, sc, stream);
+      return update_launch<kModeGradientExact>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up,
+                                               partial, sc, n, stream);
     default:
       return hipErrorInvalidValue;
   }
@@ -1472,9 +1507,10 @@ hipError_t launch_commit(float2* y, const DeviceScalars* sc, int n, hipStream_t 
 
 hipError_t renumber_temp_bytes(int n, std::size_t& bytes) {
   std::size_t sort_b = 0, scan_b = 0;
-  hipError_t e = rocprim::radix_sort_pairs(nullptr, sort_b, static_cast<const unsigned int*>(nullptr),
-                                           static_cast<unsigned int*>(nullptr), static_cast<const int*>(nullptr),
-                                           static_cast<int*>(nullptr), static_cast<std::size_t>(n), 0u, 32u);
+  hipError_t e = rocprim::radix_sort_pairs(nullptr, sort_b, static_cast<const unsigned long long*>(nullptr),
+                                           static_cast<unsigned long long*>(nullptr),
+                                           static_cast<const int*>(nullptr), static_cast<int*>(nullptr),
+                                           static_cast<std::size_t>(n), 0u, 64u);
   if (e != hipSuccess) return e;
   e = rocprim::exclusive_scan(nullptr, scan_b, static_cast<const int*>(nullptr), static_cast<int*>(nullptr), 0,
                               static_cast<std::size_t>(n) + 1, rocprim::plus<int>());
@@ -1483,14 +1519,27 @@ hipError_t renumber_temp_bytes(int n, std::size_t& bytes) {
 }
 
 hipError_t launch_morton_keys(const float2* y, const DeviceScalars* sc, int n, Renumber& r, hipStream_t stream) {
-  k_morton_keys<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(y, sc, n, r.keys_in, r.idx_in);
+  k_morton_keys<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(y, sc, n, r.component, r.perm, r.keys_in,
+                                                                    r.idx_in);
   return hipGetLastError();
 }
 
 hipError_t sort_morton(Renumber& r, int n, hipStream_t stream) {
   std::size_t tb = r.temp_bytes;
   return rocprim::radix_sort_pairs(r.temp, tb, r.keys_in, r.keys_out, r.idx_in, r.order,
-                                   static_cast<std::size_t>(n), 0u, 32u, stream);
+                                   static_cast<std::size_t>(n), 0u, static_cast<unsigned int>(r.key_bits),
+                                   stream);
+}
+
+hipError_t launch_label_init(int* label, int n, hipStream_t stream) {
+  k_label_init<<<reduce_blocks_for(n), kPointThreads, 0, stream>>>(label, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_label_step(const Csr& p, int* label, int* changed, hipStream_t stream) {
+  const int blocks = std::max(1, std::min((p.n + 3) / 4, 8192));
+  k_label_step<<<blocks, 256, 0, stream>>>(p.row_ptr, p.col, label, changed, p.n);
+  return hipGetLastError();
 }
 
 hipError_t launch_apply_order(const Renumber& r, int n, const int* perm_old, int* perm_new, const float2* y_old,
@@ -1530,6 +1579,7 @@ int exact_blocks_for(int n) { return (n + 255) / 256; }
 hipError_t launch_exact_repulsion(const float2* y, int n, float2* rep, double* z_partial, DeviceScalars* sc,
                                   hipStream_t stream) {
   k_exact_rep<<<exact_blocks_for(n), 256, 0, stream>>>(y, n, rep, z_partial, sc);
+  k_finalize_exact<<<1, 256, 0, stream>>>(z_partial, exact_blocks_for(n), sc);
   return hipGetLastError();
 }
 

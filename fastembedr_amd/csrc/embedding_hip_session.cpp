@@ -115,6 +115,7 @@ struct fastembedr_hip_tsne {
   int n = 0;
   int k = 0;
   int lanes = 16;
+  int xcds = 1;              // XCDs of the device (blocks are dispatched round-robin over them)
   hipStream_t stream = nullptr;
   Arena arena;
   Arena work_arena;         // working-order CSR copies, permutations, state double buffers
@@ -132,8 +133,11 @@ struct fastembedr_hip_tsne {
   int pi = 0;
   int* inv_perm = nullptr;              // caller's index -> working index
   fehip::Renumber rn;
-  int reorder_period = 50;
+  int reorder_period = 25;
+  int reorder_gap = 25;
+  int renumber_count = 0;
   int since_reorder = 0;
+  int label_sweeps = 0;
   float2* y_b = nullptr;    // centred layout of the current iteration (also scratch)
   float2* grad = nullptr;
 
@@ -143,6 +147,7 @@ struct fastembedr_hip_tsne {
   float2* update() const { return us[si]; }
   float2* gains() const { return gs[si]; }
   float2* exact_rep = nullptr;
+  float2* attr = nullptr;   // attractive term per row (working numbering)
   float2* tw = nullptr;
   BlockStats* partial = nullptr;
   double* dpartial = nullptr;
@@ -200,7 +205,7 @@ namespace {
 
 const char* kKernelNames[fehip::kKernelCount] = {
     "stats", "bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols", "charge_rows",
-    "conv_cols", "inverse_rows", "attract_update", "commit", "renumber"};
+    "conv_cols", "inverse_rows", "attract", "update", "commit", "renumber"};
 
 int key_bits_for(int n) {
   int b = 1;
@@ -231,8 +236,8 @@ bool alloc_working_buffers(fastembedr_hip_tsne* s) {
   if (!hip_ok(fehip::renumber_temp_bytes(n, temp), "renumber size query")) return false;
   const std::size_t nn = static_cast<std::size_t>(n);
   const std::size_t bytes = 2 * (align_up((nn + 1) * 4) + align_up(nnz * 4) + align_up(nnz * 4)) +
-                            3 * align_up(nn * 4) + 3 * align_up(nn * sizeof(float2)) + 2 * align_up(nn * 4) +
-                            3 * align_up(nn * 4) + align_up((nn + 1) * 4) + align_up(temp) + 4096;
+                            3 * align_up(nn * 4) + 3 * align_up(nn * sizeof(float2)) + 2 * align_up(nn * 8) +
+                            4 * align_up(nn * 4) + align_up((nn + 1) * 4) + align_up(temp) + 2 * 256 + 4096;
   if (!memory_preflight(bytes, "HIP openTSNE working buffers") ||
       !s->work_arena.init(bytes, "hipMalloc(HIP openTSNE working buffers)")) {
     return false;
@@ -251,22 +256,45 @@ bool alloc_working_buffers(fastembedr_hip_tsne* s) {
   s->ys[1] = a.take<float2>(nn);
   s->us[1] = a.take<float2>(nn);
   s->gs[1] = a.take<float2>(nn);
-  s->rn.keys_in = a.take<unsigned int>(nn);
-  s->rn.keys_out = a.take<unsigned int>(nn);
+  s->rn.keys_in = a.take<unsigned long long>(nn);
+  s->rn.keys_out = a.take<unsigned long long>(nn);
   s->rn.idx_in = a.take<int>(nn);
   s->rn.order = a.take<int>(nn);
   s->rn.map = a.take<int>(nn);
   s->rn.len = a.take<int>(nn + 1);
+  int* component = a.take<int>(nn);
+  int* changed = a.take<int>(1);
+  s->rn.component = component;
   s->rn.temp = a.take<char>(temp);
   s->rn.temp_bytes = temp;
-  if (s->rn.temp == nullptr) {
+  if (s->rn.temp == nullptr || changed == nullptr) {
     set_error("internal: working buffers do not fit their arena");
     return false;
   }
   std::vector<int> iota(nn);
   for (int i = 0; i < n; ++i) iota[static_cast<std::size_t>(i)] = i;
-  return hip_ok(hipMemcpy(s->perm[0], iota.data(), nn * 4, hipMemcpyHostToDevice), "perm init") &&
-         hip_ok(hipMemcpy(s->inv_perm, iota.data(), nn * 4, hipMemcpyHostToDevice), "perm init");
+  if (!hip_ok(hipMemcpy(s->perm[0], iota.data(), nn * 4, hipMemcpyHostToDevice), "perm init") ||
+      !hip_ok(hipMemcpy(s->inv_perm, iota.data(), nn * 4, hipMemcpyHostToDevice), "perm init")) {
+    return false;
+  }
+  // Connected components of P (fixed for the session): renumbering keeps
+  // each component contiguous.  Sort keys use 32 + bits(n) bits.
+  if (!hip_ok(fehip::launch_label_init(component, n, s->stream), "label init")) return false;
+  int flag = 1;
+  for (int sweep = 0; flag != 0 && sweep < 256; ++sweep) {
+    flag = 0;
+    if (!hip_ok(hipMemsetAsync(changed, 0, sizeof(int), s->stream), "label flag") ||
+        !hip_ok(fehip::launch_label_step(s->p, component, changed, s->stream), "label step") ||
+        !hip_ok(hipMemcpyAsync(&flag, changed, sizeof(int), hipMemcpyDeviceToHost, s->stream), "label flag") ||
+        !hip_ok(hipStreamSynchronize(s->stream), "label sync")) {
+      return false;
+    }
+    s->label_sweeps = sweep + 1;
+  }
+  int bits = 1;
+  while ((1LL << bits) <= static_cast<long long>(n)) ++bits;
+  s->rn.key_bits = 32 + bits;
+  return true;
 }
 
 // Renumbers points by the Morton order of the current layout: permutes the
@@ -279,6 +307,7 @@ hipError_t enqueue_renumber(fastembedr_hip_tsne* s) {
   const int next = s->wi < 0 ? 0 : 1 - s->wi;
   const Csr& src = s->work_p();
   Csr& dst = s->pw[next];
+  s->rn.perm = s->perm[s->pi];
   hipError_t e = fehip::launch_morton_keys(s->ys[s->si], s->sc, n, s->rn, s->stream);
   if (e == hipSuccess) e = fehip::sort_morton(s->rn, n, s->stream);
   if (e == hipSuccess)
@@ -293,6 +322,7 @@ hipError_t enqueue_renumber(fastembedr_hip_tsne* s) {
   s->si = 1 - s->si;
   s->pi = 1 - s->pi;
   s->since_reorder = 0;
+  ++s->renumber_count;
   return hipSuccess;
 }
 
@@ -391,7 +421,7 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   const std::size_t hh = static_cast<std::size_t>(g + 1);
   const std::size_t persistent_fixed =
       align_up(sizeof(DeviceScalars)) + align_up(nk * 4) + align_up((n + 1) * sizeof(int)) +
-      6 * align_up(static_cast<std::size_t>(n) * sizeof(float2)) + align_up(fehip::kTwiddleLen * sizeof(float2)) +
+      7 * align_up(static_cast<std::size_t>(n) * sizeof(float2)) + align_up(fehip::kTwiddleLen * sizeof(float2)) +
       align_up(fehip::kMaxReduceBlocks * sizeof(BlockStats)) + align_up(dpart * sizeof(double)) +
       3 * align_up(gg * 4) + align_up(gg * sizeof(float4)) + 2 * align_up(hh * hh * sizeof(float2)) +
       7 * align_up(g * hh * sizeof(float2)) + align_up(fehip::kMaxReduceBlocks * sizeof(double)) +
@@ -445,6 +475,7 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   s->gs[0] = s->arena.take<float2>(n);
   s->grad = s->arena.take<float2>(n);
   s->exact_rep = s->arena.take<float2>(n);
+  s->attr = s->arena.take<float2>(n);
   s->tw = s->arena.take<float2>(fehip::kTwiddleLen);
   s->partial = s->arena.take<BlockStats>(fehip::kMaxReduceBlocks);
   s->dpartial = s->arena.take<double>(dpart);
@@ -562,13 +593,26 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
 
   // Lanes per CSR row: enough to cover the mean row in a few passes.
   const double mean_row = static_cast<double>(nnz) / n;
-  int lanes = mean_row > 24.0 ? 16 : 8;
+  int lanes = mean_row > 96.0 ? 32 : (mean_row > 24.0 ? 16 : 8);
   lanes = env_int("FASTEMBEDR_HIP_ATTRACT_LANES", lanes);
   if (lanes != 8 && lanes != 16 && lanes != 32 && lanes != 64) lanes = 16;
   s->lanes = lanes;
-  s->reorder_period = env_int("FASTEMBEDR_HIP_RENUMBER_PERIOD", 50);
+  // Renumbering: before the first iteration, then after gaps that double from
+  // this value (the layout's coarse structure settles early).
+  s->reorder_period = env_int("FASTEMBEDR_HIP_RENUMBER_PERIOD", 25);
   if (const char* off = std::getenv("FASTEMBEDR_HIP_RENUMBER_PERIOD")) {
     if (std::strcmp(off, "0") == 0) s->reorder_period = 0;
+  }
+  // CDNA3/CDNA4 parts (gfx94x, gfx95x) dispatch workgroups round-robin over 8 XCDs.
+  {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    s->xcds = 1;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+        (std::strncmp(prop.gcnArchName, "gfx94", 5) == 0 || std::strncmp(prop.gcnArchName, "gfx95", 5) == 0)) {
+      s->xcds = 8;
+    }
+    s->xcds = env_int("FASTEMBEDR_HIP_XCDS", s->xcds);
   }
   if (!alloc_working_buffers(s)) {
     delete s;
@@ -825,14 +869,18 @@ int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int
   if (repulsion == FASTEMBEDR_HIP_REPULSION_EXACT) {
     ok = hip_ok(fehip::launch_exact_repulsion(s->y_a(), s->n, s->exact_rep, s->dpartial, s->sc, s->stream),
                 "exact repulsion launch") &&
-         hip_ok(fehip::launch_attract(fehip::kModeGradientExact, s->work_p(), s->y_a(), nullptr, nullptr, nullptr, s->grad,
-                                      s->exact_rep, s->gb, up, s->partial, s->sc, s->lanes, s->stream),
-                "attract launch");
+         hip_ok(fehip::launch_attract(s->work_p(), s->y_a(), s->attr, exaggeration, s->lanes, s->xcds, s->stream),
+                "attract launch") &&
+         hip_ok(fehip::launch_update(fehip::kModeGradientExact, s->y_a(), s->attr, nullptr, nullptr, nullptr, s->grad,
+                                     s->exact_rep, s->gb, up, s->partial, s->sc, s->n, s->stream),
+                "update launch");
   } else if (repulsion == FASTEMBEDR_HIP_REPULSION_GRID) {
     ok = enqueue_gradient_fields(s, true, 0) &&
-         hip_ok(fehip::launch_attract(fehip::kModeGradientGrid, s->work_p(), s->y_b, nullptr, nullptr, nullptr, s->grad,
-                                      nullptr, s->gb, up, s->partial, s->sc, s->lanes, s->stream),
-                "attract launch");
+         hip_ok(fehip::launch_attract(s->work_p(), s->y_b, s->attr, exaggeration, s->lanes, s->xcds, s->stream),
+                "attract launch") &&
+         hip_ok(fehip::launch_update(fehip::kModeGradientGrid, s->y_b, s->attr, nullptr, nullptr, nullptr, s->grad,
+                                     nullptr, s->gb, up, s->partial, s->sc, s->n, s->stream),
+                "update launch");
   } else {
     set_error("unsupported repulsion mode");
     ok = false;
@@ -876,14 +924,18 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
     // Renumber before the first iteration ever run and then every
     // reorder_period iterations; the bounding box and pending shift it needs
     // are in DeviceScalars (stats kernel above, or the previous update).
-    if (s->reorder_period > 0 && (!s->renumbered() || s->since_reorder >= s->reorder_period)) {
+    if (s->reorder_period > 0 && (!s->renumbered() || s->since_reorder >= s->reorder_gap)) {
       if (!s->timed(fehip::kKRenumber, "renumber", [&] { return enqueue_renumber(s); })) return 1;
+      s->reorder_gap = s->renumber_count == 1 ? s->reorder_period : 2 * s->reorder_gap;
     }
     ++s->since_reorder;
     if (!enqueue_gradient_fields(s, false, 0)) return 1;
-    if (!s->timed(fehip::kKAttractUpdate, "attract launch", [&] {
-          return fehip::launch_attract(fehip::kModeUpdate, s->work_p(), s->y_b, s->y_a(), s->update(), s->gains(), nullptr,
-                                       nullptr, s->gb, up, s->partial, s->sc, s->lanes, s->stream);
+    if (!s->timed(fehip::kKAttract, "attract launch", [&] {
+          return fehip::launch_attract(s->work_p(), s->y_b, s->attr, exaggeration, s->lanes, s->xcds, s->stream);
+        }) ||
+        !s->timed(fehip::kKUpdate, "update launch", [&] {
+          return fehip::launch_update(fehip::kModeUpdate, s->y_b, s->attr, s->y_a(), s->update(), s->gains(),
+                                      nullptr, nullptr, s->gb, up, s->partial, s->sc, n, s->stream);
         })) {
       return 1;
     }

@@ -10,8 +10,9 @@
 namespace fehip {
 
 // Per-session scalars that the kernels read and write on the device, so that
-// an iteration never waits for the host.  Written by the "last block" of the
-// reductions (stats -> geometry, inverse rows -> sum of q).
+// an iteration never waits for the host.  Written by the single-block
+// finalize kernels of the reductions (stats -> geometry, inverse rows -> sum
+// of q, exact repulsion -> its normaliser).
 struct alignas(16) DeviceScalars {
   float shift_x, shift_y;   // subtracted from the stored layout to centre it
   float lo_x, lo_y;         // grid origin in centred coordinates
@@ -23,10 +24,8 @@ struct alignas(16) DeviceScalars {
   float min_x, max_x, min_y, max_y;  // bounding box of the centred layout
   double exact_z;           // exact-repulsion normaliser (pairs i != j)
   double total_mass;        // sum of directed p_{j|i} over non-self columns
-  unsigned int ticket_stats;
-  unsigned int ticket_sumq;
-  unsigned int ticket_exact;
   unsigned int error_flags;  // bit 0: index out of range, bit 1: bad distance
+  unsigned int pad2;
   unsigned long long self_edges;
   int num_items;             // spread work items of the current iteration
   int pad1;
@@ -65,7 +64,8 @@ enum KernelId : int {
   kKChargeRows,
   kKConvCols,
   kKInverseRows,
-  kKAttractUpdate,
+  kKAttract,
+  kKUpdate,
   kKCommit,
   kKRenumber,
   kKernelCount
@@ -147,9 +147,14 @@ struct UpdateParams {
   float max_step_norm;
   int clip;
 };
-hipError_t launch_attract(int mode, const Csr& p, const float2* y_cur, float2* y_out, float2* update, float2* gains,
-                          float2* grad_out, const float2* exact_rep, const GridBuffers& gb, const UpdateParams& up,
-                          BlockStats* partial, DeviceScalars* sc, int lanes_per_row, hipStream_t stream);
+// Row sums of the attractive term into attr (n float2).
+hipError_t launch_attract(const Csr& p, const float2* y_cur, float2* attr, float exaggeration, int lanes_per_row,
+                          int xcds, hipStream_t stream);
+// Repulsion read-back + attr -> gradient; kModeUpdate applies the update and
+// computes the next iteration's statistics, the gradient modes write grad_out.
+hipError_t launch_update(int mode, const float2* y_cur, const float2* attr, float2* y_out, float2* update,
+                         float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
+                         const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream);
 hipError_t launch_commit(float2* y, const DeviceScalars* sc, int n, hipStream_t stream);
 
 // ---- locality renumbering ---------------------------------------------------
@@ -157,8 +162,12 @@ hipError_t launch_commit(float2* y, const DeviceScalars* sc, int n, hipStream_t 
 // CSR neighbours sit close in memory.  `order[q]` is the old working index of
 // new index q; perm maps working -> original indices.
 struct Renumber {
-  unsigned int* keys_in = nullptr;
-  unsigned int* keys_out = nullptr;
+  // key = (connected component of the point << 32) | Morton code of its position
+  unsigned long long* keys_in = nullptr;
+  unsigned long long* keys_out = nullptr;
+  const int* component = nullptr;  // per point, caller's numbering
+  const int* perm = nullptr;       // current working -> caller's index
+  int key_bits = 64;
   int* idx_in = nullptr;
   int* order = nullptr;
   int* map = nullptr;   // old working index -> new working index
@@ -175,6 +184,10 @@ hipError_t launch_apply_order(const Renumber& r, int n, const int* perm_old, int
 hipError_t scan_row_lengths(Renumber& r, int n, int* rp_new, hipStream_t stream);
 hipError_t launch_copy_rows(const Renumber& r, int n, const Csr& src, Csr& dst, hipStream_t stream);
 hipError_t launch_invert(const int* perm, int* inv, int n, hipStream_t stream);
+// Connected components of the P graph by min-label propagation with pointer
+// jumping; label[i] ends as the smallest index of i's component.
+hipError_t launch_label_init(int* label, int n, hipStream_t stream);
+hipError_t launch_label_step(const Csr& p, int* label, int* changed, hipStream_t stream);
 hipError_t launch_gather2(const float2* src, const int* idx, float2* dst, int n, hipStream_t stream);
 
 // ---- exact O(n^2) terms (gradient check and KL) ----------------------------
