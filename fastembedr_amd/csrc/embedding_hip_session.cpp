@@ -701,8 +701,8 @@ int one_shot(const int* indices, const DT* distances, const float* init, int has
   int rc = fastembedr_hip_tsne_set_state(s, y0.data(), nullptr, nullptr);
   if (rc == 0) rc = fastembedr_hip_tsne_center(s);
   const auto phase_lr = [&](float ex) {
-    return learning_rate_auto ? static_cast<float>(static_cast<double>(n) / std::max(static_cast<double>(ex), DBL_MIN))
-                              : learning_rate;
+    // fp32 n / exaggeration, as the reference computes it (src/embedding_cuda_kernels.cpp:5908-5913)
+    return learning_rate_auto ? static_cast<float>(n) / ex : learning_rate;
   };
   if (rc == 0 && early_exaggeration_iter > 0) {
     rc = fastembedr_hip_tsne_run(s, early_exaggeration_iter, early_exaggeration, initial_momentum,

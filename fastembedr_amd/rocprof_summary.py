@@ -1,0 +1,118 @@
+"""Digest of rocprofv3 CSV output into the short text summaries kept under
+profiles/ (kernel durations and HBM traffic per dispatch).
+
+    python -m fastembedr_amd.rocprof_summary trace  <kt_dir>   <command> > profiles/<name>.txt
+    python -m fastembedr_amd.rocprof_summary traffic <fetch_dir> <write_dir> <command> \
+        --json profiles/<name>.json > profiles/<name>.txt
+
+Counter units: FETCH_SIZE and WRITE_SIZE are read in KiB per dispatch and
+scaled by what the same counter reads for a device-to-device copy of known
+size in the same run (bench.py --calibrate-copy-mib).  On MI355X with
+rocprofv3 (ROCm 7.x) a 512 MiB copy reads FETCH_SIZE = 262,162 KiB and
+WRITE_SIZE = 524,288 KiB, i.e. factors 2.0 and 1.0.
+"""
+
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import glob
+import json
+import re
+import sys
+
+_OURS = re.compile(r"fehip::(?:\(anonymous namespace\)::)?(\w+)(<[^()]*>)?")
+
+
+def short_name(name: str) -> str:
+    m = _OURS.search(name)
+    if m:
+        return m.group(1) + (m.group(2) or "")
+    return name.split("(")[0][:60]
+
+
+def _one(pattern: str) -> str:
+    hits = sorted(glob.glob(pattern, recursive=True))
+    if not hits:
+        raise FileNotFoundError(pattern)
+    return hits[0]
+
+
+def trace(kt_dir: str) -> list[str]:
+    rows = list(csv.DictReader(open(_one(f"{kt_dir}/**/*kernel_stats.csv"))))
+    out = [f"{'kernel':34s} {'calls':>6s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s} {'total_ms':>10s}"]
+    for r in rows:
+        if not _OURS.search(r["Name"]):
+            continue
+        out.append(f"{short_name(r['Name']):34s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.2f} "
+                   f"{float(r['MinNs']) / 1e3:10.2f} {float(r['MaxNs']) / 1e3:10.2f} "
+                   f"{float(r['TotalDurationNs']) / 1e6:10.2f}")
+    return out
+
+
+def _counter(dir_: str, cname: str):
+    per = collections.defaultdict(list)
+    calib = None
+    for r in csv.DictReader(open(_one(f"{dir_}/**/*counter_collection.csv"))):
+        if r["Counter_Name"] != cname:
+            continue
+        v = float(r["Counter_Value"])
+        if "copyBuffer" in r["Kernel_Name"] and (calib is None or v > calib):
+            calib = v
+        if _OURS.search(r["Kernel_Name"]):
+            per[short_name(r["Kernel_Name"])].append(v)
+    return per, calib
+
+
+def traffic(fetch_dir: str, write_dir: str, copy_bytes: int) -> tuple[list[str], dict]:
+    fetch, fcal = _counter(fetch_dir, "FETCH_SIZE")
+    write, wcal = _counter(write_dir, "WRITE_SIZE")
+    if not fcal or not wcal:
+        raise RuntimeError("no calibration copy found (run bench.py with --calibrate-copy-mib)")
+    ffac = copy_bytes / (fcal * 1024.0)
+    wfac = copy_bytes / (wcal * 1024.0)
+    out = [f"calibration copy of {copy_bytes} bytes: FETCH_SIZE {fcal:.1f} KiB (factor {ffac:.3f}), "
+           f"WRITE_SIZE {wcal:.1f} KiB (factor {wfac:.3f})",
+           f"{'kernel':34s} {'dispatches':>10s} {'fetch_MB':>10s} {'write_MB':>10s} {'total_MB':>10s}"]
+    table = {}
+    for k in sorted(set(fetch) | set(write), key=lambda kk: -sum(fetch.get(kk, [0])) / max(1, len(fetch.get(kk, [0])))):
+        f = fetch.get(k, [])
+        w = write.get(k, [])
+        fb = (sum(f) / len(f)) * 1024.0 * ffac if f else 0.0
+        wb = (sum(w) / len(w)) * 1024.0 * wfac if w else 0.0
+        table[k] = {"fetch_bytes": fb, "write_bytes": wb, "dispatches": len(f)}
+        out.append(f"{k:34s} {len(f):10d} {fb / 1e6:10.2f} {wb / 1e6:10.2f} {(fb + wb) / 1e6:10.2f}")
+    return out, {"fetch_factor": ffac, "write_factor": wfac, "kernels": table}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="what", required=True)
+    t = sub.add_parser("trace")
+    t.add_argument("kt_dir")
+    t.add_argument("command")
+    c = sub.add_parser("traffic")
+    c.add_argument("fetch_dir")
+    c.add_argument("write_dir")
+    c.add_argument("command")
+    c.add_argument("--copy-mib", type=int, default=512)
+    c.add_argument("--json", default="")
+    c.add_argument("--meta", default="{}", help="JSON object stored beside the table (workload keys)")
+    a = ap.parse_args(argv)
+    if a.what == "trace":
+        lines = trace(a.kt_dir)
+    else:
+        lines, table = traffic(a.fetch_dir, a.write_dir, a.copy_mib << 20)
+        if a.json:
+            table.update(json.loads(a.meta))
+            table["command"] = a.command
+            with open(a.json, "w") as fh:
+                json.dump(table, fh, indent=1)
+    print("command: " + a.command)
+    print("\n".join(lines))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

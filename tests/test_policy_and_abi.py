@@ -1,6 +1,7 @@
 """Host logic and the C-ABI surface (no GPU compute calls)."""
 
 import ctypes
+import json
 import re
 from pathlib import Path
 
@@ -13,18 +14,32 @@ from fastembedr_amd import _lib, opentsne, synthetic
 ROOT = Path(__file__).resolve().parent.parent
 
 
-def test_auto_parameters_match_reference_constants():
-    # tests/testthat/test-tsne.R:31-56 of the reference
-    p = fe.tsne_auto_parameters(150, 30, None)
-    assert p["perplexity"] == 10
-    assert p["learning_rate"] == 150 / p["early_exaggeration"]
-    assert p["auto_kld_stop"] is False
-    assert p["auto_iter_end"] == 5000
-    assert p["rule"] == "opt_sne_learning_rate_fixed_iterations_no_expensive_kld_polling"
+GOLDEN = json.loads((ROOT / "tests" / "golden" / "reference_test_constants.json").read_text())
+
+
+@pytest.mark.parametrize("case", GOLDEN["auto_parameters"], ids=lambda c: f"n{c['n']}_k{c['k']}")
+def test_auto_parameters_match_reference_constants(case):
+    # constants asserted by the reference's tests/testthat/test-tsne.R:31-56
+    p = fe.tsne_auto_parameters(case["n"], case["k"], case["perplexity_in"])
+    for key, want in case["expect"].items():
+        if key == "learning_rate_is_n_over_early_exaggeration":
+            assert (p["learning_rate"] == case["n"] / p["early_exaggeration"]) is want
+        else:
+            assert p[key] == want, key
+
+
+def test_auto_parameters_schedule():
     big = fe.tsne_auto_parameters(70000, 90, None)
-    assert big["perplexity"] == 30
     assert big["early_exaggeration"] == 12.0
     assert big["early_exaggeration_iter"] == 250 and big["n_iter"] == 500
+
+
+def test_result_labels_follow_reference_naming():
+    lab = GOLDEN["labels"]
+    # The HIP labels take the CUDA backend's naming with the backend swapped.
+    assert opentsne.OPTIMIZER_LABEL == lab["cuda_optimizer"].replace("_cuda", "_hip")
+    assert opentsne.REPULSION_LABEL == "fft_grid_hip"
+    assert opentsne.OPTIMIZER_LABEL.startswith("opentsne_fitsne_fft_grid")
 
 
 def test_neighbor_policy():
