@@ -991,6 +991,203 @@ __global__ __launch_bounds__(256) void k_attract(const int* __restrict__ row_ptr
   }
 }
 
+// ---- tiled attraction ---------------------------------------------------------
+// Same sum as k_attract, taken over P regrouped into (row block, column tile)
+// runs (see Tiles).  A workgroup owns one block of kTileRows rows; for each
+// of its column tiles it stages the kTileCols positions y_j of that tile in
+// LDS, so the neighbour gathers read LDS instead of L2.  Each lane takes
+// kTileRun consecutive entries of the run; entries of one row are adjacent,
+// so a lane sums them in registers and adds one partial per row it touched
+// to the row's LDS accumulator.
+constexpr int kTileRun = 8;
+static_assert(kTileRun == 8, "k_attract_tiles reads a run group as two 16-byte vectors");
+
+template <int L>
+__global__ __launch_bounds__(256) void k_tile_keys(const int* __restrict__ row_ptr, const int* __restrict__ col,
+                                                   const float* __restrict__ val, int n, int col_bits,
+                                                   unsigned int* __restrict__ key,
+                                                   unsigned long long* __restrict__ pay) {
+  constexpr int RPB = 256 / L;
+  const int lane = threadIdx.x & (L - 1);
+  for (int i = static_cast<int>(blockIdx.x) * RPB + static_cast<int>(threadIdx.x) / L; i < n;
+       i += static_cast<int>(gridDim.x) * RPB) {
+    const unsigned int rb = static_cast<unsigned int>(i / kTileRows);
+    const unsigned int lr = static_cast<unsigned int>(i % kTileRows);
+    const int e1 = row_ptr[i + 1];
+    for (int e = row_ptr[i] + lane; e < e1; e += L) {
+      const int j = col[e];
+      key[e] = (rb << col_bits) | static_cast<unsigned int>(j / kTileCols);
+      pay[e] = (static_cast<unsigned long long>(__float_as_uint(val[e])) << 32) |
+               static_cast<unsigned long long>((lr << 16) | static_cast<unsigned int>(j % kTileCols));
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_tile_heads(const unsigned int* __restrict__ key, long long nnz,
+                                                    int* __restrict__ heads) {
+  for (long long p = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; p < nnz;
+       p += static_cast<long long>(gridDim.x) * 256)
+    heads[p] = (p == 0 || key[p] != key[p - 1]) ? 1 : 0;
+}
+
+// Tile metadata from the sorted keys: column tile, unpadded begin, and the
+// first tile of each row block; the tile count goes to *tile_count.
+__global__ __launch_bounds__(256) void k_tile_meta(const unsigned int* __restrict__ key,
+                                                   const int* __restrict__ heads, const int* __restrict__ pos,
+                                                   long long nnz, int col_bits, int row_blocks,
+                                                   int* __restrict__ tile_ptr, int* __restrict__ tile_cb,
+                                                   int* __restrict__ ubeg, int* __restrict__ tile_count) {
+  for (long long p = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; p < nnz;
+       p += static_cast<long long>(gridDim.x) * 256) {
+    const unsigned int k = key[p];
+    const int cur = static_cast<int>(k >> col_bits);
+    if (heads[p]) {
+      const int t = pos[p];
+      tile_cb[t] = static_cast<int>(k & ((1u << col_bits) - 1u));
+      ubeg[t] = static_cast<int>(p);
+      // this is the first tile of every row block in (previous tile's block, cur]
+      const int prev = p == 0 ? -1 : static_cast<int>(key[p - 1] >> col_bits);
+      for (int rb = prev + 1; rb <= cur; ++rb) tile_ptr[rb] = t;
+    }
+    if (p == nnz - 1) {
+      const int total = pos[p] + heads[p];
+      ubeg[total] = static_cast<int>(nnz);
+      *tile_count = total;
+      for (int rb = cur + 1; rb <= row_blocks; ++rb) tile_ptr[rb] = total;
+    }
+  }
+}
+
+// Padded tile sizes (multiples of kTileRun), zero past the last tile.
+__global__ __launch_bounds__(256) void k_tile_sizes(const int* __restrict__ ubeg, const int* __restrict__ tile_count,
+                                                    long long slots, int* __restrict__ psize) {
+  const int total = *tile_count;
+  for (long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; t < slots;
+       t += static_cast<long long>(gridDim.x) * 256) {
+    int v = 0;
+    if (t < total) {
+      const int len = ubeg[t + 1] - ubeg[t];
+      v = (len + kTileRun - 1) / kTileRun * kTileRun;
+    }
+    psize[t] = v;
+  }
+}
+
+// Entries to their padded places; the last entry of each tile fills the
+// tile's padding with empty entries (0xffffffff, p = 0).
+__global__ __launch_bounds__(256) void k_tile_scatter(const unsigned long long* __restrict__ pay,
+                                                      const int* __restrict__ heads, const int* __restrict__ pos,
+                                                      const int* __restrict__ ubeg,
+                                                      const int* __restrict__ tile_beg, long long nnz,
+                                                      unsigned int* __restrict__ ent, float* __restrict__ val) {
+  for (long long p = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; p < nnz;
+       p += static_cast<long long>(gridDim.x) * 256) {
+    const int t = pos[p] + heads[p] - 1;
+    const int u0 = ubeg[t];
+    const int b0 = tile_beg[t];
+    const unsigned long long w = pay[p];
+    const long long q = b0 + (p - u0);
+    ent[q] = static_cast<unsigned int>(w);
+    val[q] = __uint_as_float(static_cast<unsigned int>(w >> 32));
+    const int u1 = ubeg[t + 1];
+    if (p == u1 - 1) {
+      for (int r = b0 + (u1 - u0); r < tile_beg[t + 1]; ++r) {
+        ent[r] = 0xffffffffu;
+        val[r] = 0.0f;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_tile_empty(int* __restrict__ tile_ptr, int* __restrict__ tile_beg,
+                                                    int row_blocks) {
+  for (int rb = threadIdx.x; rb <= row_blocks; rb += 256) tile_ptr[rb] = 0;
+  if (threadIdx.x == 0) tile_beg[0] = 0;
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void k_attract_tiles(const unsigned int* __restrict__ ent,
+                                                       const float* __restrict__ val,
+                                                       const int* __restrict__ tile_ptr,
+                                                       const int* __restrict__ tile_cb,
+                                                       const int* __restrict__ tile_beg,
+                                                       const float2* __restrict__ y_cur, float2* __restrict__ attr,
+                                                       float exaggeration, int n, int row_blocks, int xcds) {
+  __shared__ float2 ys[kTileCols];
+  __shared__ float2 yr[kTileRows];
+  __shared__ float acc_x[kTileRows];
+  __shared__ float acc_y[kTileRows];
+  // XCD-aware: block b runs on XCD b % xcds; each XCD takes one contiguous
+  // range of row blocks, whose column tiles then stay in its L2.
+  const int xcd = static_cast<int>(blockIdx.x) % xcds;
+  const int slot = static_cast<int>(blockIdx.x) / xcds;
+  const int per_xcd = (row_blocks + xcds - 1) / xcds;
+  const int rb = xcd * per_xcd + slot;
+  if (slot >= per_xcd || rb >= row_blocks) return;  // whole workgroup
+  const int r0 = rb * kTileRows;
+  const int rows = min(kTileRows, n - r0);
+  for (int r = threadIdx.x; r < kTileRows; r += NT) {
+    acc_x[r] = 0.0f;
+    acc_y[r] = 0.0f;
+    yr[r] = r < rows ? y_cur[r0 + r] : make_float2(0.0f, 0.0f);
+  }
+  const int t1 = tile_ptr[rb + 1];
+  for (int t = tile_ptr[rb]; t < t1; ++t) {
+    const int base = tile_cb[t] * kTileCols;
+    const int cnt = min(kTileCols, n - base);
+    const int e0 = tile_beg[t];
+    const int e1 = tile_beg[t + 1];
+    __syncthreads();  // the previous tile's LDS reads are done
+    for (int q = threadIdx.x; q < cnt; q += NT) ys[q] = y_cur[base + q];
+    __syncthreads();
+    // Runs are padded to whole groups of kTileRun and start on one, so each
+    // lane reads its group with two 16-byte loads per array.
+    for (int e = e0 + static_cast<int>(threadIdx.x) * kTileRun; e < e1; e += NT * kTileRun) {
+      unsigned int w[kTileRun];
+      float p[kTileRun];
+      const uint4 w0 = *reinterpret_cast<const uint4*>(ent + e);
+      const uint4 w1 = *reinterpret_cast<const uint4*>(ent + e + 4);
+      const float4 p0 = *reinterpret_cast<const float4*>(val + e);
+      const float4 p1 = *reinterpret_cast<const float4*>(val + e + 4);
+      w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w;
+      w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
+      p[0] = p0.x; p[1] = p0.y; p[2] = p0.z; p[3] = p0.w;
+      p[4] = p1.x; p[5] = p1.y; p[6] = p1.z; p[7] = p1.w;
+      int cur = -1;
+      float ax = 0.0f, ay = 0.0f;
+#pragma unroll
+      for (int q = 0; q < kTileRun; ++q) {
+        if (w[q] == 0xffffffffu) continue;  // padding (only at the end of a run)
+        const int lr = static_cast<int>(w[q] >> 16);
+        const int lc = static_cast<int>(w[q] & 0xffffu);
+        if (lr != cur) {
+          if (cur >= 0) {
+            atomicAdd(&acc_x[cur], ax);
+            atomicAdd(&acc_y[cur], ay);
+          }
+          cur = lr;
+          ax = 0.0f;
+          ay = 0.0f;
+        }
+        const float2 yi = yr[lr];
+        const float2 yj = ys[lc];
+        const float dx = yi.x - yj.x;
+        const float dy = yi.y - yj.y;
+        const float qq = 1.0f / (1.0f + (dx * dx + dy * dy));
+        const float c = exaggeration * p[q] * qq;
+        ax += c * dx;
+        ay += c * dy;
+      }
+      if (cur >= 0) {
+        atomicAdd(&acc_x[cur], ax);
+        atomicAdd(&acc_y[cur], ay);
+      }
+    }
+  }
+  __syncthreads();
+  for (int r = threadIdx.x; r < rows; r += NT) attr[r0 + r] = make_float2(acc_x[r], acc_y[r]);
+}
+
 // Point-parallel second half of an iteration: the grid repulsion read back
 // at the point (src/tsne_neighbors.cpp:1165-1180) or an exact one, plus the
 // attraction, gives the gradient; then the gains/momentum/step-clip update
@@ -1591,6 +1788,105 @@ hipError_t launch_exact_z_double(const float2* y, int n, double* z_partial, hipS
 hipError_t launch_kl_rows(const Csr& p, const float2* y, double sum_q, double* partial, int blocks,
                           hipStream_t stream) {
   k_kl_rows<<<blocks, 256, 0, stream>>>(p.row_ptr, p.col, p.val, y, p.n, sum_q, partial);
+  return hipGetLastError();
+}
+
+// ---- tiled attraction ---------------------------------------------------------
+namespace {
+int bits_for(long long count) {  // bits needed to hold values 0 .. count - 1
+  int b = 0;
+  while (b < 62 && (1ll << b) < count) ++b;
+  return b;
+}
+}  // namespace
+
+void tiles_shape(int n, long long nnz, Tiles& t) {
+  t.n = n;
+  t.nnz = nnz;
+  t.row_blocks = (n + kTileRows - 1) / kTileRows;
+  t.col_tiles = (n + kTileCols - 1) / kTileCols;
+  t.col_bits = bits_for(t.col_tiles);
+  t.key_bits = t.col_bits + bits_for(t.row_blocks);
+  t.max_tiles = std::min<long long>(nnz, static_cast<long long>(t.row_blocks) * t.col_tiles);
+  t.padded = nnz + 7 * t.max_tiles;
+}
+
+hipError_t tiles_temp_bytes(const Tiles& t, std::size_t& bytes) {
+  std::size_t sort_b = 0, scan_b = 0, scan_t = 0;
+  const std::size_t count = static_cast<std::size_t>(std::max<long long>(t.nnz, 1));
+  hipError_t e = rocprim::radix_sort_pairs(nullptr, sort_b, static_cast<const unsigned int*>(nullptr),
+                                           static_cast<unsigned int*>(nullptr),
+                                           static_cast<const unsigned long long*>(nullptr),
+                                           static_cast<unsigned long long*>(nullptr), count, 0u,
+                                           static_cast<unsigned int>(std::max(t.key_bits, 1)));
+  if (e != hipSuccess) return e;
+  e = rocprim::exclusive_scan(nullptr, scan_b, static_cast<const int*>(nullptr), static_cast<int*>(nullptr), 0,
+                              count, rocprim::plus<int>());
+  if (e != hipSuccess) return e;
+  e = rocprim::exclusive_scan(nullptr, scan_t, static_cast<const int*>(nullptr), static_cast<int*>(nullptr), 0,
+                              static_cast<std::size_t>(t.max_tiles) + 1, rocprim::plus<int>());
+  bytes = std::max(sort_b, std::max(scan_b, scan_t));
+  return e;
+}
+
+hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream) {
+  if (t.key_bits > 32) return hipErrorInvalidValue;  // row blocks x column tiles beyond a 32-bit key
+  if (t.nnz == 0) {
+    k_tile_empty<<<1, 256, 0, stream>>>(t.tile_ptr, t.tile_beg, t.row_blocks);
+    return hipGetLastError();
+  }
+  const int key_blocks = std::min((p.n + 7) / 8, 65536);
+  k_tile_keys<32><<<key_blocks, 256, 0, stream>>>(p.row_ptr, p.col, p.val, p.n, t.col_bits, t.key_in, t.pay_in);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const std::size_t count = static_cast<std::size_t>(t.nnz);
+  std::size_t tb = t.temp_bytes;
+  // stable: entries of one (row block, column tile) keep their CSR (row) order
+  e = rocprim::radix_sort_pairs(t.temp, tb, t.key_in, t.key_out, t.pay_in, t.pay_out, count, 0u,
+                                static_cast<unsigned int>(std::max(t.key_bits, 1)), stream);
+  if (e != hipSuccess) return e;
+  const unsigned int blocks = static_cast<unsigned int>(std::min<long long>((t.nnz + 255) / 256, 65536));
+  k_tile_heads<<<blocks, 256, 0, stream>>>(t.key_out, t.nnz, t.heads);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  tb = t.temp_bytes;
+  e = rocprim::exclusive_scan(t.temp, tb, t.heads, t.pos, 0, count, rocprim::plus<int>(), stream);
+  if (e != hipSuccess) return e;
+  k_tile_meta<<<blocks, 256, 0, stream>>>(t.key_out, t.heads, t.pos, t.nnz, t.col_bits, t.row_blocks, t.tile_ptr,
+                                          t.tile_cb, t.ubeg, t.tile_count);
+  const long long slots = t.max_tiles + 1;
+  const unsigned int sblocks = static_cast<unsigned int>(std::min<long long>((slots + 255) / 256, 65536));
+  k_tile_sizes<<<sblocks, 256, 0, stream>>>(t.ubeg, t.tile_count, slots, t.psize);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  tb = t.temp_bytes;
+  e = rocprim::exclusive_scan(t.temp, tb, t.psize, t.tile_beg, 0, static_cast<std::size_t>(slots),
+                              rocprim::plus<int>(), stream);
+  if (e != hipSuccess) return e;
+  k_tile_scatter<<<blocks, 256, 0, stream>>>(t.pay_out, t.heads, t.pos, t.ubeg, t.tile_beg, t.nnz, t.ent, t.val);
+  return hipGetLastError();
+}
+
+hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int threads,
+                                int xcds, hipStream_t stream) {
+  const int per_xcd = (t.row_blocks + xcds - 1) / xcds;
+  const int blocks = per_xcd * xcds;
+  switch (threads) {
+    case 256:
+      k_attract_tiles<256><<<blocks, 256, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr,
+                                                       exaggeration, t.n, t.row_blocks, xcds);
+      break;
+    case 512:
+      k_attract_tiles<512><<<blocks, 512, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr,
+                                                       exaggeration, t.n, t.row_blocks, xcds);
+      break;
+    case 1024:
+      k_attract_tiles<1024><<<blocks, 1024, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur,
+                                                         attr, exaggeration, t.n, t.row_blocks, xcds);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -119,6 +119,7 @@ struct fastembedr_hip_tsne {
   hipStream_t stream = nullptr;
   Arena arena;
   Arena work_arena;         // working-order CSR copies, permutations, state double buffers
+  Arena tile_arena;         // tiled P for the attraction and its build scratch
   DeviceScalars* sc = nullptr;
   Csr p;                    // P in the caller's numbering (columns ascending)
   Csr pw[2];                // P in the working numbering (after renumbering)
@@ -140,6 +141,12 @@ struct fastembedr_hip_tsne {
   int label_sweeps = 0;
   float2* y_b = nullptr;    // centred layout of the current iteration (also scratch)
   float2* grad = nullptr;
+  // Attraction over tiled P (kernel k_attract_tiles) unless disabled; the
+  // tiles follow the working numbering and are rebuilt after it changes.
+  bool attract_tiled = true;
+  int tile_threads = 512;
+  fehip::Tiles tiles;
+  int tiles_for = -2;       // value of wi the tiles were built for; -2: none
 
   bool renumbered() const { return wi >= 0; }
   const Csr& work_p() const { return wi < 0 ? p : pw[wi]; }
@@ -163,6 +170,7 @@ struct fastembedr_hip_tsne {
   ~fastembedr_hip_tsne() {
     if (stream != nullptr) (void)hipStreamSynchronize(stream);
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
+    tile_arena.release();
     work_arena.release();
     arena.release();
     if (stream != nullptr) (void)hipStreamDestroy(stream);
@@ -205,7 +213,7 @@ namespace {
 
 const char* kKernelNames[fehip::kKernelCount] = {
     "stats", "bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols", "charge_rows",
-    "conv_cols", "inverse_rows", "attract", "update", "commit", "renumber"};
+    "conv_cols", "inverse_rows", "attract", "update", "commit", "renumber", "tile_build"};
 
 int key_bits_for(int n) {
   int b = 1;
@@ -295,6 +303,74 @@ bool alloc_working_buffers(fastembedr_hip_tsne* s) {
   while ((1LL << bits) <= static_cast<long long>(n)) ++bits;
   s->rn.key_bits = 32 + bits;
   return true;
+}
+
+// Tiled P and its build scratch (see fehip::Tiles).  The sort scratch is
+// sized for the whole of P and kept for the session, so rebuilding after a
+// renumbering allocates nothing.
+bool alloc_tiles(fastembedr_hip_tsne* s) {
+  fehip::Tiles& t = s->tiles;
+  fehip::tiles_shape(s->n, s->p.nnz, t);
+  if (t.key_bits > 32 || t.padded > static_cast<long long>(std::numeric_limits<int>::max())) {
+    s->attract_tiled = false;  // beyond a 32-bit sort key or int offsets: row-parallel attraction
+    return true;
+  }
+  std::size_t temp = 0;
+  if (!hip_ok(fehip::tiles_temp_bytes(t, temp), "tile build size query")) return false;
+  const std::size_t nnz = static_cast<std::size_t>(std::max<long long>(t.nnz, 1));
+  const std::size_t padded = static_cast<std::size_t>(std::max<long long>(t.padded, 1));
+  const std::size_t slots = static_cast<std::size_t>(t.max_tiles) + 1;
+  const std::size_t bytes = 2 * align_up(padded * 4) + 2 * align_up(nnz * 4) + 2 * align_up(nnz * 8) +
+                            align_up((static_cast<std::size_t>(t.row_blocks) + 1) * 4) + 4 * align_up(slots * 4) +
+                            align_up(4) + align_up(temp) + 4096;
+  if (!memory_preflight(bytes, "HIP openTSNE attraction tiles") ||
+      !s->tile_arena.init(bytes, "hipMalloc(HIP openTSNE attraction tiles)")) {
+    return false;
+  }
+  Arena& a = s->tile_arena;
+  t.ent = a.take<unsigned int>(padded);
+  t.val = a.take<float>(padded);
+  t.key_in = a.take<unsigned int>(nnz);
+  t.key_out = a.take<unsigned int>(nnz);
+  t.pay_in = a.take<unsigned long long>(nnz);
+  t.pay_out = a.take<unsigned long long>(nnz);
+  t.tile_ptr = a.take<int>(static_cast<std::size_t>(t.row_blocks) + 1);
+  t.tile_cb = a.take<int>(slots);
+  t.tile_beg = a.take<int>(slots);
+  t.ubeg = a.take<int>(slots);
+  t.psize = a.take<int>(slots);
+  t.tile_count = a.take<int>(1);
+  t.temp = a.take<char>(std::max<std::size_t>(temp, 1));
+  t.temp_bytes = temp;
+  if (t.temp == nullptr) {
+    set_error("internal: attraction tiles do not fit their arena");
+    return false;
+  }
+  // After the sort the key and payload inputs are dead: the head flags and
+  // their scan reuse them.
+  t.heads = reinterpret_cast<int*>(t.key_in);
+  t.pos = reinterpret_cast<int*>(t.pay_in);
+  return true;
+}
+
+// Attractive term of every row into s->attr at the centred layout y_cur.
+bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggeration) {
+  if (!s->attract_tiled) {
+    return s->timed(fehip::kKAttract, "attract launch", [&] {
+      return fehip::launch_attract(s->work_p(), y_cur, s->attr, exaggeration, s->lanes, s->xcds, s->stream);
+    });
+  }
+  if (s->tiles_for != s->wi) {
+    if (!s->timed(fehip::kKTileBuild, "tile build",
+                  [&] { return fehip::launch_tile_build(s->work_p(), s->tiles, s->stream); })) {
+      return false;
+    }
+    s->tiles_for = s->wi;
+  }
+  return s->timed(fehip::kKAttract, "attract launch", [&] {
+    return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->tile_threads, s->xcds,
+                                       s->stream);
+  });
 }
 
 // Renumbers points by the Morton order of the current layout: permutes the
@@ -614,7 +690,13 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
     }
     s->xcds = env_int("FASTEMBEDR_HIP_XCDS", s->xcds);
   }
-  if (!alloc_working_buffers(s)) {
+  // Attraction: tiled unless FASTEMBEDR_HIP_ATTRACT_TILED=0 (row-parallel).
+  if (const char* tiled = std::getenv("FASTEMBEDR_HIP_ATTRACT_TILED")) {
+    if (std::strcmp(tiled, "0") == 0) s->attract_tiled = false;
+  }
+  s->tile_threads = env_int("FASTEMBEDR_HIP_TILE_THREADS", s->tile_threads);
+  if (s->tile_threads != 256 && s->tile_threads != 512 && s->tile_threads != 1024) s->tile_threads = 512;
+  if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {
     delete s;
     return 1;
   }
@@ -869,15 +951,13 @@ int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int
   if (repulsion == FASTEMBEDR_HIP_REPULSION_EXACT) {
     ok = hip_ok(fehip::launch_exact_repulsion(s->y_a(), s->n, s->exact_rep, s->dpartial, s->sc, s->stream),
                 "exact repulsion launch") &&
-         hip_ok(fehip::launch_attract(s->work_p(), s->y_a(), s->attr, exaggeration, s->lanes, s->xcds, s->stream),
-                "attract launch") &&
+         enqueue_attract(s, s->y_a(), exaggeration) &&
          hip_ok(fehip::launch_update(fehip::kModeGradientExact, s->y_a(), s->attr, nullptr, nullptr, nullptr, s->grad,
                                      s->exact_rep, s->gb, up, s->partial, s->sc, s->n, s->stream),
                 "update launch");
   } else if (repulsion == FASTEMBEDR_HIP_REPULSION_GRID) {
     ok = enqueue_gradient_fields(s, true, 0) &&
-         hip_ok(fehip::launch_attract(s->work_p(), s->y_b, s->attr, exaggeration, s->lanes, s->xcds, s->stream),
-                "attract launch") &&
+         enqueue_attract(s, s->y_b, exaggeration) &&
          hip_ok(fehip::launch_update(fehip::kModeGradientGrid, s->y_b, s->attr, nullptr, nullptr, nullptr, s->grad,
                                      nullptr, s->gb, up, s->partial, s->sc, s->n, s->stream),
                 "update launch");
@@ -930,9 +1010,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
     }
     ++s->since_reorder;
     if (!enqueue_gradient_fields(s, false, 0)) return 1;
-    if (!s->timed(fehip::kKAttract, "attract launch", [&] {
-          return fehip::launch_attract(s->work_p(), s->y_b, s->attr, exaggeration, s->lanes, s->xcds, s->stream);
-        }) ||
+    if (!enqueue_attract(s, s->y_b, exaggeration) ||
         !s->timed(fehip::kKUpdate, "update launch", [&] {
           return fehip::launch_update(fehip::kModeUpdate, s->y_b, s->attr, s->y_a(), s->update(), s->gains(),
                                       nullptr, nullptr, s->gb, up, s->partial, s->sc, n, s->stream);
