@@ -2,22 +2,25 @@
 
 The compute path is the HIP library behind include/fastembedr_hip.h; this
 package holds its ctypes binding, a session wrapper, the host-side mirror of
-the reference's ``opentsne_knn()`` entry point, and synthetic inputs for the
-benchmark configurations.
+the reference's ``opentsne_knn()`` and ``transform_tsne()`` entry points, and
+synthetic inputs for the benchmark configurations.
 """
 
 from ._lib import HipBackendError, HipBackendUnavailable, available, last_error
 from .opentsne import OpenTsneResult, opentsne_knn, opentsne_neighbor_policy, tsne_auto_parameters
 from .session import TsneSession
+from .transform import TransformResult, transform_tsne
 
 __all__ = [
     "HipBackendError",
     "HipBackendUnavailable",
     "OpenTsneResult",
+    "TransformResult",
     "TsneSession",
     "available",
     "last_error",
     "opentsne_knn",
     "opentsne_neighbor_policy",
+    "transform_tsne",
     "tsne_auto_parameters",
 ]

@@ -48,6 +48,11 @@ SIGNATURES = {
     "fastembedr_hip_tsne_kernel_count": (_I, []),
     "fastembedr_hip_tsne_p_build_ms": (_I, [_P, _DP]),
     "fastembedr_hip_random_init": (_I, [_I, C.c_uint, _P]),
+    "fastembedr_hip_transform_tsne": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, C.c_double, _I, _I, C.c_double,
+                                           C.c_double, C.c_double, C.c_double, C.c_double, C.c_double,
+                                           C.c_double, _I, _I, _I, _P, _IP]),
+    "fastembedr_hip_transform_probe": (_I, [_P, _I, _P, _P, _I, _I, C.c_double, _P, C.c_double, _I, _I, _I, _I,
+                                            _P, _P, _P]),
 }
 
 REPULSION_GRID = 0

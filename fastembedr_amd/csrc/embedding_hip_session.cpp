@@ -803,6 +803,11 @@ int one_shot(const int* indices, const DT* distances, const float* init, int has
 
 }  // namespace
 
+namespace fehip {
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+void clear_last_error() { g_last_error.clear(); }
+}  // namespace fehip
+
 extern "C" {
 
 const char* fastembedr_hip_embedding_last_error(void) { return g_last_error.c_str(); }

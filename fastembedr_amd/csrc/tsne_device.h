@@ -6,8 +6,13 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <string>
 
 namespace fehip {
+
+// Thread-local message behind fastembedr_hip_embedding_last_error().
+void set_last_error(const std::string& msg);
+void clear_last_error();
 
 // Per-session scalars that the kernels read and write on the device, so that
 // an iteration never waits for the host.  Written by the single-block

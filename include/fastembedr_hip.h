@@ -175,6 +175,48 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kernel_count(void);
  * users start from the same layout. */
 FASTEMBEDR_HIP_API int fastembedr_hip_random_init(int n, unsigned int seed, float* out);
 
+/* ------------------------------------------------------------------------
+ * Fixed-reference transform.  Replaces the computation of the reference's
+ * transform_tsne_cpp (src/tsne_neighbors.cpp:1859-2109; R entry
+ * transform_tsne(), R/transform_tsne.R:57-315) for two-dimensional layouts.
+ * The reference has no GPU counterpart (R/transform_tsne.R:231-254 names a
+ * transform_tsne_cuda_cpp that src/ does not define), so the arguments are
+ * those of transform_tsne_cpp, with R's matrix layouts:
+ *   reference_layout : n_reference x 2, column-major, fp64
+ *   indices          : n_query x k, column-major, 0- or 1-based (1-based iff
+ *                      every index is in [1, n_reference])
+ *   distances        : n_query x k, column-major, fp64
+ *   y_init, out      : n_query x 2, column-major, fp64; y_init may be NULL
+ *   initialization   : 0 median, 1 weighted, 2 random
+ *   seed             : INT_MIN stands for R's NA (then 5489)
+ * max_grad_norm / max_step_norm that are not finite or <= 0 disable the clip;
+ * n_negatives is capped at n_reference; the repulsion is exact when
+ * n_reference <= exact_repulsion_threshold or n_negatives >= n_reference,
+ * and *repulsion_exact (may be NULL) reports which was used.  All arithmetic
+ * is fp64 in the reference's order. */
+FASTEMBEDR_HIP_API int fastembedr_hip_transform_tsne(
+    const double* reference_layout, int n_reference,
+    const int* indices, const double* distances, int n_query, int k,
+    const double* y_init, int initialization, double perplexity,
+    int n_iter, int early_exaggeration_iter, double learning_rate,
+    double early_exaggeration, double exaggeration,
+    double initial_momentum, double final_momentum,
+    double max_grad_norm, double max_step_norm,
+    int n_negatives, int exact_repulsion_threshold, int seed,
+    double* out, int* repulsion_exact);
+
+/* Parity probe for the transform, no counterpart in the reference: the
+ * conditional probabilities (p_out, n_query x k row-major, as the reference
+ * stores them), the median (0) or weighted (1) initialisation (init_out,
+ * n_query x 2 row-major) and one gradient at y (grad_out, n_query x 2
+ * row-major) for the given per-iteration seed.  Any output may be NULL. */
+FASTEMBEDR_HIP_API int fastembedr_hip_transform_probe(
+    const double* reference_layout, int n_reference,
+    const int* indices, const double* distances, int n_query, int k,
+    double perplexity, const double* y, double exaggeration,
+    int n_negatives, int exact_repulsion_threshold, int iter_seed,
+    int initialization, double* p_out, double* grad_out, double* init_out);
+
 /* Wall time of the P construction in milliseconds (device events). */
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_p_build_ms(const fastembedr_hip_tsne* session, double* ms);
 

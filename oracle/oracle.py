@@ -1,4 +1,4 @@
-"""ctypes view of the CPU oracle (oracle/tsne_oracle.cpp).
+"""ctypes view of the CPU oracle (oracle/tsne_oracle.cpp, oracle/transform_oracle.cpp).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg, as the checker.  The product path never loads it.
@@ -51,6 +51,16 @@ def load() -> C.CDLL:
         "tsne_oracle_kl": (D, [P, P, I, I, P]),
         "tsne_oracle_optimize": (I, [P, P, I, I, I, D, D, D, I, D, D, D, D, I, I, I, I, P, P]),
         "tsne_oracle_random_init": (None, [P, I, C.c_uint]),
+        "transform_oracle_last_error": (C.c_char_p, []),
+        "transform_oracle_offset": (I, [P, I, I, I]),
+        "transform_oracle_conditional_p": (None, [P, I, I, D, I, P]),
+        "transform_oracle_init": (None, [P, I, P, P, I, I, I, I, I, P]),
+        "transform_oracle_gradient": (None, [P, I, P, P, I, I, P, D, I, I, I, I, P]),
+        "transform_oracle_update": (None, [P, P, P, P, I, D, D, D, D]),
+        "transform_oracle_run": (I, [P, I, P, P, I, I, P, I, D, I, I, D, D, D, D, D, D, D, I, I, I, I, P]),
+        "transform_oracle_iteration_seed": (I, [I, I]),
+        "transform_oracle_hash32": (C.c_uint, [C.c_uint]),
+        "transform_oracle_xorshift": (None, [C.c_uint, I, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -186,3 +196,96 @@ def random_init(n: int, seed: int) -> np.ndarray:
     y = np.empty((n, 2), np.float32)
     load().tsne_oracle_random_init(_p(y), n, int(seed) & 0xFFFFFFFF)
     return y
+
+
+# ---------------------------------------------------------------------------
+# Fixed-reference transform (transform_oracle.cpp).  Layouts as R hands them
+# over: reference (n_ref, 2), indices / distances (nq, k), column-major
+# internally; y arrays (nq, 2) row-major float64.
+# ---------------------------------------------------------------------------
+INIT_MEDIAN, INIT_WEIGHTED, INIT_RANDOM = 0, 1, 2
+
+
+def _f64_cm(a):
+    return np.asfortranarray(a, dtype=np.float64)
+
+
+def transform_offset(indices, n_ref: int) -> int:
+    idx = np.asfortranarray(indices, dtype=np.int32)
+    return int(load().transform_oracle_offset(_p(idx), idx.shape[0], idx.shape[1], int(n_ref)))
+
+
+def transform_conditional_p(distances, perplexity: float, threads: int = 1) -> np.ndarray:
+    d = _f64_cm(distances)
+    nq, k = d.shape
+    p = np.empty((nq, k), np.float64)
+    load().transform_oracle_conditional_p(_p(d), nq, k, float(perplexity), int(threads), _p(p))
+    return p
+
+
+def transform_init(reference, indices, distances, mode: int = INIT_MEDIAN, seed: int = 4, threads: int = 1):
+    ref = _f64_cm(reference)
+    idx = np.asfortranarray(indices, dtype=np.int32)
+    d = _f64_cm(distances)
+    nq, k = idx.shape
+    y = np.empty((nq, 2), np.float64)
+    load().transform_oracle_init(_p(ref), ref.shape[0], _p(idx), _p(d), nq, k, int(mode), int(seed), int(threads),
+                                 _p(y))
+    return y
+
+
+def transform_gradient(reference, indices, p, y, exaggeration: float, n_negatives: int, exact_threshold: int,
+                       iter_seed: int, threads: int = 1) -> np.ndarray:
+    ref = _f64_cm(reference)
+    idx = np.asfortranarray(indices, dtype=np.int32)
+    pp = np.ascontiguousarray(p, np.float64)
+    yy = np.ascontiguousarray(y, np.float64)
+    nq, k = idx.shape
+    g = np.empty((nq, 2), np.float64)
+    load().transform_oracle_gradient(_p(ref), ref.shape[0], _p(idx), _p(pp), nq, k, _p(yy), float(exaggeration),
+                                     int(n_negatives), int(exact_threshold), int(iter_seed), int(threads), _p(g))
+    return g
+
+
+def transform_update(y, upd, gains, grad, lr, momentum, max_grad_norm, max_step_norm):
+    """In place on float64 (nq, 2) arrays; grad is clipped in place."""
+    load().transform_oracle_update(_p(y), _p(upd), _p(gains), _p(grad), y.shape[0], float(lr), float(momentum),
+                                   float(max_grad_norm), float(max_step_norm))
+
+
+def transform_run(reference, indices, distances, y_init=None, initialization: int = INIT_MEDIAN,
+                  perplexity: float = 5.0, n_iter: int = 250, early_exaggeration_iter: int = 0,
+                  learning_rate: float = 0.1, early_exaggeration: float = 4.0, exaggeration: float = 1.5,
+                  initial_momentum: float = 0.8, final_momentum: float = 0.8, max_grad_norm: float = 0.25,
+                  max_step_norm: float = float("inf"), n_negatives: int = 256, exact_threshold: int = 4096,
+                  seed: int = 4, threads: int = 1):
+    """Returns (layout (nq, 2) float64, exact_repulsion bool)."""
+    ref = _f64_cm(reference)
+    idx = np.asfortranarray(indices, dtype=np.int32)
+    d = _f64_cm(distances)
+    nq, k = idx.shape
+    init = None if y_init is None else _f64_cm(y_init)
+    out = np.empty((nq, 2), np.float64, order="F")
+    rc = load().transform_oracle_run(_p(ref), ref.shape[0], _p(idx), _p(d), nq, k, _p(init), int(initialization),
+                                     float(perplexity), int(n_iter), int(early_exaggeration_iter),
+                                     float(learning_rate), float(early_exaggeration), float(exaggeration),
+                                     float(initial_momentum), float(final_momentum), float(max_grad_norm),
+                                     float(max_step_norm), int(n_negatives), int(exact_threshold), int(seed),
+                                     int(threads), _p(out))
+    if rc < 0:
+        raise ValueError(load().transform_oracle_last_error().decode())
+    return np.ascontiguousarray(out), bool(rc)
+
+
+def transform_iteration_seed(seed: int, it: int) -> int:
+    return int(load().transform_oracle_iteration_seed(int(seed), int(it)))
+
+
+def hash32(v: int) -> int:
+    return int(load().transform_oracle_hash32(int(v) & 0xFFFFFFFF))
+
+
+def xorshift32(state: int, count: int) -> np.ndarray:
+    out = np.empty(count, np.uint32)
+    load().transform_oracle_xorshift(int(state) & 0xFFFFFFFF, int(count), _p(out))
+    return out

@@ -1,0 +1,166 @@
+"""HIP fixed-reference transform vs the CPU oracle (through the C ABI).
+
+Both sides compute in fp64 in the reference's operation order; the only
+differences come from the device's exp/log in the perplexity search (last-bit
+differences of the conditional probabilities).  Tolerances:
+  conditional P, gradient         relative error <= 1e-12
+  median initialisation           bit-identical; weighted relative <= 1e-14
+  whole run (layout)              max abs difference <= 1e-9 x layout scale
+"""
+
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+from fastembedr_amd import _lib, synthetic
+
+pytestmark = pytest.mark.gpu
+
+TIGHT = 1e-12
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _query_problem(n_ref=3000, nq=1200, k=30, seed=11):
+    """Reference layout (a 2-D embedding stand-in), 20-D data, query KNN."""
+    spec = synthetic.MixtureSpec(n=n_ref + nq, dim=20, components=8, mean_sd=4.0)
+    x, labels = synthetic.gaussian_mixture(spec, seed=seed)
+    rng = np.random.default_rng(seed)
+    centers = rng.normal(0, 8, size=(8, 2))
+    layout = centers[labels[:n_ref]] + rng.normal(0, 1.0, size=(n_ref, 2))
+    xr, xq = x[:n_ref].astype(np.float64), x[n_ref:].astype(np.float64)
+    d2 = (xq ** 2).sum(1)[:, None] - 2 * xq @ xr.T + (xr ** 2).sum(1)[None, :]
+    idx = np.argsort(d2, axis=1)[:, :k]
+    dist = np.sqrt(np.maximum(np.take_along_axis(d2, idx, axis=1), 0))
+    return layout, (idx + 1).astype(np.int32), dist
+
+
+@pytest.fixture(scope="module")
+def qp():
+    return _query_problem()
+
+
+def _probe(ref, idx, dist, perplexity, y=None, ex=1.0, n_neg=256, thr=4096, iter_seed=0, init=0):
+    lib = _lib.load()
+    nq, k = idx.shape
+    ref_cm = np.asfortranarray(ref, np.float64)
+    idx_cm = np.asfortranarray(idx, np.int32)
+    dist_cm = np.asfortranarray(dist, np.float64)
+    p = np.empty((nq, k), np.float64)
+    g = np.empty((nq, 2), np.float64)
+    y0 = np.empty((nq, 2), np.float64)
+    yy = None if y is None else np.ascontiguousarray(y, np.float64)
+    rc = lib.fastembedr_hip_transform_probe(
+        ref_cm.ctypes.data_as(C.c_void_p), ref.shape[0], idx_cm.ctypes.data_as(C.c_void_p),
+        dist_cm.ctypes.data_as(C.c_void_p), nq, k, float(perplexity),
+        None if yy is None else yy.ctypes.data_as(C.c_void_p), float(ex), int(n_neg), int(thr), int(iter_seed),
+        int(init), p.ctypes.data_as(C.c_void_p), g.ctypes.data_as(C.c_void_p), y0.ctypes.data_as(C.c_void_p))
+    _lib.check(rc, "transform probe")
+    return p, g, y0
+
+
+def _rel(a, b):
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def test_transform_p_and_init_match_oracle(hip, oracle_mod, qp):
+    _say("case: transform P + median/weighted init, n_ref=3000 nq=1200 k=30")
+    ref, idx, dist = qp
+    p, _, med = _probe(ref, idx, dist, 5.0, init=0)
+    p_ref = oracle_mod.transform_conditional_p(dist, 5.0)
+    assert np.abs(p - p_ref).max() <= TIGHT * np.abs(p_ref).max()
+    _say(f"bit-identical P entries: {np.mean(p == p_ref):.4f}")
+    np.testing.assert_array_equal(med, oracle_mod.transform_init(ref, idx, dist, oracle_mod.INIT_MEDIAN))
+    _, _, wt = _probe(ref, idx, dist, 5.0, init=1)
+    np.testing.assert_allclose(wt, oracle_mod.transform_init(ref, idx, dist, oracle_mod.INIT_WEIGHTED), rtol=1e-14)
+
+
+@pytest.mark.parametrize("mode", ["sampled", "exact"])
+def test_transform_gradient_matches_oracle(hip, oracle_mod, qp, mode):
+    _say(f"case: transform gradient ({mode})")
+    ref, idx, dist = qp
+    thr = 100 if mode == "sampled" else 4096
+    y = oracle_mod.transform_init(ref, idx, dist, oracle_mod.INIT_MEDIAN)
+    y = y + np.random.default_rng(2).normal(0, 0.3, size=y.shape)
+    p, g, _ = _probe(ref, idx, dist, 5.0, y=y, ex=1.5, n_neg=256, thr=thr, iter_seed=4 + 65537)
+    p_ref = oracle_mod.transform_conditional_p(dist, 5.0)
+    g_ref = oracle_mod.transform_gradient(ref, idx, p_ref, y, 1.5, 256, thr, 4 + 65537)
+    r = _rel(g, g_ref)
+    _say(f"gradient relative error {r:.3e}, bit-identical {np.mean(g == g_ref):.4f}")
+    assert r <= TIGHT
+
+
+def _run(ref, idx, dist, **kw):
+    from fastembedr_amd import transform_tsne
+
+    res = transform_tsne(ref, knn={"indices": idx, "distances": dist}, **kw)
+    return res.layout, res.config
+
+
+@pytest.mark.parametrize("case", ["sampled", "exact", "random_init_early", "weighted_clipped"])
+def test_transform_run_matches_oracle(hip, oracle_mod, qp, case):
+    ref, idx, dist = qp
+    kw = dict(perplexity=5.0, n_iter=60, learning_rate=0.1, exaggeration=1.0, seed=17)
+    okw = dict(perplexity=5.0, n_iter=60, learning_rate=0.1, exaggeration=1.0, seed=17)
+    if case == "sampled":
+        kw.update(exact_repulsion_threshold=100, n_negatives=256)
+        okw.update(exact_threshold=100, n_negatives=256)
+    elif case == "exact":
+        kw.update(exact_repulsion_threshold=4096)
+        okw.update(exact_threshold=4096, n_negatives=3000)
+    elif case == "random_init_early":
+        kw.update(initialization="random", early_exaggeration_iter=10, early_exaggeration=4.0,
+                  initial_momentum=0.5, exact_repulsion_threshold=100, n_negatives=64)
+        okw.update(initialization=oracle_mod.INIT_RANDOM, early_exaggeration_iter=10, early_exaggeration=4.0,
+                   initial_momentum=0.5, exact_threshold=100, n_negatives=64)
+    else:
+        kw.update(initialization="weighted", max_step_norm=0.05, max_grad_norm=0.1, exact_repulsion_threshold=100,
+                  n_negatives=128)
+        okw.update(initialization=oracle_mod.INIT_WEIGHTED, max_step_norm=0.05, max_grad_norm=0.1,
+                   exact_threshold=100, n_negatives=128)
+    _say(f"case: transform run {case}")
+    y, cfg = _run(ref, idx, dist, **kw)
+    y_ref, exact = oracle_mod.transform_run(ref, idx, dist, threads=8, **okw)
+    assert cfg["repulsion"] == ("exact_reference" if exact else "sampled_reference")
+    scale = np.abs(y_ref).max()
+    dev = np.abs(y - y_ref).max()
+    _say(f"max |dy| = {dev:.3e} (scale {scale:.2f}); bit-identical rows {np.mean(np.all(y == y_ref, axis=1)):.4f}")
+    assert dev <= 1e-9 * scale
+
+
+def test_transform_is_deterministic(hip, qp):
+    ref, idx, dist = qp
+    a, _ = _run(ref, idx, dist, n_iter=20, exact_repulsion_threshold=100, seed=3)
+    b, _ = _run(ref, idx, dist, n_iter=20, exact_repulsion_threshold=100, seed=3)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_transform_api_rules_and_labels(hip, qp):
+    ref, idx, dist = qp
+    y, cfg = _run(ref[:500], np.minimum(idx, 500), dist, n_iter=2)
+    assert cfg["repulsion"] == "exact_reference" and cfg["n_negatives"] == 500  # n_ref <= 4096
+    y, cfg = _run(ref, idx, dist, n_iter=2, exact_repulsion_threshold=1000)
+    assert cfg["repulsion"] == "sampled_reference" and cfg["n_negatives"] == 256
+    assert cfg["optimizer"] == "opentsne_style_fixed_reference_transform"
+    assert cfg["affinities"] == "precomputed_query_conditional"
+    assert cfg["affinity_storage"] == "flat_row_major_double"
+    assert y.shape == (idx.shape[0], 2) and np.all(np.isfinite(y))
+
+
+def test_transform_input_errors(hip, qp):
+    ref, idx, dist = qp
+    bad = idx.copy()
+    bad[3, 2] = 10 ** 6
+    with pytest.raises(_lib.HipBackendError, match="out of range"):
+        _run(ref, bad, dist, n_iter=1)
+    dneg = dist.copy()
+    dneg[0, 0] = -1.0
+    with pytest.raises(_lib.HipBackendError, match="finite and non-negative"):
+        _run(ref, idx, dneg, n_iter=1)
+    with pytest.raises(ValueError, match="two-dimensional"):
+        _run(np.zeros((10, 3)), idx, dist, n_iter=1)
