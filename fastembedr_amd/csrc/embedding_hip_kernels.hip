@@ -374,9 +374,7 @@ __device__ __forceinline__ Bilinear locate(float px, float py, const DeviceScala
 // scanned into tile ranges and work items of at most kChunk points, points
 // are scattered into tile order (LDS ranks, one global atomic per batch and
 // tile), and each work item accumulates its points' bilinear charges into a
-// (kTile + 1)^2 node window in LDS before adding the window to the grid.  A
-// wave whose points all lie in one cell (collapsed clusters) first reduces
-// its 12 charges across lanes, so LDS atomics never serialise 64-deep there.
+// (kTile + 1)^2 node window in LDS before adding the window to the grid.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int tile_of(const Bilinear& b, int ta) { return (b.y0 / kTile) * ta + b.x0 / kTile; }
 
@@ -493,11 +491,15 @@ __global__ __launch_bounds__(kPointThreads) void k_bin_scatter(const float2* __r
   }
 }
 
-__device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
-}
+// One work item (<= kChunk points of one tile).  The points are first
+// ordered by cell inside the tile (LDS counting sort over the kTile^2 cells),
+// then each lane walks kSpreadRun consecutive points of that order: points of
+// one cell share their four nodes, so a lane sums their 12 charges in
+// registers and adds them to the LDS window once per cell it meets instead of
+// once per point.  Dense cells, where many points pile onto the same nodes,
+// are what made per-point LDS atomics serialise.
+constexpr int kSpreadRun = kChunk / kPointThreads;
+static_assert(kSpreadRun * kPointThreads == kChunk, "a work item is one run per lane");
 
 __global__ __launch_bounds__(kPointThreads) void k_spread_tiles(const float2* __restrict__ binned,
                                                                 const int4* __restrict__ items,
@@ -506,51 +508,110 @@ __global__ __launch_bounds__(kPointThreads) void k_spread_tiles(const float2* __
                                                                 float* __restrict__ mass_y, int g, int ta) {
 #pragma clang fp contract(off)
   constexpr int W = kTile + 1;
+  constexpr int kCells = kTile * kTile;
   __shared__ float acc[3 * W * W];
+  __shared__ int cell_start[kCells];
+  __shared__ float2 sorted[kChunk];
   if (static_cast<int>(blockIdx.x) >= sc->num_items) return;
   const int4 it = items[blockIdx.x];
   const int tx = it.x % ta, ty = it.x / ta;
   const int x_base = tx * kTile, y_base = ty * kTile;
   for (int e = threadIdx.x; e < 3 * W * W; e += kPointThreads) acc[e] = 0.0f;
+  for (int e = threadIdx.x; e < kCells; e += kPointThreads) cell_start[e] = 0;
   __syncthreads();
   const DeviceScalars s = *sc;
-  for (int p0 = it.y; p0 < it.z; p0 += kPointThreads) {
-    const int p = p0 + static_cast<int>(threadIdx.x);
-    const bool valid = p < it.z;
-    const float2 v = valid ? binned[p] : binned[it.y];
-    const Bilinear b = locate(v.x, v.y, s, g);
-    const float w00 = valid ? (1.0f - b.tx) * (1.0f - b.ty) : 0.0f;
-    const float w10 = valid ? b.tx * (1.0f - b.ty) : 0.0f;
-    const float w01 = valid ? (1.0f - b.tx) * b.ty : 0.0f;
-    const float w11 = valid ? b.tx * b.ty : 0.0f;
-    const int node = (b.y0 - y_base) * W + (b.x0 - x_base);
-    const int lead = __shfl(node, 0, kWave);
-    if (__all(node == lead)) {
-      const float c[12] = {w00, w10, w01, w11, w00 * v.x, w10 * v.x, w01 * v.x, w11 * v.x,
-                           w00 * v.y, w10 * v.y, w01 * v.y, w11 * v.y};
-      float r[12];
+  const int count = it.z - it.y;  // <= kChunk
+  // counting sort by cell: counts and ranks
+  float2 v[kSpreadRun];
+  int cell[kSpreadRun], rank[kSpreadRun];
 #pragma unroll
-      for (int q = 0; q < 12; ++q) r[q] = wave_sum_f(c[q]);
-      if ((threadIdx.x & (kWave - 1)) == 0) {
+  for (int q = 0; q < kSpreadRun; ++q) {
+    const int p = q * kPointThreads + static_cast<int>(threadIdx.x);
+    cell[q] = -1;
+    if (p < count) {
+      v[q] = binned[it.y + p];
+      const Bilinear b = locate(v[q].x, v[q].y, s, g);
+      cell[q] = (b.y0 - y_base) * kTile + (b.x0 - x_base);
+      rank[q] = atomicAdd(&cell_start[cell[q]], 1);
+    }
+  }
+  __syncthreads();
+  // exclusive scan of the kCells counts (one per thread)
+  static_assert(kCells == kPointThreads, "one cell per thread in the scan");
+  {
+    const int t = threadIdx.x;
+    const int c = cell_start[t];
+    int incl = c;
+    __shared__ int part[kPointThreads];
+    part[t] = incl;
+    __syncthreads();
+    for (int off = 1; off < kPointThreads; off <<= 1) {
+      const int add = t >= off ? part[t - off] : 0;
+      __syncthreads();
+      part[t] += add;
+      __syncthreads();
+    }
+    cell_start[t] = part[t] - c;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kSpreadRun; ++q) {
+    if (cell[q] >= 0) sorted[cell_start[cell[q]] + rank[q]] = v[q];
+  }
+  __syncthreads();
+  // each lane: kSpreadRun consecutive points of the cell order
+  float c[12];
+  int cur = -1;
+#pragma unroll
+  for (int m = 0; m < 12; ++m) c[m] = 0.0f;
+  const int p0 = static_cast<int>(threadIdx.x) * kSpreadRun;
+#pragma unroll
+  for (int q = 0; q < kSpreadRun; ++q) {
+    const int p = p0 + q;
+    if (p >= count) break;
+    const float2 u = sorted[p];
+    const Bilinear b = locate(u.x, u.y, s, g);
+    const int node = (b.y0 - y_base) * W + (b.x0 - x_base);
+    if (node != cur) {
+      if (cur >= 0) {
 #pragma unroll
         for (int m = 0; m < 3; ++m) {
-          float* a = acc + m * W * W + lead;
-          atomicAdd(a, r[4 * m + 0]);
-          atomicAdd(a + 1, r[4 * m + 1]);
-          atomicAdd(a + W, r[4 * m + 2]);
-          atomicAdd(a + W + 1, r[4 * m + 3]);
+          float* a = acc + m * W * W + cur;
+          atomicAdd(a, c[4 * m + 0]);
+          atomicAdd(a + 1, c[4 * m + 1]);
+          atomicAdd(a + W, c[4 * m + 2]);
+          atomicAdd(a + W + 1, c[4 * m + 3]);
         }
       }
-    } else if (valid) {
-      const float mv[3] = {1.0f, v.x, v.y};
+      cur = node;
 #pragma unroll
-      for (int m = 0; m < 3; ++m) {
-        float* a = acc + m * W * W + node;
-        atomicAdd(a, m == 0 ? w00 : w00 * mv[m]);
-        atomicAdd(a + 1, m == 0 ? w10 : w10 * mv[m]);
-        atomicAdd(a + W, m == 0 ? w01 : w01 * mv[m]);
-        atomicAdd(a + W + 1, m == 0 ? w11 : w11 * mv[m]);
-      }
+      for (int m = 0; m < 12; ++m) c[m] = 0.0f;
+    }
+    const float w00 = (1.0f - b.tx) * (1.0f - b.ty);
+    const float w10 = b.tx * (1.0f - b.ty);
+    const float w01 = (1.0f - b.tx) * b.ty;
+    const float w11 = b.tx * b.ty;
+    c[0] += w00;
+    c[1] += w10;
+    c[2] += w01;
+    c[3] += w11;
+    c[4] += w00 * u.x;
+    c[5] += w10 * u.x;
+    c[6] += w01 * u.x;
+    c[7] += w11 * u.x;
+    c[8] += w00 * u.y;
+    c[9] += w10 * u.y;
+    c[10] += w01 * u.y;
+    c[11] += w11 * u.y;
+  }
+  if (cur >= 0) {
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      float* a = acc + m * W * W + cur;
+      atomicAdd(a, c[4 * m + 0]);
+      atomicAdd(a + 1, c[4 * m + 1]);
+      atomicAdd(a + W, c[4 * m + 2]);
+      atomicAdd(a + W + 1, c[4 * m + 3]);
     }
   }
   __syncthreads();

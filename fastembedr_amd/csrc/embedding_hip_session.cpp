@@ -162,6 +162,7 @@ struct fastembedr_hip_tsne {
   GridBuffers gb;
   double p_build_ms = 0.0;
   bool timing = false;
+  int timed_only = -1;      // >= 0: time only this kernel id (others run without events)
   std::vector<hipEvent_t> events;
   std::vector<int> event_kernel;
   long long launches[fehip::kKernelCount] = {};
@@ -180,7 +181,8 @@ struct fastembedr_hip_tsne {
   template <typename Launch>
   bool timed(int kernel_id, const char* what, Launch&& launch) {
     std::size_t slot = 0;
-    if (timing) {
+    const bool record = timing && (timed_only < 0 || timed_only == kernel_id);
+    if (record) {
       slot = event_kernel.size();
       while (events.size() < 2 * (slot + 1)) {
         hipEvent_t e;
@@ -191,7 +193,7 @@ struct fastembedr_hip_tsne {
       if (!hip_ok(hipEventRecord(events[2 * slot], stream), "hipEventRecord")) return false;
     }
     if (!hip_ok(launch(), what)) return false;
-    if (timing && !hip_ok(hipEventRecord(events[2 * slot + 1], stream), "hipEventRecord")) return false;
+    if (record && !hip_ok(hipEventRecord(events[2 * slot + 1], stream), "hipEventRecord")) return false;
     return true;
   }
 
@@ -1065,6 +1067,7 @@ int fastembedr_hip_tsne_set_timing(fastembedr_hip_tsne* s, int enabled) {
   if (!valid_state_args(s)) return 1;
   if (!s->harvest_timing()) return 1;
   s->timing = enabled != 0;
+  s->timed_only = enabled >= 2 ? enabled - 2 : -1;
   if (enabled) {
     std::fill(std::begin(s->launches), std::end(s->launches), 0LL);
     std::fill(std::begin(s->total_ms), std::end(s->total_ms), 0.0);

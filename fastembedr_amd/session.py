@@ -148,8 +148,15 @@ class TsneSession:
         return float(v.value)
 
     # -- timing -------------------------------------------------------------
-    def set_timing(self, enabled: bool) -> None:
-        _lib.check(self._lib.fastembedr_hip_tsne_set_timing(self._h, int(bool(enabled))), "set_timing")
+    def set_timing(self, enabled: bool, only: str | None = None) -> None:
+        """Per-kernel HIP-event timing of run(); `only` names the one kernel
+        to time (the others then run without events)."""
+        mode = int(bool(enabled))
+        if enabled and only is not None:
+            names = [self._lib.fastembedr_hip_tsne_kernel_name(i).decode()
+                     for i in range(self._lib.fastembedr_hip_tsne_kernel_count())]
+            mode = 2 + names.index(only)
+        _lib.check(self._lib.fastembedr_hip_tsne_set_timing(self._h, mode), "set_timing")
 
     def timing(self) -> dict[str, tuple[int, float]]:
         """{kernel name: (launches timed, summed ms)}."""

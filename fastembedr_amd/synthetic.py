@@ -134,6 +134,31 @@ def exact_knn_torch(x: np.ndarray, k: int, device: str = "cuda", chunk: int = 40
     return idx, dist
 
 
+def exact_query_knn_torch(reference: np.ndarray, query: np.ndarray, k: int, device: str = "cuda",
+                          chunk: int = 4096):
+    """Exact Euclidean KNN of query rows among reference rows, with torch on
+    the GPU (input preparation for the transform).  Returns numpy (indices
+    int32 0-based, distances float64), each (n_query, k)."""
+    import torch
+
+    rt = torch.as_tensor(reference, device=device, dtype=torch.float32)
+    qt = torch.as_tensor(query, device=device, dtype=torch.float32)
+    rsq = (rt * rt).sum(dim=1)
+    nq = qt.shape[0]
+    idx = np.empty((nq, k), np.int32)
+    dist = np.empty((nq, k), np.float64)
+    for s in range(0, nq, chunk):
+        e = min(nq, s + chunk)
+        q = qt[s:e]
+        d2 = (q * q).sum(dim=1)[:, None] + rsq[None, :] - 2.0 * (q @ rt.T)
+        d2.clamp_(min=0.0)
+        vals, inds = torch.topk(d2, k, dim=1, largest=False, sorted=True)
+        idx[s:e] = inds.to(torch.int32).cpu().numpy()
+        dist[s:e] = vals.sqrt().double().cpu().numpy()
+        del d2, vals, inds
+    return idx, dist
+
+
 def to_r_layout(indices: np.ndarray, distances: np.ndarray, one_based: bool = True):
     """(n, k) arrays -> column-major int32 / float32 as R would hand them over."""
     idx = np.asfortranarray(indices.astype(np.int32) + (1 if one_based else 0))
