@@ -1249,6 +1249,181 @@ __global__ __launch_bounds__(NT) void k_attract_tiles(const unsigned int* __rest
   for (int r = threadIdx.x; r < rows; r += NT) attr[r0 + r] = make_float2(acc_x[r], acc_y[r]);
 }
 
+// Wave-level helpers for the segmented variant (gfx9 DPP: row shifts within
+// 16-lane rows, row broadcasts 15 / 31, whole-wave shifts by one lane).
+// Lanes whose source lies outside the row / wave read 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, true);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, true));
+}
+constexpr int kDppRowShr = 0x110;    // + shift (1..15)
+constexpr int kDppWaveShl1 = 0x130;  // lane l reads lane l + 1
+constexpr int kDppWaveShr1 = 0x138;  // lane l reads lane l - 1
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+
+// One step of an inclusive segmented scan: (x, y, start) combined with the
+// value `shifted` lanes below; `start` marks a lane (or window) that begins
+// a segment, whose value then takes nothing from below.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void seg_step(float& x, float& y, int& start) {
+  const float px = dpp_f<CTRL, ROW_MASK>(x);
+  const float py = dpp_f<CTRL, ROW_MASK>(y);
+  const int ps = dpp_i<CTRL, ROW_MASK>(start);
+  if (!start) {
+    x += px;
+    y += py;
+    start = ps;
+  }
+}
+
+// Tiled attraction with a wave-level merge of row partial sums.  A lane's
+// kTileRun entries hold one or more rows (in order); the part of its first
+// row and of its last row are summed in registers, rows strictly inside the
+// group go straight to LDS.  A row that runs across lanes is then summed by
+// an inclusive segmented scan over the wave (DPP), and only the lane that
+// ends the row adds it to the row's accumulator, so the accumulator atomics
+// of one wave never collide.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_attract_tiles_seg(const unsigned int* __restrict__ ent,
+                                                          const float* __restrict__ val,
+                                                          const int* __restrict__ tile_ptr,
+                                                          const int* __restrict__ tile_cb,
+                                                          const int* __restrict__ tile_beg,
+                                                          const float2* __restrict__ y_cur,
+                                                          float2* __restrict__ attr, float exaggeration, int n,
+                                                          int row_blocks, int xcds) {
+  __shared__ float2 ys[kTileCols];
+  __shared__ float2 yr[kTileRows];
+  __shared__ float acc_x[kTileRows];
+  __shared__ float acc_y[kTileRows];
+  const int xcd = static_cast<int>(blockIdx.x) % xcds;
+  const int slot = static_cast<int>(blockIdx.x) / xcds;
+  const int per_xcd = (row_blocks + xcds - 1) / xcds;
+  const int rb = xcd * per_xcd + slot;
+  if (slot >= per_xcd || rb >= row_blocks) return;  // whole workgroup
+  const int r0 = rb * kTileRows;
+  const int rows = min(kTileRows, n - r0);
+  for (int r = threadIdx.x; r < kTileRows; r += NT) {
+    acc_x[r] = 0.0f;
+    acc_y[r] = 0.0f;
+    yr[r] = r < rows ? y_cur[r0 + r] : make_float2(0.0f, 0.0f);
+  }
+  const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+  const int t1 = tile_ptr[rb + 1];
+  for (int t = tile_ptr[rb]; t < t1; ++t) {
+    const int base = tile_cb[t] * kTileCols;
+    const int cnt = min(kTileCols, n - base);
+    const int e0 = tile_beg[t];
+    const int e1 = tile_beg[t + 1];
+    __syncthreads();  // the previous tile's LDS reads are done
+    for (int q = threadIdx.x; q < cnt; q += NT) ys[q] = y_cur[base + q];
+    __syncthreads();
+    // every lane of a wave runs the same number of rounds (DPP needs them all)
+    const int rounds = (e1 - e0 + NT * kTileRun - 1) / (NT * kTileRun);
+    for (int round = 0; round < rounds; ++round) {
+      const int e = e0 + (round * NT + static_cast<int>(threadIdx.x)) * kTileRun;
+      const bool active = e < e1;
+      int key[kTileRun];
+      float cx[kTileRun], cy[kTileRun];
+      if (active) {
+        const uint4 w0 = *reinterpret_cast<const uint4*>(ent + e);
+        const uint4 w1 = *reinterpret_cast<const uint4*>(ent + e + 4);
+        const float4 p0 = *reinterpret_cast<const float4*>(val + e);
+        const float4 p1 = *reinterpret_cast<const float4*>(val + e + 4);
+        const unsigned int w[kTileRun] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        const float p[kTileRun] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+        for (int q = 0; q < kTileRun; ++q) {
+          // padding (only at the end of a run, never first in a group) joins
+          // the previous entry's row with a zero contribution
+          const bool pad = w[q] == 0xffffffffu;
+          key[q] = pad ? (q > 0 ? key[q > 0 ? q - 1 : 0] : 0) : static_cast<int>(w[q] >> 16);
+          const int lc = pad ? 0 : static_cast<int>(w[q] & 0xffffu);
+          const float2 yi = yr[key[q]];
+          const float2 yj = ys[lc];
+          const float dx = yi.x - yj.x;
+          const float dy = yi.y - yj.y;
+          const float qq = 1.0f / (1.0f + (dx * dx + dy * dy));
+          const float c = exaggeration * p[q] * qq;
+          cx[q] = c * dx;
+          cy[q] = c * dy;
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < kTileRun; ++q) {
+          key[q] = -1;
+          cx[q] = 0.0f;
+          cy[q] = 0.0f;
+        }
+      }
+      const int kf = key[0];
+      const int kl = key[kTileRun - 1];
+      float hx = 0.0f, hy = 0.0f, tx = 0.0f, ty = 0.0f;
+      int mid = -1;
+      float mx = 0.0f, my = 0.0f;
+#pragma unroll
+      for (int q = 0; q < kTileRun; ++q) {
+        if (key[q] == kl) {
+          tx += cx[q];
+          ty += cy[q];
+        } else if (key[q] == kf) {
+          hx += cx[q];
+          hy += cy[q];
+        } else {  // a row that starts and ends inside this group
+          if (key[q] != mid) {
+            if (mid >= 0) {
+              atomicAdd(&acc_x[mid], mx);
+              atomicAdd(&acc_y[mid], my);
+            }
+            mid = key[q];
+            mx = 0.0f;
+            my = 0.0f;
+          }
+          mx += cx[q];
+          my += cy[q];
+        }
+      }
+      if (mid >= 0) {
+        atomicAdd(&acc_x[mid], mx);
+        atomicAdd(&acc_y[mid], my);
+      }
+      // Lane l continues lane l - 1's last row when its first row is that
+      // row; the tail of a single-row lane then carries on, a multi-row
+      // lane's tail starts afresh and its head takes the carry.
+      const int prev_kl = dpp_i<kDppWaveShr1, 0xf>(kl + 1) - 1;  // -1 on lane 0
+      const bool joins = kf >= 0 && kf == prev_kl;
+      const bool multi = kf != kl;
+      int start = (multi || !joins) ? 1 : 0;
+      seg_step<kDppRowShr + 1, 0xf>(tx, ty, start);
+      seg_step<kDppRowShr + 2, 0xf>(tx, ty, start);
+      seg_step<kDppRowShr + 4, 0xf>(tx, ty, start);
+      seg_step<kDppRowShr + 8, 0xf>(tx, ty, start);
+      seg_step<kDppRowBcast15, 0xa>(tx, ty, start);
+      seg_step<kDppRowBcast31, 0xc>(tx, ty, start);
+      // carry into a multi-row lane's head: the scanned tail of lane l - 1
+      const float carry_x = dpp_f<kDppWaveShr1, 0xf>(tx);
+      const float carry_y = dpp_f<kDppWaveShr1, 0xf>(ty);
+      const int next_kf = dpp_i<kDppWaveShl1, 0xf>(kf + 1) - 1;  // -1 on lane 63
+      if (multi && kf >= 0) {
+        atomicAdd(&acc_x[kf], hx + (joins ? carry_x : 0.0f));
+        atomicAdd(&acc_y[kf], hy + (joins ? carry_y : 0.0f));
+      }
+      const bool continued = lane != kWave - 1 && next_kf == kl;
+      if (kl >= 0 && !continued) {
+        atomicAdd(&acc_x[kl], tx);
+        atomicAdd(&acc_y[kl], ty);
+      }
+    }
+  }
+  __syncthreads();
+  for (int r = threadIdx.x; r < rows; r += NT) attr[r0 + r] = make_float2(acc_x[r], acc_y[r]);
+}
+
 // Point-parallel second half of an iteration: the grid repulsion read back
 // at the point (src/tsne_neighbors.cpp:1165-1180) or an exact one, plus the
 // attraction, gives the gradient; then the gains/momentum/step-clip update
@@ -1929,25 +2104,30 @@ hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream) {
 }
 
 hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int threads,
-                                int xcds, hipStream_t stream) {
+                                int xcds, bool wave_merge, hipStream_t stream) {
   const int per_xcd = (t.row_blocks + xcds - 1) / xcds;
   const int blocks = per_xcd * xcds;
+#define FEHIP_TILED(NT_)                                                                                          \
+  if (wave_merge)                                                                                                 \
+    k_attract_tiles_seg<NT_><<<blocks, NT_, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur,   \
+                                                         attr, exaggeration, t.n, t.row_blocks, xcds);            \
+  else                                                                                                            \
+    k_attract_tiles<NT_><<<blocks, NT_, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr, \
+                                                     exaggeration, t.n, t.row_blocks, xcds);
   switch (threads) {
     case 256:
-      k_attract_tiles<256><<<blocks, 256, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr,
-                                                       exaggeration, t.n, t.row_blocks, xcds);
+      FEHIP_TILED(256)
       break;
     case 512:
-      k_attract_tiles<512><<<blocks, 512, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr,
-                                                       exaggeration, t.n, t.row_blocks, xcds);
+      FEHIP_TILED(512)
       break;
     case 1024:
-      k_attract_tiles<1024><<<blocks, 1024, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur,
-                                                         attr, exaggeration, t.n, t.row_blocks, xcds);
+      FEHIP_TILED(1024)
       break;
     default:
       return hipErrorInvalidValue;
   }
+#undef FEHIP_TILED
   return hipGetLastError();
 }
 

@@ -145,6 +145,7 @@ struct fastembedr_hip_tsne {
   // tiles follow the working numbering and are rebuilt after it changes.
   bool attract_tiled = true;
   int tile_threads = 512;
+  bool wave_merge = true;   // k_attract_tiles_seg; FASTEMBEDR_HIP_ATTRACT_WAVE_MERGE=0: k_attract_tiles
   fehip::Tiles tiles;
   int tiles_for = -2;       // value of wi the tiles were built for; -2: none
 
@@ -371,7 +372,7 @@ bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggera
   }
   return s->timed(fehip::kKAttract, "attract launch", [&] {
     return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->tile_threads, s->xcds,
-                                       s->stream);
+                                       s->wave_merge, s->stream);
   });
 }
 
@@ -697,6 +698,7 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
     if (std::strcmp(tiled, "0") == 0) s->attract_tiled = false;
   }
   s->tile_threads = env_int("FASTEMBEDR_HIP_TILE_THREADS", s->tile_threads);
+  if (const char* wm = std::getenv("FASTEMBEDR_HIP_ATTRACT_WAVE_MERGE")) s->wave_merge = std::strcmp(wm, "0") != 0;
   if (s->tile_threads != 256 && s->tile_threads != 512 && s->tile_threads != 1024) s->tile_threads = 512;
   if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {
     delete s;

@@ -239,9 +239,10 @@ void tiles_shape(int n, long long nnz, Tiles& t);
 hipError_t tiles_temp_bytes(const Tiles& t, std::size_t& bytes);
 // Rebuilds t from the CSR (same numbering), all on `stream`.
 hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream);
-// threads: workgroup size, 256, 512 or 1024 (one row block per workgroup).
+// threads: workgroup size, 256, 512 or 1024 (one row block per workgroup);
+// wave_merge: sum row parts across the lanes of a wave before the LDS adds.
 hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int threads,
-                                int xcds, hipStream_t stream);
+                                int xcds, bool wave_merge, hipStream_t stream);
 
 // ---- exact O(n^2) terms (gradient check and KL) ----------------------------
 hipError_t launch_exact_repulsion(const float2* y, int n, float2* rep, double* z_partial, DeviceScalars* sc,
