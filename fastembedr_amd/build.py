@@ -60,12 +60,14 @@ def build(verbose: bool = True) -> Path:
     inc = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
     kobj = BUILD_DIR / "embedding_hip_kernels.o"
     tobj = BUILD_DIR / "transform_hip.o"
+    iobj = BUILD_DIR / "interp_grid_hip.o"
     sobj = BUILD_DIR / "embedding_hip_session.o"
     _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(CSRC / "embedding_hip_kernels.hip"), "-o", str(kobj)])
     _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(CSRC / "transform_hip.hip"), "-o", str(tobj)])
+    _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(CSRC / "interp_grid_hip.hip"), "-o", str(iobj)])
     _run([hipcc, *HOST_FLAGS, *inc, "-c", str(CSRC / "embedding_hip_session.cpp"), "-o", str(sobj)])
     tmp = LIB.with_suffix(".so.tmp")
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", str(kobj), str(tobj), str(sobj), "-o", str(tmp)])
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", str(kobj), str(tobj), str(iobj), str(sobj), "-o", str(tmp)])
     os.replace(tmp, LIB)
     return LIB
 

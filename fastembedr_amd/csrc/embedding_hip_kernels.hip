@@ -33,101 +33,11 @@
 #include <algorithm>
 #include <cmath>
 
+#include "device_common.h"
 #include "tsne_device.h"
 
 namespace fehip {
 namespace {
-
-constexpr int kWave = 64;
-
-constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
-
-__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
-__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
-__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
-  return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
-}
-__device__ __forceinline__ float2 cscale(float2 a, float s) { return make_float2(a.x * s, a.y * s); }
-__device__ __forceinline__ float2 conjf2(float2 a) { return make_float2(a.x, -a.y); }
-// i * a
-__device__ __forceinline__ float2 mul_i(float2 a) { return make_float2(-a.y, a.x); }
-
-// ---------------------------------------------------------------------------
-// Reductions
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
-}
-
-__device__ __forceinline__ void combine(BlockStats& a, const BlockStats& b) {
-  a.min_x = fminf(a.min_x, b.min_x);
-  a.max_x = fmaxf(a.max_x, b.max_x);
-  a.min_y = fminf(a.min_y, b.min_y);
-  a.max_y = fmaxf(a.max_y, b.max_y);
-  a.sum_x += b.sum_x;
-  a.sum_y += b.sum_y;
-}
-
-__device__ __forceinline__ BlockStats stats_identity() {
-  BlockStats s;
-  s.min_x = FLT_MAX;
-  s.max_x = -FLT_MAX;
-  s.min_y = FLT_MAX;
-  s.max_y = -FLT_MAX;
-  s.sum_x = 0.0;
-  s.sum_y = 0.0;
-  return s;
-}
-
-__device__ __forceinline__ BlockStats wave_stats(BlockStats s) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    BlockStats o;
-    o.min_x = __shfl_xor(s.min_x, off, kWave);
-    o.max_x = __shfl_xor(s.max_x, off, kWave);
-    o.min_y = __shfl_xor(s.min_y, off, kWave);
-    o.max_y = __shfl_xor(s.max_y, off, kWave);
-    o.sum_x = __shfl_xor(s.sum_x, off, kWave);
-    o.sum_y = __shfl_xor(s.sum_y, off, kWave);
-    combine(s, o);
-  }
-  return s;
-}
-
-// Block-wide reduction; the result is valid in thread 0.  Fixed order, so the
-// result is deterministic for a fixed launch shape.
-template <int NT>
-__device__ BlockStats block_stats(BlockStats s) {
-  __shared__ BlockStats part[NT / kWave];
-  s = wave_stats(s);
-  const int wave = threadIdx.x / kWave;
-  if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = s;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    BlockStats t = part[0];
-    for (int w = 1; w < NT / kWave; ++w) combine(t, part[w]);
-    s = t;
-  }
-  __syncthreads();
-  return s;
-}
-
-template <int NT>
-__device__ double block_sum(double v) {
-  __shared__ double part[NT / kWave];
-  v = wave_sum(v);
-  const int wave = threadIdx.x / kWave;
-  if ((threadIdx.x & (kWave - 1)) == 0) part[wave] = v;
-  __syncthreads();
-  double t = 0.0;
-  if (threadIdx.x == 0) {
-    for (int w = 0; w < NT / kWave; ++w) t += part[w];
-  }
-  __syncthreads();
-  return t;
-}
 
 // Grid-wide reductions write one partial per block and are finished by a
 // separate single-block kernel.  (A "last block done" finish would need a
@@ -165,6 +75,28 @@ __device__ void set_geometry(DeviceScalars* sc, const BlockStats& t, int n, int 
   sc->max_x = mxx;
   sc->min_y = mny;
   sc->max_y = mxy;
+  if (sc->lg_order > 0) {
+    // FIt-SNE interpolation grid: one square over both axes from the
+    // smallest to the largest centred coordinate, max(min_intervals,
+    // ceil(span / ints_per_unit)) boxes per axis, capped at kLgMaxNodes nodes.
+    const float lo = (mnx < mny) ? mnx : mny;
+    const float hi = (mxx > mxy) ? mxx : mxy;
+    double lspan = static_cast<double>(hi) - static_cast<double>(lo);
+    if (!(lspan > 0.0) || !isfinite(lspan)) lspan = 1.0;
+    const double want = ceil(lspan / static_cast<double>(sc->lg_ints_per_unit));
+    double boxes = want > static_cast<double>(sc->lg_min_intervals) ? want : static_cast<double>(sc->lg_min_intervals);
+    const double cap = static_cast<double>(kLgMaxNodes / sc->lg_order);
+    if (!(boxes <= cap)) boxes = cap;
+    const int nb = static_cast<int>(boxes);
+    const double w = lspan / static_cast<double>(nb);
+    sc->lg_lo = lo;
+    sc->lg_box_w = static_cast<float>(w);
+    sc->lg_box_wd = w;
+    sc->lg_node_h = static_cast<float>(w / static_cast<double>(sc->lg_order));
+    sc->lg_boxes = nb;
+    sc->lg_nodes = nb * sc->lg_order;
+    sc->lg_tiles_axis = (nb + kLgTile - 1) / kLgTile;
+  }
 }
 
 template <int NT>
@@ -424,9 +356,14 @@ __device__ int block_exclusive_scan4(int (&v)[4], int* part) {
   return total;
 }
 
+// tiles < 0: the interpolation grid's tile count, lg_tiles_axis^2, read on the
+// device.  tile_item0 (optional) receives the first work item of each tile
+// and, at [tiles], the number of items.
 __global__ __launch_bounds__(1024) void k_bin_plan(int* __restrict__ tile_count, int* __restrict__ tile_cursor,
-                                                   int4* __restrict__ items, DeviceScalars* sc, int tiles) {
+                                                   int4* __restrict__ items, DeviceScalars* sc, int tiles,
+                                                   int* __restrict__ tile_item0) {
   __shared__ int part[1024];
+  if (tiles < 0) tiles = sc->lg_tiles_axis * sc->lg_tiles_axis;
   int cnt[4], start[4], chunks[4], base[4];
   for (int q = 0; q < 4; ++q) {
     const int t = threadIdx.x * 4 + q;
@@ -442,13 +379,17 @@ __global__ __launch_bounds__(1024) void k_bin_plan(int* __restrict__ tile_count,
     const int t = threadIdx.x * 4 + q;
     if (t >= tiles) continue;
     tile_cursor[t] = start[q];
+    if (tile_item0 != nullptr) tile_item0[t] = base[q];
     for (int c = 0; c < chunks[q]; ++c) {
       const int b = start[q] + c * kChunk;
       const int e = min(start[q] + cnt[q], b + kChunk);
       items[base[q] + c] = make_int4(t, b, e, 0);
     }
   }
-  if (threadIdx.x == 0) sc->num_items = total_items;
+  if (threadIdx.x == 0) {
+    sc->num_items = total_items;
+    if (tile_item0 != nullptr) tile_item0[tiles] = total_items;
+  }
 }
 
 constexpr int kScatterPerThread = 4;
@@ -634,104 +575,6 @@ __global__ __launch_bounds__(kPointThreads) void k_commit(float2* __restrict__ y
     y[i] = make_float2(v.x - sx, v.y - sy);
   }
 }
-
-// ---------------------------------------------------------------------------
-// LDS Stockham FFT
-//
-// NSEQ sequences of length F, sequence q at s + q * F, transformed in place by
-// NT threads.  Radix-4 stages (Ns = 1, 4, 16, ...) then one radix-2 stage
-// when log2(F) is odd; every stage reads its inputs to registers, barriers,
-// and writes the Stockham-permuted outputs, so the result is in natural order.
-// Twiddles come from a 4096-entry table of e^{-2 pi i m / 4096} (computed in
-// fp64 on the host); INV conjugates them and leaves the result unscaled.
-// ---------------------------------------------------------------------------
-template <bool INV>
-__device__ __forceinline__ float2 twiddle(const float2* __restrict__ tw, int m) {
-  const float2 w = tw[m];
-  return INV ? make_float2(w.x, -w.y) : w;
-}
-
-template <int F, int NSEQ, int NT, bool INV>
-__device__ __forceinline__ void fft_lds(float2* s, const float2* __restrict__ tw) {
-  constexpr int LOG2F = ilog2(F);
-  constexpr int Q = F / 4;
-  constexpr int TOT = NSEQ * Q;
-  constexpr int BPT = (TOT + NT - 1) / NT;
-  constexpr int TWS = kTwiddleLen / F;
-#pragma unroll
-  for (int stage = 0; stage < LOG2F / 2; ++stage) {
-    const int ns = 1 << (2 * stage);
-    float2 v[BPT][4];
-#pragma unroll
-    for (int b = 0; b < BPT; ++b) {
-      const int t = threadIdx.x + b * NT;
-      if (TOT % NT == 0 || t < TOT) {
-        const int q = t / Q;
-        const int j = t - q * Q;
-        const float2* src = s + q * F;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[b][r] = src[j + r * Q];
-        const int kk = j & (ns - 1);
-        const int step = (F / (4 * ns)) * kk * TWS;
-        v[b][1] = cmul(v[b][1], twiddle<INV>(tw, step));
-        v[b][2] = cmul(v[b][2], twiddle<INV>(tw, 2 * step));
-        v[b][3] = cmul(v[b][3], twiddle<INV>(tw, 3 * step));
-        const float2 a = cadd(v[b][0], v[b][2]);
-        const float2 c = csub(v[b][0], v[b][2]);
-        const float2 d = cadd(v[b][1], v[b][3]);
-        const float2 e = csub(v[b][1], v[b][3]);
-        // forward: (-i) * e, inverse: (+i) * e
-        const float2 er = INV ? make_float2(-e.y, e.x) : make_float2(e.y, -e.x);
-        v[b][0] = cadd(a, d);
-        v[b][1] = cadd(c, er);
-        v[b][2] = csub(a, d);
-        v[b][3] = csub(c, er);
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int b = 0; b < BPT; ++b) {
-      const int t = threadIdx.x + b * NT;
-      if (TOT % NT == 0 || t < TOT) {
-        const int q = t / Q;
-        const int j = t - q * Q;
-        const int kk = j & (ns - 1);
-        float2* dst = s + q * F + (j - kk) * 4 + kk;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dst[r * ns] = v[b][r];
-      }
-    }
-    __syncthreads();
-  }
-  if (LOG2F & 1) {
-    constexpr int H2 = F / 2;
-    constexpr int TOT2 = NSEQ * H2;
-#pragma unroll
-    for (int b = 0; b < (TOT2 + NT - 1) / NT; ++b) {
-      const int t = threadIdx.x + b * NT;
-      if (TOT2 % NT == 0 || t < TOT2) {
-        const int q = t / H2;
-        const int j = t - q * H2;
-        float2* base = s + q * F;
-        const float2 v0 = base[j];
-        const float2 v1 = cmul(base[j + H2], twiddle<INV>(tw, j * TWS));
-        base[j] = cadd(v0, v1);
-        base[j + H2] = csub(v0, v1);
-      }
-    }
-    __syncthreads();
-  }
-}
-
-template <int F>
-struct Shape {
-  static constexpr int G = F / 2;
-  static constexpr int H = F / 2 + 1;
-  static constexpr int KROWS = F >= 1024 ? 1 : 1024 / F;  // single-sequence rows per block
-  static constexpr int CROWS = F >= 512 ? 1 : 512 / F;    // two-sequence rows per block
-  static constexpr int CCOLS = F >= 256 ? 1 : 256 / F;    // four-buffer columns per block
-  static constexpr int NT = 256;
-};
 
 // Row transforms of the kernel quadrant.  Row y in [0, F/2] of the wrapped
 // (F x F) kernel holds K1 = 1 / (1 + h^2 (dx^2 + dy^2)) and K2 = K1^2 at
@@ -1429,7 +1272,7 @@ __global__ __launch_bounds__(NT) void k_attract_tiles_seg(const unsigned int* __
 // attraction, gives the gradient; then the gains/momentum/step-clip update
 // (src/tsne_neighbors.cpp:1217-1256), and the bounding box and fp64 mean of
 // the new layout for the next iteration's centring and grid.
-template <int MODE>
+template <int MODE, bool LG>
 __global__ __launch_bounds__(kPointThreads) void k_update(const float2* __restrict__ y_cur,
                                                           const float2* __restrict__ attr,
                                                           float2* __restrict__ y_out, float2* __restrict__ update,
@@ -1454,6 +1297,35 @@ __global__ __launch_bounds__(kPointThreads) void k_update(const float2* __restri
       const float2 r = exact_rep[i];
       gx = r.x * inv_exact;
       gy = r.y * inv_exact;
+    } else if (LG) {
+      // Interpolation-grid read-back: the 3 x 3 nodes of the point's box with
+      // the spreading's Lagrange weights.  Per node the field holds (phi0,
+      // xi_x, xi_y); the repulsion is -h sum_a L_a [o_a phi0 + xi] / Z with
+      // o_a the point's offset from node a in units of h.
+      const LgPoint b = lg_locate(yi.x, yi.y, s);
+      float wx[kLgOrder], wy[kLgOrder];
+      lg_weights3(b.ux, wx);
+      lg_weights3(b.uy, wy);
+      const int m = s.lg_nodes;
+      const float4* f0 = field + (b.by * kLgOrder) * m + b.bx * kLgOrder;
+      const float tx = 3.0f * b.ux;
+      const float ty = 3.0f * b.uy;
+      float fx = 0.0f, fy = 0.0f;
+#pragma unroll
+      for (int a = 0; a < kLgOrder; ++a) {
+        const float oy = ty - (static_cast<float>(a) + 0.5f);
+#pragma unroll
+        for (int c = 0; c < kLgOrder; ++c) {
+          const float ox = tx - (static_cast<float>(c) + 0.5f);
+          const float w = wy[a] * wx[c];
+          const float4 f = f0[a * m + c];
+          fx += w * (ox * f.x + f.y);
+          fy += w * (oy * f.x + f.z);
+        }
+      }
+      const float scale = s.lg_node_h * s.inv_sum_q;
+      gx = -fx * scale;
+      gy = -fy * scale;
     } else {
       const Bilinear b = locate(yi.x, yi.y, s, g);
       const int a00 = b.y0 * g + b.x0;
@@ -1782,10 +1654,16 @@ hipError_t attract_launch(const Csr& p, const float2* y_cur, float2* attr, float
 template <int MODE>
 hipError_t update_launch(const float2* y_cur, const float2* attr, float2* y_out, float2* update, float2* gains,
                          float2* grad_out, const float2* exact_rep, const GridBuffers& gb, const UpdateParams& up,
-                         BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream) {
+                         BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
+                         const float4* interp_field) {
   const int blocks = reduce_blocks_for(n);
-  k_update<MODE><<<blocks, kPointThreads, 0, stream>>>(y_cur, attr, y_out, update, gains, grad_out, exact_rep,
-                                                       gb.field, gb.g, up, partial, sc, n);
+  if (interp_field != nullptr && MODE != kModeGradientExact) {
+    k_update<MODE, true><<<blocks, kPointThreads, 0, stream>>>(y_cur, attr, y_out, update, gains, grad_out,
+                                                               exact_rep, interp_field, gb.g, up, partial, sc, n);
+  } else {
+    k_update<MODE, false><<<blocks, kPointThreads, 0, stream>>>(y_cur, attr, y_out, update, gains, grad_out,
+                                                                exact_rep, gb.field, gb.g, up, partial, sc, n);
+  }
   if (MODE == kModeUpdate) k_finalize_stats<<<1, 256, 0, stream>>>(partial, blocks, sc, n, gb.g, 1);
   return hipGetLastError();
 }
@@ -1867,7 +1745,12 @@ hipError_t launch_bin_count(const float2* y_stored, float2* y_cur, const DeviceS
 
 hipError_t launch_bin_plan(GridBuffers& gb, DeviceScalars* sc, hipStream_t stream) {
   const int ta = tiles_per_axis(gb.g);
-  k_bin_plan<<<1, 1024, 0, stream>>>(gb.tile_count, gb.tile_cursor, gb.items, sc, ta * ta);
+  k_bin_plan<<<1, 1024, 0, stream>>>(gb.tile_count, gb.tile_cursor, gb.items, sc, ta * ta, nullptr);
+  return hipGetLastError();
+}
+
+hipError_t launch_interp_bin_plan(InterpBuffers& ib, DeviceScalars* sc, hipStream_t stream) {
+  k_bin_plan<<<1, 1024, 0, stream>>>(ib.tile_count, ib.tile_cursor, ib.items, sc, -1, ib.tile_item0);
   return hipGetLastError();
 }
 
@@ -1917,17 +1800,18 @@ hipError_t launch_attract(const Csr& p, const float2* y_cur, float2* attr, float
 
 hipError_t launch_update(int mode, const float2* y_cur, const float2* attr, float2* y_out, float2* update,
                          float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
-                         const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream) {
+                         const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
+                         const float4* interp_field) {
   switch (mode) {
     case kModeUpdate:
       return update_launch<kModeUpdate>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc,
-                                        n, stream);
+                                        n, stream, interp_field);
     case kModeGradientGrid:
       return update_launch<kModeGradientGrid>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up,
-                                              partial, sc, n, stream);
+                                              partial, sc, n, stream, interp_field);
     case kModeGradientExact:
       return update_launch<kModeGradientExact>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up,
-                                               partial, sc, n, stream);
+                                               partial, sc, n, stream, nullptr);
     default:
       return hipErrorInvalidValue;
   }

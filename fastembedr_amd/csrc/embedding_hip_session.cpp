@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <cfloat>
+#include <cstddef>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
@@ -148,6 +149,21 @@ struct fastembedr_hip_tsne {
   bool wave_merge = true;   // k_attract_tiles_seg; FASTEMBEDR_HIP_ATTRACT_WAVE_MERGE=0: k_attract_tiles
   fehip::Tiles tiles;
   int tiles_for = -2;       // value of wi the tiles were built for; -2: none
+  // Repulsion used by run(): the bilinear grid (reference) or the FIt-SNE
+  // interpolation grid.  The interpolation buffers are allocated on first use.
+  int repulsion = FASTEMBEDR_HIP_REPULSION_GRID;
+  int lg_min_intervals = 50;
+  float lg_ints_per_unit = 1.0f;
+  bool lg_ready = false;
+  Arena lg_arena;
+  fehip::InterpBuffers ib;
+  int lg_last_fft = 0;       // FFT length of the last interpolation-grid iteration
+  // Box counts of recent iterations, copied back asynchronously (pinned ring):
+  // slot it % kLgRing holds the geometry the update of iteration it - 1 set.
+  static constexpr int kLgRing = 8;
+  int* lg_ring = nullptr;
+  hipEvent_t lg_ev[kLgRing] = {};
+  long long lg_ring_iter[kLgRing] = {};
 
   bool renumbered() const { return wi >= 0; }
   const Csr& work_p() const { return wi < 0 ? p : pw[wi]; }
@@ -172,6 +188,11 @@ struct fastembedr_hip_tsne {
   ~fastembedr_hip_tsne() {
     if (stream != nullptr) (void)hipStreamSynchronize(stream);
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
+    for (hipEvent_t e : lg_ev) {
+      if (e != nullptr) (void)hipEventDestroy(e);
+    }
+    if (lg_ring != nullptr) (void)hipHostFree(lg_ring);
+    lg_arena.release();
     tile_arena.release();
     work_arena.release();
     arena.release();
@@ -216,7 +237,9 @@ namespace {
 
 const char* kKernelNames[fehip::kKernelCount] = {
     "stats", "bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols", "charge_rows",
-    "conv_cols", "inverse_rows", "attract", "update", "commit", "renumber", "tile_build"};
+    "conv_cols", "inverse_rows", "attract", "update", "commit", "renumber", "tile_build",
+    "interp_bin_count", "interp_bin_plan", "interp_bin_scatter", "interp_spread", "interp_gather",
+    "interp_kernel_rows", "interp_kernel_cols", "interp_charge_rows", "interp_conv_cols", "interp_inverse_rows"};
 
 int key_bits_for(int n) {
   int b = 1;
@@ -374,6 +397,135 @@ bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggera
     return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->tile_threads, s->xcds,
                                        s->wave_merge, s->stream);
   });
+}
+
+// FFT length for an interpolation grid of `nodes` nodes per axis: the
+// smallest power of two >= 2 * nodes (a zero-padded linear convolution), at
+// least 64.
+int interp_fft_len(int nodes) {
+  int f = 64;
+  while (f < 2 * nodes && f < fehip::kLgMaxFft) f <<= 1;
+  return f;
+}
+
+// Interpolation-grid buffers (sized for the largest grid) and the pinned ring
+// of box counts; allocated once per session.
+bool ensure_interp(fastembedr_hip_tsne* s) {
+  if (s->lg_ready) return true;
+  const std::size_t n = static_cast<std::size_t>(s->n);
+  const std::size_t mn = fehip::kLgMaxNodes;
+  const std::size_t gmax = fehip::kLgMaxFft / 2;
+  const std::size_t hmax = gmax + 1;
+  const std::size_t items = static_cast<std::size_t>(fehip::lg_max_items(s->n));
+  const std::size_t bytes = align_up(4 * mn * mn * 4) + align_up(mn * mn * sizeof(float4)) +
+                            2 * align_up(4 * hmax * hmax * 4) + 6 * align_up(gmax * hmax * sizeof(float2)) +
+                            align_up(fehip::kLgZPartials * sizeof(double)) +
+                            3 * align_up((fehip::kMaxTiles + 1) * sizeof(int)) + align_up(items * sizeof(int4)) +
+                            align_up(items * fehip::kLgWinVals * 4) + 4096;
+  (void)n;
+  if (!memory_preflight(bytes, "HIP openTSNE interpolation grid") ||
+      !s->lg_arena.init(bytes, "hipMalloc(HIP openTSNE interpolation grid)")) {
+    return false;
+  }
+  Arena& a = s->lg_arena;
+  fehip::InterpBuffers& ib = s->ib;
+  ib.charge = a.take<float>(4 * mn * mn);
+  ib.field = a.take<float4>(mn * mn);
+  ib.k_rows = a.take<float>(4 * hmax * hmax);
+  ib.k_hat = a.take<float>(4 * hmax * hmax);
+  for (int c = 0; c < 3; ++c) ib.c_rows[c] = a.take<float2>(gmax * hmax);
+  for (int c = 0; c < 3; ++c) ib.p_rows[c] = a.take<float2>(gmax * hmax);
+  ib.z_partial = a.take<double>(fehip::kLgZPartials);
+  ib.tile_count = a.take<int>(fehip::kMaxTiles + 1);
+  ib.tile_cursor = a.take<int>(fehip::kMaxTiles + 1);
+  ib.tile_item0 = a.take<int>(fehip::kMaxTiles + 1);
+  ib.items = a.take<int4>(items);
+  ib.windows = a.take<float>(items * fehip::kLgWinVals);
+  ib.binned = s->gb.binned;
+  if (ib.windows == nullptr) {
+    set_error("internal: interpolation grid buffers do not fit their arena");
+    return false;
+  }
+  if (!hip_ok(hipMemsetAsync(ib.tile_count, 0, (fehip::kMaxTiles + 1) * sizeof(int), s->stream),
+              "hipMemset(interpolation tiles)") ||
+      !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s->lg_ring), fastembedr_hip_tsne::kLgRing * sizeof(int)),
+              "hipHostMalloc(box ring)")) {
+    return false;
+  }
+  for (int r = 0; r < fastembedr_hip_tsne::kLgRing; ++r) {
+    if (!hip_ok(hipEventCreateWithFlags(&s->lg_ev[r], hipEventDisableTiming), "hipEventCreate(box ring)")) {
+      return false;
+    }
+  }
+  s->lg_ready = true;
+  return true;
+}
+
+// Writes the interpolation-grid specification into DeviceScalars, so that the
+// statistics finalize computes its geometry (order 0 switches it off).
+bool write_interp_spec(fastembedr_hip_tsne* s, int order) {
+  struct Spec {
+    int order, min_intervals;
+    float ints_per_unit;
+  } spec{order, s->lg_min_intervals, s->lg_ints_per_unit};
+  static_assert(offsetof(DeviceScalars, lg_min_intervals) == offsetof(DeviceScalars, lg_order) + 4 &&
+                    offsetof(DeviceScalars, lg_ints_per_unit) == offsetof(DeviceScalars, lg_order) + 8,
+                "specification fields are contiguous");
+  char* dst = reinterpret_cast<char*>(s->sc) + offsetof(DeviceScalars, lg_order);
+  return hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize(interp spec)") &&
+         hip_ok(hipMemcpy(dst, &spec, sizeof(spec), hipMemcpyHostToDevice), "hipMemcpy(interp spec)");
+}
+
+// Repulsion fields of the FIt-SNE interpolation grid at FFT length fft_len;
+// y_b receives the centred layout.
+bool enqueue_interp_fields(fastembedr_hip_tsne* s, int fft_len) {
+  const int n = s->n;
+  fehip::InterpBuffers& ib = s->ib;
+  s->lg_last_fft = fft_len;
+  return s->timed(fehip::kKLgBinCount, "interp bin_count launch",
+                  [&] { return fehip::launch_interp_bin_count(s->y_a(), s->y_b, s->sc, ib, n, s->stream); }) &&
+         s->timed(fehip::kKLgBinPlan, "interp bin_plan launch",
+                  [&] { return fehip::launch_interp_bin_plan(ib, s->sc, s->stream); }) &&
+         s->timed(fehip::kKLgBinScatter, "interp bin_scatter launch",
+                  [&] { return fehip::launch_interp_bin_scatter(s->y_b, s->sc, ib, n, s->stream); }) &&
+         s->timed(fehip::kKLgSpread, "interp spread launch",
+                  [&] { return fehip::launch_interp_spread(s->sc, ib, n, s->stream); }) &&
+         s->timed(fehip::kKLgGather, "interp gather launch",
+                  [&] { return fehip::launch_interp_gather(s->sc, ib, s->stream); }) &&
+         s->timed(fehip::kKLgKernelRows, "interp kernel_rows launch",
+                  [&] { return fehip::launch_interp_fft(0, fft_len, ib, s->sc, s->tw, n, s->stream); }) &&
+         s->timed(fehip::kKLgKernelCols, "interp kernel_cols launch",
+                  [&] { return fehip::launch_interp_fft(1, fft_len, ib, s->sc, s->tw, n, s->stream); }) &&
+         s->timed(fehip::kKLgChargeRows, "interp charge_rows launch",
+                  [&] { return fehip::launch_interp_fft(2, fft_len, ib, s->sc, s->tw, n, s->stream); }) &&
+         s->timed(fehip::kKLgConvCols, "interp conv_cols launch",
+                  [&] { return fehip::launch_interp_fft(3, fft_len, ib, s->sc, s->tw, n, s->stream); }) &&
+         s->timed(fehip::kKLgInverseRows, "interp inverse_rows launch",
+                  [&] { return fehip::launch_interp_fft(4, fft_len, ib, s->sc, s->tw, n, s->stream); });
+}
+
+// Current interpolation geometry, read synchronously.
+bool read_interp_boxes(fastembedr_hip_tsne* s, int* boxes) {
+  return hip_ok(hipMemcpyAsync(boxes, &s->sc->lg_boxes, sizeof(int), hipMemcpyDeviceToHost, s->stream),
+                "hipMemcpy(boxes)") &&
+         hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize(boxes)");
+}
+
+// Device error flags raised during iterations (so far only the interpolation
+// grid's FFT-length check, which the host's bound should never trip).
+bool check_iteration_flags(fastembedr_hip_tsne* s) {
+  if (!s->lg_ready) return true;
+  unsigned int flags = 0;
+  if (!hip_ok(hipMemcpyAsync(&flags, &s->sc->error_flags, sizeof(flags), hipMemcpyDeviceToHost, s->stream),
+              "hipMemcpy(flags)") ||
+      !hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize(flags)")) {
+    return false;
+  }
+  if (flags & fehip::kErrInterpGrid) {
+    set_error("internal: interpolation grid outgrew the FFT length chosen for it");
+    return false;
+  }
+  return true;
 }
 
 // Renumbers points by the Morton order of the current layout: permutes the
@@ -943,7 +1095,7 @@ int fastembedr_hip_tsne_set_state(fastembedr_hip_tsne* s, const float* y, const 
 }
 
 int fastembedr_hip_tsne_get_state(fastembedr_hip_tsne* s, float* y, float* update, float* gains) {
-  if (!valid_state_args(s)) return 1;
+  if (!valid_state_args(s) || !check_iteration_flags(s)) return 1;
   if (y != nullptr && !download_permuted(s, s->y_a(), y)) return 1;
   if (update != nullptr && !download_permuted(s, s->update(), update)) return 1;
   if (gains != nullptr && !download_permuted(s, s->gains(), gains)) return 1;
@@ -964,6 +1116,17 @@ int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int
          hip_ok(fehip::launch_update(fehip::kModeGradientExact, s->y_a(), s->attr, nullptr, nullptr, nullptr, s->grad,
                                      s->exact_rep, s->gb, up, s->partial, s->sc, s->n, s->stream),
                 "update launch");
+  } else if (repulsion == FASTEMBEDR_HIP_REPULSION_LAGRANGE) {
+    int boxes = 0;
+    ok = ensure_interp(s) && write_interp_spec(s, fehip::kLgOrder) &&
+         hip_ok(fehip::launch_stats(s->y_a(), s->n, s->gb.g, 0, s->partial, s->sc, s->stream), "stats launch") &&
+         read_interp_boxes(s, &boxes) &&
+         enqueue_interp_fields(s, interp_fft_len(std::min(boxes * fehip::kLgOrder, fehip::kLgMaxNodes))) &&
+         enqueue_attract(s, s->y_b, exaggeration) &&
+         hip_ok(fehip::launch_update(fehip::kModeGradientGrid, s->y_b, s->attr, nullptr, nullptr, nullptr, s->grad,
+                                     nullptr, s->gb, up, s->partial, s->sc, s->n, s->stream, s->ib.field),
+                "update launch") &&
+         check_iteration_flags(s);
   } else if (repulsion == FASTEMBEDR_HIP_REPULSION_GRID) {
     ok = enqueue_gradient_fields(s, true, 0) &&
          enqueue_attract(s, s->y_b, exaggeration) &&
@@ -1009,6 +1172,26 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
                 [&] { return fehip::launch_stats(s->y_a(), n, s->gb.g, 0, s->partial, s->sc, s->stream); })) {
     return 1;
   }
+  // Interpolation grid: the FFT length must hold 2 * nodes, and the node
+  // count is set on the device each iteration.  The host learns the box
+  // count of earlier iterations through a pinned ring and bounds the current
+  // one: with the step clip a coordinate moves at most max_step_norm per
+  // iteration, so the span grows by at most 2 max_step_norm.  It runs at most
+  // kMaxLag iterations ahead of what it knows (none without the clip).
+  const bool lg = s->repulsion == FASTEMBEDR_HIP_REPULSION_LAGRANGE;
+  constexpr int kRing = fastembedr_hip_tsne::kLgRing;
+  constexpr int kMaxLag = 3;
+  static_assert(kMaxLag + 2 <= kRing, "ring slots outlive the lag");
+  const int allowed_lag = up.clip ? kMaxLag : 0;
+  const double growth =
+      up.clip ? 2.0 * (static_cast<double>(max_step_norm) * 1.0001 + 1e-3) / static_cast<double>(s->lg_ints_per_unit)
+              : 0.0;
+  int known_boxes = 0;
+  int known_it = 0;
+  if (lg) {
+    if (!read_interp_boxes(s, &known_boxes)) return 1;
+    std::fill(std::begin(s->lg_ring_iter), std::end(s->lg_ring_iter), -1LL);
+  }
   for (int it = 0; it < n_iter; ++it) {
     // Renumber before the first iteration ever run and then every
     // reorder_period iterations; the bounding box and pending shift it needs
@@ -1018,13 +1201,44 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
       s->reorder_gap = s->renumber_count == 1 ? s->reorder_period : 2 * s->reorder_gap;
     }
     ++s->since_reorder;
-    if (!enqueue_gradient_fields(s, false, 0)) return 1;
+    if (lg) {
+      for (int r = 0; r < kRing; ++r) {
+        if (s->lg_ring_iter[r] > known_it && hipEventQuery(s->lg_ev[r]) == hipSuccess) {
+          known_it = static_cast<int>(s->lg_ring_iter[r]);
+          known_boxes = s->lg_ring[r];
+        }
+      }
+      if (it - known_it > allowed_lag) {
+        const int target = it - allowed_lag;  // its slot was enqueued by iteration target - 1 < it
+        const int slot = target % kRing;
+        if (!hip_ok(hipEventSynchronize(s->lg_ev[slot]), "hipEventSynchronize(box ring)")) return 1;
+        known_it = target;
+        known_boxes = s->lg_ring[slot];
+      }
+      const long long bound =
+          static_cast<long long>(known_boxes) + static_cast<long long>(std::ceil(growth * (it - known_it))) + 1;
+      const int nodes = static_cast<int>(std::min<long long>(bound * fehip::kLgOrder, fehip::kLgMaxNodes));
+      if (!enqueue_interp_fields(s, interp_fft_len(nodes))) return 1;
+    } else if (!enqueue_gradient_fields(s, false, 0)) {
+      return 1;
+    }
     if (!enqueue_attract(s, s->y_b, exaggeration) ||
         !s->timed(fehip::kKUpdate, "update launch", [&] {
           return fehip::launch_update(fehip::kModeUpdate, s->y_b, s->attr, s->y_a(), s->update(), s->gains(),
-                                      nullptr, nullptr, s->gb, up, s->partial, s->sc, n, s->stream);
+                                      nullptr, nullptr, s->gb, up, s->partial, s->sc, n, s->stream,
+                                      lg ? s->ib.field : nullptr);
         })) {
       return 1;
+    }
+    if (lg) {
+      const int slot = (it + 1) % kRing;
+      if (!hip_ok(hipMemcpyAsync(&s->lg_ring[slot], &s->sc->lg_boxes, sizeof(int), hipMemcpyDeviceToHost,
+                                 s->stream),
+                  "hipMemcpyAsync(box ring)") ||
+          !hip_ok(hipEventRecord(s->lg_ev[slot], s->stream), "hipEventRecord(box ring)")) {
+        return 1;
+      }
+      s->lg_ring_iter[slot] = it + 1;
     }
   }
   if (!s->timed(fehip::kKCommit, "commit launch",
@@ -1036,7 +1250,50 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
 
 int fastembedr_hip_tsne_sync(fastembedr_hip_tsne* s) {
   if (!valid_state_args(s)) return 1;
-  return hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize") ? 0 : 1;
+  return hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize") && check_iteration_flags(s) ? 0 : 1;
+}
+
+int fastembedr_hip_tsne_set_repulsion(fastembedr_hip_tsne* s, int repulsion, int n_interpolation_points,
+                                      int min_num_intervals, float ints_in_interval) {
+  if (!valid_state_args(s)) return 1;
+  g_last_error.clear();
+  if (repulsion == FASTEMBEDR_HIP_REPULSION_GRID) {
+    s->repulsion = repulsion;
+    return 0;
+  }
+  if (repulsion != FASTEMBEDR_HIP_REPULSION_LAGRANGE) {
+    set_error("run() supports the bilinear grid and the FIt-SNE interpolation grid only");
+    return 1;
+  }
+  if (n_interpolation_points != fehip::kLgOrder) {
+    set_error("the HIP interpolation grid supports 3 interpolation points per interval");
+    return 1;
+  }
+  if (min_num_intervals < 1 || !(ints_in_interval > 0.0f) || !std::isfinite(ints_in_interval)) {
+    set_error("min_num_intervals must be >= 1 and ints_in_interval positive and finite");
+    return 1;
+  }
+  s->lg_min_intervals = min_num_intervals;
+  s->lg_ints_per_unit = ints_in_interval;
+  if (!ensure_interp(s) || !write_interp_spec(s, fehip::kLgOrder)) return 1;
+  s->repulsion = repulsion;
+  return 0;
+}
+
+int fastembedr_hip_tsne_interp_info(fastembedr_hip_tsne* s, int* boxes, int* nodes, int* fft_len, float* box_width,
+                                    double* z) {
+  if (!valid_state_args(s)) return 1;
+  DeviceScalars h;
+  if (!hip_ok(hipMemcpyAsync(&h, s->sc, sizeof(h), hipMemcpyDeviceToHost, s->stream), "hipMemcpy(scalars)") ||
+      !hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize(scalars)")) {
+    return 1;
+  }
+  if (boxes != nullptr) *boxes = h.lg_boxes;
+  if (nodes != nullptr) *nodes = h.lg_nodes;
+  if (fft_len != nullptr) *fft_len = s->lg_last_fft;
+  if (box_width != nullptr) *box_width = h.lg_box_w;
+  if (z != nullptr) *z = h.sum_q - static_cast<double>(s->n);
+  return 0;
 }
 
 int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* s, double* kl) {

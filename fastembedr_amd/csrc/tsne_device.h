@@ -34,6 +34,15 @@ struct alignas(16) DeviceScalars {
   unsigned long long self_edges;
   int num_items;             // spread work items of the current iteration
   int pad1;
+  // FIt-SNE interpolation grid.  The host sets the specification (lg_order
+  // 0 = unused); the statistics finalize sets the geometry of the current
+  // layout: the square [lg_lo, lg_lo + lg_boxes * lg_box_w]^2 of centred
+  // coordinates, lg_order nodes per box and axis at spacing lg_node_h.
+  int lg_order, lg_min_intervals;
+  float lg_ints_per_unit;
+  float lg_lo, lg_box_w, lg_node_h;
+  int lg_boxes, lg_nodes, lg_tiles_axis;
+  double lg_box_wd;          // box width in fp64: points are located in fp64
 };
 
 struct BlockStats {
@@ -56,7 +65,23 @@ inline int max_spread_items(int n, int g) {
   return (n + kChunk - 1) / kChunk + tiles_per_axis(g) * tiles_per_axis(g);
 }
 
-enum ErrorBits : unsigned int { kErrIndex = 1u, kErrDistance = 2u };
+enum ErrorBits : unsigned int { kErrIndex = 1u, kErrDistance = 2u, kErrInterpGrid = 4u };
+
+// FIt-SNE interpolation grid: order-3 nodes, tiles of kLgTile x kLgTile boxes
+// (one spread window of kLgWin x kLgWin nodes x 4 charges per work item), at
+// most kLgMaxNodes nodes per axis (FFT length <= 4096).
+constexpr int kLgOrder = 3;
+constexpr int kLgTile = 16;
+constexpr int kLgWin = kLgTile * kLgOrder;
+constexpr int kLgWinNodes = kLgWin * kLgWin;
+constexpr int kLgWinVals = 4 * kLgWinNodes;
+constexpr int kLgMaxNodes = 2048;
+constexpr int kLgMaxFft = 2 * kLgMaxNodes;
+constexpr int kLgMaxTilesAxis = (kLgMaxNodes / kLgOrder + kLgTile - 1) / kLgTile;
+static_assert(kLgMaxTilesAxis * kLgMaxTilesAxis <= kMaxTiles, "interpolation tiles fit the bin plan");
+inline int lg_max_items(int n) { return (n + kChunk - 1) / kChunk + kLgMaxTilesAxis * kLgMaxTilesAxis; }
+// three spectral sums per column-pass block (<= f/2 + 1 blocks), one per row block (<= f/2)
+constexpr int kLgZPartials = 3 * (kLgMaxFft / 2 + 1) + kLgMaxFft / 2;
 
 enum KernelId : int {
   kKStats = 0,
@@ -74,6 +99,16 @@ enum KernelId : int {
   kKCommit,
   kKRenumber,
   kKTileBuild,
+  kKLgBinCount,
+  kKLgBinPlan,
+  kKLgBinScatter,
+  kKLgSpread,
+  kKLgGather,
+  kKLgKernelRows,
+  kKLgKernelCols,
+  kKLgChargeRows,
+  kKLgConvCols,
+  kKLgInverseRows,
   kKernelCount
 };
 
@@ -99,6 +134,26 @@ struct GridBuffers {
   int* tile_cursor = nullptr;  // kMaxTiles
   int4* items = nullptr;       // max_spread_items(n, g): (tile, begin, end, -)
   float2* binned = nullptr;    // n centred points in tile order
+};
+
+// Buffers of the FIt-SNE interpolation grid, sized for the largest grid
+// (kLgMaxNodes nodes per axis, FFT length kLgMaxFft).  At run time the node
+// count m and the FFT length f vary; planes use row stride m, spectra row
+// stride f / 2 + 1.
+struct InterpBuffers {
+  float* charge = nullptr;     // 4 planes of m*m: node moments m0, m1x, m1y, m2 (offsets in units of h)
+  float4* field = nullptr;     // m*m potentials (phi0, xi_x, xi_y, 0)
+  float* k_rows = nullptr;     // 4 planes of (G+1)^2: row transforms of the kernels (K, K1, Bx, By)
+  float* k_hat = nullptr;      // 4 planes of (G+1)^2: kernel spectra quadrants (K^, K1^, Cx, Cy)
+  float2* c_rows[3] = {};      // G*(G+1) each: half-spectrum rows of m0, m1x, m1y
+  float2* p_rows[3] = {};      // G*(G+1) each: half-spectrum rows of phi0, xi_x, xi_y
+  double* z_partial = nullptr; // kLgZPartials: sums of the normaliser per block
+  int* tile_count = nullptr;   // kMaxTiles, zero between iterations
+  int* tile_cursor = nullptr;  // kMaxTiles
+  int* tile_item0 = nullptr;   // kMaxTiles + 1: first work item of each tile
+  int4* items = nullptr;       // lg_max_items(n)
+  float* windows = nullptr;    // lg_max_items(n) * kLgWinVals: per-item spread windows
+  float2* binned = nullptr;    // n centred points in tile order (shared with the bilinear grid)
 };
 
 struct Csr {
@@ -144,6 +199,22 @@ hipError_t launch_charge_rows(GridBuffers& gb, const float2* tw, hipStream_t str
 hipError_t launch_conv_cols(GridBuffers& gb, const float2* tw, hipStream_t stream);
 hipError_t launch_inverse_rows(GridBuffers& gb, const float2* tw, int n, DeviceScalars* sc, hipStream_t stream);
 
+// ---- FIt-SNE interpolation grid ---------------------------------------------
+// Binning, spreading and the zero-padded convolution at FFT length fft_len
+// (a power of two in [64, kLgMaxFft] with fft_len >= 2 * lg_nodes); the
+// node count itself is read on the device.  Points must already be centred
+// into y_cur by launch_interp_bin_count.
+hipError_t launch_interp_bin_count(const float2* y_stored, float2* y_cur, const DeviceScalars* sc,
+                                   InterpBuffers& ib, int n, hipStream_t stream);
+hipError_t launch_interp_bin_plan(InterpBuffers& ib, DeviceScalars* sc, hipStream_t stream);
+hipError_t launch_interp_bin_scatter(const float2* y_cur, const DeviceScalars* sc, InterpBuffers& ib, int n,
+                                     hipStream_t stream);
+hipError_t launch_interp_spread(const DeviceScalars* sc, InterpBuffers& ib, int n, hipStream_t stream);
+hipError_t launch_interp_gather(const DeviceScalars* sc, InterpBuffers& ib, hipStream_t stream);
+// which: 0 kernel rows, 1 kernel cols, 2 charge rows, 3 conv cols, 4 inverse rows (+ normaliser)
+hipError_t launch_interp_fft(int which, int fft_len, InterpBuffers& ib, DeviceScalars* sc, const float2* tw, int n,
+                             hipStream_t stream);
+
 enum AttractMode : int { kModeUpdate = 0, kModeGradientGrid = 1, kModeGradientExact = 2 };
 struct UpdateParams {
   float exaggeration;
@@ -158,9 +229,12 @@ hipError_t launch_attract(const Csr& p, const float2* y_cur, float2* attr, float
                           int xcds, hipStream_t stream);
 // Repulsion read-back + attr -> gradient; kModeUpdate applies the update and
 // computes the next iteration's statistics, the gradient modes write grad_out.
+// interp_field != nullptr reads the FIt-SNE interpolation grid instead of the
+// bilinear one (kModeUpdate and kModeGradientGrid).
 hipError_t launch_update(int mode, const float2* y_cur, const float2* attr, float2* y_out, float2* update,
                          float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
-                         const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream);
+                         const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
+                         const float4* interp_field = nullptr);
 hipError_t launch_commit(float2* y, const DeviceScalars* sc, int n, hipStream_t stream);
 
 // ---- locality renumbering ---------------------------------------------------

@@ -130,6 +130,25 @@ class TsneSession:
                    "gradient")
         return out
 
+    def set_repulsion(self, repulsion: int = _lib.REPULSION_GRID, n_interpolation_points: int = 3,
+                      min_num_intervals: int = 50, ints_in_interval: float = 1.0) -> None:
+        """Repulsion used by run(): REPULSION_GRID (the reference's bilinear
+        grid) or REPULSION_LAGRANGE (the FIt-SNE interpolation grid with
+        openTSNE's settings)."""
+        _lib.check(self._lib.fastembedr_hip_tsne_set_repulsion(self._h, int(repulsion), int(n_interpolation_points),
+                                                               int(min_num_intervals), float(ints_in_interval)),
+                   "set_repulsion")
+
+    def interp_info(self) -> dict:
+        """Interpolation-grid geometry at the current layout and the FFT
+        length of its last iteration."""
+        b, m, f = C.c_int(), C.c_int(), C.c_int()
+        w = C.c_float()
+        z = C.c_double()
+        _lib.check(self._lib.fastembedr_hip_tsne_interp_info(self._h, C.byref(b), C.byref(m), C.byref(f),
+                                                             C.byref(w), C.byref(z)), "interp_info")
+        return {"boxes": b.value, "nodes": m.value, "fft_len": f.value, "box_w": w.value, "z": z.value}
+
     def center(self) -> None:
         _lib.check(self._lib.fastembedr_hip_tsne_center(self._h), "center")
 

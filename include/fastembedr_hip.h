@@ -154,6 +154,28 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_run(fastembedr_hip_tsne* session, int
 
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_sync(fastembedr_hip_tsne* session);
 
+/* Selects the repulsion that run() uses: FASTEMBEDR_HIP_REPULSION_GRID (the
+ * reference's bilinear grid, the default) or FASTEMBEDR_HIP_REPULSION_LAGRANGE,
+ * the FIt-SNE interpolation grid (Linderman et al. 2019), which the reference
+ * names in its method strings ("fitsne", "interpolation",
+ * src/tsne_neighbors.cpp:368) but computes with the bilinear grid.  Its
+ * settings follow openTSNE's names: n_interpolation_points per box and axis
+ * (3 is supported), min_num_intervals boxes per axis at least, one box per
+ * ints_in_interval units of the layout's span.  The node count is capped at
+ * 2048 per axis (FFT length 4096); beyond it boxes widen.  gradient() with
+ * FASTEMBEDR_HIP_REPULSION_LAGRANGE uses the settings given here (defaults 3,
+ * 50, 1).  No counterpart in the reference's ABI. */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_set_repulsion(fastembedr_hip_tsne* session, int repulsion,
+                                      int n_interpolation_points, int min_num_intervals,
+                                      float ints_in_interval);
+
+/* Geometry of the FIt-SNE interpolation grid at the current layout (boxes and
+ * nodes per axis, box width), the FFT length of its last iteration and the
+ * normaliser Z = sum_{i != j} q_ij of the last repulsion evaluated (either
+ * grid).  Any pointer may be NULL. */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_interp_info(fastembedr_hip_tsne* session, int* boxes, int* nodes,
+                                    int* fft_len, float* box_width, double* z);
+
 /* Exact KL(P || Q) at the current y (src/tsne_neighbors.cpp:1258-1285), with
  * the O(n^2) normalisation computed on the device in fp64. */
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* session, double* kl);

@@ -46,6 +46,8 @@ def load() -> C.CDLL:
         "tsne_oracle_p_free": (None, [P]),
         "tsne_oracle_gradient": (I, [P, P, I, F, I, I, I, I, I, P]),
         "tsne_oracle_grid_fields": (I, [P, P, I, I, I, P, P]),
+        "tsne_oracle_lagrange_gradient": (I, [P, P, I, F, I, I, F, I, I, P, P, P]),
+        "tsne_oracle_lagrange_weights": (None, [D, I, P]),
         "tsne_oracle_update": (None, [P, P, P, P, I, F, F, F, F, I]),
         "tsne_oracle_zero_mean": (None, [P, I]),
         "tsne_oracle_kl": (D, [P, P, I, I, P]),
@@ -148,6 +150,23 @@ class OracleP:
             raise ValueError(_err())
         return g
 
+    def lagrange_gradient(self, y: np.ndarray, exaggeration: float = 1.0, order: int = 3, min_intervals: int = 50,
+                          ints_per_unit: float = 1.0, direct: bool = False, threads: int = 1):
+        """FIt-SNE interpolation-grid gradient (an extension: the reference has
+        only the bilinear grid).  Returns (grad, geometry, z) with geometry =
+        {"boxes", "nodes", "lo", "box_w"}."""
+        y = np.ascontiguousarray(y, np.float32).reshape(self.n, 2)
+        g = np.empty((self.n, 2), np.float32)
+        geo = np.zeros(4, np.float64)
+        z = np.zeros(1, np.float64)
+        rc = load().tsne_oracle_lagrange_gradient(self.h, _p(y), self.n, float(exaggeration), int(order),
+                                                  int(min_intervals), float(ints_per_unit), int(bool(direct)),
+                                                  int(threads), _p(g), _p(geo), _p(z))
+        if rc != 0:
+            raise ValueError(_err())
+        geometry = {"boxes": int(geo[0]), "nodes": int(geo[1]), "lo": float(geo[2]), "box_w": float(geo[3])}
+        return g, geometry, float(z[0])
+
     def grid_fields(self, y: np.ndarray, grid_size: int = 0, threads: int = 1):
         """(geometry (lo_x, lo_y, h, 1/h), fields (4, g, g): q, q2, xq2, yq2)."""
         y = np.ascontiguousarray(y, np.float32).reshape(self.n, 2)
@@ -186,6 +205,12 @@ def update(y, upd, gains, grad, lr, momentum, min_gain=0.01, max_step_norm=5.0, 
     n = y.shape[0]
     load().tsne_oracle_update(_p(y), _p(upd), _p(gains), _p(grad), n, float(lr), float(momentum), float(min_gain),
                               float(max_step_norm), int(threads))
+
+
+def lagrange_weights(u: float, order: int) -> np.ndarray:
+    w = np.empty(order, np.float64)
+    load().tsne_oracle_lagrange_weights(float(u), int(order), _p(w))
+    return w
 
 
 def zero_mean(y):

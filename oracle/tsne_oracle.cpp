@@ -670,169 +670,229 @@ void gradient_exact(const CsrP& p, const float* y, int n, float ex, int threads,
 }
 
 // ---------------------------------------------------------------------------
-// extension: FIt-SNE interpolation grid (Linderman et al. 2019, Algorithm 1;
-// openTSNE's 2-D variant).  Square box [lo, lo + n_boxes * w] per axis with
-// n_boxes = max(min_intervals, ceil(span / ints_per_unit)) rounded up to an
-// FFT-friendly length; p equispaced nodes per box at (j + 1/2) w / p; charges
-// (1, x, y, x^2 + y^2) spread with order-p Lagrange weights; one kernel,
-// 1 / (1 + d^2)^2; potentials combined as
+// extension: FIt-SNE interpolation grid (Linderman et al., Nat. Methods 16,
+// 243 (2019), Algorithm 1, in its two-dimensional form).
+//
+// Geometry: one square region [lo, lo + span]^2 with lo the smallest and
+// lo + span the largest coordinate over both axes; n_boxes per axis =
+// max(min_intervals, ceil(span / ints_per_unit)), capped so that the node
+// count stays <= kLagrangeMaxNodes (the FFT length 2 * nodes <= 4096); box
+// width w = span / n_boxes.  Each box holds `order` equispaced nodes per
+// axis at (j + 1/2) w / order, so nodes are private to their box.
+// Charges (1, x, y, x^2 + y^2) are spread with order-p Lagrange weights; one
+// kernel, the squared Cauchy kernel 1 / (1 + d^2)^2 between nodes, is
+// convolved with all four; the potentials are interpolated back with the
+// same weights and combined as
 //   Z   = sum_i [(1 + |y_i|^2) phi0 - 2 (x_i phi1 + y_i phi2) + phi3] - n
 //   F_i = (y_i phi0 - (phi1, phi2)) / Z.
+// Everything after the geometry is fp64, so this is an accurate check for
+// the fp32 device version.  The convolution is a zero-padded fp64 FFT of
+// power-of-two length f >= 2 * nodes (any f >= 2 * nodes - 1 gives the same
+// linear convolution); `direct` replaces it by the O(nodes^4) node sum.
 // ---------------------------------------------------------------------------
-int lagrange_boxes(float span, int min_intervals, float ints_per_unit) {
-  int boxes = std::max(min_intervals, static_cast<int>(std::ceil(span / ints_per_unit)));
-  // FFT length is 2 * p * boxes; keep p * boxes a power of two times {1, 3}
-  // so that the transform stays a mixed radix-2/3 length.  (openTSNE rounds to
-  // a table of smooth sizes for the same reason.)
-  return boxes;
-}
+constexpr int kLagrangeMaxNodes = 2048;
 
 struct LagrangeGeometry {
   int boxes = 0;
   int order = 3;
   int nodes = 0;  // boxes * order per axis
-  float lo = 0.0f;
-  float box_w = 0.0f;
-  float node_h = 0.0f;
+  double lo = 0.0;
+  double box_w = 0.0;
+  double node_h = 0.0;
 };
 
+LagrangeGeometry lagrange_geometry(const float* y, int n, int order, int min_intervals, float ints_per_unit) {
+  float mnf = y[0], mxf = y[0];
+  for (std::size_t e = 0; e < 2 * static_cast<std::size_t>(n); ++e) {
+    mnf = std::min(mnf, y[e]);
+    mxf = std::max(mxf, y[e]);
+  }
+  double span = static_cast<double>(mxf) - static_cast<double>(mnf);
+  if (!(span > 0.0) || !std::isfinite(span)) span = 1.0;
+  long long boxes = static_cast<long long>(std::ceil(span / static_cast<double>(ints_per_unit)));
+  boxes = std::max<long long>(boxes, min_intervals);
+  boxes = std::min<long long>(boxes, kLagrangeMaxNodes / order);
+  LagrangeGeometry g;
+  g.order = order;
+  g.boxes = static_cast<int>(boxes);
+  g.nodes = g.boxes * order;
+  g.lo = static_cast<double>(mnf);
+  g.box_w = span / static_cast<double>(g.boxes);
+  g.node_h = g.box_w / order;
+  return g;
+}
+
+// Lagrange basis on the nodes (j + 1/2) / order of the unit box, at u.
+void lagrange_weights(double u, int order, double* w) {
+  for (int j = 0; j < order; ++j) {
+    const double tj = (j + 0.5) / order;
+    double num = 1.0, den = 1.0;
+    for (int l = 0; l < order; ++l) {
+      if (l == j) continue;
+      const double tl = (l + 0.5) / order;
+      num *= (u - tl);
+      den *= (tj - tl);
+    }
+    w[j] = num / den;
+  }
+}
+
+void lagrange_locate(const LagrangeGeometry& g, double v, int& box, double& u) {
+  const double rel = (v - g.lo) / g.box_w;
+  box = std::min(g.boxes - 1, std::max(0, static_cast<int>(std::floor(rel))));
+  u = rel - box;
+}
+
+// In-place iterative radix-2 FFT of length f (a power of two), fp64, with
+// twiddles tw[k] = e^{-2 pi i k / f} (conjugated for the inverse).
+void fft_pow2(std::complex<double>* a, int f, bool inv, const std::vector<std::complex<double>>& tw) {
+  for (int i = 1, j = 0; i < f; ++i) {
+    int bit = f >> 1;
+    for (; j & bit; bit >>= 1) j ^= bit;
+    j ^= bit;
+    if (i < j) std::swap(a[i], a[j]);
+  }
+  for (int len = 2; len <= f; len <<= 1) {
+    const int stride = f / len;
+    for (int i = 0; i < f; i += len) {
+      for (int k = 0; k < len / 2; ++k) {
+        const std::complex<double> w = inv ? std::conj(tw[static_cast<std::size_t>(k) * stride])
+                                           : tw[static_cast<std::size_t>(k) * stride];
+        const std::complex<double> u = a[i + k];
+        const std::complex<double> v = a[i + k + len / 2] * w;
+        a[i + k] = u + v;
+        a[i + k + len / 2] = u - v;
+      }
+    }
+  }
+}
+
+void fft2_pow2(std::vector<std::complex<double>>& a, int f, bool inv, int threads) {
+  std::vector<std::complex<double>> tw(static_cast<std::size_t>(f / 2));
+  for (int k = 0; k < f / 2; ++k) tw[static_cast<std::size_t>(k)] = std::polar(1.0, -2.0 * M_PI * k / f);
+  parallel_for(f, threads, [&](int b, int e, int) {
+    for (int r = b; r < e; ++r) fft_pow2(&a[static_cast<std::size_t>(r) * f], f, inv, tw);
+  });
+  parallel_for(f, threads, [&](int b, int e, int) {
+    std::vector<std::complex<double>> col(static_cast<std::size_t>(f));
+    for (int c = b; c < e; ++c) {
+      for (int r = 0; r < f; ++r) col[static_cast<std::size_t>(r)] = a[static_cast<std::size_t>(r) * f + c];
+      fft_pow2(col.data(), f, inv, tw);
+      for (int r = 0; r < f; ++r) a[static_cast<std::size_t>(r) * f + c] = col[static_cast<std::size_t>(r)];
+    }
+  });
+  if (inv) {
+    const double s = 1.0 / (static_cast<double>(f) * f);
+    for (auto& v : a) v *= s;
+  }
+}
+
+// Potentials phi_t at every node (nodes x nodes x 4, row-major by y then x).
+std::vector<double> lagrange_potentials(const std::vector<double>& charge, const LagrangeGeometry& g, bool direct,
+                                        int threads) {
+  const int m = g.nodes;
+  const double h2 = g.node_h * g.node_h;
+  auto kern = [&](int dx, int dy) {
+    const double q = 1.0 / (1.0 + h2 * (static_cast<double>(dx) * dx + static_cast<double>(dy) * dy));
+    return q * q;
+  };
+  std::vector<double> phi(static_cast<std::size_t>(m) * m * 4, 0.0);
+  if (direct) {
+    for (int ay = 0; ay < m; ++ay)
+      for (int ax = 0; ax < m; ++ax) {
+        double acc[4] = {0, 0, 0, 0};
+        for (int by = 0; by < m; ++by)
+          for (int bx = 0; bx < m; ++bx) {
+            const double k = kern(ax - bx, ay - by);
+            const double* c = &charge[(static_cast<std::size_t>(by) * m + bx) * 4];
+            for (int t = 0; t < 4; ++t) acc[t] += k * c[t];
+          }
+        for (int t = 0; t < 4; ++t) phi[(static_cast<std::size_t>(ay) * m + ax) * 4 + t] = acc[t];
+      }
+    return phi;
+  }
+  int f = 1;
+  while (f < 2 * m) f <<= 1;
+  std::vector<std::complex<double>> kh(static_cast<std::size_t>(f) * f, 0.0);
+  for (int r = 0; r < f; ++r) {
+    const int dy = r < f / 2 ? r : r - f;
+    if (std::abs(dy) >= m) continue;
+    for (int c = 0; c < f; ++c) {
+      const int dx = c < f / 2 ? c : c - f;
+      if (std::abs(dx) >= m) continue;
+      kh[static_cast<std::size_t>(r) * f + c] = kern(dx, dy);
+    }
+  }
+  fft2_pow2(kh, f, false, threads);
+  std::vector<std::complex<double>> buf(static_cast<std::size_t>(f) * f);
+  for (int t = 0; t < 4; t += 2) {
+    // two real charge grids per complex transform: conv(a + ib) = conv(a) + i conv(b)
+    std::fill(buf.begin(), buf.end(), std::complex<double>(0.0, 0.0));
+    for (int r = 0; r < m; ++r)
+      for (int c = 0; c < m; ++c) {
+        const double* ch = &charge[(static_cast<std::size_t>(r) * m + c) * 4];
+        buf[static_cast<std::size_t>(r) * f + c] = std::complex<double>(ch[t], ch[t + 1]);
+      }
+    fft2_pow2(buf, f, false, threads);
+    for (std::size_t e = 0; e < buf.size(); ++e) buf[e] *= kh[e];
+    fft2_pow2(buf, f, true, threads);
+    for (int r = 0; r < m; ++r)
+      for (int c = 0; c < m; ++c) {
+        const std::complex<double> v = buf[static_cast<std::size_t>(r) * f + c];
+        phi[(static_cast<std::size_t>(r) * m + c) * 4 + t] = v.real();
+        phi[(static_cast<std::size_t>(r) * m + c) * 4 + t + 1] = v.imag();
+      }
+  }
+  return phi;
+}
+
 void gradient_lagrange(const CsrP& p, const float* y, int n, float ex, int order, int min_intervals,
-                       float ints_per_unit, int threads, float* grad, LagrangeGeometry* geo_out) {
-  // Box geometry in double, then the charge / potential arithmetic in fp64 so
-  // this function is an accurate check for the fp32 device version.
-  double mn = y[0], mx = y[0];
-  for (int i = 0; i < n; ++i) {
-    mn = std::min(mn, static_cast<double>(std::min(y[2 * i], y[2 * i + 1])));
-    mx = std::max(mx, static_cast<double>(std::max(y[2 * i], y[2 * i + 1])));
-  }
-  const int boxes = lagrange_boxes(static_cast<float>(mx - mn), min_intervals, ints_per_unit);
-  const double box_w = (mx - mn) / boxes;
-  const int m = boxes * order;  // nodes per axis
-  const double node_h = box_w / order;
-  if (geo_out != nullptr) {
-    geo_out->boxes = boxes;
-    geo_out->order = order;
-    geo_out->nodes = m;
-    geo_out->lo = static_cast<float>(mn);
-    geo_out->box_w = static_cast<float>(box_w);
-    geo_out->node_h = static_cast<float>(node_h);
-  }
-  // Spread.
+                       float ints_per_unit, int threads, float* grad, LagrangeGeometry* geo_out,
+                       bool direct = false, double* z_out = nullptr) {
+  const LagrangeGeometry g = lagrange_geometry(y, n, order, min_intervals, ints_per_unit);
+  if (geo_out != nullptr) *geo_out = g;
+  const int m = g.nodes;
   std::vector<double> charge(static_cast<std::size_t>(m) * m * 4, 0.0);
   std::vector<double> wx(static_cast<std::size_t>(order)), wy(static_cast<std::size_t>(order));
-  auto weights = [&](double u, std::vector<double>& w) {
-    // u in [0, 1] within the box; nodes at (j + 0.5) / order
-    for (int j = 0; j < order; ++j) {
-      const double tj = (j + 0.5) / order;
-      double num = 1.0, den = 1.0;
-      for (int l = 0; l < order; ++l) {
-        if (l == j) continue;
-        const double tl = (l + 0.5) / order;
-        num *= (u - tl);
-        den *= (tj - tl);
-      }
-      w[static_cast<std::size_t>(j)] = num / den;
-    }
-  };
-  auto locate = [&](double v, int& box, double& u) {
-    double rel = (v - mn) / box_w;
-    box = std::min(boxes - 1, std::max(0, static_cast<int>(std::floor(rel))));
-    u = rel - box;
-  };
   for (int i = 0; i < n; ++i) {
     const double px = y[2 * i], py = y[2 * i + 1];
     int bx, by;
     double ux, uy;
-    locate(px, bx, ux);
-    locate(py, by, uy);
-    weights(ux, wx);
-    weights(uy, wy);
+    lagrange_locate(g, px, bx, ux);
+    lagrange_locate(g, py, by, uy);
+    lagrange_weights(ux, order, wx.data());
+    lagrange_weights(uy, order, wy.data());
     const double c[4] = {1.0, px, py, px * px + py * py};
-    for (int a = 0; a < order; ++a) {
+    for (int a = 0; a < order; ++a)
       for (int b = 0; b < order; ++b) {
-        const int node = (by * order + a) * m + (bx * order + b);
+        const std::size_t node = static_cast<std::size_t>(by * order + a) * m + (bx * order + b);
         const double w = wy[static_cast<std::size_t>(a)] * wx[static_cast<std::size_t>(b)];
-        for (int t = 0; t < 4; ++t) charge[static_cast<std::size_t>(node) * 4 + t] += w * c[t];
+        for (int t = 0; t < 4; ++t) charge[node * 4 + t] += w * c[t];
       }
-    }
   }
-  // Direct O(m^4) node-to-node interaction would be exact but slow; use a
-  // double-precision FFT convolution of size 2m with zero padding.
-  const int f = 2 * m;
-  std::vector<std::complex<double>> kern(static_cast<std::size_t>(f) * f);
-  for (int r = 0; r < f; ++r) {
-    const int dy = r < m ? r : r - f;
-    for (int c2 = 0; c2 < f; ++c2) {
-      const int dx = c2 < m ? c2 : c2 - f;
-      const double d2 = node_h * node_h * (static_cast<double>(dx) * dx + static_cast<double>(dy) * dy);
-      const double q = 1.0 / (1.0 + d2);
-      kern[static_cast<std::size_t>(r) * f + c2] = (r == m || c2 == m) ? 0.0 : q * q;
-    }
-  }
-  auto dft2 = [&](std::vector<std::complex<double>>& a, bool inv) {
-    // radix-2 when possible, otherwise a direct O(f^2) per line transform
-    const double sgn = inv ? 1.0 : -1.0;
-    std::vector<std::complex<double>> line(static_cast<std::size_t>(f)), out(static_cast<std::size_t>(f));
-    std::vector<std::complex<double>> tw(static_cast<std::size_t>(f));
-    for (int k2 = 0; k2 < f; ++k2) tw[static_cast<std::size_t>(k2)] = std::polar(1.0, sgn * 2.0 * M_PI * k2 / f);
-    auto transform = [&]() {
-      for (int k2 = 0; k2 < f; ++k2) {
-        std::complex<double> s = 0.0;
-        for (int x = 0; x < f; ++x) s += line[static_cast<std::size_t>(x)] * tw[static_cast<std::size_t>((static_cast<long long>(k2) * x) % f)];
-        out[static_cast<std::size_t>(k2)] = s;
-      }
-    };
-    for (int r = 0; r < f; ++r) {
-      for (int x = 0; x < f; ++x) line[static_cast<std::size_t>(x)] = a[static_cast<std::size_t>(r) * f + x];
-      transform();
-      for (int x = 0; x < f; ++x) a[static_cast<std::size_t>(r) * f + x] = out[static_cast<std::size_t>(x)];
-    }
-    for (int c2 = 0; c2 < f; ++c2) {
-      for (int x = 0; x < f; ++x) line[static_cast<std::size_t>(x)] = a[static_cast<std::size_t>(x) * f + c2];
-      transform();
-      for (int x = 0; x < f; ++x) a[static_cast<std::size_t>(x) * f + c2] = out[static_cast<std::size_t>(x)];
-    }
-    if (inv) {
-      const double s = 1.0 / (static_cast<double>(f) * f);
-      for (auto& v : a) v *= s;
-    }
-  };
-  dft2(kern, false);
-  std::vector<double> phi(static_cast<std::size_t>(m) * m * 4, 0.0);
-  for (int t = 0; t < 4; ++t) {
-    std::vector<std::complex<double>> buf(static_cast<std::size_t>(f) * f, 0.0);
-    for (int r = 0; r < m; ++r)
-      for (int c2 = 0; c2 < m; ++c2)
-        buf[static_cast<std::size_t>(r) * f + c2] = charge[(static_cast<std::size_t>(r) * m + c2) * 4 + t];
-    dft2(buf, false);
-    for (std::size_t e = 0; e < buf.size(); ++e) buf[e] *= kern[e];
-    dft2(buf, true);
-    for (int r = 0; r < m; ++r)
-      for (int c2 = 0; c2 < m; ++c2)
-        phi[(static_cast<std::size_t>(r) * m + c2) * 4 + t] = buf[static_cast<std::size_t>(r) * f + c2].real();
-  }
-  // Interpolate potentials back and combine.
+  const std::vector<double> phi = lagrange_potentials(charge, g, direct, threads);
   std::vector<double> pot(static_cast<std::size_t>(n) * 4, 0.0);
   double z = 0.0;
   for (int i = 0; i < n; ++i) {
     const double px = y[2 * i], py = y[2 * i + 1];
     int bx, by;
     double ux, uy;
-    locate(px, bx, ux);
-    locate(py, by, uy);
-    weights(ux, wx);
-    weights(uy, wy);
+    lagrange_locate(g, px, bx, ux);
+    lagrange_locate(g, py, by, uy);
+    lagrange_weights(ux, order, wx.data());
+    lagrange_weights(uy, order, wy.data());
     double ph[4] = {0, 0, 0, 0};
     for (int a = 0; a < order; ++a)
       for (int b = 0; b < order; ++b) {
-        const int node = (by * order + a) * m + (bx * order + b);
+        const std::size_t node = static_cast<std::size_t>(by * order + a) * m + (bx * order + b);
         const double w = wy[static_cast<std::size_t>(a)] * wx[static_cast<std::size_t>(b)];
-        for (int t = 0; t < 4; ++t) ph[t] += w * phi[static_cast<std::size_t>(node) * 4 + t];
+        for (int t = 0; t < 4; ++t) ph[t] += w * phi[node * 4 + t];
       }
     for (int t = 0; t < 4; ++t) pot[static_cast<std::size_t>(i) * 4 + t] = ph[t];
     z += (1.0 + px * px + py * py) * ph[0] - 2.0 * (px * ph[1] + py * ph[2]) + ph[3];
   }
   z -= n;
+  if (z_out != nullptr) *z_out = z;
   const double inv_z = 1.0 / std::max(z, static_cast<double>(FLT_MIN));
   for (int i = 0; i < n; ++i) {
     const double* ph = &pot[static_cast<std::size_t>(i) * 4];
@@ -1045,6 +1105,32 @@ int tsne_oracle_gradient(void* h, const float* y, int n, float exaggeration, int
   gradient(p, y, n, exaggeration, cfg, threads, ws, grad);
   return 0;
 }
+
+// FIt-SNE interpolation-grid gradient (extension) with its geometry
+// (boxes, nodes, lo, box width) and normaliser Z; direct != 0 convolves by
+// the O(nodes^4) node sum instead of the FFT.
+int tsne_oracle_lagrange_gradient(void* h, const float* y, int n, float exaggeration, int order, int min_intervals,
+                                  float ints_per_unit, int direct, int threads, float* grad, double* geometry,
+                                  double* z) {
+  g_error.clear();
+  const CsrP& p = *static_cast<CsrP*>(h);
+  if (p.n != n || order < 1 || min_intervals < 1 || !(ints_per_unit > 0.0f)) {
+    g_error = "invalid Lagrange gradient arguments";
+    return 1;
+  }
+  LagrangeGeometry g;
+  gradient_lagrange(p, y, n, exaggeration, order, min_intervals, ints_per_unit, threads, grad, &g, direct != 0, z);
+  if (geometry != nullptr) {
+    geometry[0] = g.boxes;
+    geometry[1] = g.nodes;
+    geometry[2] = g.lo;
+    geometry[3] = g.box_w;
+  }
+  return 0;
+}
+
+// Lagrange basis values of the given order at u (extension; for the pins).
+void tsne_oracle_lagrange_weights(double u, int order, double* w) { lagrange_weights(u, order, w); }
 
 // Grid geometry (lower_x, lower_y, spacing, 1/spacing) and the four
 // convolved grids (q, q2, xq2, yq2; each g*g row-major) for one y.
