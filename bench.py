@@ -5,17 +5,24 @@ Workload: 1,000,000 x 50 float32 Gaussian mixture
 (computed on the GPU with torch as input preparation), perplexity 30, PCA
 initialisation, and the reference schedule: 250 early-exaggeration
 iterations (exaggeration 12, momentum 0.5) then 500 (momentum 0.8), learning
-rate n / 12, reference CPU grid policy (256 nodes per axis at this n).
+rate n / 12.  Repulsion (--repulsion): by default the FIt-SNE interpolation
+grid with the configs' FFT settings (3 interpolation points per interval, at
+least 50 intervals, one interval per unit of span: the late-phase layout
+drives it to hundreds of intervals per axis); --repulsion grid runs the
+reference's bilinear grid with its CPU policy (256 nodes per axis at this n).
 
 A step is one gradient iteration (repulsion + attraction + update +
 centring).  Inputs (P, layout, optimiser state) are resident in HBM before
 the timed region; the P construction is timed separately.  After W untimed
 warm-up iterations the state is reset to the initialisation and the timed
 region runs the first K iterations of the schedule (K = 750 is the whole
-run).  The dominant kernel's duration comes from HIP events recorded on the
-library's own stream around each of its launches in the timed region; the
-other kernels run there without events.  A separate, untimed pass of the
-same K iterations brackets every kernel with events for the breakdown.
+run).  In the timed region the library runs the attraction and the kernel
+spectrum on side streams beside the rest of each iteration.  The dominant
+kernel's duration comes from HIP events recorded on the stream it runs on,
+around each of its launches in the timed region; the other kernels run
+without events.  A separate, untimed pass of the same K iterations runs the
+kernels in sequence and brackets every one with events for the breakdown
+(ms_per_repulsion_step sums the repulsion kernels of that pass).
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -48,7 +55,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--n", type=int, default=0, help="override the number of points (smaller smoke runs)")
-    ap.add_argument("--grid", type=int, default=0, help="grid nodes per axis; 0 = reference CPU policy")
+    ap.add_argument("--grid", type=int, default=0, help="bilinear grid nodes per axis; 0 = reference CPU policy")
+    ap.add_argument("--repulsion", choices=["interp", "grid"], default="interp",
+                    help="interp: FIt-SNE interpolation grid with the configs' FFT settings (3 points per "
+                         "interval, >= 50 intervals, one interval per unit); grid: the reference's bilinear grid")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--host-boundary", action="store_true",
@@ -104,7 +114,14 @@ def main() -> int:
     p_build_ms = sess.p_build_ms
     nnz = sess.nnz
     g = sess.grid_size
-    log(f"P build {p_build_ms:.1f} ms, nnz={nnz}, grid={g}")
+    interp = args.repulsion == "interp"
+    if interp:
+        from fastembedr_amd import _lib
+
+        sess.set_repulsion(_lib.REPULSION_LAGRANGE, sched["interpolation_points"], sched["min_intervals"],
+                           sched["ints_in_interval"])
+    log(f"P build {p_build_ms:.1f} ms, nnz={nnz}, repulsion={args.repulsion}"
+        + ("" if interp else f", grid={g}"))
 
     ee = sched["early_exaggeration_iter"]
     lr = n / 12.0
@@ -128,15 +145,23 @@ def main() -> int:
     sess.sync()
 
     # Breakdown pass (untimed): HIP events around every kernel give the
-    # per-kernel durations and pick the dominant kernel.
+    # per-kernel durations and pick the dominant kernel.  In this pass the
+    # library runs the iteration's kernels in sequence (no side streams), so
+    # each duration is the kernel's alone; the timed pass below overlaps the
+    # attraction and the kernel spectrum with the rest of the iteration.
     sess.set_timing(True)
     schedule_run(args.steps)
     sess.sync()
     breakdown = sess.timing()
     sess.set_timing(False)
-    per_kernel = {name: (tot / cnt if cnt else 0.0) for name, (cnt, tot) in breakdown.items()}
-    rep_kernels = ["spread", "kernel_rows", "kernel_cols", "charge_rows", "conv_cols", "inverse_rows"]
+    per_kernel = {name: (tot / cnt if cnt else 0.0) for name, (cnt, tot) in breakdown.items() if cnt}
+    # The repulsion step: every kernel from the binning of the points to the
+    # potentials on the grid (the read-back is fused into the update).
+    rep_kernels = [kname for kname in per_kernel if kname.startswith("interp_")] if interp else \
+        ["bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols", "charge_rows",
+         "conv_cols", "inverse_rows"]
     rep_ms = sum(per_kernel[kname] for kname in rep_kernels)
+    geo_end = sess.interp_info() if interp else None
     dom = max(breakdown, key=lambda kname: breakdown[kname][1])  # largest total time
     sess.set_state(y0)
     sess.center()
@@ -169,7 +194,7 @@ def main() -> int:
     alg_bytes = {"attract": 8.0 * nnz + 16.0 * n, "update": 56.0 * n}
     dom_bytes = alg_bytes.get(dom, 0.0)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9 if dom_ms > 0 else 0.0
-    traffic = measured_traffic(dom, n, nnz, g)
+    traffic = measured_traffic(dom, n, nnz, g, args.repulsion)
     log(f"{its:.1f} it/s, {ms_per_step:.3f} ms/step, repulsion {rep_ms:.3f} ms, {dom} {dom_ms:.3f} ms "
         f"({achieved:.0f} GB/s)")
     log("per-kernel ms (breakdown pass, every kernel bracketed by events): "
@@ -177,7 +202,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(sess, y0, n, lr, sched, args.cpu_seconds)
+        cpu = cpu_baseline(sess, y0, n, lr, sched, args.cpu_seconds, interp)
     sess.close()
     host_boundary = None
     if args.host_boundary:
@@ -199,14 +224,18 @@ def main() -> int:
         "config": {
             "workload": f"config{args.config}: {n} x 50 Gaussian mixture ({spec.components} components), "
                         f"exact KNN k={k}, perplexity 30, 250 early-exaggeration + 500 iterations, "
-                        f"PCA init, grid {g}x{g} ({'reference CPU policy' if args.grid == 0 else 'explicit'})",
+                        f"PCA init, "
+                        + ("FIt-SNE interpolation grid (3 points per interval, >= 50 intervals, "
+                           "1 interval per unit of span)" if interp else
+                           f"bilinear grid {g}x{g} ({'reference CPU policy' if args.grid == 0 else 'explicit'})"),
             "n": n,
             "k": k,
             "nnz": nnz,
-            "grid_nodes_per_axis": g,
+            "repulsion": args.repulsion,
             "timed_iterations": f"first {args.steps} of the 750-iteration schedule",
         },
         "ms_per_repulsion_step": round(rep_ms, 4),
+        "repulsion_kernels": rep_kernels,
         "p_build_ms": round(p_build_ms, 2),
         "per_kernel_ms": {kk: round(v, 5) for kk, v in per_kernel.items()},
         "roofline": {
@@ -218,11 +247,17 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "algorithmic_bytes": int(dom_bytes),
-            "traffic_source": TRAFFIC_FILE.name if traffic is not None else None,
+            "traffic_source": TRAFFIC_FILES[args.repulsion].name if traffic is not None else None,
         },
         "cpu_baseline": cpu,
         "host_boundary": host_boundary,
     }
+    if interp:
+        line["config"]["interp_grid_at_end"] = {"boxes_per_axis": geo_end["boxes"],
+                                                "nodes_per_axis": geo_end["nodes"],
+                                                "fft_len": geo_end["fft_len"]}
+    else:
+        line["config"]["grid_nodes_per_axis"] = g
     print(json.dumps(line), flush=True)
     return 0
 
@@ -346,18 +381,21 @@ def one_shot_from_host(idx_r, dist_r, y0, sched, lr):
             "includes": "host->device KNN copy, P build, 750 iterations, device->host layout copy"}
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "tsne_loop_config2_traffic.json"
+TRAFFIC_FILES = {"grid": ROOT / "profiles" / "tsne_loop_config2_traffic.json",
+                 "interp": ROOT / "profiles" / "tsne_loop_config2_interp_traffic.json"}
 
 
-def measured_traffic(kernel: str, n: int, nnz: int, g: int):
+def measured_traffic(kernel: str, n: int, nnz: int, g: int, repulsion: str):
     """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, calibrated
     against a copy of known size) from the committed rocprofv3 digest, when
     that digest was taken on this same workload; None otherwise."""
     try:
-        rec = json.loads(TRAFFIC_FILE.read_text())
+        rec = json.loads(TRAFFIC_FILES[repulsion].read_text())
     except (OSError, ValueError):
         return None
-    if (rec.get("n"), rec.get("nnz"), rec.get("grid")) != (n, nnz, g):
+    if (rec.get("n"), rec.get("nnz"), rec.get("repulsion")) != (n, nnz, repulsion):
+        return None
+    if repulsion == "grid" and rec.get("grid") != g:
         return None
     for name, t in rec.get("kernels", {}).items():
         if name.split("<")[0] == "k_" + kernel:
@@ -365,33 +403,37 @@ def measured_traffic(kernel: str, n: int, nnz: int, g: int):
     return None
 
 
-def cpu_baseline(sess, y0, n, lr, sched, budget_s):
+def cpu_baseline(sess, y0, n, lr, sched, budget_s, interp):
     """The CPU oracle (a restatement of the reference CPU path) on the same P
     and initialisation, timed on this host's cores for a bounded number of
-    early-exaggeration iterations (gradient + update + centring)."""
+    early-exaggeration iterations (gradient + update + centring), with the
+    same repulsion as the timed GPU run."""
     from oracle import oracle
 
     threads = min(16, os.cpu_count() or 1)
+    method = oracle.METHOD_LAGRANGE if interp else oracle.METHOD_GRID
     P = oracle.OracleP.wrap(*sess.csr())
     y = np.array(y0, np.float32, copy=True)
     oracle.zero_mean(y)
     t0 = time.perf_counter()
     y, _, _ = P.optimize(y, 1, 0, sched["early_exaggeration"], 1.0, lr, False, sched["initial_momentum"],
-                         sched["final_momentum"], threads=threads)
+                         sched["final_momentum"], method=method, threads=threads)
     one = time.perf_counter() - t0
     iters = max(1, min(400, int(budget_s / max(one, 1e-3))))
     t0 = time.perf_counter()
     P.optimize(y, iters, 0, sched["early_exaggeration"], 1.0, lr, False, sched["initial_momentum"],
-               sched["final_momentum"], threads=threads)
+               sched["final_momentum"], method=method, threads=threads)
     dt = time.perf_counter() - t0
     log(f"CPU oracle: {iters} iterations in {dt:.1f}s on {threads} threads")
+    rep = ("FIt-SNE interpolation grid (fp64 restatement: 3 points per interval, >= 50 intervals)" if interp
+           else "reference CPU grid policy")
     return {
         "value": round(iters / dt, 4),
         "unit": "iterations/s",
         "cores": threads,
         "kind": "port",
         "sample": f"{iters} early-exaggeration iterations (after 1 untimed) of the same n={n} problem, "
-                  f"same P and initialisation, reference CPU grid policy",
+                  f"same P and initialisation, {rep}",
     }
 
 

@@ -119,13 +119,23 @@ __device__ __forceinline__ float2 twiddle(const float2* __restrict__ tw, int m) 
   return INV ? make_float2(w.x, -w.y) : w;
 }
 
-template <int F, int NSEQ, int NT, bool INV>
+// Copies the F twiddles e^{-2 pi i j / F} of the global 4096-entry table into
+// LDS (the caller's next barrier publishes them); transforms then read their
+// twiddles from LDS (TWS = 1) instead of from the cache hierarchy.
+template <int F, int NT>
+__device__ __forceinline__ void stage_twiddles(float2* lds_tw, const float2* __restrict__ tw) {
+  constexpr int STRIDE = kTwiddleLen / F;
+  for (int j = threadIdx.x; j < F; j += NT) lds_tw[j] = tw[j * STRIDE];
+}
+
+// tw holds e^{-2 pi i j / (F * TWS)}: the global table (TWS = 4096 / F) or
+// one staged in LDS (TWS = 1).
+template <int F, int NSEQ, int NT, bool INV, int TWS = kTwiddleLen / F>
 __device__ __forceinline__ void fft_lds(float2* s, const float2* __restrict__ tw) {
   constexpr int LOG2F = ilog2(F);
   constexpr int Q = F / 4;
   constexpr int TOT = NSEQ * Q;
   constexpr int BPT = (TOT + NT - 1) / NT;
-  constexpr int TWS = kTwiddleLen / F;
 #pragma unroll
   for (int stage = 0; stage < LOG2F / 2; ++stage) {
     const int ns = 1 << (2 * stage);

@@ -95,7 +95,10 @@ __device__ void set_geometry(DeviceScalars* sc, const BlockStats& t, int n, int 
     sc->lg_node_h = static_cast<float>(w / static_cast<double>(sc->lg_order));
     sc->lg_boxes = nb;
     sc->lg_nodes = nb * sc->lg_order;
-    sc->lg_tiles_axis = (nb + kLgTile - 1) / kLgTile;
+    int tile = 1;
+    while ((nb + tile - 1) / tile > kLgMaxTilesAxis) tile *= 2;
+    sc->lg_tile = tile;
+    sc->lg_tiles_axis = (nb + tile - 1) / tile;
   }
 }
 
@@ -586,6 +589,8 @@ __global__ __launch_bounds__(256) void k_kernel_rows(const DeviceScalars* sc, co
                                                      float2* __restrict__ k_rows) {
   using S = Shape<F>;
   __shared__ float2 lds[S::KROWS * F];
+  __shared__ float2 tws[F];
+  stage_twiddles<F, S::NT>(tws, tw);
   const float h = sc->h;
   const int row0 = blockIdx.x * S::KROWS;
   for (int e = threadIdx.x; e < S::KROWS * F; e += S::NT) {
@@ -603,7 +608,7 @@ __global__ __launch_bounds__(256) void k_kernel_rows(const DeviceScalars* sc, co
     lds[e] = v;
   }
   __syncthreads();
-  fft_lds<F, S::KROWS, S::NT, false>(lds, tw);
+  fft_lds<F, S::KROWS, S::NT, false, 1>(lds, tws);
   for (int e = threadIdx.x; e < S::KROWS * S::H; e += S::NT) {
     const int r = e / S::H;
     const int kx = e - r * S::H;
@@ -620,6 +625,8 @@ __global__ __launch_bounds__(256) void k_kernel_cols(const float2* __restrict__ 
                                                      const float2* __restrict__ tw, float2* __restrict__ k_hat) {
   using S = Shape<F>;
   __shared__ float2 lds[S::KROWS * F];
+  __shared__ float2 tws[F];
+  stage_twiddles<F, S::NT>(tws, tw);
   const int col0 = blockIdx.x * S::KROWS;
   for (int e = threadIdx.x; e < S::KROWS * F; e += S::NT) {
     const int y = e / S::KROWS;
@@ -629,7 +636,7 @@ __global__ __launch_bounds__(256) void k_kernel_cols(const float2* __restrict__ 
     lds[c * F + y] = kx < S::H ? k_rows[ys * S::H + kx] : make_float2(0.0f, 0.0f);
   }
   __syncthreads();
-  fft_lds<F, S::KROWS, S::NT, false>(lds, tw);
+  fft_lds<F, S::KROWS, S::NT, false, 1>(lds, tws);
   for (int e = threadIdx.x; e < S::KROWS * S::H; e += S::NT) {
     const int ky = e / S::KROWS;
     const int c = e - ky * S::KROWS;
@@ -650,6 +657,8 @@ __global__ __launch_bounds__(256) void k_charge_rows(const float* __restrict__ m
                                                      float2* __restrict__ mx_rows, float2* __restrict__ my_rows) {
   using S = Shape<F>;
   __shared__ float2 lds[2 * S::CROWS * F];
+  __shared__ float2 tws[F];
+  stage_twiddles<F, S::NT>(tws, tw);
   const int row0 = blockIdx.x * S::CROWS;
   for (int e = threadIdx.x; e < S::CROWS * F; e += S::NT) {
     const int r = e / F;
@@ -665,7 +674,7 @@ __global__ __launch_bounds__(256) void k_charge_rows(const float* __restrict__ m
     lds[(2 * r + 1) * F + x] = b;
   }
   __syncthreads();
-  fft_lds<F, 2 * S::CROWS, S::NT, false>(lds, tw);
+  fft_lds<F, 2 * S::CROWS, S::NT, false, 1>(lds, tws);
   for (int e = threadIdx.x; e < S::CROWS * S::H; e += S::NT) {
     const int r = e / S::H;
     const int kx = e - r * S::H;
@@ -699,6 +708,8 @@ __global__ __launch_bounds__(256) void k_conv_cols(const float2* __restrict__ m_
   using S = Shape<F>;
   constexpr int C = S::CCOLS;
   __shared__ float2 lds[4 * C * F];
+  __shared__ float2 tws[F];
+  stage_twiddles<F, S::NT>(tws, tw);
   const int col0 = blockIdx.x * C;
   for (int e = threadIdx.x; e < C * F; e += S::NT) {
     const int y = e / C;
@@ -716,7 +727,7 @@ __global__ __launch_bounds__(256) void k_conv_cols(const float2* __restrict__ m_
     lds[(2 * C + c) * F + y] = d;
   }
   __syncthreads();
-  fft_lds<F, 3 * C, S::NT, false>(lds, tw);
+  fft_lds<F, 3 * C, S::NT, false, 1>(lds, tws);
   for (int e = threadIdx.x; e < C * F; e += S::NT) {
     const int ky = e / C;
     const int c = e - ky * C;
@@ -732,7 +743,7 @@ __global__ __launch_bounds__(256) void k_conv_cols(const float2* __restrict__ m_
     lds[(2 * C + c) * F + ky] = cscale(my, kk.y);
   }
   __syncthreads();
-  fft_lds<F, 4 * C, S::NT, true>(lds, tw);
+  fft_lds<F, 4 * C, S::NT, true, 1>(lds, tws);
   for (int e = threadIdx.x; e < C * S::G; e += S::NT) {
     const int y = e / C;
     const int c = e - y * C;
@@ -764,6 +775,8 @@ __global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__
                                                       int n, DeviceScalars* sc) {
   using S = Shape<F>;
   __shared__ float2 lds[2 * S::CROWS * F];
+  __shared__ float2 tws[F];
+  stage_twiddles<F, S::NT>(tws, tw);
   const int row0 = blockIdx.x * S::CROWS;
   for (int e = threadIdx.x; e < S::CROWS * F; e += S::NT) {
     const int r = e / F;
@@ -787,7 +800,7 @@ __global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__
     lds[(2 * r + 1) * F + kx] = v;
   }
   __syncthreads();
-  fft_lds<F, 2 * S::CROWS, S::NT, true>(lds, tw);
+  fft_lds<F, 2 * S::CROWS, S::NT, true, 1>(lds, tws);
   const float scale = 1.0f / (static_cast<float>(F) * static_cast<float>(F));
   double acc = 0.0;
   for (int e = threadIdx.x; e < S::CROWS * S::G; e += S::NT) {

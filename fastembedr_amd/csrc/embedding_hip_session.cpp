@@ -118,6 +118,15 @@ struct fastembedr_hip_tsne {
   int lanes = 16;
   int xcds = 1;              // XCDs of the device (blocks are dispatched round-robin over them)
   hipStream_t stream = nullptr;
+  // Side streams of run(): the attraction and the kernel spectrum depend only
+  // on the centred layout, so they run beside the binning, spreading and
+  // convolution of the main stream, which waits for them (events) before the
+  // convolution and the update.  All streams have the default priority.
+  hipStream_t side_attr = nullptr;
+  hipStream_t side_kern = nullptr;
+  hipEvent_t ev_ready = nullptr;  // centred layout written (main)
+  hipEvent_t ev_attr = nullptr;   // attraction done (side_attr)
+  hipEvent_t ev_kern = nullptr;   // kernel spectrum done (side_kern)
   Arena arena;
   Arena work_arena;         // working-order CSR copies, permutations, state double buffers
   Arena tile_arena;         // tiled P for the attraction and its build scratch
@@ -193,15 +202,25 @@ struct fastembedr_hip_tsne {
     }
     if (lg_ring != nullptr) (void)hipHostFree(lg_ring);
     lg_arena.release();
+    for (hipStream_t st : {side_attr, side_kern}) {
+      if (st != nullptr) (void)hipStreamSynchronize(st);
+    }
+    for (hipEvent_t e : {ev_ready, ev_attr, ev_kern}) {
+      if (e != nullptr) (void)hipEventDestroy(e);
+    }
     tile_arena.release();
     work_arena.release();
     arena.release();
-    if (stream != nullptr) (void)hipStreamDestroy(stream);
+    for (hipStream_t st : {stream, side_attr, side_kern}) {
+      if (st != nullptr) (void)hipStreamDestroy(st);
+    }
   }
 
-  // Enqueues one kernel, bracketed by events when timing is on.
+  // Enqueues one kernel, bracketed by events on stream `on` (the main stream
+  // by default) when timing is on.
   template <typename Launch>
-  bool timed(int kernel_id, const char* what, Launch&& launch) {
+  bool timed(int kernel_id, const char* what, Launch&& launch, hipStream_t on = nullptr) {
+    if (on == nullptr) on = stream;
     std::size_t slot = 0;
     const bool record = timing && (timed_only < 0 || timed_only == kernel_id);
     if (record) {
@@ -212,16 +231,23 @@ struct fastembedr_hip_tsne {
         events.push_back(e);
       }
       event_kernel.push_back(kernel_id);
-      if (!hip_ok(hipEventRecord(events[2 * slot], stream), "hipEventRecord")) return false;
+      if (!hip_ok(hipEventRecord(events[2 * slot], on), "hipEventRecord")) return false;
     }
     if (!hip_ok(launch(), what)) return false;
-    if (record && !hip_ok(hipEventRecord(events[2 * slot + 1], stream), "hipEventRecord")) return false;
+    if (record && !hip_ok(hipEventRecord(events[2 * slot + 1], on), "hipEventRecord")) return false;
+    return true;
+  }
+
+  bool sync_all() {
+    for (hipStream_t st : {stream, side_attr, side_kern}) {
+      if (st != nullptr && !hip_ok(hipStreamSynchronize(st), "hipStreamSynchronize")) return false;
+    }
     return true;
   }
 
   bool harvest_timing() {
     if (!timing || event_kernel.empty()) return true;
-    if (!hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize(timing)")) return false;
+    if (!sync_all()) return false;
     for (std::size_t s = 0; s < event_kernel.size(); ++s) {
       float ms = 0.0f;
       if (!hip_ok(hipEventElapsedTime(&ms, events[2 * s], events[2 * s + 1]), "hipEventElapsedTime")) return false;
@@ -239,7 +265,8 @@ const char* kKernelNames[fehip::kKernelCount] = {
     "stats", "bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols", "charge_rows",
     "conv_cols", "inverse_rows", "attract", "update", "commit", "renumber", "tile_build",
     "interp_bin_count", "interp_bin_plan", "interp_bin_scatter", "interp_spread", "interp_gather",
-    "interp_kernel_rows", "interp_kernel_cols", "interp_charge_rows", "interp_conv_cols", "interp_inverse_rows"};
+    "interp_kernel_rows", "interp_kernel_transpose", "interp_kernel_cols", "interp_charge_rows",
+    "interp_charge_transpose", "interp_conv_cols", "interp_potential_transpose", "interp_inverse_rows"};
 
 int key_bits_for(int n) {
   int b = 1;
@@ -379,24 +406,30 @@ bool alloc_tiles(fastembedr_hip_tsne* s) {
   return true;
 }
 
-// Attractive term of every row into s->attr at the centred layout y_cur.
-bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggeration) {
+// Attractive term of every row into s->attr at the centred layout y_cur, on
+// stream st (the main stream when null).
+bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggeration, hipStream_t st = nullptr) {
+  if (st == nullptr) st = s->stream;
   if (!s->attract_tiled) {
-    return s->timed(fehip::kKAttract, "attract launch", [&] {
-      return fehip::launch_attract(s->work_p(), y_cur, s->attr, exaggeration, s->lanes, s->xcds, s->stream);
-    });
+    return s->timed(
+        fehip::kKAttract, "attract launch",
+        [&] { return fehip::launch_attract(s->work_p(), y_cur, s->attr, exaggeration, s->lanes, s->xcds, st); }, st);
   }
   if (s->tiles_for != s->wi) {
-    if (!s->timed(fehip::kKTileBuild, "tile build",
-                  [&] { return fehip::launch_tile_build(s->work_p(), s->tiles, s->stream); })) {
+    if (!s->timed(
+            fehip::kKTileBuild, "tile build", [&] { return fehip::launch_tile_build(s->work_p(), s->tiles, st); },
+            st)) {
       return false;
     }
     s->tiles_for = s->wi;
   }
-  return s->timed(fehip::kKAttract, "attract launch", [&] {
-    return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->tile_threads, s->xcds,
-                                       s->wave_merge, s->stream);
-  });
+  return s->timed(
+      fehip::kKAttract, "attract launch",
+      [&] {
+        return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->tile_threads, s->xcds,
+                                           s->wave_merge, st);
+      },
+      st);
 }
 
 // FFT length for an interpolation grid of `nodes` nodes per axis: the
@@ -418,7 +451,8 @@ bool ensure_interp(fastembedr_hip_tsne* s) {
   const std::size_t hmax = gmax + 1;
   const std::size_t items = static_cast<std::size_t>(fehip::lg_max_items(s->n));
   const std::size_t bytes = align_up(4 * mn * mn * 4) + align_up(mn * mn * sizeof(float4)) +
-                            2 * align_up(4 * hmax * hmax * 4) + 6 * align_up(gmax * hmax * sizeof(float2)) +
+                            2 * align_up(2 * hmax * hmax * sizeof(float2)) +
+                            2 * align_up(3 * gmax * hmax * sizeof(float2)) +
                             align_up(fehip::kLgZPartials * sizeof(double)) +
                             3 * align_up((fehip::kMaxTiles + 1) * sizeof(int)) + align_up(items * sizeof(int4)) +
                             align_up(items * fehip::kLgWinVals * 4) + 4096;
@@ -431,10 +465,10 @@ bool ensure_interp(fastembedr_hip_tsne* s) {
   fehip::InterpBuffers& ib = s->ib;
   ib.charge = a.take<float>(4 * mn * mn);
   ib.field = a.take<float4>(mn * mn);
-  ib.k_rows = a.take<float>(4 * hmax * hmax);
-  ib.k_hat = a.take<float>(4 * hmax * hmax);
-  for (int c = 0; c < 3; ++c) ib.c_rows[c] = a.take<float2>(gmax * hmax);
-  for (int c = 0; c < 3; ++c) ib.p_rows[c] = a.take<float2>(gmax * hmax);
+  ib.k_rows = a.take<float2>(2 * hmax * hmax);
+  ib.k_cols = a.take<float2>(2 * hmax * hmax);
+  ib.spec_a = a.take<float2>(3 * gmax * hmax);
+  ib.spec_b = a.take<float2>(3 * gmax * hmax);
   ib.z_partial = a.take<double>(fehip::kLgZPartials);
   ib.tile_count = a.take<int>(fehip::kMaxTiles + 1);
   ib.tile_cursor = a.take<int>(fehip::kMaxTiles + 1);
@@ -476,32 +510,98 @@ bool write_interp_spec(fastembedr_hip_tsne* s, int order) {
          hip_ok(hipMemcpy(dst, &spec, sizeof(spec), hipMemcpyHostToDevice), "hipMemcpy(interp spec)");
 }
 
-// Repulsion fields of the FIt-SNE interpolation grid at FFT length fft_len;
-// y_b receives the centred layout.
-bool enqueue_interp_fields(fastembedr_hip_tsne* s, int fft_len) {
+// One iteration's gradient pieces.  The centred layout goes to y_b; the
+// attraction of y_b goes to attr; the repulsion fields (bilinear grid or
+// interpolation grid at FFT length fft_len) to the grid buffers.  With
+// `overlap` the attraction and the kernel spectrum run on the side streams
+// and the main stream waits for them (before the convolution and before
+// whatever follows this call); without it everything runs on the main stream.
+bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float exaggeration, bool overlap) {
   const int n = s->n;
   fehip::InterpBuffers& ib = s->ib;
-  s->lg_last_fft = fft_len;
-  return s->timed(fehip::kKLgBinCount, "interp bin_count launch",
-                  [&] { return fehip::launch_interp_bin_count(s->y_a(), s->y_b, s->sc, ib, n, s->stream); }) &&
-         s->timed(fehip::kKLgBinPlan, "interp bin_plan launch",
-                  [&] { return fehip::launch_interp_bin_plan(ib, s->sc, s->stream); }) &&
+  hipStream_t main = s->stream;
+  hipStream_t sa = overlap ? s->side_attr : main;
+  hipStream_t sk = overlap ? s->side_kern : main;
+  if (lg) s->lg_last_fft = fft_len;
+  // centre + count
+  if (lg) {
+    if (!s->timed(fehip::kKLgBinCount, "interp bin_count launch",
+                  [&] { return fehip::launch_interp_bin_count(s->y_a(), s->y_b, s->sc, ib, n, main); })) {
+      return false;
+    }
+  } else if (!s->timed(fehip::kKBinCount, "bin_count launch",
+                       [&] { return fehip::launch_bin_count(s->y_a(), s->y_b, s->sc, s->gb, n, main); })) {
+    return false;
+  }
+  if (overlap && (!hip_ok(hipEventRecord(s->ev_ready, main), "hipEventRecord(ready)") ||
+                  !hip_ok(hipStreamWaitEvent(sa, s->ev_ready, 0), "hipStreamWaitEvent(attraction)") ||
+                  !hip_ok(hipStreamWaitEvent(sk, s->ev_ready, 0), "hipStreamWaitEvent(kernel)"))) {
+    return false;
+  }
+  // side: attraction; kernel spectrum
+  if (!enqueue_attract(s, s->y_b, exaggeration, sa)) return false;
+  if (lg) {
+    static constexpr int kIds[3] = {fehip::kKLgKernelRows, fehip::kKLgKernelT, fehip::kKLgKernelCols};
+    for (int which = 0; which < 3; ++which) {
+      if (!s->timed(
+              kIds[which], "interpolation-grid kernel launch",
+              [&] { return fehip::launch_interp_fft(which, fft_len, ib, s->sc, s->tw, n, sk); }, sk)) {
+        return false;
+      }
+    }
+  } else if (!s->timed(
+                 fehip::kKKernelRows, "kernel_rows launch",
+                 [&] { return fehip::launch_kernel_rows(s->gb, s->sc, s->tw, sk); }, sk) ||
+             !s->timed(
+                 fehip::kKKernelCols, "kernel_cols launch",
+                 [&] { return fehip::launch_kernel_cols(s->gb, s->tw, sk); }, sk)) {
+    return false;
+  }
+  if (overlap && (!hip_ok(hipEventRecord(s->ev_attr, sa), "hipEventRecord(attraction)") ||
+                  !hip_ok(hipEventRecord(s->ev_kern, sk), "hipEventRecord(kernel)"))) {
+    return false;
+  }
+  // main: bins, spread, charge transforms
+  bool ok;
+  if (lg) {
+    ok = s->timed(fehip::kKLgBinPlan, "interp bin_plan launch",
+                  [&] { return fehip::launch_interp_bin_plan(ib, s->sc, main); }) &&
          s->timed(fehip::kKLgBinScatter, "interp bin_scatter launch",
-                  [&] { return fehip::launch_interp_bin_scatter(s->y_b, s->sc, ib, n, s->stream); }) &&
+                  [&] { return fehip::launch_interp_bin_scatter(s->y_b, s->sc, ib, n, main); }) &&
          s->timed(fehip::kKLgSpread, "interp spread launch",
-                  [&] { return fehip::launch_interp_spread(s->sc, ib, n, s->stream); }) &&
+                  [&] { return fehip::launch_interp_spread(s->sc, ib, n, main); }) &&
          s->timed(fehip::kKLgGather, "interp gather launch",
-                  [&] { return fehip::launch_interp_gather(s->sc, ib, s->stream); }) &&
-         s->timed(fehip::kKLgKernelRows, "interp kernel_rows launch",
-                  [&] { return fehip::launch_interp_fft(0, fft_len, ib, s->sc, s->tw, n, s->stream); }) &&
-         s->timed(fehip::kKLgKernelCols, "interp kernel_cols launch",
-                  [&] { return fehip::launch_interp_fft(1, fft_len, ib, s->sc, s->tw, n, s->stream); }) &&
+                  [&] { return fehip::launch_interp_gather(s->sc, ib, main); }) &&
          s->timed(fehip::kKLgChargeRows, "interp charge_rows launch",
-                  [&] { return fehip::launch_interp_fft(2, fft_len, ib, s->sc, s->tw, n, s->stream); }) &&
-         s->timed(fehip::kKLgConvCols, "interp conv_cols launch",
-                  [&] { return fehip::launch_interp_fft(3, fft_len, ib, s->sc, s->tw, n, s->stream); }) &&
+                  [&] { return fehip::launch_interp_fft(3, fft_len, ib, s->sc, s->tw, n, main); }) &&
+         s->timed(fehip::kKLgChargeT, "interp charge transpose launch",
+                  [&] { return fehip::launch_interp_fft(4, fft_len, ib, s->sc, s->tw, n, main); });
+  } else {
+    ok = s->timed(fehip::kKBinPlan, "bin_plan launch", [&] { return fehip::launch_bin_plan(s->gb, s->sc, main); }) &&
+         s->timed(fehip::kKBinScatter, "bin_scatter launch",
+                  [&] { return fehip::launch_bin_scatter(s->y_b, s->sc, s->gb, n, main); }) &&
+         s->timed(fehip::kKSpread, "spread launch",
+                  [&] { return fehip::launch_spread_tiles(s->sc, s->gb, n, main); }) &&
+         s->timed(fehip::kKChargeRows, "charge_rows launch",
+                  [&] { return fehip::launch_charge_rows(s->gb, s->tw, main); });
+  }
+  if (!ok) return false;
+  if (overlap && !hip_ok(hipStreamWaitEvent(main, s->ev_kern, 0), "hipStreamWaitEvent(main, kernel)")) return false;
+  // main: convolution and potentials
+  if (lg) {
+    ok = s->timed(fehip::kKLgConvCols, "interp conv_cols launch",
+                  [&] { return fehip::launch_interp_fft(5, fft_len, ib, s->sc, s->tw, n, main); }) &&
+         s->timed(fehip::kKLgPotentialT, "interp potential transpose launch",
+                  [&] { return fehip::launch_interp_fft(6, fft_len, ib, s->sc, s->tw, n, main); }) &&
          s->timed(fehip::kKLgInverseRows, "interp inverse_rows launch",
-                  [&] { return fehip::launch_interp_fft(4, fft_len, ib, s->sc, s->tw, n, s->stream); });
+                  [&] { return fehip::launch_interp_fft(7, fft_len, ib, s->sc, s->tw, n, main); });
+  } else {
+    ok = s->timed(fehip::kKConvCols, "conv_cols launch", [&] { return fehip::launch_conv_cols(s->gb, s->tw, main); }) &&
+         s->timed(fehip::kKInverseRows, "inverse_rows launch",
+                  [&] { return fehip::launch_inverse_rows(s->gb, s->tw, n, s->sc, main); });
+  }
+  if (!ok) return false;
+  return !overlap || hip_ok(hipStreamWaitEvent(main, s->ev_attr, 0), "hipStreamWaitEvent(main, attraction)");
 }
 
 // Current interpolation geometry, read synchronously.
@@ -619,7 +719,12 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   s->n = n;
   s->k = k;
   const int g = resolve_grid_size(n, grid_size);
-  if (!hip_ok(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate")) {
+  if (!hip_ok(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate") ||
+      !hip_ok(hipStreamCreateWithFlags(&s->side_attr, hipStreamNonBlocking), "hipStreamCreate") ||
+      !hip_ok(hipStreamCreateWithFlags(&s->side_kern, hipStreamNonBlocking), "hipStreamCreate") ||
+      !hip_ok(hipEventCreateWithFlags(&s->ev_ready, hipEventDisableTiming), "hipEventCreate") ||
+      !hip_ok(hipEventCreateWithFlags(&s->ev_attr, hipEventDisableTiming), "hipEventCreate") ||
+      !hip_ok(hipEventCreateWithFlags(&s->ev_kern, hipEventDisableTiming), "hipEventCreate")) {
     delete s;
     return 1;
   }
@@ -860,33 +965,6 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   return 0;
 }
 
-bool enqueue_gradient_fields(fastembedr_hip_tsne* s, bool stats_first, int center) {
-  const int n = s->n;
-  if (stats_first &&
-      !s->timed(fehip::kKStats, "stats launch",
-                [&] { return fehip::launch_stats(s->y_a(), n, s->gb.g, center, s->partial, s->sc, s->stream); })) {
-    return false;
-  }
-  return s->timed(fehip::kKBinCount, "bin_count launch",
-                  [&] { return fehip::launch_bin_count(s->y_a(), s->y_b, s->sc, s->gb, n, s->stream); }) &&
-         s->timed(fehip::kKBinPlan, "bin_plan launch",
-                  [&] { return fehip::launch_bin_plan(s->gb, s->sc, s->stream); }) &&
-         s->timed(fehip::kKBinScatter, "bin_scatter launch",
-                  [&] { return fehip::launch_bin_scatter(s->y_b, s->sc, s->gb, n, s->stream); }) &&
-         s->timed(fehip::kKSpread, "spread launch",
-                  [&] { return fehip::launch_spread_tiles(s->sc, s->gb, n, s->stream); }) &&
-         s->timed(fehip::kKKernelRows, "kernel_rows launch",
-                  [&] { return fehip::launch_kernel_rows(s->gb, s->sc, s->tw, s->stream); }) &&
-         s->timed(fehip::kKKernelCols, "kernel_cols launch",
-                  [&] { return fehip::launch_kernel_cols(s->gb, s->tw, s->stream); }) &&
-         s->timed(fehip::kKChargeRows, "charge_rows launch",
-                  [&] { return fehip::launch_charge_rows(s->gb, s->tw, s->stream); }) &&
-         s->timed(fehip::kKConvCols, "conv_cols launch",
-                  [&] { return fehip::launch_conv_cols(s->gb, s->tw, s->stream); }) &&
-         s->timed(fehip::kKInverseRows, "inverse_rows launch",
-                  [&] { return fehip::launch_inverse_rows(s->gb, s->tw, n, s->sc, s->stream); });
-}
-
 bool valid_state_args(const fastembedr_hip_tsne* s) {
   if (s == nullptr) {
     set_error("null HIP openTSNE session");
@@ -1121,15 +1199,15 @@ int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int
     ok = ensure_interp(s) && write_interp_spec(s, fehip::kLgOrder) &&
          hip_ok(fehip::launch_stats(s->y_a(), s->n, s->gb.g, 0, s->partial, s->sc, s->stream), "stats launch") &&
          read_interp_boxes(s, &boxes) &&
-         enqueue_interp_fields(s, interp_fft_len(std::min(boxes * fehip::kLgOrder, fehip::kLgMaxNodes))) &&
-         enqueue_attract(s, s->y_b, exaggeration) &&
+         enqueue_gradient_pieces(s, true, interp_fft_len(std::min(boxes * fehip::kLgOrder, fehip::kLgMaxNodes)),
+                                 exaggeration, false) &&
          hip_ok(fehip::launch_update(fehip::kModeGradientGrid, s->y_b, s->attr, nullptr, nullptr, nullptr, s->grad,
                                      nullptr, s->gb, up, s->partial, s->sc, s->n, s->stream, s->ib.field),
                 "update launch") &&
          check_iteration_flags(s);
   } else if (repulsion == FASTEMBEDR_HIP_REPULSION_GRID) {
-    ok = enqueue_gradient_fields(s, true, 0) &&
-         enqueue_attract(s, s->y_b, exaggeration) &&
+    ok = hip_ok(fehip::launch_stats(s->y_a(), s->n, s->gb.g, 0, s->partial, s->sc, s->stream), "stats launch") &&
+         enqueue_gradient_pieces(s, false, 0, exaggeration, false) &&
          hip_ok(fehip::launch_update(fehip::kModeGradientGrid, s->y_b, s->attr, nullptr, nullptr, nullptr, s->grad,
                                      nullptr, s->gb, up, s->partial, s->sc, s->n, s->stream),
                 "update launch");
@@ -1201,6 +1279,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
       s->reorder_gap = s->renumber_count == 1 ? s->reorder_period : 2 * s->reorder_gap;
     }
     ++s->since_reorder;
+    int fft_len = 0;
     if (lg) {
       for (int r = 0; r < kRing; ++r) {
         if (s->lg_ring_iter[r] > known_it && hipEventQuery(s->lg_ev[r]) == hipSuccess) {
@@ -1218,11 +1297,12 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
       const long long bound =
           static_cast<long long>(known_boxes) + static_cast<long long>(std::ceil(growth * (it - known_it))) + 1;
       const int nodes = static_cast<int>(std::min<long long>(bound * fehip::kLgOrder, fehip::kLgMaxNodes));
-      if (!enqueue_interp_fields(s, interp_fft_len(nodes))) return 1;
-    } else if (!enqueue_gradient_fields(s, false, 0)) {
-      return 1;
+      fft_len = interp_fft_len(nodes);
     }
-    if (!enqueue_attract(s, s->y_b, exaggeration) ||
+    // Timing every kernel (mode 1) runs the pieces in sequence, so that each
+    // duration is the kernel's alone.
+    const bool overlap = !(s->timing && s->timed_only < 0);
+    if (!enqueue_gradient_pieces(s, lg, fft_len, exaggeration, overlap) ||
         !s->timed(fehip::kKUpdate, "update launch", [&] {
           return fehip::launch_update(fehip::kModeUpdate, s->y_b, s->attr, s->y_a(), s->update(), s->gains(),
                                       nullptr, nullptr, s->gb, up, s->partial, s->sc, n, s->stream,
@@ -1250,7 +1330,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
 
 int fastembedr_hip_tsne_sync(fastembedr_hip_tsne* s) {
   if (!valid_state_args(s)) return 1;
-  return hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize") && check_iteration_flags(s) ? 0 : 1;
+  return s->sync_all() && check_iteration_flags(s) ? 0 : 1;
 }
 
 int fastembedr_hip_tsne_set_repulsion(fastembedr_hip_tsne* s, int repulsion, int n_interpolation_points,

@@ -58,6 +58,9 @@
 //   k_lg_inverse_rows     inverse row transforms, potentials per node and the
 //                         m2 phi0 sum
 //   k_lg_finalize_z       Z and its reciprocal
+// Every transform reads and writes contiguous sequences: the row spectra are
+// transposed (k_lg_transpose, 32 x 32 tiles through LDS) before each column
+// pass and back after it, and twiddles are staged in LDS.
 //
 // The FFT length f is a power of two with f >= 2 m (m nodes per axis, read
 // on the device); the host picks it from a bound on m.  Rows and columns of
@@ -78,12 +81,12 @@ constexpr int kLgThreads = 256;
 // partial-sum slots: three per convolution-pass block, then one per row block
 constexpr int kLgMaxSpecBlocks = kLgMaxFft / 2 + 1;
 constexpr int kLgRun = kChunk / kLgThreads;  // points per lane in k_lg_spread
-constexpr int kLgBoxesPerTile = kLgTile * kLgTile;
-static_assert(kLgBoxesPerTile == kLgThreads, "one box of the tile per thread in the box scan");
+constexpr int kLgBoxesPerTile = kLgMaxTile * kLgMaxTile;
+static_assert(kLgBoxesPerTile == kLgThreads, "one box of the largest tile per thread in the box scan");
 static_assert(kLgRun * kLgThreads == kChunk, "a work item is one run per lane");
 
-__device__ __forceinline__ int lg_tile_of(const LgPoint& b, int ta) {
-  return (b.by / kLgTile) * ta + b.bx / kLgTile;
+__device__ __forceinline__ int lg_tile_of(const LgPoint& b, int tile, int ta) {
+  return (b.by / tile) * ta + b.bx / tile;
 }
 
 __global__ __launch_bounds__(kLgThreads) void k_lg_bin_count(const float2* __restrict__ y_stored,
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_bin_count(const float2* __res
     const float px = r.x - s.shift_x;
     const float py = r.y - s.shift_y;
     y_cur[i] = make_float2(px, py);
-    atomicAdd(&hist[lg_tile_of(lg_locate(px, py, s), ta)], 1);
+    atomicAdd(&hist[lg_tile_of(lg_locate(px, py, s), s.lg_tile, ta)], 1);
   }
   __syncthreads();
   for (int t = threadIdx.x; t < tiles; t += kLgThreads) {
@@ -132,7 +135,7 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_bin_scatter(const float2* __r
       tile[q] = -1;
       if (i < n) {
         v[q] = y_cur[i];
-        tile[q] = lg_tile_of(lg_locate(v[q].x, v[q].y, s), ta);
+        tile[q] = lg_tile_of(lg_locate(v[q].x, v[q].y, s), s.lg_tile, ta);
         rank[q] = atomicAdd(&hist[tile[q]], 1);
       }
     }
@@ -150,17 +153,20 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_bin_scatter(const float2* __r
   }
 }
 
-// Adds one box's 9 nodes x 4 charges, summed in registers, to the window.
-__device__ __forceinline__ void lg_flush(float* acc, int box, const float (&a)[4 * kLgOrder * kLgOrder]) {
-  const int lbx = box % kLgTile;
-  const int lby = box / kLgTile;
-  const int node0 = (lby * kLgOrder) * kLgWin + lbx * kLgOrder;
+// Adds one box's 9 nodes x 4 charges, summed in registers, to the window of
+// `win` x `win` nodes (box = local index in a tile of win / 3 boxes per axis).
+__device__ __forceinline__ void lg_flush(float* acc, int box, int tile, int win,
+                                         const float (&a)[4 * kLgOrder * kLgOrder]) {
+  const int lbx = box % tile;
+  const int lby = box / tile;
+  const int wn = win * win;
+  const int node0 = (lby * kLgOrder) * win + lbx * kLgOrder;
 #pragma unroll
   for (int r = 0; r < kLgOrder; ++r) {
 #pragma unroll
     for (int c = 0; c < kLgOrder; ++c) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) atomicAdd(&acc[t * kLgWinNodes + node0 + r * kLgWin + c], a[(r * kLgOrder + c) * 4 + t]);
+      for (int t = 0; t < 4; ++t) atomicAdd(&acc[t * wn + node0 + r * win + c], a[(r * kLgOrder + c) * 4 + t]);
     }
   }
 }
@@ -171,17 +177,20 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
                                                           const DeviceScalars* sc, float* __restrict__ charge,
                                                           float* __restrict__ windows) {
 #pragma clang fp contract(off)
-  __shared__ float acc[kLgWinVals];  // [charge][node of the 48 x 48 window]
+  __shared__ float acc[kLgWinVals];  // [charge][node of the window]
   __shared__ int box_start[kLgBoxesPerTile];
   __shared__ int part[kLgThreads];
   __shared__ float2 sorted[kChunk];
   if (static_cast<int>(blockIdx.x) >= sc->num_items) return;
   const DeviceScalars s = *sc;
   const int4 it = items[blockIdx.x];
+  const int tile = s.lg_tile;
+  const int win = tile * kLgOrder;
+  const int wvals = 4 * win * win;
   const int ta = s.lg_tiles_axis;
   const int tx = it.x % ta, ty = it.x / ta;
-  const int bx0 = tx * kLgTile, by0 = ty * kLgTile;
-  for (int e = threadIdx.x; e < kLgWinVals; e += kLgThreads) acc[e] = 0.0f;
+  const int bx0 = tx * tile, by0 = ty * tile;
+  for (int e = threadIdx.x; e < wvals; e += kLgThreads) acc[e] = 0.0f;
   box_start[threadIdx.x] = 0;
   __syncthreads();
   const int count = it.z - it.y;  // <= kChunk
@@ -195,7 +204,7 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
     if (p < count) {
       v[q] = binned[it.y + p];
       const LgPoint b = lg_locate(v[q].x, v[q].y, s);
-      box[q] = (b.by - by0) * kLgTile + (b.bx - bx0);
+      box[q] = (b.by - by0) * tile + (b.bx - bx0);
       rank[q] = atomicAdd(&box_start[box[q]], 1);
     }
   }
@@ -231,9 +240,9 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
     if (p >= count) break;
     const float2 u = sorted[p];
     const LgPoint b = lg_locate(u.x, u.y, s);
-    const int lb = (b.by - by0) * kLgTile + (b.bx - bx0);
+    const int lb = (b.by - by0) * tile + (b.bx - bx0);
     if (lb != cur) {
-      if (cur >= 0) lg_flush(acc, cur, a);
+      if (cur >= 0) lg_flush(acc, cur, tile, win, a);
       cur = lb;
 #pragma unroll
       for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) a[e] = 0.0f;
@@ -243,14 +252,14 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
     lg_weights3(b.uy, wy);
     // offsets from the nodes in units of h: node c of a box sits at
     // (c + 1/2) h from the box's corner, the point at 3 u h
-    const float tx = 3.0f * b.ux;
-    const float ty = 3.0f * b.uy;
+    const float tx3 = 3.0f * b.ux;
+    const float ty3 = 3.0f * b.uy;
 #pragma unroll
     for (int r = 0; r < kLgOrder; ++r) {
-      const float oy = ty - (static_cast<float>(r) + 0.5f);
+      const float oy = ty3 - (static_cast<float>(r) + 0.5f);
 #pragma unroll
       for (int c = 0; c < kLgOrder; ++c) {
-        const float ox = tx - (static_cast<float>(c) + 0.5f);
+        const float ox = tx3 - (static_cast<float>(c) + 0.5f);
         const float w = wy[r] * wx[c];
         float* d = a + (r * kLgOrder + c) * 4;
         d[0] += w;
@@ -260,22 +269,37 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
       }
     }
   }
-  if (cur >= 0) lg_flush(acc, cur, a);
+  // A dense box spans many lanes: when every lane of the wave ends its run in
+  // the same box, the wave sums its partials first and one lane adds them.
+  const int first = __shfl(cur, 0);
+  if (__all(cur == first) && first >= 0) {
+#pragma unroll
+    for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) {
+      float t = a[e];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
+      a[e] = t;
+    }
+    if ((threadIdx.x & 63) == 0) lg_flush(acc, cur, tile, win, a);
+  } else if (cur >= 0) {
+    lg_flush(acc, cur, tile, win, a);
+  }
   __syncthreads();
   const bool sole = tile_item0[it.x + 1] - tile_item0[it.x] == 1;
   if (sole) {
     const int m = s.lg_nodes;
     const int mm = m * m;
-    for (int e = threadIdx.x; e < kLgWinVals; e += kLgThreads) {
-      const int ch = e / kLgWinNodes;
-      const int node = e - ch * kLgWinNodes;
-      const int gy = ty * kLgWin + node / kLgWin;
-      const int gx = tx * kLgWin + node % kLgWin;
+    const int wn = win * win;
+    for (int e = threadIdx.x; e < wvals; e += kLgThreads) {
+      const int ch = e / wn;
+      const int node = e - ch * wn;
+      const int gy = ty * win + node / win;
+      const int gx = tx * win + node % win;
       if (gx < m && gy < m) charge[ch * mm + gy * m + gx] = acc[e];
     }
   } else {
     float* w = windows + static_cast<std::size_t>(blockIdx.x) * kLgWinVals;
-    for (int e = threadIdx.x; e < kLgWinVals; e += kLgThreads) w[e] = acc[e];
+    for (int e = threadIdx.x; e < wvals; e += kLgThreads) w[e] = acc[e];
   }
 }
 
@@ -286,6 +310,8 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_gather(const int* __restrict_
                                                           float* __restrict__ charge) {
   const int m = sc->lg_nodes;
   const int ta = sc->lg_tiles_axis;
+  const int win = sc->lg_tile * kLgOrder;
+  const int wn = win * win;
   const int mm = m * m;
   const int total = 4 * mm;
   for (int idx = blockIdx.x * kLgThreads + threadIdx.x; idx < total; idx += gridDim.x * kLgThreads) {
@@ -293,12 +319,12 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_gather(const int* __restrict_
     const int node = idx - ch * mm;
     const int gy = node / m;
     const int gx = node - gy * m;
-    const int tx = gx / kLgWin, ty = gy / kLgWin;
+    const int tx = gx / win, ty = gy / win;
     const int t = ty * ta + tx;
     const int i0 = tile_item0[t];
     const int i1 = tile_item0[t + 1];
     if (i1 - i0 == 1) continue;
-    const int e = ch * kLgWinNodes + (gy - ty * kLgWin) * kLgWin + (gx - tx * kLgWin);
+    const int e = ch * wn + (gy - ty * win) * win + (gx - tx * win);
     float v = 0.0f;
     for (int i = i0; i < i1; ++i) v += windows[static_cast<std::size_t>(i) * kLgWinVals + e];
     charge[idx] = v;
@@ -328,23 +354,60 @@ __device__ __forceinline__ void lg_kernels(int dx, int dy, float h, float& k, fl
   k = k1 * k1;
 }
 
+// Transposes P planes of float2: plane p of src holds rows x cols (row stride
+// ld_s), of dst cols x rows (row stride ld_d).  rows (cols) is the node count
+// lg_nodes capped at rows_cap (cols_cap) when m_rows (m_cols) is set, else
+// the cap itself.  32 x 32 tiles through LDS, both sides coalesced.
+template <int P>
+__global__ __launch_bounds__(256) void k_lg_transpose(const float2* __restrict__ src, long long src_plane, int ld_s,
+                                                      float2* __restrict__ dst, long long dst_plane, int ld_d,
+                                                      int rows_cap, int m_rows, int cols_cap, int m_cols,
+                                                      const DeviceScalars* sc) {
+  __shared__ float2 tile[32][33];
+  const int m = sc->lg_nodes;
+  const int rows = m_rows ? min(m, rows_cap) : rows_cap;
+  const int cols = m_cols ? min(m, cols_cap) : cols_cap;
+  const int r0 = blockIdx.y * 32;
+  const int c0 = blockIdx.x * 32;
+  if (r0 >= rows || c0 >= cols) return;  // whole block
+  const int tx = threadIdx.x & 31;
+  const int ty = threadIdx.x >> 5;
+  const float2* sp = src + blockIdx.z * src_plane;
+  float2* dp = dst + blockIdx.z * dst_plane;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + ty + 8 * i;
+    const int c = c0 + tx;
+    if (r < rows && c < cols) tile[ty + 8 * i][tx] = sp[static_cast<long long>(r) * ld_s + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = c0 + ty + 8 * i;
+    const int r = r0 + tx;
+    if (c < cols && r < rows) dp[static_cast<long long>(c) * ld_d + r] = tile[tx][ty + 8 * i];
+  }
+}
+
 // Row transforms of the four kernels on rows y in [0, min(m, F/2 + 1)) of the
 // wrapped grid (|dx| < m, zero beyond): A = K + i K1 (both real and even in
 // dx, so the spectra are the real and imaginary parts) and B = Kx + Ky with
 // Kx = K dx (odd in dx: spectrum i Bx) and Ky = K y (even in dx: spectrum By),
-// so Re B^ = By and Im B^ = Bx.  Kept for kx in [0, F/2]: planes
-// (K^r, K1^r, Bx, By), row stride F/2 + 1.
+// so Re B^ = By and Im B^ = Bx.  Kept for kx in [0, F/2] as two float2
+// planes, (K^r, K1^r) and (Bx, By), row-major with row stride F/2 + 1.
 template <int F>
 __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_rows(const DeviceScalars* sc,
                                                                    const float2* __restrict__ tw,
-                                                                   float* __restrict__ k_rows) {
+                                                                   float2* __restrict__ k_rows) {
   using S = LgShape<F>;
   constexpr int HH = S::H * S::H;
   __shared__ float2 lds[2 * S::KR * F];
+  __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
   const float h = sc->lg_node_h;
   const int row0 = blockIdx.x * S::KR;
   if (row0 >= m) return;  // rows >= m are zero and never read
+  stage_twiddles<F, S::NT>(tws, tw);
   for (int e = threadIdx.x; e < S::KR * F; e += S::NT) {
     const int r = e / F;
     const int x = e - r * F;
@@ -357,86 +420,85 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_rows(const DeviceS
     lds[(2 * r + 1) * F + x] = make_float2(k * static_cast<float>(dx) + k * static_cast<float>(y), 0.0f);
   }
   __syncthreads();
-  fft_lds<F, 2 * S::KR, S::NT, false>(lds, tw);
+  fft_lds<F, 2 * S::KR, S::NT, false, 1>(lds, tws);
   for (int e = threadIdx.x; e < S::KR * S::H; e += S::NT) {
     const int r = e / S::H;
     const int kx = e - r * S::H;
     const int y = row0 + r;
-    if (y >= S::H) continue;
+    if (y >= S::H || y >= m) continue;
     const float2 a = lds[(2 * r) * F + kx];
     const float2 b = lds[(2 * r + 1) * F + kx];
     const int at = y * S::H + kx;
-    k_rows[at] = a.x;
-    k_rows[HH + at] = a.y;
-    k_rows[2 * HH + at] = b.y;
-    k_rows[3 * HH + at] = b.x;
+    k_rows[at] = a;
+    k_rows[HH + at] = make_float2(b.y, b.x);
   }
 }
 
-// Column transforms of the row spectra for kx in [0, F/2]: P = K^r + i K1^r
-// (even in y) gives K^ and K1^ (real); Q = Bx + By, with Bx even and By odd
-// in y, gives Cx + i Cy where the kernel spectra of Kx and Ky are i Cx and
-// i Cy.  Kept for ky in [0, F/2]: planes (K^, K1^, Cx, Cy); Cx is even in ky,
-// Cy odd.
+// Column transforms of the row spectra, read from their transpose (kx-major,
+// row stride F/2 + 1, rows y < min(m, F/2 + 1) valid): P = K^r + i K1^r (even
+// in y) gives K^ and K1^ (real); Q = Bx + By, with Bx even and By odd in y,
+// gives Cx + i Cy where the kernel spectra of Kx and Ky are i Cx and i Cy.
+// Kept for ky in [0, F/2], kx-major: planes (K^, K1^) and (Cx, Cy); Cx is
+// even in ky, Cy odd.
 template <int F>
 __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_cols(const DeviceScalars* sc,
-                                                                   const float* __restrict__ k_rows,
+                                                                   const float2* __restrict__ k_cols,
                                                                    const float2* __restrict__ tw,
-                                                                   float* __restrict__ k_hat) {
+                                                                   float2* __restrict__ k_hat) {
   using S = LgShape<F>;
   constexpr int HH = S::H * S::H;
   __shared__ float2 lds[2 * S::KR * F];
+  __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
   const int col0 = blockIdx.x * S::KR;
+  stage_twiddles<F, S::NT>(tws, tw);
   for (int e = threadIdx.x; e < S::KR * F; e += S::NT) {
-    const int y = e / S::KR;
-    const int c = e - y * S::KR;
+    const int c = e / F;
+    const int y = e - c * F;
     const int kx = col0 + c;
     const bool up = y <= S::G;
     const int ys = up ? y : F - y;
     float2 p = make_float2(0.0f, 0.0f), q = p;
     if (ys < m && kx < S::H) {
-      const int at = ys * S::H + kx;
-      p = make_float2(k_rows[at], k_rows[HH + at]);
-      const float by = k_rows[3 * HH + at];
-      q = make_float2(k_rows[2 * HH + at] + (up ? by : -by), 0.0f);
+      const int at = kx * S::H + ys;
+      p = k_cols[at];
+      const float2 b = k_cols[HH + at];  // (Bx, By)
+      q = make_float2(b.x + (up ? b.y : -b.y), 0.0f);
     }
     lds[(2 * c) * F + y] = p;
     lds[(2 * c + 1) * F + y] = q;
   }
   __syncthreads();
-  fft_lds<F, 2 * S::KR, S::NT, false>(lds, tw);
+  fft_lds<F, 2 * S::KR, S::NT, false, 1>(lds, tws);
   for (int e = threadIdx.x; e < S::KR * S::H; e += S::NT) {
-    const int ky = e / S::KR;
-    const int c = e - ky * S::KR;
+    const int c = e / S::H;
+    const int ky = e - c * S::H;
     const int kx = col0 + c;
     if (kx >= S::H) continue;
-    const float2 p = lds[(2 * c) * F + ky];
-    const float2 q = lds[(2 * c + 1) * F + ky];
-    const int at = ky * S::H + kx;
-    k_hat[at] = p.x;
-    k_hat[HH + at] = p.y;
-    k_hat[2 * HH + at] = q.x;
-    k_hat[3 * HH + at] = q.y;
+    const int at = kx * S::H + ky;
+    k_hat[at] = lds[(2 * c) * F + ky];
+    k_hat[HH + at] = lds[(2 * c + 1) * F + ky];
   }
 }
 
 // Row transforms of the charge planes: A = m0 + i m1x and B = m1y per row
 // y < m (zero-padded to F); A is separated with the Hermitian mirror,
 // X[k] = (A[k] + conj A[-k]) / 2 and Y[k] = (A[k] - conj A[-k]) / 2i; B is
-// the spectrum of a real row already.  Kept for kx in [0, F/2].
+// the spectrum of a real row already.  Kept for kx in [0, F/2], row-major
+// (row stride F/2 + 1), planes plane_stride apart.
 template <int F>
 __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceScalars* sc,
                                                                    const float* __restrict__ charge,
                                                                    const float2* __restrict__ tw,
-                                                                   float2* __restrict__ r0, float2* __restrict__ r1,
-                                                                   float2* __restrict__ r2) {
+                                                                   float2* __restrict__ rows, long long plane) {
   using S = LgShape<F>;
   __shared__ float2 lds[2 * S::CR * F];
+  __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
   const int mm = m * m;
   const int row0 = blockIdx.x * S::CR;
   if (row0 >= m) return;
+  stage_twiddles<F, S::NT>(tws, tw);
   for (int e = threadIdx.x; e < S::CR * F; e += S::NT) {
     const int r = e / F;
     const int x = e - r * F;
@@ -451,7 +513,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
     lds[(2 * r + 1) * F + x] = b;
   }
   __syncthreads();
-  fft_lds<F, 2 * S::CR, S::NT, false>(lds, tw);
+  fft_lds<F, 2 * S::CR, S::NT, false, 1>(lds, tws);
   for (int e = threadIdx.x; e < S::CR * S::H; e += S::NT) {
     const int r = e / S::H;
     const int kx = e - r * S::H;
@@ -462,60 +524,62 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
     const float2 am = conjf2(lds[(2 * r) * F + mk]);
     const float2 sa = cadd(a, am), da = csub(a, am);
     const int at = y * S::H + kx;
-    r0[at] = cscale(sa, 0.5f);
-    r1[at] = make_float2(0.5f * da.y, -0.5f * da.x);
-    r2[at] = lds[(2 * r + 1) * F + kx];
+    rows[at] = cscale(sa, 0.5f);
+    rows[plane + at] = make_float2(0.5f * da.y, -0.5f * da.x);
+    rows[2 * plane + at] = lds[(2 * r + 1) * F + kx];
   }
 }
 
-// Column pass for each stored column kx: forward transforms of M0, M1x, M1y
+// Column pass on the transposed charge spectra (kx-major, row stride F/2,
+// ky... y < m valid): for each column kx, forward transforms of M0, M1x, M1y
 // (rows >= m are the zero padding), then per ky
 //   Phi0 = M0 K^,  Xi_x = i Cx M0 - K^ M1x,  Xi_y = i Cy M0 - K^ M1y,
 // the spectral sums of Z (weight 2 for 0 < kx < F/2, whose mirror column is
 // not stored; 1/F^2 applied later)
 //   s1 = |M0|^2 K1^,  s3 = Re(conj(M1) . i C M0),  s4 = |M1|^2 K^,
-// inverse transforms, rows y < m written.
+// inverse transforms, rows y < m written kx-major.
 template <int F>
 __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceScalars* sc,
-                                                                 const float2* __restrict__ c0,
-                                                                 const float2* __restrict__ c1,
-                                                                 const float2* __restrict__ c2,
-                                                                 const float* __restrict__ k_hat,
+                                                                 const float2* __restrict__ cols_in,
+                                                                 const float2* __restrict__ k_hat,
                                                                  const float2* __restrict__ tw,
-                                                                 float2* __restrict__ p0, float2* __restrict__ p1,
-                                                                 float2* __restrict__ p2,
+                                                                 float2* __restrict__ cols_out, long long plane,
                                                                  double* __restrict__ zpart) {
   using S = LgShape<F>;
   constexpr int C = S::CC;
   constexpr int HH = S::H * S::H;
   __shared__ float2 lds[3 * C * F];
+  __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
   const int col0 = blockIdx.x * C;
-  const float2* src[3] = {c0, c1, c2};
+  stage_twiddles<F, S::NT>(tws, tw);
   for (int e = threadIdx.x; e < C * F; e += S::NT) {
-    const int y = e / C;
-    const int c = e - y * C;
+    const int c = e / F;
+    const int y = e - c * F;
     const int kx = col0 + c;
     const bool live = y < m && kx < S::H;
+    const long long at = static_cast<long long>(kx) * S::G + y;
 #pragma unroll
     for (int ch = 0; ch < 3; ++ch) {
-      lds[(ch * C + c) * F + y] = live ? src[ch][y * S::H + kx] : make_float2(0.0f, 0.0f);
+      lds[(ch * C + c) * F + y] = live ? cols_in[ch * plane + at] : make_float2(0.0f, 0.0f);
     }
   }
   __syncthreads();
-  fft_lds<F, 3 * C, S::NT, false>(lds, tw);
+  fft_lds<F, 3 * C, S::NT, false, 1>(lds, tws);
   double s1 = 0.0, s3 = 0.0, s4 = 0.0;
   for (int e = threadIdx.x; e < C * F; e += S::NT) {
-    const int ky = e / C;
-    const int c = e - ky * C;
+    const int c = e / F;
+    const int ky = e - c * F;
     const int kx = col0 + c;
     if (kx >= S::H) continue;
     const bool up = ky <= S::G;
-    const int at = (up ? ky : F - ky) * S::H + kx;
-    const float kk = k_hat[at];
-    const float k1 = k_hat[HH + at];
-    const float cx = k_hat[2 * HH + at];
-    const float cy = up ? k_hat[3 * HH + at] : -k_hat[3 * HH + at];
+    const int at = kx * S::H + (up ? ky : F - ky);
+    const float2 kk2 = k_hat[at];       // (K^, K1^)
+    const float2 cc = k_hat[HH + at];   // (Cx, Cy)
+    const float kk = kk2.x;
+    const float k1 = kk2.y;
+    const float cx = cc.x;
+    const float cy = up ? cc.y : -cc.y;
     float2& v0 = lds[(0 * C + c) * F + ky];
     float2& v1 = lds[(1 * C + c) * F + ky];
     float2& v2 = lds[(2 * C + c) * F + ky];
@@ -536,15 +600,15 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
     v2 = csub(cscale(im0, cy), cscale(my, kk));
   }
   __syncthreads();
-  fft_lds<F, 3 * C, S::NT, true>(lds, tw);
-  float2* dst[3] = {p0, p1, p2};
+  fft_lds<F, 3 * C, S::NT, true, 1>(lds, tws);
   for (int e = threadIdx.x; e < C * S::G; e += S::NT) {
-    const int y = e / C;
-    const int c = e - y * C;
+    const int c = e / S::G;
+    const int y = e - c * S::G;
     const int kx = col0 + c;
     if (y >= m || kx >= S::H) continue;
+    const long long at = static_cast<long long>(kx) * S::G + y;
 #pragma unroll
-    for (int ch = 0; ch < 3; ++ch) dst[ch][y * S::H + kx] = lds[(ch * C + c) * F + y];
+    for (int ch = 0; ch < 3; ++ch) cols_out[ch * plane + at] = lds[(ch * C + c) * F + y];
   }
   s1 = block_sum<S::NT>(s1);
   s3 = block_sum<S::NT>(s3);
@@ -556,26 +620,26 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
   }
 }
 
-// Inverse row pass: U = Phi0 + i Xi_x and V = Xi_y (spectra of real rows,
-// upper half rebuilt from conjugates); potentials for x < m scaled by 1/F^2
-// and stored per node as (phi0, xi_x, xi_y, 0); per-block sums of m2 phi0 in
-// fp64.
+// Inverse row pass on the row-major potential spectra: U = Phi0 + i Xi_x and
+// V = Xi_y (spectra of real rows, upper half rebuilt from conjugates);
+// potentials for x < m scaled by 1/F^2 and stored per node as (phi0, xi_x,
+// xi_y, 0); per-block sums of m2 phi0 in fp64.
 template <int F>
 __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_inverse_rows(const DeviceScalars* sc,
-                                                                    const float2* __restrict__ p0,
-                                                                    const float2* __restrict__ p1,
-                                                                    const float2* __restrict__ p2,
+                                                                    const float2* __restrict__ rows, long long plane,
                                                                     const float* __restrict__ charge,
                                                                     const float2* __restrict__ tw,
                                                                     float4* __restrict__ field,
                                                                     double* __restrict__ partial) {
   using S = LgShape<F>;
   __shared__ float2 lds[2 * S::CR * F];
+  __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
   const int mm = m * m;
   const int row0 = blockIdx.x * S::CR;
   double acc = 0.0;
   if (row0 < m) {  // uniform over the block
+    stage_twiddles<F, S::NT>(tws, tw);
     for (int e = threadIdx.x; e < S::CR * F; e += S::NT) {
       const int r = e / F;
       const int kx = e - r * F;
@@ -584,7 +648,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_inverse_rows(const Device
       if (y < m) {
         const bool low = kx <= S::G;
         const int at = y * S::H + (low ? kx : F - kx);
-        float2 a = p0[at], b = p1[at], c = p2[at];
+        float2 a = rows[at], b = rows[plane + at], c = rows[2 * plane + at];
         if (!low) {
           a = conjf2(a);
           b = conjf2(b);
@@ -597,7 +661,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_inverse_rows(const Device
       lds[(2 * r + 1) * F + kx] = v;
     }
     __syncthreads();
-    fft_lds<F, 2 * S::CR, S::NT, true>(lds, tw);
+    fft_lds<F, 2 * S::CR, S::NT, true, 1>(lds, tws);
     const float scale = 1.0f / (static_cast<float>(F) * static_cast<float>(F));
     for (int e = threadIdx.x; e < S::CR * S::G; e += S::NT) {
       const int r = e / S::G;
@@ -643,6 +707,10 @@ __global__ __launch_bounds__(256) void k_lg_finalize_z(const double* __restrict_
   }
 }
 
+// Buffers of one FFT length.  Spectra planes are G * H float2 (G = F/2,
+// H = F/2 + 1) apart: A holds the charge row spectra, then the potential
+// columns; B the charge columns, then the potential row spectra.  The kernel
+// row spectra and the kernel spectrum share a buffer (H * H float2 planes).
 template <int F>
 hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const float2* tw, int n,
                          hipStream_t stream) {
@@ -650,26 +718,39 @@ hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const 
   const int kblocks = (S::H + S::KR - 1) / S::KR;
   const int rblocks = (S::G + S::CR - 1) / S::CR;
   const int cblocks = (S::H + S::CC - 1) / S::CC;
+  const long long plane = static_cast<long long>(S::G) * S::H;
+  const long long kplane = static_cast<long long>(S::H) * S::H;
   double* spec_part = ib.z_partial;
   double* row_part = ib.z_partial + 3 * kLgMaxSpecBlocks;
+  const int t32h = (S::H + 31) / 32;
+  const int t32g = (S::G + 31) / 32;
   switch (which) {
     case 0:
       k_lg_kernel_rows<F><<<kblocks, S::NT, 0, stream>>>(sc, tw, ib.k_rows);
       break;
-    case 1:
-      k_lg_kernel_cols<F><<<kblocks, S::NT, 0, stream>>>(sc, ib.k_rows, tw, ib.k_hat);
+    case 1:  // (K^r, K1^r), (Bx, By): rows y < min(m, H) -> kx-major
+      k_lg_transpose<2><<<dim3(t32h, t32h, 2), 256, 0, stream>>>(ib.k_rows, kplane, S::H, ib.k_cols, kplane, S::H,
+                                                                  S::H, 1, S::H, 0, sc);
       break;
     case 2:
-      k_lg_charge_rows<F><<<rblocks, S::NT, 0, stream>>>(sc, ib.charge, tw, ib.c_rows[0], ib.c_rows[1],
-                                                          ib.c_rows[2]);
+      k_lg_kernel_cols<F><<<kblocks, S::NT, 0, stream>>>(sc, ib.k_cols, tw, ib.k_rows);
       break;
     case 3:
-      k_lg_conv_cols<F><<<cblocks, S::NT, 0, stream>>>(sc, ib.c_rows[0], ib.c_rows[1], ib.c_rows[2], ib.k_hat, tw,
-                                                        ib.p_rows[0], ib.p_rows[1], ib.p_rows[2], spec_part);
+      k_lg_charge_rows<F><<<rblocks, S::NT, 0, stream>>>(sc, ib.charge, tw, ib.spec_a, plane);
       break;
-    case 4:
-      k_lg_inverse_rows<F><<<rblocks, S::NT, 0, stream>>>(sc, ib.p_rows[0], ib.p_rows[1], ib.p_rows[2], ib.charge,
-                                                           tw, ib.field, row_part);
+    case 4:  // charge spectra, m rows x H -> kx-major (row stride G)
+      k_lg_transpose<3><<<dim3(t32h, t32g, 3), 256, 0, stream>>>(ib.spec_a, plane, S::H, ib.spec_b, plane, S::G,
+                                                                  S::G, 1, S::H, 0, sc);
+      break;
+    case 5:
+      k_lg_conv_cols<F><<<cblocks, S::NT, 0, stream>>>(sc, ib.spec_b, ib.k_rows, tw, ib.spec_a, plane, spec_part);
+      break;
+    case 6:  // potential spectra, H x m (kx-major) -> m rows x H
+      k_lg_transpose<3><<<dim3(t32g, t32h, 3), 256, 0, stream>>>(ib.spec_a, plane, S::G, ib.spec_b, plane, S::H,
+                                                                  S::H, 0, S::G, 1, sc);
+      break;
+    case 7:
+      k_lg_inverse_rows<F><<<rblocks, S::NT, 0, stream>>>(sc, ib.spec_b, plane, ib.charge, tw, ib.field, row_part);
       k_lg_finalize_z<<<1, 256, 0, stream>>>(spec_part, cblocks, row_part, rblocks, n, F, sc);
       break;
     default:

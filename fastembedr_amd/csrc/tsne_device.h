@@ -41,8 +41,9 @@ struct alignas(16) DeviceScalars {
   int lg_order, lg_min_intervals;
   float lg_ints_per_unit;
   float lg_lo, lg_box_w, lg_node_h;
-  int lg_boxes, lg_nodes, lg_tiles_axis;
-  double lg_box_wd;          // box width in fp64: points are located in fp64
+  int lg_boxes, lg_nodes;
+  int lg_tile, lg_tiles_axis;  // boxes per tile and axis (a power of two), tiles per axis
+  double lg_box_wd;            // box width in fp64: points are located in fp64
 };
 
 struct BlockStats {
@@ -67,18 +68,20 @@ inline int max_spread_items(int n, int g) {
 
 enum ErrorBits : unsigned int { kErrIndex = 1u, kErrDistance = 2u, kErrInterpGrid = 4u };
 
-// FIt-SNE interpolation grid: order-3 nodes, tiles of kLgTile x kLgTile boxes
-// (one spread window of kLgWin x kLgWin nodes x 4 charges per work item), at
-// most kLgMaxNodes nodes per axis (FFT length <= 4096).
+// FIt-SNE interpolation grid: order-3 nodes, at most kLgMaxNodes nodes per
+// axis (FFT length <= 4096).  Points are binned by tiles of T x T boxes, T the
+// smallest power of two that keeps the tiles per axis <= kLgMaxTilesAxis; a
+// work item's spread window is 3T x 3T nodes x 4 charges (at most
+// kLgWinVals floats, T <= kLgMaxTile).
 constexpr int kLgOrder = 3;
-constexpr int kLgTile = 16;
-constexpr int kLgWin = kLgTile * kLgOrder;
-constexpr int kLgWinNodes = kLgWin * kLgWin;
-constexpr int kLgWinVals = 4 * kLgWinNodes;
+constexpr int kLgMaxTile = 16;
+constexpr int kLgMaxTilesAxis = 64;
+constexpr int kLgWin = kLgMaxTile * kLgOrder;
+constexpr int kLgWinVals = 4 * kLgWin * kLgWin;
 constexpr int kLgMaxNodes = 2048;
 constexpr int kLgMaxFft = 2 * kLgMaxNodes;
-constexpr int kLgMaxTilesAxis = (kLgMaxNodes / kLgOrder + kLgTile - 1) / kLgTile;
 static_assert(kLgMaxTilesAxis * kLgMaxTilesAxis <= kMaxTiles, "interpolation tiles fit the bin plan");
+static_assert(kLgMaxTile * kLgMaxTilesAxis * kLgOrder >= kLgMaxNodes, "the largest tile covers the largest grid");
 inline int lg_max_items(int n) { return (n + kChunk - 1) / kChunk + kLgMaxTilesAxis * kLgMaxTilesAxis; }
 // three spectral sums per column-pass block (<= f/2 + 1 blocks), one per row block (<= f/2)
 constexpr int kLgZPartials = 3 * (kLgMaxFft / 2 + 1) + kLgMaxFft / 2;
@@ -105,9 +108,12 @@ enum KernelId : int {
   kKLgSpread,
   kKLgGather,
   kKLgKernelRows,
+  kKLgKernelT,
   kKLgKernelCols,
   kKLgChargeRows,
+  kKLgChargeT,
   kKLgConvCols,
+  kKLgPotentialT,
   kKLgInverseRows,
   kKernelCount
 };
@@ -143,10 +149,11 @@ struct GridBuffers {
 struct InterpBuffers {
   float* charge = nullptr;     // 4 planes of m*m: node moments m0, m1x, m1y, m2 (offsets in units of h)
   float4* field = nullptr;     // m*m potentials (phi0, xi_x, xi_y, 0)
-  float* k_rows = nullptr;     // 4 planes of (G+1)^2: row transforms of the kernels (K, K1, Bx, By)
-  float* k_hat = nullptr;      // 4 planes of (G+1)^2: kernel spectra quadrants (K^, K1^, Cx, Cy)
-  float2* c_rows[3] = {};      // G*(G+1) each: half-spectrum rows of m0, m1x, m1y
-  float2* p_rows[3] = {};      // G*(G+1) each: half-spectrum rows of phi0, xi_x, xi_y
+  float2* k_rows = nullptr;    // 2 planes of (G+1)^2: kernel row spectra ((K^r, K1^r), (Bx, By)),
+                               // then the kernel spectrum quadrant ((K^, K1^), (Cx, Cy)), kx-major
+  float2* k_cols = nullptr;    // 2 planes of (G+1)^2: the row spectra transposed
+  float2* spec_a = nullptr;    // 3 planes of G*(G+1): charge row spectra, then potential columns
+  float2* spec_b = nullptr;    // 3 planes of G*(G+1): charge columns, then potential row spectra
   double* z_partial = nullptr; // kLgZPartials: sums of the normaliser per block
   int* tile_count = nullptr;   // kMaxTiles, zero between iterations
   int* tile_cursor = nullptr;  // kMaxTiles
@@ -211,7 +218,9 @@ hipError_t launch_interp_bin_scatter(const float2* y_cur, const DeviceScalars* s
                                      hipStream_t stream);
 hipError_t launch_interp_spread(const DeviceScalars* sc, InterpBuffers& ib, int n, hipStream_t stream);
 hipError_t launch_interp_gather(const DeviceScalars* sc, InterpBuffers& ib, hipStream_t stream);
-// which: 0 kernel rows, 1 kernel cols, 2 charge rows, 3 conv cols, 4 inverse rows (+ normaliser)
+// which: 0 kernel rows, 1 kernel transpose, 2 kernel cols, 3 charge rows,
+// 4 charge transpose, 5 conv cols, 6 potential transpose, 7 inverse rows
+// (+ normaliser)
 hipError_t launch_interp_fft(int which, int fft_len, InterpBuffers& ib, DeviceScalars* sc, const float2* tw, int n,
                              hipStream_t stream);
 

@@ -42,7 +42,9 @@ CONFIGS = {
 # early-exaggeration iterations (exaggeration 12, momentum 0.5) then 500
 # iterations (momentum 0.8), learning rate n / 12 in both phases.
 SCHEDULE = dict(perplexity=30.0, k=90, early_exaggeration_iter=250, n_iter=500, early_exaggeration=12.0,
-                exaggeration=1.0, initial_momentum=0.5, final_momentum=0.8, min_gain=0.01, max_step_norm=5.0)
+                exaggeration=1.0, initial_momentum=0.5, final_momentum=0.8, min_gain=0.01, max_step_norm=5.0,
+                # FFT settings of the configs (FIt-SNE / openTSNE names)
+                interpolation_points=3, min_intervals=50, ints_in_interval=1.0)
 
 
 def gaussian_mixture(spec: MixtureSpec, seed: int = 1, n: int | None = None) -> tuple[np.ndarray, np.ndarray]:

@@ -181,11 +181,14 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_interp_info(fastembedr_hip_tsne* sess
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* session, double* kl);
 
 /* Per-kernel timing.  While enabled, run() records HIP events around every
- * kernel on the session's stream (enabled == 1), or around the kernel with
- * id enabled - 2 only (enabled >= 2), so that the other launches run without
- * event overhead; stats returns, per kernel id, the number of launches timed
- * and their summed duration in milliseconds.  Kernel ids and names:
- * fastembedr_hip_tsne_kernel_name(). */
+ * kernel (enabled == 1), or around the kernel with id enabled - 2 only
+ * (enabled >= 2), so that the other launches run without event overhead;
+ * events go on the stream the kernel runs on.  run() normally runs the
+ * attraction and the repulsion kernel spectrum on side streams beside the
+ * rest of the iteration; with every kernel timed it runs them in sequence,
+ * so that each duration is the kernel's alone.  stats returns, per kernel id,
+ * the number of launches timed and their summed duration in milliseconds.
+ * Kernel ids and names: fastembedr_hip_tsne_kernel_name(). */
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_set_timing(fastembedr_hip_tsne* session, int enabled);
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_timing_stats(fastembedr_hip_tsne* session, int max_kernels,
                                      long long* launches, double* total_ms);
