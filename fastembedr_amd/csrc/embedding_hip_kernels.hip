@@ -1531,6 +1531,43 @@ __global__ __launch_bounds__(kPointThreads) void k_morton_keys(const float2* __r
   }
 }
 
+// Estimated number of (row block, column tile) runs that P would have in a
+// candidate numbering: every step-th block of kTileRows new rows is taken,
+// the distinct column tiles of its entries are marked in an LDS bitmap
+// (`words` 32-bit words) and counted.  order maps new -> old rows and map old
+// -> new columns; null pointers stand for the identity (the current
+// numbering).  One wave per row.
+__global__ __launch_bounds__(256) void k_tile_estimate(const int* __restrict__ row_ptr, const int* __restrict__ col,
+                                                       const int* __restrict__ order, const int* __restrict__ map,
+                                                       int n, int step, int words,
+                                                       unsigned long long* __restrict__ out) {
+  extern __shared__ unsigned int bits[];
+  __shared__ unsigned int block_count;
+  const int r0 = static_cast<int>(blockIdx.x) * step * kTileRows;
+  if (r0 >= n) return;  // whole block
+  for (int w = threadIdx.x; w < words; w += 256) bits[w] = 0u;
+  if (threadIdx.x == 0) block_count = 0u;
+  __syncthreads();
+  const int r1 = min(n, r0 + kTileRows);
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+  for (int q = r0 + wave; q < r1; q += 256 / kWave) {
+    const int i = order != nullptr ? order[q] : q;
+    const int e1 = row_ptr[i + 1];
+    for (int e = row_ptr[i] + lane; e < e1; e += kWave) {
+      const int j = map != nullptr ? map[col[e]] : col[e];
+      const int t = j / kTileCols;
+      atomicOr(&bits[t >> 5], 1u << (t & 31));
+    }
+  }
+  __syncthreads();
+  unsigned int c = 0u;
+  for (int w = threadIdx.x; w < words; w += 256) c += static_cast<unsigned int>(__popc(bits[w]));
+  atomicAdd(&block_count, c);
+  __syncthreads();
+  if (threadIdx.x == 0) atomicAdd(out, static_cast<unsigned long long>(block_count));
+}
+
 __global__ __launch_bounds__(kPointThreads) void k_label_init(int* __restrict__ label, int n) {
   for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += gridDim.x * kPointThreads) label[i] = i;
 }
@@ -1891,6 +1928,18 @@ hipError_t launch_copy_rows(const Renumber& r, int n, const Csr& src, Csr& dst, 
   const int blocks = std::max(1, std::min((n + 3) / 4, 8192));
   k_copy_rows<<<blocks, 256, 0, stream>>>(r.order, r.map, src.row_ptr, src.col, src.val, dst.row_ptr, dst.col,
                                           dst.val, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_tile_estimate(const Csr& p, const int* order, const int* map, int step,
+                                unsigned long long* out, hipStream_t stream) {
+  const int tiles = (p.n + kTileCols - 1) / kTileCols;
+  const int words = (tiles + 31) / 32;
+  const int row_blocks = (p.n + kTileRows - 1) / kTileRows;
+  const int blocks = (row_blocks + step - 1) / step;
+  const std::size_t lds = static_cast<std::size_t>(words) * sizeof(unsigned int);
+  if (lds > 60 * 1024) return hipErrorInvalidValue;
+  k_tile_estimate<<<blocks, 256, lds, stream>>>(p.row_ptr, p.col, order, map, p.n, step, words, out);
   return hipGetLastError();
 }
 

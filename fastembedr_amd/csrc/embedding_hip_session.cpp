@@ -145,8 +145,11 @@ struct fastembedr_hip_tsne {
   int* inv_perm = nullptr;              // caller's index -> working index
   fehip::Renumber rn;
   int reorder_period = 25;
-  int reorder_gap = 25;
-  int renumber_count = 0;
+  int reorder_gap = 0;       // 0: check at the next iteration
+  int renumber_count = 0;    // orders applied
+  int renumber_rejected = 0; // candidate orders not better than the current one
+  unsigned long long* tile_est = nullptr;  // 2 device counters for the tile estimates
+  long long last_tile_estimate[2] = {0, 0};
   int since_reorder = 0;
   int label_sweeps = 0;
   float2* y_b = nullptr;    // centred layout of the current iteration (also scratch)
@@ -298,7 +301,7 @@ bool alloc_working_buffers(fastembedr_hip_tsne* s) {
   const std::size_t nn = static_cast<std::size_t>(n);
   const std::size_t bytes = 2 * (align_up((nn + 1) * 4) + align_up(nnz * 4) + align_up(nnz * 4)) +
                             3 * align_up(nn * 4) + 3 * align_up(nn * sizeof(float2)) + 2 * align_up(nn * 8) +
-                            4 * align_up(nn * 4) + align_up((nn + 1) * 4) + align_up(temp) + 2 * 256 + 4096;
+                            4 * align_up(nn * 4) + align_up((nn + 1) * 4) + align_up(temp) + 3 * 256 + 4096;
   if (!memory_preflight(bytes, "HIP openTSNE working buffers") ||
       !s->work_arena.init(bytes, "hipMalloc(HIP openTSNE working buffers)")) {
     return false;
@@ -325,10 +328,11 @@ bool alloc_working_buffers(fastembedr_hip_tsne* s) {
   s->rn.len = a.take<int>(nn + 1);
   int* component = a.take<int>(nn);
   int* changed = a.take<int>(1);
+  s->tile_est = a.take<unsigned long long>(2);
   s->rn.component = component;
   s->rn.temp = a.take<char>(temp);
   s->rn.temp_bytes = temp;
-  if (s->rn.temp == nullptr || changed == nullptr) {
+  if (s->rn.temp == nullptr || changed == nullptr || s->tile_est == nullptr) {
     set_error("internal: working buffers do not fit their arena");
     return false;
   }
@@ -641,6 +645,30 @@ hipError_t enqueue_renumber(fastembedr_hip_tsne* s) {
   s->rn.perm = s->perm[s->pi];
   hipError_t e = fehip::launch_morton_keys(s->ys[s->si], s->sc, n, s->rn, s->stream);
   if (e == hipSuccess) e = fehip::sort_morton(s->rn, n, s->stream);
+  if (e != hipSuccess) return e;
+  // The layout is a proxy for P's locality that can be poor (early in the
+  // optimisation points pass through one another), so the candidate order is
+  // kept only if it gives fewer attraction tiles than the current one, by a
+  // sampled estimate.  A host round trip, at renumbering points only.
+  if (s->renumbered() || s->tiles_for != -2) {
+    const int row_blocks = (n + fehip::kTileRows - 1) / fehip::kTileRows;
+    const int step = std::max(1, std::min(64, row_blocks / 128));
+    unsigned long long est[2] = {0ull, 0ull};
+    e = hipMemsetAsync(s->tile_est, 0, 2 * sizeof(unsigned long long), s->stream);
+    if (e == hipSuccess) e = fehip::launch_invert(s->rn.order, s->rn.map, n, s->stream);
+    if (e == hipSuccess) e = fehip::launch_tile_estimate(src, nullptr, nullptr, step, s->tile_est, s->stream);
+    if (e == hipSuccess) e = fehip::launch_tile_estimate(src, s->rn.order, s->rn.map, step, s->tile_est + 1, s->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(est, s->tile_est, sizeof(est), hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return e;
+    s->last_tile_estimate[0] = static_cast<long long>(est[0]) * step;
+    s->last_tile_estimate[1] = static_cast<long long>(est[1]) * step;
+    if (!(static_cast<double>(est[1]) < 0.95 * static_cast<double>(est[0]))) {
+      ++s->renumber_rejected;
+      s->since_reorder = 0;
+      return hipSuccess;  // keep the current numbering
+    }
+  }
   if (e == hipSuccess)
     e = fehip::launch_apply_order(s->rn, n, s->perm[s->pi], s->perm[1 - s->pi], s->ys[s->si], s->ys[1 - s->si],
                                   s->us[s->si], s->us[1 - s->si], s->gs[s->si], s->gs[1 - s->si], src.row_ptr,
@@ -1156,6 +1184,10 @@ int fastembedr_hip_tsne_set_state(fastembedr_hip_tsne* s, const float* y, const 
   }
   const std::size_t bytes = static_cast<std::size_t>(s->n) * sizeof(float2);
   std::vector<float> fill;
+  // a new layout: renumbering checks start again (at the next iteration,
+  // then after gaps that double)
+  s->since_reorder = 0;
+  s->reorder_gap = 0;
   if (!upload_permuted(s, y, s->y_a())) return 1;
   if (update != nullptr) {
     if (!upload_permuted(s, update, s->update())) return 1;
@@ -1274,9 +1306,9 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
     // Renumber before the first iteration ever run and then every
     // reorder_period iterations; the bounding box and pending shift it needs
     // are in DeviceScalars (stats kernel above, or the previous update).
-    if (s->reorder_period > 0 && (!s->renumbered() || s->since_reorder >= s->reorder_gap)) {
+    if (s->reorder_period > 0 && s->since_reorder >= s->reorder_gap) {
       if (!s->timed(fehip::kKRenumber, "renumber", [&] { return enqueue_renumber(s); })) return 1;
-      s->reorder_gap = s->renumber_count == 1 ? s->reorder_period : 2 * s->reorder_gap;
+      s->reorder_gap = s->reorder_gap == 0 ? s->reorder_period : 2 * s->reorder_gap;
     }
     ++s->since_reorder;
     int fft_len = 0;
@@ -1357,6 +1389,22 @@ int fastembedr_hip_tsne_set_repulsion(fastembedr_hip_tsne* s, int repulsion, int
   s->lg_ints_per_unit = ints_in_interval;
   if (!ensure_interp(s) || !write_interp_spec(s, fehip::kLgOrder)) return 1;
   s->repulsion = repulsion;
+  return 0;
+}
+
+int fastembedr_hip_tsne_attraction_info(fastembedr_hip_tsne* s, long long* tiles, int* renumbers) {
+  if (!valid_state_args(s)) return 1;
+  if (tiles != nullptr) {
+    int count = -1;
+    if (s->attract_tiled && s->tiles_for != -2) {
+      if (!s->sync_all() ||
+          !hip_ok(hipMemcpy(&count, s->tiles.tile_count, sizeof(int), hipMemcpyDeviceToHost), "hipMemcpy(tiles)")) {
+        return 1;
+      }
+    }
+    *tiles = count;
+  }
+  if (renumbers != nullptr) *renumbers = s->renumber_count;
   return 0;
 }
 

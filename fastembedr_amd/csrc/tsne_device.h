@@ -273,6 +273,11 @@ hipError_t launch_apply_order(const Renumber& r, int n, const int* perm_old, int
 hipError_t scan_row_lengths(Renumber& r, int n, int* rp_new, hipStream_t stream);
 hipError_t launch_copy_rows(const Renumber& r, int n, const Csr& src, Csr& dst, hipStream_t stream);
 hipError_t launch_invert(const int* perm, int* inv, int n, hipStream_t stream);
+// Adds to *out the distinct column tiles of every step-th row block of P in
+// the numbering given by order (new -> old rows) and map (old -> new
+// columns); null for the identity.  An estimate of the tile count / step.
+hipError_t launch_tile_estimate(const Csr& p, const int* order, const int* map, int step,
+                                unsigned long long* out, hipStream_t stream);
 // Connected components of the P graph by min-label propagation with pointer
 // jumping; label[i] ends as the smallest index of i's component.
 hipError_t launch_label_init(int* label, int n, hipStream_t stream);

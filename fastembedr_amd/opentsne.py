@@ -21,6 +21,7 @@ from .session import TsneSession
 
 OPTIMIZER_LABEL = "opentsne_fitsne_fft_grid_native_hip"
 REPULSION_LABEL = "fft_grid_hip"
+INTERP_REPULSION_LABEL = "fitsne_interpolation_grid_hip"
 PROBABILITIES_LABEL = "symmetric_sparse_knn_hip_float32"
 
 
@@ -153,12 +154,19 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
                  n_iter: int | None = None, exaggeration: float | None = None, initial_momentum: float = 0.8,
                  final_momentum: float = 0.8, min_gain: float = 0.01, max_step_norm="auto",
                  negative_gradient_method: str = "auto", record_costs: bool = False,
-                 auto_config: bool = True) -> OpenTsneResult:
+                 auto_config: bool = True, interpolation_grid: dict | None = None) -> OpenTsneResult:
     """openTSNE-style t-SNE from precomputed KNN on the HIP backend.
 
     Arguments have the meaning of R's ``opentsne_knn()``.  ``Y_init=None``
     uses the reference CPU backend's own initialisation, mt19937(seed)
     normals with sd 1e-4 (R's ``rnorm`` stream cannot be reproduced here).
+
+    The repulsion is the reference's bilinear grid for every FFT method
+    string, as in the reference (src/tsne_neighbors.cpp:354-390).
+    ``interpolation_grid`` (an extension with no R counterpart) selects the
+    FIt-SNE interpolation grid instead; it is a dict of openTSNE's settings,
+    ``n_interpolation_points`` (3), ``min_num_intervals`` (50) and
+    ``ints_in_interval`` (1.0), any of which may be omitted.
     """
     if str(backend).lower() != "hip":
         raise ValueError(f'backend "{backend}" is not part of this build; only backend = "hip" is provided. '
@@ -170,6 +178,14 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
     if n_components != 2:
         raise ValueError("HIP openTSNE FFT-grid currently supports exactly two output components.")
     method = normalize_negative_gradient_method(negative_gradient_method)
+    interp = None
+    if interpolation_grid is not None:
+        unknown = set(interpolation_grid) - {"n_interpolation_points", "min_num_intervals", "ints_in_interval"}
+        if unknown:
+            raise ValueError(f"unknown interpolation_grid settings: {sorted(unknown)}")
+        interp = (int(interpolation_grid.get("n_interpolation_points", 3)),
+                  int(interpolation_grid.get("min_num_intervals", 50)),
+                  float(interpolation_grid.get("ints_in_interval", 1.0)))
 
     idx0, dist0 = _coerce_knn(indices, distances)
     float32_input = dist0.dtype == np.float32
@@ -250,11 +266,14 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
     iters = np.zeros(0, np.int32)
     lr_early = n / early_ex if lr_auto else lr_value
     lr_normal = n / normal_ex if lr_auto else lr_value
-    if record_costs or verbose:
-        # Session route: same kernels, with the exact KL every 50 iterations.
+    if record_costs or verbose or interp is not None:
+        # Session route: same kernels, with the exact KL every 50 iterations
+        # when costs are recorded, and the interpolation grid when asked for.
         sess = TsneSession(idx_c, np.asfortranarray(dist_m, dtype=np.float32), perplexity=perplexity,
                            index_offset=offset)
         try:
+            if interp is not None:
+                sess.set_repulsion(_lib.REPULSION_LAGRANGE, *interp)
             if init is None:
                 init = np.empty((n, 2), np.float32)
                 _lib.check(_lib.load().fastembedr_hip_random_init(n, int(seed) & 0xFFFFFFFF,
@@ -273,7 +292,7 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
                     sess.run(step_n, ex, mom, lr, min_gain, step)
                     done += step_n
                     left -= step_n
-                    if done % 50 == 0 or done == total:
+                    if (record_costs or verbose) and (done % 50 == 0 or done == total):
                         costs.append(sess.kl())
                         its.append(done)
                         if verbose:
@@ -307,7 +326,10 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
         exaggeration=normal_ex, initial_momentum=initial_momentum, final_momentum=final_momentum,
         min_gain=min_gain, max_step_norm=step, initialization="user" if Y_init is not None else "random_normal",
         negative_gradient_method=method, auto_config=bool(auto_config), optimizer=OPTIMIZER_LABEL,
-        repulsion=REPULSION_LABEL, precision="float32", probabilities=PROBABILITIES_LABEL,
+        repulsion=REPULSION_LABEL if interp is None else INTERP_REPULSION_LABEL,
+        interpolation_grid=None if interp is None else dict(
+            n_interpolation_points=interp[0], min_num_intervals=interp[1], ints_in_interval=interp[2]),
+        precision="float32", probabilities=PROBABILITIES_LABEL,
         input_had_self=has_self, knn_residency="host", record_costs=bool(record_costs or verbose),
         provenance="openTSNE_style_native_hip_symmetric_knn_gpu_probability_optimizer",
     )

@@ -149,6 +149,14 @@ class TsneSession:
                                                              C.byref(w), C.byref(z)), "interp_info")
         return {"boxes": b.value, "nodes": m.value, "fft_len": f.value, "box_w": w.value, "z": z.value}
 
+    def attraction_info(self) -> dict:
+        """Tiles of the attraction's regrouped P in the current numbering and
+        the number of renumberings so far."""
+        t = C.c_longlong()
+        r = C.c_int()
+        _lib.check(self._lib.fastembedr_hip_tsne_attraction_info(self._h, C.byref(t), C.byref(r)), "attraction_info")
+        return {"tiles": int(t.value), "renumbers": int(r.value)}
+
     def center(self) -> None:
         _lib.check(self._lib.fastembedr_hip_tsne_center(self._h), "center")
 

@@ -136,6 +136,86 @@ def exact_knn_torch(x: np.ndarray, k: int, device: str = "cuda", chunk: int = 40
     return idx, dist
 
 
+def exact_knn_partitioned_torch(x: np.ndarray, labels: np.ndarray, k: int, device: str = "cuda",
+                                chunk: int = 4096):
+    """Exact Euclidean KNN excluding self, computed on the GPU with torch
+    (input preparation only), searching each part of a partition of the rows
+    (here the mixture components) and certifying the result.
+
+    Within a part the search is brute force in the part's centred
+    coordinates.  A row's k neighbours found there are exact when, for every
+    other part c, the triangle-inequality bound ||x - mu_c|| - r_c (mu_c the
+    part's mean, r_c its largest distance to it) exceeds the row's k-th
+    distance: no row of c can then be closer.  Rows that fail the
+    certificate, and rows of parts with no more than k rows, are searched by
+    brute force over all rows.  Returns numpy (indices int32, distances
+    float32), each (n, k), and the number of rows searched by brute force."""
+    import torch
+
+    xt = torch.as_tensor(x, device=device, dtype=torch.float32)
+    n = xt.shape[0]
+    idx = np.empty((n, k), np.int32)
+    dist = np.empty((n, k), np.float32)
+    lab = np.asarray(labels)
+    parts = np.unique(lab)
+    order = np.argsort(lab, kind="stable")
+    bounds = np.searchsorted(lab[order], parts)
+    ends = np.append(bounds[1:], n)
+    kth = torch.full((n,), float("inf"), device=device)
+    centers = torch.empty((parts.size, xt.shape[1]), device=device)
+    radii = torch.empty(parts.size, device=device)
+    brute = torch.zeros(n, dtype=torch.bool, device=device)
+    for c, (b, e) in enumerate(zip(bounds, ends)):
+        rows = torch.as_tensor(order[b:e], device=device, dtype=torch.int64)
+        xc = xt[rows]
+        mu = xc.mean(dim=0)
+        xc = xc - mu
+        centers[c] = mu
+        sqc = (xc * xc).sum(dim=1)
+        radii[c] = sqc.max().sqrt()
+        size = rows.numel()
+        if size <= k:
+            brute[rows] = True
+            continue
+        for s in range(0, size, chunk):
+            t = min(size, s + chunk)
+            d2 = sqc[s:t, None] + sqc[None, :] - 2.0 * (xc[s:t] @ xc.T)
+            d2.clamp_(min=0.0)
+            d2[torch.arange(t - s, device=device), torch.arange(s, t, device=device)] = float("inf")
+            vals, inds = torch.topk(d2, k, dim=1, largest=False, sorted=True)
+            sel = rows[s:t]
+            idx[sel.cpu().numpy()] = rows[inds].to(torch.int32).cpu().numpy()
+            dv = vals.sqrt()
+            dist[sel.cpu().numpy()] = dv.cpu().numpy()
+            kth[sel] = dv[:, -1]
+            del d2, vals, inds
+    # certificate: distance to every other part's centre minus its radius
+    part_of = torch.as_tensor(np.searchsorted(parts, lab), device=device, dtype=torch.int64)
+    csq = (centers * centers).sum(dim=1)
+    for s in range(0, n, 1 << 16):
+        t = min(n, s + (1 << 16))
+        xs = xt[s:t]
+        dc = ((xs * xs).sum(dim=1)[:, None] + csq[None, :] - 2.0 * (xs @ centers.T)).clamp_(min=0.0).sqrt()
+        lb = dc - radii[None, :]
+        lb[torch.arange(t - s, device=device), part_of[s:t]] = float("inf")
+        # margin for the fp32 rounding of both distance computations
+        bad = lb.min(dim=1).values <= kth[s:t] * (1.0 + 1e-4) + 1e-4
+        brute[s:t] |= bad
+    fails = torch.nonzero(brute).flatten()
+    if fails.numel():
+        sq = (xt * xt).sum(dim=1)
+        for s in range(0, fails.numel(), chunk):
+            sel = fails[s:s + chunk]
+            d2 = sq[sel, None] + sq[None, :] - 2.0 * (xt[sel] @ xt.T)
+            d2.clamp_(min=0.0)
+            d2[torch.arange(sel.numel(), device=device), sel] = float("inf")
+            vals, inds = torch.topk(d2, k, dim=1, largest=False, sorted=True)
+            idx[sel.cpu().numpy()] = inds.to(torch.int32).cpu().numpy()
+            dist[sel.cpu().numpy()] = vals.sqrt().cpu().numpy()
+            del d2, vals, inds
+    return idx, dist, int(fails.numel())
+
+
 def exact_query_knn_torch(reference: np.ndarray, query: np.ndarray, k: int, device: str = "cuda",
                           chunk: int = 4096):
     """Exact Euclidean KNN of query rows among reference rows, with torch on

@@ -176,6 +176,13 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_set_repulsion(fastembedr_hip_tsne* se
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_interp_info(fastembedr_hip_tsne* session, int* boxes, int* nodes,
                                     int* fft_len, float* box_width, double* z);
 
+/* Locality of the attraction's tiled P: the number of (row block, column
+ * tile) runs of the current working numbering (-1 before the first build,
+ * or when the row-parallel attraction is used) and the number of
+ * renumberings so far.  No counterpart in the reference. */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_attraction_info(fastembedr_hip_tsne* session, long long* tiles,
+                                        int* renumbers);
+
 /* Exact KL(P || Q) at the current y (src/tsne_neighbors.cpp:1258-1285), with
  * the O(n^2) normalisation computed on the device in fp64. */
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* session, double* kl);

@@ -196,3 +196,33 @@ def test_interp_end_to_end_kl(hip, oracle_mod, prob):
     _say(f"  boxes {info['boxes']}: KL hip={kl_hip:.5f} oracle={kl_cpu:.5f}")
     assert np.all(np.isfinite(y_hip))
     assert abs(kl_hip - kl_cpu) <= 0.01 * kl_cpu
+
+
+def test_opentsne_knn_interpolation_grid(hip, oracle_mod, prob):
+    """The API mirror's interpolation_grid option runs the same schedule on
+    the FIt-SNE grid: the layout equals a session run with the same settings
+    from the same initialisation (a few iterations: longer runs diverge by
+    the amplified reordering of float atomics, as two session runs do), and
+    the result is labelled as such."""
+    x, idx, dist, y0 = prob
+    n = x.shape[0]
+    _say("case: opentsne_knn with interpolation_grid")
+    y0 = _with_span(y0, 20.0)
+    res = hip.opentsne_knn(idx, dist, n_neighbors=45, perplexity=15.0, Y_init=y0, early_exaggeration_iter=3,
+                           n_iter=2, initial_momentum=0.5, interpolation_grid={"min_num_intervals": 40})
+    assert res.config["repulsion"] == "fitsne_interpolation_grid_hip"
+    assert res.config["interpolation_grid"] == {"n_interpolation_points": 3, "min_num_intervals": 40,
+                                                "ints_in_interval": 1.0}
+    with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+        s.set_repulsion(LAGRANGE, 3, 40, 1.0)
+        s.set_state(y0)
+        s.center()
+        y_start = s.y
+        s.run(3, 12.0, 0.5, n / 12.0, 0.01, 5.0)
+        s.run(2, 1.0, 0.8, n / 12.0, 0.01, 5.0)
+        y = s.y
+    err = rel_l2(res.layout - y_start, y - y_start)
+    _say(f"  API vs session displacement relL2 {err:.2e}")
+    assert err <= 1e-4
+    with pytest.raises(ValueError):
+        hip.opentsne_knn(idx, dist, n_neighbors=45, perplexity=15.0, interpolation_grid={"order": 3})
