@@ -401,8 +401,10 @@ def measured_traffic(kernel: str, n: int, nnz: int, g: int, repulsion: str):
         return None
     if repulsion == "grid" and rec.get("grid") != g:
         return None
+    # the timer's name is the kernel symbol's stem: "attract" is k_attract or
+    # the tiled k_attract_tiles_seg<NT>, "update" k_update<mode, grid>
     for name, t in rec.get("kernels", {}).items():
-        if name.split("<")[0] == "k_" + kernel:
+        if name.split("<")[0].startswith("k_" + kernel):
             return int(t["fetch_bytes"] + t["write_bytes"])
     return None
 

@@ -58,16 +58,16 @@ def build(verbose: bool = True) -> Path:
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     inc = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
-    kobj = BUILD_DIR / "embedding_hip_kernels.o"
-    tobj = BUILD_DIR / "transform_hip.o"
-    iobj = BUILD_DIR / "interp_grid_hip.o"
+    objs = []
+    for name in ("embedding_hip_kernels", "attraction_tiles_hip", "transform_hip", "interp_grid_hip"):
+        obj = BUILD_DIR / f"{name}.o"
+        _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(CSRC / f"{name}.hip"), "-o", str(obj)])
+        objs.append(str(obj))
     sobj = BUILD_DIR / "embedding_hip_session.o"
-    _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(CSRC / "embedding_hip_kernels.hip"), "-o", str(kobj)])
-    _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(CSRC / "transform_hip.hip"), "-o", str(tobj)])
-    _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(CSRC / "interp_grid_hip.hip"), "-o", str(iobj)])
     _run([hipcc, *HOST_FLAGS, *inc, "-c", str(CSRC / "embedding_hip_session.cpp"), "-o", str(sobj)])
+    objs.append(str(sobj))
     tmp = LIB.with_suffix(".so.tmp")
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", str(kobj), str(tobj), str(iobj), str(sobj), "-o", str(tmp)])
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)])
     os.replace(tmp, LIB)
     return LIB
 

@@ -908,378 +908,6 @@ __global__ __launch_bounds__(256) void k_attract(const int* __restrict__ row_ptr
   }
 }
 
-// ---- tiled attraction ---------------------------------------------------------
-// Same sum as k_attract, taken over P regrouped into (row block, column tile)
-// runs (see Tiles).  A workgroup owns one block of kTileRows rows; for each
-// of its column tiles it stages the kTileCols positions y_j of that tile in
-// LDS, so the neighbour gathers read LDS instead of L2.  Each lane takes
-// kTileRun consecutive entries of the run; entries of one row are adjacent,
-// so a lane sums them in registers and adds one partial per row it touched
-// to the row's LDS accumulator.
-constexpr int kTileRun = 8;
-static_assert(kTileRun == 8, "k_attract_tiles reads a run group as two 16-byte vectors");
-
-template <int L>
-__global__ __launch_bounds__(256) void k_tile_keys(const int* __restrict__ row_ptr, const int* __restrict__ col,
-                                                   const float* __restrict__ val, int n, int col_bits,
-                                                   unsigned int* __restrict__ key,
-                                                   unsigned long long* __restrict__ pay) {
-  constexpr int RPB = 256 / L;
-  const int lane = threadIdx.x & (L - 1);
-  for (int i = static_cast<int>(blockIdx.x) * RPB + static_cast<int>(threadIdx.x) / L; i < n;
-       i += static_cast<int>(gridDim.x) * RPB) {
-    const unsigned int rb = static_cast<unsigned int>(i / kTileRows);
-    const unsigned int lr = static_cast<unsigned int>(i % kTileRows);
-    const int e1 = row_ptr[i + 1];
-    for (int e = row_ptr[i] + lane; e < e1; e += L) {
-      const int j = col[e];
-      key[e] = (rb << col_bits) | static_cast<unsigned int>(j / kTileCols);
-      pay[e] = (static_cast<unsigned long long>(__float_as_uint(val[e])) << 32) |
-               static_cast<unsigned long long>((lr << 16) | static_cast<unsigned int>(j % kTileCols));
-    }
-  }
-}
-
-__global__ __launch_bounds__(256) void k_tile_heads(const unsigned int* __restrict__ key, long long nnz,
-                                                    int* __restrict__ heads) {
-  for (long long p = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; p < nnz;
-       p += static_cast<long long>(gridDim.x) * 256)
-    heads[p] = (p == 0 || key[p] != key[p - 1]) ? 1 : 0;
-}
-
-// Tile metadata from the sorted keys: column tile, unpadded begin, and the
-// first tile of each row block; the tile count goes to *tile_count.
-__global__ __launch_bounds__(256) void k_tile_meta(const unsigned int* __restrict__ key,
-                                                   const int* __restrict__ heads, const int* __restrict__ pos,
-                                                   long long nnz, int col_bits, int row_blocks,
-                                                   int* __restrict__ tile_ptr, int* __restrict__ tile_cb,
-                                                   int* __restrict__ ubeg, int* __restrict__ tile_count) {
-  for (long long p = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; p < nnz;
-       p += static_cast<long long>(gridDim.x) * 256) {
-    const unsigned int k = key[p];
-    const int cur = static_cast<int>(k >> col_bits);
-    if (heads[p]) {
-      const int t = pos[p];
-      tile_cb[t] = static_cast<int>(k & ((1u << col_bits) - 1u));
-      ubeg[t] = static_cast<int>(p);
-      // this is the first tile of every row block in (previous tile's block, cur]
-      const int prev = p == 0 ? -1 : static_cast<int>(key[p - 1] >> col_bits);
-      for (int rb = prev + 1; rb <= cur; ++rb) tile_ptr[rb] = t;
-    }
-    if (p == nnz - 1) {
-      const int total = pos[p] + heads[p];
-      ubeg[total] = static_cast<int>(nnz);
-      *tile_count = total;
-      for (int rb = cur + 1; rb <= row_blocks; ++rb) tile_ptr[rb] = total;
-    }
-  }
-}
-
-// Padded tile sizes (multiples of kTileRun), zero past the last tile.
-__global__ __launch_bounds__(256) void k_tile_sizes(const int* __restrict__ ubeg, const int* __restrict__ tile_count,
-                                                    long long slots, int* __restrict__ psize) {
-  const int total = *tile_count;
-  for (long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; t < slots;
-       t += static_cast<long long>(gridDim.x) * 256) {
-    int v = 0;
-    if (t < total) {
-      const int len = ubeg[t + 1] - ubeg[t];
-      v = (len + kTileRun - 1) / kTileRun * kTileRun;
-    }
-    psize[t] = v;
-  }
-}
-
-// Entries to their padded places; the last entry of each tile fills the
-// tile's padding with empty entries (0xffffffff, p = 0).
-__global__ __launch_bounds__(256) void k_tile_scatter(const unsigned long long* __restrict__ pay,
-                                                      const int* __restrict__ heads, const int* __restrict__ pos,
-                                                      const int* __restrict__ ubeg,
-                                                      const int* __restrict__ tile_beg, long long nnz,
-                                                      unsigned int* __restrict__ ent, float* __restrict__ val) {
-  for (long long p = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; p < nnz;
-       p += static_cast<long long>(gridDim.x) * 256) {
-    const int t = pos[p] + heads[p] - 1;
-    const int u0 = ubeg[t];
-    const int b0 = tile_beg[t];
-    const unsigned long long w = pay[p];
-    const long long q = b0 + (p - u0);
-    ent[q] = static_cast<unsigned int>(w);
-    val[q] = __uint_as_float(static_cast<unsigned int>(w >> 32));
-    const int u1 = ubeg[t + 1];
-    if (p == u1 - 1) {
-      for (int r = b0 + (u1 - u0); r < tile_beg[t + 1]; ++r) {
-        ent[r] = 0xffffffffu;
-        val[r] = 0.0f;
-      }
-    }
-  }
-}
-
-__global__ __launch_bounds__(256) void k_tile_empty(int* __restrict__ tile_ptr, int* __restrict__ tile_beg,
-                                                    int row_blocks) {
-  for (int rb = threadIdx.x; rb <= row_blocks; rb += 256) tile_ptr[rb] = 0;
-  if (threadIdx.x == 0) tile_beg[0] = 0;
-}
-
-template <int NT>
-__global__ __launch_bounds__(NT) void k_attract_tiles(const unsigned int* __restrict__ ent,
-                                                       const float* __restrict__ val,
-                                                       const int* __restrict__ tile_ptr,
-                                                       const int* __restrict__ tile_cb,
-                                                       const int* __restrict__ tile_beg,
-                                                       const float2* __restrict__ y_cur, float2* __restrict__ attr,
-                                                       float exaggeration, int n, int row_blocks, int xcds) {
-  __shared__ float2 ys[kTileCols];
-  __shared__ float2 yr[kTileRows];
-  __shared__ float acc_x[kTileRows];
-  __shared__ float acc_y[kTileRows];
-  // XCD-aware: block b runs on XCD b % xcds; each XCD takes one contiguous
-  // range of row blocks, whose column tiles then stay in its L2.
-  const int xcd = static_cast<int>(blockIdx.x) % xcds;
-  const int slot = static_cast<int>(blockIdx.x) / xcds;
-  const int per_xcd = (row_blocks + xcds - 1) / xcds;
-  const int rb = xcd * per_xcd + slot;
-  if (slot >= per_xcd || rb >= row_blocks) return;  // whole workgroup
-  const int r0 = rb * kTileRows;
-  const int rows = min(kTileRows, n - r0);
-  for (int r = threadIdx.x; r < kTileRows; r += NT) {
-    acc_x[r] = 0.0f;
-    acc_y[r] = 0.0f;
-    yr[r] = r < rows ? y_cur[r0 + r] : make_float2(0.0f, 0.0f);
-  }
-  const int t1 = tile_ptr[rb + 1];
-  for (int t = tile_ptr[rb]; t < t1; ++t) {
-    const int base = tile_cb[t] * kTileCols;
-    const int cnt = min(kTileCols, n - base);
-    const int e0 = tile_beg[t];
-    const int e1 = tile_beg[t + 1];
-    __syncthreads();  // the previous tile's LDS reads are done
-    for (int q = threadIdx.x; q < cnt; q += NT) ys[q] = y_cur[base + q];
-    __syncthreads();
-    // Runs are padded to whole groups of kTileRun and start on one, so each
-    // lane reads its group with two 16-byte loads per array.
-    for (int e = e0 + static_cast<int>(threadIdx.x) * kTileRun; e < e1; e += NT * kTileRun) {
-      unsigned int w[kTileRun];
-      float p[kTileRun];
-      const uint4 w0 = *reinterpret_cast<const uint4*>(ent + e);
-      const uint4 w1 = *reinterpret_cast<const uint4*>(ent + e + 4);
-      const float4 p0 = *reinterpret_cast<const float4*>(val + e);
-      const float4 p1 = *reinterpret_cast<const float4*>(val + e + 4);
-      w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w;
-      w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
-      p[0] = p0.x; p[1] = p0.y; p[2] = p0.z; p[3] = p0.w;
-      p[4] = p1.x; p[5] = p1.y; p[6] = p1.z; p[7] = p1.w;
-      int cur = -1;
-      float ax = 0.0f, ay = 0.0f;
-#pragma unroll
-      for (int q = 0; q < kTileRun; ++q) {
-        if (w[q] == 0xffffffffu) continue;  // padding (only at the end of a run)
-        const int lr = static_cast<int>(w[q] >> 16);
-        const int lc = static_cast<int>(w[q] & 0xffffu);
-        if (lr != cur) {
-          if (cur >= 0) {
-            atomicAdd(&acc_x[cur], ax);
-            atomicAdd(&acc_y[cur], ay);
-          }
-          cur = lr;
-          ax = 0.0f;
-          ay = 0.0f;
-        }
-        const float2 yi = yr[lr];
-        const float2 yj = ys[lc];
-        const float dx = yi.x - yj.x;
-        const float dy = yi.y - yj.y;
-        const float qq = 1.0f / (1.0f + (dx * dx + dy * dy));
-        const float c = exaggeration * p[q] * qq;
-        ax += c * dx;
-        ay += c * dy;
-      }
-      if (cur >= 0) {
-        atomicAdd(&acc_x[cur], ax);
-        atomicAdd(&acc_y[cur], ay);
-      }
-    }
-  }
-  __syncthreads();
-  for (int r = threadIdx.x; r < rows; r += NT) attr[r0 + r] = make_float2(acc_x[r], acc_y[r]);
-}
-
-// Wave-level helpers for the segmented variant (gfx9 DPP: row shifts within
-// 16-lane rows, row broadcasts 15 / 31, whole-wave shifts by one lane).
-// Lanes whose source lies outside the row / wave read 0.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, true);
-}
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, true));
-}
-constexpr int kDppRowShr = 0x110;    // + shift (1..15)
-constexpr int kDppWaveShl1 = 0x130;  // lane l reads lane l + 1
-constexpr int kDppWaveShr1 = 0x138;  // lane l reads lane l - 1
-constexpr int kDppRowBcast15 = 0x142;
-constexpr int kDppRowBcast31 = 0x143;
-
-// One step of an inclusive segmented scan: (x, y, start) combined with the
-// value `shifted` lanes below; `start` marks a lane (or window) that begins
-// a segment, whose value then takes nothing from below.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ void seg_step(float& x, float& y, int& start) {
-  const float px = dpp_f<CTRL, ROW_MASK>(x);
-  const float py = dpp_f<CTRL, ROW_MASK>(y);
-  const int ps = dpp_i<CTRL, ROW_MASK>(start);
-  if (!start) {
-    x += px;
-    y += py;
-    start = ps;
-  }
-}
-
-// Tiled attraction with a wave-level merge of row partial sums.  A lane's
-// kTileRun entries hold one or more rows (in order); the part of its first
-// row and of its last row are summed in registers, rows strictly inside the
-// group go straight to LDS.  A row that runs across lanes is then summed by
-// an inclusive segmented scan over the wave (DPP), and only the lane that
-// ends the row adds it to the row's accumulator, so the accumulator atomics
-// of one wave never collide.
-template <int NT>
-__global__ __launch_bounds__(NT) void k_attract_tiles_seg(const unsigned int* __restrict__ ent,
-                                                          const float* __restrict__ val,
-                                                          const int* __restrict__ tile_ptr,
-                                                          const int* __restrict__ tile_cb,
-                                                          const int* __restrict__ tile_beg,
-                                                          const float2* __restrict__ y_cur,
-                                                          float2* __restrict__ attr, float exaggeration, int n,
-                                                          int row_blocks, int xcds) {
-  __shared__ float2 ys[kTileCols];
-  __shared__ float2 yr[kTileRows];
-  __shared__ float acc_x[kTileRows];
-  __shared__ float acc_y[kTileRows];
-  const int xcd = static_cast<int>(blockIdx.x) % xcds;
-  const int slot = static_cast<int>(blockIdx.x) / xcds;
-  const int per_xcd = (row_blocks + xcds - 1) / xcds;
-  const int rb = xcd * per_xcd + slot;
-  if (slot >= per_xcd || rb >= row_blocks) return;  // whole workgroup
-  const int r0 = rb * kTileRows;
-  const int rows = min(kTileRows, n - r0);
-  for (int r = threadIdx.x; r < kTileRows; r += NT) {
-    acc_x[r] = 0.0f;
-    acc_y[r] = 0.0f;
-    yr[r] = r < rows ? y_cur[r0 + r] : make_float2(0.0f, 0.0f);
-  }
-  const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
-  const int t1 = tile_ptr[rb + 1];
-  for (int t = tile_ptr[rb]; t < t1; ++t) {
-    const int base = tile_cb[t] * kTileCols;
-    const int cnt = min(kTileCols, n - base);
-    const int e0 = tile_beg[t];
-    const int e1 = tile_beg[t + 1];
-    __syncthreads();  // the previous tile's LDS reads are done
-    for (int q = threadIdx.x; q < cnt; q += NT) ys[q] = y_cur[base + q];
-    __syncthreads();
-    // every lane of a wave runs the same number of rounds (DPP needs them all)
-    const int rounds = (e1 - e0 + NT * kTileRun - 1) / (NT * kTileRun);
-    for (int round = 0; round < rounds; ++round) {
-      const int e = e0 + (round * NT + static_cast<int>(threadIdx.x)) * kTileRun;
-      const bool active = e < e1;
-      int key[kTileRun];
-      float cx[kTileRun], cy[kTileRun];
-      if (active) {
-        const uint4 w0 = *reinterpret_cast<const uint4*>(ent + e);
-        const uint4 w1 = *reinterpret_cast<const uint4*>(ent + e + 4);
-        const float4 p0 = *reinterpret_cast<const float4*>(val + e);
-        const float4 p1 = *reinterpret_cast<const float4*>(val + e + 4);
-        const unsigned int w[kTileRun] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        const float p[kTileRun] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-        for (int q = 0; q < kTileRun; ++q) {
-          // padding (only at the end of a run, never first in a group) joins
-          // the previous entry's row with a zero contribution
-          const bool pad = w[q] == 0xffffffffu;
-          key[q] = pad ? (q > 0 ? key[q > 0 ? q - 1 : 0] : 0) : static_cast<int>(w[q] >> 16);
-          const int lc = pad ? 0 : static_cast<int>(w[q] & 0xffffu);
-          const float2 yi = yr[key[q]];
-          const float2 yj = ys[lc];
-          const float dx = yi.x - yj.x;
-          const float dy = yi.y - yj.y;
-          const float qq = 1.0f / (1.0f + (dx * dx + dy * dy));
-          const float c = exaggeration * p[q] * qq;
-          cx[q] = c * dx;
-          cy[q] = c * dy;
-        }
-      } else {
-#pragma unroll
-        for (int q = 0; q < kTileRun; ++q) {
-          key[q] = -1;
-          cx[q] = 0.0f;
-          cy[q] = 0.0f;
-        }
-      }
-      const int kf = key[0];
-      const int kl = key[kTileRun - 1];
-      float hx = 0.0f, hy = 0.0f, tx = 0.0f, ty = 0.0f;
-      int mid = -1;
-      float mx = 0.0f, my = 0.0f;
-#pragma unroll
-      for (int q = 0; q < kTileRun; ++q) {
-        if (key[q] == kl) {
-          tx += cx[q];
-          ty += cy[q];
-        } else if (key[q] == kf) {
-          hx += cx[q];
-          hy += cy[q];
-        } else {  // a row that starts and ends inside this group
-          if (key[q] != mid) {
-            if (mid >= 0) {
-              atomicAdd(&acc_x[mid], mx);
-              atomicAdd(&acc_y[mid], my);
-            }
-            mid = key[q];
-            mx = 0.0f;
-            my = 0.0f;
-          }
-          mx += cx[q];
-          my += cy[q];
-        }
-      }
-      if (mid >= 0) {
-        atomicAdd(&acc_x[mid], mx);
-        atomicAdd(&acc_y[mid], my);
-      }
-      // Lane l continues lane l - 1's last row when its first row is that
-      // row; the tail of a single-row lane then carries on, a multi-row
-      // lane's tail starts afresh and its head takes the carry.
-      const int prev_kl = dpp_i<kDppWaveShr1, 0xf>(kl + 1) - 1;  // -1 on lane 0
-      const bool joins = kf >= 0 && kf == prev_kl;
-      const bool multi = kf != kl;
-      int start = (multi || !joins) ? 1 : 0;
-      seg_step<kDppRowShr + 1, 0xf>(tx, ty, start);
-      seg_step<kDppRowShr + 2, 0xf>(tx, ty, start);
-      seg_step<kDppRowShr + 4, 0xf>(tx, ty, start);
-      seg_step<kDppRowShr + 8, 0xf>(tx, ty, start);
-      seg_step<kDppRowBcast15, 0xa>(tx, ty, start);
-      seg_step<kDppRowBcast31, 0xc>(tx, ty, start);
-      // carry into a multi-row lane's head: the scanned tail of lane l - 1
-      const float carry_x = dpp_f<kDppWaveShr1, 0xf>(tx);
-      const float carry_y = dpp_f<kDppWaveShr1, 0xf>(ty);
-      const int next_kf = dpp_i<kDppWaveShl1, 0xf>(kf + 1) - 1;  // -1 on lane 63
-      if (multi && kf >= 0) {
-        atomicAdd(&acc_x[kf], hx + (joins ? carry_x : 0.0f));
-        atomicAdd(&acc_y[kf], hy + (joins ? carry_y : 0.0f));
-      }
-      const bool continued = lane != kWave - 1 && next_kf == kl;
-      if (kl >= 0 && !continued) {
-        atomicAdd(&acc_x[kl], tx);
-        atomicAdd(&acc_y[kl], ty);
-      }
-    }
-  }
-  __syncthreads();
-  for (int r = threadIdx.x; r < rows; r += NT) attr[r0 + r] = make_float2(acc_x[r], acc_y[r]);
-}
-
 // Point-parallel second half of an iteration: the grid repulsion read back
 // at the point (src/tsne_neighbors.cpp:1165-1180) or an exact one, plus the
 // attraction, gives the gradient; then the gains/momentum/step-clip update
@@ -1970,110 +1598,6 @@ hipError_t launch_exact_z_double(const float2* y, int n, double* z_partial, hipS
 hipError_t launch_kl_rows(const Csr& p, const float2* y, double sum_q, double* partial, int blocks,
                           hipStream_t stream) {
   k_kl_rows<<<blocks, 256, 0, stream>>>(p.row_ptr, p.col, p.val, y, p.n, sum_q, partial);
-  return hipGetLastError();
-}
-
-// ---- tiled attraction ---------------------------------------------------------
-namespace {
-int bits_for(long long count) {  // bits needed to hold values 0 .. count - 1
-  int b = 0;
-  while (b < 62 && (1ll << b) < count) ++b;
-  return b;
-}
-}  // namespace
-
-void tiles_shape(int n, long long nnz, Tiles& t) {
-  t.n = n;
-  t.nnz = nnz;
-  t.row_blocks = (n + kTileRows - 1) / kTileRows;
-  t.col_tiles = (n + kTileCols - 1) / kTileCols;
-  t.col_bits = bits_for(t.col_tiles);
-  t.key_bits = t.col_bits + bits_for(t.row_blocks);
-  t.max_tiles = std::min<long long>(nnz, static_cast<long long>(t.row_blocks) * t.col_tiles);
-  t.padded = nnz + 7 * t.max_tiles;
-}
-
-hipError_t tiles_temp_bytes(const Tiles& t, std::size_t& bytes) {
-  std::size_t sort_b = 0, scan_b = 0, scan_t = 0;
-  const std::size_t count = static_cast<std::size_t>(std::max<long long>(t.nnz, 1));
-  hipError_t e = rocprim::radix_sort_pairs(nullptr, sort_b, static_cast<const unsigned int*>(nullptr),
-                                           static_cast<unsigned int*>(nullptr),
-                                           static_cast<const unsigned long long*>(nullptr),
-                                           static_cast<unsigned long long*>(nullptr), count, 0u,
-                                           static_cast<unsigned int>(std::max(t.key_bits, 1)));
-  if (e != hipSuccess) return e;
-  e = rocprim::exclusive_scan(nullptr, scan_b, static_cast<const int*>(nullptr), static_cast<int*>(nullptr), 0,
-                              count, rocprim::plus<int>());
-  if (e != hipSuccess) return e;
-  e = rocprim::exclusive_scan(nullptr, scan_t, static_cast<const int*>(nullptr), static_cast<int*>(nullptr), 0,
-                              static_cast<std::size_t>(t.max_tiles) + 1, rocprim::plus<int>());
-  bytes = std::max(sort_b, std::max(scan_b, scan_t));
-  return e;
-}
-
-hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream) {
-  if (t.key_bits > 32) return hipErrorInvalidValue;  // row blocks x column tiles beyond a 32-bit key
-  if (t.nnz == 0) {
-    k_tile_empty<<<1, 256, 0, stream>>>(t.tile_ptr, t.tile_beg, t.row_blocks);
-    return hipGetLastError();
-  }
-  const int key_blocks = std::min((p.n + 7) / 8, 65536);
-  k_tile_keys<32><<<key_blocks, 256, 0, stream>>>(p.row_ptr, p.col, p.val, p.n, t.col_bits, t.key_in, t.pay_in);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const std::size_t count = static_cast<std::size_t>(t.nnz);
-  std::size_t tb = t.temp_bytes;
-  // stable: entries of one (row block, column tile) keep their CSR (row) order
-  e = rocprim::radix_sort_pairs(t.temp, tb, t.key_in, t.key_out, t.pay_in, t.pay_out, count, 0u,
-                                static_cast<unsigned int>(std::max(t.key_bits, 1)), stream);
-  if (e != hipSuccess) return e;
-  const unsigned int blocks = static_cast<unsigned int>(std::min<long long>((t.nnz + 255) / 256, 65536));
-  k_tile_heads<<<blocks, 256, 0, stream>>>(t.key_out, t.nnz, t.heads);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  tb = t.temp_bytes;
-  e = rocprim::exclusive_scan(t.temp, tb, t.heads, t.pos, 0, count, rocprim::plus<int>(), stream);
-  if (e != hipSuccess) return e;
-  k_tile_meta<<<blocks, 256, 0, stream>>>(t.key_out, t.heads, t.pos, t.nnz, t.col_bits, t.row_blocks, t.tile_ptr,
-                                          t.tile_cb, t.ubeg, t.tile_count);
-  const long long slots = t.max_tiles + 1;
-  const unsigned int sblocks = static_cast<unsigned int>(std::min<long long>((slots + 255) / 256, 65536));
-  k_tile_sizes<<<sblocks, 256, 0, stream>>>(t.ubeg, t.tile_count, slots, t.psize);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  tb = t.temp_bytes;
-  e = rocprim::exclusive_scan(t.temp, tb, t.psize, t.tile_beg, 0, static_cast<std::size_t>(slots),
-                              rocprim::plus<int>(), stream);
-  if (e != hipSuccess) return e;
-  k_tile_scatter<<<blocks, 256, 0, stream>>>(t.pay_out, t.heads, t.pos, t.ubeg, t.tile_beg, t.nnz, t.ent, t.val);
-  return hipGetLastError();
-}
-
-hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int threads,
-                                int xcds, bool wave_merge, hipStream_t stream) {
-  const int per_xcd = (t.row_blocks + xcds - 1) / xcds;
-  const int blocks = per_xcd * xcds;
-#define FEHIP_TILED(NT_)                                                                                          \
-  if (wave_merge)                                                                                                 \
-    k_attract_tiles_seg<NT_><<<blocks, NT_, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur,   \
-                                                         attr, exaggeration, t.n, t.row_blocks, xcds);            \
-  else                                                                                                            \
-    k_attract_tiles<NT_><<<blocks, NT_, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr, \
-                                                     exaggeration, t.n, t.row_blocks, xcds);
-  switch (threads) {
-    case 256:
-      FEHIP_TILED(256)
-      break;
-    case 512:
-      FEHIP_TILED(512)
-      break;
-    case 1024:
-      FEHIP_TILED(1024)
-      break;
-    default:
-      return hipErrorInvalidValue;
-  }
-#undef FEHIP_TILED
   return hipGetLastError();
 }
 

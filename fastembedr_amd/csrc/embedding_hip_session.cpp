@@ -154,11 +154,10 @@ struct fastembedr_hip_tsne {
   int label_sweeps = 0;
   float2* y_b = nullptr;    // centred layout of the current iteration (also scratch)
   float2* grad = nullptr;
-  // Attraction over tiled P (kernel k_attract_tiles) unless disabled; the
+  // Attraction over tiled P (kernel k_attract_chunks) unless disabled; the
   // tiles follow the working numbering and are rebuilt after it changes.
   bool attract_tiled = true;
   int tile_threads = 512;
-  bool wave_merge = true;   // k_attract_tiles_seg; FASTEMBEDR_HIP_ATTRACT_WAVE_MERGE=0: k_attract_tiles
   fehip::Tiles tiles;
   int tiles_for = -2;       // value of wi the tiles were built for; -2: none
   // Repulsion used by run(): the bilinear grid (reference) or the FIt-SNE
@@ -403,10 +402,6 @@ bool alloc_tiles(fastembedr_hip_tsne* s) {
     set_error("internal: attraction tiles do not fit their arena");
     return false;
   }
-  // After the sort the key and payload inputs are dead: the head flags and
-  // their scan reuse them.
-  t.heads = reinterpret_cast<int*>(t.key_in);
-  t.pos = reinterpret_cast<int*>(t.pay_in);
   return true;
 }
 
@@ -430,8 +425,7 @@ bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggera
   return s->timed(
       fehip::kKAttract, "attract launch",
       [&] {
-        return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->tile_threads, s->xcds,
-                                           s->wave_merge, st);
+        return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->tile_threads, s->xcds, st);
       },
       st);
 }
@@ -983,7 +977,6 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
     if (std::strcmp(tiled, "0") == 0) s->attract_tiled = false;
   }
   s->tile_threads = env_int("FASTEMBEDR_HIP_TILE_THREADS", s->tile_threads);
-  if (const char* wm = std::getenv("FASTEMBEDR_HIP_ATTRACT_WAVE_MERGE")) s->wave_merge = std::strcmp(wm, "0") != 0;
   if (s->tile_threads != 256 && s->tile_threads != 512 && s->tile_threads != 1024) s->tile_threads = 512;
   if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {
     delete s;

@@ -287,14 +287,16 @@ hipError_t launch_gather2(const float2* src, const int* idx, float2* dst, int n,
 // ---- tiled attraction ---------------------------------------------------------
 // P regrouped for the attraction: rows in blocks of kTileRows, columns in
 // tiles of kTileCols.  The entries of one (row block, column tile) pair form
-// one contiguous run ("tile"), in row order; each entry packs the local row
-// (high 16 bits) and local column (low 16 bits) next to its value.  A row
+// one contiguous run ("tile"), in row order; each entry word packs the byte
+// offsets of its local row (high 16 bits) and local column (low 16 bits) in
+// the LDS position arrays (8 bytes per position), next to its value.  A row
 // block's tiles are tile_ptr[rb] .. tile_ptr[rb + 1]; tile t covers entries
 // tile_beg[t] .. tile_beg[t + 1] and column tile tile_cb[t].  Every run
-// starts at a multiple of 8 entries and is padded to one with empty entries
-// (0xffffffff, value 0).
+// starts at a multiple of kTileRun entries and is padded to one with copies
+// of its last entry word of value 0.
 constexpr int kTileRows = 512;
 constexpr int kTileCols = 4096;
+constexpr int kTileRun = 8;
 
 struct Tiles {
   int n = 0;
@@ -304,22 +306,21 @@ struct Tiles {
   int col_bits = 0;   // bits of the column-tile part of the sort key
   int key_bits = 0;   // col_bits + bits of the row-block part
   long long max_tiles = 0;
-  long long padded = 0;          // capacity of ent / val: nnz + 7 * max_tiles
-  unsigned int* ent = nullptr;   // padded; runs padded to groups of 8 with 0xffffffff
+  long long padded = 0;          // capacity of ent / val: nnz + (kTileRun - 1) * max_tiles
+  unsigned int* ent = nullptr;   // padded
   float* val = nullptr;          // padded; 0 in the padding
   int* tile_ptr = nullptr;       // row_blocks + 1
   int* tile_cb = nullptr;        // max_tiles + 1
-  int* tile_beg = nullptr;       // max_tiles + 1 (padded begins; multiples of 8)
+  int* tile_beg = nullptr;       // max_tiles + 1 (padded begins; multiples of kTileRun)
   int* ubeg = nullptr;           // max_tiles + 1 (begins before padding)
   int* psize = nullptr;          // max_tiles + 1 (padded sizes)
   int* tile_count = nullptr;     // 1
-  // build scratch
-  unsigned int* key_in = nullptr;  // nnz each
+  // build scratch, nnz each; after the sort the inputs hold the run heads
+  // (key_in) and their scan (pay_in)
+  unsigned int* key_in = nullptr;
   unsigned int* key_out = nullptr;
   unsigned long long* pay_in = nullptr;
   unsigned long long* pay_out = nullptr;
-  int* heads = nullptr;  // nnz, aliases key_in after the sort
-  int* pos = nullptr;    // nnz, aliases pay_in after the sort
   void* temp = nullptr;
   std::size_t temp_bytes = 0;
 };
@@ -327,10 +328,9 @@ void tiles_shape(int n, long long nnz, Tiles& t);
 hipError_t tiles_temp_bytes(const Tiles& t, std::size_t& bytes);
 // Rebuilds t from the CSR (same numbering), all on `stream`.
 hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream);
-// threads: workgroup size, 256, 512 or 1024 (one row block per workgroup);
-// wave_merge: sum row parts across the lanes of a wave before the LDS adds.
+// threads: workgroup size, 256, 512 or 1024 (one row block per workgroup).
 hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int threads,
-                                int xcds, bool wave_merge, hipStream_t stream);
+                                int xcds, hipStream_t stream);
 
 // ---- exact O(n^2) terms (gradient check and KL) ----------------------------
 hipError_t launch_exact_repulsion(const float2* y, int n, float2* rep, double* z_partial, DeviceScalars* sc,
