@@ -7,6 +7,7 @@ synthetic inputs for the benchmark configurations.
 """
 
 from ._lib import HipBackendError, HipBackendUnavailable, available, last_error
+from .knn import KnnResult, exact_knn, precompute_knn
 from .opentsne import OpenTsneResult, opentsne_knn, opentsne_neighbor_policy, tsne_auto_parameters
 from .session import TsneSession
 from .transform import TransformResult, transform_tsne
@@ -14,13 +15,16 @@ from .transform import TransformResult, transform_tsne
 __all__ = [
     "HipBackendError",
     "HipBackendUnavailable",
+    "KnnResult",
     "OpenTsneResult",
     "TransformResult",
     "TsneSession",
     "available",
+    "exact_knn",
     "last_error",
     "opentsne_knn",
     "opentsne_neighbor_policy",
+    "precompute_knn",
     "transform_tsne",
     "tsne_auto_parameters",
 ]

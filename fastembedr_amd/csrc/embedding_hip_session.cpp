@@ -24,6 +24,7 @@
 #include <vector>
 
 #include "../../include/fastembedr_hip.h"
+#include "knn_device.h"
 #include "tsne_device.h"
 
 using fehip::BlockStats;
@@ -1487,6 +1488,18 @@ int fastembedr_hip_random_init(int n, unsigned int seed, float* out) {
 int fastembedr_hip_tsne_p_build_ms(const fastembedr_hip_tsne* s, double* ms) {
   if (!valid_state_args(s) || ms == nullptr) return 1;
   *ms = s->p_build_ms;
+  return 0;
+}
+
+int fastembedr_hip_knn_exact(const float* x, int n, int d, int x_col_major, int k, int exclude_self, int x_on_device,
+                             int* indices, float* distances, int output_on_device, long long* stats) {
+  g_last_error.clear();
+  std::string err;
+  if (fehip::knn_exact_run(x, n, d, x_col_major, k, exclude_self, x_on_device, indices, distances, output_on_device,
+                           stats, err) != 0) {
+    set_error("fastembedr_hip_knn_exact: " + err);
+    return 1;
+  }
   return 0;
 }
 

@@ -1,0 +1,31 @@
+// Exact KNN on the device (knn_hip.hip): limits and the host entry that the
+// C ABI (fastembedr_hip_knn_exact) wraps.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+namespace fehip {
+
+constexpr int kKnnMaxDim = 128;    // centred rows and a query block stay in LDS
+constexpr int kKnnMaxK = 256;      // the reference's native GPU KNN limit (kMaxNativeCudaK)
+constexpr int kKnnBatch = 131072;  // queries per scan launch (candidate buffers: batch x 1024 x 8 bytes)
+
+// Element (row, col) of an n x d matrix at row * row_stride + col * col_stride.
+struct Strides {
+  long long row_stride, col_stride;
+  __host__ __device__ long long at(long long r, long long c) const { return r * row_stride + c * col_stride; }
+};
+
+// k nearest neighbours of every row of x (n x d fp32; row-major, or
+// column-major when x_col_major; on the device when input_on_device), by
+// Euclidean distance, self excluded when exclude_self.  Writes n x k
+// column-major (neighbour j of row i at j * n + i) 1-based indices and fp32
+// distances, ascending by (distance, index), to the device or the host.
+// stats (nullable, 3): rows rerun with a larger candidate set, passes, the
+// last pass's candidates per query.  Returns 0, or 1 with err set.
+int knn_exact_run(const float* x, int n, int d, int x_col_major, int k, int exclude_self, int input_on_device,
+                  int* indices, float* distances, int output_on_device, long long* stats, std::string& err);
+
+}  // namespace fehip

@@ -129,11 +129,20 @@ class OpenTsneResult:
     itercost_iterations: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
 
 
+def _is_device_knn(knn) -> bool:
+    """A device-resident KNN result (R/native_knn.R:17-37: the layout fields
+    plus "cuda" residency; here "hip")."""
+    return getattr(knn, "result_residency", None) == "hip" and getattr(knn, "device_indices", None) is not None
+
+
 def _coerce_knn(indices, distances):
     if distances is None:
         if isinstance(indices, dict) and "indices" in indices and "distances" in indices:
             distances = indices["distances"]
             indices = indices["indices"]
+        elif getattr(indices, "indices", None) is not None and getattr(indices, "distances", None) is not None:
+            distances = indices.distances
+            indices = indices.indices
         else:
             raise ValueError("`distances` is required unless `indices` is a mapping containing "
                              "`indices` and `distances`.")
@@ -187,11 +196,20 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
                   int(interpolation_grid.get("min_num_intervals", 50)),
                   float(interpolation_grid.get("ints_in_interval", 1.0)))
 
-    idx0, dist0 = _coerce_knn(indices, distances)
-    float32_input = dist0.dtype == np.float32
-    idx_s, dist_s, has_self = strip_self_neighbors(idx0, dist0, float32=float32_input)
-    n = idx_s.shape[0]
-    available = idx_s.shape[1]
+    device_knn = indices if distances is None and _is_device_knn(indices) else None
+    if device_knn is not None:
+        # device-resident, self excluded, 1-based (the reference's GPU KNN contract)
+        if not getattr(device_knn, "exclude_self", True):
+            raise ValueError("A device-resident KNN object must exclude self neighbours.")
+        n, available = int(device_knn.n), int(device_knn.k)
+        if n < 2:
+            raise ValueError("KNN input must have at least two rows and one neighbor column.")
+    else:
+        idx0, dist0 = _coerce_knn(indices, distances)
+        float32_input = dist0.dtype == np.float32
+        idx_s, dist_s, has_self = strip_self_neighbors(idx0, dist0, float32=float32_input)
+        n = idx_s.shape[0]
+        available = idx_s.shape[1]
     if available < 1:
         raise ValueError("KNN input must contain at least one non-self neighbor.")
     policy = opentsne_neighbor_policy(n, perplexity, available)
@@ -204,8 +222,9 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
         raise ValueError("`n_neighbors` is larger than the supplied KNN width.")
     if perplexity is None:
         perplexity = policy["perplexity"]
-    idx_m = idx_s[:, :n_neighbors]
-    dist_m = dist_s[:, :n_neighbors]
+    if device_knn is None:
+        idx_m = idx_s[:, :n_neighbors]
+        dist_m = dist_s[:, :n_neighbors]
     k = n_neighbors
 
     # "auto" resolution (R/tsne_control.R:70-130, 249-283; R/tsne_affinity_dispatch.R:190-217)
@@ -259,8 +278,12 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
         if init.shape != (n, 2):
             raise ValueError("incorrect format for `Y_init`.")
 
-    offset = knn_index_offset(idx_m)
-    idx_c = np.asfortranarray(idx_m, dtype=np.int32)
+    if device_knn is None:
+        offset = knn_index_offset(idx_m)
+        idx_c = np.asfortranarray(idx_m, dtype=np.int32)
+    else:
+        # column-major n x k: the first n_neighbors columns are a prefix of the buffers
+        offset = int(getattr(device_knn, "index_base", 1))
     out = np.empty((n, 2), np.float32)
     itercosts = np.zeros(0)
     iters = np.zeros(0, np.int32)
@@ -269,8 +292,12 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
     if record_costs or verbose or interp is not None:
         # Session route: same kernels, with the exact KL every 50 iterations
         # when costs are recorded, and the interpolation grid when asked for.
-        sess = TsneSession(idx_c, np.asfortranarray(dist_m, dtype=np.float32), perplexity=perplexity,
-                           index_offset=offset)
+        if device_knn is None:
+            sess = TsneSession(idx_c, np.asfortranarray(dist_m, dtype=np.float32), perplexity=perplexity,
+                               index_offset=offset)
+        else:
+            sess = TsneSession(perplexity=perplexity, index_offset=offset, n=n, k=k,
+                               device_pointers=(device_knn.indices_ptr, device_knn.distances_ptr))
         try:
             if interp is not None:
                 sess.set_repulsion(_lib.REPULSION_LAGRANGE, *interp)
@@ -304,14 +331,19 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
             sess.close()
     else:
         lib = _lib.load()
-        if dist_m.dtype == np.float64:
+        if device_knn is not None:
+            idx_p, dist_p = C.c_void_p(device_knn.indices_ptr), C.c_void_p(device_knn.distances_ptr)
+            fn = lib.fastembedr_hip_opentsne_fft_from_device_knn_float
+        elif dist_m.dtype == np.float64:
             dist_c = np.asfortranarray(dist_m, dtype=np.float64)
+            idx_p, dist_p = C.c_void_p(idx_c.ctypes.data), C.c_void_p(dist_c.ctypes.data)
             fn = lib.fastembedr_hip_opentsne_fft_from_knn
         else:
             dist_c = np.asfortranarray(dist_m, dtype=np.float32)
+            idx_p, dist_p = C.c_void_p(idx_c.ctypes.data), C.c_void_p(dist_c.ctypes.data)
             fn = lib.fastembedr_hip_opentsne_fft_from_knn_float
         init_p = None if init is None else C.c_void_p(init.ctypes.data)
-        rc = fn(C.c_void_p(idx_c.ctypes.data), C.c_void_p(dist_c.ctypes.data), init_p, int(init is not None), n,
+        rc = fn(idx_p, dist_p, init_p, int(init is not None), n,
                 k, 2, float(perplexity), int(early_exaggeration_iter), int(n_iter), float(early_ex),
                 float(normal_ex), float(lr_value), int(lr_auto), float(initial_momentum), float(final_momentum),
                 float(min_gain), float(step), int(seed) & 0xFFFFFFFF, offset, C.c_void_p(out.ctypes.data))
@@ -330,7 +362,8 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
         interpolation_grid=None if interp is None else dict(
             n_interpolation_points=interp[0], min_num_intervals=interp[1], ints_in_interval=interp[2]),
         precision="float32", probabilities=PROBABILITIES_LABEL,
-        input_had_self=has_self, knn_residency="host", record_costs=bool(record_costs or verbose),
+        input_had_self=False if device_knn is not None else has_self,
+        knn_residency="hip" if device_knn is not None else "host", record_costs=bool(record_costs or verbose),
         provenance="openTSNE_style_native_hip_symmetric_knn_gpu_probability_optimizer",
     )
     return OpenTsneResult(layout=out.astype(np.float64), config=config, itercosts=itercosts,

@@ -254,6 +254,29 @@ FASTEMBEDR_HIP_API int fastembedr_hip_transform_probe(
 /* Wall time of the P construction in milliseconds (device events). */
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_p_build_ms(const fastembedr_hip_tsne* session, double* ms);
 
+/* Exact k-nearest neighbours by Euclidean distance, the exact route of the
+ * reference's native GPU KNN (native_cuda_knn_cpp(data, k, method = "exact"),
+ * src/native_knn_bridge.cpp:102-112 -> native_cuda_knn_impl,
+ * src/native_knn_cuda_impl.cpp:511-704, finished by
+ * src/embedding_cuda_kernels.cpp:1412-1464) and of its result contract
+ * (src/native_knn_cuda_impl.cpp:427-466: layout "column_major_query_by_k",
+ * index_base 1, int32 indices, float32 distances, exclude_self).
+ *   x            n x d float32: row-major, or column-major (an R matrix) when
+ *                x_col_major; device memory when x_on_device
+ *   k            1 .. min(256, n - 1) with exclude_self (n without)
+ *   d            1 .. 128
+ *   indices      n x k column-major (neighbour j of row i at j * n + i),
+ *                1-based; device memory when output_on_device
+ *   distances    same layout, sqrt of the squared distance
+ * Neighbours are ordered by (distance, index), as an ordered dense distance
+ * matrix (tests/testthat/helper-knn.R:5-38) orders them.  stats (may be NULL,
+ * 3 values): rows rerun with a larger candidate set, passes, the last pass's
+ * candidates per query.  Returns 0, or 1 with fastembedr_hip_embedding_last_error()
+ * set. */
+FASTEMBEDR_HIP_API int fastembedr_hip_knn_exact(const float* x, int n, int d, int x_col_major, int k,
+                                                int exclude_self, int x_on_device, int* indices, float* distances,
+                                                int output_on_device, long long* stats);
+
 #ifdef __cplusplus
 }
 #endif

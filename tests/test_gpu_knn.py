@@ -1,0 +1,203 @@
+"""Exact KNN on the GPU (knn_hip.hip through fastembedr_hip_knn_exact)
+against the CPU oracle (oracle/knn_oracle.py, the ordering of the reference's
+tests/testthat/helper-knn.R:5-38).
+
+The bar: indices identical to the oracle's (ties by index included),
+distances within 2e-6 relative (fp32 square roots of fp64 squared
+distances).  Cases: row- and column-major input, self excluded or not, odd
+and small d, d above 64, k = n - 1, sizes off the tile shapes, lattice data
+with duplicates and long runs of exact ties (which take the rerun path with a
+larger candidate set), device input and device-resident output, the
+reference's argument errors, and a large input checked on sampled rows
+against a direct CPU computation.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+
+from fastembedr_amd import _lib
+from oracle import knn_oracle
+
+pytestmark = pytest.mark.gpu
+
+DIST_RTOL = 2e-6
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _check(res, x, k, exclude_self=True):
+    ref_i, ref_d = knn_oracle.exact_knn(x, k, exclude_self=exclude_self)
+    got_i = np.asarray(res.indices)
+    got_d = np.asarray(res.distances)
+    assert got_i.shape == (x.shape[0], k) and got_i.dtype == np.int32
+    assert got_d.dtype == np.float32
+    bad = np.nonzero((got_i - 1 != ref_i).any(axis=1))[0]
+    assert bad.size == 0, f"{bad.size} rows differ, first {bad[:5]}: {got_i[bad[0]] - 1} vs {ref_i[bad[0]]}"
+    np.testing.assert_allclose(got_d, ref_d, rtol=DIST_RTOL, atol=1e-30)
+
+
+def _gauss(n, d, seed, scale=1.0, offset=0.0):
+    rng = np.random.default_rng(seed)
+    return (rng.normal(size=(n, d)) * scale + offset).astype(np.float32)
+
+
+@pytest.mark.parametrize("n,d,k", [(3000, 10, 15), (1000, 2, 30), (777, 7, 5), (5, 3, 3), (130, 1, 12)])
+def test_matches_oracle(hip, n, d, k):
+    _say(f"case: exact KNN n={n} d={d} k={k}")
+    x = _gauss(n, d, seed=n + d)
+    _check(hip.exact_knn(x, k), x, k)
+
+
+def test_column_major_input_and_offset_data(hip):
+    _say("case: column-major input with a large common offset")
+    x = _gauss(2500, 12, seed=5, scale=0.5, offset=300.0)  # centring keeps the expansion accurate
+    res_c = hip.exact_knn(np.asfortranarray(x), 20)
+    res_r = hip.exact_knn(np.ascontiguousarray(x), 20)
+    np.testing.assert_array_equal(res_c.indices, res_r.indices)
+    np.testing.assert_array_equal(res_c.distances, res_r.distances)
+    _check(res_c, x, 20)
+
+
+def test_self_included(hip):
+    _say("case: exclude_self = False")
+    x = _gauss(1500, 9, seed=11)
+    res = hip.exact_knn(x, 10, exclude_self=False)
+    _check(res, x, 10, exclude_self=False)
+    assert np.all(res.indices[:, 0] == np.arange(1, 1501))
+
+
+@pytest.mark.parametrize("n,d,k", [(2000, 100, 25), (900, 65, 40), (600, 128, 8)])
+def test_wide_rows(hip, n, d, k):
+    _say(f"case: wide rows n={n} d={d} k={k}")
+    x = _gauss(n, d, seed=d)
+    _check(hip.exact_knn(x, k), x, k)
+
+
+def test_k_is_n_minus_one(hip):
+    _say("case: k = n - 1")
+    x = _gauss(70, 4, seed=2)
+    res = hip.exact_knn(x, 69)
+    _check(res, x, 69)
+    for i in range(70):
+        assert sorted(res.indices[i] - 1) == [j for j in range(70) if j != i]
+
+
+def test_max_k(hip):
+    _say("case: k = 256")
+    x = _gauss(4000, 16, seed=3)
+    _check(hip.exact_knn(x, 256), x, 256)
+
+
+@pytest.mark.parametrize("exclude_self", [True, False])
+def test_lattice_ties_and_duplicates(hip, exclude_self):
+    _say(f"case: lattice ties exclude_self={exclude_self}")
+    rng = np.random.default_rng(21)
+    x = rng.integers(0, 3, size=(2000, 6)).astype(np.float32)  # 729 distinct points, integer d2
+    res = hip.exact_knn(x, 20, exclude_self=exclude_self)
+    _check(res, x, 20, exclude_self=exclude_self)
+    _say(f"  stats {res.stats}")
+
+
+def test_rerun_path_is_taken_and_exact(hip):
+    _say("case: long tie runs force reruns")
+    rng = np.random.default_rng(22)
+    # 8 distinct points, ~375 copies each: the first candidate set (192) ends
+    # inside the run of zero distances, so no row is certified until the
+    # candidate set outgrows the run
+    x = rng.integers(0, 2, size=(3000, 3)).astype(np.float32)
+    res = hip.exact_knn(x, 60)
+    _say(f"  stats {res.stats}")
+    assert res.stats["passes"] >= 2 and res.stats["rerun_rows"] > 0
+    _check(res, x, 60)
+
+
+def test_device_input_and_output(hip):
+    from fastembedr_amd.device import DeviceMatrix
+
+    _say("case: device input, device-resident result")
+    x = _gauss(3000, 20, seed=8)
+    host = hip.exact_knn(x, 12)
+    dm = DeviceMatrix.from_host(x)
+    dev = hip.precompute_knn(dm, k=12, keep_device=True)
+    assert dev.result_residency == "hip"
+    assert dev.device_indices.shape == (12, 3000)
+    back = dev.to_host()
+    np.testing.assert_array_equal(back.indices, host.indices)
+    np.testing.assert_array_equal(back.distances, host.distances)
+    # column-major device input gives the same result
+    dev2 = hip.exact_knn(DeviceMatrix.from_host(x, col_major=True), 12)
+    np.testing.assert_array_equal(dev2.indices, host.indices)
+    np.testing.assert_array_equal(dev2.distances, host.distances)
+
+
+def test_device_knn_feeds_opentsne(hip):
+    """The device-resident result builds the same P as its host copy, and
+    opentsne_knn takes it directly (a few iterations agree within the
+    gradient tolerance: float atomics reorder sums from run to run)."""
+    from fastembedr_amd import synthetic
+    from tests.helpers import rel_l2
+
+    _say("case: device-resident KNN into the t-SNE session and opentsne_knn")
+    spec = synthetic.MixtureSpec(n=3000, dim=10, components=5, mean_sd=4.0)
+    x, _ = synthetic.gaussian_mixture(spec, seed=3)
+    x = x.astype(np.float32)
+    host = hip.precompute_knn(x, k=30)
+    dev = hip.precompute_knn(x, k=30, keep_device=True)
+    with hip.TsneSession(host.indices, host.distances, perplexity=10.0, index_offset=1) as sh, \
+            hip.TsneSession(perplexity=10.0, index_offset=1, n=dev.n, k=dev.k,
+                            device_pointers=(dev.indices_ptr, dev.distances_ptr)) as sd:
+        for a, b in zip(sh.csr(), sd.csr()):
+            np.testing.assert_array_equal(a, b)
+    y0 = synthetic.pca_init(x)
+    a = hip.opentsne_knn(host, perplexity=10.0, Y_init=y0, early_exaggeration_iter=5, n_iter=5)
+    b = hip.opentsne_knn(dev, perplexity=10.0, Y_init=y0, early_exaggeration_iter=5, n_iter=5)
+    assert b.config["knn_residency"] == "hip" and a.config["knn_residency"] == "host"
+    assert rel_l2(b.layout, a.layout) <= 1e-3
+
+
+def test_errors(hip):
+    _say("case: argument errors")
+    x = _gauss(10, 4, seed=1)
+    with pytest.raises(ValueError, match="between 1 and nrow"):
+        hip.precompute_knn(x, k=10)
+    with pytest.raises(_lib.HipBackendError, match="k exceeds"):
+        hip.exact_knn(x, 10, exclude_self=True)
+    with pytest.raises(_lib.HipBackendError, match="dimensions"):
+        hip.exact_knn(_gauss(50, 129, seed=2), 5)
+    with pytest.raises(_lib.HipBackendError, match="k up to"):
+        hip.exact_knn(_gauss(400, 3, seed=2), 257)
+    bad = _gauss(300, 5, seed=4)
+    bad[17, 2] = np.nan
+    with pytest.raises(_lib.HipBackendError, match="non-finite"):
+        hip.exact_knn(bad, 5)
+    lib = _lib.load()
+    assert lib.fastembedr_hip_knn_exact(None, 10, 4, 0, 3, 1, 0, None, None, 0, None) == 1
+    # the library still works after the errors
+    _check(hip.exact_knn(x, 3), x, 3)
+
+
+def test_large_input_sampled_rows(hip):
+    """200k points of a 20-component mixture in 50 dimensions, k = 90 (the
+    benchmark's shape at a fifth of its size): sampled rows against a direct
+    fp64 computation over all points."""
+    from fastembedr_amd import synthetic
+
+    _say("case: 200k x 50, k = 90, sampled rows")
+    spec = synthetic.MixtureSpec(n=200_000, dim=50, components=20, mean_sd=4.0)
+    x, _ = synthetic.gaussian_mixture(spec, seed=5)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    res = hip.exact_knn(x, 90)
+    _say(f"  elapsed {res.elapsed_sec:.3f} s, stats {res.stats}")
+    xd = x.astype(np.float64)
+    rows = np.random.default_rng(0).choice(x.shape[0], 64, replace=False)
+    for i in rows:
+        d2 = ((xd - xd[i]) ** 2).sum(1)
+        d2[i] = np.inf
+        order = np.lexsort((np.arange(x.shape[0]), d2))[:90]
+        np.testing.assert_array_equal(res.indices[i] - 1, order)
+        np.testing.assert_allclose(res.distances[i], np.sqrt(d2[order]), rtol=DIST_RTOL)
