@@ -10,7 +10,7 @@ namespace fehip {
 
 constexpr int kKnnMaxDim = 128;    // centred rows and a query block stay in LDS
 constexpr int kKnnMaxK = 256;      // the reference's native GPU KNN limit (kMaxNativeCudaK)
-constexpr int kKnnBatch = 131072;  // queries per scan launch (candidate buffers: batch x 1024 x 8 bytes)
+constexpr long long kKnnCandEntries = 1ll << 28;  // candidate buffer entries of a scan launch (2 GiB)
 
 // Element (row, col) of an n x d matrix at row * row_stride + col * col_stride.
 struct Strides {

@@ -10,25 +10,35 @@
 // (tests/testthat/helper-knn.R:5-38).
 //
 // Three steps, all on the device:
-//  1. prep: column means in fp64, centred copy of the data padded to an even
-//     width (xc, fp32), squared norms of the centred rows and their maximum.
-//  2. scan (k_knn_scan, MFMA-bound): a workgroup holds 128 queries (32 per
-//     wave) in LDS and streams every reference in tiles of 64 through LDS.
-//     v_mfma_f32_32x32x2f32 gives 32 x 32 dot products per wave and step;
-//     d2 = |q|^2 + |r|^2 - 2 q.r.  Each query keeps a threshold (the kp-th
-//     smallest d2 seen so far, +inf until kp were seen) and a candidate
-//     buffer of B entries in global memory; a wave owns its 32 queries, so
-//     slots come from ballots, not atomics.  When a buffer could overflow in
-//     the next tile, the wave sorts it (bitonic, across its 64 lanes) and
-//     keeps the kp best.
-//  3. finalize (k_knn_finalize): per query, the kp candidates' squared
-//     distances are recomputed exactly enough (fp64 differences of the
-//     input rows), sorted by (d2, index), and the first k written.  The
-//     result is certified when no rejected reference can beat the k-th: every
-//     rejected reference had an fp32 d2 >= the final threshold T, and the
-//     fp32 expansion is within eps = (D + 12) 2^-23 (|q|^2 + max |r|^2) of
-//     the exact value, so T - eps > d2_k suffices.  Uncertified queries are
-//     listed for a rerun with a larger kp.
+//  1. prep: column means in fp64; a centred fp32 copy xc of the data whose
+//     rows are padded with zeros to a pitch P = round_up(d, 4) + 2 (so that a
+//     64-row tile is one contiguous block and 8-byte LDS reads down a column
+//     of the tile hit distinct banks: P / 2 is odd); squared norms of the
+//     centred rows (+inf for the rows that pad the last tile) and their
+//     maximum.
+//  2. scan (k_knn_scan, MFMA-bound): a wave owns 32 queries, whose
+//     coordinates sit in its registers as MFMA A operands; a workgroup of 4
+//     waves streams every reference through LDS in tiles of 64 rows.
+//     v_mfma_f32_32x32x2f32 gives 32 x 32 dot products per step; each lane
+//     reads a float2 of its reference column per two steps (dimensions
+//     4m + 2h and 4m + 2h + 1 for half h, so both halves of the wave cover
+//     the four dimensions of chunk m).  Per (query, reference) the scan
+//     keeps s = |r|^2 - 2 q.r, which orders references as |q - r|^2 does.
+//     Each query keeps a threshold t (the kp-th smallest s seen, +inf until
+//     kp were seen) and a candidate buffer of B entries in global memory;
+//     slots come from ballots (a wave owns its rows), and when a buffer
+//     could overflow in the next tile the wave sorts it (bitonic across its
+//     64 lanes) and keeps the kp best.  The host picks B >= 2 kp + 64, so
+//     compactions are rare once t has settled.
+//  3. finalize (k_knn_finalize): per query, the candidates' squared
+//     distances are recomputed from the input rows in fp64, the query itself
+//     is dropped on request, and the rest are sorted by (d2, index); the
+//     first k are written.  The result is certified when no rejected
+//     reference can beat the k-th: each had s >= t, and s + |q|^2 is within
+//     eps = (D + 12) 2^-23 (|q|^2 + max |r|^2) of its exact squared distance
+//     (D = round_up(d, 4); fp32 rounding of the centred rows, their norms and
+//     D-term MFMA dot products), so t + |q|^2 - eps > d2_k suffices.
+//     Uncertified queries are listed for a rerun with twice the candidates.
 
 #include <hip/hip_runtime.h>
 
@@ -52,8 +62,15 @@ constexpr int kKnnWaves = kKnnThreads / kWave;
 constexpr int kKnnWaveQueries = 32;
 constexpr int kKnnQueryBlock = kKnnWaves * kKnnWaveQueries;  // 128
 constexpr int kKnnRefTile = 64;                               // two 32-column MFMA blocks
-constexpr int kKnnPitch = kKnnRefTile + 1;                    // LDS row pitch of a reference tile
 constexpr int kPrepThreads = 256;
+
+// Row pitch of xc for d dimensions: a multiple of 4 plus 2.
+__host__ __device__ constexpr int knn_pitch(int d) { return (d + 3) / 4 * 4 + 2; }
+// float2 copies per thread that stage one 64 x P tile (P <= 4 MAXM + 2).
+__host__ __device__ constexpr int knn_tile_pairs(int maxm) { return (4 * maxm + 2 + 7) / 8; }
+// xc is read up to this many floats past its last tile (whole staging copies
+// and the last query row's A loads)
+constexpr int kKnnOverRead = knn_tile_pairs(32) * 2 * kKnnThreads + 256;
 
 // ---- 1. prep --------------------------------------------------------------------
 
@@ -79,13 +96,14 @@ __global__ __launch_bounds__(kPrepThreads) void k_knn_col_means(const double* __
   }
 }
 
-// One row per thread: xc = fl32(x - mean), zero in the padding; the squared
-// norm of the stored fp32 row, summed in fp64; the norms' maximum (bits of a
-// non-negative float compare as unsigned); rows holding a NaN or an infinity
-// (or whose centred norm overflows fp32) are counted in bad_rows.  Rows n to
-// n_pad - 1 (the rest of the last 64-row tile) are zero.
+// One row per thread: xc row = fl32(x - mean), zero from column d to P - 1;
+// the squared norm of the stored fp32 row, summed in fp64; the norms'
+// maximum (bits of a non-negative float compare as unsigned); rows holding a
+// NaN or an infinity (or whose centred norm overflows fp32) are counted in
+// bad_rows.  Rows n to n_pad - 1 (the rest of the last 64-row tile) are zero
+// with norm +inf, so that no query ever accepts them.
 __global__ __launch_bounds__(kPrepThreads) void k_knn_center(const float* __restrict__ x, int n, int n_pad, int d,
-                                                              Strides st, int D, const double* __restrict__ mean,
+                                                              Strides st, int P, const double* __restrict__ mean,
                                                               float* __restrict__ xc,
                                                               float* __restrict__ nrm,
                                                               unsigned int* __restrict__ nrm_max_bits,
@@ -94,9 +112,9 @@ __global__ __launch_bounds__(kPrepThreads) void k_knn_center(const float* __rest
   float local = 0.0f;
   if (r < n) {
     double s = 0.0;
-    for (int c = 0; c < D; ++c) {
+    for (int c = 0; c < P; ++c) {
       const float v = c < d ? static_cast<float>(static_cast<double>(x[st.at(r, c)]) - mean[c]) : 0.0f;
-      xc[static_cast<long long>(r) * D + c] = v;
+      xc[static_cast<long long>(r) * P + c] = v;
       s += static_cast<double>(v) * static_cast<double>(v);
     }
     local = static_cast<float>(s);
@@ -105,13 +123,108 @@ __global__ __launch_bounds__(kPrepThreads) void k_knn_center(const float* __rest
       local = 0.0f;
     }
     nrm[r] = local;
-  } else if (r < n_pad) {  // padding rows of the last reference tile
-    for (int c = 0; c < D; ++c) xc[static_cast<long long>(r) * D + c] = 0.0f;
-    nrm[r] = 0.0f;
+  } else if (r < n_pad) {
+    for (int c = 0; c < P; ++c) xc[static_cast<long long>(r) * P + c] = 0.0f;
+    nrm[r] = INFINITY;
   }
   // wave maximum, then one atomic per wave
   for (int off = kWave / 2; off > 0; off >>= 1) local = fmaxf(local, __shfl_xor(local, off));
   if ((threadIdx.x & (kWave - 1)) == 0) atomicMax(nrm_max_bits, __float_as_uint(local));
+}
+
+// ---- locality order ----------------------------------------------------------------
+// The scan visits every reference for every query, so its result does not
+// depend on the row order; its cost does, through the number of candidates
+// a query accepts before its threshold settles.  Rows are therefore put in
+// an order where near rows are near each other: each row goes to the cell of
+// its nearest pivot (C rows spread evenly over the input), and cells are laid
+// out one after another.  A block of queries then starts its scan at its own
+// cell.
+
+// Nearest pivot (pivot j = row j * stride) of every row, by |p|^2 - 2 x.p in
+// fp32 (only the order matters here, not exactness).  One row per thread, in
+// registers (MAXP >= P, zero padded); pivots staged 32 at a time in LDS.
+template <int MAXP>
+__global__ __launch_bounds__(kPrepThreads) void k_knn_assign(const float* __restrict__ xc,
+                                                              const float* __restrict__ nrm, int n, int P, int C,
+                                                              int stride, int* __restrict__ cell) {
+  constexpr int kPiv = 32;
+  __shared__ float4 piv[kPiv * (MAXP / 4)];
+  __shared__ float pn[kPiv];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int r = static_cast<int>(blockIdx.x) * kPrepThreads + tid;
+  float x[MAXP];
+#pragma unroll
+  for (int c = 0; c < MAXP; ++c) x[c] = (r < n && c < P) ? xc[static_cast<long long>(r) * P + c] : 0.0f;
+  float best = INFINITY;
+  int best_j = 0;
+  for (int j0 = 0; j0 < C; j0 += kPiv) {
+    __syncthreads();
+    float* const pf = reinterpret_cast<float*>(piv);
+    for (int e = tid; e < kPiv * MAXP; e += kPrepThreads) {
+      const int j = e / MAXP, c = e % MAXP;
+      pf[e] = (j0 + j < C && c < P) ? xc[static_cast<long long>(j0 + j) * stride * P + c] : 0.0f;
+    }
+    if (tid < kPiv) pn[tid] = j0 + tid < C ? nrm[static_cast<long long>(j0 + tid) * stride] : INFINITY;
+    __syncthreads();
+    for (int j = 0; j < kPiv; ++j) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int c4 = 0; c4 < MAXP / 4; ++c4) {
+        const float4 v = piv[j * (MAXP / 4) + c4];
+        dot = fmaf(x[4 * c4], v.x, dot);
+        dot = fmaf(x[4 * c4 + 1], v.y, dot);
+        dot = fmaf(x[4 * c4 + 2], v.z, dot);
+        dot = fmaf(x[4 * c4 + 3], v.w, dot);
+      }
+      const float sj = fmaf(-2.0f, dot, pn[j]);
+      if (sj < best) {
+        best = sj;
+        best_j = j0 + j;
+      }
+    }
+  }
+  if (r < n) cell[r] = best_j;
+}
+
+__global__ __launch_bounds__(kPrepThreads) void k_knn_cell_count(const int* __restrict__ cell, int n,
+                                                                  int* __restrict__ count) {
+  const int r = static_cast<int>(blockIdx.x) * kPrepThreads + threadIdx.x;
+  if (r < n) atomicAdd(&count[cell[r]], 1);
+}
+
+// Exclusive prefix sum of the C cell counts, in place (C is at most a few
+// thousand: one thread).
+__global__ void k_knn_cell_offsets(int* __restrict__ count, int C) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int acc = 0;
+  for (int j = 0; j < C; ++j) {
+    const int v = count[j];
+    count[j] = acc;
+    acc += v;
+  }
+}
+
+// perm[position] = row, positions of a cell in arrival order.
+__global__ __launch_bounds__(kPrepThreads) void k_knn_cell_scatter(const int* __restrict__ cell, int n,
+                                                                    int* __restrict__ cursor, int* __restrict__ perm) {
+  const int r = static_cast<int>(blockIdx.x) * kPrepThreads + threadIdx.x;
+  if (r < n) perm[atomicAdd(&cursor[cell[r]], 1)] = r;
+}
+
+// Rows of xc and their norms in scan order; positions n .. n_pad - 1 keep
+// the padding rows (zero, norm +inf).  One float2 per thread.
+__global__ __launch_bounds__(kPrepThreads) void k_knn_permute(const float* __restrict__ xc,
+                                                               const float* __restrict__ nrm,
+                                                               const int* __restrict__ perm, int n, int n_pad, int P,
+                                                               float* __restrict__ xs, float* __restrict__ ns) {
+  const long long e = static_cast<long long>(blockIdx.x) * kPrepThreads + threadIdx.x;
+  const int half = P / 2;
+  if (e >= static_cast<long long>(n_pad) * half) return;
+  const int i = static_cast<int>(e / half), c2 = static_cast<int>(e % half);
+  const int src = i < n ? perm[i] : i;
+  reinterpret_cast<float2*>(xs)[e] = reinterpret_cast<const float2*>(xc)[static_cast<long long>(src) * half + c2];
+  if (c2 == 0) ns[i] = nrm[src];
 }
 
 // ---- sorting inside one wave ------------------------------------------------------
@@ -218,13 +331,24 @@ __device__ __forceinline__ void wave_sort_pairs(double (&d2)[PER], int (&id)[PER
 
 // ---- 2. scan ----------------------------------------------------------------------
 
+// Order-preserving bits of a float (no NaN): a < b iff key(a) < key(b) as
+// unsigned integers, negatives included.
+__device__ __forceinline__ unsigned int ordered_bits(float f) {
+  const unsigned int u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float from_ordered_bits(unsigned int o) {
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
 __device__ __forceinline__ unsigned long long cand_key(uint2 c) {
   return (static_cast<unsigned long long>(c.x) << 32) | c.y;
 }
 
-// Sorts the row's buffer and keeps its kp best (in order at its front);
-// returns the new count, and the new threshold through thr when kp were
-// seen.
+// Sorts the row's buffer of (ordered s bits, index) entries and keeps its kp
+// best (in order at its front); returns the new count, and the new
+// threshold (the kp-th s) through thr when kp were seen.
 template <int B>
 __device__ __noinline__ int compact_row(uint2* __restrict__ row_buf, int cnt, int kp, int lane, float* thr) {
   constexpr int PER = B / kWave;
@@ -251,7 +375,7 @@ __device__ __noinline__ int compact_row(uint2* __restrict__ row_buf, int cnt, in
     for (int j = 0; j < PER; ++j)
       if (j == (kp - 1) / kWave) bits = static_cast<unsigned int>(key[j] >> 32);
     bits = __shfl(static_cast<int>(bits), (kp - 1) % kWave);
-    *thr = __uint_as_float(bits);
+    *thr = from_ordered_bits(bits);
   }
   return min(cnt, kp);
 }
@@ -261,76 +385,105 @@ __device__ __forceinline__ int query_id(const int* __restrict__ qlist, int q_off
   return qlist != nullptr ? qlist[p] : q_offset + p;
 }
 
-// A reference tile's values for one thread: elements e = tid + 256 s of the
-// 64 x D tile, which is contiguous in the row-padded xc, and the norm of row
-// tid (tid < 64).
-template <int MAXD>
-struct TileRegs {
-  float v[MAXD / 4];
-  float norm;
-};
-
-template <int MAXD>
-__device__ __forceinline__ void knn_load_tile(TileRegs<MAXD>& r, const float* __restrict__ xc,
-                                              const float* __restrict__ nrm, int t, int D, int tid) {
-  const float* const src = xc + static_cast<long long>(t) * kKnnRefTile * D;
-#pragma unroll
-  for (int s = 0; s < MAXD / 4; ++s) {
-    const int e = tid + s * kKnnThreads;
-    r.v[s] = e < kKnnRefTile * D ? src[e] : 0.0f;
-  }
-  r.norm = tid < kKnnRefTile ? nrm[t * kKnnRefTile + tid] : 0.0f;
-}
-
-// Where element e = tid + 256 s goes: row e / D and column e % D, stepped
-// from (row0, col0) = (tid / D, tid % D) by (256 / D, 256 % D) with a carry,
-// so that no division is done per tile.
-struct TileWalk {
-  int row0, col0, dq, dr;
-};
-
-// Transposed into LDS: dst[k * 65 + c] (pitch 65: conflict-free), norms in
-// row D.
-template <int MAXD>
-__device__ __forceinline__ void knn_store_tile(const TileRegs<MAXD>& r, float* dst, int D, const TileWalk& w,
-                                               int tid) {
-  int row = w.row0, col = w.col0;
-#pragma unroll
-  for (int s = 0; s < MAXD / 4; ++s) {
-    if (tid + s * kKnnThreads < kKnnRefTile * D) dst[col * kKnnPitch + row] = r.v[s];
-    row += w.dq;
-    col += w.dr;
-    if (col >= D) {
-      col -= D;
-      ++row;
-    }
-  }
-  if (tid < kKnnRefTile) dst[D * kKnnPitch + tid] = r.norm;
-}
-
-// Per wave row state in LDS: threshold, count, |q|^2 and point index (-1
-// past the list's end) of each of its 32 queries.
+// Per wave row state in LDS: threshold and count of each of its 32 queries.
 struct alignas(16) WaveRows {
   float thr[kKnnWaves][kKnnWaveQueries];
   int cnt[kKnnWaves][kKnnWaveQueries];
-  float nq[kKnnWaves][kKnnWaveQueries];
-  int qid[kKnnWaves][kKnnWaveQueries];
 };
 
-// Each wave owns 32 queries; lane (c32, h) holds coordinates 2 k2 + h of
-// query c32 in registers (the A operand of every MFMA step).  A buffer row
-// is compacted to its kp best when it could overflow in the next tile
-// (cnt > B - 64); the host picks B >= 2 kp + 64 so that compactions are rare.
-// Launch bounds: 2 workgroups per CU (2 waves per SIMD, each with two
-// independent MFMA chains).
-template <int B, int MAXD>
-__global__ __launch_bounds__(kKnnThreads, 2) void k_knn_scan(const float* __restrict__ xc, const float* __restrict__ nrm,
-                                                          const int* __restrict__ qlist, int q_offset, int nq, int n,
-                                                          int D, int kp, int exclude_self, uint2* __restrict__ buf,
-                                                          float* __restrict__ thr_out, int* __restrict__ cnt_out) {
+// The dot products of a tile: per chunk m of 4 dimensions, one float2 LDS
+// read of the lane's query (dims 4m + 2h, 4m + 2h + 1) and one per block of
+// 32 references (reference c32, the same dims), then four MFMA steps.  The
+// next chunk's operands are read while the current chunk's steps run (the
+// read one chunk past the last stays inside the LDS rows and is not used);
+// the first chunk starts both accumulators from zero.
+__device__ __forceinline__ void knn_chunk_mfma(float2 a, float2 b0, float2 b1, v16f& acc0, v16f& acc1) {
+  acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b0.x, acc0, 0, 0, 0);
+  acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b1.x, acc1, 0, 0, 0);
+  acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b0.y, acc0, 0, 0, 0);
+  acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b1.y, acc1, 0, 0, 0);
+}
+
+__device__ __forceinline__ void knn_tile_dots(int chunks, const float* qa, const float* col0, const float* col1,
+                                              v16f& acc0, v16f& acc1) {
+  const float2* const q2 = reinterpret_cast<const float2*>(qa);
+  const float2* const c0 = reinterpret_cast<const float2*>(col0);
+  const float2* const c1 = reinterpret_cast<const float2*>(col1);
+  float2 xa = q2[0], x0 = c0[0], x1 = c1[0];
+  float2 ya = q2[2], y0 = c0[2], y1 = c1[2];
+  const v16f zero = {0};
+  acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, x0.x, zero, 0, 0, 0);
+  acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, x1.x, zero, 0, 0, 0);
+  acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, x0.y, acc0, 0, 0, 0);
+  acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, x1.y, acc1, 0, 0, 0);
+  for (int m = 1; m < chunks; m += 2) {
+    // chunk m is in y; read chunk m + 1 into x
+    xa = q2[2 * m + 2];
+    x0 = c0[2 * m + 2];
+    x1 = c1[2 * m + 2];
+    knn_chunk_mfma(ya, y0, y1, acc0, acc1);
+    if (m + 1 >= chunks) break;
+    // chunk m + 1 is in x; read chunk m + 2 into y
+    ya = q2[2 * m + 4];
+    y0 = c0[2 * m + 4];
+    y1 = c1[2 * m + 4];
+    knn_chunk_mfma(xa, x0, x1, acc0, acc1);
+  }
+}
+
+// One tile's staging copy for one thread: float2 number tid + 256 s
+// (s < pairs = ceil(P / 8)) of the tile's contiguous 64 x P block (the last
+// copy reads past the block's end, into the next tile or xc's tail
+// allowance, and is never used), and the norm of row tid.
+template <int MAXM>
+struct TileRegs {
+  float2 v[knn_tile_pairs(MAXM)];
+  float norm;
+};
+
+template <int MAXM>
+__device__ __forceinline__ void knn_load_tile(TileRegs<MAXM>& r, const float* __restrict__ xc,
+                                              const float* __restrict__ nrm, int t, int P, int pairs, int tid) {
+  const float2* const src = reinterpret_cast<const float2*>(xc + static_cast<long long>(t) * kKnnRefTile * P);
+#pragma unroll
+  for (int s = 0; s < knn_tile_pairs(MAXM); ++s)
+    if (s < pairs) r.v[s] = src[tid + s * kKnnThreads];
+  r.norm = tid < kKnnRefTile ? nrm[t * kKnnRefTile + tid] : 0.0f;
+}
+
+template <int MAXM>
+__device__ __forceinline__ void knn_store_tile(const TileRegs<MAXM>& r, float* dst, int pairs, int tid) {
+  float2* const d2 = reinterpret_cast<float2*>(dst);
+#pragma unroll
+  for (int s = 0; s < knn_tile_pairs(MAXM); ++s)
+    if (s < pairs) d2[tid + s * kKnnThreads] = r.v[s];
+  if (tid < kKnnRefTile) dst[pairs * 2 * kKnnThreads + tid] = r.norm;
+}
+
+// LDS of a scan block, in floats: the staged tile (pairs * 512), its 64
+// norms, then the 128 query rows (pitch P) and 4 floats for the read one
+// chunk past the last row.
+__host__ __device__ constexpr int knn_scan_lds_floats(int P) {
+  return (P + 7) / 8 * 2 * kKnnThreads + kKnnRefTile + kKnnQueryBlock * P + 4;
+}
+
+// Occupancy: 3 workgroups per CU (3 waves per SIMD) for up to 64 dimensions,
+// 2 above (their LDS, 70 KB at 128 dimensions, allows no more).
+template <int MAXM>
+constexpr int knn_scan_blocks_per_cu() {
+  return MAXM <= 16 ? 3 : 2;
+}
+
+template <int B, int MAXM>
+__global__ __launch_bounds__(kKnnThreads, knn_scan_blocks_per_cu<MAXM>()) void k_knn_scan(
+    const float* __restrict__ xc, const float* __restrict__ nrm, const int* __restrict__ qlist, int q_offset, int nq,
+    int n, int P, int chunks, int kp, uint2* __restrict__ buf, float* __restrict__ thr_out,
+    int* __restrict__ cnt_out) {
+  const int pairs = (P + 7) / 8;
+  const int norm_at = pairs * 2 * kKnnThreads;
   extern __shared__ float smem[];
-  float* const rt0 = smem;  // [D][65], then 64 norms in row D
-  float* const rt1 = rt0 + (D + 1) * kKnnPitch;
+  float* const rt = smem;                          // the current tile, then its norms
+  float* const qa = smem + norm_at + kKnnRefTile;  // the block's 128 query rows, pitch P
   __shared__ WaveRows rs;
   const int tid = static_cast<int>(threadIdx.x);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -339,76 +492,71 @@ __global__ __launch_bounds__(kKnnThreads, 2) void k_knn_scan(const float* __rest
   const int c32 = lane & 31;
   const int p0 = static_cast<int>(blockIdx.x) * kKnnQueryBlock;  // first list position of the block
 
-  // this lane's query coordinates
+  // the wave's 32 query rows to LDS (zero rows past the list's end)
   const int p_lane = p0 + wave * kKnnWaveQueries + c32;
   const int q_lane = p_lane < nq ? query_id(qlist, q_offset, p_lane) : -1;
-  float a[MAXD / 2];
-  {
-    const float* const qrow = xc + static_cast<long long>(q_lane >= 0 ? q_lane : 0) * D;
-#pragma unroll
-    for (int k2 = 0; k2 < MAXD / 2; ++k2) a[k2] = (q_lane >= 0 && 2 * k2 + h < D) ? qrow[2 * k2 + h] : 0.0f;
+  for (int r = 0; r < kKnnWaveQueries; ++r) {
+    const int q = __shfl(q_lane, r);
+    const float2* const src = reinterpret_cast<const float2*>(xc + static_cast<long long>(q >= 0 ? q : 0) * P);
+    float2* const dst = reinterpret_cast<float2*>(qa + (wave * kKnnWaveQueries + r) * P);
+    for (int e = lane; e < P / 2; e += kWave) dst[e] = q >= 0 ? src[e] : make_float2(0.0f, 0.0f);
   }
   if (lane < kKnnWaveQueries) {
-    rs.thr[wave][lane] = INFINITY;
+    rs.thr[wave][lane] = q_lane >= 0 ? INFINITY : -INFINITY;  // -inf: no row, accepts nothing
     rs.cnt[wave][lane] = 0;
-    rs.qid[wave][lane] = q_lane;
-    rs.nq[wave][lane] = q_lane >= 0 ? nrm[q_lane] : 0.0f;
   }
 
-  // references in tiles of 64; the next tile's values are loaded into
-  // registers while the current one is used
+  // References in tiles of 64, starting at the tile that holds the block's
+  // first query (rows are in locality order, so the nearest references come
+  // first and the thresholds settle early) and wrapping around.  The next
+  // tile is loaded into registers while the current one is used, and stored
+  // between two barriers.
   const int tiles = (n + kKnnRefTile - 1) / kKnnRefTile;
-  const TileWalk walk{tid / D, tid % D, kKnnThreads / D, kKnnThreads % D};
-  TileRegs<MAXD> pre;
-  knn_load_tile<MAXD>(pre, xc, nrm, 0, D, tid);
-  knn_store_tile<MAXD>(pre, rt0, D, walk, tid);
+  const int t0 = __builtin_amdgcn_readfirstlane(query_id(qlist, q_offset, p0) / kKnnRefTile);
+  auto tile_at = [tiles, t0](int t) { return t0 + t < tiles ? t0 + t : t0 + t - tiles; };
+  TileRegs<MAXM> pre;
+  knn_load_tile<MAXM>(pre, xc, nrm, tile_at(0), P, pairs, tid);
+  knn_store_tile<MAXM>(pre, rt, pairs, tid);
+  if (tiles > 1) knn_load_tile<MAXM>(pre, xc, nrm, tile_at(1), P, pairs, tid);
   __syncthreads();
   uint2* const wave_buf = buf + static_cast<long long>(p0 + wave * kKnnWaveQueries) * B;
   for (int t = 0; t < tiles; ++t) {
-    const float* const cur = (t & 1) ? rt1 : rt0;
-    if (t + 1 < tiles) knn_load_tile<MAXD>(pre, xc, nrm, t + 1, D, tid);
-    v16f acc0 = {0}, acc1 = {0};
-#pragma unroll
-    for (int k2 = 0; k2 < MAXD / 2; ++k2) {
-      if (2 * k2 >= D) break;  // D is even
-      const int k = 2 * k2 + h;
-      const float b0 = cur[k * kKnnPitch + c32];
-      const float b1 = cur[k * kKnnPitch + 32 + c32];
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[k2], b0, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[k2], b1, acc1, 0, 0, 0);
-    }
-    // filter: candidates below their query's threshold to the query's
+    const float* const cur = rt;
+    v16f acc0, acc1;
+    knn_tile_dots(chunks, qa + (wave * kKnnWaveQueries + c32) * P + 2 * h, cur + c32 * P + 2 * h,
+                  cur + (32 + c32) * P + 2 * h, acc0, acc1);
+    // filter: s = |r|^2 - 2 q.r below the row's threshold goes to the row's
     // buffer.  Output i of this lane is row 8 (i / 4) + 4 h + i % 4 of the
-    // wave's 32, column c32 of the 32-column block.  (The block loop stays
-    // rolled, which keeps the hoisted LDS reads of one block in registers.)
-#pragma unroll 1
-    for (int b = 0; b < 2; ++b) {
-      const int col = t * kKnnRefTile + b * 32 + c32;
-      const float nr = cur[D * kKnnPitch + b * 32 + c32];
+    // wave's 32, reference c32 of the 32-reference block.
+    const float nr0 = cur[norm_at + c32];
+    const float nr1 = cur[norm_at + 32 + c32];
+    const unsigned int col0 = static_cast<unsigned int>(tile_at(t) * kKnnRefTile + c32);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int row0 = 8 * g + 4 * h;
-        const float4 thr4 = *reinterpret_cast<const float4*>(&rs.thr[wave][row0]);
-        const float4 nq4 = *reinterpret_cast<const float4*>(&rs.nq[wave][row0]);
-        const int4 qid4 = *reinterpret_cast<const int4*>(&rs.qid[wave][row0]);
-        const float thr_a[4] = {thr4.x, thr4.y, thr4.z, thr4.w};
-        const float nq_a[4] = {nq4.x, nq4.y, nq4.z, nq4.w};
-        const int qid_a[4] = {qid4.x, qid4.y, qid4.z, qid4.w};
+    for (int g = 0; g < 4; ++g) {
+      const int row0 = 8 * g + 4 * h;
+      const float4 thr4 = *reinterpret_cast<const float4*>(&rs.thr[wave][row0]);
+      const float thr_a[4] = {thr4.x, thr4.y, thr4.z, thr4.w};
+      float sv[8];
+      unsigned long long m[8];
+      unsigned long long any = 0ull;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int i = 4 * g + u;
-          const float dot = b == 0 ? acc0[i] : acc1[i];
-          const float d2 = fmaxf(fmaf(-2.0f, dot, nq_a[u] + nr), 0.0f);
-          const bool pass =
-              qid_a[u] >= 0 && col < n && d2 < thr_a[u] && !(exclude_self && col == qid_a[u]);
-          const unsigned long long m = __ballot(pass);
-          if (m != 0ull) {
-            const int row = row0 + u;
-            const unsigned int half = h ? static_cast<unsigned int>(m >> 32) : static_cast<unsigned int>(m);
+      for (int u = 0; u < 4; ++u) {
+        sv[2 * u] = fmaf(-2.0f, acc0[4 * g + u], nr0);
+        sv[2 * u + 1] = fmaf(-2.0f, acc1[4 * g + u], nr1);
+        m[2 * u] = __ballot(sv[2 * u] < thr_a[u]);
+        m[2 * u + 1] = __ballot(sv[2 * u + 1] < thr_a[u]);
+        any |= m[2 * u] | m[2 * u + 1];
+      }
+      if (any != 0ull) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (m[j] != 0ull) {
+            const int row = row0 + j / 2;
+            const unsigned int half = h ? static_cast<unsigned int>(m[j] >> 32) : static_cast<unsigned int>(m[j]);
             const int base = rs.cnt[wave][row];
-            if (pass)
+            if (sv[j] < thr_a[j / 2])
               wave_buf[static_cast<long long>(row) * B + base + __popc(half & ((1u << c32) - 1u))] =
-                  make_uint2(__float_as_uint(d2), static_cast<unsigned int>(col));
+                  make_uint2(ordered_bits(sv[j]), col0 + (j & 1) * 32u);
             if (c32 == 0) rs.cnt[wave][row] = base + __popc(half);
           }
         }
@@ -426,9 +574,12 @@ __global__ __launch_bounds__(kKnnThreads, 2) void k_knn_scan(const float* __rest
         rs.thr[wave][r] = thr;
       }
     }
-    __syncthreads();  // every wave is done with the tile it read
-    if (t + 1 < tiles) knn_store_tile<MAXD>(pre, (t & 1) ? rt0 : rt1, D, walk, tid);
-    __syncthreads();
+    __syncthreads();  // every wave is done with tile t
+    if (t + 1 < tiles) {
+      knn_store_tile<MAXM>(pre, rt, pairs, tid);
+      if (t + 2 < tiles) knn_load_tile<MAXM>(pre, xc, nrm, tile_at(t + 2), P, pairs, tid);
+    }
+    __syncthreads();  // tile t + 1 is in LDS
   }
   // final: keep kp per row; the threshold is what a rejected reference beat
   for (int r = 0; r < kKnnWaveQueries; ++r) {
@@ -447,47 +598,57 @@ __global__ __launch_bounds__(kKnnThreads, 2) void k_knn_scan(const float* __rest
 // ---- 3. finalize -------------------------------------------------------------------
 
 // One wave per query: exact squared distances of the candidates from the
-// input rows (fp64), sorted by (d2, index); the first k are written as
-// 1-based indices and float distances, column-major (neighbour j of point
-// q at j * n + q).  Uncertified queries are appended to retry.
+// input rows (fp64); the query itself is dropped when exclude_self; the rest
+// are sorted by (d2, index) and the first k written as 1-based indices and
+// float distances, column-major (neighbour j of point i at j * n + i).
+// Queries and candidates are positions in the scan's row order; perm maps
+// them to input rows.  Uncertified queries (positions) are appended to retry.
 template <int B>
 __global__ __launch_bounds__(kKnnThreads) void k_knn_finalize(
-    const float* __restrict__ x, int n, int d, Strides st, const int* __restrict__ qlist, int q_offset, int nq,
-    const uint2* __restrict__ buf, const float* __restrict__ thr_in, const int* __restrict__ cnt_in,
-    const float* __restrict__ nrm, const unsigned int* __restrict__ nrm_max_bits, float eps_unit, int k,
+    const float* __restrict__ x, int n, int d, Strides st, const int* __restrict__ perm,
+    const int* __restrict__ qlist, int q_offset, int nq, const uint2* __restrict__ buf,
+    const float* __restrict__ thr_in, const int* __restrict__ cnt_in, const float* __restrict__ nrm,
+    const unsigned int* __restrict__ nrm_max_bits, float eps_unit, int k, int exclude_self,
     int* __restrict__ idx_out, float* __restrict__ dist_out, int* __restrict__ retry, int* __restrict__ retry_count,
     int* __restrict__ short_rows) {
   constexpr int PER = B / kWave;
   const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
   const int p = static_cast<int>(blockIdx.x) * kKnnWaves + static_cast<int>(threadIdx.x) / kWave;
   if (p >= nq) return;  // whole wave
-  const int q = query_id(qlist, q_offset, p);
+  const int qpos = query_id(qlist, q_offset, p);
+  const int q = perm[qpos];
   const int c = cnt_in[p];
   const uint2* cand = buf + static_cast<long long>(p) * B;
   double dd[PER];
   int id[PER];
+  bool self_here = false;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = j * kWave + lane;
     dd[j] = INFINITY;
     id[j] = 0x7fffffff;
     if (e < c) {
-      const int r = static_cast<int>(cand[e].y);
-      double s = 0.0;
-      for (int t = 0; t < d; ++t) {
-        const double diff = static_cast<double>(x[st.at(q, t)]) - static_cast<double>(x[st.at(r, t)]);
-        s = fma(diff, diff, s);
+      const int r = perm[cand[e].y];
+      if (exclude_self && r == q) {
+        self_here = true;  // sorts last
+      } else {
+        double s = 0.0;
+        for (int t = 0; t < d; ++t) {
+          const double diff = static_cast<double>(x[st.at(q, t)]) - static_cast<double>(x[st.at(r, t)]);
+          s = fma(diff, diff, s);
+        }
+        dd[j] = s;
+        id[j] = r;
       }
-      dd[j] = s;
-      id[j] = r;
     }
   }
+  const int valid = c - (__ballot(self_here) != 0ull ? 1 : 0);
   wave_sort_pairs<PER>(dd, id, lane);
   double d2k = 0.0;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = j * kWave + lane;
-    if (e < k && e < c) {
+    if (e < k && e < valid) {
       idx_out[static_cast<long long>(e) * n + q] = id[j] + 1;
       dist_out[static_cast<long long>(e) * n + q] = static_cast<float>(sqrt(dd[j]));
     }
@@ -495,14 +656,15 @@ __global__ __launch_bounds__(kKnnThreads) void k_knn_finalize(
   }
   d2k = __shfl(d2k, (k - 1) % kWave);
   if (lane == 0) {
-    if (c < k) {
+    if (valid < k) {
       atomicAdd(short_rows, 1);
     } else {
       const float thr = thr_in[p];
       if (thr < INFINITY) {
+        const double nq_d = static_cast<double>(nrm[qpos]);
         const double eps = static_cast<double>(eps_unit) *
-                           (static_cast<double>(nrm[q]) + static_cast<double>(__uint_as_float(*nrm_max_bits)));
-        if (!(static_cast<double>(thr) - eps > d2k)) retry[atomicAdd(retry_count, 1)] = q;
+                           (nq_d + static_cast<double>(__uint_as_float(*nrm_max_bits)));
+        if (!(static_cast<double>(thr) + nq_d - eps > d2k)) retry[atomicAdd(retry_count, 1)] = qpos;
       }
     }
   }
@@ -512,55 +674,58 @@ __global__ __launch_bounds__(kKnnThreads) void k_knn_finalize(
 struct KnnPass {
   const float* x;  // input rows (strides st)
   Strides st;
-  const float* xc;  // centred, padded rows (n x D)
-  const float* nrm;
+  const int* perm;   // scan position -> input row
+  const float* xc;   // centred rows in scan order, pitch P, padded to whole tiles
+  const float* nrm;  // their squared norms
   const unsigned int* nrm_max_bits;
-  int n, d, D, k, exclude_self;
+  int n, d, P, chunks, k, exclude_self;
   uint2* buf;  // candidate buffers, nq x B
   float* thr;
   int* cnt;
   int* idx_out;
   float* dist_out;
-  int* retry;        // uncertified point indices
+  int* retry;        // uncertified queries (scan positions)
   int* retry_count;  // counters[0]
   int* short_rows;   // counters[1]
 };
 
-template <int B, int MAXD>
+template <int B, int MAXM>
 hipError_t launch_scan(const KnnPass& a, int kp, const int* qlist, int q_offset, int nq, hipStream_t stream) {
-  const std::size_t lds = 2 * static_cast<std::size_t>(a.D + 1) * kKnnPitch * sizeof(float);
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_knn_scan<B, MAXD>),
+  const std::size_t lds = static_cast<std::size_t>(knn_scan_lds_floats(a.P)) * sizeof(float);
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_knn_scan<B, MAXM>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (e != hipSuccess) return e;
   const int blocks = (nq + kKnnQueryBlock - 1) / kKnnQueryBlock;
-  k_knn_scan<B, MAXD><<<blocks, kKnnThreads, lds, stream>>>(a.xc, a.nrm, qlist, q_offset, nq, a.n, a.D, kp,
-                                                            a.exclude_self, a.buf, a.thr, a.cnt);
+  k_knn_scan<B, MAXM><<<blocks, kKnnThreads, lds, stream>>>(a.xc, a.nrm, qlist, q_offset, nq, a.n, a.P, a.chunks,
+                                                            kp, a.buf, a.thr, a.cnt);
   return hipGetLastError();
 }
 
 template <int B>
 hipError_t launch_scan_finalize(const KnnPass& a, int kp, const int* qlist, int q_offset, int nq,
                                 hipStream_t stream) {
-  static_assert(kKnnMaxDim <= 128, "a thread prefetches at most 32 values of a 64-row tile");
-  hipError_t e = a.D <= 64 ? launch_scan<B, 64>(a, kp, qlist, q_offset, nq, stream)
-                           : launch_scan<B, 128>(a, kp, qlist, q_offset, nq, stream);
+  static_assert(kKnnMaxDim <= 4 * 32, "at most 32 chunks of 4 dimensions");
+  hipError_t e = a.chunks <= 16 ? launch_scan<B, 16>(a, kp, qlist, q_offset, nq, stream)
+                                : launch_scan<B, 32>(a, kp, qlist, q_offset, nq, stream);
   if (e != hipSuccess) return e;
-  const float eps_unit = static_cast<float>(a.D + 12) * 0x1.0p-23f;
+  const float eps_unit = static_cast<float>(4 * a.chunks + 12) * 0x1.0p-23f;
   k_knn_finalize<B><<<(nq + kKnnWaves - 1) / kKnnWaves, kKnnThreads, 0, stream>>>(
-      a.x, a.n, a.d, a.st, qlist, q_offset, nq, a.buf, a.thr, a.cnt, a.nrm, a.nrm_max_bits, eps_unit, a.k, a.idx_out,
-      a.dist_out, a.retry, a.retry_count, a.short_rows);
+      a.x, a.n, a.d, a.st, a.perm, qlist, q_offset, nq, a.buf, a.thr, a.cnt, a.nrm, a.nrm_max_bits, eps_unit, a.k,
+      a.exclude_self, a.idx_out, a.dist_out, a.retry, a.retry_count, a.short_rows);
   return hipGetLastError();
 }
 
-// Candidate count kp of a query: k plus a margin of max(32, k / 2) on the
-// first pass, doubled for every rerun, at most kKnnMaxCand.
+// Candidates per query: k plus a margin of max(32, k / 2) (plus the query
+// itself, which the scan does not skip) on the first pass, doubled for every
+// rerun, at most kKnnMaxCand.
 constexpr int kKnnMaxCand = 1024 - 2 * kKnnRefTile;  // 896
 
-// Smallest buffer with room for kp entries plus at least kp new ones (and a
-// tile's 64) between compactions; 1024 for the largest kp.
+// Smallest buffer with room for kp entries, a margin of max(32, kp / 4) new
+// ones and a tile's 64 between compactions (in locality order few references
+// pass a settled threshold); 1024 for the largest kp.
 int buffer_for(int kp) {
   for (int B = 128; B <= 1024; B <<= 1)
-    if (B - kKnnRefTile >= 2 * kp) return B;
+    if (B - kKnnRefTile >= kp + std::max(32, kp / 4)) return B;
   return 1024;
 }
 
@@ -622,7 +787,8 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
     err = "exact KNN supports fewer than 2^31 - 64 rows";
     return 1;
   }
-  const int D = (d + 1) / 2 * 2;
+  const int P = knn_pitch(d);
+  const int chunks = (d + 3) / 4;
   const int n_pad = (n + kKnnRefTile - 1) / kKnnRefTile * kKnnRefTile;  // whole reference tiles
   hipStream_t stream = nullptr;
   hipError_t e;
@@ -649,7 +815,8 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
   }
   const int rows_per = 4096;
   const int pblocks = (n + rows_per - 1) / rows_per;
-  if ((e = xc.alloc(static_cast<std::size_t>(n_pad) * D)) != hipSuccess || (e = nrm.alloc(n_pad)) != hipSuccess ||
+  if ((e = xc.alloc(static_cast<std::size_t>(n_pad) * P + kKnnOverRead)) != hipSuccess ||
+      (e = nrm.alloc(n_pad)) != hipSuccess ||
       (e = partial.alloc(static_cast<std::size_t>(pblocks) * d)) != hipSuccess || (e = mean.alloc(d)) != hipSuccess ||
       (e = nrm_max.alloc(1)) != hipSuccess || (e = retry.alloc(n)) != hipSuccess ||
       (e = counters.alloc(3)) != hipSuccess)
@@ -657,13 +824,15 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
   // counters: [0] uncertified rows, [1] rows with fewer than k candidates,
   // [2] rows with non-finite values
   if ((e = hipMemsetAsync(counters.p, 0, 3 * sizeof(int), stream)) != hipSuccess ||
-      (e = hipMemsetAsync(nrm_max.p, 0, sizeof(unsigned int), stream)) != hipSuccess)
+      (e = hipMemsetAsync(nrm_max.p, 0, sizeof(unsigned int), stream)) != hipSuccess ||
+      (e = hipMemsetAsync(xc.p + static_cast<std::size_t>(n_pad) * P, 0, kKnnOverRead * sizeof(float), stream)) !=
+          hipSuccess)
     return fail("hipMemset", e);
   const Strides st = x_col_major ? Strides{1, n} : Strides{d, 1};
   k_knn_col_partials<<<pblocks, kPrepThreads, 0, stream>>>(x, n, d, st, rows_per, partial.p);
   k_knn_col_means<<<1, kPrepThreads, 0, stream>>>(partial.p, pblocks, d, n, mean.p);
   k_knn_center<<<(n_pad + kPrepThreads - 1) / kPrepThreads, kPrepThreads, 0, stream>>>(
-      x, n, n_pad, d, st, D, mean.p, xc.p, nrm.p, nrm_max.p, counters.p + 2);
+      x, n, n_pad, d, st, P, mean.p, xc.p, nrm.p, nrm_max.p, counters.p + 2);
   if ((e = hipGetLastError()) != hipSuccess) return fail("KNN prep launch", e);
   {
     int bad = 0;
@@ -677,19 +846,53 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
     }
   }
 
-  // queries in batches (the candidate buffers are batch x B entries)
-  int kp = std::min(kKnnMaxCand, k + std::max(32, k / 2));
-  const int batch = std::min(n, kKnnBatch);
+  // locality order: nearest of C pivots, then rows grouped by cell
+  const int C = std::max(1, std::min(1024, n / 256));
+  const int stride = n / C;
+  DevBuf<int> cell, cursor, perm;
+  DevBuf<float> xs, ns;
+  if ((e = cell.alloc(n)) != hipSuccess || (e = cursor.alloc(C)) != hipSuccess || (e = perm.alloc(n)) != hipSuccess ||
+      (e = xs.alloc(static_cast<std::size_t>(n_pad) * P + kKnnOverRead)) != hipSuccess ||
+      (e = ns.alloc(n_pad)) != hipSuccess)
+    return fail("hipMalloc(KNN order)", e);
+  if ((e = hipMemsetAsync(cursor.p, 0, C * sizeof(int), stream)) != hipSuccess ||
+      (e = hipMemsetAsync(xs.p + static_cast<std::size_t>(n_pad) * P, 0, kKnnOverRead * sizeof(float), stream)) !=
+          hipSuccess)
+    return fail("hipMemset", e);
+  {
+    const int rb = (n + kPrepThreads - 1) / kPrepThreads;
+    if (P <= 68)
+      k_knn_assign<68><<<rb, kPrepThreads, 0, stream>>>(xc.p, nrm.p, n, P, C, stride, cell.p);
+    else
+      k_knn_assign<132><<<rb, kPrepThreads, 0, stream>>>(xc.p, nrm.p, n, P, C, stride, cell.p);
+    k_knn_cell_count<<<rb, kPrepThreads, 0, stream>>>(cell.p, n, cursor.p);
+    k_knn_cell_offsets<<<1, 64, 0, stream>>>(cursor.p, C);
+    k_knn_cell_scatter<<<rb, kPrepThreads, 0, stream>>>(cell.p, n, cursor.p, perm.p);
+    const long long pairs = static_cast<long long>(n_pad) * (P / 2);
+    k_knn_permute<<<static_cast<unsigned int>((pairs + kPrepThreads - 1) / kPrepThreads), kPrepThreads, 0, stream>>>(
+        xc.p, nrm.p, perm.p, n, n_pad, P, xs.p, ns.p);
+    if ((e = hipGetLastError()) != hipSuccess) return fail("KNN order launch", e);
+  }
+
+  // Candidate buffers: B entries per query of a launch, at most
+  // kKnnCandEntries in all; a pass launches as many queries at once as they
+  // allow (one launch for the whole input up to millions of rows, so that
+  // the grid is many rounds of workgroups deep).
+  int kp = std::min(kKnnMaxCand, k + std::max(32, k / 2) + 1);
+  const std::size_t entries =
+      std::min<std::size_t>(kKnnCandEntries, static_cast<std::size_t>(n) * static_cast<std::size_t>(buffer_for(kp)));
+  auto batch_for = [&](int kp_) {
+    return static_cast<int>(std::min<std::size_t>(static_cast<std::size_t>(n), entries / buffer_for(kp_)));
+  };
   DevBuf<uint2> buf;
   DevBuf<float> thr;
   DevBuf<int> cnt;
-  if ((e = buf.alloc(static_cast<std::size_t>(batch) * 1024)) != hipSuccess || (e = thr.alloc(batch)) != hipSuccess ||
-      (e = cnt.alloc(batch)) != hipSuccess)
+  if ((e = buf.alloc(entries)) != hipSuccess || (e = thr.alloc(n)) != hipSuccess || (e = cnt.alloc(n)) != hipSuccess)
     return fail("hipMalloc(KNN candidates)", e);
-  KnnPass pass{x,      st,     xc.p,    nrm.p,    nrm_max.p, n,       d,           D,
-               k,      exclude_self, buf.p, thr.p, cnt.p, idx_out, dist_out, retry.p,
+  KnnPass pass{x,       st,          perm.p, xs.p,  ns.p,  nrm_max.p, n,       d,        P,
+               chunks,  k,           exclude_self,  buf.p, thr.p, cnt.p,     idx_out, dist_out, retry.p,
                counters.p, counters.p + 1};
-  for (int q0 = 0; q0 < n; q0 += batch) {
+  for (int q0 = 0, batch = batch_for(kp); q0 < n; q0 += batch) {
     const int nq = std::min(batch, n - q0);
     if ((e = launch_pass(pass, kp, nullptr, q0, nq, stream)) != hipSuccess) return fail("KNN scan launch", e);
   }
@@ -721,7 +924,7 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
     if ((e = hipMemcpyAsync(list.p, retry.p, nr * sizeof(int), hipMemcpyDeviceToDevice, stream)) != hipSuccess ||
         (e = hipMemsetAsync(counters.p, 0, 2 * sizeof(int), stream)) != hipSuccess)
       return fail("KNN retry setup", e);
-    for (int q0 = 0; q0 < nr; q0 += batch) {
+    for (int q0 = 0, batch = batch_for(kp); q0 < nr; q0 += batch) {
       const int nq = std::min(batch, nr - q0);
       if ((e = launch_pass(pass, kp, list.p + q0, 0, nq, stream)) != hipSuccess) return fail("KNN retry launch", e);
     }
