@@ -23,8 +23,10 @@ struct Strides {
 // Euclidean distance, self excluded when exclude_self.  Writes n x k
 // column-major (neighbour j of row i at j * n + i) 1-based indices and fp32
 // distances, ascending by (distance, index), to the device or the host.
-// stats (nullable, 3): rows rerun with a larger candidate set, passes, the
-// last pass's candidates per query.  Returns 0, or 1 with err set.
+// stats (nullable, 5): rows rerun with a larger candidate set, passes, the
+// last pass's candidates per query, 64-row reference tiles staged (summed
+// over blocks of 128 queries) and tiles computed (summed over waves of 32
+// queries) after pruning.  Returns 0, or 1 with err set.
 int knn_exact_run(const float* x, int n, int d, int x_col_major, int k, int exclude_self, int input_on_device,
                   int* indices, float* distances, int output_on_device, long long* stats, std::string& err);
 

@@ -193,38 +193,105 @@ __global__ __launch_bounds__(kPrepThreads) void k_knn_cell_count(const int* __re
   if (r < n) atomicAdd(&count[cell[r]], 1);
 }
 
-// Exclusive prefix sum of the C cell counts, in place (C is at most a few
-// thousand: one thread).
-__global__ void k_knn_cell_offsets(int* __restrict__ count, int C) {
+// Cell layout in scan order: cell j occupies positions pad_off[j] ..
+// pad_off[j + 1] - 1, its count rounded up to whole 64-row tiles (so that no
+// tile mixes cells); real_off[j] is the number of real rows before it.
+// pad_off[C] is the number of scan positions.  C is at most a few thousand:
+// one thread.
+__global__ void k_knn_cell_offsets(const int* __restrict__ count, int C, int* __restrict__ pad_off,
+                                   int* __restrict__ real_off) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  int acc = 0;
+  int pad = 0, real = 0;
   for (int j = 0; j < C; ++j) {
     const int v = count[j];
-    count[j] = acc;
-    acc += v;
+    pad_off[j] = pad;
+    real_off[j] = real;
+    pad += (v + kKnnRefTile - 1) / kKnnRefTile * kKnnRefTile;
+    real += v;
   }
+  pad_off[C] = pad;
 }
 
-// perm[position] = row, positions of a cell in arrival order.
+// perm[position] = row (positions of a cell's real rows in arrival order;
+// the rest of its last tile keeps perm = -1), and qpos[i] = position of the
+// i-th real row in scan order.
 __global__ __launch_bounds__(kPrepThreads) void k_knn_cell_scatter(const int* __restrict__ cell, int n,
-                                                                    int* __restrict__ cursor, int* __restrict__ perm) {
+                                                                    int* __restrict__ cursor,
+                                                                    const int* __restrict__ pad_off,
+                                                                    const int* __restrict__ real_off,
+                                                                    int* __restrict__ perm, int* __restrict__ qpos) {
   const int r = static_cast<int>(blockIdx.x) * kPrepThreads + threadIdx.x;
-  if (r < n) perm[atomicAdd(&cursor[cell[r]], 1)] = r;
+  if (r >= n) return;
+  const int c = cell[r];
+  const int i = atomicAdd(&cursor[c], 1);
+  perm[pad_off[c] + i] = r;
+  qpos[real_off[c] + i] = pad_off[c] + i;
 }
 
-// Rows of xc and their norms in scan order; positions n .. n_pad - 1 keep
-// the padding rows (zero, norm +inf).  One float2 per thread.
+// Rows of xc and their norms in scan order; padding positions (perm -1) get
+// a zero row and norm +inf, which no query accepts.  One float2 per thread.
 __global__ __launch_bounds__(kPrepThreads) void k_knn_permute(const float* __restrict__ xc,
                                                                const float* __restrict__ nrm,
-                                                               const int* __restrict__ perm, int n, int n_pad, int P,
+                                                               const int* __restrict__ perm, int n_scan, int P,
                                                                float* __restrict__ xs, float* __restrict__ ns) {
   const long long e = static_cast<long long>(blockIdx.x) * kPrepThreads + threadIdx.x;
   const int half = P / 2;
-  if (e >= static_cast<long long>(n_pad) * half) return;
+  if (e >= static_cast<long long>(n_scan) * half) return;
   const int i = static_cast<int>(e / half), c2 = static_cast<int>(e % half);
-  const int src = i < n ? perm[i] : i;
-  reinterpret_cast<float2*>(xs)[e] = reinterpret_cast<const float2*>(xc)[static_cast<long long>(src) * half + c2];
-  if (c2 == 0) ns[i] = nrm[src];
+  const int src = perm[i];
+  reinterpret_cast<float2*>(xs)[e] =
+      src >= 0 ? reinterpret_cast<const float2*>(xc)[static_cast<long long>(src) * half + c2] : make_float2(0.0f, 0.0f);
+  if (c2 == 0) ns[i] = src >= 0 ? nrm[src] : INFINITY;
+}
+
+// Bounding sphere of every 64-row tile of the scan-order rows: centre c =
+// mean of the tile's real rows (norm < +inf; fp64 sums, stored fp32, pitch
+// P), |c|^2 of the stored centre, and a radius >= max |r - c| over the real
+// rows (fp64 from the stored fp32 values, rounded up).  Tiles without real
+// rows (past the last, up to a whole group of 64) get a zero centre and
+// radius -inf, which bounds every distance at +inf.  One 64-thread block per
+// tile.
+__global__ __launch_bounds__(kKnnRefTile) void k_knn_tile_bounds(const float* __restrict__ xs,
+                                                                 const float* __restrict__ ns, int n_scan, int P,
+                                                                 float* __restrict__ centre,
+                                                                 float* __restrict__ cnorm,
+                                                                 float* __restrict__ radius) {
+  __shared__ float cen[kKnnMaxDim + 8];
+  __shared__ double part[kKnnRefTile];
+  __shared__ int real[kKnnRefTile];
+  const int t = static_cast<int>(blockIdx.x);
+  const int tid = static_cast<int>(threadIdx.x);
+  const int r0 = t * kKnnRefTile;
+  const bool mine = r0 + tid < n_scan && ns[r0 + tid] < INFINITY;  // a real row
+  real[tid] = mine ? 1 : 0;
+  __syncthreads();
+  int rows = 0;
+  for (int i = 0; i < kKnnRefTile; ++i) rows += real[i];
+  for (int c = tid; c < P; c += kKnnRefTile) {
+    double s = 0.0;
+    for (int i = 0; i < kKnnRefTile; ++i)
+      if (real[i]) s += static_cast<double>(xs[static_cast<long long>(r0 + i) * P + c]);
+    const float v = rows > 0 ? static_cast<float>(s / rows) : 0.0f;
+    cen[c] = v;
+    centre[static_cast<long long>(t) * P + c] = v;
+  }
+  __syncthreads();
+  double d2 = 0.0;
+  if (mine) {
+    for (int c = 0; c < P; ++c) {
+      const double diff = static_cast<double>(xs[static_cast<long long>(r0 + tid) * P + c]) - cen[c];
+      d2 = fma(diff, diff, d2);
+    }
+  }
+  part[tid] = d2;
+  __syncthreads();
+  if (tid == 0) {
+    double m = 0.0, cc = 0.0;
+    for (int i = 0; i < kKnnRefTile; ++i) m = fmax(m, part[i]);
+    for (int c = 0; c < P; ++c) cc = fma(static_cast<double>(cen[c]), static_cast<double>(cen[c]), cc);
+    cnorm[t] = static_cast<float>(cc);
+    radius[t] = rows > 0 ? __double2float_ru(sqrt(m) * (1.0 + 0x1.0p-40)) : -INFINITY;
+  }
 }
 
 // ---- sorting inside one wave ------------------------------------------------------
@@ -385,10 +452,12 @@ __device__ __forceinline__ int query_id(const int* __restrict__ qlist, int q_off
   return qlist != nullptr ? qlist[p] : q_offset + p;
 }
 
-// Per wave row state in LDS: threshold and count of each of its 32 queries.
+// Per wave row state in LDS: threshold, count and squared norm of each of its
+// 32 queries.
 struct alignas(16) WaveRows {
   float thr[kKnnWaves][kKnnWaveQueries];
   int cnt[kKnnWaves][kKnnWaveQueries];
+  float nq[kKnnWaves][kKnnWaveQueries];  // |q|^2
 };
 
 // The dot products of a tile: per chunk m of 4 dimensions, one float2 LDS
@@ -431,40 +500,57 @@ __device__ __forceinline__ void knn_tile_dots(int chunks, const float* qa, const
   }
 }
 
-// One tile's staging copy for one thread: float2 number tid + 256 s
-// (s < pairs = ceil(P / 8)) of the tile's contiguous 64 x P block (the last
-// copy reads past the block's end, into the next tile or xc's tail
-// allowance, and is never used), and the norm of row tid.
+// One 64-row block's staging copy for one thread: float2 number tid + 256 s
+// (s < pairs = ceil(P / 8)) of the block's contiguous 64 x P rows (the last
+// copy reads past the block's end, into the next rows or the array's tail
+// allowance, and is never used), and one auxiliary float per row: aux0[row]
+// for tid < 64, aux1[row] for 64 <= tid < 128.  Reference tiles carry their
+// norms (aux0); a group's tile centres carry |c|^2 (aux0) and radii (aux1).
 template <int MAXM>
 struct TileRegs {
   float2 v[knn_tile_pairs(MAXM)];
-  float norm;
+  float aux;
 };
 
 template <int MAXM>
-__device__ __forceinline__ void knn_load_tile(TileRegs<MAXM>& r, const float* __restrict__ xc,
-                                              const float* __restrict__ nrm, int t, int P, int pairs, int tid) {
-  const float2* const src = reinterpret_cast<const float2*>(xc + static_cast<long long>(t) * kKnnRefTile * P);
+__device__ __forceinline__ void knn_load_tile(TileRegs<MAXM>& r, const float* __restrict__ rows,
+                                              const float* __restrict__ aux0, const float* __restrict__ aux1, int t,
+                                              int P, int pairs, int tid) {
+  const float2* const src = reinterpret_cast<const float2*>(rows + static_cast<long long>(t) * kKnnRefTile * P);
 #pragma unroll
   for (int s = 0; s < knn_tile_pairs(MAXM); ++s)
     if (s < pairs) r.v[s] = src[tid + s * kKnnThreads];
-  r.norm = tid < kKnnRefTile ? nrm[t * kKnnRefTile + tid] : 0.0f;
+  if (tid < kKnnRefTile)
+    r.aux = aux0[t * kKnnRefTile + tid];
+  else if (tid < 2 * kKnnRefTile && aux1 != nullptr)
+    r.aux = aux1[t * kKnnRefTile + tid - kKnnRefTile];
 }
 
+// LDS of a scan block, in floats: the staged 64 rows (pairs * 512), aux0
+// (64), aux1 (64), then the 128 query rows (pitch P) and 4 floats for the
+// read one chunk past the last row.
+__host__ __device__ constexpr int knn_lds_aux(int P) { return (P + 7) / 8 * 2 * kKnnThreads; }
+__host__ __device__ constexpr int knn_lds_queries(int P) { return knn_lds_aux(P) + 2 * kKnnRefTile; }
+__host__ __device__ constexpr int knn_scan_lds_floats(int P) { return knn_lds_queries(P) + kKnnQueryBlock * P + 4; }
+
 template <int MAXM>
-__device__ __forceinline__ void knn_store_tile(const TileRegs<MAXM>& r, float* dst, int pairs, int tid) {
+__device__ __forceinline__ void knn_store_tile(const TileRegs<MAXM>& r, float* dst, int P, int pairs, int tid) {
   float2* const d2 = reinterpret_cast<float2*>(dst);
 #pragma unroll
   for (int s = 0; s < knn_tile_pairs(MAXM); ++s)
     if (s < pairs) d2[tid + s * kKnnThreads] = r.v[s];
-  if (tid < kKnnRefTile) dst[pairs * 2 * kKnnThreads + tid] = r.norm;
+  if (tid < 2 * kKnnRefTile) dst[knn_lds_aux(P) + tid] = r.aux;
 }
 
-// LDS of a scan block, in floats: the staged tile (pairs * 512), its 64
-// norms, then the 128 query rows (pitch P) and 4 floats for the read one
-// chunk past the last row.
-__host__ __device__ constexpr int knn_scan_lds_floats(int P) {
-  return (P + 7) / 8 * 2 * kKnnThreads + kKnnRefTile + kKnnQueryBlock * P + 4;
+// Lower bound of |q - r|^2 over a ball (centre c, radius rad): (|q - c| -
+// rad)^2 when positive, with |q - c|^2 = |q|^2 + |c|^2 - 2 q.c computed in
+// fp32 and lowered by its rounding bound eps (|q|^2 + |c|^2), the square root
+// and square shaded down by 2^-20.  A ball of radius -inf (padding) bounds
+// at +inf.
+__device__ __forceinline__ float knn_ball_bound(float nq, float nc, float rad, float qc, float eps) {
+  const float d2 = nq + nc - 2.0f * qc - eps * (nq + nc);
+  const float gap = sqrtf(fmaxf(d2, 0.0f)) - rad;
+  return gap > 0.0f ? gap * gap * (1.0f - 0x1.0p-20f) : 0.0f;
 }
 
 // Occupancy: 3 workgroups per CU (3 waves per SIMD) for up to 64 dimensions,
@@ -474,17 +560,27 @@ constexpr int knn_scan_blocks_per_cu() {
   return MAXM <= 16 ? 3 : 2;
 }
 
+// Reference tiles and their groups: tiles of 64 rows, groups of 64 tiles;
+// the centres of a group's tiles are staged like a tile and screened with
+// the same MFMA steps.
+struct TileGroups {
+  const float* centre;  // 64 * groups rows of pitch P (zero past the last tile)
+  const float* cnorm;   // |c|^2 per tile
+  const float* radius;  // per tile (-inf past the last tile)
+};
+
 template <int B, int MAXM>
 __global__ __launch_bounds__(kKnnThreads, knn_scan_blocks_per_cu<MAXM>()) void k_knn_scan(
-    const float* __restrict__ xc, const float* __restrict__ nrm, const int* __restrict__ qlist, int q_offset, int nq,
-    int n, int P, int chunks, int kp, uint2* __restrict__ buf, float* __restrict__ thr_out,
-    int* __restrict__ cnt_out) {
+    const float* __restrict__ xc, const float* __restrict__ nrm, TileGroups tg, const int* __restrict__ qlist,
+    int q_offset, int nq, int n, int P, int chunks, int kp, float eps_lb, uint2* __restrict__ buf,
+    float* __restrict__ thr_out, int* __restrict__ cnt_out, unsigned long long* __restrict__ work) {
   const int pairs = (P + 7) / 8;
-  const int norm_at = pairs * 2 * kKnnThreads;
+  const int aux_at = knn_lds_aux(P);
   extern __shared__ float smem[];
-  float* const rt = smem;                          // the current tile, then its norms
-  float* const qa = smem + norm_at + kKnnRefTile;  // the block's 128 query rows, pitch P
+  float* const rt = smem;                       // the staged rows, then aux0 and aux1
+  float* const qa = smem + knn_lds_queries(P);  // the block's 128 query rows, pitch P
   __shared__ WaveRows rs;
+  __shared__ unsigned long long wave_need[kKnnWaves];
   const int tid = static_cast<int>(threadIdx.x);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid & (kWave - 1);
@@ -504,82 +600,149 @@ __global__ __launch_bounds__(kKnnThreads, knn_scan_blocks_per_cu<MAXM>()) void k
   if (lane < kKnnWaveQueries) {
     rs.thr[wave][lane] = q_lane >= 0 ? INFINITY : -INFINITY;  // -inf: no row, accepts nothing
     rs.cnt[wave][lane] = 0;
+    rs.nq[wave][lane] = q_lane >= 0 ? nrm[q_lane] : 0.0f;
   }
 
-  // References in tiles of 64, starting at the tile that holds the block's
-  // first query (rows are in locality order, so the nearest references come
-  // first and the thresholds settle early) and wrapping around.  The next
-  // tile is loaded into registers while the current one is used, and stored
-  // between two barriers.
+  // Groups of 64 tiles are visited from the group holding the block's first
+  // query (rows are in locality order, so the nearest references come first
+  // and the thresholds settle early), wrapping around.  Per group: stage its
+  // tile centres, and find per wave the tiles that can hold a candidate of
+  // one of its queries: a reference r of a tile with centre c and radius rad
+  // has |q - r| >= |q - c| - rad, and only tiles whose bound is below
+  // t + |q|^2 for some query (s = |r|^2 - 2 q.r < t) are staged.  Skipped
+  // references count as rejected: their squared distance is at least the
+  // query's threshold, as the certificate requires.  The next 64-row block
+  // (tile or group centres) is loaded into registers while one is used.
   const int tiles = (n + kKnnRefTile - 1) / kKnnRefTile;
+  const int groups = (tiles + kKnnRefTile - 1) / kKnnRefTile;
   const int t0 = __builtin_amdgcn_readfirstlane(query_id(qlist, q_offset, p0) / kKnnRefTile);
-  auto tile_at = [tiles, t0](int t) { return t0 + t < tiles ? t0 + t : t0 + t - tiles; };
-  TileRegs<MAXM> pre;
-  knn_load_tile<MAXM>(pre, xc, nrm, tile_at(0), P, pairs, tid);
-  knn_store_tile<MAXM>(pre, rt, pairs, tid);
-  if (tiles > 1) knn_load_tile<MAXM>(pre, xc, nrm, tile_at(1), P, pairs, tid);
-  __syncthreads();
+  const int g0 = t0 / kKnnRefTile;
+  const float* const qrow = qa + (wave * kKnnWaveQueries + c32) * P + 2 * h;
   uint2* const wave_buf = buf + static_cast<long long>(p0 + wave * kKnnWaveQueries) * B;
-  for (int t = 0; t < tiles; ++t) {
-    const float* const cur = rt;
-    v16f acc0, acc1;
-    knn_tile_dots(chunks, qa + (wave * kKnnWaveQueries + c32) * P + 2 * h, cur + c32 * P + 2 * h,
-                  cur + (32 + c32) * P + 2 * h, acc0, acc1);
-    // filter: s = |r|^2 - 2 q.r below the row's threshold goes to the row's
-    // buffer.  Output i of this lane is row 8 (i / 4) + 4 h + i % 4 of the
-    // wave's 32, reference c32 of the 32-reference block.
-    const float nr0 = cur[norm_at + c32];
-    const float nr1 = cur[norm_at + 32 + c32];
-    const unsigned int col0 = static_cast<unsigned int>(tile_at(t) * kKnnRefTile + c32);
+  unsigned int staged = 0, computed = 0;  // tiles staged by the block, tiles computed by the wave
+  TileRegs<MAXM> pre;
+  knn_load_tile<MAXM>(pre, tg.centre, tg.cnorm, tg.radius, g0, P, pairs, tid);
+  for (int gi = 0; gi < groups; ++gi) {
+    const int g = g0 + gi < groups ? g0 + gi : g0 + gi - groups;
+    __syncthreads();  // every wave is done with the rows in LDS
+    knn_store_tile<MAXM>(pre, rt, P, pairs, tid);
+    __syncthreads();
+    unsigned long long need;  // bit j: tile 64 g + j can hold a candidate of this wave's queries
+    {
+      v16f acc0, acc1;
+      knn_tile_dots(chunks, qrow, rt + c32 * P + 2 * h, rt + (32 + c32) * P + 2 * h, acc0, acc1);
+      const float nc0 = rt[aux_at + c32], nc1 = rt[aux_at + 32 + c32];
+      const float rd0 = rt[aux_at + kKnnRefTile + c32], rd1 = rt[aux_at + kKnnRefTile + 32 + c32];
+      bool need0 = false, need1 = false;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int row0 = 8 * g + 4 * h;
-      const float4 thr4 = *reinterpret_cast<const float4*>(&rs.thr[wave][row0]);
-      const float thr_a[4] = {thr4.x, thr4.y, thr4.z, thr4.w};
-      float sv[8];
-      unsigned long long m[8];
-      unsigned long long any = 0ull;
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int row0 = 8 * g4 + 4 * h;
+        const float4 thr4 = *reinterpret_cast<const float4*>(&rs.thr[wave][row0]);
+        const float4 nq4 = *reinterpret_cast<const float4*>(&rs.nq[wave][row0]);
+        const float thr_a[4] = {thr4.x, thr4.y, thr4.z, thr4.w};
+        const float nq_a[4] = {nq4.x, nq4.y, nq4.z, nq4.w};
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        sv[2 * u] = fmaf(-2.0f, acc0[4 * g + u], nr0);
-        sv[2 * u + 1] = fmaf(-2.0f, acc1[4 * g + u], nr1);
-        m[2 * u] = __ballot(sv[2 * u] < thr_a[u]);
-        m[2 * u + 1] = __ballot(sv[2 * u + 1] < thr_a[u]);
-        any |= m[2 * u] | m[2 * u + 1];
+        for (int u = 0; u < 4; ++u) {
+          const float lim = thr_a[u] + nq_a[u];
+          need0 |= knn_ball_bound(nq_a[u], nc0, rd0, acc0[4 * g4 + u], eps_lb) < lim;
+          need1 |= knn_ball_bound(nq_a[u], nc1, rd1, acc1[4 * g4 + u], eps_lb) < lim;
+        }
       }
-      if (any != 0ull) {
+      const unsigned long long b0 = __ballot(need0), b1 = __ballot(need1);
+      need = ((b0 | (b0 >> 32)) & 0xffffffffull) | (((b1 | (b1 >> 32)) & 0xffffffffull) << 32);
+    }
+    if (lane == 0) wave_need[wave] = need;
+    __syncthreads();
+    // Tiles are taken in order from `rot` (the block's own tile in the first
+    // group, so that the thresholds start from the nearest references), as
+    // bits of the mask rotated right by rot.
+    const int rot = gi == 0 ? t0 - g * kKnnRefTile : 0;
+    auto rotr = [](unsigned long long v, int r) { return r == 0 ? v : (v >> r) | (v << (kKnnRefTile - r)); };
+    unsigned long long todo = rotr(wave_need[0] | wave_need[1] | wave_need[2] | wave_need[3], rot);
+    need = rotr(need, rot);
+    int cur = -1;  // tile index within the group, rotated
+    if (todo != 0ull) {
+      cur = __ffsll(static_cast<long long>(todo)) - 1;
+      todo &= todo - 1ull;
+      knn_load_tile<MAXM>(pre, xc, nrm, nullptr, g * kKnnRefTile + ((cur + rot) & (kKnnRefTile - 1)), P, pairs,
+                          tid);
+    } else if (gi + 1 < groups) {
+      const int gn = g + 1 < groups ? g + 1 : 0;
+      knn_load_tile<MAXM>(pre, tg.centre, tg.cnorm, tg.radius, gn, P, pairs, tid);
+    }
+    while (cur >= 0) {
+      __syncthreads();  // every wave is done with the rows in LDS
+      knn_store_tile<MAXM>(pre, rt, P, pairs, tid);
+      __syncthreads();
+      int next = -1;
+      if (todo != 0ull) {
+        next = __ffsll(static_cast<long long>(todo)) - 1;
+        todo &= todo - 1ull;
+        knn_load_tile<MAXM>(pre, xc, nrm, nullptr, g * kKnnRefTile + ((next + rot) & (kKnnRefTile - 1)), P, pairs,
+                            tid);
+      } else if (gi + 1 < groups) {
+        const int gn = g + 1 < groups ? g + 1 : 0;
+        knn_load_tile<MAXM>(pre, tg.centre, tg.cnorm, tg.radius, gn, P, pairs, tid);
+      }
+      ++staged;
+      if ((need >> cur) & 1ull) {
+        ++computed;
+        v16f acc0, acc1;
+        knn_tile_dots(chunks, qrow, rt + c32 * P + 2 * h, rt + (32 + c32) * P + 2 * h, acc0, acc1);
+        // filter: s = |r|^2 - 2 q.r below the row's threshold goes to the
+        // row's buffer.  Output i of this lane is row 8 (i / 4) + 4 h + i % 4
+        // of the wave's 32, reference c32 of the 32-reference block.
+        const float nr0 = rt[aux_at + c32];
+        const float nr1 = rt[aux_at + 32 + c32];
+        const unsigned int col0 =
+            static_cast<unsigned int>((g * kKnnRefTile + ((cur + rot) & (kKnnRefTile - 1))) * kKnnRefTile + c32);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (m[j] != 0ull) {
-            const int row = row0 + j / 2;
-            const unsigned int half = h ? static_cast<unsigned int>(m[j] >> 32) : static_cast<unsigned int>(m[j]);
-            const int base = rs.cnt[wave][row];
-            if (sv[j] < thr_a[j / 2])
-              wave_buf[static_cast<long long>(row) * B + base + __popc(half & ((1u << c32) - 1u))] =
-                  make_uint2(ordered_bits(sv[j]), col0 + (j & 1) * 32u);
-            if (c32 == 0) rs.cnt[wave][row] = base + __popc(half);
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int row0 = 8 * g4 + 4 * h;
+          const float4 thr4 = *reinterpret_cast<const float4*>(&rs.thr[wave][row0]);
+          const float thr_a[4] = {thr4.x, thr4.y, thr4.z, thr4.w};
+          float sv[8];
+          unsigned long long m[8];
+          unsigned long long any = 0ull;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            sv[2 * u] = fmaf(-2.0f, acc0[4 * g4 + u], nr0);
+            sv[2 * u + 1] = fmaf(-2.0f, acc1[4 * g4 + u], nr1);
+            m[2 * u] = __ballot(sv[2 * u] < thr_a[u]);
+            m[2 * u + 1] = __ballot(sv[2 * u + 1] < thr_a[u]);
+            any |= m[2 * u] | m[2 * u + 1];
+          }
+          if (any != 0ull) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              if (m[j] != 0ull) {
+                const int row = row0 + j / 2;
+                const unsigned int half =
+                    h ? static_cast<unsigned int>(m[j] >> 32) : static_cast<unsigned int>(m[j]);
+                const int base = rs.cnt[wave][row];
+                if (sv[j] < thr_a[j / 2])
+                  wave_buf[static_cast<long long>(row) * B + base + __popc(half & ((1u << c32) - 1u))] =
+                      make_uint2(ordered_bits(sv[j]), col0 + (j & 1) * 32u);
+                if (c32 == 0) rs.cnt[wave][row] = base + __popc(half);
+              }
+            }
+          }
+        }
+        // rows that could overflow in the next tile: sort, keep kp
+        unsigned long long full = __ballot(lane < kKnnWaveQueries && rs.cnt[wave][c32] > B - kKnnRefTile);
+        while (full != 0ull) {
+          const int r = __ffsll(static_cast<long long>(full)) - 1;
+          full &= full - 1ull;
+          float thr = rs.thr[wave][r];
+          const int c = compact_row<B>(wave_buf + static_cast<long long>(r) * B, rs.cnt[wave][r], kp, lane, &thr);
+          if (lane == 0) {
+            rs.cnt[wave][r] = c;
+            rs.thr[wave][r] = thr;
           }
         }
       }
+      cur = next;
     }
-    // rows that could overflow in the next tile: sort, keep kp
-    unsigned long long need = __ballot(lane < kKnnWaveQueries && rs.cnt[wave][c32] > B - kKnnRefTile);
-    while (need != 0ull) {
-      const int r = __ffsll(static_cast<long long>(need)) - 1;
-      need &= need - 1ull;
-      float thr = rs.thr[wave][r];
-      const int c = compact_row<B>(wave_buf + static_cast<long long>(r) * B, rs.cnt[wave][r], kp, lane, &thr);
-      if (lane == 0) {
-        rs.cnt[wave][r] = c;
-        rs.thr[wave][r] = thr;
-      }
-    }
-    __syncthreads();  // every wave is done with tile t
-    if (t + 1 < tiles) {
-      knn_store_tile<MAXM>(pre, rt, pairs, tid);
-      if (t + 2 < tiles) knn_load_tile<MAXM>(pre, xc, nrm, tile_at(t + 2), P, pairs, tid);
-    }
-    __syncthreads();  // tile t + 1 is in LDS
   }
   // final: keep kp per row; the threshold is what a rejected reference beat
   for (int r = 0; r < kKnnWaveQueries; ++r) {
@@ -592,6 +755,10 @@ __global__ __launch_bounds__(kKnnThreads, knn_scan_blocks_per_cu<MAXM>()) void k
       thr_out[p] = thr;
       cnt_out[p] = c;
     }
+  }
+  if (lane == 0) {
+    if (wave == 0) atomicAdd(&work[0], static_cast<unsigned long long>(staged));
+    atomicAdd(&work[1], static_cast<unsigned long long>(computed));
   }
 }
 
@@ -677,8 +844,11 @@ struct KnnPass {
   const int* perm;   // scan position -> input row
   const float* xc;   // centred rows in scan order, pitch P, padded to whole tiles
   const float* nrm;  // their squared norms
+  TileGroups tg;     // bounding spheres of their 64-row tiles
   const unsigned int* nrm_max_bits;
-  int n, d, P, chunks, k, exclude_self;
+  int n;       // rows of the input (and of the output's columns)
+  int n_scan;  // scan positions (cells padded to whole tiles)
+  int d, P, chunks, k, exclude_self;
   uint2* buf;  // candidate buffers, nq x B
   float* thr;
   int* cnt;
@@ -687,6 +857,7 @@ struct KnnPass {
   int* retry;        // uncertified queries (scan positions)
   int* retry_count;  // counters[0]
   int* short_rows;   // counters[1]
+  unsigned long long* work;  // [0] tiles staged (per block), [1] tiles computed (per wave)
 };
 
 template <int B, int MAXM>
@@ -696,8 +867,9 @@ hipError_t launch_scan(const KnnPass& a, int kp, const int* qlist, int q_offset,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (e != hipSuccess) return e;
   const int blocks = (nq + kKnnQueryBlock - 1) / kKnnQueryBlock;
-  k_knn_scan<B, MAXM><<<blocks, kKnnThreads, lds, stream>>>(a.xc, a.nrm, qlist, q_offset, nq, a.n, a.P, a.chunks,
-                                                            kp, a.buf, a.thr, a.cnt);
+  const float eps_lb = static_cast<float>(4 * a.chunks + 8) * 0x1.0p-23f;
+  k_knn_scan<B, MAXM><<<blocks, kKnnThreads, lds, stream>>>(a.xc, a.nrm, a.tg, qlist, q_offset, nq, a.n_scan, a.P,
+                                                            a.chunks, kp, eps_lb, a.buf, a.thr, a.cnt, a.work);
   return hipGetLastError();
 }
 
@@ -720,12 +892,11 @@ hipError_t launch_scan_finalize(const KnnPass& a, int kp, const int* qlist, int 
 // rerun, at most kKnnMaxCand.
 constexpr int kKnnMaxCand = 1024 - 2 * kKnnRefTile;  // 896
 
-// Smallest buffer with room for kp entries, a margin of max(32, kp / 4) new
-// ones and a tile's 64 between compactions (in locality order few references
-// pass a settled threshold); 1024 for the largest kp.
+// Smallest buffer with room for kp entries plus at least kp new ones (and a
+// tile's 64) between compactions; 1024 for the largest kp.
 int buffer_for(int kp) {
   for (int B = 128; B <= 1024; B <<= 1)
-    if (B - kKnnRefTile >= kp + std::max(32, kp / 4)) return B;
+    if (B - kKnnRefTile >= 2 * kp) return B;
   return 1024;
 }
 
@@ -783,8 +954,8 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
     err = "k exceeds the number of " + std::string(exclude_self ? "non-self " : "") + "neighbors";
     return 1;
   }
-  if (n > INT_MAX - kKnnRefTile) {
-    err = "exact KNN supports fewer than 2^31 - 64 rows";
+  if (n > INT_MAX - (1 << 17)) {
+    err = "exact KNN supports fewer than 2^31 - 2^17 rows";
     return 1;
   }
   const int P = knn_pitch(d);
@@ -846,33 +1017,62 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
     }
   }
 
-  // locality order: nearest of C pivots, then rows grouped by cell
+  // Locality order: each row goes to the cell of its nearest pivot; cells
+  // are laid out one after another, each padded to whole 64-row tiles.
   const int C = std::max(1, std::min(1024, n / 256));
   const int stride = n / C;
-  DevBuf<int> cell, cursor, perm;
+  const int scan_max = n_pad + C * kKnnRefTile;  // bound on the scan positions
+  DevBuf<int> cell, cursor, pad_off, real_off, perm, qpos;
   DevBuf<float> xs, ns;
-  if ((e = cell.alloc(n)) != hipSuccess || (e = cursor.alloc(C)) != hipSuccess || (e = perm.alloc(n)) != hipSuccess ||
-      (e = xs.alloc(static_cast<std::size_t>(n_pad) * P + kKnnOverRead)) != hipSuccess ||
-      (e = ns.alloc(n_pad)) != hipSuccess)
+  if ((e = cell.alloc(n)) != hipSuccess || (e = cursor.alloc(C)) != hipSuccess ||
+      (e = pad_off.alloc(C + 1)) != hipSuccess || (e = real_off.alloc(C)) != hipSuccess ||
+      (e = perm.alloc(scan_max)) != hipSuccess || (e = qpos.alloc(n)) != hipSuccess ||
+      (e = xs.alloc(static_cast<std::size_t>(scan_max) * P + kKnnOverRead)) != hipSuccess ||
+      (e = ns.alloc(scan_max)) != hipSuccess)
     return fail("hipMalloc(KNN order)", e);
-  if ((e = hipMemsetAsync(cursor.p, 0, C * sizeof(int), stream)) != hipSuccess ||
-      (e = hipMemsetAsync(xs.p + static_cast<std::size_t>(n_pad) * P, 0, kKnnOverRead * sizeof(float), stream)) !=
-          hipSuccess)
-    return fail("hipMemset", e);
+  int n_scan = 0;
   {
     const int rb = (n + kPrepThreads - 1) / kPrepThreads;
+    if ((e = hipMemsetAsync(cursor.p, 0, C * sizeof(int), stream)) != hipSuccess ||
+        (e = hipMemsetAsync(perm.p, 0xff, scan_max * sizeof(int), stream)) != hipSuccess)
+      return fail("hipMemset", e);
     if (P <= 68)
       k_knn_assign<68><<<rb, kPrepThreads, 0, stream>>>(xc.p, nrm.p, n, P, C, stride, cell.p);
     else
       k_knn_assign<132><<<rb, kPrepThreads, 0, stream>>>(xc.p, nrm.p, n, P, C, stride, cell.p);
     k_knn_cell_count<<<rb, kPrepThreads, 0, stream>>>(cell.p, n, cursor.p);
-    k_knn_cell_offsets<<<1, 64, 0, stream>>>(cursor.p, C);
-    k_knn_cell_scatter<<<rb, kPrepThreads, 0, stream>>>(cell.p, n, cursor.p, perm.p);
-    const long long pairs = static_cast<long long>(n_pad) * (P / 2);
+    k_knn_cell_offsets<<<1, 64, 0, stream>>>(cursor.p, C, pad_off.p, real_off.p);
+    if ((e = hipGetLastError()) != hipSuccess || (e = hipMemsetAsync(cursor.p, 0, C * sizeof(int), stream)) !=
+                                                     hipSuccess)
+      return fail("KNN order launch", e);
+    k_knn_cell_scatter<<<rb, kPrepThreads, 0, stream>>>(cell.p, n, cursor.p, pad_off.p, real_off.p, perm.p, qpos.p);
+    if ((e = hipMemcpyAsync(&n_scan, pad_off.p + C, sizeof(int), hipMemcpyDeviceToHost, stream)) != hipSuccess ||
+        (e = hipStreamSynchronize(stream)) != hipSuccess)
+      return fail("KNN order", e);
+    if (n_scan < n || n_scan > scan_max || n_scan % kKnnRefTile != 0) {
+      err = "exact KNN: inconsistent cell layout";
+      return 1;
+    }
+    const long long pairs = static_cast<long long>(n_scan) * (P / 2);
     k_knn_permute<<<static_cast<unsigned int>((pairs + kPrepThreads - 1) / kPrepThreads), kPrepThreads, 0, stream>>>(
-        xc.p, nrm.p, perm.p, n, n_pad, P, xs.p, ns.p);
-    if ((e = hipGetLastError()) != hipSuccess) return fail("KNN order launch", e);
+        xc.p, nrm.p, perm.p, n_scan, P, xs.p, ns.p);
+    if ((e = hipGetLastError()) != hipSuccess ||
+        (e = hipMemsetAsync(xs.p + static_cast<std::size_t>(n_scan) * P, 0, kKnnOverRead * sizeof(float), stream)) !=
+            hipSuccess)
+      return fail("KNN order launch", e);
   }
+  // tile bounding spheres, for whole groups of 64 tiles
+  const int tiles = n_scan / kKnnRefTile;
+  const int tiles_pad = (tiles + kKnnRefTile - 1) / kKnnRefTile * kKnnRefTile;
+  DevBuf<float> tcentre, tcnorm, tradius;
+  if ((e = tcentre.alloc(static_cast<std::size_t>(tiles_pad) * P + kKnnOverRead)) != hipSuccess ||
+      (e = tcnorm.alloc(tiles_pad)) != hipSuccess || (e = tradius.alloc(tiles_pad)) != hipSuccess)
+    return fail("hipMalloc(KNN tile bounds)", e);
+  if ((e = hipMemsetAsync(tcentre.p + static_cast<std::size_t>(tiles_pad) * P, 0, kKnnOverRead * sizeof(float),
+                          stream)) != hipSuccess)
+    return fail("hipMemset", e);
+  k_knn_tile_bounds<<<tiles_pad, kKnnRefTile, 0, stream>>>(xs.p, ns.p, n_scan, P, tcentre.p, tcnorm.p, tradius.p);
+  if ((e = hipGetLastError()) != hipSuccess) return fail("KNN tile bounds launch", e);
 
   // Candidate buffers: B entries per query of a launch, at most
   // kKnnCandEntries in all; a pass launches as many queries at once as they
@@ -889,12 +1089,16 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
   DevBuf<int> cnt;
   if ((e = buf.alloc(entries)) != hipSuccess || (e = thr.alloc(n)) != hipSuccess || (e = cnt.alloc(n)) != hipSuccess)
     return fail("hipMalloc(KNN candidates)", e);
-  KnnPass pass{x,       st,          perm.p, xs.p,  ns.p,  nrm_max.p, n,       d,        P,
-               chunks,  k,           exclude_self,  buf.p, thr.p, cnt.p,     idx_out, dist_out, retry.p,
-               counters.p, counters.p + 1};
+  DevBuf<unsigned long long> work;
+  if ((e = work.alloc(2)) != hipSuccess) return fail("hipMalloc(KNN work)", e);
+  if ((e = hipMemsetAsync(work.p, 0, 2 * sizeof(unsigned long long), stream)) != hipSuccess)
+    return fail("hipMemset", e);
+  KnnPass pass{x,       st,     perm.p, xs.p,   ns.p,  TileGroups{tcentre.p, tcnorm.p, tradius.p}, nrm_max.p,
+               n,       n_scan, d,      P,      chunks, k,  exclude_self, buf.p, thr.p, cnt.p, idx_out, dist_out,
+               retry.p, counters.p, counters.p + 1, work.p};
   for (int q0 = 0, batch = batch_for(kp); q0 < n; q0 += batch) {
     const int nq = std::min(batch, n - q0);
-    if ((e = launch_pass(pass, kp, nullptr, q0, nq, stream)) != hipSuccess) return fail("KNN scan launch", e);
+    if ((e = launch_pass(pass, kp, qpos.p + q0, 0, nq, stream)) != hipSuccess) return fail("KNN scan launch", e);
   }
   int host_counts[2] = {0, 0};
   long long retried = 0;
@@ -940,9 +1144,13 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
     return fail("KNN sync", e);
   }
   if (stats != nullptr) {
+    unsigned long long w[2] = {0, 0};
+    if ((e = hipMemcpy(w, work.p, sizeof(w), hipMemcpyDeviceToHost)) != hipSuccess) return fail("KNN stats", e);
     stats[0] = retried;
     stats[1] = passes;
     stats[2] = kp;
+    stats[3] = static_cast<long long>(w[0]);
+    stats[4] = static_cast<long long>(w[1]);
   }
   return 0;
 }

@@ -119,7 +119,7 @@ def exact_knn(data, k: int, exclude_self: bool = True, keep_device: bool = False
     if not lib.fastembedr_hip_available():
         raise _lib.HipBackendUnavailable(
             "Native HIP KNN was requested, but no gfx950 device is visible. No CPU fallback is used.")
-    stats = (C.c_longlong * 3)()
+    stats = (C.c_longlong * 5)()
     t0 = time.perf_counter()
     if keep_device:
         if not 1 <= k <= MAX_K:
@@ -140,7 +140,8 @@ def exact_knn(data, k: int, exclude_self: bool = True, keep_device: bool = False
     del keep
     res.elapsed_sec = time.perf_counter() - t0
     res.exclude_self = bool(exclude_self)
-    res.stats = dict(rerun_rows=int(stats[0]), passes=int(stats[1]), candidates=int(stats[2]))
+    res.stats = dict(rerun_rows=int(stats[0]), passes=int(stats[1]), candidates=int(stats[2]),
+                     tiles_staged=int(stats[3]), tiles_computed=int(stats[4]))
     return res
 
 

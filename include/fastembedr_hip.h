@@ -270,9 +270,10 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_p_build_ms(const fastembedr_hip_tsne*
  *   distances    same layout, sqrt of the squared distance
  * Neighbours are ordered by (distance, index), as an ordered dense distance
  * matrix (tests/testthat/helper-knn.R:5-38) orders them.  stats (may be NULL,
- * 3 values): rows rerun with a larger candidate set, passes, the last pass's
- * candidates per query.  Returns 0, or 1 with fastembedr_hip_embedding_last_error()
- * set. */
+ * 5 values): rows rerun with a larger candidate set, passes, the last pass's
+ * candidates per query, 64-row reference tiles staged (summed over blocks of
+ * 128 queries) and tiles computed (summed over waves of 32 queries) after
+ * pruning.  Returns 0, or 1 with fastembedr_hip_embedding_last_error() set. */
 FASTEMBEDR_HIP_API int fastembedr_hip_knn_exact(const float* x, int n, int d, int x_col_major, int k,
                                                 int exclude_self, int x_on_device, int* indices, float* distances,
                                                 int output_on_device, long long* stats);
