@@ -57,6 +57,7 @@ SIGNATURES = {
     "fastembedr_hip_transform_probe": (_I, [_P, _I, _P, _P, _I, _I, C.c_double, _P, C.c_double, _I, _I, _I, _I,
                                             _P, _P, _P]),
     "fastembedr_hip_knn_exact": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _LLP]),
+    "fastembedr_hip_knn_query": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _I, _LLP]),
 }
 
 REPULSION_GRID = 0

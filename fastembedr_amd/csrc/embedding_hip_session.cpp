@@ -1503,4 +1503,17 @@ int fastembedr_hip_knn_exact(const float* x, int n, int d, int x_col_major, int 
   return 0;
 }
 
+int fastembedr_hip_knn_query(const float* reference, int n_reference, const float* query, int n_query, int d,
+                             int col_major, int k, int inputs_on_device, int* indices, float* distances,
+                             int output_on_device, long long* stats) {
+  g_last_error.clear();
+  std::string err;
+  if (fehip::knn_query_run(reference, n_reference, query, n_query, d, col_major, k, inputs_on_device, indices,
+                           distances, output_on_device, stats, err) != 0) {
+    set_error("fastembedr_hip_knn_query: " + err);
+    return 1;
+  }
+  return 0;
+}
+
 }  // extern "C"

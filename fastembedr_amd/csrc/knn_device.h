@@ -30,4 +30,12 @@ struct Strides {
 int knn_exact_run(const float* x, int n, int d, int x_col_major, int k, int exclude_self, int input_on_device,
                   int* indices, float* distances, int output_on_device, long long* stats, std::string& err);
 
+// k nearest references of every query row: ref (n_ref x d) and query
+// (n_query x d), both fp32 in the same layout (column-major when col_major)
+// and residency; k <= n_ref.  Writes n_query x k column-major 1-based
+// reference indices and fp32 distances; stats as above.
+int knn_query_run(const float* ref, int n_ref, const float* query, int n_query, int d, int col_major, int k,
+                  int input_on_device, int* indices, float* distances, int output_on_device, long long* stats,
+                  std::string& err);
+
 }  // namespace fehip

@@ -141,12 +141,13 @@ __global__ __launch_bounds__(kPrepThreads) void k_knn_center(const float* __rest
 // out one after another.  A block of queries then starts its scan at its own
 // cell.
 
-// Nearest pivot (pivot j = row j * stride) of every row, by |p|^2 - 2 x.p in
-// fp32 (only the order matters here, not exactness).  One row per thread, in
+// Nearest pivot (pivot j = reference row j * stride) of every row of xc, by
+// |p|^2 - 2 x.p in fp32 (only the order matters here, not exactness).  One row per thread, in
 // registers (MAXP >= P, zero padded); pivots staged 32 at a time in LDS.
 template <int MAXP>
-__global__ __launch_bounds__(kPrepThreads) void k_knn_assign(const float* __restrict__ xc,
-                                                              const float* __restrict__ nrm, int n, int P, int C,
+__global__ __launch_bounds__(kPrepThreads) void k_knn_assign(const float* __restrict__ xc, int n,
+                                                              const float* __restrict__ pivot_rows,
+                                                              const float* __restrict__ pivot_norms, int P, int C,
                                                               int stride, int* __restrict__ cell) {
   constexpr int kPiv = 32;
   __shared__ float4 piv[kPiv * (MAXP / 4)];
@@ -163,9 +164,9 @@ __global__ __launch_bounds__(kPrepThreads) void k_knn_assign(const float* __rest
     float* const pf = reinterpret_cast<float*>(piv);
     for (int e = tid; e < kPiv * MAXP; e += kPrepThreads) {
       const int j = e / MAXP, c = e % MAXP;
-      pf[e] = (j0 + j < C && c < P) ? xc[static_cast<long long>(j0 + j) * stride * P + c] : 0.0f;
+      pf[e] = (j0 + j < C && c < P) ? pivot_rows[static_cast<long long>(j0 + j) * stride * P + c] : 0.0f;
     }
-    if (tid < kPiv) pn[tid] = j0 + tid < C ? nrm[static_cast<long long>(j0 + tid) * stride] : INFINITY;
+    if (tid < kPiv) pn[tid] = j0 + tid < C ? pivot_norms[static_cast<long long>(j0 + tid) * stride] : INFINITY;
     __syncthreads();
     for (int j = 0; j < kPiv; ++j) {
       float dot = 0.0f;
@@ -226,6 +227,21 @@ __global__ __launch_bounds__(kPrepThreads) void k_knn_cell_scatter(const int* __
   const int i = atomicAdd(&cursor[c], 1);
   perm[pad_off[c] + i] = r;
   qpos[real_off[c] + i] = pad_off[c] + i;
+}
+
+// Queries of a query set in cell order (order[i] = query id), and each
+// query's home tile: the first tile of its cell among the references.
+__global__ __launch_bounds__(kPrepThreads) void k_knn_query_scatter(const int* __restrict__ cell, int n,
+                                                                     int* __restrict__ cursor,
+                                                                     const int* __restrict__ real_off,
+                                                                     const int* __restrict__ ref_pad_off,
+                                                                     int* __restrict__ order,
+                                                                     int* __restrict__ home) {
+  const int q = static_cast<int>(blockIdx.x) * kPrepThreads + threadIdx.x;
+  if (q >= n) return;
+  const int c = cell[q];
+  order[real_off[c] + atomicAdd(&cursor[c], 1)] = q;
+  home[q] = ref_pad_off[c] / kKnnRefTile;
 }
 
 // Rows of xc and their norms in scan order; padding positions (perm -1) get
@@ -571,9 +587,10 @@ struct TileGroups {
 
 template <int B, int MAXM>
 __global__ __launch_bounds__(kKnnThreads, knn_scan_blocks_per_cu<MAXM>()) void k_knn_scan(
-    const float* __restrict__ xc, const float* __restrict__ nrm, TileGroups tg, const int* __restrict__ qlist,
-    int q_offset, int nq, int n, int P, int chunks, int kp, float eps_lb, uint2* __restrict__ buf,
-    float* __restrict__ thr_out, int* __restrict__ cnt_out, unsigned long long* __restrict__ work) {
+    const float* __restrict__ xc, const float* __restrict__ nrm, TileGroups tg, const float* __restrict__ xq,
+    const float* __restrict__ nrm_q, const int* __restrict__ home, const int* __restrict__ qlist, int q_offset, int nq,
+    int n, int P, int chunks, int kp, float eps_lb, uint2* __restrict__ buf, float* __restrict__ thr_out,
+    int* __restrict__ cnt_out, unsigned long long* __restrict__ work) {
   const int pairs = (P + 7) / 8;
   const int aux_at = knn_lds_aux(P);
   extern __shared__ float smem[];
@@ -593,19 +610,21 @@ __global__ __launch_bounds__(kKnnThreads, knn_scan_blocks_per_cu<MAXM>()) void k
   const int q_lane = p_lane < nq ? query_id(qlist, q_offset, p_lane) : -1;
   for (int r = 0; r < kKnnWaveQueries; ++r) {
     const int q = __shfl(q_lane, r);
-    const float2* const src = reinterpret_cast<const float2*>(xc + static_cast<long long>(q >= 0 ? q : 0) * P);
+    const float2* const src = reinterpret_cast<const float2*>(xq + static_cast<long long>(q >= 0 ? q : 0) * P);
     float2* const dst = reinterpret_cast<float2*>(qa + (wave * kKnnWaveQueries + r) * P);
     for (int e = lane; e < P / 2; e += kWave) dst[e] = q >= 0 ? src[e] : make_float2(0.0f, 0.0f);
   }
   if (lane < kKnnWaveQueries) {
     rs.thr[wave][lane] = q_lane >= 0 ? INFINITY : -INFINITY;  // -inf: no row, accepts nothing
     rs.cnt[wave][lane] = 0;
-    rs.nq[wave][lane] = q_lane >= 0 ? nrm[q_lane] : 0.0f;
+    rs.nq[wave][lane] = q_lane >= 0 ? nrm_q[q_lane] : 0.0f;
   }
 
   // Groups of 64 tiles are visited from the group holding the block's first
-  // query (rows are in locality order, so the nearest references come first
-  // and the thresholds settle early), wrapping around.  Per group: stage its
+  // query's home tile (its own position among the references, or the first
+  // tile of its cell for a separate query set: rows are in locality order, so
+  // the nearest references come first and the thresholds settle early),
+  // wrapping around.  Per group: stage its
   // tile centres, and find per wave the tiles that can hold a candidate of
   // one of its queries: a reference r of a tile with centre c and radius rad
   // has |q - r| >= |q - c| - rad, and only tiles whose bound is below
@@ -615,7 +634,8 @@ __global__ __launch_bounds__(kKnnThreads, knn_scan_blocks_per_cu<MAXM>()) void k
   // (tile or group centres) is loaded into registers while one is used.
   const int tiles = (n + kKnnRefTile - 1) / kKnnRefTile;
   const int groups = (tiles + kKnnRefTile - 1) / kKnnRefTile;
-  const int t0 = __builtin_amdgcn_readfirstlane(query_id(qlist, q_offset, p0) / kKnnRefTile);
+  const int q_first = query_id(qlist, q_offset, p0);
+  const int t0 = __builtin_amdgcn_readfirstlane(home != nullptr ? home[q_first] : q_first / kKnnRefTile);
   const int g0 = t0 / kKnnRefTile;
   const float* const qrow = qa + (wave * kKnnWaveQueries + c32) * P + 2 * h;
   uint2* const wave_buf = buf + static_cast<long long>(p0 + wave * kKnnWaveQueries) * B;
@@ -767,23 +787,25 @@ __global__ __launch_bounds__(kKnnThreads, knn_scan_blocks_per_cu<MAXM>()) void k
 // One wave per query: exact squared distances of the candidates from the
 // input rows (fp64); the query itself is dropped when exclude_self; the rest
 // are sorted by (d2, index) and the first k written as 1-based indices and
-// float distances, column-major (neighbour j of point i at j * n + i).
-// Queries and candidates are positions in the scan's row order; perm maps
-// them to input rows.  Uncertified queries (positions) are appended to retry.
+// float distances, column-major (neighbour j of query i at j * n_out + i).
+// Queries are ids in the scan's query set (qperm maps them to query input
+// rows, identity when null); candidates are reference positions in scan
+// order (rperm maps them to reference input rows).  Uncertified queries are
+// appended to retry.
 template <int B>
 __global__ __launch_bounds__(kKnnThreads) void k_knn_finalize(
-    const float* __restrict__ x, int n, int d, Strides st, const int* __restrict__ perm,
-    const int* __restrict__ qlist, int q_offset, int nq, const uint2* __restrict__ buf,
-    const float* __restrict__ thr_in, const int* __restrict__ cnt_in, const float* __restrict__ nrm,
-    const unsigned int* __restrict__ nrm_max_bits, float eps_unit, int k, int exclude_self,
-    int* __restrict__ idx_out, float* __restrict__ dist_out, int* __restrict__ retry, int* __restrict__ retry_count,
-    int* __restrict__ short_rows) {
+    const float* __restrict__ xq_in, Strides stq, const float* __restrict__ xr_in, Strides str, int n_out, int d,
+    const int* __restrict__ qperm, const int* __restrict__ rperm, const int* __restrict__ qlist, int q_offset,
+    int nq, const uint2* __restrict__ buf, const float* __restrict__ thr_in, const int* __restrict__ cnt_in,
+    const float* __restrict__ nrm_q, const unsigned int* __restrict__ nrm_max_bits, float eps_unit, int k,
+    int exclude_self, int* __restrict__ idx_out, float* __restrict__ dist_out, int* __restrict__ retry,
+    int* __restrict__ retry_count, int* __restrict__ short_rows) {
   constexpr int PER = B / kWave;
   const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
   const int p = static_cast<int>(blockIdx.x) * kKnnWaves + static_cast<int>(threadIdx.x) / kWave;
   if (p >= nq) return;  // whole wave
-  const int qpos = query_id(qlist, q_offset, p);
-  const int q = perm[qpos];
+  const int qid = query_id(qlist, q_offset, p);
+  const int q = qperm != nullptr ? qperm[qid] : qid;
   const int c = cnt_in[p];
   const uint2* cand = buf + static_cast<long long>(p) * B;
   double dd[PER];
@@ -795,13 +817,13 @@ __global__ __launch_bounds__(kKnnThreads) void k_knn_finalize(
     dd[j] = INFINITY;
     id[j] = 0x7fffffff;
     if (e < c) {
-      const int r = perm[cand[e].y];
+      const int r = rperm[cand[e].y];
       if (exclude_self && r == q) {
         self_here = true;  // sorts last
       } else {
         double s = 0.0;
         for (int t = 0; t < d; ++t) {
-          const double diff = static_cast<double>(x[st.at(q, t)]) - static_cast<double>(x[st.at(r, t)]);
+          const double diff = static_cast<double>(xq_in[stq.at(q, t)]) - static_cast<double>(xr_in[str.at(r, t)]);
           s = fma(diff, diff, s);
         }
         dd[j] = s;
@@ -816,8 +838,8 @@ __global__ __launch_bounds__(kKnnThreads) void k_knn_finalize(
   for (int j = 0; j < PER; ++j) {
     const int e = j * kWave + lane;
     if (e < k && e < valid) {
-      idx_out[static_cast<long long>(e) * n + q] = id[j] + 1;
-      dist_out[static_cast<long long>(e) * n + q] = static_cast<float>(sqrt(dd[j]));
+      idx_out[static_cast<long long>(e) * n_out + q] = id[j] + 1;
+      dist_out[static_cast<long long>(e) * n_out + q] = static_cast<float>(sqrt(dd[j]));
     }
     if (j == (k - 1) / kWave) d2k = dd[j];
   }
@@ -828,10 +850,10 @@ __global__ __launch_bounds__(kKnnThreads) void k_knn_finalize(
     } else {
       const float thr = thr_in[p];
       if (thr < INFINITY) {
-        const double nq_d = static_cast<double>(nrm[qpos]);
+        const double nq_d = static_cast<double>(nrm_q[qid]);
         const double eps = static_cast<double>(eps_unit) *
                            (nq_d + static_cast<double>(__uint_as_float(*nrm_max_bits)));
-        if (!(static_cast<double>(thr) + nq_d - eps > d2k)) retry[atomicAdd(retry_count, 1)] = qpos;
+        if (!(static_cast<double>(thr) + nq_d - eps > d2k)) retry[atomicAdd(retry_count, 1)] = qid;
       }
     }
   }
@@ -839,22 +861,28 @@ __global__ __launch_bounds__(kKnnThreads) void k_knn_finalize(
 
 // Everything one scan + finalize pass over a list of queries needs.
 struct KnnPass {
-  const float* x;  // input rows (strides st)
-  Strides st;
-  const int* perm;   // scan position -> input row
-  const float* xc;   // centred rows in scan order, pitch P, padded to whole tiles
-  const float* nrm;  // their squared norms
-  TileGroups tg;     // bounding spheres of their 64-row tiles
+  const float* xq_in;  // query input rows (strides stq)
+  Strides stq;
+  const float* xr_in;  // reference input rows (strides str)
+  Strides str;
+  const int* qperm;    // query id -> query input row (null: identity)
+  const int* rperm;    // reference scan position -> reference input row
+  const float* xr;     // centred references in scan order, pitch P, cells padded to whole tiles
+  const float* nrm_r;  // their squared norms (+inf on padding)
+  TileGroups tg;       // bounding spheres of their 64-row tiles
+  const float* xq;     // centred queries by query id, pitch P
+  const float* nrm_q;  // their squared norms
+  const int* home;     // query id -> home tile (null: id / 64, the query is a reference position)
   const unsigned int* nrm_max_bits;
-  int n;       // rows of the input (and of the output's columns)
-  int n_scan;  // scan positions (cells padded to whole tiles)
+  int n_out;   // rows of the output (queries)
+  int n_scan;  // reference scan positions
   int d, P, chunks, k, exclude_self;
   uint2* buf;  // candidate buffers, nq x B
   float* thr;
   int* cnt;
   int* idx_out;
   float* dist_out;
-  int* retry;        // uncertified queries (scan positions)
+  int* retry;        // uncertified query ids
   int* retry_count;  // counters[0]
   int* short_rows;   // counters[1]
   unsigned long long* work;  // [0] tiles staged (per block), [1] tiles computed (per wave)
@@ -868,8 +896,9 @@ hipError_t launch_scan(const KnnPass& a, int kp, const int* qlist, int q_offset,
   if (e != hipSuccess) return e;
   const int blocks = (nq + kKnnQueryBlock - 1) / kKnnQueryBlock;
   const float eps_lb = static_cast<float>(4 * a.chunks + 8) * 0x1.0p-23f;
-  k_knn_scan<B, MAXM><<<blocks, kKnnThreads, lds, stream>>>(a.xc, a.nrm, a.tg, qlist, q_offset, nq, a.n_scan, a.P,
-                                                            a.chunks, kp, eps_lb, a.buf, a.thr, a.cnt, a.work);
+  k_knn_scan<B, MAXM><<<blocks, kKnnThreads, lds, stream>>>(a.xr, a.nrm_r, a.tg, a.xq, a.nrm_q, a.home, qlist,
+                                                            q_offset, nq, a.n_scan, a.P, a.chunks, kp, eps_lb, a.buf,
+                                                            a.thr, a.cnt, a.work);
   return hipGetLastError();
 }
 
@@ -882,8 +911,9 @@ hipError_t launch_scan_finalize(const KnnPass& a, int kp, const int* qlist, int 
   if (e != hipSuccess) return e;
   const float eps_unit = static_cast<float>(4 * a.chunks + 12) * 0x1.0p-23f;
   k_knn_finalize<B><<<(nq + kKnnWaves - 1) / kKnnWaves, kKnnThreads, 0, stream>>>(
-      a.x, a.n, a.d, a.st, a.perm, qlist, q_offset, nq, a.buf, a.thr, a.cnt, a.nrm, a.nrm_max_bits, eps_unit, a.k,
-      a.exclude_self, a.idx_out, a.dist_out, a.retry, a.retry_count, a.short_rows);
+      a.xq_in, a.stq, a.xr_in, a.str, a.n_out, a.d, a.qperm, a.rperm, qlist, q_offset, nq, a.buf, a.thr, a.cnt,
+      a.nrm_q, a.nrm_max_bits, eps_unit, a.k, a.exclude_self, a.idx_out, a.dist_out, a.retry, a.retry_count,
+      a.short_rows);
   return hipGetLastError();
 }
 
@@ -926,60 +956,53 @@ struct DevBuf {
   }
 };
 
-}  // namespace
+// A matrix handed to the KNN entry points.
+struct KnnSet {
+  const float* x;
+  int n;
+  int col_major;
+  int on_device;
+};
 
-int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int exclude_self, int input_on_device,
-                  int* idx_out_in, float* dist_out_in, int output_on_device, long long* stats, std::string& err) {
+// The whole search: references `ref`, queries `query` (null: the references
+// themselves, self excluded on request).
+int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_self, int* idx_out_in,
+            float* dist_out_in, int output_on_device, long long* stats, std::string& err) {
   auto fail = [&](const std::string& what, hipError_t e) {
     err = what + ": " + hipGetErrorString(e);
     return 1;
   };
-  if (x_in == nullptr || idx_out_in == nullptr || dist_out_in == nullptr) {
-    err = "null KNN pointer";
-    return 1;
-  }
-  if (n < 2 || d < 1 || k < 1) {
-    err = "invalid KNN dimensions (need n >= 2, d >= 1, k >= 1)";
-    return 1;
-  }
-  if (d > kKnnMaxDim) {
-    err = "exact KNN supports up to " + std::to_string(kKnnMaxDim) + " dimensions";
-    return 1;
-  }
-  if (k > kKnnMaxK) {
-    err = "exact KNN supports k up to " + std::to_string(kKnnMaxK);
-    return 1;
-  }
-  if (k > n - (exclude_self ? 1 : 0)) {
-    err = "k exceeds the number of " + std::string(exclude_self ? "non-self " : "") + "neighbors";
-    return 1;
-  }
-  if (n > INT_MAX - (1 << 17)) {
-    err = "exact KNN supports fewer than 2^31 - 2^17 rows";
-    return 1;
-  }
+  const bool self = query == nullptr;
+  const int n = ref.n;
+  const int n_out = self ? n : query->n;
   const int P = knn_pitch(d);
   const int chunks = (d + 3) / 4;
   const int n_pad = (n + kKnnRefTile - 1) / kKnnRefTile * kKnnRefTile;  // whole reference tiles
   hipStream_t stream = nullptr;
   hipError_t e;
-  DevBuf<float> x_dev, xc, nrm, dist_dev;
+  DevBuf<float> xr_dev, xq_dev, xc, nrm, xcq, nrmq, dist_dev;
   DevBuf<double> partial, mean;
   DevBuf<unsigned int> nrm_max;
   DevBuf<int> idx_dev, retry, counters;
-  const float* x = x_in;
-  if (!input_on_device) {
-    if ((e = x_dev.alloc(static_cast<std::size_t>(n) * d)) != hipSuccess) return fail("hipMalloc(KNN input)", e);
-    if ((e = hipMemcpy(x_dev.p, x_in, static_cast<std::size_t>(n) * d * sizeof(float), hipMemcpyHostToDevice)) !=
-        hipSuccess)
-      return fail("hipMemcpy(KNN input)", e);
-    x = x_dev.p;
-  }
+  auto upload = [&](const KnnSet& set, DevBuf<float>& dev, const float*& out) -> hipError_t {
+    out = set.x;
+    if (set.on_device) return hipSuccess;
+    const std::size_t bytes = static_cast<std::size_t>(set.n) * d * sizeof(float);
+    hipError_t r = dev.alloc(static_cast<std::size_t>(set.n) * d);
+    if (r == hipSuccess) r = hipMemcpy(dev.p, set.x, bytes, hipMemcpyHostToDevice);
+    out = dev.p;
+    return r;
+  };
+  const float* xr = nullptr;
+  const float* xq = nullptr;
+  if ((e = upload(ref, xr_dev, xr)) != hipSuccess) return fail("KNN reference upload", e);
+  if (!self && (e = upload(*query, xq_dev, xq)) != hipSuccess) return fail("KNN query upload", e);
   int* idx_out = idx_out_in;
   float* dist_out = dist_out_in;
   if (!output_on_device) {
-    if ((e = idx_dev.alloc(static_cast<std::size_t>(n) * k)) != hipSuccess) return fail("hipMalloc(KNN indices)", e);
-    if ((e = dist_dev.alloc(static_cast<std::size_t>(n) * k)) != hipSuccess)
+    if ((e = idx_dev.alloc(static_cast<std::size_t>(n_out) * k)) != hipSuccess)
+      return fail("hipMalloc(KNN indices)", e);
+    if ((e = dist_dev.alloc(static_cast<std::size_t>(n_out) * k)) != hipSuccess)
       return fail("hipMalloc(KNN distances)", e);
     idx_out = idx_dev.p;
     dist_out = dist_dev.p;
@@ -989,21 +1012,33 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
   if ((e = xc.alloc(static_cast<std::size_t>(n_pad) * P + kKnnOverRead)) != hipSuccess ||
       (e = nrm.alloc(n_pad)) != hipSuccess ||
       (e = partial.alloc(static_cast<std::size_t>(pblocks) * d)) != hipSuccess || (e = mean.alloc(d)) != hipSuccess ||
-      (e = nrm_max.alloc(1)) != hipSuccess || (e = retry.alloc(n)) != hipSuccess ||
+      (e = nrm_max.alloc(2)) != hipSuccess || (e = retry.alloc(n_out)) != hipSuccess ||
       (e = counters.alloc(3)) != hipSuccess)
     return fail("hipMalloc(KNN scratch)", e);
+  if (!self && ((e = xcq.alloc(static_cast<std::size_t>(n_out) * P + kKnnOverRead)) != hipSuccess ||
+                (e = nrmq.alloc(n_out)) != hipSuccess))
+    return fail("hipMalloc(KNN query scratch)", e);
   // counters: [0] uncertified rows, [1] rows with fewer than k candidates,
-  // [2] rows with non-finite values
+  // [2] rows with non-finite values; nrm_max: [0] references, [1] queries
   if ((e = hipMemsetAsync(counters.p, 0, 3 * sizeof(int), stream)) != hipSuccess ||
-      (e = hipMemsetAsync(nrm_max.p, 0, sizeof(unsigned int), stream)) != hipSuccess ||
+      (e = hipMemsetAsync(nrm_max.p, 0, 2 * sizeof(unsigned int), stream)) != hipSuccess ||
       (e = hipMemsetAsync(xc.p + static_cast<std::size_t>(n_pad) * P, 0, kKnnOverRead * sizeof(float), stream)) !=
           hipSuccess)
     return fail("hipMemset", e);
-  const Strides st = x_col_major ? Strides{1, n} : Strides{d, 1};
-  k_knn_col_partials<<<pblocks, kPrepThreads, 0, stream>>>(x, n, d, st, rows_per, partial.p);
+  const Strides str = ref.col_major ? Strides{1, n} : Strides{d, 1};
+  const Strides stq = self ? str : (query->col_major ? Strides{1, n_out} : Strides{d, 1});
+  // both sets are centred on the references' column means
+  k_knn_col_partials<<<pblocks, kPrepThreads, 0, stream>>>(xr, n, d, str, rows_per, partial.p);
   k_knn_col_means<<<1, kPrepThreads, 0, stream>>>(partial.p, pblocks, d, n, mean.p);
   k_knn_center<<<(n_pad + kPrepThreads - 1) / kPrepThreads, kPrepThreads, 0, stream>>>(
-      x, n, n_pad, d, st, P, mean.p, xc.p, nrm.p, nrm_max.p, counters.p + 2);
+      xr, n, n_pad, d, str, P, mean.p, xc.p, nrm.p, nrm_max.p, counters.p + 2);
+  if (!self) {
+    if ((e = hipMemsetAsync(xcq.p + static_cast<std::size_t>(n_out) * P, 0, kKnnOverRead * sizeof(float), stream)) !=
+        hipSuccess)
+      return fail("hipMemset", e);
+    k_knn_center<<<(n_out + kPrepThreads - 1) / kPrepThreads, kPrepThreads, 0, stream>>>(
+        xq, n_out, n_out, d, stq, P, mean.p, xcq.p, nrmq.p, nrm_max.p + 1, counters.p + 2);
+  }
   if ((e = hipGetLastError()) != hipSuccess) return fail("KNN prep launch", e);
   {
     int bad = 0;
@@ -1017,12 +1052,13 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
     }
   }
 
-  // Locality order: each row goes to the cell of its nearest pivot; cells
-  // are laid out one after another, each padded to whole 64-row tiles.
+  // Locality order: each reference goes to the cell of its nearest pivot;
+  // cells are laid out one after another, each padded to whole 64-row tiles.
+  // Separate queries are ordered by the same cells.
   const int C = std::max(1, std::min(1024, n / 256));
   const int stride = n / C;
   const int scan_max = n_pad + C * kKnnRefTile;  // bound on the scan positions
-  DevBuf<int> cell, cursor, pad_off, real_off, perm, qpos;
+  DevBuf<int> cell, cursor, pad_off, real_off, perm, qpos, qcell, qreal_off, qpad_off, qorder, qhome;
   DevBuf<float> xs, ns;
   if ((e = cell.alloc(n)) != hipSuccess || (e = cursor.alloc(C)) != hipSuccess ||
       (e = pad_off.alloc(C + 1)) != hipSuccess || (e = real_off.alloc(C)) != hipSuccess ||
@@ -1030,6 +1066,10 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
       (e = xs.alloc(static_cast<std::size_t>(scan_max) * P + kKnnOverRead)) != hipSuccess ||
       (e = ns.alloc(scan_max)) != hipSuccess)
     return fail("hipMalloc(KNN order)", e);
+  if (!self && ((e = qcell.alloc(n_out)) != hipSuccess || (e = qreal_off.alloc(C)) != hipSuccess ||
+                (e = qpad_off.alloc(C + 1)) != hipSuccess || (e = qorder.alloc(n_out)) != hipSuccess ||
+                (e = qhome.alloc(n_out)) != hipSuccess))
+    return fail("hipMalloc(KNN query order)", e);
   int n_scan = 0;
   {
     const int rb = (n + kPrepThreads - 1) / kPrepThreads;
@@ -1037,15 +1077,30 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
         (e = hipMemsetAsync(perm.p, 0xff, scan_max * sizeof(int), stream)) != hipSuccess)
       return fail("hipMemset", e);
     if (P <= 68)
-      k_knn_assign<68><<<rb, kPrepThreads, 0, stream>>>(xc.p, nrm.p, n, P, C, stride, cell.p);
+      k_knn_assign<68><<<rb, kPrepThreads, 0, stream>>>(xc.p, n, xc.p, nrm.p, P, C, stride, cell.p);
     else
-      k_knn_assign<132><<<rb, kPrepThreads, 0, stream>>>(xc.p, nrm.p, n, P, C, stride, cell.p);
+      k_knn_assign<132><<<rb, kPrepThreads, 0, stream>>>(xc.p, n, xc.p, nrm.p, P, C, stride, cell.p);
     k_knn_cell_count<<<rb, kPrepThreads, 0, stream>>>(cell.p, n, cursor.p);
     k_knn_cell_offsets<<<1, 64, 0, stream>>>(cursor.p, C, pad_off.p, real_off.p);
-    if ((e = hipGetLastError()) != hipSuccess || (e = hipMemsetAsync(cursor.p, 0, C * sizeof(int), stream)) !=
-                                                     hipSuccess)
+    if ((e = hipGetLastError()) != hipSuccess ||
+        (e = hipMemsetAsync(cursor.p, 0, C * sizeof(int), stream)) != hipSuccess)
       return fail("KNN order launch", e);
     k_knn_cell_scatter<<<rb, kPrepThreads, 0, stream>>>(cell.p, n, cursor.p, pad_off.p, real_off.p, perm.p, qpos.p);
+    if (!self) {
+      const int qb = (n_out + kPrepThreads - 1) / kPrepThreads;
+      if ((e = hipMemsetAsync(cursor.p, 0, C * sizeof(int), stream)) != hipSuccess) return fail("hipMemset", e);
+      if (P <= 68)
+        k_knn_assign<68><<<qb, kPrepThreads, 0, stream>>>(xcq.p, n_out, xc.p, nrm.p, P, C, stride, qcell.p);
+      else
+        k_knn_assign<132><<<qb, kPrepThreads, 0, stream>>>(xcq.p, n_out, xc.p, nrm.p, P, C, stride, qcell.p);
+      k_knn_cell_count<<<qb, kPrepThreads, 0, stream>>>(qcell.p, n_out, cursor.p);
+      k_knn_cell_offsets<<<1, 64, 0, stream>>>(cursor.p, C, qpad_off.p, qreal_off.p);
+      if ((e = hipGetLastError()) != hipSuccess ||
+          (e = hipMemsetAsync(cursor.p, 0, C * sizeof(int), stream)) != hipSuccess)
+        return fail("KNN query order launch", e);
+      k_knn_query_scatter<<<qb, kPrepThreads, 0, stream>>>(qcell.p, n_out, cursor.p, qreal_off.p, pad_off.p,
+                                                            qorder.p, qhome.p);
+    }
     if ((e = hipMemcpyAsync(&n_scan, pad_off.p + C, sizeof(int), hipMemcpyDeviceToHost, stream)) != hipSuccess ||
         (e = hipStreamSynchronize(stream)) != hipSuccess)
       return fail("KNN order", e);
@@ -1078,27 +1133,56 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
   // kKnnCandEntries in all; a pass launches as many queries at once as they
   // allow (one launch for the whole input up to millions of rows, so that
   // the grid is many rounds of workgroups deep).
-  int kp = std::min(kKnnMaxCand, k + std::max(32, k / 2) + 1);
-  const std::size_t entries =
-      std::min<std::size_t>(kKnnCandEntries, static_cast<std::size_t>(n) * static_cast<std::size_t>(buffer_for(kp)));
+  int kp = std::min(kKnnMaxCand, k + std::max(32, k / 2) + (self ? 1 : 0));
+  const std::size_t entries = std::min<std::size_t>(
+      kKnnCandEntries, static_cast<std::size_t>(n_out) * static_cast<std::size_t>(buffer_for(kp)));
   auto batch_for = [&](int kp_) {
-    return static_cast<int>(std::min<std::size_t>(static_cast<std::size_t>(n), entries / buffer_for(kp_)));
+    return static_cast<int>(std::min<std::size_t>(static_cast<std::size_t>(n_out), entries / buffer_for(kp_)));
   };
   DevBuf<uint2> buf;
   DevBuf<float> thr;
   DevBuf<int> cnt;
-  if ((e = buf.alloc(entries)) != hipSuccess || (e = thr.alloc(n)) != hipSuccess || (e = cnt.alloc(n)) != hipSuccess)
+  if ((e = buf.alloc(entries)) != hipSuccess || (e = thr.alloc(n_out)) != hipSuccess ||
+      (e = cnt.alloc(n_out)) != hipSuccess)
     return fail("hipMalloc(KNN candidates)", e);
   DevBuf<unsigned long long> work;
   if ((e = work.alloc(2)) != hipSuccess) return fail("hipMalloc(KNN work)", e);
   if ((e = hipMemsetAsync(work.p, 0, 2 * sizeof(unsigned long long), stream)) != hipSuccess)
     return fail("hipMemset", e);
-  KnnPass pass{x,       st,     perm.p, xs.p,   ns.p,  TileGroups{tcentre.p, tcnorm.p, tradius.p}, nrm_max.p,
-               n,       n_scan, d,      P,      chunks, k,  exclude_self, buf.p, thr.p, cnt.p, idx_out, dist_out,
-               retry.p, counters.p, counters.p + 1, work.p};
-  for (int q0 = 0, batch = batch_for(kp); q0 < n; q0 += batch) {
-    const int nq = std::min(batch, n - q0);
-    if ((e = launch_pass(pass, kp, qpos.p + q0, 0, nq, stream)) != hipSuccess) return fail("KNN scan launch", e);
+  KnnPass pass{};
+  pass.xq_in = self ? xr : xq;
+  pass.stq = stq;
+  pass.xr_in = xr;
+  pass.str = str;
+  pass.qperm = self ? perm.p : nullptr;
+  pass.rperm = perm.p;
+  pass.xr = xs.p;
+  pass.nrm_r = ns.p;
+  pass.tg = TileGroups{tcentre.p, tcnorm.p, tradius.p};
+  pass.xq = self ? xs.p : xcq.p;
+  pass.nrm_q = self ? ns.p : nrmq.p;
+  pass.home = self ? nullptr : qhome.p;
+  pass.nrm_max_bits = nrm_max.p;
+  pass.n_out = n_out;
+  pass.n_scan = n_scan;
+  pass.d = d;
+  pass.P = P;
+  pass.chunks = chunks;
+  pass.k = k;
+  pass.exclude_self = self ? exclude_self : 0;
+  pass.buf = buf.p;
+  pass.thr = thr.p;
+  pass.cnt = cnt.p;
+  pass.idx_out = idx_out;
+  pass.dist_out = dist_out;
+  pass.retry = retry.p;
+  pass.retry_count = counters.p;
+  pass.short_rows = counters.p + 1;
+  pass.work = work.p;
+  const int* main_list = self ? qpos.p : qorder.p;
+  for (int q0 = 0, batch = batch_for(kp); q0 < n_out; q0 += batch) {
+    const int nq = std::min(batch, n_out - q0);
+    if ((e = launch_pass(pass, kp, main_list + q0, 0, nq, stream)) != hipSuccess) return fail("KNN scan launch", e);
   }
   int host_counts[2] = {0, 0};
   long long retried = 0;
@@ -1135,9 +1219,9 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
     if ((e = hipStreamSynchronize(stream)) != hipSuccess) return fail("KNN retry", e);
   }
   if (!output_on_device) {
-    if ((e = hipMemcpy(idx_out_in, idx_out, static_cast<std::size_t>(n) * k * sizeof(int),
+    if ((e = hipMemcpy(idx_out_in, idx_out, static_cast<std::size_t>(n_out) * k * sizeof(int),
                        hipMemcpyDeviceToHost)) != hipSuccess ||
-        (e = hipMemcpy(dist_out_in, dist_out, static_cast<std::size_t>(n) * k * sizeof(float),
+        (e = hipMemcpy(dist_out_in, dist_out, static_cast<std::size_t>(n_out) * k * sizeof(float),
                        hipMemcpyDeviceToHost)) != hipSuccess)
       return fail("hipMemcpy(KNN output)", e);
   } else if ((e = hipStreamSynchronize(stream)) != hipSuccess) {
@@ -1153,6 +1237,68 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
     stats[4] = static_cast<long long>(w[1]);
   }
   return 0;
+}
+
+bool knn_common_checks(const float* x, int n, int d, int k, const void* idx, const void* dist, std::string& err) {
+  if (x == nullptr || idx == nullptr || dist == nullptr) {
+    err = "null KNN pointer";
+    return false;
+  }
+  if (n < 1 || d < 1 || k < 1) {
+    err = "invalid KNN dimensions (need n >= 1, d >= 1, k >= 1)";
+    return false;
+  }
+  if (d > kKnnMaxDim) {
+    err = "exact KNN supports up to " + std::to_string(kKnnMaxDim) + " dimensions";
+    return false;
+  }
+  if (k > kKnnMaxK) {
+    err = "exact KNN supports k up to " + std::to_string(kKnnMaxK);
+    return false;
+  }
+  if (n > INT_MAX - (1 << 17)) {
+    err = "exact KNN supports fewer than 2^31 - 2^17 rows";
+    return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int exclude_self, int input_on_device,
+                  int* idx_out_in, float* dist_out_in, int output_on_device, long long* stats, std::string& err) {
+  if (!knn_common_checks(x_in, n, d, k, idx_out_in, dist_out_in, err)) return 1;
+  if (n < 2) {
+    err = "invalid KNN dimensions (need n >= 2, d >= 1, k >= 1)";
+    return 1;
+  }
+  if (k > n - (exclude_self ? 1 : 0)) {
+    err = "k exceeds the number of " + std::string(exclude_self ? "non-self " : "") + "neighbors";
+    return 1;
+  }
+  const KnnSet ref{x_in, n, x_col_major, input_on_device};
+  return knn_run(ref, nullptr, d, k, exclude_self, idx_out_in, dist_out_in, output_on_device, stats, err);
+}
+
+int knn_query_run(const float* ref_in, int n_ref, const float* query_in, int n_query, int d, int col_major, int k,
+                  int input_on_device, int* idx_out, float* dist_out, int output_on_device, long long* stats,
+                  std::string& err) {
+  if (!knn_common_checks(ref_in, n_ref, d, k, idx_out, dist_out, err)) return 1;
+  if (query_in == nullptr) {
+    err = "null KNN pointer";
+    return 1;
+  }
+  if (n_query < 1 || n_query > INT_MAX - (1 << 17)) {
+    err = "invalid query count";
+    return 1;
+  }
+  if (k > n_ref) {
+    err = "k exceeds the number of reference rows";
+    return 1;
+  }
+  const KnnSet ref{ref_in, n_ref, col_major, input_on_device};
+  const KnnSet query{query_in, n_query, col_major, input_on_device};
+  return knn_run(ref, &query, d, k, 0, idx_out, dist_out, output_on_device, stats, err);
 }
 
 }  // namespace fehip

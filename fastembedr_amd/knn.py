@@ -55,6 +55,7 @@ class KnnResult:
     result_residency: str = "host"
     index_base: int = 1
     layout: str = "column_major_query_by_k"
+    n_reference: int | None = None  # query-to-reference results: rows of the reference
     stats: dict = field(default_factory=dict)
 
     @property
@@ -142,6 +143,91 @@ def exact_knn(data, k: int, exclude_self: bool = True, keep_device: bool = False
     res.exclude_self = bool(exclude_self)
     res.stats = dict(rerun_rows=int(stats[0]), passes=int(stats[1]), candidates=int(stats[2]),
                      tiles_staged=int(stats[3]), tiles_computed=int(stats[4]))
+    return res
+
+
+def _prepare_pair(reference, query):
+    """Both matrices in one layout and residency: (ref_ptr, n_ref, q_ptr, n_q, d, col_major, on_device, keep)."""
+    if isinstance(reference, DeviceMatrix) or isinstance(query, DeviceMatrix):
+        if not (isinstance(reference, DeviceMatrix) and isinstance(query, DeviceMatrix)):
+            raise ValueError("`reference` and `query` must both be host arrays or both DeviceMatrix objects.")
+        if reference.col_major != query.col_major:
+            raise ValueError("device `reference` and `query` must share one layout.")
+        if reference.d != query.d:
+            raise ValueError("`reference` and `query` must have the same number of columns.")
+        return (reference.address, reference.n, query.address, query.n, reference.d, int(reference.col_major), 1,
+                (reference, query))
+    rp, nr, dr, rcm, _, rkeep = _prepare(reference)
+    qp, nq, dq, qcm, _, qkeep = _prepare(query)
+    if dr != dq:
+        raise ValueError("`reference` and `query` must have the same number of columns.")
+    if rcm != qcm:  # one layout for both: row-major copies
+        rkeep = np.ascontiguousarray(np.asarray(rkeep), dtype=np.float32)
+        qkeep = np.ascontiguousarray(np.asarray(qkeep), dtype=np.float32)
+        rp, qp, rcm = rkeep.ctypes.data, qkeep.ctypes.data, 0
+    return rp, nr, qp, nq, dr, rcm, 0, (rkeep, qkeep)
+
+
+def exact_query_knn(reference, query, k: int, keep_device: bool = False) -> KnnResult:
+    """Exact Euclidean KNN of every row of ``query`` among the rows of
+    ``reference`` (fastembedr_hip_knn_query).  Indices are 1-based rows of
+    ``reference``; the result has one row per query."""
+    rp, nr, qp, nq, d, col_major, on_device, keep = _prepare_pair(reference, query)
+    k = int(k)
+    lib = _lib.load()
+    if not lib.fastembedr_hip_available():
+        raise _lib.HipBackendUnavailable(
+            "Native HIP KNN was requested, but no gfx950 device is visible. No CPU fallback is used.")
+    stats = (C.c_longlong * 5)()
+    t0 = time.perf_counter()
+    if keep_device:
+        if not 1 <= k <= MAX_K:
+            raise _lib.HipBackendError(f"HIP exact query KNN failed: exact KNN supports k up to {MAX_K}")
+        dev_idx = DeviceBuffer((k, nq), np.int32)
+        dev_dist = DeviceBuffer((k, nq), np.float32)
+        rc = lib.fastembedr_hip_knn_query(C.c_void_p(rp), nr, C.c_void_p(qp), nq, d, col_major, k, on_device,
+                                          C.c_void_p(dev_idx.address), C.c_void_p(dev_dist.address), 1, stats)
+        _lib.check(rc, "HIP exact query KNN")
+        res = KnnResult(nq, k, device_indices=dev_idx, device_distances=dev_dist, result_residency="hip")
+    else:
+        idx = np.empty((max(k, 0), nq), np.int32)
+        dist = np.empty((max(k, 0), nq), np.float32)
+        rc = lib.fastembedr_hip_knn_query(C.c_void_p(rp), nr, C.c_void_p(qp), nq, d, col_major, k, on_device,
+                                          C.c_void_p(idx.ctypes.data), C.c_void_p(dist.ctypes.data), 0, stats)
+        _lib.check(rc, "HIP exact query KNN")
+        res = KnnResult(nq, k, indices=idx.T, distances=dist.T)
+    del keep
+    res.elapsed_sec = time.perf_counter() - t0
+    res.exclude_self = False
+    res.stats = dict(rerun_rows=int(stats[0]), passes=int(stats[1]), candidates=int(stats[2]),
+                     tiles_staged=int(stats[3]), tiles_computed=int(stats[4]))
+    return res
+
+
+def precompute_query_knn(reference, query, k: int = 30, metric: str = "euclidean", backend: str = "hip",
+                         n_cores=None, keep_device: bool = False) -> KnnResult:
+    """Nearest reference rows of every query row (R's
+    ``precompute_query_knn()``, R/native_knn.R:333-416): one-based indices
+    into ``reference``, self not excluded.  Only the Euclidean metric and the
+    HIP backend are part of this build."""
+    if str(backend).lower() != "hip":
+        raise ValueError(f'backend "{backend}" is not part of this build; only backend = "hip" is provided. '
+                         "No CPU fallback is used for HIP-labelled runs.")
+    if isinstance(metric, (list, tuple)):
+        metric = metric[0]
+    if str(metric) != "euclidean":
+        raise ValueError(f'metric "{metric}" is not part of this build; only "euclidean" is provided.')
+    n_ref = reference.n if isinstance(reference, DeviceMatrix) else len(reference)
+    try:
+        k_int = int(k)
+        ok = float(k) == k_int
+    except (TypeError, ValueError):
+        ok = False
+    if not ok or k_int < 1 or k_int > n_ref:
+        raise ValueError("`k` must be one integer between 1 and nrow(reference).")
+    res = exact_query_knn(reference, query, k_int, keep_device=keep_device)
+    res.n_reference = n_ref
+    res.backend_requested = "hip"
     return res
 
 

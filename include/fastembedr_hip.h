@@ -278,6 +278,29 @@ FASTEMBEDR_HIP_API int fastembedr_hip_knn_exact(const float* x, int n, int d, in
                                                 int exclude_self, int x_on_device, int* indices, float* distances,
                                                 int output_on_device, long long* stats);
 
+/* Exact query-to-reference k-nearest neighbours by Euclidean distance, the
+ * exact route of the reference's native GPU query KNN
+ * (native_cuda_query_knn_cpp(data, query, k, method = "exact"),
+ * src/native_knn_bridge.cpp:115-124 -> native_cuda_query_knn_impl,
+ * src/native_knn_cuda_impl.cpp:871-; finished by
+ * finalize_cuvs_query_knn_kernel, src/embedding_cuda_kernels.cpp:1466-1503:
+ * column-major n_query x k, 1-based reference indices, sqrt of the squared
+ * distance; the caller, R/native_knn.R:333-416, requires
+ * 1 <= k <= nrow(reference)).
+ *   reference    n_reference x d float32, query n_query x d float32, both
+ *                row-major or both column-major (col_major); both in device
+ *                memory when inputs_on_device
+ *   k            1 .. min(256, n_reference);  d  1 .. 128
+ *   indices      n_query x k column-major, 1-based rows of reference; device
+ *                memory when output_on_device
+ *   distances    same layout
+ * Neighbours are ordered by (distance, index).  stats as for
+ * fastembedr_hip_knn_exact.  Returns 0, or 1 with the last error set. */
+FASTEMBEDR_HIP_API int fastembedr_hip_knn_query(const float* reference, int n_reference, const float* query,
+                                                int n_query, int d, int col_major, int k, int inputs_on_device,
+                                                int* indices, float* distances, int output_on_device,
+                                                long long* stats);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,7 +24,8 @@ first k; rows that fail the bound are ordered from the full direct distances.
 
 Pins (tests/test_knn_oracle.py): scipy's cKDTree on tie-free data, a
 pure-Python brute force (sorted by (d2, index)) on tiny inputs with
-duplicates and lattice ties, and the invariants of the result.
+duplicates and lattice ties, and the invariants of the result; the same for
+the query-to-reference search (exact_query_knn).
 """
 
 from __future__ import annotations
@@ -88,6 +89,51 @@ def exact_knn(x, k: int, exclude_self: bool = True, chunk: int = 512, margin: in
                     if exclude_self:
                         allc = allc[allc != q]
                     full = _direct_d2(xd, q, allc)
+                    order = np.lexsort((allc, full))
+                    cols, exact = allc[order], full[order]
+            idx[q] = cols[:k]
+            dist[q] = np.sqrt(exact[:k])
+    return idx, dist
+
+
+def exact_query_knn(reference, query, k: int, chunk: int = 512, margin: int = 16):
+    """Exact KNN of every row of ``query`` among the rows of ``reference``
+    (the query-to-reference search of tests/testthat/helper-knn.R:5-38 with
+    a separate ``query``): 0-based int64 reference indices and fp64
+    distances, (n_query, k), ascending by (distance, index)."""
+    ref = np.asarray(reference, dtype=np.float64)
+    qry = np.asarray(query, dtype=np.float64)
+    if ref.ndim != 2 or qry.ndim != 2 or ref.shape[1] != qry.shape[1]:
+        raise ValueError("reference and query must be matrices with the same columns")
+    n, d = ref.shape
+    k = int(k)
+    if k < 1 or k > n:
+        raise ValueError("k must be between 1 and the number of reference rows")
+    mu = ref.mean(axis=0)
+    rc, qc = ref - mu, qry - mu
+    sr = np.einsum("ij,ij->i", rc, rc)
+    sq = np.einsum("ij,ij->i", qc, qc)
+    m = min(n, k + margin)
+    eps_unit = 2.0 * (d + 4) * 2.0 ** -52
+    idx = np.empty((qry.shape[0], k), np.int64)
+    dist = np.empty((qry.shape[0], k), np.float64)
+    for s in range(0, qry.shape[0], chunk):
+        e = min(qry.shape[0], s + chunk)
+        d2 = sq[s:e, None] + sr[None, :] - 2.0 * (qc[s:e] @ rc.T)
+        part = np.argpartition(d2, m - 1, axis=1)[:, :m] if m < n else np.broadcast_to(np.arange(n), (e - s, n))
+        for r in range(e - s):
+            q = s + r
+            cols = np.asarray(part[r])
+            diff = ref[cols] - qry[q]
+            exact = np.einsum("ij,ij->i", diff, diff)
+            order = np.lexsort((cols, exact))
+            cols, exact = cols[order], exact[order]
+            if m < n:
+                rest = np.partition(d2[r], m - 1)[m - 1]
+                if not rest - eps_unit * (sq[q] + sr.max()) > exact[k - 1]:
+                    diff = ref - qry[q]
+                    full = np.einsum("ij,ij->i", diff, diff)
+                    allc = np.arange(n)
                     order = np.lexsort((allc, full))
                     cols, exact = allc[order], full[order]
             idx[q] = cols[:k]

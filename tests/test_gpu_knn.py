@@ -201,3 +201,69 @@ def test_large_input_sampled_rows(hip):
         order = np.lexsort((np.arange(x.shape[0]), d2))[:90]
         np.testing.assert_array_equal(res.indices[i] - 1, order)
         np.testing.assert_allclose(res.distances[i], np.sqrt(d2[order]), rtol=DIST_RTOL)
+
+
+# ---- query-to-reference search (fastembedr_hip_knn_query) ----------------------------
+
+
+def _check_query(res, ref, qry, k):
+    ref_i, ref_d = knn_oracle.exact_query_knn(ref, qry, k)
+    got_i = np.asarray(res.indices)
+    assert got_i.shape == (qry.shape[0], k) and got_i.dtype == np.int32
+    bad = np.nonzero((got_i - 1 != ref_i).any(axis=1))[0]
+    assert bad.size == 0, f"{bad.size} rows differ, first {bad[:5]}: {got_i[bad[0]] - 1} vs {ref_i[bad[0]]}"
+    np.testing.assert_allclose(np.asarray(res.distances), ref_d, rtol=DIST_RTOL, atol=1e-30)
+
+
+@pytest.mark.parametrize("n_ref,n_q,d,k", [(3000, 500, 10, 15), (700, 1300, 3, 30), (40, 17, 5, 40),
+                                           (2000, 300, 77, 12)])
+def test_query_matches_oracle(hip, n_ref, n_q, d, k):
+    _say(f"case: query KNN n_ref={n_ref} n_q={n_q} d={d} k={k}")
+    ref = _gauss(n_ref, d, seed=n_ref)
+    qry = _gauss(n_q, d, seed=n_q + 1) * 1.1 + 0.2
+    _check_query(hip.precompute_query_knn(ref, qry, k=k), ref, qry, k)
+
+
+def test_query_layouts_ties_and_device(hip):
+    from fastembedr_amd.device import DeviceMatrix
+
+    _say("case: query KNN column-major, queries on reference rows, device buffers")
+    rng = np.random.default_rng(41)
+    ref = rng.integers(0, 3, size=(1500, 4)).astype(np.float32)  # duplicates and exact ties
+    qry = np.concatenate([ref[:200], rng.integers(0, 3, size=(100, 4)).astype(np.float32)])
+    res = hip.exact_query_knn(ref, qry, 25)
+    _check_query(res, ref, qry, 25)
+    res_cm = hip.exact_query_knn(np.asfortranarray(ref), np.asfortranarray(qry), 25)
+    np.testing.assert_array_equal(res_cm.indices, res.indices)
+    dev = hip.exact_query_knn(DeviceMatrix.from_host(ref), DeviceMatrix.from_host(qry), 25, keep_device=True)
+    back = dev.to_host()
+    np.testing.assert_array_equal(back.indices, res.indices)
+    np.testing.assert_array_equal(back.distances, res.distances)
+
+
+def test_query_config3_shape(hip):
+    """Query-to-reference search at the transform configuration's shape, scaled
+    down (reference 20k x 50 from a 10-component mixture, 5k queries from the
+    same mixture, k = 30)."""
+    from fastembedr_amd import synthetic
+
+    _say("case: query KNN 20k refs x 5k queries x 50 dims, k = 30")
+    spec = synthetic.MixtureSpec(n=25_000, dim=50, components=10, mean_sd=4.0)
+    x, _ = synthetic.gaussian_mixture(spec, seed=12)
+    x = x.astype(np.float32)
+    ref, qry = x[:20_000], x[20_000:]
+    res = hip.exact_query_knn(ref, qry, 30)
+    _say(f"  elapsed {res.elapsed_sec:.3f} s, stats {res.stats}")
+    _check_query(res, ref, qry, 30)
+
+
+def test_query_errors(hip):
+    _say("case: query KNN argument errors")
+    ref = _gauss(20, 4, seed=1)
+    with pytest.raises(ValueError, match="between 1 and nrow"):
+        hip.precompute_query_knn(ref, ref[:3], k=21)
+    with pytest.raises(ValueError, match="same number of columns"):
+        hip.exact_query_knn(ref, _gauss(5, 3, seed=2), 3)
+    with pytest.raises(_lib.HipBackendError, match="k exceeds"):
+        hip.exact_query_knn(ref, ref[:3], 21)
+    _check_query(hip.exact_query_knn(ref, ref[:3], 20), ref, ref[:3], 20)

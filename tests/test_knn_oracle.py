@@ -95,3 +95,22 @@ def test_rejects_bad_k():
         knn_oracle.exact_knn(x, 4, exclude_self=True)
     with pytest.raises(ValueError):
         knn_oracle.exact_knn(x, 0)
+
+
+def test_query_knn_matches_kdtree_and_brute_force():
+    rng = np.random.default_rng(31)
+    ref = rng.normal(size=(800, 9))
+    qry = rng.normal(size=(150, 9))
+    idx, dist = knn_oracle.exact_query_knn(ref, qry, 12)
+    tree_d, tree_i = cKDTree(ref).query(qry, k=12)
+    np.testing.assert_array_equal(idx, tree_i)
+    np.testing.assert_allclose(dist, tree_d, rtol=1e-12, atol=1e-12)
+    # lattice ties: query rows that coincide with reference rows, ties by index
+    lat = rng.integers(0, 3, size=(60, 3)).astype(np.float64)
+    q = lat[:10] + 0.0
+    qi, qd = knn_oracle.exact_query_knn(lat, q, 8, margin=2)
+    for i in range(10):
+        d2 = ((lat - q[i]) ** 2).sum(1)
+        order = sorted(range(60), key=lambda j: (d2[j], j))[:8]
+        np.testing.assert_array_equal(qi[i], order)
+        np.testing.assert_allclose(qd[i], np.sqrt(d2[order]), atol=1e-12)
