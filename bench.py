@@ -2,10 +2,9 @@
 
 Workload: 1,000,000 x 50 float32 Gaussian mixture
 (50 components, means ~ N(0, 6^2 I), unit std), exact KNN with k = 90
-(computed on the GPU with torch as input preparation: each mixture component
-searched by brute force, every row certified exact by a triangle-inequality
-bound against the other components, failures searched against all rows;
---config 4 runs the 4,000,000-row, 200-component case), perplexity 30, PCA
+(computed on the GPU by the library's exact search, fastembedr_hip_knn_exact,
+and handed to the P build in device memory; --config 4 runs the
+4,000,000-row, 200-component case), perplexity 30, PCA
 initialisation, and the reference schedule: 250 early-exaggeration
 iterations (exaggeration 12, momentum 0.5) then 500 (momentum 0.8), learning
 rate n / 12.  Repulsion (--repulsion): by default the FIt-SNE interpolation
@@ -102,19 +101,16 @@ def main() -> int:
     n = args.n or spec.n
     k = sched["k"]
     t0 = time.perf_counter()
-    x, labels = synthetic.gaussian_mixture(spec, seed=1, n=n)
+    x, _ = synthetic.gaussian_mixture(spec, seed=1, n=n)
     log(f"data {x.shape} in {time.perf_counter() - t0:.1f}s")
-    t0 = time.perf_counter()
-    idx, dist, brute_rows = synthetic.exact_knn_partitioned_torch(x, labels, k, chunk=4096)
-    torch.cuda.synchronize()
-    log(f"exact KNN k={k} in {time.perf_counter() - t0:.1f}s (certified per component; "
-        f"{brute_rows} rows searched by brute force)")
+    # exact KNN on the GPU with the library's own search; the result stays
+    # in device memory and P is built from it there
+    knn = fe.exact_knn(np.ascontiguousarray(x, dtype=np.float32), k, keep_device=True)
+    log(f"exact KNN k={k} in {knn.elapsed_sec:.3f}s (fastembedr_hip_knn_exact, host input; {knn.stats})")
     y0 = synthetic.pca_init(x)
-    idx_r, dist_r = synthetic.to_r_layout(idx, dist, one_based=True)
-    del idx, dist
-    torch.cuda.empty_cache()
 
-    sess = fe.TsneSession(idx_r, dist_r, perplexity=sched["perplexity"], index_offset=1, grid_size=args.grid)
+    sess = fe.TsneSession(perplexity=sched["perplexity"], index_offset=1, grid_size=args.grid, n=n, k=k,
+                          device_pointers=(knn.indices_ptr, knn.distances_ptr))
     p_build_ms = sess.p_build_ms
     nnz = sess.nnz
     g = sess.grid_size
@@ -210,7 +206,9 @@ def main() -> int:
     sess.close()
     host_boundary = None
     if args.host_boundary:
-        host_boundary = one_shot_from_host(idx_r, dist_r, y0, sched, lr)
+        host_knn = knn.to_host()
+        host_boundary = one_shot_from_host(np.asfortranarray(host_knn.indices), np.asfortranarray(host_knn.distances),
+                                           y0, sched, lr)
 
     line = {
         "metric": "t-SNE gradient iterations/sec at N=1M (2D); ms per FFT repulsion step; % HBM peak",
@@ -233,6 +231,9 @@ def main() -> int:
                            "1 interval per unit of span)" if interp else
                            f"bilinear grid {g}x{g} ({'reference CPU policy' if args.grid == 0 else 'explicit'})"),
             "n": n,
+            "knn": {"engine": "fastembedr_hip_knn_exact (exact, certified)", "seconds": round(knn.elapsed_sec, 4),
+                    "tiles_computed_per_32_queries": round(knn.stats["tiles_computed"] / ((n + 31) // 32), 1),
+                    "tiles": (n + 63) // 64},
             "k": k,
             "nnz": nnz,
             "repulsion": args.repulsion,
@@ -285,9 +286,9 @@ def bench_transform(args, torch, fe, synthetic) -> int:
     x, _ = synthetic.gaussian_mixture(spec, seed=1, n=n_ref + nq)
     xr, xq = x[:n_ref], x[n_ref:]
     sched = synthetic.SCHEDULE
-    idx, dist = synthetic.exact_knn_torch(xr, sched["k"], chunk=4096)
-    idx_r, dist_r = synthetic.to_r_layout(idx, dist, one_based=True)
-    with fe.TsneSession(idx_r, dist_r, perplexity=sched["perplexity"], index_offset=1) as sess:
+    ref_knn = fe.exact_knn(np.ascontiguousarray(xr, dtype=np.float32), sched["k"], keep_device=True)
+    with fe.TsneSession(perplexity=sched["perplexity"], index_offset=1, n=n_ref, k=sched["k"],
+                        device_pointers=(ref_knn.indices_ptr, ref_knn.distances_ptr)) as sess:
         sess.set_state(synthetic.pca_init(xr))
         sess.center()
         lr = n_ref / 12.0
@@ -296,13 +297,15 @@ def bench_transform(args, torch, fe, synthetic) -> int:
         sess.run(sched["n_iter"], sched["exaggeration"], sched["final_momentum"], lr, sched["min_gain"],
                  sched["max_step_norm"])
         ref_layout = np.asarray(sess.y, np.float64)
-    qidx, qdist = synthetic.exact_query_knn_torch(xr, xq, 30)
-    torch.cuda.synchronize()
-    log(f"reference layout {ref_layout.shape}, query KNN {qidx.shape}")
+    del ref_knn
+    qknn = fe.exact_query_knn(np.ascontiguousarray(xr, dtype=np.float32), np.ascontiguousarray(xq, dtype=np.float32),
+                              30)
+    log(f"reference layout {ref_layout.shape}, query KNN {qknn.indices.shape} in {qknn.elapsed_sec:.3f}s "
+        f"(fastembedr_hip_knn_query)")
     lib = _lib.load()
     ref_cm = np.asfortranarray(ref_layout)
-    qi = np.asfortranarray(qidx + 1, dtype=np.int32)
-    qd = np.asfortranarray(qdist)
+    qi = np.asfortranarray(qknn.indices, dtype=np.int32)
+    qd = np.asfortranarray(qknn.distances, dtype=np.float64)
     out = np.empty((nq, 2), np.float64, order="F")
     params = dict(perplexity=5.0, early_iter=0, lr=0.1, early_ex=4.0, ex=1.0, m0=0.8, m1=0.8, gmax=0.25,
                   smax=float("inf"), n_neg=256, thr=4096, seed=4)
