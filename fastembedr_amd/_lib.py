@@ -58,6 +58,7 @@ SIGNATURES = {
                                             _P, _P, _P]),
     "fastembedr_hip_knn_exact": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _LLP]),
     "fastembedr_hip_knn_query": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _I, _LLP]),
+    "fastembedr_hip_structure_metrics": (_I, [_P, _I, _I, _P, _I, _P, _I, _P]),
 }
 
 REPULSION_GRID = 0

@@ -59,7 +59,7 @@ def build(verbose: bool = True) -> Path:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     inc = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
     objs = []
-    for name in ("embedding_hip_kernels", "attraction_tiles_hip", "transform_hip", "interp_grid_hip", "knn_hip"):
+    for name in ("embedding_hip_kernels", "attraction_tiles_hip", "transform_hip", "interp_grid_hip", "knn_hip", "metrics_hip"):
         obj = BUILD_DIR / f"{name}.o"
         _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(CSRC / f"{name}.hip"), "-o", str(obj)])
         objs.append(str(obj))

@@ -25,6 +25,7 @@
 
 #include "../../include/fastembedr_hip.h"
 #include "knn_device.h"
+#include "metrics_device.h"
 #include "tsne_device.h"
 
 using fehip::BlockStats;
@@ -1498,6 +1499,17 @@ int fastembedr_hip_knn_exact(const float* x, int n, int d, int x_col_major, int 
   if (fehip::knn_exact_run(x, n, d, x_col_major, k, exclude_self, x_on_device, indices, distances, output_on_device,
                            stats, err) != 0) {
     set_error("fastembedr_hip_knn_exact: " + err);
+    return 1;
+  }
+  return 0;
+}
+
+int fastembedr_hip_structure_metrics(const double* high, int n, int p_high, const double* low, int p_low,
+                                     const int* requested_k, int nk, double* out) {
+  g_last_error.clear();
+  std::string err;
+  if (fehip::structure_metrics_run(high, n, p_high, low, p_low, requested_k, nk, out, err) != 0) {
+    set_error("fastembedr_hip_structure_metrics: " + err);
     return 1;
   }
   return 0;

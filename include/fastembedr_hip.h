@@ -301,6 +301,23 @@ FASTEMBEDR_HIP_API int fastembedr_hip_knn_query(const float* reference, int n_re
                                                 int* indices, float* distances, int output_on_device,
                                                 long long* stats);
 
+/* Replaces exact_structure_metrics_cpp (src/embedding_utils.cpp:1582-1752),
+ * which R's evaluate_embedding() calls on a row sample
+ * (R/evaluate_embedding.R:483-500): trustworthiness, continuity, k-NN
+ * preservation and mean neighbour rank error of a layout against the
+ * high-dimensional rows, from full per-row rankings in both spaces (squared
+ * Euclidean distance, ties by index).
+ *   high         n x p_high fp64, column-major (host)
+ *   low          n x p_low fp64, column-major (host)
+ *   requested_k  nk values, each 1 <= k < (2n - 1) / 3
+ *   out          nk x 4 fp64, column-major: trustworthiness, continuity,
+ *                knn_preservation, mean_neighbor_rank_error
+ * 3 <= n <= 5000 (the reference's limit).  The distances are formed in the
+ * reference's operation order, so the ranks, and the metrics, are identical
+ * to the reference's.  Returns 0, or 1 with the last error set. */
+FASTEMBEDR_HIP_API int fastembedr_hip_structure_metrics(const double* high, int n, int p_high, const double* low,
+                                                        int p_low, const int* requested_k, int nk, double* out);
+
 #ifdef __cplusplus
 }
 #endif
