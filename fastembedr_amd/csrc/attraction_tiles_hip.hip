@@ -313,7 +313,7 @@ __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileSte
   }
 }
 
-// One row block per workgroup (XCD-aware: block b runs on XCD b % xcds and
+// The row block rb's attraction (XCD-aware: block b runs on XCD b % xcds and
 // each XCD takes one contiguous range of row blocks, whose column tiles then
 // stay in its L2).  The block's steps (run, round) are processed two at a
 // time from two register buffers: the next step's loads are issued before
@@ -321,21 +321,14 @@ __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileSte
 // flight.  Every load is unconditional and an odd last step is paired with
 // a step that adds nothing (it repeats the last one), so the compiler's wait
 // counts leave the prefetch in flight; every wave runs the same steps (DPP
-// needs whole waves).  Launch bounds: 2048 / NT blocks per CU, 8 waves per
-// SIMD, as many as the LDS allows.
+// needs whole waves).  Starts and ends with LDS free for the next row block
+// (every thread passes a barrier between its last LDS access and the end).
 template <int NT>
-__global__ __launch_bounds__(NT, 2048 / NT) void k_attract_tiles_seg(
-    const unsigned int* __restrict__ ent, const float* __restrict__ val, const int* __restrict__ tile_ptr,
-    const int* __restrict__ tile_cb, const int* __restrict__ tile_beg, const float2* __restrict__ y_cur,
-    float2* __restrict__ attr, float exaggeration, int n, int row_blocks, int xcds) {
-  __shared__ float2 ys[kTileCols];
-  __shared__ float2 yr[kTileRows];
-  __shared__ float2 acc[kTileRows];
-  const int xcd = static_cast<int>(blockIdx.x) % xcds;
-  const int slot = static_cast<int>(blockIdx.x) / xcds;
-  const int per_xcd = (row_blocks + xcds - 1) / xcds;
-  const int rb = xcd * per_xcd + slot;
-  if (slot >= per_xcd || rb >= row_blocks) return;  // whole workgroup
+__device__ __forceinline__ void attract_row_block(int rb, const unsigned int* __restrict__ ent,
+                                                  const float* __restrict__ val, const int* __restrict__ tile_ptr,
+                                                  const int* __restrict__ tile_cb, const int* __restrict__ tile_beg,
+                                                  const float2* __restrict__ y_cur, float2* __restrict__ attr,
+                                                  float exaggeration, int n, float2* ys, float2* yr, float2* acc) {
   const int tid = static_cast<int>(threadIdx.x);
   const int r0 = rb * kTileRows;
   const int rows = min(kTileRows, n - r0);
@@ -365,6 +358,44 @@ __global__ __launch_bounds__(NT, 2048 / NT) void k_attract_tiles_seg(
   }
   __syncthreads();
   for (int r = tid; r < rows; r += NT) attr[r0 + r] = make_float2(exaggeration * acc[r].x, exaggeration * acc[r].y);
+  __syncthreads();
+}
+
+// Workgroups take the row blocks of their XCD's range: first the one at their
+// slot, then the next unclaimed one from the XCD's counter work[xcd] (claims
+// count from the number of slots).  With one slot per row block this is one
+// row block per workgroup; with fewer, the kernel leaves LDS and wave slots
+// free for kernels that run beside it, and the dynamic claims balance the
+// row blocks' unequal work.  The last workgroup to finish resets work[] (its
+// xcds + 1 counters start and end each launch at zero).  Launch bounds:
+// 2048 / NT blocks per CU, 8 waves per SIMD, as many as the LDS allows.
+template <int NT>
+__global__ __launch_bounds__(NT, 2048 / NT) void k_attract_tiles_seg(
+    const unsigned int* __restrict__ ent, const float* __restrict__ val, const int* __restrict__ tile_ptr,
+    const int* __restrict__ tile_cb, const int* __restrict__ tile_beg, const float2* __restrict__ y_cur,
+    float2* __restrict__ attr, float exaggeration, int n, int row_blocks, int xcds, unsigned int* __restrict__ work) {
+  __shared__ float2 ys[kTileCols];
+  __shared__ float2 yr[kTileRows];
+  __shared__ float2 acc[kTileRows];
+  __shared__ int claimed;
+  const int xcd = static_cast<int>(blockIdx.x) % xcds;
+  const int slots = static_cast<int>(gridDim.x) / xcds;  // the grid is a whole number of slots per XCD
+  const int per_xcd = (row_blocks + xcds - 1) / xcds;
+  const int first = xcd * per_xcd;
+  const int end = min(row_blocks, first + per_xcd);
+  int slot = static_cast<int>(blockIdx.x) / xcds;
+  while (first + slot < end) {
+    attract_row_block<NT>(first + slot, ent, val, tile_ptr, tile_cb, tile_beg, y_cur, attr, exaggeration, n, ys, yr,
+                          acc);
+    if (threadIdx.x == 0) claimed = slots + static_cast<int>(atomicAdd(&work[xcd], 1u));
+    __syncthreads();
+    slot = claimed;
+    __syncthreads();  // every thread has read `claimed` before it is written again
+  }
+  if (threadIdx.x == 0 && atomicAdd(&work[xcds], 1u) == gridDim.x - 1) {
+    // every other workgroup has made its last claim
+    for (int x = 0; x <= xcds; ++x) atomicExch(&work[x], 0u);
+  }
 }
 
 int bits_for(long long count) {  // bits needed to hold values 0 .. count - 1
@@ -451,12 +482,14 @@ hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream) {
 }
 
 hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int threads,
-                                int xcds, hipStream_t stream) {
+                                int xcds, int slots_per_xcd, hipStream_t stream) {
+  if (t.work == nullptr || xcds < 1 || xcds > kTileMaxXcds) return hipErrorInvalidValue;
   const int per_xcd = (t.row_blocks + xcds - 1) / xcds;
-  const int blocks = per_xcd * xcds;
+  const int slots = slots_per_xcd > 0 ? std::min(slots_per_xcd, per_xcd) : per_xcd;
+  const int blocks = std::max(slots, 1) * xcds;
 #define FEHIP_TILED(NT_)                                                                                        \
   k_attract_tiles_seg<NT_><<<blocks, NT_, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, \
-                                                       attr, exaggeration, t.n, t.row_blocks, xcds);
+                                                       attr, exaggeration, t.n, t.row_blocks, xcds, t.work);
   switch (threads) {
     case 256:
       FEHIP_TILED(256)

@@ -109,13 +109,19 @@ __device__ void publish_stats(BlockStats local, BlockStats* partial) {
 }
 
 // Reduces the per-block statistics in a fixed order (deterministic) and sets
-// the grid geometry.
+// the grid geometry.  With box_out (pinned, coherent host memory) the
+// interpolation grid's box count is also stored there, so the host can learn
+// it from an event on this kernel instead of a device-to-host copy.
 __global__ __launch_bounds__(256) void k_finalize_stats(const BlockStats* __restrict__ partial, int blocks,
-                                                        DeviceScalars* sc, int n, int g, int center) {
+                                                        DeviceScalars* sc, int n, int g, int center,
+                                                        int* box_out) {
   BlockStats acc = stats_identity();
   for (int b = threadIdx.x; b < blocks; b += 256) combine(acc, partial[b]);
   acc = block_stats<256>(acc);
-  if (threadIdx.x == 0) set_geometry(sc, acc, n, g, center != 0);
+  if (threadIdx.x == 0) {
+    set_geometry(sc, acc, n, g, center != 0);
+    if (box_out != nullptr) __hip_atomic_store(box_out, sc->lg_boxes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1333,7 +1339,7 @@ template <int MODE>
 hipError_t update_launch(const float2* y_cur, const float2* attr, float2* y_out, float2* update, float2* gains,
                          float2* grad_out, const float2* exact_rep, const GridBuffers& gb, const UpdateParams& up,
                          BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
-                         const float4* interp_field) {
+                         const float4* interp_field, int* box_out) {
   const int blocks = reduce_blocks_for(n);
   if (interp_field != nullptr && MODE != kModeGradientExact) {
     k_update<MODE, true><<<blocks, kPointThreads, 0, stream>>>(y_cur, attr, y_out, update, gains, grad_out,
@@ -1342,7 +1348,7 @@ hipError_t update_launch(const float2* y_cur, const float2* attr, float2* y_out,
     k_update<MODE, false><<<blocks, kPointThreads, 0, stream>>>(y_cur, attr, y_out, update, gains, grad_out,
                                                                 exact_rep, gb.field, gb.g, up, partial, sc, n);
   }
-  if (MODE == kModeUpdate) k_finalize_stats<<<1, 256, 0, stream>>>(partial, blocks, sc, n, gb.g, 1);
+  if (MODE == kModeUpdate) k_finalize_stats<<<1, 256, 0, stream>>>(partial, blocks, sc, n, gb.g, 1, box_out);
   return hipGetLastError();
 }
 
@@ -1409,7 +1415,7 @@ hipError_t launch_stats(const float2* y, int n, int g, int center, BlockStats* p
                         hipStream_t stream) {
   const int blocks = reduce_blocks_for(n);
   k_stats<<<blocks, kPointThreads, 0, stream>>>(y, n, g, center, partial, sc);
-  k_finalize_stats<<<1, 256, 0, stream>>>(partial, blocks, sc, n, g, center);
+  k_finalize_stats<<<1, 256, 0, stream>>>(partial, blocks, sc, n, g, center, nullptr);
   return hipGetLastError();
 }
 
@@ -1479,17 +1485,17 @@ hipError_t launch_attract(const Csr& p, const float2* y_cur, float2* attr, float
 hipError_t launch_update(int mode, const float2* y_cur, const float2* attr, float2* y_out, float2* update,
                          float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
                          const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
-                         const float4* interp_field) {
+                         const float4* interp_field, int* box_out) {
   switch (mode) {
     case kModeUpdate:
       return update_launch<kModeUpdate>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc,
-                                        n, stream, interp_field);
+                                        n, stream, interp_field, box_out);
     case kModeGradientGrid:
       return update_launch<kModeGradientGrid>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up,
-                                              partial, sc, n, stream, interp_field);
+                                              partial, sc, n, stream, interp_field, nullptr);
     case kModeGradientExact:
       return update_launch<kModeGradientExact>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up,
-                                               partial, sc, n, stream, nullptr);
+                                               partial, sc, n, stream, nullptr, nullptr);
     default:
       return hipErrorInvalidValue;
   }

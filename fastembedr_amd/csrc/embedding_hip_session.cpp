@@ -160,6 +160,12 @@ struct fastembedr_hip_tsne {
   // tiles follow the working numbering and are rebuilt after it changes.
   bool attract_tiled = true;
   int tile_threads = 512;
+  // Workgroups per CU of the attraction when it runs beside the repulsion
+  // kernels (side stream): fewer than the 4 its LDS allows leave room on
+  // every CU for them (2: measured best at config 2).  Alone it takes one
+  // workgroup per row block.
+  int attract_shared_per_cu = 2;
+  int cus = 0;  // compute units of the device
   fehip::Tiles tiles;
   int tiles_for = -2;       // value of wi the tiles were built for; -2: none
   // Repulsion used by run(): the bilinear grid (reference) or the FIt-SNE
@@ -171,10 +177,12 @@ struct fastembedr_hip_tsne {
   Arena lg_arena;
   fehip::InterpBuffers ib;
   int lg_last_fft = 0;       // FFT length of the last interpolation-grid iteration
-  // Box counts of recent iterations, copied back asynchronously (pinned ring):
-  // slot it % kLgRing holds the geometry the update of iteration it - 1 set.
+  // Box counts of recent iterations (pinned coherent ring, written by the
+  // update's statistics kernel): slot it % kLgRing holds the geometry the
+  // update of iteration it - 1 set.
   static constexpr int kLgRing = 8;
   int* lg_ring = nullptr;
+  int* lg_ring_dev = nullptr;  // the ring's device address
   hipEvent_t lg_ev[kLgRing] = {};
   long long lg_ring_iter[kLgRing] = {};
 
@@ -380,7 +388,7 @@ bool alloc_tiles(fastembedr_hip_tsne* s) {
   const std::size_t slots = static_cast<std::size_t>(t.max_tiles) + 1;
   const std::size_t bytes = 2 * align_up(padded * 4) + 2 * align_up(nnz * 4) + 2 * align_up(nnz * 8) +
                             align_up((static_cast<std::size_t>(t.row_blocks) + 1) * 4) + 4 * align_up(slots * 4) +
-                            align_up(4) + align_up(temp) + 4096;
+                            align_up(4) + align_up((fehip::kTileMaxXcds + 1) * 4) + align_up(temp) + 4096;
   if (!memory_preflight(bytes, "HIP openTSNE attraction tiles") ||
       !s->tile_arena.init(bytes, "hipMalloc(HIP openTSNE attraction tiles)")) {
     return false;
@@ -398,19 +406,25 @@ bool alloc_tiles(fastembedr_hip_tsne* s) {
   t.ubeg = a.take<int>(slots);
   t.psize = a.take<int>(slots);
   t.tile_count = a.take<int>(1);
+  t.work = a.take<unsigned int>(fehip::kTileMaxXcds + 1);
   t.temp = a.take<char>(std::max<std::size_t>(temp, 1));
   t.temp_bytes = temp;
   if (t.temp == nullptr) {
     set_error("internal: attraction tiles do not fit their arena");
     return false;
   }
-  return true;
+  return hip_ok(hipMemsetAsync(t.work, 0, (fehip::kTileMaxXcds + 1) * sizeof(unsigned int), s->stream),
+                "hipMemset(attraction claims)");
 }
 
 // Attractive term of every row into s->attr at the centred layout y_cur, on
-// stream st (the main stream when null).
-bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggeration, hipStream_t st = nullptr) {
+// stream st (the main stream when null); `shared`: other kernels run beside it.
+bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggeration, hipStream_t st = nullptr,
+                     bool shared = false) {
   if (st == nullptr) st = s->stream;
+  const int slots = shared && s->cus > 0 && s->attract_shared_per_cu > 0
+                        ? s->attract_shared_per_cu * std::max(1, s->cus / s->xcds)
+                        : 0;
   if (!s->attract_tiled) {
     return s->timed(
         fehip::kKAttract, "attract launch",
@@ -427,7 +441,8 @@ bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggera
   return s->timed(
       fehip::kKAttract, "attract launch",
       [&] {
-        return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->tile_threads, s->xcds, st);
+        return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->tile_threads, s->xcds, slots,
+                                           st);
       },
       st);
 }
@@ -482,8 +497,11 @@ bool ensure_interp(fastembedr_hip_tsne* s) {
   }
   if (!hip_ok(hipMemsetAsync(ib.tile_count, 0, (fehip::kMaxTiles + 1) * sizeof(int), s->stream),
               "hipMemset(interpolation tiles)") ||
-      !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s->lg_ring), fastembedr_hip_tsne::kLgRing * sizeof(int)),
-              "hipHostMalloc(box ring)")) {
+      !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s->lg_ring), fastembedr_hip_tsne::kLgRing * sizeof(int),
+                            hipHostMallocMapped | hipHostMallocCoherent),
+              "hipHostMalloc(box ring)") ||
+      !hip_ok(hipHostGetDevicePointer(reinterpret_cast<void**>(&s->lg_ring_dev), s->lg_ring, 0),
+              "hipHostGetDevicePointer(box ring)")) {
     return false;
   }
   for (int r = 0; r < fastembedr_hip_tsne::kLgRing; ++r) {
@@ -539,7 +557,7 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
     return false;
   }
   // side: attraction; kernel spectrum
-  if (!enqueue_attract(s, s->y_b, exaggeration, sa)) return false;
+  if (!enqueue_attract(s, s->y_b, exaggeration, sa, overlap)) return false;
   if (lg) {
     static constexpr int kIds[3] = {fehip::kKLgKernelRows, fehip::kKLgKernelT, fehip::kKLgKernelCols};
     for (int which = 0; which < 3; ++which) {
@@ -972,13 +990,15 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
         (std::strncmp(prop.gcnArchName, "gfx94", 5) == 0 || std::strncmp(prop.gcnArchName, "gfx95", 5) == 0)) {
       s->xcds = 8;
     }
-    s->xcds = env_int("FASTEMBEDR_HIP_XCDS", s->xcds);
+    s->xcds = std::max(1, std::min(fehip::kTileMaxXcds, env_int("FASTEMBEDR_HIP_XCDS", s->xcds)));
+    if (hipDeviceGetAttribute(&s->cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) s->cus = 0;
   }
   // Attraction: tiled unless FASTEMBEDR_HIP_ATTRACT_TILED=0 (row-parallel).
   if (const char* tiled = std::getenv("FASTEMBEDR_HIP_ATTRACT_TILED")) {
     if (std::strcmp(tiled, "0") == 0) s->attract_tiled = false;
   }
   s->tile_threads = env_int("FASTEMBEDR_HIP_TILE_THREADS", s->tile_threads);
+  s->attract_shared_per_cu = env_int("FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU", s->attract_shared_per_cu);
   if (s->tile_threads != 256 && s->tile_threads != 512 && s->tile_threads != 1024) s->tile_threads = 512;
   if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {
     delete s;
@@ -1311,7 +1331,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
       for (int r = 0; r < kRing; ++r) {
         if (s->lg_ring_iter[r] > known_it && hipEventQuery(s->lg_ev[r]) == hipSuccess) {
           known_it = static_cast<int>(s->lg_ring_iter[r]);
-          known_boxes = s->lg_ring[r];
+          known_boxes = static_cast<volatile int*>(s->lg_ring)[r];
         }
       }
       if (it - known_it > allowed_lag) {
@@ -1319,7 +1339,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
         const int slot = target % kRing;
         if (!hip_ok(hipEventSynchronize(s->lg_ev[slot]), "hipEventSynchronize(box ring)")) return 1;
         known_it = target;
-        known_boxes = s->lg_ring[slot];
+        known_boxes = static_cast<volatile int*>(s->lg_ring)[slot];
       }
       const long long bound =
           static_cast<long long>(known_boxes) + static_cast<long long>(std::ceil(growth * (it - known_it))) + 1;
@@ -1329,22 +1349,17 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
     // Timing every kernel (mode 1) runs the pieces in sequence, so that each
     // duration is the kernel's alone.
     const bool overlap = !(s->timing && s->timed_only < 0);
+    const int slot = (it + 1) % kRing;
     if (!enqueue_gradient_pieces(s, lg, fft_len, exaggeration, overlap) ||
         !s->timed(fehip::kKUpdate, "update launch", [&] {
           return fehip::launch_update(fehip::kModeUpdate, s->y_b, s->attr, s->y_a(), s->update(), s->gains(),
                                       nullptr, nullptr, s->gb, up, s->partial, s->sc, n, s->stream,
-                                      lg ? s->ib.field : nullptr);
+                                      lg ? s->ib.field : nullptr, lg ? s->lg_ring_dev + slot : nullptr);
         })) {
       return 1;
     }
     if (lg) {
-      const int slot = (it + 1) % kRing;
-      if (!hip_ok(hipMemcpyAsync(&s->lg_ring[slot], &s->sc->lg_boxes, sizeof(int), hipMemcpyDeviceToHost,
-                                 s->stream),
-                  "hipMemcpyAsync(box ring)") ||
-          !hip_ok(hipEventRecord(s->lg_ev[slot], s->stream), "hipEventRecord(box ring)")) {
-        return 1;
-      }
+      if (!hip_ok(hipEventRecord(s->lg_ev[slot], s->stream), "hipEventRecord(box ring)")) return 1;
       s->lg_ring_iter[slot] = it + 1;
     }
   }

@@ -239,11 +239,13 @@ hipError_t launch_attract(const Csr& p, const float2* y_cur, float2* attr, float
 // Repulsion read-back + attr -> gradient; kModeUpdate applies the update and
 // computes the next iteration's statistics, the gradient modes write grad_out.
 // interp_field != nullptr reads the FIt-SNE interpolation grid instead of the
-// bilinear one (kModeUpdate and kModeGradientGrid).
+// bilinear one (kModeUpdate and kModeGradientGrid).  kModeUpdate with
+// box_out != nullptr (device pointer of pinned coherent host memory) also
+// stores the next iteration's interpolation box count there.
 hipError_t launch_update(int mode, const float2* y_cur, const float2* attr, float2* y_out, float2* update,
                          float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
                          const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
-                         const float4* interp_field = nullptr);
+                         const float4* interp_field = nullptr, int* box_out = nullptr);
 hipError_t launch_commit(float2* y, const DeviceScalars* sc, int n, hipStream_t stream);
 
 // ---- locality renumbering ---------------------------------------------------
@@ -297,6 +299,7 @@ hipError_t launch_gather2(const float2* src, const int* idx, float2* dst, int n,
 constexpr int kTileRows = 512;
 constexpr int kTileCols = 4096;
 constexpr int kTileRun = 8;
+constexpr int kTileMaxXcds = 16;
 
 struct Tiles {
   int n = 0;
@@ -315,6 +318,7 @@ struct Tiles {
   int* ubeg = nullptr;           // max_tiles + 1 (begins before padding)
   int* psize = nullptr;          // max_tiles + 1 (padded sizes)
   int* tile_count = nullptr;     // 1
+  unsigned int* work = nullptr;  // kTileMaxXcds + 1 claim counters of the attraction; zero between launches
   // build scratch, nnz each; after the sort the inputs hold the run heads
   // (key_in) and their scan (pay_in)
   unsigned int* key_in = nullptr;
@@ -328,9 +332,12 @@ void tiles_shape(int n, long long nnz, Tiles& t);
 hipError_t tiles_temp_bytes(const Tiles& t, std::size_t& bytes);
 // Rebuilds t from the CSR (same numbering), all on `stream`.
 hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream);
-// threads: workgroup size, 256, 512 or 1024 (one row block per workgroup).
+// threads: workgroup size, 256, 512 or 1024.  slots_per_xcd: workgroups per
+// XCD (<= 0: one per row block); with fewer, each claims row blocks of its
+// XCD's range until none is left.  t.work must be zero (it is after a
+// launch); xcds <= kTileMaxXcds.
 hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int threads,
-                                int xcds, hipStream_t stream);
+                                int xcds, int slots_per_xcd, hipStream_t stream);
 
 // ---- exact O(n^2) terms (gradient check and KL) ----------------------------
 hipError_t launch_exact_repulsion(const float2* y, int n, float2* rep, double* z_partial, DeviceScalars* sc,
