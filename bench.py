@@ -186,12 +186,14 @@ def main() -> int:
     ms_per_step = 1000.0 * wall / args.steps
     cnt, tot = timing[dom]
     dom_ms = tot / cnt if cnt else 0.0
-    # Algorithmic bytes per launch.  attract: P streamed once (column and
-    # value, 8 nnz), y_i read and the row sum written (16 n); the neighbour
-    # positions y_j are counted as cache-resident, as the grid reads are.
-    # update: y_i, attraction, gains, update read (32 n) and y, gains, update
-    # written (24 n).
-    alg_bytes = {"attract": 8.0 * nnz + 16.0 * n, "update": 56.0 * n}
+    # Algorithmic bytes per launch.  attract: P streamed once (a 16-bit slot
+    # word and the fp32 value per stored entry, 6 nnz), y_i read and the row
+    # sum written (16 n); the neighbour positions y_j are counted as
+    # cache-resident, as the grid reads are; bridge and padding slots are
+    # overhead, not algorithmic bytes.  update: y_i, attraction, gains,
+    # update read (32 n) and y, gains, update written (24 n).
+    layout = sess.attraction_info()
+    alg_bytes = {"attract": 6.0 * nnz + 16.0 * n, "update": 56.0 * n}
     dom_bytes = alg_bytes.get(dom, 0.0)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9 if dom_ms > 0 else 0.0
     traffic = measured_traffic(dom, n, nnz, g, args.repulsion)
@@ -236,6 +238,8 @@ def main() -> int:
                     "tiles": (n + 63) // 64},
             "k": k,
             "nnz": nnz,
+            "attraction_layout": {"runs": layout["tiles"], "slots": layout["slots"],
+                                  "slots_per_entry": round(layout["slots"] / max(nnz, 1), 4)},
             "repulsion": args.repulsion,
             "timed_iterations": f"first {args.steps} of the 750-iteration schedule",
         },

@@ -20,8 +20,11 @@
 //   k_tile_heads, scan, k_tile_meta
 //                              runs: first run per row block, column tile,
 //                              first entry, count
+//   scan                       slots per entry (itself and its bridges) ->
+//                              slot offsets
 //   k_tile_sizes, scan         padded run sizes -> padded run begins
-//   k_tile_scatter             entries to their padded places
+//   k_tile_scatter             entries and bridges to their padded places
+//   k_tile_bases               each slot group's base row into its values
 
 #include <hip/hip_runtime.h>
 
@@ -36,12 +39,21 @@
 namespace fehip {
 namespace {
 
-// An entry word holds two byte offsets into the LDS position arrays (8 bytes
-// per position): the row's in its high half, the column's in its low half,
-// so the kernel addresses LDS with no shifts.  A run's padding repeats the
-// run's last entry word with p = 0 and so adds nothing.
-static_assert(kTileRun == 8, "a lane reads its run group as two 16-byte vectors per array");
-static_assert(kTileRows * 8 <= 0x10000 && kTileCols * 8 <= 0x10000, "entry offsets are 16-bit byte offsets");
+// Slot format (kTileRun = 8 slots per lane group, a group starting at a
+// multiple of 8): the 16-bit word of a slot is (local column << 4) | step,
+// where step is the slot's row minus the previous slot's row in the group (0
+// for a group's first slot).  p is stored as its IEEE-754 bits; P is a
+// normalised joint distribution built from validated distances, so every
+// value lies in [0, 1] and bits 30 and 31 of its pattern are zero.  Those
+// bits of slots 0..4 of a group hold the group's base row (the local row of
+// its first slot, 9 bits), 2 bits per slot.  Steps above 15 are made of
+// bridge slots (p = 0) 15 rows apart; a run's padding repeats its last slot
+// with step 0 and p = 0.  Bridges and padding add nothing.
+static_assert(kTileRun == 8, "a lane reads its group as one 16-byte vector of words and two of values");
+static_assert(kTileRows <= 1024, "a group's base row fits the 10 spare bits of its first 5 values");
+static_assert(kTileCols <= 4096, "a local column fits 12 bits of a slot word");
+constexpr int kStepMax = 15;
+constexpr unsigned int kValueMask = 0x3fffffffu;
 
 constexpr int kBuildThreads = 256;
 
@@ -50,9 +62,16 @@ __device__ __forceinline__ long long grid_first() {
 }
 __device__ __forceinline__ long long grid_stride() { return static_cast<long long>(gridDim.x) * kBuildThreads; }
 
-__device__ __forceinline__ unsigned int tile_word(unsigned int local_row, unsigned int local_col) {
-  return ((local_row * 8u) << 16) | (local_col * 8u);
+// Sort payload of one entry: p's bits, local row, local column.
+__device__ __forceinline__ unsigned long long tile_payload(float p, unsigned int local_row, unsigned int local_col) {
+  return (static_cast<unsigned long long>(__float_as_uint(p)) << 32) | (local_row << 16) | local_col;
 }
+__device__ __forceinline__ int payload_row(unsigned long long w) { return static_cast<int>((w >> 16) & 0xffffu); }
+__device__ __forceinline__ int payload_col(unsigned long long w) { return static_cast<int>(w & 0xffffu); }
+
+// Bridge slots needed before an entry whose row is `gap` rows past the
+// previous entry of its run.
+__device__ __forceinline__ int bridges_for(int gap) { return gap > 0 ? (gap - 1) / kStepMax : 0; }
 
 template <int L>
 __global__ __launch_bounds__(kBuildThreads) void k_tile_keys(const int* __restrict__ row_ptr,
@@ -70,19 +89,26 @@ __global__ __launch_bounds__(kBuildThreads) void k_tile_keys(const int* __restri
     for (int e = row_ptr[i] + lane; e < e1; e += L) {
       const int j = col[e];
       key[e] = (rb << col_bits) | static_cast<unsigned int>(j / kTileCols);
-      pay[e] = (static_cast<unsigned long long>(__float_as_uint(val[e])) << 32) |
-               static_cast<unsigned long long>(tile_word(lr, static_cast<unsigned int>(j % kTileCols)));
+      pay[e] = tile_payload(val[e], lr, static_cast<unsigned int>(j % kTileCols));
     }
   }
 }
 
-__global__ __launch_bounds__(kBuildThreads) void k_tile_heads(const unsigned int* __restrict__ key, long long nnz,
-                                                              int* __restrict__ heads) {
-  for (long long p = grid_first(); p < nnz; p += grid_stride()) heads[p] = (p == 0 || key[p] != key[p - 1]) ? 1 : 0;
+// Run heads (first entry of each (row block, column tile)) and the slots each
+// entry takes: itself and its bridges.
+__global__ __launch_bounds__(kBuildThreads) void k_tile_heads(const unsigned int* __restrict__ key,
+                                                              const unsigned long long* __restrict__ pay,
+                                                              long long nnz, int* __restrict__ heads,
+                                                              int* __restrict__ slots) {
+  for (long long p = grid_first(); p < nnz; p += grid_stride()) {
+    const bool head = p == 0 || key[p] != key[p - 1];
+    heads[p] = head ? 1 : 0;
+    slots[p] = 1 + (head ? 0 : bridges_for(payload_row(pay[p]) - payload_row(pay[p - 1])));
+  }
 }
 
-// Run records from the sorted keys: column tile, first entry (before
-// padding), the first run of each row block, and the count (to *tile_count).
+// Run records from the sorted keys: column tile, first entry, the first run
+// of each row block, and the count (to *tile_count).
 __global__ __launch_bounds__(kBuildThreads) void k_tile_meta(const unsigned int* __restrict__ key,
                                                              const int* __restrict__ heads,
                                                              const int* __restrict__ pos, long long nnz, int col_bits,
@@ -109,44 +135,82 @@ __global__ __launch_bounds__(kBuildThreads) void k_tile_meta(const unsigned int*
   }
 }
 
+// Slot offset of entry u (entries and bridges before it), u <= nnz.
+__device__ __forceinline__ int slot_of(const int* __restrict__ sbeg, const int* __restrict__ slots, long long nnz,
+                                       int u) {
+  return u < nnz ? sbeg[u] : sbeg[nnz - 1] + slots[nnz - 1];
+}
+
 // Padded run sizes (multiples of kTileRun), zero past the last run.
 __global__ __launch_bounds__(kBuildThreads) void k_tile_sizes(const int* __restrict__ ubeg,
-                                                              const int* __restrict__ tile_count, long long slots,
+                                                              const int* __restrict__ tile_count, long long tiles,
+                                                              const int* __restrict__ sbeg,
+                                                              const int* __restrict__ slots, long long nnz,
                                                               int* __restrict__ psize) {
   const int total = *tile_count;
-  for (long long t = grid_first(); t < slots; t += grid_stride()) {
+  for (long long t = grid_first(); t < tiles; t += grid_stride()) {
     int v = 0;
     if (t < total) {
-      const int len = ubeg[t + 1] - ubeg[t];
+      const int len = slot_of(sbeg, slots, nnz, ubeg[t + 1]) - slot_of(sbeg, slots, nnz, ubeg[t]);
       v = (len + kTileRun - 1) / kTileRun * kTileRun;
     }
     psize[t] = v;
   }
 }
 
-// Entries to their padded places; the last entry of each run fills the
-// run's padding with copies of its own word and p = 0.
+// One slot: its word (step 0 at a group start) and p; the row of a group's
+// first slot goes to base_row, merged into the values by k_tile_bases.
+__device__ __forceinline__ void put_slot(long long q, int col, int row, int step, unsigned int p_bits,
+                                         unsigned short* __restrict__ ent, float* __restrict__ val,
+                                         unsigned short* __restrict__ base_row) {
+  const bool first = (q & (kTileRun - 1)) == 0;
+  ent[q] = static_cast<unsigned short>((col << 4) | (first ? 0 : step));
+  val[q] = __uint_as_float(p_bits);
+  if (first) base_row[q / kTileRun] = static_cast<unsigned short>(row);
+}
+
+// Entries and their bridges to their padded places; the last entry of each
+// run also fills the run's padding.
 __global__ __launch_bounds__(kBuildThreads) void k_tile_scatter(const unsigned long long* __restrict__ pay,
                                                                 const int* __restrict__ heads,
                                                                 const int* __restrict__ pos,
                                                                 const int* __restrict__ ubeg,
+                                                                const int* __restrict__ sbeg,
                                                                 const int* __restrict__ tile_beg, long long nnz,
-                                                                unsigned int* __restrict__ ent,
-                                                                float* __restrict__ val) {
+                                                                unsigned short* __restrict__ ent,
+                                                                float* __restrict__ val,
+                                                                unsigned short* __restrict__ base_row) {
   for (long long p = grid_first(); p < nnz; p += grid_stride()) {
     const int t = pos[p] + heads[p] - 1;
-    const int u0 = ubeg[t];
-    const int b0 = tile_beg[t];
+    const long long s0 = tile_beg[t] + (sbeg[p] - sbeg[ubeg[t]]);  // p's first slot (its first bridge)
     const unsigned long long w = pay[p];
-    const long long q = b0 + (p - u0);
-    ent[q] = static_cast<unsigned int>(w);
-    val[q] = __uint_as_float(static_cast<unsigned int>(w >> 32));
-    const int u1 = ubeg[t + 1];
-    if (p == u1 - 1) {
-      for (int r = b0 + (u1 - u0); r < tile_beg[t + 1]; ++r) {
-        ent[r] = static_cast<unsigned int>(w);
-        val[r] = 0.0f;
-      }
+    const int row = payload_row(w);
+    const int col = payload_col(w);
+    const int prev = heads[p] ? row : payload_row(pay[p - 1]);
+    const int nb = bridges_for(row - prev);
+    for (int m = 0; m < nb; ++m) {
+      put_slot(s0 + m, col, prev + (m + 1) * kStepMax, kStepMax, 0u, ent, val, base_row);
+    }
+    const long long q = s0 + nb;
+    put_slot(q, col, row, row - prev - nb * kStepMax, static_cast<unsigned int>(w >> 32), ent, val, base_row);
+    if (p == nnz - 1 || heads[p + 1]) {
+      for (long long r = q + 1; r < tile_beg[t + 1]; ++r) put_slot(r, col, row, 0, 0u, ent, val, base_row);
+    }
+  }
+}
+
+// Each group's base row into bits 30-31 of its first 5 values.
+__global__ __launch_bounds__(kBuildThreads) void k_tile_bases(const unsigned short* __restrict__ base_row,
+                                                              const int* __restrict__ tile_beg,
+                                                              const int* __restrict__ tile_count,
+                                                              float* __restrict__ val) {
+  const long long groups = tile_beg[*tile_count] / kTileRun;
+  for (long long g = grid_first(); g < groups; g += grid_stride()) {
+    const unsigned int b = base_row[g];
+#pragma unroll
+    for (int q = 0; q < 5; ++q) {
+      float& v = val[g * kTileRun + q];
+      v = __uint_as_float(__float_as_uint(v) | (((b >> (2 * q)) & 3u) << 30));
     }
   }
 }
@@ -212,19 +276,18 @@ __device__ __forceinline__ void seg_step(float& x, float& y, unsigned int& stop)
 // told to add nothing; as a lane's entries start at a fixed stride, the
 // active lanes are a prefix of each wave.
 struct TileGroup {
-  uint4 w0, w1;
+  uint4 w;  // 8 slot words, two per component (low half first)
   float4 p0, p1;
 };
 
 template <int NT>
-__device__ __forceinline__ TileGroup load_tile_group(const unsigned int* __restrict__ ent,
+__device__ __forceinline__ TileGroup load_tile_group(const unsigned short* __restrict__ ent,
                                                      const float* __restrict__ val, int e0, int e1, int round,
                                                      int tid) {
   const int e_lane = e0 + (round * NT + tid) * kTileRun;
   const int e = e_lane < e1 ? e_lane : e1 - kTileRun;
   TileGroup g;
-  g.w0 = *reinterpret_cast<const uint4*>(ent + e);
-  g.w1 = *reinterpret_cast<const uint4*>(ent + e + 4);
+  g.w = *reinterpret_cast<const uint4*>(ent + e);
   g.p0 = *reinterpret_cast<const float4*>(val + e);
   g.p1 = *reinterpret_cast<const float4*>(val + e + 4);
   return g;
@@ -278,25 +341,40 @@ template <int NT>
 __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileStep& s, bool live, int tid, float2* yr,
                                                float2* ys, float2* acc) {
   const bool active = live && s.e0 + (s.round * NT + tid) * kTileRun < s.e1;
-  const unsigned int w[kTileRun] = {g.w0.x, g.w0.y, g.w0.z, g.w0.w, g.w1.x, g.w1.y, g.w1.z, g.w1.w};
-  const float p[kTileRun] = {g.p0.x, g.p0.y, g.p0.z, g.p0.w, g.p1.x, g.p1.y, g.p1.z, g.p1.w};
+  const unsigned int wp[4] = {g.w.x, g.w.y, g.w.z, g.w.w};
+  const unsigned int pb[kTileRun] = {__float_as_uint(g.p0.x), __float_as_uint(g.p0.y), __float_as_uint(g.p0.z),
+                                     __float_as_uint(g.p0.w), __float_as_uint(g.p1.x), __float_as_uint(g.p1.y),
+                                     __float_as_uint(g.p1.z), __float_as_uint(g.p1.w)};
+  // Row byte offsets (8 bytes per LDS position): the base row from the spare
+  // value bits, then the steps; clamped to the block's rows.
+  unsigned int kr[kTileRun];
+  unsigned int row = 0;
+#pragma unroll
+  for (int q = 0; q < 5; ++q) row |= (pb[q] >> 30) << (2 * q);
+#pragma unroll
+  for (int q = 0; q < kTileRun; ++q) {
+    const unsigned int word = (q & 1) ? wp[q / 2] >> 16 : wp[q / 2] & 0xffffu;
+    row += word & 0xfu;
+    kr[q] = min(row, static_cast<unsigned int>(kTileRows - 1)) * 8u;
+  }
   float tx = 0.0f, ty = 0.0f;  // the current row's part
 #pragma unroll
   for (int q = 0; q < kTileRun; ++q) {
-    const unsigned int kr = w[q] >> 16;
-    const float2 c = attract_term(lds_at(yr, kr), lds_at(ys, w[q] & 0xffffu), p[q]);
-    const bool brk = q > 0 && kr != (w[q > 0 ? q - 1 : 0] >> 16);  // the previous row's part is complete
+    const unsigned int word = (q & 1) ? wp[q / 2] >> 16 : wp[q / 2] & 0xffffu;
+    const unsigned int kc = (word >> 1) & 0x7ff8u;  // (word >> 4) * 8
+    const float2 c = attract_term(lds_at(yr, kr[q]), lds_at(ys, kc), __uint_as_float(pb[q] & kValueMask));
+    const bool brk = q > 0 && kr[q] != kr[q > 0 ? q - 1 : 0];  // the previous row's part is complete
     if (brk && active) {
-      atomicAdd(&lds_at(acc, w[q > 0 ? q - 1 : 0] >> 16).x, tx);
-      atomicAdd(&lds_at(acc, w[q > 0 ? q - 1 : 0] >> 16).y, ty);
+      atomicAdd(&lds_at(acc, kr[q > 0 ? q - 1 : 0]).x, tx);
+      atomicAdd(&lds_at(acc, kr[q > 0 ? q - 1 : 0]).y, ty);
     }
     tx = (brk ? 0.0f : tx) + c.x;
     ty = (brk ? 0.0f : ty) + c.y;
   }
   // The last row's part continues lane l - 1's when the whole group is that
   // one row; the scan sums each such chain into its last lane.
-  const int kf = static_cast<int>(w[0] >> 16);
-  const int kl = static_cast<int>(w[kTileRun - 1] >> 16);
+  const int kf = static_cast<int>(kr[0]);
+  const int kl = static_cast<int>(kr[kTileRun - 1]);
   const int prev_kl = dpp_i<kDppWaveShr1, 0xf>(kl + 1) - 1;  // -1 on lane 0
   const bool start = !active || kf != kl || kf != prev_kl;
   unsigned int stop = start ? __float_as_uint(1.0f) : 0u;
@@ -315,16 +393,16 @@ __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileSte
 
 // The row block rb's attraction (XCD-aware: block b runs on XCD b % xcds and
 // each XCD takes one contiguous range of row blocks, whose column tiles then
-// stay in its L2).  The block's steps (run, round) are processed two at a
-// time from two register buffers: the next step's loads are issued before
-// the current one is summed, so each wave keeps two groups of entries in
-// flight.  Every load is unconditional and an odd last step is paired with
-// a step that adds nothing (it repeats the last one), so the compiler's wait
-// counts leave the prefetch in flight; every wave runs the same steps (DPP
-// needs whole waves).  Starts and ends with LDS free for the next row block
-// (every thread passes a barrier between its last LDS access and the end).
-template <int NT>
-__device__ __forceinline__ void attract_row_block(int rb, const unsigned int* __restrict__ ent,
+// stay in its L2).  The block's steps (run, round) go through a ring of D
+// register buffers: a buffer is refilled with the step D ahead as soon as it
+// has been summed, so each wave keeps D - 1 groups of slots in flight while
+// it sums one.  Every load is unconditional and the steps past the last
+// repeat it and add nothing, so the compiler's wait counts leave the
+// prefetch in flight; every wave runs the same steps (DPP needs whole
+// waves).  Starts and ends with LDS free for the next row block (every
+// thread passes a barrier between its last LDS access and the end).
+template <int NT, int D>
+__device__ __forceinline__ void attract_row_block(int rb, const unsigned short* __restrict__ ent,
                                                   const float* __restrict__ val, const int* __restrict__ tile_ptr,
                                                   const int* __restrict__ tile_cb, const int* __restrict__ tile_beg,
                                                   const float2* __restrict__ y_cur, float2* __restrict__ attr,
@@ -341,19 +419,24 @@ __device__ __forceinline__ void attract_row_block(int rb, const unsigned int* __
   int steps = 0;
   for (int t = t0; t < t1; ++t) steps += (tile_beg[t + 1] - tile_beg[t] + NT * kTileRun - 1) / (NT * kTileRun);
   if (steps > 0) {
-    TileStep sa{t0, 0, tile_beg[t0], tile_beg[t0 + 1]};
-    TileGroup ga = load_tile_group<NT>(ent, val, sa.e0, sa.e1, sa.round, tid);
-    for (int k = 0; k < steps; k += 2) {
-      const bool b_live = k + 1 < steps;
-      const TileStep sb = b_live ? next_tile_step<NT>(sa, tile_beg, t1) : sa;
-      const TileGroup gb = load_tile_group<NT>(ent, val, sb.e0, sb.e1, sb.round, tid);
-      if (sa.round == 0) stage_tile_columns<NT>(ys, y_cur, tile_cb[sa.t], n, tid);
-      sum_tile_group<NT>(ga, sa, true, tid, yr, ys, acc);
-      const TileStep sc = k + 2 < steps ? next_tile_step<NT>(sb, tile_beg, t1) : sb;
-      ga = load_tile_group<NT>(ent, val, sc.e0, sc.e1, sc.round, tid);
-      if (b_live && sb.round == 0) stage_tile_columns<NT>(ys, y_cur, tile_cb[sb.t], n, tid);
-      sum_tile_group<NT>(gb, sb, b_live, tid, yr, ys, acc);
-      sa = sc;
+    TileStep st[D];
+    TileGroup g[D];
+    st[0] = TileStep{t0, 0, tile_beg[t0], tile_beg[t0 + 1]};
+#pragma unroll
+    for (int d = 1; d < D; ++d) st[d] = d < steps ? next_tile_step<NT>(st[d - 1], tile_beg, t1) : st[d - 1];
+#pragma unroll
+    for (int d = 0; d < D; ++d) g[d] = load_tile_group<NT>(ent, val, st[d].e0, st[d].e1, st[d].round, tid);
+    for (int k = 0; k < steps; k += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const bool live = k + d < steps;
+        if (live && st[d].round == 0) stage_tile_columns<NT>(ys, y_cur, tile_cb[st[d].t], n, tid);
+        sum_tile_group<NT>(g[d], st[d], live, tid, yr, ys, acc);
+        // refill with step k + d + D, whose predecessor is the newest buffer
+        const TileStep newest = st[(d + D - 1) % D];
+        st[d] = k + d + D < steps ? next_tile_step<NT>(newest, tile_beg, t1) : newest;
+        g[d] = load_tile_group<NT>(ent, val, st[d].e0, st[d].e1, st[d].round, tid);
+      }
     }
   }
   __syncthreads();
@@ -368,10 +451,10 @@ __device__ __forceinline__ void attract_row_block(int rb, const unsigned int* __
 // free for kernels that run beside it, and the dynamic claims balance the
 // row blocks' unequal work.  The last workgroup to finish resets work[] (its
 // xcds + 1 counters start and end each launch at zero).  Launch bounds:
-// 2048 / NT blocks per CU, 8 waves per SIMD, as many as the LDS allows.
-template <int NT>
-__global__ __launch_bounds__(NT, 2048 / NT) void k_attract_tiles_seg(
-    const unsigned int* __restrict__ ent, const float* __restrict__ val, const int* __restrict__ tile_ptr,
+// MINB workgroups per CU (the VGPR budget of the D-deep prefetch ring).
+template <int NT, int D, int MINB>
+__global__ __launch_bounds__(NT, MINB) void k_attract_tiles_seg(
+    const unsigned short* __restrict__ ent, const float* __restrict__ val, const int* __restrict__ tile_ptr,
     const int* __restrict__ tile_cb, const int* __restrict__ tile_beg, const float2* __restrict__ y_cur,
     float2* __restrict__ attr, float exaggeration, int n, int row_blocks, int xcds, unsigned int* __restrict__ work) {
   __shared__ float2 ys[kTileCols];
@@ -385,7 +468,7 @@ __global__ __launch_bounds__(NT, 2048 / NT) void k_attract_tiles_seg(
   const int end = min(row_blocks, first + per_xcd);
   int slot = static_cast<int>(blockIdx.x) / xcds;
   while (first + slot < end) {
-    attract_row_block<NT>(first + slot, ent, val, tile_ptr, tile_cb, tile_beg, y_cur, attr, exaggeration, n, ys, yr,
+    attract_row_block<NT, D>(first + slot, ent, val, tile_ptr, tile_cb, tile_beg, y_cur, attr, exaggeration, n, ys, yr,
                           acc);
     if (threadIdx.x == 0) claimed = slots + static_cast<int>(atomicAdd(&work[xcd], 1u));
     __syncthreads();
@@ -419,7 +502,9 @@ void tiles_shape(int n, long long nnz, Tiles& t) {
   t.col_bits = bits_for(t.col_tiles);
   t.key_bits = t.col_bits + bits_for(t.row_blocks);
   t.max_tiles = std::min<long long>(nnz, static_cast<long long>(t.row_blocks) * t.col_tiles);
-  t.padded = nnz + (kTileRun - 1) * t.max_tiles;
+  // a run's rows rise by at most kTileRows - 1, so it holds at most
+  // (kTileRows - 1) / kStepMax bridges, and at most kTileRun - 1 padding slots
+  t.padded = nnz + ((kTileRows - 1) / kStepMax + kTileRun - 1) * t.max_tiles;
 }
 
 hipError_t tiles_temp_bytes(const Tiles& t, std::size_t& bytes) {
@@ -447,10 +532,13 @@ hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream) {
     return hipGetLastError();
   }
   const std::size_t count = static_cast<std::size_t>(t.nnz);
-  // after the sort the key and payload inputs are dead: the run heads and
-  // their scan reuse them
+  // after the sort the key and payload inputs are dead: the run heads, their
+  // scan and each entry's slot count reuse them; after k_tile_meta the sorted
+  // keys are dead and the scan of the slot counts takes their place
   int* heads = reinterpret_cast<int*>(t.key_in);
   int* pos = reinterpret_cast<int*>(t.pay_in);
+  int* slot_count = reinterpret_cast<int*>(t.pay_in) + t.nnz;
+  int* sbeg = reinterpret_cast<int*>(t.key_out);
   const unsigned int eb = build_blocks(t.nnz);
   k_tile_keys<32><<<std::min((p.n + 7) / 8, 65536), kBuildThreads, 0, stream>>>(p.row_ptr, p.col, p.val, p.n,
                                                                                t.col_bits, t.key_in, t.pay_in);
@@ -461,7 +549,7 @@ hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream) {
   e = rocprim::radix_sort_pairs(t.temp, tb, t.key_in, t.key_out, t.pay_in, t.pay_out, count, 0u,
                                 static_cast<unsigned int>(std::max(t.key_bits, 1)), stream);
   if (e != hipSuccess) return e;
-  k_tile_heads<<<eb, kBuildThreads, 0, stream>>>(t.key_out, t.nnz, heads);
+  k_tile_heads<<<eb, kBuildThreads, 0, stream>>>(t.key_out, t.pay_out, t.nnz, heads, slot_count);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   tb = t.temp_bytes;
@@ -469,41 +557,40 @@ hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream) {
   if (e != hipSuccess) return e;
   k_tile_meta<<<eb, kBuildThreads, 0, stream>>>(t.key_out, heads, pos, t.nnz, t.col_bits, t.row_blocks, t.tile_ptr,
                                                 t.tile_cb, t.ubeg, t.tile_count);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  tb = t.temp_bytes;
+  e = rocprim::exclusive_scan(t.temp, tb, slot_count, sbeg, 0, count, rocprim::plus<int>(), stream);
+  if (e != hipSuccess) return e;
   const long long slots = t.max_tiles + 1;
-  k_tile_sizes<<<build_blocks(slots), kBuildThreads, 0, stream>>>(t.ubeg, t.tile_count, slots, t.psize);
+  k_tile_sizes<<<build_blocks(slots), kBuildThreads, 0, stream>>>(t.ubeg, t.tile_count, slots, sbeg, slot_count,
+                                                                  t.nnz, t.psize);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   tb = t.temp_bytes;
   e = rocprim::exclusive_scan(t.temp, tb, t.psize, t.tile_beg, 0, static_cast<std::size_t>(slots),
                               rocprim::plus<int>(), stream);
   if (e != hipSuccess) return e;
-  k_tile_scatter<<<eb, kBuildThreads, 0, stream>>>(t.pay_out, heads, pos, t.ubeg, t.tile_beg, t.nnz, t.ent, t.val);
+  k_tile_scatter<<<eb, kBuildThreads, 0, stream>>>(t.pay_out, heads, pos, t.ubeg, sbeg, t.tile_beg, t.nnz, t.ent,
+                                                   t.val, t.base_row);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  k_tile_bases<<<build_blocks(t.padded / kTileRun + 1), kBuildThreads, 0, stream>>>(t.base_row, t.tile_beg,
+                                                                                    t.tile_count, t.val);
   return hipGetLastError();
 }
 
-hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int threads,
-                                int xcds, int slots_per_xcd, hipStream_t stream) {
+hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds,
+                                int slots_per_xcd, hipStream_t stream) {
   if (t.work == nullptr || xcds < 1 || xcds > kTileMaxXcds) return hipErrorInvalidValue;
   const int per_xcd = (t.row_blocks + xcds - 1) / xcds;
   const int slots = slots_per_xcd > 0 ? std::min(slots_per_xcd, per_xcd) : per_xcd;
   const int blocks = std::max(slots, 1) * xcds;
-#define FEHIP_TILED(NT_)                                                                                        \
-  k_attract_tiles_seg<NT_><<<blocks, NT_, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, \
-                                                       attr, exaggeration, t.n, t.row_blocks, xcds, t.work);
-  switch (threads) {
-    case 256:
-      FEHIP_TILED(256)
-      break;
-    case 512:
-      FEHIP_TILED(512)
-      break;
-    case 1024:
-      FEHIP_TILED(1024)
-      break;
-    default:
-      return hipErrorInvalidValue;
-  }
-#undef FEHIP_TILED
+  constexpr int NT = kTileThreads;
+  // a ring of 2 groups (one in flight while one is summed); deeper rings
+  // measured no faster at config 2, and the LDS allows 3 workgroups per CU
+  k_attract_tiles_seg<NT, 2, 3><<<blocks, NT, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur,
+                                                           attr, exaggeration, t.n, t.row_blocks, xcds, t.work);
   return hipGetLastError();
 }
 

@@ -156,12 +156,11 @@ struct fastembedr_hip_tsne {
   int label_sweeps = 0;
   float2* y_b = nullptr;    // centred layout of the current iteration (also scratch)
   float2* grad = nullptr;
-  // Attraction over tiled P (kernel k_attract_chunks) unless disabled; the
+  // Attraction over tiled P (kernel k_attract_tiles_seg) unless disabled; the
   // tiles follow the working numbering and are rebuilt after it changes.
   bool attract_tiled = true;
-  int tile_threads = 512;
   // Workgroups per CU of the attraction when it runs beside the repulsion
-  // kernels (side stream): fewer than the 4 its LDS allows leave room on
+  // kernels (side stream): fewer than the 3 its LDS allows leave room on
   // every CU for them (2: measured best at config 2).  Alone it takes one
   // workgroup per row block.
   int attract_shared_per_cu = 2;
@@ -386,7 +385,8 @@ bool alloc_tiles(fastembedr_hip_tsne* s) {
   const std::size_t nnz = static_cast<std::size_t>(std::max<long long>(t.nnz, 1));
   const std::size_t padded = static_cast<std::size_t>(std::max<long long>(t.padded, 1));
   const std::size_t slots = static_cast<std::size_t>(t.max_tiles) + 1;
-  const std::size_t bytes = 2 * align_up(padded * 4) + 2 * align_up(nnz * 4) + 2 * align_up(nnz * 8) +
+  const std::size_t bytes = align_up(padded * 2) + align_up(padded * 4) + align_up((padded / 8 + 1) * 2) +
+                            2 * align_up(nnz * 4) + 2 * align_up(nnz * 8) +
                             align_up((static_cast<std::size_t>(t.row_blocks) + 1) * 4) + 4 * align_up(slots * 4) +
                             align_up(4) + align_up((fehip::kTileMaxXcds + 1) * 4) + align_up(temp) + 4096;
   if (!memory_preflight(bytes, "HIP openTSNE attraction tiles") ||
@@ -394,7 +394,7 @@ bool alloc_tiles(fastembedr_hip_tsne* s) {
     return false;
   }
   Arena& a = s->tile_arena;
-  t.ent = a.take<unsigned int>(padded);
+  t.ent = a.take<unsigned short>(padded);
   t.val = a.take<float>(padded);
   t.key_in = a.take<unsigned int>(nnz);
   t.key_out = a.take<unsigned int>(nnz);
@@ -407,6 +407,7 @@ bool alloc_tiles(fastembedr_hip_tsne* s) {
   t.psize = a.take<int>(slots);
   t.tile_count = a.take<int>(1);
   t.work = a.take<unsigned int>(fehip::kTileMaxXcds + 1);
+  t.base_row = a.take<unsigned short>(padded / 8 + 1);
   t.temp = a.take<char>(std::max<std::size_t>(temp, 1));
   t.temp_bytes = temp;
   if (t.temp == nullptr) {
@@ -441,8 +442,7 @@ bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggera
   return s->timed(
       fehip::kKAttract, "attract launch",
       [&] {
-        return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->tile_threads, s->xcds, slots,
-                                           st);
+        return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->xcds, slots, st);
       },
       st);
 }
@@ -997,9 +997,8 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   if (const char* tiled = std::getenv("FASTEMBEDR_HIP_ATTRACT_TILED")) {
     if (std::strcmp(tiled, "0") == 0) s->attract_tiled = false;
   }
-  s->tile_threads = env_int("FASTEMBEDR_HIP_TILE_THREADS", s->tile_threads);
+
   s->attract_shared_per_cu = env_int("FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU", s->attract_shared_per_cu);
-  if (s->tile_threads != 256 && s->tile_threads != 512 && s->tile_threads != 1024) s->tile_threads = 512;
   if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {
     delete s;
     return 1;
@@ -1415,6 +1414,26 @@ int fastembedr_hip_tsne_attraction_info(fastembedr_hip_tsne* s, long long* tiles
     *tiles = count;
   }
   if (renumbers != nullptr) *renumbers = s->renumber_count;
+  return 0;
+}
+
+int fastembedr_hip_tsne_attraction_slots(fastembedr_hip_tsne* s, long long* slots) {
+  if (!valid_state_args(s)) return 1;
+  if (slots == nullptr) {
+    set_error("null pointer");
+    return 1;
+  }
+  *slots = -1;
+  if (s->attract_tiled && s->tiles_for != -2) {
+    int count = 0, total = 0;
+    if (!s->sync_all() ||
+        !hip_ok(hipMemcpy(&count, s->tiles.tile_count, sizeof(int), hipMemcpyDeviceToHost), "hipMemcpy(tiles)") ||
+        !hip_ok(hipMemcpy(&total, s->tiles.tile_beg + count, sizeof(int), hipMemcpyDeviceToHost),
+                "hipMemcpy(slots)")) {
+      return 1;
+    }
+    *slots = total;
+  }
   return 0;
 }
 

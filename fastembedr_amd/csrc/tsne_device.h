@@ -289,17 +289,18 @@ hipError_t launch_gather2(const float2* src, const int* idx, float2* dst, int n,
 // ---- tiled attraction ---------------------------------------------------------
 // P regrouped for the attraction: rows in blocks of kTileRows, columns in
 // tiles of kTileCols.  The entries of one (row block, column tile) pair form
-// one contiguous run ("tile"), in row order; each entry word packs the byte
-// offsets of its local row (high 16 bits) and local column (low 16 bits) in
-// the LDS position arrays (8 bytes per position), next to its value.  A row
-// block's tiles are tile_ptr[rb] .. tile_ptr[rb + 1]; tile t covers entries
-// tile_beg[t] .. tile_beg[t + 1] and column tile tile_cb[t].  Every run
-// starts at a multiple of kTileRun entries and is padded to one with copies
-// of its last entry word of value 0.
-constexpr int kTileRows = 512;
+// one contiguous run ("tile") of slots, in row order: a 16-bit word (local
+// column, row step from the previous slot of its group of kTileRun) and the
+// value, whose two spare top bits carry the group's base row (slot format at
+// attraction_tiles_hip.hip).  A row block's tiles are tile_ptr[rb] ..
+// tile_ptr[rb + 1]; tile t covers slots tile_beg[t] .. tile_beg[t + 1] and
+// column tile tile_cb[t].  Every run starts at a multiple of kTileRun slots
+// and is padded to one with slots of value 0.
+constexpr int kTileRows = 1024;
 constexpr int kTileCols = 4096;
 constexpr int kTileRun = 8;
 constexpr int kTileMaxXcds = 16;
+constexpr int kTileThreads = 512;
 
 struct Tiles {
   int n = 0;
@@ -309,8 +310,8 @@ struct Tiles {
   int col_bits = 0;   // bits of the column-tile part of the sort key
   int key_bits = 0;   // col_bits + bits of the row-block part
   long long max_tiles = 0;
-  long long padded = 0;          // capacity of ent / val: nnz + (kTileRun - 1) * max_tiles
-  unsigned int* ent = nullptr;   // padded
+  long long padded = 0;          // capacity of ent / val: entries + bridges + padding at most
+  unsigned short* ent = nullptr; // padded
   float* val = nullptr;          // padded; 0 in the padding
   int* tile_ptr = nullptr;       // row_blocks + 1
   int* tile_cb = nullptr;        // max_tiles + 1
@@ -318,6 +319,7 @@ struct Tiles {
   int* ubeg = nullptr;           // max_tiles + 1 (begins before padding)
   int* psize = nullptr;          // max_tiles + 1 (padded sizes)
   int* tile_count = nullptr;     // 1
+  unsigned short* base_row = nullptr;  // padded / kTileRun + 1 (build scratch)
   unsigned int* work = nullptr;  // kTileMaxXcds + 1 claim counters of the attraction; zero between launches
   // build scratch, nnz each; after the sort the inputs hold the run heads
   // (key_in) and their scan (pay_in)
@@ -332,12 +334,12 @@ void tiles_shape(int n, long long nnz, Tiles& t);
 hipError_t tiles_temp_bytes(const Tiles& t, std::size_t& bytes);
 // Rebuilds t from the CSR (same numbering), all on `stream`.
 hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream);
-// threads: workgroup size, 256, 512 or 1024.  slots_per_xcd: workgroups per
-// XCD (<= 0: one per row block); with fewer, each claims row blocks of its
-// XCD's range until none is left.  t.work must be zero (it is after a
-// launch); xcds <= kTileMaxXcds.
-hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int threads,
-                                int xcds, int slots_per_xcd, hipStream_t stream);
+// Workgroups of kTileThreads.  slots_per_xcd: workgroups per XCD (<= 0: one
+// per row block); with fewer, each claims row blocks of its XCD's range until
+// none is left.  t.work must be zero (it is after a launch);
+// xcds <= kTileMaxXcds.
+hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds,
+                                int slots_per_xcd, hipStream_t stream);
 
 // ---- exact O(n^2) terms (gradient check and KL) ----------------------------
 hipError_t launch_exact_repulsion(const float2* y, int n, float2* rep, double* z_partial, DeviceScalars* sc,

@@ -155,7 +155,9 @@ class TsneSession:
         t = C.c_longlong()
         r = C.c_int()
         _lib.check(self._lib.fastembedr_hip_tsne_attraction_info(self._h, C.byref(t), C.byref(r)), "attraction_info")
-        return {"tiles": int(t.value), "renumbers": int(r.value)}
+        s = C.c_longlong()
+        _lib.check(self._lib.fastembedr_hip_tsne_attraction_slots(self._h, C.byref(s)), "attraction_slots")
+        return {"tiles": int(t.value), "renumbers": int(r.value), "slots": int(s.value)}
 
     def center(self) -> None:
         _lib.check(self._lib.fastembedr_hip_tsne_center(self._h), "center")

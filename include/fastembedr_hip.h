@@ -183,6 +183,12 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_interp_info(fastembedr_hip_tsne* sess
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_attraction_info(fastembedr_hip_tsne* session, long long* tiles,
                                         int* renumbers);
 
+/* Size of the attraction's tiled P in the current working numbering: slots
+ * (entries, bridge slots between entries more than 15 rows apart, and the
+ * padding of each run to a multiple of 8), -1 when there is none (as for
+ * attraction_info).  No counterpart in the reference. */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_attraction_slots(fastembedr_hip_tsne* session, long long* slots);
+
 /* Exact KL(P || Q) at the current y (src/tsne_neighbors.cpp:1258-1285), with
  * the O(n^2) normalisation computed on the device in fp64. */
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* session, double* kl);

@@ -1,6 +1,7 @@
 """Tiled attraction on the GPU (P regrouped per (row block, column tile) into
-length-ordered pieces, attraction_tiles_hip.hip) against a direct fp64 sum
-over the device's own P, and against the row-parallel CSR kernel.
+runs of 16-bit slot words and values, attraction_tiles_hip.hip) against a
+direct fp64 sum over the device's own P, and against the row-parallel CSR
+kernel.
 
 The attraction alone is read from two gradients at one layout: the repulsion
 does not depend on the exaggeration, so (g(e1) - g(e2)) / (e1 - e2) is
@@ -8,8 +9,9 @@ sum_j p_ij q_ij (y_i - y_j) (src/tsne_neighbors.cpp:985-1012).
 
 Tolerance: relative L2 <= 1e-5 (fp32 sums in another order; the hardware
 reciprocal is within 1 ulp).  The cases cover many tiles per row block, rows
-whose parts in one tile are far longer than a piece (kPieceMax = 8), rows of
-one or two entries, and sizes that are not multiples of the tile shape.
+whose parts in one tile are far longer than a lane's group of 8 slots, rows
+of one or two entries, sparse runs whose rows lie more than 15 apart (bridge
+slots), and sizes that are not multiples of the tile shape.
 """
 
 import sys
@@ -23,7 +25,7 @@ from tests.helpers import rel_l2, small_problem
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
-TILE_ROWS, TILE_COLS = 512, 4096
+TILE_ROWS, TILE_COLS = 1024, 4096
 
 
 def _say(msg):
@@ -100,6 +102,27 @@ def test_tiled_attraction_long_parts(hip):
     rng = np.random.default_rng(3)
     y = (rng.standard_normal((n, 2)) * 3).astype(np.float32)
     _check(hip, idx, dist, 20.0, y, "ring")
+
+
+def scattered_knn(n, k, seed):
+    """k neighbours drawn uniformly from all rows: each (row block, column
+    tile) run holds few entries, so its rows are often more than 15 apart and
+    the slot layout needs bridge slots (and row gaps up to a whole block)."""
+    rng = np.random.default_rng(seed)
+    idx = np.empty((n, k), np.int32)
+    for i in range(n):
+        c = rng.choice(n - 1, size=k, replace=False)
+        idx[i] = c + (c >= i) + 1
+    dist = np.sort(rng.uniform(0.5, 2.0, size=(n, k)), axis=1).astype(np.float32)
+    return np.asfortranarray(idx), np.asfortranarray(dist)
+
+
+def test_tiled_attraction_sparse_runs(hip):
+    _say("case: tiled attraction, scattered neighbours n=60000 k=3 (sparse runs, bridge slots)")
+    n = 60000
+    idx, dist = scattered_knn(n, 3, 11)
+    y = (np.random.default_rng(6).standard_normal((n, 2)) * 5).astype(np.float32)
+    _check(hip, idx, dist, 1.0, y, "scattered")
 
 
 def test_tiled_matches_row_parallel(hip, mixture20k, monkeypatch):
