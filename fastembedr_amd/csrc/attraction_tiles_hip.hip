@@ -340,23 +340,26 @@ __device__ __forceinline__ void stage_tile_columns(float2* ys, const float2* __r
 template <int NT>
 __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileStep& s, bool live, int tid, float2* yr,
                                                float2* ys, float2* acc) {
-  const bool active = live && s.e0 + (s.round * NT + tid) * kTileRun < s.e1;
   const unsigned int wp[4] = {g.w.x, g.w.y, g.w.z, g.w.w};
   const unsigned int pb[kTileRun] = {__float_as_uint(g.p0.x), __float_as_uint(g.p0.y), __float_as_uint(g.p0.z),
                                      __float_as_uint(g.p0.w), __float_as_uint(g.p1.x), __float_as_uint(g.p1.y),
                                      __float_as_uint(g.p1.z), __float_as_uint(g.p1.w)};
   // Row byte offsets (8 bytes per LDS position): the base row from the spare
-  // value bits, then the steps; clamped to the block's rows.
+  // value bits (slot 0's step is 0), then the steps.  A group whose last row
+  // lies past the block (which a layout built here never holds) adds
+  // nothing; its reads stay inside the workgroup's LDS (rows < 1024 + 105).
   unsigned int kr[kTileRun];
-  unsigned int row = 0;
+  unsigned int r8 = 0;
 #pragma unroll
-  for (int q = 0; q < 5; ++q) row |= (pb[q] >> 30) << (2 * q);
+  for (int q = 0; q < 5; ++q) r8 |= (pb[q] >> 30) << (2 * q + 3);
+  kr[0] = r8;
 #pragma unroll
-  for (int q = 0; q < kTileRun; ++q) {
-    const unsigned int word = (q & 1) ? wp[q / 2] >> 16 : wp[q / 2] & 0xffffu;
-    row += word & 0xfu;
-    kr[q] = min(row, static_cast<unsigned int>(kTileRows - 1)) * 8u;
+  for (int q = 1; q < kTileRun; ++q) {
+    const unsigned int step = (q & 1) ? (wp[q / 2] >> 16) & 0xfu : wp[q / 2] & 0xfu;
+    r8 += step << 3;
+    kr[q] = r8;
   }
+  const bool active = live && s.e0 + (s.round * NT + tid) * kTileRun < s.e1 && r8 < kTileRows * 8u;
   float tx = 0.0f, ty = 0.0f;  // the current row's part
 #pragma unroll
   for (int q = 0; q < kTileRun; ++q) {
