@@ -8,7 +8,8 @@
 
 namespace fehip {
 
-constexpr int kKnnMaxDim = 128;    // centred rows and a query block stay in LDS
+constexpr int kKnnMaxDim = 128;    // scanned dimensions: centred rows and a query block stay in LDS
+constexpr int kKnnMaxInputDim = 16384;  // wider rows are scanned in a kKnnMaxDim-dimensional projection
 constexpr int kKnnMaxK = 256;      // the reference's native GPU KNN limit (kMaxNativeCudaK)
 constexpr long long kKnnCandEntries = 1ll << 28;  // candidate buffer entries of a scan launch (2 GiB)
 

@@ -132,6 +132,159 @@ __global__ __launch_bounds__(kPrepThreads) void k_knn_center(const float* __rest
   if ((threadIdx.x & (kWave - 1)) == 0) atomicMax(nrm_max_bits, __float_as_uint(local));
 }
 
+// ---- projection of wide rows -----------------------------------------------------
+// Rows wider than kKnnMaxDim are scanned in a kKnnMaxDim-dimensional
+// subspace.  With Q (d x kKnnMaxDim) of orthonormal columns,
+// |Q^T (x - y)| <= |x - y| for every pair: distances between projected rows
+// bound the true ones from below.  The scan, its screening and its
+// certificate then work on the projected rows (the certificate with a
+// margin for their fp32 rounding), and the final ranking is computed from
+// the input rows in fp64, so the result is the exact KNN whatever Q is.  A Q
+// spanning the data's leading principal directions keeps the bound tight
+// (few candidates, few reruns): it comes from block power iterations on the
+// covariance of a sample of rows.
+
+constexpr int kProjDim = kKnnMaxDim;
+// Certificate margin for projected rows, in units of 2^-23 (|q|^2 + max |r|^2):
+// rounding the fp64 projections to fp32 moves each by at most 2^-24 of its
+// length, which changes a squared distance by at most 2^-22 (|q|^2 + |r|^2);
+// the rest covers the fp64 projection and the basis' departure from exact
+// orthonormality (both below 1e-12 relative).
+constexpr int kProjSlack = 5;
+constexpr int kCovTile = 32;
+constexpr int kCovRows = 64;  // sample rows staged per step
+constexpr int kProjRows = 64;
+constexpr int kProjChunk = 32;
+
+// One 32 x 32 tile (bi, bj), bi <= bj, of the covariance of the centred
+// sample rows s * stride (s < m), fp64, mirrored into the lower tile.  Each
+// thread owns a 2 x 2 block of the tile.
+__global__ __launch_bounds__(256) void k_knn_cov(const float* __restrict__ x, Strides st, int d,
+                                                 const double* __restrict__ mean, int m, long long stride,
+                                                 double* __restrict__ cov) {
+  const int bi = static_cast<int>(blockIdx.y), bj = static_cast<int>(blockIdx.x);
+  if (bj < bi) return;  // whole block
+  __shared__ double a[kCovRows][kCovTile + 1];
+  __shared__ double b[kCovRows][kCovTile + 1];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int ti = tid / 16, tj = tid % 16;
+  double acc00 = 0.0, acc01 = 0.0, acc10 = 0.0, acc11 = 0.0;
+  for (int s0 = 0; s0 < m; s0 += kCovRows) {
+    for (int e = tid; e < kCovRows * kCovTile; e += 256) {
+      const int r = e / kCovTile, c = e % kCovTile;
+      const int s = s0 + r;
+      const int ca = bi * kCovTile + c, cb = bj * kCovTile + c;
+      const long long row = static_cast<long long>(s) * stride;
+      a[r][c] = s < m && ca < d ? static_cast<double>(x[st.at(row, ca)]) - mean[ca] : 0.0;
+      b[r][c] = s < m && cb < d ? static_cast<double>(x[st.at(row, cb)]) - mean[cb] : 0.0;
+    }
+    __syncthreads();
+    for (int r = 0; r < kCovRows; ++r) {
+      const double a0 = a[r][2 * ti], a1 = a[r][2 * ti + 1];
+      const double b0 = b[r][2 * tj], b1 = b[r][2 * tj + 1];
+      acc00 = fma(a0, b0, acc00);
+      acc01 = fma(a0, b1, acc01);
+      acc10 = fma(a1, b0, acc10);
+      acc11 = fma(a1, b1, acc11);
+    }
+    __syncthreads();
+  }
+  const double v[2][2] = {{acc00, acc01}, {acc10, acc11}};
+  for (int u = 0; u < 2; ++u) {
+    for (int w = 0; w < 2; ++w) {
+      const int i = bi * kCovTile + 2 * ti + u, j = bj * kCovTile + 2 * tj + w;
+      if (i < d && j < d) {
+        cov[static_cast<long long>(i) * d + j] = v[u][w];
+        cov[static_cast<long long>(j) * d + i] = v[u][w];
+      }
+    }
+  }
+}
+
+// y = cov q (d x d times d x kProjDim, row-major, fp64).  One block per row
+// of y, one thread per column.
+__global__ __launch_bounds__(kProjDim) void k_knn_cov_times(const double* __restrict__ cov,
+                                                            const double* __restrict__ q, int d,
+                                                            double* __restrict__ y) {
+  const long long i = blockIdx.x;
+  const int j = static_cast<int>(threadIdx.x);
+  double s = 0.0;
+  for (int c = 0; c < d; ++c) s = fma(cov[i * d + c], q[static_cast<long long>(c) * kProjDim + j], s);
+  y[i * kProjDim + j] = s;
+}
+
+// Projected rows: xc row = fl32(Q^T (x - mean)) (fp64 sums), zero in
+// columns kProjDim .. P - 1, with norms, their maximum and the count of
+// non-finite rows exactly as k_knn_center.  A block takes 64 rows; dims are
+// staged 32 at a time (the centred rows and the rows of Q); four threads
+// share a row, 32 outputs each.
+__global__ __launch_bounds__(256) void k_knn_project(const float* __restrict__ x, int n, int n_pad, int d,
+                                                     Strides st, int P, const double* __restrict__ mean,
+                                                     const double* __restrict__ q, float* __restrict__ xc,
+                                                     float* __restrict__ nrm, unsigned int* __restrict__ nrm_max_bits,
+                                                     int* __restrict__ bad_rows) {
+  __shared__ double xs[kProjRows][kProjChunk + 1];
+  __shared__ double qs[kProjChunk][kProjDim];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int r0 = static_cast<int>(blockIdx.x) * kProjRows;
+  const int lr = tid / 4;
+  const int c0 = (tid % 4) * (kProjDim / 4);
+  double acc[kProjDim / 4];
+#pragma unroll
+  for (int j = 0; j < kProjDim / 4; ++j) acc[j] = 0.0;
+  for (int k0 = 0; k0 < d; k0 += kProjChunk) {
+    for (int e = tid; e < kProjRows * kProjChunk; e += 256) {
+      const int rr = e / kProjChunk, cc = e % kProjChunk;
+      const int r = r0 + rr, c = k0 + cc;
+      xs[rr][cc] = r < n && c < d ? static_cast<double>(x[st.at(r, c)]) - mean[c] : 0.0;
+    }
+    for (int e = tid; e < kProjChunk * kProjDim; e += 256) {
+      const int cc = e / kProjDim, j = e % kProjDim;
+      qs[cc][j] = k0 + cc < d ? q[static_cast<long long>(k0 + cc) * kProjDim + j] : 0.0;
+    }
+    __syncthreads();
+    for (int cc = 0; cc < kProjChunk; ++cc) {
+      const double v = xs[lr][cc];
+#pragma unroll
+      for (int j = 0; j < kProjDim / 4; ++j) acc[j] = fma(v, qs[cc][c0 + j], acc[j]);
+    }
+    __syncthreads();
+  }
+  const int r = r0 + lr;
+  double s = 0.0;
+  if (r < n) {
+#pragma unroll
+    for (int j = 0; j < kProjDim / 4; ++j) {
+      const float v = static_cast<float>(acc[j]);
+      xc[static_cast<long long>(r) * P + c0 + j] = v;
+      s += static_cast<double>(v) * static_cast<double>(v);
+    }
+  } else if (r < n_pad) {
+    for (int j = 0; j < kProjDim / 4; ++j) xc[static_cast<long long>(r) * P + c0 + j] = 0.0f;
+  }
+  if (r < n_pad && tid % 4 == 0) {
+    for (int c = kProjDim; c < P; ++c) xc[static_cast<long long>(r) * P + c] = 0.0f;
+  }
+  // the row's four threads are adjacent lanes
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  float local = 0.0f;
+  if (tid % 4 == 0) {
+    if (r < n) {
+      local = static_cast<float>(s);
+      if (!isfinite(local)) {  // NaN/inf input, or a norm beyond fp32
+        atomicAdd(bad_rows, 1);
+        local = 0.0f;
+      }
+      nrm[r] = local;
+    } else if (r < n_pad) {
+      nrm[r] = INFINITY;
+    }
+  }
+  for (int off = kWave / 2; off > 0; off >>= 1) local = fmaxf(local, __shfl_xor(local, off));
+  if ((threadIdx.x & (kWave - 1)) == 0) atomicMax(nrm_max_bits, __float_as_uint(local));
+}
+
 // ---- locality order ----------------------------------------------------------------
 // The scan visits every reference for every query, so its result does not
 // depend on the row order; its cost does, through the number of candidates
@@ -877,6 +1030,7 @@ struct KnnPass {
   int n_out;   // rows of the output (queries)
   int n_scan;  // reference scan positions
   int d, P, chunks, k, exclude_self;
+  int proj_slack;  // certificate margin for projected rows, in units of 2^-23 (|q|^2 + max |r|^2)
   uint2* buf;  // candidate buffers, nq x B
   float* thr;
   int* cnt;
@@ -909,7 +1063,7 @@ hipError_t launch_scan_finalize(const KnnPass& a, int kp, const int* qlist, int 
   hipError_t e = a.chunks <= 16 ? launch_scan<B, 16>(a, kp, qlist, q_offset, nq, stream)
                                 : launch_scan<B, 32>(a, kp, qlist, q_offset, nq, stream);
   if (e != hipSuccess) return e;
-  const float eps_unit = static_cast<float>(4 * a.chunks + 12) * 0x1.0p-23f;
+  const float eps_unit = static_cast<float>(4 * a.chunks + 12 + a.proj_slack) * 0x1.0p-23f;
   k_knn_finalize<B><<<(nq + kKnnWaves - 1) / kKnnWaves, kKnnThreads, 0, stream>>>(
       a.xq_in, a.stq, a.xr_in, a.str, a.n_out, a.d, a.qperm, a.rperm, qlist, q_offset, nq, a.buf, a.thr, a.cnt,
       a.nrm_q, a.nrm_max_bits, eps_unit, a.k, a.exclude_self, a.idx_out, a.dist_out, a.retry, a.retry_count,
@@ -964,6 +1118,85 @@ struct KnnSet {
   int on_device;
 };
 
+// Uniform 64-bit stream (SplitMix64) and standard normals from it
+// (Box-Muller), for the power iterations' fixed start.
+struct ProjRng {
+  std::uint64_t s;
+  std::uint64_t next() {
+    std::uint64_t z = (s += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+  }
+  double uniform() { return (static_cast<double>(next() >> 11) + 0.5) * 0x1.0p-53; }
+  double normal() { return std::sqrt(-2.0 * std::log(uniform())) * std::cos(6.283185307179586 * uniform()); }
+};
+
+// Orthonormal columns for the d x kProjDim row-major matrix y (modified
+// Gram-Schmidt, two passes, fp64).  A column left without a direction of its
+// own (the data's rank below kProjDim) is redrawn at random.
+void proj_orthonormalize(std::vector<double>& y, int d, ProjRng& rng) {
+  constexpr int m = kProjDim;
+  for (int j = 0; j < m; ++j) {
+    for (int attempt = 0;; ++attempt) {
+      double before = 0.0;
+      for (int i = 0; i < d; ++i) before += y[static_cast<std::size_t>(i) * m + j] * y[static_cast<std::size_t>(i) * m + j];
+      for (int pass = 0; pass < 2; ++pass) {
+        for (int k = 0; k < j; ++k) {
+          double dot = 0.0;
+          for (int i = 0; i < d; ++i) dot += y[static_cast<std::size_t>(i) * m + k] * y[static_cast<std::size_t>(i) * m + j];
+          for (int i = 0; i < d; ++i) y[static_cast<std::size_t>(i) * m + j] -= dot * y[static_cast<std::size_t>(i) * m + k];
+        }
+      }
+      double after = 0.0;
+      for (int i = 0; i < d; ++i) after += y[static_cast<std::size_t>(i) * m + j] * y[static_cast<std::size_t>(i) * m + j];
+      if (after > 1e-20 * before && after > 0.0 && std::isfinite(after)) {
+        const double inv = 1.0 / std::sqrt(after);
+        for (int i = 0; i < d; ++i) y[static_cast<std::size_t>(i) * m + j] *= inv;
+        break;
+      }
+      for (int i = 0; i < d; ++i) y[static_cast<std::size_t>(i) * m + j] = rng.normal();
+    }
+  }
+}
+
+// Q (d x kProjDim, orthonormal columns, on the device) spanning the leading
+// principal directions of the rows of x: covariance of up to kProjSample
+// evenly spaced rows, then kProjIters block power iterations from a fixed
+// random start, each followed by an orthonormalisation on the host.
+constexpr int kProjSample = 32768;
+constexpr int kProjIters = 4;
+
+hipError_t knn_projection_basis(const float* x, Strides st, int n, int d, const double* mean, double* q_dev,
+                                hipStream_t stream) {
+  const int m = std::min(n, kProjSample);
+  const long long stride = std::max(1, n / m);
+  DevBuf<double> cov, y_dev;
+  hipError_t e;
+  if ((e = cov.alloc(static_cast<std::size_t>(d) * d)) != hipSuccess ||
+      (e = y_dev.alloc(static_cast<std::size_t>(d) * kProjDim)) != hipSuccess)
+    return e;
+  const int tiles = (d + kCovTile - 1) / kCovTile;
+  k_knn_cov<<<dim3(tiles, tiles), 256, 0, stream>>>(x, st, d, mean, m, stride, cov.p);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  std::vector<double> q(static_cast<std::size_t>(d) * kProjDim);
+  ProjRng rng{0x6b6e6e70726f6aull};
+  for (double& v : q) v = rng.normal();
+  proj_orthonormalize(q, d, rng);
+  const std::size_t bytes = q.size() * sizeof(double);
+  for (int it = 0; it < kProjIters; ++it) {
+    if ((e = hipMemcpyAsync(q_dev, q.data(), bytes, hipMemcpyHostToDevice, stream)) != hipSuccess) return e;
+    k_knn_cov_times<<<d, kProjDim, 0, stream>>>(cov.p, q_dev, d, y_dev.p);
+    if ((e = hipGetLastError()) != hipSuccess ||
+        (e = hipMemcpyAsync(q.data(), y_dev.p, bytes, hipMemcpyDeviceToHost, stream)) != hipSuccess ||
+        (e = hipStreamSynchronize(stream)) != hipSuccess)
+      return e;
+    proj_orthonormalize(q, d, rng);
+  }
+  if ((e = hipMemcpyAsync(q_dev, q.data(), bytes, hipMemcpyHostToDevice, stream)) != hipSuccess) return e;
+  return hipStreamSynchronize(stream);
+}
+
 // The whole search: references `ref`, queries `query` (null: the references
 // themselves, self excluded on request).
 int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_self, int* idx_out_in,
@@ -975,13 +1208,15 @@ int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_se
   const bool self = query == nullptr;
   const int n = ref.n;
   const int n_out = self ? n : query->n;
-  const int P = knn_pitch(d);
-  const int chunks = (d + 3) / 4;
+  const bool project = d > kKnnMaxDim;         // scan a kProjDim-dimensional projection
+  const int ds = project ? kProjDim : d;       // scanned dimensions
+  const int P = knn_pitch(ds);
+  const int chunks = (ds + 3) / 4;
   const int n_pad = (n + kKnnRefTile - 1) / kKnnRefTile * kKnnRefTile;  // whole reference tiles
   hipStream_t stream = nullptr;
   hipError_t e;
   DevBuf<float> xr_dev, xq_dev, xc, nrm, xcq, nrmq, dist_dev;
-  DevBuf<double> partial, mean;
+  DevBuf<double> partial, mean, basis;
   DevBuf<unsigned int> nrm_max;
   DevBuf<int> idx_dev, retry, counters;
   auto upload = [&](const KnnSet& set, DevBuf<float>& dev, const float*& out) -> hipError_t {
@@ -1027,17 +1262,31 @@ int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_se
     return fail("hipMemset", e);
   const Strides str = ref.col_major ? Strides{1, n} : Strides{d, 1};
   const Strides stq = self ? str : (query->col_major ? Strides{1, n_out} : Strides{d, 1});
-  // both sets are centred on the references' column means
+  // both sets are centred on the references' column means (and projected
+  // on the references' leading directions when wider than kKnnMaxDim)
   k_knn_col_partials<<<pblocks, kPrepThreads, 0, stream>>>(xr, n, d, str, rows_per, partial.p);
   k_knn_col_means<<<1, kPrepThreads, 0, stream>>>(partial.p, pblocks, d, n, mean.p);
-  k_knn_center<<<(n_pad + kPrepThreads - 1) / kPrepThreads, kPrepThreads, 0, stream>>>(
-      xr, n, n_pad, d, str, P, mean.p, xc.p, nrm.p, nrm_max.p, counters.p + 2);
+  if (project) {
+    if ((e = basis.alloc(static_cast<std::size_t>(d) * kProjDim)) != hipSuccess) return fail("hipMalloc(KNN basis)", e);
+    if ((e = knn_projection_basis(xr, str, n, d, mean.p, basis.p, stream)) != hipSuccess)
+      return fail("KNN projection basis", e);
+    k_knn_project<<<(n_pad + kProjRows - 1) / kProjRows, 256, 0, stream>>>(xr, n, n_pad, d, str, P, mean.p, basis.p,
+                                                                          xc.p, nrm.p, nrm_max.p, counters.p + 2);
+  } else {
+    k_knn_center<<<(n_pad + kPrepThreads - 1) / kPrepThreads, kPrepThreads, 0, stream>>>(
+        xr, n, n_pad, d, str, P, mean.p, xc.p, nrm.p, nrm_max.p, counters.p + 2);
+  }
   if (!self) {
     if ((e = hipMemsetAsync(xcq.p + static_cast<std::size_t>(n_out) * P, 0, kKnnOverRead * sizeof(float), stream)) !=
         hipSuccess)
       return fail("hipMemset", e);
-    k_knn_center<<<(n_out + kPrepThreads - 1) / kPrepThreads, kPrepThreads, 0, stream>>>(
-        xq, n_out, n_out, d, stq, P, mean.p, xcq.p, nrmq.p, nrm_max.p + 1, counters.p + 2);
+    if (project) {
+      k_knn_project<<<(n_out + kProjRows - 1) / kProjRows, 256, 0, stream>>>(
+          xq, n_out, n_out, d, stq, P, mean.p, basis.p, xcq.p, nrmq.p, nrm_max.p + 1, counters.p + 2);
+    } else {
+      k_knn_center<<<(n_out + kPrepThreads - 1) / kPrepThreads, kPrepThreads, 0, stream>>>(
+          xq, n_out, n_out, d, stq, P, mean.p, xcq.p, nrmq.p, nrm_max.p + 1, counters.p + 2);
+    }
   }
   if ((e = hipGetLastError()) != hipSuccess) return fail("KNN prep launch", e);
   {
@@ -1168,6 +1417,7 @@ int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_se
   pass.d = d;
   pass.P = P;
   pass.chunks = chunks;
+  pass.proj_slack = project ? kProjSlack : 0;
   pass.k = k;
   pass.exclude_self = self ? exclude_self : 0;
   pass.buf = buf.p;
@@ -1198,8 +1448,16 @@ int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_se
     }
     if (host_counts[0] == 0) break;
     if (kp == kKnnMaxCand) {
-      err = "exact KNN could not certify " + std::to_string(host_counts[0]) + " rows: more than " +
-            std::to_string(kKnnMaxCand) + " points lie within fp32 resolution of their k-th neighbour distance";
+      if (project) {
+        err = "exact KNN could not certify " + std::to_string(host_counts[0]) + " rows of " + std::to_string(d) +
+              " dimensions: their projection on " + std::to_string(kProjDim) +
+              " leading directions, which the search scans, keeps too little of their spread to bound the k-th "
+              "neighbour within " +
+              std::to_string(kKnnMaxCand) + " candidates (nearly isotropic data); reduce the dimension first";
+      } else {
+        err = "exact KNN could not certify " + std::to_string(host_counts[0]) + " rows: more than " +
+              std::to_string(kKnnMaxCand) + " points lie within fp32 resolution of their k-th neighbour distance";
+      }
       return 1;
     }
     // rerun the uncertified rows with twice the candidates
@@ -1248,8 +1506,8 @@ bool knn_common_checks(const float* x, int n, int d, int k, const void* idx, con
     err = "invalid KNN dimensions (need n >= 1, d >= 1, k >= 1)";
     return false;
   }
-  if (d > kKnnMaxDim) {
-    err = "exact KNN supports up to " + std::to_string(kKnnMaxDim) + " dimensions";
+  if (d > kKnnMaxInputDim) {
+    err = "exact KNN supports up to " + std::to_string(kKnnMaxInputDim) + " dimensions";
     return false;
   }
   if (k > kKnnMaxK) {

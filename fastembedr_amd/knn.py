@@ -24,7 +24,7 @@ import numpy as np
 from . import _lib
 from .device import DeviceBuffer, DeviceMatrix
 
-MAX_DIM = 128   # kKnnMaxDim in csrc/knn_device.h
+MAX_DIM = 16384  # kKnnMaxInputDim in csrc/knn_device.h (rows wider than 128 are scanned in a projection)
 MAX_K = 256     # kKnnMaxK in csrc/knn_device.h
 ENGINE = "native_hip_exact_mfma_l2"
 

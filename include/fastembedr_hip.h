@@ -270,7 +270,9 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_p_build_ms(const fastembedr_hip_tsne*
  *   x            n x d float32: row-major, or column-major (an R matrix) when
  *                x_col_major; device memory when x_on_device
  *   k            1 .. min(256, n - 1) with exclude_self (n without)
- *   d            1 .. 128
+ *   d            1 .. 16384; rows wider than 128 are scanned in their
+ *                projection on 128 leading principal directions (a lower
+ *                bound of every distance) and ranked exactly in full width
  *   indices      n x k column-major (neighbour j of row i at j * n + i),
  *                1-based; device memory when output_on_device
  *   distances    same layout, sqrt of the squared distance
@@ -296,7 +298,7 @@ FASTEMBEDR_HIP_API int fastembedr_hip_knn_exact(const float* x, int n, int d, in
  *   reference    n_reference x d float32, query n_query x d float32, both
  *                row-major or both column-major (col_major); both in device
  *                memory when inputs_on_device
- *   k            1 .. min(256, n_reference);  d  1 .. 128
+ *   k            1 .. min(256, n_reference);  d  1 .. 16384 (as above)
  *   indices      n_query x k column-major, 1-based rows of reference; device
  *                memory when output_on_device
  *   distances    same layout

@@ -5,7 +5,8 @@ tests/testthat/helper-knn.R:5-38).
 The bar: indices identical to the oracle's (ties by index included),
 distances within 2e-6 relative (fp32 square roots of fp64 squared
 distances).  Cases: row- and column-major input, self excluded or not, odd
-and small d, d above 64, k = n - 1, sizes off the tile shapes, lattice data
+and small d, d above 64, d above 128 (scanned in a projection: low-rank
+data up to d = 784 and isotropic data), k = n - 1, sizes off the tile shapes, lattice data
 with duplicates and long runs of exact ties (which take the rerun path with a
 larger candidate set), device input and device-resident output, the
 reference's argument errors, and a large input checked on sampled rows
@@ -76,6 +77,51 @@ def test_wide_rows(hip, n, d, k):
     _say(f"case: wide rows n={n} d={d} k={k}")
     x = _gauss(n, d, seed=d)
     _check(hip.exact_knn(x, k), x, k)
+
+
+def _low_rank(n, d, rank, seed, noise=0.05, components=8):
+    """Rows on a few clusters of a rank-`rank` subspace of R^d plus small
+    isotropic noise: the spectrum of image or expression data, whose leading
+    principal directions carry most of the variance."""
+    rng = np.random.default_rng(seed)
+    basis = np.linalg.qr(rng.normal(size=(d, rank)))[0]
+    centres = rng.normal(scale=4.0, size=(components, rank))
+    z = centres[rng.integers(0, components, size=n)] + rng.normal(size=(n, rank))
+    return (z @ basis.T + rng.normal(scale=noise, size=(n, d)) + 3.0).astype(np.float32)
+
+
+@pytest.mark.parametrize("n,d,k,rank", [(3000, 300, 20, 24), (1500, 784, 30, 60), (5000, 784, 90, 50),
+                                        (1000, 129, 10, 129)])
+def test_rows_wider_than_the_scan(hip, n, d, k, rank):
+    # d > 128: the scan runs on the projection on 128 leading directions (a
+    # lower bound of every distance); the ranking is exact in full width.
+    # rank = d is isotropic data, where the projection keeps most but not
+    # all of the variance and rows take the rerun path.
+    _say(f"case: exact KNN of rows wider than the scan n={n} d={d} k={k} rank={rank}")
+    x = _low_rank(n, d, rank, seed=d) if rank < d else _gauss(n, d, seed=d)
+    res = hip.exact_knn(x, k)
+    _say(f"  stats {res.stats}")
+    _check(res, x, k)
+    res_c = hip.exact_knn(np.asfortranarray(x), k, exclude_self=False)
+    _check(res_c, x, k, exclude_self=False)
+
+
+def test_wide_isotropic_rows_are_refused_not_approximated(hip):
+    # 200 isotropic dimensions: the 128 leading directions keep ~64 % of the
+    # spread, too little to certify k = 60 within the largest candidate set,
+    # so the search reports it instead of returning an uncertified result.
+    _say("case: exact KNN of isotropic rows n=3000 d=200 k=60 (not certifiable)")
+    with pytest.raises(_lib.HipBackendError, match="reduce the dimension"):
+        hip.exact_knn(_gauss(3000, 200, seed=3), 60)
+    x = _gauss(400, 9, seed=4)
+    _check(hip.exact_knn(x, 5), x, 5)  # the library still works afterwards
+
+
+def test_query_rows_wider_than_the_scan(hip):
+    _say("case: query KNN of rows wider than the scan n_ref=2000 n_q=400 d=512 k=15")
+    x = _low_rank(2400, 512, 40, seed=3)
+    ref, qry = x[:2000], x[2000:]
+    _check_query(hip.exact_query_knn(ref, qry, 15), ref, qry, 15)
 
 
 def test_k_is_n_minus_one(hip):
@@ -168,7 +214,7 @@ def test_errors(hip):
     with pytest.raises(_lib.HipBackendError, match="k exceeds"):
         hip.exact_knn(x, 10, exclude_self=True)
     with pytest.raises(_lib.HipBackendError, match="dimensions"):
-        hip.exact_knn(_gauss(50, 129, seed=2), 5)
+        hip.exact_knn(_gauss(20, 16385, seed=2), 5)
     with pytest.raises(_lib.HipBackendError, match="k up to"):
         hip.exact_knn(_gauss(400, 3, seed=2), 257)
     bad = _gauss(300, 5, seed=4)
