@@ -59,12 +59,15 @@ SIGNATURES = {
                                             _P, _P, _P]),
     "fastembedr_hip_knn_exact": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _LLP]),
     "fastembedr_hip_knn_query": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _I, _LLP]),
+    "fastembedr_hip_knn_exact_metric": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _LLP]),
+    "fastembedr_hip_knn_query_metric": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _LLP]),
     "fastembedr_hip_structure_metrics": (_I, [_P, _I, _I, _P, _I, _P, _I, _P]),
 }
 
 REPULSION_GRID = 0
 REPULSION_EXACT = 1
 REPULSION_LAGRANGE = 2
+KNN_METRICS = {"euclidean": 0, "cosine": 1, "correlation": 2}  # FASTEMBEDR_HIP_KNN_*
 
 
 class HipBackendUnavailable(RuntimeError):

@@ -1526,16 +1526,27 @@ int fastembedr_hip_tsne_p_build_ms(const fastembedr_hip_tsne* s, double* ms) {
   return 0;
 }
 
-int fastembedr_hip_knn_exact(const float* x, int n, int d, int x_col_major, int k, int exclude_self, int x_on_device,
-                             int* indices, float* distances, int output_on_device, long long* stats) {
+static_assert(FASTEMBEDR_HIP_KNN_EUCLIDEAN == fehip::kKnnEuclidean && FASTEMBEDR_HIP_KNN_COSINE == fehip::kKnnCosine &&
+                  FASTEMBEDR_HIP_KNN_CORRELATION == fehip::kKnnCorrelation,
+              "metric codes of the C ABI and the search agree");
+
+int fastembedr_hip_knn_exact_metric(const float* x, int n, int d, int x_col_major, int k, int exclude_self,
+                                    int metric, int x_on_device, int* indices, float* distances,
+                                    int output_on_device, long long* stats) {
   g_last_error.clear();
   std::string err;
-  if (fehip::knn_exact_run(x, n, d, x_col_major, k, exclude_self, x_on_device, indices, distances, output_on_device,
-                           stats, err) != 0) {
+  if (fehip::knn_exact_run(x, n, d, x_col_major, k, exclude_self, metric, x_on_device, indices, distances,
+                           output_on_device, stats, err) != 0) {
     set_error("fastembedr_hip_knn_exact: " + err);
     return 1;
   }
   return 0;
+}
+
+int fastembedr_hip_knn_exact(const float* x, int n, int d, int x_col_major, int k, int exclude_self, int x_on_device,
+                             int* indices, float* distances, int output_on_device, long long* stats) {
+  return fastembedr_hip_knn_exact_metric(x, n, d, x_col_major, k, exclude_self, FASTEMBEDR_HIP_KNN_EUCLIDEAN,
+                                         x_on_device, indices, distances, output_on_device, stats);
 }
 
 int fastembedr_hip_structure_metrics(const double* high, int n, int p_high, const double* low, int p_low,
@@ -1549,17 +1560,25 @@ int fastembedr_hip_structure_metrics(const double* high, int n, int p_high, cons
   return 0;
 }
 
-int fastembedr_hip_knn_query(const float* reference, int n_reference, const float* query, int n_query, int d,
-                             int col_major, int k, int inputs_on_device, int* indices, float* distances,
-                             int output_on_device, long long* stats) {
+int fastembedr_hip_knn_query_metric(const float* reference, int n_reference, const float* query, int n_query,
+                                    int d, int col_major, int k, int metric, int inputs_on_device, int* indices,
+                                    float* distances, int output_on_device, long long* stats) {
   g_last_error.clear();
   std::string err;
-  if (fehip::knn_query_run(reference, n_reference, query, n_query, d, col_major, k, inputs_on_device, indices,
-                           distances, output_on_device, stats, err) != 0) {
+  if (fehip::knn_query_run(reference, n_reference, query, n_query, d, col_major, k, metric, inputs_on_device,
+                           indices, distances, output_on_device, stats, err) != 0) {
     set_error("fastembedr_hip_knn_query: " + err);
     return 1;
   }
   return 0;
+}
+
+int fastembedr_hip_knn_query(const float* reference, int n_reference, const float* query, int n_query, int d,
+                             int col_major, int k, int inputs_on_device, int* indices, float* distances,
+                             int output_on_device, long long* stats) {
+  return fastembedr_hip_knn_query_metric(reference, n_reference, query, n_query, d, col_major, k,
+                                         FASTEMBEDR_HIP_KNN_EUCLIDEAN, inputs_on_device, indices, distances,
+                                         output_on_device, stats);
 }
 
 }  // extern "C"

@@ -28,15 +28,21 @@ struct Strides {
 // last pass's candidates per query, 64-row reference tiles staged (summed
 // over blocks of 128 queries) and tiles computed (summed over waves of 32
 // queries) after pruning.  Returns 0, or 1 with err set.
-int knn_exact_run(const float* x, int n, int d, int x_col_major, int k, int exclude_self, int input_on_device,
-                  int* indices, float* distances, int output_on_device, long long* stats, std::string& err);
+// metric: kKnnEuclidean, or kKnnCosine / kKnnCorrelation (rows normalised,
+// centred first for correlation, and distances written as 1 - cos).
+constexpr int kKnnEuclidean = 0;
+constexpr int kKnnCosine = 1;
+constexpr int kKnnCorrelation = 2;
+int knn_exact_run(const float* x, int n, int d, int x_col_major, int k, int exclude_self, int metric,
+                  int input_on_device, int* indices, float* distances, int output_on_device, long long* stats,
+                  std::string& err);
 
 // k nearest references of every query row: ref (n_ref x d) and query
 // (n_query x d), both fp32 in the same layout (column-major when col_major)
 // and residency; k <= n_ref.  Writes n_query x k column-major 1-based
 // reference indices and fp32 distances; stats as above.
 int knn_query_run(const float* ref, int n_ref, const float* query, int n_query, int d, int col_major, int k,
-                  int input_on_device, int* indices, float* distances, int output_on_device, long long* stats,
-                  std::string& err);
+                  int metric, int input_on_device, int* indices, float* distances, int output_on_device,
+                  long long* stats, std::string& err);
 
 }  // namespace fehip

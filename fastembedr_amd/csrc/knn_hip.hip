@@ -132,6 +132,39 @@ __global__ __launch_bounds__(kPrepThreads) void k_knn_center(const float* __rest
   if ((threadIdx.x & (kWave - 1)) == 0) atomicMax(nrm_max_bits, __float_as_uint(local));
 }
 
+// ---- cosine and correlation ------------------------------------------------------
+// The reference searches these metrics as Euclidean distances between rows
+// normalised to unit length, centred first for correlation
+// (src/native_knn_common.h:50-67, 119-120), and reports half the squared
+// distance, 1 - cos (:122-128; src/embedding_cuda_kernels.cpp:1441-1442).
+// One row per thread, in the reference's operation order: row mean as a
+// sequential fp64 sum / d, fl32(x - mean), sequential fp64 sum of the
+// squares of the stored values, inverse norm fl32(1 / sqrt(sum)), and each
+// value times it in fp32; a row whose sum of squares is 0 stays as it is.
+// Output row-major n x d.
+__global__ __launch_bounds__(kPrepThreads) void k_knn_normalize_rows(const float* __restrict__ x, int n, int d,
+                                                                    Strides st, int center,
+                                                                    float* __restrict__ out) {
+#pragma clang fp contract(off)
+  const int r = static_cast<int>(blockIdx.x) * kPrepThreads + threadIdx.x;
+  if (r >= n) return;
+  double mean = 0.0;
+  if (center) {
+    for (int j = 0; j < d; ++j) mean += static_cast<double>(x[st.at(r, j)]);
+    mean /= static_cast<double>(d);
+  }
+  float* row = out + static_cast<long long>(r) * d;
+  double sq = 0.0;
+  for (int j = 0; j < d; ++j) {
+    const float v = static_cast<float>(static_cast<double>(x[st.at(r, j)]) - mean);
+    row[j] = v;
+    sq += static_cast<double>(v) * static_cast<double>(v);
+  }
+  if (sq <= 0.0) return;
+  const float inv = static_cast<float>(1.0 / sqrt(sq));
+  for (int j = 0; j < d; ++j) row[j] = row[j] * inv;
+}
+
 // ---- projection of wide rows -----------------------------------------------------
 // Rows wider than kKnnMaxDim are scanned in a kKnnMaxDim-dimensional
 // subspace.  With Q (d x kKnnMaxDim) of orthonormal columns,
@@ -951,8 +984,8 @@ __global__ __launch_bounds__(kKnnThreads) void k_knn_finalize(
     const int* __restrict__ qperm, const int* __restrict__ rperm, const int* __restrict__ qlist, int q_offset,
     int nq, const uint2* __restrict__ buf, const float* __restrict__ thr_in, const int* __restrict__ cnt_in,
     const float* __restrict__ nrm_q, const unsigned int* __restrict__ nrm_max_bits, float eps_unit, int k,
-    int exclude_self, int* __restrict__ idx_out, float* __restrict__ dist_out, int* __restrict__ retry,
-    int* __restrict__ retry_count, int* __restrict__ short_rows) {
+    int exclude_self, int half_squared, int* __restrict__ idx_out, float* __restrict__ dist_out,
+    int* __restrict__ retry, int* __restrict__ retry_count, int* __restrict__ short_rows) {
   constexpr int PER = B / kWave;
   const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
   const int p = static_cast<int>(blockIdx.x) * kKnnWaves + static_cast<int>(threadIdx.x) / kWave;
@@ -992,7 +1025,7 @@ __global__ __launch_bounds__(kKnnThreads) void k_knn_finalize(
     const int e = j * kWave + lane;
     if (e < k && e < valid) {
       idx_out[static_cast<long long>(e) * n_out + q] = id[j] + 1;
-      dist_out[static_cast<long long>(e) * n_out + q] = static_cast<float>(sqrt(dd[j]));
+      dist_out[static_cast<long long>(e) * n_out + q] = static_cast<float>(half_squared ? 0.5 * dd[j] : sqrt(dd[j]));
     }
     if (j == (k - 1) / kWave) d2k = dd[j];
   }
@@ -1011,6 +1044,102 @@ __global__ __launch_bounds__(kKnnThreads) void k_knn_finalize(
     }
   }
 }
+
+// ---- full pass for the rows no candidate set certifies -------------------------------
+// A row whose k-th neighbour has more than the largest candidate set of
+// references within fp32 resolution of it (a zero row under cosine is
+// equidistant from every other row), or whose projection bounds its
+// distances too loosely, is ranked by a full pass over the references:
+// squared distances in fp64 exactly as k_knn_finalize forms them, and the
+// (d2, index) pairs below the running k-th kept in an LDS buffer, sorted and
+// cut to k whenever the next 256 could overflow it.  Exact by construction
+// (nothing below the k-th is ever dropped).  One workgroup per row.
+constexpr int kBruteBuf = 2048;
+
+__device__ void brute_sort(double* key, int* ids, int count) {
+  for (int e = count + static_cast<int>(threadIdx.x); e < kBruteBuf; e += kKnnThreads) {
+    key[e] = INFINITY;
+    ids[e] = INT_MAX;
+  }
+  __syncthreads();
+  for (int size = 2; size <= kBruteBuf; size <<= 1) {
+    for (int dist = size >> 1; dist > 0; dist >>= 1) {
+      for (int e = threadIdx.x; e < kBruteBuf / 2; e += kKnnThreads) {
+        const int lo = 2 * e - (e & (dist - 1));
+        const int hi = lo + dist;
+        const bool asc = (lo & size) == 0;
+        const double ka = key[lo], kb = key[hi];
+        const int ia = ids[lo], ib = ids[hi];
+        const bool a_gt = ka > kb || (ka == kb && ia > ib);
+        if (a_gt == asc) {
+          key[lo] = kb;
+          key[hi] = ka;
+          ids[lo] = ib;
+          ids[hi] = ia;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__global__ __launch_bounds__(kKnnThreads) void k_knn_brute(const int* __restrict__ list,
+                                                           const float* __restrict__ xq_in, Strides stq,
+                                                           const float* __restrict__ xr_in, Strides str, int n_ref,
+                                                           int d, const int* __restrict__ qperm, int k,
+                                                           int exclude_self, int half_squared, int n_out,
+                                                           int* __restrict__ idx_out, float* __restrict__ dist_out) {
+  __shared__ double key[kBruteBuf];
+  __shared__ int ids[kBruteBuf];
+  __shared__ int count;
+  __shared__ double tau_d;
+  __shared__ int tau_i;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int qid = list[blockIdx.x];
+  const int q = qperm != nullptr ? qperm[qid] : qid;
+  if (tid == 0) {
+    count = 0;
+    tau_d = INFINITY;
+    tau_i = INT_MAX;
+  }
+  __syncthreads();
+  for (int j0 = 0; j0 < n_ref; j0 += kKnnThreads) {
+    const int r = j0 + tid;
+    if (r < n_ref && !(exclude_self && r == q)) {
+      double s = 0.0;
+      for (int t = 0; t < d; ++t) {
+        const double diff = static_cast<double>(xq_in[stq.at(q, t)]) - static_cast<double>(xr_in[str.at(r, t)]);
+        s = fma(diff, diff, s);
+      }
+      if (s < tau_d || (s == tau_d && r < tau_i)) {
+        const int slot = atomicAdd(&count, 1);
+        key[slot] = s;
+        ids[slot] = r;
+      }
+    }
+    __syncthreads();
+    if (count > kBruteBuf - kKnnThreads) {  // block-uniform
+      brute_sort(key, ids, count);
+      if (tid == 0) {
+        count = k;
+        tau_d = key[k - 1];
+        tau_i = ids[k - 1];
+      }
+    }
+    __syncthreads();
+  }
+  const int c = count;
+  brute_sort(key, ids, c);
+  for (int e = tid; e < k && e < c; e += kKnnThreads) {
+    idx_out[static_cast<long long>(e) * n_out + q] = ids[e] + 1;
+    dist_out[static_cast<long long>(e) * n_out + q] = static_cast<float>(half_squared ? 0.5 * key[e] : sqrt(key[e]));
+  }
+}
+
+// Rows times references times dimensions up to which the rows left
+// uncertified by the largest candidate set go through k_knn_brute (about a
+// second); beyond it the call fails rather than run for minutes.
+constexpr double kBruteBudget = 2e11;
 
 // Everything one scan + finalize pass over a list of queries needs.
 struct KnnPass {
@@ -1031,6 +1160,7 @@ struct KnnPass {
   int n_scan;  // reference scan positions
   int d, P, chunks, k, exclude_self;
   int proj_slack;  // certificate margin for projected rows, in units of 2^-23 (|q|^2 + max |r|^2)
+  int half_squared;  // distances written as d^2 / 2 (cosine, correlation) instead of d
   uint2* buf;  // candidate buffers, nq x B
   float* thr;
   int* cnt;
@@ -1066,7 +1196,8 @@ hipError_t launch_scan_finalize(const KnnPass& a, int kp, const int* qlist, int 
   const float eps_unit = static_cast<float>(4 * a.chunks + 12 + a.proj_slack) * 0x1.0p-23f;
   k_knn_finalize<B><<<(nq + kKnnWaves - 1) / kKnnWaves, kKnnThreads, 0, stream>>>(
       a.xq_in, a.stq, a.xr_in, a.str, a.n_out, a.d, a.qperm, a.rperm, qlist, q_offset, nq, a.buf, a.thr, a.cnt,
-      a.nrm_q, a.nrm_max_bits, eps_unit, a.k, a.exclude_self, a.idx_out, a.dist_out, a.retry, a.retry_count,
+      a.nrm_q, a.nrm_max_bits, eps_unit, a.k, a.exclude_self, a.half_squared, a.idx_out, a.dist_out, a.retry,
+      a.retry_count,
       a.short_rows);
   return hipGetLastError();
 }
@@ -1199,7 +1330,7 @@ hipError_t knn_projection_basis(const float* x, Strides st, int n, int d, const 
 
 // The whole search: references `ref`, queries `query` (null: the references
 // themselves, self excluded on request).
-int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_self, int* idx_out_in,
+int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_self, int metric, int* idx_out_in,
             float* dist_out_in, int output_on_device, long long* stats, std::string& err) {
   auto fail = [&](const std::string& what, hipError_t e) {
     err = what + ": " + hipGetErrorString(e);
@@ -1232,6 +1363,27 @@ int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_se
   const float* xq = nullptr;
   if ((e = upload(ref, xr_dev, xr)) != hipSuccess) return fail("KNN reference upload", e);
   if (!self && (e = upload(*query, xq_dev, xq)) != hipSuccess) return fail("KNN query upload", e);
+  // cosine / correlation: the search runs on the normalised rows (row-major)
+  DevBuf<float> xr_unit, xq_unit;
+  bool ref_col_major = ref.col_major != 0;
+  bool query_col_major = !self && query->col_major != 0;
+  if (metric != kKnnEuclidean) {
+    const int center = metric == kKnnCorrelation ? 1 : 0;
+    if ((e = xr_unit.alloc(static_cast<std::size_t>(n) * d)) != hipSuccess ||
+        (!self && (e = xq_unit.alloc(static_cast<std::size_t>(n_out) * d)) != hipSuccess))
+      return fail("hipMalloc(KNN normalised rows)", e);
+    k_knn_normalize_rows<<<(n + kPrepThreads - 1) / kPrepThreads, kPrepThreads, 0, stream>>>(
+        xr, n, d, ref_col_major ? Strides{1, n} : Strides{d, 1}, center, xr_unit.p);
+    xr = xr_unit.p;
+    ref_col_major = false;
+    if (!self) {
+      k_knn_normalize_rows<<<(n_out + kPrepThreads - 1) / kPrepThreads, kPrepThreads, 0, stream>>>(
+          xq, n_out, d, query_col_major ? Strides{1, n_out} : Strides{d, 1}, center, xq_unit.p);
+      xq = xq_unit.p;
+      query_col_major = false;
+    }
+    if ((e = hipGetLastError()) != hipSuccess) return fail("KNN normalisation launch", e);
+  }
   int* idx_out = idx_out_in;
   float* dist_out = dist_out_in;
   if (!output_on_device) {
@@ -1260,8 +1412,8 @@ int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_se
       (e = hipMemsetAsync(xc.p + static_cast<std::size_t>(n_pad) * P, 0, kKnnOverRead * sizeof(float), stream)) !=
           hipSuccess)
     return fail("hipMemset", e);
-  const Strides str = ref.col_major ? Strides{1, n} : Strides{d, 1};
-  const Strides stq = self ? str : (query->col_major ? Strides{1, n_out} : Strides{d, 1});
+  const Strides str = ref_col_major ? Strides{1, n} : Strides{d, 1};
+  const Strides stq = self ? str : (query_col_major ? Strides{1, n_out} : Strides{d, 1});
   // both sets are centred on the references' column means (and projected
   // on the references' leading directions when wider than kKnnMaxDim)
   k_knn_col_partials<<<pblocks, kPrepThreads, 0, stream>>>(xr, n, d, str, rows_per, partial.p);
@@ -1418,6 +1570,7 @@ int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_se
   pass.P = P;
   pass.chunks = chunks;
   pass.proj_slack = project ? kProjSlack : 0;
+  pass.half_squared = metric != kKnnEuclidean ? 1 : 0;
   pass.k = k;
   pass.exclude_self = self ? exclude_self : 0;
   pass.buf = buf.p;
@@ -1448,15 +1601,29 @@ int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_se
     }
     if (host_counts[0] == 0) break;
     if (kp == kKnnMaxCand) {
+      const int nr = host_counts[0];
+      if (static_cast<double>(nr) * n * d <= kBruteBudget) {
+        // the rest by a full pass each
+        k_knn_brute<<<nr, kKnnThreads, 0, stream>>>(retry.p, pass.xq_in, pass.stq, pass.xr_in, pass.str, n, d,
+                                                     pass.qperm, k, pass.exclude_self, pass.half_squared, n_out,
+                                                     idx_out, dist_out);
+        if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(stream)) != hipSuccess)
+          return fail("KNN full pass", e);
+        retried += nr;
+        ++passes;
+        break;
+      }
       if (project) {
-        err = "exact KNN could not certify " + std::to_string(host_counts[0]) + " rows of " + std::to_string(d) +
+        err = "exact KNN could not certify " + std::to_string(nr) + " rows of " + std::to_string(d) +
               " dimensions: their projection on " + std::to_string(kProjDim) +
               " leading directions, which the search scans, keeps too little of their spread to bound the k-th "
               "neighbour within " +
-              std::to_string(kKnnMaxCand) + " candidates (nearly isotropic data); reduce the dimension first";
+              std::to_string(kKnnMaxCand) + " candidates (nearly isotropic data), and a full pass over " +
+              std::to_string(n) + " references for each would exceed the time budget; reduce the dimension first";
       } else {
-        err = "exact KNN could not certify " + std::to_string(host_counts[0]) + " rows: more than " +
-              std::to_string(kKnnMaxCand) + " points lie within fp32 resolution of their k-th neighbour distance";
+        err = "exact KNN could not certify " + std::to_string(nr) + " rows: more than " +
+              std::to_string(kKnnMaxCand) + " points lie within fp32 resolution of their k-th neighbour distance, "
+              "and a full pass for each would exceed the time budget";
       }
       return 1;
     }
@@ -1497,9 +1664,14 @@ int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_se
   return 0;
 }
 
-bool knn_common_checks(const float* x, int n, int d, int k, const void* idx, const void* dist, std::string& err) {
+bool knn_common_checks(const float* x, int n, int d, int k, int metric, const void* idx, const void* dist,
+                       std::string& err) {
   if (x == nullptr || idx == nullptr || dist == nullptr) {
     err = "null KNN pointer";
+    return false;
+  }
+  if (metric != kKnnEuclidean && metric != kKnnCosine && metric != kKnnCorrelation) {
+    err = "Native HIP KNN does not support this metric (euclidean, cosine or correlation)";
     return false;
   }
   if (n < 1 || d < 1 || k < 1) {
@@ -1523,9 +1695,10 @@ bool knn_common_checks(const float* x, int n, int d, int k, const void* idx, con
 
 }  // namespace
 
-int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int exclude_self, int input_on_device,
-                  int* idx_out_in, float* dist_out_in, int output_on_device, long long* stats, std::string& err) {
-  if (!knn_common_checks(x_in, n, d, k, idx_out_in, dist_out_in, err)) return 1;
+int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int exclude_self, int metric,
+                  int input_on_device, int* idx_out_in, float* dist_out_in, int output_on_device, long long* stats,
+                  std::string& err) {
+  if (!knn_common_checks(x_in, n, d, k, metric, idx_out_in, dist_out_in, err)) return 1;
   if (n < 2) {
     err = "invalid KNN dimensions (need n >= 2, d >= 1, k >= 1)";
     return 1;
@@ -1535,13 +1708,13 @@ int knn_exact_run(const float* x_in, int n, int d, int x_col_major, int k, int e
     return 1;
   }
   const KnnSet ref{x_in, n, x_col_major, input_on_device};
-  return knn_run(ref, nullptr, d, k, exclude_self, idx_out_in, dist_out_in, output_on_device, stats, err);
+  return knn_run(ref, nullptr, d, k, exclude_self, metric, idx_out_in, dist_out_in, output_on_device, stats, err);
 }
 
 int knn_query_run(const float* ref_in, int n_ref, const float* query_in, int n_query, int d, int col_major, int k,
-                  int input_on_device, int* idx_out, float* dist_out, int output_on_device, long long* stats,
-                  std::string& err) {
-  if (!knn_common_checks(ref_in, n_ref, d, k, idx_out, dist_out, err)) return 1;
+                  int metric, int input_on_device, int* idx_out, float* dist_out, int output_on_device,
+                  long long* stats, std::string& err) {
+  if (!knn_common_checks(ref_in, n_ref, d, k, metric, idx_out, dist_out, err)) return 1;
   if (query_in == nullptr) {
     err = "null KNN pointer";
     return 1;
@@ -1556,7 +1729,7 @@ int knn_query_run(const float* ref_in, int n_ref, const float* query_in, int n_q
   }
   const KnnSet ref{ref_in, n_ref, col_major, input_on_device};
   const KnnSet query{query_in, n_query, col_major, input_on_device};
-  return knn_run(ref, &query, d, k, 0, idx_out, dist_out, output_on_device, stats, err);
+  return knn_run(ref, &query, d, k, 0, metric, idx_out, dist_out, output_on_device, stats, err);
 }
 
 }  // namespace fehip

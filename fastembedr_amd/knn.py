@@ -2,7 +2,7 @@
 
 ``precompute_knn()`` follows R/native_knn.R:237-331 of tkcaccia/fastEmbedR
 (argument meaning, the ``1 <= k <= n - 1`` rule and its message, self always
-excluded, the result's fields) for the Euclidean metric.  Where the reference
+excluded, the result's fields) for the Euclidean, cosine and correlation metrics.  Where the reference
 routes CUDA to a FAISS GPU brute force below 100,000 rows and to cuVS
 IVF-Flat above (R/native_knn.R:99-126), this build runs one exact search for
 every size: fastembedr_hip_knn_exact, an MFMA brute force whose results are
@@ -104,16 +104,34 @@ def _prepare(data):
     return x.ctypes.data, x.shape[0], x.shape[1], 0, 0, x
 
 
-def exact_knn(data, k: int, exclude_self: bool = True, keep_device: bool = False) -> KnnResult:
-    """Exact Euclidean KNN of the rows of ``data`` among themselves.
+def _metric_code(metric) -> tuple[str, int]:
+    """The reference's metric argument (match.arg: the first of a vector) and
+    its code; "inner_product" is CUDA-only in the reference and refused."""
+    if isinstance(metric, (list, tuple)):
+        metric = metric[0]
+    name = str(metric)
+    if name == "inner_product":
+        raise ValueError("Native HIP KNN does not support this metric; raw inner product is CUDA-only "
+                         "in the reference.")
+    if name not in _lib.KNN_METRICS:
+        raise ValueError("`metric` must be one of \"euclidean\", \"cosine\", \"correlation\", \"inner_product\".")
+    return name, _lib.KNN_METRICS[name]
+
+
+def exact_knn(data, k: int, exclude_self: bool = True, keep_device: bool = False,
+              metric: str = "euclidean") -> KnnResult:
+    """Exact KNN of the rows of ``data`` among themselves: Euclidean, or
+    cosine / correlation (rows normalised, centred first for correlation, as
+    the reference does; distances 1 - cos).
 
     ``data`` is an (n, d) array (float32 is used as is, row- or column-major;
     other numeric types are converted) or a DeviceMatrix already on the GPU.
     With ``exclude_self`` the row itself never appears; without it, it
     competes at distance 0 like any duplicate.  Raises HipBackendError for
-    inputs the kernels do not take (d > 128, k > 256, k beyond the candidate
+    inputs the kernels do not take (d > 16384, k > 256, k beyond the candidate
     count, non-finite values).
     """
+    metric, code = _metric_code(metric)
     ptr, n, d, col_major, on_device, keep = _prepare(data)
     k = int(k)
     lib = _lib.load()
@@ -127,20 +145,23 @@ def exact_knn(data, k: int, exclude_self: bool = True, keep_device: bool = False
             raise _lib.HipBackendError(f"HIP exact KNN failed: exact KNN supports k up to {MAX_K}")
         dev_idx = DeviceBuffer((k, n), np.int32)
         dev_dist = DeviceBuffer((k, n), np.float32)
-        rc = lib.fastembedr_hip_knn_exact(C.c_void_p(ptr), n, d, col_major, k, int(bool(exclude_self)), on_device,
-                                          C.c_void_p(dev_idx.address), C.c_void_p(dev_dist.address), 1, stats)
+        rc = lib.fastembedr_hip_knn_exact_metric(C.c_void_p(ptr), n, d, col_major, k, int(bool(exclude_self)), code,
+                                                 on_device, C.c_void_p(dev_idx.address),
+                                                 C.c_void_p(dev_dist.address), 1, stats)
         _lib.check(rc, "HIP exact KNN")
         res = KnnResult(n, k, device_indices=dev_idx, device_distances=dev_dist, result_residency="hip")
     else:
         idx = np.empty((max(k, 0), n), np.int32)
         dist = np.empty((max(k, 0), n), np.float32)
-        rc = lib.fastembedr_hip_knn_exact(C.c_void_p(ptr), n, d, col_major, k, int(bool(exclude_self)), on_device,
-                                          C.c_void_p(idx.ctypes.data), C.c_void_p(dist.ctypes.data), 0, stats)
+        rc = lib.fastembedr_hip_knn_exact_metric(C.c_void_p(ptr), n, d, col_major, k, int(bool(exclude_self)), code,
+                                                 on_device, C.c_void_p(idx.ctypes.data),
+                                                 C.c_void_p(dist.ctypes.data), 0, stats)
         _lib.check(rc, "HIP exact KNN")
         res = KnnResult(n, k, indices=idx.T, distances=dist.T)
     del keep
     res.elapsed_sec = time.perf_counter() - t0
     res.exclude_self = bool(exclude_self)
+    res.metric = metric
     res.stats = dict(rerun_rows=int(stats[0]), passes=int(stats[1]), candidates=int(stats[2]),
                      tiles_staged=int(stats[3]), tiles_computed=int(stats[4]))
     return res
@@ -168,10 +189,12 @@ def _prepare_pair(reference, query):
     return rp, nr, qp, nq, dr, rcm, 0, (rkeep, qkeep)
 
 
-def exact_query_knn(reference, query, k: int, keep_device: bool = False) -> KnnResult:
-    """Exact Euclidean KNN of every row of ``query`` among the rows of
-    ``reference`` (fastembedr_hip_knn_query).  Indices are 1-based rows of
-    ``reference``; the result has one row per query."""
+def exact_query_knn(reference, query, k: int, keep_device: bool = False, metric: str = "euclidean") -> KnnResult:
+    """Exact KNN of every row of ``query`` among the rows of ``reference``
+    (fastembedr_hip_knn_query_metric), Euclidean or cosine / correlation as
+    exact_knn.  Indices are 1-based rows of ``reference``; the result has one
+    row per query."""
+    metric, code = _metric_code(metric)
     rp, nr, qp, nq, d, col_major, on_device, keep = _prepare_pair(reference, query)
     k = int(k)
     lib = _lib.load()
@@ -185,20 +208,23 @@ def exact_query_knn(reference, query, k: int, keep_device: bool = False) -> KnnR
             raise _lib.HipBackendError(f"HIP exact query KNN failed: exact KNN supports k up to {MAX_K}")
         dev_idx = DeviceBuffer((k, nq), np.int32)
         dev_dist = DeviceBuffer((k, nq), np.float32)
-        rc = lib.fastembedr_hip_knn_query(C.c_void_p(rp), nr, C.c_void_p(qp), nq, d, col_major, k, on_device,
-                                          C.c_void_p(dev_idx.address), C.c_void_p(dev_dist.address), 1, stats)
+        rc = lib.fastembedr_hip_knn_query_metric(C.c_void_p(rp), nr, C.c_void_p(qp), nq, d, col_major, k, code,
+                                                 on_device, C.c_void_p(dev_idx.address),
+                                                 C.c_void_p(dev_dist.address), 1, stats)
         _lib.check(rc, "HIP exact query KNN")
         res = KnnResult(nq, k, device_indices=dev_idx, device_distances=dev_dist, result_residency="hip")
     else:
         idx = np.empty((max(k, 0), nq), np.int32)
         dist = np.empty((max(k, 0), nq), np.float32)
-        rc = lib.fastembedr_hip_knn_query(C.c_void_p(rp), nr, C.c_void_p(qp), nq, d, col_major, k, on_device,
-                                          C.c_void_p(idx.ctypes.data), C.c_void_p(dist.ctypes.data), 0, stats)
+        rc = lib.fastembedr_hip_knn_query_metric(C.c_void_p(rp), nr, C.c_void_p(qp), nq, d, col_major, k, code,
+                                                 on_device, C.c_void_p(idx.ctypes.data),
+                                                 C.c_void_p(dist.ctypes.data), 0, stats)
         _lib.check(rc, "HIP exact query KNN")
         res = KnnResult(nq, k, indices=idx.T, distances=dist.T)
     del keep
     res.elapsed_sec = time.perf_counter() - t0
     res.exclude_self = False
+    res.metric = metric
     res.stats = dict(rerun_rows=int(stats[0]), passes=int(stats[1]), candidates=int(stats[2]),
                      tiles_staged=int(stats[3]), tiles_computed=int(stats[4]))
     return res
@@ -208,15 +234,12 @@ def precompute_query_knn(reference, query, k: int = 30, metric: str = "euclidean
                          n_cores=None, keep_device: bool = False) -> KnnResult:
     """Nearest reference rows of every query row (R's
     ``precompute_query_knn()``, R/native_knn.R:333-416): one-based indices
-    into ``reference``, self not excluded.  Only the Euclidean metric and the
-    HIP backend are part of this build."""
+    into ``reference``, self not excluded.  Metrics "euclidean", "cosine" and
+    "correlation" on the HIP backend."""
     if str(backend).lower() != "hip":
         raise ValueError(f'backend "{backend}" is not part of this build; only backend = "hip" is provided. '
                          "No CPU fallback is used for HIP-labelled runs.")
-    if isinstance(metric, (list, tuple)):
-        metric = metric[0]
-    if str(metric) != "euclidean":
-        raise ValueError(f'metric "{metric}" is not part of this build; only "euclidean" is provided.')
+    metric, _ = _metric_code(metric)
     n_ref = reference.n if isinstance(reference, DeviceMatrix) else len(reference)
     try:
         k_int = int(k)
@@ -225,7 +248,7 @@ def precompute_query_knn(reference, query, k: int = 30, metric: str = "euclidean
         ok = False
     if not ok or k_int < 1 or k_int > n_ref:
         raise ValueError("`k` must be one integer between 1 and nrow(reference).")
-    res = exact_query_knn(reference, query, k_int, keep_device=keep_device)
+    res = exact_query_knn(reference, query, k_int, keep_device=keep_device, metric=metric)
     res.n_reference = n_ref
     res.backend_requested = "hip"
     return res
@@ -236,18 +259,16 @@ def precompute_knn(data, k: int = 30, metric: str = "euclidean", backend: str = 
     """Nearest neighbours of every observation, itself excluded (R's
     ``precompute_knn()``, R/native_knn.R:237-331).
 
-    Only ``metric = "euclidean"`` and ``backend = "hip"`` are part of this
-    build; ``n_cores`` is accepted and ignored, as by the reference's GPU
+    Metrics "euclidean", "cosine" and "correlation" on ``backend = "hip"``
+    ("inner_product" is CUDA-only in the reference and refused); ``n_cores``
+    is accepted and ignored, as by the reference's GPU
     backends.  ``keep_device=True`` leaves the result on the GPU, as the
     reference's CUDA route does.
     """
     if str(backend).lower() != "hip":
         raise ValueError(f'backend "{backend}" is not part of this build; only backend = "hip" is provided. '
                          "No CPU fallback is used for HIP-labelled runs.")
-    if isinstance(metric, (list, tuple)):
-        metric = metric[0]
-    if str(metric) != "euclidean":
-        raise ValueError(f'metric "{metric}" is not part of this build; only "euclidean" is provided.')
+    metric, _ = _metric_code(metric)
     n = data.n if isinstance(data, DeviceMatrix) else len(data)
     try:
         k_int = int(k)
@@ -256,6 +277,6 @@ def precompute_knn(data, k: int = 30, metric: str = "euclidean", backend: str = 
         ok = False
     if not ok or k_int < 1 or k_int >= n:
         raise ValueError("`k` must be one integer between 1 and nrow(data) - 1.")
-    res = exact_knn(data, k_int, exclude_self=True, keep_device=keep_device)
+    res = exact_knn(data, k_int, exclude_self=True, keep_device=keep_device, metric=metric)
     res.backend_requested = "hip"
     return res

@@ -309,6 +309,26 @@ FASTEMBEDR_HIP_API int fastembedr_hip_knn_query(const float* reference, int n_re
                                                 int* indices, float* distances, int output_on_device,
                                                 long long* stats);
 
+/* The same two searches with the reference's other exact metrics
+ * (native_cuda_knn_cpp / native_cuda_query_knn_cpp with metric = "cosine" or
+ * "correlation", src/native_knn_cuda_impl.cpp:514-560, 875-886): rows are
+ * normalised to unit length, centred first for correlation, in the
+ * reference's operation order (src/native_knn_common.h:50-67), searched by
+ * Euclidean distance, and reported as half the squared distance, 1 - cos
+ * (src/native_knn_common.h:119-128; src/embedding_cuda_kernels.cpp:1441-1442).
+ * metric: one of the FASTEMBEDR_HIP_KNN_* codes; "inner_product" (CUDA-only
+ * in the reference) is refused.  Other arguments as above. */
+#define FASTEMBEDR_HIP_KNN_EUCLIDEAN 0
+#define FASTEMBEDR_HIP_KNN_COSINE 1
+#define FASTEMBEDR_HIP_KNN_CORRELATION 2
+FASTEMBEDR_HIP_API int fastembedr_hip_knn_exact_metric(const float* x, int n, int d, int x_col_major, int k,
+                                                       int exclude_self, int metric, int x_on_device, int* indices,
+                                                       float* distances, int output_on_device, long long* stats);
+FASTEMBEDR_HIP_API int fastembedr_hip_knn_query_metric(const float* reference, int n_reference, const float* query,
+                                                       int n_query, int d, int col_major, int k, int metric,
+                                                       int inputs_on_device, int* indices, float* distances,
+                                                       int output_on_device, long long* stats);
+
 /* Replaces exact_structure_metrics_cpp (src/embedding_utils.cpp:1582-1752),
  * which R's evaluate_embedding() calls on a row sample
  * (R/evaluate_embedding.R:483-500): trustworthiness, continuity, k-NN

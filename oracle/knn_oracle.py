@@ -26,6 +26,13 @@ Pins (tests/test_knn_oracle.py): scipy's cKDTree on tie-free data, a
 pure-Python brute force (sorted by (d2, index)) on tiny inputs with
 duplicates and lattice ties, and the invariants of the result; the same for
 the query-to-reference search (exact_query_knn).
+
+Cosine and correlation (normalize_rows, metric_knn): the reference
+normalises each fp32 row to unit length, centring it first for correlation
+(src/native_knn_common.h:50-67), searches by Euclidean distance and reports
+half the squared distance, 1 - cos (:119-128).  Pinned against scipy's
+``cdist`` cosine and correlation distances, which compute 1 - cos on their
+own, and by the invariants of unit rows.
 """
 
 from __future__ import annotations
@@ -166,3 +173,35 @@ def to_reference_layout(indices: np.ndarray, distances: np.ndarray):
     as (k, n) C-order arrays whose bytes are that layout."""
     return (np.ascontiguousarray((indices + 1).T, dtype=np.int32),
             np.ascontiguousarray(distances.T, dtype=np.float32))
+
+
+def normalize_rows(x, center: bool):
+    """Rows of ``x`` (cast to fp32) normalised as src/native_knn_common.h:50-67
+    does it: mean = sequential fp64 sum / d (centre only), v = fl32(x - mean),
+    s = sequential fp64 sum of v^2, and when s > 0 each v times
+    fl32(1 / sqrt(s)) in fp32; a row with s = 0 is left as it is."""
+    x32 = np.asarray(x, dtype=np.float32)
+    x64 = x32.astype(np.float64)
+    n, d = x32.shape
+    mean = np.cumsum(x64, axis=1)[:, -1] / max(1, d) if center else np.zeros(n)  # cumsum sums in order
+    v = (x64 - mean[:, None]).astype(np.float32)
+    sq = np.cumsum(v.astype(np.float64) ** 2, axis=1)[:, -1]  # squares of fp32 values are exact in fp64
+    inv = np.ones(n, np.float32)
+    pos = sq > 0
+    inv[pos] = (1.0 / np.sqrt(sq[pos])).astype(np.float32)
+    return np.where(pos[:, None], v * inv[:, None], v).astype(np.float32)
+
+
+def metric_knn(x, k: int, metric: str, exclude_self: bool = True, query=None):
+    """Exact KNN under "euclidean", "cosine" or "correlation": indices as
+    exact_knn / exact_query_knn of the (normalised) rows, distances sqrt(d2)
+    for euclidean and d2 / 2 = 1 - cos otherwise."""
+    if metric == "euclidean":
+        return exact_knn(x, k, exclude_self=exclude_self) if query is None else exact_query_knn(x, query, k)
+    center = {"cosine": False, "correlation": True}[metric]
+    xn = normalize_rows(x, center)
+    if query is None:
+        idx, dist = exact_knn(xn, k, exclude_self=exclude_self)
+    else:
+        idx, dist = exact_query_knn(xn, normalize_rows(query, center), k)
+    return idx, 0.5 * dist * dist

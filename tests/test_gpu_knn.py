@@ -106,13 +106,25 @@ def test_rows_wider_than_the_scan(hip, n, d, k, rank):
     _check(res_c, x, k, exclude_self=False)
 
 
-def test_wide_isotropic_rows_are_refused_not_approximated(hip):
+def test_wide_isotropic_rows(hip):
     # 200 isotropic dimensions: the 128 leading directions keep ~64 % of the
-    # spread, too little to certify k = 60 within the largest candidate set,
-    # so the search reports it instead of returning an uncertified result.
-    _say("case: exact KNN of isotropic rows n=3000 d=200 k=60 (not certifiable)")
+    # spread, too little to certify k = 60 within the largest candidate set;
+    # those rows are ranked by a full pass over the references instead.
+    _say("case: exact KNN of isotropic rows n=3000 d=200 k=60 (full pass for uncertified rows)")
+    x = _gauss(3000, 200, seed=3)
+    res = hip.exact_knn(x, 60)
+    _say(f"  stats {res.stats}")
+    assert res.stats["rerun_rows"] > 0
+    _check(res, x, 60)
+
+
+def test_wide_isotropic_rows_beyond_the_full_pass_budget_are_refused(hip):
+    # 20000 x 600 isotropic rows: no candidate set certifies them and a full
+    # pass for each (2.4e11 row-reference-dimension steps) exceeds the time
+    # budget, so the search refuses instead of returning an unproven result.
+    _say("case: exact KNN of isotropic rows n=20000 d=600 k=30 (refused)")
     with pytest.raises(_lib.HipBackendError, match="reduce the dimension"):
-        hip.exact_knn(_gauss(3000, 200, seed=3), 60)
+        hip.exact_knn(_gauss(20000, 600, seed=5), 30)
     x = _gauss(400, 9, seed=4)
     _check(hip.exact_knn(x, 5), x, 5)  # the library still works afterwards
 
@@ -122,6 +134,49 @@ def test_query_rows_wider_than_the_scan(hip):
     x = _low_rank(2400, 512, 40, seed=3)
     ref, qry = x[:2000], x[2000:]
     _check_query(hip.exact_query_knn(ref, qry, 15), ref, qry, 15)
+
+
+@pytest.mark.parametrize("metric", ["cosine", "correlation"])
+@pytest.mark.parametrize("n,d,k", [(2500, 20, 15), (800, 300, 10)])
+def test_cosine_and_correlation(hip, metric, n, d, k):
+    # rows normalised on the device in the reference's operation order
+    # (bit-identical to the oracle's), then the exact search; distances are
+    # 1 - cos = d^2 / 2.  Row scales vary over four orders of magnitude, a
+    # zero row and (for correlation) a constant row are included.
+    _say(f"case: exact KNN metric={metric} n={n} d={d} k={k}")
+    rng = np.random.default_rng(n + d)
+    x = (rng.normal(size=(n, d)) + rng.uniform(-1, 1, size=(1, d))).astype(np.float32)
+    x *= rng.uniform(0.01, 100.0, size=(n, 1)).astype(np.float32)
+    x[7] = 0.0
+    x[8] = 2.5
+    ref_i, ref_d = knn_oracle.metric_knn(x, k, metric)
+    for layout in (np.ascontiguousarray, np.asfortranarray):
+        res = hip.precompute_knn(layout(x), k=k, metric=metric)
+        assert res.metric == metric
+        got_i = np.asarray(res.indices) - 1
+        bad = np.nonzero((got_i != ref_i).any(axis=1))[0]
+        assert bad.size == 0, f"{bad.size} rows differ, first {bad[:5]}"
+        np.testing.assert_allclose(np.asarray(res.distances), ref_d, rtol=DIST_RTOL, atol=1e-7)
+    q = (rng.normal(size=(200, d))).astype(np.float32)
+    qi, qd = knn_oracle.metric_knn(x, k, metric, query=q)
+    qres = hip.precompute_query_knn(x, q, k=k, metric=metric)
+    np.testing.assert_array_equal(np.asarray(qres.indices) - 1, qi)
+    np.testing.assert_allclose(np.asarray(qres.distances), qd, rtol=DIST_RTOL, atol=1e-7)
+
+
+def test_metric_errors(hip):
+    _say("case: KNN metric errors")
+    x = _gauss(50, 4, seed=1)
+    with pytest.raises(ValueError, match="CUDA-only"):
+        hip.precompute_knn(x, k=3, metric="inner_product")
+    with pytest.raises(ValueError, match="must be one of"):
+        hip.exact_knn(x, 3, metric="manhattan")
+    lib = _lib.load()
+    idx = np.empty((3, 50), np.int32)
+    dist = np.empty((3, 50), np.float32)
+    assert lib.fastembedr_hip_knn_exact_metric(x.ctypes.data, 50, 4, 0, 3, 1, 7, 0, idx.ctypes.data,
+                                               dist.ctypes.data, 0, None) == 1
+    assert "metric" in _lib.last_error()
 
 
 def test_k_is_n_minus_one(hip):

@@ -114,3 +114,44 @@ def test_query_knn_matches_kdtree_and_brute_force():
         order = sorted(range(60), key=lambda j: (d2[j], j))[:8]
         np.testing.assert_array_equal(qi[i], order)
         np.testing.assert_allclose(qd[i], np.sqrt(d2[order]), atol=1e-12)
+
+
+@pytest.mark.parametrize("metric", ["cosine", "correlation"])
+def test_metric_distances_match_scipy(metric):
+    from scipy.spatial.distance import cdist
+
+    rng = np.random.default_rng(41)
+    x = (rng.normal(size=(300, 17)) + rng.uniform(-2, 2, size=(1, 17))).astype(np.float32)
+    idx, dist = knn_oracle.metric_knn(x, 12, metric)
+    full = cdist(x.astype(np.float64), x.astype(np.float64), metric=metric)  # 1 - cos, computed independently
+    np.fill_diagonal(full, np.inf)
+    want_i = np.argsort(full, axis=1, kind="stable")[:, :12]
+    np.testing.assert_allclose(dist, np.take_along_axis(full, want_i, 1), rtol=0, atol=2e-6)
+    # the order may differ from scipy's only where two distances agree to fp32 rounding
+    differ = idx != want_i
+    if differ.any():
+        r, c = np.nonzero(differ)
+        np.testing.assert_allclose(full[r, idx[r, c]], full[r, want_i[r, c]], atol=2e-6)
+    q = (rng.normal(size=(40, 17))).astype(np.float32)
+    qi, qd = knn_oracle.metric_knn(x, 5, metric, query=q)
+    qfull = cdist(q.astype(np.float64), x.astype(np.float64), metric=metric)
+    np.testing.assert_allclose(qd, np.sort(qfull, axis=1)[:, :5], atol=2e-6)
+
+
+def test_normalize_rows_invariants():
+    rng = np.random.default_rng(42)
+    x = rng.normal(size=(200, 9)).astype(np.float32) * rng.uniform(0.1, 100, size=(200, 1)).astype(np.float32)
+    x[5] = 0.0          # a zero row stays zero
+    x[6] = 3.25         # a constant row: zero after centring
+    xc = knn_oracle.normalize_rows(x, center=False)
+    xr = knn_oracle.normalize_rows(x, center=True)
+    norms = np.linalg.norm(xc.astype(np.float64), axis=1)
+    assert np.all(xc[5] == 0) and np.all(xr[6] == 0)
+    keep = np.ones(200, bool)
+    keep[5] = False
+    np.testing.assert_allclose(norms[keep], 1.0, atol=1e-6)
+    keep[6] = False
+    np.testing.assert_allclose(np.linalg.norm(xr[keep].astype(np.float64), axis=1), 1.0, atol=1e-6)
+    np.testing.assert_allclose(xr[keep].astype(np.float64).mean(axis=1), 0.0, atol=1e-6)
+    # a row's direction, not its scale, is what is kept
+    np.testing.assert_allclose(knn_oracle.normalize_rows(4.0 * x[:3], False), xc[:3], atol=1e-7)
