@@ -1534,7 +1534,9 @@ int knn_run(const KnnSet& ref, const KnnSet* query, int d, int k, int exclude_se
   // kKnnCandEntries in all; a pass launches as many queries at once as they
   // allow (one launch for the whole input up to millions of rows, so that
   // the grid is many rounds of workgroups deep).
-  int kp = std::min(kKnnMaxCand, k + std::max(32, k / 2) + (self ? 1 : 0));
+  // (projected rows: the bound is looser by the spread outside the
+  // projection, so the first pass starts with twice the margin)
+  int kp = std::min(kKnnMaxCand, k + (project ? 2 : 1) * std::max(32, k / 2) + (self ? 1 : 0));
   const std::size_t entries = std::min<std::size_t>(
       kKnnCandEntries, static_cast<std::size_t>(n_out) * static_cast<std::size_t>(buffer_for(kp)));
   auto batch_for = [&](int kp_) {
