@@ -62,8 +62,13 @@ def _check(hip, idx, dist, perplexity, y, label):
         s.set_state(y)
         att = attraction_device(s)
         row_ptr, col, val = s.csr()
-        tiles = s.attraction_info()["tiles"]
+        info = s.attraction_info()
+        tiles = info["tiles"]
     n = y.shape[0]
+    # slots: every entry, the bridges between entries more than 15 rows apart
+    # within a run (at most 1023 // 15 per run) and each run's padding to 8
+    assert info["slots"] % 8 == 0
+    assert len(col) <= info["slots"] <= len(col) + (1023 // 15 + 7) * info["tiles"]
     ref = attraction_numpy(row_ptr, col, val, y)
     rows = np.repeat(np.arange(n), np.diff(row_ptr))
     want_tiles = len(np.unique((rows // TILE_ROWS).astype(np.int64) * (1 << 20) + col // TILE_COLS))
