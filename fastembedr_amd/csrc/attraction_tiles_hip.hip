@@ -46,7 +46,7 @@ namespace {
 // normalised joint distribution built from validated distances, so every
 // value lies in [0, 1] and bits 30 and 31 of its pattern are zero.  Those
 // bits of slots 0..4 of a group hold the group's base row (the local row of
-// its first slot, 9 bits), 2 bits per slot.  Steps above 15 are made of
+// its first slot, 10 bits), 2 bits per slot.  Steps above 15 are made of
 // bridge slots (p = 0) 15 rows apart; a run's padding repeats its last slot
 // with step 0 and p = 0.  Bridges and padding add nothing.
 static_assert(kTileRun == 8, "a lane reads its group as one 16-byte vector of words and two of values");

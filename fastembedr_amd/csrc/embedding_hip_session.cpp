@@ -1299,16 +1299,19 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
   // Interpolation grid: the FFT length must hold 2 * nodes, and the node
   // count is set on the device each iteration.  The host learns the box
   // count of earlier iterations through a pinned ring and bounds the current
-  // one: with the step clip a coordinate moves at most max_step_norm per
-  // iteration, so the span grows by at most 2 max_step_norm.  It runs at most
-  // kMaxLag iterations ahead of what it knows (none without the clip).
+  // one.  With the step clip a point moves at most max_step_norm per
+  // iteration and so does the mean, so a centred coordinate moves at most
+  // 2 max_step_norm; the span runs from the smallest to the largest centred
+  // coordinate over both axes, so it grows by at most 4 max_step_norm.  It
+  // runs at most kMaxLag iterations ahead of what it knows (none without the
+  // clip).
   const bool lg = s->repulsion == FASTEMBEDR_HIP_REPULSION_LAGRANGE;
   constexpr int kRing = fastembedr_hip_tsne::kLgRing;
   constexpr int kMaxLag = 3;
   static_assert(kMaxLag + 2 <= kRing, "ring slots outlive the lag");
   const int allowed_lag = up.clip ? kMaxLag : 0;
   const double growth =
-      up.clip ? 2.0 * (static_cast<double>(max_step_norm) * 1.0001 + 1e-3) / static_cast<double>(s->lg_ints_per_unit)
+      up.clip ? 4.0 * (static_cast<double>(max_step_norm) * 1.0001 + 1e-3) / static_cast<double>(s->lg_ints_per_unit)
               : 0.0;
   int known_boxes = 0;
   int known_it = 0;

@@ -144,6 +144,51 @@ def test_interp_fft_length_follows_growing_span(hip, prob, clip):
     assert info["boxes"] >= 342 and info["fft_len"] == 4096
 
 
+def _drifting(y0, span):
+    """A layout with a long right tail in x and a long lower tail in y, and an
+    update that moves the bulk by (-3.4, 3.4) while the largest x moves +5 in
+    x and the smallest y moves -5 in y: the mean moves, so the centred extremes
+    move by up to 2 max_step_norm each and the two-axis span grows ~17 boxes
+    per iteration (against the 10 that a one-axis bound of 2 max_step_norm
+    allows)."""
+    y = (y0 - y0.mean(axis=0)).astype(np.float64)
+    y[:, 0] += 0.6 * np.abs(y[:, 0])
+    y[:, 1] -= 0.6 * np.abs(y[:, 1])
+    y -= y.mean(axis=0)
+    y = (y * (span / float(y.max() - y.min()))).astype(np.float32)
+    u = np.tile(np.array([-3.4, 3.4], np.float32), (len(y), 1))
+    u[np.argmax(y[:, 0])] = (5.0, 0.0)
+    u[np.argmin(y[:, 1])] = (0.0, -5.0)
+    return y, u
+
+
+def test_interp_fft_length_bound_holds_for_drifting_layout(hip, prob):
+    """The lagged FFT-length bound with a drifting layout: from 300 boxes the
+    span reaches ~351 boxes (1053 nodes, FFT length 4096) after 3 iterations.
+    Twelve iterations in one call must raise no device flag and agree with the
+    same twelve taken one call at a time (exact FFT length each time)."""
+    x, idx, dist, y0 = prob
+    _say("case: drifting layout, lagged FFT length")
+    start, u0 = _drifting(y0, 300.0)
+    with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+        s.set_repulsion(LAGRANGE, 3, 50, 1.0)
+        s.set_state(start, u0)
+        s.run(12, 1.0, 1.0, 1.0, 0.01, 5.0)
+        s.sync()
+        info = s.interp_info()
+        y_lag = s.y
+        s.set_state(start, u0)
+        for _ in range(12):
+            s.run(1, 1.0, 1.0, 1.0, 0.01, 5.0)
+        s.sync()
+        y_one = s.y
+    err = rel_l2(y_lag - start, y_one - start)
+    _say(f"  boxes {info['boxes']} fft {info['fft_len']}: displacement relL2 {err:.2e}")
+    assert np.all(np.isfinite(y_lag))
+    assert info["boxes"] >= 342 and info["fft_len"] == 4096
+    assert err <= 1e-4
+
+
 def test_interp_lagged_fft_length_agrees_with_exact(hip, prob):
     """Twelve iterations in one call (the FFT length comes from the lagged
     bound: 330 boxes known, up to 362 allowed, so length 4096) against the
