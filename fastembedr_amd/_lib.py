@@ -55,6 +55,9 @@ SIGNATURES = {
     "fastembedr_hip_transform_tsne": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, C.c_double, _I, _I, C.c_double,
                                            C.c_double, C.c_double, C.c_double, C.c_double, C.c_double,
                                            C.c_double, _I, _I, _I, _P, _IP]),
+    "fastembedr_hip_transform_tsne_noalloc": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, C.c_double, _I, _I, C.c_double,
+                                                   C.c_double, C.c_double, C.c_double, C.c_double, C.c_double,
+                                                   C.c_double, _I, _I, _I, _P, _IP]),
     "fastembedr_hip_transform_probe": (_I, [_P, _I, _P, _P, _I, _I, C.c_double, _P, C.c_double, _I, _I, _I, _I,
                                             _P, _P, _P]),
     "fastembedr_hip_knn_exact": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _LLP]),

@@ -30,6 +30,7 @@
 #include <climits>
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 #include <random>
 #include <string>
 #include <vector>
@@ -398,6 +399,53 @@ bool check_inputs(const double* ref_cm, int n_ref, const int* idx_cm, const doub
   return true;
 }
 
+// Scalar arguments of a transform run (:1880-1929); on success
+// the clip norms, the negative count and the repulsion mode are resolved in
+// place.
+struct RunArgs {
+  int n_reference, n_iter, early_iter;
+  double learning_rate, early_exaggeration, exaggeration, initial_momentum, final_momentum, max_grad, max_step;
+  int n_negatives, exact_threshold, initialization;
+  bool exact = false;
+};
+
+bool check_run_args(RunArgs& a) {
+  if (a.n_iter < 0 || a.early_iter < 0) {
+    set_last_error("iteration counts must be non-negative.");
+    return false;
+  }
+  if (a.n_iter + a.early_iter < 1) {
+    set_last_error("at least one transform iteration is required.");
+    return false;
+  }
+  if (!(a.learning_rate > 0.0)) {
+    set_last_error("`learning_rate` must be positive.");
+    return false;
+  }
+  if (!(a.early_exaggeration > 0.0) || !(a.exaggeration > 0.0)) {
+    set_last_error("exaggeration values must be positive.");
+    return false;
+  }
+  if (a.initial_momentum < 0.0 || a.final_momentum < 0.0) {
+    set_last_error("momentum values must be non-negative.");
+    return false;
+  }
+  if (a.n_negatives < 1) {
+    set_last_error("`n_negatives` must be positive.");
+    return false;
+  }
+  if (a.initialization < 0 || a.initialization > 2) {
+    set_last_error("`initialization` must be 'median', 'weighted', or 'random'.");
+    return false;
+  }
+  if (a.exact_threshold < 1) a.exact_threshold = 1;
+  if (!(a.max_grad > 0.0) || !std::isfinite(a.max_grad)) a.max_grad = DBL_MAX;
+  if (!(a.max_step > 0.0) || !std::isfinite(a.max_step)) a.max_step = DBL_MAX;
+  if (a.n_negatives > a.n_reference) a.n_negatives = a.n_reference;
+  a.exact = a.n_reference <= a.exact_threshold || a.n_negatives >= a.n_reference;
+  return true;
+}
+
 }  // namespace
 }  // namespace fehip
 
@@ -419,39 +467,14 @@ int fastembedr_hip_transform_tsne(const double* reference_layout, int n_referenc
   }
   const int offset = reference_offset(indices, static_cast<std::size_t>(n_query) * k, n_reference);
   if (!check_inputs(reference_layout, n_reference, indices, distances, n_query, k, perplexity, offset)) return 1;
-  if (n_iter < 0 || early_exaggeration_iter < 0) {
-    set_last_error("iteration counts must be non-negative.");
-    return 1;
-  }
-  if (n_iter + early_exaggeration_iter < 1) {
-    set_last_error("at least one transform iteration is required.");
-    return 1;
-  }
-  if (!(learning_rate > 0.0)) {
-    set_last_error("`learning_rate` must be positive.");
-    return 1;
-  }
-  if (!(early_exaggeration > 0.0) || !(exaggeration > 0.0)) {
-    set_last_error("exaggeration values must be positive.");
-    return 1;
-  }
-  if (initial_momentum < 0.0 || final_momentum < 0.0) {
-    set_last_error("momentum values must be non-negative.");
-    return 1;
-  }
-  if (n_negatives < 1) {
-    set_last_error("`n_negatives` must be positive.");
-    return 1;
-  }
-  if (initialization < 0 || initialization > 2) {
-    set_last_error("`initialization` must be 'median', 'weighted', or 'random'.");
-    return 1;
-  }
-  if (exact_repulsion_threshold < 1) exact_repulsion_threshold = 1;
-  if (!(max_grad_norm > 0.0) || !std::isfinite(max_grad_norm)) max_grad_norm = DBL_MAX;
-  if (!(max_step_norm > 0.0) || !std::isfinite(max_step_norm)) max_step_norm = DBL_MAX;
-  if (n_negatives > n_reference) n_negatives = n_reference;
-  const bool exact = n_reference <= exact_repulsion_threshold || n_negatives >= n_reference;
+  RunArgs ra{n_reference, n_iter, early_exaggeration_iter, learning_rate, early_exaggeration, exaggeration,
+             initial_momentum, final_momentum, max_grad_norm, max_step_norm, n_negatives, exact_repulsion_threshold,
+             initialization};
+  if (!check_run_args(ra)) return 1;
+  max_grad_norm = ra.max_grad;
+  max_step_norm = ra.max_step;
+  n_negatives = ra.n_negatives;
+  const bool exact = ra.exact;
 
   TransformBuffers b;
   if (!b.init(n_reference, n_query, k) ||
@@ -575,6 +598,250 @@ int fastembedr_hip_transform_probe(const double* reference_layout, int n_referen
       return 1;
     }
   }
+  return 0;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free transform (fastembedr_hip_transform_tsne_noalloc)
+//
+// The same kernels and operation order as fastembedr_hip_transform_tsne, with
+// the caller's arrays in device memory and the per-call work buffers in one
+// static device array instead of a hipMalloc:
+//   [0, 256)            NaHeader: validation flags and the index range
+//   reference           n_reference double2 (the layout, interleaved)
+//   p                   n_query * k fp64 conditional probabilities
+//   y, update, gains    n_query double2 each
+// Each GPU holds its own copy of the array for the life of the process; its
+// device address is looked up once per device (hipGetSymbolAddress) and only
+// that address is handed to kernels.  Every call on one GPU uses the same
+// array, so calls that overlap on one GPU race.
+// ---------------------------------------------------------------------------
+namespace fehip {
+namespace {
+
+constexpr int kNaMaxReference = 1 << 18;
+constexpr int kNaMaxQuery = 1 << 17;
+constexpr long long kNaMaxEntries = 1LL << 22;
+constexpr std::size_t kNaReferenceOffset = 256;
+constexpr std::size_t kNaPOffset = kNaReferenceOffset + sizeof(double2) * kNaMaxReference;
+constexpr std::size_t kNaStateOffset = kNaPOffset + sizeof(double) * static_cast<std::size_t>(kNaMaxEntries);
+constexpr std::size_t kNaStateStride = sizeof(double2) * kNaMaxQuery;
+constexpr std::size_t kNaScratchBytes = kNaStateOffset + 3 * kNaStateStride;
+constexpr int kNaMaxDevices = 64;
+
+struct NaHeader {
+  unsigned int flags;  // kNaBadDistance | kNaBadReference
+  int idx_min;
+  int idx_max;
+  int pad;
+};
+static_assert(sizeof(NaHeader) <= kNaReferenceOffset, "the header fits its slot");
+constexpr unsigned int kNaBadDistance = 1u;
+constexpr unsigned int kNaBadReference = 2u;
+
+}  // namespace
+}  // namespace fehip
+
+static __device__ __align__(256) unsigned char transform_scratch[fehip::kNaScratchBytes];
+
+namespace fehip {
+namespace {
+
+__global__ void k_na_clear(NaHeader* h) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    h->flags = 0u;
+    h->idx_min = INT_MAX;
+    h->idx_max = INT_MIN;
+  }
+}
+
+// Index range and distance checks of check_inputs, as a reduction: the host
+// derives the index offset and the range error from the smallest and largest
+// index.
+__global__ __launch_bounds__(256) void k_na_check_knn(const int* __restrict__ idx_cm,
+                                                      const double* __restrict__ dist_cm, long long count,
+                                                      NaHeader* h) {
+  int lo = INT_MAX, hi = INT_MIN;
+  unsigned int bad = 0u;
+  const long long stride = static_cast<long long>(gridDim.x) * 256;
+  for (long long c = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; c < count; c += stride) {
+    const int v = idx_cm[c];
+    lo = v < lo ? v : lo;
+    hi = v > hi ? v : hi;
+    const double d = dist_cm[c];
+    if (!isfinite(d) || d < 0.0) bad = 1u;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const int olo = __shfl_xor(lo, off);
+    const int ohi = __shfl_xor(hi, off);
+    lo = olo < lo ? olo : lo;
+    hi = ohi > hi ? ohi : hi;
+    bad |= static_cast<unsigned int>(__shfl_xor(static_cast<int>(bad), off));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicMin(&h->idx_min, lo);
+    atomicMax(&h->idx_max, hi);
+    if (bad != 0u) atomicOr(&h->flags, kNaBadDistance);
+  }
+}
+
+// n x 2 column-major reference layout -> interleaved, with the finiteness check.
+__global__ __launch_bounds__(256) void k_na_load_reference(const double* __restrict__ ref_cm, int n_ref,
+                                                           double2* __restrict__ ref, NaHeader* h) {
+  const int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (i >= n_ref) return;
+  const double x = ref_cm[i];
+  const double y = ref_cm[static_cast<std::size_t>(n_ref) + i];
+  if (!isfinite(x) || !isfinite(y)) atomicOr(&h->flags, kNaBadReference);
+  ref[i] = make_double2(x, y);
+}
+
+__global__ __launch_bounds__(256) void k_na_load_layout(const double* __restrict__ cm, int n,
+                                                        double2* __restrict__ rows) {
+  const int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (i < n) rows[i] = make_double2(cm[i], cm[static_cast<std::size_t>(n) + i]);
+}
+
+__global__ __launch_bounds__(256) void k_na_store_layout(const double2* __restrict__ rows, int n,
+                                                         double* __restrict__ cm) {
+  const int i = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+  if (i >= n) return;
+  const double2 v = rows[i];
+  cm[i] = v.x;
+  cm[static_cast<std::size_t>(n) + i] = v.y;
+}
+
+std::mutex g_na_mutex;
+char* g_na_scratch[kNaMaxDevices] = {};
+
+// Device address of transform_scratch on the current device, looked up on
+// the first call there.
+bool na_scratch(char** out) {
+  int dev = 0;
+  if (!ok(hipGetDevice(&dev), "hipGetDevice")) return false;
+  if (dev < 0 || dev >= kNaMaxDevices) {
+    set_last_error("allocation-free transform: device ordinal " + std::to_string(dev) + " is beyond " +
+                   std::to_string(kNaMaxDevices));
+    return false;
+  }
+  std::lock_guard<std::mutex> lock(g_na_mutex);
+  if (g_na_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    if (!ok(hipGetSymbolAddress(&p, HIP_SYMBOL(transform_scratch)), "hipGetSymbolAddress(transform scratch)")) {
+      return false;
+    }
+    g_na_scratch[dev] = static_cast<char*>(p);
+  }
+  *out = g_na_scratch[dev];
+  return true;
+}
+
+}  // namespace
+}  // namespace fehip
+
+extern "C" {
+
+int fastembedr_hip_transform_tsne_noalloc(const double* reference_layout, int n_reference, const int* indices,
+                                          const double* distances, int n_query, int k, const double* y_init,
+                                          int initialization, double perplexity, int n_iter,
+                                          int early_exaggeration_iter, double learning_rate,
+                                          double early_exaggeration, double exaggeration, double initial_momentum,
+                                          double final_momentum, double max_grad_norm, double max_step_norm,
+                                          int n_negatives, int exact_repulsion_threshold, int seed, double* out,
+                                          int* repulsion_exact) {
+  using namespace fehip;
+  clear_last_error();
+  if (out == nullptr || n_reference < 1 || n_query < 1 || k < 1 || reference_layout == nullptr ||
+      indices == nullptr || distances == nullptr) {
+    set_last_error("invalid transform arguments (NULL pointer or empty input).");
+    return 1;
+  }
+  const long long entries = static_cast<long long>(n_query) * k;
+  if (n_reference > kNaMaxReference || n_query > kNaMaxQuery || entries > kNaMaxEntries) {
+    set_last_error("allocation-free transform: input exceeds its static work buffer (n_reference <= " +
+                   std::to_string(kNaMaxReference) + ", n_query <= " + std::to_string(kNaMaxQuery) +
+                   ", n_query * k <= " + std::to_string(kNaMaxEntries) + "); use fastembedr_hip_transform_tsne");
+    return 1;
+  }
+  if (!(perplexity > 0.0)) {
+    set_last_error("`perplexity` must be positive.");
+    return 1;
+  }
+  RunArgs ra{n_reference, n_iter, early_exaggeration_iter, learning_rate, early_exaggeration, exaggeration,
+             initial_momentum, final_momentum, max_grad_norm, max_step_norm, n_negatives, exact_repulsion_threshold,
+             initialization};
+  if (!check_run_args(ra)) return 1;
+  if (initialization == 2 && y_init == nullptr) {
+    set_last_error("allocation-free transform: the random initialisation is drawn on the host; pass y_init");
+    return 1;
+  }
+  char* base = nullptr;
+  if (!na_scratch(&base)) return 1;
+  NaHeader* hdr = reinterpret_cast<NaHeader*>(base);
+  double2* ref = reinterpret_cast<double2*>(base + kNaReferenceOffset);
+  double* p = reinterpret_cast<double*>(base + kNaPOffset);
+  double2* y = reinterpret_cast<double2*>(base + kNaStateOffset);
+  double2* upd = reinterpret_cast<double2*>(base + kNaStateOffset + kNaStateStride);
+  double2* gains = reinterpret_cast<double2*>(base + kNaStateOffset + 2 * kNaStateStride);
+  hipStream_t st = nullptr;  // the null stream: no stream is created
+
+  const int check_blocks = static_cast<int>(std::min<long long>((entries + 255) / 256, 2048));
+  k_na_clear<<<1, 64, 0, st>>>(hdr);
+  k_na_check_knn<<<check_blocks, 256, 0, st>>>(indices, distances, entries, hdr);
+  k_na_load_reference<<<(n_reference + 255) / 256, 256, 0, st>>>(reference_layout, n_reference, ref, hdr);
+  NaHeader h{};
+  if (!ok(hipGetLastError(), "transform check launch") ||
+      !ok(hipMemcpyAsync(&h, hdr, sizeof(h), hipMemcpyDeviceToHost, st), "transform check download") ||
+      !ok(hipStreamSynchronize(st), "transform check sync")) {
+    return 1;
+  }
+  // 1-based iff every index is in [1, n_reference] (:1290-1302), then every
+  // index must name a reference row.
+  const int offset = (h.idx_min >= 1 && h.idx_max <= n_reference) ? 1 : 0;
+  if (static_cast<long long>(h.idx_min) - offset < 0 ||
+      static_cast<long long>(h.idx_max) - offset >= static_cast<long long>(n_reference)) {
+    set_last_error("KNN indices are out of range for `reference_layout`.");
+    return 1;
+  }
+  if ((h.flags & kNaBadDistance) != 0u) {
+    set_last_error("KNN distances must be finite and non-negative.");
+    return 1;
+  }
+  if ((h.flags & kNaBadReference) != 0u) {
+    set_last_error("`reference_layout` must be finite.");
+    return 1;
+  }
+
+  const int blocks = query_blocks(n_query);
+  k_transform_p<<<blocks, kQueryThreads, 0, st>>>(distances, n_query, k, perplexity, p);
+  if (y_init != nullptr) {
+    k_na_load_layout<<<(n_query + 255) / 256, 256, 0, st>>>(y_init, n_query, y);
+  } else {
+    k_transform_init<<<blocks, kQueryThreads, 0, st>>>(ref, indices, distances, n_query, k, offset,
+                                                      initialization == 1 ? 1 : 0, y);
+  }
+  k_transform_reset<<<blocks, kQueryThreads, 0, st>>>(upd, gains, n_query);
+  if (!ok(hipGetLastError(), "transform setup launch")) return 1;
+  const int total = early_exaggeration_iter + n_iter;
+  for (int it = 0; it < total; ++it) {
+    const bool early = it < early_exaggeration_iter;
+    const StepParams sp{early ? early_exaggeration : exaggeration, early ? initial_momentum : final_momentum,
+                        learning_rate, ra.max_grad, ra.max_step, ra.exact ? n_reference : ra.n_negatives,
+                        iteration_seed(seed, it)};
+    if (ra.exact) {
+      k_transform_step<true, false><<<blocks, kQueryThreads, 0, st>>>(ref, n_reference, indices, p, n_query, k,
+                                                                      offset, sp, y, upd, gains, nullptr);
+    } else {
+      k_transform_step<false, false><<<blocks, kQueryThreads, 0, st>>>(ref, n_reference, indices, p, n_query, k,
+                                                                       offset, sp, y, upd, gains, nullptr);
+    }
+    if (!ok(hipGetLastError(), "transform step launch")) return 1;
+  }
+  k_na_store_layout<<<(n_query + 255) / 256, 256, 0, st>>>(y, n_query, out);
+  if (!ok(hipGetLastError(), "transform store launch") || !ok(hipStreamSynchronize(st), "transform sync")) return 1;
+  if (repulsion_exact != nullptr) *repulsion_exact = ra.exact ? 1 : 0;
   return 0;
 }
 

@@ -257,6 +257,34 @@ FASTEMBEDR_HIP_API int fastembedr_hip_transform_probe(
     int n_negatives, int exact_repulsion_threshold, int iter_seed,
     int initialization, double* p_out, double* grad_out, double* init_out);
 
+/* Allocation-free variant of fastembedr_hip_transform_tsne.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops that place batches of new points
+ * against a fixed map, harnesses that forbid hipMalloc).  Same arguments,
+ * meaning, checks, error messages and result as fastembedr_hip_transform_tsne
+ * (the same kernels in the same order), except:
+ *   - reference_layout, indices, distances, y_init and out are DEVICE
+ *     pointers, in the same layouts;
+ *   - initialization 2 (random, drawn on the host) needs y_init;
+ *   - n_reference <= 262144, n_query <= 131072 and n_query * k <= 4194304;
+ *     larger inputs are refused with a message.
+ * The work buffers (conditional P, layout, update, gains, the reference in
+ * the kernels' layout) live in one static device array of 44 MB per GPU,
+ * held until the process ends; the call makes no hipMalloc/hipFree and
+ * creates no stream.  It runs on the null stream and returns when done.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * race. */
+FASTEMBEDR_HIP_API int fastembedr_hip_transform_tsne_noalloc(
+    const double* reference_layout, int n_reference,
+    const int* indices, const double* distances, int n_query, int k,
+    const double* y_init, int initialization, double perplexity,
+    int n_iter, int early_exaggeration_iter, double learning_rate,
+    double early_exaggeration, double exaggeration,
+    double initial_momentum, double final_momentum,
+    double max_grad_norm, double max_step_norm,
+    int n_negatives, int exact_repulsion_threshold, int seed,
+    double* out, int* repulsion_exact);
+
 /* Wall time of the P construction in milliseconds (device events). */
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_p_build_ms(const fastembedr_hip_tsne* session, double* ms);
 

@@ -16,6 +16,22 @@ def small_problem(n=600, dim=8, k=24, components=4, seed=3, one_based=True):
     return x, labels, idx_r, dist_r
 
 
+def query_problem(n_ref=3000, nq=1200, k=30, seed=11):
+    """A fixed-reference transform problem: a reference layout (a 2-D
+    embedding stand-in: cluster centres plus noise), 20-D mixture data, and
+    each query's exact k nearest reference rows (1-based, fp64 distances)."""
+    spec = synthetic.MixtureSpec(n=n_ref + nq, dim=20, components=8, mean_sd=4.0)
+    x, labels = synthetic.gaussian_mixture(spec, seed=seed)
+    rng = np.random.default_rng(seed)
+    centers = rng.normal(0, 8, size=(8, 2))
+    layout = centers[labels[:n_ref]] + rng.normal(0, 1.0, size=(n_ref, 2))
+    xr, xq = x[:n_ref].astype(np.float64), x[n_ref:].astype(np.float64)
+    d2 = (xq ** 2).sum(1)[:, None] - 2 * xq @ xr.T + (xr ** 2).sum(1)[None, :]
+    idx = np.argsort(d2, axis=1)[:, :k]
+    dist = np.sqrt(np.maximum(np.take_along_axis(d2, idx, axis=1), 0))
+    return layout, (idx + 1).astype(np.int32), dist
+
+
 class DeviceArray:
     """A host array copied into device memory with the HIP runtime that the
     backend library already loaded (no second runtime in the process)."""
@@ -41,6 +57,17 @@ class DeviceArray:
     @property
     def address(self) -> int:
         return int(self.ptr.value)
+
+    def to_host(self, dtype, shape, order="C") -> np.ndarray:
+        """The first prod(shape) elements, copied back to a new host array."""
+        import ctypes as C
+
+        out = np.empty(shape, dtype=dtype, order=order)
+        if out.nbytes > self.nbytes:
+            raise ValueError("read beyond the device buffer")
+        if self._hip.hipMemcpy(C.c_void_p(out.ctypes.data), self.ptr, out.nbytes, 2) != 0:
+            raise RuntimeError("hipMemcpy failed")
+        return out
 
     def free(self):
         if self.ptr:

@@ -14,7 +14,8 @@ import sys
 import numpy as np
 import pytest
 
-from fastembedr_amd import _lib, synthetic
+from fastembedr_amd import _lib
+from tests.helpers import query_problem
 
 pytestmark = pytest.mark.gpu
 
@@ -26,23 +27,9 @@ def _say(msg):
     sys.stdout.flush()
 
 
-def _query_problem(n_ref=3000, nq=1200, k=30, seed=11):
-    """Reference layout (a 2-D embedding stand-in), 20-D data, query KNN."""
-    spec = synthetic.MixtureSpec(n=n_ref + nq, dim=20, components=8, mean_sd=4.0)
-    x, labels = synthetic.gaussian_mixture(spec, seed=seed)
-    rng = np.random.default_rng(seed)
-    centers = rng.normal(0, 8, size=(8, 2))
-    layout = centers[labels[:n_ref]] + rng.normal(0, 1.0, size=(n_ref, 2))
-    xr, xq = x[:n_ref].astype(np.float64), x[n_ref:].astype(np.float64)
-    d2 = (xq ** 2).sum(1)[:, None] - 2 * xq @ xr.T + (xr ** 2).sum(1)[None, :]
-    idx = np.argsort(d2, axis=1)[:, :k]
-    dist = np.sqrt(np.maximum(np.take_along_axis(d2, idx, axis=1), 0))
-    return layout, (idx + 1).astype(np.int32), dist
-
-
 @pytest.fixture(scope="module")
 def qp():
-    return _query_problem()
+    return query_problem()
 
 
 def _probe(ref, idx, dist, perplexity, y=None, ex=1.0, n_neg=256, thr=4096, iter_seed=0, init=0):
