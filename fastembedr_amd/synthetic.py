@@ -70,6 +70,27 @@ def gaussian_mixture(spec: MixtureSpec, seed: int = 1, n: int | None = None) -> 
     return x, labels
 
 
+def mixture_queries(spec: MixtureSpec, n_query: int, seed: int = 1, query_seed: int = 2) -> np.ndarray:
+    """New points from the same mixture as gaussian_mixture(spec, seed): the
+    component means, stds and weights are drawn from `seed` exactly as there,
+    the queries' labels and noise from an independent stream `query_seed`.
+    Config 3 places 100,000 such points against the config-1 embedding."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    means = rng.normal(0.0, spec.mean_sd, size=(spec.components, spec.dim))
+    if spec.std_range is None:
+        stds = np.ones(spec.components)
+    else:
+        stds = rng.uniform(spec.std_range[0], spec.std_range[1], size=spec.components)
+    if spec.dirichlet is None:
+        weights = np.full(spec.components, 1.0 / spec.components)
+    else:
+        weights = rng.dirichlet(np.full(spec.components, spec.dirichlet))
+    qrng = np.random.Generator(np.random.PCG64(query_seed))
+    labels = qrng.choice(spec.components, size=n_query, p=weights)
+    noise = qrng.standard_normal(size=(n_query, spec.dim))
+    return (means[labels] + noise * stds[labels, None]).astype(np.float32)
+
+
 def pca_init(x: np.ndarray, n_components: int = 2, target_sd: float = 1e-4) -> np.ndarray:
     """PCA scores, centred, scaled so that the largest column sd (n - 1) is
     target_sd (R/tsne_control.R:364-389 semantics).  Returns float32 (n, 2)."""

@@ -217,6 +217,31 @@ struct KeyedValue {
   float value;
 };
 
+// Edges in ascending key order, the order the reference's std::sort of the
+// whole array gives (src/tsne_neighbors.cpp:593-596): a counting pass places
+// them by the row part of the key (key >> 32), then each row's run is sorted
+// on its own, rows in parallel.  Equal keys are summed afterwards, so their
+// relative order only matters at fp64 rounding when three or more coincide.
+void sort_edges(std::vector<KeyedValue>& edges, int n, int threads) {
+  std::vector<std::size_t> start(static_cast<std::size_t>(n) + 1, 0);
+  for (const KeyedValue& e : edges) ++start[static_cast<std::size_t>(e.key >> 32) + 1];
+  for (int i = 0; i < n; ++i) start[static_cast<std::size_t>(i) + 1] += start[static_cast<std::size_t>(i)];
+  std::vector<KeyedValue> out(edges.size());
+  {
+    std::vector<std::size_t> cursor(start.begin(), start.end() - 1);
+    for (const KeyedValue& e : edges) out[cursor[static_cast<std::size_t>(e.key >> 32)]++] = e;
+  }
+  std::vector<KeyedValue>().swap(edges);
+  parallel_for(n, threads, [&](int b, int e, int) {
+    for (int i = b; i < e; ++i) {
+      std::sort(out.begin() + static_cast<std::ptrdiff_t>(start[static_cast<std::size_t>(i)]),
+                out.begin() + static_cast<std::ptrdiff_t>(start[static_cast<std::size_t>(i) + 1]),
+                [](const KeyedValue& x, const KeyedValue& y) { return x.key < y.key; });
+    }
+  });
+  edges.swap(out);
+}
+
 // Directed KNN edges -> symmetric CSR (src/tsne_neighbors.cpp:540-648).
 // Inputs are R-ordered (column-major n x k); the reference copies distances to
 // row-major first (src/tsne_neighbors.cpp:327-352), which is what `dist_rm` is.
@@ -273,8 +298,7 @@ bool build_symmetric_p(const int* idx_cm, const float* dist_cm, int n, int k,
     g_error = "KNN graph produced no non-self t-SNE edges.";
     return false;
   }
-  std::sort(edges.begin(), edges.end(),
-            [](const KeyedValue& x, const KeyedValue& y) { return x.key < y.key; });
+  sort_edges(edges, n, t_count);
 
   out.n = n;
   out.row_ptr.assign(static_cast<std::size_t>(n) + 1, 0);

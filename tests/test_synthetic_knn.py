@@ -34,3 +34,23 @@ def test_partitioned_knn_random_partition_falls_back():
     labels = np.random.default_rng(0).integers(0, 5, size=2000).astype(np.int32)
     brute = _check(x, labels, 25)
     assert brute > 1000
+
+
+def test_mixture_queries_share_the_mixture():
+    """Config 3's queries come from config 1's mixture: each query lies within
+    a few component stds of one of the components' means (estimated from the
+    labelled rows), while a mixture drawn from another seed is far off."""
+    spec = synthetic.CONFIGS[1]
+    x, labels = synthetic.gaussian_mixture(spec, seed=1, n=20000)
+    means = np.stack([x[labels == c].mean(axis=0) for c in range(spec.components)])
+
+    def nearest_d2(q):
+        d2 = (q ** 2).sum(1)[:, None] - 2 * q @ means.T + (means ** 2).sum(1)[None, :]
+        return d2.min(axis=1)
+
+    q = synthetic.mixture_queries(spec, 3000)
+    other = synthetic.mixture_queries(spec, 3000, seed=2)
+    # within-component squared distance ~ dim * std^2 <= 50 * 1.5^2
+    assert np.median(nearest_d2(q.astype(np.float64))) < 130.0
+    assert np.median(nearest_d2(other.astype(np.float64))) > 500.0
+    np.testing.assert_array_equal(q, synthetic.mixture_queries(spec, 3000))
