@@ -15,16 +15,23 @@ reference's bilinear grid with its CPU policy (256 nodes per axis at this n).
 
 A step is one gradient iteration (repulsion + attraction + update +
 centring).  Inputs (P, layout, optimiser state) are resident in HBM before
-the timed region; the P construction is timed separately.  After W untimed
-warm-up iterations the state is reset to the initialisation and the timed
-region runs the first K iterations of the schedule (K = 750 is the whole
-run).  In the timed region the library runs the attraction and the kernel
-spectrum on side streams beside the rest of each iteration.  The dominant
-kernel's duration comes from HIP events recorded on the stream it runs on,
-around each of its launches in the timed region; the other kernels run
-without events.  A separate, untimed pass of the same K iterations runs the
-kernels in sequence and brackets every one with events for the breakdown
-(ms_per_repulsion_step sums the repulsion kernels of that pass).
+the timed region; the P construction is timed separately.  With --steps K
+the timed region is the LAST K iterations of the 750-iteration schedule
+(the late phase, where the layout's span and so the interpolation grid are
+largest): the first 750 - K iterations run untimed before it; K = 750 times
+the whole schedule.  Passes, in order (so that the last dispatches of every
+kernel belong to the timed window, which rocprof digests rely on):
+  1. W untimed warm-up iterations, then a reset to the initialisation;
+  2. the whole schedule timed from the host without events
+     (full_schedule: its mean rate);
+  3. the window with HIP events around every kernel, which runs the
+     kernels in sequence (the per-kernel breakdown, ms_per_repulsion_step);
+  4. the window timed (value), with events only around the dominant kernel,
+     on the stream it runs on; the library runs the attraction and the
+     kernel spectrum on side streams beside the rest of each iteration.
+The CPU baseline runs the oracle, a restatement of the reference's CPU
+algorithm (bilinear grid, CPU grid policy), from the layout at the start of
+the window.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -123,34 +130,53 @@ def main() -> int:
     log(f"P build {p_build_ms:.1f} ms, nnz={nnz}, repulsion={args.repulsion}"
         + ("" if interp else f", grid={g}"))
 
+    total = sched["early_exaggeration_iter"] + sched["n_iter"]
+    steps = max(1, min(args.steps, total))
+    head = total - steps  # untimed iterations before the timed window
     ee = sched["early_exaggeration_iter"]
     lr = n / 12.0
 
-    def schedule_run(count: int) -> None:
-        early = min(count, ee)
+    def schedule_run(start: int, end: int) -> None:
+        """Iterations [start, end) of the two-phase schedule."""
+        early = max(0, min(end, ee) - start)
         if early:
             sess.run(early, sched["early_exaggeration"], sched["initial_momentum"], lr, sched["min_gain"],
                      sched["max_step_norm"])
-        if count - early:
-            sess.run(count - early, sched["exaggeration"], sched["final_momentum"], lr, sched["min_gain"],
+        late = end - max(start, ee)
+        if late > 0:
+            sess.run(late, sched["exaggeration"], sched["final_momentum"], lr, sched["min_gain"],
                      sched["max_step_norm"])
 
-    # warm-up (untimed), then reset to the initialisation
-    sess.set_state(y0)
-    sess.center()
-    schedule_run(args.warmup)
-    sess.sync()
-    sess.set_state(y0)
-    sess.center()
+    def reset() -> None:
+        sess.set_state(y0)
+        sess.center()
+        sess.sync()
+
+    # 1. warm-up (untimed), then reset to the initialisation
+    reset()
+    schedule_run(0, args.warmup)
     sess.sync()
 
-    # Breakdown pass (untimed): HIP events around every kernel give the
-    # per-kernel durations and pick the dominant kernel.  In this pass the
-    # library runs the iteration's kernels in sequence (no side streams), so
-    # each duration is the kernel's alone; the timed pass below overlaps the
-    # attraction and the kernel spectrum with the rest of the iteration.
+    # 2. the whole schedule, timed from the host (no events)
+    reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    schedule_run(0, total)
+    sess.sync()
+    torch.cuda.synchronize()
+    full_wall = time.perf_counter() - t0
+    log(f"whole schedule: {total} iterations in {full_wall:.3f}s = {total / full_wall:.1f} it/s")
+
+    # 3. breakdown pass over the window: HIP events around every kernel give
+    # the per-kernel durations and pick the dominant kernel.  In this pass
+    # the library runs the iteration's kernels in sequence (no side streams),
+    # so each duration is the kernel's alone.
+    reset()
+    schedule_run(0, head)
+    sess.sync()
+    y_window = sess.y  # the layout at the start of the window (CPU baseline input)
     sess.set_timing(True)
-    schedule_run(args.steps)
+    schedule_run(head, total)
     sess.sync()
     breakdown = sess.timing()
     sess.set_timing(False)
@@ -158,53 +184,67 @@ def main() -> int:
     # The repulsion step: every kernel from the binning of the points to the
     # potentials on the grid (the read-back is fused into the update).
     rep_kernels = [kname for kname in per_kernel if kname.startswith("interp_")] if interp else \
-        ["bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols", "charge_rows",
-         "conv_cols", "inverse_rows"]
+        [kname for kname in ("bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols",
+                             "charge_rows", "conv_cols", "inverse_rows") if kname in per_kernel]
     rep_ms = sum(per_kernel[kname] for kname in rep_kernels)
-    geo_end = sess.interp_info() if interp else None
     dom = max(breakdown, key=lambda kname: breakdown[kname][1])  # largest total time
-    sess.set_state(y0)
-    sess.center()
-    sess.sync()
 
-    # Timed region: events only around the dominant kernel, so that the other
-    # launches run back to back as in an uninstrumented run.
+    # 4. the timed window: events only around the dominant kernel, so that
+    # the other launches run back to back as in an uninstrumented run.
+    reset()
+    schedule_run(0, head)
+    sess.sync()
     sess.set_timing(True, only=dom)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    schedule_run(args.steps)
+    schedule_run(head, total)
     sess.sync()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     timing = sess.timing()
     sess.set_timing(False)
+    geo_end = sess.interp_info() if interp else None
     y_final = sess.y
     if not np.all(np.isfinite(y_final)):
         log("non-finite layout after the timed region")
         return 1
-    its = args.steps / wall
-    ms_per_step = 1000.0 * wall / args.steps
+    its = steps / wall
+    ms_per_step = 1000.0 * wall / steps
     cnt, tot = timing[dom]
     dom_ms = tot / cnt if cnt else 0.0
-    # Algorithmic bytes per launch.  attract: P streamed once (a 16-bit slot
-    # word and the fp32 value per stored entry, 6 nnz), y_i read and the row
-    # sum written (16 n); the neighbour positions y_j are counted as
-    # cache-resident, as the grid reads are; bridge and padding slots are
-    # overhead, not algorithmic bytes.  update: y_i, attraction, gains,
-    # update read (32 n) and y, gains, update written (24 n).
     layout = sess.attraction_info()
-    alg_bytes = {"attract": 6.0 * nnz + 16.0 * n, "update": 56.0 * n}
+    # Algorithmic bytes per launch (SURVEY 8(d) basis).  attract: col int32 +
+    # val fp32 streamed once per stored entry and the row pointers,
+    # 8 nnz + 4 (n + 1); the neighbour positions y_j are counted as
+    # cache-resident.  The kernel's own slot format moves 6 bytes per entry
+    # (a 16-bit slot word + the fp32 value) plus 16 n (y_i read, row sum
+    # written): reported beside it.  update: y_i, attraction, gains, update
+    # read (32 n) and y, gains, update written (24 n).
+    alg_bytes = {"attract": 8.0 * nnz + 4.0 * (n + 1), "update": 56.0 * n}
     dom_bytes = alg_bytes.get(dom, 0.0)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9 if dom_ms > 0 else 0.0
+    slot_bytes = 6.0 * nnz + 16.0 * n
     traffic = measured_traffic(dom, n, nnz, g, args.repulsion)
-    log(f"{its:.1f} it/s, {ms_per_step:.3f} ms/step, repulsion {rep_ms:.3f} ms, {dom} {dom_ms:.3f} ms "
-        f"({achieved:.0f} GB/s)")
+    # The repulsion step's roofline: SURVEY 8(d)'s B_rep = 16 n + 8 n
+    # + 28 G^2 + 288 F^2 with G the grid nodes per axis and F the FFT length
+    # at the end of the window, over the summed repulsion kernels of the
+    # breakdown pass; traffic: the rocprof digest's bytes of the same kernels
+    # per iteration.
+    if interp:
+        g_nodes, f_len = geo_end["nodes"], geo_end["fft_len"]
+    else:
+        g_nodes, f_len = g, 2 * g
+    rep_bytes = 24.0 * n + 28.0 * g_nodes ** 2 + 288.0 * f_len ** 2
+    rep_achieved = rep_bytes / (rep_ms * 1e-3) / 1e9 if rep_ms > 0 else 0.0
+    rep_traffic = repulsion_traffic(n, nnz, g, args.repulsion)
+    log(f"{its:.1f} it/s over iterations {head}-{total - 1}, {ms_per_step:.3f} ms/step, repulsion {rep_ms:.3f} ms "
+        f"({rep_achieved:.0f} GB/s on B_rep), {dom} {dom_ms:.3f} ms ({achieved:.0f} GB/s)")
     log("per-kernel ms (breakdown pass, every kernel bracketed by events): "
         + ", ".join(f"{kk}={v:.4f}" for kk, v in per_kernel.items()))
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(sess, y0, n, lr, sched, args.cpu_seconds, interp)
+        cpu = cpu_baseline(sess, y_window, n, lr, sched, args.cpu_seconds, head)
     sess.close()
     host_boundary = None
     if args.host_boundary:
@@ -212,6 +252,8 @@ def main() -> int:
         host_boundary = one_shot_from_host(np.asfortranarray(host_knn.indices), np.asfortranarray(host_knn.distances),
                                            y0, sched, lr)
 
+    window = (f"last {steps} of the {total}-iteration schedule (iterations {head}-{total - 1}; the first {head} "
+              f"run untimed before the timed region)" if head else f"the whole {total}-iteration schedule")
     line = {
         "metric": "t-SNE gradient iterations/sec at N=1M (2D); ms per FFT repulsion step; % HBM peak",
         "value": round(its, 3),
@@ -241,10 +283,19 @@ def main() -> int:
             "attraction_layout": {"runs": layout["tiles"], "slots": layout["slots"],
                                   "slots_per_entry": round(layout["slots"] / max(nnz, 1), 4)},
             "repulsion": args.repulsion,
-            "timed_iterations": f"first {args.steps} of the 750-iteration schedule",
+            "timed_iterations": window,
         },
+        "full_schedule": {"iterations": total, "iterations_per_s": round(total / full_wall, 3),
+                          "ms_per_step": round(1000.0 * full_wall / total, 4),
+                          "note": "whole 750-iteration schedule timed from the host, no events"},
         "ms_per_repulsion_step": round(rep_ms, 4),
         "repulsion_kernels": rep_kernels,
+        "repulsion_roofline": {
+            "bound": "hbm", "achieved": round(rep_achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(rep_achieved / HBM_PEAK_GBS, 4), "traffic": rep_traffic,
+            "algorithmic_bytes": int(rep_bytes),
+            "basis": f"B_rep = 24 n + 28 G^2 + 288 F^2 with G = {g_nodes} nodes per axis, F = {f_len}, "
+                     f"over ms_per_repulsion_step (the repulsion kernels in sequence)"},
         "p_build_ms": round(p_build_ms, 2),
         "per_kernel_ms": {kk: round(v, 5) for kk, v in per_kernel.items()},
         "roofline": {
@@ -256,6 +307,13 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "algorithmic_bytes": int(dom_bytes),
+            "basis": "attract: 8 nnz + 4 (n + 1) (col int32 + val fp32 + row_ptr) over the kernel's mean "
+                     "event-timed duration in the timed window" if dom == "attract" else "see per-kernel bytes",
+            "slot_basis": {"bytes": int(slot_bytes), "achieved": round(slot_bytes / (dom_ms * 1e-3) / 1e9, 1)
+                           if dom_ms > 0 else 0.0,
+                           "note": "the tiled kernel's own format: 6 bytes per stored entry + 16 n"}
+            if dom == "attract" else None,
+            "kernel_ms": round(dom_ms, 5),
             "traffic_source": TRAFFIC_FILES[args.repulsion].name if traffic is not None else None,
         },
         "cpu_baseline": cpu,
@@ -272,12 +330,14 @@ def main() -> int:
 
 
 def bench_transform(args, torch, fe, synthetic) -> int:
-    """Config 3: fixed-reference transform.  Reference: the config-1 mixture
-    (70,000 x 50) embedded on the GPU with the full schedule; queries:
-    100,000 new points of the same mixture with exact k = 30 neighbours in
-    the reference; transform_tsne defaults except exaggeration 1 (perplexity
-    5, 250 iterations, learning rate 0.1, momentum 0.8, gradient clip 0.25,
-    median initialisation, 256 sampled negatives per query and iteration).
+    """Config 3: fixed-reference transform.  Reference: the config-1 data
+    (70,000 x 50) embedded on the GPU with the full schedule (FIt-SNE grid);
+    queries: 100,000 new points of the same mixture
+    (synthetic.mixture_queries) with exact k = 30 neighbours in the
+    reference; transform_tsne defaults except exaggeration 1 (perplexity 5,
+    250 iterations, learning rate 0.1, momentum 0.8, gradient clip 0.25,
+    median initialisation).  Repulsion: the reference's transform_tsne_cpp
+    mode, 256 sampled negatives per query and iteration.
     The per-iteration rate is taken from two calls (all iterations, and one)
     so that upload, P and initialisation drop out."""
     import ctypes as C
@@ -287,12 +347,16 @@ def bench_transform(args, torch, fe, synthetic) -> int:
     spec = synthetic.CONFIGS[1]
     n_ref = args.n or spec.n
     nq = 100_000 if not args.n else max(1, args.n // 2)
-    x, _ = synthetic.gaussian_mixture(spec, seed=1, n=n_ref + nq)
-    xr, xq = x[:n_ref], x[n_ref:]
+    xr, _ = synthetic.gaussian_mixture(spec, seed=1, n=n_ref)
+    xq = synthetic.mixture_queries(spec, nq)
     sched = synthetic.SCHEDULE
     ref_knn = fe.exact_knn(np.ascontiguousarray(xr, dtype=np.float32), sched["k"], keep_device=True)
     with fe.TsneSession(perplexity=sched["perplexity"], index_offset=1, n=n_ref, k=sched["k"],
                         device_pointers=(ref_knn.indices_ptr, ref_knn.distances_ptr)) as sess:
+        from fastembedr_amd import _lib as lib_
+
+        sess.set_repulsion(lib_.REPULSION_LAGRANGE, sched["interpolation_points"], sched["min_intervals"],
+                           sched["ints_in_interval"])
         sess.set_state(synthetic.pca_init(xr))
         sess.center()
         lr = n_ref / 12.0
@@ -357,8 +421,10 @@ def bench_transform(args, torch, fe, synthetic) -> int:
         "ms_per_step": round(per_iter * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f64", "data": "synthetic",
         "config": {"workload": f"config3: {nq} queries, reference {n_ref} (config-1 mixture embedded on the GPU), "
-                               f"k=30, perplexity 5, 256 sampled negatives, lr 0.1, exaggeration 1",
-                   "n_reference": n_ref, "n_query": nq, "k": 30},
+                               f"k=30, perplexity 5, lr 0.1, exaggeration 1",
+                   "n_reference": n_ref, "n_query": nq, "k": 30,
+                   "repulsion": "sampled: 256 reference points per query and iteration (transform_tsne_cpp's "
+                                "mode for n_reference > 4096)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -395,11 +461,20 @@ def one_shot_from_host(idx_r, dist_r, y0, sched, lr):
 TRAFFIC_FILES = {"grid": ROOT / "profiles" / "tsne_loop_config2_traffic.json",
                  "interp": ROOT / "profiles" / "tsne_loop_config2_interp_traffic.json"}
 
+# Kernels of the repulsion step and their launches per iteration.
+REPULSION_SYMBOLS = {
+    "interp": {"k_lg_bin_count": 1, "k_bin_plan": 1, "k_lg_bin_scatter": 1, "k_lg_spread": 1, "k_lg_gather": 1,
+               "k_lg_kernel_rows": 1, "k_lg_transpose": 3, "k_lg_kernel_cols": 1, "k_lg_charge_rows": 1,
+               "k_lg_conv_cols": 1, "k_lg_inverse_rows": 1, "k_lg_finalize_z": 1},
+    "grid": {"k_bin_count": 1, "k_bin_plan": 1, "k_bin_scatter": 1, "k_spread_tiles": 1, "k_kernel_rows": 1,
+             "k_kernel_cols": 1, "k_charge_rows": 1, "k_conv_cols": 1, "k_inverse_rows": 1, "k_finalize_sumq": 1},
+}
 
-def measured_traffic(kernel: str, n: int, nnz: int, g: int, repulsion: str):
-    """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, calibrated
-    against a copy of known size) from the committed rocprofv3 digest, when
-    that digest was taken on this same workload; None otherwise."""
+
+def _digest(n: int, nnz: int, g: int, repulsion: str):
+    """The committed rocprofv3 traffic digest (FETCH_SIZE + WRITE_SIZE per
+    dispatch, calibrated against a copy of known size), when it was taken on
+    this same workload; None otherwise."""
     try:
         rec = json.loads(TRAFFIC_FILES[repulsion].read_text())
     except (OSError, ValueError):
@@ -407,6 +482,14 @@ def measured_traffic(kernel: str, n: int, nnz: int, g: int, repulsion: str):
     if (rec.get("n"), rec.get("nnz"), rec.get("repulsion")) != (n, nnz, repulsion):
         return None
     if repulsion == "grid" and rec.get("grid") != g:
+        return None
+    return rec
+
+
+def measured_traffic(kernel: str, n: int, nnz: int, g: int, repulsion: str):
+    """HBM bytes per launch of the timer `kernel` from the digest."""
+    rec = _digest(n, nnz, g, repulsion)
+    if rec is None:
         return None
     # the timer's name is the kernel symbol's stem: "attract" is k_attract or
     # the tiled k_attract_tiles_seg<NT>, "update" k_update<mode, grid>
@@ -416,37 +499,95 @@ def measured_traffic(kernel: str, n: int, nnz: int, g: int, repulsion: str):
     return None
 
 
-def cpu_baseline(sess, y0, n, lr, sched, budget_s, interp):
-    """The CPU oracle (a restatement of the reference CPU path) on the same P
-    and initialisation, timed on this host's cores for a bounded number of
-    early-exaggeration iterations (gradient + update + centring), with the
-    same repulsion as the timed GPU run."""
+def repulsion_traffic(n: int, nnz: int, g: int, repulsion: str):
+    """HBM bytes per iteration of the repulsion kernels, from the digest."""
+    rec = _digest(n, nnz, g, repulsion)
+    if rec is None:
+        return None
+    total = 0.0
+    kernels = rec.get("kernels", {})
+    for sym, per_iter in REPULSION_SYMBOLS[repulsion].items():
+        hits = [t for name, t in kernels.items() if name.split("<")[0] == sym]
+        if not hits:
+            return None
+        total += per_iter * sum(t["fetch_bytes"] + t["write_bytes"] for t in hits) / len(hits)
+    return int(total)
+
+
+def cpu_share() -> int:
+    """Threads for the CPU baseline: the CPUs this process may run on, at
+    most 16 (one GPU's share of a GPU box's host)."""
+    try:
+        visible = len(os.sched_getaffinity(0))
+    except AttributeError:
+        visible = os.cpu_count() or 1
+    return max(1, min(16, visible))
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(sess, y_start, n, lr, sched, budget_s, start_iter):
+    """The reference's CPU algorithm, restated by the oracle
+    (src/tsne_neighbors.cpp:1076-1256: fp32 bilinear FFT grid with the CPU
+    grid policy, CSR attraction, gains/momentum update, fp64 centring), on
+    the same P, from the layout at the start of the timed window, in that
+    window's phase: at this host's thread share and at 4 threads (the
+    reference's published CPU figures use 4 cores).  The oracle's fp64
+    FIt-SNE restatement (no counterpart in the reference) is timed as an
+    extra figure."""
     from oracle import oracle
 
-    threads = min(16, os.cpu_count() or 1)
-    method = oracle.METHOD_LAGRANGE if interp else oracle.METHOD_GRID
     P = oracle.OracleP.wrap(*sess.csr())
-    y = np.array(y0, np.float32, copy=True)
-    oracle.zero_mean(y)
-    t0 = time.perf_counter()
-    y, _, _ = P.optimize(y, 1, 0, sched["early_exaggeration"], 1.0, lr, False, sched["initial_momentum"],
-                         sched["final_momentum"], method=method, threads=threads)
-    one = time.perf_counter() - t0
-    iters = max(1, min(400, int(budget_s / max(one, 1e-3))))
-    t0 = time.perf_counter()
-    P.optimize(y, iters, 0, sched["early_exaggeration"], 1.0, lr, False, sched["initial_momentum"],
-               sched["final_momentum"], method=method, threads=threads)
-    dt = time.perf_counter() - t0
-    log(f"CPU oracle: {iters} iterations in {dt:.1f}s on {threads} threads")
-    rep = ("FIt-SNE interpolation grid (fp64 restatement: 3 points per interval, >= 50 intervals)" if interp
-           else "reference CPU grid policy")
+    early = start_iter < sched["early_exaggeration_iter"]
+    phase = "early-exaggeration" if early else "normal-phase"
+
+    def rate(threads: int, method: int, budget: float):
+        def run(count):
+            y = np.array(y_start, np.float32, copy=True)
+            if early:
+                P.optimize(y, count, 0, sched["early_exaggeration"], 1.0, lr, False, sched["initial_momentum"],
+                           sched["final_momentum"], method=method, threads=threads)
+            else:
+                P.optimize(y, 0, count, sched["early_exaggeration"], sched["exaggeration"], lr, False,
+                           sched["initial_momentum"], sched["final_momentum"], method=method, threads=threads)
+
+        t0 = time.perf_counter()
+        run(1)
+        one = time.perf_counter() - t0
+        iters = max(2, min(400, int(budget / max(one, 1e-3))))
+        t0 = time.perf_counter()
+        run(iters)
+        dt = time.perf_counter() - t0
+        log(f"CPU oracle ({'bilinear' if method == oracle.METHOD_GRID else 'FIt-SNE fp64'}): {iters} {phase} "
+            f"iterations in {dt:.1f}s on {threads} threads")
+        return iters, dt
+
+    share = cpu_share()
+    it_all, dt_all = rate(share, oracle.METHOD_GRID, 0.55 * budget_s)
+    it_4, dt_4 = rate(4, oracle.METHOD_GRID, 0.3 * budget_s)
+    it_lg, dt_lg = rate(share, oracle.METHOD_LAGRANGE, 0.15 * budget_s)
     return {
-        "value": round(iters / dt, 4),
+        "value": round(it_all / dt_all, 4),
         "unit": "iterations/s",
-        "cores": threads,
+        "cores": share,
         "kind": "port",
-        "sample": f"{iters} early-exaggeration iterations (after 1 untimed) of the same n={n} problem, "
-                  f"same P and initialisation, {rep}",
+        "sample": f"{it_all} {phase} iterations of the same n={n} problem from the layout at iteration "
+                  f"{start_iter}, same P; the reference's CPU algorithm (bilinear grid, CPU policy "
+                  f"{oracle.policy_grid_size(n)} nodes per axis) restated by the oracle",
+        "cpu_model": cpu_model(),
+        "host_cpus_visible": os.cpu_count(),
+        "threads_4": {"value": round(it_4 / dt_4, 4), "cores": 4, "iterations": it_4},
+        "fitsne_fp64_oracle": {"value": round(it_lg / dt_lg, 4), "cores": share, "iterations": it_lg,
+                               "note": "the oracle's fp64 FIt-SNE interpolation grid (no counterpart in the "
+                                       "reference)"},
     }
 
 

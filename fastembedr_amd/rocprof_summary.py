@@ -3,7 +3,8 @@ profiles/ (kernel durations and HBM traffic per dispatch).
 
     python -m fastembedr_amd.rocprof_summary trace  <kt_dir>   <command> > profiles/<name>.txt
     python -m fastembedr_amd.rocprof_summary traffic <fetch_dir> <write_dir> <command> \
-        --json profiles/<name>.json > profiles/<name>.txt
+        --json profiles/<name>.json [--last N] > profiles/<name>.txt
+    python -m fastembedr_amd.rocprof_summary counters <pmc_dir> <command> --names A,B [--last N]
 
 Counter units: FETCH_SIZE and WRITE_SIZE are read in KiB per dispatch and
 scaled by what the same counter reads for a device-to-device copy of known
@@ -51,23 +52,47 @@ def trace(kt_dir: str) -> list[str]:
     return out
 
 
-def _counter(dir_: str, cname: str):
+def _dispatch_order(r: dict) -> int:
+    for key in ("Dispatch_Id", "Correlation_Id"):
+        if r.get(key, "").strip():
+            return int(r[key])
+    return 0
+
+
+def _counter(dir_: str, cname: str, last: int = 0):
+    """Per kernel, the counter's value of each dispatch in dispatch order
+    (only the last `last` dispatches when last > 0), and the largest value of
+    the calibration copy."""
     per = collections.defaultdict(list)
     calib = None
-    for r in csv.DictReader(open(_one(f"{dir_}/**/*counter_collection.csv"))):
-        if r["Counter_Name"] != cname:
-            continue
+    rows = [r for r in csv.DictReader(open(_one(f"{dir_}/**/*counter_collection.csv"))) if r["Counter_Name"] == cname]
+    rows.sort(key=_dispatch_order)
+    for r in rows:
         v = float(r["Counter_Value"])
         if "copyBuffer" in r["Kernel_Name"] and (calib is None or v > calib):
             calib = v
         if _OURS.search(r["Kernel_Name"]):
             per[short_name(r["Kernel_Name"])].append(v)
+    if last > 0:
+        per = collections.defaultdict(list, {k: v[-last:] for k, v in per.items()})
     return per, calib
 
 
-def traffic(fetch_dir: str, write_dir: str, copy_bytes: int) -> tuple[list[str], dict]:
-    fetch, fcal = _counter(fetch_dir, "FETCH_SIZE")
-    write, wcal = _counter(write_dir, "WRITE_SIZE")
+def counters(dir_: str, names: list[str], last: int = 0) -> list[str]:
+    """Mean per dispatch of each counter, per kernel of this library."""
+    cols = {c: _counter(dir_, c, last)[0] for c in names}
+    kernels = sorted({k for per in cols.values() for k in per})
+    out = [f"{'kernel':34s} {'dispatches':>10s} " + " ".join(f"{c:>26s}" for c in names)]
+    for k in kernels:
+        vals = [cols[c].get(k, []) for c in names]
+        disp = max(len(v) for v in vals)
+        out.append(f"{k:34s} {disp:10d} " + " ".join(f"{(sum(v) / len(v) if v else 0.0):26.1f}" for v in vals))
+    return out
+
+
+def traffic(fetch_dir: str, write_dir: str, copy_bytes: int, last: int = 0) -> tuple[list[str], dict]:
+    fetch, fcal = _counter(fetch_dir, "FETCH_SIZE", last)
+    write, wcal = _counter(write_dir, "WRITE_SIZE", last)
     if not fcal or not wcal:
         raise RuntimeError("no calibration copy found (run bench.py with --calibrate-copy-mib)")
     ffac = copy_bytes / (fcal * 1024.0)
@@ -99,11 +124,23 @@ def main(argv=None) -> int:
     c.add_argument("--copy-mib", type=int, default=512)
     c.add_argument("--json", default="")
     c.add_argument("--meta", default="{}", help="JSON object stored beside the table (workload keys)")
+    c.add_argument("--last", type=int, default=0, help="average only each kernel's last N dispatches")
+    p = sub.add_parser("counters")
+    p.add_argument("dir")
+    p.add_argument("command")
+    p.add_argument("--names", required=True, help="comma-separated counter names")
+    p.add_argument("--last", type=int, default=0, help="average only each kernel's last N dispatches")
     a = ap.parse_args(argv)
     if a.what == "trace":
         lines = trace(a.kt_dir)
+    elif a.what == "counters":
+        lines = counters(a.dir, a.names.split(","), a.last)
+        if a.last:
+            lines.insert(0, f"(mean per dispatch over each kernel's last {a.last} dispatches)")
     else:
-        lines, table = traffic(a.fetch_dir, a.write_dir, a.copy_mib << 20)
+        lines, table = traffic(a.fetch_dir, a.write_dir, a.copy_mib << 20, a.last)
+        if a.last:
+            lines.insert(0, f"(mean per dispatch over each kernel's last {a.last} dispatches)")
         if a.json:
             table.update(json.loads(a.meta))
             table["command"] = a.command
