@@ -42,6 +42,7 @@ SIGNATURES = {
     "fastembedr_hip_tsne_run": (_I, [_P, _I, _F, _F, _F, _F, _F]),
     "fastembedr_hip_tsne_sync": (_I, [_P]),
     "fastembedr_hip_tsne_kl": (_I, [_P, _DP]),
+    "fastembedr_hip_tsne_kl_rows": (_I, [_P, _DP, _P]),
     "fastembedr_hip_tsne_set_repulsion": (_I, [_P, _I, _I, _I, _F]),
     "fastembedr_hip_tsne_interp_info": (_I, [_P, _IP, _IP, _IP, _FP, _DP]),
     "fastembedr_hip_tsne_attraction_info": (_I, [_P, _LLP, _IP]),

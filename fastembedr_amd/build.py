@@ -36,6 +36,13 @@ DEVICE_FLAGS = [
 ]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall", "-D__HIP_PLATFORM_AMD__"]
 
+# Translation units: device code (hipcc with DEVICE_FLAGS) and the host
+# orchestration (hipcc with HOST_FLAGS).  The R package's configure fragment
+# (integration/r/configure.hip) lists the same units and flags.
+DEVICE_UNITS = ("embedding_hip_kernels", "attraction_tiles_hip", "transform_hip", "interp_grid_hip", "knn_hip",
+                "metrics_hip")
+HOST_UNITS = ("embedding_hip_session",)
+
 
 def _hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
@@ -59,13 +66,25 @@ def build(verbose: bool = True) -> Path:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     inc = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
     objs = []
-    for name in ("embedding_hip_kernels", "attraction_tiles_hip", "transform_hip", "interp_grid_hip", "knn_hip", "metrics_hip"):
-        obj = BUILD_DIR / f"{name}.o"
-        _run([hipcc, *DEVICE_FLAGS, *inc, "-c", str(CSRC / f"{name}.hip"), "-o", str(obj)])
-        objs.append(str(obj))
-    sobj = BUILD_DIR / "embedding_hip_session.o"
-    _run([hipcc, *HOST_FLAGS, *inc, "-c", str(CSRC / "embedding_hip_session.cpp"), "-o", str(sobj)])
-    objs.append(str(sobj))
+    jobs = [([hipcc, *DEVICE_FLAGS, *inc, "-c", str(CSRC / f"{name}.hip"), "-o", str(BUILD_DIR / f"{name}.o")],
+             BUILD_DIR / f"{name}.o") for name in DEVICE_UNITS]
+    jobs += [([hipcc, *HOST_FLAGS, *inc, "-c", str(CSRC / f"{name}.cpp"), "-o", str(BUILD_DIR / f"{name}.o")],
+              BUILD_DIR / f"{name}.o") for name in HOST_UNITS]
+    # the units compile independently: run them side by side
+    workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", "0")) or (os.cpu_count() or 1)))
+    pending = list(jobs)
+    running = []
+    while pending or running:
+        while pending and len(running) < workers:
+            cmd, _ = pending.pop(0)
+            print("+", " ".join(cmd), flush=True)
+            running.append((cmd, subprocess.Popen(cmd)))
+        cmd, proc = running.pop(0)
+        if proc.wait() != 0:
+            for _, other in running:
+                other.wait()
+            raise subprocess.CalledProcessError(proc.returncode, cmd)
+    objs = [str(obj) for _, obj in jobs]
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)])
     os.replace(tmp, LIB)

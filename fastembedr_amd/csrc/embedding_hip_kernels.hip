@@ -1107,12 +1107,16 @@ __global__ __launch_bounds__(256) void k_exact_z_double(const float2* __restrict
   if (threadIdx.x == 0) partial[blockIdx.x] = z;
 }
 
+// Per-row KL terms (src/tsne_neighbors.cpp:1258-1285): each row's sum in
+// fp64, written to row_out when given, and the rows' block partial sums.
 __global__ __launch_bounds__(256) void k_kl_rows(const int* __restrict__ row_ptr, const int* __restrict__ col,
                                                  const float* __restrict__ val, const float2* __restrict__ y,
-                                                 int n, double sum_q, double* __restrict__ partial) {
+                                                 int n, double sum_q, double* __restrict__ partial,
+                                                 double* __restrict__ row_out) {
   double acc = 0.0;
   for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
     const float2 yi = y[i];
+    double row = 0.0;
     for (int e = row_ptr[i]; e < row_ptr[i + 1]; ++e) {
       const float2 yj = y[col[e]];
       float r2 = 0.0f;
@@ -1122,8 +1126,10 @@ __global__ __launch_bounds__(256) void k_kl_rows(const int* __restrict__ row_ptr
       r2 += dy * dy;
       const double p = static_cast<double>(val[e]);
       const double q = (1.0 / (1.0 + static_cast<double>(r2))) / sum_q;
-      acc += p * log((p + 1e-9) / (q + 1e-9));
+      row += p * log((p + 1e-9) / (q + 1e-9));
     }
+    if (row_out != nullptr) row_out[i] = row;
+    acc += row;
   }
   acc = block_sum<256>(acc);
   if (threadIdx.x == 0) partial[blockIdx.x] = acc;
@@ -1602,8 +1608,8 @@ hipError_t launch_exact_z_double(const float2* y, int n, double* z_partial, hipS
 }
 
 hipError_t launch_kl_rows(const Csr& p, const float2* y, double sum_q, double* partial, int blocks,
-                          hipStream_t stream) {
-  k_kl_rows<<<blocks, 256, 0, stream>>>(p.row_ptr, p.col, p.val, y, p.n, sum_q, partial);
+                          hipStream_t stream, double* row_out) {
+  k_kl_rows<<<blocks, 256, 0, stream>>>(p.row_ptr, p.col, p.val, y, p.n, sum_q, partial, row_out);
   return hipGetLastError();
 }
 

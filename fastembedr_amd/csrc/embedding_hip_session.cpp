@@ -23,7 +23,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/fastembedr_hip.h"
+#include "fastembedr_hip.h"
 #include "knn_device.h"
 #include "metrics_device.h"
 #include "tsne_device.h"
@@ -1456,7 +1456,9 @@ int fastembedr_hip_tsne_interp_info(fastembedr_hip_tsne* s, int* boxes, int* nod
   return 0;
 }
 
-int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* s, double* kl) {
+int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* s, double* kl) { return fastembedr_hip_tsne_kl_rows(s, kl, nullptr); }
+
+int fastembedr_hip_tsne_kl_rows(fastembedr_hip_tsne* s, double* kl, double* row_costs) {
   if (!valid_state_args(s) || kl == nullptr) return 1;
   const int zb = fehip::exact_blocks_for(s->n);
   std::vector<double> part(static_cast<std::size_t>(std::max(zb, 1024)));
@@ -1470,7 +1472,13 @@ int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* s, double* kl) {
   for (int b = 0; b < zb; ++b) z += part[b];
   const double sum_q = static_cast<double>(static_cast<float>(std::max(z, static_cast<double>(FLT_MIN))));
   const int kb = 1024;
-  if (!hip_ok(fehip::launch_kl_rows(s->work_p(), s->y_a(), sum_q, s->dpartial, kb, s->stream), "kl launch") ||
+  // Row terms go to the gradient buffer (n 8-byte values, unused between
+  // iterations) and are returned through the permuted download, which moves
+  // 8-byte elements.
+  double* rows_dev = row_costs != nullptr ? reinterpret_cast<double*>(s->grad) : nullptr;
+  static_assert(sizeof(double) == sizeof(float2), "a row term fits one float2 slot");
+  if (!hip_ok(fehip::launch_kl_rows(s->work_p(), s->y_a(), sum_q, s->dpartial, kb, s->stream, rows_dev),
+              "kl launch") ||
       !hip_ok(hipMemcpyAsync(part.data(), s->dpartial, kb * sizeof(double), hipMemcpyDeviceToHost, s->stream),
               "copy kl partials") ||
       !hip_ok(hipStreamSynchronize(s->stream), "kl sync")) {
@@ -1479,6 +1487,10 @@ int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* s, double* kl) {
   double total = 0.0;
   for (int b = 0; b < kb; ++b) total += part[b];
   *kl = total;
+  if (row_costs != nullptr &&
+      !download_permuted(s, reinterpret_cast<const float2*>(rows_dev), reinterpret_cast<float*>(row_costs))) {
+    return 1;
+  }
   return 0;
 }
 

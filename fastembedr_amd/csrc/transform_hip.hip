@@ -35,7 +35,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/fastembedr_hip.h"
+#include "fastembedr_hip.h"
 #include "tsne_device.h"
 
 namespace fehip {

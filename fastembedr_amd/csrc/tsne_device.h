@@ -346,7 +346,8 @@ hipError_t launch_exact_repulsion(const float2* y, int n, float2* rep, double* z
                                   hipStream_t stream);
 hipError_t launch_exact_z_double(const float2* y, int n, double* z_partial, hipStream_t stream);
 int exact_blocks_for(int n);
+// row_out (n doubles, may be null) receives each row's KL term.
 hipError_t launch_kl_rows(const Csr& p, const float2* y, double sum_q, double* partial, int blocks,
-                          hipStream_t stream);
+                          hipStream_t stream, double* row_out = nullptr);
 
 }  // namespace fehip

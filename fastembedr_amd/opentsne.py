@@ -127,6 +127,9 @@ class OpenTsneResult:
     config: dict
     itercosts: np.ndarray = field(default_factory=lambda: np.zeros(0))
     itercost_iterations: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int32))
+    # per-row KL terms of the final layout when costs are recorded
+    # (src/tsne_neighbors.cpp:1816-1823), else empty
+    costs: np.ndarray = field(default_factory=lambda: np.zeros(0))
 
 
 def _is_device_knn(knn) -> bool:
@@ -287,6 +290,7 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
     out = np.empty((n, 2), np.float32)
     itercosts = np.zeros(0)
     iters = np.zeros(0, np.int32)
+    row_costs = np.zeros(0)
     lr_early = n / early_ex if lr_auto else lr_value
     lr_normal = n / normal_ex if lr_auto else lr_value
     if record_costs or verbose or interp is not None:
@@ -327,6 +331,8 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
             out = sess.y
             itercosts = np.asarray(costs)
             iters = np.asarray(its, np.int32)
+            if record_costs:
+                _, row_costs = sess.kl_rows()
         finally:
             sess.close()
     else:
@@ -367,4 +373,4 @@ def opentsne_knn(indices, distances=None, n_neighbors: int | None = None, perple
         provenance="openTSNE_style_native_hip_symmetric_knn_gpu_probability_optimizer",
     )
     return OpenTsneResult(layout=out.astype(np.float64), config=config, itercosts=itercosts,
-                          itercost_iterations=iters)
+                          itercost_iterations=iters, costs=row_costs)

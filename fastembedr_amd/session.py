@@ -176,6 +176,13 @@ class TsneSession:
         _lib.check(self._lib.fastembedr_hip_tsne_kl(self._h, C.byref(v)), "kl")
         return float(v.value)
 
+    def kl_rows(self) -> tuple[float, np.ndarray]:
+        """Exact KL and each row's term (the reference's per-row `costs`)."""
+        v = C.c_double()
+        rows = np.empty(self.n, np.float64)
+        _lib.check(self._lib.fastembedr_hip_tsne_kl_rows(self._h, C.byref(v), _ptr(rows)), "kl_rows")
+        return float(v.value), rows
+
     # -- timing -------------------------------------------------------------
     def set_timing(self, enabled: bool, only: str | None = None) -> None:
         """Per-kernel HIP-event timing of run(); `only` names the one kernel

@@ -193,6 +193,12 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_attraction_slots(fastembedr_hip_tsne*
  * the O(n^2) normalisation computed on the device in fp64. */
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* session, double* kl);
 
+/* The same KL and, when row_costs is not NULL, each row's term (n doubles,
+ * caller's numbering): the per-row costs the reference's CPU driver returns
+ * as `costs` when costs are recorded (src/tsne_neighbors.cpp:1258-1285,
+ * 1816-1823). */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kl_rows(fastembedr_hip_tsne* session, double* kl, double* row_costs);
+
 /* Per-kernel timing.  While enabled, run() records HIP events around every
  * kernel (enabled == 1), or around the kernel with id enabled - 2 only
  * (enabled >= 2), so that the other launches run without event overhead;

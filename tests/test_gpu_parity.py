@@ -215,9 +215,23 @@ def test_kl_matches_oracle(hip, oracle_mod, mid_problem):
     with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
         s.set_state(y)
         kl = s.kl()
+        kl2, rows = s.kl_rows()
         P = oracle_mod.OracleP.wrap(*s.csr())
-    ref = P.kl(y, threads=4)
+        # after iterations the session works in its own (renumbered) order
+        s.run(30, 12.0, 0.5, 3000 / 12.0)
+        s.sync()
+        y_run = s.y
+        assert s.attraction_info()["renumbers"] >= 1
+        kl_run, rows_run = s.kl_rows()
+    ref, ref_rows = P.kl(y, threads=4, row_costs=True)
     assert abs(kl - ref) <= 1e-6 * abs(ref)
+    assert kl2 == kl
+    # each row's term (the reference's per-row `costs`), in the caller's numbering
+    assert np.abs(rows - ref_rows).max() <= 1e-6 * np.abs(ref_rows).max()
+    assert abs(float(rows.sum()) - kl) <= 1e-9 * abs(kl)
+    ref_run, ref_rows_run = P.kl(y_run, threads=4, row_costs=True)
+    assert abs(kl_run - ref_run) <= 1e-6 * abs(ref_run)
+    assert np.abs(rows_run - ref_rows_run).max() <= 1e-6 * np.abs(ref_rows_run).max()
 
 
 def _one_shot(fn_name, idx, dist, init, n_early, n_norm, device=False, shape=None):
@@ -293,3 +307,6 @@ def test_opentsne_knn_api(hip):
                            early_exaggeration_iter=30, n_iter=40, seed=3, record_costs=True)
     assert list(rec.itercost_iterations) == [50, 70]
     assert np.all(np.isfinite(rec.itercosts))
+    assert rec.costs.shape == (1200,)
+    assert abs(float(rec.costs.sum()) - rec.itercosts[-1]) <= 1e-9 * abs(rec.itercosts[-1])
+    assert res.costs.size == 0
