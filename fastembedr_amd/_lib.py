@@ -56,6 +56,11 @@ SIGNATURES = {
     "fastembedr_hip_transform_tsne": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, C.c_double, _I, _I, C.c_double,
                                            C.c_double, C.c_double, C.c_double, C.c_double, C.c_double,
                                            C.c_double, _I, _I, _I, _P, _IP]),
+    "fastembedr_hip_transform_tsne_grid": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, C.c_double, _I, _I, C.c_double,
+                                                C.c_double, C.c_double, C.c_double, C.c_double, C.c_double,
+                                                C.c_double, _I, _I, _I, C.c_double, _P, _LLP]),
+    "fastembedr_hip_transform_grid_probe": (_I, [_P, _I, _P, _P, _I, _I, C.c_double, _P, _P, _I, C.c_double, _I,
+                                                 _I, C.c_double, _P, _LLP]),
     "fastembedr_hip_transform_tsne_noalloc": (_I, [_P, _I, _P, _P, _I, _I, _P, _I, C.c_double, _I, _I, C.c_double,
                                                    C.c_double, C.c_double, C.c_double, C.c_double, C.c_double,
                                                    C.c_double, _I, _I, _I, _P, _IP]),

@@ -1269,7 +1269,7 @@ struct ProjRng {
 void proj_orthonormalize(std::vector<double>& y, int d, ProjRng& rng) {
   constexpr int m = kProjDim;
   for (int j = 0; j < m; ++j) {
-    for (int attempt = 0;; ++attempt) {
+    for (;;) {
       double before = 0.0;
       for (int i = 0; i < d; ++i) before += y[static_cast<std::size_t>(i) * m + j] * y[static_cast<std::size_t>(i) * m + j];
       for (int pass = 0; pass < 2; ++pass) {

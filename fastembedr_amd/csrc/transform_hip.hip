@@ -20,8 +20,15 @@
 //
 // One thread owns one query and walks its samples in the reference's order,
 // so every sum is formed exactly as the CPU forms it: the two sampling passes
-// regenerate the same indices instead of storing them.  The reference layout
-// (16 bytes per point, 1.1 MB at 70K points) stays in L2.
+// regenerate the same indices instead of storing them.  With the reference
+// fixed, a query's iterations depend only on its own state, so one launch runs
+// the whole schedule with each query's layout, update and gains in registers
+// (k_transform_run).  The reference layout (16 bytes per point, 1.1 MB at 70K
+// points) stays in L2.
+//
+// A third repulsion, with no counterpart in the reference, precomputes the
+// reference's repulsion fields on an interpolation grid once per call and
+// interpolates them at each query (fastembedr_hip_transform_tsne_grid).
 
 #include <hip/hip_runtime.h>
 
@@ -182,75 +189,233 @@ __device__ inline double2 repulsion(const double2* __restrict__ ref, int n_ref, 
   return make_double2(gx, gy);
 }
 
+// ---- reference grid (no counterpart in the reference) ---------------------
+// The fixed reference's repulsion fields Z(y) = sum_j q(y - r_j) and
+// F(y) = sum_j q(y - r_j)^2 (y - r_j) are summed directly at the nodes of an
+// interpolation grid once per call (k_grid_fields); a query's repulsion is
+// then -F / Z with both fields interpolated (order 3, Lagrange) from the
+// 3 x 3 nodes of its box.  The grid is one square of nb x nb boxes of width
+// w from lo on both axes, 3 nodes per box and axis at 1/6, 1/2 and 5/6 of the
+// box, m = 3 nb nodes per axis, node (a, b) at (lo + (a + 1/2) h,
+// lo + (b + 1/2) h) with h = w / 3.  A query outside the square (or whose
+// interpolated Z is not positive) takes the exact sums over every reference
+// point.
+constexpr int kGridOrder = 3;
+constexpr int kGridMaxNodes = 2048;
+
+struct GridGeo {
+  double lo, w, h;
+  int nb, m;
+};
+
+__device__ inline void grid_weights(double t, double* w) {
+#pragma clang fp contract(off)
+  const double a = t - 1.0 / 6.0;
+  const double b = t - 0.5;
+  const double c = t - 5.0 / 6.0;
+  w[0] = 4.5 * (b * c);
+  w[1] = -9.0 * (a * c);
+  w[2] = 4.5 * (a * b);
+}
+
+// field: m * m double4 of (Z, Fx, Fy, 0), node (a, b) at b * m + a.
+__device__ inline bool grid_repulsion(const double4* __restrict__ field, const GridGeo& g, double yx, double yy,
+                                      double* gx, double* gy) {
+#pragma clang fp contract(off)
+  const double ux = (yx - g.lo) / g.w;
+  const double uy = (yy - g.lo) / g.w;
+  const double fx0 = floor(ux);
+  const double fy0 = floor(uy);
+  if (!(fx0 >= 0.0 && fx0 < static_cast<double>(g.nb) && fy0 >= 0.0 && fy0 < static_cast<double>(g.nb))) {
+    return false;
+  }
+  const int bx = static_cast<int>(fx0);
+  const int by = static_cast<int>(fy0);
+  double wx[3], wy[3];
+  grid_weights(ux - fx0, wx);
+  grid_weights(uy - fy0, wy);
+  double z = 0.0, fx = 0.0, fy = 0.0;
+#pragma unroll
+  for (int sb = 0; sb < kGridOrder; ++sb) {
+    const std::size_t row = static_cast<std::size_t>(by * kGridOrder + sb) * static_cast<std::size_t>(g.m);
+#pragma unroll
+    for (int sa = 0; sa < kGridOrder; ++sa) {
+      const double wgt = wx[sa] * wy[sb];
+      const double4 f = field[row + static_cast<std::size_t>(bx * kGridOrder + sa)];
+      z += wgt * f.x;
+      fx += wgt * f.y;
+      fy += wgt * f.z;
+    }
+  }
+  if (!(z > 0.0)) return false;
+  const double inv = 1.0 / z;
+  *gx = -fx * inv;
+  *gy = -fy * inv;
+  return true;
+}
+
+// One node per thread; the reference is staged through LDS in tiles and
+// summed in index order.
+constexpr int kFieldThreads = 256;
+__global__ __launch_bounds__(kFieldThreads) void k_grid_fields(const double2* __restrict__ ref, int n_ref,
+                                                               GridGeo g, double4* __restrict__ field) {
+#pragma clang fp contract(off)
+  __shared__ double2 tile[kFieldThreads];
+  const int nodes = g.m * g.m;
+  const int v = static_cast<int>(blockIdx.x) * kFieldThreads + static_cast<int>(threadIdx.x);
+  const double nx = g.lo + (static_cast<double>(v % g.m) + 0.5) * g.h;
+  const double ny = g.lo + (static_cast<double>(v / g.m) + 0.5) * g.h;
+  double z = 0.0, fx = 0.0, fy = 0.0;
+  for (int base = 0; base < n_ref; base += kFieldThreads) {
+    const int j = base + static_cast<int>(threadIdx.x);
+    __syncthreads();
+    if (j < n_ref) tile[threadIdx.x] = ref[j];
+    __syncthreads();
+    const int count = min(kFieldThreads, n_ref - base);
+    for (int t = 0; t < count; ++t) {
+      const double2 r = tile[t];
+      const double dx = nx - r.x;
+      const double dy = ny - r.y;
+      const double q = 1.0 / (1.0 + dx * dx + dy * dy);
+      const double q2 = q * q;
+      z += q;
+      fx += q2 * dx;
+      fy += q2 * dy;
+    }
+  }
+  if (v < nodes) field[v] = make_double4(z, fx, fy, 0.0);
+}
+
+// ---- one query's iteration ----------------------------------------------------
+enum RepulsionMode : int { kSampled = 0, kExact = 1, kGrid = 2 };
+
+// Attraction exaggeration * p * q * d over the query's neighbours, added to (gx, gy).
+__device__ inline void attraction(const double2* __restrict__ ref, const int* __restrict__ idx_cm,
+                                  const double* __restrict__ p_cm, int nq, int k, int offset, int i, double ex,
+                                  double yx, double yy, double& gx, double& gy) {
+#pragma clang fp contract(off)
+  for (int j = 0; j < k; ++j) {
+    const std::size_t e = static_cast<std::size_t>(j) * nq + i;
+    const double2 p = ref[idx_cm[e] - offset];
+    const double dx = yx - p.x;
+    const double dy = yy - p.y;
+    const double q = 1.0 / (1.0 + dx * dx + dy * dy);
+    const double c = ex * p_cm[e] * q;
+    gx += c * dx;
+    gy += c * dy;
+  }
+}
+
+// Gradient-norm clip, gains, momentum, step-norm clip and y += update (:2040-2075).
+__device__ inline void update_query(double gx, double gy, double momentum, double learning_rate, double max_grad,
+                                    double max_step, double2& y, double2& u, double2& w) {
+#pragma clang fp contract(off)
+  const double gn = gx * gx + gy * gy;
+  if (gn > max_grad * max_grad) {
+    const double s = max_grad / (sqrt(gn) + 1e-12);
+    gx *= s;
+    gy *= s;
+  }
+  w.x = sign0(u.x) != sign0(gx) ? w.x + 0.2 : w.x * 0.8 + 0.01;
+  if (w.x < 0.01) w.x = 0.01;
+  u.x = momentum * u.x - learning_rate * w.x * gx;
+  w.y = sign0(u.y) != sign0(gy) ? w.y + 0.2 : w.y * 0.8 + 0.01;
+  if (w.y < 0.01) w.y = 0.01;
+  u.y = momentum * u.y - learning_rate * w.y * gy;
+  const double sn = u.x * u.x + u.y * u.y;
+  if (sn > max_step * max_step) {
+    const double s = max_step / (sqrt(sn) + 1e-12);
+    u.x *= s;
+    u.y *= s;
+  }
+  y = make_double2(y.x + u.x, y.y + u.y);
+}
+
+// The repulsion of query i in the given mode; returns false when a grid query
+// took the exact sums.
+template <int MODE>
+__device__ inline bool query_repulsion(const double2* __restrict__ ref, int n_ref, int samples, std::uint32_t state,
+                                       const double4* __restrict__ field, const GridGeo& g, double yx, double yy,
+                                       double& gx, double& gy) {
+  if (MODE == kGrid) {
+    if (grid_repulsion(field, g, yx, yy, &gx, &gy)) return true;
+    const double2 r = repulsion<true>(ref, n_ref, n_ref, 0u, yx, yy);
+    gx = r.x;
+    gy = r.y;
+    return false;
+  }
+  const double2 r = repulsion<MODE == kExact>(ref, n_ref, samples, state, yx, yy);
+  gx = r.x;
+  gy = r.y;
+  return true;
+}
+
+__device__ inline std::uint32_t query_state(std::uint32_t iter_seed, int i) {
+  return hash32(iter_seed ^ (static_cast<std::uint32_t>(i + 1) * 0x9e3779b9u));
+}
+
 struct StepParams {
   double exaggeration, momentum, learning_rate, max_grad, max_step;
   int samples;      // n_reference (exact) or n_negatives (sampled)
   int iter_seed;
 };
 
-// One iteration for every query; GRAD_ONLY writes the gradient and leaves
-// the state alone.
-template <bool EXACT, bool GRAD_ONLY>
-__global__ __launch_bounds__(kQueryThreads) void k_transform_step(const double2* __restrict__ ref, int n_ref,
-                                                                  const int* __restrict__ idx_cm,
-                                                                  const double* __restrict__ p_cm, int nq, int k,
-                                                                  int offset, StepParams sp, double2* __restrict__ y,
-                                                                  double2* __restrict__ upd,
-                                                                  double2* __restrict__ gains,
-                                                                  double2* __restrict__ grad_out) {
-#pragma clang fp contract(off)
+// One gradient for every query (parity probes): grad_out, state untouched.
+template <int MODE>
+__global__ __launch_bounds__(kQueryThreads) void k_transform_gradient(
+    const double2* __restrict__ ref, int n_ref, const int* __restrict__ idx_cm, const double* __restrict__ p_cm,
+    int nq, int k, int offset, StepParams sp, const double4* __restrict__ field, GridGeo g,
+    const double2* __restrict__ y, double2* __restrict__ grad_out, unsigned long long* __restrict__ exact_count) {
   const int i = static_cast<int>(blockIdx.x) * kQueryThreads + static_cast<int>(threadIdx.x);
   if (i >= nq) return;
   const double2 yi = y[i];
-  const std::uint32_t state =
-      hash32(static_cast<std::uint32_t>(sp.iter_seed) ^ (static_cast<std::uint32_t>(i + 1) * 0x9e3779b9u));
-  const double2 rep = repulsion<EXACT>(ref, n_ref, sp.samples, state, yi.x, yi.y);
-  double gx = rep.x, gy = rep.y;
-  for (int j = 0; j < k; ++j) {
-    const std::size_t e = static_cast<std::size_t>(j) * nq + i;
-    const double2 p = ref[idx_cm[e] - offset];
-    const double dx = yi.x - p.x;
-    const double dy = yi.y - p.y;
-    const double q = 1.0 / (1.0 + dx * dx + dy * dy);
-    const double c = sp.exaggeration * p_cm[e] * q;
-    gx += c * dx;
-    gy += c * dy;
+  double gx = 0.0, gy = 0.0;
+  if (!query_repulsion<MODE>(ref, n_ref, sp.samples, query_state(static_cast<std::uint32_t>(sp.iter_seed), i), field,
+                             g, yi.x, yi.y, gx, gy)) {
+    atomicAdd(exact_count, 1ull);
   }
-  if (GRAD_ONLY) {
-    grad_out[i] = make_double2(gx, gy);
-    return;
-  }
-  const double gn = gx * gx + gy * gy;
-  if (gn > sp.max_grad * sp.max_grad) {
-    const double s = sp.max_grad / (sqrt(gn) + 1e-12);
-    gx *= s;
-    gy *= s;
-  }
-  double2 u = upd[i];
-  double2 w = gains[i];
-  w.x = sign0(u.x) != sign0(gx) ? w.x + 0.2 : w.x * 0.8 + 0.01;
-  if (w.x < 0.01) w.x = 0.01;
-  u.x = sp.momentum * u.x - sp.learning_rate * w.x * gx;
-  w.y = sign0(u.y) != sign0(gy) ? w.y + 0.2 : w.y * 0.8 + 0.01;
-  if (w.y < 0.01) w.y = 0.01;
-  u.y = sp.momentum * u.y - sp.learning_rate * w.y * gy;
-  const double sn = u.x * u.x + u.y * u.y;
-  if (sn > sp.max_step * sp.max_step) {
-    const double s = sp.max_step / (sqrt(sn) + 1e-12);
-    u.x *= s;
-    u.y *= s;
-  }
-  upd[i] = u;
-  gains[i] = w;
-  y[i] = make_double2(yi.x + u.x, yi.y + u.y);
+  attraction(ref, idx_cm, p_cm, nq, k, offset, i, sp.exaggeration, yi.x, yi.y, gx, gy);
+  grad_out[i] = make_double2(gx, gy);
 }
 
-__global__ __launch_bounds__(kQueryThreads) void k_transform_reset(double2* __restrict__ upd,
-                                                                   double2* __restrict__ gains, int nq) {
-  const int i = static_cast<int>(blockIdx.x) * kQueryThreads + static_cast<int>(threadIdx.x);
+// The whole schedule of the reference's transform loop (:1985-2080) for one
+// query per thread.  With the reference fixed, a query's iterations depend on
+// nothing but its own state, so running them back to back in registers gives
+// exactly the iteration-by-iteration result; y holds the initial layout on
+// entry and the final one on exit.
+struct RunSchedule {
+  double early_exaggeration, exaggeration, initial_momentum, final_momentum, learning_rate, max_grad, max_step;
+  int early_iter, total, samples;
+  unsigned int seed_base;  // (seed or 5489): iteration it uses seed_base + 65537 (it + 1) (:2009)
+};
+
+constexpr int kRunThreads = 64;  // small blocks spread the queries evenly over the CUs
+
+template <int MODE>
+__global__ __launch_bounds__(kRunThreads) void k_transform_run(
+    const double2* __restrict__ ref, int n_ref, const int* __restrict__ idx_cm, const double* __restrict__ p_cm,
+    int nq, int k, int offset, RunSchedule rs, const double4* __restrict__ field, GridGeo g,
+    double2* __restrict__ y, unsigned long long* __restrict__ exact_count) {
+  const int i = static_cast<int>(blockIdx.x) * kRunThreads + static_cast<int>(threadIdx.x);
   if (i >= nq) return;
-  upd[i] = make_double2(0.0, 0.0);
-  gains[i] = make_double2(1.0, 1.0);
+  double2 yi = y[i];
+  double2 u = make_double2(0.0, 0.0);
+  double2 w = make_double2(1.0, 1.0);
+  unsigned long long exact_evals = 0;
+  for (int it = 0; it < rs.total; ++it) {
+    const bool early = it < rs.early_iter;
+    const std::uint32_t iter_seed = rs.seed_base + 65537u * static_cast<std::uint32_t>(it + 1);
+    double gx = 0.0, gy = 0.0;
+    if (!query_repulsion<MODE>(ref, n_ref, rs.samples, query_state(iter_seed, i), field, g, yi.x, yi.y, gx, gy)) {
+      ++exact_evals;
+    }
+    attraction(ref, idx_cm, p_cm, nq, k, offset, i, early ? rs.early_exaggeration : rs.exaggeration, yi.x, yi.y, gx,
+               gy);
+    update_query(gx, gy, early ? rs.initial_momentum : rs.final_momentum, rs.learning_rate, rs.max_grad,
+                 rs.max_step, yi, u, w);
+  }
+  y[i] = yi;
+  if (exact_evals != 0ull) atomicAdd(exact_count, exact_evals);
 }
 
 // ---------------------------------------------------------------------------
@@ -264,11 +429,6 @@ bool ok(hipError_t e, const char* where) {
 
 int query_blocks(int nq) { return (nq + kQueryThreads - 1) / kQueryThreads; }
 
-// (seed or 5489) + 65537 (iter + 1) with wrap-around (:2009).
-int iteration_seed(int seed, int iter) {
-  const std::uint32_t base = seed == INT_MIN ? 5489u : static_cast<std::uint32_t>(seed);
-  return static_cast<int>(base + 65537u * static_cast<std::uint32_t>(iter + 1));
-}
 
 // 1 when every index is in [1, n_ref] (:1290-1302), else 0.
 int reference_offset(const int* idx_cm, std::size_t count, int n_ref) {
@@ -280,28 +440,32 @@ int reference_offset(const int* idx_cm, std::size_t count, int n_ref) {
   return (lo >= 1 && hi <= n_ref) ? 1 : 0;
 }
 
-// Device buffers of one call, carved from a single allocation.
+// Device buffers of one call, carved from a single allocation; the grid
+// mode's node fields are a second allocation once the grid size is known.
 struct TransformBuffers {
   void* base = nullptr;
+  void* field_base = nullptr;
   double2* ref = nullptr;
   int* idx = nullptr;
   double* dist = nullptr;
   double* p = nullptr;
   double2* y = nullptr;
-  double2* upd = nullptr;
-  double2* gains = nullptr;
   double2* grad = nullptr;
+  unsigned long long* counter = nullptr;
+  double4* field = nullptr;
   hipStream_t stream = nullptr;
   ~TransformBuffers() {
     if (stream != nullptr) (void)hipStreamSynchronize(stream);
+    if (field_base != nullptr) (void)hipFree(field_base);
     if (base != nullptr) (void)hipFree(base);
     if (stream != nullptr) (void)hipStreamDestroy(stream);
   }
   bool init(int n_ref, int nq, int k) {
     const auto up = [](std::size_t b) { return (b + 255) & ~static_cast<std::size_t>(255); };
     const std::size_t nk = static_cast<std::size_t>(nq) * k;
+    const std::size_t yb = up(sizeof(double2) * nq);
     const std::size_t sizes[] = {up(sizeof(double2) * n_ref), up(sizeof(int) * nk), up(sizeof(double) * nk),
-                                 up(sizeof(double) * nk), 4 * up(sizeof(double2) * nq)};
+                                 up(sizeof(double) * nk), 2 * yb, 256};
     std::size_t total = 0;
     for (std::size_t s : sizes) total += s;
     if (!ok(hipStreamCreate(&stream), "hipStreamCreate(transform)") ||
@@ -317,11 +481,16 @@ struct TransformBuffers {
     c += sizes[2];
     p = reinterpret_cast<double*>(c);
     c += sizes[3];
-    const std::size_t yb = up(sizeof(double2) * nq);
     y = reinterpret_cast<double2*>(c);
-    upd = reinterpret_cast<double2*>(c + yb);
-    gains = reinterpret_cast<double2*>(c + 2 * yb);
-    grad = reinterpret_cast<double2*>(c + 3 * yb);
+    grad = reinterpret_cast<double2*>(c + yb);
+    c += sizes[4];
+    counter = reinterpret_cast<unsigned long long*>(c);
+    return true;
+  }
+  bool init_field(int m) {
+    const std::size_t bytes = sizeof(double4) * static_cast<std::size_t>(m) * static_cast<std::size_t>(m);
+    if (!ok(hipMalloc(&field_base, bytes), "hipMalloc(reference grid)")) return false;
+    field = static_cast<double4*>(field_base);
     return true;
   }
 };
@@ -345,16 +514,71 @@ bool upload(TransformBuffers& b, const double* ref_cm, int n_ref, const int* idx
          ok(hipMemcpy(b.dist, dist_cm, nk * sizeof(double), hipMemcpyHostToDevice), "distance upload");
 }
 
-template <bool GRAD_ONLY>
-hipError_t launch_step(bool exact, const TransformBuffers& b, int n_ref, int nq, int k, int offset,
-                       const StepParams& sp) {
-  const int blocks = query_blocks(nq);
-  if (exact) {
-    k_transform_step<true, GRAD_ONLY><<<blocks, kQueryThreads, 0, b.stream>>>(
-        b.ref, n_ref, b.idx, b.p, nq, k, offset, sp, b.y, b.upd, b.gains, b.grad);
+// The grid around the reference rows and the queries' layout (interleaved
+// rows): one square over both axes, widened on each side by max(1, 5 % of
+// the span), max(min_intervals, ceil(span / ints_in_interval)) boxes per axis
+// and at most kGridMaxNodes nodes.
+GridGeo grid_geometry(const double* ref, int n_ref, const double* y, int nq, int min_intervals, double ints) {
+  double lo = DBL_MAX, hi = -DBL_MAX;
+  for (std::size_t c = 0; c < 2 * static_cast<std::size_t>(n_ref); ++c) {
+    lo = std::min(lo, ref[c]);
+    hi = std::max(hi, ref[c]);
+  }
+  for (std::size_t c = 0; c < 2 * static_cast<std::size_t>(nq); ++c) {
+    if (!std::isfinite(y[c])) continue;
+    lo = std::min(lo, y[c]);
+    hi = std::max(hi, y[c]);
+  }
+  double span = hi - lo;
+  if (!(span > 0.0) || !std::isfinite(span)) span = 1.0;
+  const double margin = std::max(1.0, 0.05 * span);
+  GridGeo g{};
+  g.lo = lo - margin;
+  span += 2.0 * margin;
+  double boxes = std::max(static_cast<double>(min_intervals), std::ceil(span / ints));
+  boxes = std::min(boxes, static_cast<double>(kGridMaxNodes / kGridOrder));
+  g.nb = static_cast<int>(boxes);
+  g.w = span / static_cast<double>(g.nb);
+  g.h = g.w / static_cast<double>(kGridOrder);
+  g.m = g.nb * kGridOrder;
+  return g;
+}
+
+hipError_t launch_grid_fields(const double2* ref, int n_ref, const GridGeo& g, double4* field, hipStream_t st) {
+  const int nodes = g.m * g.m;
+  k_grid_fields<<<(nodes + kFieldThreads - 1) / kFieldThreads, kFieldThreads, 0, st>>>(ref, n_ref, g, field);
+  return hipGetLastError();
+}
+
+hipError_t launch_run(int mode, const double2* ref, int n_ref, const int* idx, const double* p, int nq, int k,
+                      int offset, const RunSchedule& rs, const double4* field, const GridGeo& g, double2* y,
+                      unsigned long long* counter, hipStream_t st) {
+  const int blocks = (nq + kRunThreads - 1) / kRunThreads;
+  if (mode == kGrid) {
+    k_transform_run<kGrid><<<blocks, kRunThreads, 0, st>>>(ref, n_ref, idx, p, nq, k, offset, rs, field, g, y,
+                                                          counter);
+  } else if (mode == kExact) {
+    k_transform_run<kExact><<<blocks, kRunThreads, 0, st>>>(ref, n_ref, idx, p, nq, k, offset, rs, field, g, y,
+                                                           counter);
   } else {
-    k_transform_step<false, GRAD_ONLY><<<blocks, kQueryThreads, 0, b.stream>>>(
-        b.ref, n_ref, b.idx, b.p, nq, k, offset, sp, b.y, b.upd, b.gains, b.grad);
+    k_transform_run<kSampled><<<blocks, kRunThreads, 0, st>>>(ref, n_ref, idx, p, nq, k, offset, rs, field, g, y,
+                                                             counter);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gradient(int mode, const TransformBuffers& b, int n_ref, int nq, int k, int offset,
+                           const StepParams& sp, const GridGeo& g) {
+  const int blocks = query_blocks(nq);
+  if (mode == kGrid) {
+    k_transform_gradient<kGrid><<<blocks, kQueryThreads, 0, b.stream>>>(b.ref, n_ref, b.idx, b.p, nq, k, offset, sp,
+                                                                        b.field, g, b.y, b.grad, b.counter);
+  } else if (mode == kExact) {
+    k_transform_gradient<kExact><<<blocks, kQueryThreads, 0, b.stream>>>(b.ref, n_ref, b.idx, b.p, nq, k, offset,
+                                                                         sp, b.field, g, b.y, b.grad, b.counter);
+  } else {
+    k_transform_gradient<kSampled><<<blocks, kQueryThreads, 0, b.stream>>>(b.ref, n_ref, b.idx, b.p, nq, k, offset,
+                                                                           sp, b.field, g, b.y, b.grad, b.counter);
   }
   return hipGetLastError();
 }
@@ -446,6 +670,82 @@ bool check_run_args(RunArgs& a) {
   return true;
 }
 
+RunSchedule make_schedule(const RunArgs& ra, int seed) {
+  RunSchedule rs{};
+  rs.early_exaggeration = ra.early_exaggeration;
+  rs.exaggeration = ra.exaggeration;
+  rs.initial_momentum = ra.initial_momentum;
+  rs.final_momentum = ra.final_momentum;
+  rs.learning_rate = ra.learning_rate;
+  rs.max_grad = ra.max_grad;
+  rs.max_step = ra.max_step;
+  rs.early_iter = ra.early_iter;
+  rs.total = ra.early_iter + ra.n_iter;
+  rs.samples = ra.exact ? ra.n_reference : ra.n_negatives;
+  rs.seed_base = seed == INT_MIN ? 5489u : static_cast<unsigned int>(seed);
+  return rs;
+}
+
+// Conditional P of every query, then its starting layout in b.y: y_init
+// (n x 2 column-major), the random draw (per-query mt19937 seeded through
+// mix_uint32, two normal_distribution<double>(0, 1e-4) draws, :1317-1335) or
+// the median / weighted initialisation on the device.
+bool prepare_queries(TransformBuffers& b, int n_query, int k, int offset, double perplexity, const double* y_init,
+                     int initialization, int seed) {
+  const int blocks = query_blocks(n_query);
+  k_transform_p<<<blocks, kQueryThreads, 0, b.stream>>>(b.dist, n_query, k, perplexity, b.p);
+  if (!ok(hipGetLastError(), "transform P launch")) return false;
+  std::vector<double> y_host;
+  if (y_init != nullptr) {
+    y_host = rows_of(y_init, n_query);
+  } else if (initialization == 2) {
+    y_host.resize(2 * static_cast<std::size_t>(n_query));
+    const unsigned int s = seed == INT_MIN ? 5489u : static_cast<unsigned int>(seed);
+    for (int i = 0; i < n_query; ++i) {
+      std::normal_distribution<double> normal(0.0, 1.0e-4);
+      std::mt19937 rng(hash32(s ^ (static_cast<std::uint32_t>(i + 1) * 0x9e3779b9u)));
+      y_host[2 * static_cast<std::size_t>(i)] = normal(rng);
+      y_host[2 * static_cast<std::size_t>(i) + 1] = normal(rng);
+    }
+  }
+  if (!y_host.empty()) {
+    // synchronous: the staging vector dies with this function
+    return ok(hipMemcpyAsync(b.y, y_host.data(), y_host.size() * sizeof(double), hipMemcpyHostToDevice, b.stream),
+              "initial layout upload") &&
+           ok(hipStreamSynchronize(b.stream), "transform sync");
+  }
+  k_transform_init<<<blocks, kQueryThreads, 0, b.stream>>>(b.ref, b.idx, b.dist, n_query, k, offset,
+                                                          initialization == 1 ? 1 : 0, b.y);
+  return ok(hipGetLastError(), "transform init launch");
+}
+
+// b.y -> out, n x 2 column-major; waits for the stream.
+bool download_layout(TransformBuffers& b, int n_query, double* out) {
+  std::vector<double> y(2 * static_cast<std::size_t>(n_query));
+  if (!ok(hipMemcpyAsync(y.data(), b.y, y.size() * sizeof(double), hipMemcpyDeviceToHost, b.stream),
+          "layout download") ||
+      !ok(hipStreamSynchronize(b.stream), "transform sync")) {
+    return false;
+  }
+  for (int i = 0; i < n_query; ++i) {
+    out[i] = y[2 * static_cast<std::size_t>(i)];
+    out[static_cast<std::size_t>(n_query) + i] = y[2 * static_cast<std::size_t>(i) + 1];
+  }
+  return true;
+}
+
+bool check_grid_settings(int n_interpolation_points, int min_num_intervals, double ints_in_interval) {
+  if (n_interpolation_points != kGridOrder) {
+    set_last_error("the reference grid supports 3 interpolation points per interval");
+    return false;
+  }
+  if (min_num_intervals < 1 || !(ints_in_interval > 0.0) || !std::isfinite(ints_in_interval)) {
+    set_last_error("min_num_intervals must be >= 1 and ints_in_interval positive and finite");
+    return false;
+  }
+  return true;
+}
+
 }  // namespace
 }  // namespace fehip
 
@@ -471,65 +771,76 @@ int fastembedr_hip_transform_tsne(const double* reference_layout, int n_referenc
              initial_momentum, final_momentum, max_grad_norm, max_step_norm, n_negatives, exact_repulsion_threshold,
              initialization};
   if (!check_run_args(ra)) return 1;
-  max_grad_norm = ra.max_grad;
-  max_step_norm = ra.max_step;
-  n_negatives = ra.n_negatives;
-  const bool exact = ra.exact;
-
   TransformBuffers b;
   if (!b.init(n_reference, n_query, k) ||
-      !upload(b, reference_layout, n_reference, indices, distances, n_query, k)) {
+      !upload(b, reference_layout, n_reference, indices, distances, n_query, k) ||
+      !prepare_queries(b, n_query, k, offset, perplexity, y_init, initialization, seed)) {
     return 1;
   }
-  const int blocks = query_blocks(n_query);
-  k_transform_p<<<blocks, kQueryThreads, 0, b.stream>>>(b.dist, n_query, k, perplexity, b.p);
-  if (!ok(hipGetLastError(), "transform P launch")) return 1;
-  std::vector<double> y_host;
-  if (y_init != nullptr) {
-    y_host = rows_of(y_init, n_query);
-  } else if (initialization == 2) {
-    // Per-query mt19937 seeded through mix_uint32, then two draws of
-    // normal_distribution<double>(0, 1e-4) (:1317-1335).
-    y_host.resize(2 * static_cast<std::size_t>(n_query));
-    const unsigned int s = seed == INT_MIN ? 5489u : static_cast<unsigned int>(seed);
-    for (int i = 0; i < n_query; ++i) {
-      std::normal_distribution<double> normal(0.0, 1.0e-4);
-      std::mt19937 rng(hash32(s ^ (static_cast<std::uint32_t>(i + 1) * 0x9e3779b9u)));
-      y_host[2 * static_cast<std::size_t>(i)] = normal(rng);
-      y_host[2 * static_cast<std::size_t>(i) + 1] = normal(rng);
-    }
+  const GridGeo none{};
+  if (!ok(launch_run(ra.exact ? kExact : kSampled, b.ref, n_reference, b.idx, b.p, n_query, k, offset,
+                     make_schedule(ra, seed), nullptr, none, b.y, b.counter, b.stream),
+          "transform run launch") ||
+      !download_layout(b, n_query, out)) {
+    return 1;
   }
-  if (!y_host.empty()) {
-    if (!ok(hipMemcpyAsync(b.y, y_host.data(), y_host.size() * sizeof(double), hipMemcpyHostToDevice, b.stream),
-            "initial layout upload")) {
-      return 1;
-    }
-  } else {
-    k_transform_init<<<blocks, kQueryThreads, 0, b.stream>>>(b.ref, b.idx, b.dist, n_query, k, offset,
-                                                            initialization == 1 ? 1 : 0, b.y);
-    if (!ok(hipGetLastError(), "transform init launch")) return 1;
+  if (repulsion_exact != nullptr) *repulsion_exact = ra.exact ? 1 : 0;
+  return 0;
+}
+
+int fastembedr_hip_transform_tsne_grid(const double* reference_layout, int n_reference, const int* indices,
+                                       const double* distances, int n_query, int k, const double* y_init,
+                                       int initialization, double perplexity, int n_iter,
+                                       int early_exaggeration_iter, double learning_rate, double early_exaggeration,
+                                       double exaggeration, double initial_momentum, double final_momentum,
+                                       double max_grad_norm, double max_step_norm, int seed,
+                                       int n_interpolation_points, int min_num_intervals, double ints_in_interval,
+                                       double* out, long long* stats) {
+  using namespace fehip;
+  clear_last_error();
+  if (out == nullptr || n_reference < 1 || n_query < 1 || k < 1 || reference_layout == nullptr ||
+      indices == nullptr || distances == nullptr) {
+    set_last_error("invalid transform arguments (NULL pointer or empty input).");
+    return 1;
   }
-  k_transform_reset<<<blocks, kQueryThreads, 0, b.stream>>>(b.upd, b.gains, n_query);
-  if (!ok(hipGetLastError(), "transform reset launch")) return 1;
-  const int total = early_exaggeration_iter + n_iter;
-  for (int it = 0; it < total; ++it) {
-    const bool early = it < early_exaggeration_iter;
-    StepParams sp{early ? early_exaggeration : exaggeration, early ? initial_momentum : final_momentum,
-                  learning_rate, max_grad_norm, max_step_norm, exact ? n_reference : n_negatives,
-                  iteration_seed(seed, it)};
-    if (!ok(launch_step<false>(exact, b, n_reference, n_query, k, offset, sp), "transform step launch")) return 1;
+  if (!check_grid_settings(n_interpolation_points, min_num_intervals, ints_in_interval)) return 1;
+  const int offset = reference_offset(indices, static_cast<std::size_t>(n_query) * k, n_reference);
+  if (!check_inputs(reference_layout, n_reference, indices, distances, n_query, k, perplexity, offset)) return 1;
+  RunArgs ra{n_reference, n_iter, early_exaggeration_iter, learning_rate, early_exaggeration, exaggeration,
+             initial_momentum, final_momentum, max_grad_norm, max_step_norm, 1, 1, initialization};
+  if (!check_run_args(ra)) return 1;
+  TransformBuffers b;
+  if (!b.init(n_reference, n_query, k) ||
+      !upload(b, reference_layout, n_reference, indices, distances, n_query, k) ||
+      !prepare_queries(b, n_query, k, offset, perplexity, y_init, initialization, seed)) {
+    return 1;
   }
-  std::vector<double> y(2 * static_cast<std::size_t>(n_query));
-  if (!ok(hipMemcpyAsync(y.data(), b.y, y.size() * sizeof(double), hipMemcpyDeviceToHost, b.stream),
-          "layout download") ||
+  // The grid covers the reference and the queries' start; its geometry is
+  // set on the host from both.
+  std::vector<double> y0(2 * static_cast<std::size_t>(n_query));
+  if (!ok(hipMemcpyAsync(y0.data(), b.y, y0.size() * sizeof(double), hipMemcpyDeviceToHost, b.stream),
+          "initial layout download") ||
       !ok(hipStreamSynchronize(b.stream), "transform sync")) {
     return 1;
   }
-  for (int i = 0; i < n_query; ++i) {
-    out[i] = y[2 * static_cast<std::size_t>(i)];
-    out[static_cast<std::size_t>(n_query) + i] = y[2 * static_cast<std::size_t>(i) + 1];
+  const std::vector<double> ref = rows_of(reference_layout, n_reference);
+  const GridGeo g = grid_geometry(ref.data(), n_reference, y0.data(), n_query, min_num_intervals, ints_in_interval);
+  unsigned long long exact_evals = 0;
+  if (!b.init_field(g.m) || !ok(launch_grid_fields(b.ref, n_reference, g, b.field, b.stream), "grid fields launch") ||
+      !ok(hipMemsetAsync(b.counter, 0, sizeof(unsigned long long), b.stream), "counter clear") ||
+      !ok(launch_run(kGrid, b.ref, n_reference, b.idx, b.p, n_query, k, offset, make_schedule(ra, seed), b.field, g,
+                     b.y, b.counter, b.stream),
+          "transform run launch") ||
+      !ok(hipMemcpyAsync(&exact_evals, b.counter, sizeof(exact_evals), hipMemcpyDeviceToHost, b.stream),
+          "counter download") ||
+      !download_layout(b, n_query, out)) {
+    return 1;
   }
-  if (repulsion_exact != nullptr) *repulsion_exact = exact ? 1 : 0;
+  if (stats != nullptr) {
+    stats[0] = g.nb;
+    stats[1] = g.m;
+    stats[2] = static_cast<long long>(exact_evals);
+  }
   return 0;
 }
 
@@ -586,17 +897,69 @@ int fastembedr_hip_transform_probe(const double* reference_layout, int n_referen
         p_out[static_cast<std::size_t>(i) * k + j] = host[static_cast<std::size_t>(j) * n_query + i];
   }
   if (grad_out != nullptr && y != nullptr) {  // y, grad_out: n_query x 2 row-major
-    StepParams sp{exaggeration, 0.0, 0.0, 0.0, 0.0, exact ? n_reference : n_negatives, iter_seed};
+    const StepParams sp{exaggeration, 0.0, 0.0, 0.0, 0.0, exact ? n_reference : n_negatives, iter_seed};
+    const GridGeo none{};
     if (!ok(hipMemcpyAsync(b.y, y, 2 * static_cast<std::size_t>(n_query) * sizeof(double), hipMemcpyHostToDevice,
                            b.stream),
             "state upload") ||
-        !ok(launch_step<true>(exact, b, n_reference, n_query, k, offset, sp), "transform gradient launch") ||
+        !ok(launch_gradient(exact ? kExact : kSampled, b, n_reference, n_query, k, offset, sp, none),
+            "transform gradient launch") ||
         !ok(hipMemcpyAsync(grad_out, b.grad, 2 * static_cast<std::size_t>(n_query) * sizeof(double),
                            hipMemcpyDeviceToHost, b.stream),
             "gradient download") ||
         !ok(hipStreamSynchronize(b.stream), "transform sync")) {
       return 1;
     }
+  }
+  return 0;
+}
+
+int fastembedr_hip_transform_grid_probe(const double* reference_layout, int n_reference, const int* indices,
+                                        const double* distances, int n_query, int k, double perplexity,
+                                        const double* y, const double* geometry_y, int n_geometry,
+                                        double exaggeration, int n_interpolation_points, int min_num_intervals,
+                                        double ints_in_interval, double* grad_out, long long* stats) {
+  using namespace fehip;
+  clear_last_error();
+  if (n_reference < 1 || n_query < 1 || k < 1 || reference_layout == nullptr || indices == nullptr ||
+      distances == nullptr || y == nullptr || grad_out == nullptr || (geometry_y == nullptr && n_geometry != 0) ||
+      n_geometry < 0) {
+    set_last_error("invalid transform probe arguments.");
+    return 1;
+  }
+  if (!check_grid_settings(n_interpolation_points, min_num_intervals, ints_in_interval)) return 1;
+  const int offset = reference_offset(indices, static_cast<std::size_t>(n_query) * k, n_reference);
+  if (!check_inputs(reference_layout, n_reference, indices, distances, n_query, k, perplexity, offset)) return 1;
+  TransformBuffers b;
+  if (!b.init(n_reference, n_query, k) ||
+      !upload(b, reference_layout, n_reference, indices, distances, n_query, k)) {
+    return 1;
+  }
+  const std::vector<double> ref = rows_of(reference_layout, n_reference);
+  const GridGeo g = grid_geometry(ref.data(), n_reference, geometry_y != nullptr ? geometry_y : y,
+                                  geometry_y != nullptr ? n_geometry : n_query, min_num_intervals, ints_in_interval);
+  const StepParams sp{exaggeration, 0.0, 0.0, 0.0, 0.0, n_reference, 0};
+  unsigned long long exact_evals = 0;
+  k_transform_p<<<query_blocks(n_query), kQueryThreads, 0, b.stream>>>(b.dist, n_query, k, perplexity, b.p);
+  if (!ok(hipGetLastError(), "transform P launch") || !b.init_field(g.m) ||
+      !ok(launch_grid_fields(b.ref, n_reference, g, b.field, b.stream), "grid fields launch") ||
+      !ok(hipMemsetAsync(b.counter, 0, sizeof(unsigned long long), b.stream), "counter clear") ||
+      !ok(hipMemcpyAsync(b.y, y, 2 * static_cast<std::size_t>(n_query) * sizeof(double), hipMemcpyHostToDevice,
+                         b.stream),
+          "state upload") ||
+      !ok(launch_gradient(kGrid, b, n_reference, n_query, k, offset, sp, g), "transform gradient launch") ||
+      !ok(hipMemcpyAsync(grad_out, b.grad, 2 * static_cast<std::size_t>(n_query) * sizeof(double),
+                         hipMemcpyDeviceToHost, b.stream),
+          "gradient download") ||
+      !ok(hipMemcpyAsync(&exact_evals, b.counter, sizeof(exact_evals), hipMemcpyDeviceToHost, b.stream),
+          "counter download") ||
+      !ok(hipStreamSynchronize(b.stream), "transform sync")) {
+    return 1;
+  }
+  if (stats != nullptr) {
+    stats[0] = g.nb;
+    stats[1] = g.m;
+    stats[2] = static_cast<long long>(exact_evals);
   }
   return 0;
 }
@@ -609,10 +972,11 @@ int fastembedr_hip_transform_probe(const double* reference_layout, int n_referen
 // The same kernels and operation order as fastembedr_hip_transform_tsne, with
 // the caller's arrays in device memory and the per-call work buffers in one
 // static device array instead of a hipMalloc:
-//   [0, 256)            NaHeader: validation flags and the index range
+//   [0, 256)            NaHeader: validation flags, the index range and the
+//                       run's exact-evaluation counter
 //   reference           n_reference double2 (the layout, interleaved)
 //   p                   n_query * k fp64 conditional probabilities
-//   y, update, gains    n_query double2 each
+//   y                   n_query double2 (update and gains live in registers)
 // Each GPU holds its own copy of the array for the life of the process; its
 // device address is looked up once per device (hipGetSymbolAddress) and only
 // that address is handed to kernels.  Every call on one GPU uses the same
@@ -627,8 +991,7 @@ constexpr long long kNaMaxEntries = 1LL << 22;
 constexpr std::size_t kNaReferenceOffset = 256;
 constexpr std::size_t kNaPOffset = kNaReferenceOffset + sizeof(double2) * kNaMaxReference;
 constexpr std::size_t kNaStateOffset = kNaPOffset + sizeof(double) * static_cast<std::size_t>(kNaMaxEntries);
-constexpr std::size_t kNaStateStride = sizeof(double2) * kNaMaxQuery;
-constexpr std::size_t kNaScratchBytes = kNaStateOffset + 3 * kNaStateStride;
+constexpr std::size_t kNaScratchBytes = kNaStateOffset + sizeof(double2) * kNaMaxQuery;
 constexpr int kNaMaxDevices = 64;
 
 struct NaHeader {
@@ -636,6 +999,7 @@ struct NaHeader {
   int idx_min;
   int idx_max;
   int pad;
+  unsigned long long exact_evals;  // the run kernel's counter (unused by the sampled and exact modes)
 };
 static_assert(sizeof(NaHeader) <= kNaReferenceOffset, "the header fits its slot");
 constexpr unsigned int kNaBadDistance = 1u;
@@ -654,6 +1018,7 @@ __global__ void k_na_clear(NaHeader* h) {
     h->flags = 0u;
     h->idx_min = INT_MAX;
     h->idx_max = INT_MIN;
+    h->exact_evals = 0ull;
   }
 }
 
@@ -783,8 +1148,6 @@ int fastembedr_hip_transform_tsne_noalloc(const double* reference_layout, int n_
   double2* ref = reinterpret_cast<double2*>(base + kNaReferenceOffset);
   double* p = reinterpret_cast<double*>(base + kNaPOffset);
   double2* y = reinterpret_cast<double2*>(base + kNaStateOffset);
-  double2* upd = reinterpret_cast<double2*>(base + kNaStateOffset + kNaStateStride);
-  double2* gains = reinterpret_cast<double2*>(base + kNaStateOffset + 2 * kNaStateStride);
   hipStream_t st = nullptr;  // the null stream: no stream is created
 
   const int check_blocks = static_cast<int>(std::min<long long>((entries + 255) / 256, 2048));
@@ -822,22 +1185,12 @@ int fastembedr_hip_transform_tsne_noalloc(const double* reference_layout, int n_
     k_transform_init<<<blocks, kQueryThreads, 0, st>>>(ref, indices, distances, n_query, k, offset,
                                                       initialization == 1 ? 1 : 0, y);
   }
-  k_transform_reset<<<blocks, kQueryThreads, 0, st>>>(upd, gains, n_query);
   if (!ok(hipGetLastError(), "transform setup launch")) return 1;
-  const int total = early_exaggeration_iter + n_iter;
-  for (int it = 0; it < total; ++it) {
-    const bool early = it < early_exaggeration_iter;
-    const StepParams sp{early ? early_exaggeration : exaggeration, early ? initial_momentum : final_momentum,
-                        learning_rate, ra.max_grad, ra.max_step, ra.exact ? n_reference : ra.n_negatives,
-                        iteration_seed(seed, it)};
-    if (ra.exact) {
-      k_transform_step<true, false><<<blocks, kQueryThreads, 0, st>>>(ref, n_reference, indices, p, n_query, k,
-                                                                      offset, sp, y, upd, gains, nullptr);
-    } else {
-      k_transform_step<false, false><<<blocks, kQueryThreads, 0, st>>>(ref, n_reference, indices, p, n_query, k,
-                                                                       offset, sp, y, upd, gains, nullptr);
-    }
-    if (!ok(hipGetLastError(), "transform step launch")) return 1;
+  const GridGeo none{};
+  if (!ok(launch_run(ra.exact ? kExact : kSampled, ref, n_reference, indices, p, n_query, k, offset,
+                     make_schedule(ra, seed), nullptr, none, y, &hdr->exact_evals, st),
+          "transform run launch")) {
+    return 1;
   }
   k_na_store_layout<<<(n_query + 255) / 256, 256, 0, st>>>(y, n_query, out);
   if (!ok(hipGetLastError(), "transform store launch") || !ok(hipStreamSynchronize(st), "transform sync")) return 1;

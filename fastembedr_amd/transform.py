@@ -64,8 +64,16 @@ def transform_tsne(reference_layout, knn=None, reference_data=None, new_data=Non
                    exaggeration: float = 1.5, initial_momentum: float = 0.8, final_momentum: float = 0.8,
                    max_grad_norm: float = 0.25, max_step_norm: float = math.inf, n_negatives: int | None = None,
                    exact_repulsion_threshold: int = 4096, seed: int | None = 4,
-                   backend: str = "hip") -> TransformResult:
-    """Places new points against a fixed two-dimensional reference layout."""
+                   backend: str = "hip", reference_grid: dict | None = None) -> TransformResult:
+    """Places new points against a fixed two-dimensional reference layout.
+
+    ``reference_grid`` (an extension with no R counterpart) replaces the
+    reference's exact / sampled repulsion by the reference's repulsion fields
+    precomputed once on an interpolation grid and interpolated at each query
+    (fastembedr_hip_transform_tsne_grid); a dict of ``n_interpolation_points``
+    (3), ``min_num_intervals`` (50) and ``ints_in_interval`` (0.5: two boxes
+    per unit of span), any of which may be omitted.  ``n_negatives`` and
+    ``exact_repulsion_threshold`` do not apply then."""
     if str(backend).lower() != "hip":
         raise ValueError(f'backend "{backend}" is not part of this build; only backend = "hip" is provided. '
                          "No CPU fallback is used for HIP-labelled runs.")
@@ -108,6 +116,11 @@ def transform_tsne(reference_layout, knn=None, reference_data=None, new_data=Non
     out = np.empty((n_query, 2), np.float64, order="F")
     exact = C.c_int(0)
     lib = _lib.load()
+    if reference_grid is not None:
+        return _transform_grid(lib, ref_cm, idx, dist, init, initialization, perplexity, n_iter,
+                               early_exaggeration_iter, learning_rate, early_exaggeration, exaggeration,
+                               initial_momentum, final_momentum, max_grad_norm, max_step_norm, seed, seed_i,
+                               reference_grid, out)
     rc = lib.fastembedr_hip_transform_tsne(
         ref_cm.ctypes.data_as(C.c_void_p), n_ref, idx.ctypes.data_as(C.c_void_p), dist.ctypes.data_as(C.c_void_p),
         n_query, kk, None if init is None else init.ctypes.data_as(C.c_void_p), INITIALIZATIONS[initialization],
@@ -126,6 +139,42 @@ def transform_tsne(reference_layout, knn=None, reference_data=None, new_data=Non
         exact_repulsion_threshold=exact_repulsion_threshold, initialization=initialization,
         optimizer="opentsne_style_fixed_reference_transform",
         repulsion="exact_reference" if exact.value else "sampled_reference",
+        affinities="precomputed_query_conditional", affinity_storage="flat_row_major_double",
+        transform_batch_size=n_query, transform_batches=1, seed=seed,
+        transform="opentsne_style_fixed_reference")
+    return TransformResult(np.ascontiguousarray(out), config)
+
+
+GRID_DEFAULTS = {"n_interpolation_points": 3, "min_num_intervals": 50, "ints_in_interval": 0.5}
+
+
+def _transform_grid(lib, ref_cm, idx, dist, init, initialization, perplexity, n_iter, early_exaggeration_iter,
+                    learning_rate, early_exaggeration, exaggeration, initial_momentum, final_momentum,
+                    max_grad_norm, max_step_norm, seed, seed_i, settings, out) -> TransformResult:
+    unknown = set(settings) - set(GRID_DEFAULTS)
+    if unknown:
+        raise ValueError(f"unknown reference_grid settings: {sorted(unknown)}")
+    grid = {**GRID_DEFAULTS, **settings}
+    n_ref = ref_cm.shape[0]
+    n_query, kk = idx.shape
+    stats = (C.c_longlong * 3)()
+    rc = lib.fastembedr_hip_transform_tsne_grid(
+        ref_cm.ctypes.data_as(C.c_void_p), n_ref, idx.ctypes.data_as(C.c_void_p), dist.ctypes.data_as(C.c_void_p),
+        n_query, kk, None if init is None else init.ctypes.data_as(C.c_void_p), INITIALIZATIONS[initialization],
+        perplexity, n_iter, early_exaggeration_iter, float(learning_rate), float(early_exaggeration),
+        float(exaggeration), float(initial_momentum), float(final_momentum), float(max_grad_norm),
+        float(max_step_norm), seed_i, int(grid["n_interpolation_points"]), int(grid["min_num_intervals"]),
+        float(grid["ints_in_interval"]), out.ctypes.data_as(C.c_void_p), stats)
+    _lib.check(rc, "HIP t-SNE transform (reference grid)")
+    config = dict(
+        method="transform_tsne", backend="hip", n_reference=n_ref, n_query=n_query, k=kk, perplexity=perplexity,
+        n_iter=n_iter, early_exaggeration_iter=early_exaggeration_iter, learning_rate=float(learning_rate),
+        early_exaggeration=float(early_exaggeration), exaggeration=float(exaggeration),
+        initial_momentum=float(initial_momentum), final_momentum=float(final_momentum),
+        max_grad_norm=float(max_grad_norm), max_step_norm=float(max_step_norm), initialization=initialization,
+        optimizer="opentsne_style_fixed_reference_transform", repulsion="reference_grid_interpolation",
+        reference_grid=dict(grid, boxes_per_axis=int(stats[0]), nodes_per_axis=int(stats[1]),
+                            exact_evaluations=int(stats[2])),
         affinities="precomputed_query_conditional", affinity_storage="flat_row_major_double",
         transform_batch_size=n_query, transform_batches=1, seed=seed,
         transform="opentsne_style_fixed_reference")

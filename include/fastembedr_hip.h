@@ -263,6 +263,46 @@ FASTEMBEDR_HIP_API int fastembedr_hip_transform_probe(
     int n_negatives, int exact_repulsion_threshold, int iter_seed,
     int initialization, double* p_out, double* grad_out, double* init_out);
 
+/* Fixed-reference transform with the reference's repulsion precomputed on an
+ * interpolation grid (the benchmark's config 3: the reference's grid charges
+ * are precomputed once and only the query points move).  No counterpart in
+ * the reference, whose transform repulsion is exact or sampled
+ * (src/tsne_neighbors.cpp:1472-1568).  The reference's repulsion fields
+ * Z(y) = sum_j q(y - r_j) and F(y) = sum_j q(y - r_j)^2 (y - r_j),
+ * q(d) = 1 / (1 + |d|^2), are summed directly at the nodes of a grid over the
+ * reference and the queries' start (one square, widened by max(1, 5 % of the
+ * span) on each side; max(min_num_intervals, ceil(span / ints_in_interval))
+ * boxes per axis, n_interpolation_points = 3 nodes per box and axis, at most
+ * 2048 nodes per axis), once per call; each query's repulsion is -F / Z with
+ * both interpolated (order-3 Lagrange) from its box's 3 x 3 nodes, or the
+ * exact sums over every reference point when the query is outside the grid.
+ * Attraction, clips, gains and momentum are those of
+ * fastembedr_hip_transform_tsne, whose other arguments these are (seed only
+ * seeds the random initialisation).  stats (may be NULL, 3 values): boxes per
+ * axis, nodes per axis, query-iterations that took the exact sums.  The
+ * node sums cost nodes^2 x n_reference kernel evaluations. */
+FASTEMBEDR_HIP_API int fastembedr_hip_transform_tsne_grid(
+    const double* reference_layout, int n_reference,
+    const int* indices, const double* distances, int n_query, int k,
+    const double* y_init, int initialization, double perplexity,
+    int n_iter, int early_exaggeration_iter, double learning_rate,
+    double early_exaggeration, double exaggeration,
+    double initial_momentum, double final_momentum,
+    double max_grad_norm, double max_step_norm, int seed,
+    int n_interpolation_points, int min_num_intervals, double ints_in_interval,
+    double* out, long long* stats);
+
+/* Parity probe of the grid transform, no counterpart in the reference: one
+ * gradient (grad_out, n_query x 2 row-major) at y (row-major), with the grid
+ * built around the reference and geometry_y (n_geometry x 2 row-major; NULL
+ * with n_geometry 0: y itself).  stats as above. */
+FASTEMBEDR_HIP_API int fastembedr_hip_transform_grid_probe(
+    const double* reference_layout, int n_reference,
+    const int* indices, const double* distances, int n_query, int k, double perplexity,
+    const double* y, const double* geometry_y, int n_geometry, double exaggeration,
+    int n_interpolation_points, int min_num_intervals, double ints_in_interval,
+    double* grad_out, long long* stats);
+
 /* Allocation-free variant of fastembedr_hip_transform_tsne.  No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops that place batches of new points
@@ -274,8 +314,8 @@ FASTEMBEDR_HIP_API int fastembedr_hip_transform_probe(
  *   - initialization 2 (random, drawn on the host) needs y_init;
  *   - n_reference <= 262144, n_query <= 131072 and n_query * k <= 4194304;
  *     larger inputs are refused with a message.
- * The work buffers (conditional P, layout, update, gains, the reference in
- * the kernels' layout) live in one static device array of 44 MB per GPU,
+ * The work buffers (conditional P, layout, the reference in the kernels'
+ * layout, flags) live in one static device array of 40 MB per GPU,
  * held until the process ends; the call makes no hipMalloc/hipFree and
  * creates no stream.  It runs on the null stream and returns when done.
  * Every call on a GPU shares that GPU's array: calls that overlap on one GPU

@@ -60,6 +60,9 @@ def load() -> C.CDLL:
         "transform_oracle_gradient": (None, [P, I, P, P, I, I, P, D, I, I, I, I, P]),
         "transform_oracle_update": (None, [P, P, P, P, I, D, D, D, D]),
         "transform_oracle_run": (I, [P, I, P, P, I, I, P, I, D, I, I, D, D, D, D, D, D, D, I, I, I, I, P]),
+        "transform_oracle_grid_fields": (I, [P, I, P, I, I, D, I, P, P]),
+        "transform_oracle_grid_gradient": (C.c_longlong, [P, I, P, P, I, I, P, P, I, D, I, D, I, P]),
+        "transform_oracle_grid_run": (I, [P, I, P, P, I, I, P, I, D, I, I, D, D, D, D, D, D, D, I, I, D, I, P, P]),
         "transform_oracle_iteration_seed": (I, [I, I]),
         "transform_oracle_hash32": (C.c_uint, [C.c_uint]),
         "transform_oracle_xorshift": (None, [C.c_uint, I, P]),
@@ -300,6 +303,76 @@ def transform_run(reference, indices, distances, y_init=None, initialization: in
     if rc < 0:
         raise ValueError(load().transform_oracle_last_error().decode())
     return np.ascontiguousarray(out), bool(rc)
+
+
+def transform_grid_fields(reference, y, min_intervals: int = 50, ints_in_interval: float = 1.0,
+                          threads: int = 1, fields: bool = True):
+    """Reference-grid geometry around the reference and the query layout y
+    (nq, 2): ({"lo", "box_w", "boxes", "nodes"}, node fields (nodes, nodes,
+    3) = (Z, Fx, Fy) or None)."""
+    ref = _f64_cm(reference)
+    yy = np.ascontiguousarray(y, np.float64).reshape(-1, 2)
+    geo = np.zeros(4, np.float64)
+    m_guess = None
+    rc = load().transform_oracle_grid_fields(_p(ref), ref.shape[0], _p(yy), yy.shape[0], int(min_intervals),
+                                             float(ints_in_interval), int(threads), _p(geo), None)
+    if rc < 0:
+        raise ValueError(load().transform_oracle_last_error().decode())
+    m_guess = int(geo[3])
+    f = None
+    if fields:
+        f = np.empty((m_guess, m_guess, 3), np.float64)
+        load().transform_oracle_grid_fields(_p(ref), ref.shape[0], _p(yy), yy.shape[0], int(min_intervals),
+                                            float(ints_in_interval), int(threads), _p(geo), _p(f))
+    return {"lo": float(geo[0]), "box_w": float(geo[1]), "boxes": int(geo[2]), "nodes": int(geo[3])}, f
+
+
+def transform_grid_gradient(reference, indices, p, y, exaggeration: float, min_intervals: int = 50,
+                            ints_in_interval: float = 1.0, threads: int = 1, geometry_y=None):
+    """Gradient at y with the reference-grid repulsion, the grid built around
+    the reference and geometry_y (default: y): (grad (nq, 2), queries that
+    took the exact sums)."""
+    ref = _f64_cm(reference)
+    idx = np.asfortranarray(indices, dtype=np.int32)
+    pp = np.ascontiguousarray(p, np.float64)
+    yy = np.ascontiguousarray(y, np.float64)
+    gy = yy if geometry_y is None else np.ascontiguousarray(geometry_y, np.float64).reshape(-1, 2)
+    nq, k = idx.shape
+    g = np.empty((nq, 2), np.float64)
+    out = load().transform_oracle_grid_gradient(_p(ref), ref.shape[0], _p(idx), _p(pp), nq, k, _p(yy), _p(gy),
+                                                gy.shape[0], float(exaggeration), int(min_intervals),
+                                                float(ints_in_interval), int(threads), _p(g))
+    if out < 0:
+        raise ValueError(load().transform_oracle_last_error().decode())
+    return g, int(out)
+
+
+def transform_grid_run(reference, indices, distances, y_init=None, initialization: int = INIT_MEDIAN,
+                       perplexity: float = 5.0, n_iter: int = 250, early_exaggeration_iter: int = 0,
+                       learning_rate: float = 0.1, early_exaggeration: float = 4.0, exaggeration: float = 1.5,
+                       initial_momentum: float = 0.8, final_momentum: float = 0.8, max_grad_norm: float = 0.25,
+                       max_step_norm: float = float("inf"), seed: int = 4, min_intervals: int = 50,
+                       ints_in_interval: float = 1.0, threads: int = 1):
+    """Whole transform with the reference-grid repulsion: (layout (nq, 2),
+    {"boxes", "nodes", "exact_evaluations"})."""
+    ref = _f64_cm(reference)
+    idx = np.asfortranarray(indices, dtype=np.int32)
+    d = _f64_cm(distances)
+    nq, k = idx.shape
+    init = None if y_init is None else _f64_cm(y_init)
+    out = np.empty((nq, 2), np.float64, order="F")
+    stats = np.zeros(3, np.int64)
+    rc = load().transform_oracle_grid_run(_p(ref), ref.shape[0], _p(idx), _p(d), nq, k, _p(init),
+                                          int(initialization), float(perplexity), int(n_iter),
+                                          int(early_exaggeration_iter), float(learning_rate),
+                                          float(early_exaggeration), float(exaggeration), float(initial_momentum),
+                                          float(final_momentum), float(max_grad_norm), float(max_step_norm),
+                                          int(seed), int(min_intervals), float(ints_in_interval), int(threads),
+                                          _p(out), _p(stats))
+    if rc < 0:
+        raise ValueError(load().transform_oracle_last_error().decode())
+    return np.ascontiguousarray(out), {"boxes": int(stats[0]), "nodes": int(stats[1]),
+                                       "exact_evaluations": int(stats[2])}
 
 
 def transform_iteration_seed(seed: int, it: int) -> int:

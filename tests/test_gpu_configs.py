@@ -167,6 +167,22 @@ def test_config3_transform_full_size(hip, oracle_mod, config1):
     dev = np.abs(y - y_ref).max()
     _say(f"  max |dy| = {dev:.3e} (scale {scale:.2f}); bit-identical rows {np.mean(np.all(y == y_ref, axis=1)):.4f}")
     assert dev <= 1e-9 * scale
+    # the configuration's own design: the reference grid precomputed once,
+    # the whole 250-iteration schedule
+    kw["n_iter"] = 250
+    _say("  reference-grid mode, 250 iterations")
+    res = hip.transform_tsne(ref64, knn={"indices": idx, "distances": dist}, reference_grid={}, **kw)
+    y_ref, st = oracle_mod.transform_grid_run(ref64, idx, dist, min_intervals=50, ints_in_interval=0.5,
+                                              threads=THREADS, **kw)
+    cfg = res.config["reference_grid"]
+    y = np.asarray(res.layout)
+    dev = np.abs(y - y_ref).max()
+    scale = np.abs(y_ref).max()
+    _say(f"  grid {cfg['boxes_per_axis']} boxes, {cfg['nodes_per_axis']} nodes, {cfg['exact_evaluations']} exact "
+         f"evaluations; max |dy| = {dev:.3e} (scale {scale:.2f})")
+    assert (cfg["boxes_per_axis"], cfg["nodes_per_axis"], cfg["exact_evaluations"]) == \
+        (st["boxes"], st["nodes"], st["exact_evaluations"])
+    assert dev <= 1e-9 * scale
 
 
 # ---------------------------------------------------------------------------

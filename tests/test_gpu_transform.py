@@ -151,3 +151,74 @@ def test_transform_input_errors(hip, qp):
         _run(ref, idx, dneg, n_iter=1)
     with pytest.raises(ValueError, match="two-dimensional"):
         _run(np.zeros((10, 3)), idx, dist, n_iter=1)
+
+
+# ---------------------------------------------------------------------------
+# Reference-grid repulsion (fastembedr_hip_transform_tsne_grid), against the
+# oracle's fp64 restatement of the same algorithm (itself pinned against the
+# exact mode and brute-force node sums in tests/test_transform_oracle.py).
+# ---------------------------------------------------------------------------
+def _grid_probe(ref, idx, dist, y, geometry_y=None, ex=1.0, min_int=50, ints=0.5):
+    lib = _lib.load()
+    nq, k = idx.shape
+    ref_cm = np.asfortranarray(ref, np.float64)
+    idx_cm = np.asfortranarray(idx, np.int32)
+    dist_cm = np.asfortranarray(dist, np.float64)
+    yy = np.ascontiguousarray(y, np.float64)
+    gy = None if geometry_y is None else np.ascontiguousarray(geometry_y, np.float64)
+    g = np.empty((nq, 2), np.float64)
+    stats = (C.c_longlong * 3)()
+    rc = lib.fastembedr_hip_transform_grid_probe(
+        ref_cm.ctypes.data_as(C.c_void_p), ref.shape[0], idx_cm.ctypes.data_as(C.c_void_p),
+        dist_cm.ctypes.data_as(C.c_void_p), nq, k, 5.0, yy.ctypes.data_as(C.c_void_p),
+        None if gy is None else gy.ctypes.data_as(C.c_void_p), 0 if gy is None else gy.shape[0], float(ex), 3,
+        int(min_int), float(ints), g.ctypes.data_as(C.c_void_p), stats)
+    _lib.check(rc, "transform grid probe")
+    return g, [int(v) for v in stats]
+
+
+def test_transform_grid_gradient_matches_oracle(hip, oracle_mod, qp):
+    _say("case: reference-grid transform gradient, n_ref=3000 nq=1200 k=30")
+    ref, idx, dist = qp
+    y = oracle_mod.transform_init(ref, idx, dist, oracle_mod.INIT_MEDIAN)
+    y = y + np.random.default_rng(2).normal(0, 0.3, size=y.shape)
+    p_ref = oracle_mod.transform_conditional_p(dist, 5.0)
+    g, st = _grid_probe(ref, idx, dist, y, ex=1.5)
+    g_ref, outside = oracle_mod.transform_grid_gradient(ref, idx, p_ref, y, 1.5, min_intervals=50,
+                                                        ints_in_interval=0.5)
+    geo, _ = oracle_mod.transform_grid_fields(ref, y, 50, 0.5, fields=False)
+    r = _rel(g, g_ref)
+    _say(f"  grid {st[0]} boxes / {st[1]} nodes; relative error {r:.3e}, bit-identical {np.mean(g == g_ref):.4f}")
+    assert (st[0], st[1], st[2]) == (geo["boxes"], geo["nodes"], outside) == (geo["boxes"], geo["nodes"], 0)
+    assert r <= TIGHT
+    # queries outside the grid take the exact sums
+    far = y + np.array([500.0, -300.0])
+    g_far, st_far = _grid_probe(ref, idx, dist, far, geometry_y=y, ex=1.5)
+    g_far_ref, outside_far = oracle_mod.transform_grid_gradient(ref, idx, p_ref, far, 1.5, min_intervals=50,
+                                                                ints_in_interval=0.5, geometry_y=y)
+    assert st_far[2] == outside_far == far.shape[0]
+    assert _rel(g_far, g_far_ref) <= TIGHT
+
+
+@pytest.mark.parametrize("case", ["median", "weighted_early"])
+def test_transform_grid_run_matches_oracle(hip, oracle_mod, qp, case):
+    ref, idx, dist = qp
+    kw = dict(perplexity=5.0, n_iter=60, learning_rate=0.1, exaggeration=1.0, seed=17)
+    okw = dict(kw)
+    if case == "weighted_early":
+        kw.update(initialization="weighted", early_exaggeration_iter=10, early_exaggeration=4.0, initial_momentum=0.5)
+        okw.update(initialization=oracle_mod.INIT_WEIGHTED, early_exaggeration_iter=10, early_exaggeration=4.0,
+                   initial_momentum=0.5)
+    _say(f"case: reference-grid transform run ({case})")
+    res = hip.transform_tsne(ref, knn={"indices": idx, "distances": dist}, reference_grid={}, **kw)
+    y_ref, st = oracle_mod.transform_grid_run(ref, idx, dist, min_intervals=50, ints_in_interval=0.5, threads=8,
+                                              **okw)
+    cfg = res.config["reference_grid"]
+    assert res.config["repulsion"] == "reference_grid_interpolation"
+    assert (cfg["boxes_per_axis"], cfg["nodes_per_axis"], cfg["exact_evaluations"]) == \
+        (st["boxes"], st["nodes"], st["exact_evaluations"])
+    y = np.asarray(res.layout)
+    scale = np.abs(y_ref).max()
+    dev = np.abs(y - y_ref).max()
+    _say(f"  max |dy| = {dev:.3e} (scale {scale:.2f}); bit-identical rows {np.mean(np.all(y == y_ref, axis=1)):.4f}")
+    assert dev <= 1e-9 * scale

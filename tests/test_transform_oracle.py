@@ -177,3 +177,82 @@ def test_run_rejects_bad_input():
     dneg[1, 1] = -1.0
     with pytest.raises(ValueError, match="finite and non-negative"):
         oracle.transform_run(ref, idx, dneg, n_iter=1)
+
+
+# ---------------------------------------------------------------------------
+# Reference-grid repulsion (config 3's precomputed reference grid)
+# ---------------------------------------------------------------------------
+def _grid_problem(n_ref=600, nq=150, k=12, seed=3):
+    rng = np.random.default_rng(seed)
+    centers = rng.normal(0, 6, size=(5, 2))
+    lab = rng.integers(0, 5, size=n_ref)
+    ref = centers[lab] + rng.normal(0, 1.0, size=(n_ref, 2))
+    yq = ref[rng.integers(0, n_ref, size=nq)] + rng.normal(0, 0.5, size=(nq, 2))
+    d2 = ((yq[:, None, :] - ref[None, :, :]) ** 2).sum(-1)
+    idx = np.argsort(d2, axis=1)[:, :k]
+    dist = np.sqrt(np.take_along_axis(d2, idx, axis=1))
+    return ref, (idx + 1).astype(np.int32), dist, yq
+
+
+def test_grid_node_fields_are_the_direct_sums(oracle_mod):
+    """Z = sum_j q, F = sum_j q^2 (node - r_j) at every node, q = 1/(1+d^2),
+    nodes at lo + (a + 1/2) h."""
+    ref, idx, dist, yq = _grid_problem(n_ref=300, nq=40)
+    geo, f = oracle_mod.transform_grid_fields(ref, yq, min_intervals=8, ints_in_interval=100.0)
+    m = geo["nodes"]
+    assert geo["boxes"] == 8 and m == 24
+    h = geo["box_w"] / 3.0
+    nodes = geo["lo"] + (np.arange(m) + 0.5) * h
+    nx, ny = np.meshgrid(nodes, nodes)  # ny varies along axis 0: node (a, b) at f[b, a]
+    dx = nx[..., None] - ref[:, 0]
+    dy = ny[..., None] - ref[:, 1]
+    q = 1.0 / (1.0 + dx * dx + dy * dy)
+    np.testing.assert_allclose(f[..., 0], q.sum(-1), rtol=1e-12)
+    np.testing.assert_allclose(f[..., 1], (q * q * dx).sum(-1), rtol=1e-11, atol=1e-14)
+    np.testing.assert_allclose(f[..., 2], (q * q * dy).sum(-1), rtol=1e-11, atol=1e-14)
+    # the square covers the reference and the queries with a margin
+    lo, hi = geo["lo"], geo["lo"] + geo["boxes"] * geo["box_w"]
+    allpts = np.vstack([ref, yq])
+    assert lo < allpts.min() - 0.99 and hi > allpts.max() + 0.99
+
+
+def test_grid_gradient_converges_to_the_exact_mode(oracle_mod):
+    """Order-3 interpolation: the error against the exact mode's gradient
+    falls about eightfold per halving of the box width."""
+    ref, idx, dist, yq = _grid_problem()
+    p = oracle_mod.transform_conditional_p(dist, 5.0)
+    exact = oracle_mod.transform_gradient(ref, idx, p, yq, 1.0, 10 ** 6, 10 ** 6, 0)
+    errs = []
+    for ints in (2.0, 1.0, 0.5, 0.25):
+        g, outside = oracle_mod.transform_grid_gradient(ref, idx, p, yq, 1.0, min_intervals=1, ints_in_interval=ints)
+        assert outside == 0
+        errs.append(float(np.linalg.norm(g - exact) / np.linalg.norm(exact)))
+    assert all(b < a / 4.0 for a, b in zip(errs, errs[1:])), errs
+    # two boxes per unit (the HIP grid transform's default): ~0.15 %
+    assert errs[2] < 2e-3 and errs[3] < 3e-4, errs
+    # the repulsion alone (exaggeration 0 leaves the attraction out)
+    rep_exact = oracle_mod.transform_gradient(ref, idx, p, yq, 0.0, 10 ** 6, 10 ** 6, 0)
+    rep_grid, _ = oracle_mod.transform_grid_gradient(ref, idx, p, yq, 0.0, min_intervals=1, ints_in_interval=0.25)
+    assert np.linalg.norm(rep_grid - rep_exact) / np.linalg.norm(rep_exact) < 3e-4
+
+
+def test_grid_queries_outside_take_the_exact_sums(oracle_mod):
+    ref, idx, dist, yq = _grid_problem()
+    p = oracle_mod.transform_conditional_p(dist, 5.0)
+    far = yq + np.array([400.0, -350.0])
+    g, outside = oracle_mod.transform_grid_gradient(ref, idx, p, far, 1.0, geometry_y=yq)
+    assert outside == far.shape[0]
+    exact = oracle_mod.transform_gradient(ref, idx, p, far, 1.0, 10 ** 6, 10 ** 6, 0)
+    np.testing.assert_array_equal(g, exact)
+
+
+def test_grid_run_approaches_the_exact_run(oracle_mod):
+    ref, idx, dist, yq = _grid_problem()
+    kw = dict(perplexity=5.0, n_iter=40, learning_rate=0.1, exaggeration=1.0, seed=4)
+    y_exact, exact = oracle_mod.transform_run(ref, idx, dist, n_negatives=10 ** 6, exact_threshold=10 ** 6, **kw)
+    assert exact
+    y_grid, st = oracle_mod.transform_grid_run(ref, idx, dist, ints_in_interval=0.25, min_intervals=1, **kw)
+    assert st["exact_evaluations"] == 0 and st["nodes"] == 3 * st["boxes"]
+    scale = np.abs(y_exact).max()
+    # the gradient error (~2e-4 at this box width) carried through 40 steps
+    assert np.abs(y_grid - y_exact).max() < 1e-3 * scale
