@@ -377,54 +377,100 @@ def bench_transform(args, torch, fe, synthetic) -> int:
     out = np.empty((nq, 2), np.float64, order="F")
     params = dict(perplexity=5.0, early_iter=0, lr=0.1, early_ex=4.0, ex=1.0, m0=0.8, m1=0.8, gmax=0.25,
                   smax=float("inf"), n_neg=256, thr=4096, seed=4)
+    grid_settings = (3, 50, 0.5)  # points per box, min boxes, box width (the grid transform's defaults)
+    grid_stats = (C.c_longlong * 3)()
 
-    def call(iters: int) -> float:
-        exact = C.c_int(0)
+    def call(iters: int, mode: str) -> float:
         t0 = time.perf_counter()
-        rc = lib.fastembedr_hip_transform_tsne(
-            ref_cm.ctypes.data_as(C.c_void_p), n_ref, qi.ctypes.data_as(C.c_void_p), qd.ctypes.data_as(C.c_void_p),
-            nq, 30, None, 0, params["perplexity"], iters, params["early_iter"], params["lr"], params["early_ex"],
-            params["ex"], params["m0"], params["m1"], params["gmax"], params["smax"], params["n_neg"],
-            params["thr"], params["seed"], out.ctypes.data_as(C.c_void_p), C.byref(exact))
-        _lib.check(rc, "transform")
+        if mode == "grid":
+            rc = lib.fastembedr_hip_transform_tsne_grid(
+                ref_cm.ctypes.data_as(C.c_void_p), n_ref, qi.ctypes.data_as(C.c_void_p),
+                qd.ctypes.data_as(C.c_void_p), nq, 30, None, 0, params["perplexity"], iters, params["early_iter"],
+                params["lr"], params["early_ex"], params["ex"], params["m0"], params["m1"], params["gmax"],
+                params["smax"], params["seed"], *grid_settings, out.ctypes.data_as(C.c_void_p), grid_stats)
+        else:
+            exact = C.c_int(0)
+            rc = lib.fastembedr_hip_transform_tsne(
+                ref_cm.ctypes.data_as(C.c_void_p), n_ref, qi.ctypes.data_as(C.c_void_p),
+                qd.ctypes.data_as(C.c_void_p), nq, 30, None, 0, params["perplexity"], iters, params["early_iter"],
+                params["lr"], params["early_ex"], params["ex"], params["m0"], params["m1"], params["gmax"],
+                params["smax"], params["n_neg"], params["thr"], params["seed"], out.ctypes.data_as(C.c_void_p),
+                C.byref(exact))
+        _lib.check(rc, f"transform ({mode})")
         return time.perf_counter() - t0
 
-    call(2)  # warm-up
     iters = args.steps if args.steps != 750 else 250
-    t_all = call(iters)
-    t_one = call(1)
-    per_iter = (t_all - t_one) / max(1, iters - 1)
-    its = 1.0 / per_iter
-    log(f"transform: {iters} iterations in {t_all:.3f}s, 1 in {t_one:.3f}s -> {its:.1f} it/s "
-        f"({per_iter * 1e3:.3f} ms per iteration over {nq} queries)")
+
+    def rate(mode: str) -> tuple[float, float, float]:
+        """Per-iteration time from calls of `iters` and of 1 iteration (upload,
+        P, initialisation and, for the grid, the node fields drop out); the
+        median of 5 pairs."""
+        call(2, mode)  # warm-up
+        diffs, t_alls = [], []
+        for _ in range(5):
+            t_all = call(iters, mode)
+            t_one = call(1, mode)
+            diffs.append((t_all - t_one) / max(1, iters - 1))
+            t_alls.append(t_all)
+        per_iter = float(np.median(diffs))
+        log(f"transform ({mode}): {iters} iterations in {np.median(t_alls):.4f}s (whole call) -> "
+            f"{1.0 / per_iter:.1f} it/s ({per_iter * 1e3:.4f} ms per iteration over {nq} queries)")
+        return per_iter, float(np.median(t_alls)), 1.0 / per_iter
+
+    per_iter, t_call, its = rate("grid")
+    geo = [int(v) for v in grid_stats]
+    per_iter_s, t_call_s, its_s = rate("sampled")
+    # fp64 flops per query and iteration of the fused run kernel (grid mode):
+    # attraction 13 per neighbour (2 sub, 2 mul + 2 add, 1 div, 2 mul, 2 x
+    # (mul + add)); interpolation 88 (box location 4, weights 18, 9 nodes x 7,
+    # quotient 3); update 25.
+    flops_q = 13 * 30 + 88 + 25
+    tflops = flops_q * nq / per_iter / 1e12
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import oracle
 
-        threads = min(16, os.cpu_count() or 1)
+        threads = cpu_share()
         sample_q = min(nq, 20_000)
-        t0 = time.perf_counter()
-        oracle.transform_run(ref_layout, qi[:sample_q], qd[:sample_q], n_iter=1, perplexity=5.0, exaggeration=1.0,
-                             n_negatives=256, exact_threshold=4096, seed=4, threads=threads)
-        t1 = time.perf_counter() - t0
-        cpu_iters = 10
-        t0 = time.perf_counter()
-        oracle.transform_run(ref_layout, qi[:sample_q], qd[:sample_q], n_iter=cpu_iters + 1, perplexity=5.0,
-                             exaggeration=1.0, n_negatives=256, exact_threshold=4096, seed=4, threads=threads)
-        t_cpu = (time.perf_counter() - t0 - t1) / cpu_iters * (nq / sample_q)
-        cpu = {"value": round(1.0 / t_cpu, 3), "unit": "iterations/s", "cores": threads, "kind": "port",
-               "sample": f"{cpu_iters} iterations over {sample_q} of the {nq} queries, scaled to all queries"}
-        log(f"CPU oracle transform: {1.0 / t_cpu:.2f} it/s (scaled) on {threads} threads")
+
+        def cpu_rate(run, label):
+            t0 = time.perf_counter()
+            run(1)
+            t1 = time.perf_counter() - t0
+            cpu_iters = 10
+            t0 = time.perf_counter()
+            run(cpu_iters + 1)
+            t_cpu = (time.perf_counter() - t0 - t1) / cpu_iters * (nq / sample_q)
+            log(f"CPU oracle transform ({label}): {1.0 / t_cpu:.2f} it/s (scaled) on {threads} threads")
+            return round(1.0 / t_cpu, 3), cpu_iters
+
+        v_s, n_s = cpu_rate(lambda it: oracle.transform_run(
+            ref_layout, qi[:sample_q], qd[:sample_q], n_iter=it, perplexity=5.0, exaggeration=1.0, n_negatives=256,
+            exact_threshold=4096, seed=4, threads=threads), "sampled, the reference's algorithm")
+        cpu = {"value": v_s, "unit": "iterations/s", "cores": threads, "kind": "port",
+               "sample": f"{n_s} iterations over {sample_q} of the {nq} queries, scaled to all queries; the "
+                         f"reference's CPU transform (transform_tsne_cpp, 256 sampled negatives) restated by the "
+                         f"oracle",
+               "cpu_model": cpu_model(), "host_cpus_visible": os.cpu_count()}
     line = {
         "metric": "t-SNE transform iterations/sec (config 3: 100K queries against a fixed 70K reference)",
         "value": round(its, 3), "unit": "iterations/s", "n_gpus": 1, "steps": iters, "warmup": 2,
-        "ms_per_step": round(per_iter * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "ms_per_step": round(per_iter * 1e3, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f64", "data": "synthetic",
         "config": {"workload": f"config3: {nq} queries, reference {n_ref} (config-1 mixture embedded on the GPU), "
-                               f"k=30, perplexity 5, lr 0.1, exaggeration 1",
+                               f"k=30, perplexity 5, lr 0.1, exaggeration 1, {iters} iterations",
                    "n_reference": n_ref, "n_query": nq, "k": 30,
-                   "repulsion": "sampled: 256 reference points per query and iteration (transform_tsne_cpp's "
-                                "mode for n_reference > 4096)"},
+                   "repulsion": f"reference grid: the reference's repulsion fields summed once at {geo[1]} x "
+                                f"{geo[1]} nodes ({geo[0]} boxes per axis, 3 points per box, 2 boxes per unit) and "
+                                f"interpolated at each query; {geo[2]} query-iterations took the exact sums"},
+        "whole_call_seconds": round(t_call, 4),
+        "roofline": {"kernel": "k_transform_run<grid>", "bound": "fp64 VALU", "achieved": round(tflops, 3),
+                     "peak": 78.6, "unit": "TFLOP/s", "frac": round(tflops / 78.6, 4), "traffic": None,
+                     "algorithmic_flops_per_query_iteration": flops_q},
+        "sampled_mode": {"iterations_per_s": round(its_s, 3), "ms_per_step": round(per_iter_s * 1e3, 5),
+                         "whole_call_seconds": round(t_call_s, 4),
+                         "repulsion": "256 reference points sampled per query and iteration (transform_tsne_cpp's "
+                                      "mode for n_reference > 4096)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

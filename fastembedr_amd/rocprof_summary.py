@@ -40,15 +40,28 @@ def _one(pattern: str) -> str:
     return hits[0]
 
 
+def _stats_rows(kt_dir: str) -> list[tuple[str, int, float, float, float, float]]:
+    """(name, calls, avg, min, max, total ns) per kernel, from the CSV stats
+    file or, when rocprofv3 wrote its SQLite database, from its kernels view."""
+    csvs = sorted(glob.glob(f"{kt_dir}/**/*kernel_stats.csv", recursive=True))
+    if csvs:
+        return [(r["Name"], int(r["Calls"]), float(r["AverageNs"]), float(r["MinNs"]), float(r["MaxNs"]),
+                 float(r["TotalDurationNs"])) for r in csv.DictReader(open(csvs[0]))]
+    import sqlite3
+
+    con = sqlite3.connect(_one(f"{kt_dir}/**/*.db"))
+    q = ("select name, count(*), avg(end - start), min(end - start), max(end - start), sum(end - start) "
+         "from kernels group by name order by sum(end - start) desc")
+    return [(r[0], int(r[1]), float(r[2]), float(r[3]), float(r[4]), float(r[5])) for r in con.execute(q)]
+
+
 def trace(kt_dir: str) -> list[str]:
-    rows = list(csv.DictReader(open(_one(f"{kt_dir}/**/*kernel_stats.csv"))))
     out = [f"{'kernel':34s} {'calls':>6s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s} {'total_ms':>10s}"]
-    for r in rows:
-        if not _OURS.search(r["Name"]):
+    for name, calls, avg, mn, mx, tot in _stats_rows(kt_dir):
+        if not _OURS.search(name):
             continue
-        out.append(f"{short_name(r['Name']):34s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.2f} "
-                   f"{float(r['MinNs']) / 1e3:10.2f} {float(r['MaxNs']) / 1e3:10.2f} "
-                   f"{float(r['TotalDurationNs']) / 1e6:10.2f}")
+        out.append(f"{short_name(name):34s} {calls:6d} {avg / 1e3:10.2f} {mn / 1e3:10.2f} {mx / 1e3:10.2f} "
+                   f"{tot / 1e6:10.2f}")
     return out
 
 
