@@ -231,7 +231,10 @@ def main() -> int:
     # breakdown pass; traffic: the rocprof digest's bytes of the same kernels
     # per iteration.
     if interp:
-        g_nodes, f_len = geo_end["nodes"], geo_end["fft_len"]
+        # the shortest FFT length the grid needs (zero padding to >= 2 nodes);
+        # the run may use a longer one, chosen from a lagged bound
+        g_nodes = geo_end["nodes"]
+        f_len = 1 << max(6, (2 * g_nodes - 1).bit_length())
     else:
         g_nodes, f_len = g, 2 * g
     rep_bytes = 24.0 * n + 28.0 * g_nodes ** 2 + 288.0 * f_len ** 2

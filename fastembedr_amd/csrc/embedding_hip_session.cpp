@@ -587,7 +587,7 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
          s->timed(fehip::kKLgBinScatter, "interp bin_scatter launch",
                   [&] { return fehip::launch_interp_bin_scatter(s->y_b, s->sc, ib, n, main); }) &&
          s->timed(fehip::kKLgSpread, "interp spread launch",
-                  [&] { return fehip::launch_interp_spread(s->sc, ib, n, main); }) &&
+                  [&] { return fehip::launch_interp_spread(s->sc, ib, n, fft_len, main); }) &&
          s->timed(fehip::kKLgGather, "interp gather launch",
                   [&] { return fehip::launch_interp_gather(s->sc, ib, main); }) &&
          s->timed(fehip::kKLgChargeRows, "interp charge_rows launch",
@@ -1299,19 +1299,23 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
   // Interpolation grid: the FFT length must hold 2 * nodes, and the node
   // count is set on the device each iteration.  The host learns the box
   // count of earlier iterations through a pinned ring and bounds the current
-  // one.  With the step clip a point moves at most max_step_norm per
-  // iteration and so does the mean, so a centred coordinate moves at most
-  // 2 max_step_norm; the span runs from the smallest to the largest centred
-  // coordinate over both axes, so it grows by at most 4 max_step_norm.  It
-  // runs at most kMaxLag iterations ahead of what it knows (none without the
-  // clip).
+  // one.  With the step clip every update u_i has |u_i| <= s = max_step_norm,
+  // and so has their mean; a centred coordinate moves by u_i - mean(u).  The
+  // span runs from the smallest to the largest centred coordinate over both
+  // axes: two extremes on one axis separate by at most 2 s per iteration
+  // (the mean cancels), extremes on different axes by at most
+  // 2 s + |mean_x - mean_y| <= (2 + sqrt 2) s.  With boxes = ceil(span /
+  // ints_in_interval) >= span / ints_in_interval, a growth of at most d
+  // adds at most ceil(d / ints_in_interval) boxes.  The host runs at most
+  // kMaxLag iterations ahead of what it knows (none without the clip).
   const bool lg = s->repulsion == FASTEMBEDR_HIP_REPULSION_LAGRANGE;
   constexpr int kRing = fastembedr_hip_tsne::kLgRing;
   constexpr int kMaxLag = 3;
   static_assert(kMaxLag + 2 <= kRing, "ring slots outlive the lag");
   const int allowed_lag = up.clip ? kMaxLag : 0;
   const double growth =
-      up.clip ? 4.0 * (static_cast<double>(max_step_norm) * 1.0001 + 1e-3) / static_cast<double>(s->lg_ints_per_unit)
+      up.clip ? (2.0 + std::sqrt(2.0)) * (static_cast<double>(max_step_norm) * 1.0001 + 1e-3) /
+                    static_cast<double>(s->lg_ints_per_unit)
               : 0.0;
   int known_boxes = 0;
   int known_it = 0;
@@ -1344,7 +1348,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
         known_boxes = static_cast<volatile int*>(s->lg_ring)[slot];
       }
       const long long bound =
-          static_cast<long long>(known_boxes) + static_cast<long long>(std::ceil(growth * (it - known_it))) + 1;
+          static_cast<long long>(known_boxes) + static_cast<long long>(std::ceil(growth * (it - known_it)));
       const int nodes = static_cast<int>(std::min<long long>(bound * fehip::kLgOrder, fehip::kLgMaxNodes));
       fft_len = interp_fft_len(nodes);
     }

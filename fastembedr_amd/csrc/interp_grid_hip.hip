@@ -38,15 +38,16 @@
 //   k_lg_bin_count, k_bin_plan, k_lg_bin_scatter
 //                         points into tiles of 16 x 16 boxes and work items
 //                         of at most 2048 points of one tile
-//   k_lg_spread           per work item: points ordered by box in LDS; a lane
-//                         sums its run of one box in registers (9 nodes x 4
-//                         moments) and adds it to the item's 48 x 48 x 4 LDS
-//                         window once; the window goes straight to the charge
-//                         planes when the item is its tile's only one, else
-//                         to scratch
+//   k_lg_spread           per work item: points ordered by box in LDS; one
+//                         wave per box sums its points' 9 nodes x 4 moments
+//                         in registers and a butterfly across the wave, and
+//                         stores the box's nodes in the item's LDS window;
+//                         the window goes straight to the charge planes when
+//                         the item is its tile's only one, else to scratch
 //   k_lg_gather           sums the scratch windows of multi-item tiles in a
-//                         fixed order (no float atomics in global memory);
-//                         every node is written, so nothing is cleared
+//                         fixed order (no float atomics in global memory), a
+//                         workgroup per tile; every node is written, so
+//                         nothing is cleared
 //   k_lg_kernel_rows/cols spectra of K, K1 (real, even) and Kv (imaginary,
 //                         odd in its own axis), a quadrant each, two real
 //                         sequences per complex transform
@@ -153,10 +154,48 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_bin_scatter(const float2* __r
   }
 }
 
-// Adds one box's 9 nodes x 4 charges, summed in registers, to the window of
-// `win` x `win` nodes (box = local index in a tile of win / 3 boxes per axis).
-__device__ __forceinline__ void lg_flush(float* acc, int box, int tile, int win,
-                                         const float (&a)[4 * kLgOrder * kLgOrder]) {
+// One point's contributions to its box's 9 nodes x 4 moments, added to a.
+// Offsets from the nodes in units of h: node c of a box sits at (c + 1/2) h
+// from the box's corner, the point at 3 u h.
+__device__ __forceinline__ void lg_accumulate(const LgPoint& b, float (&a)[4 * kLgOrder * kLgOrder]) {
+#pragma clang fp contract(off)
+  float wx[kLgOrder], wy[kLgOrder];
+  lg_weights3(b.ux, wx);
+  lg_weights3(b.uy, wy);
+  const float tx3 = 3.0f * b.ux;
+  const float ty3 = 3.0f * b.uy;
+#pragma unroll
+  for (int r = 0; r < kLgOrder; ++r) {
+    const float oy = ty3 - (static_cast<float>(r) + 0.5f);
+#pragma unroll
+    for (int c = 0; c < kLgOrder; ++c) {
+      const float ox = tx3 - (static_cast<float>(c) + 0.5f);
+      const float w = wy[r] * wx[c];
+      float* d = a + (r * kLgOrder + c) * 4;
+      d[0] += w;
+      d[1] += w * ox;
+      d[2] += w * oy;
+      d[3] += w * (ox * ox + oy * oy);
+    }
+  }
+}
+
+// Sum over the 64 lanes of a wave (butterfly, the same order in every lane).
+__device__ __forceinline__ void lg_wave_sum(float (&a)[4 * kLgOrder * kLgOrder]) {
+#pragma unroll
+  for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) {
+    float t = a[e];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
+    a[e] = t;
+  }
+}
+
+// Writes one box's 9 nodes x 4 moments into the window of win x win nodes
+// (box = local index in a tile of win / 3 boxes per axis).  Every node
+// belongs to exactly one box, so plain stores suffice.
+__device__ __forceinline__ void lg_store_box(float* acc, int box, int tile, int win,
+                                             const float (&a)[4 * kLgOrder * kLgOrder]) {
   const int lbx = box % tile;
   const int lby = box / tile;
   const int wn = win * win;
@@ -166,31 +205,50 @@ __device__ __forceinline__ void lg_flush(float* acc, int box, int tile, int win,
 #pragma unroll
     for (int c = 0; c < kLgOrder; ++c) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) atomicAdd(&acc[t * wn + node0 + r * win + c], a[(r * kLgOrder + c) * 4 + t]);
+      for (int t = 0; t < 4; ++t) acc[t * wn + node0 + r * win + c] = a[(r * kLgOrder + c) * 4 + t];
     }
   }
 }
 
+// The window `acc` is dynamic LDS of acc_cap floats, sized by the host for
+// the largest tile its FFT length allows (a 48 x 48 x 4 window is 36 KB, the
+// late-phase 6 x 6 x 4 one 576 bytes), so that small tiles leave LDS for more
+// workgroups per CU.  A window that would not fit raises kErrInterpGrid.
+//
+// Per work item (<= kChunk points of one tile): the points are ordered by box
+// in LDS (counting sort), then each box is reduced by one wave: lanes take the
+// box's points with stride 64 and sum their 9 x 4 contributions in
+// registers, a butterfly adds the 64 lanes, and the box's nodes are stored.
+// A tile of one box (the early, compact layouts) splits the box's points over
+// the workgroup's waves and adds their sums in wave order.  Every order is
+// fixed, so the charges do not depend on scheduling.
+constexpr int kLgWaves = kLgThreads / 64;
+
 __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restrict__ binned,
                                                           const int4* __restrict__ items,
-                                                          const int* __restrict__ tile_item0,
-                                                          const DeviceScalars* sc, float* __restrict__ charge,
-                                                          float* __restrict__ windows) {
+                                                          const int* __restrict__ tile_item0, DeviceScalars* sc,
+                                                          float* __restrict__ charge, float* __restrict__ windows,
+                                                          int acc_cap) {
 #pragma clang fp contract(off)
-  __shared__ float acc[kLgWinVals];  // [charge][node of the window]
+  extern __shared__ float acc[];  // [charge][node of the window], acc_cap floats
   __shared__ int box_start[kLgBoxesPerTile];
   __shared__ int part[kLgThreads];
   __shared__ float2 sorted[kChunk];
+  __shared__ float wave_part[kLgWaves][4 * kLgOrder * kLgOrder];
   if (static_cast<int>(blockIdx.x) >= sc->num_items) return;
   const DeviceScalars s = *sc;
   const int4 it = items[blockIdx.x];
   const int tile = s.lg_tile;
   const int win = tile * kLgOrder;
   const int wvals = 4 * win * win;
+  if (wvals > acc_cap) {  // uniform over the grid: no workgroup touches LDS beyond acc_cap
+    if (threadIdx.x == 0) atomicOr(&sc->error_flags, kErrInterpGrid);
+    return;
+  }
   const int ta = s.lg_tiles_axis;
   const int tx = it.x % ta, ty = it.x / ta;
   const int bx0 = tx * tile, by0 = ty * tile;
-  for (int e = threadIdx.x; e < wvals; e += kLgThreads) acc[e] = 0.0f;
+  const int nbox = tile * tile;
   box_start[threadIdx.x] = 0;
   __syncthreads();
   const int count = it.z - it.y;  // <= kChunk
@@ -220,7 +278,7 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
       part[t] += add;
       __syncthreads();
     }
-    box_start[t] = part[t] - c;
+    box_start[t] = part[t] - c;  // exclusive start; part[t] is the inclusive end
   }
   __syncthreads();
 #pragma unroll
@@ -228,61 +286,44 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
     if (box[q] >= 0) sorted[box_start[box[q]] + rank[q]] = v[q];
   }
   __syncthreads();
-  // each lane: kLgRun consecutive points of the box order
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int lane = static_cast<int>(threadIdx.x) & 63;
   float a[4 * kLgOrder * kLgOrder];
+  if (nbox == 1) {
+    // one box: the waves take interleaved stretches of 64 points
 #pragma unroll
-  for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) a[e] = 0.0f;
-  int cur = -1;
-  const int p0 = static_cast<int>(threadIdx.x) * kLgRun;
+    for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) a[e] = 0.0f;
+    for (int p = wave * 64 + lane; p < count; p += kLgThreads) lg_accumulate(lg_locate(sorted[p].x, sorted[p].y, s), a);
+    lg_wave_sum(a);
+    if (lane == 0) {
 #pragma unroll
-  for (int q = 0; q < kLgRun; ++q) {
-    const int p = p0 + q;
-    if (p >= count) break;
-    const float2 u = sorted[p];
-    const LgPoint b = lg_locate(u.x, u.y, s);
-    const int lb = (b.by - by0) * tile + (b.bx - bx0);
-    if (lb != cur) {
-      if (cur >= 0) lg_flush(acc, cur, tile, win, a);
-      cur = lb;
+      for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) wave_part[wave][e] = a[e];
+    }
+    __syncthreads();
+    if (threadIdx.x < 4 * kLgOrder * kLgOrder) {
+      const int e = threadIdx.x;
+      float t = wave_part[0][e];
+#pragma unroll
+      for (int w = 1; w < kLgWaves; ++w) t += wave_part[w][e];
+      wave_part[0][e] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) a[e] = wave_part[0][e];
+      lg_store_box(acc, 0, tile, win, a);
+    }
+  } else {
+    for (int b = wave; b < nbox; b += kLgWaves) {
+      const int b0 = box_start[b];
+      const int b1 = part[b];
 #pragma unroll
       for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) a[e] = 0.0f;
+      for (int p = b0 + lane; p < b1; p += 64) lg_accumulate(lg_locate(sorted[p].x, sorted[p].y, s), a);
+      // uniform over the wave; with one point, lane 0 already holds it
+      if (b1 - b0 > 1) lg_wave_sum(a);
+      if (lane == 0) lg_store_box(acc, b, tile, win, a);  // empty boxes store zeros
     }
-    float wx[kLgOrder], wy[kLgOrder];
-    lg_weights3(b.ux, wx);
-    lg_weights3(b.uy, wy);
-    // offsets from the nodes in units of h: node c of a box sits at
-    // (c + 1/2) h from the box's corner, the point at 3 u h
-    const float tx3 = 3.0f * b.ux;
-    const float ty3 = 3.0f * b.uy;
-#pragma unroll
-    for (int r = 0; r < kLgOrder; ++r) {
-      const float oy = ty3 - (static_cast<float>(r) + 0.5f);
-#pragma unroll
-      for (int c = 0; c < kLgOrder; ++c) {
-        const float ox = tx3 - (static_cast<float>(c) + 0.5f);
-        const float w = wy[r] * wx[c];
-        float* d = a + (r * kLgOrder + c) * 4;
-        d[0] += w;
-        d[1] += w * ox;
-        d[2] += w * oy;
-        d[3] += w * (ox * ox + oy * oy);
-      }
-    }
-  }
-  // A dense box spans many lanes: when every lane of the wave ends its run in
-  // the same box, the wave sums its partials first and one lane adds them.
-  const int first = __shfl(cur, 0);
-  if (__all(cur == first) && first >= 0) {
-#pragma unroll
-    for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) {
-      float t = a[e];
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
-      a[e] = t;
-    }
-    if ((threadIdx.x & 63) == 0) lg_flush(acc, cur, tile, win, a);
-  } else if (cur >= 0) {
-    lg_flush(acc, cur, tile, win, a);
   }
   __syncthreads();
   const bool sole = tile_item0[it.x + 1] - tile_item0[it.x] == 1;
@@ -304,30 +345,62 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
 }
 
 // Every node of every plane; nodes of single-item tiles were written by the
-// spread itself.
+// spread itself, nodes of empty tiles get zero.  One workgroup per tile: G
+// threads share each window value, thread g summing the tile's items
+// i0 + g, i0 + g + G, ..., and the G partial sums are added in the order
+// g = 0 .. G - 1, so the result does not depend on scheduling.  A dense box
+// early in the optimisation (hundreds of items in one tile) is then summed by
+// the whole workgroup, not by one thread per node.
 __global__ __launch_bounds__(kLgThreads) void k_lg_gather(const int* __restrict__ tile_item0,
                                                           const float* __restrict__ windows, const DeviceScalars* sc,
                                                           float* __restrict__ charge) {
+  __shared__ float part[kLgThreads];
   const int m = sc->lg_nodes;
   const int ta = sc->lg_tiles_axis;
   const int win = sc->lg_tile * kLgOrder;
   const int wn = win * win;
+  const int wvals = 4 * wn;
   const int mm = m * m;
-  const int total = 4 * mm;
-  for (int idx = blockIdx.x * kLgThreads + threadIdx.x; idx < total; idx += gridDim.x * kLgThreads) {
-    const int ch = idx / mm;
-    const int node = idx - ch * mm;
-    const int gy = node / m;
-    const int gx = node - gy * m;
-    const int tx = gx / win, ty = gy / win;
-    const int t = ty * ta + tx;
+  const int per = wvals < kLgThreads ? wvals : kLgThreads;  // values per pass
+  const int groups = kLgThreads / per;                      // threads per value
+  const int g = static_cast<int>(threadIdx.x) / per;
+  const int v = static_cast<int>(threadIdx.x) - g * per;
+  for (int t = blockIdx.x; t < ta * ta; t += gridDim.x) {
     const int i0 = tile_item0[t];
     const int i1 = tile_item0[t + 1];
-    if (i1 - i0 == 1) continue;
-    const int e = ch * wn + (gy - ty * win) * win + (gx - tx * win);
-    float v = 0.0f;
-    for (int i = i0; i < i1; ++i) v += windows[static_cast<std::size_t>(i) * kLgWinVals + e];
-    charge[idx] = v;
+    if (i1 - i0 == 1) continue;  // uniform over the workgroup
+    const int tx = t % ta, ty = t / ta;
+    for (int e0 = 0; e0 < wvals; e0 += per) {
+      const int e = e0 + v;
+      float acc = 0.0f;
+      if (g < groups && e < wvals) {
+        const float* src = windows + e;
+        int i = i0 + g;
+        for (; i + 3 * groups < i1; i += 4 * groups) {
+          const float a0 = src[static_cast<std::size_t>(i) * kLgWinVals];
+          const float a1 = src[static_cast<std::size_t>(i + groups) * kLgWinVals];
+          const float a2 = src[static_cast<std::size_t>(i + 2 * groups) * kLgWinVals];
+          const float a3 = src[static_cast<std::size_t>(i + 3 * groups) * kLgWinVals];
+          acc += a0;
+          acc += a1;
+          acc += a2;
+          acc += a3;
+        }
+        for (; i < i1; i += groups) acc += src[static_cast<std::size_t>(i) * kLgWinVals];
+      }
+      __syncthreads();
+      part[threadIdx.x] = acc;
+      __syncthreads();
+      if (g == 0 && e < wvals) {
+        float sum = part[v];
+        for (int q = 1; q < groups; ++q) sum += part[q * per + v];
+        const int ch = e / wn;
+        const int node = e - ch * wn;
+        const int gy = ty * win + node / win;
+        const int gx = tx * win + node % win;
+        if (gx < m && gy < m) charge[ch * mm + gy * m + gx] = sum;
+      }
+    }
   }
 }
 
@@ -778,14 +851,26 @@ hipError_t launch_interp_bin_scatter(const float2* y_cur, const DeviceScalars* s
   return hipGetLastError();
 }
 
-hipError_t launch_interp_spread(const DeviceScalars* sc, InterpBuffers& ib, int n, hipStream_t stream) {
-  k_lg_spread<<<lg_max_items(n), kLgThreads, 0, stream>>>(ib.binned, ib.items, ib.tile_item0, sc, ib.charge,
-                                                          ib.windows);
+// The largest tile a grid of at most fft_len / 2 nodes per axis can use: the
+// smallest power of two T with ceil(boxes / T) <= kLgMaxTilesAxis, as the
+// statistics set it on the device, for the most boxes that length allows.
+int lg_tile_bound(int fft_len) {
+  const int boxes = std::max(1, (fft_len / 2) / kLgOrder);
+  int tile = 1;
+  while ((boxes + tile - 1) / tile > kLgMaxTilesAxis && tile < kLgMaxTile) tile *= 2;
+  return tile;
+}
+
+hipError_t launch_interp_spread(DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len, hipStream_t stream) {
+  const int win = lg_tile_bound(fft_len) * kLgOrder;
+  const int acc_cap = 4 * win * win;
+  k_lg_spread<<<lg_max_items(n), kLgThreads, static_cast<std::size_t>(acc_cap) * sizeof(float), stream>>>(
+      ib.binned, ib.items, ib.tile_item0, sc, ib.charge, ib.windows, acc_cap);
   return hipGetLastError();
 }
 
 hipError_t launch_interp_gather(const DeviceScalars* sc, InterpBuffers& ib, hipStream_t stream) {
-  k_lg_gather<<<2048, kLgThreads, 0, stream>>>(ib.tile_item0, ib.windows, sc, ib.charge);
+  k_lg_gather<<<kLgMaxTilesAxis * kLgMaxTilesAxis, kLgThreads, 0, stream>>>(ib.tile_item0, ib.windows, sc, ib.charge);
   return hipGetLastError();
 }
 

@@ -216,7 +216,8 @@ hipError_t launch_interp_bin_count(const float2* y_stored, float2* y_cur, const 
 hipError_t launch_interp_bin_plan(InterpBuffers& ib, DeviceScalars* sc, hipStream_t stream);
 hipError_t launch_interp_bin_scatter(const float2* y_cur, const DeviceScalars* sc, InterpBuffers& ib, int n,
                                      hipStream_t stream);
-hipError_t launch_interp_spread(const DeviceScalars* sc, InterpBuffers& ib, int n, hipStream_t stream);
+// fft_len bounds the node count and so the tile size the spread window needs.
+hipError_t launch_interp_spread(DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len, hipStream_t stream);
 hipError_t launch_interp_gather(const DeviceScalars* sc, InterpBuffers& ib, hipStream_t stream);
 // which: 0 kernel rows, 1 kernel transpose, 2 kernel cols, 3 charge rows,
 // 4 charge transpose, 5 conv cols, 6 potential transpose, 7 inverse rows
