@@ -529,7 +529,7 @@ bool write_interp_spec(fastembedr_hip_tsne* s, int order) {
 }
 
 // One iteration's gradient pieces.  The centred layout goes to y_b; the
-// attraction of y_b goes to attr; the repulsion fields (bilinear grid or
+// attraction of the layout goes to attr; the repulsion fields (bilinear grid or
 // interpolation grid at FFT length fft_len) to the grid buffers.  With
 // `overlap` the attraction and the kernel spectrum run on the side streams
 // and the main stream waits for them (before the convolution and before
@@ -541,23 +541,17 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   hipStream_t sa = overlap ? s->side_attr : main;
   hipStream_t sk = overlap ? s->side_kern : main;
   if (lg) s->lg_last_fft = fft_len;
-  // centre + count
-  if (lg) {
-    if (!s->timed(fehip::kKLgBinCount, "interp bin_count launch",
-                  [&] { return fehip::launch_interp_bin_count(s->y_a(), s->y_b, s->sc, ib, n, main); })) {
-      return false;
-    }
-  } else if (!s->timed(fehip::kKBinCount, "bin_count launch",
-                       [&] { return fehip::launch_bin_count(s->y_a(), s->y_b, s->sc, s->gb, n, main); })) {
-    return false;
-  }
+  // The attraction needs only differences y_i - y_j, so it reads the stored
+  // layout (no centring), and the kernel spectrum needs only the node spacing
+  // that the previous update's statistics set: both start at once on the
+  // side streams, beside the whole repulsion chain.
   if (overlap && (!hip_ok(hipEventRecord(s->ev_ready, main), "hipEventRecord(ready)") ||
                   !hip_ok(hipStreamWaitEvent(sa, s->ev_ready, 0), "hipStreamWaitEvent(attraction)") ||
                   !hip_ok(hipStreamWaitEvent(sk, s->ev_ready, 0), "hipStreamWaitEvent(kernel)"))) {
     return false;
   }
   // side: attraction; kernel spectrum
-  if (!enqueue_attract(s, s->y_b, exaggeration, sa, overlap)) return false;
+  if (!enqueue_attract(s, s->y_a(), exaggeration, sa, overlap)) return false;
   if (lg) {
     static constexpr int kIds[3] = {fehip::kKLgKernelRows, fehip::kKLgKernelT, fehip::kKLgKernelCols};
     for (int which = 0; which < 3; ++which) {
@@ -577,6 +571,16 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   }
   if (overlap && (!hip_ok(hipEventRecord(s->ev_attr, sa), "hipEventRecord(attraction)") ||
                   !hip_ok(hipEventRecord(s->ev_kern, sk), "hipEventRecord(kernel)"))) {
+    return false;
+  }
+  // main: centre + count
+  if (lg) {
+    if (!s->timed(fehip::kKLgBinCount, "interp bin_count launch",
+                  [&] { return fehip::launch_interp_bin_count(s->y_a(), s->y_b, s->sc, ib, n, main); })) {
+      return false;
+    }
+  } else if (!s->timed(fehip::kKBinCount, "bin_count launch",
+                       [&] { return fehip::launch_bin_count(s->y_a(), s->y_b, s->sc, s->gb, n, main); })) {
     return false;
   }
   // main: bins, spread, charge transforms
