@@ -46,6 +46,7 @@ SIGNATURES = {
     "fastembedr_hip_tsne_set_repulsion": (_I, [_P, _I, _I, _I, _F]),
     "fastembedr_hip_tsne_interp_info": (_I, [_P, _IP, _IP, _IP, _FP, _DP]),
     "fastembedr_hip_tsne_attraction_info": (_I, [_P, _LLP, _IP]),
+    "fastembedr_hip_tsne_graph_info": (_I, [_P, _LLP, _IP, _IP]),
     "fastembedr_hip_tsne_attraction_slots": (_I, [_P, _LLP]),
     "fastembedr_hip_tsne_set_timing": (_I, [_P, _I]),
     "fastembedr_hip_tsne_timing_stats": (_I, [_P, _I, _LLP, _DP]),

@@ -109,9 +109,12 @@ __device__ void publish_stats(BlockStats local, BlockStats* partial) {
 }
 
 // Reduces the per-block statistics in a fixed order (deterministic) and sets
-// the grid geometry.  With box_out (pinned, coherent host memory) the
-// interpolation grid's box count is also stored there, so the host can learn
-// it from an event on this kernel instead of a device-to-host copy.
+// the grid geometry.  With box_out (a ring of kBoxRing ints in pinned,
+// coherent host memory) the interpolation grid's box count is also stored in
+// slot sc->ring_seq % kBoxRing and the counter advanced, so the host can learn
+// it from an event on this kernel instead of a device-to-host copy.  The slot
+// is chosen on the device so that a replayed graph of the iteration writes
+// the next slot each time.
 __global__ __launch_bounds__(256) void k_finalize_stats(const BlockStats* __restrict__ partial, int blocks,
                                                         DeviceScalars* sc, int n, int g, int center,
                                                         int* box_out) {
@@ -120,7 +123,11 @@ __global__ __launch_bounds__(256) void k_finalize_stats(const BlockStats* __rest
   acc = block_stats<256>(acc);
   if (threadIdx.x == 0) {
     set_geometry(sc, acc, n, g, center != 0);
-    if (box_out != nullptr) __hip_atomic_store(box_out, sc->lg_boxes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (box_out != nullptr) {
+      const int slot = sc->ring_seq & (kBoxRing - 1);
+      __hip_atomic_store(box_out + slot, sc->lg_boxes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      sc->ring_seq = sc->ring_seq + 1;
+    }
   }
 }
 

@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cfloat>
 #include <cstddef>
 #include <cmath>
@@ -100,6 +101,18 @@ struct Arena {
   }
 };
 
+// FASTEMBEDR_HIP_GRAPH_CAPTURE: unset or empty = on; 0, false, FALSE, no, NO
+// = off (the reference's FASTEMBEDR_CUDA_GRAPH_CAPTURE switch,
+// src/embedding_cuda_kernels.cpp:170-178).
+bool graph_capture_enabled() {
+  const char* env = std::getenv("FASTEMBEDR_HIP_GRAPH_CAPTURE");
+  if (env == nullptr || env[0] == '\0') return true;
+  for (const char* off : {"0", "false", "FALSE", "no", "NO"}) {
+    if (std::strcmp(env, off) == 0) return false;
+  }
+  return true;
+}
+
 bool memory_preflight(std::size_t bytes, const char* where) {
   std::size_t free_b = 0, total_b = 0;
   if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return true;
@@ -177,13 +190,33 @@ struct fastembedr_hip_tsne {
   fehip::InterpBuffers ib;
   int lg_last_fft = 0;       // FFT length of the last interpolation-grid iteration
   // Box counts of recent iterations (pinned coherent ring, written by the
-  // update's statistics kernel): slot it % kLgRing holds the geometry the
-  // update of iteration it - 1 set.
-  static constexpr int kLgRing = 8;
+  // update's statistics kernel into slot DeviceScalars::ring_seq % kLgRing,
+  // which it then advances); lg_ring_iter[r] names the iteration whose
+  // geometry slot r holds, lg_ev[r] the event after the update that wrote it.
+  static constexpr int kLgRing = fehip::kBoxRing;
   int* lg_ring = nullptr;
   int* lg_ring_dev = nullptr;  // the ring's device address
   hipEvent_t lg_ev[kLgRing] = {};
   long long lg_ring_iter[kLgRing] = {};
+
+  // Replayed iterations (FASTEMBEDR_HIP_GRAPH_CAPTURE, on by default): one
+  // iteration's launches on the three streams (gradient pieces + update) are
+  // captured into a graph keyed by everything the launches bake in, and
+  // replayed with one hipGraphLaunch.  A key is captured the second time it
+  // is met (a one-off FFT length is not worth an instantiation); renumbering,
+  // the attraction's tile build and timed runs stay eager.
+  struct IterGraph {
+    std::array<std::uint32_t, 12> key{};
+    hipGraphExec_t exec = nullptr;
+    int seen = 0;
+    unsigned long long last_use = 0;
+  };
+  static constexpr std::size_t kMaxGraphs = 8;
+  bool graph_capture = true;
+  std::vector<IterGraph> graphs;
+  unsigned long long graph_clock = 0;
+  long long graph_launches = 0;
+  int graph_captures = 0;
 
   bool renumbered() const { return wi >= 0; }
   const Csr& work_p() const { return wi < 0 ? p : pw[wi]; }
@@ -207,6 +240,9 @@ struct fastembedr_hip_tsne {
 
   ~fastembedr_hip_tsne() {
     if (stream != nullptr) (void)hipStreamSynchronize(stream);
+    for (IterGraph& g : graphs) {
+      if (g.exec != nullptr) (void)hipGraphExecDestroy(g.exec);
+    }
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
     for (hipEvent_t e : lg_ev) {
       if (e != nullptr) (void)hipEventDestroy(e);
@@ -418,6 +454,18 @@ bool alloc_tiles(fastembedr_hip_tsne* s) {
                 "hipMemset(attraction claims)");
 }
 
+// Builds the attraction's tiles for the current working numbering on stream
+// st, unless they are built already.
+bool ensure_tiles(fastembedr_hip_tsne* s, hipStream_t st) {
+  if (!s->attract_tiled || s->tiles_for == s->wi) return true;
+  if (!s->timed(
+          fehip::kKTileBuild, "tile build", [&] { return fehip::launch_tile_build(s->work_p(), s->tiles, st); }, st)) {
+    return false;
+  }
+  s->tiles_for = s->wi;
+  return true;
+}
+
 // Attractive term of every row into s->attr at the centred layout y_cur, on
 // stream st (the main stream when null); `shared`: other kernels run beside it.
 bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggeration, hipStream_t st = nullptr,
@@ -431,14 +479,7 @@ bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggera
         fehip::kKAttract, "attract launch",
         [&] { return fehip::launch_attract(s->work_p(), y_cur, s->attr, exaggeration, s->lanes, s->xcds, st); }, st);
   }
-  if (s->tiles_for != s->wi) {
-    if (!s->timed(
-            fehip::kKTileBuild, "tile build", [&] { return fehip::launch_tile_build(s->work_p(), s->tiles, st); },
-            st)) {
-      return false;
-    }
-    s->tiles_for = s->wi;
-  }
+  if (!ensure_tiles(s, st)) return false;
   return s->timed(
       fehip::kKAttract, "attract launch",
       [&] {
@@ -626,10 +667,101 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   return !overlap || hip_ok(hipStreamWaitEvent(main, s->ev_attr, 0), "hipStreamWaitEvent(main, attraction)");
 }
 
-// Current interpolation geometry, read synchronously.
-bool read_interp_boxes(fastembedr_hip_tsne* s, int* boxes) {
+// One optimisation iteration: the gradient pieces and the update.  With
+// `ring` the update's statistics kernel also hands the new box count to the
+// host's ring (the slot is chosen on the device).
+bool enqueue_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up, bool overlap) {
+  return enqueue_gradient_pieces(s, lg, fft_len, up.exaggeration, overlap) &&
+         s->timed(fehip::kKUpdate, "update launch", [&] {
+           return fehip::launch_update(fehip::kModeUpdate, s->y_b, s->attr, s->y_a(), s->update(), s->gains(), nullptr,
+                                       nullptr, s->gb, up, s->partial, s->sc, s->n, s->stream,
+                                       lg ? s->ib.field : nullptr, lg ? s->lg_ring_dev : nullptr);
+         });
+}
+
+// Captures enqueue_iteration() into an executable graph (nothing runs).
+bool capture_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up, bool overlap,
+                       hipGraphExec_t* exec) {
+  if (!hip_ok(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture")) {
+    return false;
+  }
+  const bool enqueued = enqueue_iteration(s, lg, fft_len, up, overlap);
+  hipGraph_t graph = nullptr;
+  const hipError_t ended = hipStreamEndCapture(s->stream, &graph);
+  bool ok = enqueued && hip_ok(ended, "hipStreamEndCapture") && graph != nullptr;
+  if (ok) ok = hip_ok(hipGraphInstantiate(exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+  if (graph != nullptr) (void)hipGraphDestroy(graph);
+  return ok;
+}
+
+// Enqueues one iteration as a replayed graph when its key has a captured one,
+// captures it the second time the key is met, and runs it eagerly otherwise.
+bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up) {
+  using IterGraph = fastembedr_hip_tsne::IterGraph;
+  // Graph nodes keep the streams' order but not the tile build's host-side
+  // bookkeeping: build the tiles eagerly first.
+  if (!ensure_tiles(s, s->stream)) return false;
+  auto bits = [](float v) {
+    std::uint32_t u;
+    std::memcpy(&u, &v, sizeof(u));
+    return u;
+  };
+  const std::array<std::uint32_t, 12> key = {static_cast<std::uint32_t>(lg),
+                                             static_cast<std::uint32_t>(fft_len),
+                                             static_cast<std::uint32_t>(s->si),
+                                             static_cast<std::uint32_t>(s->wi),
+                                             static_cast<std::uint32_t>(s->attract_tiled),
+                                             static_cast<std::uint32_t>(s->attract_shared_per_cu),
+                                             bits(up.exaggeration),
+                                             bits(up.momentum),
+                                             bits(up.learning_rate),
+                                             bits(up.min_gain),
+                                             bits(up.max_step_norm),
+                                             static_cast<std::uint32_t>(up.clip)};
+  ++s->graph_clock;
+  IterGraph* g = nullptr;
+  for (IterGraph& c : s->graphs) {
+    if (c.key == key) g = &c;
+  }
+  if (g == nullptr) {
+    if (s->graphs.size() >= fastembedr_hip_tsne::kMaxGraphs) {
+      auto lru = std::min_element(s->graphs.begin(), s->graphs.end(),
+                                  [](const IterGraph& a, const IterGraph& b) { return a.last_use < b.last_use; });
+      if (lru->exec != nullptr) {
+        // an executable graph may still be in flight: drain before destroying it
+        if (!s->sync_all() || !hip_ok(hipGraphExecDestroy(lru->exec), "hipGraphExecDestroy")) return false;
+      }
+      s->graphs.erase(lru);
+    }
+    s->graphs.push_back(IterGraph{});
+    g = &s->graphs.back();
+    g->key = key;
+  }
+  g->last_use = s->graph_clock;
+  if (g->exec == nullptr && ++g->seen >= 2) {
+    if (!capture_iteration(s, lg, fft_len, up, true, &g->exec)) {
+      // A capture the runtime refuses leaves the session on eager launches.
+      if (g->exec != nullptr) (void)hipGraphExecDestroy(g->exec);
+      g->exec = nullptr;
+      (void)hipGetLastError();
+      s->graph_capture = false;
+      g_last_error.clear();
+    } else {
+      ++s->graph_captures;
+    }
+  }
+  if (g->exec == nullptr) return enqueue_iteration(s, lg, fft_len, up, true);
+  ++s->graph_launches;
+  return hip_ok(hipGraphLaunch(g->exec, s->stream), "hipGraphLaunch");
+}
+
+// Current interpolation geometry and the device's ring counter, read
+// synchronously.
+bool read_interp_boxes(fastembedr_hip_tsne* s, int* boxes, int* ring_seq) {
   return hip_ok(hipMemcpyAsync(boxes, &s->sc->lg_boxes, sizeof(int), hipMemcpyDeviceToHost, s->stream),
                 "hipMemcpy(boxes)") &&
+         hip_ok(hipMemcpyAsync(ring_seq, &s->sc->ring_seq, sizeof(int), hipMemcpyDeviceToHost, s->stream),
+                "hipMemcpy(ring counter)") &&
          hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize(boxes)");
 }
 
@@ -1003,6 +1135,7 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   }
 
   s->attract_shared_per_cu = env_int("FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU", s->attract_shared_per_cu);
+  s->graph_capture = graph_capture_enabled();
   if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {
     delete s;
     return 1;
@@ -1246,9 +1379,10 @@ int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int
                 "update launch");
   } else if (repulsion == FASTEMBEDR_HIP_REPULSION_LAGRANGE) {
     int boxes = 0;
+    int ring_seq = 0;
     ok = ensure_interp(s) && write_interp_spec(s, fehip::kLgOrder) &&
          hip_ok(fehip::launch_stats(s->y_a(), s->n, s->gb.g, 0, s->partial, s->sc, s->stream), "stats launch") &&
-         read_interp_boxes(s, &boxes) &&
+         read_interp_boxes(s, &boxes, &ring_seq) &&
          enqueue_gradient_pieces(s, true, interp_fft_len(std::min(boxes * fehip::kLgOrder, fehip::kLgMaxNodes)),
                                  exaggeration, false) &&
          hip_ok(fehip::launch_update(fehip::kModeGradientGrid, s->y_b, s->attr, nullptr, nullptr, nullptr, s->grad,
@@ -1323,10 +1457,12 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
               : 0.0;
   int known_boxes = 0;
   int known_it = 0;
+  int ring_base = 0;  // iteration it's update writes slot (ring_base + it) % kRing
   if (lg) {
-    if (!read_interp_boxes(s, &known_boxes)) return 1;
+    if (!read_interp_boxes(s, &known_boxes, &ring_base)) return 1;
     std::fill(std::begin(s->lg_ring_iter), std::end(s->lg_ring_iter), -1LL);
   }
+  auto ring_slot = [&](int it) { return static_cast<int>((static_cast<unsigned int>(ring_base) + it) % kRing); };
   for (int it = 0; it < n_iter; ++it) {
     // Renumber before the first iteration ever run and then every
     // reorder_period iterations; the bounding box and pending shift it needs
@@ -1346,7 +1482,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
       }
       if (it - known_it > allowed_lag) {
         const int target = it - allowed_lag;  // its slot was enqueued by iteration target - 1 < it
-        const int slot = target % kRing;
+        const int slot = ring_slot(target - 1);
         if (!hip_ok(hipEventSynchronize(s->lg_ev[slot]), "hipEventSynchronize(box ring)")) return 1;
         known_it = target;
         known_boxes = static_cast<volatile int*>(s->lg_ring)[slot];
@@ -1357,17 +1493,12 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
       fft_len = interp_fft_len(nodes);
     }
     // Timing every kernel (mode 1) runs the pieces in sequence, so that each
-    // duration is the kernel's alone.
+    // duration is the kernel's alone; timed runs are never replayed graphs.
     const bool overlap = !(s->timing && s->timed_only < 0);
-    const int slot = (it + 1) % kRing;
-    if (!enqueue_gradient_pieces(s, lg, fft_len, exaggeration, overlap) ||
-        !s->timed(fehip::kKUpdate, "update launch", [&] {
-          return fehip::launch_update(fehip::kModeUpdate, s->y_b, s->attr, s->y_a(), s->update(), s->gains(),
-                                      nullptr, nullptr, s->gb, up, s->partial, s->sc, n, s->stream,
-                                      lg ? s->ib.field : nullptr, lg ? s->lg_ring_dev + slot : nullptr);
-        })) {
-      return 1;
-    }
+    const int slot = ring_slot(it);
+    const bool ok = s->graph_capture && !s->timing ? enqueue_iteration_graphed(s, lg, fft_len, up)
+                                                   : enqueue_iteration(s, lg, fft_len, up, overlap);
+    if (!ok) return 1;
     if (lg) {
       if (!hip_ok(hipEventRecord(s->lg_ev[slot], s->stream), "hipEventRecord(box ring)")) return 1;
       s->lg_ring_iter[slot] = it + 1;
@@ -1445,6 +1576,14 @@ int fastembedr_hip_tsne_attraction_slots(fastembedr_hip_tsne* s, long long* slot
     }
     *slots = total;
   }
+  return 0;
+}
+
+int fastembedr_hip_tsne_graph_info(fastembedr_hip_tsne* s, long long* launches, int* captures, int* enabled) {
+  if (!valid_state_args(s)) return 1;
+  if (launches != nullptr) *launches = s->graph_launches;
+  if (captures != nullptr) *captures = s->graph_captures;
+  if (enabled != nullptr) *enabled = s->graph_capture ? 1 : 0;
   return 0;
 }
 

@@ -33,7 +33,7 @@ struct alignas(16) DeviceScalars {
   unsigned int pad2;
   unsigned long long self_edges;
   int num_items;             // spread work items of the current iteration
-  int pad1;
+  int ring_seq;              // next slot (mod kBoxRing) of the host's box-count ring
   // FIt-SNE interpolation grid.  The host sets the specification (lg_order
   // 0 = unused); the statistics finalize sets the geometry of the current
   // layout: the square [lg_lo, lg_lo + lg_boxes * lg_box_w]^2 of centred
@@ -52,6 +52,9 @@ struct BlockStats {
 };
 
 constexpr int kMaxReduceBlocks = 4096;
+// Slots of the pinned ring through which the update's statistics kernel hands
+// the interpolation grid's box count to the host (a power of two).
+constexpr int kBoxRing = 8;
 constexpr int kTwiddleLen = 4096;     // e^{-2 pi i m / 4096}, m in [0, 4096)
 constexpr int kMaxGrid = 1024;        // nodes per axis (FFT length 2048)
 

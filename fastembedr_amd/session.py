@@ -159,6 +159,14 @@ class TsneSession:
         _lib.check(self._lib.fastembedr_hip_tsne_attraction_slots(self._h, C.byref(s)), "attraction_slots")
         return {"tiles": int(t.value), "renumbers": int(r.value), "slots": int(s.value)}
 
+    def graph_info(self) -> dict:
+        """Iterations of run() replayed from captured graphs, graphs captured,
+        and whether capture is on for this session."""
+        n, c, e = C.c_longlong(), C.c_int(), C.c_int()
+        _lib.check(self._lib.fastembedr_hip_tsne_graph_info(self._h, C.byref(n), C.byref(c), C.byref(e)),
+                   "graph_info")
+        return {"launches": int(n.value), "captures": int(c.value), "enabled": bool(e.value)}
+
     def center(self) -> None:
         _lib.check(self._lib.fastembedr_hip_tsne_center(self._h), "center")
 

@@ -176,6 +176,15 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_set_repulsion(fastembedr_hip_tsne* se
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_interp_info(fastembedr_hip_tsne* session, int* boxes, int* nodes,
                                     int* fft_len, float* box_width, double* z);
 
+/* Replayed iterations of run(): how many iterations ran as a replayed graph,
+ * how many graphs were captured, and whether capture is on (it follows
+ * FASTEMBEDR_HIP_GRAPH_CAPTURE at session creation, as the reference's
+ * FASTEMBEDR_CUDA_GRAPH_CAPTURE does, src/embedding_cuda_kernels.cpp:170-178;
+ * timed runs never replay).  Any pointer may be NULL.  No counterpart in the
+ * reference's ABI. */
+FASTEMBEDR_HIP_API int fastembedr_hip_tsne_graph_info(fastembedr_hip_tsne* session, long long* launches,
+                                   int* captures, int* enabled);
+
 /* Locality of the attraction's tiled P: the number of (row block, column
  * tile) runs of the current working numbering (-1 before the first build,
  * or when the row-parallel attraction is used) and the number of
