@@ -95,8 +95,7 @@ __device__ void set_geometry(DeviceScalars* sc, const BlockStats& t, int n, int 
     sc->lg_node_h = static_cast<float>(w / static_cast<double>(sc->lg_order));
     sc->lg_boxes = nb;
     sc->lg_nodes = nb * sc->lg_order;
-    int tile = 1;
-    while ((nb + tile - 1) / tile > kLgMaxTilesAxis) tile *= 2;
+    const int tile = lg_tile_for(nb);
     sc->lg_tile = tile;
     sc->lg_tiles_axis = (nb + tile - 1) / tile;
   }
@@ -109,24 +108,27 @@ __device__ void publish_stats(BlockStats local, BlockStats* partial) {
 }
 
 // Reduces the per-block statistics in a fixed order (deterministic) and sets
-// the grid geometry.  With box_out (a ring of kBoxRing ints in pinned,
-// coherent host memory) the interpolation grid's box count is also stored in
-// slot sc->ring_seq % kBoxRing and the counter advanced, so the host can learn
-// it from an event on this kernel instead of a device-to-host copy.  The slot
-// is chosen on the device so that a replayed graph of the iteration writes
-// the next slot each time.
+// the grid geometry.  With box_out (a ring of kBoxRing slots in pinned,
+// coherent host memory) the interpolation grid's box count, tagged with the
+// sequence number sc->ring_seq, is also stored in slot ring_seq % kBoxRing
+// (one 64-bit store) and the counter advanced, so the host learns it by
+// reading host memory: no device-to-host copy and no event.  The slot is
+// chosen on the device so that a replayed graph of the iteration writes the
+// next slot each time.
 __global__ __launch_bounds__(256) void k_finalize_stats(const BlockStats* __restrict__ partial, int blocks,
                                                         DeviceScalars* sc, int n, int g, int center,
-                                                        int* box_out) {
+                                                        unsigned long long* box_out) {
   BlockStats acc = stats_identity();
   for (int b = threadIdx.x; b < blocks; b += 256) combine(acc, partial[b]);
   acc = block_stats<256>(acc);
   if (threadIdx.x == 0) {
     set_geometry(sc, acc, n, g, center != 0);
     if (box_out != nullptr) {
-      const int slot = sc->ring_seq & (kBoxRing - 1);
-      __hip_atomic_store(box_out + slot, sc->lg_boxes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-      sc->ring_seq = sc->ring_seq + 1;
+      const unsigned int seq = sc->ring_seq;
+      const unsigned long long tagged =
+          (static_cast<unsigned long long>(seq) << 32) | static_cast<unsigned int>(sc->lg_boxes);
+      __hip_atomic_store(box_out + (seq & (kBoxRing - 1)), tagged, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      sc->ring_seq = seq + 1u;
     }
   }
 }
@@ -348,22 +350,28 @@ __global__ __launch_bounds__(kPointThreads) void k_bin_count(const float2* __res
   }
 }
 
-// Exclusive scan of up to kMaxTiles counts by one block of 1024 threads
-// (four entries per thread, then a Hillis-Steele scan of the thread sums).
-__device__ int block_exclusive_scan4(int (&v)[4], int* part) {
+// Exclusive scan of up to kMaxTiles counts by one block of kPlanThreads
+// threads (kPlanPer consecutive entries per thread, then a Hillis-Steele scan
+// of the thread sums).  A block of 4 waves finds room on a CU beside the
+// attraction sooner than a block of 16 would.
+constexpr int kPlanThreads = 256;
+constexpr int kPlanPer = kMaxTiles / kPlanThreads;
+static_assert(kPlanPer * kPlanThreads == kMaxTiles, "whole entries per thread");
+__device__ int block_exclusive_scan(int (&v)[kPlanPer], int* part) {
   const int t = threadIdx.x;
-  int s = v[0] + v[1] + v[2] + v[3];
+  int s = 0;
+  for (int q = 0; q < kPlanPer; ++q) s += v[q];
   part[t] = s;
   __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
     const int add = t >= off ? part[t - off] : 0;
     __syncthreads();
     part[t] += add;
     __syncthreads();
   }
-  const int total = part[1023];
+  const int total = part[kPlanThreads - 1];
   int run = part[t] - s;
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < kPlanPer; ++q) {
     const int c = v[q];
     v[q] = run;
     run += c;
@@ -375,24 +383,25 @@ __device__ int block_exclusive_scan4(int (&v)[4], int* part) {
 // tiles < 0: the interpolation grid's tile count, lg_tiles_axis^2, read on the
 // device.  tile_item0 (optional) receives the first work item of each tile
 // and, at [tiles], the number of items.
-__global__ __launch_bounds__(1024) void k_bin_plan(int* __restrict__ tile_count, int* __restrict__ tile_cursor,
-                                                   int4* __restrict__ items, DeviceScalars* sc, int tiles,
-                                                   int* __restrict__ tile_item0) {
-  __shared__ int part[1024];
+__global__ __launch_bounds__(kPlanThreads) void k_bin_plan(int* __restrict__ tile_count,
+                                                           int* __restrict__ tile_cursor, int4* __restrict__ items,
+                                                           DeviceScalars* sc, int tiles,
+                                                           int* __restrict__ tile_item0) {
+  __shared__ int part[kPlanThreads];
   if (tiles < 0) tiles = sc->lg_tiles_axis * sc->lg_tiles_axis;
-  int cnt[4], start[4], chunks[4], base[4];
-  for (int q = 0; q < 4; ++q) {
-    const int t = threadIdx.x * 4 + q;
+  int cnt[kPlanPer], start[kPlanPer], chunks[kPlanPer], base[kPlanPer];
+  for (int q = 0; q < kPlanPer; ++q) {
+    const int t = threadIdx.x * kPlanPer + q;
     cnt[q] = t < tiles ? tile_count[t] : 0;
     if (t < tiles) tile_count[t] = 0;  // ready for the next iteration's count
     start[q] = cnt[q];
     chunks[q] = (cnt[q] + kChunk - 1) / kChunk;
     base[q] = chunks[q];
   }
-  block_exclusive_scan4(start, part);
-  const int total_items = block_exclusive_scan4(base, part);
-  for (int q = 0; q < 4; ++q) {
-    const int t = threadIdx.x * 4 + q;
+  block_exclusive_scan(start, part);
+  const int total_items = block_exclusive_scan(base, part);
+  for (int q = 0; q < kPlanPer; ++q) {
+    const int t = threadIdx.x * kPlanPer + q;
     if (t >= tiles) continue;
     tile_cursor[t] = start[q];
     if (tile_item0 != nullptr) tile_item0[t] = base[q];
@@ -1352,7 +1361,7 @@ template <int MODE>
 hipError_t update_launch(const float2* y_cur, const float2* attr, float2* y_out, float2* update, float2* gains,
                          float2* grad_out, const float2* exact_rep, const GridBuffers& gb, const UpdateParams& up,
                          BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
-                         const float4* interp_field, int* box_out) {
+                         const float4* interp_field) {
   const int blocks = reduce_blocks_for(n);
   if (interp_field != nullptr && MODE != kModeGradientExact) {
     k_update<MODE, true><<<blocks, kPointThreads, 0, stream>>>(y_cur, attr, y_out, update, gains, grad_out,
@@ -1361,7 +1370,6 @@ hipError_t update_launch(const float2* y_cur, const float2* attr, float2* y_out,
     k_update<MODE, false><<<blocks, kPointThreads, 0, stream>>>(y_cur, attr, y_out, update, gains, grad_out,
                                                                 exact_rep, gb.field, gb.g, up, partial, sc, n);
   }
-  if (MODE == kModeUpdate) k_finalize_stats<<<1, 256, 0, stream>>>(partial, blocks, sc, n, gb.g, 1, box_out);
   return hipGetLastError();
 }
 
@@ -1432,6 +1440,12 @@ hipError_t launch_stats(const float2* y, int n, int g, int center, BlockStats* p
   return hipGetLastError();
 }
 
+hipError_t launch_finalize_stats(const BlockStats* partial, int n, int g, DeviceScalars* sc,
+                                 unsigned long long* box_out, hipStream_t stream) {
+  k_finalize_stats<<<1, 256, 0, stream>>>(partial, reduce_blocks_for(n), sc, n, g, 1, box_out);
+  return hipGetLastError();
+}
+
 hipError_t launch_bin_count(const float2* y_stored, float2* y_cur, const DeviceScalars* sc, GridBuffers& gb, int n,
                             hipStream_t stream) {
   const int ta = tiles_per_axis(gb.g);
@@ -1442,12 +1456,12 @@ hipError_t launch_bin_count(const float2* y_stored, float2* y_cur, const DeviceS
 
 hipError_t launch_bin_plan(GridBuffers& gb, DeviceScalars* sc, hipStream_t stream) {
   const int ta = tiles_per_axis(gb.g);
-  k_bin_plan<<<1, 1024, 0, stream>>>(gb.tile_count, gb.tile_cursor, gb.items, sc, ta * ta, nullptr);
+  k_bin_plan<<<1, kPlanThreads, 0, stream>>>(gb.tile_count, gb.tile_cursor, gb.items, sc, ta * ta, nullptr);
   return hipGetLastError();
 }
 
 hipError_t launch_interp_bin_plan(InterpBuffers& ib, DeviceScalars* sc, hipStream_t stream) {
-  k_bin_plan<<<1, 1024, 0, stream>>>(ib.tile_count, ib.tile_cursor, ib.items, sc, -1, ib.tile_item0);
+  k_bin_plan<<<1, kPlanThreads, 0, stream>>>(ib.tile_count, ib.tile_cursor, ib.items, sc, -1, ib.tile_item0);
   return hipGetLastError();
 }
 
@@ -1498,17 +1512,17 @@ hipError_t launch_attract(const Csr& p, const float2* y_cur, float2* attr, float
 hipError_t launch_update(int mode, const float2* y_cur, const float2* attr, float2* y_out, float2* update,
                          float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
                          const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
-                         const float4* interp_field, int* box_out) {
+                         const float4* interp_field) {
   switch (mode) {
     case kModeUpdate:
       return update_launch<kModeUpdate>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc,
-                                        n, stream, interp_field, box_out);
+                                        n, stream, interp_field);
     case kModeGradientGrid:
       return update_launch<kModeGradientGrid>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up,
-                                              partial, sc, n, stream, interp_field, nullptr);
+                                              partial, sc, n, stream, interp_field);
     case kModeGradientExact:
       return update_launch<kModeGradientExact>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up,
-                                               partial, sc, n, stream, nullptr, nullptr);
+                                               partial, sc, n, stream, nullptr);
     default:
       return hipErrorInvalidValue;
   }

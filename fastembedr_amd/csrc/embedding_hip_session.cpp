@@ -22,6 +22,7 @@
 #include <limits>
 #include <random>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "fastembedr_hip.h"
@@ -133,13 +134,15 @@ struct fastembedr_hip_tsne {
   int lanes = 16;
   int xcds = 1;              // XCDs of the device (blocks are dispatched round-robin over them)
   hipStream_t stream = nullptr;
-  // Side streams of run(): the attraction and the kernel spectrum depend only
-  // on the centred layout, so they run beside the binning, spreading and
-  // convolution of the main stream, which waits for them (events) before the
-  // convolution and the update.  All streams have the default priority.
+  // Side streams of run(): the attraction depends only on the stored layout
+  // and the kernel spectrum only on the grid geometry, so they run beside the
+  // binning, spreading and convolution of the main stream, which waits for
+  // them (events) before the convolution and the update.  All streams have
+  // the default priority.
   hipStream_t side_attr = nullptr;
   hipStream_t side_kern = nullptr;
-  hipEvent_t ev_ready = nullptr;  // centred layout written (main)
+  hipEvent_t ev_layout = nullptr; // stored layout written (main)
+  hipEvent_t ev_ready = nullptr;  // grid geometry set (main)
   hipEvent_t ev_attr = nullptr;   // attraction done (side_attr)
   hipEvent_t ev_kern = nullptr;   // kernel spectrum done (side_kern)
   Arena arena;
@@ -189,15 +192,13 @@ struct fastembedr_hip_tsne {
   Arena lg_arena;
   fehip::InterpBuffers ib;
   int lg_last_fft = 0;       // FFT length of the last interpolation-grid iteration
-  // Box counts of recent iterations (pinned coherent ring, written by the
-  // update's statistics kernel into slot DeviceScalars::ring_seq % kLgRing,
-  // which it then advances); lg_ring_iter[r] names the iteration whose
-  // geometry slot r holds, lg_ev[r] the event after the update that wrote it.
+  // Box counts of recent iterations: a pinned coherent ring that the
+  // update's statistics kernel writes, slot DeviceScalars::ring_seq % kLgRing
+  // = (ring_seq << 32) | boxes, before it advances ring_seq.  The host reads
+  // it directly (no event per iteration).
   static constexpr int kLgRing = fehip::kBoxRing;
-  int* lg_ring = nullptr;
-  int* lg_ring_dev = nullptr;  // the ring's device address
-  hipEvent_t lg_ev[kLgRing] = {};
-  long long lg_ring_iter[kLgRing] = {};
+  unsigned long long* lg_ring = nullptr;
+  unsigned long long* lg_ring_dev = nullptr;  // the ring's device address
 
   // Replayed iterations (FASTEMBEDR_HIP_GRAPH_CAPTURE, on by default): one
   // iteration's launches on the three streams (gradient pieces + update) are
@@ -206,7 +207,7 @@ struct fastembedr_hip_tsne {
   // is met (a one-off FFT length is not worth an instantiation); renumbering,
   // the attraction's tile build and timed runs stay eager.
   struct IterGraph {
-    std::array<std::uint32_t, 12> key{};
+    std::array<std::uint32_t, 13> key{};
     hipGraphExec_t exec = nullptr;
     int seen = 0;
     unsigned long long last_use = 0;
@@ -244,15 +245,12 @@ struct fastembedr_hip_tsne {
       if (g.exec != nullptr) (void)hipGraphExecDestroy(g.exec);
     }
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
-    for (hipEvent_t e : lg_ev) {
-      if (e != nullptr) (void)hipEventDestroy(e);
-    }
     if (lg_ring != nullptr) (void)hipHostFree(lg_ring);
     lg_arena.release();
     for (hipStream_t st : {side_attr, side_kern}) {
       if (st != nullptr) (void)hipStreamSynchronize(st);
     }
-    for (hipEvent_t e : {ev_ready, ev_attr, ev_kern}) {
+    for (hipEvent_t e : {ev_layout, ev_ready, ev_attr, ev_kern}) {
       if (e != nullptr) (void)hipEventDestroy(e);
     }
     tile_arena.release();
@@ -313,7 +311,8 @@ const char* kKernelNames[fehip::kKernelCount] = {
     "conv_cols", "inverse_rows", "attract", "update", "commit", "renumber", "tile_build",
     "interp_bin_count", "interp_bin_plan", "interp_bin_scatter", "interp_spread", "interp_gather",
     "interp_kernel_rows", "interp_kernel_transpose", "interp_kernel_cols", "interp_charge_rows",
-    "interp_charge_transpose", "interp_conv_cols", "interp_potential_transpose", "interp_inverse_rows"};
+    "interp_charge_transpose", "interp_conv_cols", "interp_potential_transpose", "interp_inverse_rows",
+    "finalize_stats"};
 
 int key_bits_for(int n) {
   int b = 1;
@@ -538,18 +537,16 @@ bool ensure_interp(fastembedr_hip_tsne* s) {
   }
   if (!hip_ok(hipMemsetAsync(ib.tile_count, 0, (fehip::kMaxTiles + 1) * sizeof(int), s->stream),
               "hipMemset(interpolation tiles)") ||
-      !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s->lg_ring), fastembedr_hip_tsne::kLgRing * sizeof(int),
+      !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s->lg_ring),
+                            fastembedr_hip_tsne::kLgRing * sizeof(unsigned long long),
                             hipHostMallocMapped | hipHostMallocCoherent),
               "hipHostMalloc(box ring)") ||
       !hip_ok(hipHostGetDevicePointer(reinterpret_cast<void**>(&s->lg_ring_dev), s->lg_ring, 0),
               "hipHostGetDevicePointer(box ring)")) {
     return false;
   }
-  for (int r = 0; r < fastembedr_hip_tsne::kLgRing; ++r) {
-    if (!hip_ok(hipEventCreateWithFlags(&s->lg_ev[r], hipEventDisableTiming), "hipEventCreate(box ring)")) {
-      return false;
-    }
-  }
+  // no sequence number the device writes before 2^32 updates
+  for (int r = 0; r < fastembedr_hip_tsne::kLgRing; ++r) __atomic_store_n(s->lg_ring + r, ~0ull, __ATOMIC_RELEASE);
   s->lg_ready = true;
   return true;
 }
@@ -572,10 +569,14 @@ bool write_interp_spec(fastembedr_hip_tsne* s, int order) {
 // One iteration's gradient pieces.  The centred layout goes to y_b; the
 // attraction of the layout goes to attr; the repulsion fields (bilinear grid or
 // interpolation grid at FFT length fft_len) to the grid buffers.  With
-// `overlap` the attraction and the kernel spectrum run on the side streams
-// and the main stream waits for them (before the convolution and before
-// whatever follows this call); without it everything runs on the main stream.
-bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float exaggeration, bool overlap) {
+// `finalize` the previous update's statistics are finished first (the grid
+// geometry of this iteration; with the interpolation grid the box count also
+// goes to the host's ring).  With `overlap` the attraction and the kernel
+// spectrum run on the side streams and the main stream waits for them (before
+// the convolution and before whatever follows this call); without it
+// everything runs on the main stream.
+bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float exaggeration, bool overlap,
+                             bool finalize = false) {
   const int n = s->n;
   fehip::InterpBuffers& ib = s->ib;
   hipStream_t main = s->stream;
@@ -583,16 +584,26 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   hipStream_t sk = overlap ? s->side_kern : main;
   if (lg) s->lg_last_fft = fft_len;
   // The attraction needs only differences y_i - y_j, so it reads the stored
-  // layout (no centring), and the kernel spectrum needs only the node spacing
-  // that the previous update's statistics set: both start at once on the
-  // side streams, beside the whole repulsion chain.
+  // layout (no centring) and starts at once, beside the statistics' finish
+  // and the whole repulsion chain.
+  if (overlap && (!hip_ok(hipEventRecord(s->ev_layout, main), "hipEventRecord(layout)") ||
+                  !hip_ok(hipStreamWaitEvent(sa, s->ev_layout, 0), "hipStreamWaitEvent(attraction)"))) {
+    return false;
+  }
+  if (!enqueue_attract(s, s->y_a(), exaggeration, sa, overlap) ||
+      (overlap && !hip_ok(hipEventRecord(s->ev_attr, sa), "hipEventRecord(attraction)"))) {
+    return false;
+  }
+  if (finalize && !s->timed(fehip::kKFinalize, "finalize launch", [&] {
+        return fehip::launch_finalize_stats(s->partial, n, s->gb.g, s->sc, lg ? s->lg_ring_dev : nullptr, main);
+      })) {
+    return false;
+  }
+  // The kernel spectrum needs only the node spacing of the geometry.
   if (overlap && (!hip_ok(hipEventRecord(s->ev_ready, main), "hipEventRecord(ready)") ||
-                  !hip_ok(hipStreamWaitEvent(sa, s->ev_ready, 0), "hipStreamWaitEvent(attraction)") ||
                   !hip_ok(hipStreamWaitEvent(sk, s->ev_ready, 0), "hipStreamWaitEvent(kernel)"))) {
     return false;
   }
-  // side: attraction; kernel spectrum
-  if (!enqueue_attract(s, s->y_a(), exaggeration, sa, overlap)) return false;
   if (lg) {
     static constexpr int kIds[3] = {fehip::kKLgKernelRows, fehip::kKLgKernelT, fehip::kKLgKernelCols};
     for (int which = 0; which < 3; ++which) {
@@ -610,10 +621,7 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
                  [&] { return fehip::launch_kernel_cols(s->gb, s->tw, sk); }, sk)) {
     return false;
   }
-  if (overlap && (!hip_ok(hipEventRecord(s->ev_attr, sa), "hipEventRecord(attraction)") ||
-                  !hip_ok(hipEventRecord(s->ev_kern, sk), "hipEventRecord(kernel)"))) {
-    return false;
-  }
+  if (overlap && !hip_ok(hipEventRecord(s->ev_kern, sk), "hipEventRecord(kernel)")) return false;
   // main: centre + count
   if (lg) {
     if (!s->timed(fehip::kKLgBinCount, "interp bin_count launch",
@@ -630,7 +638,7 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
     ok = s->timed(fehip::kKLgBinPlan, "interp bin_plan launch",
                   [&] { return fehip::launch_interp_bin_plan(ib, s->sc, main); }) &&
          s->timed(fehip::kKLgBinScatter, "interp bin_scatter launch",
-                  [&] { return fehip::launch_interp_bin_scatter(s->y_b, s->sc, ib, n, main); }) &&
+                  [&] { return fehip::launch_interp_bin_scatter(s->y_b, s->sc, ib, n, fft_len, main); }) &&
          s->timed(fehip::kKLgSpread, "interp spread launch",
                   [&] { return fehip::launch_interp_spread(s->sc, ib, n, fft_len, main); }) &&
          s->timed(fehip::kKLgGather, "interp gather launch",
@@ -667,25 +675,27 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   return !overlap || hip_ok(hipStreamWaitEvent(main, s->ev_attr, 0), "hipStreamWaitEvent(main, attraction)");
 }
 
-// One optimisation iteration: the gradient pieces and the update.  With
-// `ring` the update's statistics kernel also hands the new box count to the
-// host's ring (the slot is chosen on the device).
-bool enqueue_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up, bool overlap) {
-  return enqueue_gradient_pieces(s, lg, fft_len, up.exaggeration, overlap) &&
+// One optimisation iteration: the previous update's statistics finished
+// (`finalize`, see enqueue_gradient_pieces), the gradient pieces and the
+// update.  The update's own statistics are finished by the next iteration or
+// by the caller, so that the next attraction can start beside that finish.
+bool enqueue_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up, bool overlap,
+                       bool finalize) {
+  return enqueue_gradient_pieces(s, lg, fft_len, up.exaggeration, overlap, finalize) &&
          s->timed(fehip::kKUpdate, "update launch", [&] {
            return fehip::launch_update(fehip::kModeUpdate, s->y_b, s->attr, s->y_a(), s->update(), s->gains(), nullptr,
                                        nullptr, s->gb, up, s->partial, s->sc, s->n, s->stream,
-                                       lg ? s->ib.field : nullptr, lg ? s->lg_ring_dev : nullptr);
+                                       lg ? s->ib.field : nullptr);
          });
 }
 
 // Captures enqueue_iteration() into an executable graph (nothing runs).
 bool capture_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up, bool overlap,
-                       hipGraphExec_t* exec) {
+                       bool finalize, hipGraphExec_t* exec) {
   if (!hip_ok(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture")) {
     return false;
   }
-  const bool enqueued = enqueue_iteration(s, lg, fft_len, up, overlap);
+  const bool enqueued = enqueue_iteration(s, lg, fft_len, up, overlap, finalize);
   hipGraph_t graph = nullptr;
   const hipError_t ended = hipStreamEndCapture(s->stream, &graph);
   bool ok = enqueued && hip_ok(ended, "hipStreamEndCapture") && graph != nullptr;
@@ -696,7 +706,8 @@ bool capture_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip
 
 // Enqueues one iteration as a replayed graph when its key has a captured one,
 // captures it the second time the key is met, and runs it eagerly otherwise.
-bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up) {
+bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up,
+                               bool finalize) {
   using IterGraph = fastembedr_hip_tsne::IterGraph;
   // Graph nodes keep the streams' order but not the tile build's host-side
   // bookkeeping: build the tiles eagerly first.
@@ -706,7 +717,8 @@ bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, con
     std::memcpy(&u, &v, sizeof(u));
     return u;
   };
-  const std::array<std::uint32_t, 12> key = {static_cast<std::uint32_t>(lg),
+  const std::array<std::uint32_t, 13> key = {static_cast<std::uint32_t>(lg),
+                                             static_cast<std::uint32_t>(finalize),
                                              static_cast<std::uint32_t>(fft_len),
                                              static_cast<std::uint32_t>(s->si),
                                              static_cast<std::uint32_t>(s->wi),
@@ -739,7 +751,7 @@ bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, con
   }
   g->last_use = s->graph_clock;
   if (g->exec == nullptr && ++g->seen >= 2) {
-    if (!capture_iteration(s, lg, fft_len, up, true, &g->exec)) {
+    if (!capture_iteration(s, lg, fft_len, up, true, finalize, &g->exec)) {
       // A capture the runtime refuses leaves the session on eager launches.
       if (g->exec != nullptr) (void)hipGraphExecDestroy(g->exec);
       g->exec = nullptr;
@@ -750,19 +762,45 @@ bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, con
       ++s->graph_captures;
     }
   }
-  if (g->exec == nullptr) return enqueue_iteration(s, lg, fft_len, up, true);
+  if (g->exec == nullptr) return enqueue_iteration(s, lg, fft_len, up, true, finalize);
   ++s->graph_launches;
   return hip_ok(hipGraphLaunch(g->exec, s->stream), "hipGraphLaunch");
 }
 
 // Current interpolation geometry and the device's ring counter, read
 // synchronously.
-bool read_interp_boxes(fastembedr_hip_tsne* s, int* boxes, int* ring_seq) {
+bool read_interp_boxes(fastembedr_hip_tsne* s, int* boxes, unsigned int* ring_seq) {
   return hip_ok(hipMemcpyAsync(boxes, &s->sc->lg_boxes, sizeof(int), hipMemcpyDeviceToHost, s->stream),
                 "hipMemcpy(boxes)") &&
          hip_ok(hipMemcpyAsync(ring_seq, &s->sc->ring_seq, sizeof(int), hipMemcpyDeviceToHost, s->stream),
                 "hipMemcpy(ring counter)") &&
          hip_ok(hipStreamSynchronize(s->stream), "hipStreamSynchronize(boxes)");
+}
+
+// Waits until the ring slot of sequence number `seq` holds it and returns its
+// box count.  The update that writes it is enqueued on the main stream: if
+// that stream has drained and the slot still lacks the number, the write
+// never happened (an error, not a wait).
+bool wait_ring(fastembedr_hip_tsne* s, unsigned int seq, int* boxes) {
+  const unsigned long long* slot = s->lg_ring + (seq & (fastembedr_hip_tsne::kLgRing - 1));
+  for (unsigned int spin = 1;; ++spin) {
+    const unsigned long long v = __atomic_load_n(slot, __ATOMIC_ACQUIRE);
+    if (static_cast<unsigned int>(v >> 32) == seq) {
+      *boxes = static_cast<int>(v & 0xffffffffull);
+      return true;
+    }
+    if (spin % 64 == 0) {
+      const hipError_t q = hipStreamQuery(s->stream);
+      if (q == hipSuccess) {
+        const unsigned long long again = __atomic_load_n(slot, __ATOMIC_ACQUIRE);
+        if (static_cast<unsigned int>(again >> 32) == seq) continue;
+        set_error("internal: the interpolation grid's box count was not handed over");
+        return false;
+      }
+      if (q != hipErrorNotReady) return hip_ok(q, "hipStreamQuery(box ring)");
+    }
+    std::this_thread::yield();
+  }
 }
 
 // Device error flags raised during iterations (so far only the interpolation
@@ -900,6 +938,7 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   if (!hip_ok(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate") ||
       !hip_ok(hipStreamCreateWithFlags(&s->side_attr, hipStreamNonBlocking), "hipStreamCreate") ||
       !hip_ok(hipStreamCreateWithFlags(&s->side_kern, hipStreamNonBlocking), "hipStreamCreate") ||
+      !hip_ok(hipEventCreateWithFlags(&s->ev_layout, hipEventDisableTiming), "hipEventCreate") ||
       !hip_ok(hipEventCreateWithFlags(&s->ev_ready, hipEventDisableTiming), "hipEventCreate") ||
       !hip_ok(hipEventCreateWithFlags(&s->ev_attr, hipEventDisableTiming), "hipEventCreate") ||
       !hip_ok(hipEventCreateWithFlags(&s->ev_kern, hipEventDisableTiming), "hipEventCreate")) {
@@ -1379,7 +1418,7 @@ int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int
                 "update launch");
   } else if (repulsion == FASTEMBEDR_HIP_REPULSION_LAGRANGE) {
     int boxes = 0;
-    int ring_seq = 0;
+    unsigned int ring_seq = 0;
     ok = ensure_interp(s) && write_interp_spec(s, fehip::kLgOrder) &&
          hip_ok(fehip::launch_stats(s->y_a(), s->n, s->gb.g, 0, s->partial, s->sc, s->stream), "stats launch") &&
          read_interp_boxes(s, &boxes, &ring_seq) &&
@@ -1457,35 +1496,47 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
               : 0.0;
   int known_boxes = 0;
   int known_it = 0;
-  int ring_base = 0;  // iteration it's update writes slot (ring_base + it) % kRing
-  if (lg) {
-    if (!read_interp_boxes(s, &known_boxes, &ring_base)) return 1;
-    std::fill(std::begin(s->lg_ring_iter), std::end(s->lg_ring_iter), -1LL);
-  }
-  auto ring_slot = [&](int it) { return static_cast<int>((static_cast<unsigned int>(ring_base) + it) % kRing); };
+  unsigned int ring_base = 0;  // iteration it's update writes sequence number ring_base + it
+  if (lg && !read_interp_boxes(s, &known_boxes, &ring_base)) return 1;
+  // Each update's statistics are finished (k_finalize_stats) at the top of
+  // the next iteration, beside the start of its attraction, or after the
+  // loop; `pending` says that the previous update's are not finished yet.
+  bool pending = false;
+  auto finish_pending = [&](unsigned long long* ring) {
+    pending = false;
+    return s->timed(fehip::kKFinalize, "finalize launch", [&] {
+      return fehip::launch_finalize_stats(s->partial, n, s->gb.g, s->sc, ring, s->stream);
+    });
+  };
   for (int it = 0; it < n_iter; ++it) {
     // Renumber before the first iteration ever run and then every
     // reorder_period iterations; the bounding box and pending shift it needs
-    // are in DeviceScalars (stats kernel above, or the previous update).
+    // are in DeviceScalars (stats kernel above, or the previous update's
+    // finished statistics).
     if (s->reorder_period > 0 && s->since_reorder >= s->reorder_gap) {
+      if (pending && !finish_pending(lg ? s->lg_ring_dev : nullptr)) return 1;
       if (!s->timed(fehip::kKRenumber, "renumber", [&] { return enqueue_renumber(s); })) return 1;
       s->reorder_gap = s->reorder_gap == 0 ? s->reorder_period : 2 * s->reorder_gap;
     }
     ++s->since_reorder;
     int fft_len = 0;
     if (lg) {
+      // the newest geometry handed over: the statistics of iteration d's
+      // update (sequence number ring_base + d) set iteration d + 1's
       for (int r = 0; r < kRing; ++r) {
-        if (s->lg_ring_iter[r] > known_it && hipEventQuery(s->lg_ev[r]) == hipSuccess) {
-          known_it = static_cast<int>(s->lg_ring_iter[r]);
-          known_boxes = static_cast<volatile int*>(s->lg_ring)[r];
+        const unsigned long long v = __atomic_load_n(s->lg_ring + r, __ATOMIC_ACQUIRE);
+        const unsigned int d = static_cast<unsigned int>(v >> 32) - ring_base;
+        if (d < static_cast<unsigned int>(it) && static_cast<int>(d) + 1 > known_it) {
+          known_it = static_cast<int>(d) + 1;
+          known_boxes = static_cast<int>(v & 0xffffffffull);
         }
       }
       if (it - known_it > allowed_lag) {
-        const int target = it - allowed_lag;  // its slot was enqueued by iteration target - 1 < it
-        const int slot = ring_slot(target - 1);
-        if (!hip_ok(hipEventSynchronize(s->lg_ev[slot]), "hipEventSynchronize(box ring)")) return 1;
+        const int target = it - allowed_lag;  // set by the statistics of iteration target - 1 < it
+        // (without the step clip that is this iteration's own geometry: finish it first)
+        if (target == it && pending && !finish_pending(s->lg_ring_dev)) return 1;
+        if (!wait_ring(s, ring_base + static_cast<unsigned int>(target - 1), &known_boxes)) return 1;
         known_it = target;
-        known_boxes = static_cast<volatile int*>(s->lg_ring)[slot];
       }
       const long long bound =
           static_cast<long long>(known_boxes) + static_cast<long long>(std::ceil(growth * (it - known_it)));
@@ -1495,15 +1546,13 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
     // Timing every kernel (mode 1) runs the pieces in sequence, so that each
     // duration is the kernel's alone; timed runs are never replayed graphs.
     const bool overlap = !(s->timing && s->timed_only < 0);
-    const int slot = ring_slot(it);
-    const bool ok = s->graph_capture && !s->timing ? enqueue_iteration_graphed(s, lg, fft_len, up)
-                                                   : enqueue_iteration(s, lg, fft_len, up, overlap);
+    const bool ok = s->graph_capture && !s->timing ? enqueue_iteration_graphed(s, lg, fft_len, up, pending)
+                                                   : enqueue_iteration(s, lg, fft_len, up, overlap, pending);
     if (!ok) return 1;
-    if (lg) {
-      if (!hip_ok(hipEventRecord(s->lg_ev[slot], s->stream), "hipEventRecord(box ring)")) return 1;
-      s->lg_ring_iter[slot] = it + 1;
-    }
+    pending = true;
   }
+  // the last update's statistics (no box count is needed from them)
+  if (pending && !finish_pending(nullptr)) return 1;
   if (!s->timed(fehip::kKCommit, "commit launch",
                 [&] { return fehip::launch_commit(s->y_a(), s->sc, n, s->stream); })) {
     return 1;

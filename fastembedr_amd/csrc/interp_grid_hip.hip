@@ -115,15 +115,24 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_bin_count(const float2* __res
 
 constexpr int kLgScatterPerThread = 4;
 
+// The workgroup's tile histogram lives in dynamic LDS of tiles_cap ints,
+// tiles_cap the most tiles the FFT length allows, and is overwritten in
+// place by the tiles' reserved base offsets (each point keeps its rank in
+// registers), so that several workgroups fit on a CU beside the attraction.
+// More tiles than tiles_cap (which the host's FFT-length bound excludes)
+// raise kErrInterpGrid.
 __global__ __launch_bounds__(kLgThreads) void k_lg_bin_scatter(const float2* __restrict__ y_cur,
-                                                               const DeviceScalars* sc,
+                                                               DeviceScalars* sc,
                                                                int* __restrict__ tile_cursor,
-                                                               float2* __restrict__ binned, int n) {
-  __shared__ int hist[kMaxTiles];
-  __shared__ int base[kMaxTiles];
+                                                               float2* __restrict__ binned, int n, int tiles_cap) {
+  extern __shared__ int hist[];  // counts, then base offsets
   const DeviceScalars s = *sc;
   const int ta = s.lg_tiles_axis;
   const int tiles = ta * ta;
+  if (tiles > tiles_cap) {  // uniform over the grid
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&sc->error_flags, kErrInterpGrid);
+    return;
+  }
   constexpr int kBatch = kLgThreads * kLgScatterPerThread;
   for (int b0 = blockIdx.x * kBatch; b0 < n; b0 += gridDim.x * kBatch) {
     for (int t = threadIdx.x; t < tiles; t += kLgThreads) hist[t] = 0;
@@ -143,12 +152,12 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_bin_scatter(const float2* __r
     __syncthreads();
     for (int t = threadIdx.x; t < tiles; t += kLgThreads) {
       const int c = hist[t];
-      if (c != 0) base[t] = atomicAdd(tile_cursor + t, c);
+      if (c != 0) hist[t] = atomicAdd(tile_cursor + t, c);
     }
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < kLgScatterPerThread; ++q) {
-      if (tile[q] >= 0) binned[base[tile[q]] + rank[q]] = v[q];
+      if (tile[q] >= 0) binned[hist[tile[q]] + rank[q]] = v[q];
     }
     __syncthreads();
   }
@@ -842,24 +851,32 @@ hipError_t launch_interp_bin_count(const float2* y_stored, float2* y_cur, const 
   return hipGetLastError();
 }
 
-hipError_t launch_interp_bin_scatter(const float2* y_cur, const DeviceScalars* sc, InterpBuffers& ib, int n,
+// Boxes per axis of a grid of at most fft_len / 2 nodes per axis.
+int lg_boxes_bound(int fft_len) { return std::max(1, std::min(fft_len / 2, kLgMaxNodes) / kLgOrder); }
+
+// The most tiles per axis any such grid is cut into (lg_tile_for, as the
+// statistics apply it on the device).
+int lg_tiles_axis_bound(int fft_len) {
+  int most = 1;
+  for (int nb = 1; nb <= lg_boxes_bound(fft_len); ++nb) most = std::max(most, (nb + lg_tile_for(nb) - 1) / lg_tile_for(nb));
+  return most;
+}
+
+hipError_t launch_interp_bin_scatter(const float2* y_cur, DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len,
                                      hipStream_t stream) {
   constexpr int kBatch = kLgThreads * kLgScatterPerThread;
   const int needed = (n + kBatch - 1) / kBatch;
   const int blocks = std::max(1, std::min(needed, 1024));
-  k_lg_bin_scatter<<<blocks, kLgThreads, 0, stream>>>(y_cur, sc, ib.tile_cursor, ib.binned, n);
+  const int ta = lg_tiles_axis_bound(fft_len);
+  const int tiles_cap = ta * ta;
+  k_lg_bin_scatter<<<blocks, kLgThreads, tiles_cap * sizeof(int), stream>>>(y_cur, sc, ib.tile_cursor, ib.binned, n,
+                                                                           tiles_cap);
   return hipGetLastError();
 }
 
-// The largest tile a grid of at most fft_len / 2 nodes per axis can use: the
-// smallest power of two T with ceil(boxes / T) <= kLgMaxTilesAxis, as the
-// statistics set it on the device, for the most boxes that length allows.
-int lg_tile_bound(int fft_len) {
-  const int boxes = std::max(1, (fft_len / 2) / kLgOrder);
-  int tile = 1;
-  while ((boxes + tile - 1) / tile > kLgMaxTilesAxis && tile < kLgMaxTile) tile *= 2;
-  return tile;
-}
+// The largest tile a grid of at most fft_len / 2 nodes per axis can use (the
+// tile grows with the box count).
+int lg_tile_bound(int fft_len) { return lg_tile_for(lg_boxes_bound(fft_len)); }
 
 hipError_t launch_interp_spread(DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len, hipStream_t stream) {
   const int win = lg_tile_bound(fft_len) * kLgOrder;

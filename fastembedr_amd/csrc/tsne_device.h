@@ -33,7 +33,7 @@ struct alignas(16) DeviceScalars {
   unsigned int pad2;
   unsigned long long self_edges;
   int num_items;             // spread work items of the current iteration
-  int ring_seq;              // next slot (mod kBoxRing) of the host's box-count ring
+  unsigned int ring_seq;     // updates that wrote the host's box-count ring so far
   // FIt-SNE interpolation grid.  The host sets the specification (lg_order
   // 0 = unused); the statistics finalize sets the geometry of the current
   // layout: the square [lg_lo, lg_lo + lg_boxes * lg_box_w]^2 of centred
@@ -53,7 +53,9 @@ struct BlockStats {
 
 constexpr int kMaxReduceBlocks = 4096;
 // Slots of the pinned ring through which the update's statistics kernel hands
-// the interpolation grid's box count to the host (a power of two).
+// the interpolation grid's box count to the host (a power of two).  Each slot
+// holds (sequence number << 32) | box count, so the host can tell which
+// update wrote it without an event.
 constexpr int kBoxRing = 8;
 constexpr int kTwiddleLen = 4096;     // e^{-2 pi i m / 4096}, m in [0, 4096)
 constexpr int kMaxGrid = 1024;        // nodes per axis (FFT length 2048)
@@ -73,11 +75,15 @@ enum ErrorBits : unsigned int { kErrIndex = 1u, kErrDistance = 2u, kErrInterpGri
 
 // FIt-SNE interpolation grid: order-3 nodes, at most kLgMaxNodes nodes per
 // axis (FFT length <= 4096).  Points are binned by tiles of T x T boxes, T the
-// smallest power of two that keeps the tiles per axis <= kLgMaxTilesAxis; a
-// work item's spread window is 3T x 3T nodes x 4 charges (at most
-// kLgWinVals floats, T <= kLgMaxTile).
+// smallest power of two that keeps the tiles per axis <= kLgTilesAxisTarget,
+// at most kLgMaxTile (then up to kLgMaxTilesAxis tiles per axis); a work
+// item's spread window is 3T x 3T nodes x 4 charges (at most kLgWinVals
+// floats).  Few, well-filled tiles keep the binning's histograms small and
+// the spreading's workgroups few: under the attraction's memory traffic every
+// round of latency-bound workgroups costs tens of microseconds.
 constexpr int kLgOrder = 3;
 constexpr int kLgMaxTile = 16;
+constexpr int kLgTilesAxisTarget = 64;
 constexpr int kLgMaxTilesAxis = 64;
 constexpr int kLgWin = kLgMaxTile * kLgOrder;
 constexpr int kLgWinVals = 4 * kLgWin * kLgWin;
@@ -85,6 +91,12 @@ constexpr int kLgMaxNodes = 2048;
 constexpr int kLgMaxFft = 2 * kLgMaxNodes;
 static_assert(kLgMaxTilesAxis * kLgMaxTilesAxis <= kMaxTiles, "interpolation tiles fit the bin plan");
 static_assert(kLgMaxTile * kLgMaxTilesAxis * kLgOrder >= kLgMaxNodes, "the largest tile covers the largest grid");
+// Boxes per tile side for a grid of nb boxes per axis (the rule above).
+__host__ __device__ inline int lg_tile_for(int nb) {
+  int tile = 1;
+  while ((nb + tile - 1) / tile > kLgTilesAxisTarget && tile < kLgMaxTile) tile *= 2;
+  return tile;
+}
 inline int lg_max_items(int n) { return (n + kChunk - 1) / kChunk + kLgMaxTilesAxis * kLgMaxTilesAxis; }
 // three spectral sums per column-pass block (<= f/2 + 1 blocks), one per row block (<= f/2)
 constexpr int kLgZPartials = 3 * (kLgMaxFft / 2 + 1) + kLgMaxFft / 2;
@@ -118,6 +130,7 @@ enum KernelId : int {
   kKLgConvCols,
   kKLgPotentialT,
   kKLgInverseRows,
+  kKFinalize,
   kKernelCount
 };
 
@@ -217,7 +230,7 @@ hipError_t launch_inverse_rows(GridBuffers& gb, const float2* tw, int n, DeviceS
 hipError_t launch_interp_bin_count(const float2* y_stored, float2* y_cur, const DeviceScalars* sc,
                                    InterpBuffers& ib, int n, hipStream_t stream);
 hipError_t launch_interp_bin_plan(InterpBuffers& ib, DeviceScalars* sc, hipStream_t stream);
-hipError_t launch_interp_bin_scatter(const float2* y_cur, const DeviceScalars* sc, InterpBuffers& ib, int n,
+hipError_t launch_interp_bin_scatter(const float2* y_cur, DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len,
                                      hipStream_t stream);
 // fft_len bounds the node count and so the tile size the spread window needs.
 hipError_t launch_interp_spread(DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len, hipStream_t stream);
@@ -241,15 +254,20 @@ struct UpdateParams {
 hipError_t launch_attract(const Csr& p, const float2* y_cur, float2* attr, float exaggeration, int lanes_per_row,
                           int xcds, hipStream_t stream);
 // Repulsion read-back + attr -> gradient; kModeUpdate applies the update and
-// computes the next iteration's statistics, the gradient modes write grad_out.
-// interp_field != nullptr reads the FIt-SNE interpolation grid instead of the
-// bilinear one (kModeUpdate and kModeGradientGrid).  kModeUpdate with
-// box_out != nullptr (device pointer of pinned coherent host memory) also
-// stores the next iteration's interpolation box count there.
+// writes per-block statistics of the new layout to `partial` (finished by
+// launch_finalize_stats), the gradient modes write grad_out.  interp_field !=
+// nullptr reads the FIt-SNE interpolation grid instead of the bilinear one
+// (kModeUpdate and kModeGradientGrid).
 hipError_t launch_update(int mode, const float2* y_cur, const float2* attr, float2* y_out, float2* update,
                          float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
                          const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
-                         const float4* interp_field = nullptr, int* box_out = nullptr);
+                         const float4* interp_field = nullptr);
+// The next iteration's centring and grid geometry from kModeUpdate's
+// statistics (one workgroup).  With box_out != nullptr (device pointer of a
+// ring of kBoxRing slots in pinned coherent host memory) the interpolation
+// grid's box count is also stored there, tagged with DeviceScalars::ring_seq.
+hipError_t launch_finalize_stats(const BlockStats* partial, int n, int g, DeviceScalars* sc,
+                                 unsigned long long* box_out, hipStream_t stream);
 hipError_t launch_commit(float2* y, const DeviceScalars* sc, int n, hipStream_t stream);
 
 // ---- locality renumbering ---------------------------------------------------

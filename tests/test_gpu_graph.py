@@ -1,21 +1,25 @@
 """Replayed iterations (FASTEMBEDR_HIP_GRAPH_CAPTURE) against eager launches.
 
 run() captures one iteration's launches on its three streams into a graph and
-replays it; the kernels and their order are the same as the eager path's, so
-a replayed run must agree with an eager one as closely as two eager runs
-agree with each other (the float atomics of the binning make two eager runs
-differ by rounding).  The switch is read when a session is created: unset or
-empty is on, "0"/"false"/"FALSE"/"no"/"NO" is off, as for the reference's
+replays it; the kernels and their order are the same as the eager path's.
+The switch is read when a session is created: unset or empty is on,
+"0"/"false"/"FALSE"/"no"/"NO" is off, as for the reference's
 FASTEMBEDR_CUDA_GRAPH_CAPTURE (src/embedding_cuda_kernels.cpp:170-178).
 
-Checked per repulsion (bilinear grid, interpolation grid):
-  * the replayed run took most iterations from graphs (graph_info);
-  * the displacement from the start differs from an eager run's by at most
-    4 x (eager vs eager) + 1e-6, relative L2, over 40 iterations that cross
-    an early-exaggeration -> normal switch (two graph keys);
+Float atomics (the attraction's row sums, the binning's order) make two eager
+runs differ by rounding, which t-SNE's early-exaggeration phase amplifies
+over tens of iterations; so the layouts are compared one iteration at a time
+and whole runs by their KL divergence.  Checked per repulsion (bilinear grid,
+interpolation grid):
+  * one replayed iteration (the third from the same state: eager, captured,
+    replayed) equals one eager iteration from that state: displacement
+    relative L2 <= max(5e-5, 4 x (eager vs eager)) (the bilinear spreading's
+    LDS float atomics alone give about 1.6e-5);
+  * 60 + 60 iterations, most replayed (graph_info), end at an exact KL within
+    0.5 % of the eager run's;
   * with a growing span (the interpolation grid's FFT length changes between
-    keys, and the host learns box counts through the device-indexed ring) the
-    final exact KL agrees with the eager run's within 0.5 %;
+    graph keys, and the host learns box counts from the device-indexed ring)
+    the final KL agrees within 0.5 %;
   * the switch's off values turn capture off.
 """
 
@@ -73,19 +77,46 @@ def _schedule(hip, idx, dist, y0, repulsion, capture, early, normal):
 
 
 @pytest.mark.parametrize("repulsion", [_lib.REPULSION_GRID, _lib.REPULSION_LAGRANGE], ids=["bilinear", "interp"])
-def test_replayed_iterations_match_eager(hip, prob, repulsion):
+def test_replayed_iteration_matches_eager(hip, prob, repulsion):
     x, idx, dist, y0 = prob
-    _say(f"case: graph replay vs eager, repulsion {repulsion}, 20 + 20 iterations")
-    start, y_e1, _, info_e = _schedule(hip, idx, dist, y0, repulsion, "0", 20, 20)
-    _, y_e2, _, _ = _schedule(hip, idx, dist, y0, repulsion, "0", 20, 20)
-    _, y_g, _, info_g = _schedule(hip, idx, dist, y0, repulsion, None, 20, 20)
-    assert not info_e["enabled"] and info_e["launches"] == 0
-    assert info_g["enabled"] and info_g["captures"] >= 2 and info_g["launches"] >= 30, info_g
+    n = y0.shape[0]
+    _say(f"case: one replayed iteration vs one eager iteration, repulsion {repulsion}")
+
+    def one(s):
+        if repulsion == _lib.REPULSION_LAGRANGE:
+            s.set_repulsion(repulsion, 3, 50, 1.0)
+        s.set_state(y0)
+        s.center()
+        start = s.y
+        s.run(1, 12.0, 0.5, n / 12.0, 0.01, 5.0)
+        return start, s.y
+
+    with _session(hip, idx, dist, None) as s:
+        for _ in range(3):  # eager (first sight of the key), captured and replayed, replayed
+            start, y_g = one(s)
+        info = s.graph_info()
+    with _session(hip, idx, dist, "0") as s:
+        start_e, y_e1 = one(s)
+        _, y_e2 = one(s)
+    np.testing.assert_array_equal(start, start_e)
     base = rel_l2(y_e2 - start, y_e1 - start)
     err = rel_l2(y_g - start, y_e1 - start)
-    _say(f"  eager vs eager {base:.2e}, graph vs eager {err:.2e}, {info_g}")
+    _say(f"  eager vs eager {base:.2e}, replayed vs eager {err:.2e}, {info}")
+    assert info["captures"] == 1 and info["launches"] == 2, info
+    assert err <= max(5e-5, 4.0 * base)
+
+
+@pytest.mark.parametrize("repulsion", [_lib.REPULSION_GRID, _lib.REPULSION_LAGRANGE], ids=["bilinear", "interp"])
+def test_replayed_schedule_kl(hip, prob, repulsion):
+    x, idx, dist, y0 = prob
+    _say(f"case: graph replay vs eager, repulsion {repulsion}, 60 + 60 iterations")
+    _, y_e, kl_e, info_e = _schedule(hip, idx, dist, y0, repulsion, "0", 60, 60)
+    _, y_g, kl_g, info_g = _schedule(hip, idx, dist, y0, repulsion, None, 60, 60)
+    _say(f"  KL eager {kl_e:.5f}, graph {kl_g:.5f}, {info_g}")
+    assert not info_e["enabled"] and info_e["launches"] == 0
+    assert info_g["enabled"] and info_g["launches"] >= 100, info_g
     assert np.all(np.isfinite(y_g))
-    assert err <= 4.0 * base + 1e-6
+    assert abs(kl_g - kl_e) <= 0.005 * kl_e
 
 
 def test_replayed_growing_span_kl(hip, prob):
