@@ -176,10 +176,11 @@ struct fastembedr_hip_tsne {
   // tiles follow the working numbering and are rebuilt after it changes.
   bool attract_tiled = true;
   // Workgroups per CU of the attraction when it runs beside the repulsion
-  // kernels (side stream): fewer than the 3 its LDS allows leave room on
-  // every CU for them (2: measured best at config 2).  Alone it takes one
-  // workgroup per row block.
-  int attract_shared_per_cu = 2;
+  // kernels (side stream), possibly fractional: fewer than the 3 its LDS
+  // allows leave room on every CU for the latency-bound repulsion chain
+  // (FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU).  Alone it takes one workgroup
+  // per row block.
+  double attract_shared_per_cu = 1.0;
   int cus = 0;  // compute units of the device
   fehip::Tiles tiles;
   int tiles_for = -2;       // value of wi the tiles were built for; -2: none
@@ -470,8 +471,9 @@ bool ensure_tiles(fastembedr_hip_tsne* s, hipStream_t st) {
 bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggeration, hipStream_t st = nullptr,
                      bool shared = false) {
   if (st == nullptr) st = s->stream;
-  const int slots = shared && s->cus > 0 && s->attract_shared_per_cu > 0
-                        ? s->attract_shared_per_cu * std::max(1, s->cus / s->xcds)
+  const int slots = shared && s->cus > 0 && s->attract_shared_per_cu > 0.0
+                        ? std::max(1, static_cast<int>(std::lround(s->attract_shared_per_cu *
+                                                                   std::max(1, s->cus / s->xcds))))
                         : 0;
   if (!s->attract_tiled) {
     return s->timed(
@@ -723,7 +725,7 @@ bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, con
                                              static_cast<std::uint32_t>(s->si),
                                              static_cast<std::uint32_t>(s->wi),
                                              static_cast<std::uint32_t>(s->attract_tiled),
-                                             static_cast<std::uint32_t>(s->attract_shared_per_cu),
+                                             static_cast<std::uint32_t>(std::lround(1000.0 * s->attract_shared_per_cu)),
                                              bits(up.exaggeration),
                                              bits(up.momentum),
                                              bits(up.learning_rate),
@@ -1173,7 +1175,11 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
     if (std::strcmp(tiled, "0") == 0) s->attract_tiled = false;
   }
 
-  s->attract_shared_per_cu = env_int("FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU", s->attract_shared_per_cu);
+  if (const char* v = std::getenv("FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU")) {
+    char* end = nullptr;
+    const double d = std::strtod(v, &end);
+    if (end != v && std::isfinite(d) && d >= 0.0) s->attract_shared_per_cu = d;
+  }
   s->graph_capture = graph_capture_enabled();
   if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {
     delete s;
