@@ -447,29 +447,39 @@ __device__ __forceinline__ void attract_row_block(int rb, const unsigned short* 
   __syncthreads();
 }
 
-// Workgroups take the row blocks of their XCD's range: first the one at their
-// slot, then the next unclaimed one from the XCD's counter work[xcd] (claims
-// count from the number of slots).  With one slot per row block this is one
-// row block per workgroup; with fewer, the kernel leaves LDS and wave slots
-// free for kernels that run beside it, and the dynamic claims balance the
-// row blocks' unequal work.  The last workgroup to finish resets work[] (its
-// xcds + 1 counters start and end each launch at zero).  Launch bounds:
-// MINB workgroups per CU (the VGPR budget of the D-deep prefetch ring).
+// Workgroups take the row blocks of their XCD's range: a primary launch's
+// first the one at their slot (slots = workgroups per XCD), then, like every
+// workgroup of a helper launch, the next unclaimed one from the XCD's counter
+// work[xcd] (claims count from `slots`).  With one slot per row block this is
+// one row block per workgroup; with fewer, the kernel leaves LDS and wave
+// slots free for kernels that run beside it, and the dynamic claims balance
+// the row blocks' unequal work.  A helper launch, enqueued later on another
+// stream once the kernels beside the primary are done, takes over the row
+// blocks still unclaimed.  The last workgroup of the pair (`total` workgroups
+// between them) resets work[] (its xcds + 1 counters start and end each
+// launch or pair at zero).  Launch bounds: MINB workgroups per CU (the VGPR
+// budget of the D-deep prefetch ring).
 template <int NT, int D, int MINB>
 __global__ __launch_bounds__(NT, MINB) void k_attract_tiles_seg(
     const unsigned short* __restrict__ ent, const float* __restrict__ val, const int* __restrict__ tile_ptr,
     const int* __restrict__ tile_cb, const int* __restrict__ tile_beg, const float2* __restrict__ y_cur,
-    float2* __restrict__ attr, float exaggeration, int n, int row_blocks, int xcds, unsigned int* __restrict__ work) {
+    float2* __restrict__ attr, float exaggeration, int n, int row_blocks, int xcds, unsigned int* __restrict__ work,
+    int slots, int helper, unsigned int total) {
   __shared__ float2 ys[kTileCols];
   __shared__ float2 yr[kTileRows];
   __shared__ float2 acc[kTileRows];
   __shared__ int claimed;
   const int xcd = static_cast<int>(blockIdx.x) % xcds;
-  const int slots = static_cast<int>(gridDim.x) / xcds;  // the grid is a whole number of slots per XCD
   const int per_xcd = (row_blocks + xcds - 1) / xcds;
   const int first = xcd * per_xcd;
   const int end = min(row_blocks, first + per_xcd);
   int slot = static_cast<int>(blockIdx.x) / xcds;
+  if (helper) {
+    if (threadIdx.x == 0) claimed = slots + static_cast<int>(atomicAdd(&work[xcd], 1u));
+    __syncthreads();
+    slot = claimed;
+    __syncthreads();
+  }
   while (first + slot < end) {
     attract_row_block<NT, D>(first + slot, ent, val, tile_ptr, tile_cb, tile_beg, y_cur, attr, exaggeration, n, ys, yr,
                           acc);
@@ -478,8 +488,8 @@ __global__ __launch_bounds__(NT, MINB) void k_attract_tiles_seg(
     slot = claimed;
     __syncthreads();  // every thread has read `claimed` before it is written again
   }
-  if (threadIdx.x == 0 && atomicAdd(&work[xcds], 1u) == gridDim.x - 1) {
-    // every other workgroup has made its last claim
+  if (threadIdx.x == 0 && atomicAdd(&work[xcds], 1u) == total - 1u) {
+    // every other workgroup (of both launches) has made its last claim
     for (int x = 0; x <= xcds; ++x) atomicExch(&work[x], 0u);
   }
 }
@@ -583,18 +593,41 @@ hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds,
-                                int slots_per_xcd, hipStream_t stream) {
-  if (t.work == nullptr || xcds < 1 || xcds > kTileMaxXcds) return hipErrorInvalidValue;
+namespace {
+
+// Workgroups per XCD of a primary launch.
+int primary_slots(const Tiles& t, int xcds, int slots_per_xcd) {
   const int per_xcd = (t.row_blocks + xcds - 1) / xcds;
-  const int slots = slots_per_xcd > 0 ? std::min(slots_per_xcd, per_xcd) : per_xcd;
-  const int blocks = std::max(slots, 1) * xcds;
+  return std::max(1, slots_per_xcd > 0 ? std::min(slots_per_xcd, per_xcd) : per_xcd);
+}
+
+hipError_t attract_launch(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds, int blocks,
+                          int slots, int helper, unsigned int total, hipStream_t stream) {
   constexpr int NT = kTileThreads;
   // a ring of 2 groups (one in flight while one is summed); deeper rings
   // measured no faster at config 2, and the LDS allows 3 workgroups per CU
   k_attract_tiles_seg<NT, 2, 3><<<blocks, NT, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur,
-                                                           attr, exaggeration, t.n, t.row_blocks, xcds, t.work);
+                                                           attr, exaggeration, t.n, t.row_blocks, xcds, t.work, slots,
+                                                           helper, total);
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds,
+                                int slots_per_xcd, int helper_per_xcd, hipStream_t stream) {
+  if (t.work == nullptr || xcds < 1 || xcds > kTileMaxXcds || helper_per_xcd < 0) return hipErrorInvalidValue;
+  const int slots = primary_slots(t, xcds, slots_per_xcd);
+  const unsigned int total = static_cast<unsigned int>((slots + helper_per_xcd) * xcds);
+  return attract_launch(t, y_cur, attr, exaggeration, xcds, slots * xcds, slots, 0, total, stream);
+}
+
+hipError_t launch_attract_tiled_helper(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration,
+                                       int xcds, int slots_per_xcd, int helper_per_xcd, hipStream_t stream) {
+  if (t.work == nullptr || xcds < 1 || xcds > kTileMaxXcds || helper_per_xcd < 1) return hipErrorInvalidValue;
+  const int slots = primary_slots(t, xcds, slots_per_xcd);
+  const unsigned int total = static_cast<unsigned int>((slots + helper_per_xcd) * xcds);
+  return attract_launch(t, y_cur, attr, exaggeration, xcds, helper_per_xcd * xcds, slots, 1, total, stream);
 }
 
 }  // namespace fehip

@@ -181,6 +181,16 @@ struct fastembedr_hip_tsne {
   // (FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU).  Alone it takes one workgroup
   // per row block.
   double attract_shared_per_cu = 1.0;
+  // Workgroups per CU of the helper launch that joins the attraction on the
+  // main stream once the repulsion chain is done, taking over the row blocks
+  // still unclaimed (FASTEMBEDR_HIP_ATTRACT_HELPER_PER_CU; 0: none).  The
+  // pair adapts to the balance of the two: a short chain leaves the helper
+  // most of the attraction, a long one leaves it nothing.
+  double attract_helper_per_cu = 1.0;
+  int helper_pending = 0;            // helper workgroups per XCD still to launch this iteration
+  int helper_slots = 0;              // the primary's workgroups per XCD
+  bool helper_span_open = false;     // the attraction's timed span ends after the helper
+  std::size_t helper_span = 0;
   int cus = 0;  // compute units of the device
   fehip::Tiles tiles;
   int tiles_for = -2;       // value of wi the tiles were built for; -2: none
@@ -208,7 +218,7 @@ struct fastembedr_hip_tsne {
   // is met (a one-off FFT length is not worth an instantiation); renumbering,
   // the attraction's tile build and timed runs stay eager.
   struct IterGraph {
-    std::array<std::uint32_t, 13> key{};
+    std::array<std::uint32_t, 14> key{};
     hipGraphExec_t exec = nullptr;
     int seen = 0;
     unsigned long long last_use = 0;
@@ -262,26 +272,34 @@ struct fastembedr_hip_tsne {
     }
   }
 
+  bool records(int kernel_id) const { return timing && (timed_only < 0 || timed_only == kernel_id); }
+
+  // Opens a timed span of kernel_id with an event on stream `on`; *slot names
+  // it for span_end (the end may be recorded on another stream).
+  bool span_begin(int kernel_id, hipStream_t on, std::size_t* slot) {
+    *slot = event_kernel.size();
+    while (events.size() < 2 * (*slot + 1)) {
+      hipEvent_t e;
+      if (!hip_ok(hipEventCreate(&e), "hipEventCreate")) return false;
+      events.push_back(e);
+    }
+    event_kernel.push_back(kernel_id);
+    return hip_ok(hipEventRecord(events[2 * *slot], on), "hipEventRecord");
+  }
+  bool span_end(std::size_t slot, hipStream_t on) {
+    return hip_ok(hipEventRecord(events[2 * slot + 1], on), "hipEventRecord");
+  }
+
   // Enqueues one kernel, bracketed by events on stream `on` (the main stream
   // by default) when timing is on.
   template <typename Launch>
   bool timed(int kernel_id, const char* what, Launch&& launch, hipStream_t on = nullptr) {
     if (on == nullptr) on = stream;
     std::size_t slot = 0;
-    const bool record = timing && (timed_only < 0 || timed_only == kernel_id);
-    if (record) {
-      slot = event_kernel.size();
-      while (events.size() < 2 * (slot + 1)) {
-        hipEvent_t e;
-        if (!hip_ok(hipEventCreate(&e), "hipEventCreate")) return false;
-        events.push_back(e);
-      }
-      event_kernel.push_back(kernel_id);
-      if (!hip_ok(hipEventRecord(events[2 * slot], on), "hipEventRecord")) return false;
-    }
+    const bool record = records(kernel_id);
+    if (record && !span_begin(kernel_id, on, &slot)) return false;
     if (!hip_ok(launch(), what)) return false;
-    if (record && !hip_ok(hipEventRecord(events[2 * slot + 1], on), "hipEventRecord")) return false;
-    return true;
+    return !record || span_end(slot, on);
   }
 
   bool sync_all() {
@@ -466,27 +484,61 @@ bool ensure_tiles(fastembedr_hip_tsne* s, hipStream_t st) {
   return true;
 }
 
+// Workgroups per XCD for `per_cu` workgroups per CU (at least one).
+int per_xcd_for(const fastembedr_hip_tsne* s, double per_cu) {
+  return std::max(1, static_cast<int>(std::lround(per_cu * std::max(1, s->cus / s->xcds))));
+}
+
 // Attractive term of every row into s->attr at the centred layout y_cur, on
-// stream st (the main stream when null); `shared`: other kernels run beside it.
+// stream st (the main stream when null); `shared`: other kernels run beside
+// it, and (tiled attraction) a helper launch follows on the main stream
+// (enqueue_attract_helper) once they are done.
 bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggeration, hipStream_t st = nullptr,
                      bool shared = false) {
   if (st == nullptr) st = s->stream;
-  const int slots = shared && s->cus > 0 && s->attract_shared_per_cu > 0.0
-                        ? std::max(1, static_cast<int>(std::lround(s->attract_shared_per_cu *
-                                                                   std::max(1, s->cus / s->xcds))))
-                        : 0;
+  s->helper_pending = 0;
+  s->helper_span_open = false;
+  const bool share = shared && s->cus > 0 && s->attract_shared_per_cu > 0.0;
+  const int slots = share ? per_xcd_for(s, s->attract_shared_per_cu) : 0;
   if (!s->attract_tiled) {
     return s->timed(
         fehip::kKAttract, "attract launch",
         [&] { return fehip::launch_attract(s->work_p(), y_cur, s->attr, exaggeration, s->lanes, s->xcds, st); }, st);
   }
   if (!ensure_tiles(s, st)) return false;
-  return s->timed(
-      fehip::kKAttract, "attract launch",
-      [&] {
-        return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->xcds, slots, st);
-      },
-      st);
+  const int helper = share && s->attract_helper_per_cu > 0.0 ? per_xcd_for(s, s->attract_helper_per_cu) : 0;
+  if (helper == 0) {
+    return s->timed(
+        fehip::kKAttract, "attract launch",
+        [&] { return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->xcds, slots, 0, st); },
+        st);
+  }
+  // the timed span runs from the primary's start to the point where the
+  // main stream has both (see enqueue_attract_helper)
+  if (s->records(fehip::kKAttract) && !s->span_begin(fehip::kKAttract, st, &s->helper_span)) return false;
+  s->helper_span_open = s->records(fehip::kKAttract);
+  s->helper_pending = helper;
+  s->helper_slots = slots;
+  return hip_ok(fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->xcds, slots, helper, st),
+                "attract launch");
+}
+
+// The helper launch of a shared tiled attraction, on the main stream, then
+// the main stream's wait for the primary (event done_attr on its stream).
+bool enqueue_attract_helper(fastembedr_hip_tsne* s, const float2* y_cur, float exaggeration, hipEvent_t done_attr) {
+  if (s->helper_pending > 0 &&
+      !hip_ok(fehip::launch_attract_tiled_helper(s->tiles, y_cur, s->attr, exaggeration, s->xcds, s->helper_slots,
+                                                 s->helper_pending, s->stream),
+              "attract helper launch")) {
+    return false;
+  }
+  s->helper_pending = 0;
+  if (!hip_ok(hipStreamWaitEvent(s->stream, done_attr, 0), "hipStreamWaitEvent(main, attraction)")) return false;
+  if (s->helper_span_open) {
+    s->helper_span_open = false;
+    return s->span_end(s->helper_span, s->stream);
+  }
+  return true;
 }
 
 // FFT length for an interpolation grid of `nodes` nodes per axis: the
@@ -674,7 +726,7 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
                   [&] { return fehip::launch_inverse_rows(s->gb, s->tw, n, s->sc, main); });
   }
   if (!ok) return false;
-  return !overlap || hip_ok(hipStreamWaitEvent(main, s->ev_attr, 0), "hipStreamWaitEvent(main, attraction)");
+  return !overlap || enqueue_attract_helper(s, s->y_a(), exaggeration, s->ev_attr);
 }
 
 // One optimisation iteration: the previous update's statistics finished
@@ -719,13 +771,14 @@ bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, con
     std::memcpy(&u, &v, sizeof(u));
     return u;
   };
-  const std::array<std::uint32_t, 13> key = {static_cast<std::uint32_t>(lg),
+  const std::array<std::uint32_t, 14> key = {static_cast<std::uint32_t>(lg),
                                              static_cast<std::uint32_t>(finalize),
                                              static_cast<std::uint32_t>(fft_len),
                                              static_cast<std::uint32_t>(s->si),
                                              static_cast<std::uint32_t>(s->wi),
                                              static_cast<std::uint32_t>(s->attract_tiled),
                                              static_cast<std::uint32_t>(std::lround(1000.0 * s->attract_shared_per_cu)),
+                                             static_cast<std::uint32_t>(std::lround(1000.0 * s->attract_helper_per_cu)),
                                              bits(up.exaggeration),
                                              bits(up.momentum),
                                              bits(up.learning_rate),
@@ -1175,10 +1228,14 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
     if (std::strcmp(tiled, "0") == 0) s->attract_tiled = false;
   }
 
-  if (const char* v = std::getenv("FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU")) {
-    char* end = nullptr;
-    const double d = std::strtod(v, &end);
-    if (end != v && std::isfinite(d) && d >= 0.0) s->attract_shared_per_cu = d;
+  for (auto [name, knob] : {std::pair<const char*, double*>{"FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU",
+                                                             &s->attract_shared_per_cu},
+                            {"FASTEMBEDR_HIP_ATTRACT_HELPER_PER_CU", &s->attract_helper_per_cu}}) {
+    if (const char* v = std::getenv(name)) {
+      char* end = nullptr;
+      const double d = std::strtod(v, &end);
+      if (end != v && std::isfinite(d) && d >= 0.0) *knob = d;
+    }
   }
   s->graph_capture = graph_capture_enabled();
   if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {

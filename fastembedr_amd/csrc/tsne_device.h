@@ -358,10 +358,14 @@ hipError_t tiles_temp_bytes(const Tiles& t, std::size_t& bytes);
 hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream);
 // Workgroups of kTileThreads.  slots_per_xcd: workgroups per XCD (<= 0: one
 // per row block); with fewer, each claims row blocks of its XCD's range until
-// none is left.  t.work must be zero (it is after a launch);
-// xcds <= kTileMaxXcds.
+// none is left.  helper_per_xcd > 0: a helper launch of that many workgroups
+// per XCD (launch_attract_tiled_helper, same arguments, enqueued later on
+// another stream) shares the claims and must follow.  t.work must be zero
+// (it is after a launch or a launch and its helper); xcds <= kTileMaxXcds.
 hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds,
-                                int slots_per_xcd, hipStream_t stream);
+                                int slots_per_xcd, int helper_per_xcd, hipStream_t stream);
+hipError_t launch_attract_tiled_helper(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration,
+                                       int xcds, int slots_per_xcd, int helper_per_xcd, hipStream_t stream);
 
 // ---- exact O(n^2) terms (gradient check and KL) ----------------------------
 hipError_t launch_exact_repulsion(const float2* y, int n, float2* rep, double* z_partial, DeviceScalars* sc,
