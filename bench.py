@@ -507,7 +507,7 @@ def one_shot_from_host(idx_r, dist_r, y0, sched, lr):
             "includes": "host->device KNN copy, P build, 750 iterations, device->host layout copy"}
 
 
-TRAFFIC_FILES = {"grid": ROOT / "profiles" / "tsne_loop_config2_traffic.json",
+TRAFFIC_FILES = {"grid": ROOT / "profiles" / "tsne_loop_config2_grid_traffic.json",
                  "interp": ROOT / "profiles" / "tsne_loop_config2_interp_traffic.json"}
 
 # Kernels of the repulsion step and their launches per iteration.
@@ -541,11 +541,14 @@ def measured_traffic(kernel: str, n: int, nnz: int, g: int, repulsion: str):
     if rec is None:
         return None
     # the timer's name is the kernel symbol's stem: "attract" is k_attract or
-    # the tiled k_attract_tiles_seg<NT>, "update" k_update<mode, grid>
-    for name, t in rec.get("kernels", {}).items():
-        if name.split("<")[0].startswith("k_" + kernel):
-            return int(t["fetch_bytes"] + t["write_bytes"])
-    return None
+    # the tiled k_attract_tiles_seg<...>, "update" k_update<mode, grid>.  The
+    # shared attraction is a pair of launches per iteration (the primary and
+    # the helper that joins it on the main stream, HELPER = true): their
+    # bytes per dispatch add up to the iteration's.
+    hits = [t for name, t in rec.get("kernels", {}).items() if name.split("<")[0].startswith("k_" + kernel)]
+    if not hits:
+        return None
+    return int(sum(t["fetch_bytes"] + t["write_bytes"] for t in hits))
 
 
 def repulsion_traffic(n: int, nnz: int, g: int, repulsion: str):

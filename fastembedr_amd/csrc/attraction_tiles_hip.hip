@@ -459,12 +459,14 @@ __device__ __forceinline__ void attract_row_block(int rb, const unsigned short* 
 // between them) resets work[] (its xcds + 1 counters start and end each
 // launch or pair at zero).  Launch bounds: MINB workgroups per CU (the VGPR
 // budget of the D-deep prefetch ring).
-template <int NT, int D, int MINB>
+// HELPER: a helper launch (its own symbol, so that profiles tell the two
+// launches of a pair apart).
+template <int NT, int D, int MINB, bool HELPER>
 __global__ __launch_bounds__(NT, MINB) void k_attract_tiles_seg(
     const unsigned short* __restrict__ ent, const float* __restrict__ val, const int* __restrict__ tile_ptr,
     const int* __restrict__ tile_cb, const int* __restrict__ tile_beg, const float2* __restrict__ y_cur,
     float2* __restrict__ attr, float exaggeration, int n, int row_blocks, int xcds, unsigned int* __restrict__ work,
-    int slots, int helper, unsigned int total) {
+    int slots, unsigned int total) {
   __shared__ float2 ys[kTileCols];
   __shared__ float2 yr[kTileRows];
   __shared__ float2 acc[kTileRows];
@@ -474,7 +476,7 @@ __global__ __launch_bounds__(NT, MINB) void k_attract_tiles_seg(
   const int first = xcd * per_xcd;
   const int end = min(row_blocks, first + per_xcd);
   int slot = static_cast<int>(blockIdx.x) / xcds;
-  if (helper) {
+  if (HELPER) {
     if (threadIdx.x == 0) claimed = slots + static_cast<int>(atomicAdd(&work[xcd], 1u));
     __syncthreads();
     slot = claimed;
@@ -606,9 +608,15 @@ hipError_t attract_launch(const Tiles& t, const float2* y_cur, float2* attr, flo
   constexpr int NT = kTileThreads;
   // a ring of 2 groups (one in flight while one is summed); deeper rings
   // measured no faster at config 2, and the LDS allows 3 workgroups per CU
-  k_attract_tiles_seg<NT, 2, 3><<<blocks, NT, 0, stream>>>(t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur,
-                                                           attr, exaggeration, t.n, t.row_blocks, xcds, t.work, slots,
-                                                           helper, total);
+  if (helper) {
+    k_attract_tiles_seg<NT, 2, 3, true><<<blocks, NT, 0, stream>>>(
+        t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr, exaggeration, t.n, t.row_blocks, xcds, t.work,
+        slots, total);
+  } else {
+    k_attract_tiles_seg<NT, 2, 3, false><<<blocks, NT, 0, stream>>>(
+        t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr, exaggeration, t.n, t.row_blocks, xcds, t.work,
+        slots, total);
+  }
   return hipGetLastError();
 }
 

@@ -1,7 +1,7 @@
 """Digest of rocprofv3 CSV output into the short text summaries kept under
 profiles/ (kernel durations and HBM traffic per dispatch).
 
-    python -m fastembedr_amd.rocprof_summary trace  <kt_dir>   <command> > profiles/<name>.txt
+    python -m fastembedr_amd.rocprof_summary trace  <kt_dir>   <command> [--last N] > profiles/<name>.txt
     python -m fastembedr_amd.rocprof_summary traffic <fetch_dir> <write_dir> <command> \
         --json profiles/<name>.json [--last N] > profiles/<name>.txt
     python -m fastembedr_amd.rocprof_summary counters <pmc_dir> <command> --names A,B [--last N]
@@ -55,9 +55,25 @@ def _stats_rows(kt_dir: str) -> list[tuple[str, int, float, float, float, float]
     return [(r[0], int(r[1]), float(r[2]), float(r[3]), float(r[4]), float(r[5])) for r in con.execute(q)]
 
 
-def trace(kt_dir: str) -> list[str]:
+def _last_rows(kt_dir: str, last: int) -> list[tuple[str, int, float, float, float, float]]:
+    """As _stats_rows, over each kernel's last `last` dispatches of the
+    per-dispatch kernel trace (CSV)."""
+    per = collections.defaultdict(list)
+    rows = list(csv.DictReader(open(_one(f"{kt_dir}/**/*kernel_trace.csv"))))
+    rows.sort(key=_dispatch_order)
+    for r in rows:
+        per[r["Kernel_Name"]].append(float(r["End_Timestamp"]) - float(r["Start_Timestamp"]))
+    out = []
+    for name, durs in per.items():
+        d = durs[-last:]
+        out.append((name, len(d), sum(d) / len(d), min(d), max(d), sum(d)))
+    out.sort(key=lambda r: -r[5])
+    return out
+
+
+def trace(kt_dir: str, last: int = 0) -> list[str]:
     out = [f"{'kernel':34s} {'calls':>6s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s} {'total_ms':>10s}"]
-    for name, calls, avg, mn, mx, tot in _stats_rows(kt_dir):
+    for name, calls, avg, mn, mx, tot in (_last_rows(kt_dir, last) if last > 0 else _stats_rows(kt_dir)):
         if not _OURS.search(name):
             continue
         out.append(f"{short_name(name):34s} {calls:6d} {avg / 1e3:10.2f} {mn / 1e3:10.2f} {mx / 1e3:10.2f} "
@@ -130,6 +146,7 @@ def main(argv=None) -> int:
     t = sub.add_parser("trace")
     t.add_argument("kt_dir")
     t.add_argument("command")
+    t.add_argument("--last", type=int, default=0, help="only each kernel's last N dispatches (per-dispatch trace)")
     c = sub.add_parser("traffic")
     c.add_argument("fetch_dir")
     c.add_argument("write_dir")
@@ -145,7 +162,9 @@ def main(argv=None) -> int:
     p.add_argument("--last", type=int, default=0, help="average only each kernel's last N dispatches")
     a = ap.parse_args(argv)
     if a.what == "trace":
-        lines = trace(a.kt_dir)
+        lines = trace(a.kt_dir, a.last)
+        if a.last:
+            lines.insert(0, f"(durations over each kernel's last {a.last} dispatches)")
     elif a.what == "counters":
         lines = counters(a.dir, a.names.split(","), a.last)
         if a.last:
