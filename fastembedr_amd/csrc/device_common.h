@@ -14,6 +14,13 @@ namespace {
 
 constexpr int kWave = 64;
 
+// Instruction-issue priority of the iteration's latency-bound chain
+// (statistics, binning, spreading, transforms, finalizes, update) over the
+// attraction that shares its CUs when the two overlap: s_setprio raises this
+// wave's priority in the CU's issue arbiter (0..3).  It does not touch queue
+// or stream priorities.
+__device__ __forceinline__ void chain_priority() { __builtin_amdgcn_s_setprio(3); }
+
 constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v / 2); }
 
 __device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }

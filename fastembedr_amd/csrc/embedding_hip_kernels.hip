@@ -118,6 +118,7 @@ __device__ void publish_stats(BlockStats local, BlockStats* partial) {
 __global__ __launch_bounds__(256) void k_finalize_stats(const BlockStats* __restrict__ partial, int blocks,
                                                         DeviceScalars* sc, int n, int g, int center,
                                                         unsigned long long* box_out) {
+  chain_priority();
   BlockStats acc = stats_identity();
   for (int b = threadIdx.x; b < blocks; b += 256) combine(acc, partial[b]);
   acc = block_stats<256>(acc);
@@ -332,6 +333,7 @@ __global__ __launch_bounds__(kPointThreads) void k_bin_count(const float2* __res
                                                              float2* __restrict__ y_cur, const DeviceScalars* sc,
                                                              int* __restrict__ tile_count, int n, int g, int ta) {
 #pragma clang fp contract(off)
+  chain_priority();
   __shared__ int hist[kMaxTiles];
   const int tiles = ta * ta;
   for (int t = threadIdx.x; t < tiles; t += kPointThreads) hist[t] = 0;
@@ -387,6 +389,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_bin_plan(int* __restrict__ til
                                                            int* __restrict__ tile_cursor, int4* __restrict__ items,
                                                            DeviceScalars* sc, int tiles,
                                                            int* __restrict__ tile_item0) {
+  chain_priority();
   __shared__ int part[kPlanThreads];
   if (tiles < 0) tiles = sc->lg_tiles_axis * sc->lg_tiles_axis;
   int cnt[kPlanPer], start[kPlanPer], chunks[kPlanPer], base[kPlanPer];
@@ -423,6 +426,7 @@ __global__ __launch_bounds__(kPointThreads) void k_bin_scatter(const float2* __r
                                                                const DeviceScalars* sc,
                                                                int* __restrict__ tile_cursor,
                                                                float2* __restrict__ binned, int n, int g, int ta) {
+  chain_priority();
   __shared__ int hist[kMaxTiles];
   __shared__ int base[kMaxTiles];
   const int tiles = ta * ta;
@@ -473,6 +477,7 @@ __global__ __launch_bounds__(kPointThreads) void k_spread_tiles(const float2* __
                                                                 float* __restrict__ mass_x,
                                                                 float* __restrict__ mass_y, int g, int ta) {
 #pragma clang fp contract(off)
+  chain_priority();
   constexpr int W = kTile + 1;
   constexpr int kCells = kTile * kTile;
   __shared__ float acc[3 * W * W];
@@ -609,6 +614,7 @@ __global__ __launch_bounds__(kPointThreads) void k_commit(float2* __restrict__ y
 template <int F>
 __global__ __launch_bounds__(256) void k_kernel_rows(const DeviceScalars* sc, const float2* __restrict__ tw,
                                                      float2* __restrict__ k_rows) {
+  chain_priority();
   using S = Shape<F>;
   __shared__ float2 lds[S::KROWS * F];
   __shared__ float2 tws[F];
@@ -645,6 +651,7 @@ __global__ __launch_bounds__(256) void k_kernel_rows(const DeviceScalars* sc, co
 template <int F>
 __global__ __launch_bounds__(256) void k_kernel_cols(const float2* __restrict__ k_rows,
                                                      const float2* __restrict__ tw, float2* __restrict__ k_hat) {
+  chain_priority();
   using S = Shape<F>;
   __shared__ float2 lds[S::KROWS * F];
   __shared__ float2 tws[F];
@@ -677,6 +684,7 @@ __global__ __launch_bounds__(256) void k_charge_rows(const float* __restrict__ m
                                                      const float* __restrict__ mass_y,
                                                      const float2* __restrict__ tw, float2* __restrict__ m_rows,
                                                      float2* __restrict__ mx_rows, float2* __restrict__ my_rows) {
+  chain_priority();
   using S = Shape<F>;
   __shared__ float2 lds[2 * S::CROWS * F];
   __shared__ float2 tws[F];
@@ -727,6 +735,7 @@ __global__ __launch_bounds__(256) void k_conv_cols(const float2* __restrict__ m_
                                                    const float2* __restrict__ tw, float2* __restrict__ x_rows,
                                                    float2* __restrict__ v1_rows, float2* __restrict__ v2_rows,
                                                    float2* __restrict__ y_rows) {
+  chain_priority();
   using S = Shape<F>;
   constexpr int C = S::CCOLS;
   __shared__ float2 lds[4 * C * F];
@@ -795,6 +804,7 @@ __global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__
                                                       float* __restrict__ mass_x, float* __restrict__ mass_y,
                                                       float4* __restrict__ field, double* __restrict__ partial,
                                                       int n, DeviceScalars* sc) {
+  chain_priority();
   using S = Shape<F>;
   __shared__ float2 lds[2 * S::CROWS * F];
   __shared__ float2 tws[F];
@@ -846,6 +856,7 @@ __global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__
 // sum_q and its fp32 reciprocal normaliser (src/tsne_neighbors.cpp:1160-1163).
 __global__ __launch_bounds__(256) void k_finalize_sumq(const double* __restrict__ partial, int blocks, int n,
                                                        DeviceScalars* sc) {
+  chain_priority();
   double tot = 0.0;
   for (int b = threadIdx.x; b < blocks; b += 256) tot += partial[b];
   tot = block_sum<256>(tot);
@@ -945,6 +956,7 @@ __global__ __launch_bounds__(kPointThreads) void k_update(const float2* __restri
                                                           BlockStats* __restrict__ partial, DeviceScalars* sc,
                                                           int n) {
 #pragma clang fp contract(off)
+  chain_priority();
   const DeviceScalars s = *sc;
   BlockStats st = stats_identity();
   const float inv_exact = (MODE == kModeGradientExact)

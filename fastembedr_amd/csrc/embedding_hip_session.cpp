@@ -176,17 +176,26 @@ struct fastembedr_hip_tsne {
   // tiles follow the working numbering and are rebuilt after it changes.
   bool attract_tiled = true;
   // Workgroups per CU of the attraction when it runs beside the repulsion
-  // kernels (side stream), possibly fractional: fewer than the 3 its LDS
-  // allows leave room on every CU for the latency-bound repulsion chain
-  // (FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU).  Alone it takes one workgroup
-  // per row block.
-  double attract_shared_per_cu = 1.0;
+  // kernels, possibly fractional: fewer than the 3 its LDS allows leave room
+  // on every CU for the latency-bound repulsion chain, whose waves also take
+  // issue priority (chain_priority) (FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU;
+  // config 2, late window, interleaved repeats: 1 per CU 3074 it/s, 1.5
+  // 3164, 2 3270, 3 2891).  Alone it takes one workgroup per row block.
+  double attract_shared_per_cu = 2.0;
   // Workgroups per CU of the helper launch that joins the attraction on the
   // main stream once the repulsion chain is done, taking over the row blocks
   // still unclaimed (FASTEMBEDR_HIP_ATTRACT_HELPER_PER_CU; 0: none).  The
   // pair adapts to the balance of the two: a short chain leaves the helper
   // most of the attraction, a long one leaves it nothing.
   double attract_helper_per_cu = 1.0;
+  // The attraction on the main stream and the repulsion chain on side_attr
+  // (the default; FASTEMBEDR_HIP_ATTRACT_MAIN=0: the attraction on side_attr
+  // with a helper launch on the main stream after the chain); the attraction
+  // then takes attract_shared_per_cu workgroups per CU and no helper.  At
+  // config 2 the chain ends last, so the update follows the chain's event
+  // (3270 against 3205 it/s in the late window, 3409 against 3340 over the
+  // whole schedule).
+  bool attract_main = true;
   int helper_pending = 0;            // helper workgroups per XCD still to launch this iteration
   int helper_slots = 0;              // the primary's workgroups per XCD
   bool helper_span_open = false;     // the attraction's timed span ends after the helper
@@ -506,7 +515,8 @@ bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggera
         [&] { return fehip::launch_attract(s->work_p(), y_cur, s->attr, exaggeration, s->lanes, s->xcds, st); }, st);
   }
   if (!ensure_tiles(s, st)) return false;
-  const int helper = share && s->attract_helper_per_cu > 0.0 ? per_xcd_for(s, s->attract_helper_per_cu) : 0;
+  const int helper =
+      share && !s->attract_main && s->attract_helper_per_cu > 0.0 ? per_xcd_for(s, s->attract_helper_per_cu) : 0;
   if (helper == 0) {
     return s->timed(
         fehip::kKAttract, "attract launch",
@@ -634,18 +644,29 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   const int n = s->n;
   fehip::InterpBuffers& ib = s->ib;
   hipStream_t main = s->stream;
-  hipStream_t sa = overlap ? s->side_attr : main;
+  // Two arrangements of an overlapped iteration.  Attraction beside (the
+  // default): the attraction runs on side_attr from the top of the
+  // iteration, the repulsion chain on the main stream, and a helper launch
+  // joins the attraction once the chain is done.  Attraction on main
+  // (attract_main): the chain runs on side_attr and the attraction on the
+  // main stream after the statistics' finish, so that whichever of the two
+  // ends last, the update follows it on its own stream when that is the
+  // attraction.
+  const bool swap = overlap && s->attract_main;
+  hipStream_t sa = overlap && !swap ? s->side_attr : main;  // attraction
+  hipStream_t chain = swap ? s->side_attr : main;           // repulsion chain
   hipStream_t sk = overlap ? s->side_kern : main;
   if (lg) s->lg_last_fft = fft_len;
   // The attraction needs only differences y_i - y_j, so it reads the stored
   // layout (no centring) and starts at once, beside the statistics' finish
   // and the whole repulsion chain.
-  if (overlap && (!hip_ok(hipEventRecord(s->ev_layout, main), "hipEventRecord(layout)") ||
-                  !hip_ok(hipStreamWaitEvent(sa, s->ev_layout, 0), "hipStreamWaitEvent(attraction)"))) {
+  if (overlap && !swap &&
+      (!hip_ok(hipEventRecord(s->ev_layout, main), "hipEventRecord(layout)") ||
+       !hip_ok(hipStreamWaitEvent(sa, s->ev_layout, 0), "hipStreamWaitEvent(attraction)"))) {
     return false;
   }
-  if (!enqueue_attract(s, s->y_a(), exaggeration, sa, overlap) ||
-      (overlap && !hip_ok(hipEventRecord(s->ev_attr, sa), "hipEventRecord(attraction)"))) {
+  if (!swap && (!enqueue_attract(s, s->y_a(), exaggeration, sa, overlap) ||
+                (overlap && !hip_ok(hipEventRecord(s->ev_attr, sa), "hipEventRecord(attraction)")))) {
     return false;
   }
   if (finalize && !s->timed(fehip::kKFinalize, "finalize launch", [&] {
@@ -655,9 +676,11 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   }
   // The kernel spectrum needs only the node spacing of the geometry.
   if (overlap && (!hip_ok(hipEventRecord(s->ev_ready, main), "hipEventRecord(ready)") ||
-                  !hip_ok(hipStreamWaitEvent(sk, s->ev_ready, 0), "hipStreamWaitEvent(kernel)"))) {
+                  !hip_ok(hipStreamWaitEvent(sk, s->ev_ready, 0), "hipStreamWaitEvent(kernel)") ||
+                  (swap && !hip_ok(hipStreamWaitEvent(chain, s->ev_ready, 0), "hipStreamWaitEvent(chain)")))) {
     return false;
   }
+  if (swap && !enqueue_attract(s, s->y_a(), exaggeration, main, true)) return false;
   if (lg) {
     static constexpr int kIds[3] = {fehip::kKLgKernelRows, fehip::kKLgKernelT, fehip::kKLgKernelCols};
     for (int which = 0; which < 3; ++which) {
@@ -676,56 +699,82 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
     return false;
   }
   if (overlap && !hip_ok(hipEventRecord(s->ev_kern, sk), "hipEventRecord(kernel)")) return false;
-  // main: centre + count
+  // chain: centre + count
   if (lg) {
-    if (!s->timed(fehip::kKLgBinCount, "interp bin_count launch",
-                  [&] { return fehip::launch_interp_bin_count(s->y_a(), s->y_b, s->sc, ib, n, main); })) {
+    if (!s->timed(
+            fehip::kKLgBinCount, "interp bin_count launch",
+            [&] { return fehip::launch_interp_bin_count(s->y_a(), s->y_b, s->sc, ib, n, chain); }, chain)) {
       return false;
     }
-  } else if (!s->timed(fehip::kKBinCount, "bin_count launch",
-                       [&] { return fehip::launch_bin_count(s->y_a(), s->y_b, s->sc, s->gb, n, main); })) {
+  } else if (!s->timed(
+                 fehip::kKBinCount, "bin_count launch",
+                 [&] { return fehip::launch_bin_count(s->y_a(), s->y_b, s->sc, s->gb, n, chain); }, chain)) {
     return false;
   }
-  // main: bins, spread, charge transforms
+  // chain: bins, spread, charge transforms
   bool ok;
   if (lg) {
-    ok = s->timed(fehip::kKLgBinPlan, "interp bin_plan launch",
-                  [&] { return fehip::launch_interp_bin_plan(ib, s->sc, main); }) &&
-         s->timed(fehip::kKLgBinScatter, "interp bin_scatter launch",
-                  [&] { return fehip::launch_interp_bin_scatter(s->y_b, s->sc, ib, n, fft_len, main); }) &&
-         s->timed(fehip::kKLgSpread, "interp spread launch",
-                  [&] { return fehip::launch_interp_spread(s->sc, ib, n, fft_len, main); }) &&
-         s->timed(fehip::kKLgGather, "interp gather launch",
-                  [&] { return fehip::launch_interp_gather(s->sc, ib, main); }) &&
-         s->timed(fehip::kKLgChargeRows, "interp charge_rows launch",
-                  [&] { return fehip::launch_interp_fft(3, fft_len, ib, s->sc, s->tw, n, main); }) &&
-         s->timed(fehip::kKLgChargeT, "interp charge transpose launch",
-                  [&] { return fehip::launch_interp_fft(4, fft_len, ib, s->sc, s->tw, n, main); });
+    ok = s->timed(
+             fehip::kKLgBinPlan, "interp bin_plan launch",
+             [&] { return fehip::launch_interp_bin_plan(ib, s->sc, chain); }, chain) &&
+         s->timed(
+             fehip::kKLgBinScatter, "interp bin_scatter launch",
+             [&] { return fehip::launch_interp_bin_scatter(s->y_b, s->sc, ib, n, fft_len, chain); }, chain) &&
+         s->timed(
+             fehip::kKLgSpread, "interp spread launch",
+             [&] { return fehip::launch_interp_spread(s->sc, ib, n, fft_len, chain); }, chain) &&
+         s->timed(
+             fehip::kKLgGather, "interp gather launch",
+             [&] { return fehip::launch_interp_gather(s->sc, ib, chain); }, chain) &&
+         s->timed(
+             fehip::kKLgChargeRows, "interp charge_rows launch",
+             [&] { return fehip::launch_interp_fft(3, fft_len, ib, s->sc, s->tw, n, chain); }, chain) &&
+         s->timed(
+             fehip::kKLgChargeT, "interp charge transpose launch",
+             [&] { return fehip::launch_interp_fft(4, fft_len, ib, s->sc, s->tw, n, chain); }, chain);
   } else {
-    ok = s->timed(fehip::kKBinPlan, "bin_plan launch", [&] { return fehip::launch_bin_plan(s->gb, s->sc, main); }) &&
-         s->timed(fehip::kKBinScatter, "bin_scatter launch",
-                  [&] { return fehip::launch_bin_scatter(s->y_b, s->sc, s->gb, n, main); }) &&
-         s->timed(fehip::kKSpread, "spread launch",
-                  [&] { return fehip::launch_spread_tiles(s->sc, s->gb, n, main); }) &&
-         s->timed(fehip::kKChargeRows, "charge_rows launch",
-                  [&] { return fehip::launch_charge_rows(s->gb, s->tw, main); });
+    ok = s->timed(
+             fehip::kKBinPlan, "bin_plan launch", [&] { return fehip::launch_bin_plan(s->gb, s->sc, chain); },
+             chain) &&
+         s->timed(
+             fehip::kKBinScatter, "bin_scatter launch",
+             [&] { return fehip::launch_bin_scatter(s->y_b, s->sc, s->gb, n, chain); }, chain) &&
+         s->timed(
+             fehip::kKSpread, "spread launch", [&] { return fehip::launch_spread_tiles(s->sc, s->gb, n, chain); },
+             chain) &&
+         s->timed(
+             fehip::kKChargeRows, "charge_rows launch",
+             [&] { return fehip::launch_charge_rows(s->gb, s->tw, chain); }, chain);
   }
   if (!ok) return false;
-  if (overlap && !hip_ok(hipStreamWaitEvent(main, s->ev_kern, 0), "hipStreamWaitEvent(main, kernel)")) return false;
-  // main: convolution and potentials
+  if (overlap && !hip_ok(hipStreamWaitEvent(chain, s->ev_kern, 0), "hipStreamWaitEvent(chain, kernel)")) {
+    return false;
+  }
+  // chain: convolution and potentials
   if (lg) {
-    ok = s->timed(fehip::kKLgConvCols, "interp conv_cols launch",
-                  [&] { return fehip::launch_interp_fft(5, fft_len, ib, s->sc, s->tw, n, main); }) &&
-         s->timed(fehip::kKLgPotentialT, "interp potential transpose launch",
-                  [&] { return fehip::launch_interp_fft(6, fft_len, ib, s->sc, s->tw, n, main); }) &&
-         s->timed(fehip::kKLgInverseRows, "interp inverse_rows launch",
-                  [&] { return fehip::launch_interp_fft(7, fft_len, ib, s->sc, s->tw, n, main); });
+    ok = s->timed(
+             fehip::kKLgConvCols, "interp conv_cols launch",
+             [&] { return fehip::launch_interp_fft(5, fft_len, ib, s->sc, s->tw, n, chain); }, chain) &&
+         s->timed(
+             fehip::kKLgPotentialT, "interp potential transpose launch",
+             [&] { return fehip::launch_interp_fft(6, fft_len, ib, s->sc, s->tw, n, chain); }, chain) &&
+         s->timed(
+             fehip::kKLgInverseRows, "interp inverse_rows launch",
+             [&] { return fehip::launch_interp_fft(7, fft_len, ib, s->sc, s->tw, n, chain); }, chain);
   } else {
-    ok = s->timed(fehip::kKConvCols, "conv_cols launch", [&] { return fehip::launch_conv_cols(s->gb, s->tw, main); }) &&
-         s->timed(fehip::kKInverseRows, "inverse_rows launch",
-                  [&] { return fehip::launch_inverse_rows(s->gb, s->tw, n, s->sc, main); });
+    ok = s->timed(
+             fehip::kKConvCols, "conv_cols launch", [&] { return fehip::launch_conv_cols(s->gb, s->tw, chain); },
+             chain) &&
+         s->timed(
+             fehip::kKInverseRows, "inverse_rows launch",
+             [&] { return fehip::launch_inverse_rows(s->gb, s->tw, n, s->sc, chain); }, chain);
   }
   if (!ok) return false;
+  if (swap) {
+    // the main stream (attraction) waits for the chain
+    return hip_ok(hipEventRecord(s->ev_attr, chain), "hipEventRecord(chain)") &&
+           hip_ok(hipStreamWaitEvent(main, s->ev_attr, 0), "hipStreamWaitEvent(main, chain)");
+  }
   return !overlap || enqueue_attract_helper(s, s->y_a(), exaggeration, s->ev_attr);
 }
 
@@ -1237,6 +1286,7 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
       if (end != v && std::isfinite(d) && d >= 0.0) *knob = d;
     }
   }
+  if (const char* v = std::getenv("FASTEMBEDR_HIP_ATTRACT_MAIN")) s->attract_main = std::strcmp(v, "0") != 0;
   s->graph_capture = graph_capture_enabled();
   if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {
     delete s;

@@ -94,6 +94,7 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_bin_count(const float2* __res
                                                              float2* __restrict__ y_cur, const DeviceScalars* sc,
                                                              int* __restrict__ tile_count, int n) {
 #pragma clang fp contract(off)
+  chain_priority();
   __shared__ int hist[kMaxTiles];
   const DeviceScalars s = *sc;
   const int ta = s.lg_tiles_axis;
@@ -125,6 +126,7 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_bin_scatter(const float2* __r
                                                                DeviceScalars* sc,
                                                                int* __restrict__ tile_cursor,
                                                                float2* __restrict__ binned, int n, int tiles_cap) {
+  chain_priority();
   extern __shared__ int hist[];  // counts, then base offsets
   const DeviceScalars s = *sc;
   const int ta = s.lg_tiles_axis;
@@ -239,6 +241,7 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
                                                           float* __restrict__ charge, float* __restrict__ windows,
                                                           int acc_cap) {
 #pragma clang fp contract(off)
+  chain_priority();
   extern __shared__ float acc[];  // [charge][node of the window], acc_cap floats
   __shared__ int box_start[kLgBoxesPerTile];
   __shared__ int part[kLgThreads];
@@ -363,6 +366,7 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
 __global__ __launch_bounds__(kLgThreads) void k_lg_gather(const int* __restrict__ tile_item0,
                                                           const float* __restrict__ windows, const DeviceScalars* sc,
                                                           float* __restrict__ charge) {
+  chain_priority();
   __shared__ float part[kLgThreads];
   const int m = sc->lg_nodes;
   const int ta = sc->lg_tiles_axis;
@@ -445,6 +449,7 @@ __global__ __launch_bounds__(256) void k_lg_transpose(const float2* __restrict__
                                                       float2* __restrict__ dst, long long dst_plane, int ld_d,
                                                       int rows_cap, int m_rows, int cols_cap, int m_cols,
                                                       const DeviceScalars* sc) {
+  chain_priority();
   __shared__ float2 tile[32][33];
   const int m = sc->lg_nodes;
   const int rows = m_rows ? min(m, rows_cap) : rows_cap;
@@ -481,6 +486,7 @@ template <int F>
 __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_rows(const DeviceScalars* sc,
                                                                    const float2* __restrict__ tw,
                                                                    float2* __restrict__ k_rows) {
+  chain_priority();
   using S = LgShape<F>;
   constexpr int HH = S::H * S::H;
   __shared__ float2 lds[2 * S::KR * F];
@@ -527,6 +533,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_cols(const DeviceS
                                                                    const float2* __restrict__ k_cols,
                                                                    const float2* __restrict__ tw,
                                                                    float2* __restrict__ k_hat) {
+  chain_priority();
   using S = LgShape<F>;
   constexpr int HH = S::H * S::H;
   __shared__ float2 lds[2 * S::KR * F];
@@ -573,6 +580,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
                                                                    const float* __restrict__ charge,
                                                                    const float2* __restrict__ tw,
                                                                    float2* __restrict__ rows, long long plane) {
+  chain_priority();
   using S = LgShape<F>;
   __shared__ float2 lds[2 * S::CR * F];
   __shared__ float2 tws[F];
@@ -627,6 +635,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
                                                                  const float2* __restrict__ tw,
                                                                  float2* __restrict__ cols_out, long long plane,
                                                                  double* __restrict__ zpart) {
+  chain_priority();
   using S = LgShape<F>;
   constexpr int C = S::CC;
   constexpr int HH = S::H * S::H;
@@ -713,6 +722,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_inverse_rows(const Device
                                                                     const float2* __restrict__ tw,
                                                                     float4* __restrict__ field,
                                                                     double* __restrict__ partial) {
+  chain_priority();
   using S = LgShape<F>;
   __shared__ float2 lds[2 * S::CR * F];
   __shared__ float2 tws[F];
@@ -767,6 +777,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_inverse_rows(const Device
 __global__ __launch_bounds__(256) void k_lg_finalize_z(const double* __restrict__ spec_part, int spec_blocks,
                                                        const double* __restrict__ row_part, int row_blocks, int n,
                                                        int fft_len, DeviceScalars* sc) {
+  chain_priority();
   double s1 = 0.0, s3 = 0.0, s4 = 0.0, t2 = 0.0;
   for (int b = threadIdx.x; b < spec_blocks; b += 256) {
     s1 += spec_part[3 * b];

@@ -20,7 +20,11 @@ interpolation grid):
   * with a growing span (the interpolation grid's FFT length changes between
     graph keys, and the host learns box counts from the device-indexed ring)
     the final KL agrees within 0.5 %;
-  * the switch's off values turn capture off.
+  * the switch's off values turn capture off;
+  * both arrangements of the overlapped iteration (the attraction on the
+    main stream with the chain beside it, the default, and the attraction
+    beside the chain with a helper launch, FASTEMBEDR_HIP_ATTRACT_MAIN=0),
+    replayed, end within 0.5 % of the eager run's KL.
 """
 
 import os
@@ -48,24 +52,27 @@ def prob():
     return x, idx, dist, synthetic.pca_init(x)
 
 
-def _session(hip, idx, dist, capture):
-    old = os.environ.get(ENV)
-    if capture is None:
-        os.environ.pop(ENV, None)
-    else:
-        os.environ[ENV] = capture
+def _session(hip, idx, dist, capture, extra=None):
+    settings = {ENV: capture, **(extra or {})}
+    old = {k: os.environ.get(k) for k in settings}
+    for k, v in settings.items():
+        if v is None:
+            os.environ.pop(k, None)
+        else:
+            os.environ[k] = v
     try:
         return hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1)
     finally:
-        if old is None:
-            os.environ.pop(ENV, None)
-        else:
-            os.environ[ENV] = old
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
 
 
-def _schedule(hip, idx, dist, y0, repulsion, capture, early, normal):
+def _schedule(hip, idx, dist, y0, repulsion, capture, early, normal, extra=None):
     n = y0.shape[0]
-    with _session(hip, idx, dist, capture) as s:
+    with _session(hip, idx, dist, capture, extra) as s:
         if repulsion == _lib.REPULSION_LAGRANGE:
             s.set_repulsion(repulsion, 3, 50, 1.0)
         s.set_state(y0)
@@ -116,6 +123,19 @@ def test_replayed_schedule_kl(hip, prob, repulsion):
     assert not info_e["enabled"] and info_e["launches"] == 0
     assert info_g["enabled"] and info_g["launches"] >= 100, info_g
     assert np.all(np.isfinite(y_g))
+    assert abs(kl_g - kl_e) <= 0.005 * kl_e
+
+
+@pytest.mark.parametrize("arrangement", ["1", "0"], ids=["attraction_main", "attraction_beside"])
+def test_overlap_arrangements_kl(hip, prob, arrangement):
+    x, idx, dist, y0 = prob
+    extra = {"FASTEMBEDR_HIP_ATTRACT_MAIN": arrangement}
+    _say(f"case: FASTEMBEDR_HIP_ATTRACT_MAIN={arrangement}, replayed vs eager, interpolation grid, 60 + 60 iterations")
+    _, y_e, kl_e, _ = _schedule(hip, idx, dist, y0, _lib.REPULSION_LAGRANGE, "0", 60, 60, extra)
+    _, y_g, kl_g, info = _schedule(hip, idx, dist, y0, _lib.REPULSION_LAGRANGE, None, 60, 60, extra)
+    _say(f"  KL eager {kl_e:.5f}, graph {kl_g:.5f}, {info}")
+    assert info["launches"] >= 100, info
+    assert np.all(np.isfinite(y_g)) and np.all(np.isfinite(y_e))
     assert abs(kl_g - kl_e) <= 0.005 * kl_e
 
 
