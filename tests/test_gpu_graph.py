@@ -16,15 +16,16 @@ interpolation grid):
     relative L2 <= max(5e-5, 4 x (eager vs eager)) (the bilinear spreading's
     LDS float atomics alone give about 1.6e-5);
   * 60 + 60 iterations, most replayed (graph_info), end at an exact KL within
-    0.5 % of the eager run's;
+    1 % of the eager run's (independent eager runs of this problem spread
+    over 0.8 % of KL: 2.8119 to 2.8343 in 16 runs on MI355X);
   * with a growing span (the interpolation grid's FFT length changes between
     graph keys, and the host learns box counts from the device-indexed ring)
-    the final KL agrees within 0.5 %;
+    the final KL agrees within 1 %;
   * the switch's off values turn capture off;
   * both arrangements of the overlapped iteration (the attraction on the
     main stream with the chain beside it, the default, and the attraction
     beside the chain with a helper launch, FASTEMBEDR_HIP_ATTRACT_MAIN=0),
-    replayed, end within 0.5 % of the eager run's KL.
+    replayed, end within 1 % of the eager run's KL.
 """
 
 import os
@@ -39,6 +40,7 @@ from tests.helpers import rel_l2, small_problem
 pytestmark = pytest.mark.gpu
 
 ENV = "FASTEMBEDR_HIP_GRAPH_CAPTURE"
+KL_TOL = 0.01
 
 
 def _say(msg):
@@ -123,7 +125,7 @@ def test_replayed_schedule_kl(hip, prob, repulsion):
     assert not info_e["enabled"] and info_e["launches"] == 0
     assert info_g["enabled"] and info_g["launches"] >= 100, info_g
     assert np.all(np.isfinite(y_g))
-    assert abs(kl_g - kl_e) <= 0.005 * kl_e
+    assert abs(kl_g - kl_e) <= KL_TOL * kl_e
 
 
 @pytest.mark.parametrize("arrangement", ["1", "0"], ids=["attraction_main", "attraction_beside"])
@@ -136,7 +138,7 @@ def test_overlap_arrangements_kl(hip, prob, arrangement):
     _say(f"  KL eager {kl_e:.5f}, graph {kl_g:.5f}, {info}")
     assert info["launches"] >= 100, info
     assert np.all(np.isfinite(y_g)) and np.all(np.isfinite(y_e))
-    assert abs(kl_g - kl_e) <= 0.005 * kl_e
+    assert abs(kl_g - kl_e) <= KL_TOL * kl_e
 
 
 def test_replayed_growing_span_kl(hip, prob):
@@ -150,7 +152,7 @@ def test_replayed_growing_span_kl(hip, prob):
     _say(f"  KL eager {kl_e:.5f}, graph {kl_g:.5f}, {info}")
     assert info["launches"] >= 250, info
     assert np.all(np.isfinite(y_g))
-    assert abs(kl_g - kl_e) <= 0.005 * kl_e
+    assert abs(kl_g - kl_e) <= KL_TOL * kl_e
 
 
 @pytest.mark.parametrize("value,enabled", [("0", False), ("false", False), ("FALSE", False), ("no", False),
