@@ -234,6 +234,7 @@ struct fastembedr_hip_tsne {
   };
   static constexpr std::size_t kMaxGraphs = 8;
   bool graph_capture = true;
+  bool capturing = false;   // an iteration is being captured (enqueue_gradient_pieces' arrangement)
   std::vector<IterGraph> graphs;
   unsigned long long graph_clock = 0;
   long long graph_launches = 0;
@@ -669,15 +670,31 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
                 (overlap && !hip_ok(hipEventRecord(s->ev_attr, sa), "hipEventRecord(attraction)")))) {
     return false;
   }
-  if (finalize && !s->timed(fehip::kKFinalize, "finalize launch", [&] {
-        return fehip::launch_finalize_stats(s->partial, n, s->gb.g, s->sc, lg ? s->lg_ring_dev : nullptr, main);
-      })) {
+  // With the attraction on the main stream, the statistics' finish heads the
+  // chain's stream when launched eagerly, so the attraction starts right
+  // after the previous update (config 2, late window: 3298 -> 3392 it/s).  A
+  // captured iteration keeps it at the head of the main stream: with two
+  // root branches its replays measured 17 % slower (3396 -> 2820 it/s over
+  // the whole schedule).
+  const bool fin_chain = swap && !s->capturing;
+  hipStream_t fin = fin_chain ? chain : main;
+  if (fin_chain && (!hip_ok(hipEventRecord(s->ev_layout, main), "hipEventRecord(layout)") ||
+               !hip_ok(hipStreamWaitEvent(chain, s->ev_layout, 0), "hipStreamWaitEvent(chain)"))) {
+    return false;
+  }
+  if (finalize && !s->timed(
+                      fehip::kKFinalize, "finalize launch",
+                      [&] {
+                        return fehip::launch_finalize_stats(s->partial, n, s->gb.g, s->sc,
+                                                            lg ? s->lg_ring_dev : nullptr, fin);
+                      },
+                      fin)) {
     return false;
   }
   // The kernel spectrum needs only the node spacing of the geometry.
-  if (overlap && (!hip_ok(hipEventRecord(s->ev_ready, main), "hipEventRecord(ready)") ||
+  if (overlap && (!hip_ok(hipEventRecord(s->ev_ready, fin), "hipEventRecord(ready)") ||
                   !hip_ok(hipStreamWaitEvent(sk, s->ev_ready, 0), "hipStreamWaitEvent(kernel)") ||
-                  (swap && !hip_ok(hipStreamWaitEvent(chain, s->ev_ready, 0), "hipStreamWaitEvent(chain)")))) {
+                  (swap && !fin_chain && !hip_ok(hipStreamWaitEvent(chain, s->ev_ready, 0), "hipStreamWaitEvent(chain)")))) {
     return false;
   }
   if (swap && !enqueue_attract(s, s->y_a(), exaggeration, main, true)) return false;
@@ -798,7 +815,9 @@ bool capture_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip
   if (!hip_ok(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture")) {
     return false;
   }
+  s->capturing = true;
   const bool enqueued = enqueue_iteration(s, lg, fft_len, up, overlap, finalize);
+  s->capturing = false;
   hipGraph_t graph = nullptr;
   const hipError_t ended = hipStreamEndCapture(s->stream, &graph);
   bool ok = enqueued && hip_ok(ended, "hipStreamEndCapture") && graph != nullptr;
