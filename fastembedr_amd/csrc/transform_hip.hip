@@ -40,6 +40,7 @@
 #include <mutex>
 #include <random>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "fastembedr_hip.h"
@@ -418,6 +419,137 @@ __global__ __launch_bounds__(kRunThreads) void k_transform_run(
   if (exact_evals != 0ull) atomicAdd(exact_count, exact_evals);
 }
 
+// Grid mode with L lanes per query (L a power of two dividing the wave): the
+// query's neighbours are dealt round-robin to its lanes, which load their
+// reference positions and p once, keep them in registers for the whole
+// schedule, and sum their part of the attraction; the parts are added by a
+// butterfly over the group (the same value in every lane).  The grid
+// repulsion's 9 nodes are split over the lanes the same way; the update (and
+// the rare exact sums of a query outside the grid) are computed by every
+// lane of the group from the same inputs, so the lanes keep identical
+// states.  L lanes per query put
+// L times as many waves in flight as k_transform_run, which waits on the
+// neighbours' positions every iteration.  The attraction is summed in
+// another order than the reference's (per lane, then across lanes).
+constexpr int kLaneThreads = 256;
+
+template <int L>
+__device__ __forceinline__ double group_sum(double v) {
+#pragma unroll
+  for (int off = 1; off < L; off <<= 1) v += __shfl_xor(v, off, L);
+  return v;
+}
+
+// grid_repulsion with the 3 x 3 nodes dealt to the group's L lanes (node
+// a = lane, lane + L, ...) and their weighted fields added by group_sum.
+template <int L>
+__device__ inline bool grid_repulsion_lanes(const double4* __restrict__ field, const GridGeo& g, double yx, double yy,
+                                            int lane, double* gx, double* gy) {
+#pragma clang fp contract(off)
+  const double ux = (yx - g.lo) / g.w;
+  const double uy = (yy - g.lo) / g.w;
+  const double fx0 = floor(ux);
+  const double fy0 = floor(uy);
+  if (!(fx0 >= 0.0 && fx0 < static_cast<double>(g.nb) && fy0 >= 0.0 && fy0 < static_cast<double>(g.nb))) {
+    return false;
+  }
+  const int bx = static_cast<int>(fx0);
+  const int by = static_cast<int>(fy0);
+  double wx[3], wy[3];
+  grid_weights(ux - fx0, wx);
+  grid_weights(uy - fy0, wy);
+  double z = 0.0, fx = 0.0, fy = 0.0;
+#pragma unroll
+  for (int a0 = 0; a0 < kGridOrder * kGridOrder; a0 += L) {
+    const int a = a0 + lane;
+    if (a < kGridOrder * kGridOrder) {
+      const int sb = a / kGridOrder;
+      const int sa = a - sb * kGridOrder;
+      const double wgt = wx[sa] * wy[sb];
+      const double4 f = field[static_cast<std::size_t>(by * kGridOrder + sb) * static_cast<std::size_t>(g.m) +
+                              static_cast<std::size_t>(bx * kGridOrder + sa)];
+      z += wgt * f.x;
+      fx += wgt * f.y;
+      fy += wgt * f.z;
+    }
+  }
+  z = group_sum<L>(z);
+  fx = group_sum<L>(fx);
+  fy = group_sum<L>(fy);
+  if (!(z > 0.0)) return false;
+  const double inv = 1.0 / z;
+  *gx = -fx * inv;
+  *gy = -fy * inv;
+  return true;
+}
+
+template <int L, int MAXJ>
+__global__ __launch_bounds__(kLaneThreads) void k_transform_grid_lanes(
+    const double2* __restrict__ ref, int n_ref, const int* __restrict__ idx_cm, const double* __restrict__ p_cm,
+    int nq, int k, int offset, RunSchedule rs, const double4* __restrict__ field, GridGeo g,
+    double2* __restrict__ y, unsigned long long* __restrict__ exact_count) {
+#pragma clang fp contract(off)
+  static_assert(L >= 1 && L <= 64 && (L & (L - 1)) == 0, "a power-of-two group within the wave");
+  const int gid = static_cast<int>(blockIdx.x) * kLaneThreads + static_cast<int>(threadIdx.x);
+  const int i = gid / L;
+  const int lane = gid & (L - 1);
+  // every lane of a group takes part in the shuffles: a group past the last
+  // query repeats the last one and writes nothing
+  const int qi = i < nq ? i : nq - 1;
+  double px[MAXJ], py[MAXJ], pj[MAXJ];
+#pragma unroll
+  for (int jj = 0; jj < MAXJ; ++jj) {
+    const int j = lane + jj * L;
+    px[jj] = 0.0;
+    py[jj] = 0.0;
+    pj[jj] = 0.0;
+    if (j < k) {
+      const std::size_t e = static_cast<std::size_t>(j) * nq + qi;
+      const double2 r = ref[idx_cm[e] - offset];
+      px[jj] = r.x;
+      py[jj] = r.y;
+      pj[jj] = p_cm[e];
+    }
+  }
+  double2 yi = y[qi];
+  double2 u = make_double2(0.0, 0.0);
+  double2 w = make_double2(1.0, 1.0);
+  unsigned long long exact_evals = 0;
+  for (int it = 0; it < rs.total; ++it) {
+    const bool early = it < rs.early_iter;
+    double gx = 0.0, gy = 0.0;
+    if (!grid_repulsion_lanes<L>(field, g, yi.x, yi.y, lane, &gx, &gy)) {
+      // outside the grid: the exact sums over every reference point (rare),
+      // taken whole by every lane of the group (the same value in each)
+      const double2 r = repulsion<true>(ref, n_ref, n_ref, 0u, yi.x, yi.y);
+      gx = r.x;
+      gy = r.y;
+      ++exact_evals;
+    }
+    const double ex = early ? rs.early_exaggeration : rs.exaggeration;
+    double ax = 0.0, ay = 0.0;
+#pragma unroll
+    for (int jj = 0; jj < MAXJ; ++jj) {
+      if (lane + jj * L < k) {
+        const double dx = yi.x - px[jj];
+        const double dy = yi.y - py[jj];
+        const double q = 1.0 / (1.0 + dx * dx + dy * dy);
+        const double c = ex * pj[jj] * q;
+        ax += c * dx;
+        ay += c * dy;
+      }
+    }
+    gx += group_sum<L>(ax);
+    gy += group_sum<L>(ay);
+    update_query(gx, gy, early ? rs.initial_momentum : rs.final_momentum, rs.learning_rate, rs.max_grad,
+                 rs.max_step, yi, u, w);
+  }
+  if (i < nq && lane == 0) {
+    y[i] = yi;
+    if (exact_evals != 0ull) atomicAdd(exact_count, exact_evals);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -554,7 +686,29 @@ hipError_t launch_run(int mode, const double2* ref, int n_ref, const int* idx, c
                       int offset, const RunSchedule& rs, const double4* field, const GridGeo& g, double2* y,
                       unsigned long long* counter, hipStream_t st) {
   const int blocks = (nq + kRunThreads - 1) / kRunThreads;
-  if (mode == kGrid) {
+  if (mode == kGrid && k <= 256 && nq > 0) {
+    // lanes per query: 4 up to 32 neighbours (8 per lane), then groups with
+    // up to 8 per lane (config 3, k = 30: 4 lanes 158k it/s, 8 lanes 119k,
+    // 16 lanes 74k, one thread per query 43k)
+    const auto lanes = [&](auto tag_l, auto tag_j) {
+      constexpr int L = decltype(tag_l)::value;
+      constexpr int J = decltype(tag_j)::value;
+      const long long threads = static_cast<long long>(nq) * L;
+      const int lb = static_cast<int>((threads + kLaneThreads - 1) / kLaneThreads);
+      k_transform_grid_lanes<L, J><<<lb, kLaneThreads, 0, st>>>(ref, n_ref, idx, p, nq, k, offset, rs, field, g, y,
+                                                                counter);
+    };
+    using I8 = std::integral_constant<int, 8>;
+    if (k <= 32) {
+      lanes(std::integral_constant<int, 4>{}, I8{});
+    } else if (k <= 64) {
+      lanes(I8{}, I8{});
+    } else if (k <= 128) {
+      lanes(std::integral_constant<int, 16>{}, I8{});
+    } else {
+      lanes(std::integral_constant<int, 32>{}, I8{});
+    }
+  } else if (mode == kGrid) {
     k_transform_run<kGrid><<<blocks, kRunThreads, 0, st>>>(ref, n_ref, idx, p, nq, k, offset, rs, field, g, y,
                                                           counter);
   } else if (mode == kExact) {
