@@ -102,12 +102,16 @@ struct Arena {
   }
 };
 
-// FASTEMBEDR_HIP_GRAPH_CAPTURE: unset or empty = on; 0, false, FALSE, no, NO
-// = off (the reference's FASTEMBEDR_CUDA_GRAPH_CAPTURE switch,
-// src/embedding_cuda_kernels.cpp:170-178).
+// FASTEMBEDR_HIP_GRAPH_CAPTURE: unset, empty, 0, false, FALSE, no, NO = off;
+// anything else = on.  The reference's FASTEMBEDR_CUDA_GRAPH_CAPTURE switch
+// (src/embedding_cuda_kernels.cpp:170-178) parses the same off values but is
+// on when unset; here eager launches are the default, being faster than
+// replays at every configuration measured on MI355X (whole 750-iteration
+// schedule, interpolation grid: config 0 8721 against 8037 it/s, config 1
+// 8105 against 7410, config 2 3416 against 3389).
 bool graph_capture_enabled() {
   const char* env = std::getenv("FASTEMBEDR_HIP_GRAPH_CAPTURE");
-  if (env == nullptr || env[0] == '\0') return true;
+  if (env == nullptr || env[0] == '\0') return false;
   for (const char* off : {"0", "false", "FALSE", "no", "NO"}) {
     if (std::strcmp(env, off) == 0) return false;
   }
@@ -220,12 +224,17 @@ struct fastembedr_hip_tsne {
   unsigned long long* lg_ring = nullptr;
   unsigned long long* lg_ring_dev = nullptr;  // the ring's device address
 
-  // Replayed iterations (FASTEMBEDR_HIP_GRAPH_CAPTURE, on by default): one
-  // iteration's launches on the three streams (gradient pieces + update) are
-  // captured into a graph keyed by everything the launches bake in, and
+  // Replayed iterations (FASTEMBEDR_HIP_GRAPH_CAPTURE, off by default): one
+  // iteration's launches (gradient pieces + update) on the main stream alone
+  // are captured into a graph keyed by everything the launches bake in, and
   // replayed with one hipGraphLaunch.  A key is captured the second time it
   // is met (a one-off FFT length is not worth an instantiation); renumbering,
-  // the attraction's tile build and timed runs stay eager.
+  // the attraction's tile build and timed runs stay eager.  The captured
+  // iteration is single-stream: on ROCm 7 a graph with parallel branches,
+  // once launched, keeps the allocations its side-branch kernels read from
+  // being returned by hipFree until the next device-wide synchronisation
+  // (4.7 GB per session at config 2, piling up over sessions), which a
+  // single-stream graph does not.
   struct IterGraph {
     std::array<std::uint32_t, 14> key{};
     hipGraphExec_t exec = nullptr;
@@ -233,8 +242,7 @@ struct fastembedr_hip_tsne {
     unsigned long long last_use = 0;
   };
   static constexpr std::size_t kMaxGraphs = 8;
-  bool graph_capture = true;
-  bool capturing = false;   // an iteration is being captured (enqueue_gradient_pieces' arrangement)
+  bool graph_capture = false;
   std::vector<IterGraph> graphs;
   unsigned long long graph_clock = 0;
   long long graph_launches = 0;
@@ -671,12 +679,9 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
     return false;
   }
   // With the attraction on the main stream, the statistics' finish heads the
-  // chain's stream when launched eagerly, so the attraction starts right
-  // after the previous update (config 2, late window: 3298 -> 3392 it/s).  A
-  // captured iteration keeps it at the head of the main stream: with two
-  // root branches its replays measured 17 % slower (3396 -> 2820 it/s over
-  // the whole schedule).
-  const bool fin_chain = swap && !s->capturing;
+  // chain's stream, so the attraction starts right after the previous update
+  // (config 2, late window: 3298 -> 3392 it/s).
+  const bool fin_chain = swap;
   hipStream_t fin = fin_chain ? chain : main;
   if (fin_chain && (!hip_ok(hipEventRecord(s->ev_layout, main), "hipEventRecord(layout)") ||
                !hip_ok(hipStreamWaitEvent(chain, s->ev_layout, 0), "hipStreamWaitEvent(chain)"))) {
@@ -809,15 +814,15 @@ bool enqueue_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip
          });
 }
 
-// Captures enqueue_iteration() into an executable graph (nothing runs).
-bool capture_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up, bool overlap,
-                       bool finalize, hipGraphExec_t* exec) {
+// Captures enqueue_iteration() on the main stream alone (no side branches,
+// whose kernels' allocations a launched graph would hold past hipFree) into an
+// executable graph (nothing runs).
+bool capture_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up, bool finalize,
+                       hipGraphExec_t* exec) {
   if (!hip_ok(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture")) {
     return false;
   }
-  s->capturing = true;
-  const bool enqueued = enqueue_iteration(s, lg, fft_len, up, overlap, finalize);
-  s->capturing = false;
+  const bool enqueued = enqueue_iteration(s, lg, fft_len, up, false, finalize);
   hipGraph_t graph = nullptr;
   const hipError_t ended = hipStreamEndCapture(s->stream, &graph);
   bool ok = enqueued && hip_ok(ended, "hipStreamEndCapture") && graph != nullptr;
@@ -874,7 +879,7 @@ bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, con
   }
   g->last_use = s->graph_clock;
   if (g->exec == nullptr && ++g->seen >= 2) {
-    if (!capture_iteration(s, lg, fft_len, up, true, finalize, &g->exec)) {
+    if (!capture_iteration(s, lg, fft_len, up, finalize, &g->exec)) {
       // A capture the runtime refuses leaves the session on eager launches.
       if (g->exec != nullptr) (void)hipGraphExecDestroy(g->exec);
       g->exec = nullptr;

@@ -177,11 +177,13 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_interp_info(fastembedr_hip_tsne* sess
                                     int* fft_len, float* box_width, double* z);
 
 /* Replayed iterations of run(): how many iterations ran as a replayed graph,
- * how many graphs were captured, and whether capture is on (it follows
- * FASTEMBEDR_HIP_GRAPH_CAPTURE at session creation, as the reference's
- * FASTEMBEDR_CUDA_GRAPH_CAPTURE does, src/embedding_cuda_kernels.cpp:170-178;
- * timed runs never replay).  Any pointer may be NULL.  No counterpart in the
- * reference's ABI. */
+ * how many graphs were captured, and whether capture is on.  Capture follows
+ * FASTEMBEDR_HIP_GRAPH_CAPTURE at session creation: off when unset, empty or
+ * 0/false/FALSE/no/NO, on otherwise (the reference's
+ * FASTEMBEDR_CUDA_GRAPH_CAPTURE, src/embedding_cuda_kernels.cpp:170-178,
+ * takes the same off values but is on when unset; eager launches measured
+ * faster on MI355X).  Timed runs never replay.  Any pointer may be NULL.  No
+ * counterpart in the reference's ABI. */
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_graph_info(fastembedr_hip_tsne* session, long long* launches,
                                    int* captures, int* enabled);
 

@@ -1,10 +1,11 @@
 """Replayed iterations (FASTEMBEDR_HIP_GRAPH_CAPTURE) against eager launches.
 
-run() captures one iteration's launches on its three streams into a graph and
-replays it; the kernels and their order are the same as the eager path's.
-The switch is read when a session is created: unset or empty is on,
-"0"/"false"/"FALSE"/"no"/"NO" is off, as for the reference's
-FASTEMBEDR_CUDA_GRAPH_CAPTURE (src/embedding_cuda_kernels.cpp:170-178).
+run() captures one iteration's launches on the main stream alone into a graph
+and replays it; the kernels and their order are the eager path's without the
+side streams.  The switch is read when a session is created: unset, empty and
+"0"/"false"/"FALSE"/"no"/"NO" are off, anything else on (the reference's
+FASTEMBEDR_CUDA_GRAPH_CAPTURE, src/embedding_cuda_kernels.cpp:170-178, takes
+the same off values but is on when unset).
 
 Float atomics (the attraction's row sums, the binning's order) make two eager
 runs differ by rounding, which t-SNE's early-exaggeration phase amplifies
@@ -21,12 +22,18 @@ interpolation grid):
   * with a growing span (the interpolation grid's FFT length changes between
     graph keys, and the host learns box counts from the device-indexed ring)
     the final KL agrees within 1 %;
-  * the switch's off values turn capture off;
-  * both arrangements of the overlapped iteration (the attraction on the
-    main stream with the chain beside it, the default, and the attraction
-    beside the chain with a helper launch, FASTEMBEDR_HIP_ATTRACT_MAIN=0),
-    replayed, end within 1 % of the eager run's KL.
+  * the switch's off values (and unset) turn capture off;
+  * both arrangements of the eager overlapped iteration (the attraction on
+    the main stream with the chain beside it, the default, and the attraction
+    beside the chain with a helper launch, FASTEMBEDR_HIP_ATTRACT_MAIN=0) end
+    within 1 % of the single-stream replayed run's KL;
+  * a closed session gives its device memory back, replayed or not (graphs
+    with parallel branches, once launched, held their side-branch kernels'
+    allocations past hipFree until a device-wide synchronisation: 4.7 GB
+    per session at config 2, piling up over sessions).
 """
+
+import ctypes as C
 
 import os
 import sys
@@ -100,7 +107,7 @@ def test_replayed_iteration_matches_eager(hip, prob, repulsion):
         s.run(1, 12.0, 0.5, n / 12.0, 0.01, 5.0)
         return start, s.y
 
-    with _session(hip, idx, dist, None) as s:
+    with _session(hip, idx, dist, "1") as s:
         for _ in range(3):  # eager (first sight of the key), captured and replayed, replayed
             start, y_g = one(s)
         info = s.graph_info()
@@ -120,7 +127,7 @@ def test_replayed_schedule_kl(hip, prob, repulsion):
     x, idx, dist, y0 = prob
     _say(f"case: graph replay vs eager, repulsion {repulsion}, 60 + 60 iterations")
     _, y_e, kl_e, info_e = _schedule(hip, idx, dist, y0, repulsion, "0", 60, 60)
-    _, y_g, kl_g, info_g = _schedule(hip, idx, dist, y0, repulsion, None, 60, 60)
+    _, y_g, kl_g, info_g = _schedule(hip, idx, dist, y0, repulsion, "1", 60, 60)
     _say(f"  KL eager {kl_e:.5f}, graph {kl_g:.5f}, {info_g}")
     assert not info_e["enabled"] and info_e["launches"] == 0
     assert info_g["enabled"] and info_g["launches"] >= 100, info_g
@@ -132,10 +139,11 @@ def test_replayed_schedule_kl(hip, prob, repulsion):
 def test_overlap_arrangements_kl(hip, prob, arrangement):
     x, idx, dist, y0 = prob
     extra = {"FASTEMBEDR_HIP_ATTRACT_MAIN": arrangement}
-    _say(f"case: FASTEMBEDR_HIP_ATTRACT_MAIN={arrangement}, replayed vs eager, interpolation grid, 60 + 60 iterations")
-    _, y_e, kl_e, _ = _schedule(hip, idx, dist, y0, _lib.REPULSION_LAGRANGE, "0", 60, 60, extra)
-    _, y_g, kl_g, info = _schedule(hip, idx, dist, y0, _lib.REPULSION_LAGRANGE, None, 60, 60, extra)
+    _say(f"case: FASTEMBEDR_HIP_ATTRACT_MAIN={arrangement}, eager vs replayed, interpolation grid, 60 + 60 iterations")
+    _, y_e, kl_e, info_e = _schedule(hip, idx, dist, y0, _lib.REPULSION_LAGRANGE, None, 60, 60, extra)
+    _, y_g, kl_g, info = _schedule(hip, idx, dist, y0, _lib.REPULSION_LAGRANGE, "1", 60, 60)
     _say(f"  KL eager {kl_e:.5f}, graph {kl_g:.5f}, {info}")
+    assert not info_e["enabled"] and info_e["launches"] == 0, info_e
     assert info["launches"] >= 100, info
     assert np.all(np.isfinite(y_g)) and np.all(np.isfinite(y_e))
     assert abs(kl_g - kl_e) <= KL_TOL * kl_e
@@ -148,16 +156,80 @@ def test_replayed_growing_span_kl(hip, prob):
     y0 = (y0 - y0.mean(axis=0)) * (4.0 / float(np.ptp(y0)))
     _say("case: graph replay vs eager, interpolation grid, growing span, 150 + 150 iterations")
     _, y_e, kl_e, _ = _schedule(hip, idx, dist, y0.astype(np.float32), _lib.REPULSION_LAGRANGE, "no", 150, 150)
-    _, y_g, kl_g, info = _schedule(hip, idx, dist, y0.astype(np.float32), _lib.REPULSION_LAGRANGE, "", 150, 150)
+    _, y_g, kl_g, info = _schedule(hip, idx, dist, y0.astype(np.float32), _lib.REPULSION_LAGRANGE, "yes", 150, 150)
     _say(f"  KL eager {kl_e:.5f}, graph {kl_g:.5f}, {info}")
     assert info["launches"] >= 250, info
     assert np.all(np.isfinite(y_g))
     assert abs(kl_g - kl_e) <= KL_TOL * kl_e
 
 
-@pytest.mark.parametrize("value,enabled", [("0", False), ("false", False), ("FALSE", False), ("no", False),
-                                           ("NO", False), ("", True), ("1", True), ("yes", True)])
+@pytest.mark.parametrize("value,enabled", [(None, False), ("", False), ("0", False), ("false", False),
+                                           ("FALSE", False), ("no", False), ("NO", False), ("1", True),
+                                           ("yes", True)])
 def test_capture_switch_values(hip, prob, value, enabled):
     x, idx, dist, y0 = prob
     with _session(hip, idx, dist, value) as s:
         assert s.graph_info()["enabled"] is enabled
+
+
+def _free_bytes() -> int:
+    """Free device memory as a caller sees it after close() (no device-wide
+    synchronisation first: deferred releases count as lost)."""
+    hip_rt = C.CDLL("libamdhip64.so.7")
+    free_b, total_b = C.c_size_t(), C.c_size_t()
+    assert hip_rt.hipMemGetInfo(C.byref(free_b), C.byref(total_b)) == 0
+    return free_b.value
+
+
+@pytest.mark.parametrize("capture", ["0", "1"], ids=["eager", "replayed"])
+def test_closed_session_returns_memory(hip, capture):
+    """Five 200,000-point sessions of config 2's mixture (perplexity 30,
+    k = 90; about 2.5 GB of device buffers each), one after another, each
+    run for 30 iterations and closed: after the first two
+    (which absorb the runtime's one-time pools, 54 and 40 MiB in a fresh
+    process) the device's free memory stays put.  The runtime may keep a
+    closed session's blocks for the next one's identical requests (free
+    memory then stays at the in-session level), so the check is that three
+    more sessions lose nothing between them.  Graphs with parallel branches
+    lost 1.4 GB per session of this problem."""
+    n, k = 200_000, 90
+    x, _ = synthetic.gaussian_mixture(synthetic.CONFIGS[2], seed=1, n=n)
+    knn = hip.exact_knn(np.ascontiguousarray(x, np.float32), k, keep_device=True)
+    y0 = synthetic.pca_init(x)
+    _say(f"case: device memory after close, n {n}, capture {capture}")
+
+    def one():
+        settings = {ENV: capture}
+        old = {key: os.environ.get(key) for key in settings}
+        os.environ.update(settings)
+        try:
+            s = hip.TsneSession(perplexity=30.0, index_offset=1, n=n, k=k,
+                                device_pointers=(knn.indices_ptr, knn.distances_ptr))
+        finally:
+            for key, v in old.items():
+                if v is None:
+                    os.environ.pop(key, None)
+                else:
+                    os.environ[key] = v
+        with s:
+            s.set_repulsion(_lib.REPULSION_LAGRANGE, 3, 50, 1.0)
+            s.set_state(y0)
+            s.center()
+            s.run(30, 12.0, 0.5, n / 12.0, 0.01, 5.0)
+            s.sync()
+            used = _free_bytes()
+            info = s.graph_info()
+        return used, info
+
+    start = _free_bytes()
+    during, after = [], []
+    for _ in range(5):
+        used, info = one()
+        during.append(used)
+        after.append(_free_bytes())
+        assert (info["launches"] >= 20) if capture == "1" else (info["launches"] == 0), info
+    mib = lambda v: f"{v / 2**20:.0f}"
+    _say(f"  free at start {mib(start)} MiB, in sessions {[mib(v) for v in during]}, "
+         f"after them {[mib(v) for v in after]}, {info}")
+    assert start - min(during) > 256 * 2**20  # the sessions did hold their buffers
+    assert after[1] - after[-1] <= 64 * 2**20
