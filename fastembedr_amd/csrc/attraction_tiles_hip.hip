@@ -40,19 +40,22 @@ namespace fehip {
 namespace {
 
 // Slot format (kTileRun = 8 slots per lane group, a group starting at a
-// multiple of 8): the 16-bit word of a slot is (local column << 4) | step,
-// where step is the slot's row minus the previous slot's row in the group (0
-// for a group's first slot).  p is stored as its IEEE-754 bits; P is a
+// multiple of 8): the 16-bit word of a slot is (local column << 3) | step,
+// so that word & 0x7ff8 is the column's LDS byte offset, and step (3 bits)
+// is the slot's row minus the previous slot's row in the group (0 for a
+// group's first slot).  p is stored as its IEEE-754 bits; P is a
 // normalised joint distribution built from validated distances, so every
 // value lies in [0, 1] and bits 30 and 31 of its pattern are zero.  Those
 // bits of slots 0..4 of a group hold the group's base row (the local row of
-// its first slot, 10 bits), 2 bits per slot.  Steps above 15 are made of
-// bridge slots (p = 0) 15 rows apart; a run's padding repeats its last slot
+// its first slot, 10 bits), 2 bits per slot.  Steps above 7 are made of
+// bridge slots (p = 0) 7 rows apart (0.003 % more slots than 15-row bridges
+// at config 2's late layout, 0.03 % at config 4's); a run's padding repeats its last slot
 // with step 0 and p = 0.  Bridges and padding add nothing.
 static_assert(kTileRun == 8, "a lane reads its group as one 16-byte vector of words and two of values");
 static_assert(kTileRows <= 1024, "a group's base row fits the 10 spare bits of its first 5 values");
 static_assert(kTileCols <= 4096, "a local column fits 12 bits of a slot word");
-constexpr int kStepMax = 15;
+constexpr int kStepMax = 7;
+constexpr unsigned int kColMask = 0x7ff8u;  // a slot word's column byte offset
 constexpr unsigned int kValueMask = 0x3fffffffu;
 
 constexpr int kBuildThreads = 256;
@@ -164,7 +167,7 @@ __device__ __forceinline__ void put_slot(long long q, int col, int row, int step
                                          unsigned short* __restrict__ ent, float* __restrict__ val,
                                          unsigned short* __restrict__ base_row) {
   const bool first = (q & (kTileRun - 1)) == 0;
-  ent[q] = static_cast<unsigned short>((col << 4) | (first ? 0 : step));
+  ent[q] = static_cast<unsigned short>((col << 3) | (first ? 0 : step));
   val[q] = __uint_as_float(p_bits);
   if (first) base_row[q / kTileRun] = static_cast<unsigned short>(row);
 }
@@ -241,34 +244,49 @@ __device__ __forceinline__ float2 attract_term(float2 yi, float2 yj, float p) {
   return make_float2(c * dx, c * dy);
 }
 
-// Wave-level helpers (gfx9 DPP: row shifts within 16-lane rows, row
-// broadcasts 15 / 31, whole-wave shifts by one lane).  Lanes whose source
-// lies outside the row / wave read 0.
+// Whole-wave shifts by one lane (gfx9 DPP); a lane whose source lies outside
+// the wave reads 0.
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, true);
 }
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, true));
-}
-constexpr int kDppRowShr = 0x110;    // + shift (1..15)
 constexpr int kDppWaveShl1 = 0x130;  // lane l reads lane l + 1
 constexpr int kDppWaveShr1 = 0x138;  // lane l reads lane l - 1
-constexpr int kDppRowBcast15 = 0x142;
-constexpr int kDppRowBcast31 = 0x143;
 
-// One step of an inclusive segmented scan: (x, y) combined with the value
-// CTRL's shift below.  `stop` holds the bits of 1.0f once the lane's window
-// reaches back to a segment start (a lane whose value takes nothing from
-// below), else 0; a source outside the row / wave reads (0, 0, 0), the
-// identity of the step.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ void seg_step(float& x, float& y, unsigned int& stop) {
-  const float take = 1.0f - __uint_as_float(stop);
-  x = fmaf(dpp_f<CTRL, ROW_MASK>(x), take, x);
-  y = fmaf(dpp_f<CTRL, ROW_MASK>(y), take, y);
-  stop = max(stop, static_cast<unsigned int>(dpp_i<CTRL, ROW_MASK>(static_cast<int>(stop))));
+// Inclusive segmented scan of (x, y) over the wave (Hillis-Steele: row
+// shifts 1, 2, 4, 8, then row broadcasts 15 and 31).  `take` is 0 on a lane
+// that starts a segment and 1 elsewhere; at each step a lane adds the
+// partial sums the step reaches, times its take, and its take becomes the
+// minimum of the two (0 once its window holds a segment start).  Each step
+// is one DPP multiply-add per value and one DPP minimum: bound_ctrl is off,
+// so a lane whose source lies outside its row (or the rows a broadcast
+// writes) is not written and keeps its partial and its take.  gfx9 needs two
+// wait states between a VALU write of a VGPR and a DPP read of it: every
+// DPP source here was written three instructions earlier, and the s_nop 1
+// at each end covers the code around the block.  Needs the whole wave
+// active.
+__device__ __forceinline__ void seg_scan(float& x, float& y, float take) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_fmac_f32_dpp %0, %0, %2 row_shr:1 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %1, %2 row_shr:1 row_mask:0xf bank_mask:0xf\n\t"
+      "v_min_f32_dpp %2, %2, %2 row_shr:1 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %0, %2 row_shr:2 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %1, %2 row_shr:2 row_mask:0xf bank_mask:0xf\n\t"
+      "v_min_f32_dpp %2, %2, %2 row_shr:2 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %0, %2 row_shr:4 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %1, %2 row_shr:4 row_mask:0xf bank_mask:0xf\n\t"
+      "v_min_f32_dpp %2, %2, %2 row_shr:4 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %0, %2 row_shr:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %1, %2 row_shr:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_min_f32_dpp %2, %2, %2 row_shr:8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %0, %2 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %1, %2 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+      "v_min_f32_dpp %2, %2, %2 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %0, %2 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %1, %2 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+      "s_nop 1"
+      : "+v"(x), "+v"(y), "+v"(take));
 }
 
 // A lane's kTileRun entries of one round of a run [e0, e1).  Lanes past the
@@ -331,12 +349,35 @@ __device__ __forceinline__ void stage_tile_columns(float2* ys, const float2* __r
   __syncthreads();
 }
 
+// Adds (x, y) to the accumulator at row byte offset k: by a plain read and
+// write when no other wave can add to that row before the next barrier
+// (`own`; a wave adds to a row at most once per group), else atomically.
+__device__ __forceinline__ void acc_add(float2* acc, unsigned int k, float x, float y, bool own) {
+  if (own) {
+    float2 v = lds_at(acc, k);
+    v.x += x;
+    v.y += y;
+    lds_at(acc, k) = v;
+  } else {
+    atomicAdd(&lds_at(acc, k).x, x);
+    atomicAdd(&lds_at(acc, k).y, y);
+  }
+}
+
 // Sum one lane group; a step that is not `live` adds nothing.  A lane's
 // entries hold one or more rows (in order); it sums each row's part in
-// registers and adds every part but the last (which its group completes)
-// straight to the row's LDS accumulator.  The last part, which may run on
-// into the next lanes, is summed over the wave by an inclusive segmented
-// scan (DPP), and only the lane that ends the row adds it.
+// registers.  Rows that begin and end inside the group go straight to the
+// row's LDS accumulator.  The last row's part, which may run on into the
+// next lanes, is summed over the wave by an inclusive segmented scan (DPP)
+// and added by the lane that ends the chain; the first row's part, when a
+// later row follows it in the group, ends the chain of lane l - 1 when it
+// continues it, and the lane adds the two together.  So a wave issues one
+// LDS add pair for the first rows and one for the chains, plus one per slot
+// position where some lane completes a row wholly inside its group (an LDS
+// float atomic costs far more than its few active lanes suggest: adding the
+// first rows at each break instead took the kernel from 1.64 to 2.01 ms at
+// config 4's ~7 entries per row and run, and from 0.230 to 0.245 ms beside
+// the repulsion at config 2).
 template <int NT>
 __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileStep& s, bool live, int tid, float2* yr,
                                                float2* ys, float2* acc) {
@@ -347,7 +388,7 @@ __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileSte
   // Row byte offsets (8 bytes per LDS position): the base row from the spare
   // value bits (slot 0's step is 0), then the steps.  A group whose last row
   // lies past the block (which a layout built here never holds) adds
-  // nothing; its reads stay inside the workgroup's LDS (rows < 1024 + 105).
+  // nothing; its reads stay inside the workgroup's LDS (rows < 1024 + 49).
   unsigned int kr[kTileRun];
   unsigned int r8 = 0;
 #pragma unroll
@@ -355,42 +396,54 @@ __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileSte
   kr[0] = r8;
 #pragma unroll
   for (int q = 1; q < kTileRun; ++q) {
-    const unsigned int step = (q & 1) ? (wp[q / 2] >> 16) & 0xfu : wp[q / 2] & 0xfu;
+    const unsigned int step = ((q & 1) ? wp[q / 2] >> 16 : wp[q / 2]) & 7u;
     r8 += step << 3;
     kr[q] = r8;
   }
   const bool active = live && s.e0 + (s.round * NT + tid) * kTileRun < s.e1 && r8 < kTileRows * 8u;
+  const unsigned int kf = kr[0];
+  const unsigned int kl = kr[kTileRun - 1];
   float tx = 0.0f, ty = 0.0f;  // the current row's part
+  float hx = 0.0f, hy = 0.0f;  // the first row's part, once a later row follows it
 #pragma unroll
   for (int q = 0; q < kTileRun; ++q) {
-    const unsigned int word = (q & 1) ? wp[q / 2] >> 16 : wp[q / 2] & 0xffffu;
-    const unsigned int kc = (word >> 1) & 0x7ff8u;  // (word >> 4) * 8
-    const float2 c = attract_term(lds_at(yr, kr[q]), lds_at(ys, kc), __uint_as_float(pb[q] & kValueMask));
-    const bool brk = q > 0 && kr[q] != kr[q > 0 ? q - 1 : 0];  // the previous row's part is complete
-    if (brk && active) {
-      atomicAdd(&lds_at(acc, kr[q > 0 ? q - 1 : 0]).x, tx);
-      atomicAdd(&lds_at(acc, kr[q > 0 ? q - 1 : 0]).y, ty);
+    const unsigned int kc = ((q & 1) ? wp[q / 2] >> 16 : wp[q / 2]) & kColMask;
+    // only slots 0..4 carry base-row bits
+    const float p = __uint_as_float(q < 5 ? pb[q] & kValueMask : pb[q]);
+    const float2 c = attract_term(lds_at(yr, kr[q]), lds_at(ys, kc), p);
+    if (q == 0) {
+      tx = c.x;
+      ty = c.y;
+      continue;
     }
+    const bool brk = kr[q] != kr[q - 1];   // the previous row's part is complete
+    const bool first = kr[q - 1] == kf;    // ... and it is the group's first row's
+    if (brk && !first && active) acc_add(acc, kr[q - 1], tx, ty, true);  // a row wholly inside the group
+    hx = brk && first ? tx : hx;
+    hy = brk && first ? ty : hy;
     tx = (brk ? 0.0f : tx) + c.x;
     ty = (brk ? 0.0f : ty) + c.y;
   }
-  // The last row's part continues lane l - 1's when the whole group is that
-  // one row; the scan sums each such chain into its last lane.
-  const int kf = static_cast<int>(kr[0]);
-  const int kl = static_cast<int>(kr[kTileRun - 1]);
-  const int prev_kl = dpp_i<kDppWaveShr1, 0xf>(kl + 1) - 1;  // -1 on lane 0
-  const bool start = !active || kf != kl || kf != prev_kl;
-  unsigned int stop = start ? __float_as_uint(1.0f) : 0u;
-  seg_step<kDppRowShr + 1, 0xf>(tx, ty, stop);
-  seg_step<kDppRowShr + 2, 0xf>(tx, ty, stop);
-  seg_step<kDppRowShr + 4, 0xf>(tx, ty, stop);
-  seg_step<kDppRowShr + 8, 0xf>(tx, ty, stop);
-  seg_step<kDppRowBcast15, 0xa>(tx, ty, stop);
-  seg_step<kDppRowBcast31, 0xc>(tx, ty, stop);
-  const int next_joins = dpp_i<kDppWaveShl1, 0xf>(start ? 0 : 1);  // 0 on lane 63
-  if (active && !next_joins) {
-    atomicAdd(&lds_at(acc, static_cast<unsigned int>(kl)).x, tx);
-    atomicAdd(&lds_at(acc, static_cast<unsigned int>(kl)).y, ty);
+  // Chains over lanes: the first row continues lane l - 1's last when they
+  // are the same row (active lanes are a prefix of the wave, so lane l - 1
+  // is active too); a lane holding one row that continues lane l - 1's
+  // extends the chain, any other lane starts one with its last row's part.
+  const bool split = kf != kl;
+  const int prev_kl = dpp_i<kDppWaveShr1, 0xf>(static_cast<int>(kl) + 1) - 1;  // -1 on lane 0
+  const bool cont = active && static_cast<int>(kf) == prev_kl;
+  seg_scan(tx, ty, cont && !split ? 1.0f : 0.0f);
+  const float px = __int_as_float(dpp_i<kDppWaveShr1, 0xf>(__float_as_int(tx)));  // lane l - 1's chain
+  const float py = __int_as_float(dpp_i<kDppWaveShr1, 0xf>(__float_as_int(ty)));
+  const int next_cont = dpp_i<kDppWaveShl1, 0xf>(cont ? 1 : 0);  // 0 on lane 63
+  // Only the wave's first and last rows can be shared with other waves
+  // (rounds and row parts are contiguous slot ranges in row order).
+  const unsigned int wave_first = __builtin_amdgcn_readfirstlane(kf);
+  const unsigned int wave_last = __builtin_amdgcn_readlane(kl, 63);
+  if (active && !next_cont) {  // the lane ends its last row's chain
+    acc_add(acc, kl, tx, ty, kl != wave_first && kl != wave_last);
+  }
+  if (active && split) {  // the first row's part, with the chain it ends
+    acc_add(acc, kf, cont ? hx + px : hx, cont ? hy + py : hy, kf != wave_first);
   }
 }
 

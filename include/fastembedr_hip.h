@@ -195,7 +195,7 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_attraction_info(fastembedr_hip_tsne* 
                                         int* renumbers);
 
 /* Size of the attraction's tiled P in the current working numbering: slots
- * (entries, bridge slots between entries more than 15 rows apart, and the
+ * (entries, bridge slots between entries more than 7 rows apart, and the
  * padding of each run to a multiple of 8), -1 when there is none (as for
  * attraction_info).  No counterpart in the reference. */
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_attraction_slots(fastembedr_hip_tsne* session, long long* slots);

@@ -10,7 +10,7 @@ sum_j p_ij q_ij (y_i - y_j) (src/tsne_neighbors.cpp:985-1012).
 Tolerance: relative L2 <= 1e-5 (fp32 sums in another order; the hardware
 reciprocal is within 1 ulp).  The cases cover many tiles per row block, rows
 whose parts in one tile are far longer than a lane's group of 8 slots, rows
-of one or two entries, sparse runs whose rows lie more than 15 apart (bridge
+of one or two entries, sparse runs whose rows lie more than 7 apart (bridge
 slots), and sizes that are not multiples of the tile shape.
 """
 
@@ -65,10 +65,10 @@ def _check(hip, idx, dist, perplexity, y, label):
         info = s.attraction_info()
         tiles = info["tiles"]
     n = y.shape[0]
-    # slots: every entry, the bridges between entries more than 15 rows apart
-    # within a run (at most 1023 // 15 per run) and each run's padding to 8
+    # slots: every entry, the bridges between entries more than 7 rows apart
+    # within a run (at most 1023 // 7 per run) and each run's padding to 8
     assert info["slots"] % 8 == 0
-    assert len(col) <= info["slots"] <= len(col) + (1023 // 15 + 7) * info["tiles"]
+    assert len(col) <= info["slots"] <= len(col) + (1023 // 7 + 7) * info["tiles"]
     ref = attraction_numpy(row_ptr, col, val, y)
     rows = np.repeat(np.arange(n), np.diff(row_ptr))
     want_tiles = len(np.unique((rows // TILE_ROWS).astype(np.int64) * (1 << 20) + col // TILE_COLS))
@@ -111,7 +111,7 @@ def test_tiled_attraction_long_parts(hip):
 
 def scattered_knn(n, k, seed):
     """k neighbours drawn uniformly from all rows: each (row block, column
-    tile) run holds few entries, so its rows are often more than 15 apart and
+    tile) run holds few entries, so its rows are often more than 7 apart and
     the slot layout needs bridge slots (and row gaps up to a whole block)."""
     rng = np.random.default_rng(seed)
     idx = np.empty((n, k), np.int32)
