@@ -182,10 +182,16 @@ struct fastembedr_hip_tsne {
   // Workgroups per CU of the attraction when it runs beside the repulsion
   // kernels, possibly fractional: fewer than the 3 its LDS allows leave room
   // on every CU for the latency-bound repulsion chain, whose waves also take
-  // issue priority (chain_priority) (FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU;
-  // config 2, late window, interleaved repeats: 1 per CU 3074 it/s, 1.5
-  // 3164, 2 3270, 3 2891).  Alone it takes one workgroup per row block.
+  // issue priority (chain_priority).  Set by FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU,
+  // else after each tile build from the tiled P's mean run length, which
+  // sets the attraction's cost per entry against the chain's per point
+  // (late window, interleaved repeats: config 2, runs of 25k slots: 1 per
+  // CU 3178 it/s, 1.25 3166, 1.5 3560, 1.75 3534, 2 3489, 2.25 3376, 2.5
+  // 3192; config 4, runs of 7.4k slots: 1.5 685, 2 781, 2.5 830, 2.75 835,
+  // 3 813): 1.5 at 16K slots or more, 2.5 at 8K or fewer, linear between.
+  // Alone it takes one workgroup per row block.
   double attract_shared_per_cu = 2.0;
+  bool attract_share_auto = true;
   // Workgroups per CU of the helper launch that joins the attraction on the
   // main stream once the repulsion chain is done, taking over the row blocks
   // still unclaimed (FASTEMBEDR_HIP_ATTRACT_HELPER_PER_CU; 0: none).  The
@@ -499,6 +505,19 @@ bool ensure_tiles(fastembedr_hip_tsne* s, hipStream_t st) {
     return false;
   }
   s->tiles_for = s->wi;
+  if (!s->attract_share_auto) return true;
+  // the attraction's share beside the chain from the mean run length (a
+  // synchronous read, once per build)
+  int count = 0, total = 0;
+  if (!hip_ok(hipMemcpyAsync(&count, s->tiles.tile_count, sizeof(int), hipMemcpyDeviceToHost, st), "tile count") ||
+      !hip_ok(hipStreamSynchronize(st), "tile count") ||
+      !hip_ok(hipMemcpyAsync(&total, s->tiles.tile_beg + count, sizeof(int), hipMemcpyDeviceToHost, st),
+              "tile slots") ||
+      !hip_ok(hipStreamSynchronize(st), "tile slots")) {
+    return false;
+  }
+  const double run = count > 0 ? static_cast<double>(total) / count : 0.0;
+  s->attract_shared_per_cu = std::clamp(2.5 - (run - 8192.0) / 8192.0, 1.5, 2.5);
   return true;
 }
 
@@ -516,14 +535,14 @@ bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggera
   if (st == nullptr) st = s->stream;
   s->helper_pending = 0;
   s->helper_span_open = false;
-  const bool share = shared && s->cus > 0 && s->attract_shared_per_cu > 0.0;
-  const int slots = share ? per_xcd_for(s, s->attract_shared_per_cu) : 0;
   if (!s->attract_tiled) {
     return s->timed(
         fehip::kKAttract, "attract launch",
         [&] { return fehip::launch_attract(s->work_p(), y_cur, s->attr, exaggeration, s->lanes, s->xcds, st); }, st);
   }
-  if (!ensure_tiles(s, st)) return false;
+  if (!ensure_tiles(s, st)) return false;  // may set attract_shared_per_cu
+  const bool share = shared && s->cus > 0 && s->attract_shared_per_cu > 0.0;
+  const int slots = share ? per_xcd_for(s, s->attract_shared_per_cu) : 0;
   const int helper =
       share && !s->attract_main && s->attract_helper_per_cu > 0.0 ? per_xcd_for(s, s->attract_helper_per_cu) : 0;
   if (helper == 0) {
@@ -1307,7 +1326,10 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
     if (const char* v = std::getenv(name)) {
       char* end = nullptr;
       const double d = std::strtod(v, &end);
-      if (end != v && std::isfinite(d) && d >= 0.0) *knob = d;
+      if (end != v && std::isfinite(d) && d >= 0.0) {
+        *knob = d;
+        if (knob == &s->attract_shared_per_cu) s->attract_share_auto = false;
+      }
     }
   }
   if (const char* v = std::getenv("FASTEMBEDR_HIP_ATTRACT_MAIN")) s->attract_main = std::strcmp(v, "0") != 0;
