@@ -183,15 +183,22 @@ struct fastembedr_hip_tsne {
   // kernels, possibly fractional: fewer than the 3 its LDS allows leave room
   // on every CU for the latency-bound repulsion chain, whose waves also take
   // issue priority (chain_priority).  Set by FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU,
-  // else after each tile build from the tiled P's mean run length, which
-  // sets the attraction's cost per entry against the chain's per point
-  // (late window, interleaved repeats: config 2, runs of 25k slots: 1 per
-  // CU 3178 it/s, 1.25 3166, 1.5 3560, 1.75 3534, 2 3489, 2.25 3376, 2.5
-  // 3192; config 4, runs of 7.4k slots: 1.5 685, 2 781, 2.5 830, 2.75 835,
-  // 3 813): 1.5 at 16K slots or more, 2.5 at 8K or fewer, linear between.
+  // else (attract_share_auto) after each tile build from the tiled P's mean
+  // run length, which sets the attraction's cost per entry against the
+  // interpolation grid chain's per point (late window, interleaved repeats:
+  // config 2, runs of 25k slots: 1 per CU 3178 it/s, 1.25 3166, 1.5 3560,
+  // 1.75 3534, 2 3489, 2.25 3376, 2.5 3192; config 4, runs of 7.4k slots:
+  // 1.5 685, 2 781, 2.5 830, 2.75 835, 3 813): 1.5 at 16K slots or more, 2.5
+  // at 8K or fewer, linear between; half a workgroup more beside the shorter
+  // bilinear grid chain (config 2: 1.5 3500, 1.75 3611, 2 3731, 2.5 3624).
   // Alone it takes one workgroup per row block.
   double attract_shared_per_cu = 2.0;
   bool attract_share_auto = true;
+  double attract_share_base = 2.0;  // from the last tile build
+  double attract_share() const {
+    if (!attract_share_auto) return attract_shared_per_cu;
+    return attract_share_base + (repulsion == FASTEMBEDR_HIP_REPULSION_LAGRANGE ? 0.0 : 0.5);
+  }
   // Workgroups per CU of the helper launch that joins the attraction on the
   // main stream once the repulsion chain is done, taking over the row blocks
   // still unclaimed (FASTEMBEDR_HIP_ATTRACT_HELPER_PER_CU; 0: none).  The
@@ -201,7 +208,7 @@ struct fastembedr_hip_tsne {
   // The attraction on the main stream and the repulsion chain on side_attr
   // (the default; FASTEMBEDR_HIP_ATTRACT_MAIN=0: the attraction on side_attr
   // with a helper launch on the main stream after the chain); the attraction
-  // then takes attract_shared_per_cu workgroups per CU and no helper.  At
+  // then takes attract_share() workgroups per CU and no helper.  At
   // config 2 the chain ends last, so the update follows the chain's event
   // (3270 against 3205 it/s in the late window, 3409 against 3340 over the
   // whole schedule).
@@ -517,7 +524,7 @@ bool ensure_tiles(fastembedr_hip_tsne* s, hipStream_t st) {
     return false;
   }
   const double run = count > 0 ? static_cast<double>(total) / count : 0.0;
-  s->attract_shared_per_cu = std::clamp(2.5 - (run - 8192.0) / 8192.0, 1.5, 2.5);
+  s->attract_share_base = std::clamp(2.5 - (run - 8192.0) / 8192.0, 1.5, 2.5);
   return true;
 }
 
@@ -540,9 +547,10 @@ bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggera
         fehip::kKAttract, "attract launch",
         [&] { return fehip::launch_attract(s->work_p(), y_cur, s->attr, exaggeration, s->lanes, s->xcds, st); }, st);
   }
-  if (!ensure_tiles(s, st)) return false;  // may set attract_shared_per_cu
-  const bool share = shared && s->cus > 0 && s->attract_shared_per_cu > 0.0;
-  const int slots = share ? per_xcd_for(s, s->attract_shared_per_cu) : 0;
+  if (!ensure_tiles(s, st)) return false;  // may set attract_share_base
+  const double per_cu = s->attract_share();
+  const bool share = shared && s->cus > 0 && per_cu > 0.0;
+  const int slots = share ? per_xcd_for(s, per_cu) : 0;
   const int helper =
       share && !s->attract_main && s->attract_helper_per_cu > 0.0 ? per_xcd_for(s, s->attract_helper_per_cu) : 0;
   if (helper == 0) {
@@ -869,7 +877,7 @@ bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, con
                                              static_cast<std::uint32_t>(s->si),
                                              static_cast<std::uint32_t>(s->wi),
                                              static_cast<std::uint32_t>(s->attract_tiled),
-                                             static_cast<std::uint32_t>(std::lround(1000.0 * s->attract_shared_per_cu)),
+                                             static_cast<std::uint32_t>(std::lround(1000.0 * s->attract_share())),
                                              static_cast<std::uint32_t>(std::lround(1000.0 * s->attract_helper_per_cu)),
                                              bits(up.exaggeration),
                                              bits(up.momentum),
