@@ -513,7 +513,7 @@ TRAFFIC_FILES = {"grid": ROOT / "profiles" / "tsne_loop_config2_grid_traffic.jso
 # Kernels of the repulsion step and their launches per iteration.
 REPULSION_SYMBOLS = {
     "interp": {"k_lg_bin_count": 1, "k_bin_plan": 1, "k_lg_bin_scatter": 1, "k_lg_spread": 1, "k_lg_gather": 1,
-               "k_lg_kernel_rows": 1, "k_lg_transpose": 3, "k_lg_kernel_cols": 1, "k_lg_charge_rows": 1,
+               "k_lg_kernel_rows": 1, "k_lg_kernel_cols": 1, "k_lg_charge_rows": 1,
                "k_lg_conv_cols": 1, "k_lg_inverse_rows": 1, "k_lg_finalize_z": 1},
     "grid": {"k_bin_count": 1, "k_bin_plan": 1, "k_bin_scatter": 1, "k_spread_tiles": 1, "k_kernel_rows": 1,
              "k_kernel_cols": 1, "k_charge_rows": 1, "k_conv_cols": 1, "k_inverse_rows": 1, "k_finalize_sumq": 1},

@@ -360,8 +360,7 @@ const char* kKernelNames[fehip::kKernelCount] = {
     "stats", "bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols", "charge_rows",
     "conv_cols", "inverse_rows", "attract", "update", "commit", "renumber", "tile_build",
     "interp_bin_count", "interp_bin_plan", "interp_bin_scatter", "interp_spread", "interp_gather",
-    "interp_kernel_rows", "interp_kernel_transpose", "interp_kernel_cols", "interp_charge_rows",
-    "interp_charge_transpose", "interp_conv_cols", "interp_potential_transpose", "interp_inverse_rows",
+    "interp_kernel_rows", "interp_kernel_cols", "interp_charge_rows", "interp_conv_cols", "interp_inverse_rows",
     "finalize_stats"};
 
 int key_bits_for(int n) {
@@ -731,11 +730,12 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   }
   if (swap && !enqueue_attract(s, s->y_a(), exaggeration, main, true)) return false;
   if (lg) {
-    static constexpr int kIds[3] = {fehip::kKLgKernelRows, fehip::kKLgKernelT, fehip::kKLgKernelCols};
-    for (int which = 0; which < 3; ++which) {
+    static constexpr int kIds[2] = {fehip::kKLgKernelRows, fehip::kKLgKernelCols};
+    static constexpr int kSteps[2] = {0, 2};
+    for (int q = 0; q < 2; ++q) {
       if (!s->timed(
-              kIds[which], "interpolation-grid kernel launch",
-              [&] { return fehip::launch_interp_fft(which, fft_len, ib, s->sc, s->tw, n, sk); }, sk)) {
+              kIds[q], "interpolation-grid kernel launch",
+              [&] { return fehip::launch_interp_fft(kSteps[q], fft_len, ib, s->sc, s->tw, n, sk); }, sk)) {
         return false;
       }
     }
@@ -777,10 +777,7 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
              [&] { return fehip::launch_interp_gather(s->sc, ib, chain); }, chain) &&
          s->timed(
              fehip::kKLgChargeRows, "interp charge_rows launch",
-             [&] { return fehip::launch_interp_fft(3, fft_len, ib, s->sc, s->tw, n, chain); }, chain) &&
-         s->timed(
-             fehip::kKLgChargeT, "interp charge transpose launch",
-             [&] { return fehip::launch_interp_fft(4, fft_len, ib, s->sc, s->tw, n, chain); }, chain);
+             [&] { return fehip::launch_interp_fft(3, fft_len, ib, s->sc, s->tw, n, chain); }, chain);
   } else {
     ok = s->timed(
              fehip::kKBinPlan, "bin_plan launch", [&] { return fehip::launch_bin_plan(s->gb, s->sc, chain); },
@@ -804,9 +801,6 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
     ok = s->timed(
              fehip::kKLgConvCols, "interp conv_cols launch",
              [&] { return fehip::launch_interp_fft(5, fft_len, ib, s->sc, s->tw, n, chain); }, chain) &&
-         s->timed(
-             fehip::kKLgPotentialT, "interp potential transpose launch",
-             [&] { return fehip::launch_interp_fft(6, fft_len, ib, s->sc, s->tw, n, chain); }, chain) &&
          s->timed(
              fehip::kKLgInverseRows, "interp inverse_rows launch",
              [&] { return fehip::launch_interp_fft(7, fft_len, ib, s->sc, s->tw, n, chain); }, chain);

@@ -59,9 +59,11 @@
 //   k_lg_inverse_rows     inverse row transforms, potentials per node and the
 //                         m2 phi0 sum
 //   k_lg_finalize_z       Z and its reciprocal
-// Every transform reads and writes contiguous sequences: the row spectra are
-// transposed (k_lg_transpose, 32 x 32 tiles through LDS) before each column
-// pass and back after it, and twiddles are staged in LDS.
+// Row transforms read and write contiguous rows; the column passes read
+// their columns straight from the row-major row spectra and write the
+// potential spectra back row-major (no transposes), with their blocks mapped
+// to columns XCD by XCD (col_block) so that the blocks sharing a cache line
+// of adjacent columns share one XCD's L2.  Twiddles are staged in LDS.
 //
 // The FFT length f is a power of two with f >= 2 m (m nodes per axis, read
 // on the device); the host picks it from a bound on m.  Rows and columns of
@@ -80,7 +82,7 @@ namespace {
 
 constexpr int kLgThreads = 256;
 // partial-sum slots: three per convolution-pass block, then one per row block
-constexpr int kLgMaxSpecBlocks = kLgMaxFft / 2 + 1;
+constexpr int kLgMaxSpecBlocks = kLgMaxColBlocks;
 constexpr int kLgRun = kChunk / kLgThreads;  // points per lane in k_lg_spread
 constexpr int kLgBoxesPerTile = kLgMaxTile * kLgMaxTile;
 static_assert(kLgBoxesPerTile == kLgThreads, "one box of the largest tile per thread in the box scan");
@@ -421,6 +423,18 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_gather(const int* __restrict_
 // Convolution.  Launch shapes per FFT length F: sequences of length F per
 // block so that small transforms still fill a workgroup.
 // ---------------------------------------------------------------------------
+
+// Column block of launch block b when `blocks` column blocks are spread over
+// col_launch(blocks) launch blocks: the blocks of XCD x (b % kLgColXcds,
+// the hardware's round-robin placement) take the x-th contiguous range, so
+// the columns of one cache line are read and written through one L2.  -1: a
+// padding block with no columns.
+__device__ __forceinline__ int col_block(int b, int blocks) {
+  const int per = (blocks + kLgColXcds - 1) / kLgColXcds;
+  const int c = (b % kLgColXcds) * per + b / kLgColXcds;
+  return c < blocks ? c : -1;
+}
+constexpr int col_launch(int blocks) { return (blocks + kLgColXcds - 1) / kLgColXcds * kLgColXcds; }
 template <int F>
 struct LgShape {
   static constexpr int G = F / 2;
@@ -438,42 +452,6 @@ __device__ __forceinline__ void lg_kernels(int dx, int dy, float h, float& k, fl
   const float oy = static_cast<float>(dy) * h;
   k1 = 1.0f / (1.0f + (ox * ox + oy * oy));
   k = k1 * k1;
-}
-
-// Transposes P planes of float2: plane p of src holds rows x cols (row stride
-// ld_s), of dst cols x rows (row stride ld_d).  rows (cols) is the node count
-// lg_nodes capped at rows_cap (cols_cap) when m_rows (m_cols) is set, else
-// the cap itself.  32 x 32 tiles through LDS, both sides coalesced.
-template <int P>
-__global__ __launch_bounds__(256) void k_lg_transpose(const float2* __restrict__ src, long long src_plane, int ld_s,
-                                                      float2* __restrict__ dst, long long dst_plane, int ld_d,
-                                                      int rows_cap, int m_rows, int cols_cap, int m_cols,
-                                                      const DeviceScalars* sc) {
-  chain_priority();
-  __shared__ float2 tile[32][33];
-  const int m = sc->lg_nodes;
-  const int rows = m_rows ? min(m, rows_cap) : rows_cap;
-  const int cols = m_cols ? min(m, cols_cap) : cols_cap;
-  const int r0 = blockIdx.y * 32;
-  const int c0 = blockIdx.x * 32;
-  if (r0 >= rows || c0 >= cols) return;  // whole block
-  const int tx = threadIdx.x & 31;
-  const int ty = threadIdx.x >> 5;
-  const float2* sp = src + blockIdx.z * src_plane;
-  float2* dp = dst + blockIdx.z * dst_plane;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = r0 + ty + 8 * i;
-    const int c = c0 + tx;
-    if (r < rows && c < cols) tile[ty + 8 * i][tx] = sp[static_cast<long long>(r) * ld_s + c];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = c0 + ty + 8 * i;
-    const int r = r0 + tx;
-    if (c < cols && r < rows) dp[static_cast<long long>(c) * ld_d + r] = tile[tx][ty + 8 * i];
-  }
 }
 
 // Row transforms of the four kernels on rows y in [0, min(m, F/2 + 1)) of the
@@ -522,15 +500,15 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_rows(const DeviceS
   }
 }
 
-// Column transforms of the row spectra, read from their transpose (kx-major,
-// row stride F/2 + 1, rows y < min(m, F/2 + 1) valid): P = K^r + i K1^r (even
-// in y) gives K^ and K1^ (real); Q = Bx + By, with Bx even and By odd in y,
-// gives Cx + i Cy where the kernel spectra of Kx and Ky are i Cx and i Cy.
-// Kept for ky in [0, F/2], kx-major: planes (K^, K1^) and (Cx, Cy); Cx is
-// even in ky, Cy odd.
+// Column transforms of the row spectra, read down the columns of the
+// row-major rows (row stride F/2 + 1, rows y < min(m, F/2 + 1) valid):
+// P = K^r + i K1^r (even in y) gives K^ and K1^ (real); Q = Bx + By, with Bx
+// even and By odd in y, gives Cx + i Cy where the kernel spectra of Kx and Ky
+// are i Cx and i Cy.  Kept for ky in [0, F/2], kx-major: planes (K^, K1^)
+// and (Cx, Cy); Cx is even in ky, Cy odd.
 template <int F>
 __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_cols(const DeviceScalars* sc,
-                                                                   const float2* __restrict__ k_cols,
+                                                                   const float2* __restrict__ k_rows,
                                                                    const float2* __restrict__ tw,
                                                                    float2* __restrict__ k_hat) {
   chain_priority();
@@ -539,7 +517,9 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_cols(const DeviceS
   __shared__ float2 lds[2 * S::KR * F];
   __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
-  const int col0 = blockIdx.x * S::KR;
+  const int cb = col_block(static_cast<int>(blockIdx.x), (S::H + S::KR - 1) / S::KR);
+  if (cb < 0) return;  // whole block
+  const int col0 = cb * S::KR;
   stage_twiddles<F, S::NT>(tws, tw);
   for (int e = threadIdx.x; e < S::KR * F; e += S::NT) {
     const int c = e / F;
@@ -549,9 +529,9 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_cols(const DeviceS
     const int ys = up ? y : F - y;
     float2 p = make_float2(0.0f, 0.0f), q = p;
     if (ys < m && kx < S::H) {
-      const int at = kx * S::H + ys;
-      p = k_cols[at];
-      const float2 b = k_cols[HH + at];  // (Bx, By)
+      const int at = ys * S::H + kx;
+      p = k_rows[at];
+      const float2 b = k_rows[HH + at];  // (Bx, By)
       q = make_float2(b.x + (up ? b.y : -b.y), 0.0f);
     }
     lds[(2 * c) * F + y] = p;
@@ -620,20 +600,21 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
   }
 }
 
-// Column pass on the transposed charge spectra (kx-major, row stride F/2,
-// ky... y < m valid): for each column kx, forward transforms of M0, M1x, M1y
-// (rows >= m are the zero padding), then per ky
+// Column pass down the columns of the row-major charge spectra (row stride
+// F/2 + 1, rows y < m valid): for each column kx, forward transforms of M0,
+// M1x, M1y (rows >= m are the zero padding), then per ky
 //   Phi0 = M0 K^,  Xi_x = i Cx M0 - K^ M1x,  Xi_y = i Cy M0 - K^ M1y,
 // the spectral sums of Z (weight 2 for 0 < kx < F/2, whose mirror column is
 // not stored; 1/F^2 applied later)
 //   s1 = |M0|^2 K1^,  s3 = Re(conj(M1) . i C M0),  s4 = |M1|^2 K^,
-// inverse transforms, rows y < m written kx-major.
+// inverse transforms, rows y < m written back row-major.  A padding block
+// (col_block) writes zero partial sums.
 template <int F>
 __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceScalars* sc,
-                                                                 const float2* __restrict__ cols_in,
+                                                                 const float2* __restrict__ rows_in,
                                                                  const float2* __restrict__ k_hat,
                                                                  const float2* __restrict__ tw,
-                                                                 float2* __restrict__ cols_out, long long plane,
+                                                                 float2* __restrict__ rows_out, long long plane,
                                                                  double* __restrict__ zpart) {
   chain_priority();
   using S = LgShape<F>;
@@ -642,17 +623,26 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
   __shared__ float2 lds[3 * C * F];
   __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
-  const int col0 = blockIdx.x * C;
+  const int cb = col_block(static_cast<int>(blockIdx.x), (S::H + C - 1) / C);
+  if (cb < 0) {  // whole block
+    if (threadIdx.x == 0) {
+      zpart[3 * blockIdx.x] = 0.0;
+      zpart[3 * blockIdx.x + 1] = 0.0;
+      zpart[3 * blockIdx.x + 2] = 0.0;
+    }
+    return;
+  }
+  const int col0 = cb * C;
   stage_twiddles<F, S::NT>(tws, tw);
   for (int e = threadIdx.x; e < C * F; e += S::NT) {
     const int c = e / F;
     const int y = e - c * F;
     const int kx = col0 + c;
     const bool live = y < m && kx < S::H;
-    const long long at = static_cast<long long>(kx) * S::G + y;
+    const long long at = static_cast<long long>(y) * S::H + kx;
 #pragma unroll
     for (int ch = 0; ch < 3; ++ch) {
-      lds[(ch * C + c) * F + y] = live ? cols_in[ch * plane + at] : make_float2(0.0f, 0.0f);
+      lds[(ch * C + c) * F + y] = live ? rows_in[ch * plane + at] : make_float2(0.0f, 0.0f);
     }
   }
   __syncthreads();
@@ -697,9 +687,9 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
     const int y = e - c * S::G;
     const int kx = col0 + c;
     if (y >= m || kx >= S::H) continue;
-    const long long at = static_cast<long long>(kx) * S::G + y;
+    const long long at = static_cast<long long>(y) * S::H + kx;
 #pragma unroll
-    for (int ch = 0; ch < 3; ++ch) cols_out[ch * plane + at] = lds[(ch * C + c) * F + y];
+    for (int ch = 0; ch < 3; ++ch) rows_out[ch * plane + at] = lds[(ch * C + c) * F + y];
   }
   s1 = block_sum<S::NT>(s1);
   s3 = block_sum<S::NT>(s3);
@@ -801,51 +791,38 @@ __global__ __launch_bounds__(256) void k_lg_finalize_z(const double* __restrict_
 }
 
 // Buffers of one FFT length.  Spectra planes are G * H float2 (G = F/2,
-// H = F/2 + 1) apart: A holds the charge row spectra, then the potential
-// columns; B the charge columns, then the potential row spectra.  The kernel
-// row spectra and the kernel spectrum share a buffer (H * H float2 planes).
+// H = F/2 + 1) apart: A holds the charge row spectra, B the potential row
+// spectra.  The kernel row spectra and the kernel spectrum have a buffer
+// each (H * H float2 planes).
 template <int F>
 hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const float2* tw, int n,
                          hipStream_t stream) {
   using S = LgShape<F>;
   const int kblocks = (S::H + S::KR - 1) / S::KR;
   const int rblocks = (S::G + S::CR - 1) / S::CR;
-  const int cblocks = (S::H + S::CC - 1) / S::CC;
+  const int cblocks = col_launch((S::H + S::CC - 1) / S::CC);
   const long long plane = static_cast<long long>(S::G) * S::H;
-  const long long kplane = static_cast<long long>(S::H) * S::H;
   double* spec_part = ib.z_partial;
   double* row_part = ib.z_partial + 3 * kLgMaxSpecBlocks;
-  const int t32h = (S::H + 31) / 32;
-  const int t32g = (S::G + 31) / 32;
+  static_assert(col_launch((S::H + S::CC - 1) / S::CC) <= kLgMaxSpecBlocks, "a partial-sum slot per column block");
   switch (which) {
     case 0:
       k_lg_kernel_rows<F><<<kblocks, S::NT, 0, stream>>>(sc, tw, ib.k_rows);
       break;
-    case 1:  // (K^r, K1^r), (Bx, By): rows y < min(m, H) -> kx-major
-      k_lg_transpose<2><<<dim3(t32h, t32h, 2), 256, 0, stream>>>(ib.k_rows, kplane, S::H, ib.k_cols, kplane, S::H,
-                                                                  S::H, 1, S::H, 0, sc);
-      break;
     case 2:
-      k_lg_kernel_cols<F><<<kblocks, S::NT, 0, stream>>>(sc, ib.k_cols, tw, ib.k_rows);
+      k_lg_kernel_cols<F><<<col_launch(kblocks), S::NT, 0, stream>>>(sc, ib.k_rows, tw, ib.k_cols);
       break;
     case 3:
       k_lg_charge_rows<F><<<rblocks, S::NT, 0, stream>>>(sc, ib.charge, tw, ib.spec_a, plane);
       break;
-    case 4:  // charge spectra, m rows x H -> kx-major (row stride G)
-      k_lg_transpose<3><<<dim3(t32h, t32g, 3), 256, 0, stream>>>(ib.spec_a, plane, S::H, ib.spec_b, plane, S::G,
-                                                                  S::G, 1, S::H, 0, sc);
-      break;
     case 5:
-      k_lg_conv_cols<F><<<cblocks, S::NT, 0, stream>>>(sc, ib.spec_b, ib.k_rows, tw, ib.spec_a, plane, spec_part);
-      break;
-    case 6:  // potential spectra, H x m (kx-major) -> m rows x H
-      k_lg_transpose<3><<<dim3(t32g, t32h, 3), 256, 0, stream>>>(ib.spec_a, plane, S::G, ib.spec_b, plane, S::H,
-                                                                  S::H, 0, S::G, 1, sc);
+      k_lg_conv_cols<F><<<cblocks, S::NT, 0, stream>>>(sc, ib.spec_a, ib.k_cols, tw, ib.spec_b, plane, spec_part);
       break;
     case 7:
       k_lg_inverse_rows<F><<<rblocks, S::NT, 0, stream>>>(sc, ib.spec_b, plane, ib.charge, tw, ib.field, row_part);
       k_lg_finalize_z<<<1, 256, 0, stream>>>(spec_part, cblocks, row_part, rblocks, n, F, sc);
       break;
+
     default:
       return hipErrorInvalidValue;
   }

@@ -98,8 +98,13 @@ __host__ __device__ inline int lg_tile_for(int nb) {
   return tile;
 }
 inline int lg_max_items(int n) { return (n + kChunk - 1) / kChunk + kLgMaxTilesAxis * kLgMaxTilesAxis; }
-// three spectral sums per column-pass block (<= f/2 + 1 blocks), one per row block (<= f/2)
-constexpr int kLgZPartials = 3 * (kLgMaxFft / 2 + 1) + kLgMaxFft / 2;
+// Column passes of the interpolation grid map their blocks to columns XCD by
+// XCD (block b on XCD b % kLgColXcds takes the next column of that XCD's
+// contiguous range), so their launches are rounded up to a multiple of it.
+constexpr int kLgColXcds = 8;
+constexpr int kLgMaxColBlocks = (kLgMaxFft / 2 + 1 + kLgColXcds - 1) / kLgColXcds * kLgColXcds;
+// three spectral sums per column-pass block, one per row block (<= f/2)
+constexpr int kLgZPartials = 3 * kLgMaxColBlocks + kLgMaxFft / 2;
 
 enum KernelId : int {
   kKStats = 0,
@@ -123,12 +128,9 @@ enum KernelId : int {
   kKLgSpread,
   kKLgGather,
   kKLgKernelRows,
-  kKLgKernelT,
   kKLgKernelCols,
   kKLgChargeRows,
-  kKLgChargeT,
   kKLgConvCols,
-  kKLgPotentialT,
   kKLgInverseRows,
   kKFinalize,
   kKernelCount
@@ -165,11 +167,11 @@ struct GridBuffers {
 struct InterpBuffers {
   float* charge = nullptr;     // 4 planes of m*m: node moments m0, m1x, m1y, m2 (offsets in units of h)
   float4* field = nullptr;     // m*m potentials (phi0, xi_x, xi_y, 0)
-  float2* k_rows = nullptr;    // 2 planes of (G+1)^2: kernel row spectra ((K^r, K1^r), (Bx, By)),
-                               // then the kernel spectrum quadrant ((K^, K1^), (Cx, Cy)), kx-major
-  float2* k_cols = nullptr;    // 2 planes of (G+1)^2: the row spectra transposed
-  float2* spec_a = nullptr;    // 3 planes of G*(G+1): charge row spectra, then potential columns
-  float2* spec_b = nullptr;    // 3 planes of G*(G+1): charge columns, then potential row spectra
+  float2* k_rows = nullptr;    // 2 planes of (G+1)^2: kernel row spectra ((K^r, K1^r), (Bx, By)), row-major
+  float2* k_cols = nullptr;    // 2 planes of (G+1)^2: the kernel spectrum quadrant ((K^, K1^), (Cx, Cy)),
+                               // kx-major
+  float2* spec_a = nullptr;    // 3 planes of G*(G+1): charge row spectra, row-major
+  float2* spec_b = nullptr;    // 3 planes of G*(G+1): potential row spectra, row-major
   double* z_partial = nullptr; // kLgZPartials: sums of the normaliser per block
   int* tile_count = nullptr;   // kMaxTiles, zero between iterations
   int* tile_cursor = nullptr;  // kMaxTiles
@@ -235,9 +237,8 @@ hipError_t launch_interp_bin_scatter(const float2* y_cur, DeviceScalars* sc, Int
 // fft_len bounds the node count and so the tile size the spread window needs.
 hipError_t launch_interp_spread(DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len, hipStream_t stream);
 hipError_t launch_interp_gather(const DeviceScalars* sc, InterpBuffers& ib, hipStream_t stream);
-// which: 0 kernel rows, 1 kernel transpose, 2 kernel cols, 3 charge rows,
-// 4 charge transpose, 5 conv cols, 6 potential transpose, 7 inverse rows
-// (+ normaliser)
+// which: 0 kernel rows, 2 kernel cols, 3 charge rows, 5 conv cols, 7 inverse
+// rows (+ normaliser); other values are invalid
 hipError_t launch_interp_fft(int which, int fft_len, InterpBuffers& ib, DeviceScalars* sc, const float2* tw, int n,
                              hipStream_t stream);
 
