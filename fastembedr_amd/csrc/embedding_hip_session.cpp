@@ -185,20 +185,16 @@ struct fastembedr_hip_tsne {
   // issue priority (chain_priority).  Set by FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU,
   // else (attract_share_auto) after each tile build from the tiled P's mean
   // run length, which sets the attraction's cost per entry against the
-  // interpolation grid chain's per point (late window, interleaved repeats:
-  // config 2, runs of 25k slots: 1 per CU 3178 it/s, 1.25 3166, 1.5 3560,
-  // 1.75 3534, 2 3489, 2.25 3376, 2.5 3192; config 4, runs of 7.4k slots:
-  // 1.5 685, 2 781, 2.5 830, 2.75 835, 3 813): 1.5 at 16K slots or more, 2.5
-  // at 8K or fewer, linear between; half a workgroup more beside the shorter
-  // bilinear grid chain (config 2: 1.5 3500, 1.75 3611, 2 3731, 2.5 3624).
-  // Alone it takes one workgroup per row block.
+  // chain's per point: 2 at 16K slots per run or more, 2.5 at 8K or fewer,
+  // linear between (late window, interleaved repeats: config 2, runs of 25k
+  // slots, interpolation grid: 1 per CU 3178 it/s, 1.25 3166, 1.5 3507, 1.75
+  // 3535, 2 3584, 2.25 3376, 2.5 3192; bilinear grid: 1.5 3500, 1.75 3611,
+  // 2 3731, 2.5 3624; config 4, runs of 7.4k slots: 1.5 685, 2 781, 2.5 830,
+  // 2.75 835, 3 813).  Alone it takes one workgroup per row block.
   double attract_shared_per_cu = 2.0;
   bool attract_share_auto = true;
   double attract_share_base = 2.0;  // from the last tile build
-  double attract_share() const {
-    if (!attract_share_auto) return attract_shared_per_cu;
-    return attract_share_base + (repulsion == FASTEMBEDR_HIP_REPULSION_LAGRANGE ? 0.0 : 0.5);
-  }
+  double attract_share() const { return attract_share_auto ? attract_share_base : attract_shared_per_cu; }
   // Workgroups per CU of the helper launch that joins the attraction on the
   // main stream once the repulsion chain is done, taking over the row blocks
   // still unclaimed (FASTEMBEDR_HIP_ATTRACT_HELPER_PER_CU; 0: none).  The
@@ -523,7 +519,7 @@ bool ensure_tiles(fastembedr_hip_tsne* s, hipStream_t st) {
     return false;
   }
   const double run = count > 0 ? static_cast<double>(total) / count : 0.0;
-  s->attract_share_base = std::clamp(2.5 - (run - 8192.0) / 8192.0, 1.5, 2.5);
+  s->attract_share_base = std::clamp(2.5 - (run - 8192.0) / 16384.0, 2.0, 2.5);
   return true;
 }
 
