@@ -149,6 +149,19 @@ struct fastembedr_hip_tsne {
   hipEvent_t ev_ready = nullptr;  // grid geometry set (main)
   hipEvent_t ev_attr = nullptr;   // attraction done (side_attr)
   hipEvent_t ev_kern = nullptr;   // kernel spectrum done (side_kern)
+  hipEvent_t ev_home = nullptr;   // the latest update done (settle)
+  // The stream that holds the latest update: the next attraction follows it
+  // there without a wait.  With update_on_chain an overlapped iteration runs
+  // its update on the chain's stream (after the chain, waiting for the
+  // attraction's event), so the two streams trade roles every iteration;
+  // settle() hands the state back to `stream` for everything else.
+  hipStream_t home = nullptr;
+  // FASTEMBEDR_HIP_UPDATE_ON_CHAIN=0: the update always on `stream`, after
+  // waiting for the chain's event.  A wait for an event that another stream
+  // has yet to signal cost ~18 us here, one for an event already signalled
+  // ~6 us; the chain ends after the attraction, so its stream should carry
+  // the update.
+  bool update_on_chain = true;
   Arena arena;
   Arena work_arena;         // working-order CSR copies, permutations, state double buffers
   Arena tile_arena;         // tiled P for the attraction and its build scratch
@@ -288,7 +301,7 @@ struct fastembedr_hip_tsne {
     for (hipStream_t st : {side_attr, side_kern}) {
       if (st != nullptr) (void)hipStreamSynchronize(st);
     }
-    for (hipEvent_t e : {ev_layout, ev_ready, ev_attr, ev_kern}) {
+    for (hipEvent_t e : {ev_layout, ev_ready, ev_attr, ev_kern, ev_home}) {
       if (e != nullptr) (void)hipEventDestroy(e);
     }
     tile_arena.release();
@@ -532,15 +545,22 @@ int per_xcd_for(const fastembedr_hip_tsne* s, double per_cu) {
 // stream st (the main stream when null); `shared`: other kernels run beside
 // it, and (tiled attraction) a helper launch follows on the main stream
 // (enqueue_attract_helper) once they are done.
+// done (optional): recorded on st right after the kernel, ahead of the
+// timing event that closes its span, so that a stream waiting for it does
+// not wait behind that event as well.
 bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggeration, hipStream_t st = nullptr,
-                     bool shared = false) {
+                     bool shared = false, hipEvent_t done = nullptr) {
   if (st == nullptr) st = s->stream;
+  auto then_done = [&](hipError_t e) { return e == hipSuccess && done != nullptr ? hipEventRecord(done, st) : e; };
   s->helper_pending = 0;
   s->helper_span_open = false;
   if (!s->attract_tiled) {
     return s->timed(
         fehip::kKAttract, "attract launch",
-        [&] { return fehip::launch_attract(s->work_p(), y_cur, s->attr, exaggeration, s->lanes, s->xcds, st); }, st);
+        [&] {
+          return then_done(fehip::launch_attract(s->work_p(), y_cur, s->attr, exaggeration, s->lanes, s->xcds, st));
+        },
+        st);
   }
   if (!ensure_tiles(s, st)) return false;  // may set attract_share_base
   const double per_cu = s->attract_share();
@@ -551,7 +571,10 @@ bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggera
   if (helper == 0) {
     return s->timed(
         fehip::kKAttract, "attract launch",
-        [&] { return fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->xcds, slots, 0, st); },
+        [&] {
+          return then_done(
+              fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->xcds, slots, 0, st));
+        },
         st);
   }
   // the timed span runs from the primary's start to the point where the
@@ -670,11 +693,27 @@ bool write_interp_spec(fastembedr_hip_tsne* s, int order) {
 // spectrum run on the side streams and the main stream waits for them (before
 // the convolution and before whatever follows this call); without it
 // everything runs on the main stream.
+// Hands the latest update back to the main stream (`stream` waits for
+// `home`), for work that is enqueued there.
+bool settle(fastembedr_hip_tsne* s) {
+  if (s->home == s->stream) return true;
+  if (!hip_ok(hipEventRecord(s->ev_home, s->home), "hipEventRecord(home)") ||
+      !hip_ok(hipStreamWaitEvent(s->stream, s->ev_home, 0), "hipStreamWaitEvent(home)")) {
+    return false;
+  }
+  s->home = s->stream;
+  return true;
+}
+
 bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float exaggeration, bool overlap,
                              bool finalize = false) {
   const int n = s->n;
   fehip::InterpBuffers& ib = s->ib;
-  hipStream_t main = s->stream;
+  // The attraction's stream: the one that holds the latest update (the other
+  // of the pair runs the chain); everything else starts from `stream`.
+  if (!(overlap && s->attract_main) && !settle(s)) return false;
+  hipStream_t main = s->home;
+  hipStream_t other = main == s->stream ? s->side_attr : s->stream;
   // Two arrangements of an overlapped iteration.  Attraction beside (the
   // default): the attraction runs on side_attr from the top of the
   // iteration, the repulsion chain on the main stream, and a helper launch
@@ -684,8 +723,8 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   // ends last, the update follows it on its own stream when that is the
   // attraction.
   const bool swap = overlap && s->attract_main;
-  hipStream_t sa = overlap && !swap ? s->side_attr : main;  // attraction
-  hipStream_t chain = swap ? s->side_attr : main;           // repulsion chain
+  hipStream_t sa = overlap && !swap ? other : main;  // attraction
+  hipStream_t chain = swap ? other : main;           // repulsion chain
   hipStream_t sk = overlap ? s->side_kern : main;
   if (lg) s->lg_last_fft = fft_len;
   // The attraction needs only differences y_i - y_j, so it reads the stored
@@ -724,7 +763,9 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
                   (swap && !fin_chain && !hip_ok(hipStreamWaitEvent(chain, s->ev_ready, 0), "hipStreamWaitEvent(chain)")))) {
     return false;
   }
-  if (swap && !enqueue_attract(s, s->y_a(), exaggeration, main, true)) return false;
+  if (swap && !enqueue_attract(s, s->y_a(), exaggeration, main, true, s->update_on_chain ? s->ev_attr : nullptr)) {
+    return false;
+  }
   if (lg) {
     static constexpr int kIds[2] = {fehip::kKLgKernelRows, fehip::kKLgKernelCols};
     static constexpr int kSteps[2] = {0, 2};
@@ -810,7 +851,14 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   }
   if (!ok) return false;
   if (swap) {
-    // the main stream (attraction) waits for the chain
+    if (s->update_on_chain) {
+      // the chain's stream waits for the attraction (ev_attr, recorded right
+      // after it) and carries the update
+      if (!hip_ok(hipStreamWaitEvent(chain, s->ev_attr, 0), "hipStreamWaitEvent(chain, attraction)")) return false;
+      s->home = chain;
+      return true;
+    }
+    // the attraction's stream waits for the chain and carries the update
     return hip_ok(hipEventRecord(s->ev_attr, chain), "hipEventRecord(chain)") &&
            hip_ok(hipStreamWaitEvent(main, s->ev_attr, 0), "hipStreamWaitEvent(main, chain)");
   }
@@ -824,11 +872,14 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
 bool enqueue_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up, bool overlap,
                        bool finalize) {
   return enqueue_gradient_pieces(s, lg, fft_len, up.exaggeration, overlap, finalize) &&
-         s->timed(fehip::kKUpdate, "update launch", [&] {
-           return fehip::launch_update(fehip::kModeUpdate, s->y_b, s->attr, s->y_a(), s->update(), s->gains(), nullptr,
-                                       nullptr, s->gb, up, s->partial, s->sc, s->n, s->stream,
-                                       lg ? s->ib.field : nullptr);
-         });
+         s->timed(
+             fehip::kKUpdate, "update launch",
+             [&] {
+               return fehip::launch_update(fehip::kModeUpdate, s->y_b, s->attr, s->y_a(), s->update(), s->gains(),
+                                           nullptr, nullptr, s->gb, up, s->partial, s->sc, s->n, s->home,
+                                           lg ? s->ib.field : nullptr);
+             },
+             s->home);
 }
 
 // Captures enqueue_iteration() on the main stream alone (no side branches,
@@ -855,7 +906,7 @@ bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, con
   using IterGraph = fastembedr_hip_tsne::IterGraph;
   // Graph nodes keep the streams' order but not the tile build's host-side
   // bookkeeping: build the tiles eagerly first.
-  if (!ensure_tiles(s, s->stream)) return false;
+  if (!settle(s) || !ensure_tiles(s, s->stream)) return false;
   auto bits = [](float v) {
     std::uint32_t u;
     std::memcpy(&u, &v, sizeof(u));
@@ -935,7 +986,7 @@ bool wait_ring(fastembedr_hip_tsne* s, unsigned int seq, int* boxes) {
       return true;
     }
     if (spin % 64 == 0) {
-      const hipError_t q = hipStreamQuery(s->stream);
+      const hipError_t q = hipStreamQuery(s->home);  // holds the latest update, after everything before it
       if (q == hipSuccess) {
         const unsigned long long again = __atomic_load_n(slot, __ATOMIC_ACQUIRE);
         if (static_cast<unsigned int>(again >> 32) == seq) continue;
@@ -1086,10 +1137,12 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
       !hip_ok(hipEventCreateWithFlags(&s->ev_layout, hipEventDisableTiming), "hipEventCreate") ||
       !hip_ok(hipEventCreateWithFlags(&s->ev_ready, hipEventDisableTiming), "hipEventCreate") ||
       !hip_ok(hipEventCreateWithFlags(&s->ev_attr, hipEventDisableTiming), "hipEventCreate") ||
-      !hip_ok(hipEventCreateWithFlags(&s->ev_kern, hipEventDisableTiming), "hipEventCreate")) {
+      !hip_ok(hipEventCreateWithFlags(&s->ev_kern, hipEventDisableTiming), "hipEventCreate") ||
+      !hip_ok(hipEventCreateWithFlags(&s->ev_home, hipEventDisableTiming), "hipEventCreate")) {
     delete s;
     return 1;
   }
+  s->home = s->stream;
   hipEvent_t t0, t1;
   (void)hipEventCreate(&t0);
   (void)hipEventCreate(&t1);
@@ -1331,6 +1384,7 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
     }
   }
   if (const char* v = std::getenv("FASTEMBEDR_HIP_ATTRACT_MAIN")) s->attract_main = std::strcmp(v, "0") != 0;
+  if (const char* v = std::getenv("FASTEMBEDR_HIP_UPDATE_ON_CHAIN")) s->update_on_chain = std::strcmp(v, "0") != 0;
   s->graph_capture = graph_capture_enabled();
   if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {
     delete s;
@@ -1618,6 +1672,11 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
     return 1;
   }
   if (n_iter == 0) return 0;
+  // every return leaves the latest update on the main stream
+  struct SettleOnExit {
+    fastembedr_hip_tsne* s;
+    ~SettleOnExit() { (void)settle(s); }
+  } settle_on_exit{s};
   fehip::UpdateParams up;
   up.exaggeration = exaggeration;
   up.momentum = momentum;
@@ -1661,7 +1720,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
   bool pending = false;
   auto finish_pending = [&](unsigned long long* ring) {
     pending = false;
-    return s->timed(fehip::kKFinalize, "finalize launch", [&] {
+    return settle(s) && s->timed(fehip::kKFinalize, "finalize launch", [&] {
       return fehip::launch_finalize_stats(s->partial, n, s->gb.g, s->sc, ring, s->stream);
     });
   };
@@ -1672,7 +1731,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
     // finished statistics).
     if (s->reorder_period > 0 && s->since_reorder >= s->reorder_gap) {
       if (pending && !finish_pending(lg ? s->lg_ring_dev : nullptr)) return 1;
-      if (!s->timed(fehip::kKRenumber, "renumber", [&] { return enqueue_renumber(s); })) return 1;
+      if (!settle(s) || !s->timed(fehip::kKRenumber, "renumber", [&] { return enqueue_renumber(s); })) return 1;
       s->reorder_gap = s->reorder_gap == 0 ? s->reorder_period : 2 * s->reorder_gap;
     }
     ++s->since_reorder;
@@ -1710,6 +1769,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
   }
   // the last update's statistics (no box count is needed from them)
   if (pending && !finish_pending(nullptr)) return 1;
+  if (!settle(s)) return 1;
   if (!s->timed(fehip::kKCommit, "commit launch",
                 [&] { return fehip::launch_commit(s->y_a(), s->sc, n, s->stream); })) {
     return 1;
