@@ -23,8 +23,10 @@ interpolation grid):
     graph keys, and the host learns box counts from the device-indexed ring)
     the final KL agrees within 1 %;
   * the switch's off values (and unset) turn capture off;
-  * both arrangements of the eager overlapped iteration (the attraction on
-    the main stream with the chain beside it, the default, and the attraction
+  * the arrangements of the eager overlapped iteration (the attraction on
+    the stream of the previous update with the chain beside it and the
+    update after the chain, the default; the same with the update always on
+    the main stream, FASTEMBEDR_HIP_UPDATE_ON_CHAIN=0; and the attraction
     beside the chain with a helper launch, FASTEMBEDR_HIP_ATTRACT_MAIN=0) end
     within 1 % of the single-stream replayed run's KL;
   * a closed session gives its device memory back, replayed or not (graphs
@@ -135,11 +137,12 @@ def test_replayed_schedule_kl(hip, prob, repulsion):
     assert abs(kl_g - kl_e) <= KL_TOL * kl_e
 
 
-@pytest.mark.parametrize("arrangement", ["1", "0"], ids=["attraction_main", "attraction_beside"])
-def test_overlap_arrangements_kl(hip, prob, arrangement):
+@pytest.mark.parametrize("arrangement,on_chain", [("1", "1"), ("1", "0"), ("0", "1")],
+                         ids=["attraction_main", "attraction_main_update_on_main", "attraction_beside"])
+def test_overlap_arrangements_kl(hip, prob, arrangement, on_chain):
     x, idx, dist, y0 = prob
-    extra = {"FASTEMBEDR_HIP_ATTRACT_MAIN": arrangement}
-    _say(f"case: FASTEMBEDR_HIP_ATTRACT_MAIN={arrangement}, eager vs replayed, interpolation grid, 60 + 60 iterations")
+    extra = {"FASTEMBEDR_HIP_ATTRACT_MAIN": arrangement, "FASTEMBEDR_HIP_UPDATE_ON_CHAIN": on_chain}
+    _say(f"case: {extra}, eager vs replayed, interpolation grid, 60 + 60 iterations")
     _, y_e, kl_e, info_e = _schedule(hip, idx, dist, y0, _lib.REPULSION_LAGRANGE, None, 60, 60, extra)
     _, y_g, kl_g, info = _schedule(hip, idx, dist, y0, _lib.REPULSION_LAGRANGE, "1", 60, 60)
     _say(f"  KL eager {kl_e:.5f}, graph {kl_g:.5f}, {info}")
