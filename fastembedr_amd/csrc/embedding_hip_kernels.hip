@@ -352,34 +352,60 @@ __global__ __launch_bounds__(kPointThreads) void k_bin_count(const float2* __res
   }
 }
 
-// Exclusive scan of up to kMaxTiles counts by one block of kPlanThreads
-// threads (kPlanPer consecutive entries per thread, then a Hillis-Steele scan
-// of the thread sums).  A block of 4 waves finds room on a CU beside the
-// attraction sooner than a block of 16 would.
+// Exclusive scans of two arrays of up to kMaxTiles counts by one block of
+// kPlanThreads threads: kPlanPer consecutive entries per thread, the thread
+// sums scanned within each wave by shuffles and across the block's waves
+// through LDS (one barrier).  A block of 4 waves finds room on a CU beside
+// the attraction sooner than a block of 16 would.
 constexpr int kPlanThreads = 256;
 constexpr int kPlanPer = kMaxTiles / kPlanThreads;
+constexpr int kPlanWaves = kPlanThreads / kWave;
 static_assert(kPlanPer * kPlanThreads == kMaxTiles, "whole entries per thread");
-__device__ int block_exclusive_scan(int (&v)[kPlanPer], int* part) {
+__device__ void block_exclusive_scan2(int (&a)[kPlanPer], int (&b)[kPlanPer], int* part, int& total_a,
+                                      int& total_b) {
   const int t = threadIdx.x;
-  int s = 0;
-  for (int q = 0; q < kPlanPer; ++q) s += v[q];
-  part[t] = s;
-  __syncthreads();
-  for (int off = 1; off < kPlanThreads; off <<= 1) {
-    const int add = t >= off ? part[t - off] : 0;
-    __syncthreads();
-    part[t] += add;
-    __syncthreads();
-  }
-  const int total = part[kPlanThreads - 1];
-  int run = part[t] - s;
+  const int lane = t & (kWave - 1);
+  const int wave = t / kWave;
+  int sa = 0, sb = 0;
   for (int q = 0; q < kPlanPer; ++q) {
-    const int c = v[q];
-    v[q] = run;
-    run += c;
+    sa += a[q];
+    sb += b[q];
+  }
+  int ia = sa, ib = sb;  // inclusive scans over the wave
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int xa = __shfl_up(ia, off, kWave);
+    const int xb = __shfl_up(ib, off, kWave);
+    if (lane >= off) {
+      ia += xa;
+      ib += xb;
+    }
+  }
+  if (lane == kWave - 1) {
+    part[wave] = ia;
+    part[kPlanWaves + wave] = ib;
   }
   __syncthreads();
-  return total;
+  int ba = 0, bb = 0;  // the sums of the waves before this one
+  total_a = 0;
+  total_b = 0;
+#pragma unroll
+  for (int w = 0; w < kPlanWaves; ++w) {
+    if (w < wave) {
+      ba += part[w];
+      bb += part[kPlanWaves + w];
+    }
+    total_a += part[w];
+    total_b += part[kPlanWaves + w];
+  }
+  int ra = ba + ia - sa, rb = bb + ib - sb;
+  for (int q = 0; q < kPlanPer; ++q) {
+    const int ca = a[q], cb = b[q];
+    a[q] = ra;
+    b[q] = rb;
+    ra += ca;
+    rb += cb;
+  }
 }
 
 // tiles < 0: the interpolation grid's tile count, lg_tiles_axis^2, read on the
@@ -401,8 +427,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_bin_plan(int* __restrict__ til
     chunks[q] = (cnt[q] + kChunk - 1) / kChunk;
     base[q] = chunks[q];
   }
-  block_exclusive_scan(start, part);
-  const int total_items = block_exclusive_scan(base, part);
+  int total_points = 0, total_items = 0;
+  block_exclusive_scan2(start, base, part, total_points, total_items);
+  (void)total_points;
   for (int q = 0; q < kPlanPer; ++q) {
     const int t = threadIdx.x * kPlanPer + q;
     if (t >= tiles) continue;
