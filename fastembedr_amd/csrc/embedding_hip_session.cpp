@@ -140,14 +140,15 @@ struct fastembedr_hip_tsne {
   hipStream_t stream = nullptr;
   // Side streams of run(): the attraction depends only on the stored layout
   // and the kernel spectrum only on the grid geometry, so they run beside the
-  // binning, spreading and convolution of the main stream, which waits for
-  // them (events) before the convolution and the update.  All streams have
+  // binning, spreading and convolution of the repulsion chain, which waits
+  // for the spectrum (an event) before the convolution; the attraction and
+  // the chain share `stream` and side_attr (see `home`).  All streams have
   // the default priority.
   hipStream_t side_attr = nullptr;
   hipStream_t side_kern = nullptr;
-  hipEvent_t ev_layout = nullptr; // stored layout written (main)
-  hipEvent_t ev_ready = nullptr;  // grid geometry set (main)
-  hipEvent_t ev_attr = nullptr;   // attraction done (side_attr)
+  hipEvent_t ev_layout = nullptr; // stored layout written (the previous update's stream)
+  hipEvent_t ev_ready = nullptr;  // grid geometry set (the chain's stream)
+  hipEvent_t ev_attr = nullptr;   // attraction done, or (update on main) the chain done
   hipEvent_t ev_kern = nullptr;   // kernel spectrum done (side_kern)
   hipEvent_t ev_home = nullptr;   // the latest update done (settle)
   // The stream that holds the latest update: the next attraction follows it
@@ -214,13 +215,13 @@ struct fastembedr_hip_tsne {
   // pair adapts to the balance of the two: a short chain leaves the helper
   // most of the attraction, a long one leaves it nothing.
   double attract_helper_per_cu = 1.0;
-  // The attraction on the main stream and the repulsion chain on side_attr
-  // (the default; FASTEMBEDR_HIP_ATTRACT_MAIN=0: the attraction on side_attr
-  // with a helper launch on the main stream after the chain); the attraction
-  // then takes attract_share() workgroups per CU and no helper.  At
-  // config 2 the chain ends last, so the update follows the chain's event
-  // (3270 against 3205 it/s in the late window, 3409 against 3340 over the
-  // whole schedule).
+  // The attraction on the stream of the previous update and the repulsion
+  // chain on the other one of `stream` and side_attr (the default;
+  // FASTEMBEDR_HIP_ATTRACT_MAIN=0: the attraction on side_attr with a helper
+  // launch on the main stream after the chain, which runs on `stream`); the
+  // attraction then takes attract_share() workgroups per CU and no helper
+  // (3270 against 3205 it/s in the late window at config 2, 3409 against
+  // 3340 over the whole schedule).
   bool attract_main = true;
   int helper_pending = 0;            // helper workgroups per XCD still to launch this iteration
   int helper_slots = 0;              // the primary's workgroups per XCD
@@ -714,14 +715,13 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   if (!(overlap && s->attract_main) && !settle(s)) return false;
   hipStream_t main = s->home;
   hipStream_t other = main == s->stream ? s->side_attr : s->stream;
-  // Two arrangements of an overlapped iteration.  Attraction beside (the
-  // default): the attraction runs on side_attr from the top of the
-  // iteration, the repulsion chain on the main stream, and a helper launch
-  // joins the attraction once the chain is done.  Attraction on main
-  // (attract_main): the chain runs on side_attr and the attraction on the
-  // main stream after the statistics' finish, so that whichever of the two
-  // ends last, the update follows it on its own stream when that is the
-  // attraction.
+  // Two arrangements of an overlapped iteration.  Attraction first
+  // (attract_main, the default): the attraction runs on the stream of the
+  // previous update, right behind it, and the chain on the other stream,
+  // which then carries the update (update_on_chain) or hands it back.
+  // Attraction beside (attract_main off): the attraction runs on side_attr
+  // from the top of the iteration, the chain on `stream`, and a helper
+  // launch joins the attraction once the chain is done.
   const bool swap = overlap && s->attract_main;
   hipStream_t sa = overlap && !swap ? other : main;  // attraction
   hipStream_t chain = swap ? other : main;           // repulsion chain
