@@ -110,15 +110,76 @@ __device__ double block_sum(double v) {
   return t;
 }
 
+// Exclusive scans of two arrays held PER consecutive entries per thread by a
+// block of NT threads (entry q of thread t is element t * PER + q): the
+// thread sums are scanned within each wave by shuffles and across the
+// block's waves through part (2 * NT / kWave ints; one barrier).  total_a and
+// total_b receive the sums over the block.
+template <int PER, int NT>
+__device__ __forceinline__ void block_exclusive_scan2(int (&a)[PER], int (&b)[PER], int* part, int& total_a,
+                                                      int& total_b) {
+  constexpr int kWaves = NT / kWave;
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const int wave = t / kWave;
+  int sa = 0, sb = 0;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    sa += a[q];
+    sb += b[q];
+  }
+  int ia = sa, ib = sb;  // inclusive scans over the wave
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int xa = __shfl_up(ia, off, kWave);
+    const int xb = __shfl_up(ib, off, kWave);
+    if (lane >= off) {
+      ia += xa;
+      ib += xb;
+    }
+  }
+  if (lane == kWave - 1) {
+    part[wave] = ia;
+    part[kWaves + wave] = ib;
+  }
+  __syncthreads();
+  int ba = 0, bb = 0;  // the sums of the waves before this one
+  total_a = 0;
+  total_b = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wave) {
+      ba += part[w];
+      bb += part[kWaves + w];
+    }
+    total_a += part[w];
+    total_b += part[kWaves + w];
+  }
+  int ra = ba + ia - sa, rb = bb + ib - sb;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int ca = a[q], cb = b[q];
+    a[q] = ra;
+    b[q] = rb;
+    ra += ca;
+    rb += cb;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // LDS Stockham FFT
 //
-// NSEQ sequences of length F, sequence q at s + q * F, transformed in place by
-// NT threads.  Radix-4 stages (Ns = 1, 4, 16, ...) then one radix-2 stage
-// when log2(F) is odd; every stage reads its inputs to registers, barriers,
-// and writes the Stockham-permuted outputs, so the result is in natural order.
-// Twiddles come from a 4096-entry table of e^{-2 pi i m / 4096} (computed in
-// fp64 on the host); INV conjugates them and leaves the result unscaled.
+// NSEQ sequences of length F = 2^a or 3 * 2^a, sequence q at s + q * F,
+// transformed in place by NT threads.  One radix-3 stage first when 3 divides
+// F, then radix-4 stages, then one radix-2 stage when F / Ns = 2 is left.  A
+// stage of radix R entered after Ns points are transformed (Ns = the product
+// of the earlier radices) takes, for each j < F / R, the inputs j + r F / R,
+// twiddles them by e^{-2 pi i r k / (Ns R)} with k = j mod Ns, and writes the
+// R-point DFT to (j - k) R + k + r Ns, so the result is in natural order.
+// Every stage reads its inputs to registers, barriers, then writes.
+// Twiddles e^{-2 pi i j / F} are staged in LDS from the global table
+// (computed in fp64 on the host); INV conjugates them and leaves the result
+// unscaled.
 // ---------------------------------------------------------------------------
 template <bool INV>
 __device__ __forceinline__ float2 twiddle(const float2* __restrict__ tw, int m) {
@@ -126,26 +187,78 @@ __device__ __forceinline__ float2 twiddle(const float2* __restrict__ tw, int m) 
   return INV ? make_float2(w.x, -w.y) : w;
 }
 
-// Copies the F twiddles e^{-2 pi i j / F} of the global 4096-entry table into
-// LDS (the caller's next barrier publishes them); transforms then read their
-// twiddles from LDS (TWS = 1) instead of from the cache hierarchy.
+// Copies the F twiddles e^{-2 pi i j / F} of the global table into LDS (the
+// caller's next barrier publishes them); transforms then read their twiddles
+// from LDS (TWS = 1) instead of from the cache hierarchy.
 template <int F, int NT>
 __device__ __forceinline__ void stage_twiddles(float2* lds_tw, const float2* __restrict__ tw) {
-  constexpr int STRIDE = kTwiddleLen / F;
-  for (int j = threadIdx.x; j < F; j += NT) lds_tw[j] = tw[j * STRIDE];
+  constexpr bool kR3 = F % 3 == 0;
+  constexpr int BASE = kR3 ? kTwiddlePow2 : 0;
+  constexpr int LEN = kR3 ? kTwiddlePow3 : kTwiddlePow2;
+  static_assert(LEN % F == 0, "F divides its part of the twiddle table");
+  constexpr int STRIDE = LEN / F;
+  for (int j = threadIdx.x; j < F; j += NT) lds_tw[j] = tw[BASE + j * STRIDE];
 }
 
-// tw holds e^{-2 pi i j / (F * TWS)}: the global table (TWS = 4096 / F) or
-// one staged in LDS (TWS = 1).
-template <int F, int NSEQ, int NT, bool INV, int TWS = kTwiddleLen / F>
-__device__ __forceinline__ void fft_lds(float2* s, const float2* __restrict__ tw) {
-  constexpr int LOG2F = ilog2(F);
-  constexpr int Q = F / 4;
-  constexpr int TOT = NSEQ * Q;
+template <int F>
+struct FftRadices {
+  static constexpr bool kR3 = F % 3 == 0;
+  static constexpr int kPow2 = kR3 ? F / 3 : F;
+  static_assert(kPow2 >= 4 && (kPow2 & (kPow2 - 1)) == 0, "F = 2^a or 3 * 2^a");
+};
+
+// The first stage when 3 divides F (Ns = 1: no twiddles).  With
+// c = cos(2 pi / 3) = -1/2 and s = sin(2 pi / 3), the DFT of (a, b, d) is
+// (a + b + d, a + c (b + d) -+ i s (b - d), a + c (b + d) +- i s (b - d)),
+// the upper signs forward.
+template <int F, int NSEQ, int NT, bool INV>
+__device__ __forceinline__ void fft_stage_r3(float2* s) {
+  constexpr int T = F / 3;
+  constexpr int TOT = NSEQ * T;
   constexpr int BPT = (TOT + NT - 1) / NT;
+  constexpr float kSin = 0.866025403784438646763723f;
+  float2 v[BPT][3];
 #pragma unroll
-  for (int stage = 0; stage < LOG2F / 2; ++stage) {
-    const int ns = 1 << (2 * stage);
+  for (int b = 0; b < BPT; ++b) {
+    const int t = threadIdx.x + b * NT;
+    if (TOT % NT == 0 || t < TOT) {
+      const int q = t / T;
+      const int j = t - q * T;
+      const float2* src = s + q * F;
+#pragma unroll
+      for (int r = 0; r < 3; ++r) v[b][r] = src[j + r * T];
+      const float2 sum = cadd(v[b][1], v[b][2]);
+      const float2 dif = csub(v[b][1], v[b][2]);
+      const float2 mid = make_float2(v[b][0].x - 0.5f * sum.x, v[b][0].y - 0.5f * sum.y);
+      // forward: -i s (b - d), inverse: +i s (b - d)
+      const float2 rot = INV ? make_float2(-kSin * dif.y, kSin * dif.x) : make_float2(kSin * dif.y, -kSin * dif.x);
+      v[b][0] = cadd(v[b][0], sum);
+      v[b][1] = cadd(mid, rot);
+      v[b][2] = csub(mid, rot);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < BPT; ++b) {
+    const int t = threadIdx.x + b * NT;
+    if (TOT % NT == 0 || t < TOT) {
+      const int q = t / T;
+      const int j = t - q * T;
+      float2* dst = s + q * F + 3 * j;
+#pragma unroll
+      for (int r = 0; r < 3; ++r) dst[r] = v[b][r];
+    }
+  }
+  __syncthreads();
+}
+
+// Radix-4 stages from Ns = NS while 4 divides F / Ns.
+template <int F, int NS, int NSEQ, int NT, bool INV, int TWS>
+__device__ __forceinline__ void fft_stages_r4(float2* s, const float2* __restrict__ tw) {
+  if constexpr ((F / NS) % 4 == 0) {
+    constexpr int Q = F / 4;
+    constexpr int TOT = NSEQ * Q;
+    constexpr int BPT = (TOT + NT - 1) / NT;
     float2 v[BPT][4];
 #pragma unroll
     for (int b = 0; b < BPT; ++b) {
@@ -156,8 +269,8 @@ __device__ __forceinline__ void fft_lds(float2* s, const float2* __restrict__ tw
         const float2* src = s + q * F;
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[b][r] = src[j + r * Q];
-        const int kk = j & (ns - 1);
-        const int step = (F / (4 * ns)) * kk * TWS;
+        const int kk = static_cast<int>(static_cast<unsigned int>(j) % NS);
+        const int step = (F / (4 * NS)) * kk * TWS;
         v[b][1] = cmul(v[b][1], twiddle<INV>(tw, step));
         v[b][2] = cmul(v[b][2], twiddle<INV>(tw, 2 * step));
         v[b][3] = cmul(v[b][3], twiddle<INV>(tw, 3 * step));
@@ -180,15 +293,16 @@ __device__ __forceinline__ void fft_lds(float2* s, const float2* __restrict__ tw
       if (TOT % NT == 0 || t < TOT) {
         const int q = t / Q;
         const int j = t - q * Q;
-        const int kk = j & (ns - 1);
+        const int kk = static_cast<int>(static_cast<unsigned int>(j) % NS);
         float2* dst = s + q * F + (j - kk) * 4 + kk;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dst[r * ns] = v[b][r];
+        for (int r = 0; r < 4; ++r) dst[r * NS] = v[b][r];
       }
     }
     __syncthreads();
-  }
-  if (LOG2F & 1) {
+    fft_stages_r4<F, NS * 4, NSEQ, NT, INV, TWS>(s, tw);
+  } else if constexpr (F / NS == 2) {
+    // last stage, radix 2 (Ns = F / 2): in place, j and j + F / 2
     constexpr int H2 = F / 2;
     constexpr int TOT2 = NSEQ * H2;
 #pragma unroll
@@ -205,6 +319,20 @@ __device__ __forceinline__ void fft_lds(float2* s, const float2* __restrict__ tw
       }
     }
     __syncthreads();
+  } else {
+    static_assert(F == NS, "radix plan ends at F");
+  }
+}
+
+// tw holds e^{-2 pi i j / (F * TWS)} for j < F * TWS (staged in LDS by
+// stage_twiddles: TWS = 1).
+template <int F, int NSEQ, int NT, bool INV, int TWS = 1>
+__device__ __forceinline__ void fft_lds(float2* s, const float2* __restrict__ tw) {
+  if constexpr (FftRadices<F>::kR3) {
+    fft_stage_r3<F, NSEQ, NT, INV>(s);
+    fft_stages_r4<F, 3, NSEQ, NT, INV, TWS>(s, tw);
+  } else {
+    fft_stages_r4<F, 1, NSEQ, NT, INV, TWS>(s, tw);
   }
 }
 

@@ -352,71 +352,24 @@ __global__ __launch_bounds__(kPointThreads) void k_bin_count(const float2* __res
   }
 }
 
-// Exclusive scans of two arrays of up to kMaxTiles counts by one block of
-// kPlanThreads threads: kPlanPer consecutive entries per thread, the thread
-// sums scanned within each wave by shuffles and across the block's waves
-// through LDS (one barrier).  A block of 4 waves finds room on a CU beside
+// The plan's scans run in one block of kPlanThreads threads, kPlanPer
+// consecutive tiles per thread.  A block of 4 waves finds room on a CU beside
 // the attraction sooner than a block of 16 would.
 constexpr int kPlanThreads = 256;
 constexpr int kPlanPer = kMaxTiles / kPlanThreads;
-constexpr int kPlanWaves = kPlanThreads / kWave;
 static_assert(kPlanPer * kPlanThreads == kMaxTiles, "whole entries per thread");
-__device__ void block_exclusive_scan2(int (&a)[kPlanPer], int (&b)[kPlanPer], int* part, int& total_a,
-                                      int& total_b) {
-  const int t = threadIdx.x;
-  const int lane = t & (kWave - 1);
-  const int wave = t / kWave;
-  int sa = 0, sb = 0;
-  for (int q = 0; q < kPlanPer; ++q) {
-    sa += a[q];
-    sb += b[q];
-  }
-  int ia = sa, ib = sb;  // inclusive scans over the wave
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int xa = __shfl_up(ia, off, kWave);
-    const int xb = __shfl_up(ib, off, kWave);
-    if (lane >= off) {
-      ia += xa;
-      ib += xb;
-    }
-  }
-  if (lane == kWave - 1) {
-    part[wave] = ia;
-    part[kPlanWaves + wave] = ib;
-  }
-  __syncthreads();
-  int ba = 0, bb = 0;  // the sums of the waves before this one
-  total_a = 0;
-  total_b = 0;
-#pragma unroll
-  for (int w = 0; w < kPlanWaves; ++w) {
-    if (w < wave) {
-      ba += part[w];
-      bb += part[kPlanWaves + w];
-    }
-    total_a += part[w];
-    total_b += part[kPlanWaves + w];
-  }
-  int ra = ba + ia - sa, rb = bb + ib - sb;
-  for (int q = 0; q < kPlanPer; ++q) {
-    const int ca = a[q], cb = b[q];
-    a[q] = ra;
-    b[q] = rb;
-    ra += ca;
-    rb += cb;
-  }
-}
 
-// tiles < 0: the interpolation grid's tile count, lg_tiles_axis^2, read on the
-// device.  tile_item0 (optional) receives the first work item of each tile
-// and, at [tiles], the number of items.
+// Each tile's first point (tile_cursor, for the scatter's reservations) and
+// work items of <= kChunk points, from the tile counts (which it clears for
+// the next iteration).  tiles < 0: the interpolation grid's tile count,
+// lg_tiles_axis^2, read on the device.  tile_item0 (optional) receives the
+// first work item of each tile and, at [tiles], the number of items.
 __global__ __launch_bounds__(kPlanThreads) void k_bin_plan(int* __restrict__ tile_count,
                                                            int* __restrict__ tile_cursor, int4* __restrict__ items,
                                                            DeviceScalars* sc, int tiles,
                                                            int* __restrict__ tile_item0) {
   chain_priority();
-  __shared__ int part[kPlanThreads];
+  __shared__ int part[2 * kPlanThreads / kWave];
   if (tiles < 0) tiles = sc->lg_tiles_axis * sc->lg_tiles_axis;
   int cnt[kPlanPer], start[kPlanPer], chunks[kPlanPer], base[kPlanPer];
   for (int q = 0; q < kPlanPer; ++q) {
@@ -428,7 +381,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_bin_plan(int* __restrict__ til
     base[q] = chunks[q];
   }
   int total_points = 0, total_items = 0;
-  block_exclusive_scan2(start, base, part, total_points, total_items);
+  block_exclusive_scan2<kPlanPer, kPlanThreads>(start, base, part, total_points, total_items);
   (void)total_points;
   for (int q = 0; q < kPlanPer; ++q) {
     const int t = threadIdx.x * kPlanPer + q;

@@ -382,7 +382,9 @@ int key_bits_for(int n) {
 bool upload_twiddles(fastembedr_hip_tsne* s) {
   std::vector<float2> host(fehip::kTwiddleLen);
   for (int m = 0; m < fehip::kTwiddleLen; ++m) {
-    const double ang = -2.0 * M_PI * static_cast<double>(m) / static_cast<double>(fehip::kTwiddleLen);
+    const bool pow2 = m < fehip::kTwiddlePow2;
+    const double ang = -2.0 * M_PI * static_cast<double>(pow2 ? m : m - fehip::kTwiddlePow2) /
+                       static_cast<double>(pow2 ? fehip::kTwiddlePow2 : fehip::kTwiddlePow3);
     host[m] = make_float2(static_cast<float>(std::cos(ang)), static_cast<float>(std::sin(ang)));
   }
   // Synchronous: `host` is released when this function returns.
@@ -607,11 +609,11 @@ bool enqueue_attract_helper(fastembedr_hip_tsne* s, const float2* y_cur, float e
 }
 
 // FFT length for an interpolation grid of `nodes` nodes per axis: the
-// smallest power of two >= 2 * nodes (a zero-padded linear convolution), at
-// least 64.
+// smallest 2^a or 3 * 2^a >= 2 * nodes (a zero-padded linear convolution;
+// the transforms take radix 3 once), at least 64, at most kLgMaxFft.
 int interp_fft_len(int nodes) {
   int f = 64;
-  while (f < 2 * nodes && f < fehip::kLgMaxFft) f <<= 1;
+  while (f < 2 * nodes && f < fehip::kLgMaxFft) f = (f & (f - 1)) == 0 ? f / 2 * 3 : f / 3 * 4;
   return f;
 }
 
@@ -1700,10 +1702,14 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
   // 2 s + |mean_x - mean_y| <= (2 + sqrt 2) s.  With boxes = ceil(span /
   // ints_in_interval) >= span / ints_in_interval, a growth of at most d
   // adds at most ceil(d / ints_in_interval) boxes.  The host runs at most
-  // kMaxLag iterations ahead of what it knows (none without the clip).
+  // kMaxLag iterations ahead of what it knows (none without the clip).  One
+  // iteration keeps the margin small enough for the FFT length to follow the
+  // grid (at 1M points late in the schedule: 108 boxes known, 126 allowed,
+  // length 768; three iterations would allow 160 and take 1024), and the
+  // queue still holds the iteration in flight while the host waits.
   const bool lg = s->repulsion == FASTEMBEDR_HIP_REPULSION_LAGRANGE;
   constexpr int kRing = fastembedr_hip_tsne::kLgRing;
-  constexpr int kMaxLag = 3;
+  constexpr int kMaxLag = 1;
   static_assert(kMaxLag + 2 <= kRing, "ring slots outlive the lag");
   const int allowed_lag = up.clip ? kMaxLag : 0;
   const double growth =

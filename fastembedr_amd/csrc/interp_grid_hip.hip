@@ -36,8 +36,8 @@
 //
 // Per iteration, after the statistics have set the geometry on the device:
 //   k_lg_bin_count, k_bin_plan, k_lg_bin_scatter
-//                         points into tiles of 16 x 16 boxes and work items
-//                         of at most 2048 points of one tile
+//                         points into tiles of T x T boxes and work items of
+//                         at most 2048 points of one tile
 //   k_lg_spread           per work item: points ordered by box in LDS; one
 //                         wave per box sums its points' 9 nodes x 4 moments
 //                         in registers and a butterfly across the wave, and
@@ -249,7 +249,10 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
   __shared__ int part[kLgThreads];
   __shared__ float2 sorted[kChunk];
   __shared__ float wave_part[kLgWaves][4 * kLgOrder * kLgOrder];
+  __shared__ int wave_total[kLgWaves];
   if (static_cast<int>(blockIdx.x) >= sc->num_items) return;
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int lane = static_cast<int>(threadIdx.x) & 63;
   const DeviceScalars s = *sc;
   const int4 it = items[blockIdx.x];
   const int tile = s.lg_tile;
@@ -281,18 +284,21 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
     }
   }
   __syncthreads();
-  {
+  {  // scan of the box counts: shuffles within each wave, wave sums through LDS
     const int t = threadIdx.x;
     const int c = box_start[t];
-    part[t] = c;
-    __syncthreads();
-    for (int off = 1; off < kLgThreads; off <<= 1) {
-      const int add = t >= off ? part[t - off] : 0;
-      __syncthreads();
-      part[t] += add;
-      __syncthreads();
+    int inc = c;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int x = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += x;
     }
-    box_start[t] = part[t] - c;  // exclusive start; part[t] is the inclusive end
+    if (lane == 63) wave_total[wave] = inc;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kLgWaves; ++w) inc += w < wave ? wave_total[w] : 0;
+    part[t] = inc;               // inclusive end
+    box_start[t] = inc - c;      // exclusive start
   }
   __syncthreads();
 #pragma unroll
@@ -300,8 +306,6 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
     if (box[q] >= 0) sorted[box_start[box[q]] + rank[q]] = v[q];
   }
   __syncthreads();
-  const int wave = static_cast<int>(threadIdx.x) >> 6;
-  const int lane = static_cast<int>(threadIdx.x) & 63;
   float a[4 * kLgOrder * kLgOrder];
   if (nbox == 1) {
     // one box: the waves take interleaved stretches of 64 points
@@ -589,7 +593,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
     const int kx = e - r * S::H;
     const int y = row0 + r;
     if (y >= m) continue;
-    const int mk = (F - kx) & (F - 1);
+    const int mk = kx == 0 ? 0 : F - kx;
     const float2 a = lds[(2 * r) * F + kx];
     const float2 am = conjf2(lds[(2 * r) * F + mk]);
     const float2 sa = cadd(a, am), da = csub(a, am);
@@ -883,11 +887,17 @@ hipError_t launch_interp_fft(int which, int fft_len, InterpBuffers& ib, DeviceSc
                              hipStream_t stream) {
   switch (fft_len) {
     case 64: return lg_fft_launch<64>(which, ib, sc, tw, n, stream);
+    case 96: return lg_fft_launch<96>(which, ib, sc, tw, n, stream);
     case 128: return lg_fft_launch<128>(which, ib, sc, tw, n, stream);
+    case 192: return lg_fft_launch<192>(which, ib, sc, tw, n, stream);
     case 256: return lg_fft_launch<256>(which, ib, sc, tw, n, stream);
+    case 384: return lg_fft_launch<384>(which, ib, sc, tw, n, stream);
     case 512: return lg_fft_launch<512>(which, ib, sc, tw, n, stream);
+    case 768: return lg_fft_launch<768>(which, ib, sc, tw, n, stream);
     case 1024: return lg_fft_launch<1024>(which, ib, sc, tw, n, stream);
+    case 1536: return lg_fft_launch<1536>(which, ib, sc, tw, n, stream);
     case 2048: return lg_fft_launch<2048>(which, ib, sc, tw, n, stream);
+    case 3072: return lg_fft_launch<3072>(which, ib, sc, tw, n, stream);
     case 4096: return lg_fft_launch<4096>(which, ib, sc, tw, n, stream);
     default: return hipErrorInvalidValue;
   }

@@ -57,7 +57,12 @@ constexpr int kMaxReduceBlocks = 4096;
 // holds (sequence number << 32) | box count, so the host can tell which
 // update wrote it without an event.
 constexpr int kBoxRing = 8;
-constexpr int kTwiddleLen = 4096;     // e^{-2 pi i m / 4096}, m in [0, 4096)
+// Twiddle table: e^{-2 pi i m / 4096} for m < 4096, then e^{-2 pi i m / 3072}
+// for m < 3072; a transform of length F = 2^a (3 * 2^a) <= 4096 takes every
+// (4096 / F)-th entry of the first part (every (3072 / F)-th of the second).
+constexpr int kTwiddlePow2 = 4096;
+constexpr int kTwiddlePow3 = 3072;
+constexpr int kTwiddleLen = kTwiddlePow2 + kTwiddlePow3;
 constexpr int kMaxGrid = 1024;        // nodes per axis (FFT length 2048)
 
 // Spreading is binned by tiles of kTile x kTile cells; each work item is at
@@ -226,7 +231,7 @@ hipError_t launch_inverse_rows(GridBuffers& gb, const float2* tw, int n, DeviceS
 
 // ---- FIt-SNE interpolation grid ---------------------------------------------
 // Binning, spreading and the zero-padded convolution at FFT length fft_len
-// (a power of two in [64, kLgMaxFft] with fft_len >= 2 * lg_nodes); the
+// (2^a or 3 * 2^a in [64, kLgMaxFft] with fft_len >= 2 * lg_nodes); the
 // node count itself is read on the device.  Points must already be centred
 // into y_cur by launch_interp_bin_count.
 hipError_t launch_interp_bin_count(const float2* y_stored, float2* y_cur, const DeviceScalars* sc,
