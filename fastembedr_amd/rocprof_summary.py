@@ -55,13 +55,26 @@ def _stats_rows(kt_dir: str) -> list[tuple[str, int, float, float, float, float]
     return [(r[0], int(r[1]), float(r[2]), float(r[3]), float(r[4]), float(r[5])) for r in con.execute(q)]
 
 
+def _window(rows: list[dict], name_key: str, last: int) -> list[dict]:
+    """The dispatches (in dispatch order) of the last `last` iterations: those
+    enqueued after the update kernel of the iteration before them (one
+    k_update per iteration), so that kernels templated on a size that changes
+    during the run (the FFT lengths) are counted only in the window.  Without
+    enough updates, every dispatch."""
+    ids = [_dispatch_order(r) for r in rows if short_name(r[name_key]).startswith("k_update")]
+    if len(ids) <= last:
+        return rows
+    first = ids[-(last + 1)]
+    return [r for r in rows if _dispatch_order(r) > first]
+
+
 def _last_rows(kt_dir: str, last: int) -> list[tuple[str, int, float, float, float, float]]:
-    """As _stats_rows, over each kernel's last `last` dispatches of the
-    per-dispatch kernel trace (CSV)."""
+    """As _stats_rows, over the last `last` iterations (_window) of the
+    per-dispatch kernel trace (CSV), at most `last` dispatches per kernel."""
     per = collections.defaultdict(list)
     rows = list(csv.DictReader(open(_one(f"{kt_dir}/**/*kernel_trace.csv"))))
     rows.sort(key=_dispatch_order)
-    for r in rows:
+    for r in _window(rows, "Kernel_Name", last):
         per[r["Kernel_Name"]].append(float(r["End_Timestamp"]) - float(r["Start_Timestamp"]))
     out = []
     for name, durs in per.items():
@@ -90,8 +103,8 @@ def _dispatch_order(r: dict) -> int:
 
 def _counter(dir_: str, cname: str, last: int = 0):
     """Per kernel, the counter's value of each dispatch in dispatch order
-    (only the last `last` dispatches when last > 0), and the largest value of
-    the calibration copy."""
+    (only the last `last` iterations, _window, at most `last` dispatches per
+    kernel, when last > 0), and the largest value of the calibration copy."""
     per = collections.defaultdict(list)
     calib = None
     rows = [r for r in csv.DictReader(open(_one(f"{dir_}/**/*counter_collection.csv"))) if r["Counter_Name"] == cname]
@@ -100,8 +113,9 @@ def _counter(dir_: str, cname: str, last: int = 0):
         v = float(r["Counter_Value"])
         if "copyBuffer" in r["Kernel_Name"] and (calib is None or v > calib):
             calib = v
+    for r in _window(rows, "Kernel_Name", last) if last > 0 else rows:
         if _OURS.search(r["Kernel_Name"]):
-            per[short_name(r["Kernel_Name"])].append(v)
+            per[short_name(r["Kernel_Name"])].append(float(r["Counter_Value"]))
     if last > 0:
         per = collections.defaultdict(list, {k: v[-last:] for k, v in per.items()})
     return per, calib
@@ -146,7 +160,7 @@ def main(argv=None) -> int:
     t = sub.add_parser("trace")
     t.add_argument("kt_dir")
     t.add_argument("command")
-    t.add_argument("--last", type=int, default=0, help="only each kernel's last N dispatches (per-dispatch trace)")
+    t.add_argument("--last", type=int, default=0, help="only the last N iterations' dispatches (per-dispatch trace)")
     c = sub.add_parser("traffic")
     c.add_argument("fetch_dir")
     c.add_argument("write_dir")
@@ -154,25 +168,25 @@ def main(argv=None) -> int:
     c.add_argument("--copy-mib", type=int, default=512)
     c.add_argument("--json", default="")
     c.add_argument("--meta", default="{}", help="JSON object stored beside the table (workload keys)")
-    c.add_argument("--last", type=int, default=0, help="average only each kernel's last N dispatches")
+    c.add_argument("--last", type=int, default=0, help="average only the last N iterations' dispatches")
     p = sub.add_parser("counters")
     p.add_argument("dir")
     p.add_argument("command")
     p.add_argument("--names", required=True, help="comma-separated counter names")
-    p.add_argument("--last", type=int, default=0, help="average only each kernel's last N dispatches")
+    p.add_argument("--last", type=int, default=0, help="average only the last N iterations' dispatches")
     a = ap.parse_args(argv)
     if a.what == "trace":
         lines = trace(a.kt_dir, a.last)
         if a.last:
-            lines.insert(0, f"(durations over each kernel's last {a.last} dispatches)")
+            lines.insert(0, f"(durations over the last {a.last} iterations, at most {a.last} dispatches per kernel)")
     elif a.what == "counters":
         lines = counters(a.dir, a.names.split(","), a.last)
         if a.last:
-            lines.insert(0, f"(mean per dispatch over each kernel's last {a.last} dispatches)")
+            lines.insert(0, f"(mean per dispatch over the last {a.last} iterations, at most {a.last} dispatches per kernel)")
     else:
         lines, table = traffic(a.fetch_dir, a.write_dir, a.copy_mib << 20, a.last)
         if a.last:
-            lines.insert(0, f"(mean per dispatch over each kernel's last {a.last} dispatches)")
+            lines.insert(0, f"(mean per dispatch over the last {a.last} iterations, at most {a.last} dispatches per kernel)")
         if a.json:
             table.update(json.loads(a.meta))
             table["command"] = a.command
