@@ -136,3 +136,40 @@ def test_exact_knn_numpy_against_sklearn():
     d_ref, i_ref = nn.kneighbors(x.astype(np.float64))
     np.testing.assert_allclose(dist, d_ref[:, 1:], rtol=1e-5, atol=1e-5)
     assert (idx == i_ref[:, 1:]).mean() > 0.999
+
+
+def test_rocprof_digest_window(tmp_path):
+    """The digests' --last N keeps the dispatches enqueued after the update
+    that precedes the last N iterations: an FFT kernel instantiated for a
+    length used only earlier in the run drops out, and each kernel keeps at
+    most N dispatches."""
+    from fastembedr_amd import rocprof_summary as rs
+
+    rows = []
+    did = 0
+
+    def add(name, value):
+        nonlocal did
+        did += 1
+        rows.append({"Dispatch_Id": str(did), "Kernel_Name": name, "Counter_Name": "FETCH_SIZE",
+                     "Counter_Value": str(value)})
+
+    add("__amd_rocclr_copyBuffer", 262166.6)
+    for it in range(6):  # lengths 512 in iterations 0-2, 768 in 3-5
+        fft = 512 if it < 3 else 768
+        add(f"void fehip::(anonymous namespace)::k_lg_conv_cols<{fft}>(...)", fft)
+        add("void fehip::(anonymous namespace)::k_attract_tiles_seg<512, 2, 3, false>(...)", 1000 + it)
+        add("void fehip::k_update<0, true>(...)", 50)
+    d = tmp_path / "pmc" / "sub"
+    d.mkdir(parents=True)
+    with open(d / "fetch_counter_collection.csv", "w") as f:
+        f.write("Dispatch_Id,Kernel_Name,Counter_Name,Counter_Value\n")
+        for r in rows:
+            f.write(f'{r["Dispatch_Id"]},"{r["Kernel_Name"]}",{r["Counter_Name"]},{r["Counter_Value"]}\n')
+    per, calib = rs._counter(str(tmp_path / "pmc"), "FETCH_SIZE", last=2)
+    assert calib == pytest.approx(262166.6)
+    assert "k_lg_conv_cols<512>" not in per
+    assert per["k_lg_conv_cols<768>"] == [768.0, 768.0]
+    assert per["k_attract_tiles_seg<512, 2, 3, false>"] == [1004.0, 1005.0]
+    per_all, _ = rs._counter(str(tmp_path / "pmc"), "FETCH_SIZE", last=0)
+    assert per_all["k_lg_conv_cols<512>"] == [512.0] * 3
