@@ -213,7 +213,7 @@ def main() -> int:
     cnt, tot = timing[dom]
     dom_ms = tot / cnt if cnt else 0.0
     layout = sess.attraction_info()
-    # Algorithmic bytes per launch (SURVEY 8(d) basis).  attract: col int32 +
+    # Algorithmic bytes per launch (the CSR basis).  attract: col int32 +
     # val fp32 streamed once per stored entry and the row pointers,
     # 8 nnz + 4 (n + 1); the neighbour positions y_j are counted as
     # cache-resident.  The kernel's own slot format moves 6 bytes per entry
@@ -225,16 +225,21 @@ def main() -> int:
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9 if dom_ms > 0 else 0.0
     slot_bytes = 6.0 * nnz + 16.0 * n
     traffic = measured_traffic(dom, n, nnz, g, args.repulsion)
-    # The repulsion step's roofline: SURVEY 8(d)'s B_rep = 16 n + 8 n
+    digest = _digest(n, nnz, g, args.repulsion)
+    traffic_source = digest["_file"] if traffic is not None and digest is not None else None
+    # The repulsion step's roofline: B_rep = 16 n + 8 n
     # + 28 G^2 + 288 F^2 with G the grid nodes per axis and F the FFT length
     # at the end of the window, over the summed repulsion kernels of the
     # breakdown pass; traffic: the rocprof digest's bytes of the same kernels
     # per iteration.
     if interp:
-        # the shortest FFT length the grid needs (zero padding to >= 2 nodes);
-        # the run may use a longer one, chosen from a lagged bound
+        # the shortest FFT length the grid can use (2^a or 3 * 2^a, at least
+        # 64, zero padding to >= 2 nodes); the run may use a longer one,
+        # chosen from a lagged bound
         g_nodes = geo_end["nodes"]
-        f_len = 1 << max(6, (2 * g_nodes - 1).bit_length())
+        f_len = 64
+        while f_len < 2 * g_nodes:
+            f_len = f_len // 2 * 3 if f_len & (f_len - 1) == 0 else f_len // 3 * 4
     else:
         g_nodes, f_len = g, 2 * g
     rep_bytes = 24.0 * n + 28.0 * g_nodes ** 2 + 288.0 * f_len ** 2
@@ -317,7 +322,7 @@ def main() -> int:
                            "note": "the tiled kernel's own format: 6 bytes per stored entry + 16 n"}
             if dom == "attract" else None,
             "kernel_ms": round(dom_ms, 5),
-            "traffic_source": TRAFFIC_FILES[args.repulsion].name if traffic is not None else None,
+            "traffic_source": traffic_source,
         },
         "cpu_baseline": cpu,
         "host_boundary": host_boundary,
@@ -403,6 +408,7 @@ def bench_transform(args, torch, fe, synthetic) -> int:
         return time.perf_counter() - t0
 
     iters = args.steps if args.steps != 750 else 250
+    exact_full = []  # query-iterations that took the exact sums, per full grid call
 
     def rate(mode: str) -> tuple[float, float, float]:
         """Per-iteration time from calls of `iters` and of 1 iteration (upload,
@@ -412,6 +418,8 @@ def bench_transform(args, torch, fe, synthetic) -> int:
         diffs, t_alls = [], []
         for _ in range(5):
             t_all = call(iters, mode)
+            if mode == "grid":
+                exact_full.append(int(grid_stats[2]))
             t_one = call(1, mode)
             diffs.append((t_all - t_one) / max(1, iters - 1))
             t_alls.append(t_all)
@@ -422,6 +430,7 @@ def bench_transform(args, torch, fe, synthetic) -> int:
 
     per_iter, t_call, its = rate("grid")
     geo = [int(v) for v in grid_stats]
+    geo[2] = max(exact_full) if exact_full else geo[2]
     per_iter_s, t_call_s, its_s = rate("sampled")
     # fp64 flops per query and iteration of the fused run kernel (grid mode):
     # attraction 13 per neighbour (2 sub, 2 mul + 2 add, 1 div, 2 mul, 2 x
@@ -465,7 +474,7 @@ def bench_transform(args, torch, fe, synthetic) -> int:
                    "n_reference": n_ref, "n_query": nq, "k": 30,
                    "repulsion": f"reference grid: the reference's repulsion fields summed once at {geo[1]} x "
                                 f"{geo[1]} nodes ({geo[0]} boxes per axis, 3 points per box, 2 boxes per unit) and "
-                                f"interpolated at each query; {geo[2]} query-iterations took the exact sums"},
+                                f"interpolated at each query; at most {geo[2]} query-iterations of a {iters}-iteration call took the exact sums"},
         "whole_call_seconds": round(t_call, 4),
         "roofline": {"kernel": "k_transform_run<grid>", "bound": "fp64 VALU", "achieved": round(tflops, 3),
                      "peak": 78.6, "unit": "TFLOP/s", "frac": round(tflops / 78.6, 4), "traffic": None,
@@ -507,8 +516,11 @@ def one_shot_from_host(idx_r, dist_r, y0, sched, lr):
             "includes": "host->device KNN copy, P build, 750 iterations, device->host layout copy"}
 
 
-TRAFFIC_FILES = {"grid": ROOT / "profiles" / "tsne_loop_config2_grid_traffic.json",
-                 "interp": ROOT / "profiles" / "tsne_loop_config2_interp_traffic.json"}
+# Committed traffic digests per repulsion; the one taken on the workload being
+# measured (same n, nnz and grid) is used.
+TRAFFIC_FILES = {"grid": [ROOT / "profiles" / "tsne_loop_config2_grid_traffic.json"],
+                 "interp": [ROOT / "profiles" / "tsne_loop_config2_interp_traffic.json",
+                            ROOT / "profiles" / "tsne_loop_config4_interp_traffic.json"]}
 
 # Kernels of the repulsion step and their launches per iteration.
 REPULSION_SYMBOLS = {
@@ -524,15 +536,18 @@ def _digest(n: int, nnz: int, g: int, repulsion: str):
     """The committed rocprofv3 traffic digest (FETCH_SIZE + WRITE_SIZE per
     dispatch, calibrated against a copy of known size), when it was taken on
     this same workload; None otherwise."""
-    try:
-        rec = json.loads(TRAFFIC_FILES[repulsion].read_text())
-    except (OSError, ValueError):
-        return None
-    if (rec.get("n"), rec.get("nnz"), rec.get("repulsion")) != (n, nnz, repulsion):
-        return None
-    if repulsion == "grid" and rec.get("grid") != g:
-        return None
-    return rec
+    for path in TRAFFIC_FILES[repulsion]:
+        try:
+            rec = json.loads(path.read_text())
+        except (OSError, ValueError):
+            continue
+        if (rec.get("n"), rec.get("nnz"), rec.get("repulsion")) != (n, nnz, repulsion):
+            continue
+        if repulsion == "grid" and rec.get("grid") != g:
+            continue
+        rec["_file"] = path.name
+        return rec
+    return None
 
 
 def measured_traffic(kernel: str, n: int, nnz: int, g: int, repulsion: str):
