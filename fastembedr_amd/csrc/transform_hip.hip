@@ -424,10 +424,10 @@ __global__ __launch_bounds__(kRunThreads) void k_transform_run(
 // reference positions and p once, keep them in registers for the whole
 // schedule, and sum their part of the attraction; the parts are added by a
 // butterfly over the group (the same value in every lane).  The grid
-// repulsion's 9 nodes are split over the lanes the same way; the update (and
-// the rare exact sums of a query outside the grid) are computed by every
-// lane of the group from the same inputs, so the lanes keep identical
-// states.  L lanes per query put
+// repulsion's 9 nodes are split over the lanes the same way; the update is
+// computed by every lane of the group from the same inputs, so the lanes
+// keep identical states (the rare exact sums of a query outside the grid are
+// taken by the whole wave and handed to the group's lanes).  L lanes per query put
 // L times as many waves in flight as k_transform_run, which waits on the
 // neighbours' positions every iteration.  The attraction is summed in
 // another order than the reference's (per lane, then across lanes).
@@ -518,13 +518,43 @@ __global__ __launch_bounds__(kLaneThreads) void k_transform_grid_lanes(
   for (int it = 0; it < rs.total; ++it) {
     const bool early = it < rs.early_iter;
     double gx = 0.0, gy = 0.0;
-    if (!grid_repulsion_lanes<L>(field, g, yi.x, yi.y, lane, &gx, &gy)) {
-      // outside the grid: the exact sums over every reference point (rare),
-      // taken whole by every lane of the group (the same value in each)
-      const double2 r = repulsion<true>(ref, n_ref, n_ref, 0u, yi.x, yi.y);
-      gx = r.x;
-      gy = r.y;
-      ++exact_evals;
+    const bool on_grid = grid_repulsion_lanes<L>(field, g, yi.x, yi.y, lane, &gx, &gy);
+    // Outside the grid: the exact sums over every reference point (rare),
+    // one such query at a time by the whole wave (its 64 lanes stride over
+    // the references, in one pass: Z = DBL_MIN + sum q and sum q^2 d, then
+    // -sum q^2 d / Z), so that a query off the grid does not hold its wave
+    // for n_ref steps per lane.  The group's lanes take the same values.
+    unsigned long long off = __ballot(!on_grid);  // uniform over the wave
+    while (off != 0ull) {
+      const int src = __ffsll(static_cast<long long>(off)) - 1;
+      const double qx = __shfl(yi.x, src, 64);
+      const double qy = __shfl(yi.y, src, 64);
+      const int lane64 = static_cast<int>(threadIdx.x) & 63;
+      double sq = 0.0, sx = 0.0, sy = 0.0;
+      for (int m = lane64; m < n_ref; m += 64) {
+        const double2 pr = ref[m];
+        const double dx = qx - pr.x;
+        const double dy = qy - pr.y;
+        const double q = 1.0 / (1.0 + dx * dx + dy * dy);
+        const double q2 = q * q;
+        sq += q;
+        sx += q2 * dx;
+        sy += q2 * dy;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        sq += __shfl_xor(sq, o, 64);
+        sx += __shfl_xor(sx, o, 64);
+        sy += __shfl_xor(sy, o, 64);
+      }
+      const int first = src & ~(L - 1);
+      if ((lane64 & ~(L - 1)) == first) {
+        const double inv = 1.0 / (DBL_MIN + sq);
+        gx = -sx * inv;
+        gy = -sy * inv;
+        ++exact_evals;
+      }
+      off &= ~((L == 64 ? ~0ull : ((1ull << L) - 1ull)) << first);
     }
     const double ex = early ? rs.early_exaggeration : rs.exaggeration;
     double ax = 0.0, ay = 0.0;
