@@ -40,7 +40,7 @@
 //                         at most 2048 points of one tile
 //   k_lg_spread           per work item: points ordered by box in LDS; one
 //                         wave per box sums its points' 9 nodes x 4 moments
-//                         in registers and a butterfly across the wave, and
+//                         in registers and DPP adds across the wave, and
 //                         stores the box's nodes in the item's LDS window;
 //                         the window goes straight to the charge planes when
 //                         the item is its tile's only one, else to scratch
@@ -193,13 +193,29 @@ __device__ __forceinline__ void lg_accumulate(const LgPoint& b, float (&a)[4 * k
   }
 }
 
-// Sum over the 64 lanes of a wave (butterfly, the same order in every lane).
+// v + (v of the lane the DPP control `ctrl` names), 0 from lanes outside
+// row_mask or without a source.
+template <int CTRL, int ROW_MASK, bool BOUND_ZERO>
+__device__ __forceinline__ float lg_dpp_add(float v) {
+  const int src = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, BOUND_ZERO);
+  return v + __int_as_float(src);
+}
+
+// Sum over the 64 lanes of a wave into lane 63, in VALU cross-lane adds: a
+// prefix sum within each row of 16 lanes (row_shr 1, 2, 4, 8) leaves each
+// row's sum in its lane 15; row_bcast 15 adds row 0's into row 1 and row 2's
+// into row 3, row_bcast 31 adds lane 31 (rows 0 + 1) into row 3.  The order
+// is fixed, so the charges do not depend on scheduling.
 __device__ __forceinline__ void lg_wave_sum(float (&a)[4 * kLgOrder * kLgOrder]) {
 #pragma unroll
   for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) {
     float t = a[e];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
+    t = lg_dpp_add<0x111, 0xf, true>(t);   // row_shr:1
+    t = lg_dpp_add<0x112, 0xf, true>(t);   // row_shr:2
+    t = lg_dpp_add<0x114, 0xf, true>(t);   // row_shr:4
+    t = lg_dpp_add<0x118, 0xf, true>(t);   // row_shr:8
+    t = lg_dpp_add<0x142, 0xa, false>(t);  // row_bcast:15 into rows 1 and 3
+    t = lg_dpp_add<0x143, 0xc, false>(t);  // row_bcast:31 into rows 2 and 3
     a[e] = t;
   }
 }
@@ -231,7 +247,8 @@ __device__ __forceinline__ void lg_store_box(float* acc, int box, int tile, int 
 // Per work item (<= kChunk points of one tile): the points are ordered by box
 // in LDS (counting sort), then each box is reduced by one wave: lanes take the
 // box's points with stride 64 and sum their 9 x 4 contributions in
-// registers, a butterfly adds the 64 lanes, and the box's nodes are stored.
+// registers, DPP adds carry the 64 lanes into one, and the box's nodes are
+// stored.
 // A tile of one box (the early, compact layouts) splits the box's points over
 // the workgroup's waves and adds their sums in wave order.  Every order is
 // fixed, so the charges do not depend on scheduling.
@@ -313,7 +330,7 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
     for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) a[e] = 0.0f;
     for (int p = wave * 64 + lane; p < count; p += kLgThreads) lg_accumulate(lg_locate(sorted[p].x, sorted[p].y, s), a);
     lg_wave_sum(a);
-    if (lane == 0) {
+    if (lane == 63) {
 #pragma unroll
       for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) wave_part[wave][e] = a[e];
     }
@@ -338,9 +355,11 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
 #pragma unroll
       for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) a[e] = 0.0f;
       for (int p = b0 + lane; p < b1; p += 64) lg_accumulate(lg_locate(sorted[p].x, sorted[p].y, s), a);
-      // uniform over the wave; with one point, lane 0 already holds it
-      if (b1 - b0 > 1) lg_wave_sum(a);
-      if (lane == 0) lg_store_box(acc, b, tile, win, a);  // empty boxes store zeros
+      // uniform over the wave: the sum lands in lane 63; with at most one
+      // point, lane 0 already holds it (zeros for an empty box)
+      const bool many = b1 - b0 > 1;
+      if (many) lg_wave_sum(a);
+      if (lane == (many ? 63 : 0)) lg_store_box(acc, b, tile, win, a);
     }
   }
   __syncthreads();
