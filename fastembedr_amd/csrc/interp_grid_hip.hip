@@ -65,7 +65,7 @@
 // to columns XCD by XCD (col_block) so that the blocks sharing a cache line
 // of adjacent columns share one XCD's L2.  Twiddles are staged in LDS.
 //
-// The FFT length f is a power of two with f >= 2 m (m nodes per axis, read
+// The FFT length f is 2^a or 3 * 2^a with f >= 2 m (m nodes per axis, read
 // on the device); the host picks it from a bound on m.  Rows and columns of
 // the padded grid that are known to be zero are skipped.
 

@@ -524,7 +524,9 @@ __global__ __launch_bounds__(kLaneThreads) void k_transform_grid_lanes(
     // the references, in one pass: Z = DBL_MIN + sum q and sum q^2 d, then
     // -sum q^2 d / Z), so that a query off the grid does not hold its wave
     // for n_ref steps per lane.  The group's lanes take the same values.
-    unsigned long long off = __ballot(!on_grid);  // uniform over the wave
+    // Groups past the last query (their results are never stored) take no
+    // part, so that they add no wave-wide passes of their own.
+    unsigned long long off = __ballot(!on_grid && i < nq);  // uniform over the wave
     while (off != 0ull) {
       const int src = __ffsll(static_cast<long long>(off)) - 1;
       const double qx = __shfl(yi.x, src, 64);
@@ -1179,14 +1181,19 @@ constexpr std::size_t kNaScratchBytes = kNaStateOffset + sizeof(double2) * kNaMa
 constexpr int kNaMaxDevices = 64;
 
 struct NaHeader {
-  unsigned int flags;  // kNaBadDistance | kNaBadReference
+  unsigned int flags;  // kNaBadReference
   int idx_min;
   int idx_max;
   int pad;
   unsigned long long exact_evals;  // the run kernel's counter (unused by the sampled and exact modes)
+  // First failing entry (column-major position) of each kind, or ULLONG_MAX:
+  // an index outside [0, n_ref) and outside [1, n_ref] (the two offsets the
+  // host may settle on), and a distance that is not finite and >= 0.  The
+  // host reports whichever comes first, as check_inputs' sequential scan does.
+  unsigned long long first_bad_index[2];
+  unsigned long long first_bad_distance;
 };
 static_assert(sizeof(NaHeader) <= kNaReferenceOffset, "the header fits its slot");
-constexpr unsigned int kNaBadDistance = 1u;
 constexpr unsigned int kNaBadReference = 2u;
 
 }  // namespace
@@ -1203,36 +1210,55 @@ __global__ void k_na_clear(NaHeader* h) {
     h->idx_min = INT_MAX;
     h->idx_max = INT_MIN;
     h->exact_evals = 0ull;
+    h->first_bad_index[0] = ULLONG_MAX;
+    h->first_bad_index[1] = ULLONG_MAX;
+    h->first_bad_distance = ULLONG_MAX;
   }
 }
 
 // Index range and distance checks of check_inputs, as a reduction: the host
-// derives the index offset and the range error from the smallest and largest
-// index.
+// derives the index offset from the smallest and largest index, and the error
+// from the first failing entry of each kind.
+__device__ inline unsigned long long wave_min_u64(unsigned long long v) {
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(v, off);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
 __global__ __launch_bounds__(256) void k_na_check_knn(const int* __restrict__ idx_cm,
                                                       const double* __restrict__ dist_cm, long long count,
-                                                      NaHeader* h) {
+                                                      int n_ref, NaHeader* h) {
   int lo = INT_MAX, hi = INT_MIN;
-  unsigned int bad = 0u;
+  unsigned long long bad0 = ULLONG_MAX, bad1 = ULLONG_MAX, badd = ULLONG_MAX;
   const long long stride = static_cast<long long>(gridDim.x) * 256;
+  // a thread's entries ascend, so its first failure of each kind is its least
   for (long long c = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; c < count; c += stride) {
     const int v = idx_cm[c];
     lo = v < lo ? v : lo;
     hi = v > hi ? v : hi;
+    const unsigned long long at = static_cast<unsigned long long>(c);
+    if ((v < 0 || v >= n_ref) && bad0 == ULLONG_MAX) bad0 = at;
+    if ((v < 1 || v > n_ref) && bad1 == ULLONG_MAX) bad1 = at;
     const double d = dist_cm[c];
-    if (!isfinite(d) || d < 0.0) bad = 1u;
+    if ((!isfinite(d) || d < 0.0) && badd == ULLONG_MAX) badd = at;
   }
   for (int off = 32; off > 0; off >>= 1) {
     const int olo = __shfl_xor(lo, off);
     const int ohi = __shfl_xor(hi, off);
     lo = olo < lo ? olo : lo;
     hi = ohi > hi ? ohi : hi;
-    bad |= static_cast<unsigned int>(__shfl_xor(static_cast<int>(bad), off));
   }
+  bad0 = wave_min_u64(bad0);
+  bad1 = wave_min_u64(bad1);
+  badd = wave_min_u64(badd);
   if ((threadIdx.x & 63) == 0) {
     atomicMin(&h->idx_min, lo);
     atomicMax(&h->idx_max, hi);
-    if (bad != 0u) atomicOr(&h->flags, kNaBadDistance);
+    if (bad0 != ULLONG_MAX) atomicMin(&h->first_bad_index[0], bad0);
+    if (bad1 != ULLONG_MAX) atomicMin(&h->first_bad_index[1], bad1);
+    if (badd != ULLONG_MAX) atomicMin(&h->first_bad_distance, badd);
   }
 }
 
@@ -1336,7 +1362,7 @@ int fastembedr_hip_transform_tsne_noalloc(const double* reference_layout, int n_
 
   const int check_blocks = static_cast<int>(std::min<long long>((entries + 255) / 256, 2048));
   k_na_clear<<<1, 64, 0, st>>>(hdr);
-  k_na_check_knn<<<check_blocks, 256, 0, st>>>(indices, distances, entries, hdr);
+  k_na_check_knn<<<check_blocks, 256, 0, st>>>(indices, distances, entries, n_reference, hdr);
   k_na_load_reference<<<(n_reference + 255) / 256, 256, 0, st>>>(reference_layout, n_reference, ref, hdr);
   NaHeader h{};
   if (!ok(hipGetLastError(), "transform check launch") ||
@@ -1346,13 +1372,15 @@ int fastembedr_hip_transform_tsne_noalloc(const double* reference_layout, int n_
   }
   // 1-based iff every index is in [1, n_reference] (:1290-1302), then every
   // index must name a reference row.
+  // check_inputs scans the entries in order and stops at the first that
+  // fails either check, so the earlier failing entry names the error.
   const int offset = (h.idx_min >= 1 && h.idx_max <= n_reference) ? 1 : 0;
-  if (static_cast<long long>(h.idx_min) - offset < 0 ||
-      static_cast<long long>(h.idx_max) - offset >= static_cast<long long>(n_reference)) {
+  const unsigned long long bad_index = h.first_bad_index[offset];
+  if (bad_index != ULLONG_MAX && bad_index <= h.first_bad_distance) {
     set_last_error("KNN indices are out of range for `reference_layout`.");
     return 1;
   }
-  if ((h.flags & kNaBadDistance) != 0u) {
+  if (h.first_bad_distance != ULLONG_MAX) {
     set_last_error("KNN distances must be finite and non-negative.");
     return 1;
   }

@@ -315,11 +315,14 @@ FASTEMBEDR_HIP_API int fastembedr_hip_transform_grid_probe(
     double* grad_out, long long* stats);
 
 /* Allocation-free variant of fastembedr_hip_transform_tsne.  No counterpart in
- * the reference: it is for callers that cannot allocate device memory (code
- * under HIP graph capture, serving loops that place batches of new points
- * against a fixed map, harnesses that forbid hipMalloc).  Same arguments,
- * meaning, checks, error messages and result as fastembedr_hip_transform_tsne
- * (the same kernels in the same order), except:
+ * the reference: it is for callers that cannot allocate device memory
+ * (serving loops that place batches of new points against a fixed map,
+ * harnesses that forbid hipMalloc).  It cannot be recorded into a HIP graph:
+ * it launches on the null stream and waits for the device twice (to read the
+ * input checks' result, and at the end).  Same arguments, meaning, checks,
+ * error messages (for an input with several faults, the one that comes first
+ * in column-major entry order, as in the allocating call) and result as
+ * fastembedr_hip_transform_tsne (the same kernels in the same order), except:
  *   - reference_layout, indices, distances, y_init and out are DEVICE
  *     pointers, in the same layouts;
  *   - initialization 2 (random, drawn on the host) needs y_init;

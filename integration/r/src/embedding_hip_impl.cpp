@@ -118,6 +118,11 @@ void check_opt_args(const OptArgs& a, int n, int k, bool init, const NumericMatr
     Rcpp::stop("HIP openTSNE FFT-grid supports between 1 and %d neighbors.", kMaxHipNeighbors);
   }
   if (a.perplexity <= 0.0) Rcpp::stop("perplexity must be positive");
+  // The CPU driver's rule (src/tsne_neighbors.cpp:1652), checked here so that
+  // the one-shot route and the cost-recording session route refuse alike.
+  if (static_cast<double>(n - 1) < 3.0 * a.perplexity) {
+    Rcpp::stop("perplexity is too large for the number of samples.");
+  }
   if (a.early_iter < 0 || a.n_iter < 0 || a.early_iter + a.n_iter < 1) {
     Rcpp::stop("HIP openTSNE FFT-grid requires at least one optimization iteration.");
   }

@@ -45,6 +45,7 @@ def load() -> C.CDLL:
         "tsne_oracle_p_copy": (None, [P, P, P, P]),
         "tsne_oracle_p_free": (None, [P]),
         "tsne_oracle_gradient": (I, [P, P, I, F, I, I, I, I, I, P]),
+        "tsne_oracle_gradient_grid_f64": (I, [P, P, I, F, I, I, P]),
         "tsne_oracle_grid_fields": (I, [P, P, I, I, I, P, P]),
         "tsne_oracle_lagrange_gradient": (I, [P, P, I, F, I, I, F, I, I, P, P, P]),
         "tsne_oracle_lagrange_weights": (None, [D, I, P]),
@@ -149,6 +150,19 @@ class OracleP:
         g = np.empty((self.n, 2), np.float32)
         rc = load().tsne_oracle_gradient(self.h, _p(y), self.n, float(exaggeration), int(method), int(grid_size),
                                          int(lagrange_order), int(min_intervals), int(threads), _p(g))
+        if rc != 0:
+            raise ValueError(_err())
+        return g
+
+    def gradient_grid_f64(self, y: np.ndarray, exaggeration: float = 1.0, grid_size: int = 0,
+                          threads: int = 1) -> np.ndarray:
+        """The bilinear grid gradient (method METHOD_GRID) with every step in
+        fp64: the same algorithm as the reference's fp32 path, evaluated with
+        fp64 rounding, so that each fp32 side's own error can be read off."""
+        y = np.ascontiguousarray(y, np.float32).reshape(self.n, 2)
+        g = np.empty((self.n, 2), np.float64)
+        rc = load().tsne_oracle_gradient_grid_f64(self.h, _p(y), self.n, float(exaggeration), int(grid_size),
+                                                  int(threads), _p(g))
         if rc != 0:
             raise ValueError(_err())
         return g

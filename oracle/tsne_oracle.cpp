@@ -367,11 +367,18 @@ int resolve_grid_size(int n, int requested) {
   return g;
 }
 
-struct Radix2Plan {
+// The bilinear grid's pieces are templates on the arithmetic type, as the
+// reference's are (FftGridWorkspaceT<T>, fft_1d_t, fft_2d_t,
+// bilinear_grid_value_t, src/tsne_neighbors.cpp:650-942): T = float is the
+// reference's path; T = double evaluates the same algorithm in fp64, the
+// yardstick that separates either fp32 side's rounding from the other's.
+template <typename T>
+struct Radix2PlanT {
+  using C = std::complex<T>;
   int size = 0;
   std::vector<int> rev;
-  std::vector<cf> up;    // e^{+2 pi i / len}, used by the transform the reference calls forward
-  std::vector<cf> down;  // e^{-2 pi i / len}
+  std::vector<C> up;    // e^{+2 pi i / len}, used by the transform the reference calls forward
+  std::vector<C> down;  // e^{-2 pi i / len}
   void build(int f) {
     if (size == f) return;
     size = f;
@@ -389,7 +396,7 @@ struct Radix2Plan {
     up.clear();
     down.clear();
     for (int len = 2; len <= f; len <<= 1) {
-      const float ang = static_cast<float>(6.283185307179586476925286766559) / static_cast<float>(len);
+      const T ang = static_cast<T>(6.283185307179586476925286766559) / static_cast<T>(len);
       up.emplace_back(std::cos(ang), std::sin(ang));
       down.emplace_back(std::cos(-ang), std::sin(-ang));
     }
@@ -400,21 +407,23 @@ struct Radix2Plan {
 // twiddle recurrence w *= root (src/tsne_neighbors.cpp:697-729).  The
 // reference's "forward" transform uses the +i exponent; the convolution below
 // only needs forward/inverse to be mutually inverse.
-void fft_radix2(cf* a, int f, bool inverse, const Radix2Plan& plan) {
+template <typename T>
+void fft_radix2(std::complex<T>* a, int f, bool inverse, const Radix2PlanT<T>& plan) {
+  using C = std::complex<T>;
   for (int i = 1; i < f; ++i) {
     const int j = plan.rev[static_cast<std::size_t>(i)];
     if (i < j) std::swap(a[i], a[j]);
   }
-  const std::vector<cf>& roots = inverse ? plan.down : plan.up;
+  const std::vector<C>& roots = inverse ? plan.down : plan.up;
   int stage = 0;
   for (int len = 2; len <= f; len <<= 1, ++stage) {
-    const cf root = roots[static_cast<std::size_t>(stage)];
+    const C root = roots[static_cast<std::size_t>(stage)];
     const int half = len >> 1;
     for (int s = 0; s < f; s += len) {
-      cf w(1.0f, 0.0f);
+      C w(T(1), T(0));
       for (int j = 0; j < half; ++j) {
-        const cf u = a[s + j];
-        const cf v = a[s + j + half] * w;
+        const C u = a[s + j];
+        const C v = a[s + j + half] * w;
         a[s + j] = u + v;
         a[s + j + half] = u - v;
         w *= root;
@@ -422,25 +431,26 @@ void fft_radix2(cf* a, int f, bool inverse, const Radix2Plan& plan) {
     }
   }
   if (inverse) {
-    const float sc = 1.0f / static_cast<float>(f);
+    const T sc = T(1) / static_cast<T>(f);
     for (int i = 0; i < f; ++i) a[i] *= sc;
   }
 }
 
 // Rows, then columns through a per-thread scratch column
 // (src/tsne_neighbors.cpp:731-758).
-void fft_2d(std::vector<cf>& grid, int f, bool inverse, int threads, const Radix2Plan& plan,
-            std::vector<cf>& scratch) {
+template <typename T>
+void fft_2d(std::vector<std::complex<T>>& grid, int f, bool inverse, int threads, const Radix2PlanT<T>& plan,
+            std::vector<std::complex<T>>& scratch) {
   parallel_for(f, threads, [&](int b, int e, int) {
-    for (int r = b; r < e; ++r) fft_radix2(grid.data() + static_cast<std::size_t>(r) * f, f, inverse, plan);
+    for (int r = b; r < e; ++r) fft_radix2<T>(grid.data() + static_cast<std::size_t>(r) * f, f, inverse, plan);
   });
   if (static_cast<int>(scratch.size()) < f * std::max(1, threads))
-    scratch.assign(static_cast<std::size_t>(f) * std::max(1, threads), cf());
+    scratch.assign(static_cast<std::size_t>(f) * std::max(1, threads), std::complex<T>());
   parallel_for(f, threads, [&](int b, int e, int t) {
-    cf* column = scratch.data() + static_cast<std::size_t>(t) * f;
+    std::complex<T>* column = scratch.data() + static_cast<std::size_t>(t) * f;
     for (int c = b; c < e; ++c) {
       for (int r = 0; r < f; ++r) column[r] = grid[static_cast<std::size_t>(r) * f + c];
-      fft_radix2(column, f, inverse, plan);
+      fft_radix2<T>(column, f, inverse, plan);
       for (int r = 0; r < f; ++r) grid[static_cast<std::size_t>(r) * f + c] = column[r];
     }
   });
@@ -448,71 +458,76 @@ void fft_2d(std::vector<cf>& grid, int f, bool inverse, int threads, const Radix
 
 // Bilinear read of a g x g grid at fractional node coordinates
 // (src/tsne_neighbors.cpp:760-781).
-float bilinear(const std::vector<float>& grid, int g, float gx, float gy) {
-  const float cx = std::max(0.0f, std::min(static_cast<float>(g - 1), gx));
-  const float cy = std::max(0.0f, std::min(static_cast<float>(g - 1), gy));
+template <typename T>
+T bilinear(const std::vector<T>& grid, int g, T gx, T gy) {
+  const T cx = std::max(T(0), std::min(static_cast<T>(g - 1), gx));
+  const T cy = std::max(T(0), std::min(static_cast<T>(g - 1), gy));
   const int x0 = std::max(0, std::min(g - 2, static_cast<int>(std::floor(cx))));
   const int y0 = std::max(0, std::min(g - 2, static_cast<int>(std::floor(cy))));
-  const float tx = cx - static_cast<float>(x0);
-  const float ty = cy - static_cast<float>(y0);
-  const float v00 = grid[static_cast<std::size_t>(y0) * g + x0];
-  const float v10 = grid[static_cast<std::size_t>(y0) * g + x0 + 1];
-  const float v01 = grid[static_cast<std::size_t>(y0 + 1) * g + x0];
-  const float v11 = grid[static_cast<std::size_t>(y0 + 1) * g + x0 + 1];
-  return (1.0f - tx) * (1.0f - ty) * v00 + tx * (1.0f - ty) * v10 +
-         (1.0f - tx) * ty * v01 + tx * ty * v11;
+  const T tx = cx - static_cast<T>(x0);
+  const T ty = cy - static_cast<T>(y0);
+  const T v00 = grid[static_cast<std::size_t>(y0) * g + x0];
+  const T v10 = grid[static_cast<std::size_t>(y0) * g + x0 + 1];
+  const T v01 = grid[static_cast<std::size_t>(y0 + 1) * g + x0];
+  const T v11 = grid[static_cast<std::size_t>(y0 + 1) * g + x0 + 1];
+  return (T(1) - tx) * (T(1) - ty) * v00 + tx * (T(1) - ty) * v10 +
+         (T(1) - tx) * ty * v01 + tx * ty * v11;
 }
 
-struct GridScratch {
+template <typename T>
+struct GridScratchT {
   int g = 0;
-  Radix2Plan plan;
-  std::vector<float> mass, mass_x, mass_y, gx, gy, q, q2, xq2, yq2;
-  std::vector<cf> f_mass, f_mx, f_my, k1, k2, work, column;
+  Radix2PlanT<T> plan;
+  std::vector<T> mass, mass_x, mass_y, gx, gy, q, q2, xq2, yq2;
+  std::vector<std::complex<T>> f_mass, f_mx, f_my, k1, k2, work, column;
 };
+using GridScratch = GridScratchT<float>;
 
 // Zero-padded circular convolution of the three charge grids with the Cauchy
 // kernel and its square (src/tsne_neighbors.cpp:842-942).
-void grid_convolve(GridScratch& ws, float spacing, int threads) {
+template <typename T>
+void grid_convolve(GridScratchT<T>& ws, T spacing, int threads) {
+  using C = std::complex<T>;
   const int g = ws.g;
   const int f = 2 * g;
   const std::size_t ff = static_cast<std::size_t>(f) * f;
   ws.plan.build(f);
-  auto pad = [&](const std::vector<float>& src, std::vector<cf>& dst) {
-    dst.assign(ff, cf(0.0f, 0.0f));
+  auto pad = [&](const std::vector<T>& src, std::vector<C>& dst) {
+    dst.assign(ff, C(T(0), T(0)));
     for (int r = 0; r < g; ++r)
       for (int c = 0; c < g; ++c)
-        dst[static_cast<std::size_t>(r) * f + c] = cf(src[static_cast<std::size_t>(r) * g + c], 0.0f);
+        dst[static_cast<std::size_t>(r) * f + c] = C(src[static_cast<std::size_t>(r) * g + c], T(0));
   };
   pad(ws.mass, ws.f_mass);
   pad(ws.mass_x, ws.f_mx);
   pad(ws.mass_y, ws.f_my);
-  ws.k1.assign(ff, cf(0.0f, 0.0f));
-  ws.k2.assign(ff, cf(0.0f, 0.0f));
+  ws.k1.assign(ff, C(T(0), T(0)));
+  ws.k2.assign(ff, C(T(0), T(0)));
   for (int dy = -(g - 1); dy <= g - 1; ++dy) {
     const int row = dy < 0 ? dy + f : dy;
-    const float oy = static_cast<float>(dy) * spacing;
+    const T oy = static_cast<T>(dy) * spacing;
     for (int dx = -(g - 1); dx <= g - 1; ++dx) {
       const int colx = dx < 0 ? dx + f : dx;
-      const float ox = static_cast<float>(dx) * spacing;
-      const float r2 = ox * ox + oy * oy;
-      const float qv = 1.0f / (1.0f + r2);
+      const T ox = static_cast<T>(dx) * spacing;
+      const T r2 = ox * ox + oy * oy;
+      const T qv = T(1) / (T(1) + r2);
       const std::size_t at = static_cast<std::size_t>(row) * f + colx;
-      ws.k1[at] = cf(qv, 0.0f);
-      ws.k2[at] = cf(qv * qv, 0.0f);
+      ws.k1[at] = C(qv, T(0));
+      ws.k2[at] = C(qv * qv, T(0));
     }
   }
-  fft_2d(ws.f_mass, f, false, threads, ws.plan, ws.column);
-  fft_2d(ws.f_mx, f, false, threads, ws.plan, ws.column);
-  fft_2d(ws.f_my, f, false, threads, ws.plan, ws.column);
-  fft_2d(ws.k1, f, false, threads, ws.plan, ws.column);
-  fft_2d(ws.k2, f, false, threads, ws.plan, ws.column);
-  auto conv = [&](const std::vector<cf>& a, const std::vector<cf>& b, std::vector<float>& out) {
+  fft_2d<T>(ws.f_mass, f, false, threads, ws.plan, ws.column);
+  fft_2d<T>(ws.f_mx, f, false, threads, ws.plan, ws.column);
+  fft_2d<T>(ws.f_my, f, false, threads, ws.plan, ws.column);
+  fft_2d<T>(ws.k1, f, false, threads, ws.plan, ws.column);
+  fft_2d<T>(ws.k2, f, false, threads, ws.plan, ws.column);
+  auto conv = [&](const std::vector<C>& a, const std::vector<C>& b, std::vector<T>& out) {
     ws.work.resize(ff);
     parallel_for(static_cast<int>(ff), threads, [&](int lo, int hi, int) {
       for (int i = lo; i < hi; ++i) ws.work[static_cast<std::size_t>(i)] = a[static_cast<std::size_t>(i)] * b[static_cast<std::size_t>(i)];
     });
-    fft_2d(ws.work, f, true, threads, ws.plan, ws.column);
-    out.assign(static_cast<std::size_t>(g) * g, 0.0f);
+    fft_2d<T>(ws.work, f, true, threads, ws.plan, ws.column);
+    out.assign(static_cast<std::size_t>(g) * g, T(0));
     for (int r = 0; r < g; ++r)
       for (int c = 0; c < g; ++c)
         out[static_cast<std::size_t>(r) * g + c] = ws.work[static_cast<std::size_t>(r) * f + c].real();
@@ -525,18 +540,19 @@ void grid_convolve(GridScratch& ws, float spacing, int threads) {
 
 // Attractive term over the CSR rows (src/tsne_neighbors.cpp:985-1012);
 // openTSNE convention, no factor 4.
-void add_attraction(const CsrP& p, const float* y, int n, float ex, int threads, float* grad) {
+template <typename T>
+void add_attraction(const CsrP& p, const float* y, int n, T ex, int threads, T* grad) {
   parallel_for(n, threads, [&](int b, int e, int) {
     for (int i = b; i < e; ++i) {
       for (int at = p.row_ptr[i]; at < p.row_ptr[i + 1]; ++at) {
         const int j = p.col[static_cast<std::size_t>(at)];
-        const float dx = y[2 * i] - y[2 * j];
-        const float dy = y[2 * i + 1] - y[2 * j + 1];
-        float r2 = 0.0f;
+        const T dx = static_cast<T>(y[2 * i]) - static_cast<T>(y[2 * j]);
+        const T dy = static_cast<T>(y[2 * i + 1]) - static_cast<T>(y[2 * j + 1]);
+        T r2 = T(0);
         r2 += dx * dx;
         r2 += dy * dy;
-        const float qv = 1.0f / (1.0f + r2);
-        const float c = ex * p.val[static_cast<std::size_t>(at)] * qv;
+        const T qv = T(1) / (T(1) + r2);
+        const T c = ex * static_cast<T>(p.val[static_cast<std::size_t>(at)]) * qv;
         grad[2 * i] += c * dx;
         grad[2 * i + 1] += c * dy;
       }
@@ -547,26 +563,28 @@ void add_attraction(const CsrP& p, const float* y, int n, float ex, int threads,
 // Bilinear FFT-grid gradient (src/tsne_neighbors.cpp:1076-1182).  Geometry:
 // square box of side 1.1 * span + 2e-3 centred on the bounding box, g nodes
 // per axis; bilinear spread of (1, x, y) charges; convolution; bilinear read
-// back; normalisation by sum(q) - n; attraction added last.
-void gradient_grid(const CsrP& p, const float* y, int n, float ex, int g, int threads,
-                   GridScratch& ws, float* grad, float* geometry_out) {
-  std::fill(grad, grad + 2 * static_cast<std::size_t>(n), 0.0f);
-  float min_x = y[0], max_x = y[0], min_y = y[1], max_y = y[1];
+// back; normalisation by sum(q) - n; attraction added last.  The layout y is
+// fp32 (the optimiser's state) for either T.
+template <typename T>
+void gradient_grid(const CsrP& p, const float* y, int n, T ex, int g, int threads,
+                   GridScratchT<T>& ws, T* grad, T* geometry_out) {
+  std::fill(grad, grad + 2 * static_cast<std::size_t>(n), T(0));
+  T min_x = y[0], max_x = y[0], min_y = y[1], max_y = y[1];
   for (int i = 1; i < n; ++i) {
-    min_x = std::min(min_x, y[2 * i]);
-    max_x = std::max(max_x, y[2 * i]);
-    min_y = std::min(min_y, y[2 * i + 1]);
-    max_y = std::max(max_y, y[2 * i + 1]);
+    min_x = std::min(min_x, static_cast<T>(y[2 * i]));
+    max_x = std::max(max_x, static_cast<T>(y[2 * i]));
+    min_y = std::min(min_y, static_cast<T>(y[2 * i + 1]));
+    max_y = std::max(max_y, static_cast<T>(y[2 * i + 1]));
   }
-  const float cx = 0.5f * (min_x + max_x);
-  const float cy = 0.5f * (min_y + max_y);
-  float span = std::max(max_x - min_x, max_y - min_y);
-  if (!std::isfinite(span) || span <= 0.0f) span = 1.0f;
-  const float half = 0.55f * span + 1.0e-3f;
-  const float lo_x = cx - half;
-  const float lo_y = cy - half;
-  const float h = (2.0f * half) / static_cast<float>(g - 1);
-  const float inv_h = 1.0f / h;
+  const T cx = T(0.5) * (min_x + max_x);
+  const T cy = T(0.5) * (min_y + max_y);
+  T span = std::max(max_x - min_x, max_y - min_y);
+  if (!std::isfinite(span) || span <= T(0)) span = T(1);
+  const T half = static_cast<T>(0.55) * span + static_cast<T>(1.0e-3);
+  const T lo_x = cx - half;
+  const T lo_y = cy - half;
+  const T h = (T(2) * half) / static_cast<T>(g - 1);
+  const T inv_h = T(1) / h;
   if (geometry_out != nullptr) {
     geometry_out[0] = lo_x;
     geometry_out[1] = lo_y;
@@ -576,26 +594,26 @@ void gradient_grid(const CsrP& p, const float* y, int n, float ex, int g, int th
 
   ws.g = g;
   const std::size_t gg = static_cast<std::size_t>(g) * g;
-  ws.mass.assign(gg, 0.0f);
-  ws.mass_x.assign(gg, 0.0f);
-  ws.mass_y.assign(gg, 0.0f);
-  ws.gx.assign(static_cast<std::size_t>(n), 0.0f);
-  ws.gy.assign(static_cast<std::size_t>(n), 0.0f);
+  ws.mass.assign(gg, T(0));
+  ws.mass_x.assign(gg, T(0));
+  ws.mass_y.assign(gg, T(0));
+  ws.gx.assign(static_cast<std::size_t>(n), T(0));
+  ws.gy.assign(static_cast<std::size_t>(n), T(0));
   for (int i = 0; i < n; ++i) {  // sequential on purpose, as in the reference
-    const float px = y[2 * i];
-    const float py = y[2 * i + 1];
-    const float ux = std::max(0.0f, std::min(static_cast<float>(g - 1), (px - lo_x) * inv_h));
-    const float uy = std::max(0.0f, std::min(static_cast<float>(g - 1), (py - lo_y) * inv_h));
+    const T px = y[2 * i];
+    const T py = y[2 * i + 1];
+    const T ux = std::max(T(0), std::min(static_cast<T>(g - 1), (px - lo_x) * inv_h));
+    const T uy = std::max(T(0), std::min(static_cast<T>(g - 1), (py - lo_y) * inv_h));
     const int x0 = std::max(0, std::min(g - 2, static_cast<int>(std::floor(ux))));
     const int y0 = std::max(0, std::min(g - 2, static_cast<int>(std::floor(uy))));
-    const float tx = ux - static_cast<float>(x0);
-    const float ty = uy - static_cast<float>(y0);
+    const T tx = ux - static_cast<T>(x0);
+    const T ty = uy - static_cast<T>(y0);
     ws.gx[static_cast<std::size_t>(i)] = ux;
     ws.gy[static_cast<std::size_t>(i)] = uy;
-    const float w00 = (1.0f - tx) * (1.0f - ty);
-    const float w10 = tx * (1.0f - ty);
-    const float w01 = (1.0f - tx) * ty;
-    const float w11 = tx * ty;
+    const T w00 = (T(1) - tx) * (T(1) - ty);
+    const T w10 = tx * (T(1) - ty);
+    const T w01 = (T(1) - tx) * ty;
+    const T w11 = tx * ty;
     const std::size_t a00 = static_cast<std::size_t>(y0) * g + x0;
     const std::size_t a10 = a00 + 1;
     const std::size_t a01 = a00 + g;
@@ -614,31 +632,31 @@ void gradient_grid(const CsrP& p, const float* y, int n, float ex, int g, int th
     ws.mass_y[a11] += w11 * py;
   }
 
-  grid_convolve(ws, h, threads);
+  grid_convolve<T>(ws, h, threads);
 
   const int t_count = std::max(1, threads);
   std::vector<double> partial(static_cast<std::size_t>(t_count), 0.0);
   parallel_for(n, t_count, [&](int b, int e, int t) {
     double acc = 0.0;
     for (int i = b; i < e; ++i)
-      acc += static_cast<double>(bilinear(ws.q, g, ws.gx[static_cast<std::size_t>(i)], ws.gy[static_cast<std::size_t>(i)]));
+      acc += static_cast<double>(bilinear<T>(ws.q, g, ws.gx[static_cast<std::size_t>(i)], ws.gy[static_cast<std::size_t>(i)]));
     partial[static_cast<std::size_t>(t)] = acc;
   });
   const double total = std::accumulate(partial.begin(), partial.end(), 0.0);
-  const float inv_z = static_cast<float>(1.0 / std::max(total - static_cast<double>(n), static_cast<double>(FLT_MIN)));
+  const T inv_z = static_cast<T>(1.0 / std::max(total - static_cast<double>(n), static_cast<double>(FLT_MIN)));
 
   parallel_for(n, t_count, [&](int b, int e, int) {
     for (int i = b; i < e; ++i) {
-      const float ux = ws.gx[static_cast<std::size_t>(i)];
-      const float uy = ws.gy[static_cast<std::size_t>(i)];
-      const float a = bilinear(ws.q2, g, ux, uy);
-      const float bx = bilinear(ws.xq2, g, ux, uy);
-      const float by = bilinear(ws.yq2, g, ux, uy);
-      grad[2 * i] = -(y[2 * i] * a - bx) * inv_z;
-      grad[2 * i + 1] = -(y[2 * i + 1] * a - by) * inv_z;
+      const T ux = ws.gx[static_cast<std::size_t>(i)];
+      const T uy = ws.gy[static_cast<std::size_t>(i)];
+      const T a = bilinear<T>(ws.q2, g, ux, uy);
+      const T bx = bilinear<T>(ws.xq2, g, ux, uy);
+      const T by = bilinear<T>(ws.yq2, g, ux, uy);
+      grad[2 * i] = -(static_cast<T>(y[2 * i]) * a - bx) * inv_z;
+      grad[2 * i + 1] = -(static_cast<T>(y[2 * i + 1]) * a - by) * inv_z;
     }
   });
-  add_attraction(p, y, n, ex, t_count, grad);
+  add_attraction<T>(p, y, n, ex, t_count, grad);
 }
 
 // Exact O(n^2) repulsion with a strided pair partition
@@ -1046,7 +1064,7 @@ void gradient(const CsrP& p, const float* y, int n, float ex, const GradientConf
     gradient_lagrange(p, y, n, ex, cfg.lagrange_order, cfg.min_intervals, cfg.ints_per_unit, threads, grad,
                       nullptr);
   } else {
-    gradient_grid(p, y, n, ex, resolve_grid_size(n, cfg.grid_size), threads, ws, grad, nullptr);
+    gradient_grid<float>(p, y, n, ex, resolve_grid_size(n, cfg.grid_size), threads, ws, grad, nullptr);
   }
 }
 
@@ -1130,6 +1148,23 @@ int tsne_oracle_gradient(void* h, const float* y, int n, float exaggeration, int
   return 0;
 }
 
+// The bilinear FFT-grid gradient of tsne_oracle_gradient (method 0) with
+// every step in fp64 (extension): the same algorithm, spread, recurrence
+// twiddles and read-back, with fp64 arithmetic; y is the fp32 layout.
+int tsne_oracle_gradient_grid_f64(void* h, const float* y, int n, float exaggeration, int grid_size, int threads,
+                                  double* grad) {
+  g_error.clear();
+  const CsrP& p = *static_cast<CsrP*>(h);
+  if (p.n != n) {
+    g_error = "P has a different number of rows";
+    return 1;
+  }
+  GridScratchT<double> ws;
+  gradient_grid<double>(p, y, n, static_cast<double>(exaggeration), resolve_grid_size(n, grid_size), threads, ws,
+                        grad, nullptr);
+  return 0;
+}
+
 // FIt-SNE interpolation-grid gradient (extension) with its geometry
 // (boxes, nodes, lo, box width) and normaliser Z; direct != 0 convolves by
 // the O(nodes^4) node sum instead of the FFT.
@@ -1164,7 +1199,7 @@ int tsne_oracle_grid_fields(void* h, const float* y, int n, int grid_size, int t
   const int g = resolve_grid_size(n, grid_size);
   GridScratch ws;
   std::vector<float> grad(2 * static_cast<std::size_t>(n));
-  gradient_grid(p, y, n, 1.0f, g, threads, ws, grad.data(), geometry);
+  gradient_grid<float>(p, y, n, 1.0f, g, threads, ws, grad.data(), geometry);
   const std::size_t gg = static_cast<std::size_t>(g) * g;
   if (fields != nullptr) {
     std::copy(ws.q.begin(), ws.q.end(), fields);

@@ -194,9 +194,11 @@ def test_closed_session_returns_memory(hip, capture):
     memory then reads at the in-session level, and the next session's
     identical requests reuse them), so a single reading may be one
     session's buffers low; a leak instead lowers every later reading.  The
-    check: over the last five sessions the readings spread by less than 1.5
-    sessions' buffers (graphs with parallel branches lost 1.4 GB per session
-    here, a spread of 5.6 GB against 2.6 GB of buffers)."""
+    check, over the last five sessions: every reading within 64 MiB of the
+    highest, except at most one that sits at the in-session level (within
+    64 MiB of the lowest in-session reading).  Graphs with parallel branches
+    lost 1.4 GB per session here; a steady leak of more than 22 MiB per
+    session fails."""
     n, k = 200_000, 90
     x, _ = synthetic.gaussian_mixture(synthetic.CONFIGS[2], seed=1, n=n)
     knn = hip.exact_knn(np.ascontiguousarray(x, np.float32), k, keep_device=True)
@@ -238,4 +240,8 @@ def test_closed_session_returns_memory(hip, capture):
          f"after them {[mib(v) for v in after]}, {info}")
     footprint = start - during[0]  # one session's buffers
     assert footprint > 256 * 2**20
-    assert max(after[2:]) - min(after[2:]) < 1.5 * footprint
+    slack = 64 * 2**20
+    top, in_session = max(after[2:]), min(during)
+    held = [v for v in after[2:] if top - v > slack]
+    assert len(held) <= 1, (after, during)
+    assert all(abs(v - in_session) <= slack for v in held), (after, during)

@@ -6,6 +6,8 @@
 * symmetrisation: the closed form P = (C + C^T) / (2 * total) with scipy.sparse;
 * grid convolution: numpy.fft on the zero-padded charge grids;
 * grid repulsion: convergence to the exact O(n^2) gradient as the grid refines;
+  its fp64 instantiation against a numpy float64 statement of the whole
+  bilinear-grid gradient (geometry, spread, numpy.fft, read-back, attraction);
 * exact gradient and KL: dense closed forms;
 * update: elementwise closed form including the sign(0) == 0 first step.
 """
@@ -148,6 +150,52 @@ def test_grid_fields_match_numpy_fft(oracle_mod, grid):
     ref = _numpy_fields(y, geom, grid)
     for c in range(4):
         assert rel_l2(fields[c], ref[c]) < 2e-5, c
+
+
+def _numpy_bilinear(field, ux, uy, g):
+    x0 = np.clip(np.floor(ux).astype(int), 0, g - 2)
+    y0 = np.clip(np.floor(uy).astype(int), 0, g - 2)
+    tx, ty = ux - x0, uy - y0
+    return ((1 - tx) * (1 - ty) * field[y0, x0] + tx * (1 - ty) * field[y0, x0 + 1]
+            + (1 - tx) * ty * field[y0 + 1, x0] + tx * ty * field[y0 + 1, x0 + 1])
+
+
+@pytest.mark.parametrize("grid", [32, 128])
+def test_fp64_grid_gradient_matches_numpy_closed_form(oracle_mod, grid):
+    """The fp64 bilinear-grid gradient (the yardstick for both fp32 sides)
+    against numpy in float64: the geometry, bilinear spread, numpy.fft
+    convolution, bilinear read-back, normalisation by sum(q) - n and the
+    dense attraction closed form."""
+    n = 500
+    x, _, idx, dist = small_problem(n=n, k=20)
+    P = oracle_mod.OracleP.build(idx, dist, 6.0)
+    rp, col, val = P.csr()
+    dense = csr_to_dense(rp, col, val, n)
+    rng = np.random.default_rng(12)
+    y = (rng.standard_normal((n, 2)) * 7).astype(np.float32)
+    y64 = y.astype(np.float64)
+    lo, hi = y64.min(0), y64.max(0)
+    span = float(max(hi - lo))
+    half = 0.55 * span + 1e-3
+    c = 0.5 * (lo + hi)
+    h = 2 * half / (grid - 1)
+    geom = (c[0] - half, c[1] - half, h, 1.0 / h)
+    q, q2, xq2, yq2 = _numpy_fields(y64, geom, grid)
+    ux = np.clip((y64[:, 0] - geom[0]) / h, 0, grid - 1)
+    uy = np.clip((y64[:, 1] - geom[1]) / h, 0, grid - 1)
+    z = _numpy_bilinear(q, ux, uy, grid).sum() - n
+    a = _numpy_bilinear(q2, ux, uy, grid)
+    rep = -np.stack([y64[:, 0] * a - _numpy_bilinear(xq2, ux, uy, grid),
+                     y64[:, 1] * a - _numpy_bilinear(yq2, ux, uy, grid)], 1) / z
+    d = y64[:, None, :] - y64[None, :, :]
+    qq = 1.0 / (1.0 + (d * d).sum(-1))
+    for ex in (1.0, 12.0):
+        want = rep + ex * ((dense * qq)[:, :, None] * d).sum(1)
+        got = P.gradient_grid_f64(y, ex, grid_size=grid, threads=3)
+        assert got.dtype == np.float64
+        assert rel_l2(got, want) < 1e-10
+        # and the fp32 path is the same algorithm, to fp32 rounding
+        assert rel_l2(P.gradient(y, ex, grid_size=grid, threads=3), got) < 1e-4
 
 
 def test_exact_gradient_closed_form(oracle_mod):

@@ -114,3 +114,19 @@ def test_impl_calls_only_declared_abi_and_files_agree():
     r_code = (RDIR / "R" / "hip_backend.R").read_text()
     used = set(re.findall(r"\b(\w+_hip\w*_cpp)\b", r_code))
     assert used <= exports, used - exports
+
+
+def test_impl_checks_perplexity_before_either_route():
+    """check_opt_args refuses n - 1 < 3 * perplexity (the CPU driver's rule,
+    src/tsne_neighbors.cpp:1652) for both the one-shot route and the
+    cost-recording session route, which calls it before branching."""
+    impl = (RDIR / "src" / "embedding_hip_impl.cpp").read_text()
+    body = impl[impl.index("void check_opt_args("):]
+    body = body[:body.index("\n}\n")]
+    assert re.search(r"n - 1\)\s*<\s*3\.0 \* a\.perplexity", body)
+    assert "perplexity is too large for the number of samples." in body
+    for entry in re.finditer(r"\nList (\w+_impl)\(", impl):
+        fn = impl[entry.end():]
+        fn = fn[:fn.index("\n}\n")]
+        if "record_costs" in fn:
+            assert fn.index("check_opt_args(") < fn.index("if (record_costs)"), entry.group(1)

@@ -131,6 +131,19 @@ def test_noalloc_transform_refusals(hip):
     dneg[0, 0] = -1.0
     rc, _, _ = _noalloc_call(ref, idx, dneg, _params(n_iter=1))
     assert rc == 1 and b"finite and non-negative" in lib.fastembedr_hip_embedding_last_error()
+    # both errors in one input: the earlier entry in column-major order names
+    # the error, in both calls (the allocating call scans the entries in order)
+    nq = idx.shape[0]
+    for (bi, bj), (di, dj) in (((3, 2), (0, 0)), ((0, 0), (5, 3)), ((7, 1), (7, 1)), ((150, 0), (2, 1))):
+        both_i, both_d = idx.copy(), dist.copy()
+        both_i[bi, bj] = 10 ** 6
+        both_d[di, dj] = np.nan
+        want_msg = b"out of range" if bj * nq + bi <= dj * nq + di else b"finite and non-negative"
+        with pytest.raises(RuntimeError) as err:
+            _host_call(ref, both_i, both_d, _params(n_iter=1))
+        assert want_msg.decode() in str(err.value)
+        rc, _, _ = _noalloc_call(ref, both_i, both_d, _params(n_iter=1))
+        assert rc == 1 and want_msg in lib.fastembedr_hip_embedding_last_error()
     # after refusals the shared buffer still gives the allocating call's result
     want, _ = _host_call(ref, idx, dist, _params(n_iter=5))
     rc, got, _ = _noalloc_call(ref, idx, dist, _params(n_iter=5))
