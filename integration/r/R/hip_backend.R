@@ -1,8 +1,8 @@
 # HIP (AMD MI355X, gfx950) backend of fastEmbedR's openTSNE path.
 #
 # These helpers are what the package's existing switch points call for
-# backend = "hip"; each switch point gains one branch (the hook list is in the
-# repository's integration notes):
+# backend = "hip"; each switch point gains one branch, shipped as unified
+# diffs against the package's files in integration/r/patches/:
 #   embedding_backend_choices()          (R/backend_info.R:102-104)  adds "hip"
 #   backend_info()                       (R/backend_info.R:2-41)     rbind(hip_backend_info_row())
 #   fast_knn_opentsne_materialized()     (R/tsne_affinity_dispatch.R:65-88)

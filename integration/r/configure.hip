@@ -59,7 +59,11 @@ if [ "$use_hip" != "0" ] && [ -n "$hipcc" ]; then
   # C ABI header and the HIP runtime API header (device buffers of the KNN).
   cppflags="$cppflags -DFASTEMBEDR_HAS_HIP -D__HIP_PLATFORM_AMD__ -I$hip_src -I$rocm_home/include"
   libs="$libs -L$rocm_home/lib -Wl,-rpath,$rocm_home/lib -lamdhip64"
+  # the object rules below must not become make's default goal when the
+  # CUDA rule (which sets it too) is absent
   hip_rule="
+.DEFAULT_GOAL := all
+
 HIPCC = $hipcc
 HIP_DEVICE_FLAGS = $hip_device_flags -I$hip_src
 HIP_HOST_FLAGS = $hip_host_flags -I$hip_src
