@@ -180,7 +180,10 @@ def main() -> int:
     sess.sync()
     breakdown = sess.timing()
     sess.set_timing(False)
-    per_kernel = {name: (tot / cnt if cnt else 0.0) for name, (cnt, tot) in breakdown.items() if cnt}
+    # milliseconds per iteration of the window: a kernel launched every
+    # iteration counts its average duration, one launched every few
+    # iterations (the interpolation grid's spread order) its share
+    per_kernel = {name: tot / steps for name, (cnt, tot) in breakdown.items() if cnt}
     # The repulsion step: every kernel from the binning of the points to the
     # potentials on the grid (the read-back is fused into the update).
     rep_kernels = [kname for kname in per_kernel if kname.startswith("interp_")] if interp else \
@@ -247,7 +250,7 @@ def main() -> int:
     rep_traffic = repulsion_traffic(n, nnz, g, args.repulsion)
     log(f"{its:.1f} it/s over iterations {head}-{total - 1}, {ms_per_step:.3f} ms/step, repulsion {rep_ms:.3f} ms "
         f"({rep_achieved:.0f} GB/s on B_rep), {dom} {dom_ms:.3f} ms ({achieved:.0f} GB/s)")
-    log("per-kernel ms (breakdown pass, every kernel bracketed by events): "
+    log("per-kernel ms per iteration (breakdown pass, every kernel bracketed by events): "
         + ", ".join(f"{kk}={v:.4f}" for kk, v in per_kernel.items()))
 
     cpu = None

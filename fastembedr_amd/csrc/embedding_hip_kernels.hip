@@ -95,9 +95,6 @@ __device__ void set_geometry(DeviceScalars* sc, const BlockStats& t, int n, int 
     sc->lg_node_h = static_cast<float>(w / static_cast<double>(sc->lg_order));
     sc->lg_boxes = nb;
     sc->lg_nodes = nb * sc->lg_order;
-    const int tile = lg_tile_for(nb);
-    sc->lg_tile = tile;
-    sc->lg_tiles_axis = (nb + tile - 1) / tile;
   }
 }
 
@@ -361,16 +358,12 @@ static_assert(kPlanPer * kPlanThreads == kMaxTiles, "whole entries per thread");
 
 // Each tile's first point (tile_cursor, for the scatter's reservations) and
 // work items of <= kChunk points, from the tile counts (which it clears for
-// the next iteration).  tiles < 0: the interpolation grid's tile count,
-// lg_tiles_axis^2, read on the device.  tile_item0 (optional) receives the
-// first work item of each tile and, at [tiles], the number of items.
+// the next iteration).
 __global__ __launch_bounds__(kPlanThreads) void k_bin_plan(int* __restrict__ tile_count,
                                                            int* __restrict__ tile_cursor, int4* __restrict__ items,
-                                                           DeviceScalars* sc, int tiles,
-                                                           int* __restrict__ tile_item0) {
+                                                           DeviceScalars* sc, int tiles) {
   chain_priority();
   __shared__ int part[2 * kPlanThreads / kWave];
-  if (tiles < 0) tiles = sc->lg_tiles_axis * sc->lg_tiles_axis;
   int cnt[kPlanPer], start[kPlanPer], chunks[kPlanPer], base[kPlanPer];
   for (int q = 0; q < kPlanPer; ++q) {
     const int t = threadIdx.x * kPlanPer + q;
@@ -387,17 +380,13 @@ __global__ __launch_bounds__(kPlanThreads) void k_bin_plan(int* __restrict__ til
     const int t = threadIdx.x * kPlanPer + q;
     if (t >= tiles) continue;
     tile_cursor[t] = start[q];
-    if (tile_item0 != nullptr) tile_item0[t] = base[q];
     for (int c = 0; c < chunks[q]; ++c) {
       const int b = start[q] + c * kChunk;
       const int e = min(start[q] + cnt[q], b + kChunk);
       items[base[q] + c] = make_int4(t, b, e, 0);
     }
   }
-  if (threadIdx.x == 0) {
-    sc->num_items = total_items;
-    if (tile_item0 != nullptr) tile_item0[tiles] = total_items;
-  }
+  if (threadIdx.x == 0) sc->num_items = total_items;
 }
 
 constexpr int kScatterPerThread = 4;
@@ -654,10 +643,13 @@ __global__ __launch_bounds__(256) void k_kernel_cols(const float2* __restrict__ 
   }
 }
 
-// Row transforms of the charges.  Row y < G of A = mass + i mass_x and of
-// B = mass_y (zero-padded to F) is transformed; the real-input spectra are
-// separated with the Hermitian mirror, M[k] = (A[k] + conj A[-k]) / 2 and
-// Mx[k] = (A[k] - conj A[-k]) / 2i, and only kx in [0, F/2] is stored.
+// Row transforms of the charges.  Row y < G of A = mass_x + i mass_y and of
+// B = mass (zero-padded to F) is transformed; the real-input spectra are
+// separated with the Hermitian mirror, Mx[k] = (A[k] + conj A[-k]) / 2 and
+// My[k] = (A[k] - conj A[-k]) / 2i, and only kx in [0, F/2] is stored.  The
+// packed pair shares one scale (|coordinate| x mass): packing mass with
+// mass_x instead would give mass's spectrum the rounding error of one |x|
+// times larger.
 template <int F>
 __global__ __launch_bounds__(256) void k_charge_rows(const float* __restrict__ mass,
                                                      const float* __restrict__ mass_x,
@@ -677,8 +669,8 @@ __global__ __launch_bounds__(256) void k_charge_rows(const float* __restrict__ m
     float2 a = make_float2(0.0f, 0.0f), b = make_float2(0.0f, 0.0f);
     if (x < S::G && y < S::G) {
       const int at = y * S::G + x;
-      a = make_float2(mass[at], mass_x[at]);
-      b = make_float2(mass_y[at], 0.0f);
+      a = make_float2(mass_x[at], mass_y[at]);
+      b = make_float2(mass[at], 0.0f);
     }
     lds[(2 * r) * F + x] = a;
     lds[(2 * r + 1) * F + x] = b;
@@ -694,9 +686,9 @@ __global__ __launch_bounds__(256) void k_charge_rows(const float* __restrict__ m
     const float2 b = conjf2(lds[(2 * r) * F + ((F - kx) & (F - 1))]);
     const float2 sum = cadd(a, b);
     const float2 dif = csub(a, b);
-    m_rows[y * S::H + kx] = cscale(sum, 0.5f);
-    mx_rows[y * S::H + kx] = make_float2(0.5f * dif.y, -0.5f * dif.x);
-    my_rows[y * S::H + kx] = lds[(2 * r + 1) * F + kx];
+    m_rows[y * S::H + kx] = lds[(2 * r + 1) * F + kx];
+    mx_rows[y * S::H + kx] = cscale(sum, 0.5f);
+    my_rows[y * S::H + kx] = make_float2(0.5f * dif.y, -0.5f * dif.x);
   }
 }
 
@@ -769,9 +761,13 @@ __global__ __launch_bounds__(256) void k_conv_cols(const float2* __restrict__ m_
 }
 
 // Inverse row pass.  The potential rows are spectra of real rows stored for
-// kx <= F/2; two of them are packed per transform, U = X + i Y and
-// V = V1 + i V2, with the upper half rebuilt from conjugates.  Outputs for
-// x < G are scaled by 1/F^2 and stored as (q2, xq2, yq2, q) per node.  The sum
+// kx <= F/2; two of them are packed per transform, U = X + i V1 (q, q2) and
+// V = V2 + i Y (xq2, yq2), with the upper half rebuilt from conjugates.  A
+// packed transform's rounding error in either part scales with the larger of
+// the two, so each pair has a common scale: q2 is never paired with xq2
+// (|x| times larger), whose error the read-back y q2 - xq2 would multiply by
+// |y| again.  Outputs for x < G are scaled by 1/F^2 and stored as (q2, xq2,
+// yq2, q) per node.  The sum
 // over points of the bilinear read of q equals sum over nodes of mass * q,
 // because read-back and spreading use the same weights; it is accumulated
 // here in fp64, and the charge grids are cleared for the next iteration.
@@ -805,8 +801,8 @@ __global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__
         V1 = conjf2(V1);
         V2 = conjf2(V2);
       }
-      u = cadd(X, mul_i(Y));
-      v = cadd(V1, mul_i(V2));
+      u = cadd(X, mul_i(V1));
+      v = cadd(V2, mul_i(Y));
     }
     lds[(2 * r) * F + kx] = u;
     lds[(2 * r + 1) * F + kx] = v;
@@ -823,7 +819,7 @@ __global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__
     const float2 u = cscale(lds[(2 * r) * F + x], scale);
     const float2 v = cscale(lds[(2 * r + 1) * F + x], scale);
     const int at = y * S::G + x;
-    field[at] = make_float4(v.x, v.y, u.y, u.x);
+    field[at] = make_float4(u.y, v.x, v.y, u.x);
     acc += static_cast<double>(mass[at]) * static_cast<double>(u.x);
     mass[at] = 0.0f;
     mass_x[at] = 0.0f;
@@ -925,11 +921,15 @@ __global__ __launch_bounds__(256) void k_attract(const int* __restrict__ row_ptr
 // at the point (src/tsne_neighbors.cpp:1165-1180) or an exact one, plus the
 // attraction, gives the gradient; then the gains/momentum/step-clip update
 // (src/tsne_neighbors.cpp:1217-1256), and the bounding box and fp64 mean of
-// the new layout for the next iteration's centring and grid.
+// the new layout for the next iteration's centring and grid.  With the
+// bilinear grid y_cur is the centred copy the binning wrote; with the
+// interpolation grid it is the stored layout, centred here (the shift of the
+// current geometry), and y_out may be the same buffer (each point is read
+// before it is written, by the same thread).
 template <int MODE, bool LG>
-__global__ __launch_bounds__(kPointThreads) void k_update(const float2* __restrict__ y_cur,
+__global__ __launch_bounds__(kPointThreads) void k_update(const float2* y_cur,
                                                           const float2* __restrict__ attr,
-                                                          float2* __restrict__ y_out, float2* __restrict__ update,
+                                                          float2* y_out, float2* __restrict__ update,
                                                           float2* __restrict__ gains, float2* __restrict__ grad_out,
                                                           const float2* __restrict__ exact_rep,
                                                           const float4* __restrict__ field, int g, UpdateParams up,
@@ -945,7 +945,8 @@ __global__ __launch_bounds__(kPointThreads) void k_update(const float2* __restri
                                                               : static_cast<double>(FLT_MIN)))
                               : 0.0f;
   for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += gridDim.x * kPointThreads) {
-    const float2 yi = y_cur[i];
+    float2 yi = y_cur[i];
+    if (LG && MODE != kModeGradientExact) yi = make_float2(yi.x - s.shift_x, yi.y - s.shift_y);
     const float2 a = attr[i];
     float gx, gy;
     if (MODE == kModeGradientExact) {
@@ -1448,12 +1449,7 @@ hipError_t launch_bin_count(const float2* y_stored, float2* y_cur, const DeviceS
 
 hipError_t launch_bin_plan(GridBuffers& gb, DeviceScalars* sc, hipStream_t stream) {
   const int ta = tiles_per_axis(gb.g);
-  k_bin_plan<<<1, kPlanThreads, 0, stream>>>(gb.tile_count, gb.tile_cursor, gb.items, sc, ta * ta, nullptr);
-  return hipGetLastError();
-}
-
-hipError_t launch_interp_bin_plan(InterpBuffers& ib, DeviceScalars* sc, hipStream_t stream) {
-  k_bin_plan<<<1, kPlanThreads, 0, stream>>>(ib.tile_count, ib.tile_cursor, ib.items, sc, -1, ib.tile_item0);
+  k_bin_plan<<<1, kPlanThreads, 0, stream>>>(gb.tile_count, gb.tile_cursor, gb.items, sc, ta * ta);
   return hipGetLastError();
 }
 

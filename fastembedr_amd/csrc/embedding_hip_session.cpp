@@ -239,6 +239,16 @@ struct fastembedr_hip_tsne {
   Arena lg_arena;
   fehip::InterpBuffers ib;
   int lg_last_fft = 0;       // FFT length of the last interpolation-grid iteration
+  // The spread's point order (working indices sorted by position) is made
+  // again every kLgOrderPeriod interpolation-grid iterations, on first use
+  // and after a renumbering (stale), and for every gradient probe.  Any
+  // permutation gives the same charges (up to the order of fp32 adds); a
+  // spatial one keeps the spread's runs long.  lg_order_due asks the next
+  // gradient pieces to make it before the spread.
+  static constexpr int kLgOrderPeriod = 8;
+  bool lg_order_stale = true;
+  bool lg_order_due = false;
+  int lg_order_age = 0;
   // Box counts of recent iterations: a pinned coherent ring that the
   // update's statistics kernel writes, slot DeviceScalars::ring_seq % kLgRing
   // = (ring_seq << 32) | boxes, before it advances ring_seq.  The host reads
@@ -369,7 +379,7 @@ namespace {
 const char* kKernelNames[fehip::kKernelCount] = {
     "stats", "bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols", "charge_rows",
     "conv_cols", "inverse_rows", "attract", "update", "commit", "renumber", "tile_build",
-    "interp_bin_count", "interp_bin_plan", "interp_bin_scatter", "interp_spread", "interp_gather",
+    "interp_order", "interp_spread",
     "interp_kernel_rows", "interp_kernel_cols", "interp_charge_rows", "interp_conv_cols", "interp_inverse_rows",
     "finalize_stats"};
 
@@ -625,14 +635,19 @@ bool ensure_interp(fastembedr_hip_tsne* s) {
   const std::size_t mn = fehip::kLgMaxNodes;
   const std::size_t gmax = fehip::kLgMaxFft / 2;
   const std::size_t hmax = gmax + 1;
-  const std::size_t items = static_cast<std::size_t>(fehip::lg_max_items(s->n));
+  std::size_t sort_bytes = 0;
+  if (!hip_ok(fehip::interp_order_temp_bytes(s->n, sort_bytes), "interp order size query")) return false;
+  constexpr std::size_t kSums = fehip::kLgSumsPerBox;
+  const std::size_t wins = static_cast<std::size_t>(fehip::lg_spread_blocks(s->n));
+  const std::size_t boxes = static_cast<std::size_t>(fehip::kLgMaxBoxes) * fehip::kLgMaxBoxes;
   const std::size_t bytes = align_up(4 * mn * mn * 4) + align_up(mn * mn * sizeof(float4)) +
                             2 * align_up(2 * hmax * hmax * sizeof(float2)) +
                             2 * align_up(3 * gmax * hmax * sizeof(float2)) +
-                            align_up(fehip::kLgZPartials * sizeof(double)) +
-                            3 * align_up((fehip::kMaxTiles + 1) * sizeof(int)) + align_up(items * sizeof(int4)) +
-                            align_up(items * fehip::kLgWinVals * 4) + 4096;
-  (void)n;
+                            align_up(fehip::kLgZPartials * sizeof(double)) + 2 * align_up(n * sizeof(int)) +
+                            align_up(2 * n * sizeof(unsigned int)) + align_up(sort_bytes) +
+                            align_up(wins * fehip::kLgTable * kSums * sizeof(float)) + align_up(boxes * sizeof(int)) +
+                            align_up(boxes * fehip::kLgSlots * sizeof(int)) + align_up(boxes * kSums * sizeof(float)) +
+                            4096;
   if (!memory_preflight(bytes, "HIP openTSNE interpolation grid") ||
       !s->lg_arena.init(bytes, "hipMalloc(HIP openTSNE interpolation grid)")) {
     return false;
@@ -646,18 +661,25 @@ bool ensure_interp(fastembedr_hip_tsne* s) {
   ib.spec_a = a.take<float2>(3 * gmax * hmax);
   ib.spec_b = a.take<float2>(3 * gmax * hmax);
   ib.z_partial = a.take<double>(fehip::kLgZPartials);
-  ib.tile_count = a.take<int>(fehip::kMaxTiles + 1);
-  ib.tile_cursor = a.take<int>(fehip::kMaxTiles + 1);
-  ib.tile_item0 = a.take<int>(fehip::kMaxTiles + 1);
-  ib.items = a.take<int4>(items);
-  ib.windows = a.take<float>(items * fehip::kLgWinVals);
-  ib.binned = s->gb.binned;
-  if (ib.windows == nullptr) {
+  ib.order = a.take<int>(n);
+  ib.order_idx = a.take<int>(n);
+  ib.order_keys = a.take<unsigned int>(2 * n);
+  ib.order_temp = a.take<unsigned char>(std::max<std::size_t>(sort_bytes, 1));
+  ib.order_temp_bytes = sort_bytes;
+  ib.tables = a.take<float>(wins * fehip::kLgTable * kSums);
+  ib.box_count = a.take<int>(boxes);
+  ib.box_list = a.take<int>(boxes * fehip::kLgSlots);
+  ib.straggler = a.take<float>(boxes * kSums);
+  s->lg_order_stale = true;
+  if (ib.straggler == nullptr) {
     set_error("internal: interpolation grid buffers do not fit their arena");
     return false;
   }
-  if (!hip_ok(hipMemsetAsync(ib.tile_count, 0, (fehip::kMaxTiles + 1) * sizeof(int), s->stream),
-              "hipMemset(interpolation tiles)") ||
+  // the box counts and the straggler planes are zero between iterations
+  // (each gather clears what it read)
+  if (!hip_ok(hipMemsetAsync(ib.box_count, 0, boxes * sizeof(int), s->stream), "hipMemset(interpolation boxes)") ||
+      !hip_ok(hipMemsetAsync(ib.straggler, 0, boxes * kSums * sizeof(float), s->stream),
+              "hipMemset(interpolation stragglers)") ||
       !hip_ok(hipHostMalloc(reinterpret_cast<void**>(&s->lg_ring),
                             fastembedr_hip_tsne::kLgRing * sizeof(unsigned long long),
                             hipHostMallocMapped | hipHostMallocCoherent),
@@ -687,7 +709,9 @@ bool write_interp_spec(fastembedr_hip_tsne* s, int order) {
          hip_ok(hipMemcpy(dst, &spec, sizeof(spec), hipMemcpyHostToDevice), "hipMemcpy(interp spec)");
 }
 
-// One iteration's gradient pieces.  The centred layout goes to y_b; the
+// One iteration's gradient pieces.  With the bilinear grid the centred
+// layout goes to y_b (the interpolation grid's spread and update centre the
+// stored layout themselves, the spread reading it in its spatial order); the
 // attraction of the layout goes to attr; the repulsion fields (bilinear grid or
 // interpolation grid at FFT length fft_len) to the grid buffers.  With
 // `finalize` the previous update's statistics are finished first (the grid
@@ -787,14 +811,9 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
     return false;
   }
   if (overlap && !hip_ok(hipEventRecord(s->ev_kern, sk), "hipEventRecord(kernel)")) return false;
-  // chain: centre + count
-  if (lg) {
-    if (!s->timed(
-            fehip::kKLgBinCount, "interp bin_count launch",
-            [&] { return fehip::launch_interp_bin_count(s->y_a(), s->y_b, s->sc, ib, n, chain); }, chain)) {
-      return false;
-    }
-  } else if (!s->timed(
+  // chain: centre + count (the interpolation grid's spread centres the
+  // layout itself)
+  if (!lg && !s->timed(
                  fehip::kKBinCount, "bin_count launch",
                  [&] { return fehip::launch_bin_count(s->y_a(), s->y_b, s->sc, s->gb, n, chain); }, chain)) {
     return false;
@@ -802,18 +821,21 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   // chain: bins, spread, charge transforms
   bool ok;
   if (lg) {
+    if (s->lg_order_due) {
+      // the spread order of this iteration's layout (any order is correct;
+      // a spatial one keeps the spread's runs of one box long)
+      if (!s->timed(
+              fehip::kKLgOrder, "interp order launch",
+              [&] { return fehip::launch_interp_order(s->y_a(), s->sc, ib, n, chain); }, chain)) {
+        return false;
+      }
+      s->lg_order_due = false;
+      s->lg_order_stale = false;
+      s->lg_order_age = 0;
+    }
     ok = s->timed(
-             fehip::kKLgBinPlan, "interp bin_plan launch",
-             [&] { return fehip::launch_interp_bin_plan(ib, s->sc, chain); }, chain) &&
-         s->timed(
-             fehip::kKLgBinScatter, "interp bin_scatter launch",
-             [&] { return fehip::launch_interp_bin_scatter(s->y_b, s->sc, ib, n, fft_len, chain); }, chain) &&
-         s->timed(
              fehip::kKLgSpread, "interp spread launch",
-             [&] { return fehip::launch_interp_spread(s->sc, ib, n, fft_len, chain); }, chain) &&
-         s->timed(
-             fehip::kKLgGather, "interp gather launch",
-             [&] { return fehip::launch_interp_gather(s->sc, ib, chain); }, chain) &&
+             [&] { return fehip::launch_interp_spread(s->y_a(), s->sc, ib, n, fft_len, chain); }, chain) &&
          s->timed(
              fehip::kKLgChargeRows, "interp charge_rows launch",
              [&] { return fehip::launch_interp_fft(3, fft_len, ib, s->sc, s->tw, n, chain); }, chain);
@@ -877,9 +899,10 @@ bool enqueue_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip
          s->timed(
              fehip::kKUpdate, "update launch",
              [&] {
-               return fehip::launch_update(fehip::kModeUpdate, s->y_b, s->attr, s->y_a(), s->update(), s->gains(),
-                                           nullptr, nullptr, s->gb, up, s->partial, s->sc, s->n, s->home,
-                                           lg ? s->ib.field : nullptr);
+               // the interpolation grid's update centres the stored layout itself
+               return fehip::launch_update(fehip::kModeUpdate, lg ? s->y_a() : s->y_b, s->attr, s->y_a(),
+                                           s->update(), s->gains(), nullptr, nullptr, s->gb, up, s->partial, s->sc,
+                                           s->n, s->home, lg ? s->ib.field : nullptr);
              },
              s->home);
 }
@@ -948,6 +971,13 @@ bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, con
     g->key = key;
   }
   g->last_use = s->graph_clock;
+  // An iteration that makes the spread order runs eagerly (it counts as a
+  // sight of its key): the radix sort's library launches stay out of
+  // captured graphs.
+  if (lg && s->lg_order_due) {
+    ++g->seen;
+    return enqueue_iteration(s, lg, fft_len, up, true, finalize);
+  }
   if (g->exec == nullptr && ++g->seen >= 2) {
     if (!capture_iteration(s, lg, fft_len, up, finalize, &g->exec)) {
       // A capture the runtime refuses leaves the session on eager launches.
@@ -1068,6 +1098,7 @@ hipError_t enqueue_renumber(fastembedr_hip_tsne* s) {
   s->pi = 1 - s->pi;
   s->since_reorder = 0;
   ++s->renumber_count;
+  s->lg_order_stale = true;  // the spread order holds working indices
   return hipSuccess;
 }
 
@@ -1632,12 +1663,13 @@ int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int
   } else if (repulsion == FASTEMBEDR_HIP_REPULSION_LAGRANGE) {
     int boxes = 0;
     unsigned int ring_seq = 0;
+    s->lg_order_due = true;  // a probe's layout may be any: order it
     ok = ensure_interp(s) && write_interp_spec(s, fehip::kLgOrder) &&
          hip_ok(fehip::launch_stats(s->y_a(), s->n, s->gb.g, 0, s->partial, s->sc, s->stream), "stats launch") &&
          read_interp_boxes(s, &boxes, &ring_seq) &&
          enqueue_gradient_pieces(s, true, interp_fft_len(std::min(boxes * fehip::kLgOrder, fehip::kLgMaxNodes)),
                                  exaggeration, false) &&
-         hip_ok(fehip::launch_update(fehip::kModeGradientGrid, s->y_b, s->attr, nullptr, nullptr, nullptr, s->grad,
+         hip_ok(fehip::launch_update(fehip::kModeGradientGrid, s->y_a(), s->attr, nullptr, nullptr, nullptr, s->grad,
                                      nullptr, s->gb, up, s->partial, s->sc, s->n, s->stream, s->ib.field),
                 "update launch") &&
          check_iteration_flags(s);
@@ -1765,6 +1797,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
       const int nodes = static_cast<int>(std::min<long long>(bound * fehip::kLgOrder, fehip::kLgMaxNodes));
       fft_len = interp_fft_len(nodes);
     }
+    if (lg) s->lg_order_due = s->lg_order_stale || s->lg_order_age >= fastembedr_hip_tsne::kLgOrderPeriod;
     // Timing every kernel (mode 1) runs the pieces in sequence, so that each
     // duration is the kernel's alone; timed runs are never replayed graphs.
     const bool overlap = !(s->timing && s->timed_only < 0);
@@ -1772,6 +1805,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
                                                    : enqueue_iteration(s, lg, fft_len, up, overlap, pending);
     if (!ok) return 1;
     pending = true;
+    if (lg) ++s->lg_order_age;  // iterations spread since the order was made
   }
   // the last update's statistics (no box count is needed from them)
   if (pending && !finish_pending(nullptr)) return 1;

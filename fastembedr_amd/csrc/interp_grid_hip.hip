@@ -35,19 +35,18 @@
 // kernels and charges; the factors of h are applied at the end.
 //
 // Per iteration, after the statistics have set the geometry on the device:
-//   k_lg_bin_count, k_bin_plan, k_lg_bin_scatter
-//                         points into tiles of T x T boxes and work items of
-//                         at most 2048 points of one tile
-//   k_lg_spread           per work item: points ordered by box in LDS; one
-//                         wave per box sums its points' 9 nodes x 4 moments
-//                         in registers and DPP adds across the wave, and
-//                         stores the box's nodes in the item's LDS window;
-//                         the window goes straight to the charge planes when
-//                         the item is its tile's only one, else to scratch
-//   k_lg_gather           sums the scratch windows of multi-item tiles in a
-//                         fixed order (no float atomics in global memory), a
-//                         workgroup per tile; every node is written, so
-//                         nothing is cleared
+//   k_lg_order_keys + radix sort
+//                         every few iterations: the spread order, points
+//                         sorted by the Morton code of their position
+//   k_lg_spread           per workgroup, 1024 consecutive points of the
+//                         spread order: each point centred and located, its
+//                         9 nodes x 4 moments summed over the runs of one box
+//                         among a wave's 64 consecutive points (DPP segmented
+//                         scan), each run's sums added into the box's slot of
+//                         an LDS table keyed by box, the occupied slots stored
+//                         to scratch and entered in their boxes' lists
+//   k_lg_gather           every node written once: the sum over its box's
+//                         listed slots (and the rare straggler atomics)
 //   k_lg_kernel_rows/cols spectra of K, K1 (real, even) and Kv (imaginary,
 //                         odd in its own axis), a quadrant each, two real
 //                         sequences per complex transform
@@ -74,6 +73,8 @@
 #include <algorithm>
 #include <cfloat>
 
+#include <rocprim/device/device_radix_sort.hpp>
+
 #include "device_common.h"
 #include "tsne_device.h"
 
@@ -83,362 +84,369 @@ namespace {
 constexpr int kLgThreads = 256;
 // partial-sum slots: three per convolution-pass block, then one per row block
 constexpr int kLgMaxSpecBlocks = kLgMaxColBlocks;
-constexpr int kLgRun = kChunk / kLgThreads;  // points per lane in k_lg_spread
-constexpr int kLgBoxesPerTile = kLgMaxTile * kLgMaxTile;
-static_assert(kLgBoxesPerTile == kLgThreads, "one box of the largest tile per thread in the box scan");
-static_assert(kLgRun * kLgThreads == kChunk, "a work item is one run per lane");
+constexpr int kLgMoments = 4 * kLgOrder * kLgOrder;  // 9 nodes x (m0, m1x, m1y, m2) per box
 
-__device__ __forceinline__ int lg_tile_of(const LgPoint& b, int tile, int ta) {
-  return (b.by / tile) * ta + b.bx / tile;
+// Node moments of a box as polynomials.  With v = u - 1/2 a point's offset
+// from the box centre (in box widths, |v| <= 1/2), node c sits at
+// v_c = (c - 1) / 3 and the order-3 Lagrange weight of node c is the degree-2
+// polynomial L_c(v); the point's offset from node c in units of the node
+// spacing h is 3 (v - v_c).  So every node moment is a fixed combination of
+// power sums of the box's points,
+//   m0(r, c)  = sum_ij A_r[i] A_c[j] S_ij,   m1x(r, c) = sum_ij A_r[i] B_c[j] S_ij,
+//   m1y(r, c) = sum_ij B_r[i] A_c[j] S_ij,
+//   m2(r, c)  = sum_ij (A_r[i] D_c[j] + D_r[i] A_c[j]) S_ij,
+// with S_ij = sum over points vy^i vx^j, A_c = L_c, B_c = L_c 3 (v - v_c),
+// D_c = L_c 9 (v - v_c)^2 (r is the node row, along y).  The spread sums
+// the 21 power sums that occur (i <= 2 with j <= 4, i in {3, 4} with
+// j <= 2) instead of 36 node moments; the gather combines them.  In v the
+// coefficients are small (|A| <= 9, |B| <= 27, |D| <= 81 at |v|^k <= 2^-k),
+// so the combination loses a few ulps at most.
+constexpr int kLgSums = 21;
+__host__ __device__ constexpr int lg_sum_index(int i, int j) { return i <= 2 ? i * 5 + j : 15 + (i - 3) * 3 + j; }
+__host__ __device__ constexpr bool lg_sum_exists(int i, int j) { return (i <= 2 && j <= 4) || (i <= 4 && j <= 2); }
+
+struct LgPoly {
+  double k[5];  // coefficients of v^0 .. v^4
+};
+constexpr double lg_node_v(int c) { return (c - 1) / 3.0; }
+constexpr LgPoly lg_poly_lin(LgPoly p, double a, double b) {  // p(v) (a v + b)
+  LgPoly q{};
+  for (int i = 0; i < 5; ++i) {
+    q.k[i] += b * p.k[i];
+    if (i + 1 < 5) q.k[i + 1] += a * p.k[i];
+  }
+  return q;
+}
+// kind 0: A_c = L_c, 1: B_c = L_c 3 (v - v_c), 2: D_c = L_c 9 (v - v_c)^2
+constexpr LgPoly lg_node_poly(int kind, int c) {
+  LgPoly p{{1.0, 0.0, 0.0, 0.0, 0.0}};
+  for (int d = 0; d < kLgOrder; ++d) {
+    if (d != c) p = lg_poly_lin(p, 1.0 / (lg_node_v(c) - lg_node_v(d)), -lg_node_v(d) / (lg_node_v(c) - lg_node_v(d)));
+  }
+  for (int t = 0; t < kind; ++t) p = lg_poly_lin(p, 3.0, -3.0 * lg_node_v(c));
+  return p;
+}
+struct LgPolyTable {
+  float k[3][kLgOrder][5];
+};
+constexpr LgPolyTable lg_poly_table() {
+  LgPolyTable t{};
+  for (int kind = 0; kind < 3; ++kind)
+    for (int c = 0; c < kLgOrder; ++c)
+      for (int i = 0; i < 5; ++i) t.k[kind][c][i] = static_cast<float>(lg_node_poly(kind, c).k[i]);
+  return t;
+}
+__constant__ LgPolyTable kLgPolys = lg_poly_table();
+static_assert(lg_poly_table().k[0][1][0] == 1.0f && lg_poly_table().k[0][1][2] == -9.0f &&
+                  lg_poly_table().k[0][0][1] == -1.5f && lg_poly_table().k[0][2][2] == 4.5f &&
+                  lg_poly_table().k[2][1][4] == -81.0f && lg_poly_table().k[1][0][3] == 13.5f,
+              "Lagrange weights on the nodes (c - 1) / 3: L_0 = 4.5 v^2 - 1.5 v, L_1 = 1 - 9 v^2");
+
+// The 21 power sums one point contributes.
+__device__ __forceinline__ void lg_power_sums(const LgPoint& b, float (&s)[kLgSums]) {
+#pragma clang fp contract(off)
+  const float vx = b.ux - 0.5f;
+  const float vy = b.uy - 0.5f;
+  float px[5], py[5];
+  px[0] = 1.0f;
+  px[1] = vx;
+  px[2] = vx * vx;
+  px[3] = px[2] * vx;
+  px[4] = px[2] * px[2];
+  py[0] = 1.0f;
+  py[1] = vy;
+  py[2] = vy * vy;
+  py[3] = py[2] * vy;
+  py[4] = py[2] * py[2];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+      if (lg_sum_exists(i, j)) s[lg_sum_index(i, j)] = i == 0 ? px[j] : (j == 0 ? py[i] : py[i] * px[j]);
+    }
+  }
 }
 
-__global__ __launch_bounds__(kLgThreads) void k_lg_bin_count(const float2* __restrict__ y_stored,
-                                                             float2* __restrict__ y_cur, const DeviceScalars* sc,
-                                                             int* __restrict__ tile_count, int n) {
+// gfx9 DPP controls: whole-wave shifts by one lane.
+constexpr int kDppWaveShl1 = 0x130;  // lane l reads lane l + 1
+constexpr int kDppWaveShr1 = 0x138;  // lane l reads lane l - 1
+
+// Inclusive segmented scan (Hillis-Steele) of the 21 sums over the wave: row
+// shifts 1, 2, 4, 8, then row broadcasts 15 (into rows 1 and 3) and 31 (into
+// rows 2 and 3).  `take` is 0 on a lane that starts a run and 1 elsewhere;
+// at each step a lane adds the partial sums the step reaches, times its take
+// (one DPP multiply-add per value: the sum is an fp32 add, take being 0 or
+// 1), and its take becomes the minimum of the two (0 once its window holds a
+// run start).  bound_ctrl is off, so a lane whose source lies outside its row
+// (or the rows a broadcast writes) is not written and keeps its partial sum
+// and its take.  gfx9 needs two wait states between a VALU write of a VGPR
+// and a DPP read of it: every DPP source here was written at least 21
+// instructions earlier, and the s_nop 1 at each end covers the code around
+// the block.  Needs the whole wave active.
+#define LG_FMAC(i, CTRL) "v_fmac_f32_dpp %" #i ", %" #i ", %21 " CTRL "\n\t"
+#define LG_SCAN_STEP(CTRL)                                                                                          \
+  LG_FMAC(0, CTRL) LG_FMAC(1, CTRL) LG_FMAC(2, CTRL) LG_FMAC(3, CTRL) LG_FMAC(4, CTRL) LG_FMAC(5, CTRL)           \
+  LG_FMAC(6, CTRL) LG_FMAC(7, CTRL) LG_FMAC(8, CTRL) LG_FMAC(9, CTRL) LG_FMAC(10, CTRL) LG_FMAC(11, CTRL)         \
+  LG_FMAC(12, CTRL) LG_FMAC(13, CTRL) LG_FMAC(14, CTRL) LG_FMAC(15, CTRL) LG_FMAC(16, CTRL) LG_FMAC(17, CTRL)     \
+  LG_FMAC(18, CTRL) LG_FMAC(19, CTRL) LG_FMAC(20, CTRL) "v_min_f32_dpp %21, %21, %21 " CTRL "\n\t"
+static_assert(kLgSums == 21, "the scan block names 21 sums");
+
+__device__ __forceinline__ void lg_seg_scan(float (&a)[kLgSums], float& take) {
+  asm volatile("s_nop 1\n\t"
+               LG_SCAN_STEP("row_shr:1 row_mask:0xf bank_mask:0xf")
+               LG_SCAN_STEP("row_shr:2 row_mask:0xf bank_mask:0xf")
+               LG_SCAN_STEP("row_shr:4 row_mask:0xf bank_mask:0xf")
+               LG_SCAN_STEP("row_shr:8 row_mask:0xf bank_mask:0xf")
+               LG_SCAN_STEP("row_bcast:15 row_mask:0xa bank_mask:0xf")
+               LG_SCAN_STEP("row_bcast:31 row_mask:0xc bank_mask:0xf")
+               "s_nop 1"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]),
+                 "+v"(a[7]), "+v"(a[8]), "+v"(a[9]), "+v"(a[10]), "+v"(a[11]), "+v"(a[12]), "+v"(a[13]),
+                 "+v"(a[14]), "+v"(a[15]), "+v"(a[16]), "+v"(a[17]), "+v"(a[18]), "+v"(a[19]), "+v"(a[20]),
+                 "+v"(take));
+}
+#undef LG_SCAN_STEP
+#undef LG_FMAC
+
+// Spread order: points sorted by the Morton code of their position on a
+// lattice of kLgOrderSub x kLgOrderSub cells per box, so that points of one
+// box are contiguous when the order is made and stay in long runs while the
+// layout drifts.  Keys use kLgOrderBits bits per axis.
+constexpr int kLgOrderSub = 4;
+constexpr int kLgOrderBits = 12;
+static_assert(kLgOrderSub * (kLgMaxNodes / kLgOrder) <= (1 << kLgOrderBits), "lattice cells fit the key");
+
+__device__ __forceinline__ unsigned int lg_interleave12(unsigned int v) {
+  v &= 0xfffu;
+  v = (v | (v << 8)) & 0x00ff00ffu;
+  v = (v | (v << 4)) & 0x0f0f0f0fu;
+  v = (v | (v << 2)) & 0x33333333u;
+  v = (v | (v << 1)) & 0x55555555u;
+  return v;
+}
+
+__global__ __launch_bounds__(kLgThreads) void k_lg_order_keys(const float2* __restrict__ y_stored,
+                                                              const DeviceScalars* sc, unsigned int* __restrict__ keys,
+                                                              int* __restrict__ idx, int n) {
 #pragma clang fp contract(off)
-  chain_priority();
-  __shared__ int hist[kMaxTiles];
   const DeviceScalars s = *sc;
-  const int ta = s.lg_tiles_axis;
-  const int tiles = ta * ta;
-  for (int t = threadIdx.x; t < tiles; t += kLgThreads) hist[t] = 0;
-  __syncthreads();
+  const double lo = static_cast<double>(s.lg_lo);
+  const double scale = static_cast<double>(kLgOrderSub) / s.lg_box_wd;
+  const int cells = kLgOrderSub * s.lg_boxes;
   for (int i = blockIdx.x * kLgThreads + threadIdx.x; i < n; i += gridDim.x * kLgThreads) {
     const float2 r = y_stored[i];
-    const float px = r.x - s.shift_x;
-    const float py = r.y - s.shift_y;
-    y_cur[i] = make_float2(px, py);
-    atomicAdd(&hist[lg_tile_of(lg_locate(px, py, s), s.lg_tile, ta)], 1);
-  }
-  __syncthreads();
-  for (int t = threadIdx.x; t < tiles; t += kLgThreads) {
-    if (hist[t] != 0) atomicAdd(tile_count + t, hist[t]);
+    const double rx = (static_cast<double>(r.x - s.shift_x) - lo) * scale;
+    const double ry = (static_cast<double>(r.y - s.shift_y) - lo) * scale;
+    const int qx = max(0, min(cells - 1, static_cast<int>(floor(rx))));
+    const int qy = max(0, min(cells - 1, static_cast<int>(floor(ry))));
+    keys[i] = lg_interleave12(static_cast<unsigned int>(qx)) | (lg_interleave12(static_cast<unsigned int>(qy)) << 1);
+    idx[i] = i;
   }
 }
 
-constexpr int kLgScatterPerThread = 4;
+// Per iteration, two kernels.  k_lg_spread: each workgroup takes kLgChunk
+// consecutive points of the spread order (`order`, working indices sorted by
+// position), so that its points fall into few boxes, and sums them in LDS,
+// in a table of kLgTable slots keyed by box (open addressing): every point is
+// centred and located, its 21 power sums (above) are summed with those of the
+// other points of its box among the wave's 64 consecutive points (an
+// inclusive segmented scan over runs of one box, lg_seg_scan), and the last
+// lane of each run finds its box's slot (atomicCAS on the slot's key) and adds
+// the run's sums into it (LDS float atomics).  The occupied slots go to the
+// workgroup's scratch with plain stores, and each is entered in its box's
+// list (kLgSlots entries; an integer atomic on the box's count).  k_lg_gather
+// then writes every node of the charge planes once: the box's listed slots
+// summed and combined into its 9 nodes x 4 moments.  Float atomics in global
+// memory (device scope: across the XCDs' L2s they resolve beyond L2, at a
+// few ns each) are left for the rare exceptions, which go to a straggler
+// array of power sums per box that the gather adds and clears: a run whose
+// chunk already fills its table (more than kLgTable boxes in kLgChunk points)
+// and a box listed by more than kLgSlots workgroups.  Any permutation gives
+// the same charges up to the order of the fp32 adds; a spatial one keeps runs
+// long and tables sparse.  A grid the FFT length cannot hold (2 m > fft_len,
+// excluded by the host's bound) raises kErrInterpGrid; both kernels then
+// write nothing.
+constexpr int kLgSteps = 4;                        // 64-point steps per wave
+constexpr int kLgChunk = kLgThreads * kLgSteps;    // points per workgroup
+static_assert(kLgChunk == kLgSpreadChunk, "the host sizes the spread's scratch by kLgSpreadChunk");
+static_assert(kLgTable == kLgThreads, "one table slot per thread in the flush");
+static_assert(kLgSums == kLgSumsPerBox, "the host sizes the sums by kLgSumsPerBox");
+// A box's count word: the slots listed (low bits) and a flag set when
+// straggler sums were added for the box (the gather reads and clears those
+// only then).
+constexpr int kLgStraggled = 1 << 30;
+constexpr int kLgCountMask = kLgStraggled - 1;
 
-// The workgroup's tile histogram lives in dynamic LDS of tiles_cap ints,
-// tiles_cap the most tiles the FFT length allows, and is overwritten in
-// place by the tiles' reserved base offsets (each point keeps its rank in
-// registers), so that several workgroups fit on a CU beside the attraction.
-// More tiles than tiles_cap (which the host's FFT-length bound excludes)
-// raise kErrInterpGrid.
-__global__ __launch_bounds__(kLgThreads) void k_lg_bin_scatter(const float2* __restrict__ y_cur,
-                                                               DeviceScalars* sc,
-                                                               int* __restrict__ tile_cursor,
-                                                               float2* __restrict__ binned, int n, int tiles_cap) {
+__global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restrict__ y_stored,
+                                                          const int* __restrict__ order, DeviceScalars* sc, int n,
+                                                          int max_nodes, float* __restrict__ table_out,
+                                                          int* __restrict__ box_count, int* __restrict__ box_list,
+                                                          float* __restrict__ straggler) {
+#pragma clang fp contract(off)
   chain_priority();
-  extern __shared__ int hist[];  // counts, then base offsets
+  __shared__ int tkey[kLgTable];                // box of each slot, -1: free
+  __shared__ float tval[kLgTable * kLgSums];    // the slots' sums
   const DeviceScalars s = *sc;
-  const int ta = s.lg_tiles_axis;
-  const int tiles = ta * ta;
-  if (tiles > tiles_cap) {  // uniform over the grid
+  const int m = s.lg_nodes;
+  if (m > max_nodes) {  // uniform over the grid
     if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&sc->error_flags, kErrInterpGrid);
     return;
   }
-  constexpr int kBatch = kLgThreads * kLgScatterPerThread;
-  for (int b0 = blockIdx.x * kBatch; b0 < n; b0 += gridDim.x * kBatch) {
-    for (int t = threadIdx.x; t < tiles; t += kLgThreads) hist[t] = 0;
-    __syncthreads();
-    float2 v[kLgScatterPerThread];
-    int tile[kLgScatterPerThread], rank[kLgScatterPerThread];
-#pragma unroll
-    for (int q = 0; q < kLgScatterPerThread; ++q) {
-      const int i = b0 + q * kLgThreads + threadIdx.x;
-      tile[q] = -1;
-      if (i < n) {
-        v[q] = y_cur[i];
-        tile[q] = lg_tile_of(lg_locate(v[q].x, v[q].y, s), s.lg_tile, ta);
-        rank[q] = atomicAdd(&hist[tile[q]], 1);
-      }
-    }
-    __syncthreads();
-    for (int t = threadIdx.x; t < tiles; t += kLgThreads) {
-      const int c = hist[t];
-      if (c != 0) hist[t] = atomicAdd(tile_cursor + t, c);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < kLgScatterPerThread; ++q) {
-      if (tile[q] >= 0) binned[hist[tile[q]] + rank[q]] = v[q];
-    }
-    __syncthreads();
-  }
-}
-
-// One point's contributions to its box's 9 nodes x 4 moments, added to a.
-// Offsets from the nodes in units of h: node c of a box sits at (c + 1/2) h
-// from the box's corner, the point at 3 u h.
-__device__ __forceinline__ void lg_accumulate(const LgPoint& b, float (&a)[4 * kLgOrder * kLgOrder]) {
-#pragma clang fp contract(off)
-  float wx[kLgOrder], wy[kLgOrder];
-  lg_weights3(b.ux, wx);
-  lg_weights3(b.uy, wy);
-  const float tx3 = 3.0f * b.ux;
-  const float ty3 = 3.0f * b.uy;
-#pragma unroll
-  for (int r = 0; r < kLgOrder; ++r) {
-    const float oy = ty3 - (static_cast<float>(r) + 0.5f);
-#pragma unroll
-    for (int c = 0; c < kLgOrder; ++c) {
-      const float ox = tx3 - (static_cast<float>(c) + 0.5f);
-      const float w = wy[r] * wx[c];
-      float* d = a + (r * kLgOrder + c) * 4;
-      d[0] += w;
-      d[1] += w * ox;
-      d[2] += w * oy;
-      d[3] += w * (ox * ox + oy * oy);
-    }
-  }
-}
-
-// v + (v of the lane the DPP control `ctrl` names), 0 from lanes outside
-// row_mask or without a source.
-template <int CTRL, int ROW_MASK, bool BOUND_ZERO>
-__device__ __forceinline__ float lg_dpp_add(float v) {
-  const int src = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, BOUND_ZERO);
-  return v + __int_as_float(src);
-}
-
-// Sum over the 64 lanes of a wave into lane 63, in VALU cross-lane adds: a
-// prefix sum within each row of 16 lanes (row_shr 1, 2, 4, 8) leaves each
-// row's sum in its lane 15; row_bcast 15 adds row 0's into row 1 and row 2's
-// into row 3, row_bcast 31 adds lane 31 (rows 0 + 1) into row 3.  The order
-// is fixed, so the charges do not depend on scheduling.
-__device__ __forceinline__ void lg_wave_sum(float (&a)[4 * kLgOrder * kLgOrder]) {
-#pragma unroll
-  for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) {
-    float t = a[e];
-    t = lg_dpp_add<0x111, 0xf, true>(t);   // row_shr:1
-    t = lg_dpp_add<0x112, 0xf, true>(t);   // row_shr:2
-    t = lg_dpp_add<0x114, 0xf, true>(t);   // row_shr:4
-    t = lg_dpp_add<0x118, 0xf, true>(t);   // row_shr:8
-    t = lg_dpp_add<0x142, 0xa, false>(t);  // row_bcast:15 into rows 1 and 3
-    t = lg_dpp_add<0x143, 0xc, false>(t);  // row_bcast:31 into rows 2 and 3
-    a[e] = t;
-  }
-}
-
-// Writes one box's 9 nodes x 4 moments into the window of win x win nodes
-// (box = local index in a tile of win / 3 boxes per axis).  Every node
-// belongs to exactly one box, so plain stores suffice.
-__device__ __forceinline__ void lg_store_box(float* acc, int box, int tile, int win,
-                                             const float (&a)[4 * kLgOrder * kLgOrder]) {
-  const int lbx = box % tile;
-  const int lby = box / tile;
-  const int wn = win * win;
-  const int node0 = (lby * kLgOrder) * win + lbx * kLgOrder;
-#pragma unroll
-  for (int r = 0; r < kLgOrder; ++r) {
-#pragma unroll
-    for (int c = 0; c < kLgOrder; ++c) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t * wn + node0 + r * win + c] = a[(r * kLgOrder + c) * 4 + t];
-    }
-  }
-}
-
-// The window `acc` is dynamic LDS of acc_cap floats, sized by the host for
-// the largest tile its FFT length allows (a 48 x 48 x 4 window is 36 KB, the
-// late-phase 6 x 6 x 4 one 576 bytes), so that small tiles leave LDS for more
-// workgroups per CU.  A window that would not fit raises kErrInterpGrid.
-//
-// Per work item (<= kChunk points of one tile): the points are ordered by box
-// in LDS (counting sort), then each box is reduced by one wave: lanes take the
-// box's points with stride 64 and sum their 9 x 4 contributions in
-// registers, DPP adds carry the 64 lanes into one, and the box's nodes are
-// stored.
-// A tile of one box (the early, compact layouts) splits the box's points over
-// the workgroup's waves and adds their sums in wave order.  Every order is
-// fixed, so the charges do not depend on scheduling.
-constexpr int kLgWaves = kLgThreads / 64;
-
-__global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restrict__ binned,
-                                                          const int4* __restrict__ items,
-                                                          const int* __restrict__ tile_item0, DeviceScalars* sc,
-                                                          float* __restrict__ charge, float* __restrict__ windows,
-                                                          int acc_cap) {
-#pragma clang fp contract(off)
-  chain_priority();
-  extern __shared__ float acc[];  // [charge][node of the window], acc_cap floats
-  __shared__ int box_start[kLgBoxesPerTile];
-  __shared__ int part[kLgThreads];
-  __shared__ float2 sorted[kChunk];
-  __shared__ float wave_part[kLgWaves][4 * kLgOrder * kLgOrder];
-  __shared__ int wave_total[kLgWaves];
-  if (static_cast<int>(blockIdx.x) >= sc->num_items) return;
-  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int nb = s.lg_boxes;
   const int lane = static_cast<int>(threadIdx.x) & 63;
-  const DeviceScalars s = *sc;
-  const int4 it = items[blockIdx.x];
-  const int tile = s.lg_tile;
-  const int win = tile * kLgOrder;
-  const int wvals = 4 * win * win;
-  if (wvals > acc_cap) {  // uniform over the grid: no workgroup touches LDS beyond acc_cap
-    if (threadIdx.x == 0) atomicOr(&sc->error_flags, kErrInterpGrid);
-    return;
-  }
-  const int ta = s.lg_tiles_axis;
-  const int tx = it.x % ta, ty = it.x / ta;
-  const int bx0 = tx * tile, by0 = ty * tile;
-  const int nbox = tile * tile;
-  box_start[threadIdx.x] = 0;
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  tkey[threadIdx.x] = -1;
+  for (int e = threadIdx.x; e < kLgTable * kLgSums; e += kLgThreads) tval[e] = 0.0f;
   __syncthreads();
-  const int count = it.z - it.y;  // <= kChunk
-  // counting sort of the item's points by box
-  float2 v[kLgRun];
-  int box[kLgRun], rank[kLgRun];
+  // a wave's steps are consecutive points of the order
+  const long long base = static_cast<long long>(blockIdx.x) * kLgChunk + static_cast<long long>(wave) * kLgSteps * 64;
+  for (int k = 0; k < kLgSteps; ++k) {
+    const long long i = base + k * 64 + lane;
+    float a[kLgSums];
+    int key = -1;  // past the end: a run of its own, never added
+    if (i < n) {
+      const float2 r = y_stored[order[i]];
+      const LgPoint b = lg_locate(r.x - s.shift_x, r.y - s.shift_y, s);
+      key = b.by * nb + b.bx;
+      lg_power_sums(b, a);
+    } else {
 #pragma unroll
-  for (int q = 0; q < kLgRun; ++q) {
-    const int p = q * kLgThreads + static_cast<int>(threadIdx.x);
-    box[q] = -1;
-    if (p < count) {
-      v[q] = binned[it.y + p];
-      const LgPoint b = lg_locate(v[q].x, v[q].y, s);
-      box[q] = (b.by - by0) * tile + (b.bx - bx0);
-      rank[q] = atomicAdd(&box_start[box[q]], 1);
+      for (int e = 0; e < kLgSums; ++e) a[e] = 0.0f;
     }
-  }
-  __syncthreads();
-  {  // scan of the box counts: shuffles within each wave, wave sums through LDS
-    const int t = threadIdx.x;
-    const int c = box_start[t];
-    int inc = c;
+    const int prev = __builtin_amdgcn_update_dpp(0, key, kDppWaveShr1, 0xf, 0xf, true);
+    const int next = __builtin_amdgcn_update_dpp(0, key, kDppWaveShl1, 0xf, 0xf, true);
+    float take = (lane == 0 || prev != key) ? 0.0f : 1.0f;
+    lg_seg_scan(a, take);
+    if (key >= 0 && (lane == 63 || next != key)) {  // the last lane of its run
+      unsigned int h = (static_cast<unsigned int>(key) * 2654435761u) >> (32 - kLgTableBits);
+      int slot = -1;
+      for (int probe = 0; probe < kLgTable; ++probe) {
+        const int old = atomicCAS(&tkey[h], -1, key);
+        if (old == -1 || old == key) {
+          slot = static_cast<int>(h);
+          break;
+        }
+        h = (h + 1u) & (kLgTable - 1);
+      }
+      if (slot >= 0) {
+        float* dst = tval + slot * kLgSums;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int x = __shfl_up(inc, off, 64);
-      if (lane >= off) inc += x;
-    }
-    if (lane == 63) wave_total[wave] = inc;
-    __syncthreads();
+        for (int e = 0; e < kLgSums; ++e) atomicAdd(dst + e, a[e]);
+      } else {
 #pragma unroll
-    for (int w = 0; w < kLgWaves; ++w) inc += w < wave ? wave_total[w] : 0;
-    part[t] = inc;               // inclusive end
-    box_start[t] = inc - c;      // exclusive start
-  }
-  __syncthreads();
-#pragma unroll
-  for (int q = 0; q < kLgRun; ++q) {
-    if (box[q] >= 0) sorted[box_start[box[q]] + rank[q]] = v[q];
-  }
-  __syncthreads();
-  float a[4 * kLgOrder * kLgOrder];
-  if (nbox == 1) {
-    // one box: the waves take interleaved stretches of 64 points
-#pragma unroll
-    for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) a[e] = 0.0f;
-    for (int p = wave * 64 + lane; p < count; p += kLgThreads) lg_accumulate(lg_locate(sorted[p].x, sorted[p].y, s), a);
-    lg_wave_sum(a);
-    if (lane == 63) {
-#pragma unroll
-      for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) wave_part[wave][e] = a[e];
-    }
-    __syncthreads();
-    if (threadIdx.x < 4 * kLgOrder * kLgOrder) {
-      const int e = threadIdx.x;
-      float t = wave_part[0][e];
-#pragma unroll
-      for (int w = 1; w < kLgWaves; ++w) t += wave_part[w][e];
-      wave_part[0][e] = t;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-#pragma unroll
-      for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) a[e] = wave_part[0][e];
-      lg_store_box(acc, 0, tile, win, a);
-    }
-  } else {
-    for (int b = wave; b < nbox; b += kLgWaves) {
-      const int b0 = box_start[b];
-      const int b1 = part[b];
-#pragma unroll
-      for (int e = 0; e < 4 * kLgOrder * kLgOrder; ++e) a[e] = 0.0f;
-      for (int p = b0 + lane; p < b1; p += 64) lg_accumulate(lg_locate(sorted[p].x, sorted[p].y, s), a);
-      // uniform over the wave: the sum lands in lane 63; with at most one
-      // point, lane 0 already holds it (zeros for an empty box)
-      const bool many = b1 - b0 > 1;
-      if (many) lg_wave_sum(a);
-      if (lane == (many ? 63 : 0)) lg_store_box(acc, b, tile, win, a);
+        for (int e = 0; e < kLgSums; ++e) {
+          unsafeAtomicAdd(straggler + static_cast<std::size_t>(key) * kLgSums + e, a[e]);
+        }
+        atomicOr(box_count + key, kLgStraggled);
+      }
     }
   }
   __syncthreads();
-  const bool sole = tile_item0[it.x + 1] - tile_item0[it.x] == 1;
-  if (sole) {
-    const int m = s.lg_nodes;
-    const int mm = m * m;
-    const int wn = win * win;
-    for (int e = threadIdx.x; e < wvals; e += kLgThreads) {
-      const int ch = e / wn;
-      const int node = e - ch * wn;
-      const int gy = ty * win + node / win;
-      const int gx = tx * win + node % win;
-      if (gx < m && gy < m) charge[ch * mm + gy * m + gx] = acc[e];
+  // occupied slots: listed in their box (beyond kLgSlots: added as
+  // stragglers), then stored to the workgroup's scratch
+  const int t = threadIdx.x;
+  const int gb = tkey[t];
+  bool listed = false;
+  if (gb >= 0) {
+    const int k = atomicAdd(box_count + gb, 1) & kLgCountMask;
+    if (k < kLgSlots) {
+      box_list[static_cast<std::size_t>(gb) * kLgSlots + k] = static_cast<int>(blockIdx.x) * kLgTable + t;
+      listed = true;
+    } else {
+#pragma unroll
+      for (int e = 0; e < kLgSums; ++e) {
+        unsafeAtomicAdd(straggler + static_cast<std::size_t>(gb) * kLgSums + e, tval[t * kLgSums + e]);
+      }
+      atomicOr(box_count + gb, kLgStraggled);
     }
-  } else {
-    float* w = windows + static_cast<std::size_t>(blockIdx.x) * kLgWinVals;
-    for (int e = threadIdx.x; e < wvals; e += kLgThreads) w[e] = acc[e];
+  }
+  if (!listed) tkey[t] = -1;
+  __syncthreads();
+  float* out = table_out + static_cast<std::size_t>(blockIdx.x) * kLgTable * kLgSums;
+  for (int e = threadIdx.x; e < kLgTable * kLgSums; e += kLgThreads) {
+    if (tkey[e / kLgSums] >= 0) out[e] = tval[e];
   }
 }
 
-// Every node of every plane; nodes of single-item tiles were written by the
-// spread itself, nodes of empty tiles get zero.  One workgroup per tile: G
-// threads share each window value, thread g summing the tile's items
-// i0 + g, i0 + g + G, ..., and the G partial sums are added in the order
-// g = 0 .. G - 1, so the result does not depend on scheduling.  A dense box
-// early in the optimisation (hundreds of items in one tile) is then summed by
-// the whole workgroup, not by one thread per node.
-__global__ __launch_bounds__(kLgThreads) void k_lg_gather(const int* __restrict__ tile_item0,
-                                                          const float* __restrict__ windows, const DeviceScalars* sc,
-                                                          float* __restrict__ charge) {
+// Every node of the m x m charge planes: a box's listed slots (at most
+// kLgSlots, in list order) and, when flagged, its straggler sums (then
+// cleared) are summed into its 21 power sums, which are combined into its 9
+// nodes x 4 moments; each box's count is cleared once its slots are read.  A
+// workgroup takes kLgGatherBoxes boxes: first each thread sums power sums of
+// the boxes (box, sum) by stride, then each thread writes node moments
+// (box, moment) by stride.
+constexpr int kLgGatherBoxes = 32;
+
+__global__ __launch_bounds__(kLgThreads) void k_lg_gather(const DeviceScalars* sc, int max_nodes,
+                                                          const float* __restrict__ table_out,
+                                                          int* __restrict__ box_count,
+                                                          const int* __restrict__ box_list,
+                                                          float* __restrict__ straggler, float* __restrict__ charge) {
+#pragma clang fp contract(off)
   chain_priority();
-  __shared__ float part[kLgThreads];
+  __shared__ float ps[kLgGatherBoxes][kLgSums];
+  __shared__ int counts[kLgGatherBoxes];
   const int m = sc->lg_nodes;
-  const int ta = sc->lg_tiles_axis;
-  const int win = sc->lg_tile * kLgOrder;
-  const int wn = win * win;
-  const int wvals = 4 * wn;
-  const int mm = m * m;
-  const int per = wvals < kLgThreads ? wvals : kLgThreads;  // values per pass
-  const int groups = kLgThreads / per;                      // threads per value
-  const int g = static_cast<int>(threadIdx.x) / per;
-  const int v = static_cast<int>(threadIdx.x) - g * per;
-  for (int t = blockIdx.x; t < ta * ta; t += gridDim.x) {
-    const int i0 = tile_item0[t];
-    const int i1 = tile_item0[t + 1];
-    if (i1 - i0 == 1) continue;  // uniform over the workgroup
-    const int tx = t % ta, ty = t / ta;
-    for (int e0 = 0; e0 < wvals; e0 += per) {
-      const int e = e0 + v;
-      float acc = 0.0f;
-      if (g < groups && e < wvals) {
-        const float* src = windows + e;
-        int i = i0 + g;
-        for (; i + 3 * groups < i1; i += 4 * groups) {
-          const float a0 = src[static_cast<std::size_t>(i) * kLgWinVals];
-          const float a1 = src[static_cast<std::size_t>(i + groups) * kLgWinVals];
-          const float a2 = src[static_cast<std::size_t>(i + 2 * groups) * kLgWinVals];
-          const float a3 = src[static_cast<std::size_t>(i + 3 * groups) * kLgWinVals];
-          acc += a0;
-          acc += a1;
-          acc += a2;
-          acc += a3;
-        }
-        for (; i < i1; i += groups) acc += src[static_cast<std::size_t>(i) * kLgWinVals];
-      }
-      __syncthreads();
-      part[threadIdx.x] = acc;
-      __syncthreads();
-      if (g == 0 && e < wvals) {
-        float sum = part[v];
-        for (int q = 1; q < groups; ++q) sum += part[q * per + v];
-        const int ch = e / wn;
-        const int node = e - ch * wn;
-        const int gy = ty * win + node / win;
-        const int gx = tx * win + node % win;
-        if (gx < m && gy < m) charge[ch * mm + gy * m + gx] = sum;
-      }
+  if (m > max_nodes) return;  // flagged by the spread
+  const int nb = sc->lg_boxes;
+  const long long mm = static_cast<long long>(m) * m;
+  const int boxes = nb * nb;
+  for (int b0 = blockIdx.x * kLgGatherBoxes; b0 < boxes; b0 += gridDim.x * kLgGatherBoxes) {
+    if (threadIdx.x < kLgGatherBoxes) {
+      const int b = b0 + static_cast<int>(threadIdx.x);
+      counts[threadIdx.x] = b < boxes ? box_count[b] : 0;
     }
+    __syncthreads();
+    for (int q = threadIdx.x; q < kLgGatherBoxes * kLgSums; q += kLgThreads) {
+      const int sub = q / kLgSums;
+      const int e = q - sub * kLgSums;
+      const int b = b0 + sub;
+      if (b >= boxes) continue;
+      const int word = counts[sub];
+      const int cnt = min(word & kLgCountMask, kLgSlots);
+      float sum = 0.0f;
+      if ((word & kLgStraggled) != 0) {
+        const std::size_t at = static_cast<std::size_t>(b) * kLgSums + e;
+        sum = straggler[at];
+        straggler[at] = 0.0f;
+      }
+      for (int k = 0; k < cnt; ++k) {
+        sum += table_out[static_cast<std::size_t>(box_list[static_cast<std::size_t>(b) * kLgSlots + k]) * kLgSums + e];
+      }
+      ps[sub][e] = sum;
+    }
+    __syncthreads();  // every count and slot of the block's boxes read
+    if (threadIdx.x < kLgGatherBoxes) {
+      const int b = b0 + static_cast<int>(threadIdx.x);
+      if (b < boxes && counts[threadIdx.x] != 0) box_count[b] = 0;
+    }
+    for (int q = threadIdx.x; q < kLgGatherBoxes * kLgMoments; q += kLgThreads) {
+      const int sub = q / kLgMoments;
+      const int v = q - sub * kLgMoments;
+      const int b = b0 + sub;
+      if (b >= boxes) continue;
+      const int node = v / 4, t = v % 4;
+      const int r = node / kLgOrder, c = node % kLgOrder;
+      // (y polynomial, x polynomial) kinds: m0 (A, A), m1x (A, B),
+      // m1y (B, A), m2 (A, D) + (D, A)
+      const int ky0 = t == 2 ? 1 : 0, kx0 = t == 1 ? 1 : (t == 3 ? 2 : 0);
+      float val = 0.0f;
+#pragma unroll
+      for (int term = 0; term < 2; ++term) {
+        if (term == 1 && t != 3) break;
+        const int ky = term == 0 ? ky0 : 2, kx = term == 0 ? kx0 : 0;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+#pragma unroll
+          for (int j = 0; j < 5; ++j) {
+            if (lg_sum_exists(i, j)) val += (kLgPolys.k[ky][r][i] * kLgPolys.k[kx][c][j]) * ps[sub][lg_sum_index(i, j)];
+          }
+        }
+      }
+      const int bx = b % nb, by = b / nb;
+      charge[t * mm + static_cast<long long>(by * kLgOrder + r) * m + bx * kLgOrder + c] = val;
+    }
+    __syncthreads();  // ps and counts reused by the next boxes
   }
 }
 
@@ -854,52 +862,49 @@ hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const 
 
 }  // namespace
 
-hipError_t launch_interp_bin_count(const float2* y_stored, float2* y_cur, const DeviceScalars* sc,
-                                   InterpBuffers& ib, int n, hipStream_t stream) {
-  const int needed = (n + kLgThreads - 1) / kLgThreads;
-  const int blocks = std::max(1, std::min(needed, 1024));
-  k_lg_bin_count<<<blocks, kLgThreads, 0, stream>>>(y_stored, y_cur, sc, ib.tile_count, n);
-  return hipGetLastError();
-}
-
 // Boxes per axis of a grid of at most fft_len / 2 nodes per axis.
 int lg_boxes_bound(int fft_len) { return std::max(1, std::min(fft_len / 2, kLgMaxNodes) / kLgOrder); }
 
-// The most tiles per axis any such grid is cut into (lg_tile_for, as the
-// statistics apply it on the device).
-int lg_tiles_axis_bound(int fft_len) {
-  int most = 1;
-  for (int nb = 1; nb <= lg_boxes_bound(fft_len); ++nb) most = std::max(most, (nb + lg_tile_for(nb) - 1) / lg_tile_for(nb));
-  return most;
-}
-
-hipError_t launch_interp_bin_scatter(const float2* y_cur, DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len,
-                                     hipStream_t stream) {
-  constexpr int kBatch = kLgThreads * kLgScatterPerThread;
-  const int needed = (n + kBatch - 1) / kBatch;
-  const int blocks = std::max(1, std::min(needed, 1024));
-  const int ta = lg_tiles_axis_bound(fft_len);
-  const int tiles_cap = ta * ta;
-  k_lg_bin_scatter<<<blocks, kLgThreads, tiles_cap * sizeof(int), stream>>>(y_cur, sc, ib.tile_cursor, ib.binned, n,
-                                                                           tiles_cap);
+hipError_t launch_interp_spread(const float2* y_stored, DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len,
+                                hipStream_t stream) {
+  const int max_nodes = lg_boxes_bound(fft_len) * kLgOrder;
+  const int blocks = lg_spread_blocks(n);
+  k_lg_spread<<<blocks, kLgThreads, 0, stream>>>(y_stored, ib.order, sc, n, max_nodes, ib.tables, ib.box_count,
+                                                  ib.box_list, ib.straggler);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // boxes of the largest grid this FFT length holds, a few per workgroup
+  const int boxes = lg_boxes_bound(fft_len) * lg_boxes_bound(fft_len);
+  const int gblocks = std::max(1, std::min((boxes + kLgGatherBoxes - 1) / kLgGatherBoxes, 8192));
+  k_lg_gather<<<gblocks, kLgThreads, 0, stream>>>(sc, max_nodes, ib.tables, ib.box_count, ib.box_list,
+                                                   ib.straggler, ib.charge);
   return hipGetLastError();
 }
 
-// The largest tile a grid of at most fft_len / 2 nodes per axis can use (the
-// tile grows with the box count).
-int lg_tile_bound(int fft_len) { return lg_tile_for(lg_boxes_bound(fft_len)); }
+// The order's sort: rocPRIM picks a block sort and ~10 merge passes up to
+// 2^20 items by default (about 0.23 ms at 1M points on MI355X); a merge-sort
+// limit of 0 makes it use the onesweep radix sort at every size.
+using LgOrderSortConfig = rocprim::radix_sort_config<rocprim::default_config, rocprim::default_config,
+                                                     rocprim::default_config, 0>;
 
-hipError_t launch_interp_spread(DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len, hipStream_t stream) {
-  const int win = lg_tile_bound(fft_len) * kLgOrder;
-  const int acc_cap = 4 * win * win;
-  k_lg_spread<<<lg_max_items(n), kLgThreads, static_cast<std::size_t>(acc_cap) * sizeof(float), stream>>>(
-      ib.binned, ib.items, ib.tile_item0, sc, ib.charge, ib.windows, acc_cap);
-  return hipGetLastError();
+hipError_t interp_order_temp_bytes(int n, std::size_t& bytes) {
+  bytes = 0;
+  return rocprim::radix_sort_pairs<LgOrderSortConfig>(nullptr, bytes, static_cast<const unsigned int*>(nullptr),
+                                   static_cast<unsigned int*>(nullptr), static_cast<const int*>(nullptr),
+                                   static_cast<int*>(nullptr), static_cast<std::size_t>(n), 0u,
+                                   static_cast<unsigned int>(2 * kLgOrderBits));
 }
 
-hipError_t launch_interp_gather(const DeviceScalars* sc, InterpBuffers& ib, hipStream_t stream) {
-  k_lg_gather<<<kLgMaxTilesAxis * kLgMaxTilesAxis, kLgThreads, 0, stream>>>(ib.tile_item0, ib.windows, sc, ib.charge);
-  return hipGetLastError();
+hipError_t launch_interp_order(const float2* y_stored, const DeviceScalars* sc, InterpBuffers& ib, int n,
+                               hipStream_t stream) {
+  const int blocks = std::max(1, std::min((n + kLgThreads - 1) / kLgThreads, 4096));
+  k_lg_order_keys<<<blocks, kLgThreads, 0, stream>>>(y_stored, sc, ib.order_keys, ib.order_idx, n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  std::size_t bytes = ib.order_temp_bytes;
+  return rocprim::radix_sort_pairs<LgOrderSortConfig>(ib.order_temp, bytes, ib.order_keys, ib.order_keys + n, ib.order_idx, ib.order,
+                                   static_cast<std::size_t>(n), 0u, static_cast<unsigned int>(2 * kLgOrderBits),
+                                   stream);
 }
 
 hipError_t launch_interp_fft(int which, int fft_len, InterpBuffers& ib, DeviceScalars* sc, const float2* tw, int n,

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstddef>
 #include <cstdint>
 #include <string>
@@ -42,7 +43,6 @@ struct alignas(16) DeviceScalars {
   float lg_ints_per_unit;
   float lg_lo, lg_box_w, lg_node_h;
   int lg_boxes, lg_nodes;
-  int lg_tile, lg_tiles_axis;  // boxes per tile and axis (a power of two), tiles per axis
   double lg_box_wd;            // box width in fp64: points are located in fp64
 };
 
@@ -79,30 +79,20 @@ inline int max_spread_items(int n, int g) {
 enum ErrorBits : unsigned int { kErrIndex = 1u, kErrDistance = 2u, kErrInterpGrid = 4u };
 
 // FIt-SNE interpolation grid: order-3 nodes, at most kLgMaxNodes nodes per
-// axis (FFT length <= 4096).  Points are binned by tiles of T x T boxes, T the
-// smallest power of two that keeps the tiles per axis <= kLgTilesAxisTarget,
-// at most kLgMaxTile (then up to kLgMaxTilesAxis tiles per axis); a work
-// item's spread window is 3T x 3T nodes x 4 charges (at most kLgWinVals
-// floats).  Few, well-filled tiles keep the binning's histograms small and
-// the spreading's workgroups few: under the attraction's memory traffic every
-// round of latency-bound workgroups costs tens of microseconds.
+// axis (FFT length <= 4096).
 constexpr int kLgOrder = 3;
-constexpr int kLgMaxTile = 16;
-constexpr int kLgTilesAxisTarget = 64;
-constexpr int kLgMaxTilesAxis = 64;
-constexpr int kLgWin = kLgMaxTile * kLgOrder;
-constexpr int kLgWinVals = 4 * kLgWin * kLgWin;
 constexpr int kLgMaxNodes = 2048;
 constexpr int kLgMaxFft = 2 * kLgMaxNodes;
-static_assert(kLgMaxTilesAxis * kLgMaxTilesAxis <= kMaxTiles, "interpolation tiles fit the bin plan");
-static_assert(kLgMaxTile * kLgMaxTilesAxis * kLgOrder >= kLgMaxNodes, "the largest tile covers the largest grid");
-// Boxes per tile side for a grid of nb boxes per axis (the rule above).
-__host__ __device__ inline int lg_tile_for(int nb) {
-  int tile = 1;
-  while ((nb + tile - 1) / tile > kLgTilesAxisTarget && tile < kLgMaxTile) tile *= 2;
-  return tile;
-}
-inline int lg_max_items(int n) { return (n + kChunk - 1) / kChunk + kLgMaxTilesAxis * kLgMaxTilesAxis; }
+constexpr int kLgMaxBoxes = kLgMaxNodes / kLgOrder;  // per axis
+// Spreading: a workgroup sums kLgSpreadChunk points of the spread order into
+// an LDS table of kLgTable slots keyed by box; each box lists up to kLgSlots
+// slots.
+constexpr int kLgSpreadChunk = 1024;
+constexpr int kLgTableBits = 8;
+constexpr int kLgTable = 1 << kLgTableBits;
+constexpr int kLgSlots = 32;
+constexpr int kLgSumsPerBox = 21;  // power sums of a box's points (the node moments' ingredients)
+inline int lg_spread_blocks(int n) { return std::max(1, (n + kLgSpreadChunk - 1) / kLgSpreadChunk); }
 // Column passes of the interpolation grid map their blocks to columns XCD by
 // XCD (block b on XCD b % kLgColXcds takes the next column of that XCD's
 // contiguous range), so their launches are rounded up to a multiple of it.
@@ -127,11 +117,8 @@ enum KernelId : int {
   kKCommit,
   kKRenumber,
   kKTileBuild,
-  kKLgBinCount,
-  kKLgBinPlan,
-  kKLgBinScatter,
+  kKLgOrder,
   kKLgSpread,
-  kKLgGather,
   kKLgKernelRows,
   kKLgKernelCols,
   kKLgChargeRows,
@@ -170,7 +157,8 @@ struct GridBuffers {
 // count m and the FFT length f vary; planes use row stride m, spectra row
 // stride f / 2 + 1.
 struct InterpBuffers {
-  float* charge = nullptr;     // 4 planes of m*m: node moments m0, m1x, m1y, m2 (offsets in units of h)
+  float* charge = nullptr;     // 4 planes of m*m: node moments m0, m1x, m1y, m2 (offsets in units of h);
+                               // zero between iterations
   float4* field = nullptr;     // m*m potentials (phi0, xi_x, xi_y, 0)
   float2* k_rows = nullptr;    // 2 planes of (G+1)^2: kernel row spectra ((K^r, K1^r), (Bx, By)), row-major
   float2* k_cols = nullptr;    // 2 planes of (G+1)^2: the kernel spectrum quadrant ((K^, K1^), (Cx, Cy)),
@@ -178,12 +166,15 @@ struct InterpBuffers {
   float2* spec_a = nullptr;    // 3 planes of G*(G+1): charge row spectra, row-major
   float2* spec_b = nullptr;    // 3 planes of G*(G+1): potential row spectra, row-major
   double* z_partial = nullptr; // kLgZPartials: sums of the normaliser per block
-  int* tile_count = nullptr;   // kMaxTiles, zero between iterations
-  int* tile_cursor = nullptr;  // kMaxTiles
-  int* tile_item0 = nullptr;   // kMaxTiles + 1: first work item of each tile
-  int4* items = nullptr;       // lg_max_items(n)
-  float* windows = nullptr;    // lg_max_items(n) * kLgWinVals: per-item spread windows
-  float2* binned = nullptr;    // n centred points in tile order (shared with the bilinear grid)
+  float* tables = nullptr;     // lg_spread_blocks(n) x kLgTable slots x kLgSumsPerBox: the spread's per-box sums
+  int* box_count = nullptr;    // boxes of the largest grid: slots listed per box, zero between iterations
+  int* box_list = nullptr;     // boxes x kLgSlots: the listed slots (workgroup * kLgTable + slot)
+  float* straggler = nullptr;  // boxes x kLgSumsPerBox: atomic exceptions, zero between iterations
+  int* order = nullptr;        // n: spread order (working indices sorted by position)
+  unsigned int* order_keys = nullptr;  // 2n: Morton keys, sorted keys
+  int* order_idx = nullptr;    // n: 0 .. n-1 (the sort's payload)
+  void* order_temp = nullptr;  // radix sort scratch
+  std::size_t order_temp_bytes = 0;
 };
 
 struct Csr {
@@ -230,18 +221,19 @@ hipError_t launch_conv_cols(GridBuffers& gb, const float2* tw, hipStream_t strea
 hipError_t launch_inverse_rows(GridBuffers& gb, const float2* tw, int n, DeviceScalars* sc, hipStream_t stream);
 
 // ---- FIt-SNE interpolation grid ---------------------------------------------
-// Binning, spreading and the zero-padded convolution at FFT length fft_len
-// (2^a or 3 * 2^a in [64, kLgMaxFft] with fft_len >= 2 * lg_nodes); the
-// node count itself is read on the device.  Points must already be centred
-// into y_cur by launch_interp_bin_count.
-hipError_t launch_interp_bin_count(const float2* y_stored, float2* y_cur, const DeviceScalars* sc,
-                                   InterpBuffers& ib, int n, hipStream_t stream);
-hipError_t launch_interp_bin_plan(InterpBuffers& ib, DeviceScalars* sc, hipStream_t stream);
-hipError_t launch_interp_bin_scatter(const float2* y_cur, DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len,
-                                     hipStream_t stream);
-// fft_len bounds the node count and so the tile size the spread window needs.
-hipError_t launch_interp_spread(DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len, hipStream_t stream);
-hipError_t launch_interp_gather(const DeviceScalars* sc, InterpBuffers& ib, hipStream_t stream);
+// Spreading and the zero-padded convolution at FFT length fft_len (2^a or
+// 3 * 2^a in [64, kLgMaxFft] with fft_len >= 2 * lg_nodes); the node count
+// itself is read on the device.  The spread reads the stored layout in
+// ib.order and adds the node moments to the charge planes, which must be
+// zero (they are after allocation and after every convolution).
+hipError_t launch_interp_spread(const float2* y_stored, DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len,
+                                hipStream_t stream);
+// The spread order of the current layout (needs this iteration's geometry):
+// working indices sorted by position.  Any permutation is correct; a spatial
+// one keeps the spread's runs long.
+hipError_t interp_order_temp_bytes(int n, std::size_t& bytes);
+hipError_t launch_interp_order(const float2* y_stored, const DeviceScalars* sc, InterpBuffers& ib, int n,
+                               hipStream_t stream);
 // which: 0 kernel rows, 2 kernel cols, 3 charge rows, 5 conv cols, 7 inverse
 // rows (+ normaliser); other values are invalid
 hipError_t launch_interp_fft(int which, int fft_len, InterpBuffers& ib, DeviceScalars* sc, const float2* tw, int n,

@@ -194,11 +194,14 @@ def test_closed_session_returns_memory(hip, capture):
     memory then reads at the in-session level, and the next session's
     identical requests reuse them), so a single reading may be one
     session's buffers low; a leak instead lowers every later reading.  The
-    check, over the last five sessions: every reading within 64 MiB of the
-    highest, except at most one that sits at the in-session level (within
-    64 MiB of the lowest in-session reading).  Graphs with parallel branches
-    lost 1.4 GB per session here; a steady leak of more than 22 MiB per
-    session fails."""
+    check, over the last five sessions: every reading is within 64 MiB of
+    the highest of them or sits at the in-session level (within 64 MiB of the
+    lowest in-session reading; the runtime has held a closed session's blocks
+    in two of five readings here, alternating with full returns), and the
+    highest is within 64 MiB of the second warm-up session's reading.  A leak
+    lowers the readings step by step, which neither level admits: graphs with
+    parallel branches lost 1.4 GB per session here; a steady leak of more than
+    about 22 MiB per session fails."""
     n, k = 200_000, 90
     x, _ = synthetic.gaussian_mixture(synthetic.CONFIGS[2], seed=1, n=n)
     knn = hip.exact_knn(np.ascontiguousarray(x, np.float32), k, keep_device=True)
@@ -243,5 +246,5 @@ def test_closed_session_returns_memory(hip, capture):
     slack = 64 * 2**20
     top, in_session = max(after[2:]), min(during)
     held = [v for v in after[2:] if top - v > slack]
-    assert len(held) <= 1, (after, during)
     assert all(abs(v - in_session) <= slack for v in held), (after, during)
+    assert top >= after[1] - slack, (after, during)

@@ -279,3 +279,56 @@ def test_opentsne_knn_interpolation_grid(hip, oracle_mod, prob):
     assert err <= 1e-4
     with pytest.raises(ValueError):
         hip.opentsne_knn(idx, dist, n_neighbors=45, perplexity=15.0, interpolation_grid={"order": 3})
+
+
+def _relabel(idx, dist, y, order):
+    """The same problem with point order[j] renamed j: KNN rows and their
+    1-based indices, and the layout."""
+    inv = np.empty_like(order)
+    inv[order] = np.arange(order.size)
+    idx_new = np.asfortranarray((inv[np.asarray(idx)[order] - 1] + 1).astype(np.int32))
+    dist_new = np.asfortranarray(np.asarray(dist)[order])
+    return idx_new, dist_new, np.ascontiguousarray(y[order])
+
+
+@pytest.mark.parametrize("n_keep", [3000, 2945])
+def test_interp_spread_independent_of_point_order(hip, oracle_mod, prob, n_keep):
+    """The spread sums each wave's runs of points that share a box, so run
+    structure must not matter: the same points in random order (runs of about
+    one point), in box order (runs of up to 64), and with a ragged last wave
+    (2945 = 46 * 64 + 1 points) give the oracle's gradient; a layout with every
+    point on one spot (one box, one run per wave) stays finite and matches."""
+    x, idx, dist, y0 = prob
+    if n_keep < idx.shape[0]:
+        small = small_problem(n=n_keep, dim=20, k=45, components=6, seed=21)
+        x, idx, dist = small[0], small[2], small[3]
+        y0 = synthetic.pca_init(x)
+    y = _with_span(y0, 60.0)
+    n = y.shape[0]
+    rng = np.random.default_rng(7)
+    boxes = np.floor((y - y.min(0)) / 1.0).astype(np.int64)
+    orders = {"random": rng.permutation(n), "box": np.lexsort((boxes[:, 0], boxes[:, 1]))}
+    _say(f"case: interpolation-grid spread under point orders, n {n}")
+    for name, order in orders.items():
+        idx_o, dist_o, y_o = _relabel(idx, dist, y, order)
+        with hip.TsneSession(idx_o, dist_o, perplexity=15.0, index_offset=1) as s:
+            s.set_repulsion(LAGRANGE, 3, 50, 1.0)
+            s.set_state(y_o)
+            g = s.gradient(1.0, LAGRANGE)
+            P = oracle_mod.OracleP.wrap(*s.csr())
+        g0, _, _ = P.lagrange_gradient(y_o, 1.0, order=3, min_intervals=50, threads=8)
+        err = rel_l2(g, g0)
+        _say(f"  {name} order: relL2 {err:.2e}")
+        assert err <= GRAD_TOL
+    # every point on one spot, plus one far away: one box holds all but one
+    y1 = np.zeros_like(y)
+    y1[-1] = (30.0, -20.0)
+    with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+        s.set_repulsion(LAGRANGE, 3, 50, 1.0)
+        s.set_state(y1)
+        g = s.gradient(1.0, LAGRANGE)
+        P = oracle_mod.OracleP.wrap(*s.csr())
+    g0, _, _ = P.lagrange_gradient(y1, 1.0, order=3, min_intervals=50, threads=8)
+    err = rel_l2(g, g0)
+    _say(f"  one crowded box: relL2 {err:.2e}")
+    assert np.all(np.isfinite(g)) and err <= GRAD_TOL
