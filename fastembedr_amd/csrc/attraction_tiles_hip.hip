@@ -26,6 +26,7 @@
 //   k_tile_scatter             entries and bridges to their padded places
 //   k_tile_bases               each slot group's base row into its values
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <rocprim/device/device_radix_sort.hpp>
@@ -657,7 +658,7 @@ int primary_slots(const Tiles& t, int xcds, int slots_per_xcd) {
 }
 
 hipError_t attract_launch(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds, int blocks,
-                          int slots, int helper, unsigned int total, hipStream_t stream) {
+                          int slots, int helper, unsigned int total, hipStream_t stream, hipEvent_t done) {
   constexpr int NT = kTileThreads;
   // a ring of 2 groups (one in flight while one is summed); deeper rings
   // measured no faster at config 2, and the LDS allows 3 workgroups per CU
@@ -665,6 +666,10 @@ hipError_t attract_launch(const Tiles& t, const float2* y_cur, float2* attr, flo
     k_attract_tiles_seg<NT, 2, 3, true><<<blocks, NT, 0, stream>>>(
         t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr, exaggeration, t.n, t.row_blocks, xcds, t.work,
         slots, total);
+  } else if (done != nullptr) {
+    hipExtLaunchKernelGGL(k_attract_tiles_seg<NT, 2, 3, false>, dim3(blocks), dim3(NT), 0, stream, nullptr, done, 0,
+                          t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr, exaggeration, t.n,
+                          t.row_blocks, xcds, t.work, slots, total);
   } else {
     k_attract_tiles_seg<NT, 2, 3, false><<<blocks, NT, 0, stream>>>(
         t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr, exaggeration, t.n, t.row_blocks, xcds, t.work,
@@ -676,11 +681,11 @@ hipError_t attract_launch(const Tiles& t, const float2* y_cur, float2* attr, flo
 }  // namespace
 
 hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds,
-                                int slots_per_xcd, int helper_per_xcd, hipStream_t stream) {
+                                int slots_per_xcd, int helper_per_xcd, hipStream_t stream, hipEvent_t done) {
   if (t.work == nullptr || xcds < 1 || xcds > kTileMaxXcds || helper_per_xcd < 0) return hipErrorInvalidValue;
   const int slots = primary_slots(t, xcds, slots_per_xcd);
   const unsigned int total = static_cast<unsigned int>((slots + helper_per_xcd) * xcds);
-  return attract_launch(t, y_cur, attr, exaggeration, xcds, slots * xcds, slots, 0, total, stream);
+  return attract_launch(t, y_cur, attr, exaggeration, xcds, slots * xcds, slots, 0, total, stream, done);
 }
 
 hipError_t launch_attract_tiled_helper(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration,
@@ -688,7 +693,7 @@ hipError_t launch_attract_tiled_helper(const Tiles& t, const float2* y_cur, floa
   if (t.work == nullptr || xcds < 1 || xcds > kTileMaxXcds || helper_per_xcd < 1) return hipErrorInvalidValue;
   const int slots = primary_slots(t, xcds, slots_per_xcd);
   const unsigned int total = static_cast<unsigned int>((slots + helper_per_xcd) * xcds);
-  return attract_launch(t, y_cur, attr, exaggeration, xcds, helper_per_xcd * xcds, slots, 1, total, stream);
+  return attract_launch(t, y_cur, attr, exaggeration, xcds, helper_per_xcd * xcds, slots, 1, total, stream, nullptr);
 }
 
 }  // namespace fehip

@@ -24,6 +24,7 @@
 //                       exact O(n^2) terms for checking (:1014-1074, :958-983,
 //                       :1258-1285)
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <rocprim/device/device_radix_sort.hpp>
@@ -1354,11 +1355,21 @@ template <int MODE>
 hipError_t update_launch(const float2* y_cur, const float2* attr, float2* y_out, float2* update, float2* gains,
                          float2* grad_out, const float2* exact_rep, const GridBuffers& gb, const UpdateParams& up,
                          BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
-                         const float4* interp_field) {
+                         const float4* interp_field, hipEvent_t done) {
   const int blocks = reduce_blocks_for(n);
   if (interp_field != nullptr && MODE != kModeGradientExact) {
-    k_update<MODE, true><<<blocks, kPointThreads, 0, stream>>>(y_cur, attr, y_out, update, gains, grad_out,
-                                                               exact_rep, interp_field, gb.g, up, partial, sc, n);
+    if (done != nullptr) {
+      hipExtLaunchKernelGGL(k_update<MODE, true>, dim3(blocks), dim3(kPointThreads), 0, stream, nullptr, done, 0,
+                            y_cur, attr, y_out, update, gains, grad_out, exact_rep, interp_field, gb.g, up, partial,
+                            sc, n);
+    } else {
+      k_update<MODE, true><<<blocks, kPointThreads, 0, stream>>>(y_cur, attr, y_out, update, gains, grad_out,
+                                                                 exact_rep, interp_field, gb.g, up, partial, sc, n);
+    }
+  } else if (done != nullptr) {
+    hipExtLaunchKernelGGL(k_update<MODE, false>, dim3(blocks), dim3(kPointThreads), 0, stream, nullptr, done, 0,
+                          y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb.field, gb.g, up, partial, sc,
+                          n);
   } else {
     k_update<MODE, false><<<blocks, kPointThreads, 0, stream>>>(y_cur, attr, y_out, update, gains, grad_out,
                                                                 exact_rep, gb.field, gb.g, up, partial, sc, n);
@@ -1500,17 +1511,17 @@ hipError_t launch_attract(const Csr& p, const float2* y_cur, float2* attr, float
 hipError_t launch_update(int mode, const float2* y_cur, const float2* attr, float2* y_out, float2* update,
                          float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
                          const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
-                         const float4* interp_field) {
+                         const float4* interp_field, hipEvent_t done) {
   switch (mode) {
     case kModeUpdate:
       return update_launch<kModeUpdate>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up, partial, sc,
-                                        n, stream, interp_field);
+                                        n, stream, interp_field, done);
     case kModeGradientGrid:
       return update_launch<kModeGradientGrid>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up,
-                                              partial, sc, n, stream, interp_field);
+                                              partial, sc, n, stream, interp_field, done);
     case kModeGradientExact:
       return update_launch<kModeGradientExact>(y_cur, attr, y_out, update, gains, grad_out, exact_rep, gb, up,
-                                               partial, sc, n, stream, nullptr);
+                                               partial, sc, n, stream, nullptr, done);
     default:
       return hipErrorInvalidValue;
   }

@@ -157,12 +157,18 @@ struct fastembedr_hip_tsne {
   // attraction's event), so the two streams trade roles every iteration;
   // settle() hands the state back to `stream` for everything else.
   hipStream_t home = nullptr;
+  // ev_layout already marks the end of the latest update, the last work on
+  // `home` (the update's launch completes it itself, so that no marker
+  // stands between the update and the attraction behind it); cleared by
+  // settle() and by every iteration's start.
+  bool layout_at_tail = false;
   // FASTEMBEDR_HIP_UPDATE_ON_CHAIN=0: the update always on `stream`, after
   // waiting for the chain's event.  A wait for an event that another stream
   // has yet to signal cost ~18 us here, one for an event already signalled
   // ~6 us; the chain ends after the attraction, so its stream should carry
   // the update.
   bool update_on_chain = true;
+  bool mark_layout = true;  // FASTEMBEDR_HIP_MARK_LAYOUT=0: a marker after the update instead
   Arena arena;
   Arena work_arena;         // working-order CSR copies, permutations, state double buffers
   Arena tile_arena;         // tiled P for the attraction and its build scratch
@@ -240,12 +246,16 @@ struct fastembedr_hip_tsne {
   fehip::InterpBuffers ib;
   int lg_last_fft = 0;       // FFT length of the last interpolation-grid iteration
   // The spread's point order (working indices sorted by position) is made
-  // again every kLgOrderPeriod interpolation-grid iterations, on first use
+  // again every lg_order_period interpolation-grid iterations, on first use
   // and after a renumbering (stale), and for every gradient probe.  Any
   // permutation gives the same charges (up to the order of fp32 adds); a
   // spatial one keeps the spread's runs long.  lg_order_due asks the next
-  // gradient pieces to make it before the spread.
-  static constexpr int kLgOrderPeriod = 8;
+  // gradient pieces to make it before the spread.  Config 2, whole schedule:
+  // 3664 / 3690 / 3677 it/s at periods 16 / 32 / 48 (a refresh costs ~0.24 ms
+  // beside the attraction; the spread slows as the order ages); the working
+  // order itself (period 0, FASTEMBEDR_HIP_LG_ORDER_PERIOD) is far from
+  // spatial late in the run (spread 109 us instead of 36).
+  int lg_order_period = 32;
   bool lg_order_stale = true;
   bool lg_order_due = false;
   int lg_order_age = 0;
@@ -582,11 +592,14 @@ bool enqueue_attract(fastembedr_hip_tsne* s, const float2* y_cur, float exaggera
   const int helper =
       share && !s->attract_main && s->attract_helper_per_cu > 0.0 ? per_xcd_for(s, s->attract_helper_per_cu) : 0;
   if (helper == 0) {
+    // the launch completes `done` itself (no marker behind the kernel)
     return s->timed(
         fehip::kKAttract, "attract launch",
         [&] {
-          return then_done(
-              fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->xcds, slots, 0, st));
+          return s->mark_layout
+                     ? fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->xcds, slots, 0, st, done)
+                     : then_done(
+                           fehip::launch_attract_tiled(s->tiles, y_cur, s->attr, exaggeration, s->xcds, slots, 0, st));
         },
         st);
   }
@@ -638,23 +651,21 @@ bool ensure_interp(fastembedr_hip_tsne* s) {
   std::size_t sort_bytes = 0;
   if (!hip_ok(fehip::interp_order_temp_bytes(s->n, sort_bytes), "interp order size query")) return false;
   constexpr std::size_t kSums = fehip::kLgSumsPerBox;
-  const std::size_t wins = static_cast<std::size_t>(fehip::lg_spread_blocks(s->n));
   const std::size_t boxes = static_cast<std::size_t>(fehip::kLgMaxBoxes) * fehip::kLgMaxBoxes;
-  const std::size_t bytes = align_up(4 * mn * mn * 4) + align_up(mn * mn * sizeof(float4)) +
+  const std::size_t bytes = align_up(mn * mn * sizeof(float)) + align_up(mn * mn * sizeof(float4)) +
                             2 * align_up(2 * hmax * hmax * sizeof(float2)) +
                             2 * align_up(3 * gmax * hmax * sizeof(float2)) +
                             align_up(fehip::kLgZPartials * sizeof(double)) + 2 * align_up(n * sizeof(int)) +
                             align_up(2 * n * sizeof(unsigned int)) + align_up(sort_bytes) +
-                            align_up(wins * fehip::kLgTable * kSums * sizeof(float)) + align_up(boxes * sizeof(int)) +
-                            align_up(boxes * fehip::kLgSlots * sizeof(int)) + align_up(boxes * kSums * sizeof(float)) +
-                            4096;
+                            align_up(static_cast<std::size_t>(fehip::kLgEntryPool) * kSums * sizeof(float)) +
+                            align_up(boxes * sizeof(int)) + align_up(boxes * kSums * sizeof(float)) + 4096;
   if (!memory_preflight(bytes, "HIP openTSNE interpolation grid") ||
       !s->lg_arena.init(bytes, "hipMalloc(HIP openTSNE interpolation grid)")) {
     return false;
   }
   Arena& a = s->lg_arena;
   fehip::InterpBuffers& ib = s->ib;
-  ib.charge = a.take<float>(4 * mn * mn);
+  ib.m2 = a.take<float>(mn * mn);
   ib.field = a.take<float4>(mn * mn);
   ib.k_rows = a.take<float2>(2 * hmax * hmax);
   ib.k_cols = a.take<float2>(2 * hmax * hmax);
@@ -666,9 +677,8 @@ bool ensure_interp(fastembedr_hip_tsne* s) {
   ib.order_keys = a.take<unsigned int>(2 * n);
   ib.order_temp = a.take<unsigned char>(std::max<std::size_t>(sort_bytes, 1));
   ib.order_temp_bytes = sort_bytes;
-  ib.tables = a.take<float>(wins * fehip::kLgTable * kSums);
+  ib.entries = a.take<float>(static_cast<std::size_t>(fehip::kLgEntryPool) * kSums);
   ib.box_count = a.take<int>(boxes);
-  ib.box_list = a.take<int>(boxes * fehip::kLgSlots);
   ib.straggler = a.take<float>(boxes * kSums);
   s->lg_order_stale = true;
   if (ib.straggler == nullptr) {
@@ -723,6 +733,7 @@ bool write_interp_spec(fastembedr_hip_tsne* s, int order) {
 // Hands the latest update back to the main stream (`stream` waits for
 // `home`), for work that is enqueued there.
 bool settle(fastembedr_hip_tsne* s) {
+  s->layout_at_tail = false;
   if (s->home == s->stream) return true;
   if (!hip_ok(hipEventRecord(s->ev_home, s->home), "hipEventRecord(home)") ||
       !hip_ok(hipStreamWaitEvent(s->stream, s->ev_home, 0), "hipStreamWaitEvent(home)")) {
@@ -739,6 +750,8 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   // The attraction's stream: the one that holds the latest update (the other
   // of the pair runs the chain); everything else starts from `stream`.
   if (!(overlap && s->attract_main) && !settle(s)) return false;
+  const bool layout_marked = overlap && s->layout_at_tail;
+  s->layout_at_tail = false;
   hipStream_t main = s->home;
   hipStream_t other = main == s->stream ? s->side_attr : s->stream;
   // Two arrangements of an overlapped iteration.  Attraction first
@@ -757,7 +770,7 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   // layout (no centring) and starts at once, beside the statistics' finish
   // and the whole repulsion chain.
   if (overlap && !swap &&
-      (!hip_ok(hipEventRecord(s->ev_layout, main), "hipEventRecord(layout)") ||
+      ((!layout_marked && !hip_ok(hipEventRecord(s->ev_layout, main), "hipEventRecord(layout)")) ||
        !hip_ok(hipStreamWaitEvent(sa, s->ev_layout, 0), "hipStreamWaitEvent(attraction)"))) {
     return false;
   }
@@ -770,7 +783,7 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   // (config 2, late window: 3298 -> 3392 it/s).
   const bool fin_chain = swap;
   hipStream_t fin = fin_chain ? chain : main;
-  if (fin_chain && (!hip_ok(hipEventRecord(s->ev_layout, main), "hipEventRecord(layout)") ||
+  if (fin_chain && ((!layout_marked && !hip_ok(hipEventRecord(s->ev_layout, main), "hipEventRecord(layout)")) ||
                !hip_ok(hipStreamWaitEvent(chain, s->ev_layout, 0), "hipStreamWaitEvent(chain)"))) {
     return false;
   }
@@ -826,7 +839,7 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
       // a spatial one keeps the spread's runs of one box long)
       if (!s->timed(
               fehip::kKLgOrder, "interp order launch",
-              [&] { return fehip::launch_interp_order(s->y_a(), s->sc, ib, n, chain); }, chain)) {
+              [&] { return fehip::launch_interp_order(s->y_a(), s->sc, ib, n, fft_len, chain); }, chain)) {
         return false;
       }
       s->lg_order_due = false;
@@ -835,7 +848,11 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
     }
     ok = s->timed(
              fehip::kKLgSpread, "interp spread launch",
-             [&] { return fehip::launch_interp_spread(s->y_a(), s->sc, ib, n, fft_len, chain); }, chain) &&
+             [&] {
+               return fehip::launch_interp_spread(s->y_a(), s->lg_order_period > 0 ? ib.order : nullptr, s->sc, ib,
+                                                  n, fft_len, chain);
+             },
+             chain) &&
          s->timed(
              fehip::kKLgChargeRows, "interp charge_rows launch",
              [&] { return fehip::launch_interp_fft(3, fft_len, ib, s->sc, s->tw, n, chain); }, chain);
@@ -895,16 +912,24 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
 // by the caller, so that the next attraction can start beside that finish.
 bool enqueue_iteration(fastembedr_hip_tsne* s, bool lg, int fft_len, const fehip::UpdateParams& up, bool overlap,
                        bool finalize) {
-  return enqueue_gradient_pieces(s, lg, fft_len, up.exaggeration, overlap, finalize) &&
-         s->timed(
-             fehip::kKUpdate, "update launch",
-             [&] {
-               // the interpolation grid's update centres the stored layout itself
-               return fehip::launch_update(fehip::kModeUpdate, lg ? s->y_a() : s->y_b, s->attr, s->y_a(),
-                                           s->update(), s->gains(), nullptr, nullptr, s->gb, up, s->partial, s->sc,
-                                           s->n, s->home, lg ? s->ib.field : nullptr);
-             },
-             s->home);
+  // An overlapped iteration's update completes ev_layout itself: the next
+  // iteration's chain waits for it, and its attraction follows the update on
+  // the same stream with no marker between them.
+  const bool mark = overlap && s->mark_layout;
+  if (!enqueue_gradient_pieces(s, lg, fft_len, up.exaggeration, overlap, finalize) ||
+      !s->timed(
+          fehip::kKUpdate, "update launch",
+          [&] {
+            // the interpolation grid's update centres the stored layout itself
+            return fehip::launch_update(fehip::kModeUpdate, lg ? s->y_a() : s->y_b, s->attr, s->y_a(), s->update(),
+                                        s->gains(), nullptr, nullptr, s->gb, up, s->partial, s->sc, s->n, s->home,
+                                        lg ? s->ib.field : nullptr, mark ? s->ev_layout : nullptr);
+          },
+          s->home)) {
+    return false;
+  }
+  s->layout_at_tail = mark;
+  return true;
 }
 
 // Captures enqueue_iteration() on the main stream alone (no side branches,
@@ -1164,14 +1189,15 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   s->n = n;
   s->k = k;
   const int g = resolve_grid_size(n, grid_size);
+  const unsigned ev_flags = hipEventDisableTiming;
   if (!hip_ok(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate") ||
       !hip_ok(hipStreamCreateWithFlags(&s->side_attr, hipStreamNonBlocking), "hipStreamCreate") ||
       !hip_ok(hipStreamCreateWithFlags(&s->side_kern, hipStreamNonBlocking), "hipStreamCreate") ||
-      !hip_ok(hipEventCreateWithFlags(&s->ev_layout, hipEventDisableTiming), "hipEventCreate") ||
-      !hip_ok(hipEventCreateWithFlags(&s->ev_ready, hipEventDisableTiming), "hipEventCreate") ||
-      !hip_ok(hipEventCreateWithFlags(&s->ev_attr, hipEventDisableTiming), "hipEventCreate") ||
-      !hip_ok(hipEventCreateWithFlags(&s->ev_kern, hipEventDisableTiming), "hipEventCreate") ||
-      !hip_ok(hipEventCreateWithFlags(&s->ev_home, hipEventDisableTiming), "hipEventCreate")) {
+      !hip_ok(hipEventCreateWithFlags(&s->ev_layout, ev_flags), "hipEventCreate") ||
+      !hip_ok(hipEventCreateWithFlags(&s->ev_ready, ev_flags), "hipEventCreate") ||
+      !hip_ok(hipEventCreateWithFlags(&s->ev_attr, ev_flags), "hipEventCreate") ||
+      !hip_ok(hipEventCreateWithFlags(&s->ev_kern, ev_flags), "hipEventCreate") ||
+      !hip_ok(hipEventCreateWithFlags(&s->ev_home, ev_flags), "hipEventCreate")) {
     delete s;
     return 1;
   }
@@ -1418,6 +1444,8 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   }
   if (const char* v = std::getenv("FASTEMBEDR_HIP_ATTRACT_MAIN")) s->attract_main = std::strcmp(v, "0") != 0;
   if (const char* v = std::getenv("FASTEMBEDR_HIP_UPDATE_ON_CHAIN")) s->update_on_chain = std::strcmp(v, "0") != 0;
+  if (const char* v = std::getenv("FASTEMBEDR_HIP_MARK_LAYOUT")) s->mark_layout = std::strcmp(v, "0") != 0;
+  if (const char* v = std::getenv("FASTEMBEDR_HIP_LG_ORDER_PERIOD")) s->lg_order_period = std::max(0, std::atoi(v));
   s->graph_capture = graph_capture_enabled();
   if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {
     delete s;
@@ -1797,7 +1825,9 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
       const int nodes = static_cast<int>(std::min<long long>(bound * fehip::kLgOrder, fehip::kLgMaxNodes));
       fft_len = interp_fft_len(nodes);
     }
-    if (lg) s->lg_order_due = s->lg_order_stale || s->lg_order_age >= fastembedr_hip_tsne::kLgOrderPeriod;
+    if (lg) {
+      s->lg_order_due = s->lg_order_period > 0 && (s->lg_order_stale || s->lg_order_age >= s->lg_order_period);
+    }
     // Timing every kernel (mode 1) runs the pieces in sequence, so that each
     // duration is the kernel's alone; timed runs are never replayed graphs.
     const bool overlap = !(s->timing && s->timed_only < 0);

@@ -40,17 +40,18 @@
 //                         sorted by the Morton code of their position
 //   k_lg_spread           per workgroup, 1024 consecutive points of the
 //                         spread order: each point centred and located, its
-//                         9 nodes x 4 moments summed over the runs of one box
-//                         among a wave's 64 consecutive points (DPP segmented
-//                         scan), each run's sums added into the box's slot of
-//                         an LDS table keyed by box, the occupied slots stored
-//                         to scratch and entered in their boxes' lists
-//   k_lg_gather           every node written once: the sum over its box's
-//                         listed slots (and the rare straggler atomics)
+//                         21 power sums (below) summed over the runs of one
+//                         box among a wave's 64 consecutive points (DPP
+//                         segmented scan), each run's sums added into the
+//                         box's slot of an LDS table keyed by box, each
+//                         occupied slot stored to the next entry of its box
 //   k_lg_kernel_rows/cols spectra of K, K1 (real, even) and Kv (imaginary,
 //                         odd in its own axis), a quadrant each, two real
 //                         sequences per complex transform
-//   k_lg_charge_rows      m0 + i m1x and m1y per complex row transform, half
+//   k_lg_charge_rows      one workgroup per row of boxes: each box's entries
+//                         (and the rare straggler sums) summed, combined into
+//                         its 9 nodes x 4 moments (m2 stored), then
+//                         m0 + i m1x and m1y per complex row transform, half
 //                         spectra kept
 //   k_lg_conv_cols        forward column transforms, spectral products for
 //                         phi0, xi_x, xi_y and the spectral sums of Z, inverse
@@ -84,7 +85,6 @@ namespace {
 constexpr int kLgThreads = 256;
 // partial-sum slots: three per convolution-pass block, then one per row block
 constexpr int kLgMaxSpecBlocks = kLgMaxColBlocks;
-constexpr int kLgMoments = 4 * kLgOrder * kLgOrder;  // 9 nodes x (m0, m1x, m1y, m2) per box
 
 // Node moments of a box as polynomials.  With v = u - 1/2 a point's offset
 // from the box centre (in box widths, |v| <= 1/2), node c sits at
@@ -136,11 +136,35 @@ constexpr LgPolyTable lg_poly_table() {
       for (int i = 0; i < 5; ++i) t.k[kind][c][i] = static_cast<float>(lg_node_poly(kind, c).k[i]);
   return t;
 }
-__constant__ LgPolyTable kLgPolys = lg_poly_table();
 static_assert(lg_poly_table().k[0][1][0] == 1.0f && lg_poly_table().k[0][1][2] == -9.0f &&
                   lg_poly_table().k[0][0][1] == -1.5f && lg_poly_table().k[0][2][2] == 4.5f &&
                   lg_poly_table().k[2][1][4] == -81.0f && lg_poly_table().k[1][0][3] == 13.5f,
               "Lagrange weights on the nodes (c - 1) / 3: L_0 = 4.5 v^2 - 1.5 v, L_1 = 1 - 9 v^2");
+
+// kLgCoef.k[r][c][t][s]: the coefficient of power sum s in moment t (m0, m1x,
+// m1y, m2) of node (r, c), from the polynomials above (exact in fp32: the
+// products of 1.5, 3, 4.5, 9, 13.5, 27, 40.5 and 81).
+struct LgCoefTable {
+  float k[kLgOrder][kLgOrder][4][kLgSums];
+};
+constexpr LgCoefTable lg_coef_table() {
+  LgCoefTable t{};
+  for (int r = 0; r < kLgOrder; ++r)
+    for (int c = 0; c < kLgOrder; ++c)
+      for (int mo = 0; mo < 4; ++mo)
+        for (int i = 0; i < 5; ++i)
+          for (int j = 0; j < 5; ++j) {
+            if (!lg_sum_exists(i, j)) continue;
+            // (y polynomial, x polynomial) kinds: m0 (A, A), m1x (A, B),
+            // m1y (B, A), m2 (A, D) + (D, A)
+            const int ky = mo == 2 ? 1 : 0, kx = mo == 1 ? 1 : (mo == 3 ? 2 : 0);
+            double v = lg_node_poly(ky, r).k[i] * lg_node_poly(kx, c).k[j];
+            if (mo == 3) v += lg_node_poly(2, r).k[i] * lg_node_poly(0, c).k[j];
+            t.k[r][c][mo][lg_sum_index(i, j)] = static_cast<float>(v);
+          }
+  return t;
+}
+__constant__ LgCoefTable kLgCoef = lg_coef_table();
 
 // The 21 power sums one point contributes.
 __device__ __forceinline__ void lg_power_sums(const LgPoint& b, float (&s)[kLgSums]) {
@@ -252,20 +276,22 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_order_keys(const float2* __re
 // other points of its box among the wave's 64 consecutive points (an
 // inclusive segmented scan over runs of one box, lg_seg_scan), and the last
 // lane of each run finds its box's slot (atomicCAS on the slot's key) and adds
-// the run's sums into it (LDS float atomics).  The occupied slots go to the
-// workgroup's scratch with plain stores, and each is entered in its box's
-// list (kLgSlots entries; an integer atomic on the box's count).  k_lg_gather
-// then writes every node of the charge planes once: the box's listed slots
-// summed and combined into its 9 nodes x 4 moments.  Float atomics in global
-// memory (device scope: across the XCDs' L2s they resolve beyond L2, at a
-// few ns each) are left for the rare exceptions, which go to a straggler
-// array of power sums per box that the gather adds and clears: a run whose
-// chunk already fills its table (more than kLgTable boxes in kLgChunk points)
-// and a box listed by more than kLgSlots workgroups.  Any permutation gives
+// the run's sums into it (LDS float atomics).  Each occupied slot then takes
+// the next of its box's entries (an integer atomic on the box's count; K
+// entries per box, K = min(kLgMaxPerBox, kLgEntryPool / boxes), so that few
+// boxes get many) and stores its sums there with plain stores.  The charge
+// row transform (k_lg_charge_rows, one workgroup per row of boxes) then sums
+// each box's entries and combines them into its 9 nodes x 4 moments.  Float
+// atomics in global memory (they resolve beyond the XCDs' L2s and cost far
+// more than the LDS path) are left for the rare exceptions, which go to a
+// straggler array of power sums per box that the row transform adds and
+// clears (only for boxes flagged in their count word): a run whose chunk
+// already fills its table (more than kLgTable boxes in kLgChunk points) and a
+// box with more than K contributing workgroups.  Any permutation gives
 // the same charges up to the order of the fp32 adds; a spatial one keeps runs
 // long and tables sparse.  A grid the FFT length cannot hold (2 m > fft_len,
-// excluded by the host's bound) raises kErrInterpGrid; both kernels then
-// write nothing.
+// excluded by the host's bound) raises kErrInterpGrid; the spread and the
+// row transform then write nothing.
 constexpr int kLgSteps = 4;                        // 64-point steps per wave
 constexpr int kLgChunk = kLgThreads * kLgSteps;    // points per workgroup
 static_assert(kLgChunk == kLgSpreadChunk, "the host sizes the spread's scratch by kLgSpreadChunk");
@@ -277,14 +303,19 @@ static_assert(kLgSums == kLgSumsPerBox, "the host sizes the sums by kLgSumsPerBo
 constexpr int kLgStraggled = 1 << 30;
 constexpr int kLgCountMask = kLgStraggled - 1;
 
+// Entries per box at nb boxes per axis (the spread and the gather agree).
+__device__ __forceinline__ int lg_entries_per_box(int nb) {
+  return max(1, min(kLgMaxPerBox, static_cast<int>(kLgEntryPool / (static_cast<long long>(nb) * nb))));
+}
+
 __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restrict__ y_stored,
                                                           const int* __restrict__ order, DeviceScalars* sc, int n,
-                                                          int max_nodes, float* __restrict__ table_out,
-                                                          int* __restrict__ box_count, int* __restrict__ box_list,
-                                                          float* __restrict__ straggler) {
+                                                          int max_nodes, float* __restrict__ entries,
+                                                          int* __restrict__ box_count, float* __restrict__ straggler) {
 #pragma clang fp contract(off)
   chain_priority();
   __shared__ int tkey[kLgTable];                // box of each slot, -1: free
+  __shared__ int tdst[kLgTable];                // the slot's entry, -1: none
   __shared__ float tval[kLgTable * kLgSums];    // the slots' sums
   const DeviceScalars s = *sc;
   const int m = s.lg_nodes;
@@ -305,7 +336,7 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
     float a[kLgSums];
     int key = -1;  // past the end: a run of its own, never added
     if (i < n) {
-      const float2 r = y_stored[order[i]];
+      const float2 r = y_stored[order != nullptr ? order[i] : static_cast<int>(i)];
       const LgPoint b = lg_locate(r.x - s.shift_x, r.y - s.shift_y, s);
       key = b.by * nb + b.bx;
       lg_power_sums(b, a);
@@ -342,16 +373,16 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
     }
   }
   __syncthreads();
-  // occupied slots: listed in their box (beyond kLgSlots: added as
-  // stragglers), then stored to the workgroup's scratch
+  // occupied slots: each takes an entry of its box (beyond K: added as
+  // stragglers), then the sums are stored, slot by slot
   const int t = threadIdx.x;
   const int gb = tkey[t];
-  bool listed = false;
+  int dst = -1;
   if (gb >= 0) {
+    const int per = lg_entries_per_box(nb);
     const int k = atomicAdd(box_count + gb, 1) & kLgCountMask;
-    if (k < kLgSlots) {
-      box_list[static_cast<std::size_t>(gb) * kLgSlots + k] = static_cast<int>(blockIdx.x) * kLgTable + t;
-      listed = true;
+    if (k < per) {
+      dst = gb * per + k;
     } else {
 #pragma unroll
       for (int e = 0; e < kLgSums; ++e) {
@@ -360,93 +391,12 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
       atomicOr(box_count + gb, kLgStraggled);
     }
   }
-  if (!listed) tkey[t] = -1;
+  tdst[t] = dst;
   __syncthreads();
-  float* out = table_out + static_cast<std::size_t>(blockIdx.x) * kLgTable * kLgSums;
-  for (int e = threadIdx.x; e < kLgTable * kLgSums; e += kLgThreads) {
-    if (tkey[e / kLgSums] >= 0) out[e] = tval[e];
-  }
-}
-
-// Every node of the m x m charge planes: a box's listed slots (at most
-// kLgSlots, in list order) and, when flagged, its straggler sums (then
-// cleared) are summed into its 21 power sums, which are combined into its 9
-// nodes x 4 moments; each box's count is cleared once its slots are read.  A
-// workgroup takes kLgGatherBoxes boxes: first each thread sums power sums of
-// the boxes (box, sum) by stride, then each thread writes node moments
-// (box, moment) by stride.
-constexpr int kLgGatherBoxes = 32;
-
-__global__ __launch_bounds__(kLgThreads) void k_lg_gather(const DeviceScalars* sc, int max_nodes,
-                                                          const float* __restrict__ table_out,
-                                                          int* __restrict__ box_count,
-                                                          const int* __restrict__ box_list,
-                                                          float* __restrict__ straggler, float* __restrict__ charge) {
-#pragma clang fp contract(off)
-  chain_priority();
-  __shared__ float ps[kLgGatherBoxes][kLgSums];
-  __shared__ int counts[kLgGatherBoxes];
-  const int m = sc->lg_nodes;
-  if (m > max_nodes) return;  // flagged by the spread
-  const int nb = sc->lg_boxes;
-  const long long mm = static_cast<long long>(m) * m;
-  const int boxes = nb * nb;
-  for (int b0 = blockIdx.x * kLgGatherBoxes; b0 < boxes; b0 += gridDim.x * kLgGatherBoxes) {
-    if (threadIdx.x < kLgGatherBoxes) {
-      const int b = b0 + static_cast<int>(threadIdx.x);
-      counts[threadIdx.x] = b < boxes ? box_count[b] : 0;
-    }
-    __syncthreads();
-    for (int q = threadIdx.x; q < kLgGatherBoxes * kLgSums; q += kLgThreads) {
-      const int sub = q / kLgSums;
-      const int e = q - sub * kLgSums;
-      const int b = b0 + sub;
-      if (b >= boxes) continue;
-      const int word = counts[sub];
-      const int cnt = min(word & kLgCountMask, kLgSlots);
-      float sum = 0.0f;
-      if ((word & kLgStraggled) != 0) {
-        const std::size_t at = static_cast<std::size_t>(b) * kLgSums + e;
-        sum = straggler[at];
-        straggler[at] = 0.0f;
-      }
-      for (int k = 0; k < cnt; ++k) {
-        sum += table_out[static_cast<std::size_t>(box_list[static_cast<std::size_t>(b) * kLgSlots + k]) * kLgSums + e];
-      }
-      ps[sub][e] = sum;
-    }
-    __syncthreads();  // every count and slot of the block's boxes read
-    if (threadIdx.x < kLgGatherBoxes) {
-      const int b = b0 + static_cast<int>(threadIdx.x);
-      if (b < boxes && counts[threadIdx.x] != 0) box_count[b] = 0;
-    }
-    for (int q = threadIdx.x; q < kLgGatherBoxes * kLgMoments; q += kLgThreads) {
-      const int sub = q / kLgMoments;
-      const int v = q - sub * kLgMoments;
-      const int b = b0 + sub;
-      if (b >= boxes) continue;
-      const int node = v / 4, t = v % 4;
-      const int r = node / kLgOrder, c = node % kLgOrder;
-      // (y polynomial, x polynomial) kinds: m0 (A, A), m1x (A, B),
-      // m1y (B, A), m2 (A, D) + (D, A)
-      const int ky0 = t == 2 ? 1 : 0, kx0 = t == 1 ? 1 : (t == 3 ? 2 : 0);
-      float val = 0.0f;
-#pragma unroll
-      for (int term = 0; term < 2; ++term) {
-        if (term == 1 && t != 3) break;
-        const int ky = term == 0 ? ky0 : 2, kx = term == 0 ? kx0 : 0;
-#pragma unroll
-        for (int i = 0; i < 5; ++i) {
-#pragma unroll
-          for (int j = 0; j < 5; ++j) {
-            if (lg_sum_exists(i, j)) val += (kLgPolys.k[ky][r][i] * kLgPolys.k[kx][c][j]) * ps[sub][lg_sum_index(i, j)];
-          }
-        }
-      }
-      const int bx = b % nb, by = b / nb;
-      charge[t * mm + static_cast<long long>(by * kLgOrder + r) * m + bx * kLgOrder + c] = val;
-    }
-    __syncthreads();  // ps and counts reused by the next boxes
+  for (int q = threadIdx.x; q < kLgTable * kLgSums; q += kLgThreads) {
+    const int slot = q / kLgSums;
+    const int d = tdst[slot];
+    if (d >= 0) entries[static_cast<std::size_t>(d) * kLgSums + (q - slot * kLgSums)] = tval[q];
   }
 }
 
@@ -581,53 +531,104 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_cols(const DeviceS
   }
 }
 
-// Row transforms of the charge planes: A = m0 + i m1x and B = m1y per row
-// y < m (zero-padded to F); A is separated with the Hermitian mirror,
-// X[k] = (A[k] + conj A[-k]) / 2 and Y[k] = (A[k] - conj A[-k]) / 2i; B is
-// the spectrum of a real row already.  Kept for kx in [0, F/2], row-major
-// (row stride F/2 + 1), planes plane_stride apart.
+// Row transforms of the charges, one workgroup per row of boxes (by < nb):
+// the row's boxes' entries (at most K per box) and, when flagged, straggler
+// sums (then cleared, with the counts) are summed into each box's 21 power
+// sums, which give the node moments of the box row's kLgOrder node rows
+// (kLgCoef); m2 goes to its plane for the inverse pass, and A = m0 + i m1x
+// and B = m1y per node row (zero-padded to F) are transformed, one node row
+// at a time.  A is separated with the Hermitian mirror, X[k] = (A[k] + conj
+// A[-k]) / 2 and Y[k] = (A[k] - conj A[-k]) / 2i; B is the spectrum of a real
+// row already.  Kept for kx in [0, F/2], row-major (row stride F/2 + 1),
+// planes `plane` apart.  Each box is read by exactly one workgroup, so its
+// count and stragglers are cleared here for the next iteration's spread.
 template <int F>
-__global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceScalars* sc,
-                                                                   const float* __restrict__ charge,
+__global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceScalars* sc, int max_nodes,
+                                                                   const float* __restrict__ entries,
+                                                                   int* __restrict__ box_count,
+                                                                   float* __restrict__ straggler,
+                                                                   float* __restrict__ m2,
                                                                    const float2* __restrict__ tw,
                                                                    float2* __restrict__ rows, long long plane) {
+#pragma clang fp contract(off)
   chain_priority();
   using S = LgShape<F>;
-  __shared__ float2 lds[2 * S::CR * F];
+  // one node row per transform batch: the workgroup needs little LDS (29 KB
+  // at F = 768), so it finds room on CUs that hold the attraction's
+  // workgroups (49 KB each, two or three per CU) when the two overlap
+  constexpr int RG = 1;
+  constexpr int NB = F / 2 / kLgOrder;          // boxes per axis this length holds
+  __shared__ float2 lds[2 * RG * F];
   __shared__ float2 tws[F];
+  __shared__ float ps[NB * kLgSums];
   const int m = sc->lg_nodes;
-  const int mm = m * m;
-  const int row0 = blockIdx.x * S::CR;
-  if (row0 >= m) return;
+  if (m > max_nodes) return;  // flagged by the spread
+  const int nb = sc->lg_boxes;
+  const int by = blockIdx.x;
+  if (by >= nb) return;
   stage_twiddles<F, S::NT>(tws, tw);
-  for (int e = threadIdx.x; e < S::CR * F; e += S::NT) {
-    const int r = e / F;
-    const int x = e - r * F;
-    const int y = row0 + r;
-    float2 a = make_float2(0.0f, 0.0f), b = a;
-    if (y < m && x < m) {
-      const int at = y * m + x;
-      a = make_float2(charge[at], charge[mm + at]);
-      b = make_float2(charge[2 * mm + at], 0.0f);
+  const int per = lg_entries_per_box(nb);
+  for (int q = threadIdx.x; q < nb * kLgSums; q += S::NT) {
+    const int bx = q / kLgSums;
+    const int e = q - bx * kLgSums;
+    const int b = by * nb + bx;
+    const int word = box_count[b];
+    const int cnt = min(word & kLgCountMask, per);
+    float sum = 0.0f;
+    if ((word & kLgStraggled) != 0) {
+      const std::size_t at = static_cast<std::size_t>(b) * kLgSums + e;
+      sum = straggler[at];
+      straggler[at] = 0.0f;
     }
-    lds[(2 * r) * F + x] = a;
-    lds[(2 * r + 1) * F + x] = b;
+    const float* src = entries + static_cast<std::size_t>(b) * per * kLgSums + e;
+    for (int k = 0; k < cnt; ++k) sum += src[static_cast<std::size_t>(k) * kLgSums];
+    ps[q] = sum;
   }
-  __syncthreads();
-  fft_lds<F, 2 * S::CR, S::NT, false, 1>(lds, tws);
-  for (int e = threadIdx.x; e < S::CR * S::H; e += S::NT) {
-    const int r = e / S::H;
-    const int kx = e - r * S::H;
-    const int y = row0 + r;
-    if (y >= m) continue;
-    const int mk = kx == 0 ? 0 : F - kx;
-    const float2 a = lds[(2 * r) * F + kx];
-    const float2 am = conjf2(lds[(2 * r) * F + mk]);
-    const float2 sa = cadd(a, am), da = csub(a, am);
-    const int at = y * S::H + kx;
-    rows[at] = cscale(sa, 0.5f);
-    rows[plane + at] = make_float2(0.5f * da.y, -0.5f * da.x);
-    rows[2 * plane + at] = lds[(2 * r + 1) * F + kx];
+  __syncthreads();  // every count of the row read
+  for (int bx = threadIdx.x; bx < nb; bx += S::NT) box_count[by * nb + bx] = 0;
+  for (int r0 = 0; r0 < kLgOrder; r0 += RG) {
+    for (int e = threadIdx.x; e < RG * F; e += S::NT) {
+      const int rr = e / F;
+      const int x = e - rr * F;
+      const int r = r0 + rr;
+      float2 a = make_float2(0.0f, 0.0f), b = a;
+      if (x < m) {
+        const int bx = x / kLgOrder;
+        const int c = x - bx * kLgOrder;
+        const float* p = ps + bx * kLgSums;
+        const float* k = kLgCoef.k[r][c][0];
+        float v0 = 0.0f, v1 = 0.0f, v2 = 0.0f, v3 = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kLgSums; ++q) {
+          const float pq = p[q];
+          v0 += k[q] * pq;
+          v1 += k[kLgSums + q] * pq;
+          v2 += k[2 * kLgSums + q] * pq;
+          v3 += k[3 * kLgSums + q] * pq;
+        }
+        a = make_float2(v0, v1);
+        b = make_float2(v2, 0.0f);
+        m2[(by * kLgOrder + r) * m + x] = v3;
+      }
+      lds[(2 * rr) * F + x] = a;
+      lds[(2 * rr + 1) * F + x] = b;
+    }
+    __syncthreads();
+    fft_lds<F, 2 * RG, S::NT, false, 1>(lds, tws);
+    for (int e = threadIdx.x; e < RG * S::H; e += S::NT) {
+      const int rr = e / S::H;
+      const int kx = e - rr * S::H;
+      const int y = by * kLgOrder + r0 + rr;  // < m
+      const int mk = kx == 0 ? 0 : F - kx;
+      const float2 a = lds[(2 * rr) * F + kx];
+      const float2 am = conjf2(lds[(2 * rr) * F + mk]);
+      const float2 sa = cadd(a, am), da = csub(a, am);
+      const int at = y * S::H + kx;
+      rows[at] = cscale(sa, 0.5f);
+      rows[plane + at] = make_float2(0.5f * da.y, -0.5f * da.x);
+      rows[2 * plane + at] = lds[(2 * rr + 1) * F + kx];
+    }
+    __syncthreads();  // lds reused by the next batch
   }
 }
 
@@ -739,7 +740,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
 template <int F>
 __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_inverse_rows(const DeviceScalars* sc,
                                                                     const float2* __restrict__ rows, long long plane,
-                                                                    const float* __restrict__ charge,
+                                                                    const float* __restrict__ m2,
                                                                     const float2* __restrict__ tw,
                                                                     float4* __restrict__ field,
                                                                     double* __restrict__ partial) {
@@ -748,7 +749,6 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_inverse_rows(const Device
   __shared__ float2 lds[2 * S::CR * F];
   __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
-  const int mm = m * m;
   const int row0 = blockIdx.x * S::CR;
   double acc = 0.0;
   if (row0 < m) {  // uniform over the block
@@ -785,7 +785,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_inverse_rows(const Device
       const float vx = lds[(2 * r + 1) * F + x].x * scale;
       const int at = y * m + x;
       field[at] = make_float4(u.x, u.y, vx, 0.0f);
-      acc += static_cast<double>(charge[3 * mm + at]) * static_cast<double>(u.x);
+      acc += static_cast<double>(m2[at]) * static_cast<double>(u.x);
     }
   }
   acc = block_sum<S::NT>(acc);
@@ -821,6 +821,9 @@ __global__ __launch_bounds__(256) void k_lg_finalize_z(const double* __restrict_
   }
 }
 
+// Boxes per axis of a grid of at most fft_len / 2 nodes per axis.
+int lg_boxes_bound(int fft_len) { return std::max(1, std::min(fft_len / 2, kLgMaxNodes) / kLgOrder); }
+
 // Buffers of one FFT length.  Spectra planes are G * H float2 (G = F/2,
 // H = F/2 + 1) apart: A holds the charge row spectra, B the potential row
 // spectra.  The kernel row spectra and the kernel spectrum have a buffer
@@ -844,13 +847,15 @@ hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const 
       k_lg_kernel_cols<F><<<col_launch(kblocks), S::NT, 0, stream>>>(sc, ib.k_rows, tw, ib.k_cols);
       break;
     case 3:
-      k_lg_charge_rows<F><<<rblocks, S::NT, 0, stream>>>(sc, ib.charge, tw, ib.spec_a, plane);
+      k_lg_charge_rows<F><<<F / 2 / kLgOrder, S::NT, 0, stream>>>(sc, lg_boxes_bound(F) * kLgOrder, ib.entries,
+                                                                  ib.box_count, ib.straggler, ib.m2, tw, ib.spec_a,
+                                                                  plane);
       break;
     case 5:
       k_lg_conv_cols<F><<<cblocks, S::NT, 0, stream>>>(sc, ib.spec_a, ib.k_cols, tw, ib.spec_b, plane, spec_part);
       break;
     case 7:
-      k_lg_inverse_rows<F><<<rblocks, S::NT, 0, stream>>>(sc, ib.spec_b, plane, ib.charge, tw, ib.field, row_part);
+      k_lg_inverse_rows<F><<<rblocks, S::NT, 0, stream>>>(sc, ib.spec_b, plane, ib.m2, tw, ib.field, row_part);
       k_lg_finalize_z<<<1, 256, 0, stream>>>(spec_part, cblocks, row_part, rblocks, n, F, sc);
       break;
 
@@ -862,22 +867,12 @@ hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const 
 
 }  // namespace
 
-// Boxes per axis of a grid of at most fft_len / 2 nodes per axis.
-int lg_boxes_bound(int fft_len) { return std::max(1, std::min(fft_len / 2, kLgMaxNodes) / kLgOrder); }
-
-hipError_t launch_interp_spread(const float2* y_stored, DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len,
-                                hipStream_t stream) {
+hipError_t launch_interp_spread(const float2* y_stored, const int* order, DeviceScalars* sc, InterpBuffers& ib, int n,
+                                int fft_len, hipStream_t stream) {
   const int max_nodes = lg_boxes_bound(fft_len) * kLgOrder;
   const int blocks = lg_spread_blocks(n);
-  k_lg_spread<<<blocks, kLgThreads, 0, stream>>>(y_stored, ib.order, sc, n, max_nodes, ib.tables, ib.box_count,
-                                                  ib.box_list, ib.straggler);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  // boxes of the largest grid this FFT length holds, a few per workgroup
-  const int boxes = lg_boxes_bound(fft_len) * lg_boxes_bound(fft_len);
-  const int gblocks = std::max(1, std::min((boxes + kLgGatherBoxes - 1) / kLgGatherBoxes, 8192));
-  k_lg_gather<<<gblocks, kLgThreads, 0, stream>>>(sc, max_nodes, ib.tables, ib.box_count, ib.box_list,
-                                                   ib.straggler, ib.charge);
+  k_lg_spread<<<blocks, kLgThreads, 0, stream>>>(y_stored, order, sc, n, max_nodes, ib.entries, ib.box_count,
+                                                  ib.straggler);
   return hipGetLastError();
 }
 
@@ -895,16 +890,20 @@ hipError_t interp_order_temp_bytes(int n, std::size_t& bytes) {
                                    static_cast<unsigned int>(2 * kLgOrderBits));
 }
 
-hipError_t launch_interp_order(const float2* y_stored, const DeviceScalars* sc, InterpBuffers& ib, int n,
+hipError_t launch_interp_order(const float2* y_stored, const DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len,
                                hipStream_t stream) {
   const int blocks = std::max(1, std::min((n + kLgThreads - 1) / kLgThreads, 4096));
   k_lg_order_keys<<<blocks, kLgThreads, 0, stream>>>(y_stored, sc, ib.order_keys, ib.order_idx, n);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  // the keys' bits: the lattice of the largest grid this FFT length holds
+  // (a grid beyond it raises kErrInterpGrid in the spread, whatever the order)
+  int axis_bits = 1;
+  while ((1 << axis_bits) < kLgOrderSub * lg_boxes_bound(fft_len)) ++axis_bits;
   std::size_t bytes = ib.order_temp_bytes;
-  return rocprim::radix_sort_pairs<LgOrderSortConfig>(ib.order_temp, bytes, ib.order_keys, ib.order_keys + n, ib.order_idx, ib.order,
-                                   static_cast<std::size_t>(n), 0u, static_cast<unsigned int>(2 * kLgOrderBits),
-                                   stream);
+  return rocprim::radix_sort_pairs<LgOrderSortConfig>(ib.order_temp, bytes, ib.order_keys, ib.order_keys + n,
+                                                      ib.order_idx, ib.order, static_cast<std::size_t>(n), 0u,
+                                                      static_cast<unsigned int>(2 * axis_bits), stream);
 }
 
 hipError_t launch_interp_fft(int which, int fft_len, InterpBuffers& ib, DeviceScalars* sc, const float2* tw, int n,

@@ -85,12 +85,13 @@ constexpr int kLgMaxNodes = 2048;
 constexpr int kLgMaxFft = 2 * kLgMaxNodes;
 constexpr int kLgMaxBoxes = kLgMaxNodes / kLgOrder;  // per axis
 // Spreading: a workgroup sums kLgSpreadChunk points of the spread order into
-// an LDS table of kLgTable slots keyed by box; each box lists up to kLgSlots
-// slots.
+// an LDS table of kLgTable slots keyed by box; each box takes the sums of up
+// to K = min(kLgMaxPerBox, kLgEntryPool / boxes) workgroups.
 constexpr int kLgSpreadChunk = 1024;
 constexpr int kLgTableBits = 8;
 constexpr int kLgTable = 1 << kLgTableBits;
-constexpr int kLgSlots = 32;
+constexpr int kLgMaxPerBox = 64;
+constexpr long long kLgEntryPool = 1LL << 20;
 constexpr int kLgSumsPerBox = 21;  // power sums of a box's points (the node moments' ingredients)
 inline int lg_spread_blocks(int n) { return std::max(1, (n + kLgSpreadChunk - 1) / kLgSpreadChunk); }
 // Column passes of the interpolation grid map their blocks to columns XCD by
@@ -157,8 +158,7 @@ struct GridBuffers {
 // count m and the FFT length f vary; planes use row stride m, spectra row
 // stride f / 2 + 1.
 struct InterpBuffers {
-  float* charge = nullptr;     // 4 planes of m*m: node moments m0, m1x, m1y, m2 (offsets in units of h);
-                               // zero between iterations
+  float* m2 = nullptr;         // m*m: node moments m2 (squared offsets in units of h), for the inverse pass
   float4* field = nullptr;     // m*m potentials (phi0, xi_x, xi_y, 0)
   float2* k_rows = nullptr;    // 2 planes of (G+1)^2: kernel row spectra ((K^r, K1^r), (Bx, By)), row-major
   float2* k_cols = nullptr;    // 2 planes of (G+1)^2: the kernel spectrum quadrant ((K^, K1^), (Cx, Cy)),
@@ -166,9 +166,8 @@ struct InterpBuffers {
   float2* spec_a = nullptr;    // 3 planes of G*(G+1): charge row spectra, row-major
   float2* spec_b = nullptr;    // 3 planes of G*(G+1): potential row spectra, row-major
   double* z_partial = nullptr; // kLgZPartials: sums of the normaliser per block
-  float* tables = nullptr;     // lg_spread_blocks(n) x kLgTable slots x kLgSumsPerBox: the spread's per-box sums
-  int* box_count = nullptr;    // boxes of the largest grid: slots listed per box, zero between iterations
-  int* box_list = nullptr;     // boxes x kLgSlots: the listed slots (workgroup * kLgTable + slot)
+  float* entries = nullptr;    // kLgEntryPool x kLgSumsPerBox: workgroups' sums per box (K per box)
+  int* box_count = nullptr;    // boxes of the largest grid: entries taken per box, zero between iterations
   float* straggler = nullptr;  // boxes x kLgSumsPerBox: atomic exceptions, zero between iterations
   int* order = nullptr;        // n: spread order (working indices sorted by position)
   unsigned int* order_keys = nullptr;  // 2n: Morton keys, sorted keys
@@ -224,15 +223,15 @@ hipError_t launch_inverse_rows(GridBuffers& gb, const float2* tw, int n, DeviceS
 // Spreading and the zero-padded convolution at FFT length fft_len (2^a or
 // 3 * 2^a in [64, kLgMaxFft] with fft_len >= 2 * lg_nodes); the node count
 // itself is read on the device.  The spread reads the stored layout in
-// ib.order and adds the node moments to the charge planes, which must be
+// `order` (working indices; nullptr: the working order itself) and adds the node moments to the charge planes, which must be
 // zero (they are after allocation and after every convolution).
-hipError_t launch_interp_spread(const float2* y_stored, DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len,
-                                hipStream_t stream);
+hipError_t launch_interp_spread(const float2* y_stored, const int* order, DeviceScalars* sc, InterpBuffers& ib, int n,
+                                int fft_len, hipStream_t stream);
 // The spread order of the current layout (needs this iteration's geometry):
 // working indices sorted by position.  Any permutation is correct; a spatial
 // one keeps the spread's runs long.
 hipError_t interp_order_temp_bytes(int n, std::size_t& bytes);
-hipError_t launch_interp_order(const float2* y_stored, const DeviceScalars* sc, InterpBuffers& ib, int n,
+hipError_t launch_interp_order(const float2* y_stored, const DeviceScalars* sc, InterpBuffers& ib, int n, int fft_len,
                                hipStream_t stream);
 // which: 0 kernel rows, 2 kernel cols, 3 charge rows, 5 conv cols, 7 inverse
 // rows (+ normaliser); other values are invalid
@@ -255,11 +254,12 @@ hipError_t launch_attract(const Csr& p, const float2* y_cur, float2* attr, float
 // writes per-block statistics of the new layout to `partial` (finished by
 // launch_finalize_stats), the gradient modes write grad_out.  interp_field !=
 // nullptr reads the FIt-SNE interpolation grid instead of the bilinear one
-// (kModeUpdate and kModeGradientGrid).
+// (kModeUpdate and kModeGradientGrid).  done != nullptr is an event that the
+// launch itself completes (the kernel's own completion, no marker behind it).
 hipError_t launch_update(int mode, const float2* y_cur, const float2* attr, float2* y_out, float2* update,
                          float2* gains, float2* grad_out, const float2* exact_rep, const GridBuffers& gb,
                          const UpdateParams& up, BlockStats* partial, DeviceScalars* sc, int n, hipStream_t stream,
-                         const float4* interp_field = nullptr);
+                         const float4* interp_field = nullptr, hipEvent_t done = nullptr);
 // The next iteration's centring and grid geometry from kModeUpdate's
 // statistics (one workgroup).  With box_out != nullptr (device pointer of a
 // ring of kBoxRing slots in pinned coherent host memory) the interpolation
@@ -360,8 +360,9 @@ hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream);
 // per XCD (launch_attract_tiled_helper, same arguments, enqueued later on
 // another stream) shares the claims and must follow.  t.work must be zero
 // (it is after a launch or a launch and its helper); xcds <= kTileMaxXcds.
+// done != nullptr: an event that the launch itself completes.
 hipError_t launch_attract_tiled(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds,
-                                int slots_per_xcd, int helper_per_xcd, hipStream_t stream);
+                                int slots_per_xcd, int helper_per_xcd, hipStream_t stream, hipEvent_t done = nullptr);
 hipError_t launch_attract_tiled_helper(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration,
                                        int xcds, int slots_per_xcd, int helper_per_xcd, hipStream_t stream);
 

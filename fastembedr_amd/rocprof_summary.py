@@ -5,6 +5,13 @@ profiles/ (kernel durations and HBM traffic per dispatch).
     python -m fastembedr_amd.rocprof_summary traffic <fetch_dir> <write_dir> <command> \
         --json profiles/<name>.json [--last N] > profiles/<name>.txt
     python -m fastembedr_amd.rocprof_summary counters <pmc_dir> <command> --names A,B [--last N]
+    python -m fastembedr_amd.rocprof_summary join <kt_dir> <traffic.json> <command> --last N [--skip M]
+
+`join` puts the kernel trace's durations beside the traffic digest's bytes
+per dispatch: GB/s and the fraction of MI355X's 8 TB/s per kernel, over the
+N iterations that end M iterations before the end of the trace (bench.py's
+timed window is the last 20; its breakdown pass, every kernel alone, the 20
+that end 750 before the end).
 
 Counter units: FETCH_SIZE and WRITE_SIZE are read in KiB per dispatch and
 scaled by what the same counter reads for a device-to-device copy of known
@@ -26,11 +33,23 @@ import sys
 _OURS = re.compile(r"fehip::(?:\(anonymous namespace\)::)?(\w+)(<[^()]*>)?")
 
 
+_ROCPRIM = re.compile(r"rocprim::(?:\w+::)*(\w+)")
+HBM_PEAK_GBS = 8000.0
+
+
 def short_name(name: str) -> str:
     m = _OURS.search(name)
     if m:
         return m.group(1) + (m.group(2) or "")
+    m = _ROCPRIM.search(name)
+    if m:
+        return "rocprim:" + m.group(1)
     return name.split("(")[0][:60]
+
+
+def ours(name: str) -> bool:
+    """A kernel this library launches: its own, or a rocPRIM primitive it calls."""
+    return bool(_OURS.search(name)) or "rocprim::" in name
 
 
 def _one(pattern: str) -> str:
@@ -55,26 +74,28 @@ def _stats_rows(kt_dir: str) -> list[tuple[str, int, float, float, float, float]
     return [(r[0], int(r[1]), float(r[2]), float(r[3]), float(r[4]), float(r[5])) for r in con.execute(q)]
 
 
-def _window(rows: list[dict], name_key: str, last: int) -> list[dict]:
-    """The dispatches (in dispatch order) of the last `last` iterations: those
-    enqueued after the update kernel of the iteration before them (one
-    k_update per iteration), so that kernels templated on a size that changes
-    during the run (the FFT lengths) are counted only in the window.  Without
-    enough updates, every dispatch."""
+def _window(rows: list[dict], name_key: str, last: int, skip: int = 0) -> list[dict]:
+    """The dispatches (in dispatch order) of `last` iterations, the last of
+    them `skip` iterations before the end: those enqueued after the update
+    kernel of the iteration before them and up to the window's last update
+    (one k_update per iteration), so that kernels templated on a size that
+    changes during the run (the FFT lengths) are counted only in the window.
+    Without enough updates, every dispatch."""
     ids = [_dispatch_order(r) for r in rows if short_name(r[name_key]).startswith("k_update")]
-    if len(ids) <= last:
+    if len(ids) <= last + skip:
         return rows
-    first = ids[-(last + 1)]
-    return [r for r in rows if _dispatch_order(r) > first]
+    first = ids[-(last + skip + 1)]
+    end = ids[-(skip + 1)]
+    return [r for r in rows if first < _dispatch_order(r) <= end]
 
 
-def _last_rows(kt_dir: str, last: int) -> list[tuple[str, int, float, float, float, float]]:
-    """As _stats_rows, over the last `last` iterations (_window) of the
-    per-dispatch kernel trace (CSV), at most `last` dispatches per kernel."""
+def _last_rows(kt_dir: str, last: int, skip: int = 0) -> list[tuple[str, int, float, float, float, float]]:
+    """As _stats_rows, over `last` iterations (_window) of the per-dispatch
+    kernel trace (CSV), at most `last` dispatches per kernel."""
     per = collections.defaultdict(list)
     rows = list(csv.DictReader(open(_one(f"{kt_dir}/**/*kernel_trace.csv"))))
     rows.sort(key=_dispatch_order)
-    for r in _window(rows, "Kernel_Name", last):
+    for r in _window(rows, "Kernel_Name", last, skip):
         per[r["Kernel_Name"]].append(float(r["End_Timestamp"]) - float(r["Start_Timestamp"]))
     out = []
     for name, durs in per.items():
@@ -87,7 +108,7 @@ def _last_rows(kt_dir: str, last: int) -> list[tuple[str, int, float, float, flo
 def trace(kt_dir: str, last: int = 0) -> list[str]:
     out = [f"{'kernel':34s} {'calls':>6s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s} {'total_ms':>10s}"]
     for name, calls, avg, mn, mx, tot in (_last_rows(kt_dir, last) if last > 0 else _stats_rows(kt_dir)):
-        if not _OURS.search(name):
+        if not ours(name):
             continue
         out.append(f"{short_name(name):34s} {calls:6d} {avg / 1e3:10.2f} {mn / 1e3:10.2f} {mx / 1e3:10.2f} "
                    f"{tot / 1e6:10.2f}")
@@ -114,7 +135,7 @@ def _counter(dir_: str, cname: str, last: int = 0):
         if "copyBuffer" in r["Kernel_Name"] and (calib is None or v > calib):
             calib = v
     for r in _window(rows, "Kernel_Name", last) if last > 0 else rows:
-        if _OURS.search(r["Kernel_Name"]):
+        if ours(r["Kernel_Name"]):
             per[short_name(r["Kernel_Name"])].append(float(r["Counter_Value"]))
     if last > 0:
         per = collections.defaultdict(list, {k: v[-last:] for k, v in per.items()})
@@ -154,6 +175,33 @@ def traffic(fetch_dir: str, write_dir: str, copy_bytes: int, last: int = 0) -> t
     return out, {"fetch_factor": ffac, "write_factor": wfac, "kernels": table}
 
 
+def join(kt_dir: str, digest: dict, last: int, skip: int = 0) -> list[str]:
+    """Per kernel of the window: dispatches, mean duration, bytes per
+    dispatch (digest), GB/s and the fraction of 8 TB/s; then the iteration's
+    totals (time summed over the kernels, which overlap where they run beside
+    each other)."""
+    table = digest.get("kernels", {})
+    out = [f"{'kernel':34s} {'disp':>5s} {'avg_us':>9s} {'MB/disp':>9s} {'GB/s':>8s} {'%peak':>6s} {'us/iter':>8s}"]
+    tot_t = tot_b = 0.0
+    for name, calls, avg, _mn, _mx, tot in _last_rows(kt_dir, last, skip):
+        if not ours(name):
+            continue
+        k = short_name(name)
+        rec = table.get(k)
+        b = rec["fetch_bytes"] + rec["write_bytes"] if rec else None
+        gbs = b / avg if b is not None and avg > 0 else None  # bytes per ns = GB/s
+        tot_t += tot / last
+        if b is not None:
+            tot_b += b * calls / last
+        out.append(f"{k:34s} {calls:5d} {avg / 1e3:9.2f} " + (f"{b / 1e6:9.2f} {gbs:8.0f} {100 * gbs / HBM_PEAK_GBS:6.1f}"
+                                                            if b is not None else f"{'-':>9s} {'-':>8s} {'-':>6s}")
+                   + f" {tot / last / 1e3:8.2f}")
+    out.append(f"{'per iteration (sum)':34s} {'':5s} {'':9s} {tot_b / 1e6:9.2f} "
+               f"{(tot_b / tot_t if tot_t else 0.0):8.0f} {100 * (tot_b / tot_t if tot_t else 0.0) / HBM_PEAK_GBS:6.1f}"
+               f" {tot_t / 1e3:8.2f}")
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="what", required=True)
@@ -174,8 +222,19 @@ def main(argv=None) -> int:
     p.add_argument("command")
     p.add_argument("--names", required=True, help="comma-separated counter names")
     p.add_argument("--last", type=int, default=0, help="average only the last N iterations' dispatches")
+    j = sub.add_parser("join")
+    j.add_argument("kt_dir")
+    j.add_argument("digest", help="traffic digest JSON (the traffic subcommand's --json)")
+    j.add_argument("command")
+    j.add_argument("--last", type=int, required=True, help="iterations in the window")
+    j.add_argument("--skip", type=int, default=0, help="iterations after the window's end")
     a = ap.parse_args(argv)
-    if a.what == "trace":
+    if a.what == "join":
+        with open(a.digest) as fh:
+            dg = json.load(fh)
+        lines = [f"(durations over {a.last} iterations ending {a.skip} before the trace's end; bytes per dispatch "
+                 f"from {a.digest.split('/')[-1]}: {dg.get('command', '')})"] + join(a.kt_dir, dg, a.last, a.skip)
+    elif a.what == "trace":
         lines = trace(a.kt_dir, a.last)
         if a.last:
             lines.insert(0, f"(durations over the last {a.last} iterations, at most {a.last} dispatches per kernel)")
@@ -189,6 +248,8 @@ def main(argv=None) -> int:
             lines.insert(0, f"(mean per dispatch over the last {a.last} iterations, at most {a.last} dispatches per kernel)")
         if a.json:
             table.update(json.loads(a.meta))
+            if a.last:
+                table["window_iterations"] = a.last
             table["command"] = a.command
             with open(a.json, "w") as fh:
                 json.dump(table, fh, indent=1)

@@ -192,16 +192,15 @@ def test_closed_session_returns_memory(hip, capture):
     one-time pools (54 and 40 MiB in a fresh process).  After a close the
     runtime sometimes keeps the closed session's blocks for a while (free
     memory then reads at the in-session level, and the next session's
-    identical requests reuse them), so a single reading may be one
-    session's buffers low; a leak instead lowers every later reading.  The
-    check, over the last five sessions: every reading is within 64 MiB of
-    the highest of them or sits at the in-session level (within 64 MiB of the
-    lowest in-session reading; the runtime has held a closed session's blocks
-    in two of five readings here, alternating with full returns), and the
-    highest is within 64 MiB of the second warm-up session's reading.  A leak
-    lowers the readings step by step, which neither level admits: graphs with
-    parallel branches lost 1.4 GB per session here; a steady leak of more than
-    about 22 MiB per session fails."""
+    identical requests reuse them), so a reading may sit anywhere between
+    the in-session level and a full return (here: two of five readings at the
+    in-session level, alternating with full returns, and once 870 MB of a
+    session's 2.7 GB held); a leak instead lowers every later reading.  The
+    check: the highest of the last three readings is within 64 MiB of the
+    second warm-up session's reading (memory comes back), and no reading
+    after the warm-up falls more than 64 MiB below the in-session level.
+    Graphs with parallel branches lost 1.4 GB per session here; a steady leak
+    of more than about 22 MiB per session fails."""
     n, k = 200_000, 90
     x, _ = synthetic.gaussian_mixture(synthetic.CONFIGS[2], seed=1, n=n)
     knn = hip.exact_knn(np.ascontiguousarray(x, np.float32), k, keep_device=True)
@@ -244,7 +243,6 @@ def test_closed_session_returns_memory(hip, capture):
     footprint = start - during[0]  # one session's buffers
     assert footprint > 256 * 2**20
     slack = 64 * 2**20
-    top, in_session = max(after[2:]), min(during)
-    held = [v for v in after[2:] if top - v > slack]
-    assert all(abs(v - in_session) <= slack for v in held), (after, during)
-    assert top >= after[1] - slack, (after, during)
+    in_session = min(during)
+    assert max(after[-3:]) >= after[1] - slack, (after, during)
+    assert min(after[2:]) >= in_session - slack, (after, during)
