@@ -496,6 +496,9 @@ def bench_transform(args, torch, fe, synthetic) -> int:
                                 f"{geo[1]} nodes ({geo[0]} boxes per axis, 3 points per box, 2 boxes per unit) and "
                                 f"interpolated at each query; at most {geo[2]} query-iterations of a {iters}-iteration call took the exact sums"},
         "whole_call_seconds": round(t_call, 4),
+        # the whole call (upload, device checks, P, initialisation, node
+        # fields, every iteration, download) per iteration
+        "whole_call_iterations_per_s": round(iters / t_call, 1),
         "roofline": {"kernel": "k_transform_run<grid>", "bound": "fp64 VALU", "achieved": round(tflops, 3),
                      "peak": 78.6, "unit": "TFLOP/s", "frac": round(tflops / 78.6, 4), "traffic": None,
                      "algorithmic_flops_per_query_iteration": flops_q},

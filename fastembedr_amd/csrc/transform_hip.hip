@@ -158,6 +158,52 @@ __global__ __launch_bounds__(kQueryThreads) void k_transform_init(const double2*
   y[i] = make_double2(out[0], out[1]);
 }
 
+// Median initialisation (the default) with L lanes per query (k <= L <= 64,
+// L divides the wave): lane a holds neighbour a's coordinates, counts the
+// neighbours below and at them with k shuffles, and the value at rank r is
+// that of a lane with less <= r < leq, as in coordinate_at_rank.
+template <int L>
+__global__ __launch_bounds__(kQueryThreads) void k_transform_init_lanes(const double2* __restrict__ ref,
+                                                                        const int* __restrict__ idx_cm, int nq,
+                                                                        int k, int offset,
+                                                                        double2* __restrict__ y) {
+#pragma clang fp contract(off)
+  static_assert(L >= 2 && L <= 64 && (64 % L) == 0, "groups tile the wave");
+  const long long t = static_cast<long long>(blockIdx.x) * kQueryThreads + threadIdx.x;
+  const int i = static_cast<int>(t / L);
+  const int lane = static_cast<int>(t % L);
+  const bool mine = i < nq && lane < k;
+  double vx = 0.0, vy = 0.0;
+  if (mine) {
+    const double2 r = ref[idx_cm[static_cast<std::size_t>(lane) * nq + i] - offset];
+    vx = r.x;
+    vy = r.y;
+  }
+  int lx = 0, ex = 0, ly = 0, ey = 0;  // neighbours below / at or below, per component
+  for (int b = 0; b < k; ++b) {        // every lane of the wave takes part (k is uniform)
+    const double bx = __shfl(vx, b, L);
+    const double by = __shfl(vy, b, L);
+    lx += bx < vx ? 1 : 0;
+    ex += bx <= vx ? 1 : 0;
+    ly += by < vy ? 1 : 0;
+    ey += by <= vy ? 1 : 0;
+  }
+  const int base = static_cast<int>(threadIdx.x & 63) & ~(L - 1);
+  const unsigned long long group = ~0ull >> (64 - L);
+  auto at_rank = [&](double v, int less, int leq, int r) {
+    const unsigned long long hit = (__ballot(mine && less <= r && r < leq) >> base) & group;
+    return __shfl(v, hit != 0ull ? __ffsll(static_cast<long long>(hit)) - 1 : 0, L);
+  };
+  const int mid = k / 2;
+  double mx = at_rank(vx, lx, ex, mid);
+  double my = at_rank(vy, ly, ey, mid);
+  if ((k & 1) == 0) {
+    mx = 0.5 * (mx + at_rank(vx, lx, ex, mid - 1));
+    my = 0.5 * (my + at_rank(vy, ly, ey, mid - 1));
+  }
+  if (i < nq && lane == 0) y[i] = make_double2(mx, my);
+}
+
 // Repulsion term of one query: sum over the samples of -(q^2 / sum_q) d.
 template <bool EXACT>
 __device__ inline double2 repulsion(const double2* __restrict__ ref, int n_ref, int samples, std::uint32_t state,
@@ -255,36 +301,135 @@ __device__ inline bool grid_repulsion(const double4* __restrict__ field, const G
   return true;
 }
 
-// One node per thread; the reference is staged through LDS in tiles and
-// summed in index order.
+// Node fields.  Each thread sums kFieldRows nodes of one column of the grid
+// over one chunk of the reference, staged through LDS in tiles and summed in
+// index order.  When the nodes alone would leave SIMDs idle (config 3: 552^2
+// nodes, 1,191 waves of 4-node threads for 1,024 SIMDs) the reference is cut
+// into chunks: one grid row of workgroups per chunk writes partial sums, and
+// k_grid_fields_sum adds them in chunk order.  The four nodes of a thread
+// share dx and 1 + dx^2 and one reciprocal (recip4).
 constexpr int kFieldThreads = 256;
-__global__ __launch_bounds__(kFieldThreads) void k_grid_fields(const double2* __restrict__ ref, int n_ref,
-                                                               GridGeo g, double4* __restrict__ field) {
-#pragma clang fp contract(off)
+constexpr int kFieldRows = 4;
+static_assert(kFieldRows % 4 == 0, "recip4 takes the rows four at a time");
+constexpr int kFieldWavesTarget = 16 * 1024;  // ~16 waves per SIMD
+constexpr int kFieldMinChunk = 4 * kFieldThreads;
+
+// q_k = 1 / d_k for four values d_k >= 1 with one reciprocal: r = 1 / p,
+// p = d0 d1 d2 d3, from the hardware estimate and two Newton-Raphson steps
+// r <- r + r (1 - p r) (each squares the relative error), then
+// 1 / d0 = r d1 d2 d3 and so on.  A few units in the last place of the
+// correctly rounded quotient; p stays finite for every d_k below 1e76.
+__device__ inline void recip4(const double* d, double* q) {
+  const double p01 = d[0] * d[1];
+  const double p23 = d[2] * d[3];
+  const double p = p01 * p23;
+  double r = __builtin_amdgcn_rcp(p);
+  r = fma(r, fma(-p, r, 1.0), r);
+  r = fma(r, fma(-p, r, 1.0), r);
+  const double i01 = r * p23;
+  const double i23 = r * p01;
+  q[0] = i01 * d[1];
+  q[1] = i01 * d[0];
+  q[2] = i23 * d[3];
+  q[3] = i23 * d[2];
+}
+
+// Threads take (column, strip of kFieldRows rows) units, columns fastest;
+// blockIdx.y is the reference chunk [y * chunk, (y + 1) * chunk).  With
+// partial == nullptr (one chunk) the fields go straight to `field`, else to
+// partial[(chunk * 3 + t) * m^2 + node], t = Z, Fx, Fy.
+__global__ __launch_bounds__(kFieldThreads) void k_grid_fields(const double2* __restrict__ ref, int n_ref, int chunk,
+                                                               GridGeo g, double4* __restrict__ field,
+                                                               double* __restrict__ partial) {
   __shared__ double2 tile[kFieldThreads];
-  const int nodes = g.m * g.m;
-  const int v = static_cast<int>(blockIdx.x) * kFieldThreads + static_cast<int>(threadIdx.x);
-  const double nx = g.lo + (static_cast<double>(v % g.m) + 0.5) * g.h;
-  const double ny = g.lo + (static_cast<double>(v / g.m) + 0.5) * g.h;
-  double z = 0.0, fx = 0.0, fy = 0.0;
-  for (int base = 0; base < n_ref; base += kFieldThreads) {
+  const int m = g.m;
+  const long long strips = (m + kFieldRows - 1) / kFieldRows;
+  const long long units = static_cast<long long>(m) * strips;
+  const long long u = static_cast<long long>(blockIdx.x) * kFieldThreads + threadIdx.x;
+  const int col = static_cast<int>(u % m);
+  const int strip = static_cast<int>(u / m);
+  const double nx = g.lo + (static_cast<double>(col) + 0.5) * g.h;
+  double ny[kFieldRows];
+#pragma unroll
+  for (int k = 0; k < kFieldRows; ++k) ny[k] = g.lo + (static_cast<double>(strip * kFieldRows + k) + 0.5) * g.h;
+  double z[kFieldRows], fx[kFieldRows], fy[kFieldRows];
+#pragma unroll
+  for (int k = 0; k < kFieldRows; ++k) z[k] = fx[k] = fy[k] = 0.0;
+  const int j0 = static_cast<int>(blockIdx.y) * chunk;
+  const int j1 = min(n_ref, j0 + chunk);
+  for (int base = j0; base < j1; base += kFieldThreads) {
     const int j = base + static_cast<int>(threadIdx.x);
     __syncthreads();
-    if (j < n_ref) tile[threadIdx.x] = ref[j];
+    if (j < j1) tile[threadIdx.x] = ref[j];
     __syncthreads();
-    const int count = min(kFieldThreads, n_ref - base);
+    const int count = min(kFieldThreads, j1 - base);
     for (int t = 0; t < count; ++t) {
       const double2 r = tile[t];
       const double dx = nx - r.x;
-      const double dy = ny - r.y;
-      const double q = 1.0 / (1.0 + dx * dx + dy * dy);
-      const double q2 = q * q;
-      z += q;
-      fx += q2 * dx;
-      fy += q2 * dy;
+      const double d1 = fma(dx, dx, 1.0);
+      double dy[kFieldRows], d[kFieldRows], q[kFieldRows];
+#pragma unroll
+      for (int k = 0; k < kFieldRows; ++k) {
+        dy[k] = ny[k] - r.y;
+        d[k] = fma(dy[k], dy[k], d1);
+      }
+#pragma unroll
+      for (int k = 0; k < kFieldRows; k += 4) recip4(d + k, q + k);
+#pragma unroll
+      for (int k = 0; k < kFieldRows; ++k) {
+        const double q2 = q[k] * q[k];
+        z[k] += q[k];
+        fx[k] = fma(q2, dx, fx[k]);
+        fy[k] = fma(q2, dy[k], fy[k]);
+      }
     }
   }
-  if (v < nodes) field[v] = make_double4(z, fx, fy, 0.0);
+  if (u >= units) return;
+  const std::size_t nodes = static_cast<std::size_t>(m) * static_cast<std::size_t>(m);
+#pragma unroll
+  for (int k = 0; k < kFieldRows; ++k) {
+    const int row = strip * kFieldRows + k;
+    if (row >= m) break;
+    const std::size_t v = static_cast<std::size_t>(row) * static_cast<std::size_t>(m) + static_cast<std::size_t>(col);
+    if (partial == nullptr) {
+      field[v] = make_double4(z[k], fx[k], fy[k], 0.0);
+    } else {
+      double* out = partial + static_cast<std::size_t>(blockIdx.y) * 3 * nodes + v;
+      out[0] = z[k];
+      out[nodes] = fx[k];
+      out[2 * nodes] = fy[k];
+    }
+  }
+}
+
+// The chunks' partial sums added in chunk order.
+__global__ __launch_bounds__(kFieldThreads) void k_grid_fields_sum(const double* __restrict__ partial, int chunks,
+                                                                   long long nodes, double4* __restrict__ field) {
+  const long long v = static_cast<long long>(blockIdx.x) * kFieldThreads + threadIdx.x;
+  if (v >= nodes) return;
+  double z = 0.0, fx = 0.0, fy = 0.0;
+  for (int c = 0; c < chunks; ++c) {
+    const double* in = partial + static_cast<std::size_t>(c) * 3 * static_cast<std::size_t>(nodes) + v;
+    z += in[0];
+    fx += in[nodes];
+    fy += in[2 * nodes];
+  }
+  field[v] = make_double4(z, fx, fy, 0.0);
+}
+
+// Reference chunks of the node fields at m nodes per axis (1: no partial
+// sums) and the chunk length (a multiple of the tile).
+struct FieldSplit {
+  int chunks, chunk;
+};
+FieldSplit field_split(int m, int n_ref) {
+  const long long strips = (m + kFieldRows - 1) / kFieldRows;
+  const long long waves = (static_cast<long long>(m) * strips + 63) / 64;
+  long long c = (kFieldWavesTarget + waves - 1) / waves;
+  c = std::max(1LL, std::min({c, 64LL, static_cast<long long>(n_ref) / kFieldMinChunk}));
+  int chunk = static_cast<int>((n_ref + c - 1) / c);
+  chunk = (chunk + kFieldThreads - 1) / kFieldThreads * kFieldThreads;
+  return FieldSplit{static_cast<int>((n_ref + chunk - 1) / chunk), chunk};
 }
 
 // ---- one query's iteration ----------------------------------------------------
@@ -593,6 +738,31 @@ bool ok(hipError_t e, const char* where) {
 
 int query_blocks(int nq) { return (nq + kQueryThreads - 1) / kQueryThreads; }
 
+// The queries' initialisation (weighted: the inverse-distance mean, else the
+// median): the lane kernel for medians of up to 64 neighbours.
+hipError_t launch_init(const double2* ref, const int* idx, const double* dist, int nq, int k, int offset,
+                       bool weighted, double2* y, hipStream_t st) {
+  const auto lanes = [&](auto tag) {
+    constexpr int L = decltype(tag)::value;
+    const long long threads = static_cast<long long>(nq) * L;
+    k_transform_init_lanes<L><<<static_cast<unsigned int>((threads + kQueryThreads - 1) / kQueryThreads),
+                                kQueryThreads, 0, st>>>(ref, idx, nq, k, offset, y);
+  };
+  if (weighted || k > 64) {
+    k_transform_init<<<query_blocks(nq), kQueryThreads, 0, st>>>(ref, idx, dist, nq, k, offset, weighted ? 1 : 0,
+                                                                 y);
+  } else if (k <= 8) {
+    lanes(std::integral_constant<int, 8>{});
+  } else if (k <= 16) {
+    lanes(std::integral_constant<int, 16>{});
+  } else if (k <= 32) {
+    lanes(std::integral_constant<int, 32>{});
+  } else {
+    lanes(std::integral_constant<int, 64>{});
+  }
+  return hipGetLastError();
+}
+
 
 // 1 when every index is in [1, n_ref] (:1290-1302), else 0.
 int reference_offset(const int* idx_cm, std::size_t count, int n_ref) {
@@ -603,6 +773,103 @@ int reference_offset(const int* idx_cm, std::size_t count, int n_ref) {
   }
   return (lo >= 1 && hi <= n_ref) ? 1 : 0;
 }
+
+// Validation of the KNN input on the device (check_inputs' index and
+// distance checks as one reduction), for the calls whose arrays are on the
+// device already: the allocating calls after their upload, and the
+// allocation-free call.
+struct NaHeader {
+  unsigned int flags;  // kNaBadReference
+  int idx_min;
+  int idx_max;
+  int pad;
+  unsigned long long exact_evals;  // the run kernel's counter (unused by the sampled and exact modes)
+  // First failing entry (column-major position) of each kind, or ULLONG_MAX:
+  // an index outside [0, n_ref) and outside [1, n_ref] (the two offsets the
+  // host may settle on), and a distance that is not finite and >= 0.  The
+  // host reports whichever comes first, as check_inputs' sequential scan does.
+  unsigned long long first_bad_index[2];
+  unsigned long long first_bad_distance;
+};
+constexpr unsigned int kNaBadReference = 2u;
+
+__global__ void k_na_clear(NaHeader* h) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    h->flags = 0u;
+    h->idx_min = INT_MAX;
+    h->idx_max = INT_MIN;
+    h->exact_evals = 0ull;
+    h->first_bad_index[0] = ULLONG_MAX;
+    h->first_bad_index[1] = ULLONG_MAX;
+    h->first_bad_distance = ULLONG_MAX;
+  }
+}
+
+// Index range and distance checks of check_inputs, as a reduction: the host
+// derives the index offset from the smallest and largest index, and the error
+// from the first failing entry of each kind.
+__device__ inline unsigned long long wave_min_u64(unsigned long long v) {
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(v, off);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
+__global__ __launch_bounds__(256) void k_na_check_knn(const int* __restrict__ idx_cm,
+                                                      const double* __restrict__ dist_cm, long long count,
+                                                      int n_ref, NaHeader* h) {
+  int lo = INT_MAX, hi = INT_MIN;
+  unsigned long long bad0 = ULLONG_MAX, bad1 = ULLONG_MAX, badd = ULLONG_MAX;
+  const long long stride = static_cast<long long>(gridDim.x) * 256;
+  // a thread's entries ascend, so its first failure of each kind is its least
+  for (long long c = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; c < count; c += stride) {
+    const int v = idx_cm[c];
+    lo = v < lo ? v : lo;
+    hi = v > hi ? v : hi;
+    const unsigned long long at = static_cast<unsigned long long>(c);
+    if ((v < 0 || v >= n_ref) && bad0 == ULLONG_MAX) bad0 = at;
+    if ((v < 1 || v > n_ref) && bad1 == ULLONG_MAX) bad1 = at;
+    const double d = dist_cm[c];
+    if ((!isfinite(d) || d < 0.0) && badd == ULLONG_MAX) badd = at;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const int olo = __shfl_xor(lo, off);
+    const int ohi = __shfl_xor(hi, off);
+    lo = olo < lo ? olo : lo;
+    hi = ohi > hi ? ohi : hi;
+  }
+  bad0 = wave_min_u64(bad0);
+  bad1 = wave_min_u64(bad1);
+  badd = wave_min_u64(badd);
+  if ((threadIdx.x & 63) == 0) {
+    atomicMin(&h->idx_min, lo);
+    atomicMax(&h->idx_max, hi);
+    if (bad0 != ULLONG_MAX) atomicMin(&h->first_bad_index[0], bad0);
+    if (bad1 != ULLONG_MAX) atomicMin(&h->first_bad_index[1], bad1);
+    if (badd != ULLONG_MAX) atomicMin(&h->first_bad_distance, badd);
+  }
+}
+
+// check_inputs' KNN result from a header filled by k_na_check_knn: the index
+// offset (1-based iff every index is in [1, n_ref], :1290-1302), or -1 after
+// setting the error of the earlier failing entry, as check_inputs' sequential
+// scan reports it (then the reference's finiteness, which it checks last).
+int knn_offset_from(const NaHeader& h, int n_ref) {
+  const int offset = (h.idx_min >= 1 && h.idx_max <= n_ref) ? 1 : 0;
+  const unsigned long long bad_index = h.first_bad_index[offset];
+  if (bad_index != ULLONG_MAX && bad_index <= h.first_bad_distance) {
+    set_last_error("KNN indices are out of range for `reference_layout`.");
+    return -1;
+  }
+  if (h.first_bad_distance != ULLONG_MAX) {
+    set_last_error("KNN distances must be finite and non-negative.");
+    return -1;
+  }
+  return offset;
+}
+
+int knn_check_blocks(long long entries) { return static_cast<int>(std::min<long long>((entries + 255) / 256, 2048)); }
 
 // Device buffers of one call, carved from a single allocation; the grid
 // mode's node fields are a second allocation once the grid size is known.
@@ -616,20 +883,30 @@ struct TransformBuffers {
   double2* y = nullptr;
   double2* grad = nullptr;
   unsigned long long* counter = nullptr;
+  NaHeader* hdr = nullptr;  // the KNN checks' result
   double4* field = nullptr;
   hipStream_t stream = nullptr;
+  hipStream_t side = nullptr;     // P beside the node fields (grid mode)
+  hipEvent_t side_done = nullptr;
   ~TransformBuffers() {
+    if (side != nullptr) (void)hipStreamSynchronize(side);
     if (stream != nullptr) (void)hipStreamSynchronize(stream);
+    if (side_done != nullptr) (void)hipEventDestroy(side_done);
+    if (side != nullptr) (void)hipStreamDestroy(side);
     if (field_base != nullptr) (void)hipFree(field_base);
     if (base != nullptr) (void)hipFree(base);
     if (stream != nullptr) (void)hipStreamDestroy(stream);
+  }
+  bool init_side() {
+    return ok(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "hipStreamCreate(transform side)") &&
+           ok(hipEventCreateWithFlags(&side_done, hipEventDisableTiming), "hipEventCreate(transform side)");
   }
   bool init(int n_ref, int nq, int k) {
     const auto up = [](std::size_t b) { return (b + 255) & ~static_cast<std::size_t>(255); };
     const std::size_t nk = static_cast<std::size_t>(nq) * k;
     const std::size_t yb = up(sizeof(double2) * nq);
     const std::size_t sizes[] = {up(sizeof(double2) * n_ref), up(sizeof(int) * nk), up(sizeof(double) * nk),
-                                 up(sizeof(double) * nk), 2 * yb, 256};
+                                 up(sizeof(double) * nk), 2 * yb, 256, up(sizeof(NaHeader))};
     std::size_t total = 0;
     for (std::size_t s : sizes) total += s;
     if (!ok(hipStreamCreate(&stream), "hipStreamCreate(transform)") ||
@@ -649,12 +926,18 @@ struct TransformBuffers {
     grad = reinterpret_cast<double2*>(c + yb);
     c += sizes[4];
     counter = reinterpret_cast<unsigned long long*>(c);
+    c += sizes[5];
+    hdr = reinterpret_cast<NaHeader*>(c);
     return true;
   }
-  bool init_field(int m) {
-    const std::size_t bytes = sizeof(double4) * static_cast<std::size_t>(m) * static_cast<std::size_t>(m);
-    if (!ok(hipMalloc(&field_base, bytes), "hipMalloc(reference grid)")) return false;
+  double* field_partial = nullptr;  // the node fields' partial sums per reference chunk (null: one chunk)
+  bool init_field(int m, int chunks) {
+    const std::size_t nodes = static_cast<std::size_t>(m) * static_cast<std::size_t>(m);
+    const std::size_t bytes = sizeof(double4) * nodes;
+    const std::size_t extra = chunks > 1 ? sizeof(double) * 3 * nodes * static_cast<std::size_t>(chunks) : 0;
+    if (!ok(hipMalloc(&field_base, bytes + extra), "hipMalloc(reference grid)")) return false;
     field = static_cast<double4*>(field_base);
+    field_partial = chunks > 1 ? reinterpret_cast<double*>(static_cast<char*>(field_base) + bytes) : nullptr;
     return true;
   }
 };
@@ -708,9 +991,21 @@ GridGeo grid_geometry(const double* ref, int n_ref, const double* y, int nq, int
   return g;
 }
 
-hipError_t launch_grid_fields(const double2* ref, int n_ref, const GridGeo& g, double4* field, hipStream_t st) {
-  const int nodes = g.m * g.m;
-  k_grid_fields<<<(nodes + kFieldThreads - 1) / kFieldThreads, kFieldThreads, 0, st>>>(ref, n_ref, g, field);
+// The node fields into b.field (b.init_field(g.m, field_split(g.m, n_ref).chunks) first).
+hipError_t launch_grid_fields(const double2* ref, int n_ref, const GridGeo& g, const TransformBuffers& b,
+                              hipStream_t st) {
+  const FieldSplit fs = field_split(g.m, n_ref);
+  const long long strips = (g.m + kFieldRows - 1) / kFieldRows;
+  const long long units = static_cast<long long>(g.m) * strips;
+  const dim3 grid(static_cast<unsigned int>((units + kFieldThreads - 1) / kFieldThreads),
+                  static_cast<unsigned int>(fs.chunks));
+  double* partial = fs.chunks > 1 ? b.field_partial : nullptr;
+  if (fs.chunks > 1 && partial == nullptr) return hipErrorInvalidValue;
+  k_grid_fields<<<grid, kFieldThreads, 0, st>>>(ref, n_ref, fs.chunk, g, b.field, partial);
+  if (fs.chunks == 1) return hipGetLastError();
+  const long long nodes = static_cast<long long>(g.m) * g.m;
+  k_grid_fields_sum<<<static_cast<unsigned int>((nodes + kFieldThreads - 1) / kFieldThreads), kFieldThreads, 0, st>>>(
+      partial, fs.chunks, nodes, b.field);
   return hipGetLastError();
 }
 
@@ -770,8 +1065,11 @@ hipError_t launch_gradient(int mode, const TransformBuffers& b, int n_ref, int n
 }
 
 // The reference's argument checks (:1880-1921); returns false with the message set.
-bool check_inputs(const double* ref_cm, int n_ref, const int* idx_cm, const double* dist_cm, int nq, int k,
-                  double perplexity, int offset) {
+// check_inputs in three parts: the scalar arguments, the KNN entries in
+// order (index range, distance finite and >= 0; the first failing entry
+// names the error) and the reference's finiteness.
+bool check_scalars(const double* ref_cm, int n_ref, const int* idx_cm, const double* dist_cm, int nq, int k,
+                   double perplexity) {
   if (ref_cm == nullptr || idx_cm == nullptr || dist_cm == nullptr) {
     set_last_error("reference_layout, indices and distances must not be NULL.");
     return false;
@@ -788,6 +1086,22 @@ bool check_inputs(const double* ref_cm, int n_ref, const int* idx_cm, const doub
     set_last_error("`perplexity` must be positive.");
     return false;
   }
+  return true;
+}
+
+bool check_reference_finite(const double* ref_cm, int n_ref) {
+  for (int i = 0; i < 2 * n_ref; ++i) {
+    if (!std::isfinite(ref_cm[i])) {
+      set_last_error("`reference_layout` must be finite.");
+      return false;
+    }
+  }
+  return true;
+}
+
+bool check_inputs(const double* ref_cm, int n_ref, const int* idx_cm, const double* dist_cm, int nq, int k,
+                  double perplexity, int offset) {
+  if (!check_scalars(ref_cm, n_ref, idx_cm, dist_cm, nq, k, perplexity)) return false;
   const std::size_t nk = static_cast<std::size_t>(nq) * k;
   for (std::size_t c = 0; c < nk; ++c) {
     const int r = idx_cm[c] - offset;
@@ -800,13 +1114,31 @@ bool check_inputs(const double* ref_cm, int n_ref, const int* idx_cm, const doub
       return false;
     }
   }
-  for (int i = 0; i < 2 * n_ref; ++i) {
-    if (!std::isfinite(ref_cm[i])) {
-      set_last_error("`reference_layout` must be finite.");
-      return false;
-    }
+  return check_reference_finite(ref_cm, n_ref);
+}
+
+// check_inputs' checks in its order with the KNN entries checked on the
+// device after the upload (one pass instead of a host scan of every entry):
+// the scalars, buffers and upload, the KNN entries, the reference's
+// finiteness.  Returns the index offset, or -1 after setting the error.
+int upload_checked(TransformBuffers& b, const double* ref_cm, int n_ref, const int* idx_cm, const double* dist_cm,
+                   int nq, int k, double perplexity) {
+  if (!check_scalars(ref_cm, n_ref, idx_cm, dist_cm, nq, k, perplexity) || !b.init(n_ref, nq, k) ||
+      !upload(b, ref_cm, n_ref, idx_cm, dist_cm, nq, k)) {
+    return -1;
   }
-  return true;
+  const long long entries = static_cast<long long>(nq) * k;
+  k_na_clear<<<1, 64, 0, b.stream>>>(b.hdr);
+  k_na_check_knn<<<knn_check_blocks(entries), 256, 0, b.stream>>>(b.idx, b.dist, entries, n_ref, b.hdr);
+  NaHeader h{};
+  if (!ok(hipGetLastError(), "transform check launch") ||
+      !ok(hipMemcpyAsync(&h, b.hdr, sizeof(h), hipMemcpyDeviceToHost, b.stream), "transform check download") ||
+      !ok(hipStreamSynchronize(b.stream), "transform check sync")) {
+    return -1;
+  }
+  const int offset = knn_offset_from(h, n_ref);
+  if (offset < 0 || !check_reference_finite(ref_cm, n_ref)) return -1;
+  return offset;
 }
 
 // Scalar arguments of a transform run (:1880-1929); on success
@@ -876,10 +1208,12 @@ RunSchedule make_schedule(const RunArgs& ra, int seed) {
 // (n x 2 column-major), the random draw (per-query mt19937 seeded through
 // mix_uint32, two normal_distribution<double>(0, 1e-4) draws, :1317-1335) or
 // the median / weighted initialisation on the device.
+// The queries' P (on p_stream, b.stream when null) and initial layout.
 bool prepare_queries(TransformBuffers& b, int n_query, int k, int offset, double perplexity, const double* y_init,
-                     int initialization, int seed) {
+                     int initialization, int seed, hipStream_t p_stream = nullptr) {
   const int blocks = query_blocks(n_query);
-  k_transform_p<<<blocks, kQueryThreads, 0, b.stream>>>(b.dist, n_query, k, perplexity, b.p);
+  k_transform_p<<<blocks, kQueryThreads, 0, p_stream != nullptr ? p_stream : b.stream>>>(b.dist, n_query, k,
+                                                                                        perplexity, b.p);
   if (!ok(hipGetLastError(), "transform P launch")) return false;
   std::vector<double> y_host;
   if (y_init != nullptr) {
@@ -900,9 +1234,8 @@ bool prepare_queries(TransformBuffers& b, int n_query, int k, int offset, double
               "initial layout upload") &&
            ok(hipStreamSynchronize(b.stream), "transform sync");
   }
-  k_transform_init<<<blocks, kQueryThreads, 0, b.stream>>>(b.ref, b.idx, b.dist, n_query, k, offset,
-                                                          initialization == 1 ? 1 : 0, b.y);
-  return ok(hipGetLastError(), "transform init launch");
+  return ok(launch_init(b.ref, b.idx, b.dist, n_query, k, offset, initialization == 1, b.y, b.stream),
+            "transform init launch");
 }
 
 // b.y -> out, n x 2 column-major; waits for the stream.
@@ -951,16 +1284,14 @@ int fastembedr_hip_transform_tsne(const double* reference_layout, int n_referenc
     set_last_error("invalid transform arguments (NULL pointer or empty input).");
     return 1;
   }
-  const int offset = reference_offset(indices, static_cast<std::size_t>(n_query) * k, n_reference);
-  if (!check_inputs(reference_layout, n_reference, indices, distances, n_query, k, perplexity, offset)) return 1;
+  TransformBuffers b;
+  const int offset =
+      upload_checked(b, reference_layout, n_reference, indices, distances, n_query, k, perplexity);
+  if (offset < 0) return 1;
   RunArgs ra{n_reference, n_iter, early_exaggeration_iter, learning_rate, early_exaggeration, exaggeration,
              initial_momentum, final_momentum, max_grad_norm, max_step_norm, n_negatives, exact_repulsion_threshold,
              initialization};
-  if (!check_run_args(ra)) return 1;
-  TransformBuffers b;
-  if (!b.init(n_reference, n_query, k) ||
-      !upload(b, reference_layout, n_reference, indices, distances, n_query, k) ||
-      !prepare_queries(b, n_query, k, offset, perplexity, y_init, initialization, seed)) {
+  if (!check_run_args(ra) || !prepare_queries(b, n_query, k, offset, perplexity, y_init, initialization, seed)) {
     return 1;
   }
   const GridGeo none{};
@@ -990,15 +1321,17 @@ int fastembedr_hip_transform_tsne_grid(const double* reference_layout, int n_ref
     return 1;
   }
   if (!check_grid_settings(n_interpolation_points, min_num_intervals, ints_in_interval)) return 1;
-  const int offset = reference_offset(indices, static_cast<std::size_t>(n_query) * k, n_reference);
-  if (!check_inputs(reference_layout, n_reference, indices, distances, n_query, k, perplexity, offset)) return 1;
+  TransformBuffers b;
+  const int offset =
+      upload_checked(b, reference_layout, n_reference, indices, distances, n_query, k, perplexity);
+  if (offset < 0) return 1;
   RunArgs ra{n_reference, n_iter, early_exaggeration_iter, learning_rate, early_exaggeration, exaggeration,
              initial_momentum, final_momentum, max_grad_norm, max_step_norm, 1, 1, initialization};
-  if (!check_run_args(ra)) return 1;
-  TransformBuffers b;
-  if (!b.init(n_reference, n_query, k) ||
-      !upload(b, reference_layout, n_reference, indices, distances, n_query, k) ||
-      !prepare_queries(b, n_query, k, offset, perplexity, y_init, initialization, seed)) {
+  // P on a side stream, beside the initialisation and the node fields; the
+  // run waits for it
+  if (!check_run_args(ra) || !b.init_side() ||
+      !prepare_queries(b, n_query, k, offset, perplexity, y_init, initialization, seed, b.side) ||
+      !ok(hipEventRecord(b.side_done, b.side), "hipEventRecord(transform P)")) {
     return 1;
   }
   // The grid covers the reference and the queries' start; its geometry is
@@ -1012,8 +1345,10 @@ int fastembedr_hip_transform_tsne_grid(const double* reference_layout, int n_ref
   const std::vector<double> ref = rows_of(reference_layout, n_reference);
   const GridGeo g = grid_geometry(ref.data(), n_reference, y0.data(), n_query, min_num_intervals, ints_in_interval);
   unsigned long long exact_evals = 0;
-  if (!b.init_field(g.m) || !ok(launch_grid_fields(b.ref, n_reference, g, b.field, b.stream), "grid fields launch") ||
+  if (!b.init_field(g.m, field_split(g.m, n_reference).chunks) ||
+      !ok(launch_grid_fields(b.ref, n_reference, g, b, b.stream), "grid fields launch") ||
       !ok(hipMemsetAsync(b.counter, 0, sizeof(unsigned long long), b.stream), "counter clear") ||
+      !ok(hipStreamWaitEvent(b.stream, b.side_done, 0), "hipStreamWaitEvent(transform P)") ||
       !ok(launch_run(kGrid, b.ref, n_reference, b.idx, b.p, n_query, k, offset, make_schedule(ra, seed), b.field, g,
                      b.y, b.counter, b.stream),
           "transform run launch") ||
@@ -1062,9 +1397,8 @@ int fastembedr_hip_transform_probe(const double* reference_layout, int n_referen
   if (!ok(hipGetLastError(), "transform P launch")) return 1;
   std::vector<double> host(std::max(nk, 2 * static_cast<std::size_t>(n_query)));
   if (init_out != nullptr) {
-    k_transform_init<<<blocks, kQueryThreads, 0, b.stream>>>(b.ref, b.idx, b.dist, n_query, k, offset,
-                                                            initialization, b.y);
-    if (!ok(hipGetLastError(), "transform init launch") ||
+    if (!ok(launch_init(b.ref, b.idx, b.dist, n_query, k, offset, initialization != 0, b.y, b.stream),
+            "transform init launch") ||
         !ok(hipMemcpyAsync(host.data(), b.y, 2 * static_cast<std::size_t>(n_query) * sizeof(double),
                            hipMemcpyDeviceToHost, b.stream),
             "init download") ||
@@ -1127,8 +1461,8 @@ int fastembedr_hip_transform_grid_probe(const double* reference_layout, int n_re
   const StepParams sp{exaggeration, 0.0, 0.0, 0.0, 0.0, n_reference, 0};
   unsigned long long exact_evals = 0;
   k_transform_p<<<query_blocks(n_query), kQueryThreads, 0, b.stream>>>(b.dist, n_query, k, perplexity, b.p);
-  if (!ok(hipGetLastError(), "transform P launch") || !b.init_field(g.m) ||
-      !ok(launch_grid_fields(b.ref, n_reference, g, b.field, b.stream), "grid fields launch") ||
+  if (!ok(hipGetLastError(), "transform P launch") || !b.init_field(g.m, field_split(g.m, n_reference).chunks) ||
+      !ok(launch_grid_fields(b.ref, n_reference, g, b, b.stream), "grid fields launch") ||
       !ok(hipMemsetAsync(b.counter, 0, sizeof(unsigned long long), b.stream), "counter clear") ||
       !ok(hipMemcpyAsync(b.y, y, 2 * static_cast<std::size_t>(n_query) * sizeof(double), hipMemcpyHostToDevice,
                          b.stream),
@@ -1180,21 +1514,7 @@ constexpr std::size_t kNaStateOffset = kNaPOffset + sizeof(double) * static_cast
 constexpr std::size_t kNaScratchBytes = kNaStateOffset + sizeof(double2) * kNaMaxQuery;
 constexpr int kNaMaxDevices = 64;
 
-struct NaHeader {
-  unsigned int flags;  // kNaBadReference
-  int idx_min;
-  int idx_max;
-  int pad;
-  unsigned long long exact_evals;  // the run kernel's counter (unused by the sampled and exact modes)
-  // First failing entry (column-major position) of each kind, or ULLONG_MAX:
-  // an index outside [0, n_ref) and outside [1, n_ref] (the two offsets the
-  // host may settle on), and a distance that is not finite and >= 0.  The
-  // host reports whichever comes first, as check_inputs' sequential scan does.
-  unsigned long long first_bad_index[2];
-  unsigned long long first_bad_distance;
-};
 static_assert(sizeof(NaHeader) <= kNaReferenceOffset, "the header fits its slot");
-constexpr unsigned int kNaBadReference = 2u;
 
 }  // namespace
 }  // namespace fehip
@@ -1203,64 +1523,6 @@ static __device__ __align__(256) unsigned char transform_scratch[fehip::kNaScrat
 
 namespace fehip {
 namespace {
-
-__global__ void k_na_clear(NaHeader* h) {
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    h->flags = 0u;
-    h->idx_min = INT_MAX;
-    h->idx_max = INT_MIN;
-    h->exact_evals = 0ull;
-    h->first_bad_index[0] = ULLONG_MAX;
-    h->first_bad_index[1] = ULLONG_MAX;
-    h->first_bad_distance = ULLONG_MAX;
-  }
-}
-
-// Index range and distance checks of check_inputs, as a reduction: the host
-// derives the index offset from the smallest and largest index, and the error
-// from the first failing entry of each kind.
-__device__ inline unsigned long long wave_min_u64(unsigned long long v) {
-  for (int off = 32; off > 0; off >>= 1) {
-    const unsigned long long o = __shfl_xor(v, off);
-    v = o < v ? o : v;
-  }
-  return v;
-}
-
-__global__ __launch_bounds__(256) void k_na_check_knn(const int* __restrict__ idx_cm,
-                                                      const double* __restrict__ dist_cm, long long count,
-                                                      int n_ref, NaHeader* h) {
-  int lo = INT_MAX, hi = INT_MIN;
-  unsigned long long bad0 = ULLONG_MAX, bad1 = ULLONG_MAX, badd = ULLONG_MAX;
-  const long long stride = static_cast<long long>(gridDim.x) * 256;
-  // a thread's entries ascend, so its first failure of each kind is its least
-  for (long long c = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; c < count; c += stride) {
-    const int v = idx_cm[c];
-    lo = v < lo ? v : lo;
-    hi = v > hi ? v : hi;
-    const unsigned long long at = static_cast<unsigned long long>(c);
-    if ((v < 0 || v >= n_ref) && bad0 == ULLONG_MAX) bad0 = at;
-    if ((v < 1 || v > n_ref) && bad1 == ULLONG_MAX) bad1 = at;
-    const double d = dist_cm[c];
-    if ((!isfinite(d) || d < 0.0) && badd == ULLONG_MAX) badd = at;
-  }
-  for (int off = 32; off > 0; off >>= 1) {
-    const int olo = __shfl_xor(lo, off);
-    const int ohi = __shfl_xor(hi, off);
-    lo = olo < lo ? olo : lo;
-    hi = ohi > hi ? ohi : hi;
-  }
-  bad0 = wave_min_u64(bad0);
-  bad1 = wave_min_u64(bad1);
-  badd = wave_min_u64(badd);
-  if ((threadIdx.x & 63) == 0) {
-    atomicMin(&h->idx_min, lo);
-    atomicMax(&h->idx_max, hi);
-    if (bad0 != ULLONG_MAX) atomicMin(&h->first_bad_index[0], bad0);
-    if (bad1 != ULLONG_MAX) atomicMin(&h->first_bad_index[1], bad1);
-    if (badd != ULLONG_MAX) atomicMin(&h->first_bad_distance, badd);
-  }
-}
 
 // n x 2 column-major reference layout -> interleaved, with the finiteness check.
 __global__ __launch_bounds__(256) void k_na_load_reference(const double* __restrict__ ref_cm, int n_ref,
@@ -1360,9 +1622,8 @@ int fastembedr_hip_transform_tsne_noalloc(const double* reference_layout, int n_
   double2* y = reinterpret_cast<double2*>(base + kNaStateOffset);
   hipStream_t st = nullptr;  // the null stream: no stream is created
 
-  const int check_blocks = static_cast<int>(std::min<long long>((entries + 255) / 256, 2048));
   k_na_clear<<<1, 64, 0, st>>>(hdr);
-  k_na_check_knn<<<check_blocks, 256, 0, st>>>(indices, distances, entries, n_reference, hdr);
+  k_na_check_knn<<<knn_check_blocks(entries), 256, 0, st>>>(indices, distances, entries, n_reference, hdr);
   k_na_load_reference<<<(n_reference + 255) / 256, 256, 0, st>>>(reference_layout, n_reference, ref, hdr);
   NaHeader h{};
   if (!ok(hipGetLastError(), "transform check launch") ||
@@ -1370,20 +1631,8 @@ int fastembedr_hip_transform_tsne_noalloc(const double* reference_layout, int n_
       !ok(hipStreamSynchronize(st), "transform check sync")) {
     return 1;
   }
-  // 1-based iff every index is in [1, n_reference] (:1290-1302), then every
-  // index must name a reference row.
-  // check_inputs scans the entries in order and stops at the first that
-  // fails either check, so the earlier failing entry names the error.
-  const int offset = (h.idx_min >= 1 && h.idx_max <= n_reference) ? 1 : 0;
-  const unsigned long long bad_index = h.first_bad_index[offset];
-  if (bad_index != ULLONG_MAX && bad_index <= h.first_bad_distance) {
-    set_last_error("KNN indices are out of range for `reference_layout`.");
-    return 1;
-  }
-  if (h.first_bad_distance != ULLONG_MAX) {
-    set_last_error("KNN distances must be finite and non-negative.");
-    return 1;
-  }
+  const int offset = knn_offset_from(h, n_reference);
+  if (offset < 0) return 1;
   if ((h.flags & kNaBadReference) != 0u) {
     set_last_error("`reference_layout` must be finite.");
     return 1;
@@ -1394,8 +1643,8 @@ int fastembedr_hip_transform_tsne_noalloc(const double* reference_layout, int n_
   if (y_init != nullptr) {
     k_na_load_layout<<<(n_query + 255) / 256, 256, 0, st>>>(y_init, n_query, y);
   } else {
-    k_transform_init<<<blocks, kQueryThreads, 0, st>>>(ref, indices, distances, n_query, k, offset,
-                                                      initialization == 1 ? 1 : 0, y);
+    const hipError_t e = launch_init(ref, indices, distances, n_query, k, offset, initialization == 1, y, st);
+    if (!ok(e, "transform init launch")) return 1;
   }
   if (!ok(hipGetLastError(), "transform setup launch")) return 1;
   const GridGeo none{};

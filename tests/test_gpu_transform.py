@@ -67,6 +67,22 @@ def test_transform_p_and_init_match_oracle(hip, oracle_mod, qp):
     np.testing.assert_allclose(wt, oracle_mod.transform_init(ref, idx, dist, oracle_mod.INIT_WEIGHTED), rtol=1e-14)
 
 
+@pytest.mark.parametrize("k", [1, 2, 5, 8, 13, 16, 30, 33, 64, 65])
+def test_median_init_all_lane_widths(hip, oracle_mod, k):
+    """The median initialisation at every lane width of its kernel (8, 16, 32
+    and 64 lanes per query) and past it (k = 65, one thread per query), with
+    tied coordinates (references on a half-unit lattice) and repeated
+    neighbours; bit-identical to the oracle."""
+    _say(f"case: median init, k={k}, tied coordinates")
+    rng = np.random.default_rng(100 + k)
+    n_ref, nq = 400, 333
+    ref = np.round(rng.normal(0.0, 3.0, (n_ref, 2)) * 2.0) / 2.0
+    idx = rng.integers(1, n_ref + 1, (nq, k)).astype(np.int32)
+    dist = np.sort(rng.uniform(0.1, 2.0, (nq, k)), axis=1)
+    _, _, med = _probe(ref, idx, dist, 0.5, init=0)
+    np.testing.assert_array_equal(med, oracle_mod.transform_init(ref, idx, dist, oracle_mod.INIT_MEDIAN))
+
+
 @pytest.mark.parametrize("mode", ["sampled", "exact"])
 def test_transform_gradient_matches_oracle(hip, oracle_mod, qp, mode):
     _say(f"case: transform gradient ({mode})")
