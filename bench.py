@@ -73,6 +73,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--host-boundary", action=argparse.BooleanOptionalAction, default=True,
                     help="also time the one-shot C-ABI call from host KNN buffers (PCIe and P build included; "
                          "on by default, reported beside `value`)")
+    ap.add_argument("--fft-sweep", action="store_true",
+                    help="instead of the bench line: the interpolation grid's repulsion kernels at FFT lengths "
+                         "768 ... 4096, the converged config-2 layout scaled until it needs them (one JSON line)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device-to-device copy of this size first (counter calibration under rocprofv3)")
     return ap.parse_args()
@@ -167,6 +170,9 @@ def main() -> int:
     torch.cuda.synchronize()
     full_wall = time.perf_counter() - t0
     log(f"whole schedule: {total} iterations in {full_wall:.3f}s = {total / full_wall:.1f} it/s")
+
+    if args.fft_sweep:
+        return fft_sweep(sess, n, nnz, sched, lr, log)
 
     # 3. breakdown pass over the window: HIP events around every kernel give
     # the per-kernel durations and pick the dominant kernel.  In this pass
@@ -354,6 +360,39 @@ def main() -> int:
     else:
         line["config"]["grid_nodes_per_axis"] = g
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def fft_sweep(sess, n, nnz, sched, lr, log) -> int:
+    """The repulsion kernels at large FFT lengths on a real 1M-point layout:
+    the converged layout (the schedule just run) scaled by s, so that its
+    span needs s times the boxes.  Per scale, 20 iterations at learning rate
+    0 (the layout does not move) with every kernel timed alone by events;
+    the step clip is off, so the host sizes each iteration's FFT from that
+    iteration's own box count (the shortest length that holds the grid)."""
+    y_end = np.asarray(sess.y, np.float64)
+    y_end -= y_end.mean(axis=0)
+    cases = []
+    for scale in (1.0, 2.8, 4.2, 5.6):
+        sess.set_state((y_end * scale).astype(np.float32))
+        sess.center()
+        sess.sync()
+        sess.set_timing(True)
+        sess.run(20, sched["exaggeration"], sched["final_momentum"], 0.0, sched["min_gain"], 0.0)
+        sess.sync()
+        br = sess.timing()
+        sess.set_timing(False)
+        info = sess.interp_info()
+        per = {name: tot / 20 for name, (cnt, tot) in br.items() if cnt and name.startswith("interp_")}
+        rep = sum(per.values())
+        cases.append({"scale": scale, "boxes_per_axis": info["boxes"], "nodes_per_axis": info["nodes"],
+                      "fft_len": info["fft_len"], "ms_per_repulsion_step": round(rep, 4),
+                      "per_kernel_ms": {kk: round(v, 5) for kk, v in per.items()}})
+        log(f"scale {scale}: {info['boxes']} boxes, {info['nodes']} nodes, FFT {info['fft_len']}: repulsion "
+            f"{rep:.3f} ms ({', '.join(f'{kk}={v:.4f}' for kk, v in per.items())})")
+    print(json.dumps({"metric": "interpolation-grid repulsion step at large FFT lengths (ms, kernels in sequence)",
+                      "n": n, "nnz": nnz, "data": "synthetic (config 2, converged layout scaled)",
+                      "cases": cases}), flush=True)
     return 0
 
 

@@ -169,18 +169,33 @@ __device__ __forceinline__ void block_exclusive_scan2(int (&a)[PER], int (&b)[PE
 // ---------------------------------------------------------------------------
 // LDS Stockham FFT
 //
-// NSEQ sequences of length F = 2^a or 3 * 2^a, sequence q at s + q * F,
-// transformed in place by NT threads.  One radix-3 stage first when 3 divides
-// F, then radix-4 stages, then one radix-2 stage when F / Ns = 2 is left.  A
-// stage of radix R entered after Ns points are transformed (Ns = the product
-// of the earlier radices) takes, for each j < F / R, the inputs j + r F / R,
-// twiddles them by e^{-2 pi i r k / (Ns R)} with k = j mod Ns, and writes the
-// R-point DFT to (j - k) R + k + r Ns, so the result is in natural order.
-// Every stage reads its inputs to registers, barriers, then writes.
+// NSEQ sequences of length F = 2^a or 3 * 2^a in LDS, transformed in place
+// by NT threads.  One radix-3 stage first when 3 divides F, then radix-16
+// stages while 16 divides what is left, then one stage of radix 8, 4 or 2
+// for the rest (F = 2048: 16, 16, 8; 768: 3, 16, 16).  A stage of radix R
+// entered after Ns points are transformed (Ns = the product of the earlier
+// radices) takes, for each j < F / R, the inputs j + r F / R, twiddles them
+// by e^{-2 pi i r k / (Ns R)} with k = j mod Ns, and writes their R-point DFT
+// (taken in registers) to (j - k) R + k + r Ns, so the result is in natural
+// order.  Every stage reads its inputs to registers, barriers, then writes.
 // Twiddles e^{-2 pi i j / F} are staged in LDS from the global table
 // (computed in fp64 on the host); INV conjugates them and leaves the result
 // unscaled.
+//
+// LDS layout: sequence q starts at q * FftPad<F>::kStride and element i sits
+// at i + i / 32 (fft_at): one pad element per 32 keeps the strided writes of
+// the early stages (stride R elements) from falling into one LDS bank.
 // ---------------------------------------------------------------------------
+template <int F>
+struct FftPad {
+  static constexpr int kStride = F + F / 32;
+};
+__device__ __forceinline__ int fft_pad(int i) { return i + (i >> 5); }
+template <int F>
+__device__ __forceinline__ int fft_at(int q, int i) {
+  return q * FftPad<F>::kStride + fft_pad(i);
+}
+
 template <bool INV>
 __device__ __forceinline__ float2 twiddle(const float2* __restrict__ tw, int m) {
   const float2 w = tw[m];
@@ -224,9 +239,8 @@ __device__ __forceinline__ void fft_stage_r3(float2* s) {
     if (TOT % NT == 0 || t < TOT) {
       const int q = t / T;
       const int j = t - q * T;
-      const float2* src = s + q * F;
 #pragma unroll
-      for (int r = 0; r < 3; ++r) v[b][r] = src[j + r * T];
+      for (int r = 0; r < 3; ++r) v[b][r] = s[fft_at<F>(q, j + r * T)];
       const float2 sum = cadd(v[b][1], v[b][2]);
       const float2 dif = csub(v[b][1], v[b][2]);
       const float2 mid = make_float2(v[b][0].x - 0.5f * sum.x, v[b][0].y - 0.5f * sum.y);
@@ -244,95 +258,157 @@ __device__ __forceinline__ void fft_stage_r3(float2* s) {
     if (TOT % NT == 0 || t < TOT) {
       const int q = t / T;
       const int j = t - q * T;
-      float2* dst = s + q * F + 3 * j;
 #pragma unroll
-      for (int r = 0; r < 3; ++r) dst[r] = v[b][r];
+      for (int r = 0; r < 3; ++r) s[fft_at<F>(q, 3 * j + r)] = v[b][r];
     }
   }
   __syncthreads();
 }
 
-// Radix-4 stages from Ns = NS while 4 divides F / Ns.
-template <int F, int NS, int NSEQ, int NT, bool INV, int TWS>
-__device__ __forceinline__ void fft_stages_r4(float2* s, const float2* __restrict__ tw) {
-  if constexpr ((F / NS) % 4 == 0) {
-    constexpr int Q = F / 4;
-    constexpr int TOT = NSEQ * Q;
-    constexpr int BPT = (TOT + NT - 1) / NT;
-    float2 v[BPT][4];
+// -i v (forward) or +i v (inverse).
+template <bool INV>
+__device__ __forceinline__ float2 rot_i(float2 v) {
+  return INV ? make_float2(-v.y, v.x) : make_float2(v.y, -v.x);
+}
+
+// 4-point DFT in place, natural order.
+template <bool INV>
+__device__ __forceinline__ void dft4(float2& a0, float2& a1, float2& a2, float2& a3) {
+  const float2 a = cadd(a0, a2);
+  const float2 c = csub(a0, a2);
+  const float2 d = cadd(a1, a3);
+  const float2 e = rot_i<INV>(csub(a1, a3));
+  a0 = cadd(a, d);
+  a1 = cadd(c, e);
+  a2 = csub(a, d);
+  a3 = csub(c, e);
+}
+
+// e^{-2 pi i m / N} (forward) or its conjugate, m < N, for the radix-8 and
+// radix-16 DFTs' internal twiddles (exact constants).
+template <bool INV>
+__device__ __forceinline__ float2 w16(int m) {
+  constexpr float c1 = 0.923879532511286756128f;  // cos(pi / 8)
+  constexpr float s1 = 0.382683432365089771728f;  // sin(pi / 8)
+  constexpr float h = 0.707106781186547524401f;   // cos(pi / 4)
+  float2 w;
+  switch (m) {
+    case 1: w = make_float2(c1, -s1); break;
+    case 2: w = make_float2(h, -h); break;
+    case 3: w = make_float2(s1, -c1); break;
+    case 6: w = make_float2(-h, -h); break;
+    case 9: w = make_float2(-c1, s1); break;
+    default: w = make_float2(1.0f, 0.0f); break;
+  }
+  return INV ? make_float2(w.x, -w.y) : w;
+}
+
+// R-point DFT in registers (R = 2, 4, 8, 16).  With n = (R / 4) n1 + n2 and
+// k = k1 + 4 k2: 4-point DFTs over n1, twiddles e^{-2 pi i n2 k1 / R}, then
+// (R / 4)-point DFTs over n2.  X[k] ends in v[dft_slot<R>(k)].
+template <int R>
+__device__ __forceinline__ constexpr int dft_slot(int k) {
+  return R <= 4 ? k : (R / 4) * (k & 3) + (k >> 2);
+}
+template <int R, bool INV>
+__device__ __forceinline__ void dft_r(float2 (&v)[R]) {
+  if constexpr (R == 2) {
+    const float2 a = v[0];
+    v[0] = cadd(a, v[1]);
+    v[1] = csub(a, v[1]);
+  } else if constexpr (R == 4) {
+    dft4<INV>(v[0], v[1], v[2], v[3]);
+  } else if constexpr (R == 8) {
+    dft4<INV>(v[0], v[2], v[4], v[6]);
+    dft4<INV>(v[1], v[3], v[5], v[7]);
+    v[3] = cmul(v[3], w16<INV>(2));  // e^{-2 pi i / 8}
+    v[5] = rot_i<INV>(v[5]);         // e^{-2 pi i 2 / 8}
+    v[7] = cmul(v[7], w16<INV>(6));  // e^{-2 pi i 3 / 8}
 #pragma unroll
-    for (int b = 0; b < BPT; ++b) {
-      const int t = threadIdx.x + b * NT;
-      if (TOT % NT == 0 || t < TOT) {
-        const int q = t / Q;
-        const int j = t - q * Q;
-        const float2* src = s + q * F;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[b][r] = src[j + r * Q];
-        const int kk = static_cast<int>(static_cast<unsigned int>(j) % NS);
-        const int step = (F / (4 * NS)) * kk * TWS;
-        v[b][1] = cmul(v[b][1], twiddle<INV>(tw, step));
-        v[b][2] = cmul(v[b][2], twiddle<INV>(tw, 2 * step));
-        v[b][3] = cmul(v[b][3], twiddle<INV>(tw, 3 * step));
-        const float2 a = cadd(v[b][0], v[b][2]);
-        const float2 c = csub(v[b][0], v[b][2]);
-        const float2 d = cadd(v[b][1], v[b][3]);
-        const float2 e = csub(v[b][1], v[b][3]);
-        // forward: (-i) * e, inverse: (+i) * e
-        const float2 er = INV ? make_float2(-e.y, e.x) : make_float2(e.y, -e.x);
-        v[b][0] = cadd(a, d);
-        v[b][1] = cadd(c, er);
-        v[b][2] = csub(a, d);
-        v[b][3] = csub(c, er);
-      }
+    for (int k1 = 0; k1 < 4; ++k1) {
+      const float2 a = v[2 * k1];
+      v[2 * k1] = cadd(a, v[2 * k1 + 1]);
+      v[2 * k1 + 1] = csub(a, v[2 * k1 + 1]);
     }
-    __syncthreads();
-#pragma unroll
-    for (int b = 0; b < BPT; ++b) {
-      const int t = threadIdx.x + b * NT;
-      if (TOT % NT == 0 || t < TOT) {
-        const int q = t / Q;
-        const int j = t - q * Q;
-        const int kk = static_cast<int>(static_cast<unsigned int>(j) % NS);
-        float2* dst = s + q * F + (j - kk) * 4 + kk;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dst[r * NS] = v[b][r];
-      }
-    }
-    __syncthreads();
-    fft_stages_r4<F, NS * 4, NSEQ, NT, INV, TWS>(s, tw);
-  } else if constexpr (F / NS == 2) {
-    // last stage, radix 2 (Ns = F / 2): in place, j and j + F / 2
-    constexpr int H2 = F / 2;
-    constexpr int TOT2 = NSEQ * H2;
-#pragma unroll
-    for (int b = 0; b < (TOT2 + NT - 1) / NT; ++b) {
-      const int t = threadIdx.x + b * NT;
-      if (TOT2 % NT == 0 || t < TOT2) {
-        const int q = t / H2;
-        const int j = t - q * H2;
-        float2* base = s + q * F;
-        const float2 v0 = base[j];
-        const float2 v1 = cmul(base[j + H2], twiddle<INV>(tw, j * TWS));
-        base[j] = cadd(v0, v1);
-        base[j + H2] = csub(v0, v1);
-      }
-    }
-    __syncthreads();
   } else {
-    static_assert(F == NS, "radix plan ends at F");
+    static_assert(R == 16, "radix 2, 4, 8 or 16");
+#pragma unroll
+    for (int n2 = 0; n2 < 4; ++n2) dft4<INV>(v[n2], v[4 + n2], v[8 + n2], v[12 + n2]);
+#pragma unroll
+    for (int k1 = 1; k1 < 4; ++k1) {
+#pragma unroll
+      for (int n2 = 1; n2 < 4; ++n2) {
+        float2& x = v[4 * k1 + n2];
+        x = (n2 * k1 == 4) ? rot_i<INV>(x) : cmul(x, w16<INV>(n2 * k1));
+      }
+    }
+#pragma unroll
+    for (int k1 = 0; k1 < 4; ++k1) dft4<INV>(v[4 * k1], v[4 * k1 + 1], v[4 * k1 + 2], v[4 * k1 + 3]);
+  }
+}
+
+// One radix-R stage from Ns = NS.
+template <int R, int F, int NS, int NSEQ, int NT, bool INV, int TWS>
+__device__ __forceinline__ void fft_stage(float2* s, const float2* __restrict__ tw) {
+  constexpr int Q = F / R;
+  constexpr int TOT = NSEQ * Q;
+  constexpr int BPT = (TOT + NT - 1) / NT;
+  float2 v[BPT][R];
+#pragma unroll
+  for (int b = 0; b < BPT; ++b) {
+    const int t = threadIdx.x + b * NT;
+    if (TOT % NT == 0 || t < TOT) {
+      const int q = t / Q;
+      const int j = t - q * Q;
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[b][r] = s[fft_at<F>(q, j + r * Q)];
+      if constexpr (NS > 1) {
+        const int kk = static_cast<int>(static_cast<unsigned int>(j) % NS);
+        const int step = (F / (R * NS)) * kk * TWS;
+#pragma unroll
+        for (int r = 1; r < R; ++r) v[b][r] = cmul(v[b][r], twiddle<INV>(tw, r * step));
+      }
+      dft_r<R, INV>(v[b]);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < BPT; ++b) {
+    const int t = threadIdx.x + b * NT;
+    if (TOT % NT == 0 || t < TOT) {
+      const int q = t / Q;
+      const int j = t - q * Q;
+      const int kk = static_cast<int>(static_cast<unsigned int>(j) % NS);
+      const int base = (j - kk) * R + kk;
+#pragma unroll
+      for (int r = 0; r < R; ++r) s[fft_at<F>(q, base + r * NS)] = v[b][dft_slot<R>(r)];
+    }
+  }
+  __syncthreads();
+}
+
+// The power-of-two stages from Ns = NS: radix 16 while 16 divides F / Ns,
+// then one stage of what is left (8, 4 or 2).
+template <int F, int NS, int NSEQ, int NT, bool INV, int TWS>
+__device__ __forceinline__ void fft_stages_pow2(float2* s, const float2* __restrict__ tw) {
+  constexpr int REM = F / NS;
+  if constexpr (REM > 1) {
+    constexpr int R = REM % 16 == 0 ? 16 : REM;
+    static_assert(R == 16 || R == 8 || R == 4 || R == 2, "radix plan ends at F");
+    fft_stage<R, F, NS, NSEQ, NT, INV, TWS>(s, tw);
+    fft_stages_pow2<F, NS * R, NSEQ, NT, INV, TWS>(s, tw);
   }
 }
 
 // tw holds e^{-2 pi i j / (F * TWS)} for j < F * TWS (staged in LDS by
-// stage_twiddles: TWS = 1).
+// stage_twiddles: TWS = 1).  s holds NSEQ sequences in the fft_at layout.
 template <int F, int NSEQ, int NT, bool INV, int TWS = 1>
 __device__ __forceinline__ void fft_lds(float2* s, const float2* __restrict__ tw) {
   if constexpr (FftRadices<F>::kR3) {
     fft_stage_r3<F, NSEQ, NT, INV>(s);
-    fft_stages_r4<F, 3, NSEQ, NT, INV, TWS>(s, tw);
+    fft_stages_pow2<F, 3, NSEQ, NT, INV, TWS>(s, tw);
   } else {
-    fft_stages_r4<F, 1, NSEQ, NT, INV, TWS>(s, tw);
+    fft_stages_pow2<F, 1, NSEQ, NT, INV, TWS>(s, tw);
   }
 }
 

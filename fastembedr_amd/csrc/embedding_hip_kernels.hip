@@ -586,7 +586,7 @@ __global__ __launch_bounds__(256) void k_kernel_rows(const DeviceScalars* sc, co
                                                      float2* __restrict__ k_rows) {
   chain_priority();
   using S = Shape<F>;
-  __shared__ float2 lds[S::KROWS * F];
+  __shared__ float2 lds[S::KROWS * FftPad<F>::kStride];
   __shared__ float2 tws[F];
   stage_twiddles<F, S::NT>(tws, tw);
   const float h = sc->h;
@@ -603,7 +603,7 @@ __global__ __launch_bounds__(256) void k_kernel_rows(const DeviceScalars* sc, co
       const float q = 1.0f / (1.0f + (ox * ox + oy * oy));
       v = make_float2(q, q * q);
     }
-    lds[e] = v;
+    lds[fft_at<F>(r, x)] = v;
   }
   __syncthreads();
   fft_lds<F, S::KROWS, S::NT, false, 1>(lds, tws);
@@ -611,7 +611,7 @@ __global__ __launch_bounds__(256) void k_kernel_rows(const DeviceScalars* sc, co
     const int r = e / S::H;
     const int kx = e - r * S::H;
     const int y = row0 + r;
-    if (y < S::H) k_rows[y * S::H + kx] = lds[r * F + kx];
+    if (y < S::H) k_rows[y * S::H + kx] = lds[fft_at<F>(r, kx)];
   }
 }
 
@@ -623,7 +623,7 @@ __global__ __launch_bounds__(256) void k_kernel_cols(const float2* __restrict__ 
                                                      const float2* __restrict__ tw, float2* __restrict__ k_hat) {
   chain_priority();
   using S = Shape<F>;
-  __shared__ float2 lds[S::KROWS * F];
+  __shared__ float2 lds[S::KROWS * FftPad<F>::kStride];
   __shared__ float2 tws[F];
   stage_twiddles<F, S::NT>(tws, tw);
   const int col0 = blockIdx.x * S::KROWS;
@@ -632,7 +632,7 @@ __global__ __launch_bounds__(256) void k_kernel_cols(const float2* __restrict__ 
     const int c = e - y * S::KROWS;
     const int kx = col0 + c;
     const int ys = y <= F / 2 ? y : F - y;
-    lds[c * F + y] = kx < S::H ? k_rows[ys * S::H + kx] : make_float2(0.0f, 0.0f);
+    lds[fft_at<F>(c, y)] = kx < S::H ? k_rows[ys * S::H + kx] : make_float2(0.0f, 0.0f);
   }
   __syncthreads();
   fft_lds<F, S::KROWS, S::NT, false, 1>(lds, tws);
@@ -640,7 +640,7 @@ __global__ __launch_bounds__(256) void k_kernel_cols(const float2* __restrict__ 
     const int ky = e / S::KROWS;
     const int c = e - ky * S::KROWS;
     const int kx = col0 + c;
-    if (kx < S::H) k_hat[ky * S::H + kx] = lds[c * F + ky];
+    if (kx < S::H) k_hat[ky * S::H + kx] = lds[fft_at<F>(c, ky)];
   }
 }
 
@@ -659,7 +659,7 @@ __global__ __launch_bounds__(256) void k_charge_rows(const float* __restrict__ m
                                                      float2* __restrict__ mx_rows, float2* __restrict__ my_rows) {
   chain_priority();
   using S = Shape<F>;
-  __shared__ float2 lds[2 * S::CROWS * F];
+  __shared__ float2 lds[2 * S::CROWS * FftPad<F>::kStride];
   __shared__ float2 tws[F];
   stage_twiddles<F, S::NT>(tws, tw);
   const int row0 = blockIdx.x * S::CROWS;
@@ -673,8 +673,8 @@ __global__ __launch_bounds__(256) void k_charge_rows(const float* __restrict__ m
       a = make_float2(mass_x[at], mass_y[at]);
       b = make_float2(mass[at], 0.0f);
     }
-    lds[(2 * r) * F + x] = a;
-    lds[(2 * r + 1) * F + x] = b;
+    lds[fft_at<F>(2 * r, x)] = a;
+    lds[fft_at<F>(2 * r + 1, x)] = b;
   }
   __syncthreads();
   fft_lds<F, 2 * S::CROWS, S::NT, false, 1>(lds, tws);
@@ -683,11 +683,11 @@ __global__ __launch_bounds__(256) void k_charge_rows(const float* __restrict__ m
     const int kx = e - r * S::H;
     const int y = row0 + r;
     if (y >= S::G) continue;
-    const float2 a = lds[(2 * r) * F + kx];
-    const float2 b = conjf2(lds[(2 * r) * F + ((F - kx) & (F - 1))]);
+    const float2 a = lds[fft_at<F>(2 * r, kx)];
+    const float2 b = conjf2(lds[fft_at<F>(2 * r, ((F - kx) & (F - 1)))]);
     const float2 sum = cadd(a, b);
     const float2 dif = csub(a, b);
-    m_rows[y * S::H + kx] = lds[(2 * r + 1) * F + kx];
+    m_rows[y * S::H + kx] = lds[fft_at<F>(2 * r + 1, kx)];
     mx_rows[y * S::H + kx] = cscale(sum, 0.5f);
     my_rows[y * S::H + kx] = make_float2(0.5f * dif.y, -0.5f * dif.x);
   }
@@ -711,7 +711,7 @@ __global__ __launch_bounds__(256) void k_conv_cols(const float2* __restrict__ m_
   chain_priority();
   using S = Shape<F>;
   constexpr int C = S::CCOLS;
-  __shared__ float2 lds[4 * C * F];
+  __shared__ float2 lds[4 * C * FftPad<F>::kStride];
   __shared__ float2 tws[F];
   stage_twiddles<F, S::NT>(tws, tw);
   const int col0 = blockIdx.x * C;
@@ -726,9 +726,9 @@ __global__ __launch_bounds__(256) void k_conv_cols(const float2* __restrict__ m_
       b = mx_rows[at];
       d = my_rows[at];
     }
-    lds[(0 * C + c) * F + y] = a;
-    lds[(1 * C + c) * F + y] = b;
-    lds[(2 * C + c) * F + y] = d;
+    lds[fft_at<F>(0 * C + c, y)] = a;
+    lds[fft_at<F>(1 * C + c, y)] = b;
+    lds[fft_at<F>(2 * C + c, y)] = d;
   }
   __syncthreads();
   fft_lds<F, 3 * C, S::NT, false, 1>(lds, tws);
@@ -738,13 +738,13 @@ __global__ __launch_bounds__(256) void k_conv_cols(const float2* __restrict__ m_
     const int kx = col0 + c;
     const int ks = ky <= F / 2 ? ky : F - ky;
     const float2 kk = kx < S::H ? k_hat[ks * S::H + kx] : make_float2(0.0f, 0.0f);
-    const float2 m = lds[(0 * C + c) * F + ky];
-    const float2 mx = lds[(1 * C + c) * F + ky];
-    const float2 my = lds[(2 * C + c) * F + ky];
-    lds[(0 * C + c) * F + ky] = cscale(m, kk.x);
-    lds[(3 * C + c) * F + ky] = cscale(m, kk.y);
-    lds[(1 * C + c) * F + ky] = cscale(mx, kk.y);
-    lds[(2 * C + c) * F + ky] = cscale(my, kk.y);
+    const float2 m = lds[fft_at<F>(0 * C + c, ky)];
+    const float2 mx = lds[fft_at<F>(1 * C + c, ky)];
+    const float2 my = lds[fft_at<F>(2 * C + c, ky)];
+    lds[fft_at<F>(0 * C + c, ky)] = cscale(m, kk.x);
+    lds[fft_at<F>(3 * C + c, ky)] = cscale(m, kk.y);
+    lds[fft_at<F>(1 * C + c, ky)] = cscale(mx, kk.y);
+    lds[fft_at<F>(2 * C + c, ky)] = cscale(my, kk.y);
   }
   __syncthreads();
   fft_lds<F, 4 * C, S::NT, true, 1>(lds, tws);
@@ -754,10 +754,10 @@ __global__ __launch_bounds__(256) void k_conv_cols(const float2* __restrict__ m_
     const int kx = col0 + c;
     if (kx >= S::H) continue;
     const int at = y * S::H + kx;
-    x_rows[at] = lds[(0 * C + c) * F + y];
-    v2_rows[at] = lds[(1 * C + c) * F + y];
-    y_rows[at] = lds[(2 * C + c) * F + y];
-    v1_rows[at] = lds[(3 * C + c) * F + y];
+    x_rows[at] = lds[fft_at<F>(0 * C + c, y)];
+    v2_rows[at] = lds[fft_at<F>(1 * C + c, y)];
+    y_rows[at] = lds[fft_at<F>(2 * C + c, y)];
+    v1_rows[at] = lds[fft_at<F>(3 * C + c, y)];
   }
 }
 
@@ -783,7 +783,7 @@ __global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__
                                                       int n, DeviceScalars* sc) {
   chain_priority();
   using S = Shape<F>;
-  __shared__ float2 lds[2 * S::CROWS * F];
+  __shared__ float2 lds[2 * S::CROWS * FftPad<F>::kStride];
   __shared__ float2 tws[F];
   stage_twiddles<F, S::NT>(tws, tw);
   const int row0 = blockIdx.x * S::CROWS;
@@ -805,8 +805,8 @@ __global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__
       u = cadd(X, mul_i(V1));
       v = cadd(V2, mul_i(Y));
     }
-    lds[(2 * r) * F + kx] = u;
-    lds[(2 * r + 1) * F + kx] = v;
+    lds[fft_at<F>(2 * r, kx)] = u;
+    lds[fft_at<F>(2 * r + 1, kx)] = v;
   }
   __syncthreads();
   fft_lds<F, 2 * S::CROWS, S::NT, true, 1>(lds, tws);
@@ -817,8 +817,8 @@ __global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__
     const int x = e - r * S::G;
     const int y = row0 + r;
     if (y >= S::G) continue;
-    const float2 u = cscale(lds[(2 * r) * F + x], scale);
-    const float2 v = cscale(lds[(2 * r + 1) * F + x], scale);
+    const float2 u = cscale(lds[fft_at<F>(2 * r, x)], scale);
+    const float2 v = cscale(lds[fft_at<F>(2 * r + 1, x)], scale);
     const int at = y * S::G + x;
     field[at] = make_float4(u.y, v.x, v.y, u.x);
     acc += static_cast<double>(mass[at]) * static_cast<double>(u.x);

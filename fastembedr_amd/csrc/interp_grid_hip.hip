@@ -421,6 +421,11 @@ struct LgShape {
   static constexpr int G = F / 2;
   static constexpr int H = F / 2 + 1;
   static constexpr int NT = F >= 2048 ? 512 : 256;
+  // kernel rows, convolution columns and inverse rows: 1024 threads from
+  // F = 3072, where one workgroup's LDS fills most of a CU (sequential, 1M
+  // points: conv 191 -> 175 us at 3072, 290 -> 276 at 4096; the charge rows,
+  // whose box sums scale badly with the threads, went 91 -> 209 us)
+  static constexpr int NTW = F >= 3072 ? 1024 : NT;
   static constexpr int KR = F >= 1024 ? 1 : 1024 / F;  // kernel rows / columns per block (two sequences each)
   static constexpr int CR = F >= 1024 ? 1 : 1024 / F;  // charge / inverse rows per block (two sequences each)
   static constexpr int CC = F >= 512 ? 1 : 512 / F;    // columns of the convolution pass (three sequences each)
@@ -442,20 +447,20 @@ __device__ __forceinline__ void lg_kernels(int dx, int dy, float h, float& k, fl
 // so Re B^ = By and Im B^ = Bx.  Kept for kx in [0, F/2] as two float2
 // planes, (K^r, K1^r) and (Bx, By), row-major with row stride F/2 + 1.
 template <int F>
-__global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_rows(const DeviceScalars* sc,
+__global__ __launch_bounds__(LgShape<F>::NTW) void k_lg_kernel_rows(const DeviceScalars* sc,
                                                                    const float2* __restrict__ tw,
                                                                    float2* __restrict__ k_rows) {
   chain_priority();
   using S = LgShape<F>;
   constexpr int HH = S::H * S::H;
-  __shared__ float2 lds[2 * S::KR * F];
+  __shared__ float2 lds[2 * S::KR * FftPad<F>::kStride];
   __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
   const float h = sc->lg_node_h;
   const int row0 = blockIdx.x * S::KR;
   if (row0 >= m) return;  // rows >= m are zero and never read
-  stage_twiddles<F, S::NT>(tws, tw);
-  for (int e = threadIdx.x; e < S::KR * F; e += S::NT) {
+  stage_twiddles<F, S::NTW>(tws, tw);
+  for (int e = threadIdx.x; e < S::KR * F; e += S::NTW) {
     const int r = e / F;
     const int x = e - r * F;
     const int y = row0 + r;
@@ -463,18 +468,18 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_rows(const DeviceS
     const int adx = dx < 0 ? -dx : dx;
     float k = 0.0f, k1 = 0.0f;
     if (adx < m && y < m) lg_kernels(dx, y, h, k, k1);
-    lds[(2 * r) * F + x] = make_float2(k, k1);
-    lds[(2 * r + 1) * F + x] = make_float2(k * static_cast<float>(dx) + k * static_cast<float>(y), 0.0f);
+    lds[fft_at<F>(2 * r, x)] = make_float2(k, k1);
+    lds[fft_at<F>(2 * r + 1, x)] = make_float2(k * static_cast<float>(dx) + k * static_cast<float>(y), 0.0f);
   }
   __syncthreads();
-  fft_lds<F, 2 * S::KR, S::NT, false, 1>(lds, tws);
-  for (int e = threadIdx.x; e < S::KR * S::H; e += S::NT) {
+  fft_lds<F, 2 * S::KR, S::NTW, false, 1>(lds, tws);
+  for (int e = threadIdx.x; e < S::KR * S::H; e += S::NTW) {
     const int r = e / S::H;
     const int kx = e - r * S::H;
     const int y = row0 + r;
     if (y >= S::H || y >= m) continue;
-    const float2 a = lds[(2 * r) * F + kx];
-    const float2 b = lds[(2 * r + 1) * F + kx];
+    const float2 a = lds[fft_at<F>(2 * r, kx)];
+    const float2 b = lds[fft_at<F>(2 * r + 1, kx)];
     const int at = y * S::H + kx;
     k_rows[at] = a;
     k_rows[HH + at] = make_float2(b.y, b.x);
@@ -495,7 +500,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_cols(const DeviceS
   chain_priority();
   using S = LgShape<F>;
   constexpr int HH = S::H * S::H;
-  __shared__ float2 lds[2 * S::KR * F];
+  __shared__ float2 lds[2 * S::KR * FftPad<F>::kStride];
   __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
   const int cb = col_block(static_cast<int>(blockIdx.x), (S::H + S::KR - 1) / S::KR);
@@ -515,8 +520,8 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_cols(const DeviceS
       const float2 b = k_rows[HH + at];  // (Bx, By)
       q = make_float2(b.x + (up ? b.y : -b.y), 0.0f);
     }
-    lds[(2 * c) * F + y] = p;
-    lds[(2 * c + 1) * F + y] = q;
+    lds[fft_at<F>(2 * c, y)] = p;
+    lds[fft_at<F>(2 * c + 1, y)] = q;
   }
   __syncthreads();
   fft_lds<F, 2 * S::KR, S::NT, false, 1>(lds, tws);
@@ -526,8 +531,8 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_cols(const DeviceS
     const int kx = col0 + c;
     if (kx >= S::H) continue;
     const int at = kx * S::H + ky;
-    k_hat[at] = lds[(2 * c) * F + ky];
-    k_hat[HH + at] = lds[(2 * c + 1) * F + ky];
+    k_hat[at] = lds[fft_at<F>(2 * c, ky)];
+    k_hat[HH + at] = lds[fft_at<F>(2 * c + 1, ky)];
   }
 }
 
@@ -558,7 +563,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
   // workgroups (49 KB each, two or three per CU) when the two overlap
   constexpr int RG = 1;
   constexpr int NB = F / 2 / kLgOrder;          // boxes per axis this length holds
-  __shared__ float2 lds[2 * RG * F];
+  __shared__ float2 lds[2 * RG * FftPad<F>::kStride];
   __shared__ float2 tws[F];
   __shared__ float ps[NB * kLgSums];
   const int m = sc->lg_nodes;
@@ -610,8 +615,8 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
         b = make_float2(v2, 0.0f);
         m2[(by * kLgOrder + r) * m + x] = v3;
       }
-      lds[(2 * rr) * F + x] = a;
-      lds[(2 * rr + 1) * F + x] = b;
+      lds[fft_at<F>(2 * rr, x)] = a;
+      lds[fft_at<F>(2 * rr + 1, x)] = b;
     }
     __syncthreads();
     fft_lds<F, 2 * RG, S::NT, false, 1>(lds, tws);
@@ -620,13 +625,13 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
       const int kx = e - rr * S::H;
       const int y = by * kLgOrder + r0 + rr;  // < m
       const int mk = kx == 0 ? 0 : F - kx;
-      const float2 a = lds[(2 * rr) * F + kx];
-      const float2 am = conjf2(lds[(2 * rr) * F + mk]);
+      const float2 a = lds[fft_at<F>(2 * rr, kx)];
+      const float2 am = conjf2(lds[fft_at<F>(2 * rr, mk)]);
       const float2 sa = cadd(a, am), da = csub(a, am);
       const int at = y * S::H + kx;
       rows[at] = cscale(sa, 0.5f);
       rows[plane + at] = make_float2(0.5f * da.y, -0.5f * da.x);
-      rows[2 * plane + at] = lds[(2 * rr + 1) * F + kx];
+      rows[2 * plane + at] = lds[fft_at<F>(2 * rr + 1, kx)];
     }
     __syncthreads();  // lds reused by the next batch
   }
@@ -642,7 +647,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
 // inverse transforms, rows y < m written back row-major.  A padding block
 // (col_block) writes zero partial sums.
 template <int F>
-__global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceScalars* sc,
+__global__ __launch_bounds__(LgShape<F>::NTW) void k_lg_conv_cols(const DeviceScalars* sc,
                                                                  const float2* __restrict__ rows_in,
                                                                  const float2* __restrict__ k_hat,
                                                                  const float2* __restrict__ tw,
@@ -652,7 +657,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
   using S = LgShape<F>;
   constexpr int C = S::CC;
   constexpr int HH = S::H * S::H;
-  __shared__ float2 lds[3 * C * F];
+  __shared__ float2 lds[3 * C * FftPad<F>::kStride];
   __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
   const int cb = col_block(static_cast<int>(blockIdx.x), (S::H + C - 1) / C);
@@ -665,8 +670,8 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
     return;
   }
   const int col0 = cb * C;
-  stage_twiddles<F, S::NT>(tws, tw);
-  for (int e = threadIdx.x; e < C * F; e += S::NT) {
+  stage_twiddles<F, S::NTW>(tws, tw);
+  for (int e = threadIdx.x; e < C * F; e += S::NTW) {
     const int c = e / F;
     const int y = e - c * F;
     const int kx = col0 + c;
@@ -674,13 +679,13 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
     const long long at = static_cast<long long>(y) * S::H + kx;
 #pragma unroll
     for (int ch = 0; ch < 3; ++ch) {
-      lds[(ch * C + c) * F + y] = live ? rows_in[ch * plane + at] : make_float2(0.0f, 0.0f);
+      lds[fft_at<F>(ch * C + c, y)] = live ? rows_in[ch * plane + at] : make_float2(0.0f, 0.0f);
     }
   }
   __syncthreads();
-  fft_lds<F, 3 * C, S::NT, false, 1>(lds, tws);
+  fft_lds<F, 3 * C, S::NTW, false, 1>(lds, tws);
   double s1 = 0.0, s3 = 0.0, s4 = 0.0;
-  for (int e = threadIdx.x; e < C * F; e += S::NT) {
+  for (int e = threadIdx.x; e < C * F; e += S::NTW) {
     const int c = e / F;
     const int ky = e - c * F;
     const int kx = col0 + c;
@@ -693,9 +698,9 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
     const float k1 = kk2.y;
     const float cx = cc.x;
     const float cy = up ? cc.y : -cc.y;
-    float2& v0 = lds[(0 * C + c) * F + ky];
-    float2& v1 = lds[(1 * C + c) * F + ky];
-    float2& v2 = lds[(2 * C + c) * F + ky];
+    float2& v0 = lds[fft_at<F>(0 * C + c, ky)];
+    float2& v1 = lds[fft_at<F>(1 * C + c, ky)];
+    float2& v2 = lds[fft_at<F>(2 * C + c, ky)];
     const float2 m0 = v0, mx = v1, my = v2;
     const float2 im0 = mul_i(m0);  // i M0
     const double wk = (kx == 0 || kx == S::G) ? 1.0 : 2.0;
@@ -713,19 +718,19 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
     v2 = csub(cscale(im0, cy), cscale(my, kk));
   }
   __syncthreads();
-  fft_lds<F, 3 * C, S::NT, true, 1>(lds, tws);
-  for (int e = threadIdx.x; e < C * S::G; e += S::NT) {
+  fft_lds<F, 3 * C, S::NTW, true, 1>(lds, tws);
+  for (int e = threadIdx.x; e < C * S::G; e += S::NTW) {
     const int c = e / S::G;
     const int y = e - c * S::G;
     const int kx = col0 + c;
     if (y >= m || kx >= S::H) continue;
     const long long at = static_cast<long long>(y) * S::H + kx;
 #pragma unroll
-    for (int ch = 0; ch < 3; ++ch) rows_out[ch * plane + at] = lds[(ch * C + c) * F + y];
+    for (int ch = 0; ch < 3; ++ch) rows_out[ch * plane + at] = lds[fft_at<F>(ch * C + c, y)];
   }
-  s1 = block_sum<S::NT>(s1);
-  s3 = block_sum<S::NT>(s3);
-  s4 = block_sum<S::NT>(s4);
+  s1 = block_sum<S::NTW>(s1);
+  s3 = block_sum<S::NTW>(s3);
+  s4 = block_sum<S::NTW>(s4);
   if (threadIdx.x == 0) {
     zpart[3 * blockIdx.x] = s1;
     zpart[3 * blockIdx.x + 1] = s3;
@@ -738,7 +743,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_conv_cols(const DeviceSca
 // potentials for x < m scaled by 1/F^2 and stored per node as (phi0, xi_x,
 // xi_y, 0); per-block sums of m2 phi0 in fp64.
 template <int F>
-__global__ __launch_bounds__(LgShape<F>::NT) void k_lg_inverse_rows(const DeviceScalars* sc,
+__global__ __launch_bounds__(LgShape<F>::NTW) void k_lg_inverse_rows(const DeviceScalars* sc,
                                                                     const float2* __restrict__ rows, long long plane,
                                                                     const float* __restrict__ m2,
                                                                     const float2* __restrict__ tw,
@@ -746,14 +751,14 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_inverse_rows(const Device
                                                                     double* __restrict__ partial) {
   chain_priority();
   using S = LgShape<F>;
-  __shared__ float2 lds[2 * S::CR * F];
+  __shared__ float2 lds[2 * S::CR * FftPad<F>::kStride];
   __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
   const int row0 = blockIdx.x * S::CR;
   double acc = 0.0;
   if (row0 < m) {  // uniform over the block
-    stage_twiddles<F, S::NT>(tws, tw);
-    for (int e = threadIdx.x; e < S::CR * F; e += S::NT) {
+    stage_twiddles<F, S::NTW>(tws, tw);
+    for (int e = threadIdx.x; e < S::CR * F; e += S::NTW) {
       const int r = e / F;
       const int kx = e - r * F;
       const int y = row0 + r;
@@ -770,25 +775,25 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_inverse_rows(const Device
         u = cadd(a, mul_i(b));
         v = c;
       }
-      lds[(2 * r) * F + kx] = u;
-      lds[(2 * r + 1) * F + kx] = v;
+      lds[fft_at<F>(2 * r, kx)] = u;
+      lds[fft_at<F>(2 * r + 1, kx)] = v;
     }
     __syncthreads();
-    fft_lds<F, 2 * S::CR, S::NT, true, 1>(lds, tws);
+    fft_lds<F, 2 * S::CR, S::NTW, true, 1>(lds, tws);
     const float scale = 1.0f / (static_cast<float>(F) * static_cast<float>(F));
-    for (int e = threadIdx.x; e < S::CR * S::G; e += S::NT) {
+    for (int e = threadIdx.x; e < S::CR * S::G; e += S::NTW) {
       const int r = e / S::G;
       const int x = e - r * S::G;
       const int y = row0 + r;
       if (y >= m || x >= m) continue;
-      const float2 u = cscale(lds[(2 * r) * F + x], scale);
-      const float vx = lds[(2 * r + 1) * F + x].x * scale;
+      const float2 u = cscale(lds[fft_at<F>(2 * r, x)], scale);
+      const float vx = lds[fft_at<F>(2 * r + 1, x)].x * scale;
       const int at = y * m + x;
       field[at] = make_float4(u.x, u.y, vx, 0.0f);
       acc += static_cast<double>(m2[at]) * static_cast<double>(u.x);
     }
   }
-  acc = block_sum<S::NT>(acc);
+  acc = block_sum<S::NTW>(acc);
   if (threadIdx.x == 0) partial[blockIdx.x] = acc;
 }
 
@@ -841,7 +846,7 @@ hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const 
   static_assert(col_launch((S::H + S::CC - 1) / S::CC) <= kLgMaxSpecBlocks, "a partial-sum slot per column block");
   switch (which) {
     case 0:
-      k_lg_kernel_rows<F><<<kblocks, S::NT, 0, stream>>>(sc, tw, ib.k_rows);
+      k_lg_kernel_rows<F><<<kblocks, S::NTW, 0, stream>>>(sc, tw, ib.k_rows);
       break;
     case 2:
       k_lg_kernel_cols<F><<<col_launch(kblocks), S::NT, 0, stream>>>(sc, ib.k_rows, tw, ib.k_cols);
@@ -852,10 +857,10 @@ hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const 
                                                                   plane);
       break;
     case 5:
-      k_lg_conv_cols<F><<<cblocks, S::NT, 0, stream>>>(sc, ib.spec_a, ib.k_cols, tw, ib.spec_b, plane, spec_part);
+      k_lg_conv_cols<F><<<cblocks, S::NTW, 0, stream>>>(sc, ib.spec_a, ib.k_cols, tw, ib.spec_b, plane, spec_part);
       break;
     case 7:
-      k_lg_inverse_rows<F><<<rblocks, S::NT, 0, stream>>>(sc, ib.spec_b, plane, ib.m2, tw, ib.field, row_part);
+      k_lg_inverse_rows<F><<<rblocks, S::NTW, 0, stream>>>(sc, ib.spec_b, plane, ib.m2, tw, ib.field, row_part);
       k_lg_finalize_z<<<1, 256, 0, stream>>>(spec_part, cblocks, row_part, rblocks, n, F, sc);
       break;
 
