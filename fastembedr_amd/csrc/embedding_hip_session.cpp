@@ -1189,6 +1189,8 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   s->n = n;
   s->k = k;
   const int g = resolve_grid_size(n, grid_size);
+  // (device-scope or no system fence on these events measured no faster:
+  // 3646 / 3578 it/s against 3671 at config 2)
   const unsigned ev_flags = hipEventDisableTiming;
   if (!hip_ok(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate") ||
       !hip_ok(hipStreamCreateWithFlags(&s->side_attr, hipStreamNonBlocking), "hipStreamCreate") ||

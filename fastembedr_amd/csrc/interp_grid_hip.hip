@@ -48,14 +48,15 @@
 //   k_lg_kernel_rows/cols spectra of K, K1 (real, even) and Kv (imaginary,
 //                         odd in its own axis), a quadrant each, two real
 //                         sequences per complex transform
-//   k_lg_charge_rows      one workgroup per row of boxes: each box's entries
-//                         (and the rare straggler sums) summed, combined into
-//                         its 9 nodes x 4 moments (m2 stored), then
-//                         m0 + i m1x and m1y per complex row transform, half
-//                         spectra kept
+//   k_lg_charge_rows      one workgroup per node row: the entries (and the
+//                         rare straggler sums) of each box of its box row
+//                         summed, combined into the row's node moments (m2
+//                         stored), then m0 + i m1x and m1y per complex row
+//                         transform, half spectra kept
 //   k_lg_conv_cols        forward column transforms, spectral products for
 //                         phi0, xi_x, xi_y and the spectral sums of Z, inverse
-//                         column transforms, in one pass
+//                         column transforms, in one pass; clears the box
+//                         counts and straggler sums for the next spread
 //   k_lg_inverse_rows     inverse row transforms, potentials per node and the
 //                         m2 phi0 sum
 //   k_lg_finalize_z       Z and its reciprocal
@@ -280,12 +281,13 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_order_keys(const float2* __re
 // the next of its box's entries (an integer atomic on the box's count; K
 // entries per box, K = min(kLgMaxPerBox, kLgEntryPool / boxes), so that few
 // boxes get many) and stores its sums there with plain stores.  The charge
-// row transform (k_lg_charge_rows, one workgroup per row of boxes) then sums
-// each box's entries and combines them into its 9 nodes x 4 moments.  Float
+// row transform (k_lg_charge_rows, one workgroup per node row) then sums
+// each box's entries and combines them into the nodes' moments.  Float
 // atomics in global memory (they resolve beyond the XCDs' L2s and cost far
 // more than the LDS path) are left for the rare exceptions, which go to a
-// straggler array of power sums per box that the row transform adds and
-// clears (only for boxes flagged in their count word): a run whose chunk
+// straggler array of power sums per box that the row transform adds (only
+// for boxes flagged in their count word; the convolution pass clears the
+// counts and those sums): a run whose chunk
 // already fills its table (more than kLgTable boxes in kLgChunk points) and a
 // box with more than K contributing workgroups.  Any permutation gives
 // the same charges up to the order of the fp32 adds; a spatial one keeps runs
@@ -298,8 +300,8 @@ static_assert(kLgChunk == kLgSpreadChunk, "the host sizes the spread's scratch b
 static_assert(kLgTable == kLgThreads, "one table slot per thread in the flush");
 static_assert(kLgSums == kLgSumsPerBox, "the host sizes the sums by kLgSumsPerBox");
 // A box's count word: the slots listed (low bits) and a flag set when
-// straggler sums were added for the box (the gather reads and clears those
-// only then).
+// straggler sums were added for the box (the row transform reads them and
+// the convolution pass clears them only then).
 constexpr int kLgStraggled = 1 << 30;
 constexpr int kLgCountMask = kLgStraggled - 1;
 
@@ -558,9 +560,11 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
 #pragma clang fp contract(off)
   chain_priority();
   using S = LgShape<F>;
-  // one node row per transform batch: the workgroup needs little LDS (29 KB
-  // at F = 768), so it finds room on CUs that hold the attraction's
-  // workgroups (49 KB each, two or three per CU) when the two overlap
+  // one node row per workgroup (blockIdx.y): three workgroups per row of
+  // boxes, each summing the row's boxes itself, so that the few, long
+  // workgroups of one per box row do not trail beside the attraction; the
+  // box counts and straggler sums are cleared by the convolution pass, once
+  // all three have read them
   constexpr int RG = 1;
   constexpr int NB = F / 2 / kLgOrder;          // boxes per axis this length holds
   __shared__ float2 lds[2 * RG * FftPad<F>::kStride];
@@ -579,19 +583,14 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
     const int b = by * nb + bx;
     const int word = box_count[b];
     const int cnt = min(word & kLgCountMask, per);
-    float sum = 0.0f;
-    if ((word & kLgStraggled) != 0) {
-      const std::size_t at = static_cast<std::size_t>(b) * kLgSums + e;
-      sum = straggler[at];
-      straggler[at] = 0.0f;
-    }
     const float* src = entries + static_cast<std::size_t>(b) * per * kLgSums + e;
+    float sum = (word & kLgStraggled) != 0 ? straggler[static_cast<std::size_t>(b) * kLgSums + e] : 0.0f;
     for (int k = 0; k < cnt; ++k) sum += src[static_cast<std::size_t>(k) * kLgSums];
     ps[q] = sum;
   }
-  __syncthreads();  // every count of the row read
-  for (int bx = threadIdx.x; bx < nb; bx += S::NT) box_count[by * nb + bx] = 0;
-  for (int r0 = 0; r0 < kLgOrder; r0 += RG) {
+  __syncthreads();
+  {
+    const int r0 = blockIdx.y;
     for (int e = threadIdx.x; e < RG * F; e += S::NT) {
       const int rr = e / F;
       const int x = e - rr * F;
@@ -633,7 +632,6 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
       rows[plane + at] = make_float2(0.5f * da.y, -0.5f * da.x);
       rows[2 * plane + at] = lds[fft_at<F>(2 * rr + 1, kx)];
     }
-    __syncthreads();  // lds reused by the next batch
   }
 }
 
@@ -652,7 +650,9 @@ __global__ __launch_bounds__(LgShape<F>::NTW) void k_lg_conv_cols(const DeviceSc
                                                                  const float2* __restrict__ k_hat,
                                                                  const float2* __restrict__ tw,
                                                                  float2* __restrict__ rows_out, long long plane,
-                                                                 double* __restrict__ zpart) {
+                                                                 double* __restrict__ zpart,
+                                                                 int* __restrict__ box_count,
+                                                                 float* __restrict__ straggler) {
   chain_priority();
   using S = LgShape<F>;
   constexpr int C = S::CC;
@@ -660,6 +660,19 @@ __global__ __launch_bounds__(LgShape<F>::NTW) void k_lg_conv_cols(const DeviceSc
   __shared__ float2 lds[3 * C * FftPad<F>::kStride];
   __shared__ float2 tws[F];
   const int m = sc->lg_nodes;
+  {
+    // the spread's box counts and straggler sums, read by every charge-row
+    // workgroup of the box, start the next spread at zero
+    const int boxes = sc->lg_boxes * sc->lg_boxes;
+    for (int b = static_cast<int>(blockIdx.x * S::NTW + threadIdx.x); b < boxes;
+         b += static_cast<int>(gridDim.x * S::NTW)) {
+      if ((box_count[b] & kLgStraggled) != 0) {
+#pragma unroll
+        for (int e = 0; e < kLgSums; ++e) straggler[static_cast<std::size_t>(b) * kLgSums + e] = 0.0f;
+      }
+      box_count[b] = 0;
+    }
+  }
   const int cb = col_block(static_cast<int>(blockIdx.x), (S::H + C - 1) / C);
   if (cb < 0) {  // whole block
     if (threadIdx.x == 0) {
@@ -852,12 +865,13 @@ hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const 
       k_lg_kernel_cols<F><<<col_launch(kblocks), S::NT, 0, stream>>>(sc, ib.k_rows, tw, ib.k_cols);
       break;
     case 3:
-      k_lg_charge_rows<F><<<F / 2 / kLgOrder, S::NT, 0, stream>>>(sc, lg_boxes_bound(F) * kLgOrder, ib.entries,
+      k_lg_charge_rows<F><<<dim3(F / 2 / kLgOrder, kLgOrder), S::NT, 0, stream>>>(sc, lg_boxes_bound(F) * kLgOrder, ib.entries,
                                                                   ib.box_count, ib.straggler, ib.m2, tw, ib.spec_a,
                                                                   plane);
       break;
     case 5:
-      k_lg_conv_cols<F><<<cblocks, S::NTW, 0, stream>>>(sc, ib.spec_a, ib.k_cols, tw, ib.spec_b, plane, spec_part);
+      k_lg_conv_cols<F><<<cblocks, S::NTW, 0, stream>>>(sc, ib.spec_a, ib.k_cols, tw, ib.spec_b, plane, spec_part,
+                                                         ib.box_count, ib.straggler);
       break;
     case 7:
       k_lg_inverse_rows<F><<<rblocks, S::NTW, 0, stream>>>(sc, ib.spec_b, plane, ib.m2, tw, ib.field, row_part);
