@@ -310,6 +310,17 @@ __device__ __forceinline__ int lg_entries_per_box(int nb) {
   return max(1, min(kLgMaxPerBox, static_cast<int>(kLgEntryPool / (static_cast<long long>(nb) * nb))));
 }
 
+// Column block of launch block b when `blocks` column blocks are spread over
+// col_launch(blocks) launch blocks: the blocks of XCD x (b % kLgColXcds,
+// the hardware's round-robin placement) take the x-th contiguous range, so
+// the columns of one cache line are read and written through one L2.  -1: a
+// padding block with no columns.
+__device__ __forceinline__ int col_block(int b, int blocks) {
+  const int per = (blocks + kLgColXcds - 1) / kLgColXcds;
+  const int c = (b % kLgColXcds) * per + b / kLgColXcds;
+  return c < blocks ? c : -1;
+}
+constexpr int col_launch(int blocks) { return (blocks + kLgColXcds - 1) / kLgColXcds * kLgColXcds; }
 __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restrict__ y_stored,
                                                           const int* __restrict__ order, DeviceScalars* sc, int n,
                                                           int max_nodes, float* __restrict__ entries,
@@ -331,8 +342,15 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
   tkey[threadIdx.x] = -1;
   for (int e = threadIdx.x; e < kLgTable * kLgSums; e += kLgThreads) tval[e] = 0.0f;
   __syncthreads();
-  // a wave's steps are consecutive points of the order
-  const long long base = static_cast<long long>(blockIdx.x) * kLgChunk + static_cast<long long>(wave) * kLgSteps * 64;
+  // a wave's steps are consecutive points of the order; the chunks of one
+  // XCD are one contiguous range of the order (col_block), a compact region
+  // of the layout, so the cache lines of y that its points share are fetched
+  // into that XCD's L2 once (round-robin chunks fetched each line into
+  // several L2s: 75 MB read per spread at config 2)
+  const int chunks = (n + kLgChunk - 1) / kLgChunk;
+  const int chunk = col_block(static_cast<int>(blockIdx.x), chunks);
+  const long long base = chunk < 0 ? static_cast<long long>(n)
+                                   : static_cast<long long>(chunk) * kLgChunk + static_cast<long long>(wave) * kLgSteps * 64;
   for (int k = 0; k < kLgSteps; ++k) {
     const long long i = base + k * 64 + lane;
     float a[kLgSums];
@@ -407,17 +425,6 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
 // block so that small transforms still fill a workgroup.
 // ---------------------------------------------------------------------------
 
-// Column block of launch block b when `blocks` column blocks are spread over
-// col_launch(blocks) launch blocks: the blocks of XCD x (b % kLgColXcds,
-// the hardware's round-robin placement) take the x-th contiguous range, so
-// the columns of one cache line are read and written through one L2.  -1: a
-// padding block with no columns.
-__device__ __forceinline__ int col_block(int b, int blocks) {
-  const int per = (blocks + kLgColXcds - 1) / kLgColXcds;
-  const int c = (b % kLgColXcds) * per + b / kLgColXcds;
-  return c < blocks ? c : -1;
-}
-constexpr int col_launch(int blocks) { return (blocks + kLgColXcds - 1) / kLgColXcds * kLgColXcds; }
 template <int F>
 struct LgShape {
   static constexpr int G = F / 2;
@@ -889,7 +896,7 @@ hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const 
 hipError_t launch_interp_spread(const float2* y_stored, const int* order, DeviceScalars* sc, InterpBuffers& ib, int n,
                                 int fft_len, hipStream_t stream) {
   const int max_nodes = lg_boxes_bound(fft_len) * kLgOrder;
-  const int blocks = lg_spread_blocks(n);
+  const int blocks = col_launch(lg_spread_blocks(n));
   k_lg_spread<<<blocks, kLgThreads, 0, stream>>>(y_stored, order, sc, n, max_nodes, ib.entries, ib.box_count,
                                                   ib.straggler);
   return hipGetLastError();
