@@ -29,6 +29,7 @@ import glob
 import json
 import re
 import sys
+import zlib
 
 _OURS = re.compile(r"fehip::(?:\(anonymous namespace\)::)?(\w+)(<[^()]*>)?")
 
@@ -43,7 +44,9 @@ def short_name(name: str) -> str:
         return m.group(1) + (m.group(2) or "")
     m = _ROCPRIM.search(name)
     if m:
-        return "rocprim:" + m.group(1)
+        # rocPRIM's kernels share a few stems (trampoline_kernel): the full
+        # name's checksum tells the instantiations apart
+        return f"rocprim:{m.group(1)}#{zlib.crc32(name.encode()) & 0xffffff:06x}"
     return name.split("(")[0][:60]
 
 
