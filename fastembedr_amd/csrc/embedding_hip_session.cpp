@@ -205,16 +205,21 @@ struct fastembedr_hip_tsne {
   // issue priority (chain_priority).  Set by FASTEMBEDR_HIP_ATTRACT_SHARED_PER_CU,
   // else (attract_share_auto) after each tile build from the tiled P's mean
   // run length, which sets the attraction's cost per entry against the
-  // chain's per point: 2 at 16K slots per run or more, 2.5 at 8K or fewer,
-  // linear between (late window, interleaved repeats: config 2, runs of 25k
-  // slots, interpolation grid: 1 per CU 3178 it/s, 1.25 3166, 1.5 3507, 1.75
-  // 3535, 2 3584, 2.25 3376, 2.5 3192; bilinear grid: 1.5 3500, 1.75 3611,
-  // 2 3731, 2.5 3624; config 4, runs of 7.4k slots: 1.5 685, 2 781, 2.5 830,
-  // 2.75 835, 3 813).  Alone it takes one workgroup per row block.
+  // chain's per point.  Bilinear grid: 2 at 16K slots per run or more, 2.5 at
+  // 8K or fewer, linear between (config 2, runs of 25k slots, late window:
+  // 2 3906 / 3877 it/s, 2.5 3735 / 3764).  Interpolation grid, whose chain
+  // now ends before the attraction: 2.5 at 16K or more, 2.75 at 8K or fewer
+  // (config 2: 2 3755 / 3774, 2.25 3767, 2.5 3790 / 3800, 3 3535; config 4,
+  // runs of 7.4k slots: 2.5 857, 2.75 880, 3 876).  Alone it takes one
+  // workgroup per row block.
   double attract_shared_per_cu = 2.0;
   bool attract_share_auto = true;
-  double attract_share_base = 2.0;  // from the last tile build
-  double attract_share() const { return attract_share_auto ? attract_share_base : attract_shared_per_cu; }
+  double attract_share_base = 2.0;     // bilinear grid, from the last tile build
+  double attract_share_base_lg = 2.5;  // interpolation grid, same
+  double attract_share() const {
+    if (!attract_share_auto) return attract_shared_per_cu;
+    return repulsion == FASTEMBEDR_HIP_REPULSION_LAGRANGE ? attract_share_base_lg : attract_share_base;
+  }
   // Workgroups per CU of the helper launch that joins the attraction on the
   // main stream once the repulsion chain is done, taking over the row blocks
   // still unclaimed (FASTEMBEDR_HIP_ATTRACT_HELPER_PER_CU; 0: none).  The
@@ -556,6 +561,7 @@ bool ensure_tiles(fastembedr_hip_tsne* s, hipStream_t st) {
   }
   const double run = count > 0 ? static_cast<double>(total) / count : 0.0;
   s->attract_share_base = std::clamp(2.5 - (run - 8192.0) / 16384.0, 2.0, 2.5);
+  s->attract_share_base_lg = std::clamp(2.75 - (run - 8192.0) / 32768.0, 2.5, 2.75);
   return true;
 }
 
