@@ -945,10 +945,9 @@ __global__ __launch_bounds__(kPointThreads) void k_update(const float2* y_cur,
                                                               ? s.exact_z
                                                               : static_cast<double>(FLT_MIN)))
                               : 0.0f;
-  for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += gridDim.x * kPointThreads) {
-    float2 yi = y_cur[i];
-    if (LG && MODE != kModeGradientExact) yi = make_float2(yi.x - s.shift_x, yi.y - s.shift_y);
-    const float2 a = attr[i];
+  // the gradient of a point at yi (centred for the interpolation grid) with
+  // attraction a
+  auto gradient_at = [&](int i, float2 yi, float2 a) {
     float gx, gy;
     if (MODE == kModeGradientExact) {
       const float2 r = exact_rep[i];
@@ -998,12 +997,14 @@ __global__ __launch_bounds__(kPointThreads) void k_update(const float2* y_cur,
     }
     gx += a.x;
     gy += a.y;
+    return make_float2(gx, gy);
+  };
+  // the update of point i from its gradient, gains and update
+  auto apply = [&](int i, float2 yi, float gx, float gy, float2 gn, float2 u) {
     if (MODE != kModeUpdate) {
       grad_out[i] = make_float2(gx, gy);
-      continue;
+      return;
     }
-    float2 gn = gains[i];
-    float2 u = update[i];
     if (sign0(u.x) != sign0(gx)) {
       gn.x += 0.2f;
     } else {
@@ -1037,6 +1038,33 @@ __global__ __launch_bounds__(kPointThreads) void k_update(const float2* y_cur,
     st.max_y = fmaxf(st.max_y, yn.y);
     st.sum_x += static_cast<double>(yn.x);
     st.sum_y += static_cast<double>(yn.y);
+  };
+  // Two points per thread and pass: every load of both (the interpolation
+  // grid's nine node fields included) is issued before either is stored,
+  // so their latencies overlap (y_out may be y_cur: each point reads its own
+  // entries before they are written)
+  const int stride = static_cast<int>(gridDim.x) * kPointThreads;
+  for (int i = blockIdx.x * kPointThreads + threadIdx.x; i < n; i += 2 * stride) {
+    const int j = i + stride < n ? i + stride : i;
+    float2 yi = y_cur[i];
+    float2 yj = y_cur[j];
+    if (LG && MODE != kModeGradientExact) {
+      yi = make_float2(yi.x - s.shift_x, yi.y - s.shift_y);
+      yj = make_float2(yj.x - s.shift_x, yj.y - s.shift_y);
+    }
+    const float2 ai = attr[i];
+    const float2 aj = attr[j];
+    float2 gni = make_float2(0.0f, 0.0f), ui = gni, gnj = gni, uj = gni;
+    if (MODE == kModeUpdate) {
+      gni = gains[i];
+      ui = update[i];
+      gnj = gains[j];
+      uj = update[j];
+    }
+    const float2 gi = gradient_at(i, yi, ai);
+    const float2 gj = gradient_at(j, yj, aj);
+    apply(i, yi, gi.x, gi.y, gni, ui);
+    if (j != i) apply(j, yj, gj.x, gj.y, gnj, uj);
   }
   if (MODE == kModeUpdate) publish_stats<kPointThreads>(st, partial);
 }
