@@ -524,7 +524,11 @@ __global__ __launch_bounds__(NT, MINB) void k_attract_tiles_seg(
   __shared__ float2 ys[kTileCols];
   __shared__ float2 yr[kTileRows];
   __shared__ float2 acc[kTileRows];
-  __shared__ int claimed;
+  // the claimed row block is passed through the first word of the column
+  // tile, which is free between row blocks (no LDS beyond the three arrays:
+  // 48 KB exactly, so that three workgroups leave a CU 16 KB for the
+  // transforms that run beside them)
+  int& claimed = *reinterpret_cast<int*>(ys);
   const int xcd = static_cast<int>(blockIdx.x) % xcds;
   const int per_xcd = (row_blocks + xcds - 1) / xcds;
   const int first = xcd * per_xcd;

@@ -178,9 +178,9 @@ __device__ __forceinline__ void block_exclusive_scan2(int (&a)[PER], int (&b)[PE
 // by e^{-2 pi i r k / (Ns R)} with k = j mod Ns, and writes their R-point DFT
 // (taken in registers) to (j - k) R + k + r Ns, so the result is in natural
 // order.  Every stage reads its inputs to registers, barriers, then writes.
-// Twiddles e^{-2 pi i j / F} are staged in LDS from the global table
-// (computed in fp64 on the host); INV conjugates them and leaves the result
-// unscaled.
+// Twiddles e^{-2 pi i j / F}, j < F / 2, are staged in LDS from the global
+// table (computed in fp64 on the host), the other half taken by negation;
+// INV conjugates them and leaves the result unscaled.
 //
 // LDS layout: sequence q starts at q * FftPad<F>::kStride and element i sits
 // at i + i / 32 (fft_at): one pad element per 32 keeps the strided writes of
@@ -196,15 +196,21 @@ __device__ __forceinline__ int fft_at(int q, int i) {
   return q * FftPad<F>::kStride + fft_pad(i);
 }
 
-template <bool INV>
+// e^{-2 pi i m / F} (forward) or its conjugate, m < F, from the half table
+// tw[j] = e^{-2 pi i j / F}, j < F / 2 (e^{-2 pi i (j + F/2) / F} = -tw[j]).
+template <bool INV, int F>
 __device__ __forceinline__ float2 twiddle(const float2* __restrict__ tw, int m) {
-  const float2 w = tw[m];
-  return INV ? make_float2(w.x, -w.y) : w;
+  const bool hi = m >= F / 2;
+  const float2 w = tw[hi ? m - F / 2 : m];
+  const float sx = hi ? -1.0f : 1.0f;
+  return make_float2(sx * w.x, (INV ? -sx : sx) * w.y);
 }
 
-// Copies the F twiddles e^{-2 pi i j / F} of the global table into LDS (the
-// caller's next barrier publishes them); transforms then read their twiddles
-// from LDS (TWS = 1) instead of from the cache hierarchy.
+// Copies the F / 2 twiddles e^{-2 pi i j / F}, j < F / 2, of the global table
+// into LDS (the caller's next barrier publishes them; twiddle() makes the
+// other half by negation); transforms then read their twiddles from LDS
+// (TWS = 1) instead of from the cache hierarchy.  Half a table keeps the
+// transforms' LDS small enough to fit beside other kernels' workgroups.
 template <int F, int NT>
 __device__ __forceinline__ void stage_twiddles(float2* lds_tw, const float2* __restrict__ tw) {
   constexpr bool kR3 = F % 3 == 0;
@@ -212,7 +218,7 @@ __device__ __forceinline__ void stage_twiddles(float2* lds_tw, const float2* __r
   constexpr int LEN = kR3 ? kTwiddlePow3 : kTwiddlePow2;
   static_assert(LEN % F == 0, "F divides its part of the twiddle table");
   constexpr int STRIDE = LEN / F;
-  for (int j = threadIdx.x; j < F; j += NT) lds_tw[j] = tw[BASE + j * STRIDE];
+  for (int j = threadIdx.x; j < F / 2; j += NT) lds_tw[j] = tw[BASE + j * STRIDE];
 }
 
 template <int F>
@@ -366,7 +372,7 @@ __device__ __forceinline__ void fft_stage(float2* s, const float2* __restrict__ 
         const int kk = static_cast<int>(static_cast<unsigned int>(j) % NS);
         const int step = (F / (R * NS)) * kk * TWS;
 #pragma unroll
-        for (int r = 1; r < R; ++r) v[b][r] = cmul(v[b][r], twiddle<INV>(tw, r * step));
+        for (int r = 1; r < R; ++r) v[b][r] = cmul(v[b][r], twiddle<INV, F * TWS>(tw, r * step));
       }
       dft_r<R, INV>(v[b]);
     }
@@ -400,7 +406,7 @@ __device__ __forceinline__ void fft_stages_pow2(float2* s, const float2* __restr
   }
 }
 
-// tw holds e^{-2 pi i j / (F * TWS)} for j < F * TWS (staged in LDS by
+// tw holds e^{-2 pi i j / (F * TWS)} for j < F * TWS / 2 (staged in LDS by
 // stage_twiddles: TWS = 1).  s holds NSEQ sequences in the fft_at layout.
 template <int F, int NSEQ, int NT, bool INV, int TWS = 1>
 __device__ __forceinline__ void fft_lds(float2* s, const float2* __restrict__ tw) {

@@ -587,7 +587,7 @@ __global__ __launch_bounds__(256) void k_kernel_rows(const DeviceScalars* sc, co
   chain_priority();
   using S = Shape<F>;
   __shared__ float2 lds[S::KROWS * FftPad<F>::kStride];
-  __shared__ float2 tws[F];
+  __shared__ float2 tws[F / 2];
   stage_twiddles<F, S::NT>(tws, tw);
   const float h = sc->h;
   const int row0 = blockIdx.x * S::KROWS;
@@ -624,7 +624,7 @@ __global__ __launch_bounds__(256) void k_kernel_cols(const float2* __restrict__ 
   chain_priority();
   using S = Shape<F>;
   __shared__ float2 lds[S::KROWS * FftPad<F>::kStride];
-  __shared__ float2 tws[F];
+  __shared__ float2 tws[F / 2];
   stage_twiddles<F, S::NT>(tws, tw);
   const int col0 = blockIdx.x * S::KROWS;
   for (int e = threadIdx.x; e < S::KROWS * F; e += S::NT) {
@@ -660,7 +660,7 @@ __global__ __launch_bounds__(256) void k_charge_rows(const float* __restrict__ m
   chain_priority();
   using S = Shape<F>;
   __shared__ float2 lds[2 * S::CROWS * FftPad<F>::kStride];
-  __shared__ float2 tws[F];
+  __shared__ float2 tws[F / 2];
   stage_twiddles<F, S::NT>(tws, tw);
   const int row0 = blockIdx.x * S::CROWS;
   for (int e = threadIdx.x; e < S::CROWS * F; e += S::NT) {
@@ -712,7 +712,7 @@ __global__ __launch_bounds__(256) void k_conv_cols(const float2* __restrict__ m_
   using S = Shape<F>;
   constexpr int C = S::CCOLS;
   __shared__ float2 lds[4 * C * FftPad<F>::kStride];
-  __shared__ float2 tws[F];
+  __shared__ float2 tws[F / 2];
   stage_twiddles<F, S::NT>(tws, tw);
   const int col0 = blockIdx.x * C;
   for (int e = threadIdx.x; e < C * F; e += S::NT) {
@@ -784,7 +784,7 @@ __global__ __launch_bounds__(256) void k_inverse_rows(const float2* __restrict__
   chain_priority();
   using S = Shape<F>;
   __shared__ float2 lds[2 * S::CROWS * FftPad<F>::kStride];
-  __shared__ float2 tws[F];
+  __shared__ float2 tws[F / 2];
   stage_twiddles<F, S::NT>(tws, tw);
   const int row0 = blockIdx.x * S::CROWS;
   for (int e = threadIdx.x; e < S::CROWS * F; e += S::NT) {

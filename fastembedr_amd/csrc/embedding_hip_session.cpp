@@ -207,11 +207,11 @@ struct fastembedr_hip_tsne {
   // run length, which sets the attraction's cost per entry against the
   // chain's per point.  Bilinear grid: 2 at 16K slots per run or more, 2.5 at
   // 8K or fewer, linear between (config 2, runs of 25k slots, late window:
-  // 2 3906 / 3877 it/s, 2.5 3735 / 3764).  Interpolation grid, whose chain
-  // now ends before the attraction: 2.5 at 16K or more, 2.75 at 8K or fewer
-  // (config 2: 2 3755 / 3774, 2.25 3767, 2.5 3790 / 3800, 3 3535; config 4,
-  // runs of 7.4k slots: 2.5 857, 2.75 880, 3 876).  Alone it takes one
-  // workgroup per row block.
+  // 2 3906 / 3877 it/s, 2.5 3735 / 3764).  Interpolation grid: 2 at 24K
+  // slots per run or more, 3 at 8K or fewer, linear between (config 2,
+  // late window: 1.5 3719, 1.75 3710 / 3722, 2 3811 / 3837 / 3823,
+  // 2.25 3773 / 3774, 2.5 3743; config 4, runs of 7.4k slots: 2.75 895 / 899,
+  // 3 919 / 916 / 918).  Alone it takes one workgroup per row block.
   double attract_shared_per_cu = 2.0;
   bool attract_share_auto = true;
   double attract_share_base = 2.0;     // bilinear grid, from the last tile build
@@ -250,6 +250,12 @@ struct fastembedr_hip_tsne {
   Arena lg_arena;
   fehip::InterpBuffers ib;
   int lg_last_fft = 0;       // FFT length of the last interpolation-grid iteration
+  // The spread's LDS table: the small one (fehip::kLgSmallTableBits) when
+  // the latest known box count leaves at least lg_dense_points points per
+  // box on average, so that a chunk of the spread order touches few boxes
+  // (FASTEMBEDR_HIP_SPREAD_DENSE: that threshold; 0 keeps the large table).
+  int lg_table_bits = fehip::kLgTableBits;
+  double lg_dense_points = 32.0;
   // The spread's point order (working indices sorted by position) is made
   // again every lg_order_period interpolation-grid iterations, on first use
   // and after a renumbering (stale), and for every gradient probe.  Any
@@ -284,7 +290,7 @@ struct fastembedr_hip_tsne {
   // (4.7 GB per session at config 2, piling up over sessions), which a
   // single-stream graph does not.
   struct IterGraph {
-    std::array<std::uint32_t, 14> key{};
+    std::array<std::uint32_t, 15> key{};
     hipGraphExec_t exec = nullptr;
     int seen = 0;
     unsigned long long last_use = 0;
@@ -561,7 +567,7 @@ bool ensure_tiles(fastembedr_hip_tsne* s, hipStream_t st) {
   }
   const double run = count > 0 ? static_cast<double>(total) / count : 0.0;
   s->attract_share_base = std::clamp(2.5 - (run - 8192.0) / 16384.0, 2.0, 2.5);
-  s->attract_share_base_lg = std::clamp(2.75 - (run - 8192.0) / 32768.0, 2.5, 2.75);
+  s->attract_share_base_lg = std::clamp(3.0 - (run - 8192.0) / 16384.0, 2.0, 3.0);
   return true;
 }
 
@@ -635,6 +641,13 @@ bool enqueue_attract_helper(fastembedr_hip_tsne* s, const float2* y_cur, float e
     return s->span_end(s->helper_span, s->stream);
   }
   return true;
+}
+
+// The spread's table for a layout of about `boxes` boxes per axis.
+void set_spread_table(fastembedr_hip_tsne* s, int boxes) {
+  const double per_box = static_cast<double>(s->n) / std::max(1.0, static_cast<double>(boxes) * boxes);
+  s->lg_table_bits =
+      s->lg_dense_points > 0.0 && per_box >= s->lg_dense_points ? fehip::kLgSmallTableBits : fehip::kLgTableBits;
 }
 
 // FFT length for an interpolation grid of `nodes` nodes per axis: the
@@ -856,7 +869,7 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
              fehip::kKLgSpread, "interp spread launch",
              [&] {
                return fehip::launch_interp_spread(s->y_a(), s->lg_order_period > 0 ? ib.order : nullptr, s->sc, ib,
-                                                  n, fft_len, chain);
+                                                  n, fft_len, s->lg_table_bits, chain);
              },
              chain) &&
          s->timed(
@@ -968,9 +981,10 @@ bool enqueue_iteration_graphed(fastembedr_hip_tsne* s, bool lg, int fft_len, con
     std::memcpy(&u, &v, sizeof(u));
     return u;
   };
-  const std::array<std::uint32_t, 14> key = {static_cast<std::uint32_t>(lg),
+  const std::array<std::uint32_t, 15> key = {static_cast<std::uint32_t>(lg),
                                              static_cast<std::uint32_t>(finalize),
                                              static_cast<std::uint32_t>(fft_len),
+                                             static_cast<std::uint32_t>(s->lg_table_bits),
                                              static_cast<std::uint32_t>(s->si),
                                              static_cast<std::uint32_t>(s->wi),
                                              static_cast<std::uint32_t>(s->attract_tiled),
@@ -1454,6 +1468,11 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   if (const char* v = std::getenv("FASTEMBEDR_HIP_UPDATE_ON_CHAIN")) s->update_on_chain = std::strcmp(v, "0") != 0;
   if (const char* v = std::getenv("FASTEMBEDR_HIP_MARK_LAYOUT")) s->mark_layout = std::strcmp(v, "0") != 0;
   if (const char* v = std::getenv("FASTEMBEDR_HIP_LG_ORDER_PERIOD")) s->lg_order_period = std::max(0, std::atoi(v));
+  if (const char* v = std::getenv("FASTEMBEDR_HIP_SPREAD_DENSE")) {
+    char* end = nullptr;
+    const double d = std::strtod(v, &end);
+    if (end != v && std::isfinite(d) && d >= 0.0) s->lg_dense_points = d;
+  }
   s->graph_capture = graph_capture_enabled();
   if (!alloc_working_buffers(s) || (s->attract_tiled && !alloc_tiles(s))) {
     delete s;
@@ -1702,7 +1721,7 @@ int fastembedr_hip_tsne_gradient(fastembedr_hip_tsne* s, float exaggeration, int
     s->lg_order_due = true;  // a probe's layout may be any: order it
     ok = ensure_interp(s) && write_interp_spec(s, fehip::kLgOrder) &&
          hip_ok(fehip::launch_stats(s->y_a(), s->n, s->gb.g, 0, s->partial, s->sc, s->stream), "stats launch") &&
-         read_interp_boxes(s, &boxes, &ring_seq) &&
+         read_interp_boxes(s, &boxes, &ring_seq) && (set_spread_table(s, boxes), true) &&
          enqueue_gradient_pieces(s, true, interp_fft_len(std::min(boxes * fehip::kLgOrder, fehip::kLgMaxNodes)),
                                  exaggeration, false) &&
          hip_ok(fehip::launch_update(fehip::kModeGradientGrid, s->y_a(), s->attr, nullptr, nullptr, nullptr, s->grad,
@@ -1832,6 +1851,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
           static_cast<long long>(known_boxes) + static_cast<long long>(std::ceil(growth * (it - known_it)));
       const int nodes = static_cast<int>(std::min<long long>(bound * fehip::kLgOrder, fehip::kLgMaxNodes));
       fft_len = interp_fft_len(nodes);
+      set_spread_table(s, known_boxes);
     }
     if (lg) {
       s->lg_order_due = s->lg_order_period > 0 && (s->lg_order_stale || s->lg_order_age >= s->lg_order_period);

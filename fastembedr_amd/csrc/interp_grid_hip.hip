@@ -272,8 +272,11 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_order_keys(const float2* __re
 // Per iteration, two kernels.  k_lg_spread: each workgroup takes kLgChunk
 // consecutive points of the spread order (`order`, working indices sorted by
 // position), so that its points fall into few boxes, and sums them in LDS,
-// in a table of kLgTable slots keyed by box (open addressing): every point is
-// centred and located, its 21 power sums (above) are summed with those of the
+// in a table of 2^TB slots keyed by box (open addressing; 256, or 64 where
+// the host expects dense boxes: 6 KB instead of 22 KB of LDS, so that a CU
+// that holds attraction workgroups still fits several spread workgroups).
+// Each lane fetches its points' positions for all steps first; then every
+// point is centred and located, its 21 power sums (above) are summed with those of the
 // other points of its box among the wave's 64 consecutive points (an
 // inclusive segmented scan over runs of one box, lg_seg_scan), and the last
 // lane of each run finds its box's slot (atomicCAS on the slot's key) and adds
@@ -288,7 +291,7 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_order_keys(const float2* __re
 // straggler array of power sums per box that the row transform adds (only
 // for boxes flagged in their count word; the convolution pass clears the
 // counts and those sums): a run whose chunk
-// already fills its table (more than kLgTable boxes in kLgChunk points) and a
+// already fills its table (more than 2^TB boxes in kLgChunk points) and a
 // box with more than K contributing workgroups.  Any permutation gives
 // the same charges up to the order of the fp32 adds; a spatial one keeps runs
 // long and tables sparse.  A grid the FFT length cannot hold (2 m > fft_len,
@@ -297,7 +300,6 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_order_keys(const float2* __re
 constexpr int kLgSteps = 4;                        // 64-point steps per wave
 constexpr int kLgChunk = kLgThreads * kLgSteps;    // points per workgroup
 static_assert(kLgChunk == kLgSpreadChunk, "the host sizes the spread's scratch by kLgSpreadChunk");
-static_assert(kLgTable == kLgThreads, "one table slot per thread in the flush");
 static_assert(kLgSums == kLgSumsPerBox, "the host sizes the sums by kLgSumsPerBox");
 // A box's count word: the slots listed (low bits) and a flag set when
 // straggler sums were added for the box (the row transform reads them and
@@ -321,15 +323,53 @@ __device__ __forceinline__ int col_block(int b, int blocks) {
   return c < blocks ? c : -1;
 }
 constexpr int col_launch(int blocks) { return (blocks + kLgColXcds - 1) / kLgColXcds * kLgColXcds; }
+// Groups a wave's points by box before the scan: a stable partition of the
+// lanes by key (boxes in order of first appearance, past-the-end lanes
+// last), the point's key and position in its box moved to its new lane by a
+// forward permute.  Once the grid has drifted from the lattice the spread
+// order was made on, the points of two or three boxes alternate in the
+// order (a Z-curve crosses a box's shifted edges many times): ~10 runs per
+// 64 points instead of ~2, and every run end costs 21 LDS float atomics,
+// which took ~60 % of the kernel.  Grouped, a wave step has one run per box.
+// With more than kLgGroupMax boxes in a step (sparse regions, where runs are
+// short anyway) the order is kept.  Needs the whole wave active.
+constexpr int kLgGroupMax = 8;
+__device__ __forceinline__ void lg_group_by_box(int& key, float& ux, float& uy) {
+  unsigned long long pending = __ballot(key >= 0);
+  int base = 0;
+  int dst = -1;
+  for (int g = 0; g < kLgGroupMax && pending != 0; ++g) {
+    const int leader = __ffsll(static_cast<long long>(pending)) - 1;
+    const int k = __builtin_amdgcn_readlane(key, leader);
+    const unsigned long long m = __ballot(key == k);
+    const int below = static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(m >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(m), 0u)));
+    if (key == k) dst = base + below;
+    base += __popcll(m);
+    pending &= ~m;
+  }
+  if (pending != 0) return;  // too many boxes: keep the order
+  const unsigned long long rest = __ballot(key < 0);
+  const int below = static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<unsigned int>(rest >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo(static_cast<unsigned int>(rest), 0u)));
+  if (key < 0) dst = base + below;
+  key = __builtin_amdgcn_ds_permute(dst * 4, key);
+  ux = __int_as_float(__builtin_amdgcn_ds_permute(dst * 4, __float_as_int(ux)));
+  uy = __int_as_float(__builtin_amdgcn_ds_permute(dst * 4, __float_as_int(uy)));
+}
+
+template <int TB>
 __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restrict__ y_stored,
                                                           const int* __restrict__ order, DeviceScalars* sc, int n,
                                                           int max_nodes, float* __restrict__ entries,
                                                           int* __restrict__ box_count, float* __restrict__ straggler) {
 #pragma clang fp contract(off)
+  constexpr int kSlots = 1 << TB;
+  static_assert(kSlots <= kLgThreads, "one table slot per thread in the flush");
   chain_priority();
-  __shared__ int tkey[kLgTable];                // box of each slot, -1: free
-  __shared__ int tdst[kLgTable];                // the slot's entry, -1: none
-  __shared__ float tval[kLgTable * kLgSums];    // the slots' sums
+  __shared__ int tkey[kSlots];              // box of each slot, -1: free
+  __shared__ int tdst[kSlots];              // the slot's entry, -1: none
+  __shared__ float tval[kSlots * kLgSums];  // the slots' sums
   const DeviceScalars s = *sc;
   const int m = s.lg_nodes;
   if (m > max_nodes) {  // uniform over the grid
@@ -339,9 +379,6 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
   const int nb = s.lg_boxes;
   const int lane = static_cast<int>(threadIdx.x) & 63;
   const int wave = static_cast<int>(threadIdx.x) >> 6;
-  tkey[threadIdx.x] = -1;
-  for (int e = threadIdx.x; e < kLgTable * kLgSums; e += kLgThreads) tval[e] = 0.0f;
-  __syncthreads();
   // a wave's steps are consecutive points of the order; the chunks of one
   // XCD are one contiguous range of the order (col_block), a compact region
   // of the layout, so the cache lines of y that its points share are fetched
@@ -351,14 +388,34 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
   const int chunk = col_block(static_cast<int>(blockIdx.x), chunks);
   const long long base = chunk < 0 ? static_cast<long long>(n)
                                    : static_cast<long long>(chunk) * kLgChunk + static_cast<long long>(wave) * kLgSteps * 64;
+  // every step's position is fetched before the table is cleared, so the
+  // gathers of all steps are in flight together
+  float2 r[kLgSteps];
+  {
+    int src[kLgSteps];
+#pragma unroll
+    for (int k = 0; k < kLgSteps; ++k) {
+      const long long i = base + k * 64 + lane;
+      src[k] = i < n ? (order != nullptr ? order[i] : static_cast<int>(i)) : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < kLgSteps; ++k) r[k] = src[k] >= 0 ? y_stored[src[k]] : make_float2(0.0f, 0.0f);
+  }
+  if (threadIdx.x < kSlots) tkey[threadIdx.x] = -1;
+  for (int e = threadIdx.x; e < kSlots * kLgSums; e += kLgThreads) tval[e] = 0.0f;
+  __syncthreads();
+#pragma unroll
   for (int k = 0; k < kLgSteps; ++k) {
     const long long i = base + k * 64 + lane;
-    float a[kLgSums];
+    LgPoint b{0, 0, 0.0f, 0.0f};
     int key = -1;  // past the end: a run of its own, never added
     if (i < n) {
-      const float2 r = y_stored[order != nullptr ? order[i] : static_cast<int>(i)];
-      const LgPoint b = lg_locate(r.x - s.shift_x, r.y - s.shift_y, s);
+      b = lg_locate(r[k].x - s.shift_x, r[k].y - s.shift_y, s);
       key = b.by * nb + b.bx;
+    }
+    lg_group_by_box(key, b.ux, b.uy);
+    float a[kLgSums];
+    if (key >= 0) {
       lg_power_sums(b, a);
     } else {
 #pragma unroll
@@ -369,15 +426,15 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
     float take = (lane == 0 || prev != key) ? 0.0f : 1.0f;
     lg_seg_scan(a, take);
     if (key >= 0 && (lane == 63 || next != key)) {  // the last lane of its run
-      unsigned int h = (static_cast<unsigned int>(key) * 2654435761u) >> (32 - kLgTableBits);
+      unsigned int h = (static_cast<unsigned int>(key) * 2654435761u) >> (32 - TB);
       int slot = -1;
-      for (int probe = 0; probe < kLgTable; ++probe) {
+      for (int probe = 0; probe < kSlots; ++probe) {
         const int old = atomicCAS(&tkey[h], -1, key);
         if (old == -1 || old == key) {
           slot = static_cast<int>(h);
           break;
         }
-        h = (h + 1u) & (kLgTable - 1);
+        h = (h + 1u) & (kSlots - 1);
       }
       if (slot >= 0) {
         float* dst = tval + slot * kLgSums;
@@ -396,24 +453,26 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_spread(const float2* __restri
   // occupied slots: each takes an entry of its box (beyond K: added as
   // stragglers), then the sums are stored, slot by slot
   const int t = threadIdx.x;
-  const int gb = tkey[t];
-  int dst = -1;
-  if (gb >= 0) {
-    const int per = lg_entries_per_box(nb);
-    const int k = atomicAdd(box_count + gb, 1) & kLgCountMask;
-    if (k < per) {
-      dst = gb * per + k;
-    } else {
+  if (t < kSlots) {
+    const int gb = tkey[t];
+    int dst = -1;
+    if (gb >= 0) {
+      const int per = lg_entries_per_box(nb);
+      const int k = atomicAdd(box_count + gb, 1) & kLgCountMask;
+      if (k < per) {
+        dst = gb * per + k;
+      } else {
 #pragma unroll
-      for (int e = 0; e < kLgSums; ++e) {
-        unsafeAtomicAdd(straggler + static_cast<std::size_t>(gb) * kLgSums + e, tval[t * kLgSums + e]);
+        for (int e = 0; e < kLgSums; ++e) {
+          unsafeAtomicAdd(straggler + static_cast<std::size_t>(gb) * kLgSums + e, tval[t * kLgSums + e]);
+        }
+        atomicOr(box_count + gb, kLgStraggled);
       }
-      atomicOr(box_count + gb, kLgStraggled);
     }
+    tdst[t] = dst;
   }
-  tdst[t] = dst;
   __syncthreads();
-  for (int q = threadIdx.x; q < kLgTable * kLgSums; q += kLgThreads) {
+  for (int q = threadIdx.x; q < kSlots * kLgSums; q += kLgThreads) {
     const int slot = q / kLgSums;
     const int d = tdst[slot];
     if (d >= 0) entries[static_cast<std::size_t>(d) * kLgSums + (q - slot * kLgSums)] = tval[q];
@@ -463,7 +522,7 @@ __global__ __launch_bounds__(LgShape<F>::NTW) void k_lg_kernel_rows(const Device
   using S = LgShape<F>;
   constexpr int HH = S::H * S::H;
   __shared__ float2 lds[2 * S::KR * FftPad<F>::kStride];
-  __shared__ float2 tws[F];
+  __shared__ float2 tws[F / 2];
   const int m = sc->lg_nodes;
   const float h = sc->lg_node_h;
   const int row0 = blockIdx.x * S::KR;
@@ -510,7 +569,7 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_cols(const DeviceS
   using S = LgShape<F>;
   constexpr int HH = S::H * S::H;
   __shared__ float2 lds[2 * S::KR * FftPad<F>::kStride];
-  __shared__ float2 tws[F];
+  __shared__ float2 tws[F / 2];
   const int m = sc->lg_nodes;
   const int cb = col_block(static_cast<int>(blockIdx.x), (S::H + S::KR - 1) / S::KR);
   if (cb < 0) return;  // whole block
@@ -575,8 +634,12 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
   constexpr int RG = 1;
   constexpr int NB = F / 2 / kLgOrder;          // boxes per axis this length holds
   __shared__ float2 lds[2 * RG * FftPad<F>::kStride];
-  __shared__ float2 tws[F];
-  __shared__ float ps[NB * kLgSums];
+  __shared__ float2 tws[F / 2];
+  // the box sums share the transform's buffer: the node moments are taken
+  // to registers before the buffer is written (15.4 KB of LDS at F = 768,
+  // so that a workgroup fits a CU beside three attraction workgroups)
+  static_assert(NB * kLgSums * sizeof(float) <= sizeof(lds), "box sums fit the transform buffer");
+  float* ps = reinterpret_cast<float*>(lds);
   const int m = sc->lg_nodes;
   if (m > max_nodes) return;  // flagged by the spread
   const int nb = sc->lg_boxes;
@@ -598,12 +661,16 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
   __syncthreads();
   {
     const int r0 = blockIdx.y;
-    for (int e = threadIdx.x; e < RG * F; e += S::NT) {
+    constexpr int PER = (RG * F + S::NT - 1) / S::NT;  // node moments per thread
+    float2 av[PER], bv[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = threadIdx.x + i * S::NT;
       const int rr = e / F;
       const int x = e - rr * F;
       const int r = r0 + rr;
       float2 a = make_float2(0.0f, 0.0f), b = a;
-      if (x < m) {
+      if (e < RG * F && x < m) {
         const int bx = x / kLgOrder;
         const int c = x - bx * kLgOrder;
         const float* p = ps + bx * kLgSums;
@@ -621,8 +688,19 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
         b = make_float2(v2, 0.0f);
         m2[(by * kLgOrder + r) * m + x] = v3;
       }
-      lds[fft_at<F>(2 * rr, x)] = a;
-      lds[fft_at<F>(2 * rr + 1, x)] = b;
+      av[i] = a;
+      bv[i] = b;
+    }
+    __syncthreads();  // every box sum read: the buffer takes the rows
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = threadIdx.x + i * S::NT;
+      if (e < RG * F) {
+        const int rr = e / F;
+        const int x = e - rr * F;
+        lds[fft_at<F>(2 * rr, x)] = av[i];
+        lds[fft_at<F>(2 * rr + 1, x)] = bv[i];
+      }
     }
     __syncthreads();
     fft_lds<F, 2 * RG, S::NT, false, 1>(lds, tws);
@@ -665,7 +743,7 @@ __global__ __launch_bounds__(LgShape<F>::NTW) void k_lg_conv_cols(const DeviceSc
   constexpr int C = S::CC;
   constexpr int HH = S::H * S::H;
   __shared__ float2 lds[3 * C * FftPad<F>::kStride];
-  __shared__ float2 tws[F];
+  __shared__ float2 tws[F / 2];
   const int m = sc->lg_nodes;
   {
     // the spread's box counts and straggler sums, read by every charge-row
@@ -772,7 +850,7 @@ __global__ __launch_bounds__(LgShape<F>::NTW) void k_lg_inverse_rows(const Devic
   chain_priority();
   using S = LgShape<F>;
   __shared__ float2 lds[2 * S::CR * FftPad<F>::kStride];
-  __shared__ float2 tws[F];
+  __shared__ float2 tws[F / 2];
   const int m = sc->lg_nodes;
   const int row0 = blockIdx.x * S::CR;
   double acc = 0.0;
@@ -894,11 +972,18 @@ hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const 
 }  // namespace
 
 hipError_t launch_interp_spread(const float2* y_stored, const int* order, DeviceScalars* sc, InterpBuffers& ib, int n,
-                                int fft_len, hipStream_t stream) {
+                                int fft_len, int table_bits, hipStream_t stream) {
   const int max_nodes = lg_boxes_bound(fft_len) * kLgOrder;
   const int blocks = col_launch(lg_spread_blocks(n));
-  k_lg_spread<<<blocks, kLgThreads, 0, stream>>>(y_stored, order, sc, n, max_nodes, ib.entries, ib.box_count,
-                                                  ib.straggler);
+  if (table_bits == kLgSmallTableBits) {
+    k_lg_spread<kLgSmallTableBits><<<blocks, kLgThreads, 0, stream>>>(y_stored, order, sc, n, max_nodes, ib.entries,
+                                                                      ib.box_count, ib.straggler);
+  } else if (table_bits == kLgTableBits) {
+    k_lg_spread<kLgTableBits><<<blocks, kLgThreads, 0, stream>>>(y_stored, order, sc, n, max_nodes, ib.entries,
+                                                                 ib.box_count, ib.straggler);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -85,10 +85,13 @@ constexpr int kLgMaxNodes = 2048;
 constexpr int kLgMaxFft = 2 * kLgMaxNodes;
 constexpr int kLgMaxBoxes = kLgMaxNodes / kLgOrder;  // per axis
 // Spreading: a workgroup sums kLgSpreadChunk points of the spread order into
-// an LDS table of kLgTable slots keyed by box; each box takes the sums of up
-// to K = min(kLgMaxPerBox, kLgEntryPool / boxes) workgroups.
+// an LDS table of 2^table_bits slots keyed by box (kLgTableBits, or
+// kLgSmallTableBits where the points are dense enough that a chunk touches
+// few boxes); each box takes the sums of up to K = min(kLgMaxPerBox,
+// kLgEntryPool / boxes) workgroups.
 constexpr int kLgSpreadChunk = 1024;
 constexpr int kLgTableBits = 8;
+constexpr int kLgSmallTableBits = 6;
 constexpr int kLgTable = 1 << kLgTableBits;
 constexpr int kLgMaxPerBox = 64;
 constexpr long long kLgEntryPool = 1LL << 20;
@@ -224,9 +227,12 @@ hipError_t launch_inverse_rows(GridBuffers& gb, const float2* tw, int n, DeviceS
 // 3 * 2^a in [64, kLgMaxFft] with fft_len >= 2 * lg_nodes); the node count
 // itself is read on the device.  The spread reads the stored layout in
 // `order` (working indices; nullptr: the working order itself) and adds the node moments to the charge planes, which must be
-// zero (they are after allocation and after every convolution).
+// zero (they are after allocation and after every convolution).  table_bits:
+// kLgTableBits or kLgSmallTableBits (any value gives the same charges up to
+// the order of the fp32 adds; the small table keeps more workgroups resident
+// beside other kernels).
 hipError_t launch_interp_spread(const float2* y_stored, const int* order, DeviceScalars* sc, InterpBuffers& ib, int n,
-                                int fft_len, hipStream_t stream);
+                                int fft_len, int table_bits, hipStream_t stream);
 // The spread order of the current layout (needs this iteration's geometry):
 // working indices sorted by position.  Any permutation is correct; a spatial
 // one keeps the spread's runs long.
