@@ -440,11 +440,23 @@ struct LgPoint {
 // The box is found in fp64, (p - lo) / w correctly rounded, as FIt-SNE does:
 // interpolation is discontinuous across box edges, and in fp32 a coordinate
 // hundreds of boxes from the corner is only known to ~1e-4 of a box width.
+// The quotient is taken as q0 = x (1/w), then q0 + r (1/w) with the exact
+// remainder r = x - q0 w (FMA): with 1/w correctly rounded and q0 within an
+// ulp, that is the correctly rounded x / w (Markstein, IBM J. Res. Dev. 34,
+// 111 (1990)) for any x that does not underflow, and x here is 0 or a
+// difference of two floats (|x| >= 2^-149, a normal double).  Three fp64
+// operations instead of the ~10 of the division sequence; checked equal to
+// the IEEE division on 2e8 random and 1.4e7 near-multiple pairs.
+__device__ __forceinline__ double lg_box_quotient(double x, const DeviceScalars& s) {
+  const double q0 = x * s.lg_inv_box_wd;
+  const double r = fma(-q0, s.lg_box_wd, x);
+  return fma(r, s.lg_inv_box_wd, q0);
+}
 __device__ __forceinline__ LgPoint lg_locate(float px, float py, const DeviceScalars& s) {
 #pragma clang fp contract(off)
   const double lo = static_cast<double>(s.lg_lo);
-  const double rx = (static_cast<double>(px) - lo) / s.lg_box_wd;
-  const double ry = (static_cast<double>(py) - lo) / s.lg_box_wd;
+  const double rx = lg_box_quotient(static_cast<double>(px) - lo, s);
+  const double ry = lg_box_quotient(static_cast<double>(py) - lo, s);
   LgPoint b;
   b.bx = max(0, min(s.lg_boxes - 1, static_cast<int>(floor(rx))));
   b.by = max(0, min(s.lg_boxes - 1, static_cast<int>(floor(ry))));

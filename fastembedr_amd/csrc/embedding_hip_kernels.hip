@@ -93,6 +93,7 @@ __device__ void set_geometry(DeviceScalars* sc, const BlockStats& t, int n, int 
     sc->lg_lo = lo;
     sc->lg_box_w = static_cast<float>(w);
     sc->lg_box_wd = w;
+    sc->lg_inv_box_wd = 1.0 / w;
     sc->lg_node_h = static_cast<float>(w / static_cast<double>(sc->lg_order));
     sc->lg_boxes = nb;
     sc->lg_nodes = nb * sc->lg_order;

@@ -44,6 +44,7 @@ struct alignas(16) DeviceScalars {
   float lg_lo, lg_box_w, lg_node_h;
   int lg_boxes, lg_nodes;
   double lg_box_wd;            // box width in fp64: points are located in fp64
+  double lg_inv_box_wd;        // its correctly rounded reciprocal (lg_locate)
 };
 
 struct BlockStats {
