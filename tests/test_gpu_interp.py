@@ -332,3 +332,49 @@ def test_interp_spread_independent_of_point_order(hip, oracle_mod, prob, n_keep)
     err = rel_l2(g, g0)
     _say(f"  one crowded box: relL2 {err:.2e}")
     assert np.all(np.isfinite(g)) and err <= GRAD_TOL
+
+
+@pytest.mark.parametrize("dense", ["0", "0.001"])
+def test_interp_spread_table_sizes(hip, oracle_mod, prob, monkeypatch, dense):
+    """The spread's two LDS tables give the oracle's gradient:
+    FASTEMBEDR_HIP_SPREAD_DENSE=0 forces the 256-slot table, 0.001 the 64-slot
+    one, whatever the density.  Gradient probes at 30, 7.5 and 0.8 points per
+    box (a fresh spread order: few boxes per wave of 64 points in the first,
+    more than eight in the last, where the grouping keeps the order and the
+    small table overflows into its straggler path), then 40 iterations of
+    run() checked step by step, so that the order ages while the grid drifts
+    away from the lattice it was made on (the case the grouping is for)."""
+    x, idx, dist, y0 = prob
+    monkeypatch.setenv("FASTEMBEDR_HIP_SPREAD_DENSE", dense)
+    n = x.shape[0]
+    for span, min_int in ((8.0, 10), (20.0, 10), (60.0, 50)):
+        y = _with_span(y0, span)
+        _say(f"case: spread table (dense threshold {dense}), gradient at span {span}")
+        with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+            s.set_repulsion(LAGRANGE, 3, min_int, 1.0)
+            s.set_state(y)
+            g = s.gradient(1.0, LAGRANGE)
+            P = oracle_mod.OracleP.wrap(*s.csr())
+        g0, _, _ = P.lagrange_gradient(y, 1.0, order=3, min_intervals=min_int, threads=8)
+        err = rel_l2(g, g0)
+        _say(f"  relL2 {err:.2e}")
+        assert np.all(np.isfinite(g)) and err <= GRAD_TOL
+    _say(f"case: spread table (dense threshold {dense}), 40 iterations step by step")
+    with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+        P = oracle_mod.OracleP.wrap(*s.csr())
+        s.set_repulsion(LAGRANGE, 3, 10, 1.0)
+        s.set_state(_with_span(y0, 8.0))
+        s.center()
+        worst = 0.0
+        for t in range(40):
+            y, u, g = s.get_state()
+            s.run(1, 1.0, 0.8, n / 12.0, 0.01, 5.0)
+            y1, _, _ = s.get_state()
+            yr, ur, gr = y.copy(), u.copy(), g.copy()
+            grad, _, _ = P.lagrange_gradient(yr, 1.0, order=3, min_intervals=10, threads=8)
+            oracle_mod.update(yr, ur, gr, grad, n / 12.0, 0.8)
+            oracle_mod.zero_mean(yr)
+            err = rel_l2(y1 - y, yr - y)
+            worst = max(worst, err)
+            assert err <= GRAD_TOL, (t, err)
+        _say(f"  worst per-step relL2 {worst:.2e}")
