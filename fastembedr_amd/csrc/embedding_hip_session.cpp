@@ -1147,6 +1147,23 @@ hipError_t enqueue_renumber(fastembedr_hip_tsne* s) {
   return hipSuccess;
 }
 
+// Iterations until the next renumbering check after one at gap `gap` (0: the
+// first, before the first iteration), for period P: checks at iterations 0,
+// P and 16P, then at gaps that double (P = 25: 0, 25, 400, 1150, ...).  The
+// check at P repairs an initial order that says little about P's locality (a
+// random initialisation); the one at 16P comes after the early exaggeration,
+// once the clusters have formed.  Every check drains the queue for its
+// estimate and an accepted one rebuilds the tiles (~2-7 ms at 1M points,
+// ~35 ms at 4M), so the old schedule 0, 25, 75, 175, 375 cost config 2's whole
+// schedule 3826 against 3926 it/s with checks at 0 and 400 only; config 4,
+// which needs a renumbering after its clusters form (its PCA order leaves the
+// attraction at 1.30 instead of 0.96 ms), 731-754 against 763.
+int next_reorder_gap(int gap, int period) {
+  if (gap == 0) return period;
+  if (gap == period) return 15 * period;
+  return 2 * gap;
+}
+
 // Host (caller's numbering) -> working numbering, through y_b as staging.
 bool upload_permuted(fastembedr_hip_tsne* s, const float* host, float2* dst) {
   const std::size_t bytes = static_cast<std::size_t>(s->n) * sizeof(float2);
@@ -1429,8 +1446,8 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   lanes = env_int("FASTEMBEDR_HIP_ATTRACT_LANES", lanes);
   if (lanes != 8 && lanes != 16 && lanes != 32 && lanes != 64) lanes = 16;
   s->lanes = lanes;
-  // Renumbering: before the first iteration, then after gaps that double from
-  // this value (the layout's coarse structure settles early).
+  // Renumbering checks: before the first iteration, after this many, after
+  // 16 times as many, then at gaps that double (next_reorder_gap).
   s->reorder_period = env_int("FASTEMBEDR_HIP_RENUMBER_PERIOD", 25);
   if (const char* off = std::getenv("FASTEMBEDR_HIP_RENUMBER_PERIOD")) {
     if (std::strcmp(off, "0") == 0) s->reorder_period = 0;
@@ -1818,14 +1835,14 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
     });
   };
   for (int it = 0; it < n_iter; ++it) {
-    // Renumber before the first iteration ever run and then every
-    // reorder_period iterations; the bounding box and pending shift it needs
-    // are in DeviceScalars (stats kernel above, or the previous update's
-    // finished statistics).
+    // Renumber before the first iteration ever run and then on the schedule
+    // of next_reorder_gap; the bounding box and pending shift it needs are in
+    // DeviceScalars (stats kernel above, or the previous update's finished
+    // statistics).
     if (s->reorder_period > 0 && s->since_reorder >= s->reorder_gap) {
       if (pending && !finish_pending(lg ? s->lg_ring_dev : nullptr)) return 1;
       if (!settle(s) || !s->timed(fehip::kKRenumber, "renumber", [&] { return enqueue_renumber(s); })) return 1;
-      s->reorder_gap = s->reorder_gap == 0 ? s->reorder_period : 2 * s->reorder_gap;
+      s->reorder_gap = next_reorder_gap(s->reorder_gap, s->reorder_period);
     }
     ++s->since_reorder;
     int fft_len = 0;
