@@ -1215,34 +1215,43 @@ __global__ __launch_bounds__(kPointThreads) void k_morton_keys(const float2* __r
 // the distinct column tiles of its entries are marked in an LDS bitmap
 // (`words` 32-bit words) and counted.  order maps new -> old rows and map old
 // -> new columns; null pointers stand for the identity (the current
-// numbering).  One wave per row.
-__global__ __launch_bounds__(256) void k_tile_estimate(const int* __restrict__ row_ptr, const int* __restrict__ col,
-                                                       const int* __restrict__ order, const int* __restrict__ map,
-                                                       int n, int step, int words,
-                                                       unsigned long long* __restrict__ out) {
+// numbering).  One wave per row, 16 waves per workgroup; a lane marks a tile
+// only when it differs from the last one it marked (a row's columns mostly
+// fall in a few tiles, and the bitmap's few words took every lane's LDS
+// atomic in turn: 0.7 ms per estimate at 1M points).
+constexpr int kEstimateThreads = 1024;
+__global__ __launch_bounds__(kEstimateThreads) void k_tile_estimate(const int* __restrict__ row_ptr,
+                                                                    const int* __restrict__ col,
+                                                                    const int* __restrict__ order,
+                                                                    const int* __restrict__ map, int n, int step,
+                                                                    int words, unsigned long long* __restrict__ out) {
   extern __shared__ unsigned int bits[];
   __shared__ unsigned int block_count;
   const int r0 = static_cast<int>(blockIdx.x) * step * kTileRows;
   if (r0 >= n) return;  // whole block
-  for (int w = threadIdx.x; w < words; w += 256) bits[w] = 0u;
+  for (int w = threadIdx.x; w < words; w += kEstimateThreads) bits[w] = 0u;
   if (threadIdx.x == 0) block_count = 0u;
   __syncthreads();
   const int r1 = min(n, r0 + kTileRows);
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
-  for (int q = r0 + wave; q < r1; q += 256 / kWave) {
+  int last = -1;
+  for (int q = r0 + wave; q < r1; q += kEstimateThreads / kWave) {
     const int i = order != nullptr ? order[q] : q;
     const int e1 = row_ptr[i + 1];
     for (int e = row_ptr[i] + lane; e < e1; e += kWave) {
       const int j = map != nullptr ? map[col[e]] : col[e];
       const int t = j / kTileCols;
-      atomicOr(&bits[t >> 5], 1u << (t & 31));
+      if (t != last) {
+        atomicOr(&bits[t >> 5], 1u << (t & 31));
+        last = t;
+      }
     }
   }
   __syncthreads();
   unsigned int c = 0u;
-  for (int w = threadIdx.x; w < words; w += 256) c += static_cast<unsigned int>(__popc(bits[w]));
-  atomicAdd(&block_count, c);
+  for (int w = threadIdx.x; w < words; w += kEstimateThreads) c += static_cast<unsigned int>(__popc(bits[w]));
+  if (c != 0u) atomicAdd(&block_count, c);
   __syncthreads();
   if (threadIdx.x == 0) atomicAdd(out, static_cast<unsigned long long>(block_count));
 }
@@ -1628,7 +1637,7 @@ hipError_t launch_tile_estimate(const Csr& p, const int* order, const int* map, 
   const int blocks = (row_blocks + step - 1) / step;
   const std::size_t lds = static_cast<std::size_t>(words) * sizeof(unsigned int);
   if (lds > 60 * 1024) return hipErrorInvalidValue;
-  k_tile_estimate<<<blocks, 256, lds, stream>>>(p.row_ptr, p.col, order, map, p.n, step, words, out);
+  k_tile_estimate<<<blocks, kEstimateThreads, lds, stream>>>(p.row_ptr, p.col, order, map, p.n, step, words, out);
   return hipGetLastError();
 }
 

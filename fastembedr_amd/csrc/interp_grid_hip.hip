@@ -638,8 +638,9 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
   // the box sums share the transform's buffer: the node moments are taken
   // to registers before the buffer is written (15.4 KB of LDS at F = 768,
   // so that a workgroup fits a CU beside three attraction workgroups)
-  static_assert(NB * kLgSums * sizeof(float) <= sizeof(lds), "box sums fit the transform buffer");
+  static_assert((NB * (kLgSums + 1) + 1) * sizeof(float) <= sizeof(lds), "box sums fit the transform buffer");
   float* ps = reinterpret_cast<float*>(lds);
+  int* pcnt = reinterpret_cast<int*>(ps + NB * kLgSums);  // entries per box, then the row's largest count
   const int m = sc->lg_nodes;
   if (m > max_nodes) return;  // flagged by the spread
   const int nb = sc->lg_boxes;
@@ -647,16 +648,54 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
   if (by >= nb) return;
   stage_twiddles<F, S::NT>(tws, tw);
   const int per = lg_entries_per_box(nb);
+  if (threadIdx.x == 0) pcnt[NB] = 0;
+  __syncthreads();
+  // the row's boxes: entry counts, straggler sums as the starting values
+  int cmax = 0;
+  for (int bx = threadIdx.x; bx < nb; bx += S::NT) {
+    const int cnt = min(box_count[by * nb + bx] & kLgCountMask, per);
+    pcnt[bx] = cnt;
+    cmax = max(cmax, cnt);
+  }
   for (int q = threadIdx.x; q < nb * kLgSums; q += S::NT) {
     const int bx = q / kLgSums;
-    const int e = q - bx * kLgSums;
     const int b = by * nb + bx;
-    const int word = box_count[b];
-    const int cnt = min(word & kLgCountMask, per);
-    const float* src = entries + static_cast<std::size_t>(b) * per * kLgSums + e;
-    float sum = (word & kLgStraggled) != 0 ? straggler[static_cast<std::size_t>(b) * kLgSums + e] : 0.0f;
-    for (int k = 0; k < cnt; ++k) sum += src[static_cast<std::size_t>(k) * kLgSums];
-    ps[q] = sum;
+    ps[q] = (box_count[b] & kLgStraggled) != 0 ? straggler[static_cast<std::size_t>(b) * kLgSums + (q - bx * kLgSums)]
+                                               : 0.0f;
+  }
+  if (cmax > 0) atomicMax(&pcnt[NB], cmax);
+  __syncthreads();
+  // the entries, in chunks of kChunk per (box, sum) work item, so that the
+  // hundreds of entries of a dense box (early in the optimisation, the 50 x
+  // 50 grid's crowded boxes) spread over the workgroup; each chunk is summed
+  // with four partial sums and added to its box's sum (an LDS float atomic
+  // when a box has several chunks)
+  constexpr int kChunk = 32;
+  const int chunks = (pcnt[NB] + kChunk - 1) / kChunk;
+  for (int it = threadIdx.x; it < nb * chunks * kLgSums; it += S::NT) {
+    const int e = it % kLgSums;
+    const int bc = it / kLgSums;
+    const int bx = bc / chunks;
+    const int c = bc - bx * chunks;
+    const int k0 = c * kChunk;
+    const int k1 = min(pcnt[bx], k0 + kChunk);
+    if (k0 >= k1) continue;
+    const float* src = entries + static_cast<std::size_t>(by * nb + bx) * per * kLgSums + e;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    int k = k0;
+    for (; k + 4 <= k1; k += 4) {
+      s0 += src[static_cast<std::size_t>(k) * kLgSums];
+      s1 += src[static_cast<std::size_t>(k + 1) * kLgSums];
+      s2 += src[static_cast<std::size_t>(k + 2) * kLgSums];
+      s3 += src[static_cast<std::size_t>(k + 3) * kLgSums];
+    }
+    for (; k < k1; ++k) s0 += src[static_cast<std::size_t>(k) * kLgSums];
+    const float part = (s0 + s1) + (s2 + s3);
+    if (chunks == 1) {
+      ps[bx * kLgSums + e] += part;
+    } else {
+      atomicAdd(&ps[bx * kLgSums + e], part);
+    }
   }
   __syncthreads();
   {

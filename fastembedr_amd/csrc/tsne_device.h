@@ -94,8 +94,13 @@ constexpr int kLgSpreadChunk = 1024;
 constexpr int kLgTableBits = 8;
 constexpr int kLgSmallTableBits = 6;
 constexpr int kLgTable = 1 << kLgTableBits;
-constexpr int kLgMaxPerBox = 64;
-constexpr long long kLgEntryPool = 1LL << 20;
+// A pool of 2^21 entries (176 MB) shared by the boxes: early in the
+// optimisation a few boxes of the 50 x 50 minimum grid hold hundreds of
+// workgroups' points, and entries beyond K fall back to float atomics on the
+// box's straggler row, all on the same 21 addresses (with K capped at 64 the
+// spread took 170 us instead of 15 in the first 50 iterations of config 2).
+constexpr int kLgMaxPerBox = 1024;
+constexpr long long kLgEntryPool = 1LL << 21;
 constexpr int kLgSumsPerBox = 21;  // power sums of a box's points (the node moments' ingredients)
 inline int lg_spread_blocks(int n) { return std::max(1, (n + kLgSpreadChunk - 1) / kLgSpreadChunk); }
 // Column passes of the interpolation grid map their blocks to columns XCD by
