@@ -317,6 +317,8 @@ struct fastembedr_hip_tsne {
   double p_build_ms = 0.0;
   bool timing = false;
   int timed_only = -1;      // >= 0: time only this kernel id (others run without events)
+  int timing_every = 1;     // with timed_only: time it on every timing_every-th iteration
+  long long timing_iter = 0;  // iterations run since timing was enabled
   std::vector<hipEvent_t> events;
   std::vector<int> event_kernel;
   long long launches[fehip::kKernelCount] = {};
@@ -344,7 +346,9 @@ struct fastembedr_hip_tsne {
     }
   }
 
-  bool records(int kernel_id) const { return timing && (timed_only < 0 || timed_only == kernel_id); }
+  bool records(int kernel_id) const {
+    return timing && (timed_only < 0 || (timed_only == kernel_id && timing_iter % timing_every == 0));
+  }
 
   // Opens a timed span of kernel_id with an event on stream `on`; *slot names
   // it for span_end (the end may be recorded on another stream).
@@ -1881,6 +1885,7 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
     if (!ok) return 1;
     pending = true;
     if (lg) ++s->lg_order_age;  // iterations spread since the order was made
+    ++s->timing_iter;
   }
   // the last update's statistics (no box count is needed from them)
   if (pending && !finish_pending(nullptr)) return 1;
@@ -2026,7 +2031,9 @@ int fastembedr_hip_tsne_set_timing(fastembedr_hip_tsne* s, int enabled) {
   if (!valid_state_args(s)) return 1;
   if (!s->harvest_timing()) return 1;
   s->timing = enabled != 0;
-  s->timed_only = enabled >= 2 ? enabled - 2 : -1;
+  s->timed_only = enabled >= 2 ? (enabled - 2) & 0xffff : -1;
+  s->timing_every = enabled >= 2 ? std::max(1, enabled >> 16) : 1;
+  s->timing_iter = 0;
   if (enabled) {
     std::fill(std::begin(s->launches), std::end(s->launches), 0LL);
     std::fill(std::begin(s->total_ms), std::end(s->total_ms), 0.0);

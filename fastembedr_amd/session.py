@@ -192,14 +192,17 @@ class TsneSession:
         return float(v.value), rows
 
     # -- timing -------------------------------------------------------------
-    def set_timing(self, enabled: bool, only: str | None = None) -> None:
+    def set_timing(self, enabled: bool, only: str | None = None, every: int = 1) -> None:
         """Per-kernel HIP-event timing of run(); `only` names the one kernel
-        to time (the others then run without events)."""
+        to time (the others then run without events), on every `every`-th
+        iteration."""
         mode = int(bool(enabled))
         if enabled and only is not None:
             names = [self._lib.fastembedr_hip_tsne_kernel_name(i).decode()
                      for i in range(self._lib.fastembedr_hip_tsne_kernel_count())]
-            mode = 2 + names.index(only)
+            if not 1 <= every < 32768:
+                raise ValueError("every must be in [1, 32767]")
+            mode = 2 + names.index(only) + (every << 16)
         _lib.check(self._lib.fastembedr_hip_tsne_set_timing(self._h, mode), "set_timing")
 
     def timing(self) -> dict[str, tuple[int, float]]:

@@ -211,9 +211,11 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kl(fastembedr_hip_tsne* session, doub
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kl_rows(fastembedr_hip_tsne* session, double* kl, double* row_costs);
 
 /* Per-kernel timing.  While enabled, run() records HIP events around every
- * kernel (enabled == 1), or around the kernel with id enabled - 2 only
- * (enabled >= 2), so that the other launches run without event overhead;
- * events go on the stream the kernel runs on.  run() normally runs the
+ * kernel (enabled == 1), or around the kernel with id (enabled - 2) & 0xffff
+ * only (enabled >= 2), so that the other launches run without event
+ * overhead, on every iteration or, with enabled >> 16 = E > 1, on every E-th
+ * iteration (the events' markers delay the launch behind them); events go on
+ * the stream the kernel runs on.  run() normally runs the
  * attraction and the repulsion kernel spectrum on side streams beside the
  * rest of the iteration; with every kernel timed it runs them in sequence,
  * so that each duration is the kernel's alone.  stats returns, per kernel id,
