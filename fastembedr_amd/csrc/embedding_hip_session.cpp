@@ -155,19 +155,24 @@ struct fastembedr_hip_tsne {
   // there without a wait.  With update_on_chain an overlapped iteration runs
   // its update on the chain's stream (after the chain, waiting for the
   // attraction's event), so the two streams trade roles every iteration;
-  // settle() hands the state back to `stream` for everything else.
+  // without it (the default) the update follows the attraction and `home`
+  // stays put.  settle() hands the state back to `stream` for everything
+  // else.
   hipStream_t home = nullptr;
   // ev_layout already marks the end of the latest update, the last work on
   // `home` (the update's launch completes it itself, so that no marker
   // stands between the update and the attraction behind it); cleared by
   // settle() and by every iteration's start.
   bool layout_at_tail = false;
-  // FASTEMBEDR_HIP_UPDATE_ON_CHAIN=0: the update always on `stream`, after
-  // waiting for the chain's event.  A wait for an event that another stream
-  // has yet to signal cost ~18 us here, one for an event already signalled
-  // ~6 us; the chain ends after the attraction, so its stream should carry
-  // the update.
-  bool update_on_chain = true;
+  // FASTEMBEDR_HIP_UPDATE_ON_CHAIN=1: the update on the chain's stream, after
+  // waiting for the attraction's event (the streams then trade roles every
+  // iteration); 0, the default: the update right behind the attraction on its
+  // stream, after waiting for the chain's event.  A wait for an event that
+  // another stream has yet to signal cost ~18 us here, one for an event
+  // already signalled ~6 us; the chain ends ~30 us before the attraction at
+  // config 2, so the attraction's stream carries the update (whole schedule
+  // 4104-4115 against 4080-4083 it/s, config 4 even).
+  bool update_on_chain = false;
   bool mark_layout = true;  // FASTEMBEDR_HIP_MARK_LAYOUT=0: a marker after the update instead
   Arena arena;
   Arena work_arena;         // working-order CSR copies, permutations, state double buffers

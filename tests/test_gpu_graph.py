@@ -25,10 +25,11 @@ interpolation grid):
   * the switch's off values (and unset) turn capture off;
   * the arrangements of the eager overlapped iteration (the attraction on
     the stream of the previous update with the chain beside it and the
-    update after the chain, the default; the same with the update always on
-    the main stream, FASTEMBEDR_HIP_UPDATE_ON_CHAIN=0; and the attraction
-    beside the chain with a helper launch, FASTEMBEDR_HIP_ATTRACT_MAIN=0) end
-    within 1 % of the single-stream replayed run's KL;
+    update right behind the attraction, the default; the same with the
+    update after the chain on the chain's stream,
+    FASTEMBEDR_HIP_UPDATE_ON_CHAIN=1; and the attraction beside the chain
+    with a helper launch, FASTEMBEDR_HIP_ATTRACT_MAIN=0) end within 1 % of
+    the single-stream replayed run's KL;
   * a closed session gives its device memory back, replayed or not (graphs
     with parallel branches, once launched, held their side-branch kernels'
     allocations past hipFree until a device-wide synchronisation: 4.7 GB
@@ -137,8 +138,8 @@ def test_replayed_schedule_kl(hip, prob, repulsion):
     assert abs(kl_g - kl_e) <= KL_TOL * kl_e
 
 
-@pytest.mark.parametrize("arrangement,on_chain", [("1", "1"), ("1", "0"), ("0", "1")],
-                         ids=["attraction_main", "attraction_main_update_on_main", "attraction_beside"])
+@pytest.mark.parametrize("arrangement,on_chain", [("1", "0"), ("1", "1"), ("0", "0")],
+                         ids=["attraction_main", "attraction_main_update_on_chain", "attraction_beside"])
 def test_overlap_arrangements_kl(hip, prob, arrangement, on_chain):
     x, idx, dist, y0 = prob
     extra = {"FASTEMBEDR_HIP_ATTRACT_MAIN": arrangement, "FASTEMBEDR_HIP_UPDATE_ON_CHAIN": on_chain}
