@@ -310,3 +310,36 @@ def test_opentsne_knn_api(hip):
     assert rec.costs.shape == (1200,)
     assert abs(float(rec.costs.sum()) - rec.itercosts[-1]) <= 1e-9 * abs(rec.itercosts[-1])
     assert res.costs.size == 0
+
+
+@pytest.mark.parametrize("every", [1, 4])
+def test_sampled_kernel_timing(hip, mid_problem, every):
+    """set_timing(only=..., every=E) brackets the named kernel on every E-th
+    iteration of run() only: 10 iterations time ceil(10 / E) attraction
+    launches, with positive durations, and no other kernel; both the timed
+    and an untimed run from the same state end with finite layouts (their
+    difference is not a check: float atomics reorder sums run to run, and
+    early exaggeration amplifies that to ~4e-3 over 15 iterations)."""
+    x, idx, dist = mid_problem
+    n = x.shape[0]
+    y0 = synthetic.pca_init(x)
+    _say(f"case: sampled timing of the attraction, every {every}")
+    layouts = []
+    for timed in (True, False):
+        with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+            s.set_state(y0)
+            s.run(5, 12.0, 0.5, n / 12.0, 0.01, 5.0)
+            s.sync()
+            if timed:
+                s.set_timing(True, only="attract", every=every)
+            s.run(10, 12.0, 0.5, n / 12.0, 0.01, 5.0)
+            s.sync()
+            if timed:
+                t = s.timing()
+                s.set_timing(False)
+                cnt, tot = t["attract"]
+                assert cnt == -(-10 // every), t
+                assert tot > 0.0
+                assert all(c == 0 for name, (c, _) in t.items() if name != "attract"), t
+            layouts.append(s.y)
+    assert all(np.all(np.isfinite(y)) for y in layouts)
