@@ -267,11 +267,13 @@ struct fastembedr_hip_tsne {
   // permutation gives the same charges (up to the order of fp32 adds); a
   // spatial one keeps the spread's runs long.  lg_order_due asks the next
   // gradient pieces to make it before the spread.  Config 2, whole schedule:
-  // 3664 / 3690 / 3677 it/s at periods 16 / 32 / 48 (a refresh costs ~0.24 ms
-  // beside the attraction; the spread slows as the order ages); the working
-  // order itself (period 0, FASTEMBEDR_HIP_LG_ORDER_PERIOD) is far from
-  // spatial late in the run (spread 109 us instead of 36).
-  int lg_order_period = 32;
+  // 4118 / 4156 / 4140 it/s at periods 32 / 64 / 128 (a refresh costs ~0.2 ms
+  // beside the attraction; the spread slows as the order ages, less since it
+  // groups each wave's points by box; at periods 16 / 32 / 48 before that,
+  // 3664 / 3690 / 3677); the working order itself (period 0,
+  // FASTEMBEDR_HIP_LG_ORDER_PERIOD) is far from spatial late in the run
+  // (spread 109 us instead of 36 before the grouping).
+  int lg_order_period = 64;
   bool lg_order_stale = true;
   bool lg_order_due = false;
   int lg_order_age = 0;
