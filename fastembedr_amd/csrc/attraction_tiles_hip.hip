@@ -7,9 +7,10 @@
 // (sum_j p_ij q_ij (y_i - y_j) per row, q_ij = 1 / (1 + |y_i - y_j|^2)), the
 // same sum as the row-parallel k_attract, taken in another order.
 //
-// A workgroup owns one block of kTileRows rows; for each of its column tiles
-// it stages the kTileCols positions y_j of that tile in LDS, so the
-// neighbour gathers read LDS instead of L2.  Each lane takes kTileRun
+// A workgroup owns one block of ROWS rows; for each of its column tiles it
+// stages the COLS positions y_j of that tile in LDS, so the neighbour
+// gathers read LDS instead of L2 (ROWS x COLS = 1024 x 4096 or 2048 x 2048,
+// Tiles::rows and cols).  Each lane takes kTileRun
 // consecutive entries of the run; entries of one row are adjacent, so a lane
 // sums them in registers, and rows that run across lanes are merged by a
 // segmented scan over the wave before one LDS add per row part.
@@ -47,14 +48,16 @@ namespace {
 // group's first slot).  p is stored as its IEEE-754 bits; P is a
 // normalised joint distribution built from validated distances, so every
 // value lies in [0, 1] and bits 30 and 31 of its pattern are zero.  Those
-// bits of slots 0..4 of a group hold the group's base row (the local row of
-// its first slot, 10 bits), 2 bits per slot.  Steps above 7 are made of
+// bits of slots 0..5 of a group hold the group's base row (the local row of
+// its first slot, 10 or 11 bits), 2 bits per slot.  Steps above 7 are made of
 // bridge slots (p = 0) 7 rows apart (0.003 % more slots than 15-row bridges
 // at config 2's late layout, 0.03 % at config 4's); a run's padding repeats its last slot
 // with step 0 and p = 0.  Bridges and padding add nothing.
 static_assert(kTileRun == 8, "a lane reads its group as one 16-byte vector of words and two of values");
-static_assert(kTileRows <= 1024, "a group's base row fits the 10 spare bits of its first 5 values");
-static_assert(kTileCols <= 4096, "a local column fits 12 bits of a slot word");
+constexpr int kBaseSlots = 6;  // slots whose spare value bits carry the base row
+static_assert(kTileRows <= 1 << (2 * kBaseSlots) && kTileRowsWide <= 1 << (2 * kBaseSlots),
+              "a group's base row fits the spare bits of its first kBaseSlots values");
+static_assert(kTileCols <= 4096 && kTileColsWide <= 4096, "a local column fits 12 bits of a slot word");
 constexpr int kStepMax = 7;
 constexpr unsigned int kColMask = 0x7ff8u;  // a slot word's column byte offset
 constexpr unsigned int kValueMask = 0x3fffffffu;
@@ -81,19 +84,20 @@ template <int L>
 __global__ __launch_bounds__(kBuildThreads) void k_tile_keys(const int* __restrict__ row_ptr,
                                                              const int* __restrict__ col,
                                                              const float* __restrict__ val, int n, int col_bits,
+                                                             int rows_log2, int cols_log2,
                                                              unsigned int* __restrict__ key,
                                                              unsigned long long* __restrict__ pay) {
   constexpr int RPB = kBuildThreads / L;
   const int lane = threadIdx.x & (L - 1);
   for (int i = static_cast<int>(blockIdx.x) * RPB + static_cast<int>(threadIdx.x) / L; i < n;
        i += static_cast<int>(gridDim.x) * RPB) {
-    const unsigned int rb = static_cast<unsigned int>(i / kTileRows);
-    const unsigned int lr = static_cast<unsigned int>(i % kTileRows);
+    const unsigned int rb = static_cast<unsigned int>(i) >> rows_log2;
+    const unsigned int lr = static_cast<unsigned int>(i) & ((1u << rows_log2) - 1u);
     const int e1 = row_ptr[i + 1];
     for (int e = row_ptr[i] + lane; e < e1; e += L) {
       const int j = col[e];
-      key[e] = (rb << col_bits) | static_cast<unsigned int>(j / kTileCols);
-      pay[e] = tile_payload(val[e], lr, static_cast<unsigned int>(j % kTileCols));
+      key[e] = (rb << col_bits) | (static_cast<unsigned int>(j) >> cols_log2);
+      pay[e] = tile_payload(val[e], lr, static_cast<unsigned int>(j) & ((1u << cols_log2) - 1u));
     }
   }
 }
@@ -203,7 +207,7 @@ __global__ __launch_bounds__(kBuildThreads) void k_tile_scatter(const unsigned l
   }
 }
 
-// Each group's base row into bits 30-31 of its first 5 values.
+// Each group's base row into bits 30-31 of its first kBaseSlots values.
 __global__ __launch_bounds__(kBuildThreads) void k_tile_bases(const unsigned short* __restrict__ base_row,
                                                               const int* __restrict__ tile_beg,
                                                               const int* __restrict__ tile_count,
@@ -212,7 +216,7 @@ __global__ __launch_bounds__(kBuildThreads) void k_tile_bases(const unsigned sho
   for (long long g = grid_first(); g < groups; g += grid_stride()) {
     const unsigned int b = base_row[g];
 #pragma unroll
-    for (int q = 0; q < 5; ++q) {
+    for (int q = 0; q < kBaseSlots; ++q) {
       float& v = val[g * kTileRun + q];
       v = __uint_as_float(__float_as_uint(v) | (((b >> (2 * q)) & 3u) << 30));
     }
@@ -334,13 +338,13 @@ __device__ __forceinline__ TileStep next_tile_step(TileStep s, const int* __rest
 // The positions of column tile `cb` to LDS, between barriers (the first
 // waits for the previous tile's readers).  Each lane issues all its loads
 // before its first write; slots past the tile's last column repeat it.
-template <int NT>
+template <int NT, int COLS>
 __device__ __forceinline__ void stage_tile_columns(float2* ys, const float2* __restrict__ y_cur, int cb, int n,
                                                    int tid) {
-  constexpr int kPer = kTileCols / NT;
-  static_assert(kTileCols % NT == 0, "whole column slots per lane");
-  const int base = cb * kTileCols;
-  const int last = min(kTileCols, n - base) - 1;
+  constexpr int kPer = COLS / NT;
+  static_assert(COLS % NT == 0, "whole column slots per lane");
+  const int base = cb * COLS;
+  const int last = min(COLS, n - base) - 1;
   float2 v[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) v[i] = y_cur[base + min(tid + i * NT, last)];
@@ -379,7 +383,7 @@ __device__ __forceinline__ void acc_add(float2* acc, unsigned int k, float x, fl
 // first rows at each break instead took the kernel from 1.64 to 2.01 ms at
 // config 4's ~7 entries per row and run, and from 0.230 to 0.245 ms beside
 // the repulsion at config 2).
-template <int NT>
+template <int NT, int ROWS>
 __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileStep& s, bool live, int tid, float2* yr,
                                                float2* ys, float2* acc) {
   const unsigned int wp[4] = {g.w.x, g.w.y, g.w.z, g.w.w};
@@ -387,13 +391,16 @@ __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileSte
                                      __float_as_uint(g.p0.w), __float_as_uint(g.p1.x), __float_as_uint(g.p1.y),
                                      __float_as_uint(g.p1.z), __float_as_uint(g.p1.w)};
   // Row byte offsets (8 bytes per LDS position): the base row from the spare
-  // value bits (slot 0's step is 0), then the steps.  A group whose last row
-  // lies past the block (which a layout built here never holds) adds
-  // nothing; its reads stay inside the workgroup's LDS (rows < 1024 + 49).
+  // value bits (slot 0's step is 0), masked to the block, then the steps.
+  // A group whose last row lies past the block (which a layout built here
+  // never holds) adds nothing; its reads stay inside the workgroup's LDS
+  // (rows < ROWS + 49).
+  static_assert(ROWS <= 1 << (2 * kBaseSlots), "the base row fits its spare bits");
   unsigned int kr[kTileRun];
   unsigned int r8 = 0;
 #pragma unroll
-  for (int q = 0; q < 5; ++q) r8 |= (pb[q] >> 30) << (2 * q + 3);
+  for (int q = 0; q < kBaseSlots; ++q) r8 |= (pb[q] >> 30) << (2 * q + 3);
+  r8 &= (ROWS - 1u) << 3;
   kr[0] = r8;
 #pragma unroll
   for (int q = 1; q < kTileRun; ++q) {
@@ -401,7 +408,7 @@ __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileSte
     r8 += step << 3;
     kr[q] = r8;
   }
-  const bool active = live && s.e0 + (s.round * NT + tid) * kTileRun < s.e1 && r8 < kTileRows * 8u;
+  const bool active = live && s.e0 + (s.round * NT + tid) * kTileRun < s.e1 && r8 < ROWS * 8u;
   const unsigned int kf = kr[0];
   const unsigned int kl = kr[kTileRun - 1];
   float tx = 0.0f, ty = 0.0f;  // the current row's part
@@ -409,8 +416,8 @@ __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileSte
 #pragma unroll
   for (int q = 0; q < kTileRun; ++q) {
     const unsigned int kc = ((q & 1) ? wp[q / 2] >> 16 : wp[q / 2]) & kColMask;
-    // only slots 0..4 carry base-row bits
-    const float p = __uint_as_float(q < 5 ? pb[q] & kValueMask : pb[q]);
+    // only the first kBaseSlots slots carry base-row bits
+    const float p = __uint_as_float(q < kBaseSlots ? pb[q] & kValueMask : pb[q]);
     const float2 c = attract_term(lds_at(yr, kr[q]), lds_at(ys, kc), p);
     if (q == 0) {
       tx = c.x;
@@ -458,16 +465,16 @@ __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileSte
 // prefetch in flight; every wave runs the same steps (DPP needs whole
 // waves).  Starts and ends with LDS free for the next row block (every
 // thread passes a barrier between its last LDS access and the end).
-template <int NT, int D>
+template <int NT, int D, int ROWS, int COLS>
 __device__ __forceinline__ void attract_row_block(int rb, const unsigned short* __restrict__ ent,
                                                   const float* __restrict__ val, const int* __restrict__ tile_ptr,
                                                   const int* __restrict__ tile_cb, const int* __restrict__ tile_beg,
                                                   const float2* __restrict__ y_cur, float2* __restrict__ attr,
                                                   float exaggeration, int n, float2* ys, float2* yr, float2* acc) {
   const int tid = static_cast<int>(threadIdx.x);
-  const int r0 = rb * kTileRows;
-  const int rows = min(kTileRows, n - r0);
-  for (int r = tid; r < kTileRows; r += NT) {
+  const int r0 = rb * ROWS;
+  const int rows = min(ROWS, n - r0);
+  for (int r = tid; r < ROWS; r += NT) {
     acc[r] = make_float2(0.0f, 0.0f);
     yr[r] = r < rows ? y_cur[r0 + r] : make_float2(0.0f, 0.0f);
   }
@@ -487,8 +494,8 @@ __device__ __forceinline__ void attract_row_block(int rb, const unsigned short* 
 #pragma unroll
       for (int d = 0; d < D; ++d) {
         const bool live = k + d < steps;
-        if (live && st[d].round == 0) stage_tile_columns<NT>(ys, y_cur, tile_cb[st[d].t], n, tid);
-        sum_tile_group<NT>(g[d], st[d], live, tid, yr, ys, acc);
+        if (live && st[d].round == 0) stage_tile_columns<NT, COLS>(ys, y_cur, tile_cb[st[d].t], n, tid);
+        sum_tile_group<NT, ROWS>(g[d], st[d], live, tid, yr, ys, acc);
         // refill with step k + d + D, whose predecessor is the newest buffer
         const TileStep newest = st[(d + D - 1) % D];
         st[d] = k + d + D < steps ? next_tile_step<NT>(newest, tile_beg, t1) : newest;
@@ -514,16 +521,16 @@ __device__ __forceinline__ void attract_row_block(int rb, const unsigned short* 
 // launch or pair at zero).  Launch bounds: MINB workgroups per CU (the VGPR
 // budget of the D-deep prefetch ring).
 // HELPER: a helper launch (its own symbol, so that profiles tell the two
-// launches of a pair apart).
-template <int NT, int D, int MINB, bool HELPER>
+// launches of a pair apart).  ROWS x COLS: the tile shape.
+template <int NT, int D, int MINB, bool HELPER, int ROWS, int COLS>
 __global__ __launch_bounds__(NT, MINB) void k_attract_tiles_seg(
     const unsigned short* __restrict__ ent, const float* __restrict__ val, const int* __restrict__ tile_ptr,
     const int* __restrict__ tile_cb, const int* __restrict__ tile_beg, const float2* __restrict__ y_cur,
     float2* __restrict__ attr, float exaggeration, int n, int row_blocks, int xcds, unsigned int* __restrict__ work,
     int slots, unsigned int total) {
-  __shared__ float2 ys[kTileCols];
-  __shared__ float2 yr[kTileRows];
-  __shared__ float2 acc[kTileRows];
+  __shared__ float2 ys[COLS];
+  __shared__ float2 yr[ROWS];
+  __shared__ float2 acc[ROWS];
   // the claimed row block is passed through the first word of the column
   // tile, which is free between row blocks (no LDS beyond the three arrays:
   // 48 KB exactly, so that three workgroups leave a CU 16 KB for the
@@ -541,8 +548,8 @@ __global__ __launch_bounds__(NT, MINB) void k_attract_tiles_seg(
     __syncthreads();
   }
   while (first + slot < end) {
-    attract_row_block<NT, D>(first + slot, ent, val, tile_ptr, tile_cb, tile_beg, y_cur, attr, exaggeration, n, ys, yr,
-                          acc);
+    attract_row_block<NT, D, ROWS, COLS>(first + slot, ent, val, tile_ptr, tile_cb, tile_beg, y_cur, attr,
+                                         exaggeration, n, ys, yr, acc);
     if (threadIdx.x == 0) claimed = slots + static_cast<int>(atomicAdd(&work[xcd], 1u));
     __syncthreads();
     slot = claimed;
@@ -567,17 +574,20 @@ unsigned int build_blocks(long long items) {
 
 }  // namespace
 
-void tiles_shape(int n, long long nnz, Tiles& t) {
+void tiles_shape(int n, long long nnz, Tiles& t, int wide) {
   t.n = n;
   t.nnz = nnz;
-  t.row_blocks = (n + kTileRows - 1) / kTileRows;
-  t.col_tiles = (n + kTileCols - 1) / kTileCols;
+  const bool w = wide == 2 || (wide == 0 && n >= kTileWideFrom);
+  t.rows = w ? kTileRowsWide : kTileRows;
+  t.cols = w ? kTileColsWide : kTileCols;
+  t.row_blocks = (n + t.rows - 1) / t.rows;
+  t.col_tiles = (n + t.cols - 1) / t.cols;
   t.col_bits = bits_for(t.col_tiles);
   t.key_bits = t.col_bits + bits_for(t.row_blocks);
   t.max_tiles = std::min<long long>(nnz, static_cast<long long>(t.row_blocks) * t.col_tiles);
-  // a run's rows rise by at most kTileRows - 1, so it holds at most
-  // (kTileRows - 1) / kStepMax bridges, and at most kTileRun - 1 padding slots
-  t.padded = nnz + ((kTileRows - 1) / kStepMax + kTileRun - 1) * t.max_tiles;
+  // a run's rows rise by at most rows - 1, so it holds at most
+  // (rows - 1) / kStepMax bridges, and at most kTileRun - 1 padding slots
+  t.padded = nnz + ((t.rows - 1) / kStepMax + kTileRun - 1) * t.max_tiles;
 }
 
 hipError_t tiles_temp_bytes(const Tiles& t, std::size_t& bytes) {
@@ -613,8 +623,9 @@ hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream) {
   int* slot_count = reinterpret_cast<int*>(t.pay_in) + t.nnz;
   int* sbeg = reinterpret_cast<int*>(t.key_out);
   const unsigned int eb = build_blocks(t.nnz);
-  k_tile_keys<32><<<std::min((p.n + 7) / 8, 65536), kBuildThreads, 0, stream>>>(p.row_ptr, p.col, p.val, p.n,
-                                                                               t.col_bits, t.key_in, t.pay_in);
+  if (t.rows != (t.rows & -t.rows) || t.cols != (t.cols & -t.cols)) return hipErrorInvalidValue;
+  k_tile_keys<32><<<std::min((p.n + 7) / 8, 65536), kBuildThreads, 0, stream>>>(
+      p.row_ptr, p.col, p.val, p.n, t.col_bits, bits_for(t.rows), bits_for(t.cols), t.key_in, t.pay_in);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   std::size_t tb = t.temp_bytes;
@@ -661,25 +672,40 @@ int primary_slots(const Tiles& t, int xcds, int slots_per_xcd) {
   return std::max(1, slots_per_xcd > 0 ? std::min(slots_per_xcd, per_xcd) : per_xcd);
 }
 
-hipError_t attract_launch(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds, int blocks,
-                          int slots, int helper, unsigned int total, hipStream_t stream, hipEvent_t done) {
+template <int ROWS, int COLS>
+hipError_t attract_launch_shape(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds,
+                                int blocks, int slots, int helper, unsigned int total, hipStream_t stream,
+                                hipEvent_t done) {
   constexpr int NT = kTileThreads;
   // a ring of 2 groups (one in flight while one is summed); deeper rings
   // measured no faster at config 2, and the LDS allows 3 workgroups per CU
   if (helper) {
-    k_attract_tiles_seg<NT, 2, 3, true><<<blocks, NT, 0, stream>>>(
+    k_attract_tiles_seg<NT, 2, 3, true, ROWS, COLS><<<blocks, NT, 0, stream>>>(
         t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr, exaggeration, t.n, t.row_blocks, xcds, t.work,
         slots, total);
   } else if (done != nullptr) {
-    hipExtLaunchKernelGGL(k_attract_tiles_seg<NT, 2, 3, false>, dim3(blocks), dim3(NT), 0, stream, nullptr, done, 0,
-                          t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr, exaggeration, t.n,
-                          t.row_blocks, xcds, t.work, slots, total);
+    hipExtLaunchKernelGGL(k_attract_tiles_seg<NT, 2, 3, false, ROWS, COLS>, dim3(blocks), dim3(NT), 0, stream,
+                          nullptr, done, 0, t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr,
+                          exaggeration, t.n, t.row_blocks, xcds, t.work, slots, total);
   } else {
-    k_attract_tiles_seg<NT, 2, 3, false><<<blocks, NT, 0, stream>>>(
+    k_attract_tiles_seg<NT, 2, 3, false, ROWS, COLS><<<blocks, NT, 0, stream>>>(
         t.ent, t.val, t.tile_ptr, t.tile_cb, t.tile_beg, y_cur, attr, exaggeration, t.n, t.row_blocks, xcds, t.work,
         slots, total);
   }
   return hipGetLastError();
+}
+
+hipError_t attract_launch(const Tiles& t, const float2* y_cur, float2* attr, float exaggeration, int xcds, int blocks,
+                          int slots, int helper, unsigned int total, hipStream_t stream, hipEvent_t done) {
+  if (t.rows == kTileRows && t.cols == kTileCols) {
+    return attract_launch_shape<kTileRows, kTileCols>(t, y_cur, attr, exaggeration, xcds, blocks, slots, helper,
+                                                      total, stream, done);
+  }
+  if (t.rows == kTileRowsWide && t.cols == kTileColsWide) {
+    return attract_launch_shape<kTileRowsWide, kTileColsWide>(t, y_cur, attr, exaggeration, xcds, blocks, slots,
+                                                              helper, total, stream, done);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace

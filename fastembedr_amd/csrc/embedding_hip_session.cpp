@@ -274,6 +274,9 @@ struct fastembedr_hip_tsne {
   // FASTEMBEDR_HIP_LG_ORDER_PERIOD) is far from spatial late in the run
   // (spread 109 us instead of 36 before the grouping).
   int lg_order_period = 64;
+  // Attraction tile shape (fehip::tiles_shape): 0 by point count, 1 the
+  // 1024 x 4096 tiles, 2 the 2048 x 2048 ones (FASTEMBEDR_HIP_TILE_SHAPE).
+  int tile_shape = 0;
   bool lg_order_stale = true;
   bool lg_order_due = false;
   int lg_order_age = 0;
@@ -513,7 +516,7 @@ bool alloc_working_buffers(fastembedr_hip_tsne* s) {
 // renumbering allocates nothing.
 bool alloc_tiles(fastembedr_hip_tsne* s) {
   fehip::Tiles& t = s->tiles;
-  fehip::tiles_shape(s->n, s->p.nnz, t);
+  fehip::tiles_shape(s->n, s->p.nnz, t, s->tile_shape);
   if (t.key_bits > 32 || t.padded > static_cast<long long>(std::numeric_limits<int>::max())) {
     s->attract_tiled = false;  // beyond a 32-bit sort key or int offsets: row-parallel attraction
     return true;
@@ -1496,6 +1499,7 @@ int create_session(const int* indices, const void* distances, bool dist_double, 
   if (const char* v = std::getenv("FASTEMBEDR_HIP_UPDATE_ON_CHAIN")) s->update_on_chain = std::strcmp(v, "0") != 0;
   if (const char* v = std::getenv("FASTEMBEDR_HIP_MARK_LAYOUT")) s->mark_layout = std::strcmp(v, "0") != 0;
   if (const char* v = std::getenv("FASTEMBEDR_HIP_LG_ORDER_PERIOD")) s->lg_order_period = std::max(0, std::atoi(v));
+  s->tile_shape = std::max(0, std::min(2, env_int("FASTEMBEDR_HIP_TILE_SHAPE", 0)));
   if (const char* v = std::getenv("FASTEMBEDR_HIP_SPREAD_DENSE")) {
     char* end = nullptr;
     const double d = std::strtod(v, &end);

@@ -328,8 +328,15 @@ hipError_t launch_gather2(const float2* src, const int* idx, float2* dst, int n,
 // tile_ptr[rb + 1]; tile t covers slots tile_beg[t] .. tile_beg[t + 1] and
 // column tile tile_cb[t].  Every run starts at a multiple of kTileRun slots
 // and is padded to one with slots of value 0.
+// Two shapes, chosen per session (tiles_shape): 1024 rows x 4096 columns,
+// or 2048 x 2048 for large n, whose short runs make the column tiles'
+// staging a large share of the bytes: the same LDS (48 KB) and about the
+// same slots per run, half the staged bytes per run.
 constexpr int kTileRows = 1024;
 constexpr int kTileCols = 4096;
+constexpr int kTileRowsWide = 2048;
+constexpr int kTileColsWide = 2048;
+constexpr int kTileWideFrom = 1 << 21;  // points from which tiles_shape picks the wide shape
 constexpr int kTileRun = 8;
 constexpr int kTileMaxXcds = 16;
 constexpr int kTileThreads = 512;
@@ -337,6 +344,8 @@ constexpr int kTileThreads = 512;
 struct Tiles {
   int n = 0;
   long long nnz = 0;
+  int rows = kTileRows;  // rows per row block: kTileRows or kTileRowsWide
+  int cols = kTileCols;  // columns per column tile: kTileCols or kTileColsWide
   int row_blocks = 0;
   int col_tiles = 0;
   int col_bits = 0;   // bits of the column-tile part of the sort key
@@ -362,7 +371,9 @@ struct Tiles {
   void* temp = nullptr;
   std::size_t temp_bytes = 0;
 };
-void tiles_shape(int n, long long nnz, Tiles& t);
+// The tile shape for n points (wide: 0 = by n, 1 = 1024 x 4096, 2 = 2048 x
+// 2048) and the capacities that follow from it.
+void tiles_shape(int n, long long nnz, Tiles& t, int wide = 0);
 hipError_t tiles_temp_bytes(const Tiles& t, std::size_t& bytes);
 // Rebuilds t from the CSR (same numbering), all on `stream`.
 hipError_t launch_tile_build(const Csr& p, Tiles& t, hipStream_t stream);

@@ -11,7 +11,9 @@ Tolerance: relative L2 <= 1e-5 (fp32 sums in another order; the hardware
 reciprocal is within 1 ulp).  The cases cover many tiles per row block, rows
 whose parts in one tile are far longer than a lane's group of 8 slots, rows
 of one or two entries, sparse runs whose rows lie more than 7 apart (bridge
-slots), and sizes that are not multiples of the tile shape.
+slots), and sizes that are not multiples of the tile shape, each in both
+tile shapes (1024 rows x 4096 columns and 2048 x 2048, the one picked from
+2**21 points; FASTEMBEDR_HIP_TILE_SHAPE forces either).
 """
 
 import sys
@@ -25,7 +27,13 @@ from tests.helpers import rel_l2, small_problem
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
-TILE_ROWS, TILE_COLS = 1024, 4096
+SHAPES = {"1": (1024, 4096), "2": (2048, 2048)}
+
+
+@pytest.fixture(params=sorted(SHAPES), ids=lambda k: "x".join(map(str, SHAPES[k])))
+def shape(request, monkeypatch):
+    monkeypatch.setenv("FASTEMBEDR_HIP_TILE_SHAPE", request.param)
+    return SHAPES[request.param]
 
 
 def _say(msg):
@@ -57,7 +65,8 @@ def ring_knn(n, k):
     return np.asfortranarray(idx.astype(np.int32)), np.asfortranarray(dist.astype(np.float32))
 
 
-def _check(hip, idx, dist, perplexity, y, label):
+def _check(hip, idx, dist, perplexity, y, label, shape):
+    tile_rows, tile_cols = shape
     with hip.TsneSession(idx, dist, perplexity=perplexity, index_offset=1) as s:
         s.set_state(y)
         att = attraction_device(s)
@@ -66,14 +75,14 @@ def _check(hip, idx, dist, perplexity, y, label):
         tiles = info["tiles"]
     n = y.shape[0]
     # slots: every entry, the bridges between entries more than 7 rows apart
-    # within a run (at most 1023 // 7 per run) and each run's padding to 8
+    # within a run (at most (rows - 1) // 7 per run) and each run's padding to 8
     assert info["slots"] % 8 == 0
-    assert len(col) <= info["slots"] <= len(col) + (1023 // 7 + 7) * info["tiles"]
+    assert len(col) <= info["slots"] <= len(col) + ((tile_rows - 1) // 7 + 7) * info["tiles"]
     ref = attraction_numpy(row_ptr, col, val, y)
     rows = np.repeat(np.arange(n), np.diff(row_ptr))
-    want_tiles = len(np.unique((rows // TILE_ROWS).astype(np.int64) * (1 << 20) + col // TILE_COLS))
+    want_tiles = len(np.unique((rows // tile_rows).astype(np.int64) * (1 << 20) + col // tile_cols))
     err = rel_l2(att, ref)
-    _say(f"  {label}: n={n} nnz={len(col)} tiles={tiles} relL2={err:.2e}")
+    _say(f"  {label} {tile_rows}x{tile_cols}: n={n} nnz={len(col)} tiles={tiles} relL2={err:.2e}")
     assert tiles == want_tiles
     assert err <= TOL
     return att
@@ -86,27 +95,27 @@ def mixture20k():
     return idx, dist, y
 
 
-def test_tiled_attraction_matches_direct_sum(hip, mixture20k):
-    _say("case: tiled attraction, mixture n=20000 k=30")
+def test_tiled_attraction_matches_direct_sum(hip, mixture20k, shape):
+    _say(f"case: tiled attraction, mixture n=20000 k=30, tiles {shape}")
     idx, dist, y = mixture20k
-    _check(hip, idx, dist, 10.0, y, "mixture")
+    _check(hip, idx, dist, 10.0, y, "mixture", shape)
 
 
-def test_tiled_attraction_short_rows(hip):
-    _say("case: tiled attraction, mixture n=13001 k=3 (pieces of 1 to 6 entries)")
+def test_tiled_attraction_short_rows(hip, shape):
+    _say(f"case: tiled attraction, mixture n=13001 k=3 (pieces of 1 to 6 entries), tiles {shape}")
     n = 13001
     x, labels, idx, dist = small_problem(n=n, dim=6, k=3, components=5, seed=8)
     y = (np.random.default_rng(5).standard_normal((n, 2)) * 10).astype(np.float32)
-    _check(hip, idx, dist, 1.0, y, "short rows")
+    _check(hip, idx, dist, 1.0, y, "short rows", shape)
 
 
-def test_tiled_attraction_long_parts(hip):
-    _say("case: tiled attraction, ring neighbours (parts of up to 60 entries)")
+def test_tiled_attraction_long_parts(hip, shape):
+    _say(f"case: tiled attraction, ring neighbours (parts of up to 60 entries), tiles {shape}")
     n, k = 9000, 60
     idx, dist = ring_knn(n, k)
     rng = np.random.default_rng(3)
     y = (rng.standard_normal((n, 2)) * 3).astype(np.float32)
-    _check(hip, idx, dist, 20.0, y, "ring")
+    _check(hip, idx, dist, 20.0, y, "ring", shape)
 
 
 def scattered_knn(n, k, seed):
@@ -122,16 +131,16 @@ def scattered_knn(n, k, seed):
     return np.asfortranarray(idx), np.asfortranarray(dist)
 
 
-def test_tiled_attraction_sparse_runs(hip):
-    _say("case: tiled attraction, scattered neighbours n=60000 k=3 (sparse runs, bridge slots)")
+def test_tiled_attraction_sparse_runs(hip, shape):
+    _say(f"case: tiled attraction, scattered neighbours n=60000 k=3 (sparse runs, bridge slots), tiles {shape}")
     n = 60000
     idx, dist = scattered_knn(n, 3, 11)
     y = (np.random.default_rng(6).standard_normal((n, 2)) * 5).astype(np.float32)
-    _check(hip, idx, dist, 1.0, y, "scattered")
+    _check(hip, idx, dist, 1.0, y, "scattered", shape)
 
 
-def test_tiled_matches_row_parallel(hip, mixture20k, monkeypatch):
-    _say("case: tiled vs row-parallel attraction")
+def test_tiled_matches_row_parallel(hip, mixture20k, shape, monkeypatch):
+    _say(f"case: tiled vs row-parallel attraction, tiles {shape}")
     idx, dist, y = mixture20k
     with hip.TsneSession(idx, dist, perplexity=10.0, index_offset=1) as s:
         s.set_state(y)
