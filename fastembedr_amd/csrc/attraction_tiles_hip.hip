@@ -339,19 +339,32 @@ __device__ __forceinline__ TileStep next_tile_step(TileStep s, const int* __rest
 // waits for the previous tile's readers).  Each lane issues all its loads
 // before its first write; slots past the tile's last column repeat it.
 template <int NT, int COLS>
+struct TileColumns {
+  static_assert(COLS % NT == 0, "whole column slots per lane");
+  static constexpr int kPer = COLS / NT;
+  float2 v[kPer];
+  // the lane's positions of column tile cb (loads only)
+  __device__ __forceinline__ void load(const float2* __restrict__ y_cur, int cb, int n, int tid) {
+    const int base = cb * COLS;
+    const int last = min(COLS, n - base) - 1;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) v[i] = y_cur[base + min(tid + i * NT, last)];
+  }
+  // to LDS, between barriers (the first waits for the previous tile's readers)
+  __device__ __forceinline__ void store(float2* ys, int tid) const {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) ys[tid + i * NT] = v[i];
+    __syncthreads();
+  }
+};
+
+template <int NT, int COLS>
 __device__ __forceinline__ void stage_tile_columns(float2* ys, const float2* __restrict__ y_cur, int cb, int n,
                                                    int tid) {
-  constexpr int kPer = COLS / NT;
-  static_assert(COLS % NT == 0, "whole column slots per lane");
-  const int base = cb * COLS;
-  const int last = min(COLS, n - base) - 1;
-  float2 v[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) v[i] = y_cur[base + min(tid + i * NT, last)];
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) ys[tid + i * NT] = v[i];
-  __syncthreads();
+  TileColumns<NT, COLS> c;
+  c.load(y_cur, cb, n, tid);
+  c.store(ys, tid);
 }
 
 // Adds (x, y) to the accumulator at row byte offset k: by a plain read and
@@ -465,7 +478,11 @@ __device__ __forceinline__ void sum_tile_group(const TileGroup& g, const TileSte
 // prefetch in flight; every wave runs the same steps (DPP needs whole
 // waves).  Starts and ends with LDS free for the next row block (every
 // thread passes a barrier between its last LDS access and the end).
-template <int NT, int D, int ROWS, int COLS>
+// PREF: a step that opens a column tile other than the block's first finds
+// the tile's positions already in registers, loaded before the step ahead of
+// it was summed, so that the switch waits only for its two barriers (4
+// positions per lane with 2048-column tiles: 8 VGPRs).
+template <int NT, int D, int ROWS, int COLS, bool PREF>
 __device__ __forceinline__ void attract_row_block(int rb, const unsigned short* __restrict__ ent,
                                                   const float* __restrict__ val, const int* __restrict__ tile_ptr,
                                                   const int* __restrict__ tile_cb, const int* __restrict__ tile_beg,
@@ -490,11 +507,22 @@ __device__ __forceinline__ void attract_row_block(int rb, const unsigned short* 
     for (int d = 1; d < D; ++d) st[d] = d < steps ? next_tile_step<NT>(st[d - 1], tile_beg, t1) : st[d - 1];
 #pragma unroll
     for (int d = 0; d < D; ++d) g[d] = load_tile_group<NT>(ent, val, st[d].e0, st[d].e1, st[d].round, tid);
+    TileColumns<NT, COLS> next;  // PREF: the positions of the tile that the next step opens
     for (int k = 0; k < steps; k += D) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
         const bool live = k + d < steps;
-        if (live && st[d].round == 0) stage_tile_columns<NT, COLS>(ys, y_cur, tile_cb[st[d].t], n, tid);
+        if (live && st[d].round == 0) {
+          if (PREF && k + d > 0) {
+            next.store(ys, tid);
+          } else {
+            stage_tile_columns<NT, COLS>(ys, y_cur, tile_cb[st[d].t], n, tid);
+          }
+        }
+        // the buffer after d holds step k + d + 1 (refilled earlier when d + 1 == D)
+        if (PREF && k + d + 1 < steps && st[(d + 1) % D].round == 0) {
+          next.load(y_cur, tile_cb[st[(d + 1) % D].t], n, tid);
+        }
         sum_tile_group<NT, ROWS>(g[d], st[d], live, tid, yr, ys, acc);
         // refill with step k + d + D, whose predecessor is the newest buffer
         const TileStep newest = st[(d + D - 1) % D];
@@ -548,7 +576,7 @@ __global__ __launch_bounds__(NT, MINB) void k_attract_tiles_seg(
     __syncthreads();
   }
   while (first + slot < end) {
-    attract_row_block<NT, D, ROWS, COLS>(first + slot, ent, val, tile_ptr, tile_cb, tile_beg, y_cur, attr,
+    attract_row_block<NT, D, ROWS, COLS, (COLS / NT <= 4)>(first + slot, ent, val, tile_ptr, tile_cb, tile_beg, y_cur, attr,
                                          exaggeration, n, ys, yr, acc);
     if (threadIdx.x == 0) claimed = slots + static_cast<int>(atomicAdd(&work[xcd], 1u));
     __syncthreads();
