@@ -336,7 +336,7 @@ constexpr int kTileRows = 1024;
 constexpr int kTileCols = 4096;
 constexpr int kTileRowsWide = 2048;
 constexpr int kTileColsWide = 2048;
-constexpr int kTileWideFrom = 1 << 21;  // points from which tiles_shape picks the wide shape
+constexpr int kTileWideFrom = 1 << 19;  // points from which tiles_shape picks the wide shape (>= 256 row blocks)
 constexpr int kTileRun = 8;
 constexpr int kTileMaxXcds = 16;
 constexpr int kTileThreads = 512;

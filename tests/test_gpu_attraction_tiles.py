@@ -13,7 +13,7 @@ whose parts in one tile are far longer than a lane's group of 8 slots, rows
 of one or two entries, sparse runs whose rows lie more than 7 apart (bridge
 slots), and sizes that are not multiples of the tile shape, each in both
 tile shapes (1024 rows x 4096 columns and 2048 x 2048, the one picked from
-2**21 points; FASTEMBEDR_HIP_TILE_SHAPE forces either).
+2**19 points; FASTEMBEDR_HIP_TILE_SHAPE forces either).
 """
 
 import sys
