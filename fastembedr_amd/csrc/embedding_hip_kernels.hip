@@ -1211,7 +1211,9 @@ __global__ __launch_bounds__(kPointThreads) void k_morton_keys(const float2* __r
 }
 
 // Estimated number of (row block, column tile) runs that P would have in a
-// candidate numbering: every step-th block of kTileRows new rows is taken,
+// candidate numbering, counted on the 1024 x 4096 shape whichever shape the
+// session's tiles have (a proxy for locality, compared between two
+// numberings): every step-th block of kTileRows new rows is taken,
 // the distinct column tiles of its entries are marked in an LDS bitmap
 // (`words` 32-bit words) and counted.  order maps new -> old rows and map old
 // -> new columns; null pointers stand for the identity (the current

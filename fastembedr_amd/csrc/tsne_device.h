@@ -328,10 +328,11 @@ hipError_t launch_gather2(const float2* src, const int* idx, float2* dst, int n,
 // tile_ptr[rb + 1]; tile t covers slots tile_beg[t] .. tile_beg[t + 1] and
 // column tile tile_cb[t].  Every run starts at a multiple of kTileRun slots
 // and is padded to one with slots of value 0.
-// Two shapes, chosen per session (tiles_shape): 1024 rows x 4096 columns,
-// or 2048 x 2048 for large n, whose short runs make the column tiles'
-// staging a large share of the bytes: the same LDS (48 KB) and about the
-// same slots per run, half the staged bytes per run.
+// Two shapes, chosen per session (tiles_shape): 2048 rows x 2048 columns
+// from kTileWideFrom points, 1024 x 4096 below (more row blocks for small
+// n).  Both take 48 KB of LDS and hold about the same slots per run; a
+// square tile stages half the positions per visit, few enough (4 per lane)
+// that the kernel loads the next tile's into registers before the switch.
 constexpr int kTileRows = 1024;
 constexpr int kTileCols = 4096;
 constexpr int kTileRowsWide = 2048;
