@@ -25,8 +25,11 @@ kernel belong to the timed window, which rocprof digests rely on):
   2. the whole schedule timed from the host without events
      (full_schedule: its mean rate);
   3. the window with HIP events around every kernel, which runs the
-     kernels in sequence (the per-kernel breakdown, ms_per_repulsion_step);
-  4. the window timed (value), with events only around the dominant kernel,
+     kernels in sequence (the per-kernel breakdown);
+  4. the window run in sequence again with one pair of events around the
+     repulsion step's kernels only (ms_per_repulsion_step: the step alone,
+     without the per-kernel events' overhead);
+  5. the window timed (value), with events only around the dominant kernel,
      on the stream it runs on, on every DOM_EVERY-th iteration (an event's
      marker delays the launch behind it); the library runs the attraction
      and the kernel spectrum on side streams beside the rest of each
@@ -201,8 +204,21 @@ def main() -> int:
     rep_kernels = [kname for kname in per_kernel if kname.startswith("interp_")] if interp else \
         [kname for kname in ("bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols",
                              "charge_rows", "conv_cols", "inverse_rows") if kname in per_kernel]
-    rep_ms = sum(per_kernel[kname] for kname in rep_kernels)
+    rep_sum_ms = sum(per_kernel[kname] for kname in rep_kernels)
     dom = max(breakdown, key=lambda kname: breakdown[kname][1])  # largest total time
+
+    # 3b. the repulsion step's span: the window in sequence again, with one
+    # pair of events around the step's kernels (kernel spectrum to
+    # potentials) instead of a pair around each of them
+    reset()
+    schedule_run(0, head)
+    sess.sync()
+    sess.set_timing(True, only="repulsion")
+    schedule_run(head, total)
+    sess.sync()
+    span_cnt, span_tot = sess.timing()["repulsion"]
+    sess.set_timing(False)
+    rep_ms = span_tot / span_cnt if span_cnt else rep_sum_ms
 
     # 4. the timed window: events only around the dominant kernel, and only
     # on every DOM_EVERY-th iteration (an event's marker delays the launch
@@ -247,8 +263,8 @@ def main() -> int:
     traffic_source = digest["_file"] if traffic is not None and digest is not None else None
     # The repulsion step's roofline: B_rep = 16 n + 8 n
     # + 28 G^2 + 288 F^2 with G the grid nodes per axis and F the FFT length
-    # at the end of the window, over the summed repulsion kernels of the
-    # breakdown pass; traffic: the rocprof digest's bytes of the same kernels
+    # at the end of the window, over the repulsion step's span in sequence
+    # (pass 3b); traffic: the rocprof digest's bytes of the same kernels
     # per iteration.
     if interp:
         # the shortest FFT length the grid can use (2^a or 3 * 2^a, at least
@@ -322,6 +338,9 @@ def main() -> int:
                           "ms_per_step": round(1000.0 * full_wall / total, 4),
                           "note": "whole 750-iteration schedule timed from the host, no events"},
         "ms_per_repulsion_step": round(rep_ms, 4),
+        "repulsion_step_basis": "the step's kernels run in sequence, one pair of HIP events around them all, "
+                                "mean over the window's iterations",
+        "repulsion_kernels_summed_ms": round(rep_sum_ms, 4),
         "repulsion_kernels": rep_kernels,
         "repulsion_roofline": {
             "bound": "hbm",
@@ -330,7 +349,7 @@ def main() -> int:
             "frac": round(rep_measured / HBM_PEAK_GBS, 4) if rep_measured else None,
             "traffic": rep_traffic,
             "basis": "measured: the traffic digest's FETCH_SIZE + WRITE_SIZE bytes of the repulsion kernels per "
-                     "iteration over ms_per_repulsion_step (the repulsion kernels in sequence)",
+                     "iteration over ms_per_repulsion_step (the repulsion step in sequence)",
             "algorithmic": {
                 "bytes": int(rep_bytes), "achieved": round(rep_alg, 1), "frac": round(rep_alg / HBM_PEAK_GBS, 4),
                 "basis": f"B_rep = 24 n + 28 G^2 + 288 F^2 with G = {g_nodes} nodes per axis, F = {f_len}; it "

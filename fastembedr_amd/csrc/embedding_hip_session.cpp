@@ -416,7 +416,7 @@ const char* kKernelNames[fehip::kKernelCount] = {
     "conv_cols", "inverse_rows", "attract", "update", "commit", "renumber", "tile_build",
     "interp_order", "interp_spread",
     "interp_kernel_rows", "interp_kernel_cols", "interp_charge_rows", "interp_conv_cols", "interp_inverse_rows",
-    "finalize_stats"};
+    "finalize_stats", "repulsion"};
 
 int key_bits_for(int n) {
   int b = 1;
@@ -838,6 +838,12 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
   if (swap && !enqueue_attract(s, s->y_a(), exaggeration, main, true, s->update_on_chain ? s->ev_attr : nullptr)) {
     return false;
   }
+  // Run in sequence (no overlap), the repulsion step's kernels are
+  // contiguous on the main stream from the kernel spectrum to the
+  // potentials: with the step the one id timed, two events bracket them all.
+  std::size_t rep_slot = 0;
+  const bool rep_span = !overlap && s->timed_only == fehip::kKRepulsion && s->records(fehip::kKRepulsion);
+  if (rep_span && !s->span_begin(fehip::kKRepulsion, main, &rep_slot)) return false;
   if (lg) {
     static constexpr int kIds[2] = {fehip::kKLgKernelRows, fehip::kKLgKernelCols};
     static constexpr int kSteps[2] = {0, 2};
@@ -923,7 +929,7 @@ bool enqueue_gradient_pieces(fastembedr_hip_tsne* s, bool lg, int fft_len, float
              fehip::kKInverseRows, "inverse_rows launch",
              [&] { return fehip::launch_inverse_rows(s->gb, s->tw, n, s->sc, chain); }, chain);
   }
-  if (!ok) return false;
+  if (!ok || (rep_span && !s->span_end(rep_slot, main))) return false;
   if (swap) {
     if (s->update_on_chain) {
       // the chain's stream waits for the attraction (ev_attr, recorded right
@@ -1888,9 +1894,10 @@ int fastembedr_hip_tsne_run(fastembedr_hip_tsne* s, int n_iter, float exaggerati
     if (lg) {
       s->lg_order_due = s->lg_order_period > 0 && (s->lg_order_stale || s->lg_order_age >= s->lg_order_period);
     }
-    // Timing every kernel (mode 1) runs the pieces in sequence, so that each
-    // duration is the kernel's alone; timed runs are never replayed graphs.
-    const bool overlap = !(s->timing && s->timed_only < 0);
+    // Timing every kernel (mode 1) or the repulsion step's span runs the
+    // pieces in sequence, so that each duration is the kernel's (the step's)
+    // alone; timed runs are never replayed graphs.
+    const bool overlap = !(s->timing && (s->timed_only < 0 || s->timed_only == fehip::kKRepulsion));
     const bool ok = s->graph_capture && !s->timing ? enqueue_iteration_graphed(s, lg, fft_len, up, pending)
                                                    : enqueue_iteration(s, lg, fft_len, up, overlap, pending);
     if (!ok) return 1;

@@ -135,6 +135,9 @@ enum KernelId : int {
   kKLgConvCols,
   kKLgInverseRows,
   kKFinalize,
+  // not a kernel: the repulsion step's span, from its first kernel to its
+  // last, run in sequence (timed only when it is the one id timed)
+  kKRepulsion,
   kKernelCount
 };
 

@@ -218,7 +218,11 @@ FASTEMBEDR_HIP_API int fastembedr_hip_tsne_kl_rows(fastembedr_hip_tsne* session,
  * the stream the kernel runs on.  run() normally runs the
  * attraction and the repulsion kernel spectrum on side streams beside the
  * rest of the iteration; with every kernel timed it runs them in sequence,
- * so that each duration is the kernel's alone.  stats returns, per kernel id,
+ * so that each duration is the kernel's alone.  The id named "repulsion" is
+ * no kernel: timed alone, it runs the iteration in sequence and brackets the
+ * repulsion step's kernels (kernel spectrum to potentials) with one pair of
+ * events, the step's duration without per-kernel event overhead.  stats
+ * returns, per kernel id,
  * the number of launches timed and their summed duration in milliseconds.
  * Kernel ids and names: fastembedr_hip_tsne_kernel_name(). */
 FASTEMBEDR_HIP_API int fastembedr_hip_tsne_set_timing(fastembedr_hip_tsne* session, int enabled);

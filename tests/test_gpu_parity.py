@@ -343,3 +343,38 @@ def test_sampled_kernel_timing(hip, mid_problem, every):
                 assert all(c == 0 for name, (c, _) in t.items() if name != "attract"), t
             layouts.append(s.y)
     assert all(np.all(np.isfinite(y)) for y in layouts)
+
+
+def test_repulsion_span_timing(hip, mid_problem):
+    """set_timing(only="repulsion") runs the iterations in sequence and
+    brackets the repulsion step's kernels with one pair of events: one span
+    per iteration, no kernel timed on its own, and each span longer than the
+    largest of the step's kernels timed one by one and within twice their
+    sum plus 50 us (the span also holds the short gaps between them)."""
+    x, idx, dist = mid_problem
+    n = x.shape[0]
+    y0 = synthetic.pca_init(x)
+    _say("case: repulsion span timing")
+    with hip.TsneSession(idx, dist, perplexity=15.0, index_offset=1) as s:
+        s.set_state(y0)
+        s.run(5, 12.0, 0.5, n / 12.0, 0.01, 5.0)
+        s.set_timing(True)
+        s.run(10, 12.0, 0.5, n / 12.0, 0.01, 5.0)
+        s.sync()
+        each = s.timing()
+        s.set_timing(True, only="repulsion")
+        s.run(10, 12.0, 0.5, n / 12.0, 0.01, 5.0)
+        s.sync()
+        span = s.timing()
+        s.set_timing(False)
+        assert np.all(np.isfinite(s.y))
+    cnt, tot = span["repulsion"]
+    assert cnt == 10, span
+    assert all(c == 0 for name, (c, _) in span.items() if name != "repulsion"), span
+    assert each["repulsion"][0] == 0, each
+    rep = [name for name in each if name.startswith("interp_") or name in (
+        "bin_count", "bin_plan", "bin_scatter", "spread", "kernel_rows", "kernel_cols", "charge_rows", "conv_cols",
+        "inverse_rows")]
+    per = {name: each[name][1] / 10 for name in rep if each[name][0]}
+    _say(f"  span {tot / cnt:.4f} ms, kernels one by one {sum(per.values()):.4f} ms ({per})")
+    assert max(per.values()) < tot / cnt < 2.0 * sum(per.values()) + 0.05
