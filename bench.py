@@ -620,7 +620,7 @@ TRAFFIC_FILES = {"grid": [ROOT / "profiles" / "tsne_loop_config2_grid_traffic.js
 # the digest's window.
 REPULSION_SYMBOLS = {
     "interp": ("k_lg_order_keys", "rocprim:", "k_lg_spread", "k_lg_kernel_rows", "k_lg_kernel_cols",
-               "k_lg_charge_rows", "k_lg_conv_cols", "k_lg_inverse_rows", "k_lg_finalize_z"),
+               "k_lg_box_chunks", "k_lg_charge_rows", "k_lg_conv_cols", "k_lg_inverse_rows", "k_lg_finalize_z"),
     "grid": ("k_bin_count", "k_bin_plan", "k_bin_scatter", "k_spread_tiles", "k_kernel_rows", "k_kernel_cols",
              "k_charge_rows", "k_conv_cols", "k_inverse_rows", "k_finalize_sumq"),
 }

@@ -48,11 +48,13 @@
 //   k_lg_kernel_rows/cols spectra of K, K1 (real, even) and Kv (imaginary,
 //                         odd in its own axis), a quadrant each, two real
 //                         sequences per complex transform
-//   k_lg_charge_rows      one workgroup per node row: the entries (and the
-//                         rare straggler sums) of each box of its box row
-//                         summed, combined into the row's node moments (m2
-//                         stored), then m0 + i m1x and m1y per complex row
-//                         transform, half spectra kept
+//   k_lg_box_chunks       every box's entries summed in chunks of 32, each
+//                         chunk's sum stored over its first entry
+//   k_lg_charge_rows      one workgroup per node row: the chunk sums (and
+//                         the rare straggler sums) of each box of its box
+//                         row summed, combined into the row's node moments
+//                         (m2 stored), then m0 + i m1x and m1y per complex
+//                         row transform, half spectra kept
 //   k_lg_conv_cols        forward column transforms, spectral products for
 //                         phi0, xi_x, xi_y and the spectral sums of Z, inverse
 //                         column transforms, in one pass; clears the box
@@ -283,9 +285,10 @@ __global__ __launch_bounds__(kLgThreads) void k_lg_order_keys(const float2* __re
 // the run's sums into it (LDS float atomics).  Each occupied slot then takes
 // the next of its box's entries (an integer atomic on the box's count; K
 // entries per box, K = min(kLgMaxPerBox, kLgEntryPool / boxes), so that few
-// boxes get many) and stores its sums there with plain stores.  The charge
-// row transform (k_lg_charge_rows, one workgroup per node row) then sums
-// each box's entries and combines them into the nodes' moments.  Float
+// boxes get many) and stores its sums there with plain stores.  Each box's
+// entries are then summed in chunks (k_lg_box_chunks), and the charge row
+// transform (k_lg_charge_rows, one workgroup per node row) sums each box's
+// chunks and combines them into the nodes' moments.  Float
 // atomics in global memory (they resolve beyond the XCDs' L2s and cost far
 // more than the LDS path) are left for the rare exceptions, which go to a
 // straggler array of power sums per box that the row transform adds (only
@@ -604,9 +607,48 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_kernel_cols(const DeviceS
   }
 }
 
+// The boxes' entries summed in chunks of kLgEntryChunk, once: one thread
+// per (box, chunk, sum) writes its chunk's sum over the chunk's first entry
+// (the only location it reads that another thread could read is its own),
+// so that the row transform reads one partial per chunk; dense boxes (early
+// in the optimisation, the 50 x 50 grid's crowded boxes) spread over as many
+// threads as they have chunks.  A grid flagged by the spread is skipped.
+constexpr int kLgEntryChunk = 32;
+__global__ __launch_bounds__(256) void k_lg_box_chunks(const DeviceScalars* sc, int max_nodes, float* entries,
+                                                       const int* __restrict__ box_count) {
+  chain_priority();
+  if (sc->lg_nodes > max_nodes) return;
+  const int nb = sc->lg_boxes;
+  const int per = lg_entries_per_box(nb);
+  const int maxc = (per + kLgEntryChunk - 1) / kLgEntryChunk;
+  const long long items = static_cast<long long>(nb) * nb * maxc * kLgSums;
+  for (long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; t < items;
+       t += static_cast<long long>(gridDim.x) * 256) {
+    const int e = static_cast<int>(t % kLgSums);
+    const long long rest = t / kLgSums;
+    const int c = static_cast<int>(rest % maxc);
+    const int b = static_cast<int>(rest / maxc);
+    const int k0 = c * kLgEntryChunk;
+    const int k1 = min(min(box_count[b] & kLgCountMask, per), k0 + kLgEntryChunk);
+    if (k0 >= k1) continue;
+    float* src = entries + (static_cast<std::size_t>(b) * per + k0) * kLgSums + e;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    int k = 0;
+    const int len = k1 - k0;
+    for (; k + 4 <= len; k += 4) {
+      s0 += src[static_cast<std::size_t>(k) * kLgSums];
+      s1 += src[static_cast<std::size_t>(k + 1) * kLgSums];
+      s2 += src[static_cast<std::size_t>(k + 2) * kLgSums];
+      s3 += src[static_cast<std::size_t>(k + 3) * kLgSums];
+    }
+    for (; k < len; ++k) s0 += src[static_cast<std::size_t>(k) * kLgSums];
+    src[0] = (s0 + s1) + (s2 + s3);
+  }
+}
+
 // Row transforms of the charges, one workgroup per row of boxes (by < nb):
-// the row's boxes' entries (at most K per box) and, when flagged, straggler
-// sums (then cleared, with the counts) are summed into each box's 21 power
+// the row's boxes' chunk sums (k_lg_box_chunks) and, when flagged, straggler
+// sums are summed into each box's 21 power
 // sums, which give the node moments of the box row's kLgOrder node rows
 // (kLgCoef); m2 goes to its plane for the inverse pass, and A = m0 + i m1x
 // and B = m1y per node row (zero-padded to F) are transformed, one node row
@@ -638,9 +680,8 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
   // the box sums share the transform's buffer: the node moments are taken
   // to registers before the buffer is written (15.4 KB of LDS at F = 768,
   // so that a workgroup fits a CU beside three attraction workgroups)
-  static_assert((NB * (kLgSums + 1) + 1) * sizeof(float) <= sizeof(lds), "box sums fit the transform buffer");
+  static_assert(NB * kLgSums * sizeof(float) <= sizeof(lds), "box sums fit the transform buffer");
   float* ps = reinterpret_cast<float*>(lds);
-  int* pcnt = reinterpret_cast<int*>(ps + NB * kLgSums);  // entries per box, then the row's largest count
   const int m = sc->lg_nodes;
   if (m > max_nodes) return;  // flagged by the spread
   const int nb = sc->lg_boxes;
@@ -648,54 +689,18 @@ __global__ __launch_bounds__(LgShape<F>::NT) void k_lg_charge_rows(const DeviceS
   if (by >= nb) return;
   stage_twiddles<F, S::NT>(tws, tw);
   const int per = lg_entries_per_box(nb);
-  if (threadIdx.x == 0) pcnt[NB] = 0;
-  __syncthreads();
-  // the row's boxes: entry counts, straggler sums as the starting values
-  int cmax = 0;
-  for (int bx = threadIdx.x; bx < nb; bx += S::NT) {
-    const int cnt = min(box_count[by * nb + bx] & kLgCountMask, per);
-    pcnt[bx] = cnt;
-    cmax = max(cmax, cnt);
-  }
+  // each box's sums: its straggler sums (when flagged) as the starting
+  // values, then its chunks' sums in chunk order
   for (int q = threadIdx.x; q < nb * kLgSums; q += S::NT) {
     const int bx = q / kLgSums;
+    const int e = q - bx * kLgSums;
     const int b = by * nb + bx;
-    ps[q] = (box_count[b] & kLgStraggled) != 0 ? straggler[static_cast<std::size_t>(b) * kLgSums + (q - bx * kLgSums)]
-                                               : 0.0f;
-  }
-  if (cmax > 0) atomicMax(&pcnt[NB], cmax);
-  __syncthreads();
-  // the entries, in chunks of kChunk per (box, sum) work item, so that the
-  // hundreds of entries of a dense box (early in the optimisation, the 50 x
-  // 50 grid's crowded boxes) spread over the workgroup; each chunk is summed
-  // with four partial sums and added to its box's sum (an LDS float atomic
-  // when a box has several chunks)
-  constexpr int kChunk = 32;
-  const int chunks = (pcnt[NB] + kChunk - 1) / kChunk;
-  for (int it = threadIdx.x; it < nb * chunks * kLgSums; it += S::NT) {
-    const int e = it % kLgSums;
-    const int bc = it / kLgSums;
-    const int bx = bc / chunks;
-    const int c = bc - bx * chunks;
-    const int k0 = c * kChunk;
-    const int k1 = min(pcnt[bx], k0 + kChunk);
-    if (k0 >= k1) continue;
-    const float* src = entries + static_cast<std::size_t>(by * nb + bx) * per * kLgSums + e;
-    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
-    int k = k0;
-    for (; k + 4 <= k1; k += 4) {
-      s0 += src[static_cast<std::size_t>(k) * kLgSums];
-      s1 += src[static_cast<std::size_t>(k + 1) * kLgSums];
-      s2 += src[static_cast<std::size_t>(k + 2) * kLgSums];
-      s3 += src[static_cast<std::size_t>(k + 3) * kLgSums];
-    }
-    for (; k < k1; ++k) s0 += src[static_cast<std::size_t>(k) * kLgSums];
-    const float part = (s0 + s1) + (s2 + s3);
-    if (chunks == 1) {
-      ps[bx * kLgSums + e] += part;
-    } else {
-      atomicAdd(&ps[bx * kLgSums + e], part);
-    }
+    const int word = box_count[b];
+    float acc = (word & kLgStraggled) != 0 ? straggler[static_cast<std::size_t>(b) * kLgSums + e] : 0.0f;
+    const int chunks = (min(word & kLgCountMask, per) + kLgEntryChunk - 1) / kLgEntryChunk;
+    const float* src = entries + static_cast<std::size_t>(b) * per * kLgSums + e;
+    for (int c = 0; c < chunks; ++c) acc += src[static_cast<std::size_t>(c) * kLgEntryChunk * kLgSums];
+    ps[q] = acc;
   }
   __syncthreads();
   {
@@ -988,11 +993,18 @@ hipError_t lg_fft_launch(int which, InterpBuffers& ib, DeviceScalars* sc, const 
     case 2:
       k_lg_kernel_cols<F><<<col_launch(kblocks), S::NT, 0, stream>>>(sc, ib.k_rows, tw, ib.k_cols);
       break;
-    case 3:
+    case 3: {
+      // every (box, chunk, sum) item of the largest grid this length holds
+      const int nbb = lg_boxes_bound(F);
+      const long long per_max = std::max(1LL, std::min<long long>(kLgMaxPerBox, kLgEntryPool / (static_cast<long long>(nbb) * nbb)));
+      const long long items = static_cast<long long>(nbb) * nbb * ((per_max + kLgEntryChunk - 1) / kLgEntryChunk) * kLgSums;
+      const unsigned int cblocks_sum = static_cast<unsigned int>(std::min<long long>((items + 255) / 256, 8192));
+      k_lg_box_chunks<<<cblocks_sum, 256, 0, stream>>>(sc, nbb * kLgOrder, ib.entries, ib.box_count);
       k_lg_charge_rows<F><<<dim3(F / 2 / kLgOrder, kLgOrder), S::NT, 0, stream>>>(sc, lg_boxes_bound(F) * kLgOrder, ib.entries,
                                                                   ib.box_count, ib.straggler, ib.m2, tw, ib.spec_a,
                                                                   plane);
       break;
+    }
     case 5:
       k_lg_conv_cols<F><<<cblocks, S::NTW, 0, stream>>>(sc, ib.spec_a, ib.k_cols, tw, ib.spec_b, plane, spec_part,
                                                          ib.box_count, ib.straggler);
