@@ -927,9 +927,11 @@ __global__ __launch_bounds__(256) void k_attract(const int* __restrict__ row_ptr
 // bilinear grid y_cur is the centred copy the binning wrote; with the
 // interpolation grid it is the stored layout, centred here (the shift of the
 // current geometry), and y_out may be the same buffer (each point is read
-// before it is written, by the same thread).
+// before it is written, by the same thread).  At least 5 waves per SIMD (the
+// second launch bound): 89 VGPRs instead of 105 with the interpolation
+// grid's nine node fields per point in flight, no spills (6 waves spill).
 template <int MODE, bool LG>
-__global__ __launch_bounds__(kPointThreads) void k_update(const float2* y_cur,
+__global__ __launch_bounds__(kPointThreads, 5) void k_update(const float2* y_cur,
                                                           const float2* __restrict__ attr,
                                                           float2* y_out, float2* __restrict__ update,
                                                           float2* __restrict__ gains, float2* __restrict__ grad_out,
