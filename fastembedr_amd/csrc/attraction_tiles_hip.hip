@@ -546,8 +546,9 @@ __device__ __forceinline__ void attract_row_block(int rb, const unsigned short* 
 // stream once the kernels beside the primary are done, takes over the row
 // blocks still unclaimed.  The last workgroup of the pair (`total` workgroups
 // between them) resets work[] (its xcds + 1 counters start and end each
-// launch or pair at zero).  Launch bounds: MINB workgroups per CU (the VGPR
-// budget of the D-deep prefetch ring).
+// launch or pair at zero).  Launch bounds: MINB is HIP's minimum of waves
+// per SIMD (3 leaves the D-deep prefetch ring up to 168 VGPRs; the 48 KB of
+// LDS hold the kernel at 3 workgroups, 6 waves per SIMD, in any case).
 // HELPER: a helper launch (its own symbol, so that profiles tell the two
 // launches of a pair apart).  ROWS x COLS: the tile shape.
 template <int NT, int D, int MINB, bool HELPER, int ROWS, int COLS>
