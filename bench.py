@@ -396,9 +396,11 @@ def fft_sweep(sess, n, nnz, sched, lr, log) -> int:
     """The repulsion kernels at large FFT lengths on a real 1M-point layout:
     the converged layout (the schedule just run) scaled by s, so that its
     span needs s times the boxes.  Per scale, 20 iterations at learning rate
-    0 (the layout does not move) with every kernel timed alone by events;
-    the step clip is off, so the host sizes each iteration's FFT from that
-    iteration's own box count (the shortest length that holds the grid)."""
+    0 (the layout does not move) with every kernel timed alone by events,
+    then 20 more with one pair of events around the repulsion step's kernels
+    (ms_per_repulsion_step, as in the main line); the step clip is off, so
+    the host sizes each iteration's FFT from that iteration's own box count
+    (the shortest length that holds the grid)."""
     y_end = np.asarray(sess.y, np.float64)
     y_end -= y_end.mean(axis=0)
     cases = []
@@ -413,12 +415,20 @@ def fft_sweep(sess, n, nnz, sched, lr, log) -> int:
         sess.set_timing(False)
         info = sess.interp_info()
         per = {name: tot / 20 for name, (cnt, tot) in br.items() if cnt and name.startswith("interp_")}
-        rep = sum(per.values())
+        rep_sum = sum(per.values())
+        sess.set_timing(True, only="repulsion")
+        sess.run(20, sched["exaggeration"], sched["final_momentum"], 0.0, sched["min_gain"], 0.0)
+        sess.sync()
+        span_cnt, span_tot = sess.timing()["repulsion"]
+        sess.set_timing(False)
+        rep = span_tot / span_cnt if span_cnt else rep_sum
         cases.append({"scale": scale, "boxes_per_axis": info["boxes"], "nodes_per_axis": info["nodes"],
                       "fft_len": info["fft_len"], "ms_per_repulsion_step": round(rep, 4),
+                      "repulsion_kernels_summed_ms": round(rep_sum, 4),
                       "per_kernel_ms": {kk: round(v, 5) for kk, v in per.items()}})
         log(f"scale {scale}: {info['boxes']} boxes, {info['nodes']} nodes, FFT {info['fft_len']}: repulsion "
-            f"{rep:.3f} ms ({', '.join(f'{kk}={v:.4f}' for kk, v in per.items())})")
+            f"{rep:.3f} ms in sequence ({rep_sum:.3f} one by one: "
+            f"{', '.join(f'{kk}={v:.4f}' for kk, v in per.items())})")
     print(json.dumps({"metric": "interpolation-grid repulsion step at large FFT lengths (ms, kernels in sequence)",
                       "n": n, "nnz": nnz, "data": "synthetic (config 2, converged layout scaled)",
                       "cases": cases}), flush=True)
